@@ -1,0 +1,99 @@
+// neon_engine.hpp -- C++ engine API over the C-ABI in neon_gptoss.h.
+//
+// The reference's GPU-work objects are C++ "Systems": the constructor
+// allocates device state and throws std::runtime_error on failure, and one
+// call per frame records the work (NeonEngine/src/water_physics.cpp:23-123,
+// :131; failures propagate to main, NeonEngine/src/main.cpp:21-26).
+// neon::Engine keeps that shape for the gpt-oss token loop: construct, load
+// weights (checkpoint tensors or deterministic random init), prefill, decode.
+// Everything goes through the C-ABI, so this header needs no HIP includes.
+#pragma once
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "neon_gptoss.h"
+
+namespace neon {
+
+class Error : public std::runtime_error {
+ public:
+  Error(neon_status s, const std::string& what)
+      : std::runtime_error(what), status_(s) {}
+  neon_status status() const { return status_; }
+
+ private:
+  neon_status status_;
+};
+
+inline void check(neon_status s, const neon_ctx* ctx) {
+  if (s != NEON_OK) {
+    const char* m = neon_last_error(ctx);
+    throw Error(s, m ? m : "neon error");
+  }
+}
+
+class Config {
+ public:
+  static Config preset(const char* name) {
+    Config c;
+    check(neon_config_preset(name, &c.cfg_), nullptr);
+    return c;
+  }
+  neon_config& raw() { return cfg_; }
+  const neon_config& raw() const { return cfg_; }
+
+ private:
+  neon_config cfg_{};
+};
+
+class Engine {
+ public:
+  Engine(const Config& cfg, int device = 0) {
+    check(neon_ctx_create(&cfg.raw(), device, &ctx_), nullptr);
+  }
+  ~Engine() { neon_ctx_destroy(ctx_); }
+  Engine(const Engine&) = delete;
+  Engine& operator=(const Engine&) = delete;
+
+  // Model loading: deterministic random init or one checkpoint tensor.
+  void init_random(uint64_t seed, void* stream = nullptr) {
+    check(neon_init_random(ctx_, seed, stream), ctx_);
+  }
+  void load_tensor(const std::string& name, const void* data, size_t bytes) {
+    check(neon_load_tensor(ctx_, name.c_str(), data, bytes), ctx_);
+  }
+
+  // Forward: prefill `batch` prompts of equal length (row-major ids), then
+  // greedy decode steps; tokens() returns prompt + generated ids per row.
+  void prefill(const std::vector<int32_t>& ids, int batch, void* stream = nullptr) {
+    if (batch < 1 || ids.size() % (size_t)batch)
+      throw Error(NEON_EINVAL, "prefill: ids.size() must be a multiple of batch");
+    check(neon_prefill(ctx_, ids.data(), batch, (int)(ids.size() / batch), stream), ctx_);
+    batch_ = batch;
+  }
+  void decode(int n_steps, void* stream = nullptr) {
+    check(neon_decode(ctx_, n_steps, stream), ctx_);
+  }
+  std::vector<int32_t> tokens(void* stream = nullptr) {
+    int n = 0;
+    check(neon_seq_len(ctx_, &n), ctx_);
+    std::vector<int32_t> out((size_t)batch_ * n);
+    check(neon_read_tokens(ctx_, 0, n, out.data(), stream), ctx_);
+    return out;
+  }
+  std::vector<float> logits(int vocab, void* stream = nullptr) {
+    std::vector<float> out((size_t)batch_ * vocab);
+    check(neon_read_logits(ctx_, out.data(), stream), ctx_);
+    return out;
+  }
+  neon_ctx* handle() { return ctx_; }
+
+ private:
+  neon_ctx* ctx_ = nullptr;
+  int batch_ = 0;
+};
+
+}  // namespace neon

@@ -1,0 +1,189 @@
+/*
+ * neon_gptoss.h -- C-ABI of the MI355X (gfx950) gpt-oss token loop.
+ *
+ * Boundary.  The reference repository (NeonEngine) has no model-loading,
+ * forward or FFI interface for this path; it is a Vulkan graphics engine whose
+ * only GPU-work idiom is the C++ "System" object: a constructor that allocates
+ * device state and throws on failure, and a per-frame call that records a
+ * fixed sequence of compute dispatches into a caller-provided command buffer
+ * (NeonEngine/src/water_physics.cpp:23-123 constructor, :131 RunSimulation,
+ * :165-436 the dispatch chain; NeonEngine/src/raytracing_system.cpp:19-68,
+ * :1217 runShaders).  This header keeps that shape with HIP in place of
+ * Vulkan: a context is created once (neon_ctx_create ~ System constructor),
+ * every call enqueues work on a caller-provided stream (~ recording into the
+ * caller's VkCommandBuffer) and returns before the GPU finishes, and the
+ * caller synchronises.  Errors come back as neon_status codes instead of
+ * exceptions (the reference throws std::runtime_error up to main,
+ * NeonEngine/src/main.cpp:21-26); no C++ exception crosses this ABI.
+ *
+ * Conventions.
+ *   - All tensor pointers passed to kernel-level entry points are DEVICE
+ *     pointers owned by the caller.  bf16 tensors are passed as uint16_t bit
+ *     patterns.  Host arrays (prompt ids, outputs of neon_read_*) are copied
+ *     before the call returns.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - A context is not thread-safe; use one context per host thread.
+ *   - MXFP4 weights use the gpt-oss checkpoint layout: codes [N][K/2] bytes
+ *     (low nibble = element 2i, high nibble = element 2i+1), E8M0 scales
+ *     [N][K/32] bytes, one per 32 consecutive elements along K.
+ */
+#ifndef NEON_GPTOSS_H
+#define NEON_GPTOSS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum neon_status {
+  NEON_OK = 0,
+  NEON_EINVAL = 1,       /* bad argument: null pointer, bad shape or size   */
+  NEON_ENOMEM = 2,       /* device or host allocation failed                */
+  NEON_EHIP = 3,         /* a HIP runtime call failed (no device, ...)      */
+  NEON_ENAN_SCALE = 4,   /* an E8M0 scale byte 0xFF (NaN) in loaded weights */
+  NEON_EKV_FULL = 5,     /* the step would write past the KV-cache capacity */
+  NEON_ERANGE_TOKEN = 6, /* a token id outside [0, vocab)                   */
+  NEON_ESTATE = 7        /* call out of order (e.g. decode before prefill)  */
+} neon_status;
+
+typedef struct neon_ctx neon_ctx;
+
+/* Model shape.  Field meaning follows the gpt-oss config (HF
+ * configuration_gpt_oss.py); max_seq / max_batch size the KV cache. */
+typedef struct neon_config {
+  int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim;
+  int32_t n_experts, top_k, intermediate, vocab;
+  int32_t sliding_window, max_seq, max_batch;
+  float rope_theta, rope_factor, rope_beta_fast, rope_beta_slow;
+  int32_t rope_orig_max_pos;
+  float rms_eps, swiglu_limit, swiglu_alpha;
+} neon_config;
+
+/* ---- context-level API (the token loop) --------------------------------- */
+
+/* Fills `out` with a preset: "gpt-oss-20b" or "gpt-oss-120b". */
+neon_status neon_config_preset(const char* name, neon_config* out);
+
+/* Validates `cfg`, selects `device`, allocates weights, KV cache and
+ * activations.  Counterpart of the System constructor idiom
+ * (NeonEngine/src/water_physics.cpp:23-123). */
+neon_status neon_ctx_create(const neon_config* cfg, int device, neon_ctx** out);
+void neon_ctx_destroy(neon_ctx* ctx);
+
+/* Text of the last error on this context (or of the last failed
+ * neon_ctx_create on this thread when ctx is NULL). */
+const char* neon_last_error(const neon_ctx* ctx);
+
+/* Deterministic random weights (counter-based RNG keyed by seed and tensor),
+ * generated on the device; the CPU oracle regenerates the same bits. */
+neon_status neon_init_random(neon_ctx* ctx, uint64_t seed, void* stream);
+
+/* Copies one named tensor from host memory (gpt-oss checkpoint names, e.g.
+ * "model.layers.3.mlp.experts.gate_up_proj_blocks").  MXFP4 scale tensors
+ * are checked for the NaN byte 0xFF (NEON_ENAN_SCALE). */
+neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
+                             const void* host_data, size_t bytes);
+
+/* Starts `batch` sequences from host prompt ids [batch][n_tokens] and runs
+ * the teacher-forced steps over the prompt; afterwards the first generated
+ * token of each sequence is available. */
+neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
+                         int n_tokens, void* stream);
+
+/* Runs `n_steps` greedy decode steps for every live sequence (each step
+ * consumes the previously generated token and produces the next one). */
+neon_status neon_decode(neon_ctx* ctx, int n_steps, void* stream);
+
+/* Synchronises `stream` and copies tokens [start, start+count) of every
+ * sequence into out [batch][count] (prompt tokens first, then generated). */
+neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
+                             int32_t* out, void* stream);
+
+/* Synchronises and copies the fp32 logits of the last step [batch][vocab]. */
+neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream);
+
+/* Number of tokens held by each sequence (prompt + generated). */
+neon_status neon_seq_len(const neon_ctx* ctx, int* out);
+
+/* Device pointer of a weight tensor (same names as neon_load_tensor), for
+ * tests and tools; *bytes receives its size. */
+neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name, void** ptr,
+                            size_t* bytes);
+
+/* ---- kernel-level API (device pointers; stream-ordered) ------------------ */
+
+/* out[32 b + j] = E2M1(code) * 2^(scale_b - 127) in fp32, bit-exact;
+ * scale 0xFF gives NaN. */
+neon_status neon_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
+                               int64_t n_blocks, float* out, void* stream);
+
+/* y[b][n] = bf16( sum_k dq(W[n][k]) x[b][k] + bias[n] ), fp32 accumulate.
+ * bias may be NULL.  K % 32 == 0, K <= 8192. */
+neon_status neon_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                            const uint16_t* bias, const uint16_t* x,
+                            uint16_t* y, int N, int K, int B, void* stream);
+
+/* bf16 GEMV (nn.Linear layout W [N][K]); bias may be NULL; K % 8 == 0. */
+neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,
+                           const uint16_t* x, uint16_t* y, int N, int K, int B,
+                           void* stream);
+
+/* out[b] = bf16( w * (x[b] * rsqrt(mean(x[b]^2) + eps)) ). */
+neon_status neon_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out,
+                         int B, int H, float eps, void* stream);
+
+/* In-place YaRN RoPE (half-split rotation) on x [n_tok][n_heads][head_dim]
+ * at positions pos[n_tok] (device int32), using cfg's rope fields. */
+neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok,
+                           int n_heads, const neon_config* cfg, void* stream);
+
+/* Router: logits = x W^T + b (fp32, one canonical reduction order), top-k
+ * over the logits (ties -> lower index), softmax over the k values.
+ * idx [B][k] int32, score [B][k] fp32, logits [B][E] fp32 (may be NULL). */
+neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
+                             const uint16_t* b, int32_t* idx, float* score,
+                             float* logits, int B, int E, int H, int k,
+                             void* stream);
+
+/* MoE block on normalised x [B][H]: router + top-k experts, each
+ * gate_up (MXFP4 [E][2I][H], bias [E][2I]) -> SwiGLU-clamp -> down (MXFP4
+ * [E][H][I], bias [E][H]), weighted sum.  out [B][H] bf16; if residual is
+ * not NULL, out = bf16(residual + bf16(moe)).  idx/score may be NULL. */
+neon_status neon_moe_layer(const uint16_t* x, const uint16_t* router_w,
+                           const uint16_t* router_b, const uint8_t* gu_codes,
+                           const uint8_t* gu_scales, const uint16_t* gu_bias,
+                           const uint8_t* dn_codes, const uint8_t* dn_scales,
+                           const uint16_t* dn_bias, const uint16_t* residual,
+                           uint16_t* out, int32_t* idx, float* score, int B,
+                           int E, int H, int I, int k, float alpha,
+                           float limit, void* stream);
+
+/* Grouped expert FFN alone (HF GptOssExperts): for each row b and slot s,
+ * expert e = idx[b][s]: gate_up GEMV -> SwiGLU-clamp -> down GEMV, weighted
+ * by score[b][s] and summed over the k slots; out as in neon_moe_layer.
+ * act is caller-provided scratch of B*k*I bf16 (no allocation here). */
+neon_status neon_moe_experts(const uint16_t* x, const int32_t* idx,
+                             const float* score, const uint8_t* gu_codes,
+                             const uint8_t* gu_scales, const uint16_t* gu_bias,
+                             const uint8_t* dn_codes, const uint8_t* dn_scales,
+                             const uint16_t* dn_bias, const uint16_t* residual,
+                             uint16_t* out, uint16_t* act, int B, int E, int H,
+                             int I, int k, float alpha, float limit,
+                             void* stream);
+
+/* GQA decode attention with per-head sinks.  q [B][Hq][D] (already rotated),
+ * caches [B][Hkv][T_max][D], sinks [Hq] bf16, pos [B] device int32 (the
+ * current token's position: keys 0..pos, or the last `window` of them when
+ * window > 0).  out [B][Hq*D] bf16.  D == 64. */
+neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
+                             const uint16_t* v_cache, const uint16_t* sinks,
+                             const int32_t* pos, uint16_t* out, int B, int Hq,
+                             int Hkv, int D, int T_max, int window,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NEON_GPTOSS_H */

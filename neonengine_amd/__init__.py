@@ -1,0 +1,276 @@
+"""neonengine_amd -- ctypes view of the gfx950 gpt-oss token-loop library.
+
+The product is libneon_gptoss.so (hand-written HIP kernels for gfx950 behind
+the C-ABI in include/neon_gptoss.h).  This module binds that ABI for Python
+callers (tests, bench.py): every call goes straight into the shared library;
+there is no Python or CPU fallback, and loading fails loudly when the library
+has not been built.
+
+Device memory for the kernel-level entry points comes from torch tensors on
+``cuda`` (HIP) devices; only their data pointers cross the boundary.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libneon_gptoss.so")
+
+NEON_OK, NEON_EINVAL, NEON_ENOMEM, NEON_EHIP = 0, 1, 2, 3
+NEON_ENAN_SCALE, NEON_EKV_FULL, NEON_ERANGE_TOKEN, NEON_ESTATE = 4, 5, 6, 7
+STATUS_NAMES = {0: "NEON_OK", 1: "NEON_EINVAL", 2: "NEON_ENOMEM", 3: "NEON_EHIP",
+                4: "NEON_ENAN_SCALE", 5: "NEON_EKV_FULL", 6: "NEON_ERANGE_TOKEN",
+                7: "NEON_ESTATE"}
+
+# Every symbol include/neon_gptoss.h declares (tests check the exports).
+EXPORTS = (
+    "neon_config_preset", "neon_ctx_create", "neon_ctx_destroy", "neon_last_error",
+    "neon_init_random", "neon_load_tensor", "neon_prefill", "neon_decode",
+    "neon_read_tokens", "neon_read_logits", "neon_seq_len", "neon_tensor_ptr",
+    "neon_mxfp4_dequant", "neon_mxfp4_gemv", "neon_gemv_bf16", "neon_rmsnorm",
+    "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
+    "neon_attn_decode",
+)
+
+
+class NeonError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+class Config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim",
+        "n_experts", "top_k", "intermediate", "vocab",
+        "sliding_window", "max_seq", "max_batch")] + [
+        (n, C.c_float) for n in ("rope_theta", "rope_factor", "rope_beta_fast", "rope_beta_slow")] + [
+        ("rope_orig_max_pos", C.c_int32)] + [
+        (n, C.c_float) for n in ("rms_eps", "swiglu_limit", "swiglu_alpha")]
+
+    def as_dict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+_lib = None
+_P, _I, _I64, _U64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_size_t
+
+
+def lib():
+    """Load libneon_gptoss.so (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m neonengine_amd._build` "
+                "(the gfx950 HIP library is required; there is no fallback)")
+        L = C.CDLL(LIB_PATH)
+        sig = {
+            "neon_config_preset": [C.c_char_p, _P],
+            "neon_ctx_create": [_P, _I, _P],
+            "neon_ctx_destroy": [_P],
+            "neon_last_error": [_P],
+            "neon_init_random": [_P, _U64, _P],
+            "neon_load_tensor": [_P, C.c_char_p, _P, _SZ],
+            "neon_prefill": [_P, _P, _I, _I, _P],
+            "neon_decode": [_P, _I, _P],
+            "neon_read_tokens": [_P, _I, _I, _P, _P],
+            "neon_read_logits": [_P, _P, _P],
+            "neon_seq_len": [_P, _P],
+            "neon_tensor_ptr": [_P, C.c_char_p, _P, _P],
+            "neon_mxfp4_dequant": [_P, _P, _I64, _P, _P],
+            "neon_mxfp4_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
+            "neon_gemv_bf16": [_P, _P, _P, _P, _I, _I, _I, _P],
+            "neon_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
+            "neon_rope_yarn": [_P, _P, _I, _I, _P, _P],
+            "neon_router_topk": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+            "neon_moe_layer": [_P] * 13 + [_I] * 5 + [_F, _F, _P],
+            "neon_moe_experts": [_P] * 12 + [_I] * 5 + [_F, _F, _P],
+            "neon_attn_decode": [_P] * 6 + [_I] * 6 + [_P],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = C.c_int
+        L.neon_ctx_destroy.restype = None
+        L.neon_last_error.restype = C.c_char_p
+        _lib = L
+    return _lib
+
+
+def _check(status: int, ctx=None):
+    if status != NEON_OK:
+        msg = lib().neon_last_error(ctx)
+        raise NeonError(status, msg.decode() if msg else "")
+
+
+def config_preset(name: str = "gpt-oss-20b", **overrides) -> Config:
+    cfg = Config()
+    _check(lib().neon_config_preset(name.encode(), C.byref(cfg)))
+    for k, v in overrides.items():
+        setattr(cfg, k, v)
+    return cfg
+
+
+def _ptr(t):
+    """Device pointer of a torch tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if hasattr(t, "data_ptr"):
+        if not t.is_contiguous():
+            raise ValueError("tensor must be contiguous")
+        return C.c_void_p(t.data_ptr())
+    return C.c_void_p(int(t))
+
+
+def _stream(stream):
+    if stream is None:
+        try:
+            import torch
+            if torch.cuda.is_available():
+                return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+        except Exception:
+            pass
+        return None
+    if hasattr(stream, "cuda_stream"):
+        return C.c_void_p(stream.cuda_stream)
+    return C.c_void_p(int(stream))
+
+
+# ---------------------------------------------------------------------------
+# kernel-level entry points (torch tensors on the HIP device; bf16 tensors may
+# be torch.bfloat16 or int16/uint16 views of the bit patterns)
+# ---------------------------------------------------------------------------
+def mxfp4_dequant(codes, scales, out, stream=None):
+    _check(lib().neon_mxfp4_dequant(_ptr(codes), _ptr(scales), scales.numel(), _ptr(out),
+                                    _stream(stream)))
+
+
+def mxfp4_gemv(codes, scales, bias, x, y, N, K, B, stream=None):
+    _check(lib().neon_mxfp4_gemv(_ptr(codes), _ptr(scales), _ptr(bias), _ptr(x), _ptr(y),
+                                 N, K, B, _stream(stream)))
+
+
+def gemv_bf16(W, bias, x, y, N, K, B, stream=None):
+    _check(lib().neon_gemv_bf16(_ptr(W), _ptr(bias), _ptr(x), _ptr(y), N, K, B,
+                                _stream(stream)))
+
+
+def rmsnorm(x, w, out, B, H, eps=1e-5, stream=None):
+    _check(lib().neon_rmsnorm(_ptr(x), _ptr(w), _ptr(out), B, H, eps, _stream(stream)))
+
+
+def rope_yarn(x, pos, n_tok, n_heads, cfg: Config, stream=None):
+    _check(lib().neon_rope_yarn(_ptr(x), _ptr(pos), n_tok, n_heads, C.byref(cfg),
+                                _stream(stream)))
+
+
+def router_topk(x, W, b, idx, score, logits, B, E, H, k, stream=None):
+    _check(lib().neon_router_topk(_ptr(x), _ptr(W), _ptr(b), _ptr(idx), _ptr(score),
+                                  _ptr(logits), B, E, H, k, _stream(stream)))
+
+
+def moe_layer(x, router_w, router_b, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
+              dn_bias, residual, out, idx, score, B, E, H, I, k, alpha=1.702, limit=7.0,
+              stream=None):
+    _check(lib().neon_moe_layer(
+        _ptr(x), _ptr(router_w), _ptr(router_b), _ptr(gu_codes), _ptr(gu_scales),
+        _ptr(gu_bias), _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(residual),
+        _ptr(out), _ptr(idx), _ptr(score), B, E, H, I, k, alpha, limit, _stream(stream)))
+
+
+def moe_experts(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
+                residual, out, act, B, E, H, I, k, alpha=1.702, limit=7.0, stream=None):
+    _check(lib().neon_moe_experts(
+        _ptr(x), _ptr(idx), _ptr(score), _ptr(gu_codes), _ptr(gu_scales), _ptr(gu_bias),
+        _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(residual), _ptr(out), _ptr(act),
+        B, E, H, I, k, alpha, limit, _stream(stream)))
+
+
+def attn_decode(q, k_cache, v_cache, sinks, pos, out, B, Hq, Hkv, D, T_max, window,
+                stream=None):
+    _check(lib().neon_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(sinks),
+                                  _ptr(pos), _ptr(out), B, Hq, Hkv, D, T_max, window,
+                                  _stream(stream)))
+
+
+# ---------------------------------------------------------------------------
+# context-level API
+# ---------------------------------------------------------------------------
+class Engine:
+    """One model context on one device (weights, KV cache, captured step)."""
+
+    def __init__(self, cfg: Config | str = "gpt-oss-20b", device: int = 0, **overrides):
+        if isinstance(cfg, str):
+            cfg = config_preset(cfg, **overrides)
+        self.cfg = cfg
+        self._ctx = C.c_void_p()
+        _check(lib().neon_ctx_create(C.byref(cfg), device, C.byref(self._ctx)))
+        self.batch = 0
+
+    def close(self):
+        if self._ctx:
+            lib().neon_ctx_destroy(self._ctx)
+            self._ctx = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _chk(self, status):
+        _check(status, self._ctx)
+
+    def init_random(self, seed: int = 0, stream=None):
+        self._chk(lib().neon_init_random(self._ctx, seed, _stream(stream)))
+
+    def load_tensor(self, name: str, data: bytes | memoryview):
+        buf = (C.c_char * len(data)).from_buffer_copy(data)
+        self._chk(lib().neon_load_tensor(self._ctx, name.encode(), buf, len(data)))
+
+    def tensor_ptr(self, name: str):
+        p, n = C.c_void_p(), C.c_size_t()
+        self._chk(lib().neon_tensor_ptr(self._ctx, name.encode(), C.byref(p), C.byref(n)))
+        return p.value, n.value
+
+    def prefill(self, ids, stream=None):
+        """ids: nested list / array [batch][n_tokens] of int."""
+        import numpy as np
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        if a.ndim == 1:
+            a = a[None, :]
+        self._chk(lib().neon_prefill(self._ctx, a.ctypes.data_as(C.c_void_p), a.shape[0],
+                                     a.shape[1], _stream(stream)))
+        self.batch = a.shape[0]
+
+    def decode(self, n_steps: int, stream=None):
+        self._chk(lib().neon_decode(self._ctx, n_steps, _stream(stream)))
+
+    def seq_len(self) -> int:
+        n = C.c_int()
+        self._chk(lib().neon_seq_len(self._ctx, C.byref(n)))
+        return n.value
+
+    def read_tokens(self, start=0, count=None, stream=None):
+        import numpy as np
+        if count is None:
+            count = self.seq_len() - start
+        out = np.empty((self.batch, count), np.int32)
+        self._chk(lib().neon_read_tokens(self._ctx, start, count,
+                                         out.ctypes.data_as(C.c_void_p), _stream(stream)))
+        return out
+
+    def read_logits(self, stream=None):
+        import numpy as np
+        out = np.empty((self.batch, self.cfg.vocab), np.float32)
+        self._chk(lib().neon_read_logits(self._ctx, out.ctypes.data_as(C.c_void_p),
+                                         _stream(stream)))
+        return out

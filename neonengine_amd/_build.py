@@ -1,0 +1,69 @@
+"""Builds libneon_gptoss.so in-tree with hipcc for gfx950.
+
+Run as ``python -m neonengine_amd._build`` or through __graft_entry__.build().
+The shared library is placed next to this file so it travels with the tree.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB = os.path.join(HERE, "libneon_gptoss.so")
+SOURCES = ["neon_kernels.hip", "neon_engine.hip"]
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # no packed-fp32 instructions: some of their forms have given silent wrong
+    # results on this hardware pool
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the gfx950 kernels)")
+
+
+def build(verbose: bool = False) -> str:
+    objs = []
+    tmp_dir = os.path.join(HERE, "_build")
+    os.makedirs(tmp_dir, exist_ok=True)
+    procs = []
+    for src in SOURCES:
+        obj = os.path.join(tmp_dir, src.replace(".hip", ".o"))
+        cmd = [hipcc()] + [f for f in HIPCC_FLAGS if f != "-shared"] + [
+            "-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, src), "-o", obj]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+        objs.append(obj)
+    for cmd, p in procs:
+        out, _ = p.communicate()
+        text = "\n".join(l for l in out.decode(errors="replace").splitlines()
+                         if "packed-fp32-ops" not in l)
+        if verbose and text.strip():
+            print(text)
+        if p.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({p.returncode}): {' '.join(cmd)}\n{text}")
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout.decode(errors='replace')}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,868 @@
+// neon_engine.hip -- the C-ABI (include/neon_gptoss.h): argument validation,
+// the model context (weights, KV cache, activations in HBM), deterministic
+// init, checkpoint-tensor loading, and the decode step, captured once into a
+// hipGraph and replayed per token.
+//
+// Shape of the boundary: a context object created once (like the reference's
+// System constructors, NeonEngine/src/water_physics.cpp:23-123) and per-step
+// calls that enqueue a fixed kernel chain on the caller's stream (like
+// WaterPhysics::RunSimulation recording its dispatch chain,
+// NeonEngine/src/water_physics.cpp:131,165-436).  No exception crosses the
+// ABI; failures come back as neon_status with text in neon_last_error.
+#include "../../include/neon_gptoss.h"
+#include "neon_common.hpp"
+#include "neon_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+using namespace neon;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+struct LayerW {
+  uint16_t *attn_norm, *wqkv, *bqkv, *wo, *bo, *sinks, *mlp_norm, *router_w,
+      *router_b, *gu_bias, *dn_bias;
+  uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
+};
+
+enum {
+  K_ATTN_NORM = 0, K_WQKV = 1, K_BQKV = 2, K_WO = 3, K_BO = 4, K_SINKS = 5,
+  K_MLP_NORM = 6, K_ROUTER_W = 7, K_ROUTER_B = 8, K_GU_CODES = 9,
+  K_GU_SCALES = 10, K_GU_BIAS = 11, K_DN_CODES = 12, K_DN_SCALES = 13,
+  K_DN_BIAS = 14, K_EMBED = 100, K_LM_HEAD = 101, K_FINAL_NORM = 102
+};
+
+struct Tensor {
+  void* ptr;
+  size_t bytes;
+};
+
+}  // namespace
+
+struct neon_ctx {
+  neon_config cfg{};
+  int device = 0;
+  std::string err;
+  // weights
+  char* arena = nullptr;
+  size_t arena_bytes = 0;
+  std::vector<LayerW> layers;
+  uint16_t *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
+  // rope
+  float *cos_t = nullptr, *sin_t = nullptr, *inv_freq = nullptr;
+  // KV cache [L][max_batch][Hkv][max_seq][D]
+  uint16_t *kc = nullptr, *vc = nullptr;
+  size_t kv_layer_elems = 0;
+  // activations / scratch
+  char* work = nullptr;
+  uint16_t *h = nullptr, *xn = nullptr, *qkv = nullptr, *attn_out = nullptr,
+           *act = nullptr;
+  int32_t* moe_idx = nullptr;
+  float* moe_score = nullptr;
+  float *part_o = nullptr, *part_ml = nullptr;
+  int32_t* attn_cnt = nullptr;
+  float* logits = nullptr;
+  float* lm_part_val = nullptr;
+  int32_t* lm_part_idx = nullptr;
+  int32_t *tokens = nullptr, *pos = nullptr, *prompt_len = nullptr,
+          *last_ids = nullptr;
+  int tok_stride = 0;
+  int lm_nblk = 0;
+  int s_full = 1, s_slide = 1;
+  // sequence state (host mirror)
+  int batch = 0;
+  int host_pos = 0;
+  bool weights_ready = false;
+  // captured decode step
+  hipStream_t cap_stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  int graph_batch = 0;
+};
+
+#define FAIL(ctx, code, ...)                                     \
+  do {                                                           \
+    char _b[512];                                                \
+    snprintf(_b, sizeof(_b), __VA_ARGS__);                       \
+    (ctx)->err = _b;                                             \
+    return (code);                                               \
+  } while (0)
+
+#define HIPCHK(ctx, call)                                                   \
+  do {                                                                      \
+    hipError_t _e = (call);                                                 \
+    if (_e != hipSuccess)                                                   \
+      FAIL(ctx, NEON_EHIP, "%s failed: %s", #call, hipGetErrorString(_e)); \
+  } while (0)
+
+static hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------
+// configuration
+// ---------------------------------------------------------------------------
+extern "C" neon_status neon_config_preset(const char* name, neon_config* out) {
+  if (!name || !out) return NEON_EINVAL;
+  neon_config c{};
+  // gpt-oss-20b shape (HF configuration_gpt_oss.py defaults, 24 layers, 32
+  // experts); the 120b shape has 36 layers and 128 experts.
+  c.n_layers = 24; c.hidden = 2880; c.n_heads = 64; c.n_kv_heads = 8;
+  c.head_dim = 64; c.n_experts = 32; c.top_k = 4; c.intermediate = 2880;
+  c.vocab = 201088; c.sliding_window = 128; c.max_seq = 4096; c.max_batch = 1;
+  c.rope_theta = 150000.0f; c.rope_factor = 32.0f; c.rope_beta_fast = 32.0f;
+  c.rope_beta_slow = 1.0f; c.rope_orig_max_pos = 4096; c.rms_eps = 1e-5f;
+  c.swiglu_limit = 7.0f; c.swiglu_alpha = 1.702f;
+  if (strcmp(name, "gpt-oss-20b") == 0) {
+  } else if (strcmp(name, "gpt-oss-120b") == 0) {
+    c.n_layers = 36; c.n_experts = 128;
+  } else {
+    return NEON_EINVAL;
+  }
+  *out = c;
+  return NEON_OK;
+}
+
+static const char* check_config(const neon_config* c) {
+  if (c->n_layers < 1 || c->n_layers > 1024) return "n_layers out of range";
+  if (c->head_dim != 64) return "head_dim must be 64";
+  if (c->hidden < 64 || c->hidden > 8192 || c->hidden % 64)
+    return "hidden must be a multiple of 64 in [64, 8192]";
+  if (c->intermediate < 64 || c->intermediate > 8192 || c->intermediate % 64)
+    return "intermediate must be a multiple of 64 in [64, 8192]";
+  if (c->n_kv_heads < 1 || c->n_heads < 1 || c->n_heads % c->n_kv_heads)
+    return "n_heads must be a multiple of n_kv_heads";
+  {
+    const int g = c->n_heads / c->n_kv_heads;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return "n_heads/n_kv_heads must be 1, 2, 4 or 8";
+  }
+  if ((int64_t)c->n_heads * c->head_dim > 8192) return "n_heads*head_dim must be <= 8192";
+  if (c->n_experts < 1 || c->n_experts > 256) return "n_experts must be in [1, 256]";
+  if (c->top_k < 1 || c->top_k > 16 || c->top_k > c->n_experts)
+    return "top_k must be in [1, min(16, n_experts)]";
+  if (c->vocab < 1) return "vocab must be positive";
+  if (c->sliding_window < 0) return "sliding_window must be >= 0";
+  if (c->max_seq < 1 || c->max_seq > (1 << 20)) return "max_seq out of range";
+  if (c->max_batch < 1 || c->max_batch > 256) return "max_batch must be in [1, 256]";
+  if (!(c->rms_eps > 0.0f)) return "rms_eps must be positive";
+  if (!(c->rope_theta > 1.0f) || !(c->rope_factor >= 1.0f)) return "bad rope parameters";
+  if (c->rope_orig_max_pos < 1) return "rope_orig_max_pos must be positive";
+  return nullptr;
+}
+
+// YaRN inverse frequencies and attention factor in fp64 (HF
+// modeling_rope_utils.py:429-483 with truncate=False as gpt-oss sets it).
+static void yarn_inv_freq(const neon_config* c, std::vector<float>& invf,
+                          double* af) {
+  const int dim = c->head_dim;
+  const double base = c->rope_theta, factor = c->rope_factor;
+  auto corr = [&](double nrot) {
+    return (dim * std::log(c->rope_orig_max_pos / (nrot * 2.0 * M_PI))) /
+           (2.0 * std::log(base));
+  };
+  double low = corr(c->rope_beta_fast), high = corr(c->rope_beta_slow);
+  if (low < 0) low = 0;
+  if (high > dim - 1) high = dim - 1;
+  if (low == high) high += 0.001;
+  invf.resize(dim / 2);
+  for (int i = 0; i < dim / 2; ++i) {
+    const double pf = std::pow(base, (2.0 * i) / dim);
+    const double extra = 1.0 / pf, inter = 1.0 / (factor * pf);
+    double ramp = (i - low) / (high - low);
+    ramp = ramp < 0 ? 0 : (ramp > 1 ? 1 : ramp);
+    const double ef = 1.0 - ramp;
+    invf[i] = (float)(inter * (1.0 - ef) + extra * ef);
+  }
+  *af = factor <= 1.0 ? 1.0 : 0.1 * std::log(factor) + 1.0;
+}
+
+// ---------------------------------------------------------------------------
+// context lifetime
+// ---------------------------------------------------------------------------
+namespace {
+struct Sizes {
+  size_t qkv_rows, embed, wqkv, wo, gu_codes, gu_scales, dn_codes, dn_scales;
+};
+Sizes sizes_of(const neon_config& c) {
+  Sizes s;
+  const size_t H = c.hidden, I = c.intermediate, E = c.n_experts;
+  s.qkv_rows = (size_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+  s.embed = (size_t)c.vocab * H;
+  s.wqkv = s.qkv_rows * H;
+  s.wo = H * (size_t)c.n_heads * c.head_dim;
+  s.gu_codes = E * 2 * I * (H / 2);
+  s.gu_scales = E * 2 * I * (H / 32);
+  s.dn_codes = E * H * (I / 2);
+  s.dn_scales = E * H * (I / 32);
+  return s;
+}
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+}  // namespace
+
+extern "C" void neon_ctx_destroy(neon_ctx* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->graph_exec) (void)hipGraphExecDestroy(ctx->graph_exec);
+  if (ctx->graph) (void)hipGraphDestroy(ctx->graph);
+  if (ctx->cap_stream) (void)hipStreamDestroy(ctx->cap_stream);
+  if (ctx->arena) (void)hipFree(ctx->arena);
+  if (ctx->kc) (void)hipFree(ctx->kc);
+  if (ctx->vc) (void)hipFree(ctx->vc);
+  if (ctx->work) (void)hipFree(ctx->work);
+  delete ctx;
+}
+
+extern "C" const char* neon_last_error(const neon_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : g_create_error.c_str();
+}
+
+static neon_status ctx_alloc(neon_ctx* ctx) {
+  const neon_config& c = ctx->cfg;
+  const Sizes sz = sizes_of(c);
+  const size_t H = c.hidden, E = c.n_experts, I = c.intermediate, L = c.n_layers;
+  // ---- weights arena ----
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+  struct LOff { size_t v[15]; };
+  std::vector<LOff> lo(L);
+  const size_t o_embed = take(sz.embed * 2), o_lm = take(sz.embed * 2),
+               o_fn = take(H * 2);
+  for (size_t l = 0; l < L; ++l) {
+    lo[l].v[K_ATTN_NORM] = take(H * 2);
+    lo[l].v[K_WQKV] = take(sz.wqkv * 2);
+    lo[l].v[K_BQKV] = take(sz.qkv_rows * 2);
+    lo[l].v[K_WO] = take(sz.wo * 2);
+    lo[l].v[K_BO] = take(H * 2);
+    lo[l].v[K_SINKS] = take((size_t)c.n_heads * 2);
+    lo[l].v[K_MLP_NORM] = take(H * 2);
+    lo[l].v[K_ROUTER_W] = take(E * H * 2);
+    lo[l].v[K_ROUTER_B] = take(E * 2);
+    lo[l].v[K_GU_CODES] = take(sz.gu_codes);
+    lo[l].v[K_GU_SCALES] = take(sz.gu_scales);
+    lo[l].v[K_GU_BIAS] = take(E * 2 * I * 2);
+    lo[l].v[K_DN_CODES] = take(sz.dn_codes);
+    lo[l].v[K_DN_SCALES] = take(sz.dn_scales);
+    lo[l].v[K_DN_BIAS] = take(E * H * 2);
+  }
+  ctx->arena_bytes = off;
+  if (hipMalloc(&ctx->arena, off) != hipSuccess) {
+    ctx->arena = nullptr;
+    FAIL(ctx, NEON_ENOMEM, "hipMalloc of %zu weight bytes failed", off);
+  }
+  char* A = ctx->arena;
+  ctx->embed = (uint16_t*)(A + o_embed);
+  ctx->lm_head = (uint16_t*)(A + o_lm);
+  ctx->final_norm = (uint16_t*)(A + o_fn);
+  ctx->layers.resize(L);
+  for (size_t l = 0; l < L; ++l) {
+    LayerW& w = ctx->layers[l];
+    w.attn_norm = (uint16_t*)(A + lo[l].v[K_ATTN_NORM]);
+    w.wqkv = (uint16_t*)(A + lo[l].v[K_WQKV]);
+    w.bqkv = (uint16_t*)(A + lo[l].v[K_BQKV]);
+    w.wo = (uint16_t*)(A + lo[l].v[K_WO]);
+    w.bo = (uint16_t*)(A + lo[l].v[K_BO]);
+    w.sinks = (uint16_t*)(A + lo[l].v[K_SINKS]);
+    w.mlp_norm = (uint16_t*)(A + lo[l].v[K_MLP_NORM]);
+    w.router_w = (uint16_t*)(A + lo[l].v[K_ROUTER_W]);
+    w.router_b = (uint16_t*)(A + lo[l].v[K_ROUTER_B]);
+    w.gu_codes = (uint8_t*)(A + lo[l].v[K_GU_CODES]);
+    w.gu_scales = (uint8_t*)(A + lo[l].v[K_GU_SCALES]);
+    w.gu_bias = (uint16_t*)(A + lo[l].v[K_GU_BIAS]);
+    w.dn_codes = (uint8_t*)(A + lo[l].v[K_DN_CODES]);
+    w.dn_scales = (uint8_t*)(A + lo[l].v[K_DN_SCALES]);
+    w.dn_bias = (uint16_t*)(A + lo[l].v[K_DN_BIAS]);
+  }
+  // ---- KV cache ----
+  ctx->kv_layer_elems = (size_t)c.max_batch * c.n_kv_heads * c.max_seq * c.head_dim;
+  const size_t kv_bytes = ctx->kv_layer_elems * L * 2;
+  if (hipMalloc(&ctx->kc, kv_bytes) != hipSuccess || hipMalloc(&ctx->vc, kv_bytes) != hipSuccess)
+    FAIL(ctx, NEON_ENOMEM, "hipMalloc of 2 x %zu KV-cache bytes failed", kv_bytes);
+  HIPCHK(ctx, hipMemset(ctx->kc, 0, kv_bytes));
+  HIPCHK(ctx, hipMemset(ctx->vc, 0, kv_bytes));
+  // ---- activations / scratch ----
+  const size_t Bm = c.max_batch, half = c.head_dim / 2;
+  ctx->s_slide = c.sliding_window > 0 ? std::max(1, std::min(8, (c.sliding_window + 63) / 64)) : 1;
+  ctx->s_full = std::max(1, std::min(32, (c.max_seq + 63) / 64));
+  const int smax = std::max(ctx->s_full, ctx->s_slide);
+  const int G = c.n_heads / c.n_kv_heads;
+  ctx->lm_nblk = gemv_default_grid(c.vocab, 4);
+  ctx->tok_stride = c.max_seq + 1;
+  off = 0;
+  const size_t o_h = take(Bm * H * 2), o_xn = take(Bm * H * 2),
+               o_qkv = take(Bm * sz.qkv_rows * 2),
+               o_ao = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
+               o_act = take(Bm * c.top_k * I * 2),
+               o_idx = take(Bm * c.top_k * 4), o_sc = take(Bm * c.top_k * 4),
+               o_po = take(Bm * c.n_kv_heads * smax * (size_t)G * c.head_dim * 4),
+               o_pml = take(Bm * c.n_kv_heads * smax * (size_t)G * 2 * 4),
+               o_cnt = take(Bm * c.n_kv_heads * 4),
+               o_lg = take(Bm * (size_t)c.vocab * 4),
+               o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
+               o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
+               o_pl = take(Bm * 4), o_last = take(Bm * 4),
+               o_cos = take((size_t)c.max_seq * half * 4),
+               o_sin = take((size_t)c.max_seq * half * 4), o_if = take(half * 4);
+  if (hipMalloc(&ctx->work, off) != hipSuccess) {
+    ctx->work = nullptr;
+    FAIL(ctx, NEON_ENOMEM, "hipMalloc of %zu scratch bytes failed", off);
+  }
+  HIPCHK(ctx, hipMemset(ctx->work, 0, off));
+  char* W = ctx->work;
+  ctx->h = (uint16_t*)(W + o_h); ctx->xn = (uint16_t*)(W + o_xn);
+  ctx->qkv = (uint16_t*)(W + o_qkv); ctx->attn_out = (uint16_t*)(W + o_ao);
+  ctx->act = (uint16_t*)(W + o_act); ctx->moe_idx = (int32_t*)(W + o_idx);
+  ctx->moe_score = (float*)(W + o_sc); ctx->part_o = (float*)(W + o_po);
+  ctx->part_ml = (float*)(W + o_pml); ctx->attn_cnt = (int32_t*)(W + o_cnt);
+  ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
+  ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
+  ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
+  ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
+  ctx->sin_t = (float*)(W + o_sin); ctx->inv_freq = (float*)(W + o_if);
+  // ---- RoPE table ----
+  std::vector<float> invf;
+  double af;
+  yarn_inv_freq(&c, invf, &af);
+  HIPCHK(ctx, hipMemcpy(ctx->inv_freq, invf.data(), half * 4, hipMemcpyHostToDevice));
+  launch_rope_table(ctx->inv_freq, (float)af, c.max_seq, (int)half, ctx->cos_t,
+                    ctx->sin_t, nullptr);
+  HIPCHK(ctx, hipGetLastError());
+  HIPCHK(ctx, hipDeviceSynchronize());
+  HIPCHK(ctx, hipStreamCreateWithFlags(&ctx->cap_stream, hipStreamNonBlocking));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_ctx_create(const neon_config* cfg, int device,
+                                       neon_ctx** out) {
+  g_create_error.clear();
+  if (!cfg || !out) {
+    g_create_error = "neon_ctx_create: null argument";
+    return NEON_EINVAL;
+  }
+  *out = nullptr;
+  if (const char* why = check_config(cfg)) {
+    g_create_error = std::string("neon_ctx_create: ") + why;
+    return NEON_EINVAL;
+  }
+  int ndev = 0;
+  hipError_t e = hipGetDeviceCount(&ndev);
+  if (e != hipSuccess || ndev < 1) {
+    g_create_error = std::string("neon_ctx_create: no HIP device (") +
+                     hipGetErrorString(e) + ")";
+    return NEON_EHIP;
+  }
+  if (device < 0 || device >= ndev) {
+    g_create_error = "neon_ctx_create: device index out of range";
+    return NEON_EINVAL;
+  }
+  if (hipSetDevice(device) != hipSuccess) {
+    g_create_error = "neon_ctx_create: hipSetDevice failed";
+    return NEON_EHIP;
+  }
+  neon_ctx* ctx = new (std::nothrow) neon_ctx();
+  if (!ctx) return NEON_ENOMEM;
+  ctx->cfg = *cfg;
+  ctx->device = device;
+  neon_status st = ctx_alloc(ctx);
+  if (st != NEON_OK) {
+    g_create_error = "neon_ctx_create: " + ctx->err;
+    neon_ctx_destroy(ctx);
+    return st;
+  }
+  *out = ctx;
+  return NEON_OK;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+// ---------------------------------------------------------------------------
+extern "C" neon_status neon_init_random(neon_ctx* ctx, uint64_t seed,
+                                        void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  const neon_config& c = ctx->cfg;
+  const Sizes sz = sizes_of(c);
+  const size_t H = c.hidden, E = c.n_experts, I = c.intermediate;
+  hipStream_t st = S(stream);
+  // std of the Irwin-Hall integer (sum of four 16-bit uniforms)
+  const double unit = std::sqrt((65536.0 * 65536.0 - 1.0) / 3.0);
+  auto mul = [&](double std) { return (float)(std / unit); };
+  auto bf = [&](uint16_t* p, size_t n, int layer, int kind, float mean, double std) {
+    launch_fill_bf16(p, (int64_t)n, seed, stream_id(layer, kind), mean, mul(std), st);
+  };
+  bf(ctx->embed, sz.embed, -1, K_EMBED, 0.0f, 0.02);
+  bf(ctx->lm_head, sz.embed, -1, K_LM_HEAD, 0.0f, 0.02);
+  bf(ctx->final_norm, H, -1, K_FINAL_NORM, 1.0f, 0.05);
+  for (int l = 0; l < c.n_layers; ++l) {
+    LayerW& w = ctx->layers[l];
+    bf(w.attn_norm, H, l, K_ATTN_NORM, 1.0f, 0.05);
+    bf(w.wqkv, sz.wqkv, l, K_WQKV, 0.0f, 0.02);
+    bf(w.bqkv, sz.qkv_rows, l, K_BQKV, 0.0f, 0.02);
+    bf(w.wo, sz.wo, l, K_WO, 0.0f, 0.02);
+    bf(w.bo, H, l, K_BO, 0.0f, 0.02);
+    bf(w.sinks, c.n_heads, l, K_SINKS, 0.0f, 1.0);
+    bf(w.mlp_norm, H, l, K_MLP_NORM, 1.0f, 0.05);
+    bf(w.router_w, E * H, l, K_ROUTER_W, 0.0f, 0.02);
+    bf(w.router_b, E, l, K_ROUTER_B, 0.0f, 0.02);
+    bf(w.gu_bias, E * 2 * I, l, K_GU_BIAS, 0.0f, 0.02);
+    bf(w.dn_bias, E * H, l, K_DN_BIAS, 0.0f, 0.02);
+    launch_fill_bytes(w.gu_codes, (int64_t)sz.gu_codes, seed, stream_id(l, K_GU_CODES), st);
+    launch_fill_scales(w.gu_scales, (int64_t)sz.gu_scales, seed, stream_id(l, K_GU_SCALES), 119, 6, st);
+    launch_fill_bytes(w.dn_codes, (int64_t)sz.dn_codes, seed, stream_id(l, K_DN_CODES), st);
+    launch_fill_scales(w.dn_scales, (int64_t)sz.dn_scales, seed, stream_id(l, K_DN_SCALES), 119, 6, st);
+  }
+  HIPCHK(ctx, hipGetLastError());
+  ctx->weights_ready = true;
+  return NEON_OK;
+}
+
+// Resolve a gpt-oss checkpoint tensor name to (device pointer, bytes, is
+// MXFP4 scale tensor, row offset inside a fused tensor).
+static neon_status resolve(neon_ctx* ctx, const char* name, Tensor* t,
+                           bool* is_scale) {
+  const neon_config& c = ctx->cfg;
+  const Sizes sz = sizes_of(c);
+  const size_t H = c.hidden, E = c.n_experts, I = c.intermediate, D = c.head_dim;
+  const size_t q_rows = (size_t)c.n_heads * D, kv_rows = (size_t)c.n_kv_heads * D;
+  *is_scale = false;
+  std::string n(name);
+  if (n == "model.embed_tokens.weight") { *t = {ctx->embed, sz.embed * 2}; return NEON_OK; }
+  if (n == "lm_head.weight") { *t = {ctx->lm_head, sz.embed * 2}; return NEON_OK; }
+  if (n == "model.norm.weight") { *t = {ctx->final_norm, H * 2}; return NEON_OK; }
+  int layer = -1, used = 0;
+  if (sscanf(name, "model.layers.%d.%n", &layer, &used) != 1 || used == 0 ||
+      layer < 0 || layer >= c.n_layers)
+    FAIL(ctx, NEON_EINVAL, "unknown tensor name '%s'", name);
+  const std::string r = n.substr(used);
+  LayerW& w = ctx->layers[layer];
+  if (r == "input_layernorm.weight") *t = {w.attn_norm, H * 2};
+  else if (r == "post_attention_layernorm.weight") *t = {w.mlp_norm, H * 2};
+  else if (r == "self_attn.q_proj.weight") *t = {w.wqkv, q_rows * H * 2};
+  else if (r == "self_attn.k_proj.weight") *t = {w.wqkv + q_rows * H, kv_rows * H * 2};
+  else if (r == "self_attn.v_proj.weight") *t = {w.wqkv + (q_rows + kv_rows) * H, kv_rows * H * 2};
+  else if (r == "self_attn.q_proj.bias") *t = {w.bqkv, q_rows * 2};
+  else if (r == "self_attn.k_proj.bias") *t = {w.bqkv + q_rows, kv_rows * 2};
+  else if (r == "self_attn.v_proj.bias") *t = {w.bqkv + q_rows + kv_rows, kv_rows * 2};
+  else if (r == "self_attn.o_proj.weight") *t = {w.wo, sz.wo * 2};
+  else if (r == "self_attn.o_proj.bias") *t = {w.bo, H * 2};
+  else if (r == "self_attn.sinks") *t = {w.sinks, (size_t)c.n_heads * 2};
+  else if (r == "mlp.router.weight") *t = {w.router_w, E * H * 2};
+  else if (r == "mlp.router.bias") *t = {w.router_b, E * 2};
+  else if (r == "mlp.experts.gate_up_proj_blocks") *t = {w.gu_codes, sz.gu_codes};
+  else if (r == "mlp.experts.gate_up_proj_scales") { *t = {w.gu_scales, sz.gu_scales}; *is_scale = true; }
+  else if (r == "mlp.experts.gate_up_proj_bias") *t = {w.gu_bias, E * 2 * I * 2};
+  else if (r == "mlp.experts.down_proj_blocks") *t = {w.dn_codes, sz.dn_codes};
+  else if (r == "mlp.experts.down_proj_scales") { *t = {w.dn_scales, sz.dn_scales}; *is_scale = true; }
+  else if (r == "mlp.experts.down_proj_bias") *t = {w.dn_bias, E * H * 2};
+  else FAIL(ctx, NEON_EINVAL, "unknown tensor name '%s'", name);
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
+                                        const void* host_data, size_t bytes) {
+  if (!ctx) return NEON_EINVAL;
+  if (!name || !host_data) FAIL(ctx, NEON_EINVAL, "neon_load_tensor: null argument");
+  Tensor t;
+  bool is_scale;
+  neon_status st = resolve(ctx, name, &t, &is_scale);
+  if (st != NEON_OK) return st;
+  if (bytes != t.bytes)
+    FAIL(ctx, NEON_EINVAL, "tensor '%s': %zu bytes given, %zu expected", name, bytes, t.bytes);
+  if (is_scale) {
+    const uint8_t* s = (const uint8_t*)host_data;
+    for (size_t i = 0; i < bytes; ++i)
+      if (s[i] == 0xFF)
+        FAIL(ctx, NEON_ENAN_SCALE, "tensor '%s': E8M0 scale 0xFF (NaN) at byte %zu", name, i);
+  }
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipMemcpy(t.ptr, host_data, bytes, hipMemcpyHostToDevice));
+  ctx->weights_ready = true;
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name,
+                                       void** ptr, size_t* bytes) {
+  if (!ctx) return NEON_EINVAL;
+  if (!name || !ptr) FAIL(ctx, NEON_EINVAL, "neon_tensor_ptr: null argument");
+  Tensor t;
+  bool is_scale;
+  neon_status st = resolve(ctx, name, &t, &is_scale);
+  if (st != NEON_OK) return st;
+  *ptr = t.ptr;
+  if (bytes) *bytes = t.bytes;
+  return NEON_OK;
+}
+
+// ---------------------------------------------------------------------------
+// the decode step: 1 + 6 L + 2 kernels, all reading positions from device
+// memory so one captured graph serves every step.
+// ---------------------------------------------------------------------------
+static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
+  const neon_config& c = ctx->cfg;
+  const int H = c.hidden, D = c.head_dim;
+  const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * D;
+  launch_embed(ctx->tokens, ctx->tok_stride, ctx->pos, ctx->embed, ctx->h, H, B, st);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = ctx->layers[l];
+    const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
+    GemvArgs q;
+    q.mode = 0; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
+    q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B; q.rpw = 4;
+    q.nblk = gemv_default_grid(q.N, q.rpw);
+    launch_gemv_bf16(q, st);
+    AttnArgs a;
+    a.q_src = ctx->qkv; a.kc = ctx->kc + (size_t)l * ctx->kv_layer_elems;
+    a.vc = ctx->vc + (size_t)l * ctx->kv_layer_elems; a.sinks = w.sinks;
+    a.pos = ctx->pos; a.cos_t = ctx->cos_t; a.sin_t = ctx->sin_t;
+    a.out = ctx->attn_out; a.part_o = ctx->part_o; a.part_ml = ctx->part_ml;
+    a.counters = ctx->attn_cnt; a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
+    a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
+    a.S = sliding ? ctx->s_slide : ctx->s_full; a.fused = 1; a.q_stride = qkv_rows;
+    launch_attn(a, st);
+    GemvArgs o;
+    o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
+    o.N = H; o.K = c.n_heads * D; o.B = B; o.rpw = 2;
+    o.nblk = gemv_default_grid(o.N, o.rpw);
+    launch_gemv_bf16(o, st);
+    launch_router(ctx->h, w.mlp_norm, c.rms_eps, ctx->xn, w.router_w, w.router_b,
+                  ctx->moe_idx, ctx->moe_score, nullptr, B, c.n_experts, H,
+                  c.top_k, st);
+    MoeArgs m;
+    m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
+    m.dn_codes = w.dn_codes; m.dn_scales = w.dn_scales; m.dn_bias = w.dn_bias;
+    m.idx = ctx->moe_idx; m.score = ctx->moe_score; m.xn = ctx->xn; m.act = ctx->act;
+    m.residual = ctx->h; m.out = ctx->h; m.B = B; m.H = H; m.I = c.intermediate;
+    m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
+    launch_moe(m, st);
+  }
+  GemvArgs lm;
+  lm.mode = 2; lm.W = ctx->lm_head; lm.x = ctx->h; lm.norm_w = ctx->final_norm;
+  lm.eps = c.rms_eps; lm.logits = ctx->logits; lm.part_val = ctx->lm_part_val;
+  lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab; lm.K = H; lm.B = B; lm.rpw = 4;
+  lm.nblk = ctx->lm_nblk;
+  launch_gemv_bf16(lm, st);
+  launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, ctx->lm_nblk,
+                        ctx->tokens, ctx->tok_stride, ctx->pos, ctx->prompt_len,
+                        ctx->last_ids, B, st);
+}
+
+static neon_status ensure_graph(neon_ctx* ctx, int B) {
+  if (ctx->graph_exec && ctx->graph_batch == B) return NEON_OK;
+  if (ctx->graph_exec) { (void)hipGraphExecDestroy(ctx->graph_exec); ctx->graph_exec = nullptr; }
+  if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
+  HIPCHK(ctx, hipStreamBeginCapture(ctx->cap_stream, hipStreamCaptureModeThreadLocal));
+  enqueue_step(ctx, B, ctx->cap_stream);
+  hipError_t le = hipGetLastError();
+  hipGraph_t g = nullptr;
+  hipError_t ee = hipStreamEndCapture(ctx->cap_stream, &g);
+  if (le != hipSuccess || ee != hipSuccess) {
+    if (g) (void)hipGraphDestroy(g);
+    FAIL(ctx, NEON_EHIP, "graph capture failed: %s / %s", hipGetErrorString(le),
+         hipGetErrorString(ee));
+  }
+  ctx->graph = g;
+  HIPCHK(ctx, hipGraphInstantiate(&ctx->graph_exec, g, nullptr, nullptr, 0));
+  ctx->graph_batch = B;
+  return NEON_OK;
+}
+
+static neon_status run_steps(neon_ctx* ctx, int n, hipStream_t st) {
+  // NEON_EAGER=1 launches the kernels directly (debugging aid); the default
+  // replays the captured step graph.
+  static const bool eager = getenv("NEON_EAGER") && getenv("NEON_EAGER")[0] == '1';
+  if (eager) {
+    for (int i = 0; i < n; ++i) enqueue_step(ctx, ctx->batch, st);
+    HIPCHK(ctx, hipGetLastError());
+    return NEON_OK;
+  }
+  neon_status s = ensure_graph(ctx, ctx->batch);
+  if (s != NEON_OK) return s;
+  for (int i = 0; i < n; ++i) HIPCHK(ctx, hipGraphLaunch(ctx->graph_exec, st));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
+                                    int n_tokens, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  const neon_config& c = ctx->cfg;
+  if (!ids) FAIL(ctx, NEON_EINVAL, "neon_prefill: null ids");
+  if (batch < 1 || batch > c.max_batch)
+    FAIL(ctx, NEON_EINVAL, "neon_prefill: batch %d outside [1, %d]", batch, c.max_batch);
+  if (n_tokens < 1) FAIL(ctx, NEON_EINVAL, "neon_prefill: n_tokens must be >= 1");
+  if (n_tokens > c.max_seq)
+    FAIL(ctx, NEON_EKV_FULL, "neon_prefill: %d tokens exceed max_seq %d", n_tokens, c.max_seq);
+  for (int64_t i = 0; i < (int64_t)batch * n_tokens; ++i)
+    if (ids[i] < 0 || ids[i] >= c.vocab)
+      FAIL(ctx, NEON_ERANGE_TOKEN, "neon_prefill: token id %d at %lld outside [0, %d)",
+           ids[i], (long long)i, c.vocab);
+  if (!ctx->weights_ready) FAIL(ctx, NEON_ESTATE, "neon_prefill: no weights loaded");
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  hipStream_t st = S(stream);
+  std::vector<int32_t> tok((size_t)batch * ctx->tok_stride, 0);
+  for (int b = 0; b < batch; ++b)
+    memcpy(&tok[(size_t)b * ctx->tok_stride], ids + (size_t)b * n_tokens, n_tokens * 4);
+  std::vector<int32_t> zeros(batch, 0), plen(batch, n_tokens);
+  HIPCHK(ctx, hipMemcpyAsync(ctx->tokens, tok.data(), tok.size() * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->pos, zeros.data(), batch * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->prompt_len, plen.data(), batch * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipStreamSynchronize(st));  // host staging buffers die here
+  ctx->batch = batch;
+  ctx->host_pos = 0;
+  neon_status s = run_steps(ctx, n_tokens, st);
+  if (s != NEON_OK) return s;
+  ctx->host_pos = n_tokens;
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_decode(neon_ctx* ctx, int n_steps, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (n_steps < 0) FAIL(ctx, NEON_EINVAL, "neon_decode: n_steps must be >= 0");
+  if (ctx->batch == 0) FAIL(ctx, NEON_ESTATE, "neon_decode: call neon_prefill first");
+  if ((int64_t)ctx->host_pos + n_steps > ctx->cfg.max_seq)
+    FAIL(ctx, NEON_EKV_FULL, "neon_decode: %d steps from position %d exceed max_seq %d",
+         n_steps, ctx->host_pos, ctx->cfg.max_seq);
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  neon_status s = run_steps(ctx, n_steps, S(stream));
+  if (s != NEON_OK) return s;
+  ctx->host_pos += n_steps;
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
+                                        int32_t* out, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (!out || start < 0 || count < 0 || start + count > ctx->host_pos + 1)
+    FAIL(ctx, NEON_EINVAL, "neon_read_tokens: range [%d, %d) outside [0, %d]", start,
+         start + count, ctx->host_pos + 1);
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipStreamSynchronize(S(stream)));
+  for (int b = 0; b < ctx->batch; ++b)
+    HIPCHK(ctx, hipMemcpy(out + (size_t)b * count,
+                          ctx->tokens + (size_t)b * ctx->tok_stride + start,
+                          (size_t)count * 4, hipMemcpyDeviceToHost));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (!out) FAIL(ctx, NEON_EINVAL, "neon_read_logits: null out");
+  if (ctx->batch == 0) FAIL(ctx, NEON_ESTATE, "neon_read_logits: no step has run");
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipStreamSynchronize(S(stream)));
+  HIPCHK(ctx, hipMemcpy(out, ctx->logits, (size_t)ctx->batch * ctx->cfg.vocab * 4,
+                        hipMemcpyDeviceToHost));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
+  if (!ctx || !out) return NEON_EINVAL;
+  *out = ctx->host_pos + (ctx->batch ? 1 : 0);
+  return NEON_OK;
+}
+
+// ---------------------------------------------------------------------------
+// kernel-level entry points: validate on the host, then launch.
+// ---------------------------------------------------------------------------
+#define KFAIL(code, ...)                          \
+  do {                                            \
+    char _b[512];                                 \
+    snprintf(_b, sizeof(_b), __VA_ARGS__);        \
+    g_create_error = _b;                          \
+    return (code);                                \
+  } while (0)
+
+#define KLAUNCHED()                                                         \
+  do {                                                                      \
+    hipError_t _e = hipGetLastError();                                      \
+    if (_e != hipSuccess) KFAIL(NEON_EHIP, "launch failed: %s", hipGetErrorString(_e)); \
+    return NEON_OK;                                                         \
+  } while (0)
+
+extern "C" neon_status neon_mxfp4_dequant(const uint8_t* codes,
+                                          const uint8_t* scales, int64_t n_blocks,
+                                          float* out, void* stream) {
+  if (!codes || !scales || !out) KFAIL(NEON_EINVAL, "neon_mxfp4_dequant: null pointer");
+  if (n_blocks < 0) KFAIL(NEON_EINVAL, "neon_mxfp4_dequant: n_blocks < 0");
+  if (n_blocks == 0) return NEON_OK;
+  launch_mxfp4_dequant(codes, scales, n_blocks, out, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                                       const uint16_t* bias, const uint16_t* x,
+                                       uint16_t* y, int N, int K, int B,
+                                       void* stream) {
+  if (!codes || !scales || !x || !y) KFAIL(NEON_EINVAL, "neon_mxfp4_gemv: null pointer");
+  if (N < 1 || B < 1 || B > 65535 || K < 32 || K % 32 || K > 8192)
+    KFAIL(NEON_EINVAL, "neon_mxfp4_gemv: bad shape N=%d K=%d B=%d", N, K, B);
+  launch_mxfp4_gemv(codes, scales, bias, x, y, N, K, B, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,
+                                      const uint16_t* x, uint16_t* y, int N, int K,
+                                      int B, void* stream) {
+  if (!W || !x || !y) KFAIL(NEON_EINVAL, "neon_gemv_bf16: null pointer");
+  if (N < 1 || B < 1 || B > 65535 || K < 8 || K % 8 || K > 8192)
+    KFAIL(NEON_EINVAL, "neon_gemv_bf16: bad shape N=%d K=%d B=%d", N, K, B);
+  GemvArgs a;
+  a.mode = 0; a.W = W; a.bias = bias; a.x = x; a.y = y; a.N = N; a.K = K; a.B = B;
+  a.rpw = 2; a.nblk = gemv_default_grid(N, a.rpw);
+  launch_gemv_bf16(a, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_rmsnorm(const uint16_t* x, const uint16_t* w,
+                                    uint16_t* out, int B, int H, float eps,
+                                    void* stream) {
+  if (!x || !w || !out) KFAIL(NEON_EINVAL, "neon_rmsnorm: null pointer");
+  if (B < 1 || H < 8 || H % 8 || H > 8192 || !(eps > 0.0f))
+    KFAIL(NEON_EINVAL, "neon_rmsnorm: bad shape B=%d H=%d eps=%g", B, H, eps);
+  launch_rmsnorm(x, w, out, B, H, eps, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok,
+                                      int n_heads, const neon_config* cfg,
+                                      void* stream) {
+  if (!x || !pos || !cfg) KFAIL(NEON_EINVAL, "neon_rope_yarn: null pointer");
+  if (n_tok < 1 || n_heads < 1 || cfg->head_dim < 2 || cfg->head_dim % 2 ||
+      cfg->head_dim > 512 || cfg->max_seq < 1 || !(cfg->rope_theta > 1.0f) ||
+      !(cfg->rope_factor >= 1.0f) || cfg->rope_orig_max_pos < 1)
+    KFAIL(NEON_EINVAL, "neon_rope_yarn: bad shape or rope parameters");
+  // Positions must lie in [0, cfg->max_seq); the table is built for that range.
+  std::vector<float> invf;
+  double af;
+  yarn_inv_freq(cfg, invf, &af);
+  const int half = cfg->head_dim / 2;
+  float *tab = nullptr;
+  const size_t tb = ((size_t)cfg->max_seq * half * 2 + half) * 4;
+  if (hipMallocAsync((void**)&tab, tb, S(stream)) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_rope_yarn: table allocation failed");
+  float* ct = tab;
+  float* stt = tab + (size_t)cfg->max_seq * half;
+  float* dinv = stt + (size_t)cfg->max_seq * half;
+  if (hipMemcpyAsync(dinv, invf.data(), half * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_rope_yarn: copy failed");
+  launch_rope_table(dinv, (float)af, cfg->max_seq, half, ct, stt, S(stream));
+  launch_rope_apply(x, pos, ct, stt, n_tok, n_heads, cfg->head_dim, S(stream));
+  if (hipStreamSynchronize(S(stream)) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_rope_yarn: synchronize failed");
+  (void)hipFreeAsync(tab, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
+                                        const uint16_t* b, int32_t* idx,
+                                        float* score, float* logits, int B, int E,
+                                        int H, int k, void* stream) {
+  if (!x || !W || !b || !idx || !score) KFAIL(NEON_EINVAL, "neon_router_topk: null pointer");
+  if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < 8 ||
+      H % 8 || H > 8192)
+    KFAIL(NEON_EINVAL, "neon_router_topk: bad shape B=%d E=%d H=%d k=%d", B, E, H, k);
+  launch_router(x, nullptr, 0.0f, nullptr, W, b, idx, score, logits, B, E, H, k, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_moe_layer(
+    const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
+    const uint8_t* gu_codes, const uint8_t* gu_scales, const uint16_t* gu_bias,
+    const uint8_t* dn_codes, const uint8_t* dn_scales, const uint16_t* dn_bias,
+    const uint16_t* residual, uint16_t* out, int32_t* idx, float* score, int B,
+    int E, int H, int I, int k, float alpha, float limit, void* stream) {
+  if (!x || !router_w || !router_b || !gu_codes || !gu_scales || !gu_bias ||
+      !dn_codes || !dn_scales || !dn_bias || !out)
+    KFAIL(NEON_EINVAL, "neon_moe_layer: null pointer");
+  if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E ||
+      H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
+    KFAIL(NEON_EINVAL, "neon_moe_layer: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
+  hipStream_t st = S(stream);
+  // scratch: act [B][k][I] bf16, then idx [B][k] and score [B][k] for the
+  // outputs the caller did not ask for
+  const size_t act_b = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
+  const size_t ib = ((size_t)B * k * 4 + 255) & ~(size_t)255;
+  char* scratch = nullptr;
+  if (hipMallocAsync((void**)&scratch, act_b + 2 * ib, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_moe_layer: scratch allocation failed");
+  uint16_t* act = (uint16_t*)scratch;
+  int32_t* d_idx = idx ? idx : (int32_t*)(scratch + act_b);
+  float* d_sc = score ? score : (float*)(scratch + act_b + ib);
+  launch_router(x, nullptr, 0.0f, nullptr, router_w, router_b, d_idx, d_sc, nullptr,
+                B, E, H, k, st);
+  MoeArgs m;
+  m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
+  m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
+  m.idx = d_idx; m.score = d_sc; m.xn = x; m.act = act; m.residual = residual;
+  m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
+  launch_moe(m, st);
+  hipError_t e = hipGetLastError();
+  (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_moe_layer: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_moe_experts(
+    const uint16_t* x, const int32_t* idx, const float* score,
+    const uint8_t* gu_codes, const uint8_t* gu_scales, const uint16_t* gu_bias,
+    const uint8_t* dn_codes, const uint8_t* dn_scales, const uint16_t* dn_bias,
+    const uint16_t* residual, uint16_t* out, uint16_t* act, int B, int E, int H,
+    int I, int k, float alpha, float limit, void* stream) {
+  if (!x || !idx || !score || !gu_codes || !gu_scales || !gu_bias || !dn_codes ||
+      !dn_scales || !dn_bias || !out || !act)
+    KFAIL(NEON_EINVAL, "neon_moe_experts: null pointer");
+  if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E ||
+      H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
+    KFAIL(NEON_EINVAL, "neon_moe_experts: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
+  // idx is device data: every entry must lie in [0, E).
+  MoeArgs m;
+  m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
+  m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
+  m.idx = idx; m.score = score; m.xn = x; m.act = act; m.residual = residual;
+  m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
+  launch_moe(m, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
+                                        const uint16_t* v_cache,
+                                        const uint16_t* sinks, const int32_t* pos,
+                                        uint16_t* out, int B, int Hq, int Hkv, int D,
+                                        int T_max, int window, void* stream) {
+  if (!q || !k_cache || !v_cache || !sinks || !pos || !out)
+    KFAIL(NEON_EINVAL, "neon_attn_decode: null pointer");
+  if (D != 64 || B < 1 || B > 65535 || Hkv < 1 || Hq < Hkv || Hq % Hkv || T_max < 1 ||
+      window < 0)
+    KFAIL(NEON_EINVAL, "neon_attn_decode: bad shape");
+  const int G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    KFAIL(NEON_EINVAL, "neon_attn_decode: Hq/Hkv must be 1, 2, 4 or 8");
+  // pos[b] must lie in [0, T_max); it is device data, so the kernel trusts it.
+  hipStream_t st = S(stream);
+  const int span = window > 0 ? std::min(window, T_max) : T_max;
+  const int S_ = std::max(1, std::min(32, (span + 63) / 64));
+  char* scratch = nullptr;
+  const size_t po = (size_t)B * Hkv * S_ * G * 64 * 4, pml = (size_t)B * Hkv * S_ * G * 2 * 4,
+               cnt = (size_t)B * Hkv * 4;
+  if (hipMallocAsync((void**)&scratch, po + pml + cnt + 512, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
+  int32_t* counters = (int32_t*)(scratch + po + pml);
+  if (hipMemsetAsync(counters, 0, cnt, st) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_attn_decode: memset failed");
+  AttnArgs a;
+  a.q_src = q; a.kc = const_cast<uint16_t*>(k_cache); a.vc = const_cast<uint16_t*>(v_cache);
+  a.sinks = sinks; a.pos = pos; a.cos_t = nullptr; a.sin_t = nullptr; a.out = out;
+  a.part_o = (float*)scratch; a.part_ml = (float*)(scratch + po); a.counters = counters;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window; a.S = S_;
+  a.fused = 0; a.q_stride = Hq * D;
+  launch_attn(a, st);
+  hipError_t e = hipGetLastError();
+  (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
+}

@@ -1,0 +1,95 @@
+// neon_internal.hpp -- host launchers of the gfx950 kernels (library-
+// internal; the public surface is include/neon_gptoss.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace neon {
+
+// ---- init -----------------------------------------------------------------
+void launch_fill_bf16(uint16_t* out, int64_t n, uint64_t seed, uint64_t stream,
+                      float mean, float mul, hipStream_t st);
+void launch_fill_bytes(uint8_t* out, int64_t n, uint64_t seed, uint64_t stream,
+                       hipStream_t st);
+void launch_fill_scales(uint8_t* out, int64_t n, uint64_t seed,
+                        uint64_t stream, int lo, int range, hipStream_t st);
+
+// ---- MXFP4 ------------------------------------------------------------------
+void launch_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
+                          int64_t n_blocks, float* out, hipStream_t st);
+void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                       const uint16_t* bias, const uint16_t* x, uint16_t* y,
+                       int N, int K, int B, hipStream_t st);
+
+// ---- bf16 GEMV with fused prologue/epilogue ---------------------------------
+struct GemvArgs {
+  int mode = 0;  // 0 store, 1 residual add into y, 2 fp32 logits + argmax parts
+  const uint16_t* W = nullptr;
+  const uint16_t* bias = nullptr;
+  const uint16_t* x = nullptr;
+  const uint16_t* norm_w = nullptr;  // fused RMSNorm of x when not NULL
+  float eps = 1e-5f;
+  uint16_t* y = nullptr;
+  float* logits = nullptr;
+  float* part_val = nullptr;
+  int32_t* part_idx = nullptr;
+  int N = 0, K = 0, B = 1;
+  int rpw = 1;   // rows per wave group
+  int nblk = 1;  // grid.x
+};
+int gemv_default_grid(int N, int rpw);
+void launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
+
+void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
+                           int nparts, int32_t* tokens, int tok_stride,
+                           int32_t* pos, const int32_t* prompt_len,
+                           int32_t* last_ids, int B, hipStream_t st);
+void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
+                  const uint16_t* embed, uint16_t* h, int H, int B,
+                  hipStream_t st);
+void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
+                    int H, float eps, hipStream_t st);
+
+// ---- RoPE ---------------------------------------------------------------------
+void launch_rope_table(const float* inv_freq, float af, int n_pos, int half,
+                       float* cos_t, float* sin_t, hipStream_t st);
+void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
+                       const float* sin_t, int n_tok, int n_heads, int D,
+                       hipStream_t st);
+
+// ---- router / MoE --------------------------------------------------------------
+void launch_router(const uint16_t* x, const uint16_t* nw, float eps,
+                   uint16_t* xn_out, const uint16_t* W, const uint16_t* bias,
+                   int32_t* idx, float* score, float* logits_out, int B, int E,
+                   int H, int k, hipStream_t st);
+
+struct MoeArgs {
+  const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
+  const uint16_t *gu_bias, *dn_bias;
+  const int32_t* idx;
+  const float* score;
+  const uint16_t* xn;        // [B][H] normalised input
+  uint16_t* act;             // [B][k][I] scratch
+  const uint16_t* residual;  // may be NULL
+  uint16_t* out;             // [B][H]
+  int B, H, I, k;
+  float alpha, limit;
+};
+void launch_moe(const MoeArgs& a, hipStream_t st);
+
+// ---- attention ------------------------------------------------------------------
+struct AttnArgs {
+  const uint16_t* q_src;  // rotated q [B][Hq][D], or raw qkv rows when fused
+  uint16_t *kc, *vc;      // [B][Hkv][T_max][D]
+  const uint16_t* sinks;  // [Hq]
+  const int32_t* pos;     // [B]
+  const float *cos_t, *sin_t;
+  uint16_t* out;          // [B][Hq*D]
+  float *part_o, *part_ml;
+  int32_t* counters;      // [B][Hkv], zero between launches
+  int B, Hq, Hkv, T_max, window, S, fused, q_stride;
+};
+void launch_attn(const AttnArgs& a, hipStream_t st);
+
+}  // namespace neon

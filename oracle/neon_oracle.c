@@ -1,0 +1,647 @@
+/*
+ * neon_oracle.c -- CPU restatement of the gpt-oss token loop (test oracle).
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py, never by the product.  See neon_oracle.h for
+ * what pins each function.
+ *
+ * Build: oracle/Makefile (gcc -O3 -march=native -fopenmp -ffp-contract=off).
+ * -ffp-contract=off matters: the RNG's float step and the router's canonical
+ * fp32 reduction must round exactly like the device code.
+ *
+ * Semantic sources (third-party text, not the reference; the reference has no
+ * implementation of this path):
+ *   HFM = transformers/models/gpt_oss/modeling_gpt_oss.py
+ *   HFC = transformers/models/gpt_oss/configuration_gpt_oss.py
+ *   HFX = transformers/integrations/mxfp4.py
+ *   HFR = transformers/modeling_rope_utils.py
+ */
+#include "neon_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* numeric helpers                                                           */
+/* ------------------------------------------------------------------------ */
+float or_bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* round-to-nearest-even fp32 -> bf16; NaN stays NaN (quiet). */
+uint16_t or_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+#define BF(x) or_bf16_to_f32(x)
+#define TOBF(x) or_f32_to_bf16(x)
+
+/* ------------------------------------------------------------------------ */
+/* RNG: SplitMix64 finaliser (Steele, Lea, Flood 2014) keyed by             */
+/* (seed, stream, index).  Gaussian-shaped values are Irwin-Hall sums of     */
+/* four 16-bit uniforms scaled by one fp32 multiply, so the device init and  */
+/* this oracle produce bit-identical tensors.                                */
+/* ------------------------------------------------------------------------ */
+static inline uint64_t mix64(uint64_t z) {
+  z ^= z >> 30;
+  z *= 0xBF58476D1CE4E5B9ull;
+  z ^= z >> 27;
+  z *= 0x94D049BB133111EBull;
+  z ^= z >> 31;
+  return z;
+}
+
+static inline uint64_t stream_key(uint64_t seed, uint64_t stream) {
+  return mix64(seed + stream * 0x9E3779B97F4A7C15ull);
+}
+
+static inline uint64_t hash_k(uint64_t key, uint64_t i) {
+  return mix64(key ^ (i * 0xD1B54A32D192ED03ull + 0x632BE59BD9B4E019ull));
+}
+
+uint64_t or_hash(uint64_t seed, uint64_t stream, uint64_t i) {
+  return hash_k(stream_key(seed, stream), i);
+}
+
+static inline int32_t gauss_int(uint64_t h) {
+  return (int32_t)((h & 0xFFFF) + ((h >> 16) & 0xFFFF) + ((h >> 32) & 0xFFFF) +
+                   (h >> 48)) -
+         131070;
+}
+
+/* multiplier that turns gauss_int (std sqrt((2^32-1)/3)) into std `std` */
+float or_gauss_mul(double std) {
+  const double unit = sqrt((65536.0 * 65536.0 - 1.0) / 3.0);
+  return (float)(std / unit);
+}
+
+void or_fill_bf16(uint64_t seed, uint64_t stream, int64_t n, float mean,
+                  double std, uint16_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+  const float mul = or_gauss_mul(std);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    float g = (float)gauss_int(hash_k(key, (uint64_t)i)) * mul;
+    out[i] = TOBF(mean + g);
+  }
+}
+
+void or_fill_bytes(uint64_t seed, uint64_t stream, int64_t n, uint8_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+#pragma omp parallel for schedule(static)
+  for (int64_t w = 0; w < (n + 7) / 8; ++w) {
+    uint64_t h = hash_k(key, (uint64_t)w);
+    for (int j = 0; j < 8 && w * 8 + j < n; ++j)
+      out[w * 8 + j] = (uint8_t)(h >> (8 * j));
+  }
+}
+
+void or_fill_scales(uint64_t seed, uint64_t stream, int64_t n, int lo,
+                    int range, uint8_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t h = hash_k(key, (uint64_t)i);
+    out[i] = (uint8_t)(lo + (int)(((h >> 32) * (uint64_t)range) >> 32));
+  }
+}
+
+uint64_t or_stream_id(int layer, int kind) {
+  return ((uint64_t)(layer + 1) << 16) | (uint64_t)kind;
+}
+
+/* ------------------------------------------------------------------------ */
+/* MXFP4 (OCP MX v1.0; HFX:29-46 LUT, HFX:271 bias 127, HFX:298-304 nibble   */
+/* order: low nibble = element 2i, high nibble = element 2i+1).              */
+/* ------------------------------------------------------------------------ */
+static const float kE2M1[16] = {+0.0f, +0.5f, +1.0f, +1.5f, +2.0f, +3.0f,
+                                +4.0f, +6.0f, -0.0f, -0.5f, -1.0f, -1.5f,
+                                -2.0f, -3.0f, -4.0f, -6.0f};
+
+static inline float e8m0_exp2(uint8_t s, float v) {
+  if (s == 0xFF) return NAN; /* E8M0 0xFF encodes NaN */
+  return ldexpf(v, (int)s - 127);
+}
+
+void or_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
+                      int64_t n_blocks, float* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t b = 0; b < n_blocks; ++b) {
+    for (int j = 0; j < 16; ++j) {
+      uint8_t byte = codes[b * 16 + j];
+      out[b * 32 + 2 * j] = e8m0_exp2(scales[b], kE2M1[byte & 0xF]);
+      out[b * 32 + 2 * j + 1] = e8m0_exp2(scales[b], kE2M1[byte >> 4]);
+    }
+  }
+}
+
+/* y[b][n] = sum_k dq(W[n][k]) x[b][k] (+ bias[n]).  W is [N][K] with the 32-
+ * blocks along K (HF *_blocks [N][K/32][16], *_scales [N][K/32]).  Products
+ * of an E2M1 value and a bf16 are exact; the block sum and the row sum are
+ * accumulated in fp64, the result rounded once to fp32 (y_f32) and once to
+ * bf16 (y). */
+void or_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                   const uint16_t* bias, const uint16_t* x, int B, int N, int K,
+                   uint16_t* y, float* y_f32) {
+  const int KB = K / 32;
+  float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
+  for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n) {
+    const uint8_t* crow = codes + (size_t)n * (K / 2);
+    const uint8_t* srow = scales + (size_t)n * KB;
+    for (int b = 0; b < B; ++b) {
+      const float* xb = xf + (size_t)b * K;
+      double acc = 0.0;
+      for (int kb = 0; kb < KB; ++kb) {
+        double part = 0.0;
+        for (int j = 0; j < 16; ++j) {
+          uint8_t byte = crow[kb * 16 + j];
+          part += (double)kE2M1[byte & 0xF] * xb[kb * 32 + 2 * j];
+          part += (double)kE2M1[byte >> 4] * xb[kb * 32 + 2 * j + 1];
+        }
+        acc += part * ldexp(1.0, (int)srow[kb] - 127);
+      }
+      if (bias) acc += (double)BF(bias[n]);
+      float r = (float)acc;
+      if (y_f32) y_f32[(size_t)b * N + n] = r;
+      if (y) y[(size_t)b * N + n] = TOBF(r);
+    }
+  }
+  free(xf);
+}
+
+/* y[b][n] = sum_k W[n][k] x[b][k] (+ bias[n]), bf16 W [N][K] (nn.Linear). */
+void or_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                  int B, int N, int K, uint16_t* y, float* y_f32) {
+  float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
+  for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n) {
+    const uint16_t* wr = W + (size_t)n * K;
+    for (int b = 0; b < B; ++b) {
+      const float* xb = xf + (size_t)b * K;
+      double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      int k = 0;
+      for (; k + 8 <= K; k += 8)
+        for (int j = 0; j < 8; ++j) acc[j] += (double)BF(wr[k + j]) * xb[k + j];
+      for (; k < K; ++k) acc[0] += (double)BF(wr[k]) * xb[k];
+      double s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) +
+                 ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+      if (bias) s += (double)BF(bias[n]);
+      float r = (float)s;
+      if (y_f32) y_f32[(size_t)b * N + n] = r;
+      if (y) y[(size_t)b * N + n] = TOBF(r);
+    }
+  }
+  free(xf);
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm (HFM:57-62): fp32 x * rsqrt(mean(x^2) + eps), times the weight in  */
+/* fp32, one rounding to bf16.                                               */
+/* ------------------------------------------------------------------------ */
+void or_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
+                uint16_t* out) {
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* xb = x + (size_t)b * H;
+    double ss = 0.0;
+    for (int i = 0; i < H; ++i) ss += (double)BF(xb[i]) * BF(xb[i]);
+    float var = (float)(ss / H);
+    float r = 1.0f / sqrtf(var + eps);
+    for (int i = 0; i < H; ++i)
+      out[(size_t)b * H + i] = TOBF(BF(w[i]) * (BF(xb[i]) * r));
+  }
+}
+
+/* ------------------------------------------------------------------------ */
+/* YaRN RoPE (HFR:429-483; gpt-oss parameters HFC:29,80-88: theta 150000,   */
+/* factor 32, beta_fast 32, beta_slow 1, original_max 4096, truncate False). */
+/* ------------------------------------------------------------------------ */
+static double corr_dim(double nrot, double dim, double base, double maxpos) {
+  return (dim * log(maxpos / (nrot * 2.0 * M_PI))) / (2.0 * log(base));
+}
+
+void or_yarn_inv_freq(const or_config* cfg, double* inv_freq,
+                      double* attn_factor) {
+  const int dim = cfg->head_dim;
+  const double base = cfg->rope_theta, factor = cfg->rope_factor;
+  double low = corr_dim(cfg->rope_beta_fast, dim, base, cfg->rope_orig_max_pos);
+  double high =
+      corr_dim(cfg->rope_beta_slow, dim, base, cfg->rope_orig_max_pos);
+  if (low < 0) low = 0;               /* truncate=False: no floor/ceil */
+  if (high > dim - 1) high = dim - 1;
+  if (low == high) high += 0.001;
+  for (int i = 0; i < dim / 2; ++i) {
+    double pos_freq = pow(base, (2.0 * i) / dim);
+    double extra = 1.0 / pos_freq, inter = 1.0 / (factor * pos_freq);
+    double ramp = (i - low) / (high - low);
+    if (ramp < 0) ramp = 0;
+    if (ramp > 1) ramp = 1;
+    double ef = 1.0 - ramp; /* inv_freq_extrapolation_factor */
+    inv_freq[i] = inter * (1.0 - ef) + extra * ef;
+  }
+  *attn_factor = factor <= 1.0 ? 1.0 : 0.1 * log(factor) + 1.0;
+}
+
+/* cos/sin tables [n_pos][D/2] in fp32.  The angle is the fp32 product of
+ * the fp32 inverse frequency and the position (as HFM:196-198 computes it);
+ * cos/sin are then scaled by the YaRN attention factor in fp32. */
+void or_rope_table(const or_config* cfg, int n_pos, float* cos_t,
+                   float* sin_t) {
+  const int half = cfg->head_dim / 2;
+  double invf[256], af;
+  or_yarn_inv_freq(cfg, invf, &af);
+  const float aff = (float)af;
+  for (int p = 0; p < n_pos; ++p)
+    for (int i = 0; i < half; ++i) {
+      float ang = (float)invf[i] * (float)p;
+      cos_t[(size_t)p * half + i] = (float)cos((double)ang) * aff;
+      sin_t[(size_t)p * half + i] = (float)sin((double)ang) * aff;
+    }
+}
+
+/* half-split rotation (HFM:215-222): out1 = x1 c - x2 s, out2 = x2 c + x1 s */
+void or_rope_apply(const uint16_t* x, int n_heads, int D, const float* c,
+                   const float* s, uint16_t* out) {
+  const int half = D / 2;
+  for (int h = 0; h < n_heads; ++h)
+    for (int i = 0; i < half; ++i) {
+      float x1 = BF(x[h * D + i]), x2 = BF(x[h * D + half + i]);
+      float o1 = x1 * c[i] - x2 * s[i];
+      float o2 = x2 * c[i] + x1 * s[i];
+      out[h * D + i] = TOBF(o1);
+      out[h * D + half + i] = TOBF(o2);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Router (HFM:117-130): logits = x W^T + b, top-k over the logits, softmax  */
+/* over the k selected values.  The logits use ONE canonical fp32 reduction  */
+/* order, identical to the device router, so top-k indices match bit for     */
+/* bit: 64 lane partials (lane l owns the 8-element units u = l + 64 i, in   */
+/* increasing k, one fmaf per element), then a xor-butterfly over offsets    */
+/* 32,16,8,4,2,1, then + bias.  Ties go to the lower expert index.           */
+/* ------------------------------------------------------------------------ */
+static float router_logit(const uint16_t* x, const uint16_t* w, int H,
+                          uint16_t bias) {
+  float p[64];
+  const int U = H / 8;
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int u = l; u < U; u += 64)
+      for (int j = 0; j < 8; ++j)
+        acc = fmaf(BF(x[u * 8 + j]), BF(w[u * 8 + j]), acc);
+    p[l] = acc;
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    float q[64];
+    for (int l = 0; l < 64; ++l) q[l] = p[l] + p[l ^ off];
+    memcpy(p, q, sizeof(p));
+  }
+  return p[0] + BF(bias);
+}
+
+void or_router(const uint16_t* x, const uint16_t* W, const uint16_t* b, int B,
+               int E, int H, int k, int32_t* idx, float* score,
+               float* logits) {
+  float* lg = (float*)malloc(sizeof(float) * E);
+  for (int r = 0; r < B; ++r) {
+    for (int e = 0; e < E; ++e)
+      lg[e] = router_logit(x + (size_t)r * H, W + (size_t)e * H, H, b[e]);
+    if (logits) memcpy(logits + (size_t)r * E, lg, sizeof(float) * E);
+    float v[64];
+    int used[1024] = {0};
+    for (int t = 0; t < k; ++t) {
+      int best = -1;
+      for (int e = 0; e < E; ++e) {
+        if (used[e]) continue;
+        if (best < 0 || lg[e] > lg[best]) best = e;
+      }
+      used[best] = 1;
+      idx[r * k + t] = best;
+      v[t] = lg[best];
+    }
+    float ex[64], s = 0.0f;
+    for (int t = 0; t < k; ++t) {
+      ex[t] = expf(v[t] - v[0]);
+      s += ex[t];
+    }
+    for (int t = 0; t < k; ++t) score[r * k + t] = ex[t] / s;
+  }
+  free(lg);
+}
+
+/* ------------------------------------------------------------------------ */
+/* SwiGLU with clamp (HFM:82-87): gate = gu[2j] clamped above at limit, up = */
+/* gu[2j+1] clamped to [-limit, limit], out = (up + 1) * gate * sigmoid(     */
+/* alpha * gate).                                                            */
+/* ------------------------------------------------------------------------ */
+void or_swiglu(const float* gu, int I, float alpha, float limit, float* out) {
+  for (int j = 0; j < I; ++j) {
+    float g = gu[2 * j], u = gu[2 * j + 1];
+    g = g > limit ? limit : g;
+    u = u > limit ? limit : (u < -limit ? -limit : u);
+    float sig = 1.0f / (1.0f + expf(-(g * alpha)));
+    out[j] = (u + 1.0f) * (g * sig);
+  }
+}
+
+/* MoE block (HFM:89-114, 145-154) on already-normalised x: router, then for
+ * each selected expert (rank order) gate_up GEMV + bias -> SwiGLU -> bf16 ->
+ * down GEMV + bias, weighted by its score and summed in fp32; one rounding
+ * to bf16. */
+void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
+                  const uint16_t* router_b, const uint8_t* gu_codes,
+                  const uint8_t* gu_scales, const uint16_t* gu_bias,
+                  const uint8_t* dn_codes, const uint8_t* dn_scales,
+                  const uint16_t* dn_bias, int B, int E, int H, int I, int k,
+                  float alpha, float limit, uint16_t* out, int32_t* idx,
+                  float* score) {
+  or_router(x, router_w, router_b, B, E, H, k, idx, score, NULL);
+  float* gu = (float*)malloc(sizeof(float) * 2 * I);
+  float* act = (float*)malloc(sizeof(float) * I);
+  uint16_t* actb = (uint16_t*)malloc(sizeof(uint16_t) * I);
+  float* dn = (float*)malloc(sizeof(float) * H);
+  float* acc = (float*)malloc(sizeof(float) * H);
+  const size_t gu_code_sz = (size_t)2 * I * (H / 2), gu_sc_sz = (size_t)2 * I * (H / 32);
+  const size_t dn_code_sz = (size_t)H * (I / 2), dn_sc_sz = (size_t)H * (I / 32);
+  for (int r = 0; r < B; ++r) {
+    for (int i = 0; i < H; ++i) acc[i] = 0.0f;
+    for (int t = 0; t < k; ++t) {
+      const int e = idx[r * k + t];
+      or_mxfp4_gemv(gu_codes + e * gu_code_sz, gu_scales + e * gu_sc_sz,
+                    gu_bias + (size_t)e * 2 * I, x + (size_t)r * H, 1, 2 * I, H,
+                    NULL, gu);
+      or_swiglu(gu, I, alpha, limit, act);
+      for (int j = 0; j < I; ++j) actb[j] = TOBF(act[j]);
+      or_mxfp4_gemv(dn_codes + e * dn_code_sz, dn_scales + e * dn_sc_sz,
+                    dn_bias + (size_t)e * H, actb, 1, H, I, NULL, dn);
+      const float sc = score[r * k + t];
+      for (int i = 0; i < H; ++i) acc[i] += sc * dn[i];
+    }
+    for (int i = 0; i < H; ++i) out[(size_t)r * H + i] = TOBF(acc[i]);
+  }
+  free(gu); free(act); free(actb); free(dn); free(acc);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Decode attention with sinks (HFM:235-263, 276-277, 292-293): for query    */
+/* head h (kv head h / (Hq/Hkv)), logits s_j = q.k_j / sqrt(D) over keys     */
+/* j in [lo, pos] (lo = pos - window + 1 for sliding layers, HF mask        */
+/* kv_idx > q_idx - window), softmax over [s_j..., sink_h], sink column      */
+/* dropped before P.V.  fp64 inside; rounded once.                            */
+/* ------------------------------------------------------------------------ */
+void or_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                    const uint16_t* sinks, int B, int Hq, int Hkv, int D,
+                    int T_max, const int32_t* pos, int window, uint16_t* out,
+                    float* out_f32) {
+  const int G = Hq / Hkv;
+  const double scale = 1.0 / sqrt((double)D);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h) {
+      const int kvh = h / G, p = pos[b];
+      int lo = 0;
+      if (window > 0 && p - window + 1 > 0) lo = p - window + 1;
+      const int n = p - lo + 1;
+      const uint16_t* qh = q + ((size_t)b * Hq + h) * D;
+      const size_t base = ((size_t)b * Hkv + kvh) * T_max;
+      double* s = (double*)malloc(sizeof(double) * n);
+      double m = (double)BF(sinks[h]);
+      for (int j = 0; j < n; ++j) {
+        const uint16_t* kr = kc + (base + lo + j) * D;
+        double d = 0.0;
+        for (int i = 0; i < D; ++i) d += (double)BF(qh[i]) * BF(kr[i]);
+        s[j] = d * scale;
+        if (s[j] > m) m = s[j];
+      }
+      double den = exp((double)BF(sinks[h]) - m);
+      double o[256] = {0};
+      for (int j = 0; j < n; ++j) {
+        double pj = exp(s[j] - m);
+        den += pj;
+        const uint16_t* vr = vc + (base + lo + j) * D;
+        for (int i = 0; i < D; ++i) o[i] += pj * BF(vr[i]);
+      }
+      for (int i = 0; i < D; ++i) {
+        float r = (float)(o[i] / den);
+        if (out_f32) out_f32[((size_t)b * Hq + h) * D + i] = r;
+        if (out) out[((size_t)b * Hq + h) * D + i] = TOBF(r);
+      }
+      free(s);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Full model                                                                */
+/* ------------------------------------------------------------------------ */
+typedef struct or_layer {
+  uint16_t *attn_norm, *wqkv, *bqkv, *wo, *bo, *sinks, *mlp_norm, *router_w,
+      *router_b, *gu_bias, *dn_bias;
+  uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
+} or_layer;
+
+struct or_model {
+  or_config cfg;
+  int batch;
+  uint16_t *embed, *lm_head, *final_norm;
+  or_layer* layers;
+  float *cos_t, *sin_t;
+  uint16_t *kc, *vc; /* [L][B][Hkv][max_seq][D] */
+  int32_t* pos;
+  uint16_t* h; /* [B][H] */
+};
+
+static void* xmalloc(size_t n) {
+  void* p = malloc(n ? n : 1);
+  if (!p) abort();
+  return p;
+}
+
+or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch) {
+  or_model* m = (or_model*)calloc(1, sizeof(or_model));
+  m->cfg = *cfg;
+  m->batch = batch;
+  const int H = cfg->hidden, D = cfg->head_dim, Hq = cfg->n_heads,
+            Hkv = cfg->n_kv_heads, E = cfg->n_experts, I = cfg->intermediate;
+  const int64_t V = cfg->vocab, QKV = (int64_t)(Hq + 2 * Hkv) * D;
+  m->embed = (uint16_t*)xmalloc(sizeof(uint16_t) * V * H);
+  m->lm_head = (uint16_t*)xmalloc(sizeof(uint16_t) * V * H);
+  m->final_norm = (uint16_t*)xmalloc(sizeof(uint16_t) * H);
+  or_fill_bf16(seed, or_stream_id(-1, OR_T_EMBED), V * H, 0.0f, 0.02, m->embed);
+  or_fill_bf16(seed, or_stream_id(-1, OR_T_LM_HEAD), V * H, 0.0f, 0.02,
+               m->lm_head);
+  or_fill_bf16(seed, or_stream_id(-1, OR_T_FINAL_NORM), H, 1.0f, 0.05,
+               m->final_norm);
+  m->layers = (or_layer*)calloc(cfg->n_layers, sizeof(or_layer));
+  for (int l = 0; l < cfg->n_layers; ++l) {
+    or_layer* L = &m->layers[l];
+#define GEN_BF(field, kind, n, mean, std)                              \
+  L->field = (uint16_t*)xmalloc(sizeof(uint16_t) * (size_t)(n));       \
+  or_fill_bf16(seed, or_stream_id(l, kind), (n), (mean), (std), L->field)
+    GEN_BF(attn_norm, OR_T_ATTN_NORM, H, 1.0f, 0.05);
+    GEN_BF(wqkv, OR_T_WQKV, QKV * H, 0.0f, 0.02);
+    GEN_BF(bqkv, OR_T_BQKV, QKV, 0.0f, 0.02);
+    GEN_BF(wo, OR_T_WO, (int64_t)H * Hq * D, 0.0f, 0.02);
+    GEN_BF(bo, OR_T_BO, H, 0.0f, 0.02);
+    GEN_BF(sinks, OR_T_SINKS, Hq, 0.0f, 1.0);
+    GEN_BF(mlp_norm, OR_T_MLP_NORM, H, 1.0f, 0.05);
+    GEN_BF(router_w, OR_T_ROUTER_W, (int64_t)E * H, 0.0f, 0.02);
+    GEN_BF(router_b, OR_T_ROUTER_B, E, 0.0f, 0.02);
+    GEN_BF(gu_bias, OR_T_GU_BIAS, (int64_t)E * 2 * I, 0.0f, 0.02);
+    GEN_BF(dn_bias, OR_T_DN_BIAS, (int64_t)E * H, 0.0f, 0.02);
+#undef GEN_BF
+    const int64_t gu_codes = (int64_t)E * 2 * I * (H / 2),
+                  gu_sc = (int64_t)E * 2 * I * (H / 32);
+    const int64_t dn_codes = (int64_t)E * H * (I / 2),
+                  dn_sc = (int64_t)E * H * (I / 32);
+    L->gu_codes = (uint8_t*)xmalloc(gu_codes);
+    L->gu_scales = (uint8_t*)xmalloc(gu_sc);
+    L->dn_codes = (uint8_t*)xmalloc(dn_codes);
+    L->dn_scales = (uint8_t*)xmalloc(dn_sc);
+    or_fill_bytes(seed, or_stream_id(l, OR_T_GU_CODES), gu_codes, L->gu_codes);
+    or_fill_scales(seed, or_stream_id(l, OR_T_GU_SCALES), gu_sc, 119, 6,
+                   L->gu_scales);
+    or_fill_bytes(seed, or_stream_id(l, OR_T_DN_CODES), dn_codes, L->dn_codes);
+    or_fill_scales(seed, or_stream_id(l, OR_T_DN_SCALES), dn_sc, 119, 6,
+                   L->dn_scales);
+  }
+  m->cos_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
+  m->sin_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
+  or_rope_table(cfg, cfg->max_seq, m->cos_t, m->sin_t);
+  const size_t kv = (size_t)cfg->n_layers * batch * Hkv * cfg->max_seq * D;
+  m->kc = (uint16_t*)calloc(kv, sizeof(uint16_t));
+  m->vc = (uint16_t*)calloc(kv, sizeof(uint16_t));
+  m->pos = (int32_t*)calloc(batch, sizeof(int32_t));
+  m->h = (uint16_t*)calloc((size_t)batch * H, sizeof(uint16_t));
+  return m;
+}
+
+void or_model_free(or_model* m) {
+  if (!m) return;
+  for (int l = 0; l < m->cfg.n_layers; ++l) {
+    or_layer* L = &m->layers[l];
+    free(L->attn_norm); free(L->wqkv); free(L->bqkv); free(L->wo); free(L->bo);
+    free(L->sinks); free(L->mlp_norm); free(L->router_w); free(L->router_b);
+    free(L->gu_bias); free(L->dn_bias); free(L->gu_codes); free(L->gu_scales);
+    free(L->dn_codes); free(L->dn_scales);
+  }
+  free(m->layers); free(m->embed); free(m->lm_head); free(m->final_norm);
+  free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc); free(m->pos);
+  free(m->h); free(m);
+}
+
+const uint16_t* or_model_hidden(const or_model* m) { return m->h; }
+int32_t or_model_pos(const or_model* m, int b) { return m->pos[b]; }
+
+const void* or_model_tensor(const or_model* m, int layer, int kind) {
+  if (layer < 0) {
+    switch (kind) {
+      case OR_T_EMBED: return m->embed;
+      case OR_T_LM_HEAD: return m->lm_head;
+      case OR_T_FINAL_NORM: return m->final_norm;
+      default: return NULL;
+    }
+  }
+  const or_layer* L = &m->layers[layer];
+  switch (kind) {
+    case OR_T_ATTN_NORM: return L->attn_norm;
+    case OR_T_WQKV: return L->wqkv;
+    case OR_T_BQKV: return L->bqkv;
+    case OR_T_WO: return L->wo;
+    case OR_T_BO: return L->bo;
+    case OR_T_SINKS: return L->sinks;
+    case OR_T_MLP_NORM: return L->mlp_norm;
+    case OR_T_ROUTER_W: return L->router_w;
+    case OR_T_ROUTER_B: return L->router_b;
+    case OR_T_GU_CODES: return L->gu_codes;
+    case OR_T_GU_SCALES: return L->gu_scales;
+    case OR_T_GU_BIAS: return L->gu_bias;
+    case OR_T_DN_CODES: return L->dn_codes;
+    case OR_T_DN_SCALES: return L->dn_scales;
+    case OR_T_DN_BIAS: return L->dn_bias;
+    default: return NULL;
+  }
+}
+
+/* Decoder layer (HFM:347-376): h += attn(norm(h)); h += moe(norm(h)); each
+ * sublayer output rounded to bf16 and added to the bf16 residual with one
+ * rounding.  Layer i is sliding iff (i + 1) is odd (HFC:75-78). */
+void or_model_step(or_model* m, const int32_t* ids, float* logits,
+                   int32_t* out_ids) {
+  const or_config* c = &m->cfg;
+  const int H = c->hidden, D = c->head_dim, Hq = c->n_heads, Hkv = c->n_kv_heads;
+  const int E = c->n_experts, I = c->intermediate, K = c->top_k;
+  const int QKV = (Hq + 2 * Hkv) * D, half = D / 2;
+  const int64_t V = c->vocab;
+  uint16_t* xn = (uint16_t*)xmalloc(sizeof(uint16_t) * H);
+  uint16_t* qkv = (uint16_t*)xmalloc(sizeof(uint16_t) * QKV);
+  uint16_t* qr = (uint16_t*)xmalloc(sizeof(uint16_t) * Hq * D);
+  uint16_t* ao = (uint16_t*)xmalloc(sizeof(uint16_t) * Hq * D);
+  uint16_t* tmp = (uint16_t*)xmalloc(sizeof(uint16_t) * H);
+  float* lg = (float*)xmalloc(sizeof(float) * V);
+  int32_t idx[64];
+  float sc[64];
+  for (int b = 0; b < m->batch; ++b) {
+    uint16_t* h = m->h + (size_t)b * H;
+    const int p = m->pos[b];
+    memcpy(h, m->embed + (size_t)ids[b] * H, sizeof(uint16_t) * H);
+    for (int l = 0; l < c->n_layers; ++l) {
+      const or_layer* L = &m->layers[l];
+      const int window = (l % 2 == 0) ? c->sliding_window : 0;
+      or_rmsnorm(h, L->attn_norm, 1, H, c->rms_eps, xn);
+      or_gemv_bf16(L->wqkv, L->bqkv, xn, 1, QKV, H, qkv, NULL);
+      const float* cr = m->cos_t + (size_t)p * half;
+      const float* sr = m->sin_t + (size_t)p * half;
+      or_rope_apply(qkv, Hq, D, cr, sr, qr);
+      const size_t lb = (((size_t)l * m->batch + b) * Hkv) * c->max_seq;
+      uint16_t kr[4096];
+      or_rope_apply(qkv + Hq * D, Hkv, D, cr, sr, kr);
+      for (int g = 0; g < Hkv; ++g) {
+        memcpy(m->kc + (lb + (size_t)g * c->max_seq + p) * D, kr + g * D,
+               sizeof(uint16_t) * D);
+        memcpy(m->vc + (lb + (size_t)g * c->max_seq + p) * D,
+               qkv + (Hq + Hkv + g) * D, sizeof(uint16_t) * D);
+      }
+      or_attn_decode(qr, m->kc + lb * D, m->vc + lb * D, L->sinks, 1, Hq, Hkv,
+                     D, c->max_seq, &p, window, ao, NULL);
+      or_gemv_bf16(L->wo, L->bo, ao, 1, H, Hq * D, tmp, NULL);
+      for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
+      or_rmsnorm(h, L->mlp_norm, 1, H, c->rms_eps, xn);
+      or_moe_layer(xn, L->router_w, L->router_b, L->gu_codes, L->gu_scales,
+                   L->gu_bias, L->dn_codes, L->dn_scales, L->dn_bias, 1, E, H,
+                   I, K, c->swiglu_alpha, c->swiglu_limit, tmp, idx, sc);
+      for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
+    }
+    or_rmsnorm(h, m->final_norm, 1, H, c->rms_eps, xn);
+    or_gemv_bf16(m->lm_head, NULL, xn, 1, (int)V, H, NULL, lg);
+    int best = 0;
+    for (int64_t v = 1; v < V; ++v)
+      if (lg[v] > lg[best]) best = (int)v;
+    if (out_ids) out_ids[b] = best;
+    if (logits) memcpy(logits + (size_t)b * V, lg, sizeof(float) * V);
+    m->pos[b] = p + 1;
+  }
+  free(xn); free(qkv); free(qr); free(ao); free(tmp); free(lg);
+}
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+/* threads the oracle's parallel loops use (reported with CPU timings) */
+int or_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}

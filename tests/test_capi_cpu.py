@@ -1,0 +1,113 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments on the host before touching a
+device (status codes of include/neon_gptoss.h)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import neonengine_amd as ne
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "neon_gptoss.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(neon_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    L = ne.lib()
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    assert sorted(ne.EXPORTS) == declared
+    for name in declared:
+        assert hasattr(L, name), name
+
+
+def test_presets():
+    c = ne.config_preset("gpt-oss-20b")
+    assert (c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim) == (24, 2880, 64, 8, 64)
+    assert (c.n_experts, c.top_k, c.intermediate, c.vocab) == (32, 4, 2880, 201088)
+    assert c.sliding_window == 128 and abs(c.rope_theta - 150000.0) < 1e-3
+    c2 = ne.config_preset("gpt-oss-120b")
+    assert (c2.n_layers, c2.n_experts) == (36, 128)
+    with pytest.raises(ne.NeonError) as e:
+        ne.config_preset("llama")
+    assert e.value.status == ne.NEON_EINVAL
+
+
+@pytest.mark.parametrize("field,value", [
+    ("head_dim", 128), ("hidden", 100), ("n_kv_heads", 3), ("top_k", 0), ("top_k", 40),
+    ("n_experts", 1000), ("max_batch", 0), ("max_seq", 0), ("rms_eps", 0.0),
+    ("intermediate", 33), ("n_heads", 12),
+])
+def test_ctx_create_rejects_bad_config(field, value):
+    cfg = ne.config_preset("gpt-oss-20b")
+    setattr(cfg, field, value)
+    ctx = C.c_void_p()
+    st = ne.lib().neon_ctx_create(C.byref(cfg), 0, C.byref(ctx))
+    assert st == ne.NEON_EINVAL
+    assert not ctx.value
+    assert ne.lib().neon_last_error(None)
+
+
+def test_ctx_create_null_args():
+    assert ne.lib().neon_ctx_create(None, 0, None) == ne.NEON_EINVAL
+
+
+def test_context_calls_reject_null_context():
+    L = ne.lib()
+    assert L.neon_init_random(None, 0, None) == ne.NEON_EINVAL
+    assert L.neon_load_tensor(None, b"lm_head.weight", None, 0) == ne.NEON_EINVAL
+    assert L.neon_prefill(None, None, 1, 1, None) == ne.NEON_EINVAL
+    assert L.neon_decode(None, 1, None) == ne.NEON_EINVAL
+    assert L.neon_read_tokens(None, 0, 1, None, None) == ne.NEON_EINVAL
+    assert L.neon_read_logits(None, None, None) == ne.NEON_EINVAL
+    assert L.neon_seq_len(None, None) == ne.NEON_EINVAL
+    L.neon_ctx_destroy(None)  # no-op
+
+
+def test_kernel_entry_points_validate_on_host():
+    L = ne.lib()
+    p = C.c_void_p(16)  # never dereferenced: validation fails first
+    assert L.neon_mxfp4_gemv(None, p, None, p, p, 8, 64, 1, None) == ne.NEON_EINVAL
+    assert L.neon_mxfp4_gemv(p, p, None, p, p, 8, 48, 1, None) == ne.NEON_EINVAL   # K % 32
+    assert L.neon_mxfp4_gemv(p, p, None, p, p, 0, 64, 1, None) == ne.NEON_EINVAL
+    assert L.neon_mxfp4_gemv(p, p, None, p, p, 8, 16384, 1, None) == ne.NEON_EINVAL
+    assert L.neon_gemv_bf16(p, None, p, p, 8, 12, 1, None) == ne.NEON_EINVAL       # K % 8
+    assert L.neon_rmsnorm(p, p, p, 1, 2880, 0.0, None) == ne.NEON_EINVAL
+    assert L.neon_router_topk(p, p, p, p, p, None, 1, 32, 2880, 40, None) == ne.NEON_EINVAL
+    assert L.neon_moe_layer(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 0, 1.702, 7.0,
+                            None) == ne.NEON_EINVAL
+    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
+    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 5, 64, 64, 0, None) == ne.NEON_EINVAL   # Hq % Hkv
+    assert L.neon_mxfp4_dequant(None, p, 1, p, None) == ne.NEON_EINVAL
+    assert L.neon_mxfp4_dequant(p, p, 0, p, None) == ne.NEON_OK  # empty is a no-op
+    assert b"K" in L.neon_last_error(None) or L.neon_last_error(None)
+
+
+def test_no_device_reports_ehip():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    cfg = ne.config_preset("gpt-oss-20b")
+    ctx = C.c_void_p()
+    assert ne.lib().neon_ctx_create(C.byref(cfg), 0, C.byref(ctx)) == ne.NEON_EHIP
+    assert b"device" in ne.lib().neon_last_error(None)
+
+
+def test_engine_header_is_self_contained_cpp(tmp_path):
+    """include/neon_engine.hpp compiles standalone against the C header."""
+    import shutil
+    import subprocess
+    gxx = shutil.which("g++")
+    if not gxx:
+        pytest.skip("no g++")
+    src = tmp_path / "t.cpp"
+    src.write_text('#include "neon_engine.hpp"\nint main(){ neon::Config c = neon::Config::preset("gpt-oss-20b"); return c.raw().n_layers == 24 ? 0 : 1; }\n')
+    r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
+                        str(src)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

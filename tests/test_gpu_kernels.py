@@ -1,0 +1,234 @@
+"""GPU parity of the kernel-level C-ABI entry points against the CPU oracle
+(same seeded inputs).  Bars: bit-exact for MXFP4 dequantisation, router
+logits and top-k indices; one bf16 rounding plus fp32-accumulation slack for
+GEMVs; 2e-2 relative max error (and much tighter in practice) for composites.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import neonengine_amd as ne
+from tests.gpu_util import bf16_err_ok, empty_dev, to_dev, to_host, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# config 0/1 distributions: E2M1 codes uniform, E8M0 exponents uniform in
+# [-8, -3] (bytes 119..124), bf16 activations ~N(0, 1), seed 0
+def mx_weights(orc, N, K, stream):
+    codes = orc.fill_bytes(0, stream, N * K // 2)
+    scales = orc.fill_scales(0, stream + 1, N * K // 32, 119, 6)
+    return codes, scales
+
+
+def test_dequant_exhaustive_bitexact(orc):
+    torch_cuda()
+    blocks = np.tile(np.arange(256, dtype=np.uint8), 256)
+    scales = np.repeat(np.arange(256, dtype=np.uint8), 16)
+    out = empty_dev((256 * 512,), np.float32)
+    say("dequant exhaustive 16x256")
+    ne.mxfp4_dequant(to_dev(blocks), to_dev(scales), out)
+    got = to_host(out)
+    want = orc.mxfp4_dequant(blocks, scales)
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    assert np.array_equal(nan_g, nan_w)
+    assert np.array_equal(got[~nan_g].view(np.uint32), want[~nan_w].view(np.uint32))
+
+
+@pytest.mark.parametrize("N", [2880, 5760, 4096])
+@pytest.mark.parametrize("B", [1, 4, 16, 64])
+def test_mxfp4_gemv_config1(orc, N, B):
+    K = 2880
+    codes, scales = mx_weights(orc, N, K, 1000 + N)
+    x = orc.fill_bf16(0, 2000 + B, B * K, 0.0, 1.0)
+    bias = orc.fill_bf16(0, 3000 + N, N, 0.0, 0.02)
+    say(f"mxfp4_gemv N={N} K={K} B={B}")
+    y = empty_dev((B, N), np.uint16)
+    ne.mxfp4_gemv(to_dev(codes), to_dev(scales), to_dev(bias), to_dev(x), y, N, K, B)
+    got = to_host(y)
+    _, ref = orc.mxfp4_gemv(codes, scales, bias, x, N, K)
+    Wabs = np.abs(orc.mxfp4_dequant(codes, scales).reshape(N, K))
+    abs_sum = np.abs(orc.bf16_to_f32(x)).reshape(B, K) @ Wabs.T
+    ok, ratio = bf16_err_ok(got, ref, abs_sum)
+    say(f"  worst error / bound = {ratio.max():.3f}")
+    assert ok.all()
+
+
+@pytest.mark.parametrize("N,K,B", [(5, 32, 1), (3, 64, 2), (130, 4096, 3), (17, 8192, 1)])
+def test_mxfp4_gemv_ragged(orc, N, K, B):
+    codes, scales = mx_weights(orc, N, K, 77)
+    x = orc.fill_bf16(0, 78, B * K, 0.0, 1.0)
+    say(f"mxfp4_gemv ragged N={N} K={K} B={B}")
+    y = empty_dev((B, N), np.uint16)
+    ne.mxfp4_gemv(to_dev(codes), to_dev(scales), None, to_dev(x), y, N, K, B)
+    _, ref = orc.mxfp4_gemv(codes, scales, None, x, N, K)
+    Wabs = np.abs(orc.mxfp4_dequant(codes, scales).reshape(N, K))
+    ok, _ = bf16_err_ok(to_host(y), ref, np.abs(orc.bf16_to_f32(x)).reshape(B, K) @ Wabs.T)
+    assert ok.all()
+
+
+def test_mxfp4_gemv_nan_scale_propagates(orc):
+    N, K = 4, 64
+    codes, scales = mx_weights(orc, N, K, 5)
+    scales = scales.copy()
+    scales[2 * (K // 32)] = 0xFF  # row 2, first block
+    x = orc.fill_bf16(0, 6, K, 0.0, 1.0)
+    y = empty_dev((1, N), np.uint16)
+    ne.mxfp4_gemv(to_dev(codes), to_dev(scales), None, to_dev(x), y, N, K, 1)
+    got = orc.bf16_to_f32(to_host(y))[0]
+    assert np.isnan(got[2]) and np.all(np.isfinite(got[[0, 1, 3]]))
+
+
+@pytest.mark.parametrize("N,K,B", [(5120, 2880, 1), (2880, 4096, 1), (7001, 2880, 2), (32, 2880, 4),
+                                   (9, 8, 1)])
+def test_gemv_bf16(orc, N, K, B):
+    W = orc.fill_bf16(0, 11, N * K, 0.0, 0.02)
+    bias = orc.fill_bf16(0, 12, N, 0.0, 0.02)
+    x = orc.fill_bf16(0, 13, B * K, 0.0, 1.0)
+    say(f"gemv_bf16 N={N} K={K} B={B}")
+    y = empty_dev((B, N), np.uint16)
+    ne.gemv_bf16(to_dev(W), to_dev(bias), to_dev(x), y, N, K, B)
+    _, ref = orc.gemv_bf16(W, bias, x, N, K)
+    abs_sum = np.abs(orc.bf16_to_f32(x)).reshape(B, K) @ np.abs(orc.bf16_to_f32(W)).reshape(N, K).T
+    ok, ratio = bf16_err_ok(to_host(y), ref, abs_sum)
+    say(f"  worst error / bound = {ratio.max():.3f}")
+    assert ok.all()
+
+
+@pytest.mark.parametrize("B,H", [(1, 2880), (3, 2880), (2, 64)])
+def test_rmsnorm(orc, B, H):
+    x = orc.fill_bf16(0, 21, B * H, 0.0, 30.0)
+    w = orc.fill_bf16(0, 22, H, 1.0, 0.05)
+    out = empty_dev((B, H), np.uint16)
+    ne.rmsnorm(to_dev(x), to_dev(w), out, B, H, 1e-5)
+    got = to_host(out).astype(np.int32)
+    want = orc.rmsnorm(x, w, 1e-5).astype(np.int32)
+    # the sum of squares is reduced in another order: at most one bf16 ulp apart
+    assert np.abs(got - want).max() <= 1
+    assert (got != want).mean() < 0.01
+
+
+def test_rope_yarn(orc):
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=40000)
+    ocfg = orc.make_config(max_seq=40000)
+    pos = np.array([0, 1, 127, 128, 2047, 4096, 32767, 39999], np.int32)
+    nh = 9
+    x = orc.fill_bf16(0, 31, len(pos) * nh * 64, 0.0, 1.0)
+    xd = to_dev(x)
+    ne.rope_yarn(xd, to_dev(pos), len(pos), nh, cfg)
+    got = to_host(xd).reshape(len(pos), nh * 64).astype(np.int32)
+    c, s = orc.rope_table(ocfg, 40000)
+    for t, p in enumerate(pos):
+        want = orc.rope_apply(x.reshape(len(pos), -1)[t], nh, 64, c[p], s[p]).astype(np.int32)
+        assert np.abs(got[t] - want).max() <= 1, p
+
+
+@pytest.mark.parametrize("B,E,k", [(1, 32, 4), (5, 128, 4), (2, 8, 8)])
+def test_router_bitexact(orc, B, E, k):
+    H = 2880
+    x = orc.fill_bf16(0, 41, B * H, 0.0, 1.0)
+    W = orc.fill_bf16(0, 42, E * H, 0.0, 0.02)
+    b = orc.fill_bf16(0, 43, E, 0.0, 0.02)
+    idx, sc, lg = empty_dev((B, k), np.int32), empty_dev((B, k), np.float32), empty_dev((B, E), np.float32)
+    ne.router_topk(to_dev(x), to_dev(W), to_dev(b), idx, sc, lg, B, E, H, k)
+    ridx, rsc, rlg = orc.router(x, W, b, E, H, k)
+    assert np.array_equal(to_host(lg).view(np.uint32), rlg.view(np.uint32))  # canonical order
+    assert np.array_equal(to_host(idx), ridx)
+    np.testing.assert_allclose(to_host(sc), rsc, rtol=2e-6)
+
+
+def test_router_tie_break_lower_index(orc):
+    H, E, k = 64, 8, 4
+    x = orc.f32_to_bf16(np.ones(H, np.float32))
+    Wf = np.zeros((E, H), np.float32)
+    Wf[[1, 2, 3, 5, 6]] = 0.5
+    W = orc.f32_to_bf16(Wf)
+    b = orc.f32_to_bf16(np.zeros(E, np.float32))
+    idx, sc = empty_dev((1, k), np.int32), empty_dev((1, k), np.float32)
+    ne.router_topk(to_dev(x), to_dev(W), to_dev(b), idx, sc, None, 1, E, H, k)
+    assert list(to_host(idx)[0]) == [1, 2, 3, 5]
+
+
+def moe_inputs(orc, E, H, I, B, seed=0):
+    """config 0: E2M1 uniform, E8M0 exponent uniform in [-8,-3], router std
+    0.02, x ~ N(0, 1) bf16, seed 0."""
+    return dict(
+        x=orc.fill_bf16(seed, 51, B * H, 0.0, 1.0),
+        rw=orc.fill_bf16(seed, 52, E * H, 0.0, 0.02),
+        rb=orc.fill_bf16(seed, 53, E, 0.0, 0.02),
+        guc=orc.fill_bytes(seed, 54, E * 2 * I * H // 2),
+        gus=orc.fill_scales(seed, 55, E * 2 * I * H // 32, 119, 6),
+        gub=orc.fill_bf16(seed, 56, E * 2 * I, 0.0, 0.02),
+        dnc=orc.fill_bytes(seed, 57, E * H * I // 2),
+        dns=orc.fill_scales(seed, 58, E * H * I // 32, 119, 6),
+        dnb=orc.fill_bf16(seed, 59, E * H, 0.0, 0.02),
+    )
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_moe_layer_config0(orc, B):
+    E, H, I, k = 32, 2880, 2880, 4
+    d = moe_inputs(orc, E, H, I, B)
+    say(f"moe_layer config0 B={B}")
+    out = empty_dev((B, H), np.uint16)
+    idx, sc = empty_dev((B, k), np.int32), empty_dev((B, k), np.float32)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    ne.moe_layer(dv["x"], dv["rw"], dv["rb"], dv["guc"], dv["gus"], dv["gub"], dv["dnc"],
+                 dv["dns"], dv["dnb"], None, out, idx, sc, B, E, H, I, k)
+    ref, ridx, rsc = orc.moe_layer(d["x"], d["rw"], d["rb"], d["guc"], d["gus"], d["gub"],
+                                   d["dnc"], d["dns"], d["dnb"], E, H, I, k)
+    assert np.array_equal(to_host(idx), ridx)  # bit-exact top-k indices
+    np.testing.assert_allclose(to_host(sc), rsc, rtol=2e-6)
+    g = orc.bf16_to_f32(to_host(out)).astype(np.float64)
+    r = orc.bf16_to_f32(ref).astype(np.float64)
+    rel = np.abs(g - r).max() / np.abs(r).max()
+    say(f"  moe rel max err {rel:.2e}, mean abs err / rms {np.abs(g - r).mean() / np.sqrt((r ** 2).mean()):.2e}")
+    assert rel < 2e-2
+
+
+def test_moe_layer_residual(orc):
+    E, H, I, k, B = 8, 256, 512, 2, 2
+    d = moe_inputs(orc, E, H, I, B, seed=3)
+    res = orc.fill_bf16(3, 60, B * H, 0.0, 10.0)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    out = empty_dev((B, H), np.uint16)
+    out2 = empty_dev((B, H), np.uint16)
+    ne.moe_layer(dv["x"], dv["rw"], dv["rb"], dv["guc"], dv["gus"], dv["gub"], dv["dnc"],
+                 dv["dns"], dv["dnb"], to_dev(res), out, None, None, B, E, H, I, k)
+    ne.moe_layer(dv["x"], dv["rw"], dv["rb"], dv["guc"], dv["gus"], dv["gub"], dv["dnc"],
+                 dv["dns"], dv["dnb"], None, out2, None, None, B, E, H, I, k)
+    m = to_host(out2)
+    want = orc.f32_to_bf16(orc.bf16_to_f32(res) + orc.bf16_to_f32(m).reshape(-1))
+    assert np.array_equal(to_host(out).reshape(-1), want)
+
+
+@pytest.mark.parametrize("T,B,window", [
+    (1, 1, 0), (5, 2, 128), (1024, 1, 0), (1024, 8, 128), (8192, 1, 0), (8192, 8, 128),
+    (8192, 8, 0), (32768, 1, 0), (32768, 4, 128), (300, 3, 0)])
+def test_attn_decode_config2(orc, T, B, window):
+    """64 q / 8 kv heads, d=64, Q/K/V and sinks ~N(0,1) bf16."""
+    Hq, Hkv, D = 64, 8, 64
+    Tm = T
+    q = orc.fill_bf16(0, 71, B * Hq * D, 0.0, 1.0)
+    kc = orc.fill_bf16(0, 72, B * Hkv * Tm * D, 0.0, 1.0)
+    vc = orc.fill_bf16(0, 73, B * Hkv * Tm * D, 0.0, 1.0)
+    sinks = orc.fill_bf16(0, 74, Hq, 0.0, 1.0)
+    pos = np.array([T - 1 - (b % 3) for b in range(B)], np.int32).clip(0)
+    say(f"attn T={T} B={B} window={window}")
+    out = empty_dev((B, Hq * D), np.uint16)
+    ne.attn_decode(to_dev(q), to_dev(kc), to_dev(vc), to_dev(sinks), to_dev(pos), out, B, Hq,
+                   Hkv, D, Tm, window)
+    _, ref = orc.attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, window)
+    g = orc.bf16_to_f32(to_host(out)).astype(np.float64)
+    r = ref.astype(np.float64)
+    err = np.abs(g - r)
+    # one bf16 rounding plus fp32 softmax/accumulation slack
+    bound = np.abs(r) * 2.0 ** -8 + 2e-5 * np.abs(r).max()
+    say(f"  worst error / bound {np.max(err / bound):.3f}")
+    assert np.all(err <= bound)

@@ -1,0 +1,175 @@
+"""GPU parity of the whole token loop (context-level C-ABI) against the CPU
+oracle: bit-identical random-init weights, identical greedy token ids for 64
+steps, and bf16-rounded logits within 2e-2 relative max error."""
+import sys
+
+import numpy as np
+import pytest
+
+import neonengine_amd as ne
+from tests.gpu_util import d2h, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+SMALL = dict(n_layers=4, hidden=512, n_heads=16, n_kv_heads=2, head_dim=64, n_experts=8,
+             top_k=4, intermediate=512, vocab=4096, sliding_window=128, max_seq=512,
+             max_batch=2)
+
+
+def pair(orc, **kw):
+    cfg = ne.config_preset("gpt-oss-20b", **kw)
+    ocfg = orc.make_config(**cfg.as_dict())
+    return cfg, ocfg
+
+
+def logits_close(g, r):
+    gb = orc_bf(g)
+    rb = orc_bf(r)
+    return np.abs(gb - rb).max() / np.abs(rb).max()
+
+
+def orc_bf(a):
+    from oracle import oracle as orc
+    return orc.bf16_to_f32(orc.f32_to_bf16(a)).astype(np.float64)
+
+
+def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
+    torch_cuda()
+    eng = ne.Engine(cfg)
+    eng.init_random(seed)
+    say(f"model parity layers={cfg.n_layers} hidden={cfg.hidden} E={cfg.n_experts} "
+        f"vocab={cfg.vocab} batch={batch} prompt={len(prompt[0])} steps={n_steps}")
+    m = orc.Model(ocfg, seed=seed, batch=batch)
+    # oracle: teacher-forced prompt, then its own greedy ids
+    ids_o = np.array([p[0] for p in prompt], np.int32)
+    for t in range(len(prompt[0])):
+        ids_o = np.array([p[t] for p in prompt], np.int32)
+        nxt, lg_o = m.step(ids_o)
+    o_tokens = [nxt.copy()]
+    o_logits = [lg_o]
+    margins = []
+    for _ in range(n_steps):
+        top2 = np.sort(lg_o, axis=1)[:, -2:]
+        margins.append(top2[:, 1] - top2[:, 0])
+        nxt, lg_o = m.step(nxt)
+        o_tokens.append(nxt.copy())
+        o_logits.append(lg_o)
+    m.close()
+    eng.prefill(prompt)
+    g_first_logits = eng.read_logits()
+    eng.decode(n_steps)
+    toks = eng.read_tokens()
+    g_last_logits = eng.read_logits()
+    eng.close()
+    n = len(prompt[0])
+    gen_g = toks[:, n:]
+    gen_o = np.stack(o_tokens, 1)[:, : n_steps + 1]
+    margins = np.stack(margins, 1)
+    same = gen_g == gen_o
+    if not same.all():
+        b, t = np.argwhere(~same)[0]
+        say(f"first divergence row {b} step {t}: gpu {gen_g[b, t]} oracle {gen_o[b, t]}, "
+            f"oracle top-2 margin there {margins[b, t - 1] if t else 'n/a'}")
+    say(f"  min oracle top-2 margin over the run: {margins.min():.4g}")
+    e1 = logits_close(g_first_logits, o_logits[0])
+    e2 = logits_close(g_last_logits, o_logits[n_steps]) if same.all() else 0.0
+    say(f"  logits rel max err: first {e1:.3e} last {e2:.3e}")
+    return same, e1, e2
+
+
+def test_init_random_matches_oracle_bits(orc):
+    torch_cuda()
+    cfg, ocfg = pair(orc, **SMALL)
+    eng = ne.Engine(cfg)
+    eng.init_random(11)
+    m = orc.Model(ocfg, seed=11, batch=1)
+    H, E, I = cfg.hidden, cfg.n_experts, cfg.intermediate
+    qkv = (cfg.n_heads + 2 * cfg.n_kv_heads) * 64
+    checks = [
+        ("model.embed_tokens.weight", -1, orc.T_EMBED, cfg.vocab * H, np.uint16),
+        ("lm_head.weight", -1, orc.T_LM_HEAD, cfg.vocab * H, np.uint16),
+        ("model.norm.weight", -1, orc.T_FINAL_NORM, H, np.uint16),
+        ("model.layers.0.input_layernorm.weight", 0, orc.T_ATTN_NORM, H, np.uint16),
+        ("model.layers.3.self_attn.sinks", 3, orc.T_SINKS, cfg.n_heads, np.uint16),
+        ("model.layers.1.mlp.router.weight", 1, orc.T_ROUTER_W, E * H, np.uint16),
+        ("model.layers.2.mlp.experts.gate_up_proj_blocks", 2, orc.T_GU_CODES, E * 2 * I * H // 2, np.uint8),
+        ("model.layers.2.mlp.experts.gate_up_proj_scales", 2, orc.T_GU_SCALES, E * 2 * I * H // 32, np.uint8),
+        ("model.layers.3.mlp.experts.down_proj_blocks", 3, orc.T_DN_CODES, E * H * I // 2, np.uint8),
+        ("model.layers.3.mlp.experts.down_proj_bias", 3, orc.T_DN_BIAS, E * H, np.uint16),
+    ]
+    for name, layer, kind, count, dt in checks:
+        ptr, nbytes = eng.tensor_ptr(name)
+        got = d2h(ptr, nbytes, dt)
+        want = m.tensor(layer, kind, count, dt)
+        assert np.array_equal(got, want), name
+    # fused q/k/v: the checkpoint's q_proj rows come first, then k, then v
+    ptr, nbytes = eng.tensor_ptr("model.layers.1.self_attn.v_proj.weight")
+    got = d2h(ptr, nbytes, np.uint16)
+    want = m.tensor(1, orc.T_WQKV, qkv * H)[(cfg.n_heads + cfg.n_kv_heads) * 64 * H:]
+    assert np.array_equal(got, want)
+    m.close()
+    eng.close()
+
+
+def test_small_model_greedy_64(orc):
+    cfg, ocfg = pair(orc, **SMALL)
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 5, [[1, 2, 3, 4000, 17, 9, 9, 300]], 64)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_small_model_batch2_and_sliding_wrap(orc):
+    """Two rows; 160 positions so the 128-key sliding window moves."""
+    cfg, ocfg = pair(orc, **SMALL)
+    prompt = [[(7 * i + 3) % 4096 for i in range(100)], [(11 * i + 5) % 4096 for i in range(100)]]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 9, prompt, 60, batch=2)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_gpt_oss_20b_greedy_64(orc):
+    """Full gpt-oss-20b shape (24 layers, 32 experts, vocab 201088)."""
+    cfg, ocfg = pair(orc, max_seq=256)
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 0, [[101, 2002, 30003, 200000]], 64)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_engine_errors_on_gpu(orc):
+    torch_cuda()
+    cfg, _ = pair(orc, **dict(SMALL, max_seq=16))
+    eng = ne.Engine(cfg)
+    with pytest.raises(ne.NeonError) as e:
+        eng.prefill([[1, 2]])
+    assert e.value.status == ne.NEON_ESTATE  # no weights yet
+    eng.init_random(1)
+    with pytest.raises(ne.NeonError) as e:
+        eng.prefill([[1, 4096]])
+    assert e.value.status == ne.NEON_ERANGE_TOKEN
+    with pytest.raises(ne.NeonError) as e:
+        eng.decode(1)
+    assert e.value.status == ne.NEON_ESTATE
+    with pytest.raises(ne.NeonError) as e:
+        eng.prefill([[1] * 17])
+    assert e.value.status == ne.NEON_EKV_FULL
+    eng.prefill([[1] * 10])
+    with pytest.raises(ne.NeonError) as e:
+        eng.decode(7)
+    assert e.value.status == ne.NEON_EKV_FULL
+    eng.decode(6)  # exactly fills the cache
+    assert eng.seq_len() == 17
+    bad = np.zeros(cfg.n_experts * 2 * cfg.intermediate * cfg.hidden // 32, np.uint8)
+    bad[5] = 0xFF
+    with pytest.raises(ne.NeonError) as e:
+        eng.load_tensor("model.layers.0.mlp.experts.gate_up_proj_scales", bad.tobytes())
+    assert e.value.status == ne.NEON_ENAN_SCALE
+    with pytest.raises(ne.NeonError) as e:
+        eng.load_tensor("model.layers.0.mlp.experts.gate_up_proj_scales", bad[:10].tobytes())
+    assert e.value.status == ne.NEON_EINVAL
+    eng.close()

@@ -1,0 +1,443 @@
+"""CPU pins of the oracle (no GPU).
+
+The reference repository has no implementation of this path, so the oracle
+is pinned by (a) closed forms and exhaustive tables from the format and
+model maths, (b) fp64 brute force with stated bounds, and (c) fixtures
+written by HF transformers' gpt_oss modules (tests/golden/make_golden.py).
+Each check is chosen so a plausible slip (swapped nibbles, wrong scale bias,
+dropped sink, wrong sliding bound, transposed weights) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+
+def e2m1_from_bits(c):
+    """E2M1 value from its bit fields (OCP MX v1.0: 1 sign, 2 exponent (bias
+    1), 1 mantissa; exponent 0 is subnormal) -- derived, not the LUT."""
+    s = -1.0 if (c >> 3) & 1 else 1.0
+    e = (c >> 1) & 3
+    m = c & 1
+    mag = (m * 0.5) if e == 0 else (1.0 + m / 2.0) * 2.0 ** (e - 1)
+    return s * mag
+
+
+# ---------------------------------------------------------------------------
+# MXFP4
+# ---------------------------------------------------------------------------
+def test_dequant_exhaustive_closed_form(orc):
+    # every (byte, scale): 256 bytes -> 16 blocks of 16 bytes, per scale
+    blocks = np.tile(np.arange(256, dtype=np.uint8), 256)  # 256 scales x 256 bytes
+    scales = np.repeat(np.arange(256, dtype=np.uint8), 16)  # one scale per 16-byte block
+    out = orc.mxfp4_dequant(blocks, scales).reshape(256, 512)
+    for s in range(256):
+        row = out[s]
+        for byte in range(256):
+            lo, hi = row[2 * byte], row[2 * byte + 1]
+            if s == 255:
+                assert np.isnan(lo) and np.isnan(hi)
+                continue
+            with np.errstate(over="ignore"):  # 2^127 * {2,3,4,6} overflows to inf
+                want_lo = np.float32(e2m1_from_bits(byte & 15) * 2.0 ** (s - 127))
+                want_hi = np.float32(e2m1_from_bits(byte >> 4) * 2.0 ** (s - 127))
+            assert lo.tobytes() == want_lo.tobytes(), (s, byte)
+            assert hi.tobytes() == want_hi.tobytes(), (s, byte)
+
+
+def test_dequant_matches_hf(orc, golden):
+    blocks, sc = golden["mxfp4_blocks"], golden["mxfp4_scales"]
+    ours = orc.mxfp4_dequant(blocks.reshape(-1), sc.reshape(-1)).reshape(blocks.shape[0], -1)
+    hf = golden["mxfp4_deq"]
+    assert ours.shape == hf.shape
+    assert np.array_equal(ours.view(np.uint32), hf.view(np.uint32))
+
+
+def test_e8m0_matches_torch(orc):
+    torch = pytest.importorskip("torch")
+    if not hasattr(torch, "float8_e8m0fnu"):
+        pytest.skip("torch lacks float8_e8m0fnu")
+    b = torch.arange(256, dtype=torch.uint8)
+    ref = b.view(torch.float8_e8m0fnu).to(torch.float32).numpy()
+    # code 2 is E2M1 1.0, so the dequantised value is the scale itself
+    ours = orc.mxfp4_dequant(np.full(256 * 16, 0x22, np.uint8), np.arange(256, dtype=np.uint8))
+    ours = ours.reshape(256, 32)[:, 0]
+    assert np.isnan(ref[255]) and np.isnan(ours[255])
+    assert np.array_equal(ours[:255].view(np.uint32), ref[:255].view(np.uint32))
+
+
+def dq_np(orc, codes, scales, N, K):
+    return orc.mxfp4_dequant(codes, scales).reshape(N, K).astype(np.float64)
+
+
+@pytest.mark.parametrize("N,K,B", [(64, 256, 1), (96, 2880, 3), (5, 32, 2)])
+def test_mxfp4_gemv_vs_fp64(orc, N, K, B):
+    rng = np.random.default_rng(N + K + B)
+    codes = rng.integers(0, 256, N * K // 2, dtype=np.uint8)
+    scales = rng.integers(119, 125, N * K // 32, dtype=np.uint8)
+    bias = orc.f32_to_bf16(rng.standard_normal(N).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((B, K)).astype(np.float32))
+    y, yf = orc.mxfp4_gemv(codes, scales, bias, x, N, K)
+    Wd = dq_np(orc, codes, scales, N, K)
+    ref = orc.bf16_to_f32(x).astype(np.float64) @ Wd.T + orc.bf16_to_f32(bias)
+    # fp64 accumulation, one rounding to fp32
+    assert np.all(np.abs(yf - ref) <= np.abs(ref) * 2.0 ** -23 + 1e-30)
+    assert np.array_equal(y, orc.f32_to_bf16(yf))
+    # a transposed weight or dropped bias would be far outside this
+    y2, _ = orc.mxfp4_gemv(codes, scales, None, x, N, K)
+    assert not np.array_equal(y2, y)
+
+
+def test_mxfp4_gemv_matches_hf_expert(orc, golden):
+    blocks = golden["experts_gu_blocks"][0].reshape(-1)
+    scales = golden["experts_gu_scales"][0].reshape(-1)
+    bias = orc.f32_to_bf16(golden["experts_gu_bias"][0])
+    x = orc.f32_to_bf16(golden["experts_x"])
+    _, yf = orc.mxfp4_gemv(blocks, scales, bias, x, 128, 64)
+    np.testing.assert_allclose(yf, golden["experts_gate_up_e0"], rtol=1e-5, atol=1e-5)
+
+
+def test_gemv_bf16_vs_fp64(orc):
+    rng = np.random.default_rng(3)
+    N, K, B = 77, 2880, 2
+    W = orc.f32_to_bf16(0.02 * rng.standard_normal((N, K)).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.standard_normal(N).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((B, K)).astype(np.float32))
+    y, yf = orc.gemv_bf16(W, bias, x, N, K)
+    ref = orc.bf16_to_f32(x).astype(np.float64) @ orc.bf16_to_f32(W).astype(np.float64).T
+    ref += orc.bf16_to_f32(bias)
+    assert np.all(np.abs(yf - ref) <= np.abs(ref) * 2.0 ** -23 + 1e-12)
+    assert np.array_equal(y, orc.f32_to_bf16(yf))
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+def test_rmsnorm_constant_vector(orc):
+    H = 2880
+    for c in (1.0, -3.5, 1e-3, 250.0):
+        x = orc.f32_to_bf16(np.full(H, c, np.float32))
+        w = orc.f32_to_bf16(np.linspace(0.5, 1.5, H).astype(np.float32))
+        out = orc.rmsnorm(x, w, 1e-5)[0]
+        cb = float(orc.bf16_to_f32(x[:1])[0])
+        r = np.float32(1.0) / np.sqrt(np.float32(cb * cb + 1e-5), dtype=np.float32)
+        want = orc.f32_to_bf16(orc.bf16_to_f32(w) * (np.float32(cb) * r))
+        assert np.array_equal(out, want)
+
+
+def test_rmsnorm_matches_hf(orc, golden):
+    x = orc.f32_to_bf16(golden["rms_x"])
+    w = orc.f32_to_bf16(golden["rms_w"])
+    out = orc.bf16_to_f32(orc.rmsnorm(x, w, 1e-5))
+    ref = golden["rms_out"]
+    # ours is HF's fp32 result rounded once to bf16
+    assert np.all(np.abs(out - ref) <= np.abs(ref) * 2.0 ** -8 * 1.001)
+
+
+# ---------------------------------------------------------------------------
+# YaRN RoPE
+# ---------------------------------------------------------------------------
+def test_yarn_matches_hf(orc, golden):
+    cfg = orc.make_config()
+    inv, af = orc.yarn_inv_freq(cfg)
+    np.testing.assert_allclose(inv, golden["yarn_inv_freq"], rtol=2e-7)
+    assert abs(af - golden["yarn_attn_factor"][0]) < 1e-12
+    assert abs(af - (0.1 * math.log(32.0) + 1.0)) < 1e-12
+    # the ramp: highest frequencies extrapolate (= 1/base^(2i/d)), lowest interpolate
+    assert inv[0] == pytest.approx(1.0)
+    assert inv[-1] == pytest.approx(1.0 / (32.0 * 150000.0 ** (62 / 64)), rel=1e-12)
+
+
+def test_rope_table_and_apply_match_hf(orc, golden):
+    cfg = orc.make_config()
+    pos = golden["rope_positions"]
+    c, s = orc.rope_table(cfg, int(pos.max()) + 1)
+    # ours is the correctly rounded fp32 inverse frequency; torch's fp32 pow
+    # is off by one ulp in a few entries, which shifts the fp32 angle by at
+    # most pos * 2^-23 * inv_freq (<= 1), times the attention factor 1.35
+    tol = (2e-6 + 1.7e-7 * pos.astype(np.float64))[:, None]
+    assert np.all(np.abs(c[pos] - golden["rope_cos"][:, :32]) <= tol)
+    assert np.all(np.abs(s[pos] - golden["rope_sin"][:, :32]) <= tol)
+    # halves repeat (HFM emb = freqs; cos/sin are [.., D/2] tiled by the apply)
+    assert golden["rope_cos"].shape[1] in (32, 64)
+    x = golden["rope_x"]  # [T][3 heads][64], bf16-exact
+    for t, p in enumerate(pos):
+        out = orc.bf16_to_f32(orc.rope_apply(orc.f32_to_bf16(x[t]), 3, 64, c[p], s[p]))
+        ref = golden["rope_out"][t].reshape(-1)
+        xt = np.abs(x[t])
+        pair = np.concatenate([xt[:, :32] + xt[:, 32:]] * 2, axis=1).reshape(-1)
+        # one bf16 rounding, plus the table difference above times |x1|+|x2|
+        assert np.all(np.abs(out - ref) <= np.abs(ref) * 2.0 ** -8 + tol[t, 0] * pair + 1e-6), p
+
+
+def test_rope_invariants(orc):
+    cfg = orc.make_config()
+    c, s = orc.rope_table(cfg, 3000)
+    _, af = orc.yarn_inv_freq(cfg)
+    rng = np.random.default_rng(5)
+    x = orc.f32_to_bf16(rng.standard_normal(4 * 64).astype(np.float32))
+    xf = orc.bf16_to_f32(x).reshape(4, 64)
+    # position 0 is the identity times the attention factor
+    out0 = orc.rope_apply(x, 4, 64, c[0], s[0])
+    assert np.array_equal(out0, orc.f32_to_bf16(xf.reshape(-1) * np.float32(af)))
+    # every position preserves the per-pair norm times the factor
+    for p in (1, 77, 2999):
+        o = orc.bf16_to_f32(orc.rope_apply(x, 4, 64, c[p], s[p])).reshape(4, 64)
+        n_in = xf[:, :32] ** 2 + xf[:, 32:] ** 2
+        n_out = o[:, :32] ** 2 + o[:, 32:] ** 2
+        np.testing.assert_allclose(n_out, n_in * af * af, rtol=2e-2, atol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------
+def test_router_bruteforce(orc):
+    rng = np.random.default_rng(11)
+    B, E, H, k = 6, 32, 2880, 4
+    x = orc.f32_to_bf16(rng.standard_normal((B, H)).astype(np.float32))
+    W = orc.f32_to_bf16(0.02 * rng.standard_normal((E, H)).astype(np.float32))
+    b = orc.f32_to_bf16(0.02 * rng.standard_normal(E).astype(np.float32))
+    idx, sc, lg = orc.router(x, W, b, E, H, k)
+    ref = orc.bf16_to_f32(x).astype(np.float64) @ orc.bf16_to_f32(W).astype(np.float64).T
+    ref += orc.bf16_to_f32(b)
+    np.testing.assert_allclose(lg, ref, rtol=1e-5, atol=1e-5)
+    for r in range(B):
+        order = sorted(range(E), key=lambda e: (-lg[r, e], e))[:k]
+        assert list(idx[r]) == order
+        v = lg[r, order].astype(np.float64)
+        p = np.exp(v - v[0]) / np.exp(v - v[0]).sum()
+        np.testing.assert_allclose(sc[r], p, rtol=1e-6)
+        assert abs(sc[r].sum() - 1.0) < 1e-6 and np.all(np.diff(sc[r]) <= 0)
+
+
+def test_router_ties_pick_lower_index(orc):
+    H, E, k = 64, 8, 4
+    x = orc.f32_to_bf16(np.ones((1, H), np.float32))
+    W = np.zeros((E, H), np.float32)
+    W[[1, 3, 5, 6]] = 0.5  # four equal maxima...
+    W[2] = 0.5             # ...and a fifth equal one at index 2
+    idx, sc, _ = orc.router(x, orc.f32_to_bf16(W), orc.f32_to_bf16(np.zeros(E, np.float32)), E, H, k)
+    assert list(idx[0]) == [1, 2, 3, 5]
+    np.testing.assert_allclose(sc[0], 0.25)
+
+
+def test_router_matches_hf(orc, golden):
+    x, W, b = (orc.f32_to_bf16(golden[k]) for k in ("router_x", "router_w", "router_b"))
+    idx, sc, lg = orc.router(x, W, b, 8, 64, 4)
+    np.testing.assert_allclose(lg, golden["router_logits"], rtol=1e-5, atol=1e-6)
+    assert np.array_equal(idx, golden["router_idx"])
+    np.testing.assert_allclose(sc, golden["router_scores"], rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU with clamp / experts
+# ---------------------------------------------------------------------------
+def test_swiglu_special_cases(orc):
+    alpha, lim = 1.702, 7.0
+    sig = lambda z: 1.0 / (1.0 + math.exp(-z))
+    cases = [  # (gate, up) -> expected
+        (10.0, 0.0, 7.0 * sig(7.0 * alpha)),          # gate clamped above at 7
+        (-10.0, 0.0, -10.0 * sig(-10.0 * alpha)),     # no lower clamp on gate
+        (1.0, 20.0, 8.0 * sig(alpha)),                # up clamped to 7 -> (7+1)
+        (1.0, -20.0, -6.0 * sig(alpha)),              # up clamped to -7 -> (-7+1)
+        (0.0, 3.0, 0.0),
+    ]
+    gu = np.array([v for g, u, _ in cases for v in (g, u)], np.float32)
+    out = orc.swiglu(gu, alpha, lim)
+    np.testing.assert_allclose(out, [e for *_, e in cases], rtol=1e-6, atol=1e-7)
+
+
+def test_swiglu_matches_hf(orc, golden):
+    out = orc.swiglu(golden["experts_gate_up_e0"][0])
+    np.testing.assert_allclose(out, golden["experts_glu_e0"][0], rtol=1e-5, atol=1e-5)
+
+
+def test_expert_composition_matches_hf(orc, golden):
+    """gate_up -> SwiGLU -> bf16 -> down -> weighted sum, with the HF
+    routing fixed (the oracle's or_moe_layer composes the same pieces)."""
+    g = golden
+    xs = orc.f32_to_bf16(g["experts_x"])
+    out = np.zeros((3, 64))
+    for t in range(3):
+        for e, w in zip(g["experts_idx"][t], g["experts_w"][t]):
+            _, gu = orc.mxfp4_gemv(g["experts_gu_blocks"][e].reshape(-1),
+                                   g["experts_gu_scales"][e].reshape(-1),
+                                   orc.f32_to_bf16(g["experts_gu_bias"][e]), xs[t], 128, 64)
+            act = orc.f32_to_bf16(orc.swiglu(gu[0]))
+            _, dn = orc.mxfp4_gemv(g["experts_dn_blocks"][e].reshape(-1),
+                                   g["experts_dn_scales"][e].reshape(-1),
+                                   orc.f32_to_bf16(g["experts_dn_bias"][e]), act, 64, 64)
+            out[t] += w * dn[0]
+    ref = g["experts_out"]
+    # the only deviation is the bf16 rounding of the SwiGLU output
+    assert np.max(np.abs(out - ref)) <= 1e-2 * np.max(np.abs(ref))
+
+
+def test_moe_layer_composes_router_and_experts(orc):
+    rng = np.random.default_rng(2)
+    B, E, H, I, k = 2, 8, 64, 64, 3
+    x = orc.f32_to_bf16(rng.standard_normal((B, H)).astype(np.float32))
+    rw = orc.f32_to_bf16(0.2 * rng.standard_normal((E, H)).astype(np.float32))
+    rb = orc.f32_to_bf16(0.1 * rng.standard_normal(E).astype(np.float32))
+    guc = rng.integers(0, 256, E * 2 * I * H // 2, dtype=np.uint8)
+    gus = rng.integers(119, 125, E * 2 * I * H // 32, dtype=np.uint8)
+    gub = orc.f32_to_bf16(0.1 * rng.standard_normal(E * 2 * I).astype(np.float32))
+    dnc = rng.integers(0, 256, E * H * I // 2, dtype=np.uint8)
+    dns = rng.integers(119, 125, E * H * I // 32, dtype=np.uint8)
+    dnb = orc.f32_to_bf16(0.1 * rng.standard_normal(E * H).astype(np.float32))
+    out, idx, sc = orc.moe_layer(x, rw, rb, guc, gus, gub, dnc, dns, dnb, E, H, I, k)
+    ridx, rsc, _ = orc.router(x, rw, rb, E, H, k)
+    assert np.array_equal(idx, ridx) and np.array_equal(sc, rsc)
+    gsz, gss, dsz, dss = 2 * I * H // 2, 2 * I * H // 32, H * I // 2, H * I // 32
+    for r in range(B):
+        acc = np.zeros(H, np.float32)
+        for t in range(k):
+            e = idx[r, t]
+            _, gu = orc.mxfp4_gemv(guc[e * gsz:(e + 1) * gsz], gus[e * gss:(e + 1) * gss],
+                                   gub[e * 2 * I:(e + 1) * 2 * I], x[r], 2 * I, H)
+            act = orc.f32_to_bf16(orc.swiglu(gu[0]))
+            _, dn = orc.mxfp4_gemv(dnc[e * dsz:(e + 1) * dsz], dns[e * dss:(e + 1) * dss],
+                                   dnb[e * H:(e + 1) * H], act, H, I)
+            acc += np.float32(sc[r, t]) * dn[0]
+        assert np.array_equal(out[r], orc.f32_to_bf16(acc))
+
+
+# ---------------------------------------------------------------------------
+# attention with sinks
+# ---------------------------------------------------------------------------
+def naive_attn(q, k, v, sink, window):
+    T = k.shape[0]
+    lo = max(0, T - window) if window else 0
+    s = (k[lo:] @ q) / math.sqrt(q.shape[0])
+    m = max(s.max(), sink)
+    p = np.exp(s - m)
+    return (p @ v[lo:]) / (p.sum() + math.exp(sink - m))
+
+
+@pytest.mark.parametrize("T,window", [(1, 0), (7, 0), (300, 0), (300, 128), (100, 128), (129, 128)])
+def test_attn_vs_naive_fp64(orc, T, window):
+    rng = np.random.default_rng(T + window)
+    B, Hq, Hkv, D, Tm = 2, 8, 2, 64, 320
+    q = orc.f32_to_bf16(rng.standard_normal((B, Hq, D)).astype(np.float32))
+    kc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    sinks = orc.f32_to_bf16(rng.standard_normal(Hq).astype(np.float32))
+    pos = np.array([T - 1, max(0, T - 3)], np.int32)
+    _, of = orc.attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, window)
+    qf, kf, vf, sf = (orc.bf16_to_f32(a).astype(np.float64) for a in (q, kc, vc, sinks))
+    for b in range(B):
+        for h in range(Hq):
+            g = h // (Hq // Hkv)
+            n = pos[b] + 1
+            ref = naive_attn(qf[b, h], kf[b, g, :n], vf[b, g, :n], sf[h], window)
+            np.testing.assert_allclose(of[b].reshape(Hq, D)[h], ref, rtol=1e-5, atol=1e-6)
+
+
+def test_attn_special_cases(orc):
+    rng = np.random.default_rng(9)
+    Hq, Hkv, D, Tm = 8, 8, 64, 16
+    q = orc.f32_to_bf16(rng.standard_normal((1, Hq, D)).astype(np.float32))
+    kc = orc.f32_to_bf16(rng.standard_normal((1, Hkv, Tm, D)).astype(np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((1, Hkv, Tm, D)).astype(np.float32))
+    qf, kf, vf = (orc.bf16_to_f32(a).astype(np.float64) for a in (q, kc, vc))
+    # T = 1: weight 1 / (1 + e^(sink - s))
+    sinks = orc.f32_to_bf16(np.linspace(-2, 2, Hq).astype(np.float32))
+    _, of = orc.attn_decode(q, kc, vc, sinks, 1, Hq, Hkv, D, Tm, np.array([0], np.int32), 0)
+    for h in range(Hq):
+        s = qf[0, h] @ kf[0, h, 0] / 8.0
+        w = 1.0 / (1.0 + math.exp(orc.bf16_to_f32(sinks)[h] - s))
+        np.testing.assert_allclose(of[0].reshape(Hq, D)[h], w * vf[0, h, 0], rtol=1e-5, atol=1e-7)
+    # sink = -inf reduces to plain softmax attention
+    ninf = np.full(Hq, 0xFF80, np.uint16)
+    _, of = orc.attn_decode(q, kc, vc, ninf, 1, Hq, Hkv, D, Tm, np.array([9], np.int32), 0)
+    for h in range(Hq):
+        s = kf[0, h, :10] @ qf[0, h] / 8.0
+        p = np.exp(s - s.max())
+        np.testing.assert_allclose(of[0].reshape(Hq, D)[h], (p / p.sum()) @ vf[0, h, :10],
+                                   rtol=1e-5, atol=1e-7)
+    # sliding: keys before the window contribute exactly nothing
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[0, :, :5] = 0x7F00  # huge keys/values outside a 4-wide window at pos 8
+    vc2[0, :, :5] = 0x7F00
+    a, _ = orc.attn_decode(q, kc, vc, sinks, 1, Hq, Hkv, D, Tm, np.array([8], np.int32), 4)
+    b, _ = orc.attn_decode(q, kc2, vc2, sinks, 1, Hq, Hkv, D, Tm, np.array([8], np.int32), 4)
+    assert np.array_equal(a, b)
+
+
+def test_attn_matches_hf(orc, golden):
+    g = golden
+    q, k, v = (orc.f32_to_bf16(g[n]) for n in ("attn_q", "attn_k", "attn_v"))
+    sinks = orc.f32_to_bf16(g["attn_sinks"])
+    T = k.shape[1]
+    pos = np.array([T - 1], np.int32)
+    for name, window in (("full", 0), ("sliding", int(g["attn_window"][0]))):
+        _, of = orc.attn_decode(q[None], k[None], v[None], sinks, 1, 8, 2, 64, T, pos, window)
+        np.testing.assert_allclose(of.reshape(8, 64), g[f"attn_out_{name}"], rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# RNG (shared bit-for-bit with the device init)
+# ---------------------------------------------------------------------------
+def test_rng_statistics_and_determinism(orc):
+    a = orc.fill_bf16(0, 1234, 1 << 20, 0.0, 0.02)
+    assert np.array_equal(a, orc.fill_bf16(0, 1234, 1 << 20, 0.0, 0.02))
+    assert not np.array_equal(a, orc.fill_bf16(1, 1234, 1 << 20, 0.0, 0.02))
+    assert not np.array_equal(a, orc.fill_bf16(0, 1235, 1 << 20, 0.0, 0.02))
+    f = orc.bf16_to_f32(a)
+    assert abs(f.mean()) < 1e-4 and abs(f.std() - 0.02) < 2e-4
+    n = orc.bf16_to_f32(orc.fill_bf16(0, 7, 1 << 18, 1.0, 0.05))
+    assert abs(n.mean() - 1.0) < 1e-3 and abs(n.std() - 0.05) < 1e-3
+    sc = orc.fill_scales(0, 9, 1 << 18)
+    assert sc.min() == 119 and sc.max() == 124
+    assert np.all(np.abs(np.bincount(sc)[119:] / sc.size - 1 / 6) < 0.01)
+    by = orc.fill_bytes(0, 10, 1 << 18)
+    nib = np.concatenate([by & 15, by >> 4])
+    assert np.all(np.abs(np.bincount(nib, minlength=16) / nib.size - 1 / 16) < 0.01)
+    # the first bytes are the little-endian bytes of hash(seed, stream, 0)
+    h = orc.hash64(0, 10, 0)
+    assert list(by[:8]) == [(h >> (8 * j)) & 255 for j in range(8)]
+
+
+# ---------------------------------------------------------------------------
+# full model
+# ---------------------------------------------------------------------------
+def test_model_matches_hf(orc, golden):
+    g = golden
+    names = ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "n_experts", "top_k",
+             "intermediate", "vocab", "sliding_window", "max_seq")
+    cfg = orc.make_config(**dict(zip(names, (int(v) for v in g["model_cfg"]))), max_batch=1)
+    m = orc.Model(cfg, seed=int(g["model_seed"][0]), batch=1)
+    ours = np.stack([m.step(np.array([t]))[1][0] for t in g["model_ids"]])
+    m.close()
+    ref = g["model_logits"]
+    # HF runs in fp32 end to end; the oracle rounds activations to bf16 at the
+    # model's storage points, which bounds the difference at the 1e-2 scale.
+    # Where HF's own router has a near-tie between the k-th and (k+1)-th
+    # expert (margin < 0.01, far below the bf16 noise of the router input),
+    # the discrete expert choice is ill-conditioned and that position is
+    # excused; every other position must agree.
+    k = int(g["model_cfg"][6])
+    rs = np.sort(g["model_router_logits"], axis=-1)          # [L][T][E]
+    margin = (rs[..., -k] - rs[..., -k - 1]).min(axis=0)     # [T]
+    ok = margin >= 1e-2
+    assert ok.sum() >= len(ok) - 2
+    err = np.abs(ours - ref).max(axis=1) / np.abs(ref).max(axis=1)
+    assert np.all(err[ok] < 3e-2), err
+    lt = np.sort(ref, 1)[:, -2:]
+    lmargin = (lt[:, 1] - lt[:, 0]) / np.abs(ref).max(axis=1)
+    agree = np.argmax(ours, 1) == np.argmax(ref, 1)
+    assert np.all((agree | (lmargin < 3e-2))[ok])
+
+
+def test_model_deterministic_and_batched(orc):
+    cfg = orc.make_config(n_layers=2, hidden=128, n_heads=8, n_kv_heads=2, n_experts=4, top_k=2,
+                          intermediate=128, vocab=512, sliding_window=4, max_seq=16, max_batch=2)
+    m1 = orc.Model(cfg, seed=3, batch=2)
+    m2 = orc.Model(cfg, seed=3, batch=1)
+    ids = np.array([10, 20], np.int32)
+    for _ in range(6):
+        a, la = m1.step(ids)
+        b, lb = m2.step(ids[:1])
+        assert a[0] == b[0] and np.array_equal(la[0], lb[0])
+        ids = a
+    m1.close()
+    m2.close()
