@@ -104,6 +104,19 @@ neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
 /* Synchronises and copies the fp32 logits of the last step [batch][vocab]. */
 neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream);
 
+/* Synchronises and copies one activation buffer of the last step (for
+ * parity tests of the fused chain; "last layer" = the final decoder layer):
+ *   "hidden"    residual stream before the final norm, bf16 [batch][hidden]
+ *   "qkv"       last layer's q/k/v projection (before RoPE), bf16
+ *               [batch][(n_heads + 2 n_kv_heads) head_dim]
+ *   "attn_out"  last layer's attention output, bf16 [batch][n_heads head_dim]
+ *   "moe_in"    last layer's normalised MoE input, bf16 [batch][hidden]
+ *   "moe_idx"   last layer's expert ids, int32 [batch][top_k]
+ *   "moe_score" last layer's routing weights, fp32 [batch][top_k]
+ * `bytes` must equal the buffer's size. */
+neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
+                                 size_t bytes, void* stream);
+
 /* Number of tokens held by each sequence (prompt + generated). */
 neon_status neon_seq_len(const neon_ctx* ctx, int* out);
 

@@ -27,7 +27,8 @@ STATUS_NAMES = {0: "NEON_OK", 1: "NEON_EINVAL", 2: "NEON_ENOMEM", 3: "NEON_EHIP"
 EXPORTS = (
     "neon_config_preset", "neon_ctx_create", "neon_ctx_destroy", "neon_last_error",
     "neon_init_random", "neon_load_tensor", "neon_prefill", "neon_decode",
-    "neon_read_tokens", "neon_read_logits", "neon_seq_len", "neon_tensor_ptr",
+    "neon_read_tokens", "neon_read_logits", "neon_read_activation", "neon_seq_len",
+    "neon_tensor_ptr",
     "neon_mxfp4_dequant", "neon_mxfp4_gemv", "neon_gemv_bf16", "neon_rmsnorm",
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
     "neon_attn_decode",
@@ -77,6 +78,7 @@ def lib():
             "neon_decode": [_P, _I, _P],
             "neon_read_tokens": [_P, _I, _I, _P, _P],
             "neon_read_logits": [_P, _P, _P],
+            "neon_read_activation": [_P, C.c_char_p, _P, _SZ, _P],
             "neon_seq_len": [_P, _P],
             "neon_tensor_ptr": [_P, C.c_char_p, _P, _P],
             "neon_mxfp4_dequant": [_P, _P, _I64, _P, _P],
@@ -267,6 +269,23 @@ class Engine:
         self._chk(lib().neon_read_tokens(self._ctx, start, count,
                                          out.ctypes.data_as(C.c_void_p), _stream(stream)))
         return out
+
+    def read_activation(self, name: str, stream=None):
+        """One activation buffer of the last step (see neon_read_activation)."""
+        import numpy as np
+        c = self.cfg
+        width = {"hidden": c.hidden, "moe_in": c.hidden, "moe_idx": c.top_k,
+                 "moe_score": c.top_k, "qkv": (c.n_heads + 2 * c.n_kv_heads) * c.head_dim,
+                 "attn_out": c.n_heads * c.head_dim}[name]
+        dt = {"moe_idx": np.int32, "moe_score": np.float32}.get(name, np.uint16)
+        out = np.empty((self.batch, width), dt)
+        self._chk(lib().neon_read_activation(self._ctx, name.encode(),
+                                             out.ctypes.data_as(C.c_void_p), out.nbytes,
+                                             _stream(stream)))
+        return out
+
+    def read_hidden(self, stream=None):
+        return self.read_activation("hidden", stream)
 
     def read_logits(self, stream=None):
         import numpy as np

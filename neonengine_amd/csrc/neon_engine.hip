@@ -660,6 +660,31 @@ extern "C" neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream)
   return NEON_OK;
 }
 
+extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
+                                            void* out, size_t bytes, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (!name || !out) FAIL(ctx, NEON_EINVAL, "neon_read_activation: null argument");
+  if (ctx->batch == 0) FAIL(ctx, NEON_ESTATE, "neon_read_activation: no step has run");
+  const neon_config& c = ctx->cfg;
+  const size_t B = ctx->batch;
+  const void* src = nullptr;
+  size_t n = 0;
+  const std::string nm(name);
+  if (nm == "hidden") { src = ctx->h; n = B * c.hidden * 2; }
+  else if (nm == "qkv") { src = ctx->qkv; n = B * (c.n_heads + 2 * c.n_kv_heads) * c.head_dim * 2; }
+  else if (nm == "attn_out") { src = ctx->attn_out; n = B * c.n_heads * c.head_dim * 2; }
+  else if (nm == "moe_in") { src = ctx->xn; n = B * c.hidden * 2; }
+  else if (nm == "moe_idx") { src = ctx->moe_idx; n = B * c.top_k * 4; }
+  else if (nm == "moe_score") { src = ctx->moe_score; n = B * c.top_k * 4; }
+  else FAIL(ctx, NEON_EINVAL, "neon_read_activation: unknown buffer '%s'", name);
+  if (bytes != n)
+    FAIL(ctx, NEON_EINVAL, "neon_read_activation: '%s' holds %zu bytes, %zu requested", name, n, bytes);
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipStreamSynchronize(S(stream)));
+  HIPCHK(ctx, hipMemcpy(out, src, n, hipMemcpyDeviceToHost));
+  return NEON_OK;
+}
+
 extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
   if (!ctx || !out) return NEON_EINVAL;
   *out = ctx->host_pos + (ctx->batch ? 1 : 0);

@@ -192,8 +192,8 @@ __device__ __forceinline__ float bf16_row_partial(const uint4 (&w)[P],
 
 // Block-wide: x[K] (bf16, global) -> LDS, optionally RMS-normalised with
 // weight nw (HFM:57-62: fp32 x * rsqrt(mean(x^2) + eps), times the weight in
-// fp32, one rounding to bf16).  If xn_out is not NULL, block 0 also writes the
-// normalised vector to global memory.
+// fp32, one rounding to bf16).  If xn_out is not NULL the block also writes
+// the normalised vector there (callers pass it from one block per row only).
 __device__ void block_load_x(uint4* __restrict__ xs,
                              const uint16_t* __restrict__ x,
                              const uint16_t* __restrict__ nw, float eps, int K,
@@ -236,8 +236,7 @@ __device__ void block_load_x(uint4* __restrict__ xs,
                        bf_hi(b4[j]) * (bf_hi(a4[j]) * r));
     const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
     xs[i] = o;
-    if (xn_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0)
-      reinterpret_cast<uint4*>(xn_out)[i] = o;
+    if (xn_out != nullptr) reinterpret_cast<uint4*>(xn_out)[i] = o;
   }
   __syncthreads();
 }

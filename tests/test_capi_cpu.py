@@ -66,6 +66,7 @@ def test_context_calls_reject_null_context():
     assert L.neon_decode(None, 1, None) == ne.NEON_EINVAL
     assert L.neon_read_tokens(None, 0, 1, None, None) == ne.NEON_EINVAL
     assert L.neon_read_logits(None, None, None) == ne.NEON_EINVAL
+    assert L.neon_read_activation(None, b"hidden", None, 0, None) == ne.NEON_EINVAL
     assert L.neon_seq_len(None, None) == ne.NEON_EINVAL
     L.neon_ctx_destroy(None)  # no-op
 

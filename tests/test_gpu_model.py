@@ -53,14 +53,13 @@ def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
         nxt, lg_o = m.step(ids_o)
     o_tokens = [nxt.copy()]
     o_logits = [lg_o]
-    margins = []
     for _ in range(n_steps):
-        top2 = np.sort(lg_o, axis=1)[:, -2:]
-        margins.append(top2[:, 1] - top2[:, 0])
         nxt, lg_o = m.step(nxt)
         o_tokens.append(nxt.copy())
         o_logits.append(lg_o)
     m.close()
+    # margins[b, t]: top-2 gap of the logits that produced generated token t
+    margins = np.stack([np.diff(np.sort(lg, axis=1)[:, -2:], axis=1)[:, 0] for lg in o_logits], 1)
     eng.prefill(prompt)
     g_first_logits = eng.read_logits()
     eng.decode(n_steps)
@@ -70,12 +69,11 @@ def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
     n = len(prompt[0])
     gen_g = toks[:, n:]
     gen_o = np.stack(o_tokens, 1)[:, : n_steps + 1]
-    margins = np.stack(margins, 1)
     same = gen_g == gen_o
     if not same.all():
         b, t = np.argwhere(~same)[0]
         say(f"first divergence row {b} step {t}: gpu {gen_g[b, t]} oracle {gen_o[b, t]}, "
-            f"oracle top-2 margin there {margins[b, t - 1] if t else 'n/a'}")
+            f"oracle top-2 margin there {margins[b, t]:.4g}")
     say(f"  min oracle top-2 margin over the run: {margins.min():.4g}")
     e1 = logits_close(g_first_logits, o_logits[0])
     e2 = logits_close(g_last_logits, o_logits[n_steps]) if same.all() else 0.0
