@@ -35,47 +35,107 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
 }
 
-// acc + a.lo*b.lo + a.hi*b.hi  (v_dot2_f32_bf16)
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
-                                         __builtin_bit_cast(bf16x2_t, b), acc,
-                                         false);
-}
-// 8 bf16 x 8 bf16
-__device__ __forceinline__ float dot8_bf16(const uint4& w, const uint4& x,
+// ---- canonical dot products ---------------------------------------------
+// Every reduction on the decode path uses one fixed order of IEEE fp32 fused
+// multiply-adds so the CPU oracle (oracle/neon_oracle.c, or_c_* functions)
+// reproduces it bit for bit.  (v_dot2_f32_bf16 is not used: on gfx950 its
+// result is not the correctly rounded 3-term sum, so it cannot be mirrored.)
+
+// 8 bf16 weights x 8 fp32 x values, element order 0..7, one fmaf each.
+__device__ __forceinline__ float fma8_bf16(const uint4& w, const float* x,
                                            float acc) {
-  acc = dot2_bf16(w.x, x.x, acc);
-  acc = dot2_bf16(w.y, x.y, acc);
-  acc = dot2_bf16(w.z, x.z, acc);
-  acc = dot2_bf16(w.w, x.w, acc);
+  acc = __builtin_fmaf(bf_lo(w.x), x[0], acc);
+  acc = __builtin_fmaf(bf_hi(w.x), x[1], acc);
+  acc = __builtin_fmaf(bf_lo(w.y), x[2], acc);
+  acc = __builtin_fmaf(bf_hi(w.y), x[3], acc);
+  acc = __builtin_fmaf(bf_lo(w.z), x[4], acc);
+  acc = __builtin_fmaf(bf_hi(w.z), x[5], acc);
+  acc = __builtin_fmaf(bf_lo(w.w), x[6], acc);
+  acc = __builtin_fmaf(bf_hi(w.w), x[7], acc);
+  return acc;
+}
+// 8 bf16 x 8 bf16 (both packed), element order 0..7.
+__device__ __forceinline__ float fma8_bf16x2(const uint4& w, const uint4& x,
+                                             float acc) {
+  acc = __builtin_fmaf(bf_lo(w.x), bf_lo(x.x), acc);
+  acc = __builtin_fmaf(bf_hi(w.x), bf_hi(x.x), acc);
+  acc = __builtin_fmaf(bf_lo(w.y), bf_lo(x.y), acc);
+  acc = __builtin_fmaf(bf_hi(w.y), bf_hi(x.y), acc);
+  acc = __builtin_fmaf(bf_lo(w.z), bf_lo(x.z), acc);
+  acc = __builtin_fmaf(bf_hi(w.z), bf_hi(x.z), acc);
+  acc = __builtin_fmaf(bf_lo(w.w), bf_lo(x.w), acc);
+  acc = __builtin_fmaf(bf_hi(w.w), bf_hi(x.w), acc);
   return acc;
 }
 
 // ---- MXFP4 -----------------------------------------------------------------
-// Two E2M1 values of byte `sel` of `w` as a bf16 pair (lo = low nibble),
-// unscaled (v_cvt_scalef32_pk_bf16_fp4 with scale 1.0: exact).
+typedef float float2_v __attribute__((ext_vector_type(2)));
+// E2M1 values of byte `SEL` of `w` (x = low nibble = even element), exact
+// (v_cvt_scalef32_pk_f32_fp4 with scale 1.0).
 template <int SEL>
-__device__ __forceinline__ uint32_t fp4x2_to_bf16x2(uint32_t w) {
-  bf16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, SEL);
-  return __builtin_bit_cast(uint32_t, r);
+__device__ __forceinline__ float2_v fp4x2_to_f32(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, SEL);
 }
-// 32 E2M1 values (16 bytes) dotted with 32 bf16 x values (4 x uint4).
-__device__ __forceinline__ float fp4_unit_dot(const uint4& c, const uint4* x) {
+// Canonical MXFP4 unit (32 elements, 16 code bytes): t = fmaf chain over the
+// 32 elements in increasing k of E2M1(code) * x, starting from 0.
+__device__ __forceinline__ float fp4_unit_dot(const uint4& c, const float* x) {
   const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-  float acc = 0.0f;
+  float t = 0.0f;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    acc = dot2_bf16(fp4x2_to_bf16x2<0>(cw[q]), x[q].x, acc);
-    acc = dot2_bf16(fp4x2_to_bf16x2<1>(cw[q]), x[q].y, acc);
-    acc = dot2_bf16(fp4x2_to_bf16x2<2>(cw[q]), x[q].z, acc);
-    acc = dot2_bf16(fp4x2_to_bf16x2<3>(cw[q]), x[q].w, acc);
+    float2_v v0 = fp4x2_to_f32<0>(cw[q]), v1 = fp4x2_to_f32<1>(cw[q]);
+    float2_v v2 = fp4x2_to_f32<2>(cw[q]), v3 = fp4x2_to_f32<3>(cw[q]);
+    t = __builtin_fmaf(v0.x, x[8 * q + 0], t);
+    t = __builtin_fmaf(v0.y, x[8 * q + 1], t);
+    t = __builtin_fmaf(v1.x, x[8 * q + 2], t);
+    t = __builtin_fmaf(v1.y, x[8 * q + 3], t);
+    t = __builtin_fmaf(v2.x, x[8 * q + 4], t);
+    t = __builtin_fmaf(v2.y, x[8 * q + 5], t);
+    t = __builtin_fmaf(v3.x, x[8 * q + 6], t);
+    t = __builtin_fmaf(v3.y, x[8 * q + 7], t);
   }
-  return acc;
+  return t;
 }
-// v * 2^(s - 127); E8M0 0xFF is NaN.
+// v * 2^(s - 127) (exact, IEEE ldexp); E8M0 0xFF is NaN.
 __device__ __forceinline__ float e8m0_scale(float v, uint32_t s) {
   float r = __builtin_amdgcn_ldexpf(v, (int)s - 127);
   return s == 0xFFu ? __builtin_nanf("") : r;
+}
+
+// ---- correctly rounded square root for positive normal x: the hardware
+// estimate (v_sqrt_f32, within 1 ulp) corrected by one step that compares x
+// with s_dn * s and s_up * s through exact fused residuals (the candidate
+// whose half-ulp interval contains sqrt(x) wins).  Equal to IEEE sqrtf.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  float s = __builtin_amdgcn_sqrtf(x);
+  const float s_dn = __builtin_bit_cast(float, __builtin_bit_cast(int32_t, s) - 1);
+  const float s_up = __builtin_bit_cast(float, __builtin_bit_cast(int32_t, s) + 1);
+  const float r_dn = __builtin_fmaf(-s_dn, s, x);
+  const float r_up = __builtin_fmaf(-s_up, s, x);
+  s = (r_dn <= 0.0f) ? s_dn : s;
+  s = (r_up > 0.0f) ? s_up : s;
+  return s;
+}
+
+// ---- exp: Cody-Waite reduction by ln 2 (two-part constant) and a degree-7
+// Taylor polynomial in Horner form, all fp32 fmaf.  The oracle evaluates the
+// same operation sequence, so both sides agree bit for bit.
+__host__ __device__ __forceinline__ float neon_expf(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e43p+6f) return __builtin_inff();
+  if (x < -0x1.9fe36ap+6f) return 0.0f;
+  const float n = __builtin_rintf(x * 0x1.715476p+0f);
+  float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
+  r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
+  p = __builtin_fmaf(p, r, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-5f);
+  p = __builtin_fmaf(p, r, 0x1.555556p-3f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
 }
 
 // ---- wave reductions (xor butterfly over 64 lanes) ------------------------

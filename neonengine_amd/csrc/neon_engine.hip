@@ -58,7 +58,7 @@ struct neon_ctx {
   std::vector<LayerW> layers;
   uint16_t *embed = nullptr, *lm_head = nullptr, *final_norm = nullptr;
   // rope
-  float *cos_t = nullptr, *sin_t = nullptr, *inv_freq = nullptr;
+  float *cos_t = nullptr, *sin_t = nullptr;
   // KV cache [L][max_batch][Hkv][max_seq][D]
   uint16_t *kc = nullptr, *vc = nullptr;
   size_t kv_layer_elems = 0;
@@ -183,6 +183,27 @@ static void yarn_inv_freq(const neon_config* c, std::vector<float>& invf,
   *af = factor <= 1.0 ? 1.0 : 0.1 * std::log(factor) + 1.0;
 }
 
+// cos/sin tables [n_pos][head_dim/2] in fp32: angle = fp32(inv_freq) *
+// fp32(pos) (HFM:196-198), cos/sin in fp64 rounded to fp32, times the fp32
+// attention factor.  Built on the host so every position is identical to the
+// oracle's table.
+static void rope_table_host(const neon_config* c, int n_pos,
+                            std::vector<float>& ct, std::vector<float>& st) {
+  std::vector<float> invf;
+  double af;
+  yarn_inv_freq(c, invf, &af);
+  const float aff = (float)af;
+  const int half = c->head_dim / 2;
+  ct.resize((size_t)n_pos * half);
+  st.resize((size_t)n_pos * half);
+  for (int p = 0; p < n_pos; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float ang = invf[i] * (float)p;
+      ct[(size_t)p * half + i] = (float)std::cos((double)ang) * aff;
+      st[(size_t)p * half + i] = (float)std::sin((double)ang) * aff;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // context lifetime
 // ---------------------------------------------------------------------------
@@ -288,8 +309,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   HIPCHK(ctx, hipMemset(ctx->vc, 0, kv_bytes));
   // ---- activations / scratch ----
   const size_t Bm = c.max_batch, half = c.head_dim / 2;
-  ctx->s_slide = c.sliding_window > 0 ? std::max(1, std::min(8, (c.sliding_window + 63) / 64)) : 1;
-  ctx->s_full = std::max(1, std::min(32, (c.max_seq + 63) / 64));
+  ctx->s_slide = attn_splits(c.max_seq, c.sliding_window);
+  ctx->s_full = attn_splits(c.max_seq, 0);
   const int smax = std::max(ctx->s_full, ctx->s_slide);
   const int G = c.n_heads / c.n_kv_heads;
   ctx->lm_nblk = gemv_default_grid(c.vocab, 4);
@@ -308,7 +329,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
                o_pl = take(Bm * 4), o_last = take(Bm * 4),
                o_cos = take((size_t)c.max_seq * half * 4),
-               o_sin = take((size_t)c.max_seq * half * 4), o_if = take(half * 4);
+               o_sin = take((size_t)c.max_seq * half * 4);
   if (hipMalloc(&ctx->work, off) != hipSuccess) {
     ctx->work = nullptr;
     FAIL(ctx, NEON_ENOMEM, "hipMalloc of %zu scratch bytes failed", off);
@@ -324,15 +345,12 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
   ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
-  ctx->sin_t = (float*)(W + o_sin); ctx->inv_freq = (float*)(W + o_if);
+  ctx->sin_t = (float*)(W + o_sin);
   // ---- RoPE table ----
-  std::vector<float> invf;
-  double af;
-  yarn_inv_freq(&c, invf, &af);
-  HIPCHK(ctx, hipMemcpy(ctx->inv_freq, invf.data(), half * 4, hipMemcpyHostToDevice));
-  launch_rope_table(ctx->inv_freq, (float)af, c.max_seq, (int)half, ctx->cos_t,
-                    ctx->sin_t, nullptr);
-  HIPCHK(ctx, hipGetLastError());
+  std::vector<float> ct, st;
+  rope_table_host(&c, c.max_seq, ct, st);
+  HIPCHK(ctx, hipMemcpy(ctx->cos_t, ct.data(), ct.size() * 4, hipMemcpyHostToDevice));
+  HIPCHK(ctx, hipMemcpy(ctx->sin_t, st.data(), st.size() * 4, hipMemcpyHostToDevice));
   HIPCHK(ctx, hipDeviceSynchronize());
   HIPCHK(ctx, hipStreamCreateWithFlags(&ctx->cap_stream, hipStreamNonBlocking));
   return NEON_OK;
@@ -762,25 +780,23 @@ extern "C" neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok
       !(cfg->rope_factor >= 1.0f) || cfg->rope_orig_max_pos < 1)
     KFAIL(NEON_EINVAL, "neon_rope_yarn: bad shape or rope parameters");
   // Positions must lie in [0, cfg->max_seq); the table is built for that range.
-  std::vector<float> invf;
-  double af;
-  yarn_inv_freq(cfg, invf, &af);
+  std::vector<float> ct, stb;
+  rope_table_host(cfg, cfg->max_seq, ct, stb);
   const int half = cfg->head_dim / 2;
-  float *tab = nullptr;
-  const size_t tb = ((size_t)cfg->max_seq * half * 2 + half) * 4;
-  if (hipMallocAsync((void**)&tab, tb, S(stream)) != hipSuccess)
+  float* tab = nullptr;
+  const size_t tn = (size_t)cfg->max_seq * half;
+  if (hipMallocAsync((void**)&tab, tn * 2 * 4, S(stream)) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_rope_yarn: table allocation failed");
-  float* ct = tab;
-  float* stt = tab + (size_t)cfg->max_seq * half;
-  float* dinv = stt + (size_t)cfg->max_seq * half;
-  if (hipMemcpyAsync(dinv, invf.data(), half * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess)
+  if (hipMemcpyAsync(tab, ct.data(), tn * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess ||
+      hipMemcpyAsync(tab + tn, stb.data(), tn * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess)
     KFAIL(NEON_EHIP, "neon_rope_yarn: copy failed");
-  launch_rope_table(dinv, (float)af, cfg->max_seq, half, ct, stt, S(stream));
-  launch_rope_apply(x, pos, ct, stt, n_tok, n_heads, cfg->head_dim, S(stream));
-  if (hipStreamSynchronize(S(stream)) != hipSuccess)
+  launch_rope_apply(x, pos, tab, tab + tn, n_tok, n_heads, cfg->head_dim, S(stream));
+  hipError_t e = hipGetLastError();
+  if (hipStreamSynchronize(S(stream)) != hipSuccess)  // host tables die here
     KFAIL(NEON_EHIP, "neon_rope_yarn: synchronize failed");
   (void)hipFreeAsync(tab, S(stream));
-  KLAUNCHED();
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_rope_yarn: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
 }
 
 extern "C" neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
@@ -869,8 +885,7 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
     KFAIL(NEON_EINVAL, "neon_attn_decode: Hq/Hkv must be 1, 2, 4 or 8");
   // pos[b] must lie in [0, T_max); it is device data, so the kernel trusts it.
   hipStream_t st = S(stream);
-  const int span = window > 0 ? std::min(window, T_max) : T_max;
-  const int S_ = std::max(1, std::min(32, (span + 63) / 64));
+  const int S_ = attn_splits(T_max, window);
   char* scratch = nullptr;
   const size_t po = (size_t)B * Hkv * S_ * G * 64 * 4, pml = (size_t)B * Hkv * S_ * G * 2 * 4,
                cnt = (size_t)B * Hkv * 4;

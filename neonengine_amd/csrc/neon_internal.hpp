@@ -52,8 +52,6 @@ void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
                     int H, float eps, hipStream_t st);
 
 // ---- RoPE ---------------------------------------------------------------------
-void launch_rope_table(const float* inv_freq, float af, int n_pos, int half,
-                       float* cos_t, float* sin_t, hipStream_t st);
 void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
                        const float* sin_t, int n_tok, int n_heads, int D,
                        hipStream_t st);
@@ -91,5 +89,7 @@ struct AttnArgs {
   int B, Hq, Hkv, T_max, window, S, fused, q_stride;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
+// number of key splits used for a cache of T_max rows (window 0 = full layer)
+int attn_splits(int T_max, int window);
 
 }  // namespace neon

@@ -104,13 +104,26 @@ void launch_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
                      dim3(256), 0, st, codes, scales, nb, out);
 }
 
+
 // ===========================================================================
 // Shared GEMV machinery.  Lane l of a wave owns the 16-byte units
 // u = l + 64 p (p < P) of every row it processes; x for those units stays in
-// registers, so each weight byte is loaded exactly once, 1 KB contiguous per
-// wave instruction.  MXFP4 unit = 32 elements (16 B codes + 1 scale byte);
-// bf16 unit = 8 elements.
+// registers as fp32, so each weight byte is loaded exactly once, 1 KB
+// contiguous per wave instruction.  MXFP4 unit = 32 elements (16 B codes + 1
+// scale byte); bf16 unit = 8 elements.
+//
+// Canonical row dot (restated bit for bit by the oracle's or_c_* GEMVs):
+//   lane partial a_l, for p = 0..P-1, u = l + 64 p < U:
+//     bf16 : a = fmaf(w_k, x_k, a) for the unit's 8 elements in increasing k
+//     MXFP4: t = fmaf(E2M1_k, x_k, t) from t = 0 over the unit's 32 elements,
+//            then a = a + t * 2^(s_u - 127)   (exact scaling, one rounding)
+//   then the xor butterfly a_l = a_l + a_{l^off}, off = 32, 16, 8, 4, 2, 1.
 // ===========================================================================
+__device__ __forceinline__ void unpack8(const uint4& v, float* o) {
+  o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
+  o[4] = bf_lo(v.z); o[5] = bf_hi(v.z); o[6] = bf_lo(v.w); o[7] = bf_hi(v.w);
+}
+
 template <int P>
 struct Fp4Row {
   uint4 c[P];
@@ -137,16 +150,19 @@ __device__ __forceinline__ void fp4_load_row(Fp4Row<P>& r,
 
 template <int P>
 __device__ __forceinline__ float fp4_row_partial(const Fp4Row<P>& r,
-                                                 const uint4 (&xr)[P][4]) {
+                                                 const float (&xr)[P][32],
+                                                 int U, int lane) {
   float acc = 0.0f;
 #pragma unroll
-  for (int p = 0; p < P; ++p) acc += e8m0_scale(fp4_unit_dot(r.c[p], xr[p]), r.s[p]);
+  for (int p = 0; p < P; ++p)
+    if (lane + 64 * p < U)
+      acc = __fadd_rn(acc, e8m0_scale(fp4_unit_dot(r.c[p], xr[p]), r.s[p]));
   return acc;
 }
 
-// x (bf16 [K], LDS) -> per-lane registers for MXFP4 units
+// x (bf16 [K] in LDS) -> fp32 registers for the lane's MXFP4 units
 template <int P>
-__device__ __forceinline__ void fp4_load_x(uint4 (&xr)[P][4],
+__device__ __forceinline__ void fp4_load_x(float (&xr)[P][32],
                                            const uint4* __restrict__ xs, int U,
                                            int lane) {
 #pragma unroll
@@ -154,18 +170,18 @@ __device__ __forceinline__ void fp4_load_x(uint4 (&xr)[P][4],
     const int u = lane + 64 * p;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      xr[p][q] = (u < U) ? xs[u * 4 + q] : make_uint4(0, 0, 0, 0);
+      unpack8((u < U) ? xs[u * 4 + q] : make_uint4(0, 0, 0, 0), &xr[p][8 * q]);
   }
 }
 
 template <int P>
-__device__ __forceinline__ void bf16_load_x(uint4 (&xr)[P],
+__device__ __forceinline__ void bf16_load_x(float (&xr)[P][8],
                                             const uint4* __restrict__ xs,
                                             int U, int lane) {
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int u = lane + 64 * p;
-    xr[p] = (u < U) ? xs[u] : make_uint4(0, 0, 0, 0);
+    unpack8((u < U) ? xs[u] : make_uint4(0, 0, 0, 0), xr[p]);
   }
 }
 
@@ -183,22 +199,27 @@ __device__ __forceinline__ void bf16_load_row(uint4 (&w)[P],
 
 template <int P>
 __device__ __forceinline__ float bf16_row_partial(const uint4 (&w)[P],
-                                                  const uint4 (&xr)[P]) {
+                                                  const float (&xr)[P][8],
+                                                  int U, int lane) {
   float acc = 0.0f;
 #pragma unroll
-  for (int p = 0; p < P; ++p) acc = dot8_bf16(w[p], xr[p], acc);
+  for (int p = 0; p < P; ++p)
+    if (lane + 64 * p < U) acc = fma8_bf16(w[p], xr[p], acc);
   return acc;
 }
 
 // Block-wide: x[K] (bf16, global) -> LDS, optionally RMS-normalised with
-// weight nw (HFM:57-62: fp32 x * rsqrt(mean(x^2) + eps), times the weight in
-// fp32, one rounding to bf16).  If xn_out is not NULL the block also writes
-// the normalised vector there (callers pass it from one block per row only).
+// weight nw (HFM:57-62).  Canonical form (oracle or_c_rmsnorm): wave 0 forms
+// ss with lane partials ss = fmaf(x_k, x_k, ss) over the units
+// u = l + 64 p (8 elements each, increasing k) and the xor butterfly; then
+// r = 1 / sqrt(ss / K + eps) with correctly rounded fp32 division and square
+// root; y_k = bf16(w_k * (x_k * r)).  If xn_out is not NULL the block also
+// writes the normalised vector there (callers pass it from one block per row).
 __device__ void block_load_x(uint4* __restrict__ xs,
                              const uint16_t* __restrict__ x,
                              const uint16_t* __restrict__ nw, float eps, int K,
                              uint16_t* __restrict__ xn_out) {
-  __shared__ float red[16];
+  __shared__ float r_s;
   const int U8 = K / 8;
   const uint4* xv = reinterpret_cast<const uint4*>(x);
   if (nw == nullptr) {
@@ -206,34 +227,31 @@ __device__ void block_load_x(uint4* __restrict__ xs,
     __syncthreads();
     return;
   }
-  float ss = 0.0f;
-  for (int i = threadIdx.x; i < U8; i += blockDim.x) {
-    const uint4 v = xv[i];
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float ss = 0.0f;
+    for (int u = lane; u < U8; u += 64) {
+      float f[8];
+      unpack8(xv[u], f);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float a = bf_lo(w4[j]), b = bf_hi(w4[j]);
-      ss = fmaf(a, a, ss);
-      ss = fmaf(b, b, ss);
+      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
     }
+    ss = wave_sum(ss);
+    if (lane == 0)
+      r_s = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
   }
-  ss = wave_sum(ss);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) red[wave] = ss;
   __syncthreads();
-  float tot = 0.0f;
-  const int nwaves = blockDim.x >> 6;
-  for (int i = 0; i < nwaves; ++i) tot += red[i];
-  const float r = 1.0f / sqrtf(tot / (float)K + eps);
+  const float r = r_s;
   const uint4* wv = reinterpret_cast<const uint4*>(nw);
   for (int i = threadIdx.x; i < U8; i += blockDim.x) {
-    const uint4 v = xv[i], w = wv[i];
-    const uint32_t a4[4] = {v.x, v.y, v.z, v.w}, b4[4] = {w.x, w.y, w.z, w.w};
+    float a[8], b[8];
+    unpack8(xv[i], a);
+    unpack8(wv[i], b);
     uint32_t o4[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      o4[j] = pack_bf2(bf_lo(b4[j]) * (bf_lo(a4[j]) * r),
-                       bf_hi(b4[j]) * (bf_hi(a4[j]) * r));
+      o4[j] = pack_bf2(__fmul_rn(b[2 * j], __fmul_rn(a[2 * j], r)),
+                       __fmul_rn(b[2 * j + 1], __fmul_rn(a[2 * j + 1], r)));
     const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
     xs[i] = o;
     if (xn_out != nullptr) reinterpret_cast<uint4*>(xn_out)[i] = o;
@@ -244,9 +262,9 @@ __device__ void block_load_x(uint4* __restrict__ xs,
 constexpr int kMaxK = 8192;  // LDS holds x [K] bf16 (16 KB)
 
 // ===========================================================================
-// Standalone MXFP4 GEMV: y[b][n] = bf16(sum_k dq(W[n][k]) x[b][k] + bias[n]).
+// Standalone MXFP4 GEMV: y[b][n] = bf16(dot(W[n], x[b]) + bias[n]).
 // grid (ceil(N / (4 rpw)), 1, B), block 256; wave w of block i owns rows
-// [(4i + w) rpw, +rpw).  Next row's codes are loaded while the current row is
+// [(4i + w) rpw, +rpw).  The next row's codes load while the current row is
 // reduced.
 // ===========================================================================
 template <int P>
@@ -264,16 +282,16 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv(
     fp4_load_row<P>(cur, codes + (size_t)r0 * (K / 2), scales + (size_t)r0 * U,
                     U, lane);
   block_load_x(xs, x + (size_t)b * K, nullptr, 0.0f, K, nullptr);
-  uint4 xr[P][4];
+  float xr[P][32];
   fp4_load_x<P>(xr, xs, U, lane);
   for (int r = r0; r < r1; ++r) {
     Fp4Row<P> nxt;
     if (r + 1 < r1)
       fp4_load_row<P>(nxt, codes + (size_t)(r + 1) * (K / 2),
                       scales + (size_t)(r + 1) * U, U, lane);
-    float acc = wave_sum(fp4_row_partial<P>(cur, xr));
+    float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
     if (lane == 0) {
-      if (bias) acc += bf2f(bias[r]);
+      if (bias) acc = __fadd_rn(acc, bf2f(bias[r]));
       y[(size_t)b * N + r] = f2bf(acc);
     }
     cur = nxt;
@@ -306,11 +324,11 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
 
 // ===========================================================================
 // bf16 GEMV with fused prologue (optional RMSNorm of x) and epilogue:
-//   MODE_STORE : y[b][n] = bf16(acc + bias[n])
-//   MODE_RESID : y[b][n] = bf16(y[b][n] + bf16(acc + bias[n]))  (residual add,
+//   MODE_STORE : y[b][n] = bf16(dot + bias[n])
+//   MODE_RESID : y[b][n] = bf16(y[b][n] + bf16(dot + bias[n]))  (residual add,
 //                HFM:365,375)
-//   MODE_LOGITS: logits[b][n] = acc (fp32), plus the block's (max, argmax)
-//                written to part_val/part_idx [B][gridDim.x]
+//   MODE_LOGITS: logits[b][n] = dot (fp32), plus the block's (max, lowest
+//                argmax) written to part_val/part_idx [B][gridDim.x]
 // grid (nblk, 1, B), block 256; rows are grid-strided in groups of rpw per
 // wave so huge N (lm_head) runs on a bounded grid.
 // ===========================================================================
@@ -334,7 +352,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   uint4 cur[P];
   if (g < ngroups) bf16_load_row<P>(cur, W + (size_t)g * rpw * K, U, lane);
   block_load_x(xs, x + (size_t)b * K, nw, eps, K, nullptr);
-  uint4 xr[P];
+  float xr[P][8];
   bf16_load_x<P>(xr, xs, U, lane);
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
@@ -342,17 +360,18 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
     const int r0 = g * rpw, r1 = min(r0 + rpw, N);
     for (int r = r0; r < r1; ++r) {
       uint4 nxt[P];
-      const int rn = (r + 1 < r1) ? r + 1 : ((g + gstride < ngroups) ? (g + gstride) * rpw : -1);
+      const int rn = (r + 1 < r1) ? r + 1
+                                  : ((g + gstride < ngroups) ? (g + gstride) * rpw : -1);
       if (rn >= 0) bf16_load_row<P>(nxt, W + (size_t)rn * K, U, lane);
-      const float acc = wave_sum(bf16_row_partial<P>(cur, xr));
+      const float acc = wave_sum(bf16_row_partial<P>(cur, xr, U, lane));
       if (MODE == MODE_LOGITS) {
         if (acc > best_v) { best_v = acc; best_i = r; }
         if (lane == 0) logits[(size_t)b * N + r] = acc;
       } else if (lane == 0) {
-        const float v = acc + (bias ? bf2f(bias[r]) : 0.0f);
+        const float v = bias ? __fadd_rn(acc, bf2f(bias[r])) : acc;
         const size_t o = (size_t)b * N + r;
         if (MODE == MODE_STORE) y[o] = f2bf(v);
-        else y[o] = f2bf(bf2f(y[o]) + bf2f(f2bf(v)));
+        else y[o] = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
       }
 #pragma unroll
       for (int p = 0; p < P; ++p) cur[p] = nxt[p];
@@ -411,8 +430,9 @@ void launch_gemv_bf16(const GemvArgs& a, hipStream_t st) {
 
 // ===========================================================================
 // Final argmax over the lm_head partials; advances the sequence.
-// grid B, block 256.  tokens[b][pos+1] receives the greedy id unless that
-// slot still belongs to the prompt (teacher forcing); pos[b] += 1.
+// grid B, block 256.  Greedy id = largest logit, ties to the lowest index.
+// tokens[b][pos+1] receives it unless that slot still belongs to the prompt
+// (teacher forcing); pos[b] += 1.
 // ===========================================================================
 __global__ __launch_bounds__(256) void k_argmax_advance(
     const float* __restrict__ part_val, const int32_t* __restrict__ part_idx,
@@ -482,7 +502,7 @@ void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
 }
 
 // ===========================================================================
-// Standalone RMSNorm: out[b] = bf16(w * (x[b] * rsqrt(mean(x[b]^2) + eps)))
+// Standalone RMSNorm (canonical form of block_load_x)
 // ===========================================================================
 __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
                                                  const uint16_t* __restrict__ w,
@@ -490,9 +510,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
                                                  int H, float eps) {
   __shared__ uint4 xs[kMaxK / 8];
   const int b = blockIdx.x;
-  block_load_x(xs, x + (size_t)b * H, w, eps, H, nullptr);
-  uint4* dst = reinterpret_cast<uint4*>(out + (size_t)b * H);
-  for (int i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = xs[i];
+  block_load_x(xs, x + (size_t)b * H, w, eps, H, out + (size_t)b * H);
 }
 
 void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
@@ -501,29 +519,10 @@ void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
 }
 
 // ===========================================================================
-// YaRN RoPE table: cos/sin [n_pos][half] in fp32 (HFM:196-198; HF
-// modeling_rope_utils.py:429-483).  angle = fp32(inv_freq) * fp32(pos); cos
-// and sin evaluated in fp64, rounded to fp32, times the fp32 attention factor.
+// RoPE (HFM:215-222): half-split rotation with the host-built YaRN table
+// (cos/sin [n_pos][D/2] fp32, HF modeling_rope_utils.py:429-483):
+//   o1 = x1 c - x2 s,  o2 = x2 c + x1 s   (each product and sum rounded)
 // ===========================================================================
-__global__ void k_rope_table(const float* __restrict__ inv_freq, float af,
-                             int n_pos, int half, float* __restrict__ cos_t,
-                             float* __restrict__ sin_t) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)n_pos * half) return;
-  const int p = (int)(i / half), f = (int)(i % half);
-  const float ang = __fmul_rn(inv_freq[f], (float)p);
-  cos_t[i] = __fmul_rn((float)cos((double)ang), af);
-  sin_t[i] = __fmul_rn((float)sin((double)ang), af);
-}
-
-void launch_rope_table(const float* inv_freq, float af, int n_pos, int half,
-                       float* cos_t, float* sin_t, hipStream_t st) {
-  const int64_t n = (int64_t)n_pos * half;
-  hipLaunchKernelGGL(k_rope_table, dim3((unsigned)((n + 255) / 256)), dim3(256),
-                     0, st, inv_freq, af, n_pos, half, cos_t, sin_t);
-}
-
-// half-split rotation (HFM:215-222) of one head's pair (x1, x2)
 __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,
                                           float& o1, float& o2) {
   o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
@@ -560,17 +559,16 @@ void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
 }
 
 // ===========================================================================
-// Router (HFM:117-130), one block per batch row, 16 waves.  Optional fused
+// Router (HFM:117-130), one block per batch row, 8 waves.  Optional fused
 // RMSNorm prologue (then the normalised x is also written to xn_out for the
-// experts).  Logits use one canonical fp32 order, restated by the oracle:
-// lane l accumulates, with one fmaf per element in increasing k, the 8-element
-// units u = l + 64 i; then a xor butterfly over 32,16,8,4,2,1; then + bias.
-// Top-k by value with ties to the lower expert index; softmax over the k.
+// experts).  Logits: the canonical bf16 row dot + bias (fp32 add).  Top-k by
+// value, ties to the lower expert index; softmax over the k selected values:
+// e_t = exp(v_t - v_0) (neon_expf), s = sum in rank order, score_t = e_t / s.
 // ===========================================================================
 constexpr int kMaxExperts = 256;
 
 template <int P>
-__global__ __launch_bounds__(1024) void k_router(
+__global__ __launch_bounds__(512) void k_router(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
     const uint16_t* __restrict__ bias, int32_t* __restrict__ idx,
@@ -584,28 +582,12 @@ __global__ __launch_bounds__(1024) void k_router(
   const int U = H / 8;
   block_load_x(xs, x + (size_t)b * H, nw, eps, H,
                xn_out ? xn_out + (size_t)b * H : nullptr);
-  uint4 xr[P];
+  float xr[P][8];
   bf16_load_x<P>(xr, xs, U, lane);
   for (int e = wave; e < E; e += nwaves) {
-    const uint16_t* wr = W + (size_t)e * H;
-    float acc = 0.0f;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int u = lane + 64 * p;
-      if (u < U) {
-        const uint4 w = *reinterpret_cast<const uint4*>(wr + (size_t)u * 8);
-        const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
-        const uint32_t x4[4] = {xr[p].x, xr[p].y, xr[p].z, xr[p].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc = __builtin_fmaf(bf_lo(x4[j]), bf_lo(w4[j]), acc);
-          acc = __builtin_fmaf(bf_hi(x4[j]), bf_hi(w4[j]), acc);
-        }
-      }
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-      acc = __fadd_rn(acc, __shfl_xor(acc, off, 64));
+    uint4 w[P];
+    bf16_load_row<P>(w, W + (size_t)e * H, U, lane);
+    const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
     if (lane == 0) lg[e] = __fadd_rn(acc, bf2f(bias[e]));
   }
   __syncthreads();
@@ -637,12 +619,12 @@ __global__ __launch_bounds__(1024) void k_router(
     if (lane == 0) {
       float ex[16], s = 0.0f;
       for (int t = 0; t < k; ++t) {
-        ex[t] = expf(vals[t] - vals[0]);
-        s += ex[t];
+        ex[t] = neon_expf(__fsub_rn(vals[t], vals[0]));
+        s = __fadd_rn(s, ex[t]);
       }
       for (int t = 0; t < k; ++t) {
         idx[b * k + t] = ids[t];
-        score[b * k + t] = ex[t] / s;
+        score[b * k + t] = __fdiv_rn(ex[t], s);
       }
     }
   }
@@ -656,13 +638,13 @@ void launch_router(const uint16_t* x, const uint16_t* nw, float eps,
   switch (P) {
 #define R_CASE(PP)                                                           \
   case PP:                                                                   \
-    hipLaunchKernelGGL(k_router<PP>, dim3(B), dim3(1024), 0, st, x, nw, eps, \
+    hipLaunchKernelGGL(k_router<PP>, dim3(B), dim3(512), 0, st, x, nw, eps,  \
                        xn_out, W, bias, idx, score, logits_out, E, H, k);    \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)
     default:
-      hipLaunchKernelGGL(k_router<16>, dim3(B), dim3(1024), 0, st, x, nw, eps,
+      hipLaunchKernelGGL(k_router<16>, dim3(B), dim3(512), 0, st, x, nw, eps,
                          xn_out, W, bias, idx, score, logits_out, E, H, k);
 #undef R_CASE
   }
@@ -672,17 +654,19 @@ void launch_router(const uint16_t* x, const uint16_t* nw, float eps,
 // MoE expert FFN (HFM:82-112).
 // gate_up + SwiGLU: grid (ceil(I / (4 jpw)), k, B), block 256.  Wave w of
 // block i owns intermediate columns j in [(4i + w) jpw, +jpw); the gate row
-// 2j and up row 2j+1 (interleaved, HFM:83) are computed together, then
-//   gate = min(gate, limit); up = clamp(up, -limit, limit);
-//   act  = (up + 1) * gate * sigmoid(alpha * gate)        (HFM:84-87)
-// rounded once to bf16 (the down projection's input).
+// 2j and up row 2j+1 (interleaved, HFM:83) are computed together:
+//   g = dot + bias, u = dot + bias (fp32 adds)
+//   g = min(g, limit); u = clamp(u, -limit, limit)              (HFM:84-85)
+//   act = bf16((u + 1) * (g * (1 / (1 + exp(-(g * alpha))))))  (HFM:86-87)
+// each product, sum and quotient rounded separately (no contraction).
 // ===========================================================================
 __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
                                               float limit) {
   g = g > limit ? limit : g;
   u = u > limit ? limit : (u < -limit ? -limit : u);
-  const float sig = 1.0f / (1.0f + expf(-(g * alpha)));
-  return (u + 1.0f) * (g * sig);
+  const float e = neon_expf(-__fmul_rn(g, alpha));
+  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+  return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
 }
 
 template <int P>
@@ -709,7 +693,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
                     scales + (size_t)(2 * j0 + 1) * U, U, lane);
   }
   block_load_x(xs, xn + (size_t)b * H, nullptr, 0.0f, H, nullptr);
-  uint4 xr[P][4];
+  float xr[P][32];
   fp4_load_x<P>(xr, xs, U, lane);
   uint16_t* out = act + ((size_t)b * k + slot) * I;
   for (int j = j0; j < j1; ++j) {
@@ -720,10 +704,11 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
       fp4_load_row<P>(nu, codes + (size_t)(2 * j + 3) * (H / 2),
                       scales + (size_t)(2 * j + 3) * U, U, lane);
     }
-    const float g = wave_sum(fp4_row_partial<P>(cg, xr));
-    const float u = wave_sum(fp4_row_partial<P>(cu, xr));
+    const float g = wave_sum(fp4_row_partial<P>(cg, xr, U, lane));
+    const float u = wave_sum(fp4_row_partial<P>(cu, xr, U, lane));
     if (lane == 0) {
-      const float gb = g + bf2f(bias[2 * j]), ub = u + bf2f(bias[2 * j + 1]);
+      const float gb = __fadd_rn(g, bf2f(bias[2 * j]));
+      const float ub = __fadd_rn(u, bf2f(bias[2 * j + 1]));
       out[j] = f2bf(swiglu_clamp(gb, ub, alpha, limit));
     }
     cg = ng;
@@ -732,9 +717,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
 }
 
 // down + weighted sum (+ residual): grid (ceil(H / rpw), B), block 64 k (wave
-// s handles top-k slot s).  All k waves compute the same rows; block combine
-// y = sum_s score_s (dot_s + bias_s) in slot order (HFM:111-112), one
-// rounding to bf16, then out = bf16(residual + y) when residual is given.
+// s handles top-k slot s).  All k waves compute the same rows; the block
+// combines y = fmaf(score_s, dot_s + bias_s, y) in slot order from y = 0
+// (HFM:111-112), one rounding to bf16, then out = bf16(residual + y) when
+// residual is given.
 template <int P>
 __global__ __launch_bounds__(1024) void k_moe_down(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
@@ -753,7 +739,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   if (n0 < n1)
     fp4_load_row<P>(cur, codes + (size_t)n0 * (I / 2), scales + (size_t)n0 * U,
                     U, lane);
-  uint4 xr[P][4];
+  float xr[P][32];
   fp4_load_x<P>(xr, reinterpret_cast<const uint4*>(act + ((size_t)b * k + slot) * I),
                 U, lane);
   for (int n = n0; n < n1; ++n) {
@@ -761,18 +747,18 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     if (n + 1 < n1)
       fp4_load_row<P>(nxt, codes + (size_t)(n + 1) * (I / 2),
                       scales + (size_t)(n + 1) * U, U, lane);
-    const float acc = wave_sum(fp4_row_partial<P>(cur, xr));
-    if (lane == 0) red[slot][n - n0] = acc + bf2f(bias[n]);
+    const float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
+    if (lane == 0) red[slot][n - n0] = __fadd_rn(acc, bf2f(bias[n]));
     cur = nxt;
   }
   __syncthreads();
   if (threadIdx.x < n1 - n0) {
     const int t = threadIdx.x, n = n0 + t;
     float y = 0.0f;
-    for (int s = 0; s < k; ++s) y += score[b * k + s] * red[s][t];
+    for (int s = 0; s < k; ++s) y = __builtin_fmaf(score[b * k + s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
-    out[o] = residual ? f2bf(bf2f(residual[o]) + bf2f(m)) : m;
+    out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
   }
 }
 
@@ -805,13 +791,20 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 // before P.V.  Keys j in [lo, pos] with lo = pos - window + 1 on sliding
 // layers (HF mask kv_idx > q_idx - window).
 //
-// grid (S, Hkv, B), one wave per block.  Split s handles 64-key chunks
-// [s nch / S, (s+1) nch / S) with an online softmax; the G = Hq/Hkv query
-// heads of the kv head share every K/V load.  QK: lane = key, full K row
-// (128 B) per lane.  PV: lane = (key group kg = lane>>3, dim octet dq =
-// lane&7), V loads of 1 KB per wave instruction, then a 3-step xor reduce.
-// S > 1: partial (m, l, o) to global; the last split block to arrive (agent-
-// scope atomic counter) merges them with the sink.
+// grid (S, Hkv, B), one wave per block.  Canonical form (oracle
+// or_c_attn_decode):
+//   chunks of 64 keys from lo; split s takes chunks [s nch / S, (s+1) nch / S).
+//   score (lane = key): a = fmaf(q_d, k_d, a) over d = 0..63, times 1/8.
+//   per chunk and head: m' = max(m, max_j s_j); alpha = exp(m - m');
+//     p_j = exp(s_j - m'); l = fmaf(l, alpha, butterfly_sum(p_j));
+//     lane (kg = lane>>3, dq = lane&7) accumulators o *= alpha, then
+//     o = fmaf(p_j, v_j[8 dq + e], o) over the lane's keys j = kg + 8 i.
+//   o reduced over kg with xor 8, 16, 32.
+//   merge (split order s = 0..S-1): M = max(sink, m_s...);
+//     den = exp(sink - M); f_s = exp(m_s - M) (0 for empty splits);
+//     den = fmaf(l_s, f_s, den); acc = fmaf(f_s, o_s, acc); out = bf16(acc * (1/den))
+// S > 1: partials go to global memory and the last split block to arrive
+// (agent-scope atomic counter) merges them; S == 1 merges in registers.
 // fused != 0: q_src is the raw qkv row ([Hq + 2 Hkv] heads); the block rotates
 // q itself (YaRN table), and the block owning key `pos` also rotates k and
 // appends k/v to the caches (stream order makes them visible to later steps).
@@ -827,9 +820,9 @@ __global__ __launch_bounds__(64) void k_attn_decode(
     float* __restrict__ part_o, float* __restrict__ part_ml,
     int32_t* __restrict__ counters, int Hq, int Hkv, int T_max, int window,
     int fused, int q_stride) {
-  __shared__ uint4 qs[G][kD / 8];     // rotated q, bf16
+  __shared__ float qf[G][kD];          // rotated q (bf16 values) as fp32
   __shared__ uint4 knew[kD / 8], vnew[kD / 8];
-  __shared__ float ps[G][64];         // probabilities of the current chunk
+  __shared__ float ps[G][64];          // probabilities of the current chunk
   __shared__ int is_last_s;
   const int S = gridDim.x, s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
@@ -844,7 +837,6 @@ __global__ __launch_bounds__(64) void k_attn_decode(
   // ---- q (and the new k/v) into LDS -------------------------------------
   {
     const uint16_t* qrow = q_src + (size_t)b * q_stride;
-    uint16_t* qs16 = reinterpret_cast<uint16_t*>(&qs[0][0]);
     if (fused) {
       const float* cr = cos_t + (size_t)p * (kD / 2);
       const float* sr = sin_t + (size_t)p * (kD / 2);
@@ -853,8 +845,8 @@ __global__ __launch_bounds__(64) void k_attn_decode(
         const uint16_t* qh = qrow + (size_t)(g * G + hh) * kD;
         float o1, o2;
         rope_pair(bf2f(qh[f]), bf2f(qh[f + kD / 2]), cr[f], sr[f], o1, o2);
-        qs16[hh * kD + f] = f2bf(o1);
-        qs16[hh * kD + f + kD / 2] = f2bf(o2);
+        qf[hh][f] = bf2f(f2bf(o1));
+        qf[hh][f + kD / 2] = bf2f(f2bf(o2));
       }
       if (owns_new && lane < kD / 2) {
         const uint16_t* kh = qrow + (size_t)(Hq + g) * kD;
@@ -869,9 +861,9 @@ __global__ __launch_bounds__(64) void k_attn_decode(
         reinterpret_cast<uint32_t*>(vnew)[lane] = vh[lane];
       }
     } else {
-      for (int t = lane; t < G * (kD / 8); t += 64) {
-        const int hh = t / (kD / 8), u = t % (kD / 8);
-        qs[hh][u] = reinterpret_cast<const uint4*>(qrow + (size_t)(g * G + hh) * kD)[u];
+      for (int t = lane; t < G * kD; t += 64) {
+        const int hh = t / kD, d = t % kD;
+        qf[hh][d] = bf2f(qrow[(size_t)(g * G + hh) * kD + d]);
       }
     }
     __syncthreads();
@@ -889,45 +881,48 @@ __global__ __launch_bounds__(64) void k_attn_decode(
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[hh][e] = 0.0f;
   }
-  const float scale = 0.125f;  // 1/sqrt(64), HFM:277
   const int kg = lane >> 3, dq = lane & 7;
 
   for (int c = c0; c < c1; ++c) {
     // ---- scores: lane = key -------------------------------------------
     const int j = lo + c * 64 + lane;
     const bool valid = j <= p;
-    uint4 kr[kD / 8];
-    if (valid) {
-      if (fused && j == p) {
+    float kf[kD];
+    {
+      uint4 kr[kD / 8];
+      if (valid) {
+        if (fused && j == p) {
 #pragma unroll
-        for (int u = 0; u < kD / 8; ++u) kr[u] = knew[u];
+          for (int u = 0; u < kD / 8; ++u) kr[u] = knew[u];
+        } else {
+          const uint4* src = reinterpret_cast<const uint4*>(kc + (kv_base + j) * kD);
+#pragma unroll
+          for (int u = 0; u < kD / 8; ++u) kr[u] = src[u];
+        }
       } else {
-        const uint4* src = reinterpret_cast<const uint4*>(kc + (kv_base + j) * kD);
 #pragma unroll
-        for (int u = 0; u < kD / 8; ++u) kr[u] = src[u];
+        for (int u = 0; u < kD / 8; ++u) kr[u] = make_uint4(0, 0, 0, 0);
       }
-    } else {
 #pragma unroll
-      for (int u = 0; u < kD / 8; ++u) kr[u] = make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < kD / 8; ++u) unpack8(kr[u], &kf[8 * u]);
     }
     float sc[G];
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
       float a = 0.0f;
 #pragma unroll
-      for (int u = 0; u < kD / 8; ++u) a = dot8_bf16(kr[u], qs[hh][u], a);
-      sc[hh] = valid ? a * scale : -INFINITY;
+      for (int d = 0; d < kD; ++d) a = __builtin_fmaf(qf[hh][d], kf[d], a);
+      sc[hh] = valid ? __fmul_rn(a, 0.125f) : -INFINITY;  // 1/sqrt(64), HFM:277
     }
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
-      const float cm = wave_max(sc[hh]);
-      const float mn = fmaxf(m[hh], cm);
-      const float alpha = expf(m[hh] - mn);
-      const float pj = valid ? expf(sc[hh] - mn) : 0.0f;
-      l[hh] = l[hh] * alpha + wave_sum(pj);
+      const float mn = fmaxf(m[hh], wave_max(sc[hh]));
+      const float alpha = neon_expf(__fsub_rn(m[hh], mn));
+      const float pj = valid ? neon_expf(__fsub_rn(sc[hh], mn)) : 0.0f;
+      l[hh] = __builtin_fmaf(l[hh], alpha, wave_sum(pj));
       m[hh] = mn;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[hh][e] *= alpha;
+      for (int e = 0; e < 8; ++e) o[hh][e] = __fmul_rn(o[hh][e], alpha);
       ps[hh][lane] = pj;
     }
     __syncthreads();
@@ -940,13 +935,13 @@ __global__ __launch_bounds__(64) void k_attn_decode(
         uint4 v;
         if (fused && jk == p) v = vnew[dq];
         else v = reinterpret_cast<const uint4*>(vc + (kv_base + jk) * kD)[dq];
-        const float vf[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
-                             bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+        float vf[8];
+        unpack8(v, vf);
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
           const float pv = ps[hh][jj];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[hh][e] = fmaf(pv, vf[e], o[hh][e]);
+          for (int e = 0; e < 8; ++e) o[hh][e] = __builtin_fmaf(pv, vf[e], o[hh][e]);
         }
       }
     }
@@ -958,9 +953,9 @@ __global__ __launch_bounds__(64) void k_attn_decode(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float v = o[hh][e];
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
+      v = __fadd_rn(v, __shfl_xor(v, 8, 64));
+      v = __fadd_rn(v, __shfl_xor(v, 16, 64));
+      v = __fadd_rn(v, __shfl_xor(v, 32, 64));
       o[hh][e] = v;
     }
 
@@ -969,13 +964,16 @@ __global__ __launch_bounds__(64) void k_attn_decode(
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) {
         const float sk = bf2f(sinks[g * G + hh]);
-        const float M = fmaxf(m[hh], sk);
-        const float f = expf(m[hh] - M);
-        const float inv = 1.0f / (l[hh] * f + expf(sk - M));
+        const float M = fmaxf(sk, m[hh]);
+        float den = neon_expf(__fsub_rn(sk, M));
+        const float f = (m[hh] == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(m[hh], M));
+        den = __builtin_fmaf(l[hh], f, den);
+        const float inv = __fdiv_rn(1.0f, den);
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          w[e] = pack_bf2(o[hh][2 * e] * f * inv, o[hh][2 * e + 1] * f * inv);
+          w[e] = pack_bf2(__fmul_rn(__builtin_fmaf(f, o[hh][2 * e], 0.0f), inv),
+                          __fmul_rn(__builtin_fmaf(f, o[hh][2 * e + 1], 0.0f), inv));
         reinterpret_cast<uint4*>(out + (size_t)b * Hq * kD +
                                  (size_t)(g * G + hh) * kD)[dq] =
             make_uint4(w[0], w[1], w[2], w[3]);
@@ -1018,25 +1016,23 @@ __global__ __launch_bounds__(64) void k_attn_decode(
     if (hh < G) {
       const float sk = bf2f(sinks[g * G + hh]);
       float M = sk;
-      for (int t = 0; t < S; ++t)
-        M = fmaxf(M, part_ml[((pbase + t) * G + hh) * 2]);
-      float den = expf(sk - M);
+      for (int t = 0; t < S; ++t) M = fmaxf(M, part_ml[((pbase + t) * G + hh) * 2]);
+      float den = neon_expf(__fsub_rn(sk, M));
       float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       for (int t = 0; t < S; ++t) {
         const float mt = part_ml[((pbase + t) * G + hh) * 2];
         const float lt = part_ml[((pbase + t) * G + hh) * 2 + 1];
-        const float f = (mt == -INFINITY) ? 0.0f : expf(mt - M);
-        den += lt * f;
+        const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
+        den = __builtin_fmaf(lt, f, den);
         const float* src = part_o + ((pbase + t) * G + hh) * kD + dq * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          acc[e] = fmaf(f, src[e], acc[e]);
+        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f, src[e], acc[e]);
       }
-      const float inv = 1.0f / den;
+      const float inv = __fdiv_rn(1.0f, den);
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+        w[e] = pack_bf2(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
       reinterpret_cast<uint4*>(out + (size_t)b * Hq * kD +
                                (size_t)(g * G + hh) * kD)[dq] =
           make_uint4(w[0], w[1], w[2], w[3]);
@@ -1062,6 +1058,12 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
     default: A_CASE(8)
   }
 #undef A_CASE
+}
+
+int attn_splits(int T_max, int window) {
+  const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
+  const int s = (span + 63) / 64;
+  return s < 1 ? 1 : (s > 32 ? 32 : s);
 }
 
 }  // namespace neon

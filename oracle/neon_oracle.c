@@ -284,6 +284,232 @@ void or_rope_apply(const uint16_t* x, int n_heads, int D, const float* c,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Canonical fp32 forms.  The device evaluates every reduction of the decode  */
+/* path in one fixed order of IEEE fp32 operations (explicit fused multiply- */
+/* adds, a 64-lane xor butterfly); the or_c_* functions restate that order   */
+/* so GPU and oracle agree bit for bit.  Each is pinned against the fp64     */
+/* functions above by the CPU tests (fp32 error bounds).                     */
+/* ------------------------------------------------------------------------ */
+
+/* exp: Cody-Waite reduction by a two-part ln 2 and a degree-7 Taylor       */
+/* polynomial in Horner form (same operation sequence as the device).        */
+float or_expf(float x) {
+  if (x != x) return x;
+  if (x > 0x1.62e43p+6f) return INFINITY;
+  if (x < -0x1.9fe36ap+6f) return 0.0f;
+  const float n = rintf(x * 0x1.715476p+0f);
+  float r = fmaf(-n, 0x1.62e4p-1f, x);
+  r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+  float p = 0x1.a01a02p-13f;
+  p = fmaf(p, r, 0x1.6c16c2p-10f);
+  p = fmaf(p, r, 0x1.111112p-7f);
+  p = fmaf(p, r, 0x1.555556p-5f);
+  p = fmaf(p, r, 0x1.555556p-3f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)n);
+}
+
+/* v[l] = v[l] + v[l ^ off] for off = 32, 16, 8, 4, 2, 1; result v[0] */
+static float c_butterfly64(float* v) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    float t[64];
+    for (int l = 0; l < 64; ++l) t[l] = v[l] + v[l ^ off];
+    memcpy(v, t, sizeof(t));
+  }
+  return v[0];
+}
+
+/* bf16 row . fp32 x: lane l owns the 8-element units u = l + 64 p. */
+static float c_dot_bf16(const uint16_t* w, const float* x, int K) {
+  const int U = K / 8;
+  float a[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int u = l; u < U; u += 64)
+      for (int j = 0; j < 8; ++j) acc = fmaf(BF(w[u * 8 + j]), x[u * 8 + j], acc);
+    a[l] = acc;
+  }
+  return c_butterfly64(a);
+}
+
+/* MXFP4 row . fp32 x: lane l owns the 32-element units u = l + 64 p; per unit
+ * t = fmaf chain from 0, then acc = acc + t * 2^(s - 127) (0xFF: NaN). */
+static float c_dot_fp4(const uint8_t* codes, const uint8_t* scales,
+                       const float* x, int K) {
+  const int U = K / 32;
+  float a[64];
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int u = l; u < U; u += 64) {
+      float t = 0.0f;
+      for (int j = 0; j < 16; ++j) {
+        const uint8_t byte = codes[u * 16 + j];
+        t = fmaf(kE2M1[byte & 0xF], x[u * 32 + 2 * j], t);
+        t = fmaf(kE2M1[byte >> 4], x[u * 32 + 2 * j + 1], t);
+      }
+      acc = acc + e8m0_exp2(scales[u], t);
+    }
+    a[l] = acc;
+  }
+  return c_butterfly64(a);
+}
+
+void or_c_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                    int B, int N, int K, uint16_t* y, float* y_f32) {
+  float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
+  for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int b = 0; b < B; ++b) {
+      float r = c_dot_bf16(W + (size_t)n * K, xf + (size_t)b * K, K);
+      if (bias) r = r + BF(bias[n]);
+      if (y_f32) y_f32[(size_t)b * N + n] = r;
+      if (y) y[(size_t)b * N + n] = TOBF(r);
+    }
+  free(xf);
+}
+
+void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                     const uint16_t* bias, const uint16_t* x, int B, int N,
+                     int K, uint16_t* y, float* y_f32) {
+  float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
+  for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
+#pragma omp parallel for schedule(static)
+  for (int n = 0; n < N; ++n)
+    for (int b = 0; b < B; ++b) {
+      float r = c_dot_fp4(codes + (size_t)n * (K / 2), scales + (size_t)n * (K / 32),
+                          xf + (size_t)b * K, K);
+      if (bias) r = r + BF(bias[n]);
+      if (y_f32) y_f32[(size_t)b * N + n] = r;
+      if (y) y[(size_t)b * N + n] = TOBF(r);
+    }
+  free(xf);
+}
+
+/* RMSNorm, canonical: ss by the 64-lane unit order and butterfly;
+ * r = 1 / sqrt(ss / H + eps); y = bf16(w * (x * r)). */
+void or_c_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
+                  uint16_t* out) {
+  const int U = H / 8;
+  for (int b = 0; b < B; ++b) {
+    const uint16_t* xb = x + (size_t)b * H;
+    float a[64];
+    for (int l = 0; l < 64; ++l) {
+      float ss = 0.0f;
+      for (int u = l; u < U; u += 64)
+        for (int j = 0; j < 8; ++j) {
+          const float v = BF(xb[u * 8 + j]);
+          ss = fmaf(v, v, ss);
+        }
+      a[l] = ss;
+    }
+    const float ss = c_butterfly64(a);
+    const float r = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int i = 0; i < H; ++i)
+      out[(size_t)b * H + i] = TOBF(BF(w[i]) * (BF(xb[i]) * r));
+  }
+}
+
+int or_attn_splits(int T_max, int window) {
+  const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
+  const int s = (span + 63) / 64;
+  return s < 1 ? 1 : (s > 32 ? 32 : s);
+}
+
+/* Decode attention with sinks, canonical split form (device k_attn_decode):
+ * 64-key chunks from lo, split s owns chunks [s nch / S, (s+1) nch / S);
+ * online softmax per split with lane-local P.V accumulators (lane = key group
+ * kg x dim octet dq), reduced over kg by xor 8, 16, 32; splits merged in
+ * order with the sink.  D must be 64. */
+void or_c_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                      const uint16_t* sinks, int B, int Hq, int Hkv, int D,
+                      int T_max, const int32_t* pos, int window, int S,
+                      uint16_t* out, float* out_f32) {
+  const int G = Hq / Hkv;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hq; ++h) {
+      const int g = h / G, p = pos[b];
+      const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
+      const int n = p - lo + 1, nch = (n + 63) / 64;
+      const size_t base = ((size_t)b * Hkv + g) * T_max;
+      float qf[64];
+      for (int d = 0; d < 64; ++d) qf[d] = BF(q[((size_t)b * Hq + h) * D + d]);
+      float pm[32], pl[32], po[32][64];
+      for (int s = 0; s < S; ++s) {
+        const int c0 = (int)((int64_t)s * nch / S), c1 = (int)((int64_t)(s + 1) * nch / S);
+        float m = -INFINITY, l = 0.0f;
+        float o[64][8]; /* [lane = kg*8 + dq][e] */
+        for (int ln = 0; ln < 64; ++ln)
+          for (int e = 0; e < 8; ++e) o[ln][e] = 0.0f;
+        for (int c = c0; c < c1; ++c) {
+          float sc[64], pj[64];
+          int valid[64];
+          float cm = -INFINITY;
+          for (int ln = 0; ln < 64; ++ln) {
+            const int j = lo + c * 64 + ln;
+            valid[ln] = j <= p;
+            if (!valid[ln]) { sc[ln] = -INFINITY; continue; }
+            const uint16_t* kr = kc + (base + j) * D;
+            float a = 0.0f;
+            for (int d = 0; d < 64; ++d) a = fmaf(qf[d], BF(kr[d]), a);
+            sc[ln] = a * 0.125f;
+            if (sc[ln] > cm) cm = sc[ln];
+          }
+          const float mn = m > cm ? m : cm;
+          const float alpha = or_expf(m - mn);
+          for (int ln = 0; ln < 64; ++ln) pj[ln] = valid[ln] ? or_expf(sc[ln] - mn) : 0.0f;
+          float tmp[64];
+          memcpy(tmp, pj, sizeof(tmp));
+          l = fmaf(l, alpha, c_butterfly64(tmp));
+          m = mn;
+          for (int ln = 0; ln < 64; ++ln)
+            for (int e = 0; e < 8; ++e) o[ln][e] = o[ln][e] * alpha;
+          for (int ln = 0; ln < 64; ++ln) {
+            const int kg = ln >> 3, dq = ln & 7;
+            for (int i = 0; i < 8; ++i) {
+              const int jj = kg + 8 * i, jk = lo + c * 64 + jj;
+              if (jk > p) continue;
+              const uint16_t* vr = vc + (base + jk) * D + dq * 8;
+              for (int e = 0; e < 8; ++e) o[ln][e] = fmaf(pj[jj], BF(vr[e]), o[ln][e]);
+            }
+          }
+        }
+        /* reduce over kg (lane bits 3..5): xor 8, then 16, then 32 */
+        for (int step = 1; step <= 4; step <<= 1) {
+          float t[64][8];
+          for (int ln = 0; ln < 64; ++ln)
+            for (int e = 0; e < 8; ++e) t[ln][e] = o[ln][e] + o[ln ^ (8 * step)][e];
+          memcpy(o, t, sizeof(t));
+        }
+        pm[s] = m;
+        pl[s] = l;
+        for (int dq = 0; dq < 8; ++dq)
+          for (int e = 0; e < 8; ++e) po[s][dq * 8 + e] = o[dq][e];
+      }
+      const float sk = BF(sinks[h]);
+      float M = sk;
+      for (int s = 0; s < S; ++s) M = M > pm[s] ? M : pm[s];
+      float den = or_expf(sk - M);
+      float acc[64];
+      for (int d = 0; d < 64; ++d) acc[d] = 0.0f;
+      for (int s = 0; s < S; ++s) {
+        const float f = (pm[s] == -INFINITY) ? 0.0f : or_expf(pm[s] - M);
+        den = fmaf(pl[s], f, den);
+        for (int d = 0; d < 64; ++d) acc[d] = fmaf(f, po[s][d], acc[d]);
+      }
+      const float inv = 1.0f / den;
+      for (int d = 0; d < 64; ++d) {
+        const float r = acc[d] * inv;
+        if (out_f32) out_f32[((size_t)b * Hq + h) * D + d] = r;
+        if (out) out[((size_t)b * Hq + h) * D + d] = TOBF(r);
+      }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Router (HFM:117-130): logits = x W^T + b, top-k over the logits, softmax  */
 /* over the k selected values.  The logits use ONE canonical fp32 reduction  */
 /* order, identical to the device router, so top-k indices match bit for     */
@@ -332,7 +558,7 @@ void or_router(const uint16_t* x, const uint16_t* W, const uint16_t* b, int B,
     }
     float ex[64], s = 0.0f;
     for (int t = 0; t < k; ++t) {
-      ex[t] = expf(v[t] - v[0]);
+      ex[t] = or_expf(v[t] - v[0]);
       s += ex[t];
     }
     for (int t = 0; t < k; ++t) score[r * k + t] = ex[t] / s;
@@ -350,15 +576,15 @@ void or_swiglu(const float* gu, int I, float alpha, float limit, float* out) {
     float g = gu[2 * j], u = gu[2 * j + 1];
     g = g > limit ? limit : g;
     u = u > limit ? limit : (u < -limit ? -limit : u);
-    float sig = 1.0f / (1.0f + expf(-(g * alpha)));
+    float sig = 1.0f / (1.0f + or_expf(-(g * alpha)));
     out[j] = (u + 1.0f) * (g * sig);
   }
 }
 
-/* MoE block (HFM:89-114, 145-154) on already-normalised x: router, then for
- * each selected expert (rank order) gate_up GEMV + bias -> SwiGLU -> bf16 ->
- * down GEMV + bias, weighted by its score and summed in fp32; one rounding
- * to bf16. */
+/* MoE block (HFM:89-114, 145-154) on already-normalised x, canonical form:
+ * router, then for each selected expert (rank order) gate_up GEMV + bias ->
+ * SwiGLU -> bf16 -> down GEMV + bias, acc = fmaf(score, out, acc) from 0;
+ * one rounding to bf16. */
 void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
                   const uint16_t* router_b, const uint8_t* gu_codes,
                   const uint8_t* gu_scales, const uint16_t* gu_bias,
@@ -378,15 +604,15 @@ void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
     for (int i = 0; i < H; ++i) acc[i] = 0.0f;
     for (int t = 0; t < k; ++t) {
       const int e = idx[r * k + t];
-      or_mxfp4_gemv(gu_codes + e * gu_code_sz, gu_scales + e * gu_sc_sz,
-                    gu_bias + (size_t)e * 2 * I, x + (size_t)r * H, 1, 2 * I, H,
-                    NULL, gu);
+      or_c_mxfp4_gemv(gu_codes + e * gu_code_sz, gu_scales + e * gu_sc_sz,
+                      gu_bias + (size_t)e * 2 * I, x + (size_t)r * H, 1, 2 * I,
+                      H, NULL, gu);
       or_swiglu(gu, I, alpha, limit, act);
       for (int j = 0; j < I; ++j) actb[j] = TOBF(act[j]);
-      or_mxfp4_gemv(dn_codes + e * dn_code_sz, dn_scales + e * dn_sc_sz,
-                    dn_bias + (size_t)e * H, actb, 1, H, I, NULL, dn);
+      or_c_mxfp4_gemv(dn_codes + e * dn_code_sz, dn_scales + e * dn_sc_sz,
+                      dn_bias + (size_t)e * H, actb, 1, H, I, NULL, dn);
       const float sc = score[r * k + t];
-      for (int i = 0; i < H; ++i) acc[i] += sc * dn[i];
+      for (int i = 0; i < H; ++i) acc[i] = fmaf(sc, dn[i], acc[i]);
     }
     for (int i = 0; i < H; ++i) out[(size_t)r * H + i] = TOBF(acc[i]);
   }
@@ -459,6 +685,10 @@ struct or_model {
   uint16_t *kc, *vc; /* [L][B][Hkv][max_seq][D] */
   int32_t* pos;
   uint16_t* h; /* [B][H] */
+  /* last step, batch row 0, last layer: buffers named like the device's */
+  uint16_t *t_qkv, *t_attn, *t_moe_in;
+  int32_t t_idx[64];
+  float t_score[64];
 };
 
 static void* xmalloc(size_t n) {
@@ -523,6 +753,9 @@ or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch) {
   m->vc = (uint16_t*)calloc(kv, sizeof(uint16_t));
   m->pos = (int32_t*)calloc(batch, sizeof(int32_t));
   m->h = (uint16_t*)calloc((size_t)batch * H, sizeof(uint16_t));
+  m->t_qkv = (uint16_t*)calloc((size_t)QKV, sizeof(uint16_t));
+  m->t_attn = (uint16_t*)calloc((size_t)Hq * D, sizeof(uint16_t));
+  m->t_moe_in = (uint16_t*)calloc((size_t)H, sizeof(uint16_t));
   return m;
 }
 
@@ -537,7 +770,18 @@ void or_model_free(or_model* m) {
   }
   free(m->layers); free(m->embed); free(m->lm_head); free(m->final_norm);
   free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc); free(m->pos);
-  free(m->h); free(m);
+  free(m->h); free(m->t_qkv); free(m->t_attn); free(m->t_moe_in); free(m);
+}
+
+const void* or_model_trace(const or_model* m, int what) {
+  switch (what) {
+    case 0: return m->t_qkv;
+    case 1: return m->t_attn;
+    case 2: return m->t_moe_in;
+    case 3: return m->t_idx;
+    case 4: return m->t_score;
+    default: return NULL;
+  }
 }
 
 const uint16_t* or_model_hidden(const or_model* m) { return m->h; }
@@ -575,7 +819,9 @@ const void* or_model_tensor(const or_model* m, int layer, int kind) {
 
 /* Decoder layer (HFM:347-376): h += attn(norm(h)); h += moe(norm(h)); each
  * sublayer output rounded to bf16 and added to the bf16 residual with one
- * rounding.  Layer i is sliding iff (i + 1) is odd (HFC:75-78). */
+ * rounding.  Layer i is sliding iff (i + 1) is odd (HFC:75-78).  Every
+ * reduction uses the canonical or_c_* forms, so the step is bit-identical to
+ * the device's. */
 void or_model_step(or_model* m, const int32_t* ids, float* logits,
                    int32_t* out_ids) {
   const or_config* c = &m->cfg;
@@ -598,8 +844,8 @@ void or_model_step(or_model* m, const int32_t* ids, float* logits,
     for (int l = 0; l < c->n_layers; ++l) {
       const or_layer* L = &m->layers[l];
       const int window = (l % 2 == 0) ? c->sliding_window : 0;
-      or_rmsnorm(h, L->attn_norm, 1, H, c->rms_eps, xn);
-      or_gemv_bf16(L->wqkv, L->bqkv, xn, 1, QKV, H, qkv, NULL);
+      or_c_rmsnorm(h, L->attn_norm, 1, H, c->rms_eps, xn);
+      or_c_gemv_bf16(L->wqkv, L->bqkv, xn, 1, QKV, H, qkv, NULL);
       const float* cr = m->cos_t + (size_t)p * half;
       const float* sr = m->sin_t + (size_t)p * half;
       or_rope_apply(qkv, Hq, D, cr, sr, qr);
@@ -612,18 +858,26 @@ void or_model_step(or_model* m, const int32_t* ids, float* logits,
         memcpy(m->vc + (lb + (size_t)g * c->max_seq + p) * D,
                qkv + (Hq + Hkv + g) * D, sizeof(uint16_t) * D);
       }
-      or_attn_decode(qr, m->kc + lb * D, m->vc + lb * D, L->sinks, 1, Hq, Hkv,
-                     D, c->max_seq, &p, window, ao, NULL);
-      or_gemv_bf16(L->wo, L->bo, ao, 1, H, Hq * D, tmp, NULL);
+      or_c_attn_decode(qr, m->kc + lb * D, m->vc + lb * D, L->sinks, 1, Hq,
+                       Hkv, D, c->max_seq, &p, window,
+                       or_attn_splits(c->max_seq, window), ao, NULL);
+      or_c_gemv_bf16(L->wo, L->bo, ao, 1, H, Hq * D, tmp, NULL);
       for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
-      or_rmsnorm(h, L->mlp_norm, 1, H, c->rms_eps, xn);
+      or_c_rmsnorm(h, L->mlp_norm, 1, H, c->rms_eps, xn);
       or_moe_layer(xn, L->router_w, L->router_b, L->gu_codes, L->gu_scales,
                    L->gu_bias, L->dn_codes, L->dn_scales, L->dn_bias, 1, E, H,
                    I, K, c->swiglu_alpha, c->swiglu_limit, tmp, idx, sc);
+      if (b == 0 && l == c->n_layers - 1) {
+        memcpy(m->t_qkv, qkv, sizeof(uint16_t) * QKV);
+        memcpy(m->t_attn, ao, sizeof(uint16_t) * Hq * D);
+        memcpy(m->t_moe_in, xn, sizeof(uint16_t) * H);
+        memcpy(m->t_idx, idx, sizeof(int32_t) * K);
+        memcpy(m->t_score, sc, sizeof(float) * K);
+      }
       for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
     }
-    or_rmsnorm(h, m->final_norm, 1, H, c->rms_eps, xn);
-    or_gemv_bf16(m->lm_head, NULL, xn, 1, (int)V, H, NULL, lg);
+    or_c_rmsnorm(h, m->final_norm, 1, H, c->rms_eps, xn);
+    or_c_gemv_bf16(m->lm_head, NULL, xn, 1, (int)V, H, NULL, lg);
     int best = 0;
     for (int64_t v = 1; v < V; ++v)
       if (lg[v] > lg[best]) best = (int)v;

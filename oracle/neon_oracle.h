@@ -29,6 +29,10 @@
  *                     T = 1 closed form; HF eager_attention_forward fixtures.
  *   or_model_*        composition of the above; HF GptOssForCausalLM fixture
  *                     on a tiny fp32 config.
+ *   or_c_*, or_expf   canonical fp32 forms that restate the device's exact
+ *                     operation order; pinned against the fp64 functions
+ *                     (fp32 error bounds) and or_expf against exp (ulps).
+ *   or_router, or_swiglu and or_moe_layer use the canonical forms.
  */
 #ifndef NEON_ORACLE_H
 #define NEON_ORACLE_H
@@ -96,6 +100,21 @@ void or_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                     int Hq, int Hkv, int D, int T_max, const int32_t* pos,
                     int window, uint16_t* out, float* out_f32);
 
+/* ---- canonical fp32 forms (bit-identical to the device kernels) ----------- */
+float or_expf(float x);
+void or_c_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                    int B, int N, int K, uint16_t* y, float* y_f32);
+void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                     const uint16_t* bias, const uint16_t* x, int B, int N,
+                     int K, uint16_t* y, float* y_f32);
+void or_c_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
+                  uint16_t* out);
+int or_attn_splits(int T_max, int window);
+void or_c_attn_decode(const uint16_t* q, const uint16_t* k_cache,
+                      const uint16_t* v_cache, const uint16_t* sinks, int B,
+                      int Hq, int Hkv, int D, int T_max, const int32_t* pos,
+                      int window, int S, uint16_t* out, float* out_f32);
+
 /* ---- full model (random init, identical to neon_init_random) -------------- */
 typedef struct or_model or_model;
 or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch);
@@ -111,6 +130,10 @@ int32_t or_model_pos(const or_model* m, int b);
 /* Tensor access for tests: returns a pointer into the model's weights. */
 const void* or_model_tensor(const or_model* m, int layer, int kind);
 int or_num_threads(void);
+/* Last step's last-layer activations of batch row 0 (tests): 0 qkv (bf16),
+ * 1 attention output (bf16), 2 MoE input (bf16), 3 expert ids (int32),
+ * 4 routing weights (fp32). */
+const void* or_model_trace(const or_model* m, int what);
 
 /* tensor kinds (shared with the product's init streams) */
 enum {

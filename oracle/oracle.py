@@ -108,6 +108,13 @@ def _declare(L):
         "or_model_pos": (C.c_int32, [_P, _I]),
         "or_model_tensor": (_P, [_P, _I, _I]),
         "or_num_threads": (_I, []),
+        "or_model_trace": (_P, [_P, _I]),
+        "or_expf": (_F, [_F]),
+        "or_c_gemv_bf16": (None, [_P, _P, _P, _I, _I, _I, _P, _P]),
+        "or_c_mxfp4_gemv": (None, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
+        "or_c_rmsnorm": (None, [_P, _P, _I, _I, _F, _P]),
+        "or_attn_splits": (_I, [_I, _I]),
+        "or_c_attn_decode": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -276,6 +283,56 @@ def attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, T_max, pos, window):
     return out, outf
 
 
+# ---- canonical fp32 forms (bit-identical to the device kernels) -------------
+def expf(x: float) -> float:
+    return lib().or_expf(x)
+
+
+def c_gemv_bf16(W, bias, x, N, K):
+    W, x = _c(W, np.uint16), _c(x, np.uint16)
+    B = x.size // K
+    bias = None if bias is None else _c(bias, np.uint16)
+    y = np.empty((B, N), np.uint16)
+    yf = np.empty((B, N), np.float32)
+    lib().or_c_gemv_bf16(_p(W), _p(bias), _p(x), B, N, K, _p(y), _p(yf))
+    return y, yf
+
+
+def c_mxfp4_gemv(codes, scales, bias, x, N, K):
+    codes, scales, x = _c(codes, np.uint8), _c(scales, np.uint8), _c(x, np.uint16)
+    B = x.size // K
+    bias = None if bias is None else _c(bias, np.uint16)
+    y = np.empty((B, N), np.uint16)
+    yf = np.empty((B, N), np.float32)
+    lib().or_c_mxfp4_gemv(_p(codes), _p(scales), _p(bias), _p(x), B, N, K, _p(y), _p(yf))
+    return y, yf
+
+
+def c_rmsnorm(x, w, eps=1e-5):
+    x, w = _c(x, np.uint16), _c(w, np.uint16)
+    H = w.size
+    B = x.size // H
+    out = np.empty((B, H), np.uint16)
+    lib().or_c_rmsnorm(_p(x), _p(w), B, H, eps, _p(out))
+    return out
+
+
+def attn_splits(T_max, window) -> int:
+    return lib().or_attn_splits(T_max, window)
+
+
+def c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, T_max, pos, window, S=None):
+    q, kc, vc, sinks = _c(q, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16), _c(sinks, np.uint16)
+    pos = _c(pos, np.int32)
+    if S is None:
+        S = attn_splits(T_max, window)
+    out = np.empty((B, Hq * D), np.uint16)
+    outf = np.empty((B, Hq * D), np.float32)
+    lib().or_c_attn_decode(_p(q), _p(kc), _p(vc), _p(sinks), B, Hq, Hkv, D, T_max,
+                           _p(pos), window, S, _p(out), _p(outf))
+    return out, outf
+
+
 class Model:
     """Random-init gpt-oss model (bit-identical weights to neon_init_random)."""
 
@@ -305,6 +362,19 @@ class Model:
         p = lib().or_model_hidden(self._h)
         n = self.batch * self.cfg.hidden
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(n,)).copy()
+
+    def trace(self):
+        """Last step's last-layer activations of row 0 (same names as
+        neon_read_activation)."""
+        c = self.cfg
+        qkv = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+
+        def arr(what, ctype, n):
+            p = lib().or_model_trace(self._h, what)
+            return np.ctypeslib.as_array(C.cast(p, C.POINTER(ctype)), shape=(n,)).copy()
+        return {"qkv": arr(0, C.c_uint16, qkv), "attn_out": arr(1, C.c_uint16, c.n_heads * c.head_dim),
+                "moe_in": arr(2, C.c_uint16, c.hidden), "moe_idx": arr(3, C.c_int32, c.top_k),
+                "moe_score": arr(4, C.c_float, c.top_k)}
 
     def tensor(self, layer, kind, count, dtype=np.uint16):
         p = lib().or_model_tensor(self._h, layer, kind)

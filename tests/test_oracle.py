@@ -441,3 +441,101 @@ def test_model_deterministic_and_batched(orc):
         ids = a
     m1.close()
     m2.close()
+
+
+# ---------------------------------------------------------------------------
+# canonical fp32 forms (what the device computes bit for bit), pinned to the
+# fp64 functions above and to the mathematics
+# ---------------------------------------------------------------------------
+def test_expf_accuracy(orc):
+    xs = np.concatenate([np.linspace(-103.9, 88.7, 200001, dtype=np.float32),
+                         np.array([0.0, -0.0, 1e-30, -1e-30, 88.72, -87.3, 1.0, -1.0], np.float32)])
+    got = np.array([orc.expf(float(x)) for x in xs[::7]], np.float32)
+    ref = np.exp(xs[::7].astype(np.float64))
+    normal = ref >= 2.0 ** -126
+    ulp = np.spacing(ref[normal].astype(np.float32)).astype(np.float64)
+    err_ulp = np.abs(got[normal] - ref[normal]) / ulp
+    assert err_ulp.max() <= 2.0, err_ulp.max()
+    assert orc.expf(0.0) == 1.0 and orc.expf(-200.0) == 0.0
+    assert orc.expf(100.0) == float("inf") and np.isnan(orc.expf(float("nan")))
+    # subnormal results stay within one subnormal step
+    sub = ~normal & (ref > 0)
+    assert np.all(np.abs(got[sub] - ref[sub]) <= 2.0 ** -149 * 2)
+
+
+def fp32_bound(abs_sum, K):
+    """|fp32 fma-chain result - exact| <= gamma * sum|terms|, gamma ~ (K/64 + 7) u."""
+    return (K / 64 + 8) * 2.0 ** -24 * abs_sum + 1e-30
+
+
+@pytest.mark.parametrize("N,K,B", [(64, 2880, 2), (33, 4096, 1), (7, 8, 3), (5, 520, 1)])
+def test_c_gemv_bf16_vs_fp64(orc, N, K, B):
+    rng = np.random.default_rng(K + N)
+    W = orc.f32_to_bf16(0.02 * rng.standard_normal((N, K)).astype(np.float32))
+    bias = orc.f32_to_bf16(rng.standard_normal(N).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((B, K)).astype(np.float32))
+    y, yf = orc.c_gemv_bf16(W, bias, x, N, K)
+    _, ref = orc.gemv_bf16(W, bias, x, N, K)
+    Wf, xf = orc.bf16_to_f32(W).astype(np.float64), orc.bf16_to_f32(x).astype(np.float64)
+    abs_sum = np.abs(xf) @ np.abs(Wf).T + np.abs(orc.bf16_to_f32(bias))
+    assert np.all(np.abs(yf.astype(np.float64) - ref) <= fp32_bound(abs_sum, K))
+    assert np.array_equal(y, orc.f32_to_bf16(yf))
+
+
+@pytest.mark.parametrize("N,K,B", [(64, 2880, 2), (9, 32, 1), (12, 4096, 2), (5, 2112, 1)])
+def test_c_mxfp4_gemv_vs_fp64(orc, N, K, B):
+    rng = np.random.default_rng(N * K)
+    codes = rng.integers(0, 256, N * K // 2, dtype=np.uint8)
+    scales = rng.integers(119, 125, N * K // 32, dtype=np.uint8)
+    bias = orc.f32_to_bf16(rng.standard_normal(N).astype(np.float32))
+    x = orc.f32_to_bf16(rng.standard_normal((B, K)).astype(np.float32))
+    y, yf = orc.c_mxfp4_gemv(codes, scales, bias, x, N, K)
+    _, ref = orc.mxfp4_gemv(codes, scales, bias, x, N, K)
+    Wa = np.abs(orc.mxfp4_dequant(codes, scales).reshape(N, K)).astype(np.float64)
+    abs_sum = np.abs(orc.bf16_to_f32(x)).astype(np.float64) @ Wa.T + np.abs(orc.bf16_to_f32(bias))
+    assert np.all(np.abs(yf.astype(np.float64) - ref) <= fp32_bound(abs_sum, K / 4))
+    assert np.array_equal(y, orc.f32_to_bf16(yf))
+
+
+def test_c_rmsnorm_vs_fp64(orc):
+    rng = np.random.default_rng(4)
+    x = orc.f32_to_bf16(30 * rng.standard_normal((3, 2880)).astype(np.float32))
+    w = orc.f32_to_bf16(1 + 0.05 * rng.standard_normal(2880).astype(np.float32))
+    a = orc.c_rmsnorm(x, w).astype(np.int32)
+    b = orc.rmsnorm(x, w).astype(np.int32)
+    assert np.abs(a - b).max() <= 1 and (a != b).mean() < 0.01
+    # constant vector closed form holds exactly for the canonical form too
+    xc = orc.f32_to_bf16(np.full(2880, -3.5, np.float32))
+    assert np.array_equal(orc.c_rmsnorm(xc, w), orc.rmsnorm(xc, w))
+
+
+@pytest.mark.parametrize("T,window,S", [(1, 0, 1), (300, 0, 5), (300, 128, 2), (1000, 0, 32),
+                                         (129, 128, 2), (70, 0, 8), (5, 0, 3)])
+def test_c_attn_vs_fp64(orc, T, window, S):
+    rng = np.random.default_rng(T * 7 + S)
+    B, Hq, Hkv, D = 2, 8, 2, 64
+    Tm = T + 3
+    q = orc.f32_to_bf16(rng.standard_normal((B, Hq, D)).astype(np.float32))
+    kc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    sinks = orc.f32_to_bf16(rng.standard_normal(Hq).astype(np.float32))
+    pos = np.array([T - 1, max(0, T - 2)], np.int32)
+    _, a = orc.c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, window, S)
+    _, r = orc.attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, window)
+    np.testing.assert_allclose(a, r, rtol=2e-5, atol=2e-6)
+
+
+def test_c_attn_split_count_only_reorders(orc):
+    """Different split counts give results equal to fp32 rounding."""
+    rng = np.random.default_rng(8)
+    B, Hq, Hkv, D, Tm = 1, 8, 8, 64, 700
+    q = orc.f32_to_bf16(rng.standard_normal((B, Hq, D)).astype(np.float32))
+    kc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    vc = orc.f32_to_bf16(rng.standard_normal((B, Hkv, Tm, D)).astype(np.float32))
+    sinks = orc.f32_to_bf16(rng.standard_normal(Hq).astype(np.float32))
+    pos = np.array([699], np.int32)
+    outs = [orc.c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, 0, S)[1] for S in (1, 3, 11)]
+    for o in outs[1:]:
+        np.testing.assert_allclose(o, outs[0], rtol=1e-5, atol=1e-6)
+    assert orc.attn_splits(4096, 128) == 2 and orc.attn_splits(4096, 0) == 32
+    assert orc.attn_splits(100, 0) == 2 and orc.attn_splits(1, 0) == 1
