@@ -128,6 +128,29 @@ def cpu_baseline(seed: int, prompt_len: int, steps: int):
                        f"not the reference")
 
 
+COPY_BYTES = 256 << 20
+
+
+def moe_only(ne, torch, args):
+    """MoE launch pairs over all layers' experts, then three copies of a
+    256 MiB buffer (a plain copy kernel of known traffic: 256 MiB read and
+    256 MiB written per dispatch)."""
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=64, max_batch=1)
+    eng = ne.Engine(cfg, device=0)
+    stream = torch.cuda.current_stream()
+    eng.init_random(args.seed, stream)
+    torch.cuda.synchronize()
+    moe_s = time_moe(ne, torch, eng, cfg, max(args.moe_reps, 1))
+    eng.close()
+    src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, "
+        f"{moe_bytes(cfg) / moe_s / 1e9:.0f} GB/s; copy kernel {COPY_BYTES} B x3 done")
+
+
 def load_traffic():
     path = os.path.join(ROOT, "profiles", "moe_experts_traffic.json")
     if os.path.exists(path):
@@ -147,6 +170,9 @@ def main():
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--moe-only", action="store_true",
+                    help="only the MoE launch-pair timing plus a plain 256 MiB device copy "
+                         "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -164,6 +190,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.moe_only:
+        moe_only(ne, torch, args)
+        return
     max_seq = args.prompt + args.warmup + args.steps + 8
     cfg = ne.config_preset("gpt-oss-20b", max_seq=max_seq, max_batch=1)
     log(f"[bench] creating gpt-oss-20b context (max_seq {max_seq})")
@@ -199,10 +228,12 @@ def main():
     toks = eng.read_tokens(args.prompt, 8)
     log(f"[bench] first generated ids {toks[0].tolist()}")
 
-    moe_s = time_moe(ne, torch, eng, cfg, args.moe_reps)
     mb = moe_bytes(cfg)
-    moe_gbs = mb / moe_s / 1e9
-    log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, {moe_gbs:.0f} GB/s")
+    moe_s = moe_gbs = None
+    if args.moe_reps > 0:  # 0 skips it (profiling runs that want only the decode loop)
+        moe_s = time_moe(ne, torch, eng, cfg, args.moe_reps)
+        moe_gbs = mb / moe_s / 1e9
+        log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, {moe_gbs:.0f} GB/s")
     eng.close()
 
     cpu = None
@@ -232,10 +263,11 @@ def main():
         "step_hbm_gbs": round(bpt * tok_s / 1e9, 1),
         "step_hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"kernel": "MoE expert FFN (k_moe_gate_up + k_moe_down), batch 1, 4 experts",
-                     "bound": "hbm", "achieved": round(moe_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(moe_gbs / HBM_PEAK_GBS, 4),
+                     "bound": "hbm", "achieved": moe_gbs and round(moe_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": moe_gbs and round(moe_gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic(), "bytes_per_launch": mb,
-                     "us_per_launch": round(moe_s * 1e6, 3)},
+                     "us_per_launch": moe_s and round(moe_s * 1e6, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -68,8 +68,7 @@ struct neon_ctx {
            *act = nullptr;
   int32_t* moe_idx = nullptr;
   float* moe_score = nullptr;
-  float *part_o = nullptr, *part_ml = nullptr;
-  int32_t* attn_cnt = nullptr;
+  float* router_lg = nullptr;
   float* logits = nullptr;
   float* lm_part_val = nullptr;
   int32_t* lm_part_idx = nullptr;
@@ -311,8 +310,6 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   const size_t Bm = c.max_batch, half = c.head_dim / 2;
   ctx->s_slide = attn_splits(c.max_seq, c.sliding_window);
   ctx->s_full = attn_splits(c.max_seq, 0);
-  const int smax = std::max(ctx->s_full, ctx->s_slide);
-  const int G = c.n_heads / c.n_kv_heads;
   ctx->lm_nblk = gemv_default_grid(c.vocab, 4);
   ctx->tok_stride = c.max_seq + 1;
   off = 0;
@@ -321,9 +318,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_ao = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
                o_act = take(Bm * c.top_k * I * 2),
                o_idx = take(Bm * c.top_k * 4), o_sc = take(Bm * c.top_k * 4),
-               o_po = take(Bm * c.n_kv_heads * smax * (size_t)G * c.head_dim * 4),
-               o_pml = take(Bm * c.n_kv_heads * smax * (size_t)G * 2 * 4),
-               o_cnt = take(Bm * c.n_kv_heads * 4),
+               o_rlg = take(Bm * c.n_experts * 4),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -339,8 +334,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->h = (uint16_t*)(W + o_h); ctx->xn = (uint16_t*)(W + o_xn);
   ctx->qkv = (uint16_t*)(W + o_qkv); ctx->attn_out = (uint16_t*)(W + o_ao);
   ctx->act = (uint16_t*)(W + o_act); ctx->moe_idx = (int32_t*)(W + o_idx);
-  ctx->moe_score = (float*)(W + o_sc); ctx->part_o = (float*)(W + o_po);
-  ctx->part_ml = (float*)(W + o_pml); ctx->attn_cnt = (int32_t*)(W + o_cnt);
+  ctx->moe_score = (float*)(W + o_sc);
+  ctx->router_lg = (float*)(W + o_rlg);
   ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
@@ -538,8 +533,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     a.q_src = ctx->qkv; a.kc = ctx->kc + (size_t)l * ctx->kv_layer_elems;
     a.vc = ctx->vc + (size_t)l * ctx->kv_layer_elems; a.sinks = w.sinks;
     a.pos = ctx->pos; a.cos_t = ctx->cos_t; a.sin_t = ctx->sin_t;
-    a.out = ctx->attn_out; a.part_o = ctx->part_o; a.part_ml = ctx->part_ml;
-    a.counters = ctx->attn_cnt; a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
+    a.out = ctx->attn_out; a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.fused = 1; a.q_stride = qkv_rows;
     launch_attn(a, st);
@@ -548,13 +542,17 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     o.N = H; o.K = c.n_heads * D; o.B = B; o.rpw = 2;
     o.nblk = gemv_default_grid(o.N, o.rpw);
     launch_gemv_bf16(o, st);
-    launch_router(ctx->h, w.mlp_norm, c.rms_eps, ctx->xn, w.router_w, w.router_b,
-                  ctx->moe_idx, ctx->moe_score, nullptr, B, c.n_experts, H,
-                  c.top_k, st);
+    RouterArgs r;
+    r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
+    r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
+    r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
+    launch_router(r, st);
     MoeArgs m;
     m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
     m.dn_codes = w.dn_codes; m.dn_scales = w.dn_scales; m.dn_bias = w.dn_bias;
-    m.idx = ctx->moe_idx; m.score = ctx->moe_score; m.xn = ctx->xn; m.act = ctx->act;
+    m.router_lg = ctx->router_lg; m.idx = nullptr; m.score = nullptr;
+    m.idx_out = ctx->moe_idx; m.score_out = ctx->moe_score; m.E = c.n_experts;
+    m.xn = ctx->xn; m.act = ctx->act;
     m.residual = ctx->h; m.out = ctx->h; m.B = B; m.H = H; m.I = c.intermediate;
     m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
     launch_moe(m, st);
@@ -807,8 +805,18 @@ extern "C" neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
   if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < 8 ||
       H % 8 || H > 8192)
     KFAIL(NEON_EINVAL, "neon_router_topk: bad shape B=%d E=%d H=%d k=%d", B, E, H, k);
-  launch_router(x, nullptr, 0.0f, nullptr, W, b, idx, score, logits, B, E, H, k, S(stream));
-  KLAUNCHED();
+  hipStream_t st = S(stream);
+  float* scratch = nullptr;
+  if (!logits && hipMallocAsync((void**)&scratch, (size_t)B * E * 4, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_router_topk: scratch allocation failed");
+  RouterArgs r;
+  r.x = x; r.W = W; r.bias = b; r.lg_out = logits ? logits : scratch; r.idx = idx;
+  r.score = score; r.B = B; r.E = E; r.H = H; r.k = k;
+  launch_router(r, st);
+  hipError_t e = hipGetLastError();
+  if (scratch) (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_router_topk: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
 }
 
 extern "C" neon_status neon_moe_layer(
@@ -824,22 +832,22 @@ extern "C" neon_status neon_moe_layer(
       H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
     KFAIL(NEON_EINVAL, "neon_moe_layer: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
   hipStream_t st = S(stream);
-  // scratch: act [B][k][I] bf16, then idx [B][k] and score [B][k] for the
-  // outputs the caller did not ask for
+  // scratch: act [B][k][I] bf16, then the router logits [B][E]
   const size_t act_b = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
-  const size_t ib = ((size_t)B * k * 4 + 255) & ~(size_t)255;
   char* scratch = nullptr;
-  if (hipMallocAsync((void**)&scratch, act_b + 2 * ib, st) != hipSuccess)
+  if (hipMallocAsync((void**)&scratch, act_b + (size_t)B * E * 4, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_moe_layer: scratch allocation failed");
   uint16_t* act = (uint16_t*)scratch;
-  int32_t* d_idx = idx ? idx : (int32_t*)(scratch + act_b);
-  float* d_sc = score ? score : (float*)(scratch + act_b + ib);
-  launch_router(x, nullptr, 0.0f, nullptr, router_w, router_b, d_idx, d_sc, nullptr,
-                B, E, H, k, st);
+  float* lg = (float*)(scratch + act_b);
+  RouterArgs r;
+  r.x = x; r.W = router_w; r.bias = router_b; r.lg_out = lg;
+  r.B = B; r.E = E; r.H = H; r.k = k;
+  launch_router(r, st);
   MoeArgs m;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
   m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
-  m.idx = d_idx; m.score = d_sc; m.xn = x; m.act = act; m.residual = residual;
+  m.router_lg = lg; m.idx = nullptr; m.score = nullptr; m.idx_out = idx;
+  m.score_out = score; m.E = E; m.xn = x; m.act = act; m.residual = residual;
   m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
   launch_moe(m, st);
   hipError_t e = hipGetLastError();
@@ -864,7 +872,8 @@ extern "C" neon_status neon_moe_experts(
   MoeArgs m;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
   m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
-  m.idx = idx; m.score = score; m.xn = x; m.act = act; m.residual = residual;
+  m.router_lg = nullptr; m.idx = idx; m.score = score; m.idx_out = nullptr;
+  m.score_out = nullptr; m.E = E; m.xn = x; m.act = act; m.residual = residual;
   m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
   launch_moe(m, S(stream));
   KLAUNCHED();
@@ -885,24 +894,11 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
     KFAIL(NEON_EINVAL, "neon_attn_decode: Hq/Hkv must be 1, 2, 4 or 8");
   // pos[b] must lie in [0, T_max); it is device data, so the kernel trusts it.
   hipStream_t st = S(stream);
-  const int S_ = attn_splits(T_max, window);
-  char* scratch = nullptr;
-  const size_t po = (size_t)B * Hkv * S_ * G * 64 * 4, pml = (size_t)B * Hkv * S_ * G * 2 * 4,
-               cnt = (size_t)B * Hkv * 4;
-  if (hipMallocAsync((void**)&scratch, po + pml + cnt + 512, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
-  int32_t* counters = (int32_t*)(scratch + po + pml);
-  if (hipMemsetAsync(counters, 0, cnt, st) != hipSuccess)
-    KFAIL(NEON_EHIP, "neon_attn_decode: memset failed");
   AttnArgs a;
   a.q_src = q; a.kc = const_cast<uint16_t*>(k_cache); a.vc = const_cast<uint16_t*>(v_cache);
   a.sinks = sinks; a.pos = pos; a.cos_t = nullptr; a.sin_t = nullptr; a.out = out;
-  a.part_o = (float*)scratch; a.part_ml = (float*)(scratch + po); a.counters = counters;
-  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window; a.S = S_;
-  a.fused = 0; a.q_stride = Hq * D;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window;
+  a.S = attn_splits(T_max, window); a.fused = 0; a.q_stride = Hq * D;
   launch_attn(a, st);
-  hipError_t e = hipGetLastError();
-  (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
-  return NEON_OK;
+  KLAUNCHED();
 }

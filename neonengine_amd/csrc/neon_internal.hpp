@@ -57,16 +57,29 @@ void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
                        hipStream_t st);
 
 // ---- router / MoE --------------------------------------------------------------
-void launch_router(const uint16_t* x, const uint16_t* nw, float eps,
-                   uint16_t* xn_out, const uint16_t* W, const uint16_t* bias,
-                   int32_t* idx, float* score, float* logits_out, int B, int E,
-                   int H, int k, hipStream_t st);
+struct RouterArgs {
+  const uint16_t* x = nullptr;       // [B][H]
+  const uint16_t* norm_w = nullptr;  // fused RMSNorm of x when not NULL
+  float eps = 1e-5f;
+  uint16_t* xn_out = nullptr;        // normalised x [B][H] (may be NULL)
+  const uint16_t *W = nullptr, *bias = nullptr;
+  float* lg_out = nullptr;           // logits [B][E]
+  int32_t* idx = nullptr;            // top-k outputs (NULL: logits only)
+  float* score = nullptr;
+  int B = 1, E = 0, H = 0, k = 0;
+};
+// router logits, then (when a.idx) the top-k / softmax
+void launch_router(const RouterArgs& a, hipStream_t st);
 
 struct MoeArgs {
   const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
   const uint16_t *gu_bias, *dn_bias;
-  const int32_t* idx;
-  const float* score;
+  const float* router_lg;    // [B][E] router logits: experts chosen in-kernel
+  const int32_t* idx;        // else the given expert ids [B][k] ...
+  const float* score;        // ... and weights [B][k]
+  int32_t* idx_out;          // chosen ids / weights (may be NULL)
+  float* score_out;
+  int E;
   const uint16_t* xn;        // [B][H] normalised input
   uint16_t* act;             // [B][k][I] scratch
   const uint16_t* residual;  // may be NULL
@@ -84,8 +97,6 @@ struct AttnArgs {
   const int32_t* pos;     // [B]
   const float *cos_t, *sin_t;
   uint16_t* out;          // [B][Hq*D]
-  float *part_o, *part_ml;
-  int32_t* counters;      // [B][Hkv], zero between launches
   int B, Hq, Hkv, T_max, window, S, fused, q_stride;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);

@@ -160,28 +160,86 @@ __device__ __forceinline__ float fp4_row_partial(const Fp4Row<P>& r,
   return acc;
 }
 
-// x (bf16 [K] in LDS) -> fp32 registers for the lane's MXFP4 units
+// x (bf16, global) -> fp32 registers for the lane's MXFP4 units
+// u = lane + 64 p (32 elements = 4 x 16 B each); lanes past U get zeros.
 template <int P>
-__device__ __forceinline__ void fp4_load_x(float (&xr)[P][32],
-                                           const uint4* __restrict__ xs, int U,
-                                           int lane) {
+__device__ __forceinline__ void wave_load_x_fp4(float (&xr)[P][32],
+                                                const uint16_t* __restrict__ x,
+                                                int U, int lane) {
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  uint4 raw[P][4];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int u = lane + 64 * p;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      unpack8((u < U) ? xs[u * 4 + q] : make_uint4(0, 0, 0, 0), &xr[p][8 * q]);
+    for (int q = 0; q < 4; ++q) raw[p][q] = (u < U) ? xv[u * 4 + q] : make_uint4(0, 0, 0, 0);
   }
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) unpack8(raw[p][q], &xr[p][8 * q]);
 }
 
+// x (bf16, global) -> fp32 registers for the lane's bf16 units u = lane + 64 p,
+// optionally RMS-normalised (HFM:57-62).  The canonical RMSNorm (oracle
+// or_c_rmsnorm) sums squares with exactly these lane partials: ss = fmaf(x_k,
+// x_k, ss) over the lane's units in increasing k, then the xor butterfly, so
+// every wave forms the identical r = 1 / sqrt(ss / K + eps) (correctly rounded
+// division and square root) on its own, with no LDS and no barrier;
+// y_k = bf16(w_k * (x_k * r)).  If xn_out is not NULL the wave also stores the
+// normalised vector there (callers pass it from one wave per row).
 template <int P>
-__device__ __forceinline__ void bf16_load_x(float (&xr)[P][8],
-                                            const uint4* __restrict__ xs,
-                                            int U, int lane) {
+__device__ __forceinline__ void wave_load_x_bf16(float (&xr)[P][8],
+                                                 const uint16_t* __restrict__ x,
+                                                 const uint16_t* __restrict__ nw,
+                                                 float eps, int K, int lane,
+                                                 uint16_t* __restrict__ xn_out) {
+  const int U = K / 8;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  uint4 raw[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int u = lane + 64 * p;
-    unpack8((u < U) ? xs[u] : make_uint4(0, 0, 0, 0), xr[p]);
+    raw[p] = (u < U) ? xv[u] : make_uint4(0, 0, 0, 0);
+  }
+  if (nw == nullptr) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) unpack8(raw[p], xr[p]);
+    return;
+  }
+  uint4 wr[P];
+  const uint4* wv = reinterpret_cast<const uint4*>(nw);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = lane + 64 * p;
+    wr[p] = (u < U) ? wv[u] : make_uint4(0, 0, 0, 0);
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    if (lane + 64 * p < U) {
+      float f[8];
+      unpack8(raw[p], f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = lane + 64 * p;
+    float a[8], w8[8];
+    unpack8(raw[p], a);
+    unpack8(wr[p], w8);
+    uint32_t o4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o4[j] = pack_bf2(__fmul_rn(w8[2 * j], __fmul_rn(a[2 * j], r)),
+                       __fmul_rn(w8[2 * j + 1], __fmul_rn(a[2 * j + 1], r)));
+    const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    unpack8((u < U) ? o : make_uint4(0, 0, 0, 0), xr[p]);
+    if (xn_out != nullptr && u < U) reinterpret_cast<uint4*>(xn_out)[u] = o;
   }
 }
 
@@ -208,58 +266,6 @@ __device__ __forceinline__ float bf16_row_partial(const uint4 (&w)[P],
   return acc;
 }
 
-// Block-wide: x[K] (bf16, global) -> LDS, optionally RMS-normalised with
-// weight nw (HFM:57-62).  Canonical form (oracle or_c_rmsnorm): wave 0 forms
-// ss with lane partials ss = fmaf(x_k, x_k, ss) over the units
-// u = l + 64 p (8 elements each, increasing k) and the xor butterfly; then
-// r = 1 / sqrt(ss / K + eps) with correctly rounded fp32 division and square
-// root; y_k = bf16(w_k * (x_k * r)).  If xn_out is not NULL the block also
-// writes the normalised vector there (callers pass it from one block per row).
-__device__ void block_load_x(uint4* __restrict__ xs,
-                             const uint16_t* __restrict__ x,
-                             const uint16_t* __restrict__ nw, float eps, int K,
-                             uint16_t* __restrict__ xn_out) {
-  __shared__ float r_s;
-  const int U8 = K / 8;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  if (nw == nullptr) {
-    for (int i = threadIdx.x; i < U8; i += blockDim.x) xs[i] = xv[i];
-    __syncthreads();
-    return;
-  }
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    float ss = 0.0f;
-    for (int u = lane; u < U8; u += 64) {
-      float f[8];
-      unpack8(xv[u], f);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0)
-      r_s = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
-  }
-  __syncthreads();
-  const float r = r_s;
-  const uint4* wv = reinterpret_cast<const uint4*>(nw);
-  for (int i = threadIdx.x; i < U8; i += blockDim.x) {
-    float a[8], b[8];
-    unpack8(xv[i], a);
-    unpack8(wv[i], b);
-    uint32_t o4[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o4[j] = pack_bf2(__fmul_rn(b[2 * j], __fmul_rn(a[2 * j], r)),
-                       __fmul_rn(b[2 * j + 1], __fmul_rn(a[2 * j + 1], r)));
-    const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-    xs[i] = o;
-    if (xn_out != nullptr) reinterpret_cast<uint4*>(xn_out)[i] = o;
-  }
-  __syncthreads();
-}
-
-constexpr int kMaxK = 8192;  // LDS holds x [K] bf16 (16 KB)
 
 // ===========================================================================
 // Standalone MXFP4 GEMV: y[b][n] = bf16(dot(W[n], x[b]) + bias[n]).
@@ -272,18 +278,15 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
     uint16_t* __restrict__ y, int N, int K, int rpw) {
-  __shared__ uint4 xs[kMaxK / 8];
   const int U = K / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.z;
   const int r0 = (blockIdx.x * 4 + wave) * rpw;
   const int r1 = min(r0 + rpw, N);
+  if (r0 >= r1) return;
   Fp4Row<P> cur;
-  if (r0 < r1)
-    fp4_load_row<P>(cur, codes + (size_t)r0 * (K / 2), scales + (size_t)r0 * U,
-                    U, lane);
-  block_load_x(xs, x + (size_t)b * K, nullptr, 0.0f, K, nullptr);
+  fp4_load_row<P>(cur, codes + (size_t)r0 * (K / 2), scales + (size_t)r0 * U, U, lane);
   float xr[P][32];
-  fp4_load_x<P>(xr, xs, U, lane);
+  wave_load_x_fp4<P>(xr, x + (size_t)b * K, U, lane);
   for (int r = r0; r < r1; ++r) {
     Fp4Row<P> nxt;
     if (r + 1 < r1)
@@ -341,7 +344,6 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
     uint16_t* __restrict__ y, float* __restrict__ logits,
     float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K,
     int rpw) {
-  __shared__ uint4 xs[kMaxK / 8];
   __shared__ float bv_s[4];
   __shared__ int32_t bi_s[4];
   const int U = K / 8, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -351,9 +353,8 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   int g = blockIdx.x * 4 + wave;
   uint4 cur[P];
   if (g < ngroups) bf16_load_row<P>(cur, W + (size_t)g * rpw * K, U, lane);
-  block_load_x(xs, x + (size_t)b * K, nw, eps, K, nullptr);
   float xr[P][8];
-  bf16_load_x<P>(xr, xs, U, lane);
+  if (g < ngroups) wave_load_x_bf16<P>(xr, x + (size_t)b * K, nw, eps, K, lane, nullptr);
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
   for (; g < ngroups; g += gstride) {
@@ -502,20 +503,33 @@ void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
 }
 
 // ===========================================================================
-// Standalone RMSNorm (canonical form of block_load_x)
+// Standalone RMSNorm (canonical form of wave_load_x_bf16), one wave per row
 // ===========================================================================
-__global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t* __restrict__ x,
-                                                 const uint16_t* __restrict__ w,
-                                                 uint16_t* __restrict__ out,
-                                                 int H, float eps) {
-  __shared__ uint4 xs[kMaxK / 8];
+template <int P>
+__global__ __launch_bounds__(64) void k_rmsnorm(const uint16_t* __restrict__ x,
+                                                const uint16_t* __restrict__ w,
+                                                uint16_t* __restrict__ out,
+                                                int H, float eps) {
   const int b = blockIdx.x;
-  block_load_x(xs, x + (size_t)b * H, w, eps, H, out + (size_t)b * H);
+  float xr[P][8];
+  wave_load_x_bf16<P>(xr, x + (size_t)b * H, w, eps, H, threadIdx.x,
+                      out + (size_t)b * H);
 }
 
 void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
                     int H, float eps, hipStream_t st) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(B), dim3(256), 0, st, x, w, out, H, eps);
+  const int P = (H / 8 + 63) / 64;
+  switch (P) {
+#define N_CASE(PP)                                                             \
+  case PP:                                                                     \
+    hipLaunchKernelGGL(k_rmsnorm<PP>, dim3(B), dim3(64), 0, st, x, w, out, H,  \
+                       eps);                                                   \
+    break;
+    N_CASE(1) N_CASE(2) N_CASE(3) N_CASE(4) N_CASE(5) N_CASE(6) N_CASE(7)
+    N_CASE(8)
+    default: N_CASE(16)
+#undef N_CASE
+  }
 }
 
 // ===========================================================================
@@ -559,95 +573,116 @@ void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
 }
 
 // ===========================================================================
-// Router (HFM:117-130), one block per batch row, 8 waves.  Optional fused
-// RMSNorm prologue (then the normalised x is also written to xn_out for the
-// experts).  Logits: the canonical bf16 row dot + bias (fp32 add).  Top-k by
-// value, ties to the lower expert index; softmax over the k selected values:
+// Router (HFM:117-130).
+// k_router_logits: grid (E, B), one wave per (expert, row) forms the row's
+// (optionally RMS-normalised) input in registers and the expert's logit =
+// canonical bf16 row dot + bias (fp32 add).  Wave (0, b) stores the
+// normalised row to xn_out for the experts.
+// route_topk: one wave selects the top k of a row's E logits by value, ties
+// to the lower expert index, and forms the softmax over them:
 // e_t = exp(v_t - v_0) (neon_expf), s = sum in rank order, score_t = e_t / s.
+// Every MoE block runs it on the logits itself, so no block waits on another.
 // ===========================================================================
 constexpr int kMaxExperts = 256;
+constexpr int kMaxTopK = 16;
 
 template <int P>
-__global__ __launch_bounds__(512) void k_router(
+__global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
-    const uint16_t* __restrict__ bias, int32_t* __restrict__ idx,
-    float* __restrict__ score, float* __restrict__ logits_out, int E, int H,
-    int k) {
-  __shared__ uint4 xs[kMaxK / 8];
-  __shared__ float lg[kMaxExperts];
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nwaves = blockDim.x >> 6;
+    const uint16_t* __restrict__ bias, float* __restrict__ lg_out, int E,
+    int H) {
+  const int e = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int U = H / 8;
-  block_load_x(xs, x + (size_t)b * H, nw, eps, H,
-               xn_out ? xn_out + (size_t)b * H : nullptr);
+  uint4 w[P];
+  bf16_load_row<P>(w, W + (size_t)e * H, U, lane);
   float xr[P][8];
-  bf16_load_x<P>(xr, xs, U, lane);
-  for (int e = wave; e < E; e += nwaves) {
-    uint4 w[P];
-    bf16_load_row<P>(w, W + (size_t)e * H, U, lane);
-    const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
-    if (lane == 0) lg[e] = __fadd_rn(acc, bf2f(bias[e]));
-  }
-  __syncthreads();
-  if (wave == 0) {
-    if (logits_out)
-      for (int e = lane; e < E; e += 64) logits_out[(size_t)b * E + e] = lg[e];
-    float vals[16];
-    int32_t ids[16];
-    uint64_t used[kMaxExperts / 64] = {0, 0, 0, 0};
-    for (int t = 0; t < k; ++t) {
-      float v = -INFINITY;
-      int32_t i = 0x7fffffff;
-      for (int e = lane; e < E; e += 64) {
-        if ((used[e >> 6] >> (e & 63)) & 1ull) continue;
-        if (i == 0x7fffffff || lg[e] > v) { v = lg[e]; i = e; }
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, 64);
-        const int32_t oi = __shfl_xor(i, off, 64);
-        const bool take = (oi != 0x7fffffff) &&
-                          (i == 0x7fffffff || ov > v || (ov == v && oi < i));
-        if (take) { v = ov; i = oi; }
-      }
-      used[i >> 6] |= 1ull << (i & 63);
-      vals[t] = v;
-      ids[t] = i;
-    }
-    if (lane == 0) {
-      float ex[16], s = 0.0f;
-      for (int t = 0; t < k; ++t) {
-        ex[t] = neon_expf(__fsub_rn(vals[t], vals[0]));
-        s = __fadd_rn(s, ex[t]);
-      }
-      for (int t = 0; t < k; ++t) {
-        idx[b * k + t] = ids[t];
-        score[b * k + t] = __fdiv_rn(ex[t], s);
-      }
-    }
-  }
+  wave_load_x_bf16<P>(xr, x + (size_t)b * H, nw, eps, H, lane,
+                      (xn_out != nullptr && e == 0) ? xn_out + (size_t)b * H : nullptr);
+  const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
+  if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias[e]));
 }
 
-void launch_router(const uint16_t* x, const uint16_t* nw, float eps,
-                   uint16_t* xn_out, const uint16_t* W, const uint16_t* bias,
-                   int32_t* idx, float* score, float* logits_out, int B, int E,
-                   int H, int k, hipStream_t st) {
-  const int P = (H / 8 + 63) / 64;
+// One wave; all lanes return the same ids[0..k) and scores[0..k).
+__device__ __forceinline__ void route_topk(const float* __restrict__ lg, int E,
+                                           int k, int lane, int32_t* ids,
+                                           float* scores) {
+  float v[kMaxExperts / 64];
+#pragma unroll
+  for (int q = 0; q < kMaxExperts / 64; ++q) {
+    const int e = lane + 64 * q;
+    v[q] = e < E ? lg[e] : -INFINITY;
+  }
+  uint32_t used = 0;
+  float vals[kMaxTopK];
+#pragma unroll
+  for (int t = 0; t < kMaxTopK; ++t) {
+    if (t >= k) continue;  // k is wave-uniform; continue keeps the loop unrollable
+    float bv = -INFINITY;
+    int32_t bi = 0x7fffffff;
+#pragma unroll
+    for (int q = 0; q < kMaxExperts / 64; ++q) {
+      const int e = lane + 64 * q;
+      if (e < E && !((used >> q) & 1u) && (bi == 0x7fffffff || v[q] > bv)) {
+        bv = v[q];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int32_t oi = __shfl_xor(bi, off, 64);
+      const bool take = (oi != 0x7fffffff) &&
+                        (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
+      if (take) { bv = ov; bi = oi; }
+    }
+    if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+    vals[t] = bv;
+    ids[t] = bi;
+  }
+  float ex[kMaxTopK], sum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < kMaxTopK; ++t) {
+    if (t >= k) continue;
+    ex[t] = neon_expf(__fsub_rn(vals[t], vals[0]));
+    sum = __fadd_rn(sum, ex[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < kMaxTopK; ++t)
+    if (t < k) scores[t] = __fdiv_rn(ex[t], sum);
+}
+
+__global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
+                                             int32_t* __restrict__ idx,
+                                             float* __restrict__ score, int E,
+                                             int k) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  int32_t ids[kMaxTopK];
+  float sc[kMaxTopK];
+  route_topk(lg + (size_t)b * E, E, k, lane, ids, sc);
+#pragma unroll
+  for (int t = 0; t < kMaxTopK; ++t)
+    if (t < k && t == lane) { idx[b * k + t] = ids[t]; score[b * k + t] = sc[t]; }
+}
+
+void launch_router(const RouterArgs& a, hipStream_t st) {
+  const int P = (a.H / 8 + 63) / 64;
+  dim3 grid(a.E, a.B);
   switch (P) {
-#define R_CASE(PP)                                                           \
-  case PP:                                                                   \
-    hipLaunchKernelGGL(k_router<PP>, dim3(B), dim3(512), 0, st, x, nw, eps,  \
-                       xn_out, W, bias, idx, score, logits_out, E, H, k);    \
+#define R_CASE(PP)                                                            \
+  case PP:                                                                    \
+    hipLaunchKernelGGL(k_router_logits<PP>, grid, dim3(64), 0, st, a.x,       \
+                       a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E, \
+                       a.H);                                                  \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)
-    default:
-      hipLaunchKernelGGL(k_router<16>, dim3(B), dim3(512), 0, st, x, nw, eps,
-                         xn_out, W, bias, idx, score, logits_out, E, H, k);
+    default: R_CASE(16)
 #undef R_CASE
   }
+  if (a.idx != nullptr)
+    hipLaunchKernelGGL(k_topk, dim3(a.B), dim3(64), 0, st, a.lg_out, a.idx,
+                       a.score, a.E, a.k);
 }
 
 // ===========================================================================
@@ -669,32 +704,62 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
   return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
 }
 
+// Expert choice: from the router logits (route_topk) when lg != NULL, else
+// from the given idx/score arrays.
+__device__ __forceinline__ void moe_route(const float* __restrict__ lg,
+                                          const int32_t* __restrict__ idx_in,
+                                          const float* __restrict__ score_in,
+                                          int b, int E, int k, int lane,
+                                          int32_t* ids, float* sc) {
+  if (lg != nullptr) {
+    route_topk(lg + (size_t)b * E, E, k, lane, ids, sc);
+  } else {
+#pragma unroll
+    for (int t = 0; t < kMaxTopK; ++t) {
+      if (t < k) {
+        ids[t] = idx_in[b * k + t];
+        sc[t] = score_in[b * k + t];
+      }
+    }
+  }
+}
+
 template <int P>
 __global__ __launch_bounds__(256) void k_moe_gate_up(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
-    const uint16_t* __restrict__ gu_bias, const int32_t* __restrict__ idx,
+    const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
+    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
+    int32_t* __restrict__ idx_out, float* __restrict__ score_out, int E,
     const uint16_t* __restrict__ xn, uint16_t* __restrict__ act, int H, int I,
     int k, int jpw, float alpha, float limit) {
-  __shared__ uint4 xs[kMaxK / 8];
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = idx[b * k + slot];
+  int32_t ids[kMaxTopK];
+  float rsc[kMaxTopK];
+  moe_route(router_lg, idx_in, score_in, b, E, k, lane, ids, rsc);
+  if (blockIdx.x == 0 && slot == 0 && wave == 0 && idx_out != nullptr) {
+#pragma unroll
+    for (int t = 0; t < kMaxTopK; ++t)
+      if (t < k && t == lane) { idx_out[b * k + t] = ids[t]; score_out[b * k + t] = rsc[t]; }
+  }
+  int e = ids[0];
+#pragma unroll
+  for (int t = 1; t < kMaxTopK; ++t)
+    if (t < k && t == slot) e = ids[t];
   const size_t rows = (size_t)2 * I;
   const uint8_t* codes = gu_codes + (size_t)e * rows * (H / 2);
   const uint8_t* scales = gu_scales + (size_t)e * rows * U;
   const uint16_t* bias = gu_bias + (size_t)e * rows;
   const int j0 = (blockIdx.x * 4 + wave) * jpw;
   const int j1 = min(j0 + jpw, I);
+  if (j0 >= j1) return;
   Fp4Row<P> cg, cu;
-  if (j0 < j1) {
-    fp4_load_row<P>(cg, codes + (size_t)(2 * j0) * (H / 2),
-                    scales + (size_t)(2 * j0) * U, U, lane);
-    fp4_load_row<P>(cu, codes + (size_t)(2 * j0 + 1) * (H / 2),
-                    scales + (size_t)(2 * j0 + 1) * U, U, lane);
-  }
-  block_load_x(xs, xn + (size_t)b * H, nullptr, 0.0f, H, nullptr);
+  fp4_load_row<P>(cg, codes + (size_t)(2 * j0) * (H / 2),
+                  scales + (size_t)(2 * j0) * U, U, lane);
+  fp4_load_row<P>(cu, codes + (size_t)(2 * j0 + 1) * (H / 2),
+                  scales + (size_t)(2 * j0 + 1) * U, U, lane);
   float xr[P][32];
-  fp4_load_x<P>(xr, xs, U, lane);
+  wave_load_x_fp4<P>(xr, xn + (size_t)b * H, U, lane);
   uint16_t* out = act + ((size_t)b * k + slot) * I;
   for (int j = j0; j < j1; ++j) {
     Fp4Row<P> ng, nu;
@@ -724,13 +789,20 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
 template <int P>
 __global__ __launch_bounds__(1024) void k_moe_down(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
-    const uint16_t* __restrict__ dn_bias, const int32_t* __restrict__ idx,
-    const float* __restrict__ score, const uint16_t* __restrict__ act,
-    const uint16_t* residual, uint16_t* out, int H, int I, int k, int rpw) {
-  __shared__ float red[16][64];
+    const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
+    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
+    int E, const uint16_t* __restrict__ act, const uint16_t* residual,
+    uint16_t* out, int H, int I, int k, int rpw) {
+  __shared__ float red[kMaxTopK][64];
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
-  const int e = idx[b * k + slot];
+  int32_t ids[kMaxTopK];
+  float rsc[kMaxTopK];
+  moe_route(router_lg, idx_in, score_in, b, E, k, lane, ids, rsc);
+  int e = ids[0];
+#pragma unroll
+  for (int t = 1; t < kMaxTopK; ++t)
+    if (t < k && t == slot) e = ids[t];
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
@@ -740,8 +812,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     fp4_load_row<P>(cur, codes + (size_t)n0 * (I / 2), scales + (size_t)n0 * U,
                     U, lane);
   float xr[P][32];
-  fp4_load_x<P>(xr, reinterpret_cast<const uint4*>(act + ((size_t)b * k + slot) * I),
-                U, lane);
+  wave_load_x_fp4<P>(xr, act + ((size_t)b * k + slot) * I, U, lane);
   for (int n = n0; n < n1; ++n) {
     Fp4Row<P> nxt;
     if (n + 1 < n1)
@@ -755,7 +826,9 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   if (threadIdx.x < n1 - n0) {
     const int t = threadIdx.x, n = n0 + t;
     float y = 0.0f;
-    for (int s = 0; s < k; ++s) y = __builtin_fmaf(score[b * k + s], red[s][t], y);
+#pragma unroll
+    for (int s = 0; s < kMaxTopK; ++s)
+      if (s < k) y = __builtin_fmaf(rsc[s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
@@ -772,12 +845,13 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 #define M_CASE(PP)                                                            \
   case PP:                                                                    \
     hipLaunchKernelGGL(k_moe_gate_up<PP>, dim3(gblk, a.k, a.B), dim3(256), 0, \
-                       st, a.gu_codes, a.gu_scales, a.gu_bias, a.idx, a.xn,   \
+                       st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,   \
+                       a.idx, a.score, a.idx_out, a.score_out, a.E, a.xn,     \
                        a.act, a.H, a.I, a.k, jpw, a.alpha, a.limit);          \
     hipLaunchKernelGGL(k_moe_down<PP>, dim3(dblk, a.B), dim3(64 * a.k), 0,   \
-                       st, a.dn_codes, a.dn_scales, a.dn_bias, a.idx,         \
-                       a.score, a.act, a.residual, a.out, a.H, a.I, a.k,      \
-                       rpw);                                                  \
+                       st, a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg,   \
+                       a.idx, a.score, a.E, a.act, a.residual, a.out, a.H,    \
+                       a.I, a.k, rpw);                                        \
     break;
     M_CASE(1) M_CASE(2) M_CASE(3)
     default: M_CASE(4)
@@ -791,11 +865,10 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 // before P.V.  Keys j in [lo, pos] with lo = pos - window + 1 on sliding
 // layers (HF mask kv_idx > q_idx - window).
 //
-// grid (S, Hkv, B), one wave per block.  Canonical form (oracle
-// or_c_attn_decode):
+// Canonical form (oracle or_c_attn_decode), S splits:
 //   chunks of 64 keys from lo; split s takes chunks [s nch / S, (s+1) nch / S).
 //   score (lane = key): a = fmaf(q_d, k_d, a) over d = 0..63, times 1/8.
-//   per chunk and head: m' = max(m, max_j s_j); alpha = exp(m - m');
+//   per chunk: m' = max(m, max_j s_j); alpha = exp(m - m');
 //     p_j = exp(s_j - m'); l = fmaf(l, alpha, butterfly_sum(p_j));
 //     lane (kg = lane>>3, dq = lane&7) accumulators o *= alpha, then
 //     o = fmaf(p_j, v_j[8 dq + e], o) over the lane's keys j = kg + 8 i.
@@ -803,267 +876,196 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 //   merge (split order s = 0..S-1): M = max(sink, m_s...);
 //     den = exp(sink - M); f_s = exp(m_s - M) (0 for empty splits);
 //     den = fmaf(l_s, f_s, den); acc = fmaf(f_s, o_s, acc); out = bf16(acc * (1/den))
-// S > 1: partials go to global memory and the last split block to arrive
-// (agent-scope atomic counter) merges them; S == 1 merges in registers.
+//
+// grid (Hq, B), block S waves (S <= 16): one block per query head, wave w
+// computes split w, the partials meet in LDS and wave 0 merges them -- no
+// cross-block traffic.  Block x = hh * Hkv + g handles head g * G + hh, so
+// with 8 kv heads the G heads of a group share an XCD (blocks are dealt to
+// the 8 XCDs round-robin) and read their K/V once into that XCD's L2.
 // fused != 0: q_src is the raw qkv row ([Hq + 2 Hkv] heads); the block rotates
-// q itself (YaRN table), and the block owning key `pos` also rotates k and
-// appends k/v to the caches (stream order makes them visible to later steps).
+// its q (YaRN table); the block of the group's first head appends the rotated
+// k and v of position pos to the caches, and every block uses its own copy of
+// that row for key pos.
 // ===========================================================================
 constexpr int kD = 64;
+constexpr int kMaxSplits = 16;
 
-template <int G>
-__global__ __launch_bounds__(64) void k_attn_decode(
+__global__ __launch_bounds__(64 * kMaxSplits) void k_attn_decode(
     const uint16_t* __restrict__ q_src, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, const uint16_t* __restrict__ sinks,
     const int32_t* __restrict__ pos_arr, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, uint16_t* __restrict__ out,
-    float* __restrict__ part_o, float* __restrict__ part_ml,
-    int32_t* __restrict__ counters, int Hq, int Hkv, int T_max, int window,
-    int fused, int q_stride) {
-  __shared__ float qf[G][kD];          // rotated q (bf16 values) as fp32
+    const float* __restrict__ sin_t, uint16_t* __restrict__ out, int Hq,
+    int Hkv, int T_max, int window, int fused, int q_stride) {
+  __shared__ __align__(16) float qf[kD];
   __shared__ uint4 knew[kD / 8], vnew[kD / 8];
-  __shared__ float ps[G][64];          // probabilities of the current chunk
-  __shared__ int is_last_s;
-  const int S = gridDim.x, s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int lane = threadIdx.x;
+  __shared__ float ps[kMaxSplits][64];
+  __shared__ float part_o[kMaxSplits][kD];
+  __shared__ float part_m[kMaxSplits], part_l[kMaxSplits];
+  const int S = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = blockIdx.x % Hkv, hh = blockIdx.x / Hkv, b = blockIdx.y;
+  const int G = Hq / Hkv, h = g * G + hh;
   const int p = pos_arr[b];
   const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
   const int n = p - lo + 1;
   const int nch = (n + 63) >> 6;
-  const int c0 = (int)((int64_t)s * nch / S), c1 = (int)((int64_t)(s + 1) * nch / S);
-  const bool owns_new = fused && c0 < c1 && c1 == nch;
+  const int c0 = (int)((int64_t)w * nch / S), c1 = (int)((int64_t)(w + 1) * nch / S);
   const size_t kv_base = ((size_t)b * Hkv + g) * T_max;
 
-  // ---- q (and the new k/v) into LDS -------------------------------------
+  // ---- q (and the new k/v row) into LDS ---------------------------------
   {
     const uint16_t* qrow = q_src + (size_t)b * q_stride;
     if (fused) {
       const float* cr = cos_t + (size_t)p * (kD / 2);
       const float* sr = sin_t + (size_t)p * (kD / 2);
-      for (int t = lane; t < G * (kD / 2); t += 64) {
-        const int hh = t / (kD / 2), f = t % (kD / 2);
-        const uint16_t* qh = qrow + (size_t)(g * G + hh) * kD;
+      if (tid < kD / 2) {
+        const uint16_t* qh = qrow + (size_t)h * kD;
         float o1, o2;
-        rope_pair(bf2f(qh[f]), bf2f(qh[f + kD / 2]), cr[f], sr[f], o1, o2);
-        qf[hh][f] = bf2f(f2bf(o1));
-        qf[hh][f + kD / 2] = bf2f(f2bf(o2));
-      }
-      if (owns_new && lane < kD / 2) {
+        rope_pair(bf2f(qh[tid]), bf2f(qh[tid + kD / 2]), cr[tid], sr[tid], o1, o2);
+        qf[tid] = bf2f(f2bf(o1));
+        qf[tid + kD / 2] = bf2f(f2bf(o2));
+      } else if (tid >= 64 && tid < 64 + kD / 2) {
+        const int t = tid - 64;
         const uint16_t* kh = qrow + (size_t)(Hq + g) * kD;
         float o1, o2;
-        rope_pair(bf2f(kh[lane]), bf2f(kh[lane + kD / 2]), cr[lane], sr[lane],
-                  o1, o2);
+        rope_pair(bf2f(kh[t]), bf2f(kh[t + kD / 2]), cr[t], sr[t], o1, o2);
         uint16_t* kn16 = reinterpret_cast<uint16_t*>(knew);
-        kn16[lane] = f2bf(o1);
-        kn16[lane + kD / 2] = f2bf(o2);
+        kn16[t] = f2bf(o1);
+        kn16[t + kD / 2] = f2bf(o2);
         const uint32_t* vh =
             reinterpret_cast<const uint32_t*>(qrow + (size_t)(Hq + Hkv + g) * kD);
-        reinterpret_cast<uint32_t*>(vnew)[lane] = vh[lane];
+        reinterpret_cast<uint32_t*>(vnew)[t] = vh[t];
       }
-    } else {
-      for (int t = lane; t < G * kD; t += 64) {
-        const int hh = t / kD, d = t % kD;
-        qf[hh][d] = bf2f(qrow[(size_t)(g * G + hh) * kD + d]);
-      }
+    } else if (tid < kD) {
+      qf[tid] = bf2f(qrow[(size_t)h * kD + tid]);
     }
     __syncthreads();
-    if (owns_new && lane < kD / 8) {
-      reinterpret_cast<uint4*>(kc + (kv_base + p) * kD)[lane] = knew[lane];
-      reinterpret_cast<uint4*>(vc + (kv_base + p) * kD)[lane] = vnew[lane];
+    if (fused && hh == 0 && tid < kD / 8) {
+      reinterpret_cast<uint4*>(kc + (kv_base + p) * kD)[tid] = knew[tid];
+      reinterpret_cast<uint4*>(vc + (kv_base + p) * kD)[tid] = vnew[tid];
     }
   }
+  // New-row sources for key p: this block's LDS copy when fused, else the
+  // cache (written before the launch).
+  const int p_lds = fused ? p : -1;
 
-  float m[G], l[G], o[G][8];
+  // q stays in LDS: every lane reads the same address (a broadcast), which
+  // leaves the registers to the chunk's K and V loads.
+  const float4* q4 = reinterpret_cast<const float4*>(qf);
+  float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) {
-    m[hh] = -INFINITY;
-    l[hh] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[hh][e] = 0.0f;
-  }
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
   const int kg = lane >> 3, dq = lane & 7;
 
   for (int c = c0; c < c1; ++c) {
-    // ---- scores: lane = key -------------------------------------------
-    const int j = lo + c * 64 + lane;
+    const int cb = lo + c * 64;
+    const int j = cb + lane;
     const bool valid = j <= p;
-    float kf[kD];
+    // issue every K and V load of the chunk before any arithmetic
+    uint4 kr[kD / 8], vr[8];
     {
-      uint4 kr[kD / 8];
-      if (valid) {
-        if (fused && j == p) {
+      const bool kg_ = valid && j != p_lds;
+      const uint4* src = reinterpret_cast<const uint4*>(kc + (kv_base + (kg_ ? j : lo)) * kD);
 #pragma unroll
-          for (int u = 0; u < kD / 8; ++u) kr[u] = knew[u];
-        } else {
-          const uint4* src = reinterpret_cast<const uint4*>(kc + (kv_base + j) * kD);
+      for (int u = 0; u < kD / 8; ++u) kr[u] = kg_ ? src[u] : make_uint4(0, 0, 0, 0);
 #pragma unroll
-          for (int u = 0; u < kD / 8; ++u) kr[u] = src[u];
-        }
-      } else {
+      for (int i = 0; i < 8; ++i) {
+        const int jk = cb + kg + 8 * i;
+        const bool vg = jk <= p && jk != p_lds;
+        vr[i] = vg ? reinterpret_cast<const uint4*>(vc + (kv_base + jk) * kD)[dq]
+                   : make_uint4(0, 0, 0, 0);
+      }
+      if (valid && j == p_lds) {
 #pragma unroll
-        for (int u = 0; u < kD / 8; ++u) kr[u] = make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < kD / 8; ++u) kr[u] = knew[u];
       }
 #pragma unroll
-      for (int u = 0; u < kD / 8; ++u) unpack8(kr[u], &kf[8 * u]);
+      for (int i = 0; i < 8; ++i)
+        if (cb + kg + 8 * i == p_lds) vr[i] = vnew[dq];
     }
-    float sc[G];
+    float a = 0.0f;
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      float a = 0.0f;
-#pragma unroll
-      for (int d = 0; d < kD; ++d) a = __builtin_fmaf(qf[hh][d], kf[d], a);
-      sc[hh] = valid ? __fmul_rn(a, 0.125f) : -INFINITY;  // 1/sqrt(64), HFM:277
+    for (int u = 0; u < kD / 8; ++u) {
+      float kf[8];
+      unpack8(kr[u], kf);
+      const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
+      a = __builtin_fmaf(qa.x, kf[0], a);
+      a = __builtin_fmaf(qa.y, kf[1], a);
+      a = __builtin_fmaf(qa.z, kf[2], a);
+      a = __builtin_fmaf(qa.w, kf[3], a);
+      a = __builtin_fmaf(qb.x, kf[4], a);
+      a = __builtin_fmaf(qb.y, kf[5], a);
+      a = __builtin_fmaf(qb.z, kf[6], a);
+      a = __builtin_fmaf(qb.w, kf[7], a);
     }
+    const float sc = valid ? __fmul_rn(a, 0.125f) : -INFINITY;  // 1/sqrt(64), HFM:277
+    const float mn = fmaxf(m, wave_max(sc));
+    const float alpha = neon_expf(__fsub_rn(m, mn));
+    const float pj = valid ? neon_expf(__fsub_rn(sc, mn)) : 0.0f;
+    l = __builtin_fmaf(l, alpha, wave_sum(pj));
+    m = mn;
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      const float mn = fmaxf(m[hh], wave_max(sc[hh]));
-      const float alpha = neon_expf(__fsub_rn(m[hh], mn));
-      const float pj = valid ? neon_expf(__fsub_rn(sc[hh], mn)) : 0.0f;
-      l[hh] = __builtin_fmaf(l[hh], alpha, wave_sum(pj));
-      m[hh] = mn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[hh][e] = __fmul_rn(o[hh][e], alpha);
-      ps[hh][lane] = pj;
-    }
-    __syncthreads();
-    // ---- P.V: lane = (key group, dim octet) ---------------------------
+    for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], alpha);
+    ps[w][lane] = pj;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int jj = kg + 8 * i;
-      const int jk = lo + c * 64 + jj;
-      if (jk <= p) {
-        uint4 v;
-        if (fused && jk == p) v = vnew[dq];
-        else v = reinterpret_cast<const uint4*>(vc + (kv_base + jk) * kD)[dq];
+      if (cb + jj <= p) {
         float vf[8];
-        unpack8(v, vf);
+        unpack8(vr[i], vf);
+        const float pv = ps[w][jj];
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-          const float pv = ps[hh][jj];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[hh][e] = __builtin_fmaf(pv, vf[e], o[hh][e]);
-        }
+        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pv, vf[e], o[e]);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   // reduce o over the 8 key groups (lane bits 3..5)
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = o[hh][e];
-      v = __fadd_rn(v, __shfl_xor(v, 8, 64));
-      v = __fadd_rn(v, __shfl_xor(v, 16, 64));
-      v = __fadd_rn(v, __shfl_xor(v, 32, 64));
-      o[hh][e] = v;
-    }
-
-  if (S == 1) {
-    if (kg == 0) {
-#pragma unroll
-      for (int hh = 0; hh < G; ++hh) {
-        const float sk = bf2f(sinks[g * G + hh]);
-        const float M = fmaxf(sk, m[hh]);
-        float den = neon_expf(__fsub_rn(sk, M));
-        const float f = (m[hh] == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(m[hh], M));
-        den = __builtin_fmaf(l[hh], f, den);
-        const float inv = __fdiv_rn(1.0f, den);
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = pack_bf2(__fmul_rn(__builtin_fmaf(f, o[hh][2 * e], 0.0f), inv),
-                          __fmul_rn(__builtin_fmaf(f, o[hh][2 * e + 1], 0.0f), inv));
-        reinterpret_cast<uint4*>(out + (size_t)b * Hq * kD +
-                                 (size_t)(g * G + hh) * kD)[dq] =
-            make_uint4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    return;
+  for (int e = 0; e < 8; ++e) {
+    float v = o[e];
+    v = __fadd_rn(v, __shfl_xor(v, 8, 64));
+    v = __fadd_rn(v, __shfl_xor(v, 16, 64));
+    v = __fadd_rn(v, __shfl_xor(v, 32, 64));
+    o[e] = v;
   }
-
-  // ---- split-KV: publish the partial, the last block merges -------------
-  const size_t pbase = ((size_t)b * Hkv + g) * S;
   if (kg == 0) {
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      float4* dst = reinterpret_cast<float4*>(part_o + ((pbase + s) * G + hh) * kD + dq * 8);
-      dst[0] = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
-      dst[1] = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
-    }
+    for (int e = 0; e < 8; ++e) part_o[w][dq * 8 + e] = o[e];
   }
-  if (lane < G) {
-    float mv = m[0], lv = l[0];
-#pragma unroll
-    for (int hh = 1; hh < G; ++hh)
-      if (lane == hh) { mv = m[hh]; lv = l[hh]; }
-    part_ml[((pbase + s) * G + lane) * 2 + 0] = mv;
-    part_ml[((pbase + s) * G + lane) * 2 + 1] = lv;
-  }
-  __threadfence();
-  if (lane == 0) {
-    const int prev = __hip_atomic_fetch_add(&counters[b * Hkv + g], 1,
-                                            __ATOMIC_ACQ_REL,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    is_last_s = (prev == S - 1);
-  }
+  if (lane == 0) { part_m[w] = m; part_l[w] = l; }
   __syncthreads();
-  if (!is_last_s) return;
-  __threadfence();
-  // lane -> (head hh = lane / 8, dims dq*8 .. +8)
-  {
-    const int hh = lane >> 3;
-    if (hh < G) {
-      const float sk = bf2f(sinks[g * G + hh]);
-      float M = sk;
-      for (int t = 0; t < S; ++t) M = fmaxf(M, part_ml[((pbase + t) * G + hh) * 2]);
-      float den = neon_expf(__fsub_rn(sk, M));
-      float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int t = 0; t < S; ++t) {
-        const float mt = part_ml[((pbase + t) * G + hh) * 2];
-        const float lt = part_ml[((pbase + t) * G + hh) * 2 + 1];
-        const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
-        den = __builtin_fmaf(lt, f, den);
-        const float* src = part_o + ((pbase + t) * G + hh) * kD + dq * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(f, src[e], acc[e]);
-      }
-      const float inv = __fdiv_rn(1.0f, den);
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = pack_bf2(__fmul_rn(acc[2 * e], inv), __fmul_rn(acc[2 * e + 1], inv));
-      reinterpret_cast<uint4*>(out + (size_t)b * Hq * kD +
-                               (size_t)(g * G + hh) * kD)[dq] =
-          make_uint4(w[0], w[1], w[2], w[3]);
-    }
+  if (w != 0) return;
+  // ---- merge the S partials in split order; lane = output dim -----------
+  const float sk = bf2f(sinks[h]);
+  float M = sk;
+  for (int t = 0; t < S; ++t) M = fmaxf(M, part_m[t]);
+  float den = neon_expf(__fsub_rn(sk, M));
+  float acc = 0.0f;
+  for (int t = 0; t < S; ++t) {
+    const float mt = part_m[t];
+    const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
+    den = __builtin_fmaf(part_l[t], f, den);
+    acc = __builtin_fmaf(f, part_o[t][lane], acc);
   }
-  if (lane == 0)
-    __hip_atomic_store(&counters[b * Hkv + g], 0, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+  out[(size_t)b * Hq * kD + (size_t)h * kD + lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
 }
 
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  const int G = a.Hq / a.Hkv;
-  dim3 grid(a.S, a.Hkv, a.B);
-#define A_CASE(GG)                                                             \
-  case GG:                                                                     \
-    hipLaunchKernelGGL(k_attn_decode<GG>, grid, dim3(64), 0, st, a.q_src,      \
-                       a.kc, a.vc, a.sinks, a.pos, a.cos_t, a.sin_t, a.out,    \
-                       a.part_o, a.part_ml, a.counters, a.Hq, a.Hkv, a.T_max,  \
-                       a.window, a.fused, a.q_stride);                         \
-    break;
-  switch (G) {
-    A_CASE(1) A_CASE(2) A_CASE(4)
-    default: A_CASE(8)
-  }
-#undef A_CASE
+  hipLaunchKernelGGL(k_attn_decode, dim3(a.Hq, a.B), dim3(64 * a.S), 0, st,
+                     a.q_src, a.kc, a.vc, a.sinks, a.pos, a.cos_t, a.sin_t,
+                     a.out, a.Hq, a.Hkv, a.T_max, a.window, a.fused, a.q_stride);
 }
 
 int attn_splits(int T_max, int window) {
   const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
   const int s = (span + 63) / 64;
-  return s < 1 ? 1 : (s > 32 ? 32 : s);
+  return s < 1 ? 1 : (s > kMaxSplits ? kMaxSplits : s);
 }
 
 }  // namespace neon

@@ -1,0 +1,98 @@
+"""Summarise rocprofv3 output of the decode loop.
+
+    python -m neonengine_amd.profile_summary <run_kernel_trace.csv> \
+        --last-steps K --kernels-per-step N [--bytes name=BYTES ...]
+    python -m neonengine_amd.profile_summary --pmc <run_counter_collection.csv>
+
+The first form reads a kernel trace; the second averages each counter per
+dispatch and kernel name (rocprofv3 --pmc output, e.g. FETCH_SIZE and
+WRITE_SIZE in KiB per dispatch).
+
+Keeps the last K decode steps (K * N dispatches, N = 1 + 6 n_layers + 2 for
+the gpt-oss step), groups the dispatches by kernel name and prints a Markdown
+table: calls per step, average duration, share of step time, and -- for the
+kernels given algorithmic bytes per launch -- achieved GB/s.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import re
+import sys
+from collections import defaultdict
+
+
+def short(name: str) -> str:
+    name = re.sub(r"\(.*$", "", name)          # drop argument list
+    name = re.sub(r"^void\s+", "", name)
+    name = name.replace("neon::", "")
+    return name
+
+
+def pmc_summary(path: str):
+    vals = defaultdict(float)
+    disp = defaultdict(set)
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            key = (short(r["Kernel_Name"]), r["Counter_Name"])
+            vals[key] += float(r["Counter_Value"])
+            disp[key].add(r.get("Dispatch_Id") or r.get("Correlation_Id"))
+    print("| kernel | counter | dispatches | avg per dispatch |")
+    print("|---|---|---|---|")
+    for key in sorted(vals):
+        n = len(disp[key])
+        print(f"| {key[0]} | {key[1]} | {n} | {vals[key] / n:.1f} |")
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("trace")
+    ap.add_argument("--pmc", action="store_true", help="the file is counter_collection.csv")
+    ap.add_argument("--last-steps", type=int)
+    ap.add_argument("--kernels-per-step", type=int)
+    ap.add_argument("--bytes", action="append", default=[],
+                    help="kernel-name-regex=bytes_per_launch")
+    a = ap.parse_args(argv)
+    if a.pmc:
+        pmc_summary(a.trace)
+        return
+    if not a.last_steps or not a.kernels_per_step:
+        sys.exit("--last-steps and --kernels-per-step are required for a kernel trace")
+    rows = []
+    with open(a.trace) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    n = a.last_steps * a.kernels_per_step
+    if len(rows) < n:
+        sys.exit(f"trace has {len(rows)} dispatches, fewer than {n}")
+    rows = rows[-n:]
+    span_ns = rows[-1][1] - rows[0][0]
+    busy = defaultdict(int)
+    cnt = defaultdict(int)
+    for s, e, k in rows:
+        busy[short(k)] += e - s
+        cnt[short(k)] += 1
+    total_busy = sum(busy.values())
+    byts = {}
+    for spec in a.bytes:
+        pat, b = spec.rsplit("=", 1)
+        byts[pat] = int(b)
+    step_us = span_ns / a.last_steps / 1e3
+    print(f"decode steps: {a.last_steps}; wall per step {step_us:.1f} us; "
+          f"kernel-busy per step {total_busy / a.last_steps / 1e3:.1f} us "
+          f"({100 * total_busy / span_ns:.1f}% of wall; the rest is launch gaps)\n")
+    print("| kernel | calls/step | avg us | us/step | % busy | GB/s |")
+    print("|---|---|---|---|---|---|")
+    for k in sorted(busy, key=lambda k: -busy[k]):
+        avg = busy[k] / cnt[k] / 1e3
+        gbs = ""
+        for pat, b in byts.items():
+            if re.search(pat, k):
+                gbs = f"{b / (avg * 1e-6) / 1e9:.0f}"
+        print(f"| {k} | {cnt[k] / a.last_steps:g} | {avg:.2f} | "
+              f"{busy[k] / a.last_steps / 1e3:.1f} | {100 * busy[k] / total_busy:.1f} | {gbs} |")
+
+
+if __name__ == "__main__":
+    main()
