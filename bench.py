@@ -132,9 +132,9 @@ COPY_BYTES = 256 << 20
 
 
 def moe_only(ne, torch, args):
-    """MoE launch pairs over all layers' experts, then three copies of a
-    256 MiB buffer (a plain copy kernel of known traffic: 256 MiB read and
-    256 MiB written per dispatch)."""
+    """MoE launch pairs over all layers' experts, then three passes of a plain
+    elementwise kernel over a 256 MiB buffer (known traffic: 256 MiB read and
+    256 MiB written per dispatch), the yardstick for the traffic counters."""
     cfg = ne.config_preset("gpt-oss-20b", max_seq=64, max_batch=1)
     eng = ne.Engine(cfg, device=0)
     stream = torch.cuda.current_stream()
@@ -144,8 +144,8 @@ def moe_only(ne, torch, args):
     eng.close()
     src = torch.ones(COPY_BYTES, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
+    for _ in range(3):  # one elementwise dispatch each: 256 MiB in, 256 MiB out
+        torch.bitwise_not(src, out=dst)
     torch.cuda.synchronize()
     log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, "
         f"{moe_bytes(cfg) / moe_s / 1e9:.0f} GB/s; copy kernel {COPY_BYTES} B x3 done")
@@ -168,7 +168,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--moe-reps", type=int, default=20)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--moe-only", action="store_true",
                     help="only the MoE launch-pair timing plus a plain 256 MiB device copy "

@@ -70,6 +70,8 @@ neon_status neon_config_preset(const char* name, neon_config* out);
  * activations.  Counterpart of the System constructor idiom
  * (NeonEngine/src/water_physics.cpp:23-123). */
 neon_status neon_ctx_create(const neon_config* cfg, int device, neon_ctx** out);
+/* Waits for the device to finish the context's queued work, then releases
+ * it.  NULL is ignored. */
 void neon_ctx_destroy(neon_ctx* ctx);
 
 /* Text of the last error on this context (or of the last failed

@@ -229,6 +229,10 @@ size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 extern "C" void neon_ctx_destroy(neon_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
+  // Work enqueued by neon_prefill/neon_decode may still run on the caller's
+  // stream: wait for it before the graph, its kernel arguments and the
+  // buffers it reads are released.
+  (void)hipDeviceSynchronize();
   if (ctx->graph_exec) (void)hipGraphExecDestroy(ctx->graph_exec);
   if (ctx->graph) (void)hipGraphDestroy(ctx->graph);
   if (ctx->cap_stream) (void)hipStreamDestroy(ctx->cap_stream);

@@ -12,6 +12,7 @@
 #include "neon_internal.hpp"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace neon {
 
@@ -835,27 +836,45 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   }
 }
 
+// Rows per wave: gate_up columns per wave (jpw) and down rows per block
+// (rpw).  NEON_MOE_JPW / NEON_MOE_RPW override them (tuning aid; read once).
+static int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  const int x = atoi(v);
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
 void launch_moe(const MoeArgs& a, hipStream_t st) {
-  const int P = (a.H / 32 + 63) / 64;
-  const int jpw = 4;
+  static const int jpw = env_int("NEON_MOE_JPW", 4, 1, 64);
+  static const int rpw = env_int("NEON_MOE_RPW", 8, 1, 64);  // red[][64] bound
+  const int Pg = (a.H / 32 + 63) / 64;  // gate_up reduces over H
+  const int Pd = (a.I / 32 + 63) / 64;  // down reduces over I
   const int gblk = (a.I + 4 * jpw - 1) / (4 * jpw);
-  const int rpw = 8;
   const int dblk = (a.H + rpw - 1) / rpw;
-  switch (P) {
-#define M_CASE(PP)                                                            \
+  switch (Pg) {
+#define G_CASE(PP)                                                            \
   case PP:                                                                    \
     hipLaunchKernelGGL(k_moe_gate_up<PP>, dim3(gblk, a.k, a.B), dim3(256), 0, \
                        st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,   \
                        a.idx, a.score, a.idx_out, a.score_out, a.E, a.xn,     \
                        a.act, a.H, a.I, a.k, jpw, a.alpha, a.limit);          \
+    break;
+    G_CASE(1) G_CASE(2) G_CASE(3)
+    default: G_CASE(4)
+#undef G_CASE
+  }
+  switch (Pd) {
+#define D_CASE(PP)                                                            \
+  case PP:                                                                    \
     hipLaunchKernelGGL(k_moe_down<PP>, dim3(dblk, a.B), dim3(64 * a.k), 0,   \
                        st, a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg,   \
                        a.idx, a.score, a.E, a.act, a.residual, a.out, a.H,    \
                        a.I, a.k, rpw);                                        \
     break;
-    M_CASE(1) M_CASE(2) M_CASE(3)
-    default: M_CASE(4)
-#undef M_CASE
+    D_CASE(1) D_CASE(2) D_CASE(3)
+    default: D_CASE(4)
+#undef D_CASE
   }
 }
 
