@@ -28,6 +28,9 @@ HIPCC_FLAGS = [
     # every fused multiply-add on the decode path is written out explicitly
     # (the CPU oracle mirrors the exact operation sequence)
     "-ffp-contract=off",
+    # LDS holds only what a kernel declares: no compiler-promoted private
+    # arrays in LDS
+    "-mllvm", "--disable-promote-alloca-to-lds",
     "-Wall",
     "-Wno-unused-function",
 ]

@@ -536,6 +536,18 @@ static float router_logit(const uint16_t* x, const uint16_t* w, int H,
   return p[0] + BF(bias);
 }
 
+/* The router's total order on experts: larger logit first, NaN after every
+ * number, ties (equal values, or both NaN) to the lower expert index.  Expert
+ * i's rank is the number of experts ordered before it; the top k are the
+ * ranks 0..k-1.  For finite logits this is "top k by value, ties to the
+ * lower index" (HFM:126-130 with torch.topk's tie rule made explicit). */
+static int ranks_before(float vj, int j, float vi, int i) {
+  const int nj = vj != vj, ni = vi != vi;
+  if (nj != ni) return ni;
+  if (!nj && vj != vi) return vj > vi;
+  return j < i;
+}
+
 void or_router(const uint16_t* x, const uint16_t* W, const uint16_t* b, int B,
                int E, int H, int k, int32_t* idx, float* score,
                float* logits) {
@@ -545,16 +557,13 @@ void or_router(const uint16_t* x, const uint16_t* W, const uint16_t* b, int B,
       lg[e] = router_logit(x + (size_t)r * H, W + (size_t)e * H, H, b[e]);
     if (logits) memcpy(logits + (size_t)r * E, lg, sizeof(float) * E);
     float v[64];
-    int used[1024] = {0};
-    for (int t = 0; t < k; ++t) {
-      int best = -1;
-      for (int e = 0; e < E; ++e) {
-        if (used[e]) continue;
-        if (best < 0 || lg[e] > lg[best]) best = e;
+    for (int i = 0; i < E; ++i) {
+      int rank = 0;
+      for (int j = 0; j < E; ++j) rank += ranks_before(lg[j], j, lg[i], i);
+      if (rank < k) {
+        idx[r * k + rank] = i;
+        v[rank] = lg[i];
       }
-      used[best] = 1;
-      idx[r * k + t] = best;
-      v[t] = lg[best];
     }
     float ex[64], s = 0.0f;
     for (int t = 0; t < k; ++t) {

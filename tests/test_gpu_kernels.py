@@ -162,6 +162,24 @@ def test_router_tie_break_lower_index(orc):
     assert list(to_host(idx)[0]) == [1, 2, 3, 5]
 
 
+@pytest.mark.parametrize("k", [4, 6, 8])
+def test_router_total_order_with_nan(orc, k):
+    """NaN and -inf logits: the GPU ranks experts exactly like the oracle."""
+    H, E = 64, 8
+    x = orc.f32_to_bf16(np.ones(H, np.float32))
+    W = orc.f32_to_bf16(np.zeros((E, H), np.float32))
+    b = orc.f32_to_bf16(np.array([2, np.nan, 5, 5, -np.inf, np.nan, 1, 5], np.float32))
+    idx, sc = empty_dev((1, k), np.int32), empty_dev((1, k), np.float32)
+    say(f"router total order with NaN, k={k}")
+    ne.router_topk(to_dev(x), to_dev(W), to_dev(b), idx, sc, None, 1, E, H, k)
+    ridx, rsc, _ = orc.router(x.reshape(1, H), W, b, E, H, k)
+    assert np.array_equal(to_host(idx), ridx)
+    got = to_host(sc)
+    assert np.array_equal(np.isnan(got), np.isnan(rsc))  # NaN payloads may differ
+    ok = ~np.isnan(rsc)
+    assert np.array_equal(got[ok].view(np.uint32), rsc[ok].view(np.uint32))
+
+
 def moe_inputs(orc, E, H, I, B, seed=0):
     """config 0: E2M1 uniform, E8M0 exponent uniform in [-8,-3], router std
     0.02, x ~ N(0, 1) bf16, seed 0."""

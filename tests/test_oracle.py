@@ -220,6 +220,31 @@ def test_router_ties_pick_lower_index(orc):
     np.testing.assert_allclose(sc[0], 0.25)
 
 
+def router_nan_case(orc):
+    """Logits [2, NaN, 5, 5, -inf, NaN, 1, 5] (H = 64, x = 1, biases carry the
+    values).  Total order: numbers by value, ties to the lower index, NaN
+    last (ties among NaNs to the lower index)."""
+    H, E = 64, 8
+    x = orc.f32_to_bf16(np.ones((1, H), np.float32))
+    W = orc.f32_to_bf16(np.zeros((E, H), np.float32))
+    b = orc.f32_to_bf16(np.array([2, np.nan, 5, 5, -np.inf, np.nan, 1, 5], np.float32))
+    return x, W, b, E, H
+
+
+@pytest.mark.parametrize("k,want", [(4, [2, 3, 7, 0]), (6, [2, 3, 7, 0, 6, 4]),
+                                    (8, [2, 3, 7, 0, 6, 4, 1, 5])])
+def test_router_total_order_with_nan(orc, k, want):
+    x, W, b, E, H = router_nan_case(orc)
+    idx, sc, _ = orc.router(x, W, b, E, H, k)
+    assert list(idx[0]) == want
+    if k <= 6:  # no NaN chosen: a proper softmax over the chosen values
+        v = np.array([5, 5, 5, 2, 1, -np.inf][:k], np.float64)
+        p = np.exp(v - v[0]) / np.exp(v - v[0]).sum()
+        np.testing.assert_allclose(sc[0], p, rtol=1e-6)
+    else:
+        assert np.isnan(sc[0]).all()
+
+
 def test_router_matches_hf(orc, golden):
     x, W, b = (orc.f32_to_bf16(golden[k]) for k in ("router_x", "router_w", "router_b"))
     idx, sc, lg = orc.router(x, W, b, 8, 64, 4)
