@@ -580,14 +580,18 @@ void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
 // (optionally RMS-normalised) input in registers and the expert's logit =
 // canonical bf16 row dot + bias (fp32 add).  Wave (0, b) stores the
 // normalised row to xn_out for the experts.
-// wave_route: one wave ranks a row's E logits in the router's total order --
+// wave_topk: one wave chooses a row's experts.  The router's total order is
 // larger logit first, NaN after every number, ties (equal values, or both
-// NaN) to the lower expert index -- keeps the first k, and forms the softmax
-// over them: e_t = exp(v_t - v_0) (neon_expf), s = sum in rank order,
-// score_t = e_t / s.  Each expert's rank is the number of experts ordered
-// before it, counted against the logits staged in LDS, so the whole choice
-// costs two LDS round trips and no cross-lane reduction chain.  Every MoE
-// block runs it on the logits itself, so no block waits on another.
+// NaN) to the lower expert index.  Each logit maps to a 64-bit key that is
+// larger exactly when the expert comes earlier (an order-preserving integer
+// image of the float in the high half, NaN as 0, -0 as +0; the complement of
+// the index in the low half); an expert's rank is the number of larger keys,
+// counted with v_readlane over the keys held one per lane (E steps of a few
+// instructions).  Rows without NaN take a shorter path with the same result:
+// plain float compares (-0 == +0) with ties to the lower index.  The experts of rank t < k are the chosen ones, in rank
+// order; their weights are e_t = exp(v_t - v_0) (neon_expf), s = sum in rank
+// order, e_t / s.  Every MoE wave runs it on the logits itself, so no block
+// waits on another.
 // ===========================================================================
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
@@ -596,6 +600,99 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+__device__ __forceinline__ uint64_t route_key(float v, int i) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  u = (u == 0x80000000u) ? 0u : u;                         // -0 ranks as +0
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);          // order-preserving
+  u = (v != v) ? 0u : u;                                   // NaN after numbers
+  return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+// Chosen experts of one row, in the wave's LDS slice.
+struct TopK {
+  int32_t id[kMaxTopK];
+  float sc[kMaxTopK];  // weights (when asked for), else the chosen logits
+};
+
+// One wave; lg = the row's E logits (global).  On return t.id[0..k) (and,
+// with WEIGHTS, t.sc[0..k)) are visible to the wave.
+template <bool WEIGHTS>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
+                                          int k, int lane, TopK& t) {
+  constexpr int NQ = kMaxExperts / 64;
+  float v[NQ];
+  uint32_t khi[NQ], klo[NQ];
+  int rank[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int e = lane + 64 * q;
+    v[q] = (64 * q < E && e < E) ? lg[e] : 0.0f;
+    const uint64_t key = route_key(v[q], e);
+    khi[q] = (uint32_t)(key >> 32);
+    klo[q] = (uint32_t)key;
+    rank[q] = 0;
+  }
+  bool nan = false;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) nan |= v[q] != v[q];
+  if (E <= 64 && __ballot(nan) == 0) {
+    // one expert per lane, no NaN in the row: plain float compares
+    // (-0 == +0), ties to the lower index, branch-free
+    const float vi = v[0];
+    int r = 0;
+#pragma unroll 4
+    for (int j = 0; j < E; ++j) {
+      const float vj = readlane_f(vi, j);
+      r += (int)((vj > vi) | ((vj == vi) & (j < lane)));
+    }
+    rank[0] = r;
+  } else if (__ballot(nan) == 0) {
+#pragma unroll
+    for (int jq = 0; jq < NQ; ++jq) {
+      if (64 * jq >= E) continue;  // uniform
+      const int jn = min(64, E - 64 * jq);
+      for (int jl = 0; jl < jn; ++jl) {
+        const float vj = readlane_f(v[jq], jl);
+        const int j = 64 * jq + jl;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          if (64 * q < E) rank[q] += (vj > v[q] || (vj == v[q] && j < lane + 64 * q)) ? 1 : 0;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int jq = 0; jq < NQ; ++jq) {
+      if (64 * jq >= E) continue;  // uniform
+      const int jn = min(64, E - 64 * jq);
+      for (int jl = 0; jl < jn; ++jl) {
+        const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)khi[jq], jl) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((int)klo[jq], jl);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          if (64 * q < E) rank[q] += kj > (((uint64_t)khi[q] << 32) | klo[q]) ? 1 : 0;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int e = lane + 64 * q;
+    if (64 * q < E && e < E && rank[q] < k) { t.id[rank[q]] = e; t.sc[rank[q]] = v[q]; }
+  }
+  wave_lds_sync();
+  if (WEIGHTS) {
+    const float et = lane < k ? neon_expf(__fsub_rn(t.sc[lane], t.sc[0])) : 0.0f;
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) sum = __fadd_rn(sum, readlane_f(et, i));
+    wave_lds_sync();  // every lane has read t.sc before it is overwritten
+    if (lane < k) t.sc[lane] = __fdiv_rn(et, sum);
+    wave_lds_sync();
+  }
 }
 
 template <int P>
@@ -615,76 +712,14 @@ __global__ __launch_bounds__(64) void k_router_logits(
   if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias[e]));
 }
 
-struct RouteLds {
-  float lg[kMaxExperts];
-  int32_t id[kMaxTopK];
-  float sc[kMaxTopK];
-};
-
-// true when expert j (logit vj) is ordered before expert i (logit vi)
-__device__ __forceinline__ bool ranks_before(float vj, int j, float vi, int i) {
-  const bool nj = vj != vj, ni = vi != vi;
-  if (nj != ni) return ni;
-  if (!nj && vj != vi) return vj > vi;
-  return j < i;
-}
-
-// One wave.  lg != NULL: route from the row's logits; else copy the given
-// ids/weights.  On return r.id[0..k) and r.sc[0..k) are visible to the wave
-// (other waves need a block barrier).  Requires k <= E, k <= kMaxTopK and
-// E <= kMaxExperts (checked on the host).
-__device__ __forceinline__ void wave_route(const float* __restrict__ lg,
-                                        const int32_t* __restrict__ idx_in,
-                                        const float* __restrict__ score_in,
-                                        int E, int k, int lane, RouteLds& r) {
-  if (lg == nullptr) {
-    if (lane < k) { r.id[lane] = idx_in[lane]; r.sc[lane] = score_in[lane]; }
-    wave_lds_sync();
-    return;
-  }
-  for (int e = lane; e < E; e += 64) r.lg[e] = lg[e];
-  wave_lds_sync();
-  for (int i = lane; i < E; i += 64) {
-    const float vi = r.lg[i];
-    int rank = 0;
-#pragma unroll 4
-    for (int j = 0; j < E; ++j) rank += ranks_before(r.lg[j], j, vi, i) ? 1 : 0;
-    if (rank < k) { r.id[rank] = i; r.sc[rank] = vi; }
-  }
-  wave_lds_sync();
-  if (lane == 0) {
-    const float v0 = r.sc[0];
-    float s = 0.0f;
-    for (int t = 0; t < k; ++t) {
-      const float e = neon_expf(__fsub_rn(r.sc[t], v0));
-      r.sc[t] = e;
-      s = __fadd_rn(s, e);
-    }
-    for (int t = 0; t < k; ++t) r.sc[t] = __fdiv_rn(r.sc[t], s);
-  }
-  wave_lds_sync();
-}
-
-// Row b of the router logits, or of the given ids/weights.
-__device__ __forceinline__ void wave_route_row(const float* __restrict__ lg,
-                                               const int32_t* __restrict__ idx_in,
-                                               const float* __restrict__ score_in,
-                                               int b, int E, int k, int lane,
-                                               RouteLds& r) {
-  if (lg != nullptr)
-    wave_route(lg + (size_t)b * E, nullptr, nullptr, E, k, lane, r);
-  else
-    wave_route(nullptr, idx_in + (size_t)b * k, score_in + (size_t)b * k, E, k, lane, r);
-}
-
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
                                              int32_t* __restrict__ idx,
                                              float* __restrict__ score, int E,
                                              int k) {
-  __shared__ RouteLds rl;
+  __shared__ TopK t;
   const int b = blockIdx.x, lane = threadIdx.x;
-  wave_route(lg + (size_t)b * E, nullptr, nullptr, E, k, lane, rl);
-  if (lane < k) { idx[b * k + lane] = rl.id[lane]; score[b * k + lane] = rl.sc[lane]; }
+  wave_topk<true>(lg + (size_t)b * E, E, k, lane, t);
+  if (lane < k) { idx[b * k + lane] = t.id[lane]; score[b * k + lane] = t.sc[lane]; }
 }
 
 void launch_router(const RouterArgs& a, hipStream_t st) {
@@ -707,6 +742,17 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
                        a.score, a.E, a.k);
 }
 
+// Expert id of `slot` for row b: chosen from the router logits when lg is
+// given (also its weight into t.sc when WEIGHTS), else read from idx.
+template <bool WEIGHTS>
+__device__ __forceinline__ int moe_expert(const float* __restrict__ lg,
+                                          const int32_t* __restrict__ idx, int b,
+                                          int E, int k, int slot, int lane, TopK& t) {
+  if (lg == nullptr) return idx[b * k + slot];
+  wave_topk<WEIGHTS>(lg + (size_t)b * E, E, k, lane, t);
+  return t.id[slot];
+}
+
 // ===========================================================================
 // MoE expert FFN (HFM:82-112).
 // gate_up + SwiGLU: grid (ceil(I / (4 jpw)), k, B), block 256.  Wave w of
@@ -726,26 +772,33 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
   return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
 }
 
+// gate_up's expert for (b, slot); wave 0 of block (0, slot 0) also writes
+// the row's chosen ids and weights to idx_out/score_out when given.
+__device__ __forceinline__ int moe_gate_up_expert(
+    const float* __restrict__ lg, const int32_t* __restrict__ idx,
+    int32_t* __restrict__ idx_out, float* __restrict__ score_out, int b, int E,
+    int k, int slot, int lane, int wave, TopK& t) {
+  if (lg != nullptr && idx_out != nullptr && blockIdx.x == 0 && slot == 0 && wave == 0) {
+    const int e = moe_expert<true>(lg, idx, b, E, k, slot, lane, t);
+    if (lane < k) { idx_out[b * k + lane] = t.id[lane]; score_out[b * k + lane] = t.sc[lane]; }
+    return e;
+  }
+  return moe_expert<false>(lg, idx, b, E, k, slot, lane, t);
+}
+
 template <int P>
 __global__ __launch_bounds__(256) void k_moe_gate_up(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
     const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
-    int32_t* __restrict__ idx_out, float* __restrict__ score_out, int E,
-    const uint16_t* __restrict__ xn, uint16_t* __restrict__ act, int H, int I,
-    int k, int jpw, float alpha, float limit) {
-  __shared__ RouteLds rl;
+    const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
+    float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
+    uint16_t* __restrict__ act, int H, int I, int k, int jpw, float alpha,
+    float limit) {
+  __shared__ TopK tk[4];
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (wave == 0) {
-    wave_route_row(router_lg, idx_in, score_in, b, E, k, lane, rl);
-    if (blockIdx.x == 0 && slot == 0 && idx_out != nullptr && lane < k) {
-      idx_out[b * k + lane] = rl.id[lane];
-      score_out[b * k + lane] = rl.sc[lane];
-    }
-  }
-  __syncthreads();
-  const int e = rl.id[slot];
+  const int e = moe_gate_up_expert(router_lg, idx, idx_out, score_out, b, E, k,
+                                   slot, lane, wave, tk[wave]);
   const size_t rows = (size_t)2 * I;
   const uint8_t* codes = gu_codes + (size_t)e * rows * (H / 2);
   const uint8_t* scales = gu_scales + (size_t)e * rows * U;
@@ -790,17 +843,15 @@ template <int P>
 __global__ __launch_bounds__(1024) void k_moe_down(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
     const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
-    int E, const uint16_t* __restrict__ act, const uint16_t* residual,
-    uint16_t* out, int H, int I, int k, int rpw) {
+    const int32_t* __restrict__ idx, const float* __restrict__ score, int E,
+    const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
+    int H, int I, int k, int rpw) {
   __shared__ float red[kMaxTopK][64];
-  __shared__ RouteLds rl;
+  __shared__ TopK tk[kMaxTopK];
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
-  if (slot == 0)
-    wave_route_row(router_lg, idx_in, score_in, b, E, k, lane, rl);
-  __syncthreads();
-  const int e = rl.id[slot];
+  const int e = slot == 0 ? moe_expert<true>(router_lg, idx, b, E, k, slot, lane, tk[0])
+                          : moe_expert<false>(router_lg, idx, b, E, k, slot, lane, tk[slot]);
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
@@ -826,7 +877,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) y = __builtin_fmaf(rl.sc[s], red[s][t], y);
+      if (s < k) y = __builtin_fmaf(router_lg ? tk[0].sc[s] : score[b * k + s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
@@ -860,34 +911,49 @@ struct Fp4Tile {
   uint32_t s[NI];
 };
 
+// Loads without branches (nu >= 1): a lane past the tile re-reads its last
+// unit and discards it, so every load is issued unconditionally and the
+// compiler can wait for each one in turn instead of for all of them.
 template <int NI>
 __device__ __forceinline__ void fp4_tile_load(Fp4Tile<NI>& t,
                                               const uint8_t* __restrict__ codes,
                                               const uint8_t* __restrict__ scales,
                                               int nu, int lane) {
+  // scale bytes first: unit i then waits only for code load i
 #pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int f = lane + 64 * i;
-    if (f < nu) {
-      t.c[i] = *reinterpret_cast<const uint4*>(codes + (size_t)f * 16);
-      t.s[i] = scales[f];
-    } else {
-      t.c[i] = make_uint4(0, 0, 0, 0);
-      t.s[i] = 127;
-    }
-  }
+  for (int i = 0; i < NI; ++i) t.s[i] = scales[min(lane + 64 * i, nu - 1)];
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    t.c[i] = *reinterpret_cast<const uint4*>(codes + (size_t)min(lane + 64 * i, nu - 1) * 16);
 }
 
-// bf16 x[K] -> xs (chunk-major fp32), threads [t0, t0 + nt) of the caller.
-__device__ __forceinline__ void x_to_lds(const uint16_t* __restrict__ x,
-                                         float4* xs, int U, int t, int nt) {
+// bf16 x[K] -> xs (chunk-major fp32) in two halves, so the x loads can be
+// issued before a tile's loads and waited for on their own (the vector-memory
+// counter drains in issue order).  Thread t of nt handles 16-byte words
+// w = t + nt j (w covers elements 8 w .. 8 w + 7), j < NX.
+template <int NX>
+__device__ __forceinline__ void x_load_raw(const uint16_t* __restrict__ x,
+                                           uint4 (&raw)[NX], int U, int t, int nt) {
   const uint4* xv = reinterpret_cast<const uint4*>(x);
-  for (int w = t; w < U * 4; w += nt) {  // w covers elements 8 w .. 8 w + 7
-    float f[8];
-    unpack8(xv[w], f);
-    const int u = w >> 2, q = (w & 3) * 2;
-    xs[q * U + u] = make_float4(f[0], f[1], f[2], f[3]);
-    xs[(q + 1) * U + u] = make_float4(f[4], f[5], f[6], f[7]);
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int w = t + nt * j;
+    raw[j] = w < U * 4 ? xv[w] : make_uint4(0, 0, 0, 0);
+  }
+}
+template <int NX>
+__device__ __forceinline__ void x_store_lds(const uint4 (&raw)[NX], float4* xs,
+                                            int U, int t, int nt) {
+#pragma unroll
+  for (int j = 0; j < NX; ++j) {
+    const int w = t + nt * j;
+    if (w < U * 4) {
+      float f[8];
+      unpack8(raw[j], f);
+      const int u = w >> 2, q = (w & 3) * 2;
+      xs[q * U + u] = make_float4(f[0], f[1], f[2], f[3]);
+      xs[(q + 1) * U + u] = make_float4(f[4], f[5], f[6], f[7]);
+    }
   }
 }
 
@@ -971,98 +1037,93 @@ __device__ __forceinline__ float tile_reduce8(const float* ex, int nrows, int U,
 
 // gate_up + SwiGLU, tiled: grid (ceil(I / 16), k, B), block 256.  The block
 // serves one (token, slot); wave w owns columns j0 = 16 i + 4 w .. + 3, i.e.
-// the 8 rows 2 j0 .. 2 j0 + 7 (gate/up interleaved).  Wave 0 routes and
-// every wave reads the chosen expert from LDS; x is converted into LDS once
-// per block.  Dynamic LDS: xs (U * 128 B) + 4 waves * 8 U floats.
-template <int P>
+// the 8 rows 2 j0 .. 2 j0 + 7 (gate/up interleaved).  Every wave routes on
+// its own (the logits are E floats) so it can issue its tile loads at once;
+// x is converted into LDS while those loads are in flight.  Dynamic LDS: xs
+// (U * 128 B) + 4 waves * 8 U floats.
+template <int NI>  // NI = ceil(8 U / 64): loads per lane for an 8-row tile
 __global__ __launch_bounds__(256) void k_moe_gate_up_t(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
     const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
-    int32_t* __restrict__ idx_out, float* __restrict__ score_out, int E,
-    const uint16_t* __restrict__ xn, uint16_t* __restrict__ act, int H, int I,
-    int k, float alpha, float limit) {
-  constexpr int NI = kTileRows * P;  // ceil(8 rows * 64 P units / 64 lanes)
+    const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
+    float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
+    uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit) {
   extern __shared__ __align__(16) char smem[];
-  __shared__ RouteLds rl;
+  __shared__ TopK tk[4];
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float4* xs = reinterpret_cast<float4*>(smem);
   float* ex = reinterpret_cast<float*>(smem + (size_t)U * 128) + wave * kTileRows * U;
-  if (wave == 0) {
-    wave_route_row(router_lg, idx_in, score_in, b, E, k, lane, rl);
-    if (blockIdx.x == 0 && slot == 0 && idx_out != nullptr && lane < k) {
-      idx_out[b * k + lane] = rl.id[lane];
-      score_out[b * k + lane] = rl.sc[lane];
-    }
-  }
-  x_to_lds(xn + (size_t)b * H, xs, U, threadIdx.x, blockDim.x);
-  __syncthreads();
-  const int e = rl.id[slot];
-  const int j0 = blockIdx.x * 16 + wave * 4;
-  if (j0 >= I) return;
-  const int ncol = min(4, I - j0), nrows = 2 * ncol, nu = nrows * U;
-  const size_t rows = (size_t)2 * I, r0 = (size_t)e * rows + 2 * j0;
+  const int e = moe_gate_up_expert(router_lg, idx, idx_out, score_out, b, E, k,
+                                   slot, lane, wave, tk[wave]);
+  const int j0 = blockIdx.x * 16 + wave * 4;  // I % 16 == 0: a full 8-row tile
+  const int nu = kTileRows * U;
+  const size_t rows = (size_t)2 * I, r0 = (size_t)e * rows + 2 * (size_t)j0;
+  // x and bias loads first, then the tile's loads: staging x waits only for x
+  uint4 xraw[(NI + 7) / 8];  // ceil(4 U / 256) words per thread (U <= 8 NI)
+  x_load_raw(xn + (size_t)b * H, xraw, U, threadIdx.x, 256);
+  const int my_row = lane >> 3;
+  const uint16_t bias_b = gu_bias[r0 + my_row];
   Fp4Tile<NI> w;
   fp4_tile_load<NI>(w, gu_codes + r0 * (H / 2), gu_scales + r0 * U, nu, lane);
-  const int my_row = lane >> 3;
-  const float bias = my_row < nrows ? bf2f(gu_bias[r0 + my_row]) : 0.0f;
+  x_store_lds(xraw, xs, U, threadIdx.x, 256);
+  __syncthreads();
   fp4_tile_units<NI>(w, xs, ex, U, nu, lane);
   wave_lds_sync();
-  const float tot = __fadd_rn(tile_reduce8<P>(ex, nrows, U, lane), bias);
+  const float tot = __fadd_rn(tile_reduce8<4>(ex, kTileRows, U, lane), bf2f(bias_b));
   const float up = __shfl_xor(tot, 8, 64);  // gate row 2c in lane 16c, up row in 16c + 8
-  const int c = lane >> 4;
-  if ((lane & 15) == 0 && c < ncol)
-    act[((size_t)b * k + slot) * I + j0 + c] = f2bf(swiglu_clamp(tot, up, alpha, limit));
+  if ((lane & 15) == 0)
+    act[((size_t)b * k + slot) * I + j0 + (lane >> 4)] = f2bf(swiglu_clamp(tot, up, alpha, limit));
 }
 
 // down + weighted sum (+ residual), tiled: grid (ceil(H / 8), B), block 256,
-// k <= 4.  Wave w handles top-k slot w: its slot's act row goes to the
-// wave's own LDS slice, and it computes the block's 8 output rows of that
-// slot's expert.  The block then combines y = fmaf(score_s, dot_s + bias_s, y)
-// in slot order from 0 (HFM:111-112), rounds to bf16, and adds the residual
-// when given.  Dynamic LDS: 4 waves * (U * 128 B + 8 U floats).
-template <int P>
+// k <= 4.  Wave w handles top-k slot w: it routes on its own, issues the
+// loads of its slot's 8-row tile, stages its slot's act row in its own LDS
+// slice, and reduces the 8 rows.  The block then combines
+// y = fmaf(score_s, dot_s + bias_s, y) in slot order from 0 (HFM:111-112),
+// rounds to bf16, and adds the residual when given.  Dynamic LDS: 4 waves *
+// (U * 128 B + 8 U floats).
+template <int NI>  // NI = ceil(8 U / 64): loads per lane for an 8-row tile
 __global__ __launch_bounds__(256) void k_moe_down_t(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
     const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx_in, const float* __restrict__ score_in,
-    int E, const uint16_t* __restrict__ act, const uint16_t* residual,
-    uint16_t* out, int H, int I, int k) {
-  constexpr int NI = kTileRows * P;
+    const int32_t* __restrict__ idx, const float* __restrict__ score, int E,
+    const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
+    int H, int I, int k) {
   extern __shared__ __align__(16) char smem[];
   __shared__ float red[4][kTileRows];
-  __shared__ RouteLds rl;
+  __shared__ TopK tk[4];
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float4* xs = reinterpret_cast<float4*>(smem + (size_t)wave * (U * 128 + kTileRows * U * 4));
   float* ex = reinterpret_cast<float*>(reinterpret_cast<char*>(xs) + (size_t)U * 128);
-  if (wave == 0)
-    wave_route_row(router_lg, idx_in, score_in, b, E, k, lane, rl);
-  __syncthreads();
-  const int n0 = blockIdx.x * kTileRows, nrows = min(kTileRows, H - n0), nu = nrows * U;
+  const int n0 = blockIdx.x * kTileRows;  // H % 8 == 0: a full 8-row tile
+  const int nu = kTileRows * U;
   const int my_row = lane >> 3;
   const int slot = wave;  // k <= 4 on this path
   if (slot < k) {
-    const int e = rl.id[slot];
+    const int e = slot == 0 ? moe_expert<true>(router_lg, idx, b, E, k, slot, lane, tk[0])
+                            : moe_expert<false>(router_lg, idx, b, E, k, slot, lane, tk[slot]);
     const size_t r0 = (size_t)e * H + n0;
+    uint4 xraw[(NI + 1) / 2];  // ceil(4 U / 64) words per lane (U <= 8 NI); x and bias first
+    x_load_raw(act + ((size_t)b * k + slot) * I, xraw, U, lane, 64);
+    const uint16_t bias_b = dn_bias[r0 + my_row];
     Fp4Tile<NI> w;
     fp4_tile_load<NI>(w, dn_codes + r0 * (I / 2), dn_scales + r0 * U, nu, lane);
-    const float bias = my_row < nrows ? bf2f(dn_bias[r0 + my_row]) : 0.0f;
-    x_to_lds(act + ((size_t)b * k + slot) * I, xs, U, lane, 64);
+    x_store_lds(xraw, xs, U, lane, 64);
     wave_lds_sync();
     fp4_tile_units<NI>(w, xs, ex, U, nu, lane);
     wave_lds_sync();
-    const float tot = __fadd_rn(tile_reduce8<P>(ex, nrows, U, lane), bias);
+    const float tot = __fadd_rn(tile_reduce8<4>(ex, kTileRows, U, lane), bf2f(bias_b));
     if ((lane & 7) == 0) red[slot][my_row] = tot;
   }
   __syncthreads();
-  if (threadIdx.x < nrows) {
+  if (threadIdx.x < kTileRows) {
     const int t = threadIdx.x, n = n0 + t;
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      if (s < k) y = __builtin_fmaf(rl.sc[s], red[s][t], y);
+      if (s < k) y = __builtin_fmaf(router_lg ? tk[0].sc[s] : score[b * k + s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
@@ -1080,12 +1141,12 @@ static int env_int(const char* name, int dflt, int lo, int hi) {
 
 // The row-per-wave kernels are the default (measured faster at the 20b shape:
 // 23.1 vs 25.6 us per pair).  NEON_MOE_KERNEL=tile selects the tiled
-// kernels where they apply: 256 U (gate_up) and 640 U (down) bytes of
-// dynamic LDS and top-k <= 4.
+// kernels where they apply: full tiles (I % 16 == 0, H % 8 == 0), 256 U
+// (gate_up) and 640 U (down) bytes of dynamic LDS, and top-k <= 4.
 static bool moe_use_tiled(const MoeArgs& a) {
   static const bool tile = getenv("NEON_MOE_KERNEL") && !strcmp(getenv("NEON_MOE_KERNEL"), "tile");
-  return tile && a.k <= 4 && 256 * (a.H / 32) <= 60 * 1024 &&
-         640 * (a.I / 32) <= 60 * 1024;
+  return tile && a.k <= 4 && a.I % 16 == 0 && a.H % kTileRows == 0 &&
+         256 * (a.H / 32) <= 60 * 1024 && 640 * (a.I / 32) <= 60 * 1024;
 }
 
 void launch_moe(const MoeArgs& a, hipStream_t st) {
@@ -1093,30 +1154,24 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
   const int Pd = (a.I / 32 + 63) / 64;  // down reduces over I
   if (moe_use_tiled(a)) {
     const size_t lg = (size_t)256 * (a.H / 32), ld = (size_t)640 * (a.I / 32);
-    const int gblk = (a.I + 15) / 16, dblk = (a.H + kTileRows - 1) / kTileRows;
-    switch (Pg) {
-#define TG_CASE(PP)                                                               \
-  case PP:                                                                        \
-    hipLaunchKernelGGL(k_moe_gate_up_t<PP>, dim3(gblk, a.k, a.B), dim3(256), lg, \
-                       st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,      \
-                       a.idx, a.score, a.idx_out, a.score_out, a.E, a.xn,        \
-                       a.act, a.H, a.I, a.k, a.alpha, a.limit);                  \
-    break;
-      TG_CASE(1)
-      default: TG_CASE(2)
-#undef TG_CASE
-    }
-    switch (Pd) {
-#define TD_CASE(PP)                                                               \
-  case PP:                                                                        \
-    hipLaunchKernelGGL(k_moe_down_t<PP>, dim3(dblk, a.B), dim3(256), ld, st,     \
-                       a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg, a.idx,   \
-                       a.score, a.E, a.act, a.residual, a.out, a.H, a.I, a.k);   \
-    break;
-      TD_CASE(1)
-      default: TD_CASE(2)
-#undef TD_CASE
-    }
+    const int gblk = a.I / 16, dblk = a.H / kTileRows;
+    const int nig = (kTileRows * (a.H / 32) + 63) / 64, nid = (kTileRows * (a.I / 32) + 63) / 64;
+    // gate_up first, then down (down reads the activations gate_up writes)
+#define TG(NIV)                                                                 \
+  hipLaunchKernelGGL(k_moe_gate_up_t<NIV>, dim3(gblk, a.k, a.B), dim3(256), lg, \
+                     st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,      \
+                     a.idx, a.idx_out, a.score_out, a.E, a.xn, a.act, a.H,     \
+                     a.I, a.k, a.alpha, a.limit)
+#define TD(NIV)                                                                 \
+  hipLaunchKernelGGL(k_moe_down_t<NIV>, dim3(dblk, a.B), dim3(256), ld, st,    \
+                     a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg, a.idx,   \
+                     a.score, a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
+    if (nig <= 2) TG(2); else if (nig <= 4) TG(4); else if (nig <= 8) TG(8);
+    else if (nig <= 12) TG(12); else if (nig <= 16) TG(16); else TG(24);
+    if (nid <= 2) TD(2); else if (nid <= 4) TD(4); else if (nid <= 8) TD(8);
+    else if (nid <= 12) TD(12); else if (nid <= 16) TD(16); else TD(24);
+#undef TG
+#undef TD
     return;
   }
   static const int jpw = env_int("NEON_MOE_JPW", 4, 1, 64);
@@ -1128,8 +1183,8 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
   case PP:                                                                    \
     hipLaunchKernelGGL(k_moe_gate_up<PP>, dim3(gblk, a.k, a.B), dim3(256), 0, \
                        st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,   \
-                       a.idx, a.score, a.idx_out, a.score_out, a.E, a.xn,     \
-                       a.act, a.H, a.I, a.k, jpw, a.alpha, a.limit);          \
+                       a.idx, a.idx_out, a.score_out, a.E, a.xn, a.act, a.H,  \
+                       a.I, a.k, jpw, a.alpha, a.limit);                      \
     break;
     G_CASE(1) G_CASE(2) G_CASE(3)
     default: G_CASE(4)
