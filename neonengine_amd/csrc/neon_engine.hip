@@ -69,6 +69,7 @@ struct neon_ctx {
   int32_t* moe_idx = nullptr;
   float* moe_score = nullptr;
   float* router_lg = nullptr;
+  float *attn_po = nullptr, *attn_pml = nullptr;  // split partials
   float* logits = nullptr;
   float* lm_part_val = nullptr;
   int32_t* lm_part_idx = nullptr;
@@ -314,7 +315,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   const size_t Bm = c.max_batch, half = c.head_dim / 2;
   ctx->s_slide = attn_splits(c.max_seq, c.sliding_window);
   ctx->s_full = attn_splits(c.max_seq, 0);
-  ctx->lm_nblk = gemv_default_grid(c.vocab, 4);
+  ctx->lm_nblk = gemv_default_grid(c.vocab);
   ctx->tok_stride = c.max_seq + 1;
   off = 0;
   const size_t o_h = take(Bm * H * 2), o_xn = take(Bm * H * 2),
@@ -323,6 +324,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_act = take(Bm * c.top_k * I * 2),
                o_idx = take(Bm * c.top_k * 4), o_sc = take(Bm * c.top_k * 4),
                o_rlg = take(Bm * c.n_experts * 4),
+               o_apo = take(Bm * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * c.head_dim * 4),
+               o_apml = take(Bm * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -340,6 +343,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->act = (uint16_t*)(W + o_act); ctx->moe_idx = (int32_t*)(W + o_idx);
   ctx->moe_score = (float*)(W + o_sc);
   ctx->router_lg = (float*)(W + o_rlg);
+  ctx->attn_po = (float*)(W + o_apo); ctx->attn_pml = (float*)(W + o_apml);
   ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
@@ -530,21 +534,22 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
     GemvArgs q;
     q.mode = 0; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
-    q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B; q.rpw = 4;
-    q.nblk = gemv_default_grid(q.N, q.rpw);
+    q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B;
+    q.nblk = gemv_default_grid(q.N);
     launch_gemv_bf16(q, st);
     AttnArgs a;
     a.q_src = ctx->qkv; a.kc = ctx->kc + (size_t)l * ctx->kv_layer_elems;
     a.vc = ctx->vc + (size_t)l * ctx->kv_layer_elems; a.sinks = w.sinks;
     a.pos = ctx->pos; a.cos_t = ctx->cos_t; a.sin_t = ctx->sin_t;
-    a.out = ctx->attn_out; a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
+    a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml;
+    a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.fused = 1; a.q_stride = qkv_rows;
     launch_attn(a, st);
     GemvArgs o;
     o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
-    o.N = H; o.K = c.n_heads * D; o.B = B; o.rpw = 2;
-    o.nblk = gemv_default_grid(o.N, o.rpw);
+    o.N = H; o.K = c.n_heads * D; o.B = B;
+    o.nblk = gemv_default_grid(o.N);
     launch_gemv_bf16(o, st);
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
@@ -564,7 +569,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
   GemvArgs lm;
   lm.mode = 2; lm.W = ctx->lm_head; lm.x = ctx->h; lm.norm_w = ctx->final_norm;
   lm.eps = c.rms_eps; lm.logits = ctx->logits; lm.part_val = ctx->lm_part_val;
-  lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab; lm.K = H; lm.B = B; lm.rpw = 4;
+  lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab; lm.K = H; lm.B = B;
   lm.nblk = ctx->lm_nblk;
   launch_gemv_bf16(lm, st);
   launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, ctx->lm_nblk,
@@ -758,7 +763,7 @@ extern "C" neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,
     KFAIL(NEON_EINVAL, "neon_gemv_bf16: bad shape N=%d K=%d B=%d", N, K, B);
   GemvArgs a;
   a.mode = 0; a.W = W; a.bias = bias; a.x = x; a.y = y; a.N = N; a.K = K; a.B = B;
-  a.rpw = 2; a.nblk = gemv_default_grid(N, a.rpw);
+  a.nblk = gemv_default_grid(N);
   launch_gemv_bf16(a, S(stream));
   KLAUNCHED();
 }
@@ -898,11 +903,20 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
     KFAIL(NEON_EINVAL, "neon_attn_decode: Hq/Hkv must be 1, 2, 4 or 8");
   // pos[b] must lie in [0, T_max); it is device data, so the kernel trusts it.
   hipStream_t st = S(stream);
+  const int nsplit = attn_splits(T_max, window);
+  const size_t np = (size_t)B * Hq * nsplit;
+  float* scratch = nullptr;  // split partials: o [np][D], then (m, l) [np][2]
+  if (hipMallocAsync((void**)&scratch, np * (D + 2) * 4, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
   AttnArgs a;
   a.q_src = q; a.kc = const_cast<uint16_t*>(k_cache); a.vc = const_cast<uint16_t*>(v_cache);
   a.sinks = sinks; a.pos = pos; a.cos_t = nullptr; a.sin_t = nullptr; a.out = out;
+  a.part_o = scratch; a.part_ml = scratch + np * D;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window;
-  a.S = attn_splits(T_max, window); a.fused = 0; a.q_stride = Hq * D;
+  a.S = nsplit; a.fused = 0; a.q_stride = Hq * D;
   launch_attn(a, st);
-  KLAUNCHED();
+  hipError_t e = hipGetLastError();
+  (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
 }

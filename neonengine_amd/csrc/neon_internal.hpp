@@ -35,10 +35,9 @@ struct GemvArgs {
   float* part_val = nullptr;
   int32_t* part_idx = nullptr;
   int N = 0, K = 0, B = 1;
-  int rpw = 1;   // rows per wave group
-  int nblk = 1;  // grid.x
+  int nblk = 1;  // grid.x (rows go in groups of 4 per wave, grid-strided)
 };
-int gemv_default_grid(int N, int rpw);
+int gemv_default_grid(int N);
 void launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
 
 void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
@@ -97,6 +96,8 @@ struct AttnArgs {
   const int32_t* pos;     // [B]
   const float *cos_t, *sin_t;
   uint16_t* out;          // [B][Hq*D]
+  float* part_o;          // [B][Hq][S][D] split partials (scratch)
+  float* part_ml;         // [B][Hq][S][2]
   int B, Hq, Hkv, T_max, window, S, fused, q_stride;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);

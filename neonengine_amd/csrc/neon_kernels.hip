@@ -182,6 +182,72 @@ __device__ __forceinline__ void wave_load_x_fp4(float (&xr)[P][32],
     for (int q = 0; q < 4; ++q) unpack8(raw[p][q], &xr[p][8 * q]);
 }
 
+// The loads of x (and of the norm weights) are issued on their own, before
+// any weight-row loads, so that waiting for x does not wait for the rows
+// (the vector-memory counter drains in issue order).  NORM is a template
+// argument, not a run-time test, so that no branch separates the norm-weight
+// loads from their use (the compiler would sink them into it).
+template <int P>
+struct XBf16Raw {
+  uint4 x[P], w[P];
+};
+template <int P, bool NORM>
+__device__ __forceinline__ void wave_x_bf16_issue(XBf16Raw<P>& r,
+                                                  const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ nw,
+                                                  int K, int lane) {
+  // unconditional, clamped loads (no branch, see bf16_load_row); padded units
+  // are zeroed in wave_x_bf16_finish
+  const int U = K / 8;
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const uint4* wv = reinterpret_cast<const uint4*>(nw);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = min(lane + 64 * p, U - 1);
+    r.x[p] = xv[u];
+    if (NORM) r.w[p] = wv[u];
+  }
+}
+template <int P, bool NORM>
+__device__ __forceinline__ void wave_x_bf16_finish(float (&xr)[P][8],
+                                                   const XBf16Raw<P>& r,
+                                                   float eps, int K, int lane,
+                                                   uint16_t* __restrict__ xn_out) {
+  const int U = K / 8;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  if (!NORM) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) unpack8((lane + 64 * p < U) ? r.x[p] : zero, xr[p]);
+    return;
+  }
+  // padded units are zeroed and add exactly +0, so no divergent branch is needed
+  float ss = 0.0f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    float f[8];
+    unpack8((lane + 64 * p < U) ? r.x[p] : zero, f);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
+  }
+  ss = wave_sum(ss);
+  const float rs = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = lane + 64 * p;
+    float a[8], w8[8];
+    unpack8(r.x[p], a);
+    unpack8(r.w[p], w8);
+    uint32_t o4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o4[j] = pack_bf2(__fmul_rn(w8[2 * j], __fmul_rn(a[2 * j], rs)),
+                       __fmul_rn(w8[2 * j + 1], __fmul_rn(a[2 * j + 1], rs)));
+    const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    unpack8((u < U) ? o : zero, xr[p]);
+    if (xn_out != nullptr && u < U) reinterpret_cast<uint4*>(xn_out)[u] = o;
+  }
+}
+
 // x (bf16, global) -> fp32 registers for the lane's bf16 units u = lane + 64 p,
 // optionally RMS-normalised (HFM:57-62).  The canonical RMSNorm (oracle
 // or_c_rmsnorm) sums squares with exactly these lane partials: ss = fmaf(x_k,
@@ -196,52 +262,13 @@ __device__ __forceinline__ void wave_load_x_bf16(float (&xr)[P][8],
                                                  const uint16_t* __restrict__ nw,
                                                  float eps, int K, int lane,
                                                  uint16_t* __restrict__ xn_out) {
-  const int U = K / 8;
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-  uint4 raw[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-    raw[p] = (u < U) ? xv[u] : make_uint4(0, 0, 0, 0);
-  }
-  if (nw == nullptr) {
-#pragma unroll
-    for (int p = 0; p < P; ++p) unpack8(raw[p], xr[p]);
-    return;
-  }
-  uint4 wr[P];
-  const uint4* wv = reinterpret_cast<const uint4*>(nw);
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-    wr[p] = (u < U) ? wv[u] : make_uint4(0, 0, 0, 0);
-  }
-  float ss = 0.0f;
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    if (lane + 64 * p < U) {
-      float f[8];
-      unpack8(raw[p], f);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
-    }
-  }
-  ss = wave_sum(ss);
-  const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-    float a[8], w8[8];
-    unpack8(raw[p], a);
-    unpack8(wr[p], w8);
-    uint32_t o4[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      o4[j] = pack_bf2(__fmul_rn(w8[2 * j], __fmul_rn(a[2 * j], r)),
-                       __fmul_rn(w8[2 * j + 1], __fmul_rn(a[2 * j + 1], r)));
-    const uint4 o = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-    unpack8((u < U) ? o : make_uint4(0, 0, 0, 0), xr[p]);
-    if (xn_out != nullptr && u < U) reinterpret_cast<uint4*>(xn_out)[u] = o;
+  XBf16Raw<P> r;
+  if (nw != nullptr) {
+    wave_x_bf16_issue<P, true>(r, x, nw, K, lane);
+    wave_x_bf16_finish<P, true>(xr, r, eps, K, lane, xn_out);
+  } else {
+    wave_x_bf16_issue<P, false>(r, x, nw, K, lane);
+    wave_x_bf16_finish<P, false>(xr, r, eps, K, lane, xn_out);
   }
 }
 
@@ -249,11 +276,13 @@ template <int P>
 __device__ __forceinline__ void bf16_load_row(uint4 (&w)[P],
                                               const uint16_t* __restrict__ row,
                                               int U, int lane) {
+  // Every load is issued (padded units re-read the row's last unit and are
+  // dropped by bf16_row_partial): a load under a divergent branch forces the
+  // compiler to wait for all outstanding loads before any use.
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-    w[p] = (u < U) ? *reinterpret_cast<const uint4*>(row + (size_t)u * 8)
-                   : make_uint4(0, 0, 0, 0);
+    const int u = min(lane + 64 * p, U - 1);
+    w[p] = *reinterpret_cast<const uint4*>(row + (size_t)u * 8);
   }
 }
 
@@ -263,8 +292,10 @@ __device__ __forceinline__ float bf16_row_partial(const uint4 (&w)[P],
                                                   int U, int lane) {
   float acc = 0.0f;
 #pragma unroll
-  for (int p = 0; p < P; ++p)
-    if (lane + 64 * p < U) acc = fma8_bf16(w[p], xr[p], acc);
+  for (int p = 0; p < P; ++p) {
+    const float t = fma8_bf16(w[p], xr[p], acc);
+    acc = (lane + 64 * p < U) ? t : acc;  // padded units leave acc untouched
+  }
   return acc;
 }
 
@@ -334,53 +365,116 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
 //                HFM:365,375)
 //   MODE_LOGITS: logits[b][n] = dot (fp32), plus the block's (max, lowest
 //                argmax) written to part_val/part_idx [B][gridDim.x]
-// grid (nblk, 1, B), block 256; rows are grid-strided in groups of rpw per
-// wave so huge N (lm_head) runs on a bounded grid.
+// grid (nblk, 1, B), block 256; a wave takes groups of 4 consecutive rows
+// (grid-strided, so huge N such as lm_head runs on a bounded grid), loads
+// all 4 rows before any arithmetic and reduces them together with the
+// 4-row xor butterfly (bit-identical to 4 separate butterflies); lane 16 r
+// then holds row r, so the 4 epilogues run in parallel lanes.
 // ===========================================================================
 enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
+constexpr int kGemvRows = 4;
 
-template <int P, int MODE>
+// xor butterfly of 4 rows at once (see wave_sum_8rows); lane l returns the
+// total of row l >> 4.
+__device__ __forceinline__ float wave_sum_4rows(float a0, float a1, float a2,
+                                                float a3, int lane) {
+  const bool u32 = (lane & 32) != 0, u16 = (lane & 16) != 0;
+  const float b0 = __fadd_rn(u32 ? a2 : a0, __shfl_xor(u32 ? a0 : a2, 32, 64));
+  const float b1 = __fadd_rn(u32 ? a3 : a1, __shfl_xor(u32 ? a1 : a3, 32, 64));
+  float t = __fadd_rn(u16 ? b1 : b0, __shfl_xor(u16 ? b0 : b1, 16, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 8, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  return t;
+}
+
+// One group of 4 rows.  FIRST: the wave's first group, which also finishes
+// the input (and its RMSNorm) from the raw loads issued before the rows, so
+// that work overlaps the row loads; later groups reuse xr.
+template <int P, int MODE, bool NORM, bool FIRST>
+__device__ __forceinline__ void gemv_bf16_group(
+    int g, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+    uint16_t bias_first, float (&xr)[P][8], const XBf16Raw<P>& xraw, float eps,
+    uint16_t* __restrict__ y, float* __restrict__ logits, int b, int N, int K,
+    int lane, float& best_v, int32_t& best_i) {
+  const int U = K / 8;
+  const int my_row = lane >> 4;  // row of the group this lane holds after the reduction
+  const int r0 = g * kGemvRows, nr = min(kGemvRows, N - r0);
+  uint4 w0[P], w1[P], w2[P], w3[P];
+  bf16_load_row<P>(w0, W + (size_t)r0 * K, U, lane);
+  bf16_load_row<P>(w1, W + (size_t)min(r0 + 1, N - 1) * K, U, lane);
+  bf16_load_row<P>(w2, W + (size_t)min(r0 + 2, N - 1) * K, U, lane);
+  bf16_load_row<P>(w3, W + (size_t)min(r0 + 3, N - 1) * K, U, lane);
+  uint16_t bias_b = bias_first;  // the first group's bias was loaded before x
+  if (!FIRST && MODE != MODE_LOGITS && bias != nullptr)
+    bias_b = bias[r0 + min(my_row, nr - 1)];
+  if (FIRST) {
+    __builtin_amdgcn_sched_barrier(0);  // all row loads issue before the norm's math
+    wave_x_bf16_finish<P, NORM>(xr, xraw, eps, K, lane, nullptr);
+  }
+  const float tot = wave_sum_4rows(bf16_row_partial<P>(w0, xr, U, lane),
+                                   bf16_row_partial<P>(w1, xr, U, lane),
+                                   bf16_row_partial<P>(w2, xr, U, lane),
+                                   bf16_row_partial<P>(w3, xr, U, lane), lane);
+  const int r = r0 + my_row;
+  if (my_row < nr) {
+    if (MODE == MODE_LOGITS) {
+      if (tot > best_v) { best_v = tot; best_i = r; }  // rows rise within a lane
+      if ((lane & 15) == 0) logits[(size_t)b * N + r] = tot;
+    } else if ((lane & 15) == 0) {
+      const float v = bias ? __fadd_rn(tot, bf2f(bias_b)) : tot;
+      const size_t o = (size_t)b * N + r;
+      if (MODE == MODE_STORE) y[o] = f2bf(v);
+      else y[o] = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
+    }
+  }
+}
+
+template <int P, int MODE, bool NORM>
 __global__ __launch_bounds__(256) void k_gemv_bf16(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ y, float* __restrict__ logits,
-    float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K,
-    int rpw) {
+    float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K) {
   __shared__ float bv_s[4];
   __shared__ int32_t bi_s[4];
-  const int U = K / 8, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.z;
-  const int ngroups = (N + rpw - 1) / rpw;
+  const int ngroups = (N + kGemvRows - 1) / kGemvRows;
   const int gstride = gridDim.x * 4;
-  int g = blockIdx.x * 4 + wave;
-  uint4 cur[P];
-  if (g < ngroups) bf16_load_row<P>(cur, W + (size_t)g * rpw * K, U, lane);
+  const int g0 = blockIdx.x * 4 + wave;
+  // The first group's bias, then the input, go out before any row load:
+  // waiting for them then does not wait for the rows (the vector-memory
+  // counter drains in issue order).  Both loads are unconditional (clamped
+  // addresses) so that no branch makes the compiler wait for everything.
+  uint16_t bias_first = 0;
+  if (MODE != MODE_LOGITS) {
+    const int rb = min(g0 * kGemvRows + (lane >> 4), N - 1);
+    bias_first = (bias != nullptr ? bias : W)[rb];
+  }
   float xr[P][8];
-  if (g < ngroups) wave_load_x_bf16<P>(xr, x + (size_t)b * K, nw, eps, K, lane, nullptr);
+  XBf16Raw<P> xraw;
+  wave_x_bf16_issue<P, NORM>(xraw, x + (size_t)b * K, nw, K, lane);
+  __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from mixing them with the rows
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
-  for (; g < ngroups; g += gstride) {
-    const int r0 = g * rpw, r1 = min(r0 + rpw, N);
-    for (int r = r0; r < r1; ++r) {
-      uint4 nxt[P];
-      const int rn = (r + 1 < r1) ? r + 1
-                                  : ((g + gstride < ngroups) ? (g + gstride) * rpw : -1);
-      if (rn >= 0) bf16_load_row<P>(nxt, W + (size_t)rn * K, U, lane);
-      const float acc = wave_sum(bf16_row_partial<P>(cur, xr, U, lane));
-      if (MODE == MODE_LOGITS) {
-        if (acc > best_v) { best_v = acc; best_i = r; }
-        if (lane == 0) logits[(size_t)b * N + r] = acc;
-      } else if (lane == 0) {
-        const float v = bias ? __fadd_rn(acc, bf2f(bias[r])) : acc;
-        const size_t o = (size_t)b * N + r;
-        if (MODE == MODE_STORE) y[o] = f2bf(v);
-        else y[o] = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
-      }
-#pragma unroll
-      for (int p = 0; p < P; ++p) cur[p] = nxt[p];
-    }
+  if (g0 < ngroups) {
+    gemv_bf16_group<P, MODE, NORM, true>(g0, W, bias, bias_first, xr, xraw, eps, y,
+                                         logits, b, N, K, lane, best_v, best_i);
+    for (int g = g0 + gstride; g < ngroups; g += gstride)
+      gemv_bf16_group<P, MODE, NORM, false>(g, W, bias, 0, xr, xraw, eps, y, logits, b,
+                                            N, K, lane, best_v, best_i);
   }
   if (MODE == MODE_LOGITS) {
+    // lanes 0, 16, 32, 48 hold the wave's candidates: keep the larger value,
+    // the lower row on ties
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const float ov = __shfl_xor(best_v, off, 64);
+      const int32_t oi = __shfl_xor(best_i, off, 64);
+      if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }
+    }
     if (lane == 0) { bv_s[wave] = best_v; bi_s[wave] = best_i; }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -396,9 +490,14 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
 
 template <int P, int MODE>
 static void launch_gemv_bf16_p(const GemvArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((k_gemv_bf16<P, MODE>), dim3(a.nblk, 1, a.B), dim3(256), 0,
-                     st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
-                     a.part_val, a.part_idx, a.N, a.K, a.rpw);
+  if (a.norm_w != nullptr)
+    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, true>), dim3(a.nblk, 1, a.B), dim3(256),
+                       0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
+                       a.part_val, a.part_idx, a.N, a.K);
+  else
+    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, false>), dim3(a.nblk, 1, a.B), dim3(256),
+                       0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
+                       a.part_val, a.part_idx, a.N, a.K);
 }
 
 template <int MODE>
@@ -417,8 +516,8 @@ static void launch_gemv_bf16_m(const GemvArgs& a, hipStream_t st) {
   }
 }
 
-int gemv_default_grid(int N, int rpw) {
-  const int ngroups = (N + rpw - 1) / rpw;
+int gemv_default_grid(int N) {
+  const int ngroups = (N + kGemvRows - 1) / kGemvRows;
   const int nblk = (ngroups + 3) / 4;
   return nblk < 2048 ? nblk : 2048;
 }
@@ -695,7 +794,7 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
   }
 }
 
-template <int P>
+template <int P, bool NORM>
 __global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
@@ -703,13 +802,19 @@ __global__ __launch_bounds__(64) void k_router_logits(
     int H) {
   const int e = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   const int U = H / 8;
+  const uint16_t bias_e = bias[e];  // bias, x and norm loads first, then the row
+  XBf16Raw<P> xraw;
+  wave_x_bf16_issue<P, NORM>(xraw, x + (size_t)b * H, nw, H, lane);
+  __builtin_amdgcn_sched_barrier(0);
   uint4 w[P];
   bf16_load_row<P>(w, W + (size_t)e * H, U, lane);
+  __builtin_amdgcn_sched_barrier(0);
   float xr[P][8];
-  wave_load_x_bf16<P>(xr, x + (size_t)b * H, nw, eps, H, lane,
-                      (xn_out != nullptr && e == 0) ? xn_out + (size_t)b * H : nullptr);
+  wave_x_bf16_finish<P, NORM>(xr, xraw, eps, H, lane,
+                              (xn_out != nullptr && e == 0) ? xn_out + (size_t)b * H
+                                                            : nullptr);
   const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
-  if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias[e]));
+  if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias_e));
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
@@ -726,11 +831,16 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
   const int P = (a.H / 8 + 63) / 64;
   dim3 grid(a.E, a.B);
   switch (P) {
-#define R_CASE(PP)                                                            \
-  case PP:                                                                    \
-    hipLaunchKernelGGL(k_router_logits<PP>, grid, dim3(64), 0, st, a.x,       \
-                       a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E, \
-                       a.H);                                                  \
+#define R_CASE(PP)                                                               \
+  case PP:                                                                       \
+    if (a.norm_w != nullptr)                                                     \
+      hipLaunchKernelGGL((k_router_logits<PP, true>), grid, dim3(64), 0, st, a.x, \
+                         a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E,  \
+                         a.H);                                                   \
+    else                                                                         \
+      hipLaunchKernelGGL((k_router_logits<PP, false>), grid, dim3(64), 0, st,    \
+                         a.x, a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out,  \
+                         a.E, a.H);                                              \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)
@@ -742,14 +852,23 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
                        a.score, a.E, a.k);
 }
 
-// Expert id of `slot` for row b: chosen from the router logits when lg is
-// given (also its weight into t.sc when WEIGHTS), else read from idx.
+// Row b's experts into the wave's LDS slice t: chosen from the router logits
+// when lg is given, else copied from idx (and score, when WEIGHTS).  Returns
+// the expert of `slot`.  Both ways the ids/weights are then read from LDS.
 template <bool WEIGHTS>
 __device__ __forceinline__ int moe_expert(const float* __restrict__ lg,
-                                          const int32_t* __restrict__ idx, int b,
+                                          const int32_t* __restrict__ idx,
+                                          const float* __restrict__ score, int b,
                                           int E, int k, int slot, int lane, TopK& t) {
-  if (lg == nullptr) return idx[b * k + slot];
-  wave_topk<WEIGHTS>(lg + (size_t)b * E, E, k, lane, t);
+  if (lg != nullptr) {
+    wave_topk<WEIGHTS>(lg + (size_t)b * E, E, k, lane, t);
+  } else {
+    if (lane < k) {
+      t.id[lane] = idx[b * k + lane];
+      if (WEIGHTS) t.sc[lane] = score[b * k + lane];
+    }
+    wave_lds_sync();
+  }
   return t.id[slot];
 }
 
@@ -779,11 +898,11 @@ __device__ __forceinline__ int moe_gate_up_expert(
     int32_t* __restrict__ idx_out, float* __restrict__ score_out, int b, int E,
     int k, int slot, int lane, int wave, TopK& t) {
   if (lg != nullptr && idx_out != nullptr && blockIdx.x == 0 && slot == 0 && wave == 0) {
-    const int e = moe_expert<true>(lg, idx, b, E, k, slot, lane, t);
+    const int e = moe_expert<true>(lg, idx, nullptr, b, E, k, slot, lane, t);
     if (lane < k) { idx_out[b * k + lane] = t.id[lane]; score_out[b * k + lane] = t.sc[lane]; }
     return e;
   }
-  return moe_expert<false>(lg, idx, b, E, k, slot, lane, t);
+  return moe_expert<false>(lg, idx, nullptr, b, E, k, slot, lane, t);
 }
 
 template <int P>
@@ -850,8 +969,8 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   __shared__ TopK tk[kMaxTopK];
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
-  const int e = slot == 0 ? moe_expert<true>(router_lg, idx, b, E, k, slot, lane, tk[0])
-                          : moe_expert<false>(router_lg, idx, b, E, k, slot, lane, tk[slot]);
+  const int e = slot == 0 ? moe_expert<true>(router_lg, idx, score, b, E, k, slot, lane, tk[0])
+                          : moe_expert<false>(router_lg, idx, score, b, E, k, slot, lane, tk[slot]);
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
@@ -877,7 +996,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) y = __builtin_fmaf(router_lg ? tk[0].sc[s] : score[b * k + s], red[s][t], y);
+      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
@@ -1102,8 +1221,8 @@ __global__ __launch_bounds__(256) void k_moe_down_t(
   const int my_row = lane >> 3;
   const int slot = wave;  // k <= 4 on this path
   if (slot < k) {
-    const int e = slot == 0 ? moe_expert<true>(router_lg, idx, b, E, k, slot, lane, tk[0])
-                            : moe_expert<false>(router_lg, idx, b, E, k, slot, lane, tk[slot]);
+    const int e = slot == 0 ? moe_expert<true>(router_lg, idx, score, b, E, k, slot, lane, tk[0])
+                            : moe_expert<false>(router_lg, idx, score, b, E, k, slot, lane, tk[slot]);
     const size_t r0 = (size_t)e * H + n0;
     uint4 xraw[(NI + 1) / 2];  // ceil(4 U / 64) words per lane (U <= 8 NI); x and bias first
     x_load_raw(act + ((size_t)b * k + slot) * I, xraw, U, lane, 64);
@@ -1123,7 +1242,7 @@ __global__ __launch_bounds__(256) void k_moe_down_t(
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      if (s < k) y = __builtin_fmaf(router_lg ? tk[0].sc[s] : score[b * k + s], red[s][t], y);
+      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][t], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
@@ -1222,55 +1341,100 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 //     den = exp(sink - M); f_s = exp(m_s - M) (0 for empty splits);
 //     den = fmaf(l_s, f_s, den); acc = fmaf(f_s, o_s, acc); out = bf16(acc * (1/den))
 //
-// grid (Hq, B), block S waves (S <= 16): one block per query head, wave w
-// computes split w, the partials meet in LDS and wave 0 merges them -- no
-// cross-block traffic.  Block x = hh * Hkv + g handles head g * G + hh, so
-// with 8 kv heads the G heads of a group share an XCD (blocks are dealt to
-// the 8 XCDs round-robin) and read their K/V once into that XCD's L2.
-// fused != 0: q_src is the raw qkv row ([Hq + 2 Hkv] heads); the block rotates
-// its q (YaRN table); the block of the group's first head appends the rotated
-// k and v of position pos to the caches, and every block uses its own copy of
-// that row for key pos.
+// k_attn_split: grid (Hkv S, B), block 64 G (G = Hq / Hkv query heads per kv
+// head).  Block (g, s) serves split s of kv head g for all G query heads of
+// the group: each 64-key chunk of K and V is loaded from HBM once into LDS
+// (one 16-byte word per thread) and read by the G waves, one wave per query
+// head.  The next chunk's words are loaded into registers while the current
+// chunk is computed.  K rows sit in LDS with their eight 16-byte words
+// rotated by the key index, so the 64 lanes of a wave, one key each, read
+// distinct banks.  Each wave writes its split's (o, m, l) partial; the last
+// split always holds key pos, so with fused != 0 (q_src = raw qkv rows) the
+// block of split S - 1 rotates the new k row (YaRN table), uses its own LDS
+// copy of the new k/v row for key pos and appends it to the caches; every
+// block rotates its q heads.
+// k_attn_merge: grid (Hq, B), 64 lanes (lane = output dim), merges the S
+// partials of a head in split order with the sink.
 // ===========================================================================
 constexpr int kD = 64;
-constexpr int kMaxSplits = 16;
+constexpr int kMaxSplits = 32;
 
-__global__ __launch_bounds__(64 * kMaxSplits) void k_attn_decode(
+// Words of the 64-key chunk starting at key CB: word WD = 8 j + ch is
+// 16-byte word ch of key CB + j; a thread owns words tid and tid + nt
+// (nt >= 256).  Keys past p read as zero; key p_lds is taken from LDS at
+// store time.  (Macros on plain locals: the words stay in registers while
+// the loads are in flight.)
+#define ATTN_LOAD_WORD(KW, VW, WD, CB)                                          \
+  do {                                                                          \
+    KW = make_uint4(0, 0, 0, 0);                                                \
+    VW = make_uint4(0, 0, 0, 0);                                                \
+    const int key_ = (CB) + ((WD) >> 3);                                        \
+    if ((WD) < 512 && key_ <= p && key_ != p_lds) {                             \
+      KW = reinterpret_cast<const uint4*>(kc + (kv_base + key_) * kD)[(WD) & 7]; \
+      VW = reinterpret_cast<const uint4*>(vc + (kv_base + key_) * kD)[(WD) & 7]; \
+    }                                                                           \
+  } while (0)
+#define ATTN_STORE_WORD(KW, VW, WD, CB, BUF)                                    \
+  do {                                                                          \
+    if ((WD) < 512) {                                                           \
+      const int j_ = (WD) >> 3, ch_ = (WD) & 7;                                 \
+      if ((CB) + j_ == p_lds) { /* two stores, not a select of addresses */    \
+        kt[BUF][j_ * 8 + ((ch_ + j_) & 7)] = knew[ch_];                         \
+        vt[BUF][j_ * 8 + ch_] = vnew[ch_];                                      \
+      } else {                                                                  \
+        kt[BUF][j_ * 8 + ((ch_ + j_) & 7)] = (KW);                              \
+        vt[BUF][j_ * 8 + ch_] = (VW);                                           \
+      }                                                                         \
+    }                                                                           \
+  } while (0)
+
+__global__ __launch_bounds__(512) void k_attn_split(
     const uint16_t* __restrict__ q_src, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, const uint16_t* __restrict__ sinks,
-    const int32_t* __restrict__ pos_arr, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, uint16_t* __restrict__ out, int Hq,
-    int Hkv, int T_max, int window, int fused, int q_stride) {
-  __shared__ __align__(16) float qf[kD];
-  __shared__ uint4 knew[kD / 8], vnew[kD / 8];
-  __shared__ float ps[kMaxSplits][64];
-  __shared__ float part_o[kMaxSplits][kD];
-  __shared__ float part_m[kMaxSplits], part_l[kMaxSplits];
-  const int S = blockDim.x >> 6;
+    uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int Hq, int Hkv,
+    int G, int T_max, int window, int S, int fused, int q_stride) {
+  __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
+  __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
+  __shared__ __align__(16) float qs[8][kD];
+  __shared__ float ps[8][64];
+  __shared__ __align__(16) uint4 knew[kD / 8], vnew[kD / 8];
+  // blockDim = 64 max(G, 4): waves w >= G only help stage the tiles
+  const int nt = blockDim.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int g = blockIdx.x % Hkv, hh = blockIdx.x / Hkv, b = blockIdx.y;
-  const int G = Hq / Hkv, h = g * G + hh;
+  const bool active = w < G;
+  const int g = blockIdx.x % Hkv, s = blockIdx.x / Hkv, b = blockIdx.y;
+  const int h = g * G + (active ? w : 0);
   const int p = pos_arr[b];
   const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
   const int n = p - lo + 1;
   const int nch = (n + 63) >> 6;
-  const int c0 = (int)((int64_t)w * nch / S), c1 = (int)((int64_t)(w + 1) * nch / S);
+  const int c0 = (int)((int64_t)s * nch / S), c1 = (int)((int64_t)(s + 1) * nch / S);
   const size_t kv_base = ((size_t)b * Hkv + g) * T_max;
+  const bool last = s == S - 1;
+  const int p_lds = (fused && last) ? p : -1;  // key served from LDS
 
-  // ---- q (and the new k/v row) into LDS ---------------------------------
+  // first chunk's words into registers (key p comes from LDS later)
+  uint4 nk0, nk1, nv0, nv1;  // the next chunk's words, in flight meanwhile
+  if (c0 < c1) {
+    ATTN_LOAD_WORD(nk0, nv0, tid, lo + c0 * 64);
+    ATTN_LOAD_WORD(nk1, nv1, tid + nt, lo + c0 * 64);
+  }
+
+  // ---- q heads (and the new k/v row for the last split) into LDS ----------
   {
     const uint16_t* qrow = q_src + (size_t)b * q_stride;
     if (fused) {
       const float* cr = cos_t + (size_t)p * (kD / 2);
       const float* sr = sin_t + (size_t)p * (kD / 2);
-      if (tid < kD / 2) {
+      if (active && lane < kD / 2) {
         const uint16_t* qh = qrow + (size_t)h * kD;
         float o1, o2;
-        rope_pair(bf2f(qh[tid]), bf2f(qh[tid + kD / 2]), cr[tid], sr[tid], o1, o2);
-        qf[tid] = bf2f(f2bf(o1));
-        qf[tid + kD / 2] = bf2f(f2bf(o2));
-      } else if (tid >= 64 && tid < 64 + kD / 2) {
-        const int t = tid - 64;
+        rope_pair(bf2f(qh[lane]), bf2f(qh[lane + kD / 2]), cr[lane], sr[lane], o1, o2);
+        qs[w][lane] = bf2f(f2bf(o1));
+        qs[w][lane + kD / 2] = bf2f(f2bf(o2));
+      } else if (last && w == 0) {
+        const int t = lane - kD / 2;
         const uint16_t* kh = qrow + (size_t)(Hq + g) * kD;
         float o1, o2;
         rope_pair(bf2f(kh[t]), bf2f(kh[t + kD / 2]), cr[t], sr[t], o1, o2);
@@ -1281,58 +1445,41 @@ __global__ __launch_bounds__(64 * kMaxSplits) void k_attn_decode(
             reinterpret_cast<const uint32_t*>(qrow + (size_t)(Hq + Hkv + g) * kD);
         reinterpret_cast<uint32_t*>(vnew)[t] = vh[t];
       }
-    } else if (tid < kD) {
-      qf[tid] = bf2f(qrow[(size_t)h * kD + tid]);
-    }
-    __syncthreads();
-    if (fused && hh == 0 && tid < kD / 8) {
-      reinterpret_cast<uint4*>(kc + (kv_base + p) * kD)[tid] = knew[tid];
-      reinterpret_cast<uint4*>(vc + (kv_base + p) * kD)[tid] = vnew[tid];
+    } else if (active) {
+      qs[w][lane] = bf2f(qrow[(size_t)h * kD + lane]);
     }
   }
-  // New-row sources for key p: this block's LDS copy when fused, else the
-  // cache (written before the launch).
-  const int p_lds = fused ? p : -1;
+  __syncthreads();
+  if (fused && last && tid < kD / 8) {
+    reinterpret_cast<uint4*>(kc + (kv_base + p) * kD)[tid] = knew[tid];
+    reinterpret_cast<uint4*>(vc + (kv_base + p) * kD)[tid] = vnew[tid];
+  }
+  if (c0 < c1) {
+    ATTN_STORE_WORD(nk0, nv0, tid, lo + c0 * 64, 0);
+    ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + c0 * 64, 0);
+  }
+  __syncthreads();
 
-  // q stays in LDS: every lane reads the same address (a broadcast), which
-  // leaves the registers to the chunk's K and V loads.
-  const float4* q4 = reinterpret_cast<const float4*>(qf);
+  const float4* q4 = reinterpret_cast<const float4*>(qs[w]);
   float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.0f;
   const int kg = lane >> 3, dq = lane & 7;
 
   for (int c = c0; c < c1; ++c) {
-    const int cb = lo + c * 64;
-    const int j = cb + lane;
-    const bool valid = j <= p;
-    // issue every K and V load of the chunk before any arithmetic
-    uint4 kr[kD / 8], vr[8];
-    {
-      const bool kg_ = valid && j != p_lds;
-      const uint4* src = reinterpret_cast<const uint4*>(kc + (kv_base + (kg_ ? j : lo)) * kD);
-#pragma unroll
-      for (int u = 0; u < kD / 8; ++u) kr[u] = kg_ ? src[u] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int jk = cb + kg + 8 * i;
-        const bool vg = jk <= p && jk != p_lds;
-        vr[i] = vg ? reinterpret_cast<const uint4*>(vc + (kv_base + jk) * kD)[dq]
-                   : make_uint4(0, 0, 0, 0);
-      }
-      if (valid && j == p_lds) {
-#pragma unroll
-        for (int u = 0; u < kD / 8; ++u) kr[u] = knew[u];
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (cb + kg + 8 * i == p_lds) vr[i] = vnew[dq];
+    const int buf = (c - c0) & 1;
+    if (c + 1 < c1) {
+      ATTN_LOAD_WORD(nk0, nv0, tid, lo + (c + 1) * 64);
+      ATTN_LOAD_WORD(nk1, nv1, tid + nt, lo + (c + 1) * 64);
     }
+    const int cb = lo + c * 64;
+    if (active) {
+    const bool valid = cb + lane <= p;
     float a = 0.0f;
 #pragma unroll
     for (int u = 0; u < kD / 8; ++u) {
       float kf[8];
-      unpack8(kr[u], kf);
+      unpack8(kt[buf][lane * 8 + ((u + lane) & 7)], kf);
       const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
       a = __builtin_fmaf(qa.x, kf[0], a);
       a = __builtin_fmaf(qa.y, kf[1], a);
@@ -1352,24 +1499,26 @@ __global__ __launch_bounds__(64 * kMaxSplits) void k_attn_decode(
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], alpha);
     ps[w][lane] = pj;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wave_lds_sync();
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int jj = kg + 8 * i;
       if (cb + jj <= p) {
         float vf[8];
-        unpack8(vr[i], vf);
+        unpack8(vt[buf][jj * 8 + dq], vf);
         const float pv = ps[w][jj];
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pv, vf[e], o[e]);
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }  // active
+    if (c + 1 < c1) {
+      ATTN_STORE_WORD(nk0, nv0, tid, lo + (c + 1) * 64, buf ^ 1);
+      ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + (c + 1) * 64, buf ^ 1);
+    }
+    __syncthreads();  // tile buf is free, tile buf ^ 1 and ps are complete
   }
+  if (!active) return;
   // reduce o over the 8 key groups (lane bits 3..5)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -1379,32 +1528,57 @@ __global__ __launch_bounds__(64 * kMaxSplits) void k_attn_decode(
     v = __fadd_rn(v, __shfl_xor(v, 32, 64));
     o[e] = v;
   }
+  const size_t pi = ((size_t)b * Hq + h) * S + s;
   if (kg == 0) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part_o[w][dq * 8 + e] = o[e];
+    float4* po = reinterpret_cast<float4*>(part_o + pi * kD + dq * 8);
+    po[0] = make_float4(o[0], o[1], o[2], o[3]);
+    po[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
-  if (lane == 0) { part_m[w] = m; part_l[w] = l; }
-  __syncthreads();
-  if (w != 0) return;
-  // ---- merge the S partials in split order; lane = output dim -----------
-  const float sk = bf2f(sinks[h]);
-  float M = sk;
-  for (int t = 0; t < S; ++t) M = fmaxf(M, part_m[t]);
-  float den = neon_expf(__fsub_rn(sk, M));
-  float acc = 0.0f;
-  for (int t = 0; t < S; ++t) {
-    const float mt = part_m[t];
-    const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
-    den = __builtin_fmaf(part_l[t], f, den);
-    acc = __builtin_fmaf(f, part_o[t][lane], acc);
-  }
-  out[(size_t)b * Hq * kD + (size_t)h * kD + lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+  if (lane == 0) { part_ml[pi * 2] = m; part_ml[pi * 2 + 1] = l; }
 }
 
+__global__ __launch_bounds__(64) void k_attn_merge(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq,
+    int S) {
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const size_t pi = ((size_t)b * Hq + h) * S;
+  // every load first: the head's S partial rows (lane = dim) and one (m, l)
+  // per lane, then the merge in split order from registers
+  float ov[kMaxSplits];
+#pragma unroll
+  for (int t = 0; t < kMaxSplits; ++t)
+    ov[t] = t < S ? part_o[(pi + t) * kD + lane] : 0.0f;
+  const float mt_l = lane < S ? part_ml[(pi + lane) * 2] : -INFINITY;
+  const float lt_l = lane < S ? part_ml[(pi + lane) * 2 + 1] : 0.0f;
+  const float sk = bf2f(sinks[h]);
+  float M = sk;
+  for (int t = 0; t < S; ++t) M = fmaxf(M, readlane_f(mt_l, t));
+  float den = neon_expf(__fsub_rn(sk, M));
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < kMaxSplits; ++t) {
+    if (t < S) {
+      const float mt = readlane_f(mt_l, t);
+      const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
+      den = __builtin_fmaf(readlane_f(lt_l, t), f, den);
+      acc = __builtin_fmaf(f, ov[t], acc);
+    }
+  }
+  out[((size_t)b * Hq + h) * kD + lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+}
+
+#undef ATTN_LOAD_WORD
+#undef ATTN_STORE_WORD
+
 void launch_attn(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(k_attn_decode, dim3(a.Hq, a.B), dim3(64 * a.S), 0, st,
-                     a.q_src, a.kc, a.vc, a.sinks, a.pos, a.cos_t, a.sin_t,
-                     a.out, a.Hq, a.Hkv, a.T_max, a.window, a.fused, a.q_stride);
+  const int G = a.Hq / a.Hkv;  // 1, 2, 4 or 8 (checked on the host)
+  hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * a.S, a.B), dim3(64 * (G < 4 ? 4 : G)),
+                     0, st, a.q_src, a.kc, a.vc, a.pos, a.cos_t, a.sin_t, a.part_o,
+                     a.part_ml, a.Hq, a.Hkv, G, a.T_max, a.window, a.S, a.fused,
+                     a.q_stride);
+  hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
+                     a.part_ml, a.sinks, a.out, a.Hq, a.S);
 }
 
 int attn_splits(int T_max, int window) {

@@ -415,10 +415,11 @@ void or_c_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
 int or_attn_splits(int T_max, int window) {
   const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
   const int s = (span + 63) / 64;
-  return s < 1 ? 1 : (s > 16 ? 16 : s);
+  return s < 1 ? 1 : (s > 32 ? 32 : s);
 }
 
-/* Decode attention with sinks, canonical split form (device k_attn_decode):
+/* Decode attention with sinks, canonical split form (device k_attn_split +
+ * k_attn_merge):
  * 64-key chunks from lo, split s owns chunks [s nch / S, (s+1) nch / S);
  * online softmax per split with lane-local P.V accumulators (lane = key group
  * kg x dim octet dq), reduced over kg by xor 8, 16, 32; splits merged in
