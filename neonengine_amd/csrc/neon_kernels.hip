@@ -132,6 +132,9 @@ struct Fp4Row {
   uint32_t s[P];
 };
 
+// Loads without branches: a lane past U re-reads the row's last unit and
+// fp4_row_partial drops it.  A load under a divergent branch would make the
+// compiler wait for every outstanding load before the first use.
 template <int P>
 __device__ __forceinline__ void fp4_load_row(Fp4Row<P>& r,
                                              const uint8_t* __restrict__ codes,
@@ -139,14 +142,9 @@ __device__ __forceinline__ void fp4_load_row(Fp4Row<P>& r,
                                              int U, int lane) {
 #pragma unroll
   for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-    if (u < U) {
-      r.c[p] = *reinterpret_cast<const uint4*>(codes + (size_t)u * 16);
-      r.s[p] = scales[u];
-    } else {
-      r.c[p] = make_uint4(0, 0, 0, 0);
-      r.s[p] = 127;
-    }
+    const int u = min(lane + 64 * p, U - 1);
+    r.c[p] = *reinterpret_cast<const uint4*>(codes + (size_t)u * 16);
+    r.s[p] = scales[u];
   }
 }
 
@@ -156,30 +154,47 @@ __device__ __forceinline__ float fp4_row_partial(const Fp4Row<P>& r,
                                                  int U, int lane) {
   float acc = 0.0f;
 #pragma unroll
-  for (int p = 0; p < P; ++p)
-    if (lane + 64 * p < U)
-      acc = __fadd_rn(acc, e8m0_scale(fp4_unit_dot(r.c[p], xr[p]), r.s[p]));
+  for (int p = 0; p < P; ++p) {
+    const float t = __fadd_rn(acc, e8m0_scale(fp4_unit_dot(r.c[p], xr[p]), r.s[p]));
+    acc = (lane + 64 * p < U) ? t : acc;  // padded units leave acc untouched
+  }
   return acc;
 }
 
 // x (bf16, global) -> fp32 registers for the lane's MXFP4 units
 // u = lane + 64 p (32 elements = 4 x 16 B each); lanes past U get zeros.
+// Issue and finish are separate so that callers can put the loads ahead of
+// the weight rows and wait for them alone.
+template <int P>
+__device__ __forceinline__ void x_fp4_issue(uint4 (&raw)[P][4],
+                                            const uint16_t* __restrict__ x, int U,
+                                            int lane) {
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = min(lane + 64 * p, U - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) raw[p][q] = xv[u * 4 + q];
+  }
+}
+template <int P>
+__device__ __forceinline__ void x_fp4_finish(float (&xr)[P][32],
+                                             const uint4 (&raw)[P][4], int U,
+                                             int lane) {
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      unpack8((lane + 64 * p < U) ? raw[p][q] : zero, &xr[p][8 * q]);
+}
 template <int P>
 __device__ __forceinline__ void wave_load_x_fp4(float (&xr)[P][32],
                                                 const uint16_t* __restrict__ x,
                                                 int U, int lane) {
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
   uint4 raw[P][4];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int u = lane + 64 * p;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) raw[p][q] = (u < U) ? xv[u * 4 + q] : make_uint4(0, 0, 0, 0);
-  }
-#pragma unroll
-  for (int p = 0; p < P; ++p)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) unpack8(raw[p][q], &xr[p][8 * q]);
+  x_fp4_issue<P>(raw, x, U, lane);
+  x_fp4_finish<P>(xr, raw, U, lane);
 }
 
 // The loads of x (and of the norm weights) are issued on their own, before
@@ -373,6 +388,34 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
 // ===========================================================================
 enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
 constexpr int kGemvRows = 4;
+
+// xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
+// lanes of an xor pair hold the same sum after every step (fp32 addition
+// commutes), so at step `off` a lane keeps half of its rows and sends the
+// other half: 7 + 3 shuffles, bit-identical to 8 separate butterflies.  Lane
+// l returns the total of row l >> 3.
+__device__ __forceinline__ float xchg(float keep, float send, int off) {
+  return __fadd_rn(keep, __shfl_xor(send, off, 64));
+}
+__device__ __forceinline__ float wave_sum_8rows(float a0, float a1, float a2,
+                                                float a3, float a4, float a5,
+                                                float a6, float a7, int lane) {
+  const bool u32 = (lane & 32) != 0, u16 = (lane & 16) != 0, u8 = (lane & 8) != 0;
+  // off 32: lanes without bit 5 keep rows 0-3, the others rows 4-7
+  const float b0 = xchg(u32 ? a4 : a0, u32 ? a0 : a4, 32);
+  const float b1 = xchg(u32 ? a5 : a1, u32 ? a1 : a5, 32);
+  const float b2 = xchg(u32 ? a6 : a2, u32 ? a2 : a6, 32);
+  const float b3 = xchg(u32 ? a7 : a3, u32 ? a3 : a7, 32);
+  // off 16: keep rows {0,1} or {2,3} of the group
+  const float c0 = xchg(u16 ? b2 : b0, u16 ? b0 : b2, 16);
+  const float c1 = xchg(u16 ? b3 : b1, u16 ? b1 : b3, 16);
+  // off 8: keep row 0 or 1
+  float t = xchg(u8 ? c1 : c0, u8 ? c0 : c1, 8);
+  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  return t;
+}
 
 // xor butterfly of 4 rows at once (see wave_sum_8rows); lane l returns the
 // total of row l >> 4.
@@ -701,6 +744,17 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// A load that stays where it is written.  The compiler sinks a plain load
+// whose only use sits in a branch (a lane-0 epilogue) into that branch, where
+// it issues last and is waited for alone; a relaxed atomic load is never
+// moved, and at workgroup scope it is the same hardware load.
+__device__ __forceinline__ uint32_t load_pinned_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint16_t load_pinned_u16(const uint16_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
@@ -721,17 +775,27 @@ struct TopK {
 
 // One wave; lg = the row's E logits (global).  On return t.id[0..k) (and,
 // with WEIGHTS, t.sc[0..k)) are visible to the wave.
+constexpr int kRouteQ = kMaxExperts / 64;  // logits per lane
+
+// The row's logits, one per lane per 64 experts (unconditional, clamped
+// loads; lanes past E are masked in wave_topk_rank).
+__device__ __forceinline__ void wave_topk_issue(const float* __restrict__ lg, int E,
+                                                int lane, float (&v)[kRouteQ]) {
+#pragma unroll
+  for (int q = 0; q < kRouteQ; ++q) v[q] = lg[min(lane + 64 * q, E - 1)];
+}
+
 template <bool WEIGHTS>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
-                                          int k, int lane, TopK& t) {
-  constexpr int NQ = kMaxExperts / 64;
+__device__ __forceinline__ void wave_topk_rank(const float (&vin)[kRouteQ], int E,
+                                               int k, int lane, TopK& t) {
+  constexpr int NQ = kRouteQ;
   float v[NQ];
   uint32_t khi[NQ], klo[NQ];
   int rank[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int e = lane + 64 * q;
-    v[q] = (64 * q < E && e < E) ? lg[e] : 0.0f;
+    v[q] = (e < E) ? vin[q] : 0.0f;
     const uint64_t key = route_key(v[q], e);
     khi[q] = (uint32_t)(key >> 32);
     klo[q] = (uint32_t)key;
@@ -794,6 +858,14 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
   }
 }
 
+template <bool WEIGHTS>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
+                                          int k, int lane, TopK& t) {
+  float v[kRouteQ];
+  wave_topk_issue(lg, E, lane, v);
+  wave_topk_rank<WEIGHTS>(v, E, k, lane, t);
+}
+
 template <int P, bool NORM>
 __global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
@@ -853,23 +925,58 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
 }
 
 // Row b's experts into the wave's LDS slice t: chosen from the router logits
-// when lg is given, else copied from idx (and score, when WEIGHTS).  Returns
-// the expert of `slot`.  Both ways the ids/weights are then read from LDS.
+// when lg is given, else copied from idx (and score, when WEIGHTS).  The
+// loads (moe_route_issue) are separate from the choice (moe_route_finish) so
+// that a kernel issues them, and its activation loads, before anything waits.
+// Both ways the ids/weights are then read from LDS.
+// Logits (lg path), or the given id (bits) and weight in v[0], v[1] (idx
+// path): one set of slots for both, so the compiler cannot merge the two
+// paths' loads into a store through a pointer chosen at run time (which
+// would put the struct in scratch memory).
+struct RouteRaw {
+  float v[kRouteQ];
+};
+
+template <bool WEIGHTS>
+__device__ __forceinline__ void moe_route_issue(const float* __restrict__ lg,
+                                                const int32_t* __restrict__ idx,
+                                                const float* __restrict__ score,
+                                                int b, int E, int k, int lane,
+                                                RouteRaw& r) {
+  if (lg != nullptr) {
+    wave_topk_issue(lg + (size_t)b * E, E, lane, r.v);
+  } else {
+    const int t = min(lane, k - 1);
+    r.v[0] = __builtin_bit_cast(float, idx[b * k + t]);
+    if (WEIGHTS) r.v[1] = score[b * k + t];
+  }
+}
+
+// Returns the expert of `slot`.
+template <bool WEIGHTS>
+__device__ __forceinline__ int moe_route_finish(const float* __restrict__ lg, int E,
+                                                int k, int slot, int lane,
+                                                const RouteRaw& r, TopK& t) {
+  if (lg != nullptr) {
+    wave_topk_rank<WEIGHTS>(r.v, E, k, lane, t);
+  } else {
+    if (lane < k) {
+      t.id[lane] = __builtin_bit_cast(int32_t, r.v[0]);
+      if (WEIGHTS) t.sc[lane] = r.v[1];
+    }
+    wave_lds_sync();
+  }
+  return t.id[slot];
+}
+
 template <bool WEIGHTS>
 __device__ __forceinline__ int moe_expert(const float* __restrict__ lg,
                                           const int32_t* __restrict__ idx,
                                           const float* __restrict__ score, int b,
                                           int E, int k, int slot, int lane, TopK& t) {
-  if (lg != nullptr) {
-    wave_topk<WEIGHTS>(lg + (size_t)b * E, E, k, lane, t);
-  } else {
-    if (lane < k) {
-      t.id[lane] = idx[b * k + lane];
-      if (WEIGHTS) t.sc[lane] = score[b * k + lane];
-    }
-    wave_lds_sync();
-  }
-  return t.id[slot];
+  RouteRaw r;
+  moe_route_issue<WEIGHTS>(lg, idx, score, b, E, k, lane, r);
+  return moe_route_finish<WEIGHTS>(lg, E, k, slot, lane, r, t);
 }
 
 // ===========================================================================
@@ -894,112 +1001,132 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
 // gate_up's expert for (b, slot); wave 0 of block (0, slot 0) also writes
 // the row's chosen ids and weights to idx_out/score_out when given.
 __device__ __forceinline__ int moe_gate_up_expert(
-    const float* __restrict__ lg, const int32_t* __restrict__ idx,
-    int32_t* __restrict__ idx_out, float* __restrict__ score_out, int b, int E,
-    int k, int slot, int lane, int wave, TopK& t) {
+    const float* __restrict__ lg, const RouteRaw& rr, int32_t* __restrict__ idx_out,
+    float* __restrict__ score_out, int b, int E, int k, int slot, int lane, int wave,
+    TopK& t) {
   if (lg != nullptr && idx_out != nullptr && blockIdx.x == 0 && slot == 0 && wave == 0) {
-    const int e = moe_expert<true>(lg, idx, nullptr, b, E, k, slot, lane, t);
+    const int e = moe_route_finish<true>(lg, E, k, slot, lane, rr, t);
     if (lane < k) { idx_out[b * k + lane] = t.id[lane]; score_out[b * k + lane] = t.sc[lane]; }
     return e;
   }
-  return moe_expert<false>(lg, idx, nullptr, b, E, k, slot, lane, t);
+  return moe_route_finish<false>(lg, E, k, slot, lane, rr, t);
 }
 
+constexpr int kMoeJpw = 4;  // gate_up: intermediate columns per wave
+constexpr int kMoeRpw = 4;  // down: output rows per block
+
+// Load order of both row kernels: routing inputs and the activation vector
+// (neither depends on the expert), then the routing choice, then the bias and
+// every weight row of the wave at once (unconditional, clamped addresses);
+// the math then waits for one load at a time, in issue order.
 template <int P>
 __global__ __launch_bounds__(256) void k_moe_gate_up(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
     const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
     const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
     float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
-    uint16_t* __restrict__ act, int H, int I, int k, int jpw, float alpha,
-    float limit) {
+    uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit) {
   __shared__ TopK tk[4];
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = moe_gate_up_expert(router_lg, idx, idx_out, score_out, b, E, k,
-                                   slot, lane, wave, tk[wave]);
+  RouteRaw rr;
+  moe_route_issue<false>(router_lg, idx, nullptr, b, E, k, lane, rr);
+  uint4 xraw[P][4];
+  x_fp4_issue<P>(xraw, xn + (size_t)b * H, U, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int e = moe_gate_up_expert(router_lg, rr, idx_out, score_out, b, E, k, slot,
+                                   lane, wave, tk[wave]);
+  const int j0 = (blockIdx.x * 4 + wave) * kMoeJpw;
+  if (j0 >= I) return;
   const size_t rows = (size_t)2 * I;
   const uint8_t* codes = gu_codes + (size_t)e * rows * (H / 2);
   const uint8_t* scales = gu_scales + (size_t)e * rows * U;
   const uint16_t* bias = gu_bias + (size_t)e * rows;
-  const int j0 = (blockIdx.x * 4 + wave) * jpw;
-  const int j1 = min(j0 + jpw, I);
-  if (j0 >= j1) return;
-  Fp4Row<P> cg, cu;
-  fp4_load_row<P>(cg, codes + (size_t)(2 * j0) * (H / 2),
-                  scales + (size_t)(2 * j0) * U, U, lane);
-  fp4_load_row<P>(cu, codes + (size_t)(2 * j0 + 1) * (H / 2),
-                  scales + (size_t)(2 * j0 + 1) * U, U, lane);
+  // lane 16 c (+8) will hold column j0 + c's gate (up) total
+  const int jl = min(j0 + (lane >> 4), I - 1);
+  const uint32_t bgu = load_pinned_u32(reinterpret_cast<const uint32_t*>(bias + 2 * jl));
+  Fp4Row<P> rw[2 * kMoeJpw];  // gate row 2j and up row 2j+1 are adjacent (HFM:83)
+#pragma unroll
+  for (int r = 0; r < 2 * kMoeJpw; ++r) {
+    const int row = 2 * min(j0 + r / 2, I - 1) + (r & 1);
+    fp4_load_row<P>(rw[r], codes + (size_t)row * (H / 2), scales + (size_t)row * U, U,
+                    lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float xr[P][32];
-  wave_load_x_fp4<P>(xr, xn + (size_t)b * H, U, lane);
-  uint16_t* out = act + ((size_t)b * k + slot) * I;
-  for (int j = j0; j < j1; ++j) {
-    Fp4Row<P> ng, nu;
-    if (j + 1 < j1) {
-      fp4_load_row<P>(ng, codes + (size_t)(2 * j + 2) * (H / 2),
-                      scales + (size_t)(2 * j + 2) * U, U, lane);
-      fp4_load_row<P>(nu, codes + (size_t)(2 * j + 3) * (H / 2),
-                      scales + (size_t)(2 * j + 3) * U, U, lane);
-    }
-    const float g = wave_sum(fp4_row_partial<P>(cg, xr, U, lane));
-    const float u = wave_sum(fp4_row_partial<P>(cu, xr, U, lane));
-    if (lane == 0) {
-      const float gb = __fadd_rn(g, bf2f(bias[2 * j]));
-      const float ub = __fadd_rn(u, bf2f(bias[2 * j + 1]));
-      out[j] = f2bf(swiglu_clamp(gb, ub, alpha, limit));
-    }
-    cg = ng;
-    cu = nu;
+  x_fp4_finish<P>(xr, xraw, U, lane);
+  // rows g0 u0 g1 u1 ...: lane l holds row l >> 3 (bit-identical butterflies)
+  const float t = wave_sum_8rows(
+      fp4_row_partial<P>(rw[0], xr, U, lane), fp4_row_partial<P>(rw[1], xr, U, lane),
+      fp4_row_partial<P>(rw[2], xr, U, lane), fp4_row_partial<P>(rw[3], xr, U, lane),
+      fp4_row_partial<P>(rw[4], xr, U, lane), fp4_row_partial<P>(rw[5], xr, U, lane),
+      fp4_row_partial<P>(rw[6], xr, U, lane), fp4_row_partial<P>(rw[7], xr, U, lane),
+      lane);
+  const float tu = __shfl_xor(t, 8, 64);  // lane 16 c receives the up total
+  const int j = j0 + (lane >> 4);
+  if ((lane & 15) == 0 && j < I) {
+    const float gb = __fadd_rn(t, bf_lo(bgu));
+    const float ub = __fadd_rn(tu, bf_hi(bgu));
+    act[((size_t)b * k + slot) * I + j] = f2bf(swiglu_clamp(gb, ub, alpha, limit));
   }
 }
 
-// down + weighted sum (+ residual): grid (ceil(H / rpw), B), block 64 k (wave
-// s handles top-k slot s).  All k waves compute the same rows; the block
-// combines y = fmaf(score_s, dot_s + bias_s, y) in slot order from y = 0
-// (HFM:111-112), one rounding to bf16, then out = bf16(residual + y) when
-// residual is given.
+// down + weighted sum (+ residual): grid (ceil(H / kMoeRpw), B), block 64 k
+// (wave s handles top-k slot s).  The k waves compute the same kMoeRpw rows
+// for their experts; the block combines y = fmaf(score_s, dot_s + bias_s, y)
+// in slot order from y = 0 (HFM:111-112), one rounding to bf16, then
+// out = bf16(residual + y) when residual is given.
 template <int P>
 __global__ __launch_bounds__(1024) void k_moe_down(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
     const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
     const int32_t* __restrict__ idx, const float* __restrict__ score, int E,
     const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
-    int H, int I, int k, int rpw) {
-  __shared__ float red[kMaxTopK][64];
+    int H, int I, int k) {
+  __shared__ float red[kMaxTopK][kMoeRpw];
   __shared__ TopK tk[kMaxTopK];
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
-  const int e = slot == 0 ? moe_expert<true>(router_lg, idx, score, b, E, k, slot, lane, tk[0])
-                          : moe_expert<false>(router_lg, idx, score, b, E, k, slot, lane, tk[slot]);
+  const int n0 = blockIdx.x * kMoeRpw;
+  RouteRaw rr;
+  moe_route_issue<true>(router_lg, idx, score, b, E, k, lane, rr);
+  uint4 xraw[P][4];
+  x_fp4_issue<P>(xraw, act + ((size_t)b * k + slot) * I, U, lane);
+  // wave 0, lane t < kMoeRpw combines row n0 + t (out stands in for a
+  // missing residual: same shape, read and ignored)
+  const uint16_t res = load_pinned_u16((residual != nullptr ? residual : out) +
+                                       (size_t)b * H + min(n0 + (lane & 3), H - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  // every wave forms the weights too (one code path; slot 0's are used)
+  const int e = moe_route_finish<true>(router_lg, E, k, slot, lane, rr, tk[slot]);
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
-  const int n0 = blockIdx.x * rpw, n1 = min(n0 + rpw, H);
-  Fp4Row<P> cur;
-  if (n0 < n1)
-    fp4_load_row<P>(cur, codes + (size_t)n0 * (I / 2), scales + (size_t)n0 * U,
-                    U, lane);
-  float xr[P][32];
-  wave_load_x_fp4<P>(xr, act + ((size_t)b * k + slot) * I, U, lane);
-  for (int n = n0; n < n1; ++n) {
-    Fp4Row<P> nxt;
-    if (n + 1 < n1)
-      fp4_load_row<P>(nxt, codes + (size_t)(n + 1) * (I / 2),
-                      scales + (size_t)(n + 1) * U, U, lane);
-    const float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
-    if (lane == 0) red[slot][n - n0] = __fadd_rn(acc, bf2f(bias[n]));
-    cur = nxt;
+  const uint16_t bl = load_pinned_u16(bias + min(n0 + (lane >> 4), H - 1));  // lane 16 r: row r
+  Fp4Row<P> rw[kMoeRpw];
+#pragma unroll
+  for (int r = 0; r < kMoeRpw; ++r) {
+    const int n = min(n0 + r, H - 1);
+    fp4_load_row<P>(rw[r], codes + (size_t)n * (I / 2), scales + (size_t)n * U, U, lane);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  float xr[P][32];
+  x_fp4_finish<P>(xr, xraw, U, lane);
+  const float t = wave_sum_4rows(
+      fp4_row_partial<P>(rw[0], xr, U, lane), fp4_row_partial<P>(rw[1], xr, U, lane),
+      fp4_row_partial<P>(rw[2], xr, U, lane), fp4_row_partial<P>(rw[3], xr, U, lane),
+      lane);
+  if ((lane & 15) == 0) red[slot][lane >> 4] = __fadd_rn(t, bf2f(bl));
   __syncthreads();
-  if (threadIdx.x < n1 - n0) {
-    const int t = threadIdx.x, n = n0 + t;
+  if (threadIdx.x < min(kMoeRpw, H - n0)) {
+    const int r = threadIdx.x, n = n0 + r;
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][t], y);
+      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][r], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
-    out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
+    out[o] = residual ? f2bf(__fadd_rn(bf2f(res), bf2f(m))) : m;
   }
 }
 
@@ -1113,34 +1240,6 @@ __device__ __forceinline__ float tile_row_partial(const float* ex, int r,
   return acc;
 }
 
-// xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
-// lanes of an xor pair hold the same sum after every step (fp32 addition
-// commutes), so at step `off` a lane keeps half of its rows and sends the
-// other half: 7 + 3 shuffles, bit-identical to 8 separate butterflies.  Lane
-// l returns the total of row l >> 3.
-__device__ __forceinline__ float xchg(float keep, float send, int off) {
-  return __fadd_rn(keep, __shfl_xor(send, off, 64));
-}
-__device__ __forceinline__ float wave_sum_8rows(float a0, float a1, float a2,
-                                                float a3, float a4, float a5,
-                                                float a6, float a7, int lane) {
-  const bool u32 = (lane & 32) != 0, u16 = (lane & 16) != 0, u8 = (lane & 8) != 0;
-  // off 32: lanes without bit 5 keep rows 0-3, the others rows 4-7
-  const float b0 = xchg(u32 ? a4 : a0, u32 ? a0 : a4, 32);
-  const float b1 = xchg(u32 ? a5 : a1, u32 ? a1 : a5, 32);
-  const float b2 = xchg(u32 ? a6 : a2, u32 ? a2 : a6, 32);
-  const float b3 = xchg(u32 ? a7 : a3, u32 ? a3 : a7, 32);
-  // off 16: keep rows {0,1} or {2,3} of the group
-  const float c0 = xchg(u16 ? b2 : b0, u16 ? b0 : b2, 16);
-  const float c1 = xchg(u16 ? b3 : b1, u16 ? b1 : b3, 16);
-  // off 8: keep row 0 or 1
-  float t = xchg(u8 ? c1 : c0, u8 ? c0 : c1, 8);
-  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
-  return t;
-}
-
 template <int P>
 __device__ __forceinline__ float tile_reduce8(const float* ex, int nrows, int U,
                                               int lane) {
@@ -1173,8 +1272,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up_t(
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float4* xs = reinterpret_cast<float4*>(smem);
   float* ex = reinterpret_cast<float*>(smem + (size_t)U * 128) + wave * kTileRows * U;
-  const int e = moe_gate_up_expert(router_lg, idx, idx_out, score_out, b, E, k,
-                                   slot, lane, wave, tk[wave]);
+  RouteRaw rr;
+  moe_route_issue<false>(router_lg, idx, nullptr, b, E, k, lane, rr);
+  const int e = moe_gate_up_expert(router_lg, rr, idx_out, score_out, b, E, k, slot,
+                                   lane, wave, tk[wave]);
   const int j0 = blockIdx.x * 16 + wave * 4;  // I % 16 == 0: a full 8-row tile
   const int nu = kTileRows * U;
   const size_t rows = (size_t)2 * I, r0 = (size_t)e * rows + 2 * (size_t)j0;
@@ -1293,17 +1394,15 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 #undef TD
     return;
   }
-  static const int jpw = env_int("NEON_MOE_JPW", 4, 1, 64);
-  static const int rpw = env_int("NEON_MOE_RPW", 4, 1, 64);  // red[][64] bound
-  const int gblk = (a.I + 4 * jpw - 1) / (4 * jpw);
-  const int dblk = (a.H + rpw - 1) / rpw;
+  const int gblk = (a.I + 4 * kMoeJpw - 1) / (4 * kMoeJpw);
+  const int dblk = (a.H + kMoeRpw - 1) / kMoeRpw;
   switch (Pg) {
 #define G_CASE(PP)                                                            \
   case PP:                                                                    \
     hipLaunchKernelGGL(k_moe_gate_up<PP>, dim3(gblk, a.k, a.B), dim3(256), 0, \
                        st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,   \
                        a.idx, a.idx_out, a.score_out, a.E, a.xn, a.act, a.H,  \
-                       a.I, a.k, jpw, a.alpha, a.limit);                      \
+                       a.I, a.k, a.alpha, a.limit);                           \
     break;
     G_CASE(1) G_CASE(2) G_CASE(3)
     default: G_CASE(4)
@@ -1315,7 +1414,7 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_moe_down<PP>, dim3(dblk, a.B), dim3(64 * a.k), 0,   \
                        st, a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg,   \
                        a.idx, a.score, a.E, a.act, a.residual, a.out, a.H,    \
-                       a.I, a.k, rpw);                                        \
+                       a.I, a.k);                                             \
     break;
     D_CASE(1) D_CASE(2) D_CASE(3)
     default: D_CASE(4)
