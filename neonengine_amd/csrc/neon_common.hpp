@@ -25,14 +25,19 @@ __device__ __forceinline__ float bf_hi(uint32_t w) {
   return __builtin_bit_cast(float, w & 0xffff0000u);
 }
 // round to nearest even; NaN stays a quiet NaN
-__host__ __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __builtin_bit_cast(uint32_t, f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+// fp32 -> bf16, round to nearest even; a NaN keeps its sign and top payload
+// bits and gets the quiet bit (the oracle's or_f2bf).  gfx950 does this in
+// one instruction, v_cvt_pk_bf16_f32 (two values per instruction); its
+// results equal the integer form (u + 0x7fff + lsb) >> 16, NaN -> (u >> 16) |
+// 0x40, for all 2^32 inputs (compared exhaustively on an MI355X).
+typedef __bf16 neon_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float neon_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  const neon_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, neon_bf16x2));
 }
 
 // ---- canonical dot products ---------------------------------------------

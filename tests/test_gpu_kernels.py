@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import neonengine_amd as ne
+from tests import rounding_cases
 from tests.gpu_util import bf16_err_ok, empty_dev, to_dev, to_host, torch_cuda
 
 pytestmark = pytest.mark.gpu
@@ -107,6 +108,18 @@ def test_gemv_bf16(orc, N, K, B):
     ok, ratio = bf16_err_ok(got, ref, abs_sum)
     say(f"  bit-exact; worst error / fp64 bound = {ratio.max():.3f}")
     assert ok.all()
+
+
+def test_gemv_bf16_output_rounding(orc):
+    """The kernels' fp32 -> bf16 output rounding at its edge cases (ties to
+    even both ways, overflow to inf, subnormal ties, NaN): hand-derived bits,
+    see tests/rounding_cases.py."""
+    Wb, x, bias, want, N, K = rounding_cases.gemv_inputs(orc)
+    y = empty_dev((1, N), np.uint16)
+    ne.gemv_bf16(to_dev(Wb.reshape(-1)), to_dev(bias), to_dev(x), y, N, K, 1)
+    got = to_host(y)[0]
+    assert np.array_equal(got[: N - 1], want), [hex(v) for v in got]
+    assert np.isnan(orc.bf16_to_f32(got[N - 1:]))[0]
 
 
 @pytest.mark.parametrize("B,H", [(1, 2880), (3, 2880), (2, 64)])

@@ -507,6 +507,20 @@ def test_c_gemv_bf16_vs_fp64(orc, N, K, B):
     assert np.array_equal(y, orc.f32_to_bf16(yf))
 
 
+def test_c_gemv_bf16_output_rounding(orc):
+    """The oracle's fp32 -> bf16 rounding (C and numpy) at hand-derived edge
+    cases: ties to even both ways, overflow to inf, subnormal ties, NaN."""
+    from tests import rounding_cases
+    Wb, x, bias, want, N, K = rounding_cases.gemv_inputs(orc)
+    y, yf = orc.c_gemv_bf16(Wb, bias, x, N, K)
+    assert np.array_equal(y[0, : N - 1], want), [hex(v) for v in y[0]]
+    assert np.isnan(orc.bf16_to_f32(y[0, N - 1:]))[0]
+    exact = np.array([sum(np.float64(v) * c for v, c in zip(w, (1, 1, 1, 0.5)))
+                      for w, _ in rounding_cases.ROWS])
+    assert np.array_equal(yf[0, : N - 1].astype(np.float64), exact)  # the sums are exact
+    assert np.array_equal(orc.f32_to_bf16(yf[0, : N - 1]), want)
+
+
 @pytest.mark.parametrize("N,K,B", [(64, 2880, 2), (9, 32, 1), (12, 4096, 2), (5, 2112, 1)])
 def test_c_mxfp4_gemv_vs_fp64(orc, N, K, B):
     rng = np.random.default_rng(N * K)
