@@ -197,6 +197,91 @@ __device__ __forceinline__ void wave_load_x_fp4(float (&xr)[P][32],
   x_fp4_finish<P>(xr, raw, U, lane);
 }
 
+// Two rows with the partial last pass shared.  With P passes over U units,
+// the last pass has r = U - 64 (P - 1) units; when r <= 32 one pass covers
+// both rows' tails: lanes [0, r) take row A's units 64 (P - 1) + l, lanes
+// [r, 2r) row B's (lanes past 2r re-read a valid unit and are ignored).  Row
+// B's tail value then moves to lane l - r, so every lane adds the same unit
+// values in the same order as the one-row form (bit-identical), with a
+// quarter fewer unit computations at U = 90.
+template <int P>
+struct Fp4RowPair {
+  uint4 c[2][P - 1];
+  uint32_t s[2][P - 1];
+  uint4 tc;
+  uint32_t ts;
+};
+
+template <int P>
+__device__ __forceinline__ void fp4_load_pair(Fp4RowPair<P>& q,
+                                              const uint8_t* __restrict__ ca,
+                                              const uint8_t* __restrict__ sa,
+                                              const uint8_t* __restrict__ cb,
+                                              const uint8_t* __restrict__ sb, int U,
+                                              int lane) {
+#pragma unroll
+  for (int p = 0; p < P - 1; ++p) {
+    const int u = lane + 64 * p;  // < 64 (P - 1) < U
+    q.c[0][p] = *reinterpret_cast<const uint4*>(ca + (size_t)u * 16);
+    q.s[0][p] = sa[u];
+    q.c[1][p] = *reinterpret_cast<const uint4*>(cb + (size_t)u * 16);
+    q.s[1][p] = sb[u];
+  }
+  const int r = U - 64 * (P - 1);
+  const bool in_b = lane >= r;
+  const int ut = 64 * (P - 1) + min(in_b ? lane - r : lane, r - 1);
+  q.tc = *reinterpret_cast<const uint4*>((in_b ? cb : ca) + (size_t)ut * 16);
+  q.ts = (in_b ? sb : sa)[ut];
+}
+
+// x for the paired form: full passes as usual, the last pass at the lane's
+// tail unit (lanes [r, 2r) repeat lanes [0, r)).
+template <int P>
+__device__ __forceinline__ void x_fp4_issue_pair(uint4 (&raw)[P][4],
+                                                 const uint16_t* __restrict__ x, int U,
+                                                 int lane) {
+  const uint4* xv = reinterpret_cast<const uint4*>(x);
+  const int r = U - 64 * (P - 1);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = p < P - 1 ? lane + 64 * p
+                            : 64 * (P - 1) + min(lane >= r ? lane - r : lane, r - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) raw[p][q] = xv[u * 4 + q];
+  }
+}
+template <int P>
+__device__ __forceinline__ void x_fp4_finish_pair(float (&xr)[P][32],
+                                                  const uint4 (&raw)[P][4]) {
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) unpack8(raw[p][q], &xr[p][8 * q]);
+}
+
+// Canonical lane partials of both rows (see fp4_row_partial).
+template <int P>
+__device__ __forceinline__ void fp4_pair_partials(const Fp4RowPair<P>& q,
+                                                  const float (&xr)[P][32], int U,
+                                                  int lane, float& a, float& b) {
+  const int r = U - 64 * (P - 1);
+  a = 0.0f;
+  b = 0.0f;
+#pragma unroll
+  for (int p = 0; p < P - 1; ++p) {
+    a = __fadd_rn(a, e8m0_scale(fp4_unit_dot(q.c[0][p], xr[p]), q.s[0][p]));
+    b = __fadd_rn(b, e8m0_scale(fp4_unit_dot(q.c[1][p], xr[p]), q.s[1][p]));
+  }
+  const float t = e8m0_scale(fp4_unit_dot(q.tc, xr[P - 1]), q.ts);
+  const float tb = __shfl(t, min(lane + r, 63), 64);  // row B's tail, from lane l + r
+  const float a2 = __fadd_rn(a, t), b2 = __fadd_rn(b, tb);
+  a = lane < r ? a2 : a;
+  b = lane < r ? b2 : b;
+}
+
+// Host side: the paired form applies when the last pass has at most 32 units.
+inline bool fp4_pair_ok(int U, int P) { return P >= 2 && U - 64 * (P - 1) <= 32; }
+
 // The loads of x (and of the norm weights) are issued on their own, before
 // any weight-row loads, so that waiting for x does not wait for the rows
 // (the vector-memory counter drains in issue order).  NORM is a template
@@ -1012,6 +1097,17 @@ __device__ __forceinline__ int moe_gate_up_expert(
   return moe_route_finish<false>(lg, E, k, slot, lane, rr, t);
 }
 
+// One routing per block: wave 0 chooses (into the block's t), the others
+// wait at the barrier and read t.  Saves the other waves' top-k work, which
+// would otherwise compete for the SIMDs with the expert math.
+__device__ __forceinline__ void moe_gate_up_route_block(
+    const float* __restrict__ lg, const RouteRaw& rr, int32_t* __restrict__ idx_out,
+    float* __restrict__ score_out, int b, int E, int k, int slot, int lane, int wave,
+    TopK& t) {
+  if (wave == 0) (void)moe_gate_up_expert(lg, rr, idx_out, score_out, b, E, k, slot, lane, 0, t);
+  __syncthreads();
+}
+
 constexpr int kMoeJpw = 4;  // gate_up: intermediate columns per wave
 constexpr int kMoeRpw = 4;  // down: output rows per block
 
@@ -1019,23 +1115,24 @@ constexpr int kMoeRpw = 4;  // down: output rows per block
 // (neither depends on the expert), then the routing choice, then the bias and
 // every weight row of the wave at once (unconditional, clamped addresses);
 // the math then waits for one load at a time, in issue order.
-template <int P>
+template <int P, bool PAIR>
 __global__ __launch_bounds__(256) void k_moe_gate_up(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
     const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
     const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
     float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
     uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit) {
-  __shared__ TopK tk[4];
+  __shared__ TopK tk;
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   RouteRaw rr;
-  moe_route_issue<false>(router_lg, idx, nullptr, b, E, k, lane, rr);
+  if (wave == 0) moe_route_issue<false>(router_lg, idx, nullptr, b, E, k, lane, rr);
   uint4 xraw[P][4];
-  x_fp4_issue<P>(xraw, xn + (size_t)b * H, U, lane);
+  if (PAIR) x_fp4_issue_pair<P>(xraw, xn + (size_t)b * H, U, lane);
+  else x_fp4_issue<P>(xraw, xn + (size_t)b * H, U, lane);
   __builtin_amdgcn_sched_barrier(0);
-  const int e = moe_gate_up_expert(router_lg, rr, idx_out, score_out, b, E, k, slot,
-                                   lane, wave, tk[wave]);
+  moe_gate_up_route_block(router_lg, rr, idx_out, score_out, b, E, k, slot, lane, wave, tk);
+  const int e = tk.id[slot];
   const int j0 = (blockIdx.x * 4 + wave) * kMoeJpw;
   if (j0 >= I) return;
   const size_t rows = (size_t)2 * I;
@@ -1045,23 +1142,38 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
   // lane 16 c (+8) will hold column j0 + c's gate (up) total
   const int jl = min(j0 + (lane >> 4), I - 1);
   const uint32_t bgu = load_pinned_u32(reinterpret_cast<const uint32_t*>(bias + 2 * jl));
-  Fp4Row<P> rw[2 * kMoeJpw];  // gate row 2j and up row 2j+1 are adjacent (HFM:83)
+  // gate row 2j and up row 2j+1 are adjacent (HFM:83); rows g0 u0 g1 u1 ...
+  float a[2 * kMoeJpw];
+  if constexpr (PAIR) {
+    Fp4RowPair<P> rp[kMoeJpw];  // the (gate, up) rows of column j0 + c as a pair
 #pragma unroll
-  for (int r = 0; r < 2 * kMoeJpw; ++r) {
-    const int row = 2 * min(j0 + r / 2, I - 1) + (r & 1);
-    fp4_load_row<P>(rw[r], codes + (size_t)row * (H / 2), scales + (size_t)row * U, U,
-                    lane);
+    for (int c = 0; c < kMoeJpw; ++c) {
+      const int row = 2 * min(j0 + c, I - 1);
+      fp4_load_pair<P>(rp[c], codes + (size_t)row * (H / 2), scales + (size_t)row * U,
+                       codes + (size_t)(row + 1) * (H / 2), scales + (size_t)(row + 1) * U,
+                       U, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float xr[P][32];
+    x_fp4_finish_pair<P>(xr, xraw);
+#pragma unroll
+    for (int c = 0; c < kMoeJpw; ++c) fp4_pair_partials<P>(rp[c], xr, U, lane, a[2 * c], a[2 * c + 1]);
+  } else {
+    Fp4Row<P> rw[2 * kMoeJpw];
+#pragma unroll
+    for (int r = 0; r < 2 * kMoeJpw; ++r) {
+      const int row = 2 * min(j0 + r / 2, I - 1) + (r & 1);
+      fp4_load_row<P>(rw[r], codes + (size_t)row * (H / 2), scales + (size_t)row * U, U,
+                      lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float xr[P][32];
+    x_fp4_finish<P>(xr, xraw, U, lane);
+#pragma unroll
+    for (int r = 0; r < 2 * kMoeJpw; ++r) a[r] = fp4_row_partial<P>(rw[r], xr, U, lane);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  float xr[P][32];
-  x_fp4_finish<P>(xr, xraw, U, lane);
-  // rows g0 u0 g1 u1 ...: lane l holds row l >> 3 (bit-identical butterflies)
-  const float t = wave_sum_8rows(
-      fp4_row_partial<P>(rw[0], xr, U, lane), fp4_row_partial<P>(rw[1], xr, U, lane),
-      fp4_row_partial<P>(rw[2], xr, U, lane), fp4_row_partial<P>(rw[3], xr, U, lane),
-      fp4_row_partial<P>(rw[4], xr, U, lane), fp4_row_partial<P>(rw[5], xr, U, lane),
-      fp4_row_partial<P>(rw[6], xr, U, lane), fp4_row_partial<P>(rw[7], xr, U, lane),
-      lane);
+  // lane l holds row l >> 3 (bit-identical to separate butterflies)
+  const float t = wave_sum_8rows(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], lane);
   const float tu = __shfl_xor(t, 8, 64);  // lane 16 c receives the up total
   const int j = j0 + (lane >> 4);
   if ((lane & 15) == 0 && j < I) {
@@ -1076,7 +1188,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
 // for their experts; the block combines y = fmaf(score_s, dot_s + bias_s, y)
 // in slot order from y = 0 (HFM:111-112), one rounding to bf16, then
 // out = bf16(residual + y) when residual is given.
-template <int P>
+template <int P, bool PAIR>
 __global__ __launch_bounds__(1024) void k_moe_down(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
     const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
@@ -1084,38 +1196,55 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
     int H, int I, int k) {
   __shared__ float red[kMaxTopK][kMoeRpw];
-  __shared__ TopK tk[kMaxTopK];
+  __shared__ TopK tk;  // wave 0 routes for the block
   const int b = blockIdx.y;
   const int U = I / 32, lane = threadIdx.x & 63, slot = threadIdx.x >> 6;
   const int n0 = blockIdx.x * kMoeRpw;
   RouteRaw rr;
-  moe_route_issue<true>(router_lg, idx, score, b, E, k, lane, rr);
+  if (slot == 0) moe_route_issue<true>(router_lg, idx, score, b, E, k, lane, rr);
   uint4 xraw[P][4];
-  x_fp4_issue<P>(xraw, act + ((size_t)b * k + slot) * I, U, lane);
+  if (PAIR) x_fp4_issue_pair<P>(xraw, act + ((size_t)b * k + slot) * I, U, lane);
+  else x_fp4_issue<P>(xraw, act + ((size_t)b * k + slot) * I, U, lane);
   // wave 0, lane t < kMoeRpw combines row n0 + t (out stands in for a
   // missing residual: same shape, read and ignored)
   const uint16_t res = load_pinned_u16((residual != nullptr ? residual : out) +
                                        (size_t)b * H + min(n0 + (lane & 3), H - 1));
   __builtin_amdgcn_sched_barrier(0);
-  // every wave forms the weights too (one code path; slot 0's are used)
-  const int e = moe_route_finish<true>(router_lg, E, k, slot, lane, rr, tk[slot]);
+  if (slot == 0) (void)moe_route_finish<true>(router_lg, E, k, 0, lane, rr, tk);
+  __syncthreads();
+  const int e = tk.id[slot];
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
   const uint16_t bl = load_pinned_u16(bias + min(n0 + (lane >> 4), H - 1));  // lane 16 r: row r
-  Fp4Row<P> rw[kMoeRpw];
+  float a[kMoeRpw];
+  if constexpr (PAIR) {
+    Fp4RowPair<P> rp[kMoeRpw / 2];
 #pragma unroll
-  for (int r = 0; r < kMoeRpw; ++r) {
-    const int n = min(n0 + r, H - 1);
-    fp4_load_row<P>(rw[r], codes + (size_t)n * (I / 2), scales + (size_t)n * U, U, lane);
+    for (int c = 0; c < kMoeRpw / 2; ++c) {
+      const int na = min(n0 + 2 * c, H - 1), nb = min(n0 + 2 * c + 1, H - 1);
+      fp4_load_pair<P>(rp[c], codes + (size_t)na * (I / 2), scales + (size_t)na * U,
+                       codes + (size_t)nb * (I / 2), scales + (size_t)nb * U, U, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float xr[P][32];
+    x_fp4_finish_pair<P>(xr, xraw);
+#pragma unroll
+    for (int c = 0; c < kMoeRpw / 2; ++c) fp4_pair_partials<P>(rp[c], xr, U, lane, a[2 * c], a[2 * c + 1]);
+  } else {
+    Fp4Row<P> rw[kMoeRpw];
+#pragma unroll
+    for (int r = 0; r < kMoeRpw; ++r) {
+      const int n = min(n0 + r, H - 1);
+      fp4_load_row<P>(rw[r], codes + (size_t)n * (I / 2), scales + (size_t)n * U, U, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float xr[P][32];
+    x_fp4_finish<P>(xr, xraw, U, lane);
+#pragma unroll
+    for (int r = 0; r < kMoeRpw; ++r) a[r] = fp4_row_partial<P>(rw[r], xr, U, lane);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  float xr[P][32];
-  x_fp4_finish<P>(xr, xraw, U, lane);
-  const float t = wave_sum_4rows(
-      fp4_row_partial<P>(rw[0], xr, U, lane), fp4_row_partial<P>(rw[1], xr, U, lane),
-      fp4_row_partial<P>(rw[2], xr, U, lane), fp4_row_partial<P>(rw[3], xr, U, lane),
-      lane);
+  const float t = wave_sum_4rows(a[0], a[1], a[2], a[3], lane);
   if ((lane & 15) == 0) red[slot][lane >> 4] = __fadd_rn(t, bf2f(bl));
   __syncthreads();
   if (threadIdx.x < min(kMoeRpw, H - n0)) {
@@ -1123,7 +1252,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     float y = 0.0f;
 #pragma unroll
     for (int s = 0; s < kMaxTopK; ++s)
-      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][r], y);
+      if (s < k) y = __builtin_fmaf(tk.sc[s], red[s][r], y);
     const uint16_t m = f2bf(y);
     const size_t o = (size_t)b * H + n;
     out[o] = residual ? f2bf(__fadd_rn(bf2f(res), bf2f(m))) : m;
@@ -1396,30 +1525,31 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
   }
   const int gblk = (a.I + 4 * kMoeJpw - 1) / (4 * kMoeJpw);
   const int dblk = (a.H + kMoeRpw - 1) / kMoeRpw;
+  static const bool no_pair = getenv("NEON_MOE_NOPAIR") != nullptr;  // A/B switch
+  const bool pg = !no_pair && fp4_pair_ok(a.H / 32, Pg), pd = !no_pair && fp4_pair_ok(a.I / 32, Pd);
+#define G_LAUNCH(PP, PR)                                                           \
+  hipLaunchKernelGGL((k_moe_gate_up<PP, PR>), dim3(gblk, a.k, a.B), dim3(256), 0, \
+                     st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg, a.idx,  \
+                     a.idx_out, a.score_out, a.E, a.xn, a.act, a.H, a.I, a.k,     \
+                     a.alpha, a.limit)
+#define D_LAUNCH(PP, PR)                                                            \
+  hipLaunchKernelGGL((k_moe_down<PP, PR>), dim3(dblk, a.B), dim3(64 * a.k), 0, st, \
+                     a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg, a.idx,        \
+                     a.score, a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
   switch (Pg) {
-#define G_CASE(PP)                                                            \
-  case PP:                                                                    \
-    hipLaunchKernelGGL(k_moe_gate_up<PP>, dim3(gblk, a.k, a.B), dim3(256), 0, \
-                       st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,   \
-                       a.idx, a.idx_out, a.score_out, a.E, a.xn, a.act, a.H,  \
-                       a.I, a.k, a.alpha, a.limit);                           \
-    break;
-    G_CASE(1) G_CASE(2) G_CASE(3)
-    default: G_CASE(4)
-#undef G_CASE
+    case 1: G_LAUNCH(1, false); break;
+    case 2: if (pg) G_LAUNCH(2, true); else G_LAUNCH(2, false); break;
+    case 3: if (pg) G_LAUNCH(3, true); else G_LAUNCH(3, false); break;
+    default: if (pg) G_LAUNCH(4, true); else G_LAUNCH(4, false); break;
   }
   switch (Pd) {
-#define D_CASE(PP)                                                            \
-  case PP:                                                                    \
-    hipLaunchKernelGGL(k_moe_down<PP>, dim3(dblk, a.B), dim3(64 * a.k), 0,   \
-                       st, a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg,   \
-                       a.idx, a.score, a.E, a.act, a.residual, a.out, a.H,    \
-                       a.I, a.k);                                             \
-    break;
-    D_CASE(1) D_CASE(2) D_CASE(3)
-    default: D_CASE(4)
-#undef D_CASE
+    case 1: D_LAUNCH(1, false); break;
+    case 2: if (pd) D_LAUNCH(2, true); else D_LAUNCH(2, false); break;
+    case 3: if (pd) D_LAUNCH(3, true); else D_LAUNCH(3, false); break;
+    default: if (pd) D_LAUNCH(4, true); else D_LAUNCH(4, false); break;
   }
+#undef G_LAUNCH
+#undef D_LAUNCH
 }
 
 // ===========================================================================
