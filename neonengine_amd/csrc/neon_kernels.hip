@@ -812,13 +812,12 @@ void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
 // NaN) to the lower expert index.  Each logit maps to a 64-bit key that is
 // larger exactly when the expert comes earlier (an order-preserving integer
 // image of the float in the high half, NaN as 0, -0 as +0; the complement of
-// the index in the low half); an expert's rank is the number of larger keys,
-// counted with v_readlane over the keys held one per lane (E steps of a few
-// instructions).  Rows without NaN take a shorter path with the same result:
-// plain float compares (-0 == +0) with ties to the lower index.  The experts of rank t < k are the chosen ones, in rank
-// order; their weights are e_t = exp(v_t - v_0) (neon_expf), s = sum in rank
-// order, e_t / s.  Every MoE wave runs it on the logits itself, so no block
-// waits on another.
+// the index in the low half); an expert's rank is the number of larger keys.
+// The keys go to LDS and every lane counts over them with broadcast reads
+// (at E <= 32 the two halves of the wave each count half of the keys).  The
+// experts of rank t < k are the chosen ones, in rank order; their weights
+// are e_t = exp(v_t - v_0) (neon_expf), s = sum in rank order, e_t / s.  Each
+// MoE block runs it on the logits itself, so no block waits on another.
 // ===========================================================================
 constexpr int kMaxExperts = 256;
 constexpr int kMaxTopK = 16;
@@ -852,10 +851,11 @@ __device__ __forceinline__ uint64_t route_key(float v, int i) {
   return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
 }
 
-// Chosen experts of one row, in the wave's LDS slice.
+// Chosen experts of one row, in the routing wave's LDS.
 struct TopK {
   int32_t id[kMaxTopK];
   float sc[kMaxTopK];  // weights (when asked for), else the chosen logits
+  uint64_t key[kMaxExperts];  // the row's route keys (ranking scratch)
 };
 
 // One wave; lg = the row's E logits (global).  On return t.id[0..k) (and,
@@ -875,62 +875,48 @@ __device__ __forceinline__ void wave_topk_rank(const float (&vin)[kRouteQ], int 
                                                int k, int lane, TopK& t) {
   constexpr int NQ = kRouteQ;
   float v[NQ];
-  uint32_t khi[NQ], klo[NQ];
-  int rank[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int e = lane + 64 * q;
     v[q] = (e < E) ? vin[q] : 0.0f;
-    const uint64_t key = route_key(v[q], e);
-    khi[q] = (uint32_t)(key >> 32);
-    klo[q] = (uint32_t)key;
-    rank[q] = 0;
+    if (e < E) t.key[e] = route_key(v[q], e);
   }
-  bool nan = false;
+  wave_lds_sync();
+  // rank = number of larger keys; keys are read back from LDS (broadcast
+  // reads), so the loop is plain vector compares with no scalar round trips
+  if (E <= 32) {
+    // lanes l and l + 32 share expert l: each counts over half of the keys
+    const int i = lane & 31, h = lane >> 5;
+    const uint64_t ki = t.key[min(i, E - 1)];
+    int r0 = 0, r1 = 0;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) nan |= v[q] != v[q];
-  if (E <= 64 && __ballot(nan) == 0) {
-    // one expert per lane, no NaN in the row: plain float compares
-    // (-0 == +0), ties to the lower index, branch-free
-    const float vi = v[0];
-    int r = 0;
-#pragma unroll 4
-    for (int j = 0; j < E; ++j) {
-      const float vj = readlane_f(vi, j);
-      r += (int)((vj > vi) | ((vj == vi) & (j < lane)));
+    for (int jj = 0; jj < 16; jj += 2) {
+      const int j = 16 * h + jj;
+      r0 += (j < E && t.key[min(j, E - 1)] > ki) ? 1 : 0;
+      r1 += (j + 1 < E && t.key[min(j + 1, E - 1)] > ki) ? 1 : 0;
     }
-    rank[0] = r;
-  } else if (__ballot(nan) == 0) {
-#pragma unroll
-    for (int jq = 0; jq < NQ; ++jq) {
-      if (64 * jq >= E) continue;  // uniform
-      const int jn = min(64, E - 64 * jq);
-      for (int jl = 0; jl < jn; ++jl) {
-        const float vj = readlane_f(v[jq], jl);
-        const int j = 64 * jq + jl;
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-          if (64 * q < E) rank[q] += (vj > v[q] || (vj == v[q] && j < lane + 64 * q)) ? 1 : 0;
-      }
-    }
+    int r = r0 + r1;
+    r += __shfl_xor(r, 32, 64);
+    if (lane < E && r < k) { t.id[r] = lane; t.sc[r] = v[0]; }
   } else {
+    uint64_t ki[NQ];
+    int rank[NQ];
 #pragma unroll
-    for (int jq = 0; jq < NQ; ++jq) {
-      if (64 * jq >= E) continue;  // uniform
-      const int jn = min(64, E - 64 * jq);
-      for (int jl = 0; jl < jn; ++jl) {
-        const uint64_t kj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)khi[jq], jl) << 32) |
-                            (uint32_t)__builtin_amdgcn_readlane((int)klo[jq], jl);
-#pragma unroll
-        for (int q = 0; q < NQ; ++q)
-          if (64 * q < E) rank[q] += kj > (((uint64_t)khi[q] << 32) | klo[q]) ? 1 : 0;
-      }
+    for (int q = 0; q < NQ; ++q) {
+      ki[q] = t.key[min(lane + 64 * q, E - 1)];
+      rank[q] = 0;
     }
-  }
+    for (int j = 0; j < E; ++j) {
+      const uint64_t kj = t.key[j];
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    const int e = lane + 64 * q;
-    if (64 * q < E && e < E && rank[q] < k) { t.id[rank[q]] = e; t.sc[rank[q]] = v[q]; }
+      for (int q = 0; q < NQ; ++q)
+        if (64 * q < E) rank[q] += kj > ki[q] ? 1 : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int e = lane + 64 * q;
+      if (e < E && rank[q] < k) { t.id[rank[q]] = e; t.sc[rank[q]] = v[q]; }
+    }
   }
   wave_lds_sync();
   if (WEIGHTS) {
@@ -1259,274 +1245,12 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   }
 }
 
-// ===========================================================================
-// MoE expert FFN, tiled form (NEON_MOE_KERNEL=tile).
-//
-// A wave owns a tile of TR consecutive rows of one expert matrix.  Rows are
-// contiguous in memory, so the tile is one run of nu = rows * U 16-byte code
-// units (U = K / 32; unit f = r U + u is row r, units u of the row) and nu
-// scale bytes.  Lane l loads units f = l + 64 i: every load instruction covers
-// 1 KB of consecutive bytes and no lane idles (at K = 2880 the row-per-wave
-// form leaves 38 of 64 lanes idle on the second unit of every row).
-//
-// x lives in LDS as fp32 in chunk-major order (xs[q U + u] = elements
-// 32 u + 4 q .. + 3), so lanes reading consecutive units read consecutive
-// 16-byte words.  Each lane computes the canonical unit value
-// ldexp(fmaf chain over the unit's 32 elements, s - 127) of its units and
-// stores it to ex[f] in the wave's LDS slice; lane c then forms the canonical
-// lane partial of every row, 0 + ex[r U + c] + ex[r U + c + 64] + ..., the
-// exact operation sequence of the row-per-wave form, so results are
-// bit-identical to it and to the oracle.
-// ===========================================================================
-constexpr int kTileRows = 8;
-
-template <int NI>
-struct Fp4Tile {
-  uint4 c[NI];
-  uint32_t s[NI];
-};
-
-// Loads without branches (nu >= 1): a lane past the tile re-reads its last
-// unit and discards it, so every load is issued unconditionally and the
-// compiler can wait for each one in turn instead of for all of them.
-template <int NI>
-__device__ __forceinline__ void fp4_tile_load(Fp4Tile<NI>& t,
-                                              const uint8_t* __restrict__ codes,
-                                              const uint8_t* __restrict__ scales,
-                                              int nu, int lane) {
-  // scale bytes first: unit i then waits only for code load i
-#pragma unroll
-  for (int i = 0; i < NI; ++i) t.s[i] = scales[min(lane + 64 * i, nu - 1)];
-#pragma unroll
-  for (int i = 0; i < NI; ++i)
-    t.c[i] = *reinterpret_cast<const uint4*>(codes + (size_t)min(lane + 64 * i, nu - 1) * 16);
-}
-
-// bf16 x[K] -> xs (chunk-major fp32) in two halves, so the x loads can be
-// issued before a tile's loads and waited for on their own (the vector-memory
-// counter drains in issue order).  Thread t of nt handles 16-byte words
-// w = t + nt j (w covers elements 8 w .. 8 w + 7), j < NX.
-template <int NX>
-__device__ __forceinline__ void x_load_raw(const uint16_t* __restrict__ x,
-                                           uint4 (&raw)[NX], int U, int t, int nt) {
-  const uint4* xv = reinterpret_cast<const uint4*>(x);
-#pragma unroll
-  for (int j = 0; j < NX; ++j) {
-    const int w = t + nt * j;
-    raw[j] = w < U * 4 ? xv[w] : make_uint4(0, 0, 0, 0);
-  }
-}
-template <int NX>
-__device__ __forceinline__ void x_store_lds(const uint4 (&raw)[NX], float4* xs,
-                                            int U, int t, int nt) {
-#pragma unroll
-  for (int j = 0; j < NX; ++j) {
-    const int w = t + nt * j;
-    if (w < U * 4) {
-      float f[8];
-      unpack8(raw[j], f);
-      const int u = w >> 2, q = (w & 3) * 2;
-      xs[q * U + u] = make_float4(f[0], f[1], f[2], f[3]);
-      xs[(q + 1) * U + u] = make_float4(f[4], f[5], f[6], f[7]);
-    }
-  }
-}
-
-// Unit values of the tile into ex[f].
-template <int NI>
-__device__ __forceinline__ void fp4_tile_units(const Fp4Tile<NI>& t,
-                                               const float4* xs, float* ex,
-                                               int U, int nu, int lane) {
-  const int step = 64 % U;  // f += 64 moves the unit index by 64 mod U
-  int u = lane % U;
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int f = lane + 64 * i;
-    if (f < nu) {
-      float xv[32];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float4 v = xs[q * U + u];
-        xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
-      }
-      ex[f] = e8m0_scale(fp4_unit_dot(t.c[i], xv), t.s[i]);
-    }
-    u += step;
-    u = u >= U ? u - U : u;
-  }
-}
-
-// Canonical lane partial of row r (rows >= nrows give 0).
-template <int P>
-__device__ __forceinline__ float tile_row_partial(const float* ex, int r,
-                                                  int nrows, int U, int lane) {
-  float acc = 0.0f;
-  if (r < nrows) {
-#pragma unroll
-    for (int p = 0; p < P; ++p)
-      if (lane + 64 * p < U) acc = __fadd_rn(acc, ex[r * U + lane + 64 * p]);
-  }
-  return acc;
-}
-
-template <int P>
-__device__ __forceinline__ float tile_reduce8(const float* ex, int nrows, int U,
-                                              int lane) {
-  return wave_sum_8rows(tile_row_partial<P>(ex, 0, nrows, U, lane),
-                        tile_row_partial<P>(ex, 1, nrows, U, lane),
-                        tile_row_partial<P>(ex, 2, nrows, U, lane),
-                        tile_row_partial<P>(ex, 3, nrows, U, lane),
-                        tile_row_partial<P>(ex, 4, nrows, U, lane),
-                        tile_row_partial<P>(ex, 5, nrows, U, lane),
-                        tile_row_partial<P>(ex, 6, nrows, U, lane),
-                        tile_row_partial<P>(ex, 7, nrows, U, lane), lane);
-}
-
-// gate_up + SwiGLU, tiled: grid (ceil(I / 16), k, B), block 256.  The block
-// serves one (token, slot); wave w owns columns j0 = 16 i + 4 w .. + 3, i.e.
-// the 8 rows 2 j0 .. 2 j0 + 7 (gate/up interleaved).  Every wave routes on
-// its own (the logits are E floats) so it can issue its tile loads at once;
-// x is converted into LDS while those loads are in flight.  Dynamic LDS: xs
-// (U * 128 B) + 4 waves * 8 U floats.
-template <int NI>  // NI = ceil(8 U / 64): loads per lane for an 8-row tile
-__global__ __launch_bounds__(256) void k_moe_gate_up_t(
-    const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
-    const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
-    float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
-    uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit) {
-  extern __shared__ __align__(16) char smem[];
-  __shared__ TopK tk[4];
-  const int slot = blockIdx.y, b = blockIdx.z;
-  const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float4* xs = reinterpret_cast<float4*>(smem);
-  float* ex = reinterpret_cast<float*>(smem + (size_t)U * 128) + wave * kTileRows * U;
-  RouteRaw rr;
-  moe_route_issue<false>(router_lg, idx, nullptr, b, E, k, lane, rr);
-  const int e = moe_gate_up_expert(router_lg, rr, idx_out, score_out, b, E, k, slot,
-                                   lane, wave, tk[wave]);
-  const int j0 = blockIdx.x * 16 + wave * 4;  // I % 16 == 0: a full 8-row tile
-  const int nu = kTileRows * U;
-  const size_t rows = (size_t)2 * I, r0 = (size_t)e * rows + 2 * (size_t)j0;
-  // x and bias loads first, then the tile's loads: staging x waits only for x
-  uint4 xraw[(NI + 7) / 8];  // ceil(4 U / 256) words per thread (U <= 8 NI)
-  x_load_raw(xn + (size_t)b * H, xraw, U, threadIdx.x, 256);
-  const int my_row = lane >> 3;
-  const uint16_t bias_b = gu_bias[r0 + my_row];
-  Fp4Tile<NI> w;
-  fp4_tile_load<NI>(w, gu_codes + r0 * (H / 2), gu_scales + r0 * U, nu, lane);
-  x_store_lds(xraw, xs, U, threadIdx.x, 256);
-  __syncthreads();
-  fp4_tile_units<NI>(w, xs, ex, U, nu, lane);
-  wave_lds_sync();
-  const float tot = __fadd_rn(tile_reduce8<4>(ex, kTileRows, U, lane), bf2f(bias_b));
-  const float up = __shfl_xor(tot, 8, 64);  // gate row 2c in lane 16c, up row in 16c + 8
-  if ((lane & 15) == 0)
-    act[((size_t)b * k + slot) * I + j0 + (lane >> 4)] = f2bf(swiglu_clamp(tot, up, alpha, limit));
-}
-
-// down + weighted sum (+ residual), tiled: grid (ceil(H / 8), B), block 256,
-// k <= 4.  Wave w handles top-k slot w: it routes on its own, issues the
-// loads of its slot's 8-row tile, stages its slot's act row in its own LDS
-// slice, and reduces the 8 rows.  The block then combines
-// y = fmaf(score_s, dot_s + bias_s, y) in slot order from 0 (HFM:111-112),
-// rounds to bf16, and adds the residual when given.  Dynamic LDS: 4 waves *
-// (U * 128 B + 8 U floats).
-template <int NI>  // NI = ceil(8 U / 64): loads per lane for an 8-row tile
-__global__ __launch_bounds__(256) void k_moe_down_t(
-    const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
-    const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
-    const int32_t* __restrict__ idx, const float* __restrict__ score, int E,
-    const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
-    int H, int I, int k) {
-  extern __shared__ __align__(16) char smem[];
-  __shared__ float red[4][kTileRows];
-  __shared__ TopK tk[4];
-  const int b = blockIdx.y;
-  const int U = I / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float4* xs = reinterpret_cast<float4*>(smem + (size_t)wave * (U * 128 + kTileRows * U * 4));
-  float* ex = reinterpret_cast<float*>(reinterpret_cast<char*>(xs) + (size_t)U * 128);
-  const int n0 = blockIdx.x * kTileRows;  // H % 8 == 0: a full 8-row tile
-  const int nu = kTileRows * U;
-  const int my_row = lane >> 3;
-  const int slot = wave;  // k <= 4 on this path
-  if (slot < k) {
-    const int e = slot == 0 ? moe_expert<true>(router_lg, idx, score, b, E, k, slot, lane, tk[0])
-                            : moe_expert<false>(router_lg, idx, score, b, E, k, slot, lane, tk[slot]);
-    const size_t r0 = (size_t)e * H + n0;
-    uint4 xraw[(NI + 1) / 2];  // ceil(4 U / 64) words per lane (U <= 8 NI); x and bias first
-    x_load_raw(act + ((size_t)b * k + slot) * I, xraw, U, lane, 64);
-    const uint16_t bias_b = dn_bias[r0 + my_row];
-    Fp4Tile<NI> w;
-    fp4_tile_load<NI>(w, dn_codes + r0 * (I / 2), dn_scales + r0 * U, nu, lane);
-    x_store_lds(xraw, xs, U, lane, 64);
-    wave_lds_sync();
-    fp4_tile_units<NI>(w, xs, ex, U, nu, lane);
-    wave_lds_sync();
-    const float tot = __fadd_rn(tile_reduce8<4>(ex, kTileRows, U, lane), bf2f(bias_b));
-    if ((lane & 7) == 0) red[slot][my_row] = tot;
-  }
-  __syncthreads();
-  if (threadIdx.x < kTileRows) {
-    const int t = threadIdx.x, n = n0 + t;
-    float y = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-      if (s < k) y = __builtin_fmaf(tk[0].sc[s], red[s][t], y);
-    const uint16_t m = f2bf(y);
-    const size_t o = (size_t)b * H + n;
-    out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
-  }
-}
-
-// Rows per wave: gate_up columns per wave (jpw) and down rows per block
-// (rpw).  NEON_MOE_JPW / NEON_MOE_RPW override them (tuning aid; read once).
-static int env_int(const char* name, int dflt, int lo, int hi) {
-  const char* v = getenv(name);
-  if (!v || !*v) return dflt;
-  const int x = atoi(v);
-  return x < lo ? lo : (x > hi ? hi : x);
-}
-
-// The row-per-wave kernels are the default (measured faster at the 20b shape:
-// 23.1 vs 25.6 us per pair).  NEON_MOE_KERNEL=tile selects the tiled
-// kernels where they apply: full tiles (I % 16 == 0, H % 8 == 0), 256 U
-// (gate_up) and 640 U (down) bytes of dynamic LDS, and top-k <= 4.
-static bool moe_use_tiled(const MoeArgs& a) {
-  static const bool tile = getenv("NEON_MOE_KERNEL") && !strcmp(getenv("NEON_MOE_KERNEL"), "tile");
-  return tile && a.k <= 4 && a.I % 16 == 0 && a.H % kTileRows == 0 &&
-         256 * (a.H / 32) <= 60 * 1024 && 640 * (a.I / 32) <= 60 * 1024;
-}
-
 void launch_moe(const MoeArgs& a, hipStream_t st) {
   const int Pg = (a.H / 32 + 63) / 64;  // gate_up reduces over H
   const int Pd = (a.I / 32 + 63) / 64;  // down reduces over I
-  if (moe_use_tiled(a)) {
-    const size_t lg = (size_t)256 * (a.H / 32), ld = (size_t)640 * (a.I / 32);
-    const int gblk = a.I / 16, dblk = a.H / kTileRows;
-    const int nig = (kTileRows * (a.H / 32) + 63) / 64, nid = (kTileRows * (a.I / 32) + 63) / 64;
-    // gate_up first, then down (down reads the activations gate_up writes)
-#define TG(NIV)                                                                 \
-  hipLaunchKernelGGL(k_moe_gate_up_t<NIV>, dim3(gblk, a.k, a.B), dim3(256), lg, \
-                     st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg,      \
-                     a.idx, a.idx_out, a.score_out, a.E, a.xn, a.act, a.H,     \
-                     a.I, a.k, a.alpha, a.limit)
-#define TD(NIV)                                                                 \
-  hipLaunchKernelGGL(k_moe_down_t<NIV>, dim3(dblk, a.B), dim3(256), ld, st,    \
-                     a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg, a.idx,   \
-                     a.score, a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
-    if (nig <= 2) TG(2); else if (nig <= 4) TG(4); else if (nig <= 8) TG(8);
-    else if (nig <= 12) TG(12); else if (nig <= 16) TG(16); else TG(24);
-    if (nid <= 2) TD(2); else if (nid <= 4) TD(4); else if (nid <= 8) TD(8);
-    else if (nid <= 12) TD(12); else if (nid <= 16) TD(16); else TD(24);
-#undef TG
-#undef TD
-    return;
-  }
   const int gblk = (a.I + 4 * kMoeJpw - 1) / (4 * kMoeJpw);
   const int dblk = (a.H + kMoeRpw - 1) / kMoeRpw;
-  static const bool no_pair = getenv("NEON_MOE_NOPAIR") != nullptr;  // A/B switch
-  const bool pg = !no_pair && fp4_pair_ok(a.H / 32, Pg), pd = !no_pair && fp4_pair_ok(a.I / 32, Pd);
+  const bool pg = fp4_pair_ok(a.H / 32, Pg), pd = fp4_pair_ok(a.I / 32, Pd);
 #define G_LAUNCH(PP, PR)                                                           \
   hipLaunchKernelGGL((k_moe_gate_up<PP, PR>), dim3(gblk, a.k, a.B), dim3(256), 0, \
                      st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg, a.idx,  \
