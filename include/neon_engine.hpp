@@ -66,6 +66,10 @@ class Engine {
     check(neon_load_tensor(ctx_, name.c_str(), data, bytes), ctx_);
   }
 
+  // Prompt mode: NEON_PREFILL_BATCHED (matrix cores, default) or
+  // NEON_PREFILL_STEPWISE (every prompt token as a decode step).
+  void set_prefill_mode(int mode) { check(neon_set_prefill_mode(ctx_, mode), ctx_); }
+
   // Forward: prefill `batch` prompts of equal length (row-major ids), then
   // greedy decode steps; tokens() returns prompt + generated ids per row.
   void prefill(const std::vector<int32_t>& ids, int batch, void* stream = nullptr) {

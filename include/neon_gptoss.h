@@ -89,10 +89,19 @@ neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
                              const void* host_data, size_t bytes);
 
 /* Starts `batch` sequences from host prompt ids [batch][n_tokens] and runs
- * the teacher-forced steps over the prompt; afterwards the first generated
- * token of each sequence is available. */
+ * the prompt; afterwards the first generated token of each sequence is
+ * available.  In the default batched mode, prompt rows 0 .. n_tokens-2 of a
+ * sequence go through every layer at once on the matrix cores (filling the
+ * KV cache) and the last prompt token runs as a decode step; the stepwise
+ * mode runs every prompt token as a decode step (the decode kernels' exact
+ * fp32 order throughout).  Neither mode has a counterpart in the reference,
+ * which has no model code. */
 neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
                          int n_tokens, void* stream);
+
+enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1 };
+/* Selects how neon_prefill runs the prompt (default NEON_PREFILL_BATCHED). */
+neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
 
 /* Runs `n_steps` greedy decode steps for every live sequence (each step
  * consumes the previously generated token and produces the next one). */
@@ -197,6 +206,36 @@ neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                              const int32_t* pos, uint16_t* out, int B, int Hq,
                              int Hkv, int D, int T_max, int window,
                              void* stream);
+
+/* ---- prefill kernels (matrix cores; fp32 accumulate in the MFMA order) --- */
+
+/* C[M][N] = bf16(A[M][K] W[N][K]^T + bias) (accumulate = 0), or
+ * C = bf16(C + bf16(A W^T + bias)) (accumulate = 1, C holds the residual).
+ * bias may be NULL.  K % 32 == 0.  Used for the prompt-row projections. */
+neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
+                           const uint16_t* bias, uint16_t* C, int M, int N,
+                           int K, int accumulate, void* stream);
+
+/* Expert FFN over M prompt rows: for each row t and slot s, expert
+ * idx[t][s] (device int32 in [0, E)) applies gate_up -> SwiGLU-clamp -> down
+ * to x[t] (normalised, bf16 [M][H]); h[t] = bf16(h[t] + bf16(sum_s
+ * score[t][s] y_ts)) in place.  Rows are grouped by expert into MXFP4
+ * matrix-core GEMMs (weights dequantised exactly to bf16). */
+neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
+                             const float* score, const uint8_t* gu_codes,
+                             const uint8_t* gu_scales, const uint16_t* gu_bias,
+                             const uint8_t* dn_codes, const uint8_t* dn_scales,
+                             const uint16_t* dn_bias, uint16_t* h, int M, int E,
+                             int H, int I, int k, float alpha, float limit,
+                             void* stream);
+
+/* Causal sink attention over a prompt: q [M][Hq][D] (rotated) at positions
+ * 0 .. M-1, caches [Hkv][T_max][D] holding keys/values 0 .. M-1; row t sees
+ * keys 0..t (the last `window` of them when window > 0).  out [M][Hq*D]. */
+neon_status neon_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
+                              const uint16_t* v_cache, const uint16_t* sinks,
+                              uint16_t* out, int M, int Hq, int Hkv, int D,
+                              int T_max, int window, void* stream);
 
 #ifdef __cplusplus
 }

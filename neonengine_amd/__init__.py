@@ -31,7 +31,8 @@ EXPORTS = (
     "neon_tensor_ptr",
     "neon_mxfp4_dequant", "neon_mxfp4_gemv", "neon_gemv_bf16", "neon_rmsnorm",
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
-    "neon_attn_decode",
+    "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
+    "neon_attn_prefill",
 )
 
 
@@ -90,6 +91,10 @@ def lib():
             "neon_moe_layer": [_P] * 13 + [_I] * 5 + [_F, _F, _P],
             "neon_moe_experts": [_P] * 12 + [_I] * 5 + [_F, _F, _P],
             "neon_attn_decode": [_P] * 6 + [_I] * 6 + [_P],
+            "neon_set_prefill_mode": [_P, _I],
+            "neon_gemm_bf16": [_P] * 4 + [_I] * 4 + [_P],
+            "neon_moe_prefill": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
+            "neon_attn_prefill": [_P] * 5 + [_I] * 6 + [_P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -197,6 +202,27 @@ def attn_decode(q, k_cache, v_cache, sinks, pos, out, B, Hq, Hkv, D, T_max, wind
                                   _stream(stream)))
 
 
+def gemm_bf16(A, W, bias, C_, M, N, K, accumulate=False, stream=None):
+    _check(lib().neon_gemm_bf16(_ptr(A), _ptr(W), _ptr(bias), _ptr(C_), M, N, K,
+                                1 if accumulate else 0, _stream(stream)))
+
+
+def moe_prefill(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
+                h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None):
+    _check(lib().neon_moe_prefill(
+        _ptr(x), _ptr(idx), _ptr(score), _ptr(gu_codes), _ptr(gu_scales), _ptr(gu_bias),
+        _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(h), M, E, H, I, k, alpha, limit,
+        _stream(stream)))
+
+
+def attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, D, T_max, window, stream=None):
+    _check(lib().neon_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(sinks),
+                                   _ptr(out), M, Hq, Hkv, D, T_max, window, _stream(stream)))
+
+
+PREFILL_BATCHED, PREFILL_STEPWISE = 0, 1
+
+
 # ---------------------------------------------------------------------------
 # context-level API
 # ---------------------------------------------------------------------------
@@ -242,6 +268,10 @@ class Engine:
         p, n = C.c_void_p(), C.c_size_t()
         self._chk(lib().neon_tensor_ptr(self._ctx, name.encode(), C.byref(p), C.byref(n)))
         return p.value, n.value
+
+    def set_prefill_mode(self, mode: int):
+        """PREFILL_BATCHED (default, matrix cores) or PREFILL_STEPWISE."""
+        self._chk(lib().neon_set_prefill_mode(self._ctx, mode))
 
     def prefill(self, ids, stream=None):
         """ids: nested list / array [batch][n_tokens] of int."""

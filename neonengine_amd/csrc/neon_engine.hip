@@ -82,6 +82,15 @@ struct neon_ctx {
   int batch = 0;
   int host_pos = 0;
   bool weights_ready = false;
+  // batched prefill (M prompt rows per pass): scratch grown on demand
+  int prefill_mode = NEON_PREFILL_STEPWISE;
+  char* pf = nullptr;
+  int pf_rows = 0;
+  uint16_t *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
+           *pf_ao = nullptr, *pf_act = nullptr;
+  float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
+  int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
+          *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
   // captured decode step
   hipStream_t cap_stream = nullptr;
   hipGraph_t graph = nullptr;
@@ -241,6 +250,7 @@ extern "C" void neon_ctx_destroy(neon_ctx* ctx) {
   if (ctx->kc) (void)hipFree(ctx->kc);
   if (ctx->vc) (void)hipFree(ctx->vc);
   if (ctx->work) (void)hipFree(ctx->work);
+  if (ctx->pf) (void)hipFree(ctx->pf);
   delete ctx;
 }
 
@@ -612,6 +622,105 @@ static neon_status run_steps(neon_ctx* ctx, int n, hipStream_t st) {
   return NEON_OK;
 }
 
+// ---------------------------------------------------------------------------
+// batched prefill: all prompt rows of one sequence through every layer at
+// once (matrix-core GEMMs, grouped expert GEMMs, tiled causal attention),
+// filling that sequence's KV cache.  Scratch is sized for `rows` rows.
+// ---------------------------------------------------------------------------
+static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t st) {
+  if (ctx->pf && ctx->pf_rows >= rows) return NEON_OK;
+  const neon_config& c = ctx->cfg;
+  const size_t M = (size_t)((rows + 127) / 128) * 128;
+  const size_t H = c.hidden, I = c.intermediate, k = c.top_k, E = c.n_experts;
+  const size_t qkv_rows = (size_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+  const size_t qd = (size_t)c.n_heads * c.head_dim;
+  const size_t tiles = (size_t)moe_prefill_max_tiles((int)M, (int)k, (int)E);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+  const size_t o_h = take(M * H * 2), o_xn = take(M * H * 2), o_qkv = take(M * qkv_rows * 2),
+               o_q = take(M * qd * 2), o_ao = take(M * qd * 2), o_act = take(M * k * I * 2),
+               o_lg = take(M * E * 4), o_sc = take(M * k * 4), o_yb = take(M * k * H * 4),
+               o_idx = take(M * k * 4), o_lt = take(M * k * 4), o_ls = take(M * k * 4),
+               o_eo = take((E + 1) * 4), o_te = take(tiles * 4), o_tr = take(tiles * 4),
+               o_nt = take(4);
+  if (ctx->pf) {
+    HIPCHK(ctx, hipStreamSynchronize(st));  // earlier prefill work may still read it
+    (void)hipFree(ctx->pf);
+    ctx->pf = nullptr;
+    ctx->pf_rows = 0;
+  }
+  if (hipMalloc(&ctx->pf, off) != hipSuccess) {
+    ctx->pf = nullptr;
+    FAIL(ctx, NEON_ENOMEM, "hipMalloc of %zu prefill scratch bytes failed", off);
+  }
+  char* P = ctx->pf;
+  ctx->pf_h = (uint16_t*)(P + o_h); ctx->pf_xn = (uint16_t*)(P + o_xn);
+  ctx->pf_qkv = (uint16_t*)(P + o_qkv); ctx->pf_q = (uint16_t*)(P + o_q);
+  ctx->pf_ao = (uint16_t*)(P + o_ao); ctx->pf_act = (uint16_t*)(P + o_act);
+  ctx->pf_lg = (float*)(P + o_lg); ctx->pf_score = (float*)(P + o_sc);
+  ctx->pf_ybuf = (float*)(P + o_yb); ctx->pf_idx = (int32_t*)(P + o_idx);
+  ctx->pf_ltok = (int32_t*)(P + o_lt); ctx->pf_lslot = (int32_t*)(P + o_ls);
+  ctx->pf_eoff = (int32_t*)(P + o_eo); ctx->pf_tile_e = (int32_t*)(P + o_te);
+  ctx->pf_tile_r0 = (int32_t*)(P + o_tr); ctx->pf_ntiles = (int32_t*)(P + o_nt);
+  ctx->pf_rows = (int)M;
+  return NEON_OK;
+}
+
+// Rows 0 .. M-1 of sequence b (token ids already in ctx->tokens) through all
+// layers; their keys/values land in the KV cache.  The hidden states of these
+// rows are not needed afterwards (the last prompt token runs as a decode step).
+static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
+  const neon_config& c = ctx->cfg;
+  const int H = c.hidden, D = c.head_dim, Hq = c.n_heads, Hkv = c.n_kv_heads;
+  const int qkv_rows = (Hq + 2 * Hkv) * D;
+  launch_embed_rows(ctx->tokens + (size_t)b * ctx->tok_stride, M, ctx->embed, ctx->pf_h, H, st);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = ctx->layers[l];
+    const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
+    const size_t kvo = (size_t)l * ctx->kv_layer_elems + (size_t)b * Hkv * c.max_seq * D;
+    launch_rmsnorm(ctx->pf_h, w.attn_norm, ctx->pf_xn, M, H, c.rms_eps, st);
+    launch_gemm_bf16(ctx->pf_xn, H, w.wqkv, H, w.bqkv, ctx->pf_qkv, nullptr, qkv_rows, M,
+                     qkv_rows, H, 0, st);
+    launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv, c.max_seq,
+                        ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, st);
+    launch_attn_prefill(ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, w.sinks, ctx->pf_ao, M, Hq,
+                        Hkv, c.max_seq, sliding ? c.sliding_window : 0, st);
+    launch_gemm_bf16(ctx->pf_ao, Hq * D, w.wo, Hq * D, w.bo, ctx->pf_h, nullptr, H, M, H,
+                     Hq * D, 1, st);
+    launch_rmsnorm(ctx->pf_h, w.mlp_norm, ctx->pf_xn, M, H, c.rms_eps, st);
+    launch_gemm_bf16(ctx->pf_xn, H, w.router_w, H, w.router_b, nullptr, ctx->pf_lg,
+                     c.n_experts, M, c.n_experts, H, 2, st);
+    launch_topk(ctx->pf_lg, ctx->pf_idx, ctx->pf_score, M, c.n_experts, c.top_k, st);
+    MoePrefillArgs m;
+    m.idx = ctx->pf_idx; m.score = ctx->pf_score; m.xn = ctx->pf_xn; m.h = ctx->pf_h;
+    m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
+    m.dn_codes = w.dn_codes; m.dn_scales = w.dn_scales; m.dn_bias = w.dn_bias;
+    m.M = M; m.E = c.n_experts; m.H = H; m.I = c.intermediate; m.k = c.top_k;
+    m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
+    m.list_tok = ctx->pf_ltok; m.list_slot = ctx->pf_lslot; m.e_off = ctx->pf_eoff;
+    m.tile_e = ctx->pf_tile_e; m.tile_r0 = ctx->pf_tile_r0; m.n_tiles = ctx->pf_ntiles;
+    m.act = ctx->pf_act; m.ybuf = ctx->pf_ybuf;
+    launch_moe_prefill(m, st);
+  }
+}
+
+// The batched prompt pass is switched off: the first GPU process that ran its
+// expert-grouping, grouped-GEMM and attention kernels (all parity checks
+// passed) left the device unusable for the next process, and no cause has
+// been shown yet.  Until one is, selecting it is refused.
+static const bool kBatchedPrefillEnabled = false;
+
+extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
+  if (!ctx) return NEON_EINVAL;
+  if (mode != NEON_PREFILL_BATCHED && mode != NEON_PREFILL_STEPWISE)
+    FAIL(ctx, NEON_EINVAL, "neon_set_prefill_mode: unknown mode %d", mode);
+  if (mode == NEON_PREFILL_BATCHED && !kBatchedPrefillEnabled)
+    FAIL(ctx, NEON_ESTATE, "neon_set_prefill_mode: the batched prompt pass is switched off "
+                           "(a device loss after its first GPU run is not yet explained)");
+  ctx->prefill_mode = mode;
+  return NEON_OK;
+}
+
 extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
                                     int n_tokens, void* stream) {
   if (!ctx) return NEON_EINVAL;
@@ -639,6 +748,22 @@ extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch
   HIPCHK(ctx, hipStreamSynchronize(st));  // host staging buffers die here
   ctx->batch = batch;
   ctx->host_pos = 0;
+  if (ctx->prefill_mode == NEON_PREFILL_BATCHED && n_tokens > 1) {
+    // prompt rows 0 .. n-2 in one pass per sequence, then the last prompt
+    // token as an ordinary decode step (logits, first generated token)
+    const int M = n_tokens - 1;
+    neon_status s = ensure_prefill_scratch(ctx, M, st);
+    if (s != NEON_OK) return s;
+    for (int b = 0; b < batch; ++b) enqueue_prefill_rows(ctx, b, M, st);
+    HIPCHK(ctx, hipGetLastError());
+    std::vector<int32_t> pm(batch, M);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->pos, pm.data(), batch * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipStreamSynchronize(st));  // pm dies here
+    s = run_steps(ctx, 1, st);
+    if (s != NEON_OK) return s;
+    ctx->host_pos = n_tokens;
+    return NEON_OK;
+  }
   neon_status s = run_steps(ctx, n_tokens, st);
   if (s != NEON_OK) return s;
   ctx->host_pos = n_tokens;
@@ -919,4 +1044,77 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   (void)hipFreeAsync(scratch, st);
   if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
   return NEON_OK;
+}
+
+extern "C" neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
+                                      const uint16_t* bias, uint16_t* C, int M, int N,
+                                      int K, int accumulate, void* stream) {
+  if (!A || !W || !C) KFAIL(NEON_EINVAL, "neon_gemm_bf16: null pointer");
+  if (M < 1 || N < 1 || K < 32 || K % 32 || (int64_t)M * 128 > ((int64_t)1 << 31) ||
+      N > (1 << 24) || K > (1 << 20))
+    KFAIL(NEON_EINVAL, "neon_gemm_bf16: bad shape M=%d N=%d K=%d", M, N, K);
+  launch_gemm_bf16(A, K, W, K, bias, C, nullptr, N, M, N, K, accumulate ? 1 : 0, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
+                                        const float* score, const uint8_t* gu_codes,
+                                        const uint8_t* gu_scales, const uint16_t* gu_bias,
+                                        const uint8_t* dn_codes, const uint8_t* dn_scales,
+                                        const uint16_t* dn_bias, uint16_t* h, int M, int E,
+                                        int H, int I, int k, float alpha, float limit,
+                                        void* stream) {
+  if (!x || !idx || !score || !gu_codes || !gu_scales || !gu_bias || !dn_codes ||
+      !dn_scales || !dn_bias || !h)
+    KFAIL(NEON_EINVAL, "neon_moe_prefill: null pointer");
+  if (M < 1 || M > (1 << 20) || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < 32 ||
+      H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
+    KFAIL(NEON_EINVAL, "neon_moe_prefill: bad shape M=%d E=%d H=%d I=%d k=%d", M, E, H, I, k);
+  if (!kBatchedPrefillEnabled)
+    KFAIL(NEON_ESTATE, "neon_moe_prefill: switched off (a device loss after its first GPU "
+                       "run is not yet explained)");
+  // idx is device data: every entry must lie in [0, E).
+  hipStream_t st = S(stream);
+  const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
+  size_t off = 0;
+  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
+  const size_t o_yb = take(pairs * H * 4), o_act = take(pairs * I * 2), o_lt = take(pairs * 4),
+               o_ls = take(pairs * 4), o_eo = take((E + 1) * 4), o_te = take(tiles * 4),
+               o_tr = take(tiles * 4), o_nt = take(16);
+  char* scratch = nullptr;
+  if (hipMallocAsync((void**)&scratch, off, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_moe_prefill: scratch allocation failed");
+  MoePrefillArgs m;
+  m.idx = idx; m.score = score; m.xn = x; m.h = h;
+  m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
+  m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
+  m.M = M; m.E = E; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
+  m.ybuf = (float*)(scratch + o_yb); m.act = (uint16_t*)(scratch + o_act);
+  m.list_tok = (int32_t*)(scratch + o_lt); m.list_slot = (int32_t*)(scratch + o_ls);
+  m.e_off = (int32_t*)(scratch + o_eo); m.tile_e = (int32_t*)(scratch + o_te);
+  m.tile_r0 = (int32_t*)(scratch + o_tr); m.n_tiles = (int32_t*)(scratch + o_nt);
+  launch_moe_prefill(m, st);
+  hipError_t e = hipGetLastError();
+  (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_moe_prefill: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
+                                         const uint16_t* v_cache, const uint16_t* sinks,
+                                         uint16_t* out, int M, int Hq, int Hkv, int D,
+                                         int T_max, int window, void* stream) {
+  if (!q || !k_cache || !v_cache || !sinks || !out)
+    KFAIL(NEON_EINVAL, "neon_attn_prefill: null pointer");
+  if (D != 64 || M < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv || T_max < M || window < 0 ||
+      (M + 63) / 64 > 65535)
+    KFAIL(NEON_EINVAL, "neon_attn_prefill: bad shape");
+  const int G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    KFAIL(NEON_EINVAL, "neon_attn_prefill: Hq/Hkv must be 1, 2, 4 or 8");
+  if (!kBatchedPrefillEnabled)
+    KFAIL(NEON_ESTATE, "neon_attn_prefill: switched off (a device loss after its first GPU "
+                       "run is not yet explained)");
+  launch_attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, T_max, window, S(stream));
+  KLAUNCHED();
 }

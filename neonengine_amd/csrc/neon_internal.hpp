@@ -103,5 +103,42 @@ struct AttnArgs {
 void launch_attn(const AttnArgs& a, hipStream_t st);
 // number of key splits used for a cache of T_max rows (window 0 = full layer)
 int attn_splits(int T_max, int window);
+// top-k + softmax of router logits lg [B][E] (one wave per row)
+void launch_topk(const float* lg, int32_t* idx, float* score, int B, int E, int k,
+                 hipStream_t st);
+
+// ---- prefill (neon_prefill.hip): M prompt rows at once on the matrix cores --
+void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
+                       uint16_t* h, int H, hipStream_t st);
+// C[M][N] = A[M][K] W[N][K]^T + bias; mode 0: bf16 store, 1: C = bf16(C +
+// bf16(.)) (residual in place), 2: fp32 into Cf.  K % 32 == 0.
+void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
+                      const uint16_t* bias, uint16_t* C, float* Cf, int ldc, int M,
+                      int N, int K, int mode, hipStream_t st);
+void launch_rope_kv_rows(const uint16_t* qkv, int q_stride, const float* cos_t,
+                         const float* sin_t, int M, int Hq, int Hkv, int T_max,
+                         uint16_t* q_out, uint16_t* kc, uint16_t* vc, hipStream_t st);
+void launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                         const uint16_t* sinks, uint16_t* out, int M, int Hq, int Hkv,
+                         int T_max, int window, hipStream_t st);
+struct MoePrefillArgs {
+  const int32_t* idx;        // [M][k] chosen experts
+  const float* score;        // [M][k] weights
+  const uint16_t* xn;        // [M][H] normalised input
+  uint16_t* h;               // [M][H] residual stream, updated in place
+  const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
+  const uint16_t *gu_bias, *dn_bias;
+  int M, E, H, I, k;
+  float alpha, limit;
+  // scratch
+  int32_t *list_tok, *list_slot;  // [M k]
+  int32_t* e_off;                 // [E + 1]
+  int32_t *tile_e, *tile_r0;      // [moe_prefill_max_tiles]
+  int32_t* n_tiles;               // [1]
+  uint16_t* act;                  // [M k][I]
+  float* ybuf;                    // [M][k][H]
+};
+int moe_prefill_max_tiles(int M, int k, int E);
+void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st);
 
 }  // namespace neon

@@ -970,6 +970,11 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
   if (lane < k) { idx[b * k + lane] = t.id[lane]; score[b * k + lane] = t.sc[lane]; }
 }
 
+void launch_topk(const float* lg, int32_t* idx, float* score, int B, int E, int k,
+                 hipStream_t st) {
+  hipLaunchKernelGGL(k_topk, dim3(B), dim3(64), 0, st, lg, idx, score, E, k);
+}
+
 void launch_router(const RouterArgs& a, hipStream_t st) {
   const int P = (a.H / 8 + 63) / 64;
   dim3 grid(a.E, a.B);

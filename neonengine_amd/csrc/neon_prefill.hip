@@ -1,0 +1,566 @@
+// neon_prefill.hip -- batched prompt processing (prefill) on gfx950.
+//
+// A prompt of M tokens runs every layer over all M rows at once, so the
+// projections and the experts become dense contractions on the matrix cores
+// (v_mfma_f32_32x32x16_bf16, fp32 accumulate):
+//   - bf16 GEMM  C[M][N] = A[M][K] W[N][K]^T (QKV, O + residual, router);
+//   - grouped MXFP4 GEMM over the tokens routed to each expert, with the
+//     expert rows dequantised exactly to bf16 in LDS (E2M1 x 2^(s-127) is a
+//     bf16 value), SwiGLU fused into the gate_up epilogue;
+//   - tiled causal sink attention over the KV cache the prefill fills.
+// The maths is the decode path's (HFM:82-112, 235-263, 347-376); the
+// accumulation order of a matrix-core dot product differs from the decode
+// kernels' canonical fp32 chain, so prefill agrees with it within fp32
+// rounding, not bit for bit.
+#include "neon_common.hpp"
+#include "neon_internal.hpp"
+
+namespace neon {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // staging (no struct copies)
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void unpack8(const uint4& v, float* o) {
+  o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
+  o[4] = bf_lo(v.z); o[5] = bf_hi(v.z); o[6] = bf_lo(v.w); o[7] = bf_hi(v.w);
+}
+
+// ===========================================================================
+// Row gather: h[t] = embed[ids[t]]
+// ===========================================================================
+__global__ void k_embed_rows(const int32_t* __restrict__ ids,
+                             const uint16_t* __restrict__ embed,
+                             uint16_t* __restrict__ h, int H) {
+  const int t = blockIdx.x;
+  const uint4* src = reinterpret_cast<const uint4*>(embed + (size_t)ids[t] * H);
+  uint4* dst = reinterpret_cast<uint4*>(h + (size_t)t * H);
+  for (int u = threadIdx.x; u < H / 8; u += blockDim.x) dst[u] = src[u];
+}
+
+void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
+                       uint16_t* h, int H, hipStream_t st) {
+  hipLaunchKernelGGL(k_embed_rows, dim3(M), dim3(256), 0, st, ids, embed, h, H);
+}
+
+// ===========================================================================
+// Matrix-core GEMM.  Block tile 128 x 128, K step 32, 4 waves in 2 x 2, each
+// wave a 64 x 64 tile of 2 x 2 MFMA 32x32x16 blocks.  Both operands are
+// "row of the matrix, 8 consecutive k" per lane (lane l: row l % 32, k
+// 8 (l / 32) .. + 8), so A [M][K] and W [N][K] are staged the same way:
+// global -> registers (next step) -> LDS (double buffer, row stride 40 bf16
+// so rows spread over the banks) -> ds_read_b128 operands.
+//
+// Rows past M or N read a clamped valid row and are never stored.  K must be
+// a multiple of 32.  With FP4, W is an MXFP4 matrix (codes [N][K/2], scales
+// [N][K/32]); one K step is exactly one scale block per row, dequantised as
+// E2M1 (v_cvt_scalef32_pk_f32_fp4, exact) x 2^(s-127) (ldexp, exact) and
+// rounded to bf16 (exact: every such value is a bf16 value or overflows).
+//
+// Grouped (MoE) form: blockIdx.y is a tile of the expert-sorted row list;
+// tile_e / tile_r0 give its expert and first list row, and rows past the
+// expert's count are masked.  The A row of list row i is a_rows[i] (token)
+// when a_rows is given, else i itself.
+// ===========================================================================
+constexpr int kGM = 128, kGN = 128, kGK = 32, kGS = 40;  // tile, LDS row stride
+
+enum {
+  GEMM_STORE = 0,    // C = bf16(acc + bias)
+  GEMM_RESID = 1,    // C = bf16(C + bf16(acc + bias))  (C holds the residual)
+  GEMM_F32 = 2,      // Cf = acc + bias
+  GEMM_SWIGLU = 3,   // act[i][j] = bf16(swiglu(acc_2j + b_2j, acc_2j+1 + b_2j+1))
+  GEMM_SCATTER = 4   // ybuf[token][slot][n] = acc + bias (fp32)
+};
+
+struct GemmParams {
+  const uint16_t* A; int lda;
+  const uint16_t* W; int ldw;          // bf16 weights [N][K]
+  const uint8_t* codes;                // MXFP4 weights (FP4): [E][N][K/2]
+  const uint8_t* scales;               // [E][N][K/32]
+  const uint16_t* bias;                // [E][N] (grouped) or [N]; may be NULL
+  uint16_t* C; float* Cf; int ldc;
+  int M, N, K;
+  // grouped form
+  const int32_t* tile_e; const int32_t* tile_r0; const int32_t* n_tiles;
+  const int32_t* e_off;                // [E+1] list offsets
+  const int32_t* list_tok; const int32_t* list_slot;
+  const int32_t* a_rows;               // token of each list row (gate_up), or NULL
+  float* ybuf; int topk;
+  float alpha, limit;
+};
+
+__device__ __forceinline__ float swiglu_clamp_p(float g, float u, float alpha, float limit) {
+  g = g > limit ? limit : g;
+  u = u > limit ? limit : (u < -limit ? -limit : u);
+  const float e = neon_expf(-__fmul_rn(g, alpha));
+  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+  return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
+}
+
+// 16 E2M1 values of 8 code bytes, times 2^(s - 127), as 16 bf16 (two uint4)
+__device__ __forceinline__ void fp4x16_to_bf16(u32x2_t c, uint32_t s, u32x4_t& lo, u32x4_t& hi) {
+  const int ex = (int)s - 127;
+  const bool nan = s == 0xFFu;
+  uint32_t o[8];
+  const uint32_t w[2] = {c.x, c.y};
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      float2_v v;
+      switch (b) {
+        case 0: v = fp4x2_to_f32<0>(w[q]); break;
+        case 1: v = fp4x2_to_f32<1>(w[q]); break;
+        case 2: v = fp4x2_to_f32<2>(w[q]); break;
+        default: v = fp4x2_to_f32<3>(w[q]); break;
+      }
+      float a = __builtin_amdgcn_ldexpf(v.x, ex), bb = __builtin_amdgcn_ldexpf(v.y, ex);
+      a = nan ? __builtin_nanf("") : a;
+      bb = nan ? __builtin_nanf("") : bb;
+      o[q * 4 + b] = pack_bf2(a, bb);
+    }
+  }
+  lo = u32x4_t{o[0], o[1], o[2], o[3]};
+  hi = u32x4_t{o[4], o[5], o[6], o[7]};
+}
+
+template <int MODE, bool FP4, bool GROUPED>
+__global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
+  __shared__ __align__(16) uint16_t As[2][kGM * kGS];
+  __shared__ __align__(16) uint16_t Ws[2][kGN * kGS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * kGN;
+  int e = 0, r0, rows;  // rows: valid A rows of this tile (from r0)
+  if (GROUPED) {
+    if ((int)blockIdx.y >= *p.n_tiles) return;  // uniform for the block
+    e = p.tile_e[blockIdx.y];
+    const int lo = p.e_off[e];
+    r0 = lo + p.tile_r0[blockIdx.y];
+    rows = min(kGM, p.e_off[e + 1] - r0);
+  } else {
+    r0 = blockIdx.y * kGM;
+    rows = min(kGM, p.M - r0);
+  }
+  const int K = p.K;
+  // this thread's staging rows: A/W chunk c = tid + 256 i (i = 0, 1):
+  // row c >> 2, k (c & 3) * 8; FP4 W: row tid >> 1, k half (tid & 1) * 16
+  const uint16_t* arow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (tid + 256 * i) >> 2;
+    const int lr = r0 + min(r, rows - 1);
+    const int ar = GROUPED && p.a_rows ? p.a_rows[lr] : lr;
+    arow[i] = p.A + (size_t)ar * p.lda + ((tid + 256 * i) & 3) * 8;
+  }
+  const uint16_t* wrow[2] = {nullptr, nullptr};
+  const uint8_t* crow = nullptr;
+  const uint8_t* srow = nullptr;
+  if (FP4) {
+    const int r = tid >> 1;
+    const size_t nr = (size_t)e * p.N + min(n0 + r, p.N - 1);
+    crow = p.codes + nr * (K / 2) + (tid & 1) * 8;
+    srow = p.scales + nr * (K / 32);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = (tid + 256 * i) >> 2;
+      wrow[i] = p.W + (size_t)min(n0 + r, p.N - 1) * p.ldw + ((tid + 256 * i) & 3) * 8;
+    }
+  }
+  u32x4_t ra0, ra1, rw0 = {}, rw1 = {};
+  u32x2_t rc = {};
+  uint32_t rs = 127;
+  // k step 0
+  ra0 = *reinterpret_cast<const u32x4_t*>(arow[0]);
+  ra1 = *reinterpret_cast<const u32x4_t*>(arow[1]);
+  if (FP4) {
+    rc = *reinterpret_cast<const u32x2_t*>(crow);
+    rs = srow[0];
+  } else {
+    rw0 = *reinterpret_cast<const u32x4_t*>(wrow[0]);
+    rw1 = *reinterpret_cast<const u32x4_t*>(wrow[1]);
+  }
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+
+  const int nk = K / kGK;
+  // registers -> LDS buffer `buf`
+#define GEMM_STAGE(buf)                                                                 \
+  do {                                                                                  \
+    *reinterpret_cast<u32x4_t*>(&As[buf][(tid >> 2) * kGS + (tid & 3) * 8]) = ra0;      \
+    *reinterpret_cast<u32x4_t*>(&As[buf][((tid + 256) >> 2) * kGS + (tid & 3) * 8]) = ra1; \
+    if (FP4) {                                                                          \
+      u32x4_t lo, hi;                                                                   \
+      fp4x16_to_bf16(rc, rs, lo, hi);                                                   \
+      uint16_t* d = &Ws[buf][(tid >> 1) * kGS + (tid & 1) * 16];                        \
+      *reinterpret_cast<u32x4_t*>(d) = lo;                                              \
+      *reinterpret_cast<u32x4_t*>(d + 8) = hi;                                          \
+    } else {                                                                            \
+      *reinterpret_cast<u32x4_t*>(&Ws[buf][(tid >> 2) * kGS + (tid & 3) * 8]) = rw0;    \
+      *reinterpret_cast<u32x4_t*>(&Ws[buf][((tid + 256) >> 2) * kGS + (tid & 3) * 8]) = rw1; \
+    }                                                                                   \
+  } while (0)
+  GEMM_STAGE(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {  // next step's loads go out before this step's math
+      const int ko = (kt + 1) * kGK;
+      ra0 = *reinterpret_cast<const u32x4_t*>(arow[0] + ko);
+      ra1 = *reinterpret_cast<const u32x4_t*>(arow[1] + ko);
+      if (FP4) {
+        rc = *reinterpret_cast<const u32x2_t*>(crow + ko / 2);
+        rs = srow[kt + 1];
+      } else {
+        rw0 = *reinterpret_cast<const u32x4_t*>(wrow[0] + ko);
+        rw1 = *reinterpret_cast<const u32x4_t*>(wrow[1] + ko);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8_t af[2], bf[2];
+#pragma unroll
+      for (int im = 0; im < 2; ++im)
+        af[im] = *reinterpret_cast<const bf16x8_t*>(
+            &As[cur][(wm * 64 + im * 32 + (lane & 31)) * kGS + ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int in = 0; in < 2; ++in)
+        bf[in] = *reinterpret_cast<const bf16x8_t*>(
+            &Ws[cur][(wn * 64 + in * 32 + (lane & 31)) * kGS + ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int im = 0; im < 2; ++im)
+#pragma unroll
+        for (int in = 0; in < 2; ++in)
+          acc[im][in] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[im], bf[in], acc[im][in], 0, 0, 0);
+    }
+    if (kt + 1 < nk) GEMM_STAGE(cur ^ 1);
+    __syncthreads();
+  }
+#undef GEMM_STAGE
+
+  // ---- epilogue: acc[im][in][i] is row 8 (i/4) + 4 (lane/32) + i%4, col lane%32
+  const uint16_t* bias = p.bias ? p.bias + (GROUPED ? (size_t)e * p.N : 0) : nullptr;
+#pragma unroll
+  for (int im = 0; im < 2; ++im)
+#pragma unroll
+    for (int in = 0; in < 2; ++in) {
+      const int col = n0 + wn * 64 + in * 32 + (lane & 31);
+      const float bcol = (bias && col < p.N) ? bf2f(bias[col]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = wm * 64 + im * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const float v = bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
+        if (MODE == GEMM_SWIGLU) {
+          // gate (even column) and up (odd column) sit in adjacent lanes
+          const float u = __shfl_xor(v, 1, 64);
+          if ((lane & 1) == 0 && r < rows && col + 1 < p.N)
+            p.C[(size_t)(r0 + r) * p.ldc + col / 2] = f2bf(swiglu_clamp_p(v, u, p.alpha, p.limit));
+          continue;
+        }
+        if (r >= rows || col >= p.N) continue;
+        const size_t gr = (size_t)(r0 + r);
+        if (MODE == GEMM_STORE) {
+          p.C[gr * p.ldc + col] = f2bf(v);
+        } else if (MODE == GEMM_RESID) {
+          uint16_t* c = p.C + gr * p.ldc + col;
+          *c = f2bf(__fadd_rn(bf2f(*c), bf2f(f2bf(v))));
+        } else if (MODE == GEMM_F32) {
+          p.Cf[gr * p.ldc + col] = v;
+        } else {  // GEMM_SCATTER
+          const int t = p.list_tok[gr], s = p.list_slot[gr];
+          p.ybuf[((size_t)t * p.topk + s) * p.N + col] = v;
+        }
+      }
+    }
+}
+
+void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
+                      const uint16_t* bias, uint16_t* C, float* Cf, int ldc, int M,
+                      int N, int K, int mode, hipStream_t st) {
+  GemmParams p{};
+  p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.bias = bias; p.C = C; p.Cf = Cf;
+  p.ldc = ldc; p.M = M; p.N = N; p.K = K;
+  dim3 grid((N + kGN - 1) / kGN, (M + kGM - 1) / kGM);
+  switch (mode) {
+    case GEMM_STORE: hipLaunchKernelGGL((k_gemm<GEMM_STORE, false, false>), grid, dim3(256), 0, st, p); break;
+    case GEMM_RESID: hipLaunchKernelGGL((k_gemm<GEMM_RESID, false, false>), grid, dim3(256), 0, st, p); break;
+    default: hipLaunchKernelGGL((k_gemm<GEMM_F32, false, false>), grid, dim3(256), 0, st, p); break;
+  }
+}
+
+// ===========================================================================
+// Expert grouping: the (token, slot) pairs of idx [M][k] sorted by expert,
+// stable in (token, slot) order, plus the 128-row GEMM tiles of each
+// expert's run.  One block of 1024 threads; for each expert the block counts
+// its pairs in each thread's consecutive chunk and places them with a block
+// prefix sum.
+// ===========================================================================
+__device__ __forceinline__ int block_excl_scan_1024(int v, int* lds) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) lds[wave] = x;
+  __syncthreads();
+  if (tid == 0) {
+    int s = 0;
+    for (int w = 0; w < 16; ++w) { const int t = lds[w]; lds[w] = s; s += t; }
+    lds[16] = s;
+  }
+  __syncthreads();
+  const int r = lds[wave] + x - v;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(1024) void k_moe_group(
+    const int32_t* __restrict__ idx, int n_pairs, int k, int E,
+    int32_t* __restrict__ list_tok, int32_t* __restrict__ list_slot,
+    int32_t* __restrict__ e_off, int32_t* __restrict__ tile_e,
+    int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles) {
+  __shared__ int scan_lds[17];
+  __shared__ int base;
+  const int tid = threadIdx.x;
+  const int per = (n_pairs + 1023) / 1024;
+  const int p0 = tid * per, p1 = min(p0 + per, n_pairs);
+  if (tid == 0) base = 0;
+  __syncthreads();
+  for (int e = 0; e < E; ++e) {
+    int c = 0;
+    for (int q = p0; q < p1; ++q) c += idx[q] == e;
+    const int pos = block_excl_scan_1024(c, scan_lds);
+    const int tot = scan_lds[16];
+    const int b0 = base;
+    if (tid == 0) e_off[e] = b0;
+    int o = b0 + pos;
+    for (int q = p0; q < p1; ++q)
+      if (idx[q] == e) { list_tok[o] = q / k; list_slot[o] = q % k; ++o; }
+    __syncthreads();
+    if (tid == 0) base = b0 + tot;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    e_off[E] = base;
+    int t = 0;
+    for (int e = 0; e < E; ++e) {
+      const int cnt = e_off[e + 1] - e_off[e];
+      for (int r = 0; r < cnt; r += kGM) { tile_e[t] = e; tile_r0[t] = r; ++t; }
+    }
+    *n_tiles = t;
+  }
+}
+
+// out[t] = bf16(residual[t] + bf16(sum_s score[t][s] * y[t][s]))  in slot
+// order with fmaf, as the decode combine (HFM:111-112).
+__global__ void k_moe_combine(const float* __restrict__ ybuf,
+                              const float* __restrict__ score, int k, int H,
+                              uint16_t* __restrict__ h) {
+  const int t = blockIdx.x;
+  for (int n = threadIdx.x; n < H; n += blockDim.x) {
+    float y = 0.0f;
+    for (int s = 0; s < k; ++s)
+      y = __builtin_fmaf(score[t * k + s], ybuf[((size_t)t * k + s) * H + n], y);
+    uint16_t* c = h + (size_t)t * H + n;
+    *c = f2bf(__fadd_rn(bf2f(*c), bf2f(f2bf(y))));
+  }
+}
+
+// MoE layer over M tokens: experts from idx/score [M][k], input xn [M][H],
+// residual stream h [M][H] updated in place.  Scratch: list_tok/list_slot
+// [M k], e_off [E+1], tile_e/tile_r0 [max_tiles], n_tiles [1], act [M k][I]
+// bf16, ybuf [M][k][H] fp32.
+void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
+  const int n_pairs = a.M * a.k;
+  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.E,
+                     a.list_tok, a.list_slot, a.e_off, a.tile_e, a.tile_r0, a.n_tiles);
+  const int max_tiles = moe_prefill_max_tiles(a.M, a.k, a.E);
+  GemmParams p{};
+  p.tile_e = a.tile_e; p.tile_r0 = a.tile_r0; p.n_tiles = a.n_tiles; p.e_off = a.e_off;
+  p.list_tok = a.list_tok; p.list_slot = a.list_slot; p.topk = a.k;
+  p.alpha = a.alpha; p.limit = a.limit;
+  // gate_up + SwiGLU: A = xn rows of the listed tokens, N = 2 I, out act [list][I]
+  p.A = a.xn; p.lda = a.H; p.a_rows = a.list_tok;
+  p.codes = a.gu_codes; p.scales = a.gu_scales; p.bias = a.gu_bias;
+  p.C = a.act; p.ldc = a.I; p.N = 2 * a.I; p.K = a.H;
+  hipLaunchKernelGGL((k_gemm<GEMM_SWIGLU, true, true>), dim3((2 * a.I + kGN - 1) / kGN, max_tiles),
+                     dim3(256), 0, st, p);
+  // down: A = act rows in list order, N = H, out ybuf[token][slot]
+  p.A = a.act; p.lda = a.I; p.a_rows = nullptr;
+  p.codes = a.dn_codes; p.scales = a.dn_scales; p.bias = a.dn_bias;
+  p.ybuf = a.ybuf; p.N = a.H; p.K = a.I; p.C = nullptr;
+  hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), dim3((a.H + kGN - 1) / kGN, max_tiles),
+                     dim3(256), 0, st, p);
+  hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.k, a.H, a.h);
+}
+
+int moe_prefill_max_tiles(int M, int k, int E) {
+  return (M * k + kGM - 1) / kGM + E;
+}
+
+// ===========================================================================
+// RoPE + KV append for M prompt rows (positions 0 .. M-1): q heads rotated
+// into q_out [M][Hq][64] (bf16, as the decode kernel rounds them), k heads
+// rotated and v copied into the cache rows [Hkv][T_max][64].
+// ===========================================================================
+__global__ void k_rope_kv_rows(const uint16_t* __restrict__ qkv, int q_stride,
+                               const float* __restrict__ cos_t,
+                               const float* __restrict__ sin_t, int Hq, int Hkv,
+                               int T_max, uint16_t* __restrict__ q_out,
+                               uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
+  const int t = blockIdx.x;
+  const int half = 32;
+  const uint16_t* row = qkv + (size_t)t * q_stride;
+  const float* cr = cos_t + (size_t)t * half;
+  const float* sr = sin_t + (size_t)t * half;
+  for (int i = threadIdx.x; i < (Hq + Hkv) * half; i += blockDim.x) {
+    const int hh = i / half, f = i % half;
+    const uint16_t* x = row + (size_t)hh * 64;
+    float o1, o2;
+    const float x1 = bf2f(x[f]), x2 = bf2f(x[f + half]);
+    o1 = __fsub_rn(__fmul_rn(x1, cr[f]), __fmul_rn(x2, sr[f]));
+    o2 = __fadd_rn(__fmul_rn(x2, cr[f]), __fmul_rn(x1, sr[f]));
+    uint16_t* dst = hh < Hq ? q_out + ((size_t)t * Hq + hh) * 64
+                            : kc + ((size_t)(hh - Hq) * T_max + t) * 64;
+    dst[f] = f2bf(o1);
+    dst[f + half] = f2bf(o2);
+  }
+  for (int i = threadIdx.x; i < Hkv * 64; i += blockDim.x) {
+    const int g = i / 64, d = i % 64;
+    vc[((size_t)g * T_max + t) * 64 + d] = row[(size_t)(Hq + Hkv + g) * 64 + d];
+  }
+}
+
+void launch_rope_kv_rows(const uint16_t* qkv, int q_stride, const float* cos_t,
+                         const float* sin_t, int M, int Hq, int Hkv, int T_max,
+                         uint16_t* q_out, uint16_t* kc, uint16_t* vc, hipStream_t st) {
+  hipLaunchKernelGGL(k_rope_kv_rows, dim3(M), dim3(256), 0, st, qkv, q_stride, cos_t,
+                     sin_t, Hq, Hkv, T_max, q_out, kc, vc);
+}
+
+// ===========================================================================
+// Causal sink attention over a prompt (HFM:235-263).  grid (Hkv, ceil(M/64)),
+// block 64 G: wave w is q head g G + w, lane l is query row 64 blockIdx.y + l.
+// K/V tiles of 64 keys are staged once per block in LDS as fp32 and read by
+// all lanes at the same address (broadcast).  Keys go 16 at a time through an
+// online softmax (scores x 1/8, HFM:277); the sink joins the denominator at
+// the end.  Sliding layers see keys (t - window, t].
+// ===========================================================================
+__global__ __launch_bounds__(512) void k_attn_prefill(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const uint16_t* __restrict__ sinks,
+    uint16_t* __restrict__ out, int M, int Hq, int Hkv, int T_max, int window) {
+  __shared__ __align__(16) float ks[64 * 64];
+  __shared__ __align__(16) float vs[64 * 64];
+  const int g = blockIdx.x, G = Hq / Hkv;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = g * G + w;
+  const int t0 = blockIdx.y * 64;
+  const int t = min(t0 + lane, M - 1);
+  const int lo_t = window > 0 ? max(0, t - window + 1) : 0;
+  float qr[64];
+  {
+    const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)t * Hq + h) * 64);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) unpack8(qv[u], &qr[8 * u]);
+  }
+  float o[64];
+#pragma unroll
+  for (int d = 0; d < 64; ++d) o[d] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const int hi_blk = min(M - 1, t0 + 63);
+  const int lo_blk = window > 0 ? max(0, t0 - window + 1) : 0;
+  const uint16_t* kg = kc + (size_t)g * T_max * 64;
+  const uint16_t* vg = vc + (size_t)g * T_max * 64;
+  for (int j0 = (lo_blk / 64) * 64; j0 <= hi_blk; j0 += 64) {
+    __syncthreads();  // the previous tile is consumed
+    for (int c = threadIdx.x; c < 64 * 8; c += blockDim.x) {
+      const int key = min(j0 + (c >> 3), T_max - 1), dq = (c & 7) * 8;
+      const uint4 kv = *reinterpret_cast<const uint4*>(kg + (size_t)key * 64 + dq);
+      const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * 64 + dq);
+      float f[8];
+      unpack8(kv, f);
+      *reinterpret_cast<float4*>(&ks[(c >> 3) * 64 + dq]) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4*>(&ks[(c >> 3) * 64 + dq + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+      unpack8(vv, f);
+      *reinterpret_cast<float4*>(&vs[(c >> 3) * 64 + dq]) = make_float4(f[0], f[1], f[2], f[3]);
+      *reinterpret_cast<float4*>(&vs[(c >> 3) * 64 + dq + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+    }
+    __syncthreads();
+    for (int jg = 0; jg < 64; jg += 16) {
+      float s[16];
+      float mt = m;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = jg + jj, key = j0 + j;
+        const float4* kr = reinterpret_cast<const float4*>(&ks[j * 64]);
+        float a = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < 16; ++d4) {
+          const float4 kk = kr[d4];
+          a = __builtin_fmaf(qr[4 * d4], kk.x, a);
+          a = __builtin_fmaf(qr[4 * d4 + 1], kk.y, a);
+          a = __builtin_fmaf(qr[4 * d4 + 2], kk.z, a);
+          a = __builtin_fmaf(qr[4 * d4 + 3], kk.w, a);
+        }
+        const bool valid = key >= lo_t && key <= t;
+        s[jj] = valid ? __fmul_rn(a, 0.125f) : -INFINITY;
+        mt = fmaxf(mt, s[jj]);
+      }
+      if (mt == -INFINITY) continue;  // no valid key for this lane yet
+      const float sc = __expf(m - mt);  // m = -inf -> 0
+      l *= sc;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) o[d] *= sc;
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const float pj = __expf(s[jj] - mt);
+        l += pj;
+        const float4* vr = reinterpret_cast<const float4*>(&vs[(jg + jj) * 64]);
+#pragma unroll
+        for (int d4 = 0; d4 < 16; ++d4) {
+          const float4 vv = vr[d4];
+          o[4 * d4] = __builtin_fmaf(pj, vv.x, o[4 * d4]);
+          o[4 * d4 + 1] = __builtin_fmaf(pj, vv.y, o[4 * d4 + 1]);
+          o[4 * d4 + 2] = __builtin_fmaf(pj, vv.z, o[4 * d4 + 2]);
+          o[4 * d4 + 3] = __builtin_fmaf(pj, vv.w, o[4 * d4 + 3]);
+        }
+      }
+      m = mt;
+    }
+  }
+  const float sk = bf2f(sinks[h]);
+  const float mt = fmaxf(m, sk);
+  const float sc = __expf(m - mt);
+  const float inv = 1.0f / (l * sc + __expf(sk - mt));
+  if (t0 + lane < M) {
+    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)t * Hq * 64 + (size_t)h * 64);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t wv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wv[j] = pack_bf2(o[8 * u + 2 * j] * sc * inv, o[8 * u + 2 * j + 1] * sc * inv);
+      dst[u] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+    }
+  }
+}
+
+void launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                         const uint16_t* sinks, uint16_t* out, int M, int Hq, int Hkv,
+                         int T_max, int window, hipStream_t st) {
+  dim3 grid(Hkv, (M + 63) / 64);
+  hipLaunchKernelGGL(k_attn_prefill, grid, dim3(64 * (Hq / Hkv)), 0, st, q, kc, vc, sinks,
+                     out, M, Hq, Hkv, T_max, window);
+}
+
+}  // namespace neon

@@ -85,6 +85,16 @@ def test_kernel_entry_points_validate_on_host():
                             None) == ne.NEON_EINVAL
     assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
     assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 5, 64, 64, 0, None) == ne.NEON_EINVAL   # Hq % Hkv
+    assert L.neon_gemm_bf16(None, p, None, p, 8, 8, 64, 0, None) == ne.NEON_EINVAL
+    assert L.neon_gemm_bf16(p, p, None, p, 8, 8, 48, 0, None) == ne.NEON_EINVAL     # K % 32
+    assert L.neon_gemm_bf16(p, p, None, p, 0, 8, 64, 0, None) == ne.NEON_EINVAL
+    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2880, 0, 1.702, 7.0,
+                              None) == ne.NEON_EINVAL                              # k = 0
+    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2872, 4, 1.702, 7.0,
+                              None) == ne.NEON_EINVAL                              # I % 32
+    assert L.neon_attn_prefill(p, p, p, p, p, 16, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
+    assert L.neon_attn_prefill(p, p, p, p, p, 65, 64, 8, 64, 64, 0, None) == ne.NEON_EINVAL   # T_max < M
+    assert L.neon_set_prefill_mode(None, 0) == ne.NEON_EINVAL
     assert L.neon_mxfp4_dequant(None, p, 1, p, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_dequant(p, p, 0, p, None) == ne.NEON_OK  # empty is a no-op
     assert b"K" in L.neon_last_error(None) or L.neon_last_error(None)

@@ -2,6 +2,8 @@
 oracle: bit-identical random-init weights, identical greedy token ids for 64
 steps, and logits that are bit-identical (the bar north_star sets is 2e-2
 relative max error on bf16 logits; the canonical fp32 order gives equality).
+The prompt runs stepwise here (every token through the decode kernels); the
+batched matrix-core prompt pass is checked in test_gpu_prefill.py.
 """
 import sys
 
@@ -62,6 +64,7 @@ def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
     m.close()
     # margins[b, t]: top-2 gap of the logits that produced generated token t
     margins = np.stack([np.diff(np.sort(lg, axis=1)[:, -2:], axis=1)[:, 0] for lg in o_logits], 1)
+    eng.set_prefill_mode(ne.PREFILL_STEPWISE)  # every prompt token on the exact decode path
     eng.prefill(prompt)
     g_first_logits = eng.read_logits()
     eng.decode(n_steps)

@@ -1,0 +1,208 @@
+"""GPU checks of the batched prefill: matrix-core GEMMs, grouped MXFP4 expert
+GEMMs and the tiled causal sink attention, then the whole prompt pass.
+
+The matrix cores accumulate in their own order, so unlike the decode kernels
+these are not bit-identical to the canonical oracle.  The bars:
+  - GEMM: within one bf16 rounding of the fp64 product plus fp32-accumulation
+    slack (2^-17 of the sum of |terms|), per element;
+  - experts and attention: the fp32 results of the canonical oracle within a
+    stated relative bound (one bf16 rounding of the intermediate activations
+    can differ, and the fast exp of the prefill attention);
+  - whole prompt: north_star's 2e-2 relative bound on the logits, and the same
+    greedy ids as the exact stepwise path wherever the reference's top-2
+    margin exceeds that bound.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import neonengine_amd as ne
+from tests.gpu_util import bf16_err_ok, empty_dev, to_dev, to_host, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+# The first GPU process that ran the expert-grouping / grouped-GEMM /
+# prompt-attention kernels passed every check here, yet the next process on
+# that box found no device.  No cause has been shown, so those kernels are
+# switched off in the library (their entry points return NEON_ESTATE) and
+# their tests are skipped; the plain GEMM ran alone in a process that left the
+# device healthy and stays on.
+OFF = pytest.mark.skip(reason="batched prompt pass switched off: a device loss followed its "
+                              "first GPU run; cause not yet shown")
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("M,N,K", [(2047, 5120, 2880), (300, 2880, 4096), (5, 32, 2880),
+                                   (129, 200, 64)])
+def test_gemm_bf16(orc, M, N, K):
+    A = orc.fill_bf16(0, 31, M * K, 0.0, 1.0)
+    W = orc.fill_bf16(0, 32, N * K, 0.0, 0.02)
+    bias = orc.fill_bf16(0, 33, N, 0.0, 0.02)
+    say(f"gemm_bf16 M={M} N={N} K={K}")
+    C = empty_dev((M, N), np.uint16)
+    ne.gemm_bf16(to_dev(A), to_dev(W), to_dev(bias), C, M, N, K)
+    got = to_host(C)
+    Af = orc.bf16_to_f32(A).reshape(M, K).astype(np.float64)
+    Wf = orc.bf16_to_f32(W).reshape(N, K).astype(np.float64)
+    bf = orc.bf16_to_f32(bias).astype(np.float64)
+    ref = Af @ Wf.T + bf
+    abs_sum = np.abs(Af) @ np.abs(Wf).T + np.abs(bf)
+    ok, ratio = bf16_err_ok(got, ref, abs_sum)
+    say(f"  worst error / bound = {ratio.max():.3f}")
+    assert ok.all()
+
+
+def test_gemm_bf16_residual(orc):
+    M, N, K = 70, 2880, 4096
+    A = orc.fill_bf16(1, 34, M * K, 0.0, 1.0)
+    W = orc.fill_bf16(1, 35, N * K, 0.0, 0.02)
+    res = orc.fill_bf16(1, 36, M * N, 0.0, 5.0)
+    C = to_dev(res)
+    ne.gemm_bf16(to_dev(A), to_dev(W), None, C, M, N, K, accumulate=True)
+    got = to_host(C).reshape(M, N)
+    # y = bf16(res + bf16(dot)): compare against the exact dot rounded the same way
+    Af = orc.bf16_to_f32(A).reshape(M, K).astype(np.float64)
+    Wf = orc.bf16_to_f32(W).reshape(N, K).astype(np.float64)
+    dot = Af @ Wf.T
+    ref = orc.bf16_to_f32(res).reshape(M, N).astype(np.float64) + dot
+    abs_sum = np.abs(Af) @ np.abs(Wf).T
+    bound = 2.0 ** -7 * np.abs(ref) + 2.0 ** -8 * np.abs(dot) + 2.0 ** -17 * abs_sum + 1e-30
+    err = np.abs(orc.bf16_to_f32(got).astype(np.float64) - ref)
+    say(f"gemm residual: worst error / bound = {(err / bound).max():.3f}")
+    assert (err <= bound).all()
+
+
+def moe_weights(orc, E, H, I, seed):
+    return dict(
+        rw=orc.fill_bf16(seed, 52, E * H, 0.0, 0.02),
+        rb=orc.fill_bf16(seed, 53, E, 0.0, 0.02),
+        guc=orc.fill_bytes(seed, 54, E * 2 * I * H // 2),
+        gus=orc.fill_scales(seed, 55, E * 2 * I * H // 32, 119, 6),
+        gub=orc.fill_bf16(seed, 56, E * 2 * I, 0.0, 0.02),
+        dnc=orc.fill_bytes(seed, 57, E * H * I // 2),
+        dns=orc.fill_scales(seed, 58, E * H * I // 32, 119, 6),
+        dnb=orc.fill_bf16(seed, 59, E * H, 0.0, 0.02),
+    )
+
+
+@OFF
+@pytest.mark.parametrize("M,E,H,I,k", [(300, 32, 2880, 2880, 4), (37, 8, 256, 512, 2)])
+def test_moe_prefill_vs_oracle(orc, M, E, H, I, k):
+    """Rows grouped by expert into MXFP4 matrix-core GEMMs vs the canonical
+    per-row MoE (experts and weights from the oracle's router)."""
+    d = moe_weights(orc, E, H, I, seed=2)
+    x = orc.fill_bf16(2, 51, M * H, 0.0, 1.0)
+    ref, ridx, rsc = orc.moe_layer(x, d["rw"], d["rb"], d["guc"], d["gus"], d["gub"], d["dnc"],
+                                   d["dns"], d["dnb"], E, H, I, k)
+    say(f"moe_prefill M={M} E={E} H={H} I={I} k={k}")
+    h = to_dev(np.zeros((M, H), np.uint16))  # residual 0: h becomes bf16(moe)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    ne.moe_prefill(to_dev(x), to_dev(ridx), to_dev(rsc), dv["guc"], dv["gus"], dv["gub"],
+                   dv["dnc"], dv["dns"], dv["dnb"], h, M, E, H, I, k)
+    got = orc.bf16_to_f32(to_host(h)).astype(np.float64)
+    r = orc.bf16_to_f32(ref).astype(np.float64)
+    err = np.abs(got - r)
+    rel = err.max() / np.abs(r).max()
+    same = (to_host(h) == ref).mean()
+    say(f"  max error / max|ref| = {rel:.3e}, median |err| / rms = "
+        f"{np.median(err) / np.sqrt((r ** 2).mean()):.3e}, bit-equal fraction {same:.3f}")
+    assert rel < 2e-2
+    assert np.median(err) <= 2.0 ** -8 * np.sqrt((r ** 2).mean())
+
+
+@OFF
+@pytest.mark.parametrize("window", [0, 64])
+def test_attn_prefill_vs_oracle(orc, window):
+    M, Hq, Hkv, D, T = 200, 8, 2, 64, 256
+    q = orc.fill_bf16(4, 61, M * Hq * D, 0.0, 1.0)
+    kc = orc.fill_bf16(4, 62, Hkv * T * D, 0.0, 1.0)
+    vc = orc.fill_bf16(4, 63, Hkv * T * D, 0.0, 1.0)
+    sinks = orc.fill_bf16(4, 64, Hq, 0.0, 1.0)
+    say(f"attn_prefill M={M} Hq={Hq} Hkv={Hkv} window={window}")
+    out = empty_dev((M, Hq * D), np.uint16)
+    ne.attn_prefill(to_dev(q), to_dev(kc), to_dev(vc), to_dev(sinks), out, M, Hq, Hkv, D, T,
+                    window)
+    got = to_host(out)
+    # every row is the decode attention of its own position over the same cache
+    kcb = np.broadcast_to(kc.reshape(1, -1), (M, kc.size))
+    vcb = np.broadcast_to(vc.reshape(1, -1), (M, vc.size))
+    _, ref = orc.attn_decode(q, kcb, vcb, sinks, M, Hq, Hkv, D, T,
+                             np.arange(M, dtype=np.int32), window)
+    vmax = np.abs(orc.bf16_to_f32(vc)).max()
+    ok, ratio = bf16_err_ok(got, ref, np.full(ref.shape, vmax), k_eps=2.0 ** -14)
+    say(f"  worst error / bound = {ratio.max():.3f}")
+    assert ok.all()
+
+
+SMALL = dict(n_layers=4, hidden=512, n_heads=16, n_kv_heads=2, head_dim=64, n_experts=8,
+             top_k=4, intermediate=512, vocab=4096, sliding_window=128, max_seq=512,
+             max_batch=2)
+
+
+def prompt_pass(cfg, seed, prompt, n_steps, mode):
+    eng = ne.Engine(cfg)
+    eng.init_random(seed)
+    eng.set_prefill_mode(mode)
+    eng.prefill(prompt)
+    first = eng.read_logits()
+    eng.decode(n_steps)
+    toks = eng.read_tokens()[:, len(prompt[0]):]
+    eng.close()
+    return first, toks
+
+
+def compare_modes(cfg, seed, prompt, n_steps):
+    """Batched prompt pass vs the stepwise one (decode kernels, bit-identical
+    to the oracle)."""
+    torch_cuda()
+    say(f"prefill modes layers={cfg.n_layers} hidden={cfg.hidden} batch={len(prompt)} "
+        f"prompt={len(prompt[0])}")
+    lg_s, tok_s = prompt_pass(cfg, seed, prompt, n_steps, ne.PREFILL_STEPWISE)
+    lg_b, tok_b = prompt_pass(cfg, seed, prompt, n_steps, ne.PREFILL_BATCHED)
+    rel = np.abs(lg_b - lg_s).max() / np.abs(lg_s).max()
+    top2 = np.sort(lg_s, axis=1)[:, -2:]
+    margin = (top2[:, 1] - top2[:, 0]) / np.abs(lg_s).max(axis=1)
+    say(f"  logits rel max err {rel:.3e}; first-token top-2 margin (relative) {margin}")
+    assert rel < 2e-2
+    for b in range(len(prompt)):
+        if margin[b] > 2e-2:  # a decisive first token must agree
+            assert tok_b[b, 0] == tok_s[b, 0]
+    agree = (tok_b == tok_s).all(axis=1)
+    say(f"  greedy ids identical over {n_steps + 1} tokens per row: {agree}")
+    return rel, agree
+
+
+@OFF
+def test_small_model_batched_prefill():
+    """Two rows, 150-token prompts: several 128-row GEMM tiles and the moving
+    128-key sliding window inside the prompt."""
+    cfg = ne.config_preset("gpt-oss-20b", **SMALL)
+    prompt = [[(7 * i + 3) % 4096 for i in range(150)], [(11 * i + 5) % 4096 for i in range(150)]]
+    compare_modes(cfg, 9, prompt, 16)
+
+
+@OFF
+def test_gpt_oss_20b_batched_prefill():
+    """Full 20b shape, 300-token prompt."""
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=512)
+    prompt = [[(1009 * i + 17) % 201088 for i in range(300)]]
+    compare_modes(cfg, 0, prompt, 16)
+
+
+def test_prefill_mode_validation():
+    torch_cuda()
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_seq=16))
+    eng = ne.Engine(cfg)
+    with pytest.raises(ne.NeonError) as e:
+        eng.set_prefill_mode(7)
+    assert e.value.status == ne.NEON_EINVAL
+    with pytest.raises(ne.NeonError) as e:  # switched off (see OFF)
+        eng.set_prefill_mode(ne.PREFILL_BATCHED)
+    assert e.value.status == ne.NEON_ESTATE
+    eng.set_prefill_mode(ne.PREFILL_STEPWISE)
+    eng.close()
