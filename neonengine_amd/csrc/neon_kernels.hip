@@ -1350,7 +1350,8 @@ __global__ __launch_bounds__(512) void k_attn_split(
     const uint16_t* __restrict__ q_src, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int Hq, int Hkv,
+    float* __restrict__ part_o, float* __restrict__ part_ml,
+    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv,
     int G, int T_max, int window, int S, int fused, int q_stride) {
   __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
   __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
@@ -1486,6 +1487,26 @@ __global__ __launch_bounds__(512) void k_attn_split(
     v = __fadd_rn(v, __shfl_xor(v, 32, 64));
     o[e] = v;
   }
+  if (S == 1) {
+    // one split: the merge with the sink happens here, with exactly the
+    // operations k_attn_merge applies to a single partial
+    if (kg == 0) {
+      const float sk = bf2f(sinks[h]);
+      const float M = fmaxf(sk, m);
+      float den = neon_expf(__fsub_rn(sk, M));
+      const float f = (m == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(m, M));
+      den = __builtin_fmaf(l, f, den);
+      const float inv = __fdiv_rn(1.0f, den);
+      uint32_t w4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w4[e] = pack_bf2(__fmul_rn(__builtin_fmaf(f, o[2 * e], 0.0f), inv),
+                         __fmul_rn(__builtin_fmaf(f, o[2 * e + 1], 0.0f), inv));
+      *reinterpret_cast<uint4*>(out + ((size_t)b * Hq + h) * kD + dq * 8) =
+          make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+    return;
+  }
   const size_t pi = ((size_t)b * Hq + h) * S + s;
   if (kg == 0) {
     float4* po = reinterpret_cast<float4*>(part_o + pi * kD + dq * 8);
@@ -1533,16 +1554,21 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;  // 1, 2, 4 or 8 (checked on the host)
   hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * a.S, a.B), dim3(64 * (G < 4 ? 4 : G)),
                      0, st, a.q_src, a.kc, a.vc, a.pos, a.cos_t, a.sin_t, a.part_o,
-                     a.part_ml, a.Hq, a.Hkv, G, a.T_max, a.window, a.S, a.fused,
-                     a.q_stride);
-  hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
-                     a.part_ml, a.sinks, a.out, a.Hq, a.S);
+                     a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G, a.T_max, a.window, a.S,
+                     a.fused, a.q_stride);
+  if (a.S > 1)  // one split finishes in the split kernel
+    hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
+                       a.part_ml, a.sinks, a.out, a.Hq, a.S);
 }
 
+// Key splits for a cache of T_max rows: spans of at most 4 chunks (256 keys,
+// e.g. the 128-key sliding window) stay in one split, which finishes in the
+// split kernel (no merge launch); longer spans use one split per 64-key
+// chunk, at most 32.
 int attn_splits(int T_max, int window) {
   const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
   const int s = (span + 63) / 64;
-  return s < 1 ? 1 : (s > kMaxSplits ? kMaxSplits : s);
+  return s <= 4 ? 1 : (s > kMaxSplits ? kMaxSplits : s);
 }
 
 }  // namespace neon

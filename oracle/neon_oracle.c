@@ -412,10 +412,12 @@ void or_c_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
   }
 }
 
+/* Split count of the device attention (attn_splits): spans of at most 4
+ * chunks (256 keys) use one split, longer ones one split per chunk, max 32. */
 int or_attn_splits(int T_max, int window) {
   const int span = window > 0 ? (window < T_max ? window : T_max) : T_max;
   const int s = (span + 63) / 64;
-  return s < 1 ? 1 : (s > 32 ? 32 : s);
+  return s <= 4 ? 1 : (s > 32 ? 32 : s);
 }
 
 /* Decode attention with sinks, canonical split form (device k_attn_split +

@@ -576,5 +576,6 @@ def test_c_attn_split_count_only_reorders(orc):
     outs = [orc.c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, Tm, pos, 0, S)[1] for S in (1, 3, 11)]
     for o in outs[1:]:
         np.testing.assert_allclose(o, outs[0], rtol=1e-5, atol=1e-6)
-    assert orc.attn_splits(4096, 128) == 2 and orc.attn_splits(4096, 0) == 32
-    assert orc.attn_splits(100, 0) == 2 and orc.attn_splits(1, 0) == 1
+    assert orc.attn_splits(4096, 128) == 1 and orc.attn_splits(4096, 0) == 32
+    assert orc.attn_splits(100, 0) == 1 and orc.attn_splits(1, 0) == 1
+    assert orc.attn_splits(256, 0) == 1 and orc.attn_splits(257, 0) == 5
