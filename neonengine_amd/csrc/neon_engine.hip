@@ -325,7 +325,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   const size_t Bm = c.max_batch, half = c.head_dim / 2;
   ctx->s_slide = attn_splits(c.max_seq, c.sliding_window);
   ctx->s_full = attn_splits(c.max_seq, 0);
-  ctx->lm_nblk = gemv_default_grid(c.vocab);
+  ctx->lm_nblk = gemv_default_grid(c.vocab, 2);
   ctx->tok_stride = c.max_seq + 1;
   off = 0;
   const size_t o_h = take(Bm * H * 2), o_xn = take(Bm * H * 2),
@@ -545,7 +545,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     GemvArgs q;
     q.mode = 0; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
     q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B;
-    q.nblk = gemv_default_grid(q.N);
+    q.nblk = gemv_default_grid(q.N, q.mode);
     launch_gemv_bf16(q, st);
     AttnArgs a;
     a.q_src = ctx->qkv; a.kc = ctx->kc + (size_t)l * ctx->kv_layer_elems;
@@ -559,7 +559,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     GemvArgs o;
     o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
     o.N = H; o.K = c.n_heads * D; o.B = B;
-    o.nblk = gemv_default_grid(o.N);
+    o.nblk = gemv_default_grid(o.N, o.mode);
     launch_gemv_bf16(o, st);
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
@@ -888,7 +888,7 @@ extern "C" neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,
     KFAIL(NEON_EINVAL, "neon_gemv_bf16: bad shape N=%d K=%d B=%d", N, K, B);
   GemvArgs a;
   a.mode = 0; a.W = W; a.bias = bias; a.x = x; a.y = y; a.N = N; a.K = K; a.B = B;
-  a.nblk = gemv_default_grid(N);
+  a.nblk = gemv_default_grid(N, a.mode);
   launch_gemv_bf16(a, S(stream));
   KLAUNCHED();
 }

@@ -35,9 +35,10 @@ struct GemvArgs {
   float* part_val = nullptr;
   int32_t* part_idx = nullptr;
   int N = 0, K = 0, B = 1;
-  int nblk = 1;  // grid.x (rows go in groups of 4 per wave, grid-strided)
+  int nblk = 1;  // grid.x (gemv_default_grid; wave row groups are grid-strided)
 };
-int gemv_default_grid(int N);
+// grid.x for N rows in `mode` (the rows per wave group depend on the mode)
+int gemv_default_grid(int N, int mode);
 void launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
 
 void launch_argmax_advance(const float* part_val, const int32_t* part_idx,

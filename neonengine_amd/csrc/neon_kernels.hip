@@ -465,14 +465,14 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
 //                HFM:365,375)
 //   MODE_LOGITS: logits[b][n] = dot (fp32), plus the block's (max, lowest
 //                argmax) written to part_val/part_idx [B][gridDim.x]
-// grid (nblk, 1, B), block 256; a wave takes groups of 4 consecutive rows
+// grid (nblk, 1, B), block 256; a wave takes groups of R consecutive rows
 // (grid-strided, so huge N such as lm_head runs on a bounded grid), loads
-// all 4 rows before any arithmetic and reduces them together with the
-// 4-row xor butterfly (bit-identical to 4 separate butterflies); lane 16 r
-// then holds row r, so the 4 epilogues run in parallel lanes.
+// all R rows before any arithmetic and reduces them together with the
+// R-row xor butterfly (bit-identical to R separate butterflies); lane
+// (64 / R) r then holds row r, so the R epilogues run in parallel lanes.
+// R = 2 for the projections (more waves in flight), 4 for lm_head.
 // ===========================================================================
 enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
-constexpr int kGemvRows = 4;
 
 // xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
 // lanes of an xor pair hold the same sum after every step (fp32 addition
@@ -517,23 +517,38 @@ __device__ __forceinline__ float wave_sum_4rows(float a0, float a1, float a2,
   return t;
 }
 
-// One group of 4 rows.  FIRST: the wave's first group, which also finishes
+// xor butterfly of 2 rows at once (see wave_sum_8rows); lane l returns the
+// total of row l >> 5.
+__device__ __forceinline__ float wave_sum_2rows(float a0, float a1, int lane) {
+  const bool u32 = (lane & 32) != 0;
+  float t = __fadd_rn(u32 ? a1 : a0, __shfl_xor(u32 ? a0 : a1, 32, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 16, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 8, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
+  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  return t;
+}
+
+template <int R>
+constexpr int log2_rows() { return R == 4 ? 2 : (R == 2 ? 1 : 0); }
+
+// One group of R rows.  FIRST: the wave's first group, which also finishes
 // the input (and its RMSNorm) from the raw loads issued before the rows, so
 // that work overlaps the row loads; later groups reuse xr.
-template <int P, int MODE, bool NORM, bool FIRST>
+template <int P, int MODE, bool NORM, bool FIRST, int R>
 __device__ __forceinline__ void gemv_bf16_group(
     int g, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     uint16_t bias_first, float (&xr)[P][8], const XBf16Raw<P>& xraw, float eps,
     uint16_t* __restrict__ y, float* __restrict__ logits, int b, int N, int K,
     int lane, float& best_v, int32_t& best_i) {
   const int U = K / 8;
-  const int my_row = lane >> 4;  // row of the group this lane holds after the reduction
-  const int r0 = g * kGemvRows, nr = min(kGemvRows, N - r0);
-  uint4 w0[P], w1[P], w2[P], w3[P];
-  bf16_load_row<P>(w0, W + (size_t)r0 * K, U, lane);
-  bf16_load_row<P>(w1, W + (size_t)min(r0 + 1, N - 1) * K, U, lane);
-  bf16_load_row<P>(w2, W + (size_t)min(r0 + 2, N - 1) * K, U, lane);
-  bf16_load_row<P>(w3, W + (size_t)min(r0 + 3, N - 1) * K, U, lane);
+  constexpr int LS = 6 - log2_rows<R>();  // lane (1 << LS) r holds row r after the sum
+  const int my_row = lane >> LS;
+  const int r0 = g * R, nr = min(R, N - r0);
+  uint4 w[R][P];
+#pragma unroll
+  for (int r = 0; r < R; ++r) bf16_load_row<P>(w[r], W + (size_t)min(r0 + r, N - 1) * K, U, lane);
   uint16_t bias_b = bias_first;  // the first group's bias was loaded before x
   if (!FIRST && MODE != MODE_LOGITS && bias != nullptr)
     bias_b = bias[r0 + min(my_row, nr - 1)];
@@ -541,16 +556,24 @@ __device__ __forceinline__ void gemv_bf16_group(
     __builtin_amdgcn_sched_barrier(0);  // all row loads issue before the norm's math
     wave_x_bf16_finish<P, NORM>(xr, xraw, eps, K, lane, nullptr);
   }
-  const float tot = wave_sum_4rows(bf16_row_partial<P>(w0, xr, U, lane),
-                                   bf16_row_partial<P>(w1, xr, U, lane),
-                                   bf16_row_partial<P>(w2, xr, U, lane),
-                                   bf16_row_partial<P>(w3, xr, U, lane), lane);
+  float tot;
+  if constexpr (R == 4)
+    tot = wave_sum_4rows(bf16_row_partial<P>(w[0], xr, U, lane),
+                         bf16_row_partial<P>(w[1], xr, U, lane),
+                         bf16_row_partial<P>(w[2], xr, U, lane),
+                         bf16_row_partial<P>(w[3], xr, U, lane), lane);
+  else if constexpr (R == 2)
+    tot = wave_sum_2rows(bf16_row_partial<P>(w[0], xr, U, lane),
+                         bf16_row_partial<P>(w[1], xr, U, lane), lane);
+  else
+    tot = wave_sum(bf16_row_partial<P>(w[0], xr, U, lane));
   const int r = r0 + my_row;
+  constexpr int kLead = (1 << LS) - 1;  // lanes with (lane & kLead) == 0 store
   if (my_row < nr) {
     if (MODE == MODE_LOGITS) {
       if (tot > best_v) { best_v = tot; best_i = r; }  // rows rise within a lane
-      if ((lane & 15) == 0) logits[(size_t)b * N + r] = tot;
-    } else if ((lane & 15) == 0) {
+      if ((lane & kLead) == 0) logits[(size_t)b * N + r] = tot;
+    } else if ((lane & kLead) == 0) {
       const float v = bias ? __fadd_rn(tot, bf2f(bias_b)) : tot;
       const size_t o = (size_t)b * N + r;
       if (MODE == MODE_STORE) y[o] = f2bf(v);
@@ -559,7 +582,7 @@ __device__ __forceinline__ void gemv_bf16_group(
   }
 }
 
-template <int P, int MODE, bool NORM>
+template <int P, int MODE, bool NORM, int R>
 __global__ __launch_bounds__(256) void k_gemv_bf16(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
@@ -569,7 +592,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   __shared__ int32_t bi_s[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int b = blockIdx.z;
-  const int ngroups = (N + kGemvRows - 1) / kGemvRows;
+  const int ngroups = (N + R - 1) / R;
   const int gstride = gridDim.x * 4;
   const int g0 = blockIdx.x * 4 + wave;
   // The first group's bias, then the input, go out before any row load:
@@ -578,7 +601,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   // addresses) so that no branch makes the compiler wait for everything.
   uint16_t bias_first = 0;
   if (MODE != MODE_LOGITS) {
-    const int rb = min(g0 * kGemvRows + (lane >> 4), N - 1);
+    const int rb = min(g0 * R + (lane >> (6 - log2_rows<R>())), N - 1);
     bias_first = (bias != nullptr ? bias : W)[rb];
   }
   float xr[P][8];
@@ -588,17 +611,17 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
   if (g0 < ngroups) {
-    gemv_bf16_group<P, MODE, NORM, true>(g0, W, bias, bias_first, xr, xraw, eps, y,
-                                         logits, b, N, K, lane, best_v, best_i);
+    gemv_bf16_group<P, MODE, NORM, true, R>(g0, W, bias, bias_first, xr, xraw, eps, y,
+                                            logits, b, N, K, lane, best_v, best_i);
     for (int g = g0 + gstride; g < ngroups; g += gstride)
-      gemv_bf16_group<P, MODE, NORM, false>(g, W, bias, 0, xr, xraw, eps, y, logits, b,
-                                            N, K, lane, best_v, best_i);
+      gemv_bf16_group<P, MODE, NORM, false, R>(g, W, bias, 0, xr, xraw, eps, y, logits, b,
+                                               N, K, lane, best_v, best_i);
   }
   if (MODE == MODE_LOGITS) {
-    // lanes 0, 16, 32, 48 hold the wave's candidates: keep the larger value,
-    // the lower row on ties
+    // lanes 64 r / R hold the wave's candidates: keep the larger value, the
+    // lower row on ties
 #pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
+    for (int off = 64 / R; off <= 32; off <<= 1) {
       const float ov = __shfl_xor(best_v, off, 64);
       const int32_t oi = __shfl_xor(best_i, off, 64);
       if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }
@@ -616,14 +639,20 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   }
 }
 
+// rows per wave group: 4 for lm_head, 2 for the projections (measured: the
+// QKV shape ran 8.3 us with 2 rows per wave against 9.4 us with 4)
+template <int MODE>
+constexpr int gemv_rows() { return MODE == MODE_LOGITS ? 4 : 2; }
+
 template <int P, int MODE>
 static void launch_gemv_bf16_p(const GemvArgs& a, hipStream_t st) {
+  constexpr int R = gemv_rows<MODE>();
   if (a.norm_w != nullptr)
-    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, true>), dim3(a.nblk, 1, a.B), dim3(256),
+    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, true, R>), dim3(a.nblk, 1, a.B), dim3(256),
                        0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
                        a.part_val, a.part_idx, a.N, a.K);
   else
-    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, false>), dim3(a.nblk, 1, a.B), dim3(256),
+    hipLaunchKernelGGL((k_gemv_bf16<P, MODE, false, R>), dim3(a.nblk, 1, a.B), dim3(256),
                        0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
                        a.part_val, a.part_idx, a.N, a.K);
 }
@@ -644,8 +673,9 @@ static void launch_gemv_bf16_m(const GemvArgs& a, hipStream_t st) {
   }
 }
 
-int gemv_default_grid(int N) {
-  const int ngroups = (N + kGemvRows - 1) / kGemvRows;
+int gemv_default_grid(int N, int mode) {
+  const int R = mode == MODE_LOGITS ? gemv_rows<MODE_LOGITS>() : gemv_rows<MODE_STORE>();
+  const int ngroups = (N + R - 1) / R;
   const int nblk = (ngroups + 3) / 4;
   return nblk < 2048 ? nblk : 2048;
 }
