@@ -1291,10 +1291,17 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
                      st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg, a.idx,  \
                      a.idx_out, a.score_out, a.E, a.xn, a.act, a.H, a.I, a.k,     \
                      a.alpha, a.limit)
+  // When gate_up records the chosen experts and weights (idx_out/score_out),
+  // down reads them instead of ranking the logits again: gate_up has finished
+  // before down starts (same stream), and the values are the same.
+  const bool dn_ids = a.router_lg != nullptr && a.idx_out != nullptr && a.score_out != nullptr;
+  const float* dn_lg = dn_ids ? nullptr : a.router_lg;
+  const int32_t* dn_idx = dn_ids ? a.idx_out : a.idx;
+  const float* dn_score = dn_ids ? a.score_out : a.score;
 #define D_LAUNCH(PP, PR)                                                            \
   hipLaunchKernelGGL((k_moe_down<PP, PR>), dim3(dblk, a.B), dim3(64 * a.k), 0, st, \
-                     a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg, a.idx,        \
-                     a.score, a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
+                     a.dn_codes, a.dn_scales, a.dn_bias, dn_lg, dn_idx, dn_score,   \
+                     a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
   switch (Pg) {
     case 1: G_LAUNCH(1, false); break;
     case 2: if (pg) G_LAUNCH(2, true); else G_LAUNCH(2, false); break;
