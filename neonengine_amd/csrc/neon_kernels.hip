@@ -1340,8 +1340,9 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 // head).  Block (g, s) serves split s of kv head g for all G query heads of
 // the group: each 64-key chunk of K and V is loaded from HBM once into LDS
 // (one 16-byte word per thread) and read by the G waves, one wave per query
-// head.  The next chunk's words are loaded into registers while the current
-// chunk is computed.  K rows sit in LDS with their eight 16-byte words
+// head.  The words of two chunks are in flight at once: both first tiles are
+// staged before the loop, then chunk c + 2 loads while chunk c is computed.
+// K rows sit in LDS with their eight 16-byte words
 // rotated by the key index, so the 64 lanes of a wave, one key each, read
 // distinct banks.  Each wave writes its split's (o, m, l) partial; the last
 // split always holds key pos, so with fused != 0 (q_src = raw qkv rows) the
@@ -1410,11 +1411,18 @@ __global__ __launch_bounds__(512) void k_attn_split(
   const bool last = s == S - 1;
   const int p_lds = (fused && last) ? p : -1;  // key served from LDS
 
-  // first chunk's words into registers (key p comes from LDS later)
-  uint4 nk0, nk1, nv0, nv1;  // the next chunk's words, in flight meanwhile
+  // the first two chunks' words into registers (key p comes from LDS
+  // later): both tiles are staged before the loop, so a split of two chunks
+  // (the 128-key sliding window) never waits for memory inside it
+  uint4 nk0, nk1, nv0, nv1;  // chunk c0, later the chunk two ahead
+  uint4 pk0, pk1, pv0, pv1;  // chunk c0 + 1
   if (c0 < c1) {
     ATTN_LOAD_WORD(nk0, nv0, tid, lo + c0 * 64);
     ATTN_LOAD_WORD(nk1, nv1, tid + nt, lo + c0 * 64);
+  }
+  if (c0 + 1 < c1) {
+    ATTN_LOAD_WORD(pk0, pv0, tid, lo + (c0 + 1) * 64);
+    ATTN_LOAD_WORD(pk1, pv1, tid + nt, lo + (c0 + 1) * 64);
   }
 
   // ---- q heads (and the new k/v row for the last split) into LDS ----------
@@ -1454,6 +1462,10 @@ __global__ __launch_bounds__(512) void k_attn_split(
     ATTN_STORE_WORD(nk0, nv0, tid, lo + c0 * 64, 0);
     ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + c0 * 64, 0);
   }
+  if (c0 + 1 < c1) {
+    ATTN_STORE_WORD(pk0, pv0, tid, lo + (c0 + 1) * 64, 1);
+    ATTN_STORE_WORD(pk1, pv1, tid + nt, lo + (c0 + 1) * 64, 1);
+  }
   __syncthreads();
 
   const float4* q4 = reinterpret_cast<const float4*>(qs[w]);
@@ -1464,9 +1476,9 @@ __global__ __launch_bounds__(512) void k_attn_split(
 
   for (int c = c0; c < c1; ++c) {
     const int buf = (c - c0) & 1;
-    if (c + 1 < c1) {
-      ATTN_LOAD_WORD(nk0, nv0, tid, lo + (c + 1) * 64);
-      ATTN_LOAD_WORD(nk1, nv1, tid + nt, lo + (c + 1) * 64);
+    if (c + 2 < c1) {  // chunk c + 2 goes into this tile once it is consumed
+      ATTN_LOAD_WORD(nk0, nv0, tid, lo + (c + 2) * 64);
+      ATTN_LOAD_WORD(nk1, nv1, tid + nt, lo + (c + 2) * 64);
     }
     const int cb = lo + c * 64;
     if (active) {
@@ -1508,11 +1520,12 @@ __global__ __launch_bounds__(512) void k_attn_split(
       }
     }
     }  // active
-    if (c + 1 < c1) {
-      ATTN_STORE_WORD(nk0, nv0, tid, lo + (c + 1) * 64, buf ^ 1);
-      ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + (c + 1) * 64, buf ^ 1);
+    __syncthreads();  // tile buf and ps are consumed
+    if (c + 2 < c1) {  // visible to the readers of iteration c + 2 after the
+                       // barrier that ends iteration c + 1
+      ATTN_STORE_WORD(nk0, nv0, tid, lo + (c + 2) * 64, buf);
+      ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + (c + 2) * 64, buf);
     }
-    __syncthreads();  // tile buf is free, tile buf ^ 1 and ps are complete
   }
   if (!active) return;
   // reduce o over the 8 key groups (lane bits 3..5)

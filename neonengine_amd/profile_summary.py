@@ -52,6 +52,9 @@ def main(argv=None):
     ap.add_argument("--kernels-per-step", type=int)
     ap.add_argument("--bytes", action="append", default=[],
                     help="kernel-name-regex=bytes_per_launch")
+    ap.add_argument("--layer-parity", action="store_true",
+                    help="also split per-layer kernels by layer parity (even layers are "
+                         "the sliding-window layers of gpt-oss)")
     a = ap.parse_args(argv)
     if a.pmc:
         pmc_summary(a.trace)
@@ -63,6 +66,8 @@ def main(argv=None):
         for r in csv.DictReader(f):
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
     rows.sort()
+    # runtime copy kernels (reads of results) are not part of a step
+    rows = [r for r in rows if not short(r[2]).startswith("__amd")]
     n = a.last_steps * a.kernels_per_step
     if len(rows) < n:
         sys.exit(f"trace has {len(rows)} dispatches, fewer than {n}")
@@ -92,6 +97,23 @@ def main(argv=None):
                 gbs = f"{b / (avg * 1e-6) / 1e9:.0f}"
         print(f"| {k} | {cnt[k] / a.last_steps:g} | {avg:.2f} | "
               f"{busy[k] / a.last_steps / 1e3:.1f} | {100 * busy[k] / total_busy:.1f} | {gbs} |")
+    if a.layer_parity:
+        # occurrence index of each kernel inside its step: for a kernel launched
+        # once per layer, even occurrences are even layers
+        par = defaultdict(list)
+        for st in range(a.last_steps):
+            seen = defaultdict(int)
+            for s, e, k in rows[st * a.kernels_per_step:(st + 1) * a.kernels_per_step]:
+                name = short(k)
+                par[(name, seen[name] % 2)].append(e - s)
+                seen[name] += 1
+        print("\n| kernel | even occurrences avg us | odd occurrences avg us |")
+        print("|---|---|---|")
+        for k in sorted(busy, key=lambda k: -busy[k]):
+            ev, od = par.get((k, 0), []), par.get((k, 1), [])
+            if not od:
+                continue
+            print(f"| {k} | {sum(ev) / len(ev) / 1e3:.2f} | {sum(od) / len(od) / 1e3:.2f} |")
 
 
 if __name__ == "__main__":
