@@ -639,10 +639,11 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   }
 }
 
-// rows per wave group: 4 for lm_head, 2 for the projections (measured: the
-// QKV shape ran 8.3 us with 2 rows per wave against 9.4 us with 4)
+// rows per wave group, measured at the 20b shapes: QKV (store) 8.7 us with 2
+// rows against 9.4 with 1 or 4; O (residual) 7.1 us with 1 against 7.5 with
+// 2; lm_head (logits) 4
 template <int MODE>
-constexpr int gemv_rows() { return MODE == MODE_LOGITS ? 4 : 2; }
+constexpr int gemv_rows() { return MODE == MODE_LOGITS ? 4 : (MODE == MODE_RESID ? 1 : 2); }
 
 template <int P, int MODE>
 static void launch_gemv_bf16_p(const GemvArgs& a, hipStream_t st) {
@@ -674,10 +675,12 @@ static void launch_gemv_bf16_m(const GemvArgs& a, hipStream_t st) {
 }
 
 int gemv_default_grid(int N, int mode) {
-  const int R = mode == MODE_LOGITS ? gemv_rows<MODE_LOGITS>() : gemv_rows<MODE_STORE>();
+  const int R = mode == MODE_LOGITS ? gemv_rows<MODE_LOGITS>()
+                                    : (mode == MODE_RESID ? gemv_rows<MODE_RESID>()
+                                                          : gemv_rows<MODE_STORE>());
   const int ngroups = (N + R - 1) / R;
   const int nblk = (ngroups + 3) / 4;
-  return nblk < 2048 ? nblk : 2048;
+  return nblk < 4096 ? nblk : 4096;  // lm_head: 4096 blocks measured 1% faster than 2048
 }
 
 void launch_gemv_bf16(const GemvArgs& a, hipStream_t st) {
