@@ -260,9 +260,19 @@ class Engine:
     def init_random(self, seed: int = 0, stream=None):
         self._chk(lib().neon_init_random(self._ctx, seed, _stream(stream)))
 
-    def load_tensor(self, name: str, data: bytes | memoryview):
-        buf = (C.c_char * len(data)).from_buffer_copy(data)
-        self._chk(lib().neon_load_tensor(self._ctx, name.encode(), buf, len(data)))
+    def load_tensor(self, name: str, data):
+        """data: bytes, memoryview or a C-contiguous numpy array (read in place)."""
+        import numpy as np
+        a = np.frombuffer(data, dtype=np.uint8) if not isinstance(data, np.ndarray) else data
+        if not a.flags.c_contiguous:
+            raise ValueError(f"load_tensor({name!r}): data must be contiguous")
+        self._chk(lib().neon_load_tensor(self._ctx, name.encode(), C.c_void_p(a.ctypes.data),
+                                         a.nbytes))
+
+    def load_checkpoint(self, path: str, strict: bool = True) -> int:
+        """Loads a local gpt-oss safetensors checkpoint (file or directory)."""
+        from .loader import load_checkpoint
+        return load_checkpoint(self, path, strict=strict)
 
     def tensor_ptr(self, name: str):
         p, n = C.c_void_p(), C.c_size_t()
@@ -270,7 +280,7 @@ class Engine:
         return p.value, n.value
 
     def set_prefill_mode(self, mode: int):
-        """PREFILL_BATCHED (default, matrix cores) or PREFILL_STEPWISE."""
+        """PREFILL_STEPWISE (default: teacher-forced decode steps) or PREFILL_BATCHED."""
         self._chk(lib().neon_set_prefill_mode(self._ctx, mode))
 
     def prefill(self, ids, stream=None):
