@@ -1387,6 +1387,35 @@ constexpr int kMaxSplits = 32;
     }                                                                           \
   } while (0)
 
+// One wave merges the S partials of head h (rows pi0 .. pi0 + S - 1 of
+// part_o / part_ml) with the sink, lane = output dim.  Every load goes out
+// first; each lane t < S computes its split's factor f_t = exp(m_t - M) (0 for
+// an empty split), then den and acc take the splits in order with fmaf.
+__device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o,
+                                                const float* __restrict__ part_ml,
+                                                size_t pi0, int S, float sk, int lane,
+                                                uint16_t* __restrict__ out_row) {
+  float ov[kMaxSplits];
+#pragma unroll
+  for (int t = 0; t < kMaxSplits; ++t)
+    ov[t] = t < S ? part_o[(pi0 + t) * kD + lane] : 0.0f;
+  const float mt_l = lane < S ? part_ml[(pi0 + lane) * 2] : -INFINITY;
+  const float lt_l = lane < S ? part_ml[(pi0 + lane) * 2 + 1] : 0.0f;
+  const float M = fmaxf(sk, wave_max(mt_l));
+  const float f_l = (mt_l == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt_l, M));
+  float den = neon_expf(__fsub_rn(sk, M));
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < kMaxSplits; ++t) {
+    if (t < S) {
+      const float f = readlane_f(f_l, t);
+      den = __builtin_fmaf(readlane_f(lt_l, t), f, den);
+      acc = __builtin_fmaf(f, ov[t], acc);
+    }
+  }
+  out_row[lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+}
+
 __global__ __launch_bounds__(512) void k_attn_split(
     const uint16_t* __restrict__ q_src, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
@@ -1573,31 +1602,9 @@ __global__ __launch_bounds__(64) void k_attn_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq,
     int S) {
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const size_t pi = ((size_t)b * Hq + h) * S;
-  // every load first: the head's S partial rows (lane = dim) and one (m, l)
-  // per lane, then the merge in split order from registers
-  float ov[kMaxSplits];
-#pragma unroll
-  for (int t = 0; t < kMaxSplits; ++t)
-    ov[t] = t < S ? part_o[(pi + t) * kD + lane] : 0.0f;
-  const float mt_l = lane < S ? part_ml[(pi + lane) * 2] : -INFINITY;
-  const float lt_l = lane < S ? part_ml[(pi + lane) * 2 + 1] : 0.0f;
-  const float sk = bf2f(sinks[h]);
-  float M = sk;
-  for (int t = 0; t < S; ++t) M = fmaxf(M, readlane_f(mt_l, t));
-  float den = neon_expf(__fsub_rn(sk, M));
-  float acc = 0.0f;
-#pragma unroll
-  for (int t = 0; t < kMaxSplits; ++t) {
-    if (t < S) {
-      const float mt = readlane_f(mt_l, t);
-      const float f = (mt == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt, M));
-      den = __builtin_fmaf(readlane_f(lt_l, t), f, den);
-      acc = __builtin_fmaf(f, ov[t], acc);
-    }
-  }
-  out[((size_t)b * Hq + h) * kD + lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+  const int h = blockIdx.x, b = blockIdx.y;
+  attn_merge_head(part_o, part_ml, ((size_t)b * Hq + h) * S, S, bf2f(sinks[h]), threadIdx.x,
+                  out + ((size_t)b * Hq + h) * kD);
 }
 
 #undef ATTN_LOAD_WORD
