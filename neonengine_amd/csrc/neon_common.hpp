@@ -143,22 +143,53 @@ __host__ __device__ __forceinline__ float neon_expf(float x) {
   return __builtin_ldexpf(p, (int)n);
 }
 
-// ---- wave reductions (xor butterfly over 64 lanes) ------------------------
+// ---- lane exchange: lane l receives lane (l ^ OFF)'s value ----------------
+// The values __shfl_xor(v, OFF, 64) gives, without the LDS permute unit (a
+// round trip through the LDS queue per step): DPP quad permutes for OFF 1
+// and 2, two row shifts and a select for 4, a row rotate by 8 for 8, and the
+// gfx950 permlane swaps for 16 and 32.  Reductions written with it are
+// bit-identical to the __shfl_xor form.
+template <int OFF>
+__device__ __forceinline__ int xor_lane_i(int v) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (OFF == 1) {
+    return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);  // quad_perm [1,0,3,2]
+  } else if constexpr (OFF == 2) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);  // quad_perm [2,3,0,1]
+  } else if constexpr (OFF == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, true);  // row_shl 4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr 4
+    return (lane & 4) ? dn : up;
+  } else if constexpr (OFF == 8) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, true);  // row_ror 8
+  } else if constexpr (OFF == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? (int)p[0] : (int)p[1];
+  } else {
+    static_assert(OFF == 32, "xor_lane: OFF must be 1, 2, 4, 8, 16 or 32");
+    const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? (int)p[0] : (int)p[1];
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {
+  return __builtin_bit_cast(float, xor_lane_i<OFF>(__builtin_bit_cast(int, v)));
+}
+
+// ---- wave reductions (xor butterfly over 64 lanes, off = 32 .. 1) ---------
+template <int OFF = 32>
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += xor_lane<OFF>(v);
+  if constexpr (OFF > 1) return wave_sum<OFF / 2>(v);
+  else return v;
 }
+template <int OFF = 32>
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  v = fmaxf(v, xor_lane<OFF>(v));
+  if constexpr (OFF > 1) return wave_max<OFF / 2>(v);
+  else return v;
 }
-__device__ __forceinline__ float half_wave_sum(float v) {
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float half_wave_sum(float v) { return wave_sum<16>(v); }
 
 // ---- counter-based RNG (SplitMix64 finaliser), identical to the oracle ----
 __host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {

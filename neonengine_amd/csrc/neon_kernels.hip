@@ -472,6 +472,18 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
 // (64 / R) r then holds row r, so the R epilogues run in parallel lanes.
 // R = 2 for the projections (more waves in flight), 4 for lm_head.
 // ===========================================================================
+// (value, index) candidates of lanes l ^ OFF for OFF = LO, 2 LO, .. HI: keep
+// the larger value, the lower index on ties (an order-free reduction)
+template <int LO, int HI>
+__device__ __forceinline__ void argmax_steps(float& v, int32_t& i) {
+  if constexpr (LO <= HI) {
+    const float ov = xor_lane<LO>(v);
+    const int32_t oi = xor_lane_i<LO>(i);
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    argmax_steps<2 * LO, HI>(v, i);
+  }
+}
+
 enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
 
 // xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
@@ -479,26 +491,27 @@ enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
 // commutes), so at step `off` a lane keeps half of its rows and sends the
 // other half: 7 + 3 shuffles, bit-identical to 8 separate butterflies.  Lane
 // l returns the total of row l >> 3.
-__device__ __forceinline__ float xchg(float keep, float send, int off) {
-  return __fadd_rn(keep, __shfl_xor(send, off, 64));
+template <int OFF>
+__device__ __forceinline__ float xchg(float keep, float send) {
+  return __fadd_rn(keep, xor_lane<OFF>(send));
 }
 __device__ __forceinline__ float wave_sum_8rows(float a0, float a1, float a2,
                                                 float a3, float a4, float a5,
                                                 float a6, float a7, int lane) {
   const bool u32 = (lane & 32) != 0, u16 = (lane & 16) != 0, u8 = (lane & 8) != 0;
   // off 32: lanes without bit 5 keep rows 0-3, the others rows 4-7
-  const float b0 = xchg(u32 ? a4 : a0, u32 ? a0 : a4, 32);
-  const float b1 = xchg(u32 ? a5 : a1, u32 ? a1 : a5, 32);
-  const float b2 = xchg(u32 ? a6 : a2, u32 ? a2 : a6, 32);
-  const float b3 = xchg(u32 ? a7 : a3, u32 ? a3 : a7, 32);
+  const float b0 = xchg<32>(u32 ? a4 : a0, u32 ? a0 : a4);
+  const float b1 = xchg<32>(u32 ? a5 : a1, u32 ? a1 : a5);
+  const float b2 = xchg<32>(u32 ? a6 : a2, u32 ? a2 : a6);
+  const float b3 = xchg<32>(u32 ? a7 : a3, u32 ? a3 : a7);
   // off 16: keep rows {0,1} or {2,3} of the group
-  const float c0 = xchg(u16 ? b2 : b0, u16 ? b0 : b2, 16);
-  const float c1 = xchg(u16 ? b3 : b1, u16 ? b1 : b3, 16);
+  const float c0 = xchg<16>(u16 ? b2 : b0, u16 ? b0 : b2);
+  const float c1 = xchg<16>(u16 ? b3 : b1, u16 ? b1 : b3);
   // off 8: keep row 0 or 1
-  float t = xchg(u8 ? c1 : c0, u8 ? c0 : c1, 8);
-  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  float t = xchg<8>(u8 ? c1 : c0, u8 ? c0 : c1);
+  t = __fadd_rn(t, xor_lane<4>(t));
+  t = __fadd_rn(t, xor_lane<2>(t));
+  t = __fadd_rn(t, xor_lane<1>(t));
   return t;
 }
 
@@ -507,13 +520,13 @@ __device__ __forceinline__ float wave_sum_8rows(float a0, float a1, float a2,
 __device__ __forceinline__ float wave_sum_4rows(float a0, float a1, float a2,
                                                 float a3, int lane) {
   const bool u32 = (lane & 32) != 0, u16 = (lane & 16) != 0;
-  const float b0 = __fadd_rn(u32 ? a2 : a0, __shfl_xor(u32 ? a0 : a2, 32, 64));
-  const float b1 = __fadd_rn(u32 ? a3 : a1, __shfl_xor(u32 ? a1 : a3, 32, 64));
-  float t = __fadd_rn(u16 ? b1 : b0, __shfl_xor(u16 ? b0 : b1, 16, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 8, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  const float b0 = __fadd_rn(u32 ? a2 : a0, xor_lane<32>(u32 ? a0 : a2));
+  const float b1 = __fadd_rn(u32 ? a3 : a1, xor_lane<32>(u32 ? a1 : a3));
+  float t = __fadd_rn(u16 ? b1 : b0, xor_lane<16>(u16 ? b0 : b1));
+  t = __fadd_rn(t, xor_lane<8>(t));
+  t = __fadd_rn(t, xor_lane<4>(t));
+  t = __fadd_rn(t, xor_lane<2>(t));
+  t = __fadd_rn(t, xor_lane<1>(t));
   return t;
 }
 
@@ -521,12 +534,12 @@ __device__ __forceinline__ float wave_sum_4rows(float a0, float a1, float a2,
 // total of row l >> 5.
 __device__ __forceinline__ float wave_sum_2rows(float a0, float a1, int lane) {
   const bool u32 = (lane & 32) != 0;
-  float t = __fadd_rn(u32 ? a1 : a0, __shfl_xor(u32 ? a0 : a1, 32, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 16, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 8, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 4, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 2, 64));
-  t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+  float t = __fadd_rn(u32 ? a1 : a0, xor_lane<32>(u32 ? a0 : a1));
+  t = __fadd_rn(t, xor_lane<16>(t));
+  t = __fadd_rn(t, xor_lane<8>(t));
+  t = __fadd_rn(t, xor_lane<4>(t));
+  t = __fadd_rn(t, xor_lane<2>(t));
+  t = __fadd_rn(t, xor_lane<1>(t));
   return t;
 }
 
@@ -620,12 +633,7 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   if (MODE == MODE_LOGITS) {
     // lanes 64 r / R hold the wave's candidates: keep the larger value, the
     // lower row on ties
-#pragma unroll
-    for (int off = 64 / R; off <= 32; off <<= 1) {
-      const float ov = __shfl_xor(best_v, off, 64);
-      const int32_t oi = __shfl_xor(best_i, off, 64);
-      if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }
-    }
+    argmax_steps<64 / R, 32>(best_v, best_i);
     if (lane == 0) { bv_s[wave] = best_v; bi_s[wave] = best_i; }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -712,12 +720,7 @@ __global__ __launch_bounds__(256) void k_argmax_advance(
     const int32_t pi = part_idx[(size_t)b * nparts + t];
     if (pv > v || (pv == v && pi < i)) { v = pv; i = pi; }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(v, off, 64);
-    const int32_t oi = __shfl_xor(i, off, 64);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-  }
+  argmax_steps<1, 32>(v, i);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) { sv[wave] = v; si[wave] = i; }
   __syncthreads();
@@ -929,7 +932,7 @@ __device__ __forceinline__ void wave_topk_rank(const float (&vin)[kRouteQ], int 
       r1 += (j + 1 < E && t.key[min(j + 1, E - 1)] > ki) ? 1 : 0;
     }
     int r = r0 + r1;
-    r += __shfl_xor(r, 32, 64);
+    r += xor_lane_i<32>(r);
     if (lane < E && r < k) { t.id[r] = lane; t.sc[r] = v[0]; }
   } else {
     uint64_t ki[NQ];
@@ -1198,7 +1201,7 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
   }
   // lane l holds row l >> 3 (bit-identical to separate butterflies)
   const float t = wave_sum_8rows(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], lane);
-  const float tu = __shfl_xor(t, 8, 64);  // lane 16 c receives the up total
+  const float tu = xor_lane<8>(t);  // lane 16 c receives the up total
   const int j = j0 + (lane >> 4);
   if ((lane & 15) == 0 && j < I) {
     const float gb = __fadd_rn(t, bf_lo(bgu));
@@ -1564,9 +1567,9 @@ __global__ __launch_bounds__(512) void k_attn_split(
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float v = o[e];
-    v = __fadd_rn(v, __shfl_xor(v, 8, 64));
-    v = __fadd_rn(v, __shfl_xor(v, 16, 64));
-    v = __fadd_rn(v, __shfl_xor(v, 32, 64));
+    v = __fadd_rn(v, xor_lane<8>(v));
+    v = __fadd_rn(v, xor_lane<16>(v));
+    v = __fadd_rn(v, xor_lane<32>(v));
     o[e] = v;
   }
   if (S == 1) {
