@@ -125,10 +125,7 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 // ---- exp: Cody-Waite reduction by ln 2 (two-part constant) and a degree-7
 // Taylor polynomial in Horner form, all fp32 fmaf.  The oracle evaluates the
 // same operation sequence, so both sides agree bit for bit.
-__host__ __device__ __forceinline__ float neon_expf(float x) {
-  if (x != x) return x;
-  if (x > 0x1.62e43p+6f) return __builtin_inff();
-  if (x < -0x1.9fe36ap+6f) return 0.0f;
+__host__ __device__ __forceinline__ float neon_expf_core(float x) {
   const float n = __builtin_rintf(x * 0x1.715476p+0f);
   float r = __builtin_fmaf(-n, 0x1.62e4p-1f, x);
   r = __builtin_fmaf(-n, 0x1.7f7d1cp-20f, r);
@@ -141,6 +138,29 @@ __host__ __device__ __forceinline__ float neon_expf(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   return __builtin_ldexpf(p, (int)n);
+}
+
+// The range checks are selects, not branches (a divergent branch costs a
+// wave both paths and the exec-mask bookkeeping); the polynomial runs on
+// every x, and its result is kept only where x is in range.
+__host__ __device__ __forceinline__ float neon_expf(float x) {
+  const float v = neon_expf_core(x);
+  const float r = x > 0x1.62e43p+6f ? __builtin_inff() : (x < -0x1.9fe36ap+6f ? 0.0f : v);
+  return x != x ? x : r;
+}
+
+// A load that stays where it is written.  The compiler sinks a plain load
+// whose only use sits in a branch (a lane-0 epilogue) into that branch, where
+// it issues last and is waited for alone; a relaxed atomic load is never
+// moved, and at workgroup scope it is the same hardware load.
+__device__ __forceinline__ uint32_t load_pinned_u32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ uint16_t load_pinned_u16(const uint16_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ float load_pinned_f32(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // ---- lane exchange: lane l receives lane (l ^ OFF)'s value ----------------

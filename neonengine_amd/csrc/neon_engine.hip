@@ -65,7 +65,7 @@ struct neon_ctx {
   // activations / scratch
   char* work = nullptr;
   uint16_t *h = nullptr, *xn = nullptr, *qkv = nullptr, *attn_out = nullptr,
-           *act = nullptr;
+           *act = nullptr, *q_rot = nullptr;  // q_rot: rotated q heads [B][Hq][D]
   int32_t* moe_idx = nullptr;
   float* moe_score = nullptr;
   float* router_lg = nullptr;
@@ -331,6 +331,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   const size_t o_h = take(Bm * H * 2), o_xn = take(Bm * H * 2),
                o_qkv = take(Bm * sz.qkv_rows * 2),
                o_ao = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
+               o_qr = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
                o_act = take(Bm * c.top_k * I * 2),
                o_idx = take(Bm * c.top_k * 4), o_sc = take(Bm * c.top_k * 4),
                o_rlg = take(Bm * c.n_experts * 4),
@@ -350,6 +351,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   char* W = ctx->work;
   ctx->h = (uint16_t*)(W + o_h); ctx->xn = (uint16_t*)(W + o_xn);
   ctx->qkv = (uint16_t*)(W + o_qkv); ctx->attn_out = (uint16_t*)(W + o_ao);
+  ctx->q_rot = (uint16_t*)(W + o_qr);
   ctx->act = (uint16_t*)(W + o_act); ctx->moe_idx = (int32_t*)(W + o_idx);
   ctx->moe_score = (float*)(W + o_sc);
   ctx->router_lg = (float*)(W + o_rlg);
@@ -542,19 +544,23 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
+    uint16_t* kc_l = ctx->kc + (size_t)l * ctx->kv_layer_elems;
+    uint16_t* vc_l = ctx->vc + (size_t)l * ctx->kv_layer_elems;
+    // QKV projection; its epilogue rotates q and k (RoPE-YaRN table) and
+    // appends k, v at cache row pos
     GemvArgs q;
-    q.mode = 0; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
+    q.mode = 3; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
     q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B;
     q.nblk = gemv_default_grid(q.N, q.mode);
+    q.pos = ctx->pos; q.cos_t = ctx->cos_t; q.sin_t = ctx->sin_t; q.q_out = ctx->q_rot;
+    q.kc = kc_l; q.vc = vc_l; q.Hq = c.n_heads; q.Hkv = c.n_kv_heads; q.T_max = c.max_seq;
     launch_gemv_bf16(q, st);
     AttnArgs a;
-    a.q_src = ctx->qkv; a.kc = ctx->kc + (size_t)l * ctx->kv_layer_elems;
-    a.vc = ctx->vc + (size_t)l * ctx->kv_layer_elems; a.sinks = w.sinks;
-    a.pos = ctx->pos; a.cos_t = ctx->cos_t; a.sin_t = ctx->sin_t;
+    a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
     a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml;
     a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
-    a.S = sliding ? ctx->s_slide : ctx->s_full; a.fused = 1; a.q_stride = qkv_rows;
+    a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
     launch_attn(a, st);
     GemvArgs o;
     o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
@@ -1034,11 +1040,11 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   if (hipMallocAsync((void**)&scratch, np * (D + 2) * 4, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
   AttnArgs a;
-  a.q_src = q; a.kc = const_cast<uint16_t*>(k_cache); a.vc = const_cast<uint16_t*>(v_cache);
-  a.sinks = sinks; a.pos = pos; a.cos_t = nullptr; a.sin_t = nullptr; a.out = out;
+  a.q = q; a.kc = k_cache; a.vc = v_cache;
+  a.sinks = sinks; a.pos = pos; a.out = out;
   a.part_o = scratch; a.part_ml = scratch + np * D;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window;
-  a.S = nsplit; a.fused = 0; a.q_stride = Hq * D;
+  a.S = nsplit; a.q_stride = Hq * D;
   launch_attn(a, st);
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);

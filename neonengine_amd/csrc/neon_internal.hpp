@@ -23,8 +23,21 @@ void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
                        int N, int K, int B, hipStream_t st);
 
 // ---- bf16 GEMV with fused prologue/epilogue ---------------------------------
+// QKV mode outputs: rotated q heads [B][Hq][64], and k (rotated) / v rows
+// written at cache row pos[b] of kc / vc [B][Hkv][T_max][64]
+struct RopeArgs {
+  const int32_t* pos = nullptr;
+  const float* cos_t = nullptr;  // [T_max][32]
+  const float* sin_t = nullptr;
+  uint16_t* q_out = nullptr;
+  uint16_t* kc = nullptr;
+  uint16_t* vc = nullptr;
+  int Hq = 0, Hkv = 0, T_max = 0;
+};
+
 struct GemvArgs {
-  int mode = 0;  // 0 store, 1 residual add into y, 2 fp32 logits + argmax parts
+  int mode = 0;  // 0 store, 1 residual add into y, 2 fp32 logits + argmax parts,
+                 // 3 QKV projection (store) + RoPE + KV-cache append
   const uint16_t* W = nullptr;
   const uint16_t* bias = nullptr;
   const uint16_t* x = nullptr;
@@ -36,6 +49,11 @@ struct GemvArgs {
   int32_t* part_idx = nullptr;
   int N = 0, K = 0, B = 1;
   int nblk = 1;  // grid.x (gemv_default_grid; wave row groups are grid-strided)
+  // mode 3 only (head_dim 64; N = (Hq + 2 Hkv) 64)
+  const int32_t* pos = nullptr;
+  const float *cos_t = nullptr, *sin_t = nullptr;
+  uint16_t *q_out = nullptr, *kc = nullptr, *vc = nullptr;
+  int Hq = 0, Hkv = 0, T_max = 0;
 };
 // grid.x for N rows in `mode` (the rows per wave group depend on the mode)
 int gemv_default_grid(int N, int mode);
@@ -91,15 +109,14 @@ void launch_moe(const MoeArgs& a, hipStream_t st);
 
 // ---- attention ------------------------------------------------------------------
 struct AttnArgs {
-  const uint16_t* q_src;  // rotated q [B][Hq][D], or raw qkv rows when fused
-  uint16_t *kc, *vc;      // [B][Hkv][T_max][D]
+  const uint16_t* q;      // rotated q [B][q_stride] (head h at h*D)
+  const uint16_t *kc, *vc;  // [B][Hkv][T_max][D], key pos already appended
   const uint16_t* sinks;  // [Hq]
   const int32_t* pos;     // [B]
-  const float *cos_t, *sin_t;
   uint16_t* out;          // [B][Hq*D]
   float* part_o;          // [B][Hq][S][D] split partials (scratch)
   float* part_ml;         // [B][Hq][S][2]
-  int B, Hq, Hkv, T_max, window, S, fused, q_stride;
+  int B, Hq, Hkv, T_max, window, S, q_stride;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
 // number of key splits used for a cache of T_max rows (window 0 = full layer)

@@ -484,7 +484,24 @@ __device__ __forceinline__ void argmax_steps(float& v, int32_t& i) {
   }
 }
 
-enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2 };
+enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2, MODE_QKV = 3 };
+
+// RoPE (HFM:149-231) on one (x1, x2) = (dim d, dim d + 32) pair of a head:
+// o1 = x1 c - x2 s, o2 = x2 c + x1 s, each product rounded.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,
+                                          float& o1, float& o2) {
+  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+  o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+}
+
+// Row r of wave group g.  MODE_QKV pairs dims d and d + 32 of one 64-dim
+// head (group g: head g / 32, d = g % 32) so that the RoPE pair of a q or k
+// head finishes in one wave; the other modes take R consecutive rows.
+template <int MODE, int R>
+__device__ __forceinline__ int group_row(int g, int r) {
+  if constexpr (MODE == MODE_QKV) return ((g >> 5) << 6) + (g & 31) + 32 * r;
+  else return g * R + r;
+}
 
 // xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
 // lanes of an xor pair hold the same sum after every step (fp32 addition
@@ -554,17 +571,24 @@ __device__ __forceinline__ void gemv_bf16_group(
     int g, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     uint16_t bias_first, float (&xr)[P][8], const XBf16Raw<P>& xraw, float eps,
     uint16_t* __restrict__ y, float* __restrict__ logits, int b, int N, int K,
-    int lane, float& best_v, int32_t& best_i) {
+    int lane, float& best_v, int32_t& best_i, const RopeArgs& rp, int p) {
   const int U = K / 8;
   constexpr int LS = 6 - log2_rows<R>();  // lane (1 << LS) r holds row r after the sum
   const int my_row = lane >> LS;
-  const int r0 = g * R, nr = min(R, N - r0);
+  const int r0 = g * R;
+  const int nr = MODE == MODE_QKV ? R : min(R, N - r0);  // QKV: N is a multiple of 64
   uint4 w[R][P];
 #pragma unroll
-  for (int r = 0; r < R; ++r) bf16_load_row<P>(w[r], W + (size_t)min(r0 + r, N - 1) * K, U, lane);
+  for (int r = 0; r < R; ++r)
+    bf16_load_row<P>(w[r], W + (size_t)min(group_row<MODE, R>(g, r), N - 1) * K, U, lane);
+  float rc = 0.0f, rs = 0.0f;  // RoPE cos / sin of dim g % 32 at position p
+  if (MODE == MODE_QKV) {
+    rc = load_pinned_f32(rp.cos_t + (size_t)p * 32 + (g & 31));
+    rs = load_pinned_f32(rp.sin_t + (size_t)p * 32 + (g & 31));
+  }
   uint16_t bias_b = bias_first;  // the first group's bias was loaded before x
   if (!FIRST && MODE != MODE_LOGITS && bias != nullptr)
-    bias_b = bias[r0 + min(my_row, nr - 1)];
+    bias_b = bias[group_row<MODE, R>(g, min(my_row, nr - 1))];
   if (FIRST) {
     __builtin_amdgcn_sched_barrier(0);  // all row loads issue before the norm's math
     wave_x_bf16_finish<P, NORM>(xr, xraw, eps, K, lane, nullptr);
@@ -580,9 +604,31 @@ __device__ __forceinline__ void gemv_bf16_group(
                          bf16_row_partial<P>(w[1], xr, U, lane), lane);
   else
     tot = wave_sum(bf16_row_partial<P>(w[0], xr, U, lane));
-  const int r = r0 + my_row;
+  const int r = group_row<MODE, R>(g, my_row);
   constexpr int kLead = (1 << LS) - 1;  // lanes with (lane & kLead) == 0 store
-  if (my_row < nr) {
+  if constexpr (MODE == MODE_QKV) {
+    // lanes 0-31 hold dim d of head g / 32, lanes 32-63 dim d + 32: the
+    // projection row is stored as is; q and k heads are rotated (the decode
+    // attention reads q from q_out) and k, v go to cache row p
+    const int head = g >> 5, dd = (g & 31) + 32 * my_row;
+    const uint16_t yv = f2bf(bias ? __fadd_rn(tot, bf2f(bias_b)) : tot);
+    const float yf = bf2f(yv);
+    const float other = xor_lane<32>(yf);
+    if ((lane & kLead) == 0) {
+      y[(size_t)b * N + r] = yv;
+      if (head < rp.Hq + rp.Hkv) {
+        float o1, o2;
+        rope_pair(my_row ? other : yf, my_row ? yf : other, rc, rs, o1, o2);
+        const uint16_t o = f2bf(my_row ? o2 : o1);
+        if (head < rp.Hq)
+          rp.q_out[((size_t)b * rp.Hq + head) * 64 + dd] = o;
+        else
+          rp.kc[(((size_t)b * rp.Hkv + head - rp.Hq) * rp.T_max + p) * 64 + dd] = o;
+      } else {
+        rp.vc[(((size_t)b * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p) * 64 + dd] = yv;
+      }
+    }
+  } else if (my_row < nr) {
     if (MODE == MODE_LOGITS) {
       if (tot > best_v) { best_v = tot; best_i = r; }  // rows rise within a lane
       if ((lane & kLead) == 0) logits[(size_t)b * N + r] = tot;
@@ -600,7 +646,8 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ y, float* __restrict__ logits,
-    float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K) {
+    float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K,
+    RopeArgs rp) {
   __shared__ float bv_s[4];
   __shared__ int32_t bi_s[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -612,9 +659,12 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   // waiting for them then does not wait for the rows (the vector-memory
   // counter drains in issue order).  Both loads are unconditional (clamped
   // addresses) so that no branch makes the compiler wait for everything.
+  const int p = MODE == MODE_QKV ? (int)load_pinned_u32(
+                                        reinterpret_cast<const uint32_t*>(rp.pos) + b)
+                                  : 0;
   uint16_t bias_first = 0;
   if (MODE != MODE_LOGITS) {
-    const int rb = min(g0 * R + (lane >> (6 - log2_rows<R>())), N - 1);
+    const int rb = min(group_row<MODE, R>(g0, lane >> (6 - log2_rows<R>())), N - 1);
     bias_first = (bias != nullptr ? bias : W)[rb];
   }
   float xr[P][8];
@@ -625,10 +675,10 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   int32_t best_i = 0x7fffffff;
   if (g0 < ngroups) {
     gemv_bf16_group<P, MODE, NORM, true, R>(g0, W, bias, bias_first, xr, xraw, eps, y,
-                                            logits, b, N, K, lane, best_v, best_i);
+                                            logits, b, N, K, lane, best_v, best_i, rp, p);
     for (int g = g0 + gstride; g < ngroups; g += gstride)
       gemv_bf16_group<P, MODE, NORM, false, R>(g, W, bias, 0, xr, xraw, eps, y, logits, b,
-                                               N, K, lane, best_v, best_i);
+                                               N, K, lane, best_v, best_i, rp, p);
   }
   if (MODE == MODE_LOGITS) {
     // lanes 64 r / R hold the wave's candidates: keep the larger value, the
@@ -653,17 +703,24 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
 template <int MODE>
 constexpr int gemv_rows() { return MODE == MODE_LOGITS ? 4 : (MODE == MODE_RESID ? 1 : 2); }
 
+static RopeArgs rope_args(const GemvArgs& a) {
+  RopeArgs r;
+  r.pos = a.pos; r.cos_t = a.cos_t; r.sin_t = a.sin_t; r.q_out = a.q_out;
+  r.kc = a.kc; r.vc = a.vc; r.Hq = a.Hq; r.Hkv = a.Hkv; r.T_max = a.T_max;
+  return r;
+}
+
 template <int P, int MODE>
 static void launch_gemv_bf16_p(const GemvArgs& a, hipStream_t st) {
   constexpr int R = gemv_rows<MODE>();
   if (a.norm_w != nullptr)
     hipLaunchKernelGGL((k_gemv_bf16<P, MODE, true, R>), dim3(a.nblk, 1, a.B), dim3(256),
                        0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
-                       a.part_val, a.part_idx, a.N, a.K);
+                       a.part_val, a.part_idx, a.N, a.K, rope_args(a));
   else
     hipLaunchKernelGGL((k_gemv_bf16<P, MODE, false, R>), dim3(a.nblk, 1, a.B), dim3(256),
                        0, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
-                       a.part_val, a.part_idx, a.N, a.K);
+                       a.part_val, a.part_idx, a.N, a.K, rope_args(a));
 }
 
 template <int MODE>
@@ -684,8 +741,9 @@ static void launch_gemv_bf16_m(const GemvArgs& a, hipStream_t st) {
 
 int gemv_default_grid(int N, int mode) {
   const int R = mode == MODE_LOGITS ? gemv_rows<MODE_LOGITS>()
-                                    : (mode == MODE_RESID ? gemv_rows<MODE_RESID>()
-                                                          : gemv_rows<MODE_STORE>());
+                : mode == MODE_RESID ? gemv_rows<MODE_RESID>()
+                : mode == MODE_QKV   ? gemv_rows<MODE_QKV>()
+                                     : gemv_rows<MODE_STORE>();
   const int ngroups = (N + R - 1) / R;
   const int nblk = (ngroups + 3) / 4;
   return nblk < 4096 ? nblk : 4096;  // lm_head: 4096 blocks measured 1% faster than 2048
@@ -695,6 +753,7 @@ void launch_gemv_bf16(const GemvArgs& a, hipStream_t st) {
   switch (a.mode) {
     case MODE_STORE: launch_gemv_bf16_m<MODE_STORE>(a, st); break;
     case MODE_RESID: launch_gemv_bf16_m<MODE_RESID>(a, st); break;
+    case MODE_QKV: launch_gemv_bf16_m<MODE_QKV>(a, st); break;
     default: launch_gemv_bf16_m<MODE_LOGITS>(a, st); break;
   }
 }
@@ -802,11 +861,6 @@ void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
 // (cos/sin [n_pos][D/2] fp32, HF modeling_rope_utils.py:429-483):
 //   o1 = x1 c - x2 s,  o2 = x2 c + x1 s   (each product and sum rounded)
 // ===========================================================================
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,
-                                          float& o1, float& o2) {
-  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
-}
 
 // In-place RoPE on x [n_tok][n_heads][D] with per-token positions.
 __global__ void k_rope_apply(uint16_t* __restrict__ x,
@@ -864,16 +918,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// A load that stays where it is written.  The compiler sinks a plain load
-// whose only use sits in a branch (a lane-0 epilogue) into that branch, where
-// it issues last and is waited for alone; a relaxed atomic load is never
-// moved, and at workgroup scope it is the same hardware load.
-__device__ __forceinline__ uint32_t load_pinned_u32(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ uint16_t load_pinned_u16(const uint16_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
 
 __device__ __forceinline__ float readlane_f(float v, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
@@ -1342,19 +1386,19 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 //     den = exp(sink - M); f_s = exp(m_s - M) (0 for empty splits);
 //     den = fmaf(l_s, f_s, den); acc = fmaf(f_s, o_s, acc); out = bf16(acc * (1/den))
 //
-// k_attn_split: grid (Hkv S, B), block 64 G (G = Hq / Hkv query heads per kv
-// head).  Block (g, s) serves split s of kv head g for all G query heads of
-// the group: each 64-key chunk of K and V is loaded from HBM once into LDS
-// (one 16-byte word per thread) and read by the G waves, one wave per query
-// head.  The words of two chunks are in flight at once: both first tiles are
-// staged before the loop, then chunk c + 2 loads while chunk c is computed.
-// K rows sit in LDS with their eight 16-byte words
-// rotated by the key index, so the 64 lanes of a wave, one key each, read
-// distinct banks.  Each wave writes its split's (o, m, l) partial; the last
-// split always holds key pos, so with fused != 0 (q_src = raw qkv rows) the
-// block of split S - 1 rotates the new k row (YaRN table), uses its own LDS
-// copy of the new k/v row for key pos and appends it to the caches; every
-// block rotates its q heads.
+// k_attn_split: grid (Hkv NHB S, B) with NHB = G / HB (G = Hq / Hkv query
+// heads per kv head), block 64 max(HB, 4).  Block (g, hb, s) serves split s
+// of kv head g for the HB query heads g G + hb HB + w, one wave each: each
+// 64-key chunk of K and V is loaded from HBM once per block into LDS (one
+// 16-byte word per thread) and read by its HB waves.  HB = G shares a chunk
+// among all heads of the group (many splits); HB = 1 spreads a one-split span
+// (the sliding window) over G times more CUs.  The words of two chunks are in
+// flight at once: both first tiles are staged before the loop, then chunk
+// c + 2 loads while chunk c is computed.  K rows sit in LDS with their eight
+// 16-byte words rotated by the key index, so the 64 lanes of a wave, one key
+// each, read distinct banks.  q is rotated and k / v of position pos are in
+// the cache already (the QKV projection writes them).  Each wave writes its
+// split's (o, m, l) partial, or with one split the finished output.
 // k_attn_merge: grid (Hq, B), 64 lanes (lane = output dim), merges the S
 // partials of a head in split order with the sink.
 // ===========================================================================
@@ -1363,30 +1407,24 @@ constexpr int kMaxSplits = 32;
 
 // Words of the 64-key chunk starting at key CB: word WD = 8 j + ch is
 // 16-byte word ch of key CB + j; a thread owns words tid and tid + nt
-// (nt >= 256).  Keys past p read as zero; key p_lds is taken from LDS at
-// store time.  (Macros on plain locals: the words stay in registers while
-// the loads are in flight.)
+// (nt >= 256).  Keys past p read as zero.  (Macros on plain locals: the
+// words stay in registers while the loads are in flight.)
 #define ATTN_LOAD_WORD(KW, VW, WD, CB)                                          \
   do {                                                                          \
     KW = make_uint4(0, 0, 0, 0);                                                \
     VW = make_uint4(0, 0, 0, 0);                                                \
     const int key_ = (CB) + ((WD) >> 3);                                        \
-    if ((WD) < 512 && key_ <= p && key_ != p_lds) {                             \
+    if ((WD) < 512 && key_ <= p) {                                              \
       KW = reinterpret_cast<const uint4*>(kc + (kv_base + key_) * kD)[(WD) & 7]; \
       VW = reinterpret_cast<const uint4*>(vc + (kv_base + key_) * kD)[(WD) & 7]; \
     }                                                                           \
   } while (0)
-#define ATTN_STORE_WORD(KW, VW, WD, CB, BUF)                                    \
+#define ATTN_STORE_WORD(KW, VW, WD, BUF)                                        \
   do {                                                                          \
     if ((WD) < 512) {                                                           \
       const int j_ = (WD) >> 3, ch_ = (WD) & 7;                                 \
-      if ((CB) + j_ == p_lds) { /* two stores, not a select of addresses */    \
-        kt[BUF][j_ * 8 + ((ch_ + j_) & 7)] = knew[ch_];                         \
-        vt[BUF][j_ * 8 + ch_] = vnew[ch_];                                      \
-      } else {                                                                  \
-        kt[BUF][j_ * 8 + ((ch_ + j_) & 7)] = (KW);                              \
-        vt[BUF][j_ * 8 + ch_] = (VW);                                           \
-      }                                                                         \
+      kt[BUF][j_ * 8 + ((ch_ + j_) & 7)] = (KW);                                \
+      vt[BUF][j_ * 8 + ch_] = (VW);                                             \
     }                                                                           \
   } while (0)
 
@@ -1420,35 +1458,36 @@ __device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o
 }
 
 __global__ __launch_bounds__(512) void k_attn_split(
-    const uint16_t* __restrict__ q_src, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
-    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv,
-    int G, int T_max, int window, int S, int fused, int q_stride) {
+    int G, int HB, int T_max, int window, int S, int q_stride) {
   __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
   __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
   __shared__ __align__(16) float qs[8][kD];
   __shared__ float ps[8][64];
-  __shared__ __align__(16) uint4 knew[kD / 8], vnew[kD / 8];
-  // blockDim = 64 max(G, 4): waves w >= G only help stage the tiles
+  // blockDim = 64 max(HB, 4): waves w >= HB only help stage the tiles
   const int nt = blockDim.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const bool active = w < G;
-  const int g = blockIdx.x % Hkv, s = blockIdx.x / Hkv, b = blockIdx.y;
-  const int h = g * G + (active ? w : 0);
+  const bool active = w < HB;
+  const int NHB = G / HB;
+  const int g = blockIdx.x % Hkv, hb = (blockIdx.x / Hkv) % NHB, s = blockIdx.x / (Hkv * NHB);
+  const int b = blockIdx.y;
+  const int h = g * G + hb * HB + (active ? w : 0);
+  // q first (it does not depend on the position), then the position
+  const uint16_t qv = q[(size_t)b * q_stride + (size_t)h * kD + lane];
+  const uint16_t sink_raw = load_pinned_u16(sinks + h);  // used at the end (one split)
   const int p = pos_arr[b];
   const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
   const int n = p - lo + 1;
   const int nch = (n + 63) >> 6;
   const int c0 = (int)((int64_t)s * nch / S), c1 = (int)((int64_t)(s + 1) * nch / S);
   const size_t kv_base = ((size_t)b * Hkv + g) * T_max;
-  const bool last = s == S - 1;
-  const int p_lds = (fused && last) ? p : -1;  // key served from LDS
 
-  // the first two chunks' words into registers (key p comes from LDS
-  // later): both tiles are staged before the loop, so a split of two chunks
-  // (the 128-key sliding window) never waits for memory inside it
+  // the first two chunks' words into registers: both tiles are staged before
+  // the loop, so a split of two chunks (the 128-key sliding window) never
+  // waits for memory inside it
   uint4 nk0, nk1, nv0, nv1;  // chunk c0, later the chunk two ahead
   uint4 pk0, pk1, pv0, pv1;  // chunk c0 + 1
   if (c0 < c1) {
@@ -1459,51 +1498,27 @@ __global__ __launch_bounds__(512) void k_attn_split(
     ATTN_LOAD_WORD(pk0, pv0, tid, lo + (c0 + 1) * 64);
     ATTN_LOAD_WORD(pk1, pv1, tid + nt, lo + (c0 + 1) * 64);
   }
-
-  // ---- q heads (and the new k/v row for the last split) into LDS ----------
-  {
-    const uint16_t* qrow = q_src + (size_t)b * q_stride;
-    if (fused) {
-      const float* cr = cos_t + (size_t)p * (kD / 2);
-      const float* sr = sin_t + (size_t)p * (kD / 2);
-      if (active && lane < kD / 2) {
-        const uint16_t* qh = qrow + (size_t)h * kD;
-        float o1, o2;
-        rope_pair(bf2f(qh[lane]), bf2f(qh[lane + kD / 2]), cr[lane], sr[lane], o1, o2);
-        qs[w][lane] = bf2f(f2bf(o1));
-        qs[w][lane + kD / 2] = bf2f(f2bf(o2));
-      } else if (last && w == 0) {
-        const int t = lane - kD / 2;
-        const uint16_t* kh = qrow + (size_t)(Hq + g) * kD;
-        float o1, o2;
-        rope_pair(bf2f(kh[t]), bf2f(kh[t + kD / 2]), cr[t], sr[t], o1, o2);
-        uint16_t* kn16 = reinterpret_cast<uint16_t*>(knew);
-        kn16[t] = f2bf(o1);
-        kn16[t + kD / 2] = f2bf(o2);
-        const uint32_t* vh =
-            reinterpret_cast<const uint32_t*>(qrow + (size_t)(Hq + Hkv + g) * kD);
-        reinterpret_cast<uint32_t*>(vnew)[t] = vh[t];
-      }
-    } else if (active) {
-      qs[w][lane] = bf2f(qrow[(size_t)h * kD + lane]);
-    }
-  }
-  __syncthreads();
-  if (fused && last && tid < kD / 8) {
-    reinterpret_cast<uint4*>(kc + (kv_base + p) * kD)[tid] = knew[tid];
-    reinterpret_cast<uint4*>(vc + (kv_base + p) * kD)[tid] = vnew[tid];
-  }
+  if (active) qs[w][lane] = bf2f(qv);
   if (c0 < c1) {
-    ATTN_STORE_WORD(nk0, nv0, tid, lo + c0 * 64, 0);
-    ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + c0 * 64, 0);
+    ATTN_STORE_WORD(nk0, nv0, tid, 0);
+    ATTN_STORE_WORD(nk1, nv1, tid + nt, 0);
   }
   if (c0 + 1 < c1) {
-    ATTN_STORE_WORD(pk0, pv0, tid, lo + (c0 + 1) * 64, 1);
-    ATTN_STORE_WORD(pk1, pv1, tid + nt, lo + (c0 + 1) * 64, 1);
+    ATTN_STORE_WORD(pk0, pv0, tid, 1);
+    ATTN_STORE_WORD(pk1, pv1, tid + nt, 1);
   }
   __syncthreads();
 
-  const float4* q4 = reinterpret_cast<const float4*>(qs[w]);
+  // q of this wave's head in registers (one LDS pass for all chunks)
+  float qf[kD];
+  {
+    const float4* q4 = reinterpret_cast<const float4*>(qs[w]);
+#pragma unroll
+    for (int i = 0; i < kD / 4; ++i) {
+      const float4 v = q4[i];
+      qf[4 * i] = v.x; qf[4 * i + 1] = v.y; qf[4 * i + 2] = v.z; qf[4 * i + 3] = v.w;
+    }
+  }
   float m = -INFINITY, l = 0.0f, o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = 0.0f;
@@ -1517,49 +1532,52 @@ __global__ __launch_bounds__(512) void k_attn_split(
     }
     const int cb = lo + c * 64;
     if (active) {
-    const bool valid = cb + lane <= p;
-    float a = 0.0f;
+      const bool valid = cb + lane <= p;
+      // the key row of this lane: all eight words first, then the chain
+      uint4 kw[kD / 8];
 #pragma unroll
-    for (int u = 0; u < kD / 8; ++u) {
-      float kf[8];
-      unpack8(kt[buf][lane * 8 + ((u + lane) & 7)], kf);
-      const float4 qa = q4[2 * u], qb = q4[2 * u + 1];
-      a = __builtin_fmaf(qa.x, kf[0], a);
-      a = __builtin_fmaf(qa.y, kf[1], a);
-      a = __builtin_fmaf(qa.z, kf[2], a);
-      a = __builtin_fmaf(qa.w, kf[3], a);
-      a = __builtin_fmaf(qb.x, kf[4], a);
-      a = __builtin_fmaf(qb.y, kf[5], a);
-      a = __builtin_fmaf(qb.z, kf[6], a);
-      a = __builtin_fmaf(qb.w, kf[7], a);
-    }
-    const float sc = valid ? __fmul_rn(a, 0.125f) : -INFINITY;  // 1/sqrt(64), HFM:277
-    const float mn = fmaxf(m, wave_max(sc));
-    const float alpha = neon_expf(__fsub_rn(m, mn));
-    const float pj = valid ? neon_expf(__fsub_rn(sc, mn)) : 0.0f;
-    l = __builtin_fmaf(l, alpha, wave_sum(pj));
-    m = mn;
+      for (int u = 0; u < kD / 8; ++u) kw[u] = kt[buf][lane * 8 + ((u + lane) & 7)];
+      float a = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], alpha);
-    ps[w][lane] = pj;
-    wave_lds_sync();
+      for (int u = 0; u < kD / 8; ++u) {
+        float kf[8];
+        unpack8(kw[u], kf);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int jj = kg + 8 * i;
-      if (cb + jj <= p) {
-        float vf[8];
-        unpack8(vt[buf][jj * 8 + dq], vf);
-        const float pv = ps[w][jj];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pv, vf[e], o[e]);
+        for (int e = 0; e < 8; ++e) a = __builtin_fmaf(qf[8 * u + e], kf[e], a);
       }
-    }
+      const float sc = valid ? __fmul_rn(a, 0.125f) : -INFINITY;  // 1/sqrt(64), HFM:277
+      const float mn = fmaxf(m, wave_max(sc));
+      const float alpha = neon_expf(__fsub_rn(m, mn));
+      const float pj = valid ? neon_expf(__fsub_rn(sc, mn)) : 0.0f;
+      l = __builtin_fmaf(l, alpha, wave_sum(pj));
+      m = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], alpha);
+      // p of key j at (j % 8) * 8 + j / 8: lane (kg, dq) reads its keys
+      // kg + 8 i as eight consecutive floats
+      ps[w][(lane & 7) * 8 + (lane >> 3)] = pj;
+      wave_lds_sync();
+      uint4 vw[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) vw[i] = vt[buf][(kg + 8 * i) * 8 + dq];
+      const float4 pa = *reinterpret_cast<const float4*>(&ps[w][kg * 8]);
+      const float4 pb = *reinterpret_cast<const float4*>(&ps[w][kg * 8 + 4]);
+      const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+      // keys past p have p = 0 and zero words: fmaf(0, 0, o) == o exactly
+      // (o is never -0), so they need no branch
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float vf[8];
+        unpack8(vw[i], vf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(pv[i], vf[e], o[e]);
+      }
     }  // active
     __syncthreads();  // tile buf and ps are consumed
     if (c + 2 < c1) {  // visible to the readers of iteration c + 2 after the
                        // barrier that ends iteration c + 1
-      ATTN_STORE_WORD(nk0, nv0, tid, lo + (c + 2) * 64, buf);
-      ATTN_STORE_WORD(nk1, nv1, tid + nt, lo + (c + 2) * 64, buf);
+      ATTN_STORE_WORD(nk0, nv0, tid, buf);
+      ATTN_STORE_WORD(nk1, nv1, tid + nt, buf);
     }
   }
   if (!active) return;
@@ -1576,7 +1594,7 @@ __global__ __launch_bounds__(512) void k_attn_split(
     // one split: the merge with the sink happens here, with exactly the
     // operations k_attn_merge applies to a single partial
     if (kg == 0) {
-      const float sk = bf2f(sinks[h]);
+      const float sk = bf2f(sink_raw);
       const float M = fmaxf(sk, m);
       float den = neon_expf(__fsub_rn(sk, M));
       const float f = (m == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(m, M));
@@ -1615,10 +1633,13 @@ __global__ __launch_bounds__(64) void k_attn_merge(
 
 void launch_attn(const AttnArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;  // 1, 2, 4 or 8 (checked on the host)
-  hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * a.S, a.B), dim3(64 * (G < 4 ? 4 : G)),
-                     0, st, a.q_src, a.kc, a.vc, a.pos, a.cos_t, a.sin_t, a.part_o,
-                     a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G, a.T_max, a.window, a.S,
-                     a.fused, a.q_stride);
+  // one split: a block per query head (more CUs for a short span); several:
+  // a block per (kv head, split) serving the whole group
+  const int HB = a.S == 1 ? 1 : G;
+  hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * (G / HB) * a.S, a.B),
+                     dim3(64 * (HB < 4 ? 4 : HB)), 0, st, a.q, a.kc, a.vc, a.pos,
+                     a.part_o, a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G, HB, a.T_max,
+                     a.window, a.S, a.q_stride);
   if (a.S > 1)  // one split finishes in the split kernel
     hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
                        a.part_ml, a.sinks, a.out, a.Hq, a.S);
