@@ -8,8 +8,10 @@ The first form reads a kernel trace; the second averages each counter per
 dispatch and kernel name (rocprofv3 --pmc output, e.g. FETCH_SIZE and
 WRITE_SIZE in KiB per dispatch).
 
-Keeps the last K decode steps (K * N dispatches, N = 1 + 7 n_layers + 2 for
-the gpt-oss step), groups the dispatches by kernel name and prints a Markdown
+Keeps the last K decode steps (K * N dispatches; the gpt-oss step has
+N = 1 + 6 n_layers + (one attention merge per layer with several key splits)
++ 2, i.e. 159 at the 20b shape with a 4096-row cache), groups the dispatches
+by kernel name and prints a Markdown
 table: calls per step, average duration, share of step time, and -- for the
 kernels given algorithmic bytes per launch -- achieved GB/s.
 """
