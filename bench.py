@@ -187,6 +187,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--batch", type=int, default=1,
+                    help="sequences decoded together (the headline metric is batch 1; "
+                         "larger batches are reported as a separate line)")
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -213,35 +216,38 @@ def main():
     if args.moe_only:
         moe_only(ne, torch, args)
         return
+    B = args.batch
     max_seq = args.prompt + args.warmup + args.steps + 8
-    cfg = ne.config_preset("gpt-oss-20b", max_seq=max_seq, max_batch=1)
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=max_seq, max_batch=B)
     log(f"[bench] creating gpt-oss-20b context (max_seq {max_seq})")
     eng = ne.Engine(cfg, device=0)
     stream = torch.cuda.current_stream()
     eng.init_random(args.seed, stream)
     rng = np.random.default_rng(args.seed)
-    prompt = rng.integers(0, cfg.vocab, size=(1, args.prompt), dtype=np.int64)
+    prompt = rng.integers(0, cfg.vocab, size=(B, args.prompt), dtype=np.int64)
     t0 = time.perf_counter()
     eng.prefill(prompt, stream)  # first pass: allocates prefill scratch, captures the step
     torch.cuda.synchronize()
     log(f"[bench] prompt of {args.prompt} tokens (first, untimed pass): "
         f"{time.perf_counter() - t0:.2f}s")
-    # timed prompt pass (batched: rows 0..P-2 on the matrix cores, then one decode step)
-    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    pt0 = time.perf_counter()
-    p0.record(stream)
-    eng.prefill(prompt, stream)
-    p1.record(stream)
-    torch.cuda.synchronize()
-    pre_s = max(time.perf_counter() - pt0, p0.elapsed_time(p1) * 1e-3)
-    # the library's default prompt mode is stepwise (every prompt token through
-    # the decode graph); the batched matrix-core pass is switched off for now
-    prefill = {"tokens": args.prompt, "ms": round(pre_s * 1e3, 3),
-               "tokens_per_s": round(args.prompt / pre_s, 1),
-               "mode": "stepwise (teacher-forced decode steps)",
-               "flop_batched_form": prefill_flops(cfg, args.prompt)}
-    log(f"[bench] prompt pass: {pre_s * 1e3:.1f} ms = {args.prompt / pre_s:.0f} tok/s")
+    prefill = None
+    if B == 1:
+        # timed prompt pass; the library's default prompt mode is stepwise
+        # (every prompt token through the decode graph); the batched
+        # matrix-core pass is switched off for now
+        p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        pt0 = time.perf_counter()
+        p0.record(stream)
+        eng.prefill(prompt, stream)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        pre_s = max(time.perf_counter() - pt0, p0.elapsed_time(p1) * 1e-3)
+        prefill = {"tokens": args.prompt, "ms": round(pre_s * 1e3, 3),
+                   "tokens_per_s": round(args.prompt / pre_s, 1),
+                   "mode": "stepwise (teacher-forced decode steps)",
+                   "flop_batched_form": prefill_flops(cfg, args.prompt)}
+        log(f"[bench] prompt pass: {pre_s * 1e3:.1f} ms = {args.prompt / pre_s:.0f} tok/s")
     eng.decode(args.warmup, stream)
     torch.cuda.synchronize()
     log(f"[bench] warm-up {args.warmup} steps done")
@@ -256,25 +262,25 @@ def main():
     wall = time.perf_counter() - t0
     gpu_s = e0.elapsed_time(e1) * 1e-3
     elapsed = max(wall, gpu_s)
-    tok_s = args.steps / elapsed
+    tok_s = B * args.steps / elapsed  # whole-job tokens (B sequences)
     kv0 = args.prompt + args.warmup
     kv_mid = kv0 + args.steps // 2
     bpt = step_bytes(cfg, kv_mid)
-    log(f"[bench] {args.steps} steps in {elapsed * 1e3:.1f} ms -> {tok_s:.1f} tok/s "
-        f"({bpt * tok_s / 1e9:.0f} GB/s algorithmic)")
+    log(f"[bench] {args.steps} steps x batch {B} in {elapsed * 1e3:.1f} ms -> {tok_s:.1f} tok/s"
+        + (f" ({bpt * tok_s / 1e9:.0f} GB/s algorithmic)" if B == 1 else ""))
     toks = eng.read_tokens(args.prompt, 8)
     log(f"[bench] first generated ids {toks[0].tolist()}")
 
     mb = moe_bytes(cfg)
     moe_s = moe_gbs = None
-    if args.moe_reps > 0:  # 0 skips it (profiling runs that want only the decode loop)
+    if args.moe_reps > 0 and B == 1:  # 0 skips it (profiling runs that want only the decode loop)
         moe_s = time_moe(ne, torch, eng, cfg, args.moe_reps)
         moe_gbs = mb / moe_s / 1e9
         log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, {moe_gbs:.0f} GB/s")
     eng.close()
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and B == 1:
         log("[bench] CPU baseline (build's oracle) ...")
         cpu = cpu_baseline(args.seed, 4, args.cpu_steps)
         log(f"[bench] CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads")
@@ -292,13 +298,14 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16 activations, mxfp4 experts, fp32 accumulate",
         "data": "synthetic (random-init weights, uniform random prompt ids)",
-        "config": {"workload": "gpt-oss-20b-shaped greedy decode, batch 1, after a "
+        "config": {"workload": f"gpt-oss-20b-shaped greedy decode, batch {B}, after a "
                                f"{args.prompt}-token prompt (BASELINE config 3)",
-                   "batch": 1, "prompt": args.prompt,
+                   "batch": B, "prompt": args.prompt,
                    "kv_len": [kv0, kv0 + args.steps], "parallelism": "none (1 GPU)"},
-        "step_bytes_per_token": bpt,
-        "step_hbm_gbs": round(bpt * tok_s / 1e9, 1),
-        "step_hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBS, 4),
+        # bytes per token of a batch-1 step (at batch > 1 weights are shared)
+        "step_bytes_per_token": bpt if B == 1 else None,
+        "step_hbm_gbs": round(bpt * tok_s / 1e9, 1) if B == 1 else None,
+        "step_hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBS, 4) if B == 1 else None,
         "roofline": {"kernel": "MoE expert FFN (k_moe_gate_up + k_moe_down), batch 1, 4 experts",
                      "bound": "hbm", "achieved": moe_gbs and round(moe_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",

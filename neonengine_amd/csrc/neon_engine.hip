@@ -368,6 +368,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   HIPCHK(ctx, hipMemcpy(ctx->sin_t, st.data(), st.size() * 4, hipMemcpyHostToDevice));
   HIPCHK(ctx, hipDeviceSynchronize());
   HIPCHK(ctx, hipStreamCreateWithFlags(&ctx->cap_stream, hipStreamNonBlocking));
+  HIPCHK(ctx, gemv_batched_prepare());
   return NEON_OK;
 }
 
@@ -536,6 +537,19 @@ extern "C" neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name,
 // the decode step: 1 + 6 L + 2 kernels, all reading positions from device
 // memory so one captured graph serves every step.
 // ---------------------------------------------------------------------------
+// One projection of the step: the batch-1 kernel, or for B >= 2 the batched
+// kernel that reads each weight row once for all rows (same bits).  Returns
+// the grid width (the lm_head argmax partials per row).
+static int launch_gemv_step(GemvArgs& a, int B, hipStream_t st) {
+  if (B >= 2 && gemv_batched_supported(a)) {
+    a.nblk = gemv_bt_grid(a.N, a.mode);
+    (void)launch_gemv_bf16_batched(a, st);  // launch errors surface at hipGetLastError
+    return a.nblk;
+  }
+  launch_gemv_bf16(a, st);
+  return a.nblk;
+}
+
 static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
   const neon_config& c = ctx->cfg;
   const int H = c.hidden, D = c.head_dim;
@@ -554,7 +568,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     q.nblk = gemv_default_grid(q.N, q.mode);
     q.pos = ctx->pos; q.cos_t = ctx->cos_t; q.sin_t = ctx->sin_t; q.q_out = ctx->q_rot;
     q.kc = kc_l; q.vc = vc_l; q.Hq = c.n_heads; q.Hkv = c.n_kv_heads; q.T_max = c.max_seq;
-    launch_gemv_bf16(q, st);
+    launch_gemv_step(q, B, st);
     AttnArgs a;
     a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
     a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml;
@@ -566,7 +580,7 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
     o.N = H; o.K = c.n_heads * D; o.B = B;
     o.nblk = gemv_default_grid(o.N, o.mode);
-    launch_gemv_bf16(o, st);
+    launch_gemv_step(o, B, st);
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
@@ -587,8 +601,8 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
   lm.eps = c.rms_eps; lm.logits = ctx->logits; lm.part_val = ctx->lm_part_val;
   lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab; lm.K = H; lm.B = B;
   lm.nblk = ctx->lm_nblk;
-  launch_gemv_bf16(lm, st);
-  launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, ctx->lm_nblk,
+  const int lm_parts = launch_gemv_step(lm, B, st);
+  launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, lm_parts,
                         ctx->tokens, ctx->tok_stride, ctx->pos, ctx->prompt_len,
                         ctx->last_ids, B, st);
 }

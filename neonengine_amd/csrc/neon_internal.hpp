@@ -58,6 +58,16 @@ struct GemvArgs {
 // grid.x for N rows in `mode` (the rows per wave group depend on the mode)
 int gemv_default_grid(int N, int mode);
 void launch_gemv_bf16(const GemvArgs& a, hipStream_t st);
+// B >= 2: every weight row read once for up to 16 batch rows (K = 2880 or
+// 4096; nblk from gemv_bt_grid).  Outputs bit-identical to launch_gemv_bf16.
+hipError_t launch_gemv_bf16_batched(const GemvArgs& a, hipStream_t st);
+// shapes and modes the batched kernel covers (QKV and lm_head with RMSNorm,
+// O without; K / 8 units in 1, 2, 3, 4, 6 or 8 passes of 64)
+bool gemv_batched_supported(const GemvArgs& a);
+// opts the batched kernels in to their LDS size (once per device, outside
+// any stream capture)
+hipError_t gemv_batched_prepare();
+int gemv_bt_grid(int N, int mode);
 
 void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
                            int nparts, int32_t* tokens, int tok_stride,

@@ -772,6 +772,290 @@ void launch_gemv_bf16(const GemvArgs& a, hipStream_t st) {
 }
 
 // ===========================================================================
+// Batched bf16 GEMV (2 <= B): every weight row is read from HBM once per step
+// and dotted with up to BT inputs held in LDS.  Block = 8 waves; its rows
+// b0 .. b0 + BT - 1 are RMS-normalised (or copied) into LDS as bf16 units
+// first (waves w and w + 8 of the row index), then the waves grid-stride
+// over groups of R weight rows.
+//
+// Every (row, b) total is the canonical one of the batch-1 kernel: lane l
+// accumulates its units u = l + 64 p in order with 8 fmaf each, and the R BT
+// lane partials are reduced by one multi-value xor butterfly (bit-identical
+// to R BT separate butterflies, see wave_sum_nvals), so batch b's outputs
+// equal a batch-1 step's bit for bit.
+// ===========================================================================
+
+// xor butterfly (off = 32 .. 1) of N values at once: at each step a lane keeps
+// half of its values and sends the other half (fp32 addition commutes, so
+// both lanes of a pair hold the same sums); lane l returns value
+// l >> (6 - log2 N) when N <= 64.
+template <int N, int OFF = 32>
+__device__ __forceinline__ float wave_sum_nvals(const float (&a)[N], int lane) {
+  if constexpr (N == 1) {
+    if constexpr (OFF >= 1) return wave_sum<OFF>(a[0]);
+    else return a[0];
+  } else {
+    static_assert(OFF >= 1, "wave_sum_nvals: at most 64 values");
+    const bool up = (lane & OFF) != 0;
+    float h[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i)
+      h[i] = __fadd_rn(up ? a[i + N / 2] : a[i], xor_lane<OFF>(up ? a[i] : a[i + N / 2]));
+    return wave_sum_nvals<N / 2, OFF / 2>(h, lane);
+  }
+}
+
+template <int N>
+constexpr int log2_n() { return N <= 1 ? 0 : 1 + log2_n<N / 2>(); }
+
+template <int P, int MODE, bool NORM, int R, int BT>
+__global__ __launch_bounds__(512) void k_gemv_bf16_bt(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
+    uint16_t* __restrict__ y, float* __restrict__ logits,
+    float* __restrict__ part_val, int32_t* __restrict__ part_idx, int N, int K, int B,
+    RopeArgs rp) {
+  extern __shared__ __align__(16) uint4 xs[];  // [BT][U] normalised inputs (bf16 units)
+  __shared__ float bv_s[8][BT];
+  __shared__ int32_t bi_s[8][BT];
+  constexpr int NV = R * BT;                    // values per lane group
+  constexpr int LS = 6 - log2_n<NV>();          // lane (1 << LS) v holds value v
+  static_assert(NV <= 64, "R * BT must be at most 64");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int U = K / 8;
+  const int b0 = blockIdx.z * BT;
+  // ---- inputs into LDS ----------------------------------------------------
+  for (int bb = wave; bb < BT; bb += 8) {
+    const int b = b0 + bb;
+    if (b < B) {
+      XBf16Raw<P> raw;
+      float xr[P][8];
+      wave_x_bf16_issue<P, NORM>(raw, x + (size_t)b * K, nw, K, lane);
+      wave_x_bf16_finish<P, NORM>(xr, raw, eps, K, lane, nullptr);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int u = lane + 64 * p;
+        if (u < U)
+          xs[bb * U + u] = make_uint4(pack_bf2(xr[p][0], xr[p][1]), pack_bf2(xr[p][2], xr[p][3]),
+                                      pack_bf2(xr[p][4], xr[p][5]), pack_bf2(xr[p][6], xr[p][7]));
+      }
+    } else {
+      for (int u = lane; u < U; u += 64) xs[bb * U + u] = make_uint4(0, 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  // the value this lane holds after the butterfly: (row r, batch row bb)
+  const int v_l = lane >> LS, r_l = v_l / BT, bb_l = v_l % BT, b_l = b0 + bb_l;
+  const bool lead = (lane & ((1 << LS) - 1)) == 0 && b_l < B;
+  const int p_l = MODE == MODE_QKV ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.pos) +
+                                                          min(b_l, B - 1))
+                                   : 0;
+  float best_v = -INFINITY;
+  int32_t best_i = 0x7fffffff;
+  const int ngroups = (N + R - 1) / R;
+  for (int g = blockIdx.x * 8 + wave; g < ngroups; g += gridDim.x * 8) {
+    uint4 w[R][P];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      bf16_load_row<P>(w[r], W + (size_t)min(group_row<MODE, R>(g, r), N - 1) * K, U, lane);
+    const int row_l = group_row<MODE, R>(g, r_l);
+    uint16_t bias_l = 0;
+    if (MODE != MODE_LOGITS && bias != nullptr) bias_l = load_pinned_u16(bias + min(row_l, N - 1));
+    float rc = 0.0f, rs = 0.0f;
+    if (MODE == MODE_QKV) {
+      rc = load_pinned_f32(rp.cos_t + (size_t)p_l * 32 + (g & 31));
+      rs = load_pinned_f32(rp.sin_t + (size_t)p_l * 32 + (g & 31));
+    }
+    float acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const bool in = lane + 64 * p < U;  // padded units leave the sums untouched
+      const int u = min(lane + 64 * p, U - 1);
+      float wf[R][8];  // the R rows' unit p, unpacked once for all BT inputs
+#pragma unroll
+      for (int r = 0; r < R; ++r) unpack8(w[r][p], wf[r]);
+#pragma unroll
+      for (int b4 = 0; b4 < BT; b4 += 4) {
+        // four inputs at a time; the barrier keeps the scheduler from hoisting
+        // every LDS read of the unit (BT x 4 registers) ahead of the math
+        constexpr int NB = BT < 4 ? BT : 4;
+        uint4 xv[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) xv[i] = xs[(b4 + i) * U + u];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          float xf[8];
+          unpack8(xv[i], xf);
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float t = acc[r * BT + b4 + i];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t = __builtin_fmaf(wf[r][e], xf[e], t);
+            acc[r * BT + b4 + i] = in ? t : acc[r * BT + b4 + i];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    const float tot = wave_sum_nvals<NV>(acc, lane);
+    if constexpr (MODE == MODE_QKV) {
+      // R = 2: lanes with r_l = 0 hold dim d, r_l = 1 dim d + 32 of head g / 32
+      const int head = g >> 5, dd = (g & 31) + 32 * r_l;
+      const uint16_t yv = f2bf(bias ? __fadd_rn(tot, bf2f(bias_l)) : tot);
+      const float yf = bf2f(yv);
+      const float other = xor_lane<32>(yf);
+      if (lead) {
+        y[(size_t)b_l * N + row_l] = yv;
+        if (head < rp.Hq + rp.Hkv) {
+          float o1, o2;
+          rope_pair(r_l ? other : yf, r_l ? yf : other, rc, rs, o1, o2);
+          const uint16_t o = f2bf(r_l ? o2 : o1);
+          if (head < rp.Hq)
+            rp.q_out[((size_t)b_l * rp.Hq + head) * 64 + dd] = o;
+          else
+            rp.kc[(((size_t)b_l * rp.Hkv + head - rp.Hq) * rp.T_max + p_l) * 64 + dd] = o;
+        } else {
+          rp.vc[(((size_t)b_l * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p_l) * 64 + dd] = yv;
+        }
+      }
+    } else if constexpr (MODE == MODE_LOGITS) {
+      if (row_l < N) {
+        if (tot > best_v) { best_v = tot; best_i = row_l; }  // rows rise within a lane
+        if (lead) logits[(size_t)b_l * N + row_l] = tot;
+      }
+    } else {
+      if (lead && row_l < N) {
+        const float v = bias ? __fadd_rn(tot, bf2f(bias_l)) : tot;
+        const size_t o = (size_t)b_l * N + row_l;
+        if (MODE == MODE_STORE) y[o] = f2bf(v);
+        else y[o] = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
+      }
+    }
+  }
+  if constexpr (MODE == MODE_LOGITS) {
+    // lanes with r_l = 0 (lane < 64 / R) end with their batch row's best
+    argmax_steps<64 / R, 32>(best_v, best_i);
+    if (lane < 64 / R && (lane & ((1 << LS) - 1)) == 0) { bv_s[wave][bb_l] = best_v; bi_s[wave][bb_l] = best_i; }
+    __syncthreads();
+    if (threadIdx.x < BT && b0 + (int)threadIdx.x < B) {
+      const int bb = threadIdx.x;
+      float v = bv_s[0][bb];
+      int32_t i = bi_s[0][bb];
+      for (int w8 = 1; w8 < 8; ++w8)
+        if (bv_s[w8][bb] > v || (bv_s[w8][bb] == v && bi_s[w8][bb] < i)) { v = bv_s[w8][bb]; i = bi_s[w8][bb]; }
+      part_val[(size_t)(b0 + bb) * gridDim.x + blockIdx.x] = v;
+      part_idx[(size_t)(b0 + bb) * gridDim.x + blockIdx.x] = i;
+    }
+  }
+}
+
+template <int MODE>
+constexpr int gemv_bt_rows() { return 2; }  // R BT <= 32 values per lane group
+
+// inputs per block for a batch of B (>= 2) rows
+static int gemv_bt_width(int B) { return B <= 2 ? 2 : (B <= 4 ? 4 : (B <= 8 ? 8 : 16)); }
+
+int gemv_bt_grid(int N, int mode) {
+  const int R = mode == MODE_LOGITS ? gemv_bt_rows<MODE_LOGITS>() : gemv_bt_rows<MODE_STORE>();
+  const int ngroups = (N + R - 1) / R;
+  const int nblk = (ngroups + 7) / 8;
+  return nblk < 256 ? nblk : 256;  // one 8-wave block per CU; waves stride over the groups
+}
+
+// Inputs in LDS: BT x K / 8 16-byte units (up to 128 KB for 16 rows of
+// K = 4096), more than the 64 KB a launch gets without opting in.
+template <int P, int MODE, bool NORM, int BT>
+static hipError_t gemv_bt_optin() {
+  constexpr int R = gemv_bt_rows<MODE>();
+  constexpr size_t lds_max = (size_t)BT * 64 * P * 16;
+  if (lds_max <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_bf16_bt<P, MODE, NORM, R, BT>),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+}
+
+template <int P, int MODE, bool NORM, int BT>
+static hipError_t launch_gemv_bt_pbt(const GemvArgs& a, hipStream_t st) {
+  constexpr int R = gemv_bt_rows<MODE>();
+  const size_t lds = (size_t)BT * (a.K / 8) * 16;
+  hipLaunchKernelGGL((k_gemv_bf16_bt<P, MODE, NORM, R, BT>), dim3(a.nblk, 1, (a.B + BT - 1) / BT),
+                     dim3(512), lds, st, a.W, a.bias, a.x, a.norm_w, a.eps, a.y, a.logits,
+                     a.part_val, a.part_idx, a.N, a.K, a.B, rope_args(a));
+  return hipSuccess;
+}
+
+template <int P, int MODE, bool NORM>
+static hipError_t gemv_bt_optin_p() {
+  hipError_t e = gemv_bt_optin<P, MODE, NORM, 2>();
+  if (e == hipSuccess) e = gemv_bt_optin<P, MODE, NORM, 4>();
+  if (e == hipSuccess) e = gemv_bt_optin<P, MODE, NORM, 8>();
+  if (e == hipSuccess) e = gemv_bt_optin<P, MODE, NORM, 16>();
+  return e;
+}
+
+template <int MODE, bool NORM>
+static hipError_t gemv_bt_optin_m() {
+  hipError_t e = gemv_bt_optin_p<1, MODE, NORM>();
+  if (e == hipSuccess) e = gemv_bt_optin_p<2, MODE, NORM>();
+  if (e == hipSuccess) e = gemv_bt_optin_p<3, MODE, NORM>();
+  if (e == hipSuccess) e = gemv_bt_optin_p<4, MODE, NORM>();
+  if (e == hipSuccess) e = gemv_bt_optin_p<6, MODE, NORM>();
+  if (e == hipSuccess) e = gemv_bt_optin_p<8, MODE, NORM>();
+  return e;
+}
+
+hipError_t gemv_batched_prepare() {
+  hipError_t e = gemv_bt_optin_m<MODE_QKV, true>();
+  if (e == hipSuccess) e = gemv_bt_optin_m<MODE_RESID, false>();
+  if (e == hipSuccess) e = gemv_bt_optin_m<MODE_LOGITS, true>();
+  return e;
+}
+
+template <int P, int MODE, bool NORM>
+static hipError_t launch_gemv_bt_pn(const GemvArgs& a, hipStream_t st) {
+  switch (gemv_bt_width(a.B)) {
+    case 2: return launch_gemv_bt_pbt<P, MODE, NORM, 2>(a, st);
+    case 4: return launch_gemv_bt_pbt<P, MODE, NORM, 4>(a, st);
+    case 8: return launch_gemv_bt_pbt<P, MODE, NORM, 8>(a, st);
+    default: return launch_gemv_bt_pbt<P, MODE, NORM, 16>(a, st);
+  }
+}
+
+// The step's three batched projections: QKV and lm_head with the RMSNorm
+// prologue, O without it.
+template <int MODE, bool NORM>
+static hipError_t launch_gemv_bt_m(const GemvArgs& a, hipStream_t st) {
+  switch ((a.K / 8 + 63) / 64) {
+    case 1: return launch_gemv_bt_pn<1, MODE, NORM>(a, st);
+    case 2: return launch_gemv_bt_pn<2, MODE, NORM>(a, st);
+    case 3: return launch_gemv_bt_pn<3, MODE, NORM>(a, st);
+    case 4: return launch_gemv_bt_pn<4, MODE, NORM>(a, st);
+    case 6: return launch_gemv_bt_pn<6, MODE, NORM>(a, st);
+    case 8: return launch_gemv_bt_pn<8, MODE, NORM>(a, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool gemv_batched_supported(const GemvArgs& a) {
+  const int P = (a.K / 8 + 63) / 64;
+  const bool p_ok = P == 1 || P == 2 || P == 3 || P == 4 || P == 6 || P == 8;
+  const bool form_ok = (a.mode == MODE_QKV && a.norm_w != nullptr) ||
+                       (a.mode == MODE_RESID && a.norm_w == nullptr) ||
+                       (a.mode == MODE_LOGITS && a.norm_w != nullptr);
+  return p_ok && form_ok && a.K % 8 == 0;
+}
+
+hipError_t launch_gemv_bf16_batched(const GemvArgs& a, hipStream_t st) {
+  if (!gemv_batched_supported(a)) return hipErrorInvalidValue;
+  switch (a.mode) {
+    case MODE_QKV: return launch_gemv_bt_m<MODE_QKV, true>(a, st);
+    case MODE_RESID: return launch_gemv_bt_m<MODE_RESID, false>(a, st);
+    default: return launch_gemv_bt_m<MODE_LOGITS, true>(a, st);
+  }
+}
+
+// ===========================================================================
 // Final argmax over the lm_head partials; advances the sequence.
 // grid B, block 256.  Greedy id = largest logit, ties to the lowest index.
 // tokens[b][pos+1] receives it unless that slot still belongs to the prompt

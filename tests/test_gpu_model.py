@@ -139,6 +139,27 @@ def test_small_model_batch2_and_sliding_wrap(orc):
     assert e1 < 2e-2 and e2 < 2e-2
 
 
+@pytest.mark.parametrize("batch", [5, 16])
+def test_small_model_batched_decode(orc, batch):
+    """Batch 5 (a padded 8-row input block) and 16 (a full one): the batched
+    projections read each weight row once for all rows and must give every
+    row the batch-1 bits."""
+    cfg, ocfg = pair(orc, **dict(SMALL, max_batch=batch, max_seq=160))
+    prompt = [[(13 * i + 7 * b + 1) % 4096 for i in range(9 + b)][:9] for b in range(batch)]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 21, prompt, 24, batch=batch)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_gpt_oss_20b_batch4(orc):
+    """20b shape, 4 rows: the batched projections at K = 2880 and 4096."""
+    cfg, ocfg = pair(orc, max_seq=64, max_batch=4)
+    prompt = [[101 + b, 2002, 30003 + 7 * b, 200000 - b] for b in range(4)]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 3, prompt, 8, batch=4)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
 def test_gpt_oss_20b_greedy_64(orc):
     """Full gpt-oss-20b shape (24 layers, 32 experts, vocab 201088)."""
     cfg, ocfg = pair(orc, max_seq=256)
