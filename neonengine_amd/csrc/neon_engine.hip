@@ -581,20 +581,27 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     o.N = H; o.K = c.n_heads * D; o.B = B;
     o.nblk = gemv_default_grid(o.N, o.mode);
     launch_gemv_step(o, B, st);
+    // batch >= 2: the top-k runs once per row before the experts, which then
+    // group the rows by expert (each used expert's weights read once);
+    // batch 1: the expert kernels choose from the logits themselves
+    const bool grouped = B >= 2 && B * c.top_k <= 64;
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
+    r.idx = grouped ? ctx->moe_idx : nullptr; r.score = grouped ? ctx->moe_score : nullptr;
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
     launch_router(r, st);
     MoeArgs m;
     m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
     m.dn_codes = w.dn_codes; m.dn_scales = w.dn_scales; m.dn_bias = w.dn_bias;
-    m.router_lg = ctx->router_lg; m.idx = nullptr; m.score = nullptr;
-    m.idx_out = ctx->moe_idx; m.score_out = ctx->moe_score; m.E = c.n_experts;
-    m.xn = ctx->xn; m.act = ctx->act;
+    m.router_lg = grouped ? nullptr : ctx->router_lg;
+    m.idx = grouped ? ctx->moe_idx : nullptr; m.score = grouped ? ctx->moe_score : nullptr;
+    m.idx_out = grouped ? nullptr : ctx->moe_idx; m.score_out = grouped ? nullptr : ctx->moe_score;
+    m.E = c.n_experts; m.xn = ctx->xn; m.act = ctx->act;
     m.residual = ctx->h; m.out = ctx->h; m.B = B; m.H = H; m.I = c.intermediate;
     m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
-    launch_moe(m, st);
+    if (grouped && moe_batched_supported(m)) launch_moe_batched(m, st);
+    else launch_moe(m, st);
   }
   GemvArgs lm;
   lm.mode = 2; lm.W = ctx->lm_head; lm.x = ctx->h; lm.norm_w = ctx->final_norm;

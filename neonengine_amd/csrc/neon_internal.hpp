@@ -116,6 +116,10 @@ struct MoeArgs {
   float alpha, limit;
 };
 void launch_moe(const MoeArgs& a, hipStream_t st);
+// 2 <= B, B k <= 64, idx / score given (router_lg NULL): each used expert's
+// weights read once for all rows that chose it; bit-identical to launch_moe
+bool moe_batched_supported(const MoeArgs& a);
+void launch_moe_batched(const MoeArgs& a, hipStream_t st);
 
 // ---- attention ------------------------------------------------------------------
 struct AttnArgs {

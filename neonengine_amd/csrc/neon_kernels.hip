@@ -1627,6 +1627,253 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   }
 }
 
+// ===========================================================================
+// Batched experts (2 <= B, B k <= 64): rows that chose the same expert share
+// one read of its weights.  idx / score [B][k] come from the top-k kernel.
+// Pair q = b k + s is row b's slot s; lane q of a wave holds idx[q], and
+// __ballot(idx == e) lists the pairs of expert e in row order.
+//
+// gate_up: grid (ceil(I / 16), min(E, B k)); block (x, u) serves the u-th
+// used expert (ascending id) on intermediate columns 16 x .. 16 x + 15 for
+// every pair that chose it.  down: grid ceil(H / 4); block serves output rows
+// 4 x .. 4 x + 3 for every row b: each wave takes every fourth used expert,
+// reads its 4 rows once and dots them with the act row of each pair that
+// chose it; the block then combines row b's k slots in slot order (the same
+// fmaf chain as the batch-1 kernel) and adds the residual.  Each (row, pair)
+// dot is the canonical one of the batch-1 kernels, so the outputs are
+// bit-identical to a batch-1 step.
+// ===========================================================================
+// Register "copies" the compiler cannot see through: inside the per-pair
+// loops the weight words are laundered once per iteration, so the E2M1
+// conversions are not hoisted out of the loop (which keeps every converted
+// value live and drops the kernel to one wave per SIMD).  No code is emitted.
+__device__ __forceinline__ void launder(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+__device__ __forceinline__ void launder(uint32_t& v) { asm volatile("" : "+v"(v)); }
+template <int P>
+__device__ __forceinline__ void launder(Fp4RowPair<P>& q) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int p = 0; p < P - 1; ++p) { launder(q.c[i][p]); launder(q.s[i][p]); }
+  launder(q.tc);
+  launder(q.ts);
+}
+template <int P>
+__device__ __forceinline__ void launder(Fp4Row<P>& r) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) { launder(r.c[p]); launder(r.s[p]); }
+}
+
+template <int P, bool PAIR>
+__global__ __launch_bounds__(256) void k_moe_gate_up_bt(
+    const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
+    const uint16_t* __restrict__ gu_bias, const int32_t* __restrict__ idx, int E,
+    const uint16_t* __restrict__ xn, uint16_t* __restrict__ act, int B, int H, int I,
+    int k, float alpha, float limit) {
+  const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nk = B * k;
+  const int my_id = lane < nk ? idx[lane] : -1;
+  // the u-th used expert and its pairs (uniform across the block)
+  int e = -1;
+  uint64_t pairs = 0;
+  for (int ee = 0, cnt = 0; ee < E; ++ee) {
+    const uint64_t bal = __ballot(my_id == ee);
+    if (bal != 0) {
+      if (cnt == (int)blockIdx.y) { e = ee; pairs = bal; break; }
+      ++cnt;
+    }
+  }
+  if (e < 0) return;  // fewer used experts than blocks in y
+  const int j0 = (blockIdx.x * 4 + wave) * kMoeJpw;
+  if (j0 >= I) return;
+  const size_t rows = (size_t)2 * I;
+  const uint8_t* codes = gu_codes + (size_t)e * rows * (H / 2);
+  const uint8_t* scales = gu_scales + (size_t)e * rows * U;
+  const uint16_t* bias = gu_bias + (size_t)e * rows;
+  const int jl = min(j0 + (lane >> 4), I - 1);
+  const uint32_t bgu = load_pinned_u32(reinterpret_cast<const uint32_t*>(bias + 2 * jl));
+  // the wave's 8 rows, once for all pairs
+  Fp4RowPair<P> rp[kMoeJpw];
+  Fp4Row<P> rw[PAIR ? 1 : 2 * kMoeJpw];
+  if constexpr (PAIR) {
+#pragma unroll
+    for (int c = 0; c < kMoeJpw; ++c) {
+      const int row = 2 * min(j0 + c, I - 1);
+      fp4_load_pair<P>(rp[c], codes + (size_t)row * (H / 2), scales + (size_t)row * U,
+                       codes + (size_t)(row + 1) * (H / 2), scales + (size_t)(row + 1) * U,
+                       U, lane);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 2 * kMoeJpw; ++r) {
+      const int row = 2 * min(j0 + r / 2, I - 1) + (r & 1);
+      fp4_load_row<P>(rw[r], codes + (size_t)row * (H / 2), scales + (size_t)row * U, U, lane);
+    }
+  }
+  // pairs in row order; the next pair's input loads while this one is reduced
+  int q = __builtin_ctzll(pairs);
+  uint4 xraw[P][4];
+  if (PAIR) x_fp4_issue_pair<P>(xraw, xn + (size_t)(q / k) * H, U, lane);
+  else x_fp4_issue<P>(xraw, xn + (size_t)(q / k) * H, U, lane);
+  while (true) {
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int c = 0; c < kMoeJpw; ++c) launder(rp[c]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2 * kMoeJpw; ++r) launder(rw[r]);
+    }
+    float xr[P][32];
+    if (PAIR) x_fp4_finish_pair<P>(xr, xraw);
+    else x_fp4_finish<P>(xr, xraw, U, lane);
+    pairs &= pairs - 1;
+    const int qn = pairs ? __builtin_ctzll(pairs) : q;
+    if (pairs) {
+      if (PAIR) x_fp4_issue_pair<P>(xraw, xn + (size_t)(qn / k) * H, U, lane);
+      else x_fp4_issue<P>(xraw, xn + (size_t)(qn / k) * H, U, lane);
+    }
+    float a[2 * kMoeJpw];
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int c = 0; c < kMoeJpw; ++c) fp4_pair_partials<P>(rp[c], xr, U, lane, a[2 * c], a[2 * c + 1]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 2 * kMoeJpw; ++r) a[r] = fp4_row_partial<P>(rw[r], xr, U, lane);
+    }
+    const float t = wave_sum_8rows(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], lane);
+    const float tu = xor_lane<8>(t);  // lane 16 c receives the up total
+    const int j = j0 + (lane >> 4);
+    if ((lane & 15) == 0 && j < I) {
+      const float gb = __fadd_rn(t, bf_lo(bgu));
+      const float ub = __fadd_rn(tu, bf_hi(bgu));
+      act[(size_t)q * I + j] = f2bf(swiglu_clamp(gb, ub, alpha, limit));
+    }
+    if (!pairs) break;
+    q = qn;
+  }
+}
+
+template <int P, bool PAIR>
+__global__ __launch_bounds__(256) void k_moe_down_bt(
+    const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
+    const uint16_t* __restrict__ dn_bias, const int32_t* __restrict__ idx,
+    const float* __restrict__ score, int E, const uint16_t* __restrict__ act,
+    const uint16_t* residual, uint16_t* out, int B, int H, int I, int k) {
+  __shared__ float red[64][kMoeRpw];  // [pair][row]: dot + bias
+  const int U = I / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nk = B * k;
+  const int n0 = blockIdx.x * kMoeRpw;
+  const int my_id = lane < nk ? idx[lane] : -1;
+  // every fourth used expert, starting at this wave's index
+  for (int ee = 0, cnt = 0; ee < E; ++ee) {
+    const uint64_t bal = __ballot(my_id == ee);
+    if (bal == 0) continue;
+    if ((cnt++ & 3) != wave) continue;
+    const uint8_t* codes = dn_codes + (size_t)ee * H * (I / 2);
+    const uint8_t* scales = dn_scales + (size_t)ee * H * U;
+    const uint16_t bl = load_pinned_u16(dn_bias + (size_t)ee * H + min(n0 + (lane >> 4), H - 1));
+    Fp4RowPair<P> rp[kMoeRpw / 2];
+    Fp4Row<P> rw[PAIR ? 1 : kMoeRpw];
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int c = 0; c < kMoeRpw / 2; ++c) {
+        const int na = min(n0 + 2 * c, H - 1), nb = min(n0 + 2 * c + 1, H - 1);
+        fp4_load_pair<P>(rp[c], codes + (size_t)na * (I / 2), scales + (size_t)na * U,
+                         codes + (size_t)nb * (I / 2), scales + (size_t)nb * U, U, lane);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < kMoeRpw; ++r) {
+        const int n = min(n0 + r, H - 1);
+        fp4_load_row<P>(rw[r], codes + (size_t)n * (I / 2), scales + (size_t)n * U, U, lane);
+      }
+    }
+    uint64_t pairs = bal;
+    int q = __builtin_ctzll(pairs);
+    uint4 xraw[P][4];
+    if (PAIR) x_fp4_issue_pair<P>(xraw, act + (size_t)q * I, U, lane);
+    else x_fp4_issue<P>(xraw, act + (size_t)q * I, U, lane);
+    while (true) {
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int c = 0; c < kMoeRpw / 2; ++c) launder(rp[c]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < kMoeRpw; ++r) launder(rw[r]);
+      }
+      float xr[P][32];
+      if (PAIR) x_fp4_finish_pair<P>(xr, xraw);
+      else x_fp4_finish<P>(xr, xraw, U, lane);
+      pairs &= pairs - 1;
+      const int qn = pairs ? __builtin_ctzll(pairs) : q;
+      if (pairs) {
+        if (PAIR) x_fp4_issue_pair<P>(xraw, act + (size_t)qn * I, U, lane);
+        else x_fp4_issue<P>(xraw, act + (size_t)qn * I, U, lane);
+      }
+      float a[kMoeRpw];
+      if constexpr (PAIR) {
+#pragma unroll
+        for (int c = 0; c < kMoeRpw / 2; ++c) fp4_pair_partials<P>(rp[c], xr, U, lane, a[2 * c], a[2 * c + 1]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < kMoeRpw; ++r) a[r] = fp4_row_partial<P>(rw[r], xr, U, lane);
+      }
+      const float t = wave_sum_4rows(a[0], a[1], a[2], a[3], lane);
+      if ((lane & 15) == 0) red[q][lane >> 4] = __fadd_rn(t, bf2f(bl));
+      if (!pairs) break;
+      q = qn;
+    }
+  }
+  __syncthreads();
+  // row b, output row n0 + r: y = fmaf(score_s, red_s, y) over the slots in order
+  for (int t = threadIdx.x; t < B * kMoeRpw; t += blockDim.x) {
+    const int b = t / kMoeRpw, r = t % kMoeRpw, n = n0 + r;
+    if (n >= H) continue;
+    float y = 0.0f;
+    for (int s2 = 0; s2 < k; ++s2) y = __builtin_fmaf(score[b * k + s2], red[b * k + s2][r], y);
+    const uint16_t m = f2bf(y);
+    const size_t o = (size_t)b * H + n;
+    out[o] = residual ? f2bf(__fadd_rn(bf2f(residual[o]), bf2f(m))) : m;
+  }
+}
+
+bool moe_batched_supported(const MoeArgs& a) {
+  return a.B >= 2 && a.B * a.k <= 64 && a.idx != nullptr && a.score != nullptr &&
+         a.router_lg == nullptr && a.k <= kMaxTopK;
+}
+
+void launch_moe_batched(const MoeArgs& a, hipStream_t st) {
+  const int Pg = (a.H / 32 + 63) / 64, Pd = (a.I / 32 + 63) / 64;
+  const int gblk = (a.I + 4 * kMoeJpw - 1) / (4 * kMoeJpw);
+  const int dblk = (a.H + kMoeRpw - 1) / kMoeRpw;
+  const int used_max = a.E < a.B * a.k ? a.E : a.B * a.k;
+  const bool pg = fp4_pair_ok(a.H / 32, Pg), pd = fp4_pair_ok(a.I / 32, Pd);
+#define GB_LAUNCH(PP, PR)                                                                    \
+  hipLaunchKernelGGL((k_moe_gate_up_bt<PP, PR>), dim3(gblk, used_max), dim3(256), 0, st,    \
+                     a.gu_codes, a.gu_scales, a.gu_bias, a.idx, a.E, a.xn, a.act, a.B, a.H, \
+                     a.I, a.k, a.alpha, a.limit)
+#define DB_LAUNCH(PP, PR)                                                                    \
+  hipLaunchKernelGGL((k_moe_down_bt<PP, PR>), dim3(dblk), dim3(256), 0, st, a.dn_codes,     \
+                     a.dn_scales, a.dn_bias, a.idx, a.score, a.E, a.act, a.residual, a.out,  \
+                     a.B, a.H, a.I, a.k)
+  switch (Pg) {
+    case 1: GB_LAUNCH(1, false); break;
+    case 2: if (pg) GB_LAUNCH(2, true); else GB_LAUNCH(2, false); break;
+    case 3: if (pg) GB_LAUNCH(3, true); else GB_LAUNCH(3, false); break;
+    default: if (pg) GB_LAUNCH(4, true); else GB_LAUNCH(4, false); break;
+  }
+  switch (Pd) {
+    case 1: DB_LAUNCH(1, false); break;
+    case 2: if (pd) DB_LAUNCH(2, true); else DB_LAUNCH(2, false); break;
+    case 3: if (pd) DB_LAUNCH(3, true); else DB_LAUNCH(3, false); break;
+    default: if (pd) DB_LAUNCH(4, true); else DB_LAUNCH(4, false); break;
+  }
+#undef GB_LAUNCH
+#undef DB_LAUNCH
+}
+
 void launch_moe(const MoeArgs& a, hipStream_t st) {
   const int Pg = (a.H / 32 + 63) / 64;  // gate_up reduces over H
   const int Pd = (a.I / 32 + 63) / 64;  // down reduces over I
