@@ -66,8 +66,9 @@ class Engine {
     check(neon_load_tensor(ctx_, name.c_str(), data, bytes), ctx_);
   }
 
-  // Prompt mode: NEON_PREFILL_BATCHED (matrix cores, default) or
-  // NEON_PREFILL_STEPWISE (every prompt token as a decode step).
+  // Prompt mode: NEON_PREFILL_CHUNKED (16 prompt rows per pass, default),
+  // NEON_PREFILL_STEPWISE (every prompt token as a decode step) or
+  // NEON_PREFILL_BATCHED (matrix cores; switched off).
   void set_prefill_mode(int mode) { check(neon_set_prefill_mode(ctx_, mode), ctx_); }
 
   // Forward: prefill `batch` prompts of equal length (row-major ids), then

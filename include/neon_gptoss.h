@@ -90,17 +90,21 @@ neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
 
 /* Starts `batch` sequences from host prompt ids [batch][n_tokens] and runs
  * the prompt; afterwards the first generated token of each sequence is
- * available.  In the default batched mode, prompt rows 0 .. n_tokens-2 of a
- * sequence go through every layer at once on the matrix cores (filling the
- * KV cache) and the last prompt token runs as a decode step; the stepwise
- * mode runs every prompt token as a decode step (the decode kernels' exact
- * fp32 order throughout).  Neither mode has a counterpart in the reference,
- * which has no model code. */
+ * available.  Modes (neon_set_prefill_mode):
+ *  - NEON_PREFILL_CHUNKED (default): prompt rows 0 .. n_tokens-2 of a
+ *    sequence go through every layer 16 rows at a time with the batched decode
+ *    kernels (each weight row read once per 16 rows, causal attention over the
+ *    sequence's cache), then the last prompt token runs as a decode step.
+ *    Bit-identical to NEON_PREFILL_STEPWISE.
+ *  - NEON_PREFILL_STEPWISE: every prompt token as a decode step.
+ *  - NEON_PREFILL_BATCHED: all rows at once on the matrix cores; switched off
+ *    (selecting it returns NEON_ESTATE).
+ * None has a counterpart in the reference, which has no model code. */
 neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
                          int n_tokens, void* stream);
 
-enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1 };
-/* Selects how neon_prefill runs the prompt (default NEON_PREFILL_BATCHED). */
+enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1, NEON_PREFILL_CHUNKED = 2 };
+/* Selects how neon_prefill runs the prompt (default NEON_PREFILL_CHUNKED). */
 neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
 
 /* Runs `n_steps` greedy decode steps for every live sequence (each step

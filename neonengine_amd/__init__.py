@@ -220,7 +220,7 @@ def attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, D, T_max, window, 
                                    _ptr(out), M, Hq, Hkv, D, T_max, window, _stream(stream)))
 
 
-PREFILL_BATCHED, PREFILL_STEPWISE = 0, 1
+PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED = 0, 1, 2
 
 
 # ---------------------------------------------------------------------------
@@ -280,7 +280,8 @@ class Engine:
         return p.value, n.value
 
     def set_prefill_mode(self, mode: int):
-        """PREFILL_STEPWISE (default: teacher-forced decode steps) or PREFILL_BATCHED."""
+        """PREFILL_CHUNKED (default: 16 prompt rows per pass), PREFILL_STEPWISE
+        (every prompt token as a decode step) or PREFILL_BATCHED (switched off)."""
         self._chk(lib().neon_set_prefill_mode(self._ctx, mode))
 
     def prefill(self, ids, stream=None):

@@ -48,6 +48,10 @@ struct Tensor {
 
 }  // namespace
 
+// Prompt rows run through the layers together in the chunked prompt pass (the
+// batched decode kernels take up to 16 rows; the experts up to 64 row-slots).
+constexpr int kPromptRows = 16;
+
 struct neon_ctx {
   neon_config cfg{};
   int device = 0;
@@ -83,7 +87,7 @@ struct neon_ctx {
   int host_pos = 0;
   bool weights_ready = false;
   // batched prefill (M prompt rows per pass): scratch grown on demand
-  int prefill_mode = NEON_PREFILL_STEPWISE;
+  int prefill_mode = NEON_PREFILL_CHUNKED;
   char* pf = nullptr;
   int pf_rows = 0;
   uint16_t *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
@@ -91,6 +95,8 @@ struct neon_ctx {
   float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
   int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
           *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
+  // prompt passes: positions and sequences of the rows of one pass
+  int32_t *row_pos = nullptr, *row_seq = nullptr;
   // captured decode step
   hipStream_t cap_stream = nullptr;
   hipGraph_t graph = nullptr;
@@ -322,21 +328,25 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   HIPCHK(ctx, hipMemset(ctx->kc, 0, kv_bytes));
   HIPCHK(ctx, hipMemset(ctx->vc, 0, kv_bytes));
   // ---- activations / scratch ----
+  // Bm sequences; Br rows per pass (a prompt pass runs up to kPromptRows
+  // rows of one sequence at once)
   const size_t Bm = c.max_batch, half = c.head_dim / 2;
+  const size_t Br = std::max<size_t>(Bm, kPromptRows);
   ctx->s_slide = attn_splits(c.max_seq, c.sliding_window);
   ctx->s_full = attn_splits(c.max_seq, 0);
   ctx->lm_nblk = gemv_default_grid(c.vocab, 2);
   ctx->tok_stride = c.max_seq + 1;
   off = 0;
-  const size_t o_h = take(Bm * H * 2), o_xn = take(Bm * H * 2),
-               o_qkv = take(Bm * sz.qkv_rows * 2),
-               o_ao = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
-               o_qr = take(Bm * (size_t)c.n_heads * c.head_dim * 2),
-               o_act = take(Bm * c.top_k * I * 2),
-               o_idx = take(Bm * c.top_k * 4), o_sc = take(Bm * c.top_k * 4),
-               o_rlg = take(Bm * c.n_experts * 4),
-               o_apo = take(Bm * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * c.head_dim * 4),
-               o_apml = take(Bm * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
+  const size_t o_h = take(Br * H * 2), o_xn = take(Br * H * 2),
+               o_qkv = take(Br * sz.qkv_rows * 2),
+               o_ao = take(Br * (size_t)c.n_heads * c.head_dim * 2),
+               o_qr = take(Br * (size_t)c.n_heads * c.head_dim * 2),
+               o_act = take(Br * c.top_k * I * 2),
+               o_idx = take(Br * c.top_k * 4), o_sc = take(Br * c.top_k * 4),
+               o_rlg = take(Br * c.n_experts * 4),
+               o_apo = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * c.head_dim * 4),
+               o_apml = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
+               o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -361,6 +371,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
   ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
   ctx->sin_t = (float*)(W + o_sin);
+  ctx->row_pos = (int32_t*)(W + o_rpos); ctx->row_seq = (int32_t*)(W + o_rseq);
   // ---- RoPE table ----
   std::vector<float> ct, st;
   rope_table_host(&c, c.max_seq, ct, st);
@@ -550,11 +561,15 @@ static int launch_gemv_step(GemvArgs& a, int B, hipStream_t st) {
   return a.nblk;
 }
 
-static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
+// Rows 0 .. B-1 through embed and every layer: row b is token pos[b] of
+// sequence seq[b] (seq NULL: sequence b), its k / v land at that sequence's
+// cache row pos[b], and it attends to that sequence's keys up to pos[b].
+static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t* seq,
+                         hipStream_t st) {
   const neon_config& c = ctx->cfg;
   const int H = c.hidden, D = c.head_dim;
   const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * D;
-  launch_embed(ctx->tokens, ctx->tok_stride, ctx->pos, ctx->embed, ctx->h, H, B, st);
+  launch_embed(ctx->tokens, ctx->tok_stride, pos, seq, ctx->embed, ctx->h, H, B, st);
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
@@ -566,12 +581,13 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     q.mode = 3; q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->h; q.norm_w = w.attn_norm;
     q.eps = c.rms_eps; q.y = ctx->qkv; q.N = qkv_rows; q.K = H; q.B = B;
     q.nblk = gemv_default_grid(q.N, q.mode);
-    q.pos = ctx->pos; q.cos_t = ctx->cos_t; q.sin_t = ctx->sin_t; q.q_out = ctx->q_rot;
-    q.kc = kc_l; q.vc = vc_l; q.Hq = c.n_heads; q.Hkv = c.n_kv_heads; q.T_max = c.max_seq;
+    q.pos = pos; q.cos_t = ctx->cos_t; q.sin_t = ctx->sin_t; q.q_out = ctx->q_rot;
+    q.kc = kc_l; q.vc = vc_l; q.seq = seq; q.Hq = c.n_heads; q.Hkv = c.n_kv_heads;
+    q.T_max = c.max_seq;
     launch_gemv_step(q, B, st);
     AttnArgs a;
-    a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
-    a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml;
+    a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = pos;
+    a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml; a.seq = seq;
     a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
@@ -603,6 +619,14 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
     if (grouped && moe_batched_supported(m)) launch_moe_batched(m, st);
     else launch_moe(m, st);
   }
+}
+
+// The decode step: every sequence's row through the layers, then lm_head and
+// the argmax that writes the next token and advances pos.
+static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
+  const neon_config& c = ctx->cfg;
+  const int H = c.hidden;
+  enqueue_rows(ctx, B, ctx->pos, nullptr, st);
   GemvArgs lm;
   lm.mode = 2; lm.W = ctx->lm_head; lm.x = ctx->h; lm.norm_w = ctx->final_norm;
   lm.eps = c.rms_eps; lm.logits = ctx->logits; lm.part_val = ctx->lm_part_val;
@@ -739,7 +763,8 @@ static const bool kBatchedPrefillEnabled = false;
 
 extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
   if (!ctx) return NEON_EINVAL;
-  if (mode != NEON_PREFILL_BATCHED && mode != NEON_PREFILL_STEPWISE)
+  if (mode != NEON_PREFILL_BATCHED && mode != NEON_PREFILL_STEPWISE &&
+      mode != NEON_PREFILL_CHUNKED)
     FAIL(ctx, NEON_EINVAL, "neon_set_prefill_mode: unknown mode %d", mode);
   if (mode == NEON_PREFILL_BATCHED && !kBatchedPrefillEnabled)
     FAIL(ctx, NEON_ESTATE, "neon_set_prefill_mode: the batched prompt pass is switched off "
@@ -775,6 +800,33 @@ extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch
   HIPCHK(ctx, hipStreamSynchronize(st));  // host staging buffers die here
   ctx->batch = batch;
   ctx->host_pos = 0;
+  if (ctx->prefill_mode == NEON_PREFILL_CHUNKED && n_tokens > 1) {
+    // prompt rows 0 .. n-2 of each sequence, kPromptRows at a time through the
+    // layers (their k / v fill the cache; row p attends to keys <= p), then
+    // the last prompt token as an ordinary decode step (logits, first token).
+    // The passes' (position, sequence) rows are staged up front and stay
+    // alive until the stream is synchronised below.
+    const int M = n_tokens - 1;
+    const int per_seq = (M + kPromptRows - 1) / kPromptRows;
+    std::vector<int32_t> rows((size_t)batch * per_seq * 2 * kPromptRows, 0);
+    for (int b = 0; b < batch; ++b)
+      for (int i = 0; i < per_seq; ++i) {
+        const int p0 = i * kPromptRows, R = std::min(kPromptRows, M - p0);
+        int32_t* r = &rows[((size_t)b * per_seq + i) * 2 * kPromptRows];
+        for (int j = 0; j < R; ++j) { r[j] = p0 + j; r[kPromptRows + j] = b; }
+        HIPCHK(ctx, hipMemcpyAsync(ctx->row_pos, r, R * 4, hipMemcpyHostToDevice, st));
+        HIPCHK(ctx, hipMemcpyAsync(ctx->row_seq, r + kPromptRows, R * 4, hipMemcpyHostToDevice, st));
+        enqueue_rows(ctx, R, ctx->row_pos, ctx->row_seq, st);
+      }
+    HIPCHK(ctx, hipGetLastError());
+    std::vector<int32_t> pm(batch, M);
+    HIPCHK(ctx, hipMemcpyAsync(ctx->pos, pm.data(), batch * 4, hipMemcpyHostToDevice, st));
+    HIPCHK(ctx, hipStreamSynchronize(st));  // rows and pm die here
+    neon_status s = run_steps(ctx, 1, st);
+    if (s != NEON_OK) return s;
+    ctx->host_pos = n_tokens;
+    return NEON_OK;
+  }
   if (ctx->prefill_mode == NEON_PREFILL_BATCHED && n_tokens > 1) {
     // prompt rows 0 .. n-2 in one pass per sequence, then the last prompt
     // token as an ordinary decode step (logits, first generated token)
@@ -1063,7 +1115,7 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   AttnArgs a;
   a.q = q; a.kc = k_cache; a.vc = v_cache;
   a.sinks = sinks; a.pos = pos; a.out = out;
-  a.part_o = scratch; a.part_ml = scratch + np * D;
+  a.part_o = scratch; a.part_ml = scratch + np * D; a.seq = nullptr;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window;
   a.S = nsplit; a.q_stride = Hq * D;
   launch_attn(a, st);

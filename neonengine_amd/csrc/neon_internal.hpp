@@ -32,6 +32,7 @@ struct RopeArgs {
   uint16_t* q_out = nullptr;
   uint16_t* kc = nullptr;
   uint16_t* vc = nullptr;
+  const int32_t* seq = nullptr;  // KV-cache sequence of each row (NULL: row b is sequence b)
   int Hq = 0, Hkv = 0, T_max = 0;
 };
 
@@ -53,6 +54,7 @@ struct GemvArgs {
   const int32_t* pos = nullptr;
   const float *cos_t = nullptr, *sin_t = nullptr;
   uint16_t *q_out = nullptr, *kc = nullptr, *vc = nullptr;
+  const int32_t* seq = nullptr;  // KV-cache sequence of each row (NULL: identity)
   int Hq = 0, Hkv = 0, T_max = 0;
 };
 // grid.x for N rows in `mode` (the rows per wave group depend on the mode)
@@ -74,6 +76,7 @@ void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
                            int32_t* pos, const int32_t* prompt_len,
                            int32_t* last_ids, int B, hipStream_t st);
 void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
+                  const int32_t* seq,
                   const uint16_t* embed, uint16_t* h, int H, int B,
                   hipStream_t st);
 void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
@@ -130,6 +133,7 @@ struct AttnArgs {
   uint16_t* out;          // [B][Hq*D]
   float* part_o;          // [B][Hq][S][D] split partials (scratch)
   float* part_ml;         // [B][Hq][S][2]
+  const int32_t* seq;     // KV-cache sequence of each row, or NULL (row b = sequence b)
   int B, Hq, Hkv, T_max, window, S, q_stride;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);

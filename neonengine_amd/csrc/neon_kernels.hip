@@ -584,7 +584,7 @@ __device__ __forceinline__ void gemv_bf16_group(
     int g, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     uint16_t bias_first, float (&xr)[P][8], const XBf16Raw<P>& xraw, float eps,
     uint16_t* __restrict__ y, float* __restrict__ logits, int b, int N, int K,
-    int lane, float& best_v, int32_t& best_i, const RopeArgs& rp, int p) {
+    int lane, float& best_v, int32_t& best_i, const RopeArgs& rp, int p, int sq) {
   const int U = K / 8;
   constexpr int LS = 6 - log2_rows<R>();  // lane (1 << LS) r holds row r after the sum
   const int my_row = lane >> LS;
@@ -636,9 +636,9 @@ __device__ __forceinline__ void gemv_bf16_group(
         if (head < rp.Hq)
           rp.q_out[((size_t)b * rp.Hq + head) * 64 + dd] = o;
         else
-          rp.kc[(((size_t)b * rp.Hkv + head - rp.Hq) * rp.T_max + p) * 64 + dd] = o;
+          rp.kc[(((size_t)sq * rp.Hkv + head - rp.Hq) * rp.T_max + p) * 64 + dd] = o;
       } else {
-        rp.vc[(((size_t)b * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p) * 64 + dd] = yv;
+        rp.vc[(((size_t)sq * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p) * 64 + dd] = yv;
       }
     }
   } else if (my_row < nr) {
@@ -675,6 +675,10 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   const int p = MODE == MODE_QKV ? (int)load_pinned_u32(
                                         reinterpret_cast<const uint32_t*>(rp.pos) + b)
                                   : 0;
+  // the KV-cache sequence of row b (rows of one prompt share a sequence)
+  const int sq = (MODE == MODE_QKV && rp.seq != nullptr)
+                     ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.seq) + b)
+                     : b;
   uint16_t bias_first = 0;
   if (MODE != MODE_LOGITS) {
     const int rb = min(group_row<MODE, R>(g0, lane >> (6 - log2_rows<R>())), N - 1);
@@ -688,10 +692,10 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   int32_t best_i = 0x7fffffff;
   if (g0 < ngroups) {
     gemv_bf16_group<P, MODE, NORM, true, R>(g0, W, bias, bias_first, xr, xraw, eps, y,
-                                            logits, b, N, K, lane, best_v, best_i, rp, p);
+                                            logits, b, N, K, lane, best_v, best_i, rp, p, sq);
     for (int g = g0 + gstride; g < ngroups; g += gstride)
       gemv_bf16_group<P, MODE, NORM, false, R>(g, W, bias, 0, xr, xraw, eps, y, logits, b,
-                                               N, K, lane, best_v, best_i, rp, p);
+                                               N, K, lane, best_v, best_i, rp, p, sq);
   }
   if (MODE == MODE_LOGITS) {
     // lanes 64 r / R hold the wave's candidates: keep the larger value, the
@@ -719,7 +723,7 @@ constexpr int gemv_rows() { return MODE == MODE_LOGITS ? 4 : (MODE == MODE_RESID
 static RopeArgs rope_args(const GemvArgs& a) {
   RopeArgs r;
   r.pos = a.pos; r.cos_t = a.cos_t; r.sin_t = a.sin_t; r.q_out = a.q_out;
-  r.kc = a.kc; r.vc = a.vc; r.Hq = a.Hq; r.Hkv = a.Hkv; r.T_max = a.T_max;
+  r.kc = a.kc; r.vc = a.vc; r.seq = a.seq; r.Hq = a.Hq; r.Hkv = a.Hkv; r.T_max = a.T_max;
   return r;
 }
 
@@ -850,6 +854,10 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_bt(
   const int p_l = MODE == MODE_QKV ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.pos) +
                                                           min(b_l, B - 1))
                                    : 0;
+  const int s_l = (MODE == MODE_QKV && rp.seq != nullptr)
+                      ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.seq) +
+                                             min(b_l, B - 1))
+                      : b_l;
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
   const int ngroups = (N + R - 1) / R;
@@ -915,9 +923,9 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_bt(
           if (head < rp.Hq)
             rp.q_out[((size_t)b_l * rp.Hq + head) * 64 + dd] = o;
           else
-            rp.kc[(((size_t)b_l * rp.Hkv + head - rp.Hq) * rp.T_max + p_l) * 64 + dd] = o;
+            rp.kc[(((size_t)s_l * rp.Hkv + head - rp.Hq) * rp.T_max + p_l) * 64 + dd] = o;
         } else {
-          rp.vc[(((size_t)b_l * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p_l) * 64 + dd] = yv;
+          rp.vc[(((size_t)s_l * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p_l) * 64 + dd] = yv;
         }
       }
     } else if constexpr (MODE == MODE_LOGITS) {
@@ -1106,21 +1114,22 @@ void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
 // Embedding gather: h[b] = embed[tokens[b][pos[b]]]
 // ===========================================================================
 __global__ void k_embed(const int32_t* __restrict__ tokens, int tok_stride,
-                        const int32_t* __restrict__ pos,
+                        const int32_t* __restrict__ pos, const int32_t* __restrict__ seq,
                         const uint16_t* __restrict__ embed,
                         uint16_t* __restrict__ h, int H) {
   const int b = blockIdx.x;
-  const int32_t id = tokens[(size_t)b * tok_stride + pos[b]];
+  const int sq = seq != nullptr ? seq[b] : b;  // row b embeds token pos[b] of sequence sq
+  const int32_t id = tokens[(size_t)sq * tok_stride + pos[b]];
   const uint4* src = reinterpret_cast<const uint4*>(embed + (size_t)id * H);
   uint4* dst = reinterpret_cast<uint4*>(h + (size_t)b * H);
   for (int i = threadIdx.x; i < H / 8; i += blockDim.x) dst[i] = src[i];
 }
 
 void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
-                  const uint16_t* embed, uint16_t* h, int H, int B,
+                  const int32_t* seq, const uint16_t* embed, uint16_t* h, int H, int B,
                   hipStream_t st) {
   hipLaunchKernelGGL(k_embed, dim3(B), dim3(256), 0, st, tokens, tok_stride,
-                     pos, embed, h, H);
+                     pos, seq, embed, h, H);
 }
 
 // ===========================================================================
@@ -2005,8 +2014,9 @@ __global__ __launch_bounds__(512) void k_attn_split(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     float* __restrict__ part_o, float* __restrict__ part_ml,
-    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv,
-    int G, int HB, int T_max, int window, int S, int q_stride) {
+    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
+    const int32_t* __restrict__ seq, int Hq, int Hkv, int G, int HB, int T_max, int window,
+    int S, int q_stride) {
   __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
   __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
   __shared__ __align__(16) float qs[8][kD];
@@ -2023,11 +2033,12 @@ __global__ __launch_bounds__(512) void k_attn_split(
   const uint16_t qv = q[(size_t)b * q_stride + (size_t)h * kD + lane];
   const uint16_t sink_raw = load_pinned_u16(sinks + h);  // used at the end (one split)
   const int p = pos_arr[b];
+  const int sq = seq != nullptr ? seq[b] : b;  // the row's KV-cache sequence
   const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
   const int n = p - lo + 1;
   const int nch = (n + 63) >> 6;
   const int c0 = (int)((int64_t)s * nch / S), c1 = (int)((int64_t)(s + 1) * nch / S);
-  const size_t kv_base = ((size_t)b * Hkv + g) * T_max;
+  const size_t kv_base = ((size_t)sq * Hkv + g) * T_max;
 
   // the first two chunks' words into registers: both tiles are staged before
   // the loop, so a split of two chunks (the 128-key sliding window) never
@@ -2182,8 +2193,8 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   const int HB = a.S == 1 ? 1 : G;
   hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * (G / HB) * a.S, a.B),
                      dim3(64 * (HB < 4 ? 4 : HB)), 0, st, a.q, a.kc, a.vc, a.pos,
-                     a.part_o, a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G, HB, a.T_max,
-                     a.window, a.S, a.q_stride);
+                     a.part_o, a.part_ml, a.sinks, a.out, a.seq, a.Hq, a.Hkv, G, HB,
+                     a.T_max, a.window, a.S, a.q_stride);
   if (a.S > 1)  // one split finishes in the split kernel
     hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
                        a.part_ml, a.sinks, a.out, a.Hq, a.S);

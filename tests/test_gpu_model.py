@@ -43,7 +43,7 @@ def orc_bf(a):
     return orc.bf16_to_f32(orc.f32_to_bf16(a)).astype(np.float64)
 
 
-def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
+def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1, mode=ne.PREFILL_STEPWISE):
     torch_cuda()
     eng = ne.Engine(cfg)
     eng.init_random(seed)
@@ -64,7 +64,7 @@ def run_parity(orc, cfg, ocfg, seed, prompt, n_steps, batch=1):
     m.close()
     # margins[b, t]: top-2 gap of the logits that produced generated token t
     margins = np.stack([np.diff(np.sort(lg, axis=1)[:, -2:], axis=1)[:, 0] for lg in o_logits], 1)
-    eng.set_prefill_mode(ne.PREFILL_STEPWISE)  # every prompt token on the exact decode path
+    eng.set_prefill_mode(mode)  # both modes run the exact decode kernels
     eng.prefill(prompt)
     g_first_logits = eng.read_logits()
     eng.decode(n_steps)
@@ -156,6 +156,26 @@ def test_gpt_oss_20b_batch4(orc):
     cfg, ocfg = pair(orc, max_seq=64, max_batch=4)
     prompt = [[101 + b, 2002, 30003 + 7 * b, 200000 - b] for b in range(4)]
     same, e1, e2 = run_parity(orc, cfg, ocfg, 3, prompt, 8, batch=4)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_small_model_chunked_prompt(orc):
+    """Two 40-token prompts in passes of 16, 16 and 7 rows (the last pass
+    partial), then 24 greedy steps: bit-identical to the oracle."""
+    cfg, ocfg = pair(orc, **dict(SMALL, max_seq=96))
+    prompt = [[(5 * i + 1) % 4096 for i in range(40)], [(9 * i + 2) % 4096 for i in range(40)]]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 17, prompt, 24, batch=2, mode=ne.PREFILL_CHUNKED)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_gpt_oss_20b_chunked_prompt(orc):
+    """20b shape, a 150-token prompt in 10 passes: the 128-key sliding window
+    moves inside the prompt."""
+    cfg, ocfg = pair(orc, max_seq=192)
+    prompt = [[(1009 * i + 17) % 201088 for i in range(150)]]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 2, prompt, 8, mode=ne.PREFILL_CHUNKED)
     assert same.all()
     assert e1 < 2e-2 and e2 < 2e-2
 

@@ -205,4 +205,5 @@ def test_prefill_mode_validation():
         eng.set_prefill_mode(ne.PREFILL_BATCHED)
     assert e.value.status == ne.NEON_ESTATE
     eng.set_prefill_mode(ne.PREFILL_STEPWISE)
+    eng.set_prefill_mode(ne.PREFILL_CHUNKED)
     eng.close()
