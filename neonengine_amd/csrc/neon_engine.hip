@@ -65,7 +65,10 @@ struct neon_ctx {
   float *cos_t = nullptr, *sin_t = nullptr;
   // KV cache [L][max_batch][Hkv][max_seq][D]
   uint16_t *kc = nullptr, *vc = nullptr;
-  size_t kv_layer_elems = 0;
+  // per layer: element offset into kc / vc, cache rows per (sequence, kv
+  // head) and the position -> row mask (ring caches on sliding layers)
+  std::vector<size_t> kv_off;
+  std::vector<int> kv_rows, kv_mask;
   // activations / scratch
   char* work = nullptr;
   uint16_t *h = nullptr, *xn = nullptr, *qkv = nullptr, *attn_out = nullptr,
@@ -321,8 +324,26 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
     w.dn_bias = (uint16_t*)(A + lo[l].v[K_DN_BIAS]);
   }
   // ---- KV cache ----
-  ctx->kv_layer_elems = (size_t)c.max_batch * c.n_kv_heads * c.max_seq * c.head_dim;
-  const size_t kv_bytes = ctx->kv_layer_elems * L * 2;
+  // Full layers keep every position.  A sliding layer only ever reads the
+  // last `window` keys, so it keeps a power-of-two ring of at least
+  // window + kPromptRows rows (a prompt pass appends kPromptRows rows before
+  // its attention reads the oldest key of its first row's window): position
+  // p lives in row p & (rows - 1).
+  ctx->kv_off.assign(L, 0);
+  ctx->kv_rows.assign(L, c.max_seq);
+  ctx->kv_mask.assign(L, -1);
+  size_t kv_elems = 0;
+  for (size_t l = 0; l < L; ++l) {
+    const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
+    if (sliding) {
+      int ring = 1;
+      while (ring < c.sliding_window + kPromptRows) ring <<= 1;
+      if (ring < c.max_seq) { ctx->kv_rows[l] = ring; ctx->kv_mask[l] = ring - 1; }
+    }
+    ctx->kv_off[l] = kv_elems;
+    kv_elems += (size_t)c.max_batch * c.n_kv_heads * ctx->kv_rows[l] * c.head_dim;
+  }
+  const size_t kv_bytes = kv_elems * 2;
   if (hipMalloc(&ctx->kc, kv_bytes) != hipSuccess || hipMalloc(&ctx->vc, kv_bytes) != hipSuccess)
     FAIL(ctx, NEON_ENOMEM, "hipMalloc of 2 x %zu KV-cache bytes failed", kv_bytes);
   HIPCHK(ctx, hipMemset(ctx->kc, 0, kv_bytes));
@@ -573,8 +594,8 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
-    uint16_t* kc_l = ctx->kc + (size_t)l * ctx->kv_layer_elems;
-    uint16_t* vc_l = ctx->vc + (size_t)l * ctx->kv_layer_elems;
+    uint16_t* kc_l = ctx->kc + ctx->kv_off[l];
+    uint16_t* vc_l = ctx->vc + ctx->kv_off[l];
     // QKV projection; its epilogue rotates q and k (RoPE-YaRN table) and
     // appends k, v at cache row pos
     GemvArgs q;
@@ -583,13 +604,14 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     q.nblk = gemv_default_grid(q.N, q.mode);
     q.pos = pos; q.cos_t = ctx->cos_t; q.sin_t = ctx->sin_t; q.q_out = ctx->q_rot;
     q.kc = kc_l; q.vc = vc_l; q.seq = seq; q.Hq = c.n_heads; q.Hkv = c.n_kv_heads;
-    q.T_max = c.max_seq;
+    q.T_max = ctx->kv_rows[l]; q.key_mask = ctx->kv_mask[l];
     launch_gemv_step(q, B, st);
     AttnArgs a;
     a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = pos;
     a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml; a.seq = seq;
     a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
-    a.T_max = c.max_seq; a.window = sliding ? c.sliding_window : 0;
+    a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
+    a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
     launch_attn(a, st);
     GemvArgs o;
@@ -728,14 +750,15 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
-    const size_t kvo = (size_t)l * ctx->kv_layer_elems + (size_t)b * Hkv * c.max_seq * D;
+    // (this switched-off pass needs caches of every position: see neon_set_prefill_mode)
+    const size_t kvo = ctx->kv_off[l] + (size_t)b * Hkv * ctx->kv_rows[l] * D;
     launch_rmsnorm(ctx->pf_h, w.attn_norm, ctx->pf_xn, M, H, c.rms_eps, st);
     launch_gemm_bf16(ctx->pf_xn, H, w.wqkv, H, w.bqkv, ctx->pf_qkv, nullptr, qkv_rows, M,
                      qkv_rows, H, 0, st);
-    launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv, c.max_seq,
-                        ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, st);
+    launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv,
+                        ctx->kv_rows[l], ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, st);
     launch_attn_prefill(ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, w.sinks, ctx->pf_ao, M, Hq,
-                        Hkv, c.max_seq, sliding ? c.sliding_window : 0, st);
+                        Hkv, ctx->kv_rows[l], sliding ? c.sliding_window : 0, st);
     launch_gemm_bf16(ctx->pf_ao, Hq * D, w.wo, Hq * D, w.bo, ctx->pf_h, nullptr, H, M, H,
                      Hq * D, 1, st);
     launch_rmsnorm(ctx->pf_h, w.mlp_norm, ctx->pf_xn, M, H, c.rms_eps, st);
@@ -1116,7 +1139,7 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   a.q = q; a.kc = k_cache; a.vc = v_cache;
   a.sinks = sinks; a.pos = pos; a.out = out;
   a.part_o = scratch; a.part_ml = scratch + np * D; a.seq = nullptr;
-  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.window = window;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.key_mask = -1; a.window = window;
   a.S = nsplit; a.q_stride = Hq * D;
   launch_attn(a, st);
   hipError_t e = hipGetLastError();

@@ -33,7 +33,8 @@ struct RopeArgs {
   uint16_t* kc = nullptr;
   uint16_t* vc = nullptr;
   const int32_t* seq = nullptr;  // KV-cache sequence of each row (NULL: row b is sequence b)
-  int Hq = 0, Hkv = 0, T_max = 0;
+  int Hq = 0, Hkv = 0, T_max = 0;  // T_max: cache rows per (sequence, kv head)
+  int key_mask = -1;  // position p sits in cache row p & key_mask (ring caches: rows - 1)
 };
 
 struct GemvArgs {
@@ -56,6 +57,7 @@ struct GemvArgs {
   uint16_t *q_out = nullptr, *kc = nullptr, *vc = nullptr;
   const int32_t* seq = nullptr;  // KV-cache sequence of each row (NULL: identity)
   int Hq = 0, Hkv = 0, T_max = 0;
+  int key_mask = -1;
 };
 // grid.x for N rows in `mode` (the rows per wave group depend on the mode)
 int gemv_default_grid(int N, int mode);
@@ -135,6 +137,9 @@ struct AttnArgs {
   float* part_ml;         // [B][Hq][S][2]
   const int32_t* seq;     // KV-cache sequence of each row, or NULL (row b = sequence b)
   int B, Hq, Hkv, T_max, window, S, q_stride;
+  // key j sits in cache row j & key_mask: -1 for a cache of every position,
+  // rows - 1 for a power-of-two ring that holds the last `rows` positions
+  int key_mask;
 };
 void launch_attn(const AttnArgs& a, hipStream_t st);
 // number of key splits used for a cache of T_max rows (window 0 = full layer)

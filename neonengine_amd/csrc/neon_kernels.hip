@@ -636,9 +636,9 @@ __device__ __forceinline__ void gemv_bf16_group(
         if (head < rp.Hq)
           rp.q_out[((size_t)b * rp.Hq + head) * 64 + dd] = o;
         else
-          rp.kc[(((size_t)sq * rp.Hkv + head - rp.Hq) * rp.T_max + p) * 64 + dd] = o;
+          rp.kc[(((size_t)sq * rp.Hkv + head - rp.Hq) * rp.T_max + (p & rp.key_mask)) * 64 + dd] = o;
       } else {
-        rp.vc[(((size_t)sq * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p) * 64 + dd] = yv;
+        rp.vc[(((size_t)sq * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + (p & rp.key_mask)) * 64 + dd] = yv;
       }
     }
   } else if (my_row < nr) {
@@ -724,6 +724,7 @@ static RopeArgs rope_args(const GemvArgs& a) {
   RopeArgs r;
   r.pos = a.pos; r.cos_t = a.cos_t; r.sin_t = a.sin_t; r.q_out = a.q_out;
   r.kc = a.kc; r.vc = a.vc; r.seq = a.seq; r.Hq = a.Hq; r.Hkv = a.Hkv; r.T_max = a.T_max;
+  r.key_mask = a.key_mask;
   return r;
 }
 
@@ -923,9 +924,9 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_bt(
           if (head < rp.Hq)
             rp.q_out[((size_t)b_l * rp.Hq + head) * 64 + dd] = o;
           else
-            rp.kc[(((size_t)s_l * rp.Hkv + head - rp.Hq) * rp.T_max + p_l) * 64 + dd] = o;
+            rp.kc[(((size_t)s_l * rp.Hkv + head - rp.Hq) * rp.T_max + (p_l & rp.key_mask)) * 64 + dd] = o;
         } else {
-          rp.vc[(((size_t)s_l * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + p_l) * 64 + dd] = yv;
+          rp.vc[(((size_t)s_l * rp.Hkv + head - rp.Hq - rp.Hkv) * rp.T_max + (p_l & rp.key_mask)) * 64 + dd] = yv;
         }
       }
     } else if constexpr (MODE == MODE_LOGITS) {
@@ -1968,8 +1969,9 @@ constexpr int kMaxSplits = 32;
     VW = make_uint4(0, 0, 0, 0);                                                \
     const int key_ = (CB) + ((WD) >> 3);                                        \
     if ((WD) < 512 && key_ <= p) {                                              \
-      KW = reinterpret_cast<const uint4*>(kc + (kv_base + key_) * kD)[(WD) & 7]; \
-      VW = reinterpret_cast<const uint4*>(vc + (kv_base + key_) * kD)[(WD) & 7]; \
+      const size_t row_ = kv_base + (uint32_t)(key_ & key_mask);                \
+      KW = reinterpret_cast<const uint4*>(kc + row_ * kD)[(WD) & 7];            \
+      VW = reinterpret_cast<const uint4*>(vc + row_ * kD)[(WD) & 7];            \
     }                                                                           \
   } while (0)
 #define ATTN_STORE_WORD(KW, VW, WD, BUF)                                        \
@@ -2015,8 +2017,8 @@ __global__ __launch_bounds__(512) void k_attn_split(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
-    const int32_t* __restrict__ seq, int Hq, int Hkv, int G, int HB, int T_max, int window,
-    int S, int q_stride) {
+    const int32_t* __restrict__ seq, int Hq, int Hkv, int G, int HB, int T_max, int key_mask,
+    int window, int S, int q_stride) {
   __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
   __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
   __shared__ __align__(16) float qs[8][kD];
@@ -2194,7 +2196,7 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * (G / HB) * a.S, a.B),
                      dim3(64 * (HB < 4 ? 4 : HB)), 0, st, a.q, a.kc, a.vc, a.pos,
                      a.part_o, a.part_ml, a.sinks, a.out, a.seq, a.Hq, a.Hkv, G, HB,
-                     a.T_max, a.window, a.S, a.q_stride);
+                     a.T_max, a.key_mask, a.window, a.S, a.q_stride);
   if (a.S > 1)  // one split finishes in the split kernel
     hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
                        a.part_ml, a.sinks, a.out, a.Hq, a.S);

@@ -170,6 +170,18 @@ def test_small_model_chunked_prompt(orc):
     assert e1 < 2e-2 and e2 < 2e-2
 
 
+def test_small_model_sliding_ring_wraps(orc):
+    """max_seq 700: the sliding layers keep a 256-row ring (window 128 + one
+    prompt pass of 16 rows, rounded up to a power of two).  A 600-token prompt
+    and 40 steps wrap it twice; every id and the logits must still equal the
+    oracle's, which keeps every position."""
+    cfg, ocfg = pair(orc, **dict(SMALL, max_seq=700, max_batch=1))
+    prompt = [[(31 * i + 11) % 4096 for i in range(600)]]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 23, prompt, 40, mode=ne.PREFILL_CHUNKED)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
 def test_gpt_oss_20b_chunked_prompt(orc):
     """20b shape, a 150-token prompt in 10 passes: the 128-key sliding window
     moves inside the prompt."""
