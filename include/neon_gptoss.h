@@ -119,6 +119,16 @@ neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
 /* Synchronises and copies the fp32 logits of the last step [batch][vocab]. */
 neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream);
 
+/* Next-token choice of the decode steps: temperature 0 (the default) is
+ * greedy argmax; temperature > 0 samples from softmax(logits / temperature)
+ * restricted to the smallest top-probability set of mass >= top_p (nucleus,
+ * top_p in (0, 1]; 1 keeps every token), with a counter-based RNG keyed by
+ * (seed, sequence, position), so a run is reproducible.  Prompt tokens are
+ * still teacher-forced.  (The reference has no model code; this is the
+ * sampling step of SURVEY's next-component list.) */
+neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
+                              uint64_t seed);
+
 /* Synchronises and copies one activation buffer of the last step (for
  * parity tests of the fused chain; "last layer" = the final decoder layer):
  *   "hidden"    residual stream before the final norm, bf16 [batch][hidden]
@@ -210,6 +220,12 @@ neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                              const int32_t* pos, uint16_t* out, int B, int Hq,
                              int Hkv, int D, int T_max, int window,
                              void* stream);
+
+/* One draw per row from logits [B][V] (device fp32), as neon_set_sampling
+ * describes; pos [B] (device int32) keys the RNG; out_ids [B] device int32.
+ * temperature > 0, top_p in (0, 1]. */
+neon_status neon_sample(const float* logits, int B, int V, float temperature, float top_p,
+                        uint64_t seed, const int32_t* pos, int32_t* out_ids, void* stream);
 
 /* ---- prefill kernels (matrix cores; fp32 accumulate in the MFMA order) --- */
 

@@ -32,7 +32,7 @@ EXPORTS = (
     "neon_mxfp4_dequant", "neon_mxfp4_gemv", "neon_gemv_bf16", "neon_rmsnorm",
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
-    "neon_attn_prefill",
+    "neon_attn_prefill", "neon_set_sampling", "neon_sample",
 )
 
 
@@ -95,6 +95,8 @@ def lib():
             "neon_gemm_bf16": [_P] * 4 + [_I] * 4 + [_P],
             "neon_moe_prefill": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
             "neon_attn_prefill": [_P] * 5 + [_I] * 6 + [_P],
+            "neon_set_sampling": [_P, _F, _F, _U64],
+            "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -220,6 +222,11 @@ def attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, D, T_max, window, 
                                    _ptr(out), M, Hq, Hkv, D, T_max, window, _stream(stream)))
 
 
+def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=None):
+    _check(lib().neon_sample(_ptr(logits), B, V, temperature, top_p, seed, _ptr(pos),
+                             _ptr(out_ids), _stream(stream)))
+
+
 PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED = 0, 1, 2
 
 
@@ -283,6 +290,11 @@ class Engine:
         """PREFILL_CHUNKED (default: 16 prompt rows per pass), PREFILL_STEPWISE
         (every prompt token as a decode step) or PREFILL_BATCHED (switched off)."""
         self._chk(lib().neon_set_prefill_mode(self._ctx, mode))
+
+    def set_sampling(self, temperature: float = 0.0, top_p: float = 1.0, seed: int = 0):
+        """temperature 0: greedy; else softmax(logits / temperature) within the
+        top-p nucleus, reproducible for a given seed."""
+        self._chk(lib().neon_set_sampling(self._ctx, temperature, top_p, seed))
 
     def prefill(self, ids, stream=None):
         """ids: nested list / array [batch][n_tokens] of int."""

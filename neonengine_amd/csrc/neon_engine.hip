@@ -98,6 +98,10 @@ struct neon_ctx {
   float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
   int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
           *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
+  // next-token choice (temperature 0: greedy argmax)
+  float temperature = 0.0f, top_p = 1.0f;
+  uint64_t sample_seed = 0;
+  float* sample_scratch = nullptr;  // [max_batch][vocab] exp values
   // prompt passes: positions and sequences of the rows of one pass
   int32_t *row_pos = nullptr, *row_seq = nullptr;
   // captured decode step
@@ -368,6 +372,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_apo = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * c.head_dim * 4),
                o_apml = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
                o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
+               o_samp = take(Bm * (size_t)c.vocab * 4),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -393,6 +398,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
   ctx->sin_t = (float*)(W + o_sin);
   ctx->row_pos = (int32_t*)(W + o_rpos); ctx->row_seq = (int32_t*)(W + o_rseq);
+  ctx->sample_scratch = (float*)(W + o_samp);
   // ---- RoPE table ----
   std::vector<float> ct, st;
   rope_table_host(&c, c.max_seq, ct, st);
@@ -655,9 +661,14 @@ static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
   lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab; lm.K = H; lm.B = B;
   lm.nblk = ctx->lm_nblk;
   const int lm_parts = launch_gemv_step(lm, B, st);
-  launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, lm_parts,
-                        ctx->tokens, ctx->tok_stride, ctx->pos, ctx->prompt_len,
-                        ctx->last_ids, B, st);
+  if (ctx->temperature > 0.0f)
+    launch_sample(ctx->logits, B, c.vocab, ctx->temperature, ctx->top_p, ctx->sample_seed,
+                  ctx->pos, ctx->sample_scratch, ctx->last_ids, ctx->tokens, ctx->tok_stride,
+                  ctx->prompt_len, true, st);
+  else
+    launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, lm_parts,
+                          ctx->tokens, ctx->tok_stride, ctx->pos, ctx->prompt_len,
+                          ctx->last_ids, B, st);
 }
 
 static neon_status ensure_graph(neon_ctx* ctx, int B) {
@@ -869,6 +880,25 @@ extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch
   neon_status s = run_steps(ctx, n_tokens, st);
   if (s != NEON_OK) return s;
   ctx->host_pos = n_tokens;
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
+                                         uint64_t seed) {
+  if (!ctx) return NEON_EINVAL;
+  if (!(temperature >= 0.0f) || !(top_p > 0.0f && top_p <= 1.0f) ||
+      !(temperature < 3.0e38f))
+    FAIL(ctx, NEON_EINVAL, "neon_set_sampling: temperature %g must be >= 0 and finite, "
+                           "top_p %g in (0, 1]", temperature, top_p);
+  ctx->temperature = temperature;
+  ctx->top_p = top_p;
+  ctx->sample_seed = seed;
+  // the captured step holds the choice kernel and its arguments
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipDeviceSynchronize());
+  if (ctx->graph_exec) { (void)hipGraphExecDestroy(ctx->graph_exec); ctx->graph_exec = nullptr; }
+  if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
+  ctx->graph_batch = 0;
   return NEON_OK;
 }
 
@@ -1145,6 +1175,26 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);
   if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_sample(const float* logits, int B, int V, float temperature,
+                                   float top_p, uint64_t seed, const int32_t* pos,
+                                   int32_t* out_ids, void* stream) {
+  if (!logits || !pos || !out_ids) KFAIL(NEON_EINVAL, "neon_sample: null pointer");
+  if (B < 1 || B > 65535 || V < 1 || !(temperature > 0.0f) || !(temperature < 3.0e38f) ||
+      !(top_p > 0.0f && top_p <= 1.0f))
+    KFAIL(NEON_EINVAL, "neon_sample: bad shape or sampling parameters");
+  hipStream_t st = S(stream);
+  float* scratch = nullptr;  // the exp values [B][V]
+  if (hipMallocAsync((void**)&scratch, (size_t)B * V * 4, st) != hipSuccess)
+    KFAIL(NEON_ENOMEM, "neon_sample: scratch allocation failed");
+  // pos is read only (advance = false): cast for the shared kernel signature
+  launch_sample(logits, B, V, temperature, top_p, seed, const_cast<int32_t*>(pos), scratch,
+                out_ids, nullptr, 0, nullptr, false, st);
+  hipError_t e = hipGetLastError();
+  (void)hipFreeAsync(scratch, st);
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_sample: launch failed: %s", hipGetErrorString(e));
   return NEON_OK;
 }
 

@@ -1112,6 +1112,149 @@ void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
 }
 
 // ===========================================================================
+// Sampling (temperature T > 0, nucleus top_p in (0, 1]) for one row per
+// block of 1024 threads:
+//   m = max_i l_i;  e_i = exp((l_i - m) / T);  Z = sum e_i
+//   t = the largest fp32 value with  sum_{e_i >= t} e_i >= top_p Z
+//       (a bit-by-bit search over the positive floats; t = 0 keeps all)
+//   u = uniform [0, 1) from SplitMix64(seed, row, position)
+//   id = the first vocab index where the running sum of kept e_i exceeds
+//        u sum_{e_i >= t} e_i
+// The e_i go to scratch [B][V] once; every sum is per thread over a fixed
+// index set, then over the waves in order, so a draw is reproducible.
+// With `advance` the block also writes the token and advances pos like the
+// greedy argmax (teacher forcing inside the prompt).
+// ===========================================================================
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// sum over the block (1024 threads) in wave order; every thread gets it
+__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // red is free
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) t = __fadd_rn(t, red[w]);
+  return t;
+}
+__device__ __forceinline__ float block_max_1024(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) t = fmaxf(t, red[w]);
+  return t;
+}
+
+__global__ __launch_bounds__(1024) void k_sample(
+    const float* __restrict__ logits, int V, float inv_temp, float top_p, uint64_t seed,
+    int32_t* __restrict__ pos, float* __restrict__ scratch, int32_t* __restrict__ out_ids,
+    int32_t* __restrict__ tokens, int tok_stride, const int32_t* __restrict__ prompt_len,
+    int advance) {
+  __shared__ float red[16];
+  __shared__ float scan[1024];
+  __shared__ int32_t pick;
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float* l = logits + (size_t)b * V;
+  float* e = scratch + (size_t)b * V;
+  const int p = pos[b];
+  float m = -INFINITY;
+  for (int i = tid; i < V; i += 1024) m = fmaxf(m, l[i]);
+  m = block_max_1024(m, red);
+  float z = 0.0f;
+  for (int i = tid; i < V; i += 1024) {
+    const float v = neon_expf(__fmul_rn(__fsub_rn(l[i], m), inv_temp));
+    e[i] = v;
+    z = __fadd_rn(z, v);
+  }
+  z = block_sum_1024(z, red);  // also orders the e[] stores before the reads below
+  uint32_t t_bits = 0;          // threshold as positive-float bits (0: keep all)
+  float kept = z;
+  if (top_p < 1.0f) {
+    const float goal = __fmul_rn(top_p, z);
+    for (int bit = 30; bit >= 0; --bit) {
+      const uint32_t cand = t_bits | (1u << bit);
+      const float t = __builtin_bit_cast(float, cand);
+      float s = 0.0f;
+      for (int i = tid; i < V; i += 1024) {
+        const float v = e[i];
+        s = __fadd_rn(s, v >= t ? v : 0.0f);
+      }
+      s = block_sum_1024(s, red);
+      if (s >= goal) { t_bits = cand; kept = s; }  // uniform: every thread has s
+    }
+  }
+  const float t = __builtin_bit_cast(float, t_bits);
+  const uint64_t r = splitmix64(seed ^ splitmix64(((uint64_t)(uint32_t)b << 32) | (uint32_t)p));
+  const float u = (float)(r >> 40) * 0x1.0p-24f;
+  const float target = __fmul_rn(u, kept);
+  // running sums in vocab order: thread tid owns the contiguous slice
+  // [tid C, tid C + C) of kept values; block prefix over the threads
+  const int C = (V + 1023) / 1024;
+  const int i0 = min(tid * C, V), i1 = min(i0 + C, V);
+  float local = 0.0f;
+  for (int i = i0; i < i1; ++i) { const float v = e[i]; local = __fadd_rn(local, v >= t ? v : 0.0f); }
+  scan[tid] = local;
+  if (tid == 0) pick = -1;
+  __syncthreads();
+  if (tid == 0) {  // exclusive prefix in thread order (one thread: a fixed order)
+    float acc = 0.0f;
+    for (int k2 = 0; k2 < 1024; ++k2) { const float x = scan[k2]; scan[k2] = acc; acc = __fadd_rn(acc, x); }
+  }
+  __syncthreads();
+  {
+    // the thread whose slice holds the target walks it; its own running sum
+    // may round differently from the prefix, so it ends on its last kept
+    // index if the walk does not cross the target
+    float run = scan[tid];
+    if (run <= target && local > 0.0f && __fadd_rn(run, local) > target) {
+      int last = -1, found = -1;
+      for (int i = i0; i < i1; ++i) {
+        const float v = e[i];
+        if (v >= t) {
+          last = i;
+          run = __fadd_rn(run, v);
+          if (run > target) { found = i; break; }
+        }
+      }
+      pick = found >= 0 ? found : last;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int32_t id = pick;
+    if (id < 0) {  // target at the very top (rounding): the last kept index
+      for (int i = V - 1; i >= 0; --i) if (e[i] >= t) { id = i; break; }
+      if (id < 0) id = 0;
+    }
+    out_ids[b] = id;
+    if (advance) {
+      if (p + 1 >= prompt_len[b]) tokens[(size_t)b * tok_stride + p + 1] = id;
+      pos[b] = p + 1;
+    }
+  }
+}
+
+void launch_sample(const float* logits, int B, int V, float temperature, float top_p,
+                   uint64_t seed, int32_t* pos, float* scratch, int32_t* out_ids,
+                   int32_t* tokens, int tok_stride, const int32_t* prompt_len, bool advance,
+                   hipStream_t st) {
+  hipLaunchKernelGGL(k_sample, dim3(B), dim3(1024), 0, st, logits, V, 1.0f / temperature,
+                     top_p, seed, pos, scratch, out_ids, tokens, tok_stride, prompt_len,
+                     advance ? 1 : 0);
+}
+
+// ===========================================================================
 // Embedding gather: h[b] = embed[tokens[b][pos[b]]]
 // ===========================================================================
 __global__ void k_embed(const int32_t* __restrict__ tokens, int tok_stride,

@@ -68,12 +68,18 @@ def test_context_calls_reject_null_context():
     assert L.neon_read_logits(None, None, None) == ne.NEON_EINVAL
     assert L.neon_read_activation(None, b"hidden", None, 0, None) == ne.NEON_EINVAL
     assert L.neon_seq_len(None, None) == ne.NEON_EINVAL
+    assert L.neon_set_sampling(None, 1.0, 0.9, 0) == ne.NEON_EINVAL
     L.neon_ctx_destroy(None)  # no-op
 
 
 def test_kernel_entry_points_validate_on_host():
     L = ne.lib()
     p = C.c_void_p(16)  # never dereferenced: validation fails first
+    assert L.neon_sample(None, 1, 8, 1.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL
+    assert L.neon_sample(p, 1, 8, 0.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL   # temperature
+    assert L.neon_sample(p, 1, 8, 1.0, 0.0, 0, p, p, None) == ne.NEON_EINVAL   # top_p
+    assert L.neon_sample(p, 1, 8, 1.0, 1.5, 0, p, p, None) == ne.NEON_EINVAL
+    assert L.neon_sample(p, 0, 8, 1.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_gemv(None, p, None, p, p, 8, 64, 1, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 8, 48, 1, None) == ne.NEON_EINVAL   # K % 32
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 0, 64, 1, None) == ne.NEON_EINVAL
