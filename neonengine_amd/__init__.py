@@ -67,6 +67,15 @@ def lib():
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `python -m neonengine_amd._build` "
                 "(the gfx950 HIP library is required; there is no fallback)")
+        # One HIP runtime per process: torch bundles its own libamdhip64 (same
+        # soname, libamdhip64.so.7), and a process that loads /opt/rocm's copy
+        # through this library first and torch's afterwards holds two runtimes,
+        # of which ours then sees no device.  Loading torch first makes the
+        # library's libamdhip64.so.7 dependency resolve to torch's copy.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         sig = {
             "neon_config_preset": [C.c_char_p, _P],
@@ -288,7 +297,8 @@ class Engine:
 
     def set_prefill_mode(self, mode: int):
         """PREFILL_CHUNKED (default: 16 prompt rows per pass), PREFILL_STEPWISE
-        (every prompt token as a decode step) or PREFILL_BATCHED (switched off)."""
+        (every prompt token as a decode step) or PREFILL_BATCHED (all prompt rows at
+        once on the matrix cores; equal to the others up to bf16 rounding)."""
         self._chk(lib().neon_set_prefill_mode(self._ctx, mode))
 
     def set_sampling(self, temperature: float = 0.0, top_p: float = 1.0, seed: int = 0):

@@ -43,7 +43,9 @@ def d2h(ptr, nbytes, dtype):
     """Copy nbytes from a raw device pointer into a numpy array."""
     global _hip
     if _hip is None:
-        _hip = C.CDLL("libamdhip64.so")
+        import neonengine_amd as ne
+        ne.lib()  # torch first, then the library: their HIP runtime is this one
+        _hip = C.CDLL("libamdhip64.so.7")
         _hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
         _hip.hipMemcpy.restype = C.c_int
     out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)

@@ -119,6 +119,7 @@ def test_no_device_reports_ehip():
 def test_engine_header_is_self_contained_cpp(tmp_path):
     """include/neon_engine.hpp compiles standalone against the C header."""
     import shutil
+    import ast
     import subprocess
     gxx = shutil.which("g++")
     if not gxx:
@@ -128,3 +129,21 @@ def test_engine_header_is_self_contained_cpp(tmp_path):
     r = subprocess.run([gxx, "-std=c++17", "-fsyntax-only", "-I", os.path.join(ROOT, "include"),
                         str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_one_hip_runtime_per_process():
+    """Loading the library before torch must not map a second HIP runtime:
+    torch bundles libamdhip64.so.7 under its own path, and a process holding
+    both copies sees no device through the library's."""
+    import ast
+    import subprocess
+    import sys
+    pytest.importorskip("torch")
+    code = ("import neonengine_amd as ne; ne.lib(); import torch; "
+            "print(sorted({l.split()[-1] for l in open('/proc/self/maps') "
+            "if 'libamdhip64' in l or 'libhsa-runtime64' in l}))")
+    out = subprocess.run([sys.executable, "-c", code], cwd=ROOT, capture_output=True,
+                         text=True, timeout=300, check=True).stdout
+    maps = ast.literal_eval(out.strip().splitlines()[-1])
+    assert sum("libamdhip64" in m for m in maps) == 1, maps
+    assert sum("libhsa-runtime64" in m for m in maps) == 1, maps
