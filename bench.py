@@ -187,6 +187,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--model", default="gpt-oss-20b", choices=["gpt-oss-20b", "gpt-oss-120b"],
+                    help="model shape (the headline metric is quoted on gpt-oss-20b)")
     ap.add_argument("--batch", type=int, default=1,
                     help="sequences decoded together (the headline metric is batch 1; "
                          "larger batches are reported as a separate line)")
@@ -218,8 +220,8 @@ def main():
         return
     B = args.batch
     max_seq = args.prompt + args.warmup + args.steps + 8
-    cfg = ne.config_preset("gpt-oss-20b", max_seq=max_seq, max_batch=B)
-    log(f"[bench] creating gpt-oss-20b context (max_seq {max_seq})")
+    cfg = ne.config_preset(args.model, max_seq=max_seq, max_batch=B)
+    log(f"[bench] creating {args.model} context (max_seq {max_seq})")
     eng = ne.Engine(cfg, device=0)
     stream = torch.cuda.current_stream()
     eng.init_random(args.seed, stream)
@@ -231,11 +233,8 @@ def main():
     log(f"[bench] prompt of {args.prompt} tokens (first, untimed pass): "
         f"{time.perf_counter() - t0:.2f}s")
     prefill = None
-    if B == 1:
-        # timed prompt pass in the library's default mode: prompt rows 16 at a
-        # time through the batched decode kernels (bit-identical to running
-        # every prompt token as a decode step); the matrix-core pass is
-        # switched off for now
+
+    def timed_prefill():
         p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         pt0 = time.perf_counter()
@@ -243,11 +242,32 @@ def main():
         eng.prefill(prompt, stream)
         p1.record(stream)
         torch.cuda.synchronize()
-        pre_s = max(time.perf_counter() - pt0, p0.elapsed_time(p1) * 1e-3)
+        return max(time.perf_counter() - pt0, p0.elapsed_time(p1) * 1e-3)
+
+    if B == 1:
+        # the matrix-core prompt pass (all rows at once; equal to the exact
+        # modes up to bf16 rounding), first once untimed for its scratch
+        eng.set_prefill_mode(ne.PREFILL_BATCHED)
+        eng.prefill(prompt, stream)
+        mfma_s = timed_prefill()
+        log(f"[bench] matrix-core prompt pass: {mfma_s * 1e3:.1f} ms = "
+            f"{args.prompt / mfma_s:.0f} tok/s")
+        # then the library's default mode, whose cache the decode steps use:
+        # prompt rows 16 at a time through the batched decode kernels
+        # (bit-identical to running every prompt token as a decode step)
+        eng.set_prefill_mode(ne.PREFILL_CHUNKED)
+        pre_s = timed_prefill()
+        flops = prefill_flops(cfg, args.prompt)
         prefill = {"tokens": args.prompt, "ms": round(pre_s * 1e3, 3),
                    "tokens_per_s": round(args.prompt / pre_s, 1),
                    "mode": "chunked (16 prompt rows per pass through the batched decode kernels)",
-                   "flop_batched_form": prefill_flops(cfg, args.prompt)}
+                   "matrix_core_pass": {
+                       "ms": round(mfma_s * 1e3, 3),
+                       "tokens_per_s": round(args.prompt / mfma_s, 1),
+                       "tflop_per_s": round(flops / mfma_s / 1e12, 1),
+                       "frac_of_bf16_mfma_peak": round(flops / mfma_s / 1e12
+                                                       / MFMA_BF16_PEAK_TFLOPS, 4)},
+                   "flop_batched_form": flops}
         log(f"[bench] prompt pass: {pre_s * 1e3:.1f} ms = {args.prompt / pre_s:.0f} tok/s")
     eng.decode(args.warmup, stream)
     torch.cuda.synchronize()
@@ -274,14 +294,15 @@ def main():
 
     mb = moe_bytes(cfg)
     moe_s = moe_gbs = None
-    if args.moe_reps > 0 and B == 1:  # 0 skips it (profiling runs that want only the decode loop)
+    headline = B == 1 and args.model == "gpt-oss-20b"
+    if args.moe_reps > 0 and headline:  # 0 skips it (profiling runs that want only the decode loop)
         moe_s = time_moe(ne, torch, eng, cfg, args.moe_reps)
         moe_gbs = mb / moe_s / 1e9
         log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, {moe_gbs:.0f} GB/s")
     eng.close()
 
     cpu = None
-    if not args.no_cpu_baseline and B == 1:
+    if not args.no_cpu_baseline and headline:
         log("[bench] CPU baseline (build's oracle) ...")
         cpu = cpu_baseline(args.seed, 4, args.cpu_steps)
         log(f"[bench] CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads")
@@ -299,8 +320,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16 activations, mxfp4 experts, fp32 accumulate",
         "data": "synthetic (random-init weights, uniform random prompt ids)",
-        "config": {"workload": f"gpt-oss-20b-shaped greedy decode, batch {B}, after a "
-                               f"{args.prompt}-token prompt (BASELINE config 3)",
+        "config": {"workload": f"{args.model}-shaped greedy decode, batch {B}, after a "
+                               f"{args.prompt}-token prompt (BASELINE config "
+                               f"{3 if args.model == 'gpt-oss-20b' else 4})",
                    "batch": B, "prompt": args.prompt,
                    "kv_len": [kv0, kv0 + args.steps], "parallelism": "none (1 GPU)"},
         # bytes per token of a batch-1 step (at batch > 1 weights are shared)
@@ -311,7 +333,7 @@ def main():
                      "bound": "hbm", "achieved": moe_gbs and round(moe_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": moe_gbs and round(moe_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic(), "bytes_per_launch": mb,
+                     "traffic": load_traffic() if moe_gbs else None, "bytes_per_launch": mb,
                      "us_per_launch": moe_s and round(moe_s * 1e6, 3)},
         "cpu_baseline": cpu,
         "prefill": prefill,

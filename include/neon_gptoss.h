@@ -97,8 +97,10 @@ neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
  *    sequence's cache), then the last prompt token runs as a decode step.
  *    Bit-identical to NEON_PREFILL_STEPWISE.
  *  - NEON_PREFILL_STEPWISE: every prompt token as a decode step.
- *  - NEON_PREFILL_BATCHED: all rows at once on the matrix cores; switched off
- *    (selecting it returns NEON_ESTATE).
+ *  - NEON_PREFILL_BATCHED: all prompt rows of a sequence at once on the
+ *    matrix cores (bf16 MFMA GEMMs, grouped MXFP4 expert GEMMs, tiled causal
+ *    prompt attention); agrees with the other modes to bf16 rounding, not
+ *    bit for bit.
  * None has a counterpart in the reference, which has no model code. */
 neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
                          int n_tokens, void* stream);

@@ -94,7 +94,7 @@ struct neon_ctx {
   char* pf = nullptr;
   int pf_rows = 0;
   uint16_t *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
-           *pf_ao = nullptr, *pf_act = nullptr;
+           *pf_ao = nullptr, *pf_act = nullptr, *pf_ks = nullptr, *pf_vs = nullptr;
   float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
   int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
           *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
@@ -726,7 +726,8 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
                o_lg = take(M * E * 4), o_sc = take(M * k * 4), o_yb = take(M * k * H * 4),
                o_idx = take(M * k * 4), o_lt = take(M * k * 4), o_ls = take(M * k * 4),
                o_eo = take((E + 1) * 4), o_te = take(tiles * 4), o_tr = take(tiles * 4),
-               o_nt = take(4);
+               o_nt = take(4), o_ks = take(M * c.n_kv_heads * c.head_dim * 2),
+               o_vs = take(M * c.n_kv_heads * c.head_dim * 2);
   if (ctx->pf) {
     HIPCHK(ctx, hipStreamSynchronize(st));  // earlier prefill work may still read it
     (void)hipFree(ctx->pf);
@@ -746,6 +747,7 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
   ctx->pf_ltok = (int32_t*)(P + o_lt); ctx->pf_lslot = (int32_t*)(P + o_ls);
   ctx->pf_eoff = (int32_t*)(P + o_eo); ctx->pf_tile_e = (int32_t*)(P + o_te);
   ctx->pf_tile_r0 = (int32_t*)(P + o_tr); ctx->pf_ntiles = (int32_t*)(P + o_nt);
+  ctx->pf_ks = (uint16_t*)(P + o_ks); ctx->pf_vs = (uint16_t*)(P + o_vs);
   ctx->pf_rows = (int)M;
   return NEON_OK;
 }
@@ -753,6 +755,9 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
 // Rows 0 .. M-1 of sequence b (token ids already in ctx->tokens) through all
 // layers; their keys/values land in the KV cache.  The hidden states of these
 // rows are not needed afterwards (the last prompt token runs as a decode step).
+// A sliding layer with a ring cache (fewer rows than positions) gets its keys
+// and values staged for all M rows first, so that the prompt attention sees
+// every row; only the last rows that fit its ring are then stored in it.
 static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
   const neon_config& c = ctx->cfg;
   const int H = c.hidden, D = c.head_dim, Hq = c.n_heads, Hkv = c.n_kv_heads;
@@ -761,15 +766,21 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
-    // (this switched-off pass needs caches of every position: see neon_set_prefill_mode)
     const size_t kvo = ctx->kv_off[l] + (size_t)b * Hkv * ctx->kv_rows[l] * D;
+    const bool ring = ctx->kv_mask[l] >= 0;
+    uint16_t* kd = ring ? ctx->pf_ks : ctx->kc + kvo;
+    uint16_t* vd = ring ? ctx->pf_vs : ctx->vc + kvo;
+    const int Td = ring ? ctx->pf_rows : ctx->kv_rows[l];
     launch_rmsnorm(ctx->pf_h, w.attn_norm, ctx->pf_xn, M, H, c.rms_eps, st);
     launch_gemm_bf16(ctx->pf_xn, H, w.wqkv, H, w.bqkv, ctx->pf_qkv, nullptr, qkv_rows, M,
                      qkv_rows, H, 0, st);
-    launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv,
-                        ctx->kv_rows[l], ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, st);
-    launch_attn_prefill(ctx->pf_q, ctx->kc + kvo, ctx->vc + kvo, w.sinks, ctx->pf_ao, M, Hq,
-                        Hkv, ctx->kv_rows[l], sliding ? c.sliding_window : 0, st);
+    launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv, Td,
+                        ctx->pf_q, kd, vd, st);
+    launch_attn_prefill(ctx->pf_q, kd, vd, w.sinks, ctx->pf_ao, M, Hq, Hkv, Td,
+                        sliding ? c.sliding_window : 0, st);
+    if (ring)
+      launch_kv_ring_store(ctx->pf_ks, ctx->pf_vs, Td, std::max(0, M - ctx->kv_rows[l]), M,
+                           Hkv, ctx->kv_rows[l], ctx->kc + kvo, ctx->vc + kvo, st);
     launch_gemm_bf16(ctx->pf_ao, Hq * D, w.wo, Hq * D, w.bo, ctx->pf_h, nullptr, H, M, H,
                      Hq * D, 1, st);
     launch_rmsnorm(ctx->pf_h, w.mlp_norm, ctx->pf_xn, M, H, c.rms_eps, st);
@@ -789,11 +800,9 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
   }
 }
 
-// The batched prompt pass is switched off: the first GPU process that ran its
-// expert-grouping, grouped-GEMM and attention kernels (all parity checks
-// passed) left the device unusable for the next process, and no cause has
-// been shown yet.  Until one is, selecting it is refused.
-static const bool kBatchedPrefillEnabled = false;
+// The batched prompt pass (matrix-core GEMMs, grouped experts, tiled prompt
+// attention).  Kept behind one switch so that it can be refused as a whole.
+static const bool kBatchedPrefillEnabled = true;
 
 extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
   if (!ctx) return NEON_EINVAL;
@@ -801,8 +810,7 @@ extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
       mode != NEON_PREFILL_CHUNKED)
     FAIL(ctx, NEON_EINVAL, "neon_set_prefill_mode: unknown mode %d", mode);
   if (mode == NEON_PREFILL_BATCHED && !kBatchedPrefillEnabled)
-    FAIL(ctx, NEON_ESTATE, "neon_set_prefill_mode: the batched prompt pass is switched off "
-                           "(a device loss after its first GPU run is not yet explained)");
+    FAIL(ctx, NEON_ESTATE, "neon_set_prefill_mode: the batched prompt pass is switched off");
   ctx->prefill_mode = mode;
   return NEON_OK;
 }
@@ -1223,8 +1231,7 @@ extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
       H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
     KFAIL(NEON_EINVAL, "neon_moe_prefill: bad shape M=%d E=%d H=%d I=%d k=%d", M, E, H, I, k);
   if (!kBatchedPrefillEnabled)
-    KFAIL(NEON_ESTATE, "neon_moe_prefill: switched off (a device loss after its first GPU "
-                       "run is not yet explained)");
+    KFAIL(NEON_ESTATE, "neon_moe_prefill: the batched prompt pass is switched off");
   // idx is device data: every entry must lie in [0, E).
   hipStream_t st = S(stream);
   const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
@@ -1265,8 +1272,7 @@ extern "C" neon_status neon_attn_prefill(const uint16_t* q, const uint16_t* k_ca
   if (G != 1 && G != 2 && G != 4 && G != 8)
     KFAIL(NEON_EINVAL, "neon_attn_prefill: Hq/Hkv must be 1, 2, 4 or 8");
   if (!kBatchedPrefillEnabled)
-    KFAIL(NEON_ESTATE, "neon_attn_prefill: switched off (a device loss after its first GPU "
-                       "run is not yet explained)");
+    KFAIL(NEON_ESTATE, "neon_attn_prefill: the batched prompt pass is switched off");
   launch_attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, T_max, window, S(stream));
   KLAUNCHED();
 }

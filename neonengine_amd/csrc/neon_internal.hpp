@@ -165,6 +165,8 @@ void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
 void launch_rope_kv_rows(const uint16_t* qkv, int q_stride, const float* cos_t,
                          const float* sin_t, int M, int Hq, int Hkv, int T_max,
                          uint16_t* q_out, uint16_t* kc, uint16_t* vc, hipStream_t st);
+void launch_kv_ring_store(const uint16_t* ks, const uint16_t* vs, int S, int t0, int M,
+                          int Hkv, int R, uint16_t* kc, uint16_t* vc, hipStream_t st);
 void launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                          const uint16_t* sinks, uint16_t* out, int M, int Hq, int Hkv,
                          int T_max, int window, hipStream_t st);

@@ -447,6 +447,27 @@ void launch_rope_kv_rows(const uint16_t* qkv, int q_stride, const float* cos_t,
                      sin_t, Hq, Hkv, T_max, q_out, kc, vc);
 }
 
+// Keys / values of prompt rows t0 .. M-1, staged as [Hkv][S][64], into a
+// sliding layer's ring cache [Hkv][R][64] (R a power of two, row t at t & (R-1)).
+__global__ void k_kv_ring_store(const uint16_t* __restrict__ ks,
+                                const uint16_t* __restrict__ vs, int S, int t0, int Hkv,
+                                int R, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
+  const int t = t0 + blockIdx.x;
+  const int r = t & (R - 1);
+  for (int i = threadIdx.x; i < Hkv * 64; i += blockDim.x) {
+    const int g = i >> 6, d = i & 63;
+    kc[((size_t)g * R + r) * 64 + d] = ks[((size_t)g * S + t) * 64 + d];
+    vc[((size_t)g * R + r) * 64 + d] = vs[((size_t)g * S + t) * 64 + d];
+  }
+}
+
+void launch_kv_ring_store(const uint16_t* ks, const uint16_t* vs, int S, int t0, int M,
+                          int Hkv, int R, uint16_t* kc, uint16_t* vc, hipStream_t st) {
+  if (M <= t0) return;
+  hipLaunchKernelGGL(k_kv_ring_store, dim3(M - t0), dim3(256), 0, st, ks, vs, S, t0, Hkv,
+                     R, kc, vc);
+}
+
 // ===========================================================================
 // Causal sink attention over a prompt (HFM:235-263).  grid (Hkv, ceil(M/64)),
 // block 64 G: wave w is q head g G + w, lane l is query row 64 blockIdx.y + l.
