@@ -151,6 +151,28 @@ def test_small_model_batched_decode(orc, batch):
     assert e1 < 2e-2 and e2 < 2e-2
 
 
+@pytest.mark.parametrize("batch", [1, 8])
+def test_small_model_128_experts(orc, batch):
+    """E = 128 (the 120b router width): the two-quarter top-k ranking and, at
+    batch 8, the expert grouping over 128 candidate experts."""
+    cfg, ocfg = pair(orc, **dict(SMALL, n_experts=128, intermediate=256, max_batch=batch,
+                                 max_seq=64))
+    prompt = [[(17 * i + 3 * b + 2) % 4096 for i in range(6)] for b in range(batch)]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 29, prompt, 16, batch=batch)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
+def test_small_model_batch32(orc):
+    """Batch 32: two 16-row input blocks per projection, and the per-row expert
+    kernels (32 rows x 4 slots is past the grouped kernels' 64 pairs)."""
+    cfg, ocfg = pair(orc, **dict(SMALL, max_batch=32, max_seq=48))
+    prompt = [[(7 * i + 5 * b + 1) % 4096 for i in range(5)] for b in range(32)]
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 31, prompt, 10, batch=32)
+    assert same.all()
+    assert e1 < 2e-2 and e2 < 2e-2
+
+
 def test_gpt_oss_20b_batch4(orc):
     """20b shape, 4 rows: the batched projections at K = 2880 and 4096."""
     cfg, ocfg = pair(orc, max_seq=64, max_batch=4)
