@@ -192,6 +192,8 @@ def main():
     ap.add_argument("--batch", type=int, default=1,
                     help="sequences decoded together (the headline metric is batch 1; "
                          "larger batches are reported as a separate line)")
+    ap.add_argument("--matrix", action="store_true",
+                    help="run steps of 2+ sequences on the matrix cores (NEON_DECODE_MATRIX)")
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -225,6 +227,8 @@ def main():
     eng = ne.Engine(cfg, device=0)
     stream = torch.cuda.current_stream()
     eng.init_random(args.seed, stream)
+    if args.matrix:
+        eng.set_decode_mode(ne.DECODE_MATRIX)
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, cfg.vocab, size=(B, args.prompt), dtype=np.int64)
     t0 = time.perf_counter()
@@ -324,6 +328,7 @@ def main():
                                f"{args.prompt}-token prompt (BASELINE config "
                                f"{3 if args.model == 'gpt-oss-20b' else 4})",
                    "batch": B, "prompt": args.prompt,
+                   "decode_mode": "matrix" if args.matrix and B > 1 else "exact",
                    "kv_len": [kv0, kv0 + args.steps], "parallelism": "none (1 GPU)"},
         # bytes per token of a batch-1 step (at batch > 1 weights are shared)
         "step_bytes_per_token": bpt if B == 1 else None,

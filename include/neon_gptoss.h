@@ -109,6 +109,20 @@ enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1, NEON_PREFILL_CHUNKED
 /* Selects how neon_prefill runs the prompt (default NEON_PREFILL_CHUNKED). */
 neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
 
+enum { NEON_DECODE_EXACT = 0, NEON_DECODE_MATRIX = 1 };
+/* Selects how decode steps of two or more sequences run (a step of one
+ * sequence always runs the exact kernels):
+ *  - NEON_DECODE_EXACT (default): every dot product in the canonical fp32
+ *    order, so each sequence's logits are bit-identical to decoding it alone;
+ *  - NEON_DECODE_MATRIX: every weight row read once per step with the
+ *    sequences in the M dimension of v_mfma_f32_16x16x32_bf16 tiles (expert
+ *    rows dequantised exactly to bf16); the same rounding points, with fp32
+ *    additions in another order.  Needs max_batch <= 64, output widths that
+ *    are multiples of 16 and reductions that are multiples of 32 up to 4096
+ *    (NEON_EINVAL otherwise).
+ * No counterpart in the reference, which has no model code. */
+neon_status neon_set_decode_mode(neon_ctx* ctx, int mode);
+
 /* Runs `n_steps` greedy decode steps for every live sequence (each step
  * consumes the previously generated token and produces the next one). */
 neon_status neon_decode(neon_ctx* ctx, int n_steps, void* stream);
@@ -126,8 +140,8 @@ neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream);
  * restricted to the smallest top-probability set of mass >= top_p (nucleus,
  * top_p in (0, 1]; 1 keeps every token), with a counter-based RNG keyed by
  * (seed, sequence, position), so a run is reproducible.  Prompt tokens are
- * still teacher-forced.  (The reference has no model code; this is the
- * sampling step of SURVEY's next-component list.) */
+ * still teacher-forced.  (The reference has no model code, so nothing here
+ * has a counterpart in it.) */
 neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
                               uint64_t seed);
 
@@ -164,6 +178,13 @@ neon_status neon_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
 neon_status neon_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
                             const uint16_t* bias, const uint16_t* x,
                             uint16_t* y, int N, int K, int B, void* stream);
+
+/* y[b][n] = bf16(sum_k x[b][k] W[n][k] + bias[n]) for B <= 64 rows on the
+ * matrix cores (the projection kernel of NEON_DECODE_MATRIX): N a multiple
+ * of 16, K a multiple of 32 up to 4096, bias may be NULL.  Equal to
+ * neon_gemv_bf16 up to the order of the fp32 additions. */
+neon_status neon_gemv_bf16_mfma(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                                uint16_t* y, int N, int K, int B, void* stream);
 
 /* bf16 GEMV (nn.Linear layout W [N][K]); bias may be NULL; K % 8 == 0. */
 neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,

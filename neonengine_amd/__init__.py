@@ -32,7 +32,8 @@ EXPORTS = (
     "neon_mxfp4_dequant", "neon_mxfp4_gemv", "neon_gemv_bf16", "neon_rmsnorm",
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
-    "neon_attn_prefill", "neon_set_sampling", "neon_sample",
+    "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
+    "neon_gemv_bf16_mfma",
 )
 
 
@@ -106,6 +107,8 @@ def lib():
             "neon_attn_prefill": [_P] * 5 + [_I] * 6 + [_P],
             "neon_set_sampling": [_P, _F, _F, _U64],
             "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P],
+            "neon_set_decode_mode": [_P, _I],
+            "neon_gemv_bf16_mfma": [_P, _P, _P, _P, _I, _I, _I, _P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -175,6 +178,11 @@ def gemv_bf16(W, bias, x, y, N, K, B, stream=None):
                                 _stream(stream)))
 
 
+def gemv_bf16_mfma(W, bias, x, y, N, K, B, stream=None):
+    _check(lib().neon_gemv_bf16_mfma(_ptr(W), _ptr(bias), _ptr(x), _ptr(y), N, K, B,
+                                     _stream(stream)))
+
+
 def rmsnorm(x, w, out, B, H, eps=1e-5, stream=None):
     _check(lib().neon_rmsnorm(_ptr(x), _ptr(w), _ptr(out), B, H, eps, _stream(stream)))
 
@@ -237,6 +245,7 @@ def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=N
 
 
 PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED = 0, 1, 2
+DECODE_EXACT, DECODE_MATRIX = 0, 1
 
 
 # ---------------------------------------------------------------------------
@@ -294,6 +303,12 @@ class Engine:
         p, n = C.c_void_p(), C.c_size_t()
         self._chk(lib().neon_tensor_ptr(self._ctx, name.encode(), C.byref(p), C.byref(n)))
         return p.value, n.value
+
+    def set_decode_mode(self, mode: int):
+        """DECODE_EXACT (default: batched steps bit-identical to batch 1) or
+        DECODE_MATRIX (steps of 2+ sequences on the matrix cores; equal to
+        the exact steps up to the order of fp32 additions)."""
+        self._chk(lib().neon_set_decode_mode(self._ctx, mode))
 
     def set_prefill_mode(self, mode: int):
         """PREFILL_CHUNKED (default: 16 prompt rows per pass), PREFILL_STEPWISE

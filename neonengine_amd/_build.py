@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libneon_gptoss.so")
-SOURCES = ["neon_kernels.hip", "neon_prefill.hip", "neon_engine.hip"]
+SOURCES = ["neon_kernels.hip", "neon_prefill.hip", "neon_mx.hip", "neon_engine.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

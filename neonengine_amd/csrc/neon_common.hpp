@@ -107,6 +107,14 @@ __device__ __forceinline__ float e8m0_scale(float v, uint32_t s) {
   return s == 0xFFu ? __builtin_nanf("") : r;
 }
 
+// RoPE (HFM:149-231) on one (x1, x2) = (dim d, dim d + 32) pair of a head:
+// o1 = x1 c - x2 s, o2 = x2 c + x1 s, each product rounded.
+__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,
+                                          float& o1, float& o2) {
+  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+  o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+}
+
 // ---- correctly rounded square root for positive normal x: the hardware
 // estimate (v_sqrt_f32, within 1 ulp) corrected by one step that compares x
 // with s_dn * s and s_up * s through exact fused residuals (the candidate
@@ -147,6 +155,18 @@ __host__ __device__ __forceinline__ float neon_expf(float x) {
   const float v = neon_expf_core(x);
   const float r = x > 0x1.62e43p+6f ? __builtin_inff() : (x < -0x1.9fe36ap+6f ? 0.0f : v);
   return x != x ? x : r;
+}
+
+// SwiGLU with clamp (HFM:83-87) on g = gate + bias, u = up + bias:
+// g = min(g, limit); u = clamp(u, -limit, limit);
+// act = (u + 1) * (g * (1 / (1 + exp(-(g * alpha))))), each step rounded.
+__device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
+                                              float limit) {
+  g = g > limit ? limit : g;
+  u = u > limit ? limit : (u < -limit ? -limit : u);
+  const float e = neon_expf(-__fmul_rn(g, alpha));
+  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+  return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
 }
 
 // A load that stays where it is written.  The compiler sinks a plain load

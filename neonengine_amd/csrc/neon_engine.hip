@@ -102,6 +102,11 @@ struct neon_ctx {
   float temperature = 0.0f, top_p = 1.0f;
   uint64_t sample_seed = 0;
   float* sample_scratch = nullptr;  // [max_batch][vocab] exp values
+  // batched steps on the matrix cores (max_batch >= 2)
+  int decode_mode = NEON_DECODE_EXACT;
+  float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
+  float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
+  int32_t* mx_part_idx = nullptr;
   // prompt passes: positions and sequences of the rows of one pass
   int32_t *row_pos = nullptr, *row_seq = nullptr;
   // captured decode step
@@ -373,6 +378,9 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_apml = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
                o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
                o_samp = take(Bm * (size_t)c.vocab * 4),
+               o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
+               o_mxv = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
+               o_mxi = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -399,6 +407,11 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->sin_t = (float*)(W + o_sin);
   ctx->row_pos = (int32_t*)(W + o_rpos); ctx->row_seq = (int32_t*)(W + o_rseq);
   ctx->sample_scratch = (float*)(W + o_samp);
+  if (Bm > 1) {
+    ctx->mx_ybuf = (float*)(W + o_mxy);
+    ctx->mx_part_val = (float*)(W + o_mxv);
+    ctx->mx_part_idx = (int32_t*)(W + o_mxi);
+  }
   // ---- RoPE table ----
   std::vector<float> ct, st;
   rope_table_host(&c, c.max_seq, ct, st);
@@ -651,7 +664,77 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
 
 // The decode step: every sequence's row through the layers, then lm_head and
 // the argmax that writes the next token and advances pos.
+// B >= 2 rows of a decode step on the matrix cores: every weight row read
+// once per step, the rows in the M dimension of the MFMA tiles.  Same
+// kernels' maths and rounding points as enqueue_rows; only the order of the
+// fp32 additions inside each dot product differs.
+static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
+  const neon_config& c = ctx->cfg;
+  const int H = c.hidden, D = c.head_dim, I = c.intermediate;
+  const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * D;
+  launch_embed(ctx->tokens, ctx->tok_stride, ctx->pos, nullptr, ctx->embed, ctx->h, H, B, st);
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = ctx->layers[l];
+    const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
+    uint16_t* kc_l = ctx->kc + ctx->kv_off[l];
+    uint16_t* vc_l = ctx->vc + ctx->kv_off[l];
+    launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
+    MxArgs q{};
+    q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.y = ctx->qkv;
+    q.B = B; q.N = qkv_rows; q.K = H;
+    launch_mx_gemv(q, 0, st);
+    launch_mx_rope_append(ctx->qkv, ctx->pos, nullptr, ctx->cos_t, ctx->sin_t, ctx->q_rot, kc_l,
+                          vc_l, B, c.n_heads, c.n_kv_heads, ctx->kv_rows[l], ctx->kv_mask[l],
+                          st);
+    AttnArgs a;
+    a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
+    a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml; a.seq = nullptr;
+    a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
+    a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
+    a.window = sliding ? c.sliding_window : 0;
+    a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
+    launch_attn(a, st);
+    MxArgs o{};
+    o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
+    o.B = B; o.N = H; o.K = c.n_heads * D;
+    launch_mx_gemv(o, 1, st);
+    RouterArgs r;
+    r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
+    r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
+    r.idx = ctx->moe_idx; r.score = ctx->moe_score;
+    r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
+    launch_router(r, st);
+    MxArgs gu{};
+    gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.bias = w.gu_bias; gu.x = ctx->xn;
+    gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.B = B; gu.N = 2 * I; gu.K = H;
+    gu.E = c.n_experts; gu.k = c.top_k; gu.alpha = c.swiglu_alpha; gu.limit = c.swiglu_limit;
+    MxArgs dn{};
+    dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.bias = w.dn_bias; dn.x = ctx->act;
+    dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.B = B; dn.N = H; dn.K = I;
+    dn.E = c.n_experts; dn.k = c.top_k;
+    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
+  }
+  launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
+  MxArgs lm{};
+  lm.W = ctx->lm_head; lm.x = ctx->xn; lm.out_f = ctx->logits;
+  lm.part_val = ctx->mx_part_val; lm.part_idx = ctx->mx_part_idx;
+  lm.B = B; lm.N = c.vocab; lm.K = H;
+  launch_mx_gemv(lm, 2, st);
+}
+
 static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
+  if (ctx->decode_mode == NEON_DECODE_MATRIX && B >= 2) {
+    const neon_config& c = ctx->cfg;
+    enqueue_rows_mx(ctx, B, st);
+    if (ctx->temperature > 0.0f)
+      launch_sample(ctx->logits, B, c.vocab, ctx->temperature, ctx->top_p, ctx->sample_seed,
+                    ctx->pos, ctx->sample_scratch, ctx->last_ids, ctx->tokens, ctx->tok_stride,
+                    ctx->prompt_len, true, st);
+    else
+      launch_argmax_advance(ctx->mx_part_val, ctx->mx_part_idx, c.vocab / 16, ctx->tokens,
+                            ctx->tok_stride, ctx->pos, ctx->prompt_len, ctx->last_ids, B, st);
+    return;
+  }
   const neon_config& c = ctx->cfg;
   const int H = c.hidden;
   enqueue_rows(ctx, B, ctx->pos, nullptr, st);
@@ -891,6 +974,33 @@ extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch
   return NEON_OK;
 }
 
+extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
+  if (!ctx) return NEON_EINVAL;
+  if (mode != NEON_DECODE_EXACT && mode != NEON_DECODE_MATRIX)
+    FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: unknown mode %d", mode);
+  if (mode == NEON_DECODE_MATRIX) {
+    const neon_config& c = ctx->cfg;
+    const int H = c.hidden, qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+    if (c.max_batch < 2 || c.max_batch > kMxMaxRows)
+      FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: the matrix-core steps need max_batch in "
+                             "[2, %d], not %d", kMxMaxRows, c.max_batch);
+    if (!mx_shape_ok(qkv_rows, H, c.max_batch) || !mx_shape_ok(H, c.n_heads * c.head_dim, 2) ||
+        !mx_shape_ok(c.vocab, H, 2) || !mx_shape_ok(2 * c.intermediate, H, 2) ||
+        !mx_shape_ok(H, c.intermediate, 2))
+      FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: the matrix-core steps need every output "
+                             "width a multiple of 16 and every reduction a multiple of 32 "
+                             "up to %d", kMxMaxK);
+  }
+  ctx->decode_mode = mode;
+  // the captured step holds the step's kernels
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  HIPCHK(ctx, hipDeviceSynchronize());
+  if (ctx->graph_exec) { (void)hipGraphExecDestroy(ctx->graph_exec); ctx->graph_exec = nullptr; }
+  if (ctx->graph) { (void)hipGraphDestroy(ctx->graph); ctx->graph = nullptr; }
+  ctx->graph_batch = 0;
+  return NEON_OK;
+}
+
 extern "C" neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
                                          uint64_t seed) {
   if (!ctx) return NEON_EINVAL;
@@ -1017,6 +1127,19 @@ extern "C" neon_status neon_mxfp4_gemv(const uint8_t* codes, const uint8_t* scal
   if (N < 1 || B < 1 || B > 65535 || K < 32 || K % 32 || K > 8192)
     KFAIL(NEON_EINVAL, "neon_mxfp4_gemv: bad shape N=%d K=%d B=%d", N, K, B);
   launch_mxfp4_gemv(codes, scales, bias, x, y, N, K, B, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" neon_status neon_gemv_bf16_mfma(const uint16_t* W, const uint16_t* bias,
+                                           const uint16_t* x, uint16_t* y, int N, int K, int B,
+                                           void* stream) {
+  if (!W || !x || !y) KFAIL(NEON_EINVAL, "neon_gemv_bf16_mfma: null pointer");
+  if (!mx_shape_ok(N, K, B))
+    KFAIL(NEON_EINVAL, "neon_gemv_bf16_mfma: need N %% 16 == 0, K %% 32 == 0, K <= %d, "
+                       "1 <= B <= %d (N=%d K=%d B=%d)", kMxMaxK, kMxMaxRows, N, K, B);
+  MxArgs a{};
+  a.W = W; a.bias = bias; a.x = x; a.y = y; a.B = B; a.N = N; a.K = K;
+  launch_mx_gemv(a, 0, S(stream));
   KLAUNCHED();
 }
 

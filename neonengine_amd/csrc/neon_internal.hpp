@@ -127,6 +127,35 @@ struct MoeArgs {
   float alpha, limit;
 };
 void launch_moe(const MoeArgs& a, hipStream_t st);
+
+// ---- batched decode on the matrix cores (neon_mx.hip) ----------------------
+constexpr int kMxMaxRows = 64;   // rows per step
+constexpr int kMxMaxK = 4096;    // reduction length
+struct MxArgs {
+  const void* W;             // bf16 [N][K], or MXFP4 codes [E][N][K/2] (expert modes)
+  const uint8_t* scales;     // MXFP4 scales [E][N][K/32] (expert modes)
+  const uint16_t* bias;      // [N], [E][N] (expert modes) or NULL (dense modes)
+  const uint16_t* x;         // input rows of K bf16: [B][K]; gate_up [B][K]; down [B k][K]
+  uint16_t* y;               // store / residual [B][N]; gate_up: act [B k][N / 2]
+  float* out_f;              // logits [B][N]; down: per-pair dot + bias [B k][N]
+  float* part_val;           // logits: per-block (max, lowest index) [B][N / 16]
+  int32_t* part_idx;
+  const int32_t* idx;        // expert modes: experts of the B k (row, slot) pairs
+  int B, N, K, E, k;
+  float alpha, limit;
+};
+bool mx_shape_ok(int N, int K, int B);
+// mode 0: y = bf16(x W^T + bias); 1: y = bf16(y + bf16(x W^T + bias));
+// 2: logits = x W^T (fp32) with per-block argmax partials
+void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);
+// experts of B rows: gate_up + SwiGLU into act, down + bias per pair, then the
+// slot-ordered combine h = bf16(h + bf16(sum_s score_s (dot_s + bias_s)))
+void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
+                   hipStream_t st);
+void launch_mx_rope_append(const uint16_t* qkv, const int32_t* pos, const int32_t* seq,
+                           const float* cos_t, const float* sin_t, uint16_t* q_out,
+                           uint16_t* kc, uint16_t* vc, int B, int Hq, int Hkv, int T_max,
+                           int key_mask, hipStream_t st);
 // 2 <= B, B k <= 64, idx / score given (router_lg NULL): each used expert's
 // weights read once for all rows that chose it; bit-identical to launch_moe
 bool moe_batched_supported(const MoeArgs& a);

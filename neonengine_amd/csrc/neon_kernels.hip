@@ -499,13 +499,6 @@ __device__ __forceinline__ void argmax_steps(float& v, int32_t& i) {
 
 enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2, MODE_QKV = 3 };
 
-// RoPE (HFM:149-231) on one (x1, x2) = (dim d, dim d + 32) pair of a head:
-// o1 = x1 c - x2 s, o2 = x2 c + x1 s, each product rounded.
-__device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,
-                                          float& o1, float& o2) {
-  o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
-}
 
 // Row r of wave group g.  MODE_QKV pairs dims d and d + 32 of one 64-dim
 // head (group g: head g / 32, d = g % 32) so that the RoPE pair of a q or k
@@ -1595,14 +1588,6 @@ __device__ __forceinline__ int moe_expert(const float* __restrict__ lg,
 //   act = bf16((u + 1) * (g * (1 / (1 + exp(-(g * alpha))))))  (HFM:86-87)
 // each product, sum and quotient rounded separately (no contraction).
 // ===========================================================================
-__device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
-                                              float limit) {
-  g = g > limit ? limit : g;
-  u = u > limit ? limit : (u < -limit ? -limit : u);
-  const float e = neon_expf(-__fmul_rn(g, alpha));
-  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
-  return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
-}
 
 // gate_up's expert for (b, slot); wave 0 of block (0, slot 0) also writes
 // the row's chosen ids and weights to idx_out/score_out when given.

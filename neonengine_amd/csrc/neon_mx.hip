@@ -1,0 +1,342 @@
+// neon_mx.hip -- batched decode steps (2 <= B <= 64 rows) on the matrix cores.
+//
+// The exact batched kernels keep every dot product in the canonical fp32
+// order of the batch-1 kernels, which makes them VALU-bound from B = 16 on.
+// Here each weight row is read once per step and the B rows ride in the M
+// dimension of v_mfma_f32_16x16x32_bf16 (fp32 accumulate):
+//   - a block owns 16 weight rows; its 4 waves split K into interleaved
+//     units of 32 elements (lane group g of wave w takes unit 16 i + 4 w + g
+//     in iteration i, so the 4 groups of one MFMA cover 4 different units and
+//     one lane loads 64 contiguous bytes of its row per iteration);
+//   - bf16 rows feed the B operand as loaded; MXFP4 expert rows go through
+//     v_cvt_scalef32_pk_bf16_fp4 (E2M1 x 2^(s-127) is a bf16 value, so the
+//     dequantisation is exact);
+//   - the expert kernels find their expert and its (token, slot) pairs
+//     themselves: block y serves the y-th used expert in ascending id.
+// Only the order of fp32 additions differs from the exact path (products
+// of two bf16 values are exact in fp32), and every rounding point, bias,
+// SwiGLU clamp and the slot-ordered combine are the exact path's
+// (HFM:82-112, 347-376).
+#include "neon_common.hpp"
+#include "neon_internal.hpp"
+
+namespace neon {
+
+typedef __bf16 mx_bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 mx_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float mx_f32x4 __attribute__((ext_vector_type(4)));
+
+enum { MX_STORE = 0, MX_RESID = 1, MX_LOGITS = 2, MX_GATE_UP = 3, MX_DOWN = 4 };
+
+typedef uint32_t mx_u32x4 __attribute__((ext_vector_type(4)));
+
+// weights are read once per step: non-temporal loads keep them out of the way
+__device__ __forceinline__ uint4 mx_load_nt(const void* p) {
+  const mx_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const mx_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ mx_bf16x8 mx_as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(mx_bf16x8, v);
+}
+
+// 8 E2M1 codes (one dword, low nibble = even element) times 2^(s-127) as bf16
+__device__ __forceinline__ mx_bf16x8 mx_fp4x8(uint32_t c, float scale) {
+  const mx_bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 0);
+  const mx_bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 1);
+  const mx_bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 2);
+  const mx_bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(c, scale, 3);
+  mx_bf16x8 r;
+  r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+  r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+  return r;
+}
+
+__device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
+  const float ov = __shfl_xor(v, off);
+  const int oi = __shfl_xor(i, off);
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+// One block: weight rows n0 .. n0+15 (of expert e for the expert modes) for
+// all R rows.  BT = row tiles of 16 (R <= 16 BT); IT = K iterations per wave
+// (K <= 512 IT).
+template <int BT, int IT, int MODE>
+__global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
+  constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
+  __shared__ mx_f32x4 red[3][BT][64];
+  __shared__ int s_rows[64];
+  __shared__ unsigned long long s_used[4];
+  __shared__ int s_e, s_R;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, U = K / 32;
+  const int n0 = blockIdx.x * 16;
+  int R = a.B, e = 0;
+  if constexpr (MOE) {
+    // the blockIdx.y-th used expert (ascending id) and its pairs q = b k + s
+    const int nk = a.B * a.k;
+    if (threadIdx.x < 4) s_used[threadIdx.x] = 0ull;
+    __syncthreads();
+    int id[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int q = lane + 64 * c;
+      id[c] = (w == 0 && q < nk) ? a.idx[q] : -1;
+      if (id[c] >= 0) atomicOr(&s_used[id[c] >> 6], 1ull << (id[c] & 63));
+    }
+    __syncthreads();
+    if (w == 0) {
+      int y = blockIdx.y, ee = -1;
+      for (int wd = 0; wd < 4 && ee < 0; ++wd) {
+        unsigned long long m = s_used[wd];
+        const int pc = __popcll(m);
+        if (y < pc) {
+          for (int t = 0; t < y; ++t) m &= m - 1;
+          ee = wd * 64 + __builtin_ctzll(m);
+        } else {
+          y -= pc;
+        }
+      }
+      int base = 0;
+      if (ee >= 0) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const unsigned long long bal = __ballot(id[c] == ee);
+          if (id[c] == ee)
+            s_rows[base + __popcll(bal & ((1ull << lane) - 1ull))] = lane + 64 * c;
+          base += __popcll(bal);
+        }
+      }
+      if (lane == 0) { s_e = ee; s_R = base; }
+    }
+    __syncthreads();
+    e = s_e;
+    R = s_R;
+    if (e < 0) return;  // fewer used experts than blocks in y (uniform)
+  }
+  // this lane's weight row and its A rows (one per row tile)
+  const int n = n0 + j;
+  const uint16_t* wrow = nullptr;
+  const uint8_t* crow = nullptr;
+  const uint8_t* srow = nullptr;
+  if constexpr (MOE) {
+    crow = static_cast<const uint8_t*>(a.W) + ((size_t)e * N + n) * (K / 2);
+    srow = a.scales + ((size_t)e * N + n) * U;
+  } else {
+    wrow = static_cast<const uint16_t*>(a.W) + (size_t)n * K;
+  }
+  const uint16_t* xrow[BT];
+  bool rv[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    const int r = 16 * bt + j;
+    rv[bt] = r < R;
+    const int rc = rv[bt] ? r : R - 1;
+    int xr = rc;
+    if constexpr (MODE == MX_GATE_UP) xr = s_rows[rc] / a.k;
+    if constexpr (MODE == MX_DOWN) xr = s_rows[rc];
+    xrow[bt] = a.x + (size_t)xr * K;
+  }
+  // every weight load of the wave first (the stream), then the MFMAs
+  uint4 wq[IT][MOE ? 1 : 4];
+  float wsc[MOE ? IT : 1];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int ur = 16 * it + 4 * w + g;
+    const int u = ur < U ? ur : U - 1;
+    if constexpr (MOE) {
+      wq[it][0] = mx_load_nt(crow + (size_t)u * 16);
+      const uint32_t s = __builtin_nontemporal_load(srow + u);
+      wsc[it] = __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        wq[it][t] = mx_load_nt(wrow + (size_t)u * 32 + 8 * t);
+    }
+  }
+  mx_f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int ur = 16 * it + 4 * w + g;
+    const bool uv = ur < U;
+    const int u = uv ? ur : U - 1;
+    uint4 xq[BT][4];
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)u * 32 + 8 * t);
+        const bool keep = uv && rv[bt];  // a zero A value drops a padded unit or row
+        xq[bt][t] = keep ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      mx_bf16x8 bw;
+      if constexpr (MOE) {
+        const uint4 c = wq[it][0];
+        const uint32_t cw = t == 0 ? c.x : t == 1 ? c.y : t == 2 ? c.z : c.w;
+        bw = mx_fp4x8(cw, wsc[it]);
+      } else {
+        bw = mx_as_bf16x8(wq[it][t]);
+      }
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt)
+        if (16 * bt < R)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw,
+                                                            acc[bt], 0, 0, 0);
+    }
+  }
+  // waves 1..3 hand their partial sums to wave 0, which adds them in order
+  if (w > 0) {
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    if (16 * bt >= R) break;
+    mx_f32x4 tot = acc[bt];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const mx_f32x4 p = red[v][bt][lane];
+      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
+      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 16 * bt + 4 * g + r;  // row of A / output row
+      const bool ok = ri < R;
+      const float d = tot[r];
+      if constexpr (MODE == MX_STORE || MODE == MX_RESID) {
+        if (ok) {
+          const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
+          const size_t o = (size_t)ri * N + n;
+          if (MODE == MX_STORE) a.y[o] = f2bf(v);
+          else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
+        }
+      } else if constexpr (MODE == MX_LOGITS) {
+        if (ok) a.out_f[(size_t)ri * N + n] = d;
+        float bv = ok ? d : -INFINITY;
+        int bi = n;
+        mx_argmax_step(bv, bi, 1);
+        mx_argmax_step(bv, bi, 2);
+        mx_argmax_step(bv, bi, 4);
+        mx_argmax_step(bv, bi, 8);
+        if (ok && j == 0) {
+          a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
+          a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
+        }
+      } else if constexpr (MODE == MX_GATE_UP) {
+        // rows 2c (gate) and 2c+1 (up) sit in lanes j and j ^ 1
+        const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        const float other = __shfl_xor(v, 1);
+        if (ok && (j & 1) == 0) {
+          const int q = s_rows[ri];
+          a.y[(size_t)q * (N / 2) + n / 2] = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
+        }
+      } else {  // MX_DOWN: dot + bias per pair, combined later in slot order
+        if (ok) {
+          const int q = s_rows[ri];
+          a.out_f[(size_t)q * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        }
+      }
+    }
+  }
+}
+
+// Row b's k slots in slot order from 0 (the exact path's fmaf chain), one
+// rounding to bf16, then h = bf16(h + y).
+__global__ __launch_bounds__(256) void k_mx_combine(const float* __restrict__ ybuf,
+                                                    const float* __restrict__ score,
+                                                    uint16_t* __restrict__ h, int H, int k) {
+  const int b = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= H) return;
+  float y = 0.0f;
+  for (int s = 0; s < k; ++s)
+    y = __builtin_fmaf(score[b * k + s], ybuf[((size_t)b * k + s) * H + n], y);
+  const size_t o = (size_t)b * H + n;
+  h[o] = f2bf(__fadd_rn(bf2f(h[o]), bf2f(f2bf(y))));
+}
+
+// q and k heads of row b rotated at position pos[b] (bf16 in and out, the
+// QKV epilogue's arithmetic); k and v appended at cache row pos & key_mask of
+// sequence seq[b] (b when seq is null).
+__global__ __launch_bounds__(256) void k_mx_rope_append(
+    const uint16_t* __restrict__ qkv, const int32_t* __restrict__ pos,
+    const int32_t* __restrict__ seq, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int Hq, int Hkv, int T_max, int key_mask) {
+  const int b = blockIdx.x;
+  const int p = pos[b], sq = seq ? seq[b] : b;
+  const int rows = (Hq + 2 * Hkv) * 64;
+  const uint16_t* row = qkv + (size_t)b * rows;
+  const size_t crow = (size_t)(p & key_mask);
+  for (int i = threadIdx.x; i < (Hq + Hkv) * 32; i += blockDim.x) {
+    const int hh = i >> 5, f = i & 31;
+    float o1, o2;
+    rope_pair(bf2f(row[hh * 64 + f]), bf2f(row[hh * 64 + f + 32]), cos_t[(size_t)p * 32 + f],
+              sin_t[(size_t)p * 32 + f], o1, o2);
+    uint16_t* dst = hh < Hq ? q_out + ((size_t)b * Hq + hh) * 64
+                            : kc + (((size_t)sq * Hkv + hh - Hq) * T_max + crow) * 64;
+    dst[f] = f2bf(o1);
+    dst[f + 32] = f2bf(o2);
+  }
+  for (int i = threadIdx.x; i < Hkv * 64; i += blockDim.x) {
+    const int gg = i >> 6, d = i & 63;
+    vc[(((size_t)sq * Hkv + gg) * T_max + crow) * 64 + d] = row[(Hq + Hkv) * 64 + i];
+  }
+}
+
+template <int MODE, int BT>
+static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
+  const int it = (a.K / 32 + 15) / 16;
+  if (it <= 2) hipLaunchKernelGGL((k_mx_gemv<BT, 2, MODE>), grid, dim3(256), 0, st, a);
+  else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv<BT, 4, MODE>), grid, dim3(256), 0, st, a);
+  else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv<BT, 6, MODE>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((k_mx_gemv<BT, 8, MODE>), grid, dim3(256), 0, st, a);
+}
+
+template <int MODE>
+static void mx_launch(const MxArgs& a, dim3 grid, hipStream_t st) {
+  switch ((a.B + 15) / 16) {
+    case 1: mx_launch_it<MODE, 1>(a, grid, st); break;
+    case 2: mx_launch_it<MODE, 2>(a, grid, st); break;
+    case 3: mx_launch_it<MODE, 3>(a, grid, st); break;
+    default: mx_launch_it<MODE, 4>(a, grid, st); break;
+  }
+}
+
+bool mx_shape_ok(int N, int K, int B) {
+  return B >= 1 && B <= kMxMaxRows && N >= 16 && N % 16 == 0 && K >= 32 && K % 32 == 0 &&
+         K <= kMxMaxK;
+}
+
+void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
+  const dim3 grid(a.N / 16);
+  if (mode == MX_STORE) mx_launch<MX_STORE>(a, grid, st);
+  else if (mode == MX_RESID) mx_launch<MX_RESID>(a, grid, st);
+  else mx_launch<MX_LOGITS>(a, grid, st);
+}
+
+void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
+                   hipStream_t st) {
+  const int used = std::min(gate_up.E, gate_up.B * gate_up.k);
+  mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 16, used), st);
+  mx_launch<MX_DOWN>(down, dim3(down.N / 16, used), st);
+  hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
+                     down.out_f, score, h, down.N, down.k);
+}
+
+void launch_mx_rope_append(const uint16_t* qkv, const int32_t* pos, const int32_t* seq,
+                           const float* cos_t, const float* sin_t, uint16_t* q_out,
+                           uint16_t* kc, uint16_t* vc, int B, int Hq, int Hkv, int T_max,
+                           int key_mask, hipStream_t st) {
+  hipLaunchKernelGGL(k_mx_rope_append, dim3(B), dim3(256), 0, st, qkv, pos, seq, cos_t, sin_t,
+                     q_out, kc, vc, Hq, Hkv, T_max, key_mask);
+}
+
+}  // namespace neon

@@ -85,6 +85,11 @@ def test_kernel_entry_points_validate_on_host():
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 0, 64, 1, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 8, 16384, 1, None) == ne.NEON_EINVAL
     assert L.neon_gemv_bf16(p, None, p, p, 8, 12, 1, None) == ne.NEON_EINVAL       # K % 8
+    assert L.neon_gemv_bf16_mfma(p, None, p, p, 24, 64, 1, None) == ne.NEON_EINVAL  # N % 16
+    assert L.neon_gemv_bf16_mfma(p, None, p, p, 32, 48, 1, None) == ne.NEON_EINVAL  # K % 32
+    assert L.neon_gemv_bf16_mfma(p, None, p, p, 32, 8192, 1, None) == ne.NEON_EINVAL  # K > 4096
+    assert L.neon_gemv_bf16_mfma(p, None, p, p, 32, 64, 65, None) == ne.NEON_EINVAL  # B > 64
+    assert L.neon_gemv_bf16_mfma(None, None, p, p, 32, 64, 1, None) == ne.NEON_EINVAL
     assert L.neon_rmsnorm(p, p, p, 1, 2880, 0.0, None) == ne.NEON_EINVAL
     assert L.neon_router_topk(p, p, p, p, p, None, 1, 32, 2880, 40, None) == ne.NEON_EINVAL
     assert L.neon_moe_layer(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 0, 1.702, 7.0,

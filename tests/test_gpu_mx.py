@@ -1,0 +1,137 @@
+"""GPU checks of the matrix-core batched decode steps (NEON_DECODE_MATRIX).
+
+The matrix cores add the fp32 products of each dot product in their own order,
+so these steps are not bit-identical to the exact batched steps.  The bars:
+  - the projection kernel (neon_gemv_bf16_mfma): within one bf16 rounding of
+    the fp64 product plus fp32-accumulation slack (2^-17 of the sum of
+    |terms|), per element;
+  - whole steps: the first step's logits within north_star's 2e-2 relative
+    bound of the exact step's (the prompt runs through the exact kernels in
+    both modes), the same first token wherever the exact top-2 margin
+    exceeds that bound, and the greedy ids of the following steps reported.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import neonengine_amd as ne
+from tests.gpu_util import bf16_err_ok, empty_dev, fix_routing, to_dev, to_host, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    from oracle import oracle
+    return oracle
+
+
+@pytest.mark.parametrize("N,K,B,with_bias", [(5120, 2880, 16, True), (2880, 4096, 64, True),
+                                             (32, 2880, 5, True), (4096, 64, 33, False),
+                                             (201088, 2880, 2, False)])
+def test_gemv_bf16_mfma(orc, N, K, B, with_bias):
+    torch_cuda()
+    say(f"gemv_bf16_mfma N={N} K={K} B={B} bias={with_bias}")
+    W = orc.fill_bf16(5, 71, N * K, 0.0, 0.02)
+    x = orc.fill_bf16(5, 72, B * K, 0.0, 1.0)
+    bias = orc.fill_bf16(5, 73, N, 0.0, 0.5) if with_bias else None
+    y = empty_dev((B, N), np.uint16)
+    ne.gemv_bf16_mfma(to_dev(W), to_dev(bias) if with_bias else None, to_dev(x), y, N, K, B)
+    got = to_host(y)
+    Wf = orc.bf16_to_f32(W).reshape(N, K).astype(np.float64)
+    xf = orc.bf16_to_f32(x).reshape(B, K).astype(np.float64)
+    bf = orc.bf16_to_f32(bias).astype(np.float64) if with_bias else np.zeros(N)
+    ref = xf @ Wf.T + bf
+    abs_sum = np.abs(xf) @ np.abs(Wf).T + np.abs(bf)
+    ok, ratio = bf16_err_ok(got, ref, abs_sum)
+    say(f"  worst error / bound = {ratio.max():.3f}")
+    assert ok.all()
+
+
+def run(cfg, seed, prompt, n_steps, mode, fixed_routing=False):
+    eng = ne.Engine(cfg)
+    eng.init_random(seed)
+    if fixed_routing:
+        fix_routing(eng, cfg)
+    eng.set_decode_mode(mode)
+    eng.prefill(prompt)
+    first = eng.read_logits()
+    eng.decode(n_steps)
+    toks = eng.read_tokens()[:, len(prompt[0]):]
+    eng.close()
+    return first, toks
+
+
+def compare(cfg, seed, B, plen, n_steps, fixed_routing=False):
+    torch_cuda()
+    say(f"decode modes layers={cfg.n_layers} hidden={cfg.hidden} E={cfg.n_experts} B={B} "
+        f"prompt={plen} fixed_routing={fixed_routing}")
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, cfg.vocab, size=(B, plen)).tolist()
+    lg_e, tok_e = run(cfg, seed, prompt, n_steps, ne.DECODE_EXACT, fixed_routing)
+    lg_m, tok_m = run(cfg, seed, prompt, n_steps, ne.DECODE_MATRIX, fixed_routing)
+    rel = np.abs(lg_m - lg_e).max() / np.abs(lg_e).max()
+    top2 = np.sort(lg_e, axis=1)[:, -2:]
+    margin = (top2[:, 1] - top2[:, 0]) / np.abs(lg_e).max(axis=1)
+    agree = (tok_m == tok_e).all(axis=1)
+    say(f"  first-step logits rel max err {rel:.3e}; rows with identical ids over "
+        f"{n_steps + 1} tokens: {agree.sum()}/{B}")
+    assert rel < 2e-2
+    for b in range(B):
+        if margin[b] > 2e-2:
+            assert tok_m[b, 0] == tok_e[b, 0]
+    return rel, agree
+
+
+SMALL = dict(n_layers=4, hidden=512, n_heads=16, n_kv_heads=2, head_dim=64, n_experts=8,
+             top_k=4, intermediate=512, vocab=4096, sliding_window=128, max_seq=256)
+
+
+@pytest.mark.parametrize("B", [2, 5, 16, 33, 64])
+def test_small_model_matrix_steps(B):
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=B))
+    compare(cfg, 3, B, 20, 24)
+
+
+def test_small_model_128_experts_matrix():
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_experts=128, max_batch=16))
+    compare(cfg, 5, 16, 12, 16)
+
+
+def test_gpt_oss_20b_width_matrix_steps():
+    """Full 20b width (2880 hidden, 64 / 8 heads, 32 experts, vocab 201088),
+    16 sequences: one layer with free routing, then four layers with the
+    routing fixed (router weights 0, distinct biases).  With random weights
+    and 32 experts, some rows' 4th and 5th router logits lie within rounding
+    of each other; across 16 rows and several layers one of them picks the
+    other expert in one mode, and that row's logits then differ by far more
+    than rounding (0.61 measured at four layers with free routing, while
+    every buffer of a one-layer step agrees to 2e-3)."""
+    cfg = ne.config_preset("gpt-oss-20b", n_layers=1, max_seq=64, max_batch=16)
+    compare(cfg, 1, 16, 24, 16)
+    cfg = ne.config_preset("gpt-oss-20b", n_layers=4, max_seq=64, max_batch=16)
+    compare(cfg, 1, 16, 24, 16, fixed_routing=True)
+
+
+def test_decode_mode_validation():
+    torch_cuda()
+    eng = ne.Engine(ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=1)))
+    with pytest.raises(ne.NeonError) as e:
+        eng.set_decode_mode(ne.DECODE_MATRIX)  # one sequence only
+    assert e.value.status == ne.NEON_EINVAL
+    with pytest.raises(ne.NeonError) as e:
+        eng.set_decode_mode(3)
+    assert e.value.status == ne.NEON_EINVAL
+    eng.set_decode_mode(ne.DECODE_EXACT)
+    eng.close()
+    eng = ne.Engine(ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=65)))
+    with pytest.raises(ne.NeonError) as e:
+        eng.set_decode_mode(ne.DECODE_MATRIX)
+    assert e.value.status == ne.NEON_EINVAL
+    eng.close()

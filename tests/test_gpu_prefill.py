@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 
 import neonengine_amd as ne
-from tests.gpu_util import bf16_err_ok, empty_dev, to_dev, to_host, torch_cuda
+from tests.gpu_util import bf16_err_ok, empty_dev, fix_routing, to_dev, to_host, torch_cuda
 
 pytestmark = pytest.mark.gpu
 
@@ -132,17 +132,6 @@ def test_attn_prefill_vs_oracle(orc, window):
 SMALL = dict(n_layers=4, hidden=512, n_heads=16, n_kv_heads=2, head_dim=64, n_experts=8,
              top_k=4, intermediate=512, vocab=4096, sliding_window=128, max_seq=512,
              max_batch=2)
-
-
-def fix_routing(eng, cfg):
-    """Router weights 0 and distinct biases: every row of layer l picks the
-    same 4 experts, so no near-tied router logit can flip between modes."""
-    E = cfg.n_experts
-    for layer in range(cfg.n_layers):
-        p = f"model.layers.{layer}.mlp.router."
-        eng.load_tensor(p + "weight", np.zeros(E * cfg.hidden, np.uint16))
-        bias = np.array([1.0 - 0.25 * ((e + 3 * layer) % E) for e in range(E)], np.float32)
-        eng.load_tensor(p + "bias", (bias.view(np.uint32) >> 16).astype(np.uint16))  # exact
 
 
 def prompt_pass(cfg, seed, prompt, n_steps, mode, fixed_routing=False):
