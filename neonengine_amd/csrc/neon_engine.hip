@@ -107,6 +107,7 @@ struct neon_ctx {
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
+  int32_t* mx_route = nullptr;       // used experts and their pair lists
   // prompt passes: positions and sequences of the rows of one pass
   int32_t *row_pos = nullptr, *row_seq = nullptr;
   // captured decode step
@@ -381,6 +382,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
                o_mxv = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_mxi = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
+               o_mxr = take(Bm > 1 ? (size_t)66 * 256 * 4 : 0),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -411,6 +413,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
     ctx->mx_ybuf = (float*)(W + o_mxy);
     ctx->mx_part_val = (float*)(W + o_mxv);
     ctx->mx_part_idx = (int32_t*)(W + o_mxi);
+    ctx->mx_route = (int32_t*)(W + o_mxr);
   }
   // ---- RoPE table ----
   std::vector<float> ct, st;
@@ -706,11 +709,13 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     launch_router(r, st);
     MxArgs gu{};
     gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.bias = w.gu_bias; gu.x = ctx->xn;
-    gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.B = B; gu.N = 2 * I; gu.K = H;
+    gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.route = ctx->mx_route; gu.B = B; gu.N = 2 * I;
+    gu.K = H;
     gu.E = c.n_experts; gu.k = c.top_k; gu.alpha = c.swiglu_alpha; gu.limit = c.swiglu_limit;
     MxArgs dn{};
     dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.bias = w.dn_bias; dn.x = ctx->act;
-    dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.B = B; dn.N = H; dn.K = I;
+    dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
+    dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k;
     launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
   }
@@ -985,11 +990,11 @@ extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
       FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: the matrix-core steps need max_batch in "
                              "[2, %d], not %d", kMxMaxRows, c.max_batch);
     if (!mx_shape_ok(qkv_rows, H, c.max_batch) || !mx_shape_ok(H, c.n_heads * c.head_dim, 2) ||
-        !mx_shape_ok(c.vocab, H, 2) || !mx_shape_ok(2 * c.intermediate, H, 2) ||
-        !mx_shape_ok(H, c.intermediate, 2))
+        !mx_shape_ok(c.vocab, H, 2) ||
+        !mx_moe_shape_ok(H, c.intermediate, c.n_experts, c.top_k, c.max_batch))
       FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: the matrix-core steps need every output "
-                             "width a multiple of 16 and every reduction a multiple of 32 "
-                             "up to %d", kMxMaxK);
+                             "width a multiple of 16 (expert widths of 64), every reduction "
+                             "a multiple of 32 up to %d and max_batch * top_k <= 256", kMxMaxK);
   }
   ctx->decode_mode = mode;
   // the captured step holds the step's kernels

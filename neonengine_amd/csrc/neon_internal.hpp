@@ -141,10 +141,14 @@ struct MxArgs {
   float* part_val;           // logits: per-block (max, lowest index) [B][N / 16]
   int32_t* part_idx;
   const int32_t* idx;        // expert modes: experts of the B k (row, slot) pairs
+  const int32_t* route;      // expert modes: used experts, counts, pair lists
+                             // [2 S + 64 S] ints, S = min(E, B k), written by
+                             // launch_mx_moe before the expert kernels
   int B, N, K, E, k;
   float alpha, limit;
 };
 bool mx_shape_ok(int N, int K, int B);
+bool mx_moe_shape_ok(int H, int I, int E, int k, int B);
 // mode 0: y = bf16(x W^T + bias); 1: y = bf16(y + bf16(x W^T + bias));
 // 2: logits = x W^T (fp32) with per-block argmax partials
 void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);

@@ -58,73 +58,100 @@ __device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
 
-// One block: weight rows n0 .. n0+15 (of expert e for the expert modes) for
-// all R rows.  BT = row tiles of 16 (R <= 16 BT); IT = K iterations per wave
-// (K <= 512 IT).
+// Pairs of every used expert, once per layer: route[y] = the y-th used expert
+// (ascending id; -1 past the last), route[S + y] = its pair count, and
+// route[2 S + 64 y + r] its r-th pair q = b k + s in ascending q, for the
+// S = min(E, B k) block rows of the expert kernels.
+__global__ __launch_bounds__(256) void k_mx_route(const int32_t* __restrict__ idx, int nk,
+                                                  int E, int S, int32_t* __restrict__ route) {
+  __shared__ int cnt_e[256];
+  __shared__ int slot_of[256];
+  __shared__ int wave_used[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  cnt_e[t] = 0;
+  __syncthreads();
+  const int e = t < nk ? idx[t] : -1;
+  if (e >= 0) atomicAdd(&cnt_e[e], 1);
+  __syncthreads();
+  // slot of expert t = used experts below it: a ballot prefix over the 256
+  // flags, lane-parallel (no serial loop over experts)
+  const int c = t < E ? cnt_e[t] : 0;
+  const unsigned long long bal = __ballot(c > 0);
+  if (lane == 0) wave_used[w] = __popcll(bal);
+  __syncthreads();
+  const int before = (w > 0 ? wave_used[0] : 0) + (w > 1 ? wave_used[1] : 0) +
+                     (w > 2 ? wave_used[2] : 0);
+  const int slot = before + __popcll(bal & ((1ull << lane) - 1ull));
+  const int n_used = wave_used[0] + wave_used[1] + wave_used[2] + wave_used[3];
+  if (c > 0) {
+    slot_of[t] = slot;
+    route[slot] = t;
+    route[S + slot] = c;
+  }
+  if (t >= n_used && t < S) {
+    route[t] = -1;
+    route[S + t] = 0;
+  }
+  __syncthreads();
+  if (e >= 0) {
+    int r = 0;
+    for (int q = 0; q < t; ++q) r += idx[q] == e;
+    route[2 * S + 64 * slot_of[e] + r] = t;
+  }
+}
+
+// One block: weight rows n0 .. n0 + 16 TT - 1 (of one expert in the expert
+// modes) for all R rows; its 4 waves split K.  BT = row tiles of 16
+// (R <= 16 BT); IT = K iterations per wave (K <= 512 IT); TT = weight tiles
+// of 16 rows per wave (4 for MXFP4 rows, whose B operand is a quarter of the
+// A operand's bytes, so that each activation fragment feeds 4 MFMAs).
+// Element order: a bf16 lane (j, g) reads elements 128 (4 i + w) + 32 t + 8 g
+// in step t of iteration i, so one load instruction covers 64 contiguous
+// bytes of each of its 16 rows; an MXFP4 lane group g reads unit
+// u = 16 i + 4 w + g (16 code bytes, one scale) and feeds its elements
+// 32 u + 8 t in step t.
 template <int BT, int IT, int MODE>
 __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
-  __shared__ mx_f32x4 red[3][BT][64];
-  __shared__ int s_rows[64];
-  __shared__ unsigned long long s_used[4];
-  __shared__ int s_e, s_R;
+  constexpr int TT = MOE ? 4 : 1;
+  __shared__ mx_f32x4 red[3][TT][BT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * TT;
   int R = a.B, e = 0;
+  const int32_t* rows = nullptr;
   if constexpr (MOE) {
-    // the blockIdx.y-th used expert (ascending id) and its pairs q = b k + s
-    const int nk = a.B * a.k;
-    if (threadIdx.x < 4) s_used[threadIdx.x] = 0ull;
-    __syncthreads();
-    int id[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int q = lane + 64 * c;
-      id[c] = (w == 0 && q < nk) ? a.idx[q] : -1;
-      if (id[c] >= 0) atomicOr(&s_used[id[c] >> 6], 1ull << (id[c] & 63));
-    }
-    __syncthreads();
-    if (w == 0) {
-      int y = blockIdx.y, ee = -1;
-      for (int wd = 0; wd < 4 && ee < 0; ++wd) {
-        unsigned long long m = s_used[wd];
-        const int pc = __popcll(m);
-        if (y < pc) {
-          for (int t = 0; t < y; ++t) m &= m - 1;
-          ee = wd * 64 + __builtin_ctzll(m);
-        } else {
-          y -= pc;
-        }
-      }
-      int base = 0;
-      if (ee >= 0) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const unsigned long long bal = __ballot(id[c] == ee);
-          if (id[c] == ee)
-            s_rows[base + __popcll(bal & ((1ull << lane) - 1ull))] = lane + 64 * c;
-          base += __popcll(bal);
-        }
-      }
-      if (lane == 0) { s_e = ee; s_R = base; }
-    }
-    __syncthreads();
-    e = s_e;
-    R = s_R;
-    if (e < 0) return;  // fewer used experts than blocks in y (uniform)
+    const int S = gridDim.y;
+    e = a.route[blockIdx.y];
+    if (e < 0) return;  // fewer used experts than block rows (uniform)
+    R = a.route[S + blockIdx.y];
+    rows = a.route + 2 * S + 64 * blockIdx.y;
   }
-  // this lane's weight row and its A rows (one per row tile)
-  const int n = n0 + j;
-  const uint16_t* wrow = nullptr;
-  const uint8_t* crow = nullptr;
-  const uint8_t* srow = nullptr;
-  if constexpr (MOE) {
-    crow = static_cast<const uint8_t*>(a.W) + ((size_t)e * N + n) * (K / 2);
-    srow = a.scales + ((size_t)e * N + n) * U;
-  } else {
-    wrow = static_cast<const uint16_t*>(a.W) + (size_t)n * K;
+  // weight loads first (the stream), then the activation rows
+  uint4 wq[IT][MOE ? TT : 4];
+  float wsc[MOE ? IT : 1][TT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if constexpr (MOE) {
+      const int ur = 16 * it + 4 * w + g;
+      const int u = ur < U ? ur : U - 1;
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const size_t row = (size_t)e * N + n0 + 16 * tt + j;
+        wq[it][tt] = mx_load_nt(static_cast<const uint8_t*>(a.W) + row * (K / 2) + (size_t)u * 16);
+        const uint32_t sb = __builtin_nontemporal_load(a.scales + row * U + u);
+        wsc[it][tt] = __builtin_amdgcn_ldexpf(1.0f, (int)sb - 127);
+      }
+    } else {
+      const uint16_t* wrow = static_cast<const uint16_t*>(a.W) + (size_t)(n0 + j) * K;
+      const int base = 128 * (4 * it + w);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int el = base + 32 * t < K ? base + 32 * t + 8 * g : 8 * g;
+        wq[it][t] = mx_load_nt(wrow + el);
+      }
+    }
   }
   const uint16_t* xrow[BT];
   bool rv[BT];
@@ -134,114 +161,120 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
     rv[bt] = r < R;
     const int rc = rv[bt] ? r : R - 1;
     int xr = rc;
-    if constexpr (MODE == MX_GATE_UP) xr = s_rows[rc] / a.k;
-    if constexpr (MODE == MX_DOWN) xr = s_rows[rc];
+    if constexpr (MODE == MX_GATE_UP) xr = rows[rc] / a.k;
+    if constexpr (MODE == MX_DOWN) xr = rows[rc];
     xrow[bt] = a.x + (size_t)xr * K;
   }
-  // every weight load of the wave first (the stream), then the MFMAs
-  uint4 wq[IT][MOE ? 1 : 4];
-  float wsc[MOE ? IT : 1];
+  mx_f32x4 acc[TT][BT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) acc[tt][bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    const int ur = 16 * it + 4 * w + g;
-    const int u = ur < U ? ur : U - 1;
+    int xel[4];
+    bool xok[4];
     if constexpr (MOE) {
-      wq[it][0] = mx_load_nt(crow + (size_t)u * 16);
-      const uint32_t s = __builtin_nontemporal_load(srow + u);
-      wsc[it] = __builtin_amdgcn_ldexpf(1.0f, (int)s - 127);
+      const int ur = 16 * it + 4 * w + g;
+      const int u = ur < U ? ur : U - 1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) { xel[t] = 32 * u + 8 * t; xok[t] = ur < U; }
     } else {
+      const int base = 128 * (4 * it + w);
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        wq[it][t] = mx_load_nt(wrow + (size_t)u * 32 + 8 * t);
+      for (int t = 0; t < 4; ++t) {
+        xok[t] = base + 32 * t < K;
+        xel[t] = xok[t] ? base + 32 * t + 8 * g : 8 * g;
+      }
     }
-  }
-  mx_f32x4 acc[BT];
-#pragma unroll
-  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int it = 0; it < IT; ++it) {
-    const int ur = 16 * it + 4 * w + g;
-    const bool uv = ur < U;
-    const int u = uv ? ur : U - 1;
     uint4 xq[BT][4];
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + (size_t)u * 32 + 8 * t);
-        const bool keep = uv && rv[bt];  // a zero A value drops a padded unit or row
-        xq[bt][t] = keep ? v : make_uint4(0u, 0u, 0u, 0u);
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + xel[t]);
+        // a zero A value drops a padded element range or row
+        xq[bt][t] = (xok[t] && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      mx_bf16x8 bw;
-      if constexpr (MOE) {
-        const uint4 c = wq[it][0];
-        const uint32_t cw = t == 0 ? c.x : t == 1 ? c.y : t == 2 ? c.z : c.w;
-        bw = mx_fp4x8(cw, wsc[it]);
-      } else {
-        bw = mx_as_bf16x8(wq[it][t]);
-      }
 #pragma unroll
-      for (int bt = 0; bt < BT; ++bt)
-        if (16 * bt < R)
-          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw,
-                                                            acc[bt], 0, 0, 0);
+      for (int tt = 0; tt < TT; ++tt) {
+        mx_bf16x8 bw;
+        if constexpr (MOE) {
+          const uint4 c = wq[it][tt];
+          const uint32_t cw = t == 0 ? c.x : t == 1 ? c.y : t == 2 ? c.z : c.w;
+          bw = mx_fp4x8(cw, wsc[it][tt]);
+        } else {
+          bw = mx_as_bf16x8(wq[it][t]);
+        }
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt)
+          if (16 * bt < R)
+            acc[tt][bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw,
+                                                                  acc[tt][bt], 0, 0, 0);
+      }
     }
   }
   // waves 1..3 hand their partial sums to wave 0, which adds them in order
   if (w > 0) {
 #pragma unroll
-    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
+    for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) red[w - 1][tt][bt][lane] = acc[tt][bt];
   }
   __syncthreads();
   if (w != 0) return;
 #pragma unroll
-  for (int bt = 0; bt < BT; ++bt) {
-    if (16 * bt >= R) break;
-    mx_f32x4 tot = acc[bt];
+  for (int tt = 0; tt < TT; ++tt) {
+    const int n = n0 + 16 * tt + j;
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
-      const mx_f32x4 p = red[v][bt][lane];
-      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
-      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
-    }
+    for (int bt = 0; bt < BT; ++bt) {
+      if (16 * bt >= R) break;
+      mx_f32x4 tot = acc[tt][bt];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ri = 16 * bt + 4 * g + r;  // row of A / output row
-      const bool ok = ri < R;
-      const float d = tot[r];
-      if constexpr (MODE == MX_STORE || MODE == MX_RESID) {
-        if (ok) {
-          const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
-          const size_t o = (size_t)ri * N + n;
-          if (MODE == MX_STORE) a.y[o] = f2bf(v);
-          else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
-        }
-      } else if constexpr (MODE == MX_LOGITS) {
-        if (ok) a.out_f[(size_t)ri * N + n] = d;
-        float bv = ok ? d : -INFINITY;
-        int bi = n;
-        mx_argmax_step(bv, bi, 1);
-        mx_argmax_step(bv, bi, 2);
-        mx_argmax_step(bv, bi, 4);
-        mx_argmax_step(bv, bi, 8);
-        if (ok && j == 0) {
-          a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
-          a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
-        }
-      } else if constexpr (MODE == MX_GATE_UP) {
-        // rows 2c (gate) and 2c+1 (up) sit in lanes j and j ^ 1
-        const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
-        const float other = __shfl_xor(v, 1);
-        if (ok && (j & 1) == 0) {
-          const int q = s_rows[ri];
-          a.y[(size_t)q * (N / 2) + n / 2] = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
-        }
-      } else {  // MX_DOWN: dot + bias per pair, combined later in slot order
-        if (ok) {
-          const int q = s_rows[ri];
-          a.out_f[(size_t)q * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+      for (int v = 0; v < 3; ++v) {
+        const mx_f32x4 p = red[v][tt][bt][lane];
+        tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
+        tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ri = 16 * bt + 4 * g + r;  // row of A / output row
+        const bool ok = ri < R;
+        const float d = tot[r];
+        if constexpr (MODE == MX_STORE || MODE == MX_RESID) {
+          if (ok) {
+            const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
+            const size_t o = (size_t)ri * N + n;
+            if (MODE == MX_STORE) a.y[o] = f2bf(v);
+            else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
+          }
+        } else if constexpr (MODE == MX_LOGITS) {
+          if (ok) a.out_f[(size_t)ri * N + n] = d;
+          float bv = ok ? d : -INFINITY;
+          int bi = n;
+          mx_argmax_step(bv, bi, 1);
+          mx_argmax_step(bv, bi, 2);
+          mx_argmax_step(bv, bi, 4);
+          mx_argmax_step(bv, bi, 8);
+          if (ok && j == 0) {
+            a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
+            a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
+          }
+        } else if constexpr (MODE == MX_GATE_UP) {
+          // rows 2c (gate) and 2c+1 (up) sit in lanes j and j ^ 1
+          const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+          const float other = __shfl_xor(v, 1);
+          if (ok && (j & 1) == 0) {
+            const int q = rows[ri];
+            a.y[(size_t)q * (N / 2) + n / 2] = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
+          }
+        } else {  // MX_DOWN: dot + bias per pair, combined later in slot order
+          if (ok) {
+            const int q = rows[ri];
+            a.out_f[(size_t)q * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+          }
         }
       }
     }
@@ -315,6 +348,11 @@ bool mx_shape_ok(int N, int K, int B) {
          K <= kMxMaxK;
 }
 
+bool mx_moe_shape_ok(int H, int I, int E, int k, int B) {
+  return mx_shape_ok(2 * I, H, B) && mx_shape_ok(H, I, B) && (2 * I) % 64 == 0 && H % 64 == 0 &&
+         E >= 1 && E <= 256 && B * k <= 256;
+}
+
 void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
   const dim3 grid(a.N / 16);
   if (mode == MX_STORE) mx_launch<MX_STORE>(a, grid, st);
@@ -324,9 +362,11 @@ void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
 
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
                    hipStream_t st) {
-  const int used = std::min(gate_up.E, gate_up.B * gate_up.k);
-  mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 16, used), st);
-  mx_launch<MX_DOWN>(down, dim3(down.N / 16, used), st);
+  const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
+  hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx, gate_up.B * gate_up.k,
+                     gate_up.E, S, const_cast<int32_t*>(gate_up.route));
+  mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 64, S), st);
+  mx_launch<MX_DOWN>(down, dim3(down.N / 64, S), st);
   hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
                      down.out_f, score, h, down.N, down.k);
 }
