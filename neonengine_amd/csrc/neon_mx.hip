@@ -4,10 +4,10 @@
 // order of the batch-1 kernels, which makes them VALU-bound from B = 16 on.
 // Here each weight row is read once per step and the B rows ride in the M
 // dimension of v_mfma_f32_16x16x32_bf16 (fp32 accumulate):
-//   - a block owns 16 weight rows; its 4 waves split K into interleaved
-//     units of 32 elements (lane group g of wave w takes unit 16 i + 4 w + g
-//     in iteration i, so the 4 groups of one MFMA cover 4 different units and
-//     one lane loads 64 contiguous bytes of its row per iteration);
+//   - a block owns 16 weight rows (64 for MXFP4 expert rows, 4 tiles per
+//     wave); its 4 waves split K, and each load instruction reads 64
+//     contiguous bytes of each of its 16 rows (the element orders are at
+//     k_mx_gemv);
 //   - bf16 rows feed the B operand as loaded; MXFP4 expert rows go through
 //     v_cvt_scalef32_pk_bf16_fp4 (E2M1 x 2^(s-127) is a bf16 value, so the
 //     dequantisation is exact);
@@ -100,6 +100,13 @@ __global__ __launch_bounds__(256) void k_mx_route(const int32_t* __restrict__ id
   }
 }
 
+// MXFP4 unit of lane group g of wave w in iteration i: a wave takes 8
+// consecutive units (128 code bytes of each row, one cache line) in two
+// successive iterations, the 4 waves 32 units per iteration pair.
+__device__ __forceinline__ int mx_unit(int it, int w, int g) {
+  return 32 * (it >> 1) + 8 * w + 4 * (it & 1) + g;
+}
+
 // One block: weight rows n0 .. n0 + 16 TT - 1 (of one expert in the expert
 // modes) for all R rows; its 4 waves split K.  BT = row tiles of 16
 // (R <= 16 BT); IT = K iterations per wave (K <= 512 IT); TT = weight tiles
@@ -108,7 +115,7 @@ __global__ __launch_bounds__(256) void k_mx_route(const int32_t* __restrict__ id
 // Element order: a bf16 lane (j, g) reads elements 128 (4 i + w) + 32 t + 8 g
 // in step t of iteration i, so one load instruction covers 64 contiguous
 // bytes of each of its 16 rows; an MXFP4 lane group g reads unit
-// u = 16 i + 4 w + g (16 code bytes, one scale) and feeds its elements
+// u = mx_unit(i, w, g) (16 code bytes, one scale) and feeds its elements
 // 32 u + 8 t in step t.
 template <int BT, int IT, int MODE>
 __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
@@ -134,13 +141,13 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
     if constexpr (MOE) {
-      const int ur = 16 * it + 4 * w + g;
+      const int ur = mx_unit(it, w, g);
       const int u = ur < U ? ur : U - 1;
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         const size_t row = (size_t)e * N + n0 + 16 * tt + j;
         wq[it][tt] = mx_load_nt(static_cast<const uint8_t*>(a.W) + row * (K / 2) + (size_t)u * 16);
-        const uint32_t sb = __builtin_nontemporal_load(a.scales + row * U + u);
+        const uint32_t sb = a.scales[row * U + u];  // cached: a line serves 4 iterations
         wsc[it][tt] = __builtin_amdgcn_ldexpf(1.0f, (int)sb - 127);
       }
     } else {
@@ -175,7 +182,7 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
     int xel[4];
     bool xok[4];
     if constexpr (MOE) {
-      const int ur = 16 * it + 4 * w + g;
+      const int ur = mx_unit(it, w, g);
       const int u = ur < U ? ur : U - 1;
 #pragma unroll
       for (int t = 0; t < 4; ++t) { xel[t] = 32 * u + 8 * t; xok[t] = ur < U; }
