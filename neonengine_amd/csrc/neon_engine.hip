@@ -108,6 +108,13 @@ struct neon_ctx {
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
   int32_t* mx_route = nullptr;       // used experts and their pair lists
+  // the weights in MFMA lane order for the matrix-core steps (allocated when
+  // that mode is first selected; refreshed before a step after any change)
+  struct MxLayer { uint16_t *wqkv, *wo; uint8_t *gu_c, *gu_s, *dn_c, *dn_s; };
+  char* mx_w = nullptr;
+  std::vector<MxLayer> mxp;
+  uint16_t* mx_lm = nullptr;
+  bool mx_dirty = true;
   // prompt passes: positions and sequences of the rows of one pass
   int32_t *row_pos = nullptr, *row_seq = nullptr;
   // captured decode step
@@ -270,6 +277,7 @@ extern "C" void neon_ctx_destroy(neon_ctx* ctx) {
   if (ctx->vc) (void)hipFree(ctx->vc);
   if (ctx->work) (void)hipFree(ctx->work);
   if (ctx->pf) (void)hipFree(ctx->pf);
+  if (ctx->mx_w) (void)hipFree(ctx->mx_w);
   delete ctx;
 }
 
@@ -507,6 +515,7 @@ extern "C" neon_status neon_init_random(neon_ctx* ctx, uint64_t seed,
   }
   HIPCHK(ctx, hipGetLastError());
   ctx->weights_ready = true;
+  ctx->mx_dirty = true;
   return NEON_OK;
 }
 
@@ -571,6 +580,7 @@ extern "C" neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
   HIPCHK(ctx, hipSetDevice(ctx->device));
   HIPCHK(ctx, hipMemcpy(t.ptr, host_data, bytes, hipMemcpyHostToDevice));
   ctx->weights_ready = true;
+  ctx->mx_dirty = true;
   return NEON_OK;
 }
 
@@ -683,7 +693,8 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     uint16_t* vc_l = ctx->vc + ctx->kv_off[l];
     launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
     MxArgs q{};
-    q.W = w.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.y = ctx->qkv;
+    const neon_ctx::MxLayer& mp = ctx->mxp[l];
+    q.W = w.wqkv; q.Wp = mp.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.y = ctx->qkv;
     q.B = B; q.N = qkv_rows; q.K = H;
     launch_mx_gemv(q, 0, st);
     launch_mx_rope_append(ctx->qkv, ctx->pos, nullptr, ctx->cos_t, ctx->sin_t, ctx->q_rot, kc_l,
@@ -698,7 +709,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
     launch_attn(a, st);
     MxArgs o{};
-    o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
+    o.W = w.wo; o.Wp = mp.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
     o.B = B; o.N = H; o.K = c.n_heads * D;
     launch_mx_gemv(o, 1, st);
     RouterArgs r;
@@ -708,12 +719,14 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
     launch_router(r, st);
     MxArgs gu{};
-    gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.bias = w.gu_bias; gu.x = ctx->xn;
+    gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.Wp = mp.gu_c; gu.sp = mp.gu_s;
+    gu.bias = w.gu_bias; gu.x = ctx->xn;
     gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.route = ctx->mx_route; gu.B = B; gu.N = 2 * I;
     gu.K = H;
     gu.E = c.n_experts; gu.k = c.top_k; gu.alpha = c.swiglu_alpha; gu.limit = c.swiglu_limit;
     MxArgs dn{};
-    dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.bias = w.dn_bias; dn.x = ctx->act;
+    dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.Wp = mp.dn_c; dn.sp = mp.dn_s;
+    dn.bias = w.dn_bias; dn.x = ctx->act;
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k;
@@ -721,7 +734,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
   }
   launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
   MxArgs lm{};
-  lm.W = ctx->lm_head; lm.x = ctx->xn; lm.out_f = ctx->logits;
+  lm.W = ctx->lm_head; lm.Wp = ctx->mx_lm; lm.x = ctx->xn; lm.out_f = ctx->logits;
   lm.part_val = ctx->mx_part_val; lm.part_idx = ctx->mx_part_idx;
   lm.B = B; lm.N = c.vocab; lm.K = H;
   launch_mx_gemv(lm, 2, st);
@@ -779,7 +792,29 @@ static neon_status ensure_graph(neon_ctx* ctx, int B) {
   return NEON_OK;
 }
 
+// Packs every weight the matrix-core steps read into MFMA lane order (stream
+// ordered, before the step that needs it; never inside a captured graph).
+static void mx_repack(neon_ctx* ctx, hipStream_t st) {
+  const neon_config& c = ctx->cfg;
+  const int H = c.hidden, I = c.intermediate, E = c.n_experts;
+  const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const LayerW& w = ctx->layers[l];
+    const neon_ctx::MxLayer& m = ctx->mxp[l];
+    launch_mx_pack_bf16(w.wqkv, qkv_rows, H, m.wqkv, st);
+    launch_mx_pack_bf16(w.wo, H, c.n_heads * c.head_dim, m.wo, st);
+    launch_mx_pack_fp4(w.gu_codes, w.gu_scales, E, 2 * I, H, m.gu_c, m.gu_s, st);
+    launch_mx_pack_fp4(w.dn_codes, w.dn_scales, E, H, I, m.dn_c, m.dn_s, st);
+  }
+  launch_mx_pack_bf16(ctx->lm_head, c.vocab, H, ctx->mx_lm, st);
+}
+
 static neon_status run_steps(neon_ctx* ctx, int n, hipStream_t st) {
+  if (ctx->decode_mode == NEON_DECODE_MATRIX && ctx->batch >= 2 && ctx->mx_dirty) {
+    mx_repack(ctx, st);
+    HIPCHK(ctx, hipGetLastError());
+    ctx->mx_dirty = false;
+  }
   // NEON_EAGER=1 launches the kernels directly (debugging aid); the default
   // replays the captured step graph.
   static const bool eager = getenv("NEON_EAGER") && getenv("NEON_EAGER")[0] == '1';
@@ -995,6 +1030,38 @@ extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
       FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: the matrix-core steps need every output "
                              "width a multiple of 16 (expert widths of 64), every reduction "
                              "a multiple of 32 up to %d and max_batch * top_k <= 256", kMxMaxK);
+  }
+  if (mode == NEON_DECODE_MATRIX && !ctx->mx_w) {
+    const neon_config& c = ctx->cfg;
+    const int H = c.hidden, I = c.intermediate, E = c.n_experts;
+    const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
+    const size_t b_qkv = mx_packed_bf16_bytes(qkv_rows, H);
+    const size_t b_o = mx_packed_bf16_bytes(H, c.n_heads * c.head_dim);
+    const size_t p_gu = mx_packed_fp4_pieces(E, 2 * I, H), p_dn = mx_packed_fp4_pieces(E, H, I);
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off = align_up(off + bytes); return o; };
+    std::vector<size_t> o(6 * c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+      o[6 * l + 0] = take(b_qkv); o[6 * l + 1] = take(b_o);
+      o[6 * l + 2] = take(p_gu * 16); o[6 * l + 3] = take(p_gu);
+      o[6 * l + 4] = take(p_dn * 16); o[6 * l + 5] = take(p_dn);
+    }
+    const size_t o_lm = take(mx_packed_bf16_bytes(c.vocab, H));
+    HIPCHK(ctx, hipSetDevice(ctx->device));
+    if (hipMalloc(&ctx->mx_w, off) != hipSuccess) {
+      ctx->mx_w = nullptr;
+      FAIL(ctx, NEON_ENOMEM, "neon_set_decode_mode: hipMalloc of %zu bytes for the matrix-core "
+                             "weight copies failed", off);
+    }
+    ctx->mxp.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+      neon_ctx::MxLayer& m = ctx->mxp[l];
+      m.wqkv = (uint16_t*)(ctx->mx_w + o[6 * l + 0]); m.wo = (uint16_t*)(ctx->mx_w + o[6 * l + 1]);
+      m.gu_c = (uint8_t*)(ctx->mx_w + o[6 * l + 2]); m.gu_s = (uint8_t*)(ctx->mx_w + o[6 * l + 3]);
+      m.dn_c = (uint8_t*)(ctx->mx_w + o[6 * l + 4]); m.dn_s = (uint8_t*)(ctx->mx_w + o[6 * l + 5]);
+    }
+    ctx->mx_lm = (uint16_t*)(ctx->mx_w + o_lm);
+    ctx->mx_dirty = true;
   }
   ctx->decode_mode = mode;
   // the captured step holds the step's kernels

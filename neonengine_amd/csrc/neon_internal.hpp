@@ -141,6 +141,8 @@ struct MxArgs {
   float* part_val;           // logits: per-block (max, lowest index) [B][N / 16]
   int32_t* part_idx;
   const int32_t* idx;        // expert modes: experts of the B k (row, slot) pairs
+  const void* Wp;            // the same weights in MFMA lane order (mx_pack_*), or NULL
+  const uint8_t* sp;         // packed MXFP4 scales (with Wp, expert modes)
   const int32_t* route;      // expert modes: used experts, counts, pair lists
                              // [2 S + 64 S] ints, S = min(E, B k), written by
                              // launch_mx_moe before the expert kernels
@@ -149,6 +151,13 @@ struct MxArgs {
 };
 bool mx_shape_ok(int N, int K, int B);
 bool mx_moe_shape_ok(int H, int I, int E, int k, int B);
+// MFMA lane-order copies (each load instruction of the matrix-core kernels
+// then reads 1 KB contiguous): sizes in bytes, and the packing launches.
+size_t mx_packed_bf16_bytes(int N, int K);
+size_t mx_packed_fp4_pieces(int E, int N, int K);  // 16-byte code pieces = scale bytes
+void launch_mx_pack_bf16(const uint16_t* W, int N, int K, uint16_t* P, hipStream_t st);
+void launch_mx_pack_fp4(const uint8_t* codes, const uint8_t* scales, int E, int N, int K,
+                        uint8_t* Pc, uint8_t* Ps, hipStream_t st);
 // mode 0: y = bf16(x W^T + bias); 1: y = bf16(y + bf16(x W^T + bias));
 // 2: logits = x W^T (fp32) with per-block argmax partials
 void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);

@@ -117,7 +117,7 @@ __device__ __forceinline__ int mx_unit(int it, int w, int g) {
 // bytes of each of its 16 rows; an MXFP4 lane group g reads unit
 // u = mx_unit(i, w, g) (16 code bytes, one scale) and feeds its elements
 // 32 u + 8 t in step t.
-template <int BT, int IT, int MODE>
+template <int BT, int IT, int MODE, bool PACKED>
 __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
   constexpr int TT = MOE ? 4 : 1;
@@ -150,6 +150,14 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
         const uint32_t sb = a.scales[row * U + u];  // cached: a line serves 4 iterations
         wsc[it][tt] = __builtin_amdgcn_ldexpf(1.0f, (int)sb - 127);
       }
+    } else if constexpr (PACKED) {
+      // [N/16][NCH][t][g][j][8]: lane l = j + 16 g reads piece ... * 64 + l
+      const int NCH = (K + 127) / 128;
+      const int ch = min(4 * it + w, NCH - 1);
+      const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        wq[it][t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
     } else {
       const uint16_t* wrow = static_cast<const uint16_t*>(a.W) + (size_t)(n0 + j) * K;
       const int base = 128 * (4 * it + w);
@@ -288,6 +296,149 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   }
 }
 
+// Expert rows for at most 16 rows per expert (B <= 16).  A block of 4 waves
+// owns 256 rows of one expert (64 per wave in 4 tiles of 16) and each wave
+// runs the whole K, so nothing is reduced across waves.  The expert's
+// activation rows go through LDS 512 elements (16 units) at a time, double
+// buffered, and serve all 256 rows; the next chunk's weights are loaded into
+// registers while the current one is used.  Per half-iteration the order is:
+// activation loads (c + 1), weight loads (c + 1), barrier, MFMAs on chunk c,
+// activation rows (c + 1) into LDS -- loads complete in issue order, so the
+// LDS writes never wait for the weight stream.  Lane group g takes units
+// 16 c + 4 g + s (s = 0..3) of chunk c: 64 contiguous code bytes per lane.
+template <int MODE, bool PACKED>
+__global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
+  constexpr int CKU = 16, CK = 32 * CKU, XS = CK + 8;
+  __shared__ __align__(16) uint16_t xs[2][16][XS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, U = K / 32;
+  const int S = gridDim.y;
+  const int e = a.route[blockIdx.y];
+  if (e < 0) return;  // fewer used experts than block rows (uniform)
+  const int R = a.route[S + blockIdx.y];  // 1 .. 16
+  const int32_t* rows = a.route + 2 * S + 64 * blockIdx.y;
+  const int nw0 = blockIdx.x * 256 + 64 * w;  // the wave's first row
+  const bool wave_on = nw0 < N;               // uniform per wave
+  const int nch = (U + CKU - 1) / CKU;
+  // staging: thread tid copies 8-element pieces (tid & 15) + 16 q of row tid >> 4
+  const int sr = tid >> 4, sp = tid & 15;
+  const bool s_ok = sr < R;
+  int xr = 0;
+  if (s_ok) xr = MODE == MX_GATE_UP ? rows[sr] / a.k : rows[sr];
+  const uint16_t* xsrc = a.x + (size_t)xr * K;
+  const uint8_t* codes = static_cast<const uint8_t*>(a.W);
+  auto x_load = [&](int c, uint4 (&xv)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int el = c * CK + 8 * (sp + 16 * q);
+      xv[q] = (s_ok && el < K) ? *reinterpret_cast<const uint4*>(xsrc + el)
+                               : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto x_store = [&](int buf, const uint4 (&xv)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<uint4*>(&xs[buf][sr][8 * (sp + 16 * q)]) = xv[q];
+  };
+  auto w_load = [&](int c, uint4 (&wv)[4][4], float (&sv)[4][4]) {
+    if (!wave_on) return;
+    if constexpr (PACKED) {
+      // [E][N/16][nch][su][g][j] pieces of 16 code bytes (scales: one byte each)
+      const uint8_t* Pc = static_cast<const uint8_t*>(a.Wp);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const size_t et = (size_t)e * (N / 16) + nw0 / 16 + tt;
+#pragma unroll
+        for (int su = 0; su < 4; ++su) {
+          const size_t piece = ((et * nch + c) * 4 + su) * 64 + lane;
+          wv[tt][su] = mx_load_nt(Pc + piece * 16);
+          sv[tt][su] = __builtin_amdgcn_ldexpf(1.0f, (int)a.sp[piece] - 127);
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const size_t row = (size_t)e * N + nw0 + 16 * tt + j;
+#pragma unroll
+      for (int su = 0; su < 4; ++su) {
+        const int ur = CKU * c + 4 * g + su;
+        const int u = ur < U ? ur : U - 1;
+        wv[tt][su] = mx_load_nt(codes + row * (K / 2) + (size_t)u * 16);
+        sv[tt][su] = __builtin_amdgcn_ldexpf(1.0f, (int)a.scales[row * U + u] - 127);
+      }
+    }
+  };
+  mx_f32x4 acc[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) acc[tt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int c, int buf, const uint4 (&wv)[4][4], const float (&sv)[4][4]) {
+#pragma unroll
+    for (int su = 0; su < 4; ++su) {
+      const int ur = CKU * c + 4 * g + su;
+      const bool uv = ur < U;  // a zero A value drops a padded unit
+      uint4 af[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&xs[buf][j][32 * (4 * g + su) + 8 * t]);
+        af[t] = uv ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const uint4 cw = wv[tt][su];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t word = t == 0 ? cw.x : t == 1 ? cw.y : t == 2 ? cw.z : cw.w;
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              mx_as_bf16x8(af[t]), mx_fp4x8(word, sv[tt][su]), acc[tt], 0, 0, 0);
+        }
+      }
+    }
+  };
+  uint4 wA[4][4], wB[4][4];
+  float sA[4][4], sB[4][4];
+  uint4 xv[4];
+  x_load(0, xv);
+  w_load(0, wA, sA);
+  x_store(0, xv);
+  for (int c = 0; c < nch; c += 2) {
+    const bool has1 = c + 1 < nch, has2 = c + 2 < nch;
+    if (has1) x_load(c + 1, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has1) w_load(c + 1, wB, sB);
+    __syncthreads();  // chunk c staged; chunk c - 1's buffer is free
+    if (wave_on) compute(c, 0, wA, sA);
+    if (has1) x_store(1, xv);
+    if (!has1) break;
+    if (has2) x_load(c + 2, xv);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has2) w_load(c + 2, wA, sA);
+    __syncthreads();  // chunk c + 1 staged; chunk c's buffer is free
+    if (wave_on) compute(c + 1, 1, wB, sB);
+    if (has2) x_store(0, xv);
+  }
+  if (!wave_on) return;
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int n = nw0 + 16 * tt + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 4 * g + r;
+      const bool ok = ri < R;
+      const float d = acc[tt][r];
+      if constexpr (MODE == MX_GATE_UP) {
+        const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        const float other = __shfl_xor(v, 1);
+        if (ok && (j & 1) == 0)
+          a.y[(size_t)rows[ri] * (N / 2) + n / 2] = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
+      } else {
+        if (ok) a.out_f[(size_t)rows[ri] * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+      }
+    }
+  }
+}
+
 // Row b's k slots in slot order from 0 (the exact path's fmaf chain), one
 // rounding to bf16, then h = bf16(h + y).
 __global__ __launch_bounds__(256) void k_mx_combine(const float* __restrict__ ybuf,
@@ -331,23 +482,32 @@ __global__ __launch_bounds__(256) void k_mx_rope_append(
   }
 }
 
-template <int MODE, int BT>
+template <int MODE, int BT, bool PK>
 static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
   const int it = (a.K / 32 + 15) / 16;
-  if (it <= 2) hipLaunchKernelGGL((k_mx_gemv<BT, 2, MODE>), grid, dim3(256), 0, st, a);
-  else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv<BT, 4, MODE>), grid, dim3(256), 0, st, a);
-  else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv<BT, 6, MODE>), grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((k_mx_gemv<BT, 8, MODE>), grid, dim3(256), 0, st, a);
+  if (it <= 2) hipLaunchKernelGGL((k_mx_gemv<BT, 2, MODE, PK>), grid, dim3(256), 0, st, a);
+  else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv<BT, 4, MODE, PK>), grid, dim3(256), 0, st, a);
+  else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv<BT, 6, MODE, PK>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((k_mx_gemv<BT, 8, MODE, PK>), grid, dim3(256), 0, st, a);
 }
 
+template <int MODE, bool PK>
+static void mx_launch_pk(const MxArgs& a, dim3 grid, hipStream_t st) {
+  switch ((a.B + 15) / 16) {
+    case 1: mx_launch_it<MODE, 1, PK>(a, grid, st); break;
+    case 2: mx_launch_it<MODE, 2, PK>(a, grid, st); break;
+    case 3: mx_launch_it<MODE, 3, PK>(a, grid, st); break;
+    default: mx_launch_it<MODE, 4, PK>(a, grid, st); break;
+  }
+}
+
+// the expert modes read the checkpoint layout; the dense modes the packed
+// copy when there is one
 template <int MODE>
 static void mx_launch(const MxArgs& a, dim3 grid, hipStream_t st) {
-  switch ((a.B + 15) / 16) {
-    case 1: mx_launch_it<MODE, 1>(a, grid, st); break;
-    case 2: mx_launch_it<MODE, 2>(a, grid, st); break;
-    case 3: mx_launch_it<MODE, 3>(a, grid, st); break;
-    default: mx_launch_it<MODE, 4>(a, grid, st); break;
-  }
+  constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
+  if (!MOE && a.Wp) mx_launch_pk<MODE, !MOE>(a, grid, st);
+  else mx_launch_pk<MODE, false>(a, grid, st);
 }
 
 bool mx_shape_ok(int N, int K, int B) {
@@ -372,8 +532,20 @@ void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
   hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx, gate_up.B * gate_up.k,
                      gate_up.E, S, const_cast<int32_t*>(gate_up.route));
-  mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 64, S), st);
-  mx_launch<MX_DOWN>(down, dim3(down.N / 64, S), st);
+  if (gate_up.B <= 16 && gate_up.Wp && down.Wp) {
+    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + 255) / 256, S),
+                       dim3(256), 0, st, gate_up);
+    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + 255) / 256, S), dim3(256), 0,
+                       st, down);
+  } else if (gate_up.B <= 16) {
+    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, false>), dim3((gate_up.N + 255) / 256, S),
+                       dim3(256), 0, st, gate_up);
+    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, false>), dim3((down.N + 255) / 256, S), dim3(256),
+                       0, st, down);
+  } else {
+    mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 64, S), st);
+    mx_launch<MX_DOWN>(down, dim3(down.N / 64, S), st);
+  }
   hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
                      down.out_f, score, h, down.N, down.k);
 }
@@ -384,6 +556,73 @@ void launch_mx_rope_append(const uint16_t* qkv, const int32_t* pos, const int32_
                            int key_mask, hipStream_t st) {
   hipLaunchKernelGGL(k_mx_rope_append, dim3(B), dim3(256), 0, st, qkv, pos, seq, cos_t, sin_t,
                      q_out, kc, vc, Hq, Hkv, T_max, key_mask);
+}
+
+// ---- MFMA lane-order copies ------------------------------------------------
+// bf16 [N][K] -> [N/16][NCH][t][g][j][8 elements], NCH = ceil(K / 128): piece
+// (T, ch, t, g, j) holds row 16 T + j, elements 128 ch + 32 t + 8 g .. + 7
+// (zeros past K), the 16 bytes lane j + 16 g of k_mx_gemv loads in step t.
+__global__ __launch_bounds__(256) void k_mx_pack_bf16(const uint16_t* __restrict__ W, int N,
+                                                      int K, uint16_t* __restrict__ P) {
+  const int NCH = (K + 127) / 128;
+  const size_t total = (size_t)(N / 16) * NCH * 256;
+  for (size_t p = (size_t)blockIdx.x * 256 + threadIdx.x; p < total;
+       p += (size_t)gridDim.x * 256) {
+    const int j = p & 15, g = (p >> 4) & 3, t = (p >> 6) & 3;
+    const size_t rest = p >> 8;
+    const int ch = (int)(rest % NCH);
+    const size_t T = rest / NCH;
+    const int el = ch * 128 + 32 * t + 8 * g;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (el < K) v = *reinterpret_cast<const uint4*>(W + (T * 16 + j) * (size_t)K + el);
+    *reinterpret_cast<uint4*>(P + p * 8) = v;
+  }
+}
+
+// MXFP4 [E][N][U units of 16 code bytes] (+ scales [E][N][U]) ->
+// [E][N/16][nch][su][g][j] pieces, nch = ceil(U / 16): piece (e, T, c, su, g, j)
+// holds unit 16 c + 4 g + su of row 16 T + j (zero codes and scale 127 past U),
+// what lane j + 16 g of k_mx_moe16 loads for slot su of chunk c.
+__global__ __launch_bounds__(256) void k_mx_pack_fp4(const uint8_t* __restrict__ codes,
+                                                     const uint8_t* __restrict__ scales, int E,
+                                                     int N, int K, uint8_t* __restrict__ Pc,
+                                                     uint8_t* __restrict__ Ps) {
+  const int U = K / 32, nch = (U + 15) / 16;
+  const size_t total = (size_t)E * (N / 16) * nch * 256;
+  for (size_t p = (size_t)blockIdx.x * 256 + threadIdx.x; p < total;
+       p += (size_t)gridDim.x * 256) {
+    const int j = p & 15, g = (p >> 4) & 3, su = (p >> 6) & 3;
+    const size_t rest = p >> 8;
+    const int c = (int)(rest % nch);
+    const size_t row = (rest / nch) * 16 + j;  // e N + 16 T + j
+    const int u = 16 * c + 4 * g + su;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    uint8_t sc = 127;
+    if (u < U) {
+      v = *reinterpret_cast<const uint4*>(codes + row * (size_t)(K / 2) + (size_t)u * 16);
+      sc = scales[row * (size_t)U + u];
+    }
+    *reinterpret_cast<uint4*>(Pc + p * 16) = v;
+    Ps[p] = sc;
+  }
+}
+
+size_t mx_packed_bf16_bytes(int N, int K) {
+  return (size_t)(N / 16) * ((K + 127) / 128) * 256 * 16;
+}
+
+size_t mx_packed_fp4_pieces(int E, int N, int K) {
+  return (size_t)E * (N / 16) * ((K / 32 + 15) / 16) * 256;
+}
+
+void launch_mx_pack_bf16(const uint16_t* W, int N, int K, uint16_t* P, hipStream_t st) {
+  hipLaunchKernelGGL(k_mx_pack_bf16, dim3(2048), dim3(256), 0, st, W, N, K, P);
+}
+
+void launch_mx_pack_fp4(const uint8_t* codes, const uint8_t* scales, int E, int N, int K,
+                        uint8_t* Pc, uint8_t* Ps, hipStream_t st) {
+  hipLaunchKernelGGL(k_mx_pack_fp4, dim3(2048), dim3(256), 0, st, codes, scales, E, N, K, Pc,
+                     Ps);
 }
 
 }  // namespace neon
