@@ -296,7 +296,9 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   }
 }
 
-// Expert rows for at most 16 rows per expert (B <= 16).  A block of 4 waves
+// Expert rows, 16 of an expert's rows per block (its pair list split into
+// groups of 16; the groups of one expert are neighbouring blocks, so the
+// later ones find the weights in cache).  A block of 4 waves
 // owns 256 rows of one expert (64 per wave in 4 tiles of 16) and each wave
 // runs the whole K, so nothing is reduced across waves.  The expert's
 // activation rows go through LDS 512 elements (16 units) at a time, double
@@ -313,11 +315,17 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
-  const int S = gridDim.y;
-  const int e = a.route[blockIdx.y];
-  if (e < 0) return;  // fewer used experts than block rows (uniform)
-  const int R = a.route[S + blockIdx.y];  // 1 .. 16
-  const int32_t* rows = a.route + 2 * S + 64 * blockIdx.y;
+  // block row y = slot G + group: rows 16 group .. 16 group + 15 of the
+  // slot's pair list (G = ceil(B / 16) groups per used-expert slot)
+  const int G = (a.B + 15) / 16;
+  const int slot = blockIdx.y / G, grp = blockIdx.y % G;
+  const int S = gridDim.y / G;
+  const int e = a.route[slot];
+  if (e < 0) return;  // fewer used experts than slots (uniform)
+  const int Rall = a.route[S + slot];
+  if (16 * grp >= Rall) return;  // (uniform)
+  const int R = min(16, Rall - 16 * grp);
+  const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
   const int nw0 = blockIdx.x * 256 + 64 * w;  // the wave's first row
   const bool wave_on = nw0 < N;               // uniform per wave
   const int nch = (U + CKU - 1) / CKU;
@@ -532,11 +540,12 @@ void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
   hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx, gate_up.B * gate_up.k,
                      gate_up.E, S, const_cast<int32_t*>(gate_up.route));
-  if (gate_up.B <= 16 && gate_up.Wp && down.Wp) {
-    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + 255) / 256, S),
+  const int G = (gate_up.B + 15) / 16;
+  if (gate_up.Wp && down.Wp) {
+    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + 255) / 256, S * G),
                        dim3(256), 0, st, gate_up);
-    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + 255) / 256, S), dim3(256), 0,
-                       st, down);
+    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + 255) / 256, S * G),
+                       dim3(256), 0, st, down);
   } else if (gate_up.B <= 16) {
     hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, false>), dim3((gate_up.N + 255) / 256, S),
                        dim3(256), 0, st, gate_up);
