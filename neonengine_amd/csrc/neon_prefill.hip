@@ -323,41 +323,46 @@ __device__ __forceinline__ int block_excl_scan_1024(int v, int* lds) {
   return r;
 }
 
-__global__ __launch_bounds__(1024) void k_moe_group(
-    const int32_t* __restrict__ idx, int n_pairs, int k, int E,
-    int32_t* __restrict__ list_tok, int32_t* __restrict__ list_slot,
-    int32_t* __restrict__ e_off, int32_t* __restrict__ tile_e,
-    int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles) {
-  __shared__ int scan_lds[17];
-  __shared__ int base;
+// Expert grouping, step 1 (one block): pairs per expert (LDS atomics), the
+// offsets e_off[0..E] and the 128-row tiles (tile_e, tile_r0, n_tiles).
+__global__ __launch_bounds__(1024) void k_moe_count(
+    const int32_t* __restrict__ idx, int n_pairs, int E, int32_t* __restrict__ e_off,
+    int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles) {
+  __shared__ int cnt[256];
   const int tid = threadIdx.x;
-  const int per = (n_pairs + 1023) / 1024;
-  const int p0 = tid * per, p1 = min(p0 + per, n_pairs);
-  if (tid == 0) base = 0;
+  if (tid < 256) cnt[tid] = 0;
   __syncthreads();
-  for (int e = 0; e < E; ++e) {
-    int c = 0;
-    for (int q = p0; q < p1; ++q) c += idx[q] == e;
-    const int pos = block_excl_scan_1024(c, scan_lds);
-    const int tot = scan_lds[16];
-    const int b0 = base;
-    if (tid == 0) e_off[e] = b0;
-    int o = b0 + pos;
-    for (int q = p0; q < p1; ++q)
-      if (idx[q] == e) { list_tok[o] = q / k; list_slot[o] = q % k; ++o; }
-    __syncthreads();
-    if (tid == 0) base = b0 + tot;
-    __syncthreads();
-  }
+  for (int q = tid; q < n_pairs; q += 1024) atomicAdd(&cnt[idx[q]], 1);
+  __syncthreads();
   if (tid == 0) {
-    e_off[E] = base;
-    int t = 0;
+    int base = 0, t = 0;
     for (int e = 0; e < E; ++e) {
-      const int cnt = e_off[e + 1] - e_off[e];
-      for (int r = 0; r < cnt; r += kGM) { tile_e[t] = e; tile_r0[t] = r; ++t; }
+      e_off[e] = base;
+      const int c = cnt[e];
+      for (int r = 0; r < c; r += kGM) { tile_e[t] = e; tile_r0[t] = r; ++t; }
+      base += c;
     }
+    e_off[E] = base;
     *n_tiles = t;
   }
+}
+
+// Expert grouping, step 2 (block e): the pairs q that chose expert e, in
+// increasing q, at e_off[e] ..: (token q / k, slot q % k).  Thread tid holds
+// pairs tid * per .. tid * per + per - 1; one block scan orders the threads.
+__global__ __launch_bounds__(1024) void k_moe_group(
+    const int32_t* __restrict__ idx, int n_pairs, int k, const int32_t* __restrict__ e_off,
+    int32_t* __restrict__ list_tok, int32_t* __restrict__ list_slot) {
+  __shared__ int scan_lds[17];
+  const int e = blockIdx.x, tid = threadIdx.x;
+  const int per = (n_pairs + 1023) / 1024;
+  const int p0 = tid * per, p1 = min(p0 + per, n_pairs);
+  int c = 0;
+  for (int q = p0; q < p1; ++q) c += idx[q] == e;
+  const int pos = block_excl_scan_1024(c, scan_lds);
+  int o = e_off[e] + pos;
+  for (int q = p0; q < p1; ++q)
+    if (idx[q] == e) { list_tok[o] = q / k; list_slot[o] = q % k; ++o; }
 }
 
 // out[t] = bf16(residual[t] + bf16(sum_s score[t][s] * y[t][s]))  in slot
@@ -381,8 +386,10 @@ __global__ void k_moe_combine(const float* __restrict__ ybuf,
 // bf16, ybuf [M][k][H] fp32.
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   const int n_pairs = a.M * a.k;
-  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.E,
-                     a.list_tok, a.list_slot, a.e_off, a.tile_e, a.tile_r0, a.n_tiles);
+  hipLaunchKernelGGL(k_moe_count, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.E, a.e_off,
+                     a.tile_e, a.tile_r0, a.n_tiles);
+  hipLaunchKernelGGL(k_moe_group, dim3(a.E), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.e_off,
+                     a.list_tok, a.list_slot);
   const int max_tiles = moe_prefill_max_tiles(a.M, a.k, a.E);
   GemmParams p{};
   p.tile_e = a.tile_e; p.tile_r0 = a.tile_r0; p.n_tiles = a.n_tiles; p.e_off = a.e_off;
