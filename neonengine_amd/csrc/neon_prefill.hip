@@ -476,109 +476,183 @@ void launch_kv_ring_store(const uint16_t* ks, const uint16_t* vs, int S, int t0,
 }
 
 // ===========================================================================
-// Causal sink attention over a prompt (HFM:235-263).  grid (Hkv, ceil(M/64)),
-// block 64 G: wave w is q head g G + w, lane l is query row 64 blockIdx.y + l.
-// K/V tiles of 64 keys are staged once per block in LDS as fp32 and read by
-// all lanes at the same address (broadcast).  Keys go 16 at a time through an
-// online softmax (scores x 1/8, HFM:277); the sink joins the denominator at
-// the end.  Sliding layers see keys (t - window, t].
+// Causal sink attention over a prompt (HFM:235-263) on the matrix cores.
+// grid (Hkv, ceil(M/64)), block 64 G: wave w is q head g G + w for the 64
+// query rows t0 .. t0+63 of block row y.  Per tile of 64 keys (staged once per
+// block in LDS: K as [key][dim], V transposed as [dim][key]):
+//   S^T = K Q^T  (v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 dims from LDS,
+//                 B = 32 dims x 16 queries from registers); lane (j, g) holds
+//                 S^T[key 16 kt + 4 g + r][query 16 qt + j];
+//   scores x 1/8 (HFM:277), causal / window mask, online softmax per query
+//   (max over the 4 lane groups by xor 16, 32);
+//   O^T += V^T P^T  (A = 16 dims x 8 keys of V^T, B = the same 8 keys of P^T
+//                    as the lane already holds them: keys 32 p + 4 g + r and
+//                    32 p + 16 + 4 g + r), with P split into bf16 hi + lo so
+//                    the products keep ~16 bits of P.
+// The sink joins the denominator at the end.  Sliding layers see keys
+// (t - window, t].
 // ===========================================================================
+typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ pf_bf16x8 pf_as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(pf_bf16x8, v);
+}
+
 __global__ __launch_bounds__(512) void k_attn_prefill(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const uint16_t* __restrict__ sinks,
     uint16_t* __restrict__ out, int M, int Hq, int Hkv, int T_max, int window) {
-  __shared__ __align__(16) float ks[64 * 64];
-  __shared__ __align__(16) float vs[64 * 64];
-  const int g = blockIdx.x, G = Hq / Hkv;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = g * G + w;
+  constexpr int VT = 64 + 8;  // V^T row stride (bf16): 8 pad breaks bank conflicts
+  __shared__ __align__(16) uint16_t ks[64 * 64];
+  __shared__ __align__(16) uint16_t vt[64 * VT];
+  const int gkv = blockIdx.x, G = Hq / Hkv;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int j = lane & 15, g = lane >> 4;
+  const int h = gkv * G + w;
   const int t0 = blockIdx.y * 64;
-  const int t = min(t0 + lane, M - 1);
-  const int lo_t = window > 0 ? max(0, t - window + 1) : 0;
-  float qr[64];
-  {
-    const uint4* qv = reinterpret_cast<const uint4*>(q + ((size_t)t * Hq + h) * 64);
+  // Q^T fragments: query 16 qt + j, dims 32 h2 + 8 g .. + 7
+  uint4 qf[4][2];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) unpack8(qv[u], &qr[8 * u]);
+  for (int qt = 0; qt < 4; ++qt) {
+    const int t = min(t0 + 16 * qt + j, M - 1);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+      qf[qt][h2] = *reinterpret_cast<const uint4*>(q + ((size_t)t * Hq + h) * 64 + 32 * h2 + 8 * g);
   }
-  float o[64];
+  pf_f32x4 o[4][4];  // [qt][dt]: O^T[dim 16 dt + 4 g + r][query 16 qt + j]
 #pragma unroll
-  for (int d = 0; d < 64; ++d) o[d] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
+  for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[qt][dt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m[4], l[4];  // per query column (qt, j); l is this lane's partial sum
+#pragma unroll
+  for (int qt = 0; qt < 4; ++qt) { m[qt] = -INFINITY; l[qt] = 0.0f; }
   const int hi_blk = min(M - 1, t0 + 63);
   const int lo_blk = window > 0 ? max(0, t0 - window + 1) : 0;
-  const uint16_t* kg = kc + (size_t)g * T_max * 64;
-  const uint16_t* vg = vc + (size_t)g * T_max * 64;
+  const uint16_t* kg = kc + (size_t)gkv * T_max * 64;
+  const uint16_t* vg = vc + (size_t)gkv * T_max * 64;
   for (int j0 = (lo_blk / 64) * 64; j0 <= hi_blk; j0 += 64) {
     __syncthreads();  // the previous tile is consumed
-    for (int c = threadIdx.x; c < 64 * 8; c += blockDim.x) {
-      const int key = min(j0 + (c >> 3), T_max - 1), dq = (c & 7) * 8;
+    for (int c = tid; c < 64 * 8; c += blockDim.x) {
+      const int kl = c >> 3, dq = (c & 7) * 8;
+      const int key = min(j0 + kl, T_max - 1);
       const uint4 kv = *reinterpret_cast<const uint4*>(kg + (size_t)key * 64 + dq);
       const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * 64 + dq);
-      float f[8];
-      unpack8(kv, f);
-      *reinterpret_cast<float4*>(&ks[(c >> 3) * 64 + dq]) = make_float4(f[0], f[1], f[2], f[3]);
-      *reinterpret_cast<float4*>(&ks[(c >> 3) * 64 + dq + 4]) = make_float4(f[4], f[5], f[6], f[7]);
-      unpack8(vv, f);
-      *reinterpret_cast<float4*>(&vs[(c >> 3) * 64 + dq]) = make_float4(f[0], f[1], f[2], f[3]);
-      *reinterpret_cast<float4*>(&vs[(c >> 3) * 64 + dq + 4]) = make_float4(f[4], f[5], f[6], f[7]);
+      *reinterpret_cast<uint4*>(&ks[kl * 64 + dq]) = kv;
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(dq + 2 * e) * VT + kl] = (uint16_t)(vw[e] & 0xFFFFu);
+        vt[(dq + 2 * e + 1) * VT + kl] = (uint16_t)(vw[e] >> 16);
+      }
     }
     __syncthreads();
-    for (int jg = 0; jg < 64; jg += 16) {
-      float s[16];
-      float mt = m;
+    // S^T tiles
+    pf_f32x4 sacc[4][4];  // [kt][qt]
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int j = jg + jj, key = j0 + j;
-        const float4* kr = reinterpret_cast<const float4*>(&ks[j * 64]);
-        float a = 0.0f;
+    for (int kt = 0; kt < 4; ++kt) {
+      const uint4 ka0 = *reinterpret_cast<const uint4*>(&ks[(16 * kt + j) * 64 + 8 * g]);
+      const uint4 ka1 = *reinterpret_cast<const uint4*>(&ks[(16 * kt + j) * 64 + 32 + 8 * g]);
 #pragma unroll
-        for (int d4 = 0; d4 < 16; ++d4) {
-          const float4 kk = kr[d4];
-          a = __builtin_fmaf(qr[4 * d4], kk.x, a);
-          a = __builtin_fmaf(qr[4 * d4 + 1], kk.y, a);
-          a = __builtin_fmaf(qr[4 * d4 + 2], kk.z, a);
-          a = __builtin_fmaf(qr[4 * d4 + 3], kk.w, a);
-        }
-        const bool valid = key >= lo_t && key <= t;
-        s[jj] = valid ? __fmul_rn(a, 0.125f) : -INFINITY;
-        mt = fmaxf(mt, s[jj]);
+      for (int qt = 0; qt < 4; ++qt) {
+        pf_f32x4 acc = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(ka0), pf_as_bf16x8(qf[qt][0]),
+                                                     acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(ka1), pf_as_bf16x8(qf[qt][1]),
+                                                     acc, 0, 0, 0);
+        sacc[kt][qt] = acc;
       }
-      if (mt == -INFINITY) continue;  // no valid key for this lane yet
-      const float sc = __expf(m - mt);  // m = -inf -> 0
-      l *= sc;
+    }
+    // scale, mask, online softmax; P^T (hi, lo) packed per key pair p
+    uint4 phi[4][2], plo[4][2];  // [qt][p]
 #pragma unroll
-      for (int d = 0; d < 64; ++d) o[d] *= sc;
+    for (int qt = 0; qt < 4; ++qt) {
+      const int t = t0 + 16 * qt + j;
+      const int lo_t = window > 0 ? max(0, t - window + 1) : 0;
+      float sv[4][4];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const float pj = __expf(s[jj] - mt);
-        l += pj;
-        const float4* vr = reinterpret_cast<const float4*>(&vs[(jg + jj) * 64]);
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int d4 = 0; d4 < 16; ++d4) {
-          const float4 vv = vr[d4];
-          o[4 * d4] = __builtin_fmaf(pj, vv.x, o[4 * d4]);
-          o[4 * d4 + 1] = __builtin_fmaf(pj, vv.y, o[4 * d4 + 1]);
-          o[4 * d4 + 2] = __builtin_fmaf(pj, vv.z, o[4 * d4 + 2]);
-          o[4 * d4 + 3] = __builtin_fmaf(pj, vv.w, o[4 * d4 + 3]);
+        for (int r = 0; r < 4; ++r) {
+          const int key = j0 + 16 * kt + 4 * g + r;
+          const bool valid = key >= lo_t && key <= t;
+          sv[kt][r] = valid ? __fmul_rn(sacc[kt][qt][r], 0.125f) : -INFINITY;
+          mx = fmaxf(mx, sv[kt][r]);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mt = fmaxf(m[qt], mx);
+      const float sc = mt == -INFINITY ? 1.0f : __expf(m[qt] - mt);  // m = -inf -> 0
+      l[qt] *= sc;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        o[qt][dt][0] *= sc; o[qt][dt][1] *= sc; o[qt][dt][2] *= sc; o[qt][dt][3] *= sc;
+      }
+      m[qt] = mt;
+      float pv[4][4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pv[kt][r] = sv[kt][r] == -INFINITY ? 0.0f : __expf(sv[kt][r] - mt);
+          l[qt] += pv[kt][r];
+        }
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int half = 0; half < 2; ++half)
+#pragma unroll
+          for (int r2 = 0; r2 < 2; ++r2) {
+            const float a0 = pv[2 * pp + half][2 * r2], a1 = pv[2 * pp + half][2 * r2 + 1];
+            const uint16_t h0 = f2bf(a0), h1 = f2bf(a1);
+            const uint16_t l0 = f2bf(a0 - bf2f(h0)), l1 = f2bf(a1 - bf2f(h1));
+            hw[2 * half + r2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+            lw[2 * half + r2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+          }
+        phi[qt][pp] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        plo[qt][pp] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+      }
+    }
+    // O^T += V^T P^T
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint16_t* vrow = &vt[(16 * dt + j) * VT];
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const uint2 va = *reinterpret_cast<const uint2*>(vrow + 32 * pp + 4 * g);
+        const uint2 vb = *reinterpret_cast<const uint2*>(vrow + 32 * pp + 16 + 4 * g);
+        const uint4 vfrag = make_uint4(va.x, va.y, vb.x, vb.y);
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              pf_as_bf16x8(vfrag), pf_as_bf16x8(phi[qt][pp]), o[qt][dt], 0, 0, 0);
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              pf_as_bf16x8(vfrag), pf_as_bf16x8(plo[qt][pp]), o[qt][dt], 0, 0, 0);
         }
       }
-      m = mt;
     }
   }
   const float sk = bf2f(sinks[h]);
-  const float mt = fmaxf(m, sk);
-  const float sc = __expf(m - mt);
-  const float inv = 1.0f / (l * sc + __expf(sk - mt));
-  if (t0 + lane < M) {
-    uint4* dst = reinterpret_cast<uint4*>(out + (size_t)t * Hq * 64 + (size_t)h * 64);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      uint32_t wv[4];
+  for (int qt = 0; qt < 4; ++qt) {
+    float lt = l[qt];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
+    const float mt = fmaxf(m[qt], sk);
+    const float sc = __expf(m[qt] - mt);
+    const float inv = 1.0f / (lt * sc + __expf(sk - mt));
+    const int t = t0 + 16 * qt + j;
+    if (t < M) {
+      uint16_t* dst = out + (size_t)t * Hq * 64 + (size_t)h * 64;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wv[j] = pack_bf2(o[8 * u + 2 * j] * sc * inv, o[8 * u + 2 * j + 1] * sc * inv);
-      dst[u] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint32_t w0 = pack_bf2(o[qt][dt][0] * sc * inv, o[qt][dt][1] * sc * inv);
+        const uint32_t w1 = pack_bf2(o[qt][dt][2] * sc * inv, o[qt][dt][3] * sc * inv);
+        *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * g) = make_uint2(w0, w1);
+      }
     }
   }
 }
