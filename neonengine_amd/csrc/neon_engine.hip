@@ -707,7 +707,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
     a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
-    launch_attn(a, st);
+    launch_mx_attn(a, st);
     MxArgs o{};
     o.W = w.wo; o.Wp = mp.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
     o.B = B; o.N = H; o.K = c.n_heads * D;

@@ -189,6 +189,9 @@ struct AttnArgs {
   // rows - 1 for a power-of-two ring that holds the last `rows` positions
   int key_mask;
 };
+// decode attention of the matrix-core steps (same partials and merge as launch_attn)
+void launch_mx_attn(const AttnArgs& a, hipStream_t st);
+void launch_attn_merge(const AttnArgs& a, hipStream_t st);
 void launch_attn(const AttnArgs& a, hipStream_t st);
 // number of key splits used for a cache of T_max rows (window 0 = full layer)
 int attn_splits(int T_max, int window);

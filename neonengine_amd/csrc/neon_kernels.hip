@@ -2316,6 +2316,11 @@ __global__ __launch_bounds__(64) void k_attn_merge(
 #undef ATTN_LOAD_WORD
 #undef ATTN_STORE_WORD
 
+void launch_attn_merge(const AttnArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o, a.part_ml,
+                     a.sinks, a.out, a.Hq, a.S);
+}
+
 void launch_attn(const AttnArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;  // 1, 2, 4 or 8 (checked on the host)
   // one split: a block per query head (more CUs for a short span); several:

@@ -447,6 +447,160 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   }
 }
 
+// Decode attention of the matrix-core steps (HFM:235-263): block = one wave
+// for (kv head g, key split s, row b); the G query heads of g are the query
+// columns of v_mfma_f32_16x16x32_bf16 (columns G .. 15 are zero).  The split's
+// 64-key chunks go through LDS (K as [key][dim], V transposed), loaded 1 KB
+// contiguous per instruction with each key at its cache row (pos & key_mask
+// for a ring); S^T = K Q^T, scores x 1/8, keys past the row's position
+// masked, online softmax per head, O^T += V^T P^T with P in bf16 hi + lo.
+// One split finishes with the sink here; several leave (o, m, l) partials in
+// the exact kernels' layout for k_attn_merge.
+__global__ __launch_bounds__(64) void k_mx_attn(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
+    const int32_t* __restrict__ seq, float* __restrict__ part_o, float* __restrict__ part_ml,
+    const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv, int G,
+    int T_max, int key_mask, int window, int S, int q_stride) {
+  constexpr int VT = 64 + 8;
+  __shared__ __align__(16) uint16_t ks[64 * 64];
+  __shared__ __align__(16) uint16_t vt[64 * VT];
+  const int lane = threadIdx.x, j = lane & 15, gq = lane >> 4;
+  const int g = blockIdx.x % Hkv, sp = blockIdx.x / Hkv, b = blockIdx.y;
+  const int p = pos_arr[b];
+  const int sq = seq != nullptr ? seq[b] : b;
+  const int lo = (window > 0 && p - window + 1 > 0) ? p - window + 1 : 0;
+  const int nch = (p - lo + 1 + 63) >> 6;
+  const int c0 = (int)((int64_t)sp * nch / S), c1 = (int)((int64_t)(sp + 1) * nch / S);
+  const size_t kv_base = ((size_t)sq * Hkv + g) * T_max;
+  const bool hv = j < G;
+  const int h = g * G + (hv ? j : 0);
+  uint4 qf[2];
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2)
+    qf[h2] = hv ? *reinterpret_cast<const uint4*>(q + (size_t)b * q_stride + (size_t)h * 64 +
+                                                  32 * h2 + 8 * gq)
+                : make_uint4(0u, 0u, 0u, 0u);
+  mx_f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  float m = -INFINITY, l = 0.0f;
+  for (int c = c0; c < c1; ++c) {
+    const int kb = lo + 64 * c;
+    __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kl = 8 * i + (lane >> 3), dq = (lane & 7) * 8;
+      const int key = min(kb + kl, p);  // keys past p are masked below
+      const size_t row = kv_base + (size_t)(key & key_mask);
+      const uint4 kv = *reinterpret_cast<const uint4*>(kc + row * 64 + dq);
+      const uint4 vv = *reinterpret_cast<const uint4*>(vc + row * 64 + dq);
+      *reinterpret_cast<uint4*>(&ks[kl * 64 + dq]) = kv;
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(dq + 2 * e) * VT + kl] = (uint16_t)(vw[e] & 0xFFFFu);
+        vt[(dq + 2 * e + 1) * VT + kl] = (uint16_t)(vw[e] >> 16);
+      }
+    }
+    __syncthreads();
+    float sv[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const uint4 ka0 = *reinterpret_cast<const uint4*>(&ks[(16 * kt + j) * 64 + 8 * gq]);
+      const uint4 ka1 = *reinterpret_cast<const uint4*>(&ks[(16 * kt + j) * 64 + 32 + 8 * gq]);
+      mx_f32x4 acc = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(ka0), mx_as_bf16x8(qf[0]), acc,
+                                                   0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(ka1), mx_as_bf16x8(qf[1]), acc,
+                                                   0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool valid = kb + 16 * kt + 4 * gq + r <= p;
+        sv[kt][r] = valid ? __fmul_rn(acc[r], 0.125f) : -INFINITY;
+        mx = fmaxf(mx, sv[kt][r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mt = fmaxf(m, mx);
+    const float sc = mt == -INFINITY ? 1.0f : __expf(m - mt);  // m = -inf -> 0
+    l *= sc;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt][0] *= sc; o[dt][1] *= sc; o[dt][2] *= sc; o[dt][3] *= sc;
+    }
+    m = mt;
+    float pv[4][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pv[kt][r] = sv[kt][r] == -INFINITY ? 0.0f : __expf(sv[kt][r] - mt);
+        l += pv[kt][r];
+      }
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const float a0 = pv[2 * pp + half][2 * r2], a1 = pv[2 * pp + half][2 * r2 + 1];
+          const uint16_t h0 = f2bf(a0), h1 = f2bf(a1);
+          const uint16_t l0 = f2bf(a0 - bf2f(h0)), l1 = f2bf(a1 - bf2f(h1));
+          hw[2 * half + r2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          lw[2 * half + r2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+        }
+      const uint4 phi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      const uint4 plo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* vrow = &vt[(16 * dt + j) * VT];
+        const uint2 va = *reinterpret_cast<const uint2*>(vrow + 32 * pp + 4 * gq);
+        const uint2 vb = *reinterpret_cast<const uint2*>(vrow + 32 * pp + 16 + 4 * gq);
+        const uint4 vfrag = make_uint4(va.x, va.y, vb.x, vb.y);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(vfrag), mx_as_bf16x8(phi),
+                                                        o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(vfrag), mx_as_bf16x8(plo),
+                                                        o[dt], 0, 0, 0);
+      }
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!hv) return;
+  if (S == 1) {
+    const float sk = bf2f(sinks[h]);
+    const float M = fmaxf(m, sk);
+    const float f = m == -INFINITY ? 0.0f : __expf(m - M);
+    const float inv = 1.0f / (l * f + __expf(sk - M));
+    uint16_t* dst = out + ((size_t)b * Hq + h) * 64;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint32_t w0 = pack_bf2(o[dt][0] * f * inv, o[dt][1] * f * inv);
+      const uint32_t w1 = pack_bf2(o[dt][2] * f * inv, o[dt][3] * f * inv);
+      *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * gq) = make_uint2(w0, w1);
+    }
+  } else {
+    const size_t pi = ((size_t)b * Hq + h) * S + sp;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      *reinterpret_cast<float4*>(part_o + pi * 64 + 16 * dt + 4 * gq) =
+          make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+    if (gq == 0) { part_ml[pi * 2] = m; part_ml[pi * 2 + 1] = l; }
+  }
+}
+
+void launch_mx_attn(const AttnArgs& a, hipStream_t st) {
+  const int G = a.Hq / a.Hkv;
+  hipLaunchKernelGGL(k_mx_attn, dim3(a.Hkv * a.S, a.B), dim3(64), 0, st, a.q, a.kc, a.vc,
+                     a.pos, a.seq, a.part_o, a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G,
+                     a.T_max, a.key_mask, a.window, a.S, a.q_stride);
+  if (a.S > 1) launch_attn_merge(a, st);
+}
+
 // Row b's k slots in slot order from 0 (the exact path's fmaf chain), one
 // rounding to bf16, then h = bf16(h + y).
 __global__ __launch_bounds__(256) void k_mx_combine(const float* __restrict__ ybuf,
