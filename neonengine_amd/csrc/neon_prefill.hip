@@ -7,7 +7,8 @@
 //   - grouped MXFP4 GEMM over the tokens routed to each expert, with the
 //     expert rows dequantised exactly to bf16 in LDS (E2M1 x 2^(s-127) is a
 //     bf16 value), SwiGLU fused into the gate_up epilogue;
-//   - tiled causal sink attention over the KV cache the prefill fills.
+//   - tiled causal sink attention over the KV cache the prefill fills, on
+//     the matrix cores as well (S^T = K Q^T, O^T += V^T P^T).
 // The maths is the decode path's (HFM:82-112, 235-263, 347-376); the
 // accumulation order of a matrix-core dot product differs from the decode
 // kernels' canonical fp32 chain, so prefill agrees with it within fp32
