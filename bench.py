@@ -197,6 +197,8 @@ def main():
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prompt-only", type=int, default=0, metavar="N",
+                    help="profiling aid: run the matrix-core prompt pass N times and exit")
     ap.add_argument("--moe-only", action="store_true",
                     help="only the MoE launch-pair timing plus a plain 256 MiB device copy "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -219,6 +221,18 @@ def main():
     torch.cuda.set_device(0)
     if args.moe_only:
         moe_only(ne, torch, args)
+        return
+    if args.prompt_only:
+        cfg = ne.config_preset(args.model, max_seq=args.prompt + 8, max_batch=1)
+        eng = ne.Engine(cfg, device=0)
+        eng.init_random(args.seed)
+        eng.set_prefill_mode(ne.PREFILL_BATCHED)
+        prompt = np.random.default_rng(args.seed).integers(0, cfg.vocab, size=(1, args.prompt))
+        for i in range(args.prompt_only):
+            eng.prefill(prompt)
+            torch.cuda.synchronize()
+            log(f"[bench] matrix-core prompt pass {i + 1}/{args.prompt_only} done")
+        eng.close()
         return
     B = args.batch
     max_seq = args.prompt + args.warmup + args.steps + 8
