@@ -46,7 +46,7 @@ void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
 }
 
 // ===========================================================================
-// Matrix-core GEMM.  Block tile 128 x 128, K step 32, 4 waves in 2 x 2, each
+// Matrix-core GEMM.  Block tile 128 x 128, K step 64, 4 waves in 2 x 2, each
 // wave a 64 x 64 tile of 2 x 2 MFMA 32x32x16 blocks.  Both operands are
 // "row of the matrix, 8 consecutive k" per lane (lane l: row l % 32, k
 // 8 (l / 32) .. + 8), so A [M][K] and W [N][K] are staged the same way:
@@ -54,8 +54,10 @@ void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
 // so rows spread over the banks) -> ds_read_b128 operands.
 //
 // Rows past M or N read a clamped valid row and are never stored.  K must be
-// a multiple of 32.  With FP4, W is an MXFP4 matrix (codes [N][K/2], scales
-// [N][K/32]); one K step is exactly one scale block per row, dequantised as
+// a multiple of 32; when it is not one of 64, the last step's upper 32
+// elements are zeros (a zero A value and a zero code add nothing).  With FP4,
+// W is an MXFP4 matrix (codes [N][K/2], scales [N][K/32]); a thread stages
+// one scale block (32 values) of one row per step, dequantised as
 // E2M1 (v_cvt_scalef32_pk_f32_fp4, exact) x 2^(s-127) (ldexp, exact) and
 // rounded to bf16 (exact: every such value is a bf16 value or overflows).
 //
@@ -64,7 +66,7 @@ void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
 // expert's count are masked.  The A row of list row i is a_rows[i] (token)
 // when a_rows is given, else i itself.
 // ===========================================================================
-constexpr int kGM = 128, kGN = 128, kGK = 32, kGS = 40;  // tile, LDS row stride
+constexpr int kGM = 128, kGN = 128, kGK = 64, kGS = 72;  // tile, LDS row stride
 
 enum {
   GEMM_STORE = 0,    // C = bf16(acc + bias)
@@ -147,42 +149,54 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   const int K = p.K;
   // this thread's staging rows: A/W chunk c = tid + 256 i (i = 0, 1):
   // row c >> 2, k (c & 3) * 8; FP4 W: row tid >> 1, k half (tid & 1) * 16
-  const uint16_t* arow[2];
+  // staging: thread tid copies the 8-element piece (tid & 7) of rows
+  // (tid + 256 i) >> 3, i = 0..3 (128 rows x 64 elements per step)
+  const int pc = (tid & 7) * 8;
+  const uint16_t* arow[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (tid + 256 * i) >> 2;
+  for (int i = 0; i < 4; ++i) {
+    const int r = (tid + 256 * i) >> 3;
     const int lr = r0 + min(r, rows - 1);
     const int ar = GROUPED && p.a_rows ? p.a_rows[lr] : lr;
-    arow[i] = p.A + (size_t)ar * p.lda + ((tid + 256 * i) & 3) * 8;
+    arow[i] = p.A + (size_t)ar * p.lda + pc;
   }
-  const uint16_t* wrow[2] = {nullptr, nullptr};
+  const uint16_t* wrow[4] = {nullptr, nullptr, nullptr, nullptr};
   const uint8_t* crow = nullptr;
   const uint8_t* srow = nullptr;
+  const int half = tid & 1;  // FP4: which scale block (32 values) of the step
   if (FP4) {
     const int r = tid >> 1;
     const size_t nr = (size_t)e * p.N + min(n0 + r, p.N - 1);
-    crow = p.codes + nr * (K / 2) + (tid & 1) * 8;
-    srow = p.scales + nr * (K / 32);
+    crow = p.codes + nr * (K / 2) + half * 16;
+    srow = p.scales + nr * (K / 32) + half;
   } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = (tid + 256 * i) >> 2;
-      wrow[i] = p.W + (size_t)min(n0 + r, p.N - 1) * p.ldw + ((tid + 256 * i) & 3) * 8;
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid + 256 * i) >> 3;
+      wrow[i] = p.W + (size_t)min(n0 + r, p.N - 1) * p.ldw + pc;
     }
   }
-  u32x4_t ra0, ra1, rw0 = {}, rw1 = {};
-  u32x2_t rc = {};
+  const u32x4_t z4 = {0u, 0u, 0u, 0u};
+  u32x4_t ra[4], rw[4] = {z4, z4, z4, z4};
+  u32x4_t rc = z4;
   uint32_t rs = 127;
-  // k step 0
-  ra0 = *reinterpret_cast<const u32x4_t*>(arow[0]);
-  ra1 = *reinterpret_cast<const u32x4_t*>(arow[1]);
-  if (FP4) {
-    rc = *reinterpret_cast<const u32x2_t*>(crow);
-    rs = srow[0];
-  } else {
-    rw0 = *reinterpret_cast<const u32x4_t*>(wrow[0]);
-    rw1 = *reinterpret_cast<const u32x4_t*>(wrow[1]);
-  }
+  // the loads of the step at element ko; pieces past K are zeros
+  auto load_step = [&](int ko) {
+    const bool aok = ko + pc < K;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      ra[i] = aok ? *reinterpret_cast<const u32x4_t*>(arow[i] + ko) : z4;
+    if (FP4) {
+      const bool cok = ko + 32 * half < K;
+      rc = cok ? *reinterpret_cast<const u32x4_t*>(crow + ko / 2) : z4;
+      rs = cok ? srow[ko / 32] : 127u;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        rw[i] = aok ? *reinterpret_cast<const u32x4_t*>(wrow[i] + ko) : z4;
+    }
+  };
+  load_step(0);
   f32x16_t acc[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -191,41 +205,33 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
 
-  const int nk = K / kGK;
+  const int nk = (K + kGK - 1) / kGK;
   // registers -> LDS buffer `buf`
 #define GEMM_STAGE(buf)                                                                 \
   do {                                                                                  \
-    *reinterpret_cast<u32x4_t*>(&As[buf][(tid >> 2) * kGS + (tid & 3) * 8]) = ra0;      \
-    *reinterpret_cast<u32x4_t*>(&As[buf][((tid + 256) >> 2) * kGS + (tid & 3) * 8]) = ra1; \
+    for (int i = 0; i < 4; ++i)                                                         \
+      *reinterpret_cast<u32x4_t*>(&As[buf][((tid + 256 * i) >> 3) * kGS + pc]) = ra[i]; \
     if (FP4) {                                                                          \
       u32x4_t lo, hi;                                                                   \
-      fp4x16_to_bf16(rc, rs, lo, hi);                                                   \
-      uint16_t* d = &Ws[buf][(tid >> 1) * kGS + (tid & 1) * 16];                        \
+      uint16_t* d = &Ws[buf][(tid >> 1) * kGS + half * 32];                             \
+      fp4x16_to_bf16(u32x2_t{rc.x, rc.y}, rs, lo, hi);                                  \
       *reinterpret_cast<u32x4_t*>(d) = lo;                                              \
       *reinterpret_cast<u32x4_t*>(d + 8) = hi;                                          \
+      fp4x16_to_bf16(u32x2_t{rc.z, rc.w}, rs, lo, hi);                                  \
+      *reinterpret_cast<u32x4_t*>(d + 16) = lo;                                         \
+      *reinterpret_cast<u32x4_t*>(d + 24) = hi;                                         \
     } else {                                                                            \
-      *reinterpret_cast<u32x4_t*>(&Ws[buf][(tid >> 2) * kGS + (tid & 3) * 8]) = rw0;    \
-      *reinterpret_cast<u32x4_t*>(&Ws[buf][((tid + 256) >> 2) * kGS + (tid & 3) * 8]) = rw1; \
+      for (int i = 0; i < 4; ++i)                                                       \
+        *reinterpret_cast<u32x4_t*>(&Ws[buf][((tid + 256 * i) >> 3) * kGS + pc]) = rw[i]; \
     }                                                                                   \
   } while (0)
   GEMM_STAGE(0);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) {  // next step's loads go out before this step's math
-      const int ko = (kt + 1) * kGK;
-      ra0 = *reinterpret_cast<const u32x4_t*>(arow[0] + ko);
-      ra1 = *reinterpret_cast<const u32x4_t*>(arow[1] + ko);
-      if (FP4) {
-        rc = *reinterpret_cast<const u32x2_t*>(crow + ko / 2);
-        rs = srow[kt + 1];
-      } else {
-        rw0 = *reinterpret_cast<const u32x4_t*>(wrow[0] + ko);
-        rw1 = *reinterpret_cast<const u32x4_t*>(wrow[1] + ko);
-      }
-    }
+    if (kt + 1 < nk) load_step((kt + 1) * kGK);  // next step's loads before this step's math
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < kGK / 16; ++ks) {
       bf16x8_t af[2], bf[2];
 #pragma unroll
       for (int im = 0; im < 2; ++im)

@@ -29,8 +29,9 @@ def say(*a):
     sys.stdout.flush()
 
 
+# (67, 48, 96): K not a multiple of the 64-deep K step (zero-filled tail)
 @pytest.mark.parametrize("M,N,K", [(2047, 5120, 2880), (300, 2880, 4096), (5, 32, 2880),
-                                   (129, 200, 64)])
+                                   (129, 200, 64), (67, 48, 96)])
 def test_gemm_bf16(orc, M, N, K):
     A = orc.fill_bf16(0, 31, M * K, 0.0, 1.0)
     W = orc.fill_bf16(0, 32, N * K, 0.0, 0.02)
@@ -82,7 +83,9 @@ def moe_weights(orc, E, H, I, seed):
     )
 
 
-@pytest.mark.parametrize("M,E,H,I,k", [(300, 32, 2880, 2880, 4), (37, 8, 256, 512, 2)])
+# (29, 8, 288, 352, 2): H and I not multiples of the 64-deep K step
+@pytest.mark.parametrize("M,E,H,I,k", [(300, 32, 2880, 2880, 4), (37, 8, 256, 512, 2),
+                                       (29, 8, 288, 352, 2)])
 def test_moe_prefill_vs_oracle(orc, M, E, H, I, k):
     """Rows grouped by expert into MXFP4 matrix-core GEMMs vs the canonical
     per-row MoE (experts and weights from the oracle's router)."""
