@@ -299,18 +299,23 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
 // Expert rows, 16 of an expert's rows per block (its pair list split into
 // groups of 16; the groups of one expert are neighbouring blocks, so the
 // later ones find the weights in cache).  A block of 4 waves
-// owns 256 rows of one expert (64 per wave in 4 tiles of 16) and each wave
-// runs the whole K, so nothing is reduced across waves.  The expert's
+// owns 64 kMxMoeTiles rows of one expert (16 kMxMoeTiles per wave) and each
+// wave runs the whole K, so nothing is reduced across waves.  The expert's
 // activation rows go through LDS 512 elements (16 units) at a time, double
-// buffered, and serve all 256 rows; the next chunk's weights are loaded into
+// buffered, and serve all of its rows; the next chunk's weights are loaded into
 // registers while the current one is used.  Per half-iteration the order is:
 // activation loads (c + 1), weight loads (c + 1), barrier, MFMAs on chunk c,
 // activation rows (c + 1) into LDS -- loads complete in issue order, so the
 // LDS writes never wait for the weight stream.  Lane group g takes units
 // 16 c + 4 g + s (s = 0..3) of chunk c: 64 contiguous code bytes per lane.
+// weight tiles of 16 rows per wave (2: 160-odd VGPRs, 3 waves per SIMD, so a
+// 20b-shape launch at 16 rows fits the CUs in one round) and rows per block
+constexpr int kMxMoeTiles = 2, kMxMoeRows = 64 * kMxMoeTiles;
+
 template <int MODE, bool PACKED>
 __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   constexpr int CKU = 16, CK = 32 * CKU, XS = CK + 8;
+  constexpr int TT = kMxMoeTiles;  // weight tiles of 16 rows per wave
   __shared__ __align__(16) uint16_t xs[2][16][XS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
@@ -326,7 +331,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   if (16 * grp >= Rall) return;  // (uniform)
   const int R = min(16, Rall - 16 * grp);
   const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
-  const int nw0 = blockIdx.x * 256 + 64 * w;  // the wave's first row
+  const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;  // the wave's first row
   const bool wave_on = nw0 < N;               // uniform per wave
   const int nch = (U + CKU - 1) / CKU;
   // staging: thread tid copies 8-element pieces (tid & 15) + 16 q of row tid >> 4
@@ -349,13 +354,13 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
     for (int q = 0; q < 4; ++q)
       *reinterpret_cast<uint4*>(&xs[buf][sr][8 * (sp + 16 * q)]) = xv[q];
   };
-  auto w_load = [&](int c, uint4 (&wv)[4][4], float (&sv)[4][4]) {
+  auto w_load = [&](int c, uint4 (&wv)[TT][4], float (&sv)[TT][4]) {
     if (!wave_on) return;
     if constexpr (PACKED) {
       // [E][N/16][nch][su][g][j] pieces of 16 code bytes (scales: one byte each)
       const uint8_t* Pc = static_cast<const uint8_t*>(a.Wp);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < TT; ++tt) {
         const size_t et = (size_t)e * (N / 16) + nw0 / 16 + tt;
 #pragma unroll
         for (int su = 0; su < 4; ++su) {
@@ -367,7 +372,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
       return;
     }
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
+    for (int tt = 0; tt < TT; ++tt) {
       const size_t row = (size_t)e * N + nw0 + 16 * tt + j;
 #pragma unroll
       for (int su = 0; su < 4; ++su) {
@@ -378,10 +383,10 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
       }
     }
   };
-  mx_f32x4 acc[4];
+  mx_f32x4 acc[TT];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) acc[tt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  auto compute = [&](int c, int buf, const uint4 (&wv)[4][4], const float (&sv)[4][4]) {
+  for (int tt = 0; tt < TT; ++tt) acc[tt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int c, int buf, const uint4 (&wv)[TT][4], const float (&sv)[TT][4]) {
 #pragma unroll
     for (int su = 0; su < 4; ++su) {
       const int ur = CKU * c + 4 * g + su;
@@ -393,7 +398,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
         af[t] = uv ? v : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < TT; ++tt) {
         const uint4 cw = wv[tt][su];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -404,8 +409,8 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
       }
     }
   };
-  uint4 wA[4][4], wB[4][4];
-  float sA[4][4], sB[4][4];
+  uint4 wA[TT][4], wB[TT][4];
+  float sA[TT][4], sB[TT][4];
   uint4 xv[4];
   x_load(0, xv);
   w_load(0, wA, sA);
@@ -428,7 +433,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   }
   if (!wave_on) return;
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < TT; ++tt) {
     const int n = nw0 + 16 * tt + j;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -696,14 +701,14 @@ void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score
                      gate_up.E, S, const_cast<int32_t*>(gate_up.route));
   const int G = (gate_up.B + 15) / 16;
   if (gate_up.Wp && down.Wp) {
-    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + 255) / 256, S * G),
+    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
                        dim3(256), 0, st, gate_up);
-    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + 255) / 256, S * G),
+    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
                        dim3(256), 0, st, down);
   } else if (gate_up.B <= 16) {
-    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, false>), dim3((gate_up.N + 255) / 256, S),
+    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, false>), dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S),
                        dim3(256), 0, st, gate_up);
-    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, false>), dim3((down.N + 255) / 256, S), dim3(256),
+    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, false>), dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S), dim3(256),
                        0, st, down);
   } else {
     mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 64, S), st);
