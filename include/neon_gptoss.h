@@ -162,7 +162,10 @@ neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
 neon_status neon_seq_len(const neon_ctx* ctx, int* out);
 
 /* Device pointer of a weight tensor (same names as neon_load_tensor), for
- * tests and tools; *bytes receives its size. */
+ * tests and tools; *bytes receives its size.  Read it freely; bytes written
+ * through it bypass neon_load_tensor's checks, and the NEON_DECODE_MATRIX
+ * steps keep reading their packed copy until the next neon_load_tensor or
+ * neon_init_random. */
 neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name, void** ptr,
                             size_t* bytes);
 
