@@ -169,6 +169,49 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
   return __fmul_rn(__fadd_rn(u, 1.0f), __fmul_rn(g, sig));
 }
 
+// Pairs of every used expert for the matrix-core expert kernels, from the
+// experts ids[0 .. nk) of the pairs q = b k + s (nk <= 256, E <= 256):
+// route[y] = the y-th used expert (ascending id; -1 past the last),
+// route[S + y] = its pair count, route[2 S + 64 y + r] = its r-th pair in
+// ascending q.  Every thread of the block calls it (threads 0 .. 255 work);
+// cnt_e / slot_of hold 256 ints, wave_used 4, all in LDS.  Slots come from a
+// lane-parallel ballot prefix over the 256 expert flags.
+__device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E, int S,
+                                               int32_t* __restrict__ route, int* cnt_e,
+                                               int* slot_of, int* wave_used) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t < 256) cnt_e[t] = 0;
+  __syncthreads();
+  const int e = t < nk ? ids[t] : -1;
+  if (e >= 0) atomicAdd(&cnt_e[e], 1);
+  __syncthreads();
+  const int c = (t < 256 && t < E) ? cnt_e[t] : 0;
+  const unsigned long long bal = __ballot(c > 0);
+  if (t < 256 && lane == 0) wave_used[w] = __popcll(bal);
+  __syncthreads();
+  if (t < 256) {
+    const int before = (w > 0 ? wave_used[0] : 0) + (w > 1 ? wave_used[1] : 0) +
+                       (w > 2 ? wave_used[2] : 0);
+    const int slot = before + __popcll(bal & ((1ull << lane) - 1ull));
+    const int n_used = wave_used[0] + wave_used[1] + wave_used[2] + wave_used[3];
+    if (c > 0) {
+      slot_of[t] = slot;
+      route[slot] = t;
+      route[S + slot] = c;
+    }
+    if (t >= n_used && t < S) {
+      route[t] = -1;
+      route[S + t] = 0;
+    }
+  }
+  __syncthreads();
+  if (e >= 0) {
+    int r = 0;
+    for (int q = 0; q < t; ++q) r += ids[q] == e;
+    route[2 * S + 64 * slot_of[e] + r] = t;
+  }
+}
+
 // A load that stays where it is written.  The compiler sinks a plain load
 // whose only use sits in a branch (a lane-0 epilogue) into that branch, where
 // it issues last and is waited for alone; a relaxed atomic load is never

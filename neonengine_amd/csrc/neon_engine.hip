@@ -715,9 +715,11 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
-    r.idx = ctx->moe_idx; r.score = ctx->moe_score;
+    r.idx = nullptr; r.score = nullptr;  // the top-k runs with the route lists
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
     launch_router(r, st);
+    launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
+                      ctx->mx_route, st);
     MxArgs gu{};
     gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.Wp = mp.gu_c; gu.sp = mp.gu_s;
     gu.bias = w.gu_bias; gu.x = ctx->xn;
@@ -730,7 +732,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k;
-    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
+    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, true, st);
   }
   launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
   MxArgs lm{};

@@ -1493,6 +1493,36 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
   if (lane < k) { idx[b * k + lane] = t.id[lane]; score[b * k + lane] = t.sc[lane]; }
 }
 
+// Top-k of every row (k_topk's ranking) and the matrix-core experts' route
+// lists (mx_route_lists) in one launch: wave w of 16 ranks rows w, w + 16, ...
+__global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ lg, int B, int E,
+                                                     int k, int32_t* __restrict__ idx,
+                                                     float* __restrict__ score, int S,
+                                                     int32_t* __restrict__ route) {
+  __shared__ TopK t[16];
+  __shared__ int32_t pair_e[256];
+  __shared__ int cnt_e[256], slot_of[256], wave_used[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int b = w; b < B; b += 16) {
+    wave_topk<true>(lg + (size_t)b * E, E, k, lane, t[w]);
+    if (lane < k) {
+      const int32_t id = t[w].id[lane];
+      idx[b * k + lane] = id;
+      score[b * k + lane] = t[w].sc[lane];
+      pair_e[b * k + lane] = id;
+    }
+  }
+  __syncthreads();
+  mx_route_lists(pair_e, B * k, E, S, route, cnt_e, slot_of, wave_used);
+}
+
+void launch_topk_route(const float* lg, int32_t* idx, float* score, int B, int E, int k,
+                       int32_t* route, hipStream_t st) {
+  const int S = B * k < E ? B * k : E;
+  hipLaunchKernelGGL(k_topk_route, dim3(1), dim3(1024), 0, st, lg, B, E, k, idx, score, S,
+                     route);
+}
+
 void launch_topk(const float* lg, int32_t* idx, float* score, int B, int E, int k,
                  hipStream_t st) {
   hipLaunchKernelGGL(k_topk, dim3(B), dim3(64), 0, st, lg, idx, score, E, k);

@@ -64,40 +64,8 @@ __device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
 // S = min(E, B k) block rows of the expert kernels.
 __global__ __launch_bounds__(256) void k_mx_route(const int32_t* __restrict__ idx, int nk,
                                                   int E, int S, int32_t* __restrict__ route) {
-  __shared__ int cnt_e[256];
-  __shared__ int slot_of[256];
-  __shared__ int wave_used[4];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  cnt_e[t] = 0;
-  __syncthreads();
-  const int e = t < nk ? idx[t] : -1;
-  if (e >= 0) atomicAdd(&cnt_e[e], 1);
-  __syncthreads();
-  // slot of expert t = used experts below it: a ballot prefix over the 256
-  // flags, lane-parallel (no serial loop over experts)
-  const int c = t < E ? cnt_e[t] : 0;
-  const unsigned long long bal = __ballot(c > 0);
-  if (lane == 0) wave_used[w] = __popcll(bal);
-  __syncthreads();
-  const int before = (w > 0 ? wave_used[0] : 0) + (w > 1 ? wave_used[1] : 0) +
-                     (w > 2 ? wave_used[2] : 0);
-  const int slot = before + __popcll(bal & ((1ull << lane) - 1ull));
-  const int n_used = wave_used[0] + wave_used[1] + wave_used[2] + wave_used[3];
-  if (c > 0) {
-    slot_of[t] = slot;
-    route[slot] = t;
-    route[S + slot] = c;
-  }
-  if (t >= n_used && t < S) {
-    route[t] = -1;
-    route[S + t] = 0;
-  }
-  __syncthreads();
-  if (e >= 0) {
-    int r = 0;
-    for (int q = 0; q < t; ++q) r += idx[q] == e;
-    route[2 * S + 64 * slot_of[e] + r] = t;
-  }
+  __shared__ int cnt_e[256], slot_of[256], wave_used[4];
+  mx_route_lists(idx, nk, E, S, route, cnt_e, slot_of, wave_used);
 }
 
 // MXFP4 unit of lane group g of wave w in iteration i: a wave takes 8
@@ -695,10 +663,11 @@ void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
 }
 
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
-                   hipStream_t st) {
+                   bool route_ready, hipStream_t st) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
-  hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx, gate_up.B * gate_up.k,
-                     gate_up.E, S, const_cast<int32_t*>(gate_up.route));
+  if (!route_ready)
+    hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx,
+                       gate_up.B * gate_up.k, gate_up.E, S, const_cast<int32_t*>(gate_up.route));
   const int G = (gate_up.B + 15) / 16;
   if (gate_up.Wp && down.Wp) {
     hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
