@@ -113,14 +113,20 @@ def test_small_model_128_experts_matrix():
     within rounding of each other, so the two modes may route a row
     differently; the step's expert ids are read back, and every row routed
     the same way must agree within 2e-2 (at most 4 of 16 may differ)."""
-    torch_cuda()
     cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_layers=1, n_experts=128, max_batch=16))
     say("matrix mode, 128 experts, one layer, 16 rows")
-    prompt = np.random.default_rng(5).integers(0, cfg.vocab, size=(16, 12)).tolist()
+    routed_alike_compare(cfg, 5, 16, 12, 12)
+
+
+def routed_alike_compare(cfg, seed, B, plen, min_same):
+    """First-step logits of both modes for rows whose experts agree (the
+    step's moe_idx is read back); returns (rows alike, worst rel error)."""
+    torch_cuda()
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, size=(B, plen)).tolist()
     got = {}
     for mode in (ne.DECODE_EXACT, ne.DECODE_MATRIX):
         eng = ne.Engine(cfg)
-        eng.init_random(5)
+        eng.init_random(seed)
         eng.set_decode_mode(mode)
         eng.prefill(prompt)
         got[mode] = (eng.read_logits(), eng.read_activation("moe_idx"))
@@ -128,9 +134,18 @@ def test_small_model_128_experts_matrix():
     (lg_e, id_e), (lg_m, id_m) = got[ne.DECODE_EXACT], got[ne.DECODE_MATRIX]
     same = (np.sort(id_e, axis=1) == np.sort(id_m, axis=1)).all(axis=1)
     rel = np.abs(lg_m - lg_e).max(axis=1) / np.abs(lg_e).max(axis=1)
-    say(f"  rows routed alike {same.sum()}/16; worst rel error among them {rel[same].max():.3e}")
-    assert same.sum() >= 12
+    say(f"  rows routed alike {same.sum()}/{B}; worst rel error among them {rel[same].max():.3e}")
+    assert same.sum() >= min_same
     assert (rel[same] < 2e-2).all()
+
+
+def test_gpt_oss_120b_width_matrix_one_layer():
+    """The 120b shape's width (128 experts, 2880 hidden, vocab 201088), one
+    layer, 16 rows: the matrix-core step against the exact one, row by row
+    wherever the routing agrees."""
+    cfg = ne.config_preset("gpt-oss-120b", n_layers=1, max_seq=64, max_batch=16)
+    say("matrix mode, 120b width, one layer, 16 rows")
+    routed_alike_compare(cfg, 8, 16, 10, 12)
 
 
 def test_gpt_oss_20b_width_matrix_steps():
