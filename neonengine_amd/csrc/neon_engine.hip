@@ -732,7 +732,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k;
-    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, true, st);
+    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
   }
   launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
   MxArgs lm{};

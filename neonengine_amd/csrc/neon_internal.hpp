@@ -163,9 +163,10 @@ void launch_mx_pack_fp4(const uint8_t* codes, const uint8_t* scales, int E, int 
 void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);
 // experts of B rows: gate_up + SwiGLU into act, down + bias per pair, then the
 // slot-ordered combine h = bf16(h + bf16(sum_s score_s (dot_s + bias_s)))
-// (route_ready: the lists were built by launch_topk_route)
+// (the route lists come from launch_topk_route; the weights from the packed
+// copies in Wp / sp)
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
-                   bool route_ready, hipStream_t st);
+                   hipStream_t st);
 // top-k of B rows of router logits and the route lists of their pairs
 // (B k <= 256, E <= 256) in one launch
 void launch_topk_route(const float* lg, int32_t* idx, float* score, int B, int E, int k,

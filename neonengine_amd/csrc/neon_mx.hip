@@ -4,15 +4,17 @@
 // order of the batch-1 kernels, which makes them VALU-bound from B = 16 on.
 // Here each weight row is read once per step and the B rows ride in the M
 // dimension of v_mfma_f32_16x16x32_bf16 (fp32 accumulate):
-//   - a block owns 16 weight rows (64 for MXFP4 expert rows, 4 tiles per
-//     wave); its 4 waves split K, and each load instruction reads 64
-//     contiguous bytes of each of its 16 rows (the element orders are at
-//     k_mx_gemv);
-//   - bf16 rows feed the B operand as loaded; MXFP4 expert rows go through
-//     v_cvt_scalef32_pk_bf16_fp4 (E2M1 x 2^(s-127) is a bf16 value, so the
-//     dequantisation is exact);
-//   - the expert kernels find their expert and its (token, slot) pairs
-//     themselves: block y serves the y-th used expert in ascending id.
+//   - projections and lm_head (k_mx_gemv): a block owns 16 weight rows and
+//     its 4 waves split K;
+//   - experts (k_mx_moe16): a block owns 64 kMxMoeTiles rows of one used
+//     expert for up to 16 of its (row, slot) pairs, whose activation rows it
+//     stages in LDS; the used experts and their pairs come from
+//     k_topk_route; MXFP4 rows go through v_cvt_scalef32_pk_bf16_fp4 (E2M1 x
+//     2^(s-127) is a bf16 value, so the dequantisation is exact);
+//   - the weights come from copies packed in MFMA lane order (k_mx_pack_*),
+//     so that a load instruction reads 1 KB contiguous;
+//   - attention (k_mx_attn): K Q^T and V^T P^T with a kv head's query heads
+//     as the query columns.
 // Only the order of fp32 additions differs from the exact path (products
 // of two bf16 values are exact in fp32), and every rounding point, bias,
 // SwiGLU clamp and the slot-ordered combine are the exact path's
@@ -58,67 +60,24 @@ __device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
 
-// Pairs of every used expert, once per layer: route[y] = the y-th used expert
-// (ascending id; -1 past the last), route[S + y] = its pair count, and
-// route[2 S + 64 y + r] its r-th pair q = b k + s in ascending q, for the
-// S = min(E, B k) block rows of the expert kernels.
-__global__ __launch_bounds__(256) void k_mx_route(const int32_t* __restrict__ idx, int nk,
-                                                  int E, int S, int32_t* __restrict__ route) {
-  __shared__ int cnt_e[256], slot_of[256], wave_used[4];
-  mx_route_lists(idx, nk, E, S, route, cnt_e, slot_of, wave_used);
-}
-
-// MXFP4 unit of lane group g of wave w in iteration i: a wave takes 8
-// consecutive units (128 code bytes of each row, one cache line) in two
-// successive iterations, the 4 waves 32 units per iteration pair.
-__device__ __forceinline__ int mx_unit(int it, int w, int g) {
-  return 32 * (it >> 1) + 8 * w + 4 * (it & 1) + g;
-}
-
-// One block: weight rows n0 .. n0 + 16 TT - 1 (of one expert in the expert
-// modes) for all R rows; its 4 waves split K.  BT = row tiles of 16
-// (R <= 16 BT); IT = K iterations per wave (K <= 512 IT); TT = weight tiles
-// of 16 rows per wave (4 for MXFP4 rows, whose B operand is a quarter of the
-// A operand's bytes, so that each activation fragment feeds 4 MFMAs).
-// Element order: a bf16 lane (j, g) reads elements 128 (4 i + w) + 32 t + 8 g
-// in step t of iteration i, so one load instruction covers 64 contiguous
-// bytes of each of its 16 rows; an MXFP4 lane group g reads unit
-// u = mx_unit(i, w, g) (16 code bytes, one scale) and feeds its elements
-// 32 u + 8 t in step t.
+// Projections and lm_head: a block owns weight rows n0 .. n0 + 15 for all B
+// rows, and its 4 waves split K.  BT = row tiles of 16 (B <= 16 BT); IT = K
+// iterations per wave (K <= 512 IT).  Lane (j, g) reads elements
+// 128 (4 i + w) + 32 t + 8 g .. + 7 of its row in step t of iteration i: one
+// load instruction covers 64 contiguous bytes of each of 16 rows in the
+// checkpoint layout, or 1 KB contiguous in the packed copy (PACKED).
 template <int BT, int IT, int MODE, bool PACKED>
 __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
-  constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
-  constexpr int TT = MOE ? 4 : 1;
-  __shared__ mx_f32x4 red[3][TT][BT][64];
+  __shared__ mx_f32x4 red[3][BT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
-  const int N = a.N, K = a.K, U = K / 32;
-  const int n0 = blockIdx.x * 16 * TT;
-  int R = a.B, e = 0;
-  const int32_t* rows = nullptr;
-  if constexpr (MOE) {
-    const int S = gridDim.y;
-    e = a.route[blockIdx.y];
-    if (e < 0) return;  // fewer used experts than block rows (uniform)
-    R = a.route[S + blockIdx.y];
-    rows = a.route + 2 * S + 64 * blockIdx.y;
-  }
+  const int N = a.N, K = a.K, R = a.B;
+  const int n0 = blockIdx.x * 16;
   // weight loads first (the stream), then the activation rows
-  uint4 wq[IT][MOE ? TT : 4];
-  float wsc[MOE ? IT : 1][TT];
+  uint4 wq[IT][4];
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    if constexpr (MOE) {
-      const int ur = mx_unit(it, w, g);
-      const int u = ur < U ? ur : U - 1;
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        const size_t row = (size_t)e * N + n0 + 16 * tt + j;
-        wq[it][tt] = mx_load_nt(static_cast<const uint8_t*>(a.W) + row * (K / 2) + (size_t)u * 16);
-        const uint32_t sb = a.scales[row * U + u];  // cached: a line serves 4 iterations
-        wsc[it][tt] = __builtin_amdgcn_ldexpf(1.0f, (int)sb - 127);
-      }
-    } else if constexpr (PACKED) {
+    if constexpr (PACKED) {
       // [N/16][NCH][t][g][j][8]: lane l = j + 16 g reads piece ... * 64 + l
       const int NCH = (K + 127) / 128;
       const int ch = min(4 * it + w, NCH - 1);
@@ -142,145 +101,86 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   for (int bt = 0; bt < BT; ++bt) {
     const int r = 16 * bt + j;
     rv[bt] = r < R;
-    const int rc = rv[bt] ? r : R - 1;
-    int xr = rc;
-    if constexpr (MODE == MX_GATE_UP) xr = rows[rc] / a.k;
-    if constexpr (MODE == MX_DOWN) xr = rows[rc];
-    xrow[bt] = a.x + (size_t)xr * K;
+    xrow[bt] = a.x + (size_t)(rv[bt] ? r : R - 1) * K;
   }
-  mx_f32x4 acc[TT][BT];
+  mx_f32x4 acc[BT];
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-    for (int bt = 0; bt < BT; ++bt) acc[tt][bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    int xel[4];
-    bool xok[4];
-    if constexpr (MOE) {
-      const int ur = mx_unit(it, w, g);
-      const int u = ur < U ? ur : U - 1;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) { xel[t] = 32 * u + 8 * t; xok[t] = ur < U; }
-    } else {
-      const int base = 128 * (4 * it + w);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        xok[t] = base + 32 * t < K;
-        xel[t] = xok[t] ? base + 32 * t + 8 * g : 8 * g;
-      }
-    }
+    const int base = 128 * (4 * it + w);
     uint4 xq[BT][4];
 #pragma unroll
-    for (int bt = 0; bt < BT; ++bt)
+    for (int t = 0; t < 4; ++t) {
+      const bool ok = base + 32 * t < K;
+      const int el = ok ? base + 32 * t + 8 * g : 8 * g;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + xel[t]);
+      for (int bt = 0; bt < BT; ++bt) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + el);
         // a zero A value drops a padded element range or row
-        xq[bt][t] = (xok[t] && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);
+        xq[bt][t] = (ok && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);
       }
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
+      const mx_bf16x8 bw = mx_as_bf16x8(wq[it][t]);
 #pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        mx_bf16x8 bw;
-        if constexpr (MOE) {
-          const uint4 c = wq[it][tt];
-          const uint32_t cw = t == 0 ? c.x : t == 1 ? c.y : t == 2 ? c.z : c.w;
-          bw = mx_fp4x8(cw, wsc[it][tt]);
-        } else {
-          bw = mx_as_bf16x8(wq[it][t]);
-        }
-#pragma unroll
-        for (int bt = 0; bt < BT; ++bt)
-          if (16 * bt < R)
-            acc[tt][bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw,
-                                                                  acc[tt][bt], 0, 0, 0);
-      }
+      for (int bt = 0; bt < BT; ++bt)
+        if (16 * bt < R)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw, acc[bt],
+                                                            0, 0, 0);
     }
   }
   // waves 1..3 hand their partial sums to wave 0, which adds them in order
   if (w > 0) {
 #pragma unroll
-    for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-      for (int bt = 0; bt < BT; ++bt) red[w - 1][tt][bt][lane] = acc[tt][bt];
+    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
   }
   __syncthreads();
   if (w != 0) return;
+  const int n = n0 + j;
 #pragma unroll
-  for (int tt = 0; tt < TT; ++tt) {
-    const int n = n0 + 16 * tt + j;
+  for (int bt = 0; bt < BT; ++bt) {
+    if (16 * bt >= R) break;
+    mx_f32x4 tot = acc[bt];
 #pragma unroll
-    for (int bt = 0; bt < BT; ++bt) {
-      if (16 * bt >= R) break;
-      mx_f32x4 tot = acc[tt][bt];
+    for (int v = 0; v < 3; ++v) {
+      const mx_f32x4 p = red[v][bt][lane];
+      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
+      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+    }
 #pragma unroll
-      for (int v = 0; v < 3; ++v) {
-        const mx_f32x4 p = red[v][tt][bt][lane];
-        tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
-        tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ri = 16 * bt + 4 * g + r;  // row of A / output row
-        const bool ok = ri < R;
-        const float d = tot[r];
-        if constexpr (MODE == MX_STORE || MODE == MX_RESID) {
-          if (ok) {
-            const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
-            const size_t o = (size_t)ri * N + n;
-            if (MODE == MX_STORE) a.y[o] = f2bf(v);
-            else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
-          }
-        } else if constexpr (MODE == MX_LOGITS) {
-          if (ok) a.out_f[(size_t)ri * N + n] = d;
-          float bv = ok ? d : -INFINITY;
-          int bi = n;
-          mx_argmax_step(bv, bi, 1);
-          mx_argmax_step(bv, bi, 2);
-          mx_argmax_step(bv, bi, 4);
-          mx_argmax_step(bv, bi, 8);
-          if (ok && j == 0) {
-            a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
-            a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
-          }
-        } else if constexpr (MODE == MX_GATE_UP) {
-          // rows 2c (gate) and 2c+1 (up) sit in lanes j and j ^ 1
-          const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
-          const float other = __shfl_xor(v, 1);
-          if (ok && (j & 1) == 0) {
-            const int q = rows[ri];
-            a.y[(size_t)q * (N / 2) + n / 2] = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
-          }
-        } else {  // MX_DOWN: dot + bias per pair, combined later in slot order
-          if (ok) {
-            const int q = rows[ri];
-            a.out_f[(size_t)q * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
-          }
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 16 * bt + 4 * g + r;  // row of A / output row
+      const bool ok = ri < R;
+      const float d = tot[r];
+      if constexpr (MODE == MX_LOGITS) {
+        if (ok) a.out_f[(size_t)ri * N + n] = d;
+        float bv = ok ? d : -INFINITY;
+        int bi = n;
+        mx_argmax_step(bv, bi, 1);
+        mx_argmax_step(bv, bi, 2);
+        mx_argmax_step(bv, bi, 4);
+        mx_argmax_step(bv, bi, 8);
+        if (ok && j == 0) {
+          a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
+          a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
         }
+      } else if (ok) {
+        const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
+        const size_t o = (size_t)ri * N + n;
+        if (MODE == MX_STORE) a.y[o] = f2bf(v);
+        else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
       }
     }
   }
 }
 
-// Expert rows, 16 of an expert's rows per block (its pair list split into
-// groups of 16; the groups of one expert are neighbouring blocks, so the
-// later ones find the weights in cache).  A block of 4 waves
-// owns 64 kMxMoeTiles rows of one expert (16 kMxMoeTiles per wave) and each
-// wave runs the whole K, so nothing is reduced across waves.  The expert's
-// activation rows go through LDS 512 elements (16 units) at a time, double
-// buffered, and serve all of its rows; the next chunk's weights are loaded into
-// registers while the current one is used.  Per half-iteration the order is:
-// activation loads (c + 1), weight loads (c + 1), barrier, MFMAs on chunk c,
-// activation rows (c + 1) into LDS -- loads complete in issue order, so the
-// LDS writes never wait for the weight stream.  Lane group g takes units
-// 16 c + 4 g + s (s = 0..3) of chunk c: 64 contiguous code bytes per lane.
 // weight tiles of 16 rows per wave (2: 160-odd VGPRs, 3 waves per SIMD, so a
 // 20b-shape launch at 16 rows fits the CUs in one round) and rows per block
 constexpr int kMxMoeTiles = 2, kMxMoeRows = 64 * kMxMoeTiles;
 
-template <int MODE, bool PACKED>
+template <int MODE>
 __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   constexpr int CKU = 16, CK = 32 * CKU, XS = CK + 8;
   constexpr int TT = kMxMoeTiles;  // weight tiles of 16 rows per wave
@@ -308,7 +208,6 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   int xr = 0;
   if (s_ok) xr = MODE == MX_GATE_UP ? rows[sr] / a.k : rows[sr];
   const uint16_t* xsrc = a.x + (size_t)xr * K;
-  const uint8_t* codes = static_cast<const uint8_t*>(a.W);
   auto x_load = [&](int c, uint4 (&xv)[4]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -322,32 +221,19 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
     for (int q = 0; q < 4; ++q)
       *reinterpret_cast<uint4*>(&xs[buf][sr][8 * (sp + 16 * q)]) = xv[q];
   };
+  // packed codes [E][N/16][nch][su][g][j] pieces of 16 bytes (scales: one
+  // byte each): lane l = j + 16 g reads piece ... * 64 + l
+  const uint8_t* Pc = static_cast<const uint8_t*>(a.Wp);
   auto w_load = [&](int c, uint4 (&wv)[TT][4], float (&sv)[TT][4]) {
     if (!wave_on) return;
-    if constexpr (PACKED) {
-      // [E][N/16][nch][su][g][j] pieces of 16 code bytes (scales: one byte each)
-      const uint8_t* Pc = static_cast<const uint8_t*>(a.Wp);
-#pragma unroll
-      for (int tt = 0; tt < TT; ++tt) {
-        const size_t et = (size_t)e * (N / 16) + nw0 / 16 + tt;
-#pragma unroll
-        for (int su = 0; su < 4; ++su) {
-          const size_t piece = ((et * nch + c) * 4 + su) * 64 + lane;
-          wv[tt][su] = mx_load_nt(Pc + piece * 16);
-          sv[tt][su] = __builtin_amdgcn_ldexpf(1.0f, (int)a.sp[piece] - 127);
-        }
-      }
-      return;
-    }
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
-      const size_t row = (size_t)e * N + nw0 + 16 * tt + j;
+      const size_t et = (size_t)e * (N / 16) + nw0 / 16 + tt;
 #pragma unroll
       for (int su = 0; su < 4; ++su) {
-        const int ur = CKU * c + 4 * g + su;
-        const int u = ur < U ? ur : U - 1;
-        wv[tt][su] = mx_load_nt(codes + row * (K / 2) + (size_t)u * 16);
-        sv[tt][su] = __builtin_amdgcn_ldexpf(1.0f, (int)a.scales[row * U + u] - 127);
+        const size_t piece = ((et * nch + c) * 4 + su) * 64 + lane;
+        wv[tt][su] = mx_load_nt(Pc + piece * 16);
+        sv[tt][su] = __builtin_amdgcn_ldexpf(1.0f, (int)a.sp[piece] - 127);
       }
     }
   };
@@ -636,12 +522,10 @@ static void mx_launch_pk(const MxArgs& a, dim3 grid, hipStream_t st) {
   }
 }
 
-// the expert modes read the checkpoint layout; the dense modes the packed
-// copy when there is one
+// the packed copy when there is one, else the checkpoint layout
 template <int MODE>
 static void mx_launch(const MxArgs& a, dim3 grid, hipStream_t st) {
-  constexpr bool MOE = MODE == MX_GATE_UP || MODE == MX_DOWN;
-  if (!MOE && a.Wp) mx_launch_pk<MODE, !MOE>(a, grid, st);
+  if (a.Wp) mx_launch_pk<MODE, true>(a, grid, st);
   else mx_launch_pk<MODE, false>(a, grid, st);
 }
 
@@ -663,26 +547,14 @@ void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
 }
 
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
-                   bool route_ready, hipStream_t st) {
+                   hipStream_t st) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
-  if (!route_ready)
-    hipLaunchKernelGGL(k_mx_route, dim3(1), dim3(256), 0, st, gate_up.idx,
-                       gate_up.B * gate_up.k, gate_up.E, S, const_cast<int32_t*>(gate_up.route));
   const int G = (gate_up.B + 15) / 16;
-  if (gate_up.Wp && down.Wp) {
-    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, true>), dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
-                       dim3(256), 0, st, gate_up);
-    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, true>), dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
-                       dim3(256), 0, st, down);
-  } else if (gate_up.B <= 16) {
-    hipLaunchKernelGGL((k_mx_moe16<MX_GATE_UP, false>), dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S),
-                       dim3(256), 0, st, gate_up);
-    hipLaunchKernelGGL((k_mx_moe16<MX_DOWN, false>), dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S), dim3(256),
-                       0, st, down);
-  } else {
-    mx_launch<MX_GATE_UP>(gate_up, dim3(gate_up.N / 64, S), st);
-    mx_launch<MX_DOWN>(down, dim3(down.N / 64, S), st);
-  }
+  hipLaunchKernelGGL(k_mx_moe16<MX_GATE_UP>,
+                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G), dim3(256), 0, st,
+                     gate_up);
+  hipLaunchKernelGGL(k_mx_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
+                     dim3(256), 0, st, down);
   hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
                      down.out_f, score, h, down.N, down.k);
 }
