@@ -176,9 +176,11 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   }
 }
 
-// weight tiles of 16 rows per wave (2: 160-odd VGPRs, 3 waves per SIMD, so a
-// 20b-shape launch at 16 rows fits the CUs in one round) and rows per block
-constexpr int kMxMoeTiles = 2, kMxMoeRows = 64 * kMxMoeTiles;
+// weight tiles of 16 rows per wave and rows per block.  Measured at the 20b
+// shape (tok/s at B = 16 / 64): 4 tiles (228 VGPRs, 2 waves per SIMD)
+// 3754 / 7924, 2 tiles (146 VGPRs) 4141 / 9400, 1 tile 4206 / 9499 -- more
+// waves in flight beat the activation reuse of wider waves.
+constexpr int kMxMoeTiles = 1, kMxMoeRows = 64 * kMxMoeTiles;
 
 template <int MODE>
 __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
