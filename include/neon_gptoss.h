@@ -171,6 +171,16 @@ neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name, void** ptr,
 
 /* ---- kernel-level API (device pointers; stream-ordered) ------------------ */
 
+/* Synchronises `stream`, then reports (and clears) the status bits that the
+ * kernel-level calls on the current device have set since the last check:
+ * NEON_EINVAL when an expert id given in device memory (neon_moe_experts,
+ * neon_moe_prefill) lay outside [0, E).  Such a slot is dropped (adds 0)
+ * instead of reading past the expert arrays.  The context-level reads
+ * (neon_read_tokens / _logits / _activation) make the same check for the
+ * context's own kernels.  (The reference has no counterpart: its Systems
+ * throw on the host and do no device-side validation.) */
+neon_status neon_device_check(void* stream);
+
 /* out[32 b + j] = E2M1(code) * 2^(scale_b - 127) in fp32, bit-exact;
  * scale 0xFF gives NaN. */
 neon_status neon_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
@@ -227,7 +237,8 @@ neon_status neon_moe_layer(const uint16_t* x, const uint16_t* router_w,
 /* Grouped expert FFN alone (HF GptOssExperts): for each row b and slot s,
  * expert e = idx[b][s]: gate_up GEMV -> SwiGLU-clamp -> down GEMV, weighted
  * by score[b][s] and summed over the k slots; out as in neon_moe_layer.
- * act is caller-provided scratch of B*k*I bf16 (no allocation here). */
+ * act is caller-provided scratch of B*k*I bf16 (no allocation here).  An id
+ * outside [0, E) drops its slot; neon_device_check then returns NEON_EINVAL. */
 neon_status neon_moe_experts(const uint16_t* x, const int32_t* idx,
                              const float* score, const uint8_t* gu_codes,
                              const uint8_t* gu_scales, const uint16_t* gu_bias,
@@ -266,7 +277,8 @@ neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
  * idx[t][s] (device int32 in [0, E)) applies gate_up -> SwiGLU-clamp -> down
  * to x[t] (normalised, bf16 [M][H]); h[t] = bf16(h[t] + bf16(sum_s
  * score[t][s] y_ts)) in place.  Rows are grouped by expert into MXFP4
- * matrix-core GEMMs (weights dequantised exactly to bf16). */
+ * matrix-core GEMMs (weights dequantised exactly to bf16).  An id outside
+ * [0, E) drops its slot; neon_device_check then returns NEON_EINVAL. */
 neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
                              const float* score, const uint8_t* gu_codes,
                              const uint8_t* gu_scales, const uint16_t* gu_bias,

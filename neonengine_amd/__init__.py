@@ -33,7 +33,7 @@ EXPORTS = (
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
     "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
-    "neon_gemv_bf16_mfma",
+    "neon_gemv_bf16_mfma", "neon_device_check",
 )
 
 
@@ -109,6 +109,7 @@ def lib():
             "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P],
             "neon_set_decode_mode": [_P, _I],
             "neon_gemv_bf16_mfma": [_P, _P, _P, _P, _I, _I, _I, _P],
+            "neon_device_check": [_P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -124,6 +125,12 @@ def _check(status: int, ctx=None):
     if status != NEON_OK:
         msg = lib().neon_last_error(ctx)
         raise NeonError(status, msg.decode() if msg else "")
+
+
+def device_check(stream=None):
+    """Synchronise and raise NeonError(NEON_EINVAL) if a kernel-level call on
+    the current device saw an expert id outside [0, E) since the last check."""
+    _check(lib().neon_device_check(stream))
 
 
 def config_preset(name: str = "gpt-oss-20b", **overrides) -> Config:

@@ -107,6 +107,11 @@ __device__ __forceinline__ float e8m0_scale(float v, uint32_t s) {
   return s == 0xFFu ? __builtin_nanf("") : r;
 }
 
+// Sets status bits in the caller's status word (a vector-memory atomic).
+__device__ __forceinline__ void flag_dev_err(int32_t* err, int32_t bits) {
+  if (err != nullptr) atomicOr(err, bits);
+}
+
 // RoPE (HFM:149-231) on one (x1, x2) = (dim d, dim d + 32) pair of a head:
 // o1 = x1 c - x2 s, o2 = x2 c + x1 s, each product rounded.
 __device__ __forceinline__ void rope_pair(float x1, float x2, float c, float s,

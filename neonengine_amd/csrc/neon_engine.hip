@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -82,6 +83,7 @@ struct neon_ctx {
   int32_t* lm_part_idx = nullptr;
   int32_t *tokens = nullptr, *pos = nullptr, *prompt_len = nullptr,
           *last_ids = nullptr;
+  int32_t* dev_err = nullptr;  // status word the step's kernels set (kDevErr* bits)
   int tok_stride = 0;
   int lm_nblk = 0;
   int s_full = 1, s_slide = 1;
@@ -394,7 +396,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
-               o_pl = take(Bm * 4), o_last = take(Bm * 4),
+               o_pl = take(Bm * 4), o_last = take(Bm * 4), o_err = take(4),
                o_cos = take((size_t)c.max_seq * half * 4),
                o_sin = take((size_t)c.max_seq * half * 4);
   if (hipMalloc(&ctx->work, off) != hipSuccess) {
@@ -414,6 +416,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
   ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
+  ctx->dev_err = (int32_t*)(W + o_err);
   ctx->sin_t = (float*)(W + o_sin);
   ctx->row_pos = (int32_t*)(W + o_rpos); ctx->row_seq = (int32_t*)(W + o_rseq);
   ctx->sample_scratch = (float*)(W + o_samp);
@@ -669,7 +672,7 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     m.idx_out = grouped ? nullptr : ctx->moe_idx; m.score_out = grouped ? nullptr : ctx->moe_score;
     m.E = c.n_experts; m.xn = ctx->xn; m.act = ctx->act;
     m.residual = ctx->h; m.out = ctx->h; m.B = B; m.H = H; m.I = c.intermediate;
-    m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
+    m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit; m.err = ctx->dev_err;
     if (grouped && moe_batched_supported(m)) launch_moe_batched(m, st);
     else launch_moe(m, st);
   }
@@ -726,12 +729,13 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.route = ctx->mx_route; gu.B = B; gu.N = 2 * I;
     gu.K = H;
     gu.E = c.n_experts; gu.k = c.top_k; gu.alpha = c.swiglu_alpha; gu.limit = c.swiglu_limit;
+    gu.err = ctx->dev_err;
     MxArgs dn{};
     dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.Wp = mp.dn_c; dn.sp = mp.dn_s;
     dn.bias = w.dn_bias; dn.x = ctx->act;
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
     dn.N = H; dn.K = I;
-    dn.E = c.n_experts; dn.k = c.top_k;
+    dn.E = c.n_experts; dn.k = c.top_k; dn.err = ctx->dev_err;
     launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
   }
   launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
@@ -920,7 +924,7 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
     m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit;
     m.list_tok = ctx->pf_ltok; m.list_slot = ctx->pf_lslot; m.e_off = ctx->pf_eoff;
     m.tile_e = ctx->pf_tile_e; m.tile_r0 = ctx->pf_tile_r0; m.n_tiles = ctx->pf_ntiles;
-    m.act = ctx->pf_act; m.ybuf = ctx->pf_ybuf;
+    m.act = ctx->pf_act; m.ybuf = ctx->pf_ybuf; m.err = ctx->dev_err;
     launch_moe_prefill(m, st);
   }
 }
@@ -1108,6 +1112,17 @@ extern "C" neon_status neon_decode(neon_ctx* ctx, int n_steps, void* stream) {
   return NEON_OK;
 }
 
+// After a synchronisation: the status bits the context's kernels set since
+// the last check (read and cleared).
+static neon_status check_dev_err(neon_ctx* ctx) {
+  int32_t bits = 0;
+  HIPCHK(ctx, hipMemcpy(&bits, ctx->dev_err, 4, hipMemcpyDeviceToHost));
+  if (bits == 0) return NEON_OK;
+  HIPCHK(ctx, hipMemset(ctx->dev_err, 0, 4));
+  FAIL(ctx, NEON_EINVAL, "a kernel of this context saw an expert id outside [0, %d) "
+       "(status bits 0x%x); that slot was dropped", ctx->cfg.n_experts, bits);
+}
+
 extern "C" neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
                                         int32_t* out, void* stream) {
   if (!ctx) return NEON_EINVAL;
@@ -1120,7 +1135,7 @@ extern "C" neon_status neon_read_tokens(neon_ctx* ctx, int start, int count,
     HIPCHK(ctx, hipMemcpy(out + (size_t)b * count,
                           ctx->tokens + (size_t)b * ctx->tok_stride + start,
                           (size_t)count * 4, hipMemcpyDeviceToHost));
-  return NEON_OK;
+  return check_dev_err(ctx);
 }
 
 extern "C" neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream) {
@@ -1131,7 +1146,7 @@ extern "C" neon_status neon_read_logits(neon_ctx* ctx, float* out, void* stream)
   HIPCHK(ctx, hipStreamSynchronize(S(stream)));
   HIPCHK(ctx, hipMemcpy(out, ctx->logits, (size_t)ctx->batch * ctx->cfg.vocab * 4,
                         hipMemcpyDeviceToHost));
-  return NEON_OK;
+  return check_dev_err(ctx);
 }
 
 extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
@@ -1156,7 +1171,7 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
   HIPCHK(ctx, hipSetDevice(ctx->device));
   HIPCHK(ctx, hipStreamSynchronize(S(stream)));
   HIPCHK(ctx, hipMemcpy(out, src, n, hipMemcpyDeviceToHost));
-  return NEON_OK;
+  return check_dev_err(ctx);
 }
 
 extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
@@ -1182,6 +1197,38 @@ extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
     if (_e != hipSuccess) KFAIL(NEON_EHIP, "launch failed: %s", hipGetErrorString(_e)); \
     return NEON_OK;                                                         \
   } while (0)
+
+// One status word per device for the kernel-level calls (allocated on a
+// device's first such call, held until the process ends).
+static std::mutex g_status_mu;
+static int32_t* g_status_word[256];
+
+static int32_t* device_status_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return nullptr;
+  std::lock_guard<std::mutex> lk(g_status_mu);
+  if (g_status_word[dev] == nullptr) {
+    int32_t* p = nullptr;
+    if (hipMalloc((void**)&p, 256) != hipSuccess) return nullptr;
+    if (hipMemset(p, 0, 256) != hipSuccess) { (void)hipFree(p); return nullptr; }
+    g_status_word[dev] = p;
+  }
+  return g_status_word[dev];
+}
+
+extern "C" neon_status neon_device_check(void* stream) {
+  int32_t* w = device_status_word();
+  if (w == nullptr) KFAIL(NEON_EHIP, "neon_device_check: no status word on this device");
+  if (hipStreamSynchronize(S(stream)) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_device_check: stream synchronisation failed");
+  int32_t bits = 0;
+  if (hipMemcpy(&bits, w, 4, hipMemcpyDeviceToHost) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_device_check: status read failed");
+  if (bits == 0) return NEON_OK;
+  if (hipMemset(w, 0, 4) != hipSuccess) KFAIL(NEON_EHIP, "neon_device_check: status clear failed");
+  KFAIL(NEON_EINVAL, "a kernel-level call saw an expert id outside [0, E) (status bits 0x%x); "
+        "that slot was dropped", bits);
+}
 
 extern "C" neon_status neon_mxfp4_dequant(const uint8_t* codes,
                                           const uint8_t* scales, int64_t n_blocks,
@@ -1320,6 +1367,7 @@ extern "C" neon_status neon_moe_layer(
   m.router_lg = lg; m.idx = nullptr; m.score = nullptr; m.idx_out = idx;
   m.score_out = score; m.E = E; m.xn = x; m.act = act; m.residual = residual;
   m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
+  m.err = device_status_word();
   launch_moe(m, st);
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);
@@ -1339,14 +1387,17 @@ extern "C" neon_status neon_moe_experts(
   if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E ||
       H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
     KFAIL(NEON_EINVAL, "neon_moe_experts: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
-  // idx is device data: every entry must lie in [0, E).
+  // idx is device data: an entry outside [0, E) drops its slot and sets the
+  // device status word (neon_device_check reports it).
   MoeArgs m;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
   m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
   m.router_lg = nullptr; m.idx = idx; m.score = score; m.idx_out = nullptr;
   m.score_out = nullptr; m.E = E; m.xn = x; m.act = act; m.residual = residual;
   m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
-  launch_moe(m, S(stream));
+  m.err = device_status_word();
+  if (moe_batched_supported(m)) launch_moe_batched(m, S(stream));
+  else launch_moe(m, S(stream));
   KLAUNCHED();
 }
 
@@ -1429,7 +1480,8 @@ extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
     KFAIL(NEON_EINVAL, "neon_moe_prefill: bad shape M=%d E=%d H=%d I=%d k=%d", M, E, H, I, k);
   if (!kBatchedPrefillEnabled)
     KFAIL(NEON_ESTATE, "neon_moe_prefill: the batched prompt pass is switched off");
-  // idx is device data: every entry must lie in [0, E).
+  // idx is device data: an entry outside [0, E) drops its slot and sets the
+  // device status word (neon_device_check reports it).
   hipStream_t st = S(stream);
   const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
   size_t off = 0;
@@ -1449,6 +1501,7 @@ extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
   m.list_tok = (int32_t*)(scratch + o_lt); m.list_slot = (int32_t*)(scratch + o_ls);
   m.e_off = (int32_t*)(scratch + o_eo); m.tile_e = (int32_t*)(scratch + o_te);
   m.tile_r0 = (int32_t*)(scratch + o_tr); m.n_tiles = (int32_t*)(scratch + o_nt);
+  m.err = device_status_word();
   launch_moe_prefill(m, st);
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);

@@ -110,7 +110,12 @@ struct RouterArgs {
 // router logits, then (when a.idx) the top-k / softmax
 void launch_router(const RouterArgs& a, hipStream_t st);
 
+// Status bits a kernel sets (vector atomicOr) in the caller's status word
+// when its input breaks a precondition it can only see on the device.
+constexpr int32_t kDevErrExpertId = 1;  // an expert id outside [0, E)
+
 struct MoeArgs {
+  int32_t* err = nullptr;    // status word (kDevErr* bits), may be NULL
   const uint8_t *gu_codes, *gu_scales, *dn_codes, *dn_scales;
   const uint16_t *gu_bias, *dn_bias;
   const float* router_lg;    // [B][E] router logits: experts chosen in-kernel
@@ -132,6 +137,7 @@ void launch_moe(const MoeArgs& a, hipStream_t st);
 constexpr int kMxMaxRows = 64;   // rows per step
 constexpr int kMxMaxK = 4096;    // reduction length
 struct MxArgs {
+  int32_t* err = nullptr;    // status word (kDevErr* bits), may be NULL
   const void* W;             // bf16 [N][K], or MXFP4 codes [E][N][K/2] (expert modes)
   const uint8_t* scales;     // MXFP4 scales [E][N][K/32] (expert modes)
   const uint16_t* bias;      // [N], [E][N] (expert modes) or NULL (dense modes)
@@ -222,6 +228,7 @@ void launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* 
                          const uint16_t* sinks, uint16_t* out, int M, int Hq, int Hkv,
                          int T_max, int window, hipStream_t st);
 struct MoePrefillArgs {
+  int32_t* err = nullptr;    // status word (kDevErr* bits), may be NULL
   const int32_t* idx;        // [M][k] chosen experts
   const float* score;        // [M][k] weights
   const uint16_t* xn;        // [M][H] normalised input

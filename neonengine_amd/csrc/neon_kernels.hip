@@ -1657,7 +1657,8 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
     const uint16_t* __restrict__ gu_bias, const float* __restrict__ router_lg,
     const int32_t* __restrict__ idx, int32_t* __restrict__ idx_out,
     float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn,
-    uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit) {
+    uint16_t* __restrict__ act, int H, int I, int k, float alpha, float limit,
+    int32_t* __restrict__ err) {
   __shared__ TopK tk;
   const int slot = blockIdx.y, b = blockIdx.z;
   const int U = H / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1669,6 +1670,10 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(
   __builtin_amdgcn_sched_barrier(0);
   moe_gate_up_route_block(router_lg, rr, idx_out, score_out, b, E, k, slot, lane, wave, tk);
   const int e = tk.id[slot];
+  if ((unsigned)e >= (unsigned)E) {  // a caller-given id out of range (uniform)
+    if (threadIdx.x == 0 && blockIdx.x == 0) flag_dev_err(err, kDevErrExpertId);
+    return;  // the down kernel drops this slot
+  }
   const int j0 = (blockIdx.x * 4 + wave) * kMoeJpw;
   if (j0 >= I) return;
   const size_t rows = (size_t)2 * I;
@@ -1730,7 +1735,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     const uint16_t* __restrict__ dn_bias, const float* __restrict__ router_lg,
     const int32_t* __restrict__ idx, const float* __restrict__ score, int E,
     const uint16_t* __restrict__ act, const uint16_t* residual, uint16_t* out,
-    int H, int I, int k) {
+    int H, int I, int k, int32_t* __restrict__ err) {
   __shared__ float red[kMaxTopK][kMoeRpw];
   __shared__ TopK tk;  // wave 0 routes for the block
   const int b = blockIdx.y;
@@ -1748,7 +1753,12 @@ __global__ __launch_bounds__(1024) void k_moe_down(
   __builtin_amdgcn_sched_barrier(0);
   if (slot == 0) (void)moe_route_finish<true>(router_lg, E, k, 0, lane, rr, tk);
   __syncthreads();
-  const int e = tk.id[slot];
+  // a caller-given id out of range (uniform per wave): the slot reads expert
+  // 0's rows (in bounds) and contributes 0
+  const int e_raw = tk.id[slot];
+  const bool e_ok = (unsigned)e_raw < (unsigned)E;
+  const int e = e_ok ? e_raw : 0;
+  if (!e_ok && lane == 0 && blockIdx.x == 0) flag_dev_err(err, kDevErrExpertId);
   const uint8_t* codes = dn_codes + (size_t)e * H * (I / 2);
   const uint8_t* scales = dn_scales + (size_t)e * H * U;
   const uint16_t* bias = dn_bias + (size_t)e * H;
@@ -1781,7 +1791,7 @@ __global__ __launch_bounds__(1024) void k_moe_down(
     for (int r = 0; r < kMoeRpw; ++r) a[r] = fp4_row_partial<P>(rw[r], xr, U, lane);
   }
   const float t = wave_sum_4rows(a[0], a[1], a[2], a[3], lane);
-  if ((lane & 15) == 0) red[slot][lane >> 4] = __fadd_rn(t, bf2f(bl));
+  if ((lane & 15) == 0) red[slot][lane >> 4] = e_ok ? __fadd_rn(t, bf2f(bl)) : 0.0f;
   __syncthreads();
   if (threadIdx.x < min(kMoeRpw, H - n0)) {
     const int r = threadIdx.x, n = n0 + r;
@@ -1928,12 +1938,19 @@ __global__ __launch_bounds__(256) void k_moe_down_bt(
     const uint8_t* __restrict__ dn_codes, const uint8_t* __restrict__ dn_scales,
     const uint16_t* __restrict__ dn_bias, const int32_t* __restrict__ idx,
     const float* __restrict__ score, int E, const uint16_t* __restrict__ act,
-    const uint16_t* residual, uint16_t* out, int B, int H, int I, int k) {
+    const uint16_t* residual, uint16_t* out, int B, int H, int I, int k,
+    int32_t* __restrict__ err) {
   __shared__ float red[64][kMoeRpw];  // [pair][row]: dot + bias
   const int U = I / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nk = B * k;
   const int n0 = blockIdx.x * kMoeRpw;
   const int my_id = lane < nk ? idx[lane] : -1;
+  // a pair whose id lies outside [0, E) matches no expert and contributes 0
+  for (int i = threadIdx.x; i < 64 * kMoeRpw; i += blockDim.x) (&red[0][0])[i] = 0.0f;
+  if (blockIdx.x == 0 && wave == 0 &&
+      __ballot(lane < nk && (unsigned)my_id >= (unsigned)E) != 0 && lane == 0)
+    flag_dev_err(err, kDevErrExpertId);
+  __syncthreads();
   // every fourth used expert, starting at this wave's index
   for (int ee = 0, cnt = 0; ee < E; ++ee) {
     const uint64_t bal = __ballot(my_id == ee);
@@ -2025,7 +2042,7 @@ void launch_moe_batched(const MoeArgs& a, hipStream_t st) {
 #define DB_LAUNCH(PP, PR)                                                                    \
   hipLaunchKernelGGL((k_moe_down_bt<PP, PR>), dim3(dblk), dim3(256), 0, st, a.dn_codes,     \
                      a.dn_scales, a.dn_bias, a.idx, a.score, a.E, a.act, a.residual, a.out,  \
-                     a.B, a.H, a.I, a.k)
+                     a.B, a.H, a.I, a.k, a.err)
   switch (Pg) {
     case 1: GB_LAUNCH(1, false); break;
     case 2: if (pg) GB_LAUNCH(2, true); else GB_LAUNCH(2, false); break;
@@ -2052,7 +2069,7 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
   hipLaunchKernelGGL((k_moe_gate_up<PP, PR>), dim3(gblk, a.k, a.B), dim3(256), 0, \
                      st, a.gu_codes, a.gu_scales, a.gu_bias, a.router_lg, a.idx,  \
                      a.idx_out, a.score_out, a.E, a.xn, a.act, a.H, a.I, a.k,     \
-                     a.alpha, a.limit)
+                     a.alpha, a.limit, a.err)
   // When gate_up records the chosen experts and weights (idx_out/score_out),
   // down reads them instead of ranking the logits again: gate_up has finished
   // before down starts (same stream), and the values are the same.
@@ -2063,7 +2080,7 @@ void launch_moe(const MoeArgs& a, hipStream_t st) {
 #define D_LAUNCH(PP, PR)                                                            \
   hipLaunchKernelGGL((k_moe_down<PP, PR>), dim3(dblk, a.B), dim3(64 * a.k), 0, st, \
                      a.dn_codes, a.dn_scales, a.dn_bias, dn_lg, dn_idx, dn_score,   \
-                     a.E, a.act, a.residual, a.out, a.H, a.I, a.k)
+                     a.E, a.act, a.residual, a.out, a.H, a.I, a.k, a.err)
   switch (Pg) {
     case 1: G_LAUNCH(1, false); break;
     case 2: if (pg) G_LAUNCH(2, true); else G_LAUNCH(2, false); break;

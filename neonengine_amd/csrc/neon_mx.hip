@@ -197,7 +197,11 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   const int S = gridDim.y / G;
   const int e = a.route[slot];
   if (e < 0) return;  // fewer used experts than slots (uniform)
-  const int Rall = a.route[S + slot];
+  if (e >= a.E) {     // a corrupt route table: never read past the experts
+    if (tid == 0) flag_dev_err(a.err, kDevErrExpertId);
+    return;
+  }
+  const int Rall = min(a.route[S + slot], 64);
   if (16 * grp >= Rall) return;  // (uniform)
   const int R = min(16, Rall - 16 * grp);
   const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
@@ -208,7 +212,11 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   const int sr = tid >> 4, sp = tid & 15;
   const bool s_ok = sr < R;
   int xr = 0;
-  if (s_ok) xr = MODE == MX_GATE_UP ? rows[sr] / a.k : rows[sr];
+  if (s_ok) {
+    // pair index -> input row (clamped: a corrupt list still reads in bounds)
+    const unsigned q = min((unsigned)rows[sr], (unsigned)(a.B * a.k - 1));
+    xr = MODE == MX_GATE_UP ? (int)q / a.k : (int)q;
+  }
   const uint16_t* xsrc = a.x + (size_t)xr * K;
   auto x_load = [&](int c, uint4 (&xv)[4]) {
 #pragma unroll
@@ -294,7 +302,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int ri = 4 * g + r;
-      const bool ok = ri < R;
+      const bool ok = ri < R && (unsigned)rows[min(ri, R - 1)] < (unsigned)(a.B * a.k);
       const float d = acc[tt][r];
       if constexpr (MODE == MX_GATE_UP) {
         const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));

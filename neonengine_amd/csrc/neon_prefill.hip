@@ -334,12 +334,20 @@ __device__ __forceinline__ int block_excl_scan_1024(int v, int* lds) {
 // offsets e_off[0..E] and the 128-row tiles (tile_e, tile_r0, n_tiles).
 __global__ __launch_bounds__(1024) void k_moe_count(
     const int32_t* __restrict__ idx, int n_pairs, int E, int32_t* __restrict__ e_off,
-    int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles) {
+    int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles,
+    int32_t* __restrict__ err) {
   __shared__ int cnt[256];
   const int tid = threadIdx.x;
   if (tid < 256) cnt[tid] = 0;
   __syncthreads();
-  for (int q = tid; q < n_pairs; q += 1024) atomicAdd(&cnt[idx[q]], 1);
+  bool bad = false;
+  for (int q = tid; q < n_pairs; q += 1024) {
+    const int e = idx[q];
+    // a pair whose id lies outside [0, E) joins no group; the combine drops it
+    if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[e], 1);
+    else bad = true;
+  }
+  if (bad) flag_dev_err(err, kDevErrExpertId);
   __syncthreads();
   if (tid == 0) {
     int base = 0, t = 0;
@@ -375,13 +383,17 @@ __global__ __launch_bounds__(1024) void k_moe_group(
 // out[t] = bf16(residual[t] + bf16(sum_s score[t][s] * y[t][s]))  in slot
 // order with fmaf, as the decode combine (HFM:111-112).
 __global__ void k_moe_combine(const float* __restrict__ ybuf,
-                              const float* __restrict__ score, int k, int H,
+                              const float* __restrict__ score,
+                              const int32_t* __restrict__ idx, int E, int k, int H,
                               uint16_t* __restrict__ h) {
   const int t = blockIdx.x;
   for (int n = threadIdx.x; n < H; n += blockDim.x) {
     float y = 0.0f;
-    for (int s = 0; s < k; ++s)
-      y = __builtin_fmaf(score[t * k + s], ybuf[((size_t)t * k + s) * H + n], y);
+    for (int s = 0; s < k; ++s) {
+      // pairs with an id outside [0, E) were never computed: they add 0
+      const bool ok = (unsigned)idx[t * k + s] < (unsigned)E;
+      y = __builtin_fmaf(score[t * k + s], ok ? ybuf[((size_t)t * k + s) * H + n] : 0.0f, y);
+    }
     uint16_t* c = h + (size_t)t * H + n;
     *c = f2bf(__fadd_rn(bf2f(*c), bf2f(f2bf(y))));
   }
@@ -394,7 +406,7 @@ __global__ void k_moe_combine(const float* __restrict__ ybuf,
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   const int n_pairs = a.M * a.k;
   hipLaunchKernelGGL(k_moe_count, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.E, a.e_off,
-                     a.tile_e, a.tile_r0, a.n_tiles);
+                     a.tile_e, a.tile_r0, a.n_tiles, a.err);
   hipLaunchKernelGGL(k_moe_group, dim3(a.E), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.e_off,
                      a.list_tok, a.list_slot);
   const int max_tiles = moe_prefill_max_tiles(a.M, a.k, a.E);
@@ -414,7 +426,8 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   p.ybuf = a.ybuf; p.N = a.H; p.K = a.I; p.C = nullptr;
   hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), dim3((a.H + kGN - 1) / kGN, max_tiles),
                      dim3(256), 0, st, p);
-  hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.k, a.H, a.h);
+  hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.idx, a.E,
+                     a.k, a.H, a.h);
 }
 
 int moe_prefill_max_tiles(int M, int k, int E) {

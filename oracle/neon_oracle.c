@@ -114,6 +114,32 @@ void or_fill_scales(uint64_t seed, uint64_t stream, int64_t n, int lo,
   }
 }
 
+/* Elements [start, start + n) of the or_fill_bytes / or_fill_scales streams
+ * (start of a byte range must be a multiple of 8: one hash word fills 8
+ * bytes).  Lets the oracle regenerate one expert's slice of a stacked expert
+ * tensor without materialising the whole tensor. */
+void or_fill_bytes_at(uint64_t seed, uint64_t stream, int64_t start, int64_t n,
+                      uint8_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+  const int64_t w0 = start / 8;
+#pragma omp parallel for schedule(static)
+  for (int64_t w = 0; w < (n + 7) / 8; ++w) {
+    uint64_t h = hash_k(key, (uint64_t)(w0 + w));
+    for (int j = 0; j < 8 && w * 8 + j < n; ++j)
+      out[w * 8 + j] = (uint8_t)(h >> (8 * j));
+  }
+}
+
+void or_fill_scales_at(uint64_t seed, uint64_t stream, int64_t start, int64_t n,
+                       int lo, int range, uint8_t* out) {
+  const uint64_t key = stream_key(seed, stream);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t h = hash_k(key, (uint64_t)(start + i));
+    out[i] = (uint8_t)(lo + (int)(((h >> 32) * (uint64_t)range) >> 32));
+  }
+}
+
 uint64_t or_stream_id(int layer, int kind) {
   return ((uint64_t)(layer + 1) << 16) | (uint64_t)kind;
 }
@@ -356,8 +382,10 @@ static float c_dot_fp4(const uint8_t* codes, const uint8_t* scales,
   return c_butterfly64(a);
 }
 
-void or_c_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
-                    int B, int N, int K, uint16_t* y, float* y_f32) {
+/* Scalar statements of the canonical GEMVs (the definitions; used by the
+ * tests to check the vector forms below). */
+void or_c_gemv_bf16_ref(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                        int B, int N, int K, uint16_t* y, float* y_f32) {
   float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
   for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
 #pragma omp parallel for schedule(static)
@@ -371,9 +399,9 @@ void or_c_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
   free(xf);
 }
 
-void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
-                     const uint16_t* bias, const uint16_t* x, int B, int N,
-                     int K, uint16_t* y, float* y_f32) {
+void or_c_mxfp4_gemv_ref(const uint8_t* codes, const uint8_t* scales,
+                         const uint16_t* bias, const uint16_t* x, int B, int N,
+                         int K, uint16_t* y, float* y_f32) {
   float* xf = (float*)malloc(sizeof(float) * (size_t)B * K);
   for (int64_t i = 0; i < (int64_t)B * K; ++i) xf[i] = BF(x[i]);
 #pragma omp parallel for schedule(static)
@@ -386,6 +414,130 @@ void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
       if (y) y[(size_t)b * N + n] = TOBF(r);
     }
   free(xf);
+}
+
+/* Vector forms: the same per-lane operation sequence with the 64 lanes held
+ * in eight 8-wide AVX2 registers.  Operands are transposed to lane-minor
+ * order [pass][element][lane] (units past U are zero: fmaf(0, 0, acc) = acc
+ * because acc, started at +0, is never -0), so each fmaf of the scalar form
+ * becomes one lane of a vfmadd, and the butterfly keeps the scalar pairing
+ * (fp32 addition is commutative, so l + (l ^ off) equals (l ^ off) + l). */
+#include <immintrin.h>
+
+static inline float butterfly_v8(__m256 a[8]) {
+  __m256 t0 = _mm256_add_ps(a[0], a[4]), t1 = _mm256_add_ps(a[1], a[5]);  /* xor 32 */
+  __m256 t2 = _mm256_add_ps(a[2], a[6]), t3 = _mm256_add_ps(a[3], a[7]);
+  t0 = _mm256_add_ps(t0, t2); t1 = _mm256_add_ps(t1, t3);                 /* xor 16 */
+  t0 = _mm256_add_ps(t0, t1);                                             /* xor 8 */
+  __m128 lo = _mm256_castps256_ps128(t0), hi = _mm256_extractf128_ps(t0, 1);
+  __m128 u = _mm_add_ps(lo, hi);                                          /* xor 4 */
+  u = _mm_add_ps(u, _mm_movehl_ps(u, u));                                 /* xor 2 */
+  u = _mm_add_ss(u, _mm_shuffle_ps(u, u, 1));                             /* xor 1 */
+  return _mm_cvtss_f32(u);
+}
+
+/* x rows -> [B][P][E][64] fp32, E = elements per unit (8 bf16 / 32 fp4) */
+static float* lane_major_x(const uint16_t* x, int B, int K, int E, int P) {
+  const int U = K / E;
+  float* xt = (float*)aligned_alloc(32, sizeof(float) * (size_t)B * P * E * 64);
+  for (int b = 0; b < B; ++b)
+    for (int p = 0; p < P; ++p)
+      for (int e = 0; e < E; ++e)
+        for (int l = 0; l < 64; ++l) {
+          const int u = l + 64 * p;
+          xt[(((size_t)b * P + p) * E + e) * 64 + l] =
+              u < U ? BF(x[(size_t)b * K + (size_t)u * E + e]) : 0.0f;
+        }
+  return xt;
+}
+
+void or_c_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                    int B, int N, int K, uint16_t* y, float* y_f32) {
+  /* one row: the transposition would cost more than it saves */
+  if (B == 1) { or_c_gemv_bf16_ref(W, bias, x, B, N, K, y, y_f32); return; }
+  const int U = K / 8, P = (U + 63) / 64;
+  float* xt = lane_major_x(x, B, K, 8, P);
+#pragma omp parallel
+  {
+    float* wt = (float*)aligned_alloc(32, sizeof(float) * (size_t)P * 8 * 64);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      const uint16_t* w = W + (size_t)n * K;
+      for (int p = 0; p < P; ++p)
+        for (int l = 0; l < 64; ++l) {
+          const int u = l + 64 * p;
+          for (int e = 0; e < 8; ++e)
+            wt[(p * 8 + e) * 64 + l] = u < U ? BF(w[u * 8 + e]) : 0.0f;
+        }
+      for (int b = 0; b < B; ++b) {
+        const float* xb = xt + (size_t)b * P * 8 * 64;
+        __m256 a[8];
+        for (int v = 0; v < 8; ++v) a[v] = _mm256_setzero_ps();
+        for (int pe = 0; pe < P * 8; ++pe)
+          for (int v = 0; v < 8; ++v)
+            a[v] = _mm256_fmadd_ps(_mm256_load_ps(wt + pe * 64 + 8 * v),
+                                   _mm256_load_ps(xb + pe * 64 + 8 * v), a[v]);
+        float r = butterfly_v8(a);
+        if (bias) r = r + BF(bias[n]);
+        if (y_f32) y_f32[(size_t)b * N + n] = r;
+        if (y) y[(size_t)b * N + n] = TOBF(r);
+      }
+    }
+    free(wt);
+  }
+  free(xt);
+}
+
+void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                     const uint16_t* bias, const uint16_t* x, int B, int N,
+                     int K, uint16_t* y, float* y_f32) {
+  if (B == 1) { or_c_mxfp4_gemv_ref(codes, scales, bias, x, B, N, K, y, y_f32); return; }
+  const int U = K / 32, P = (U + 63) / 64;
+  float* xt = lane_major_x(x, B, K, 32, P);
+#pragma omp parallel
+  {
+    float* wt = (float*)aligned_alloc(32, sizeof(float) * (size_t)P * 32 * 64);
+    float* sf = (float*)aligned_alloc(32, sizeof(float) * (size_t)P * 64);
+#pragma omp for schedule(static)
+    for (int n = 0; n < N; ++n) {
+      const uint8_t* c = codes + (size_t)n * (K / 2);
+      const uint8_t* s = scales + (size_t)n * U;
+      for (int p = 0; p < P; ++p)
+        for (int l = 0; l < 64; ++l) {
+          const int u = l + 64 * p;
+          for (int j = 0; j < 16; ++j) {
+            const uint8_t byte = u < U ? c[u * 16 + j] : 0;
+            wt[(p * 32 + 2 * j) * 64 + l] = kE2M1[byte & 0xF];
+            wt[(p * 32 + 2 * j + 1) * 64 + l] = kE2M1[byte >> 4];
+          }
+          /* t * 2^(s-127) rounded once equals ldexpf(t, s - 127): every
+           * 2^(s-127), s < 255, is an exact fp32 (2^-127 a subnormal) */
+          sf[p * 64 + l] = u < U ? e8m0_exp2(s[u], 1.0f) : 1.0f;
+        }
+      for (int b = 0; b < B; ++b) {
+        const float* xb = xt + (size_t)b * P * 32 * 64;
+        __m256 a[8];
+        for (int v = 0; v < 8; ++v) a[v] = _mm256_setzero_ps();
+        for (int p = 0; p < P; ++p) {
+          __m256 t[8];
+          for (int v = 0; v < 8; ++v) t[v] = _mm256_setzero_ps();
+          for (int e = 0; e < 32; ++e)
+            for (int v = 0; v < 8; ++v)
+              t[v] = _mm256_fmadd_ps(_mm256_load_ps(wt + (p * 32 + e) * 64 + 8 * v),
+                                     _mm256_load_ps(xb + (p * 32 + e) * 64 + 8 * v), t[v]);
+          for (int v = 0; v < 8; ++v)
+            a[v] = _mm256_add_ps(a[v], _mm256_mul_ps(t[v], _mm256_load_ps(sf + p * 64 + 8 * v)));
+        }
+        float r = butterfly_v8(a);
+        if (bias) r = r + BF(bias[n]);
+        if (y_f32) y_f32[(size_t)b * N + n] = r;
+        if (y) y[(size_t)b * N + n] = TOBF(r);
+      }
+    }
+    free(wt);
+    free(sf);
+  }
+  free(xt);
 }
 
 /* RMSNorm, canonical: ss by the 64-lane unit order and butterfly;
@@ -520,8 +672,14 @@ void or_c_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
 /* increasing k, one fmaf per element), then a xor-butterfly over offsets    */
 /* 32,16,8,4,2,1, then + bias.  Ties go to the lower expert index.           */
 /* ------------------------------------------------------------------------ */
+static int g_router_fp64 = 0;  /* set with the accumulation mode */
 static float router_logit(const uint16_t* x, const uint16_t* w, int H,
                           uint16_t bias) {
+  if (g_router_fp64) {
+    double d = 0.0;
+    for (int i = 0; i < H; ++i) d += (double)BF(x[i]) * BF(w[i]);
+    return (float)d + BF(bias);
+  }
   float p[64];
   const int U = H / 8;
   for (int l = 0; l < 64; ++l) {
@@ -593,10 +751,90 @@ void or_swiglu(const float* gu, int I, float alpha, float limit, float* out) {
   }
 }
 
+/* Accumulation mode of the model functions: 0 = the canonical fp32 orders
+ * (bit-identical to the device), 1 = fp64 accumulation rounded once (the
+ * or_gemv_* / or_rmsnorm / or_attn_decode forms).  Mode 1 exists to measure
+ * how far a mere change of summation order moves the model's outputs. */
+static int g_acc_mode = 0;
+void or_set_accumulation(int mode) { g_acc_mode = mode; g_router_fp64 = mode; }
+
+static void m_gemv_bf16(const uint16_t* W, const uint16_t* bias, const uint16_t* x, int B,
+                        int N, int K, uint16_t* y, float* y_f32) {
+  if (g_acc_mode) or_gemv_bf16(W, bias, x, B, N, K, y, y_f32);
+  else or_c_gemv_bf16(W, bias, x, B, N, K, y, y_f32);
+}
+static void m_gemv_fp4(const uint8_t* codes, const uint8_t* scales, const uint16_t* bias,
+                       const uint16_t* x, int B, int N, int K, uint16_t* y, float* y_f32) {
+  if (g_acc_mode) or_mxfp4_gemv(codes, scales, bias, x, B, N, K, y, y_f32);
+  else or_c_mxfp4_gemv(codes, scales, bias, x, B, N, K, y, y_f32);
+}
+static void m_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
+                      uint16_t* out) {
+  if (g_acc_mode) or_rmsnorm(x, w, B, H, eps, out);
+  else or_c_rmsnorm(x, w, B, H, eps, out);
+}
+
+/* One row's experts (HFM:89-114), canonical form: for each slot t (rank
+ * order) gate_up GEMV + bias -> SwiGLU -> bf16 -> down GEMV + bias, then
+ * acc = fmaf(score_t, out, acc) from 0; one rounding to bf16.  Slot t's
+ * weights come through the pointer arrays (the expert idx[t] already
+ * resolved by the caller). */
+static void moe_row_slots(const uint16_t* x, int H, int I, int k, const float* score,
+                          const uint8_t* const* guc, const uint8_t* const* gus,
+                          const uint16_t* const* gub, const uint8_t* const* dnc,
+                          const uint8_t* const* dns, const uint16_t* const* dnb,
+                          float alpha, float limit, uint16_t* out) {
+  float* gu = (float*)malloc(sizeof(float) * 2 * I);
+  float* act = (float*)malloc(sizeof(float) * I);
+  uint16_t* actb = (uint16_t*)malloc(sizeof(uint16_t) * I);
+  float* dn = (float*)malloc(sizeof(float) * H);
+  float* acc = (float*)malloc(sizeof(float) * H);
+  for (int i = 0; i < H; ++i) acc[i] = 0.0f;
+  for (int t = 0; t < k; ++t) {
+    m_gemv_fp4(guc[t], gus[t], gub[t], x, 1, 2 * I, H, NULL, gu);
+    or_swiglu(gu, I, alpha, limit, act);
+    for (int j = 0; j < I; ++j) actb[j] = TOBF(act[j]);
+    m_gemv_fp4(dnc[t], dns[t], dnb[t], actb, 1, H, I, NULL, dn);
+    for (int i = 0; i < H; ++i) acc[i] = fmaf(score[t], dn[i], acc[i]);
+  }
+  for (int i = 0; i < H; ++i) out[i] = TOBF(acc[i]);
+  free(gu); free(act); free(actb); free(dn); free(acc);
+}
+
+/* Experts with given ids and weights (HF GptOssExperts, HFM:89-114), the
+ * canonical moe_row_slots per row.  A slot whose id lies outside [0, E) adds
+ * nothing (the device kernels drop it and flag the call). */
+void or_moe_experts(const uint16_t* x, const int32_t* idx, const float* score,
+                    const uint8_t* gu_codes, const uint8_t* gu_scales,
+                    const uint16_t* gu_bias, const uint8_t* dn_codes,
+                    const uint8_t* dn_scales, const uint16_t* dn_bias, int B, int E,
+                    int H, int I, int k, float alpha, float limit, uint16_t* out) {
+  const size_t gu_code_sz = (size_t)2 * I * (H / 2), gu_sc_sz = (size_t)2 * I * (H / 32);
+  const size_t dn_code_sz = (size_t)H * (I / 2), dn_sc_sz = (size_t)H * (I / 32);
+  for (int r = 0; r < B; ++r) {
+    const uint8_t *guc[64], *gus[64], *dnc[64], *dns[64];
+    const uint16_t *gub[64], *dnb[64];
+    float sc[64];
+    int n = 0;
+    for (int t = 0; t < k; ++t) {
+      const int32_t e = idx[r * k + t];
+      if (e < 0 || e >= E) continue;
+      guc[n] = gu_codes + (size_t)e * gu_code_sz; gus[n] = gu_scales + (size_t)e * gu_sc_sz;
+      gub[n] = gu_bias + (size_t)e * 2 * I;
+      dnc[n] = dn_codes + (size_t)e * dn_code_sz; dns[n] = dn_scales + (size_t)e * dn_sc_sz;
+      dnb[n] = dn_bias + (size_t)e * H;
+      sc[n] = score[r * k + t];
+      ++n;
+    }
+    /* dropped slots add exactly 0 (fmaf(s, 0, acc) = acc), so the remaining
+     * slots in order give the same bits */
+    moe_row_slots(x + (size_t)r * H, H, I, n, sc, guc, gus, gub, dnc, dns, dnb, alpha, limit,
+                  out + (size_t)r * H);
+  }
+}
+
 /* MoE block (HFM:89-114, 145-154) on already-normalised x, canonical form:
- * router, then for each selected expert (rank order) gate_up GEMV + bias ->
- * SwiGLU -> bf16 -> down GEMV + bias, acc = fmaf(score, out, acc) from 0;
- * one rounding to bf16. */
+ * router, then moe_row_slots over the selected experts. */
 void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
                   const uint16_t* router_b, const uint8_t* gu_codes,
                   const uint8_t* gu_scales, const uint16_t* gu_bias,
@@ -605,30 +843,60 @@ void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
                   float alpha, float limit, uint16_t* out, int32_t* idx,
                   float* score) {
   or_router(x, router_w, router_b, B, E, H, k, idx, score, NULL);
-  float* gu = (float*)malloc(sizeof(float) * 2 * I);
-  float* act = (float*)malloc(sizeof(float) * I);
-  uint16_t* actb = (uint16_t*)malloc(sizeof(uint16_t) * I);
-  float* dn = (float*)malloc(sizeof(float) * H);
-  float* acc = (float*)malloc(sizeof(float) * H);
   const size_t gu_code_sz = (size_t)2 * I * (H / 2), gu_sc_sz = (size_t)2 * I * (H / 32);
   const size_t dn_code_sz = (size_t)H * (I / 2), dn_sc_sz = (size_t)H * (I / 32);
-  for (int r = 0; r < B; ++r) {
-    for (int i = 0; i < H; ++i) acc[i] = 0.0f;
-    for (int t = 0; t < k; ++t) {
-      const int e = idx[r * k + t];
-      or_c_mxfp4_gemv(gu_codes + e * gu_code_sz, gu_scales + e * gu_sc_sz,
-                      gu_bias + (size_t)e * 2 * I, x + (size_t)r * H, 1, 2 * I,
-                      H, NULL, gu);
-      or_swiglu(gu, I, alpha, limit, act);
-      for (int j = 0; j < I; ++j) actb[j] = TOBF(act[j]);
-      or_c_mxfp4_gemv(dn_codes + e * dn_code_sz, dn_scales + e * dn_sc_sz,
-                      dn_bias + (size_t)e * H, actb, 1, H, I, NULL, dn);
-      const float sc = score[r * k + t];
-      for (int i = 0; i < H; ++i) acc[i] = fmaf(sc, dn[i], acc[i]);
+  if (B >= 2) {
+    /* the same per-(row, slot) GEMVs, with the rows that chose an expert in
+     * one call (its weights transposed once); then each row's slots are
+     * combined in slot order as in moe_row_slots */
+    float* dn = (float*)malloc(sizeof(float) * (size_t)B * k * H);
+    uint16_t* xs = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)B * k * H);
+    uint16_t* acts = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)B * k * I);
+    float* gu = (float*)malloc(sizeof(float) * (size_t)B * k * 2 * I);
+    float* dq = (float*)malloc(sizeof(float) * (size_t)B * k * H);
+    float* act = (float*)malloc(sizeof(float) * I);
+    int* pairs = (int*)malloc(sizeof(int) * (size_t)B * k);
+    for (int e = 0; e < E; ++e) {
+      int n = 0;
+      for (int q = 0; q < B * k; ++q)
+        if (idx[q] == e) pairs[n++] = q;
+      if (n == 0) continue;
+      for (int i = 0; i < n; ++i)
+        memcpy(xs + (size_t)i * H, x + (size_t)(pairs[i] / k) * H, sizeof(uint16_t) * H);
+      m_gemv_fp4(gu_codes + e * gu_code_sz, gu_scales + e * gu_sc_sz,
+                 gu_bias + (size_t)e * 2 * I, xs, n, 2 * I, H, NULL, gu);
+      for (int i = 0; i < n; ++i) {
+        or_swiglu(gu + (size_t)i * 2 * I, I, alpha, limit, act);
+        for (int j = 0; j < I; ++j) acts[(size_t)i * I + j] = TOBF(act[j]);
+      }
+      m_gemv_fp4(dn_codes + e * dn_code_sz, dn_scales + e * dn_sc_sz,
+                 dn_bias + (size_t)e * H, acts, n, H, I, NULL, dq);
+      for (int i = 0; i < n; ++i)
+        memcpy(dn + (size_t)pairs[i] * H, dq + (size_t)i * H, sizeof(float) * H);
     }
-    for (int i = 0; i < H; ++i) out[(size_t)r * H + i] = TOBF(acc[i]);
+    for (int r = 0; r < B; ++r)
+      for (int i = 0; i < H; ++i) {
+        float acc = 0.0f;
+        for (int t = 0; t < k; ++t)
+          acc = fmaf(score[r * k + t], dn[((size_t)r * k + t) * H + i], acc);
+        out[(size_t)r * H + i] = TOBF(acc);
+      }
+    free(dn); free(xs); free(acts); free(gu); free(dq); free(act); free(pairs);
+    return;
   }
-  free(gu); free(act); free(actb); free(dn); free(acc);
+  for (int r = 0; r < B; ++r) {
+    const uint8_t *guc[64], *gus[64], *dnc[64], *dns[64];
+    const uint16_t *gub[64], *dnb[64];
+    for (int t = 0; t < k; ++t) {
+      const size_t e = (size_t)idx[r * k + t];
+      guc[t] = gu_codes + e * gu_code_sz; gus[t] = gu_scales + e * gu_sc_sz;
+      gub[t] = gu_bias + e * 2 * I;
+      dnc[t] = dn_codes + e * dn_code_sz; dns[t] = dn_scales + e * dn_sc_sz;
+      dnb[t] = dn_bias + e * H;
+    }
+    moe_row_slots(x + (size_t)r * H, H, I, k, score + r * k, guc, gus, gub, dnc, dns, dnb,
+                  alpha, limit, out + (size_t)r * H);
+  }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -697,6 +965,12 @@ struct or_model {
   uint16_t *kc, *vc; /* [L][B][Hkv][max_seq][D] */
   int32_t* pos;
   uint16_t* h; /* [B][H] */
+  /* lazy experts: the MXFP4 codes and scales are not kept; each step
+   * regenerates the chosen experts' slices from the counter RNG into these
+   * k-slot buffers (for shapes whose experts do not fit in host memory) */
+  int lazy;
+  uint64_t seed;
+  uint8_t *lz_guc, *lz_gus, *lz_dnc, *lz_dns;
   /* last step, batch row 0, last layer: buffers named like the device's */
   uint16_t *t_qkv, *t_attn, *t_moe_in;
   int32_t t_idx[64];
@@ -710,9 +984,15 @@ static void* xmalloc(size_t n) {
 }
 
 or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch) {
+  return or_model_create_ex(cfg, seed, batch, 0);
+}
+
+or_model* or_model_create_ex(const or_config* cfg, uint64_t seed, int batch, int flags) {
   or_model* m = (or_model*)calloc(1, sizeof(or_model));
   m->cfg = *cfg;
   m->batch = batch;
+  m->seed = seed;
+  m->lazy = (flags & OR_LAZY_EXPERTS) != 0;
   const int H = cfg->hidden, D = cfg->head_dim, Hq = cfg->n_heads,
             Hkv = cfg->n_kv_heads, E = cfg->n_experts, I = cfg->intermediate;
   const int64_t V = cfg->vocab, QKV = (int64_t)(Hq + 2 * Hkv) * D;
@@ -746,6 +1026,7 @@ or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch) {
                   gu_sc = (int64_t)E * 2 * I * (H / 32);
     const int64_t dn_codes = (int64_t)E * H * (I / 2),
                   dn_sc = (int64_t)E * H * (I / 32);
+    if (m->lazy) continue;
     L->gu_codes = (uint8_t*)xmalloc(gu_codes);
     L->gu_scales = (uint8_t*)xmalloc(gu_sc);
     L->dn_codes = (uint8_t*)xmalloc(dn_codes);
@@ -756,6 +1037,13 @@ or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch) {
     or_fill_bytes(seed, or_stream_id(l, OR_T_DN_CODES), dn_codes, L->dn_codes);
     or_fill_scales(seed, or_stream_id(l, OR_T_DN_SCALES), dn_sc, 119, 6,
                    L->dn_scales);
+  }
+  if (m->lazy) {
+    const size_t k = (size_t)cfg->top_k;
+    m->lz_guc = (uint8_t*)xmalloc(k * 2 * I * (H / 2));
+    m->lz_gus = (uint8_t*)xmalloc(k * 2 * I * (H / 32));
+    m->lz_dnc = (uint8_t*)xmalloc(k * H * (I / 2));
+    m->lz_dns = (uint8_t*)xmalloc(k * H * (I / 32));
   }
   m->cos_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
   m->sin_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
@@ -782,7 +1070,52 @@ void or_model_free(or_model* m) {
   }
   free(m->layers); free(m->embed); free(m->lm_head); free(m->final_norm);
   free(m->cos_t); free(m->sin_t); free(m->kc); free(m->vc); free(m->pos);
-  free(m->h); free(m->t_qkv); free(m->t_attn); free(m->t_moe_in); free(m);
+  free(m->h); free(m->t_qkv); free(m->t_attn); free(m->t_moe_in);
+  free(m->lz_guc); free(m->lz_gus); free(m->lz_dnc); free(m->lz_dns); free(m);
+}
+
+static size_t tensor_bytes(const or_config* c, int kind) {
+  const size_t H = c->hidden, E = c->n_experts, I = c->intermediate, V = c->vocab;
+  const size_t QKV = (size_t)(c->n_heads + 2 * c->n_kv_heads) * c->head_dim;
+  const size_t HD = (size_t)c->n_heads * c->head_dim;
+  switch (kind) {
+    case OR_T_EMBED: case OR_T_LM_HEAD: return V * H * 2;
+    case OR_T_FINAL_NORM: case OR_T_ATTN_NORM: case OR_T_MLP_NORM: case OR_T_BO: return H * 2;
+    case OR_T_WQKV: return QKV * H * 2;
+    case OR_T_BQKV: return QKV * 2;
+    case OR_T_WO: return H * HD * 2;
+    case OR_T_SINKS: return (size_t)c->n_heads * 2;
+    case OR_T_ROUTER_W: return E * H * 2;
+    case OR_T_ROUTER_B: return E * 2;
+    case OR_T_GU_CODES: return E * 2 * I * (H / 2);
+    case OR_T_GU_SCALES: return E * 2 * I * (H / 32);
+    case OR_T_GU_BIAS: return E * 2 * I * 2;
+    case OR_T_DN_CODES: return E * H * (I / 2);
+    case OR_T_DN_SCALES: return E * H * (I / 32);
+    case OR_T_DN_BIAS: return E * H * 2;
+    default: return 0;
+  }
+}
+
+int or_model_set_tensor(or_model* m, int layer, int kind, const void* data, size_t bytes) {
+  void* p = (void*)or_model_tensor(m, layer, kind);
+  if (p == NULL || bytes != tensor_bytes(&m->cfg, kind)) return -1;
+  memcpy(p, data, bytes);
+  return 0;
+}
+
+/* Synthetic KV history for timing: every layer's cache rows 0 .. n_pos-1 of
+ * every sequence hold N(0,1) bf16 keys and values, and every sequence is at
+ * position n_pos (the next step attends over n_pos + 1 keys). */
+void or_model_fill_kv(or_model* m, int n_pos, uint64_t seed) {
+  const or_config* c = &m->cfg;
+  const size_t D = c->head_dim, T = c->max_seq;
+  const size_t n_streams = (size_t)c->n_layers * m->batch * c->n_kv_heads;
+  for (size_t s = 0; s < n_streams; ++s) {
+    or_fill_bf16(seed, 0x10000u + 2 * s, (int64_t)n_pos * D, 0.0f, 1.0, m->kc + s * T * D);
+    or_fill_bf16(seed, 0x10001u + 2 * s, (int64_t)n_pos * D, 0.0f, 1.0, m->vc + s * T * D);
+  }
+  for (int b = 0; b < m->batch; ++b) m->pos[b] = n_pos;
 }
 
 const void* or_model_trace(const or_model* m, int what) {
@@ -829,75 +1162,122 @@ const void* or_model_tensor(const or_model* m, int layer, int kind) {
   }
 }
 
+/* Experts of rows 0 .. B-1 (normalised xn [B][H]) for layer l -> out [B][H]
+ * (bf16), ids and weights [B][k].  Lazy models regenerate each chosen
+ * expert's slice from the counter RNG (the same bytes init wrote). */
+static void model_moe(or_model* m, int l, const uint16_t* xn, int B, uint16_t* out,
+                      int32_t* idx, float* sc) {
+  const or_config* c = &m->cfg;
+  const int H = c->hidden, E = c->n_experts, I = c->intermediate, K = c->top_k;
+  const or_layer* L = &m->layers[l];
+  if (!m->lazy) {
+    or_moe_layer(xn, L->router_w, L->router_b, L->gu_codes, L->gu_scales, L->gu_bias,
+                 L->dn_codes, L->dn_scales, L->dn_bias, B, E, H, I, K, c->swiglu_alpha,
+                 c->swiglu_limit, out, idx, sc);
+    return;
+  }
+  or_router(xn, L->router_w, L->router_b, B, E, H, K, idx, sc, NULL);
+  const size_t gcs = (size_t)2 * I * (H / 2), gss = (size_t)2 * I * (H / 32);
+  const size_t dcs = (size_t)H * (I / 2), dss = (size_t)H * (I / 32);
+  for (int r = 0; r < B; ++r) {
+    const uint8_t *guc[64], *gus[64], *dnc[64], *dns[64];
+    const uint16_t *gub[64], *dnb[64];
+    for (int t = 0; t < K; ++t) {
+      const size_t e = (size_t)idx[r * K + t];
+      uint8_t* a = m->lz_guc + t * gcs; uint8_t* b2 = m->lz_gus + t * gss;
+      uint8_t* d = m->lz_dnc + t * dcs; uint8_t* f = m->lz_dns + t * dss;
+      or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_GU_CODES), (int64_t)(e * gcs),
+                       (int64_t)gcs, a);
+      or_fill_scales_at(m->seed, or_stream_id(l, OR_T_GU_SCALES), (int64_t)(e * gss),
+                        (int64_t)gss, 119, 6, b2);
+      or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_DN_CODES), (int64_t)(e * dcs),
+                       (int64_t)dcs, d);
+      or_fill_scales_at(m->seed, or_stream_id(l, OR_T_DN_SCALES), (int64_t)(e * dss),
+                        (int64_t)dss, 119, 6, f);
+      guc[t] = a; gus[t] = b2; dnc[t] = d; dns[t] = f;
+      gub[t] = L->gu_bias + e * 2 * I; dnb[t] = L->dn_bias + e * H;
+    }
+    moe_row_slots(xn + (size_t)r * H, H, I, K, sc + r * K, guc, gus, gub, dnc, dns, dnb,
+                  c->swiglu_alpha, c->swiglu_limit, out + (size_t)r * H);
+  }
+}
+
 /* Decoder layer (HFM:347-376): h += attn(norm(h)); h += moe(norm(h)); each
  * sublayer output rounded to bf16 and added to the bf16 residual with one
  * rounding.  Layer i is sliding iff (i + 1) is odd (HFC:75-78).  Every
  * reduction uses the canonical or_c_* forms, so the step is bit-identical to
- * the device's. */
+ * the device's.  The rows of a step go through the layers together (each
+ * weight row is read once per step); every row's arithmetic is the same as
+ * if it ran alone. */
 void or_model_step(or_model* m, const int32_t* ids, float* logits,
                    int32_t* out_ids) {
   const or_config* c = &m->cfg;
   const int H = c->hidden, D = c->head_dim, Hq = c->n_heads, Hkv = c->n_kv_heads;
-  const int E = c->n_experts, I = c->intermediate, K = c->top_k;
+  const int K = c->top_k, B = m->batch;
   const int QKV = (Hq + 2 * Hkv) * D, half = D / 2;
   const int64_t V = c->vocab;
-  uint16_t* xn = (uint16_t*)xmalloc(sizeof(uint16_t) * H);
-  uint16_t* qkv = (uint16_t*)xmalloc(sizeof(uint16_t) * QKV);
-  uint16_t* qr = (uint16_t*)xmalloc(sizeof(uint16_t) * Hq * D);
-  uint16_t* ao = (uint16_t*)xmalloc(sizeof(uint16_t) * Hq * D);
-  uint16_t* tmp = (uint16_t*)xmalloc(sizeof(uint16_t) * H);
-  float* lg = (float*)xmalloc(sizeof(float) * V);
-  int32_t idx[64];
-  float sc[64];
-  for (int b = 0; b < m->batch; ++b) {
-    uint16_t* h = m->h + (size_t)b * H;
-    const int p = m->pos[b];
-    memcpy(h, m->embed + (size_t)ids[b] * H, sizeof(uint16_t) * H);
-    for (int l = 0; l < c->n_layers; ++l) {
-      const or_layer* L = &m->layers[l];
-      const int window = (l % 2 == 0) ? c->sliding_window : 0;
-      or_c_rmsnorm(h, L->attn_norm, 1, H, c->rms_eps, xn);
-      or_c_gemv_bf16(L->wqkv, L->bqkv, xn, 1, QKV, H, qkv, NULL);
+  const size_t T = (size_t)c->max_seq;
+  uint16_t* xn = (uint16_t*)xmalloc(sizeof(uint16_t) * B * H);
+  uint16_t* qkv = (uint16_t*)xmalloc(sizeof(uint16_t) * B * QKV);
+  uint16_t* qr = (uint16_t*)xmalloc(sizeof(uint16_t) * B * Hq * D);
+  uint16_t* ao = (uint16_t*)xmalloc(sizeof(uint16_t) * B * Hq * D);
+  uint16_t* tmp = (uint16_t*)xmalloc(sizeof(uint16_t) * B * H);
+  float* lg = (float*)xmalloc(sizeof(float) * V * B);
+  int32_t* idx = (int32_t*)xmalloc(sizeof(int32_t) * B * K);
+  float* sc = (float*)xmalloc(sizeof(float) * B * K);
+  for (int b = 0; b < B; ++b)
+    memcpy(m->h + (size_t)b * H, m->embed + (size_t)ids[b] * H, sizeof(uint16_t) * H);
+  for (int l = 0; l < c->n_layers; ++l) {
+    const or_layer* L = &m->layers[l];
+    const int window = (l % 2 == 0) ? c->sliding_window : 0;
+    uint16_t* kc_l = m->kc + (size_t)l * B * Hkv * T * D;
+    uint16_t* vc_l = m->vc + (size_t)l * B * Hkv * T * D;
+    m_rmsnorm(m->h, L->attn_norm, B, H, c->rms_eps, xn);
+    m_gemv_bf16(L->wqkv, L->bqkv, xn, B, QKV, H, qkv, NULL);
+    for (int b = 0; b < B; ++b) {
+      const int p = m->pos[b];
       const float* cr = m->cos_t + (size_t)p * half;
       const float* sr = m->sin_t + (size_t)p * half;
-      or_rope_apply(qkv, Hq, D, cr, sr, qr);
-      const size_t lb = (((size_t)l * m->batch + b) * Hkv) * c->max_seq;
+      const uint16_t* qb = qkv + (size_t)b * QKV;
+      or_rope_apply(qb, Hq, D, cr, sr, qr + (size_t)b * Hq * D);
       uint16_t kr[4096];
-      or_rope_apply(qkv + Hq * D, Hkv, D, cr, sr, kr);
+      or_rope_apply(qb + Hq * D, Hkv, D, cr, sr, kr);
       for (int g = 0; g < Hkv; ++g) {
-        memcpy(m->kc + (lb + (size_t)g * c->max_seq + p) * D, kr + g * D,
-               sizeof(uint16_t) * D);
-        memcpy(m->vc + (lb + (size_t)g * c->max_seq + p) * D,
-               qkv + (Hq + Hkv + g) * D, sizeof(uint16_t) * D);
+        const size_t row = (((size_t)b * Hkv + g) * T + p) * D;
+        memcpy(kc_l + row, kr + g * D, sizeof(uint16_t) * D);
+        memcpy(vc_l + row, qb + (Hq + Hkv + g) * D, sizeof(uint16_t) * D);
       }
-      or_c_attn_decode(qr, m->kc + lb * D, m->vc + lb * D, L->sinks, 1, Hq,
-                       Hkv, D, c->max_seq, &p, window,
-                       or_attn_splits(c->max_seq, window), ao, NULL);
-      or_c_gemv_bf16(L->wo, L->bo, ao, 1, H, Hq * D, tmp, NULL);
-      for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
-      or_c_rmsnorm(h, L->mlp_norm, 1, H, c->rms_eps, xn);
-      or_moe_layer(xn, L->router_w, L->router_b, L->gu_codes, L->gu_scales,
-                   L->gu_bias, L->dn_codes, L->dn_scales, L->dn_bias, 1, E, H,
-                   I, K, c->swiglu_alpha, c->swiglu_limit, tmp, idx, sc);
-      if (b == 0 && l == c->n_layers - 1) {
-        memcpy(m->t_qkv, qkv, sizeof(uint16_t) * QKV);
-        memcpy(m->t_attn, ao, sizeof(uint16_t) * Hq * D);
-        memcpy(m->t_moe_in, xn, sizeof(uint16_t) * H);
-        memcpy(m->t_idx, idx, sizeof(int32_t) * K);
-        memcpy(m->t_score, sc, sizeof(float) * K);
-      }
-      for (int i = 0; i < H; ++i) h[i] = TOBF(BF(h[i]) + BF(tmp[i]));
     }
-    or_c_rmsnorm(h, m->final_norm, 1, H, c->rms_eps, xn);
-    or_c_gemv_bf16(m->lm_head, NULL, xn, 1, (int)V, H, NULL, lg);
+    if (g_acc_mode)
+      or_attn_decode(qr, kc_l, vc_l, L->sinks, B, Hq, Hkv, D, (int)T, m->pos, window, ao, NULL);
+    else
+      or_c_attn_decode(qr, kc_l, vc_l, L->sinks, B, Hq, Hkv, D, (int)T, m->pos, window,
+                       or_attn_splits((int)T, window), ao, NULL);
+    m_gemv_bf16(L->wo, L->bo, ao, B, H, Hq * D, tmp, NULL);
+    for (size_t i = 0; i < (size_t)B * H; ++i) m->h[i] = TOBF(BF(m->h[i]) + BF(tmp[i]));
+    m_rmsnorm(m->h, L->mlp_norm, B, H, c->rms_eps, xn);
+    model_moe(m, l, xn, B, tmp, idx, sc);
+    if (l == c->n_layers - 1) {
+      memcpy(m->t_qkv, qkv, sizeof(uint16_t) * QKV);
+      memcpy(m->t_attn, ao, sizeof(uint16_t) * Hq * D);
+      memcpy(m->t_moe_in, xn, sizeof(uint16_t) * H);
+      memcpy(m->t_idx, idx, sizeof(int32_t) * K);
+      memcpy(m->t_score, sc, sizeof(float) * K);
+    }
+    for (size_t i = 0; i < (size_t)B * H; ++i) m->h[i] = TOBF(BF(m->h[i]) + BF(tmp[i]));
+  }
+  m_rmsnorm(m->h, m->final_norm, B, H, c->rms_eps, xn);
+  m_gemv_bf16(m->lm_head, NULL, xn, B, (int)V, H, NULL, lg);
+  for (int b = 0; b < B; ++b) {
+    const float* lb = lg + (size_t)b * V;
     int best = 0;
     for (int64_t v = 1; v < V; ++v)
-      if (lg[v] > lg[best]) best = (int)v;
+      if (lb[v] > lb[best]) best = (int)v;
     if (out_ids) out_ids[b] = best;
-    if (logits) memcpy(logits + (size_t)b * V, lg, sizeof(float) * V);
-    m->pos[b] = p + 1;
+    if (logits) memcpy(logits + (size_t)b * V, lb, sizeof(float) * V);
+    m->pos[b] = m->pos[b] + 1;
   }
-  free(xn); free(qkv); free(qr); free(ao); free(tmp); free(lg);
+  free(xn); free(qkv); free(qr); free(ao); free(tmp); free(lg); free(idx); free(sc);
 }
 
 #ifdef _OPENMP

@@ -62,6 +62,11 @@ void or_fill_bf16(uint64_t seed, uint64_t stream, int64_t n, float mean,
 void or_fill_bytes(uint64_t seed, uint64_t stream, int64_t n, uint8_t* out);
 void or_fill_scales(uint64_t seed, uint64_t stream, int64_t n, int lo,
                     int range, uint8_t* out);
+/* elements [start, start + n) of the same streams (start % 8 == 0 for bytes) */
+void or_fill_bytes_at(uint64_t seed, uint64_t stream, int64_t start, int64_t n,
+                      uint8_t* out);
+void or_fill_scales_at(uint64_t seed, uint64_t stream, int64_t start, int64_t n,
+                       int lo, int range, uint8_t* out);
 
 /* ---- numeric helpers ------------------------------------------------------ */
 float or_bf16_to_f32(uint16_t b);
@@ -95,6 +100,12 @@ void or_moe_layer(const uint16_t* x, const uint16_t* router_w,
                   const uint16_t* dn_bias, int B, int E, int H, int I, int k,
                   float alpha, float limit, uint16_t* out, int32_t* idx,
                   float* score);
+/* experts with given ids [B][k] and weights; ids outside [0, E) are dropped */
+void or_moe_experts(const uint16_t* x, const int32_t* idx, const float* score,
+                    const uint8_t* gu_codes, const uint8_t* gu_scales,
+                    const uint16_t* gu_bias, const uint8_t* dn_codes,
+                    const uint8_t* dn_scales, const uint16_t* dn_bias, int B, int E,
+                    int H, int I, int k, float alpha, float limit, uint16_t* out);
 void or_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                     const uint16_t* v_cache, const uint16_t* sinks, int B,
                     int Hq, int Hkv, int D, int T_max, const int32_t* pos,
@@ -109,6 +120,14 @@ void or_c_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
                      int K, uint16_t* y, float* y_f32);
 void or_c_rmsnorm(const uint16_t* x, const uint16_t* w, int B, int H, float eps,
                   uint16_t* out);
+/* scalar statements of or_c_gemv_bf16 / or_c_mxfp4_gemv (one fmaf at a time
+ * per lane); the functions above compute the same bits with AVX2 over the
+ * 64 lanes */
+void or_c_gemv_bf16_ref(const uint16_t* W, const uint16_t* bias, const uint16_t* x,
+                        int B, int N, int K, uint16_t* y, float* y_f32);
+void or_c_mxfp4_gemv_ref(const uint8_t* codes, const uint8_t* scales,
+                         const uint16_t* bias, const uint16_t* x, int B, int N,
+                         int K, uint16_t* y, float* y_f32);
 int or_attn_splits(int T_max, int window);
 void or_c_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                       const uint16_t* v_cache, const uint16_t* sinks, int B,
@@ -118,6 +137,22 @@ void or_c_attn_decode(const uint16_t* q, const uint16_t* k_cache,
 /* ---- full model (random init, identical to neon_init_random) -------------- */
 typedef struct or_model or_model;
 or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch);
+/* flags: OR_LAZY_EXPERTS keeps no MXFP4 expert codes/scales in memory and
+ * regenerates the chosen experts' slices each step (same bits; for the
+ * 120b shape, whose experts exceed host memory).  or_model_tensor returns
+ * NULL for those tensors then. */
+enum { OR_LAZY_EXPERTS = 1 };
+or_model* or_model_create_ex(const or_config* cfg, uint64_t seed, int batch, int flags);
+/* Synthetic KV history (N(0,1) keys and values at positions 0 .. n_pos-1 of
+ * every layer and sequence; positions set to n_pos).  Timing only. */
+void or_model_fill_kv(or_model* m, int n_pos, uint64_t seed);
+/* Overwrites one weight tensor (layer -1 for embed / lm_head / final norm);
+ * bytes must equal its size.  Returns 0, or -1 on a bad kind or size. */
+int or_model_set_tensor(or_model* m, int layer, int kind, const void* data, size_t bytes);
+/* Accumulation of the model functions: 0 = canonical fp32 orders (default,
+ * bit-identical to the device), 1 = fp64 accumulation rounded once.  Mode 1
+ * measures how far a change of summation order alone moves the outputs. */
+void or_set_accumulation(int mode);
 void or_model_free(or_model* m);
 /* One decode step for every sequence: consumes ids[b] at position pos[b],
  * writes logits (fp32 [B][V], may be NULL) and greedy ids. */

@@ -100,8 +100,15 @@ def _declare(L):
         "or_router": (None, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P]),
         "or_swiglu": (None, [_P, _I, _F, _F, _P]),
         "or_moe_layer": (None, [_P] * 9 + [_I] * 5 + [_F, _F, _P, _P, _P]),
+        "or_moe_experts": (None, [_P] * 9 + [_I] * 5 + [_F, _F, _P]),
         "or_attn_decode": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P, _P]),
         "or_model_create": (_P, [_P, _U64, _I]),
+        "or_model_create_ex": (_P, [_P, _U64, _I, _I]),
+        "or_model_fill_kv": (None, [_P, _I, _U64]),
+        "or_model_set_tensor": (_I, [_P, _I, _I, _P, C.c_size_t]),
+        "or_set_accumulation": (None, [_I]),
+        "or_fill_bytes_at": (None, [_U64, _U64, _I64, _I64, _P]),
+        "or_fill_scales_at": (None, [_U64, _U64, _I64, _I64, _I, _I, _P]),
         "or_model_free": (None, [_P]),
         "or_model_step": (None, [_P, _P, _P, _P]),
         "or_model_hidden": (_P, [_P]),
@@ -113,6 +120,8 @@ def _declare(L):
         "or_c_gemv_bf16": (None, [_P, _P, _P, _I, _I, _I, _P, _P]),
         "or_c_mxfp4_gemv": (None, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
         "or_c_rmsnorm": (None, [_P, _P, _I, _I, _F, _P]),
+        "or_c_gemv_bf16_ref": (None, [_P, _P, _P, _I, _I, _I, _P, _P]),
+        "or_c_mxfp4_gemv_ref": (None, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
         "or_attn_splits": (_I, [_I, _I]),
         "or_c_attn_decode": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _I, _P, _P]),
     }
@@ -166,6 +175,24 @@ def fill_scales(seed, stream, n, lo=119, rng=6) -> np.ndarray:
     out = np.empty(n, np.uint8)
     lib().or_fill_scales(seed, stream, n, lo, rng, _p(out))
     return out
+
+
+def fill_bytes_at(seed, stream, start, n) -> np.ndarray:
+    out = np.empty(n, np.uint8)
+    lib().or_fill_bytes_at(seed, stream, start, n, _p(out))
+    return out
+
+
+def fill_scales_at(seed, stream, start, n, lo=119, rng=6) -> np.ndarray:
+    out = np.empty(n, np.uint8)
+    lib().or_fill_scales_at(seed, stream, start, n, lo, rng, _p(out))
+    return out
+
+
+def set_accumulation(mode: int) -> None:
+    """0: canonical fp32 orders (default); 1: fp64 accumulation (for measuring
+    the model's sensitivity to summation order)."""
+    lib().or_set_accumulation(mode)
 
 
 def num_threads() -> int:
@@ -273,6 +300,19 @@ def moe_layer(x, rw, rb, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_b
     return out, idx, sc
 
 
+def moe_experts(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
+                E, H, I, k, alpha=1.702, limit=7.0):
+    """Given ids/weights [B][k]; a slot whose id lies outside [0, E) adds nothing."""
+    x = _c(x, np.uint16)
+    B = x.size // H
+    out = np.empty((B, H), np.uint16)
+    args = [_c(idx, np.int32), _c(score, np.float32), _c(gu_codes, np.uint8),
+            _c(gu_scales, np.uint8), _c(gu_bias, np.uint16), _c(dn_codes, np.uint8),
+            _c(dn_scales, np.uint8), _c(dn_bias, np.uint16)]
+    lib().or_moe_experts(_p(x), *[_p(a) for a in args], B, E, H, I, k, alpha, limit, _p(out))
+    return out
+
+
 def attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, T_max, pos, window):
     q, kc, vc, sinks = _c(q, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16), _c(sinks, np.uint16)
     pos = _c(pos, np.int32)
@@ -308,6 +348,28 @@ def c_mxfp4_gemv(codes, scales, bias, x, N, K):
     return y, yf
 
 
+def c_gemv_bf16_ref(W, bias, x, N, K):
+    """Scalar statement of c_gemv_bf16 (same bits, one lane at a time)."""
+    W, x = _c(W, np.uint16), _c(x, np.uint16)
+    B = x.size // K
+    bias = None if bias is None else _c(bias, np.uint16)
+    y = np.empty((B, N), np.uint16)
+    yf = np.empty((B, N), np.float32)
+    lib().or_c_gemv_bf16_ref(_p(W), _p(bias), _p(x), B, N, K, _p(y), _p(yf))
+    return y, yf
+
+
+def c_mxfp4_gemv_ref(codes, scales, bias, x, N, K):
+    """Scalar statement of c_mxfp4_gemv (same bits, one lane at a time)."""
+    codes, scales, x = _c(codes, np.uint8), _c(scales, np.uint8), _c(x, np.uint16)
+    B = x.size // K
+    bias = None if bias is None else _c(bias, np.uint16)
+    y = np.empty((B, N), np.uint16)
+    yf = np.empty((B, N), np.float32)
+    lib().or_c_mxfp4_gemv_ref(_p(codes), _p(scales), _p(bias), _p(x), B, N, K, _p(y), _p(yf))
+    return y, yf
+
+
 def c_rmsnorm(x, w, eps=1e-5):
     x, w = _c(x, np.uint16), _c(w, np.uint16)
     H = w.size
@@ -336,10 +398,16 @@ def c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, T_max, pos, window, S=None):
 class Model:
     """Random-init gpt-oss model (bit-identical weights to neon_init_random)."""
 
-    def __init__(self, cfg: OrConfig, seed: int, batch: int = 1):
+    LAZY_EXPERTS = 1
+
+    def __init__(self, cfg: OrConfig, seed: int, batch: int = 1, lazy_experts: bool = False):
+        """lazy_experts: keep no MXFP4 expert tensors; regenerate the chosen
+        experts each step (same bits; needed where the experts exceed host
+        memory, e.g. the 120b shape)."""
         self.cfg = cfg
         self.batch = batch
-        self._h = lib().or_model_create(C.byref(cfg), seed, batch)
+        flags = self.LAZY_EXPERTS if lazy_experts else 0
+        self._h = lib().or_model_create_ex(C.byref(cfg), seed, batch, flags)
         if not self._h:
             raise MemoryError("or_model_create failed")
 
@@ -357,6 +425,15 @@ class Model:
         lg = np.empty((self.batch, self.cfg.vocab), np.float32) if want_logits else None
         lib().or_model_step(self._h, _p(ids), _p(lg), _p(out))
         return out, lg
+
+    def set_tensor(self, layer, kind, data):
+        a = np.ascontiguousarray(data)
+        if lib().or_model_set_tensor(self._h, layer, kind, _p(a), a.nbytes) != 0:
+            raise ValueError(f"set_tensor(layer {layer}, kind {kind}): bad kind or size")
+
+    def fill_kv(self, n_pos, seed=1234):
+        """Synthetic N(0,1) KV history at positions 0..n_pos-1 (timing only)."""
+        lib().or_model_fill_kv(self._h, n_pos, seed)
 
     def hidden(self):
         p = lib().or_model_hidden(self._h)

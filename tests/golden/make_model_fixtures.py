@@ -1,0 +1,106 @@
+"""Writes tests/golden/model_fixtures.npz: the CPU oracle's greedy runs at the
+BASELINE shapes that take the oracle minutes (too long to run inside a GPU
+test).  Each case stores its inputs (seed, prompt ids) and, per generated
+token, the oracle's greedy id, the SHA-256 of its fp32 logits row (the GPU
+exact path is bit-identical to the oracle, so a digest is the whole check),
+the top-2 margin and the top-8 (id, value) pairs for diagnosis.
+
+Cases:
+  long20b   config 3: gpt-oss-20b shape, a 2048-token prompt uniform over the
+            vocab, then 64 greedy steps (batch 1).
+  b16_20b   config 3: gpt-oss-20b shape, 16 sequences of 8 prompt tokens,
+            then 32 greedy steps at batch 16.
+  l120b     config 4: gpt-oss-120b shape (36 layers, 128 experts; the oracle
+            regenerates each chosen expert from the counter RNG, so the
+            65 GB of experts never sit in host memory), 4 prompt tokens, then
+            24 greedy steps.
+
+Run: python tests/golden/make_model_fixtures.py [case ...]   (CPU only; the
+20b prompt case takes about 40 minutes on 8 cores).  Test infrastructure: it
+runs the oracle, never the product.
+"""
+import hashlib
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+from oracle import oracle as orc  # noqa: E402
+
+OUT = os.path.join(ROOT, "tests", "golden", "model_fixtures.npz")
+
+CASES = {
+    "long20b": dict(shape="20b", seed=0, batch=1, prompt_len=2048, steps=64, max_seq=2176,
+                    prompt_seed=2048),
+    "b16_20b": dict(shape="20b", seed=1, batch=16, prompt_len=8, steps=32, max_seq=64,
+                    prompt_seed=16),
+    "l120b": dict(shape="120b", seed=2, batch=1, prompt_len=4, steps=24, max_seq=64,
+                  prompt_seed=120),
+}
+
+
+def prompt_ids(case):
+    rng = np.random.default_rng(case["prompt_seed"])
+    return rng.integers(0, orc.GPT_OSS_20B["vocab"], (case["batch"], case["prompt_len"]),
+                        dtype=np.int32)
+
+
+def digest(row):
+    return np.frombuffer(hashlib.sha256(np.ascontiguousarray(row, np.float32).tobytes()).digest(),
+                         np.uint8)
+
+
+def run_case(name):
+    case = CASES[name]
+    shape = orc.GPT_OSS_20B if case["shape"] == "20b" else orc.GPT_OSS_120B
+    B = case["batch"]
+    cfg = orc.make_config(**dict(shape, max_seq=case["max_seq"], max_batch=B))
+    prompt = prompt_ids(case)
+    t0 = time.time()
+    m = orc.Model(cfg, seed=case["seed"], batch=B, lazy_experts=case["shape"] == "120b")
+    print(f"[{name}] model ready in {time.time() - t0:.0f}s", flush=True)
+    for t in range(case["prompt_len"] - 1):
+        m.step(prompt[:, t], want_logits=False)
+        if t % 128 == 0:
+            print(f"[{name}] prompt {t}/{case['prompt_len']} {time.time() - t0:.0f}s", flush=True)
+    ids = prompt[:, -1]
+    n = case["steps"] + 1
+    out_ids = np.zeros((B, n), np.int32)
+    sha = np.zeros((B, n, 32), np.uint8)
+    margin = np.zeros((B, n), np.float32)
+    top_id = np.zeros((B, n, 8), np.int32)
+    top_val = np.zeros((B, n, 8), np.float32)
+    for s in range(n):
+        ids, lg = m.step(ids)
+        for b in range(B):
+            order = np.argsort(-lg[b], kind="stable")[:8]
+            top_id[b, s] = order
+            top_val[b, s] = lg[b, order]
+            margin[b, s] = lg[b, order[0]] - lg[b, order[1]]
+            sha[b, s] = digest(lg[b])
+        out_ids[:, s] = ids
+        print(f"[{name}] step {s}/{n} ids {ids[:4]} {time.time() - t0:.0f}s", flush=True)
+    m.close()
+    return {f"{name}__{k}": v for k, v in dict(
+        prompt=prompt, ids=out_ids, sha=sha, margin=margin, top_id=top_id, top_val=top_val,
+        meta=np.array([case["seed"], B, case["prompt_len"], case["steps"], case["max_seq"],
+                       36 if case["shape"] == "120b" else 24], np.int64)).items()}
+
+
+def main(names):
+    data = {}
+    if os.path.exists(OUT):
+        with np.load(OUT, allow_pickle=False) as z:
+            data = {k: z[k] for k in z.files}
+    for name in names:
+        data = {k: v for k, v in data.items() if not k.startswith(name + "__")}
+        data.update(run_case(name))
+        np.savez_compressed(OUT, **data)
+        print(f"[{name}] written to {OUT}", flush=True)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:] or list(CASES))

@@ -244,10 +244,88 @@ def test_moe_layer_residual(orc):
     assert np.array_equal(to_host(out).reshape(-1), want)
 
 
+@pytest.mark.parametrize("B", [1, 4, 16, 20])
+def test_moe_experts_config0(orc, B):
+    """Caller-given ids / weights (the router's) through neon_moe_experts:
+    B = 1 runs the per-row kernels, 4 and 16 the grouped kernels (each used
+    expert read once for its rows), 20 (80 pairs) the per-row kernels again;
+    all bit-identical to the canonical per-row oracle."""
+    E, H, I, k = 32, 2880, 2880, 4
+    d = moe_inputs(orc, E, H, I, B, seed=4)
+    _, ridx, rsc = orc.moe_layer(d["x"], d["rw"], d["rb"], d["guc"], d["gus"], d["gub"],
+                                 d["dnc"], d["dns"], d["dnb"], E, H, I, k)
+    say(f"moe_experts config0 B={B}")
+    dv = {n: to_dev(v) for n, v in d.items()}
+    out = empty_dev((B, H), np.uint16)
+    act = empty_dev((B * k * I,), np.uint16)
+    ne.moe_experts(dv["x"], to_dev(ridx), to_dev(rsc), dv["guc"], dv["gus"], dv["gub"],
+                   dv["dnc"], dv["dns"], dv["dnb"], None, out, act, B, E, H, I, k)
+    ne.device_check()
+    want = orc.moe_experts(d["x"], ridx, rsc, d["guc"], d["gus"], d["gub"], d["dnc"], d["dns"],
+                           d["dnb"], E, H, I, k)
+    got = to_host(out)
+    say(f"  mismatches vs canonical oracle: {(got != want).sum()}/{got.size}")
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_moe_experts_drops_out_of_range_ids(orc, B):
+    """An expert id outside [0, E) in device memory: the slot is dropped (adds
+    0, no read past the expert arrays) and neon_device_check reports
+    NEON_EINVAL once; the other slots are unchanged."""
+    E, H, I, k = 8, 256, 512, 2
+    d = moe_inputs(orc, E, H, I, B, seed=5)
+    _, ridx, rsc = orc.moe_layer(d["x"], d["rw"], d["rb"], d["guc"], d["gus"], d["gub"],
+                                 d["dnc"], d["dns"], d["dnb"], E, H, I, k)
+    ridx = ridx.copy()
+    ridx[0, 1] = E          # one past the last expert
+    if B > 1:
+        ridx[B - 1, 0] = -1  # negative
+    dv = {n: to_dev(v) for n, v in d.items()}
+    out = empty_dev((B, H), np.uint16)
+    act = empty_dev((B * k * I,), np.uint16)
+    ne.device_check()  # clean start
+    ne.moe_experts(dv["x"], to_dev(ridx), to_dev(rsc), dv["guc"], dv["gus"], dv["gub"],
+                   dv["dnc"], dv["dns"], dv["dnb"], None, out, act, B, E, H, I, k)
+    with pytest.raises(ne.NeonError) as e:
+        ne.device_check()
+    assert e.value.status == ne.NEON_EINVAL
+    ne.device_check()  # the status word was cleared
+    want = orc.moe_experts(d["x"], ridx, rsc, d["guc"], d["gus"], d["gub"], d["dnc"], d["dns"],
+                           d["dnb"], E, H, I, k)
+    assert np.array_equal(to_host(out), want)
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+def test_moe_layer_config4(orc, B):
+    """BASELINE config 4's MoE: 128 experts, H = I = 2880, top-4, at batch 1,
+    16 and 64 (router + experts through neon_moe_layer): ids, weights and
+    outputs bit-identical to the canonical oracle."""
+    E, H, I, k = 128, 2880, 2880, 4
+    d = moe_inputs(orc, E, H, I, B, seed=6)
+    say(f"moe_layer config4 E={E} B={B}")
+    out = empty_dev((B, H), np.uint16)
+    idx, sc = empty_dev((B, k), np.int32), empty_dev((B, k), np.float32)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    ne.moe_layer(dv["x"], dv["rw"], dv["rb"], dv["guc"], dv["gus"], dv["gub"], dv["dnc"],
+                 dv["dns"], dv["dnb"], None, out, idx, sc, B, E, H, I, k)
+    ref, ridx, rsc = orc.moe_layer(d["x"], d["rw"], d["rb"], d["guc"], d["gus"], d["gub"],
+                                   d["dnc"], d["dns"], d["dnb"], E, H, I, k)
+    say(f"  distinct experts used: {len(np.unique(ridx))}")
+    assert np.array_equal(to_host(idx), ridx)
+    assert np.array_equal(to_host(sc).view(np.uint32), rsc.view(np.uint32))
+    got = to_host(out)
+    say(f"  mismatches vs canonical oracle: {(got != ref).sum()}/{got.size}")
+    assert np.array_equal(got, ref)
+
+
 @pytest.mark.parametrize("T,B,window,Tm", [
     (1, 1, 0, 1), (5, 2, 128, 5), (1024, 1, 0, 1024), (1024, 8, 128, 1024), (8192, 1, 0, 8192),
     (8192, 8, 128, 8192), (8192, 8, 0, 8192), (32768, 1, 0, 32768), (32768, 4, 128, 32768),
-    (300, 3, 0, 300), (1, 2, 128, 256), (3, 1, 0, 2048), (200, 2, 128, 4096)])
+    (300, 3, 0, 300), (1, 2, 128, 256), (3, 1, 0, 2048), (200, 2, 128, 4096),
+    # config 2 at batch 32
+    (1024, 32, 0, 1024), (1024, 32, 128, 1024), (8192, 32, 0, 8192), (8192, 32, 128, 8192),
+    (32768, 32, 0, 32768), (32768, 32, 128, 32768)])
 def test_attn_decode_config2(orc, T, B, window, Tm):
     """64 q / 8 kv heads, d=64, Q/K/V and sinks ~N(0,1) bf16 (T keys live in a
     cache of Tm rows; small T in a large cache leaves empty splits)."""

@@ -109,6 +109,34 @@ def test_moe_prefill_vs_oracle(orc, M, E, H, I, k):
     assert np.median(err) <= 2.0 ** -8 * np.sqrt((r ** 2).mean())
 
 
+def test_moe_prefill_drops_out_of_range_ids(orc):
+    """Ids outside [0, E) given to neon_moe_prefill: those pairs join no
+    expert group, add 0 in the combine, and neon_device_check reports
+    NEON_EINVAL; the other pairs match the oracle with the slots dropped."""
+    M, E, H, I, k = 37, 8, 256, 512, 2
+    d = moe_weights(orc, E, H, I, seed=4)
+    x = orc.fill_bf16(4, 51, M * H, 0.0, 1.0)
+    _, ridx, rsc = orc.moe_layer(x, d["rw"], d["rb"], d["guc"], d["gus"], d["gub"], d["dnc"],
+                                 d["dns"], d["dnb"], E, H, I, k)
+    ridx = ridx.copy()
+    ridx[3, 0], ridx[20, 1], ridx[36, 0] = E, -7, 1000
+    want = orc.moe_experts(x, ridx, rsc, d["guc"], d["gus"], d["gub"], d["dnc"], d["dns"],
+                           d["dnb"], E, H, I, k)
+    h = to_dev(np.zeros((M, H), np.uint16))
+    dv = {n: to_dev(v) for n, v in d.items()}
+    ne.device_check()
+    ne.moe_prefill(to_dev(x), to_dev(ridx), to_dev(rsc), dv["guc"], dv["gus"], dv["gub"],
+                   dv["dnc"], dv["dns"], dv["dnb"], h, M, E, H, I, k)
+    with pytest.raises(ne.NeonError) as e:
+        ne.device_check()
+    assert e.value.status == ne.NEON_EINVAL
+    got = orc.bf16_to_f32(to_host(h)).astype(np.float64)
+    r = orc.bf16_to_f32(want).astype(np.float64)
+    rel = np.abs(got - r).max() / np.abs(r).max()
+    say(f"moe_prefill with dropped ids: max error / max|ref| = {rel:.3e}")
+    assert rel < 2e-2
+
+
 @pytest.mark.parametrize("window", [0, 64])
 def test_attn_prefill_vs_oracle(orc, window):
     M, Hq, Hkv, D, T = 200, 8, 2, 64, 256
