@@ -234,6 +234,25 @@ neon_status neon_moe_layer(const uint16_t* x, const uint16_t* router_w,
                            int E, int H, int I, int k, float alpha,
                            float limit, void* stream);
 
+/* neon_moe_layer for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * same arguments and bit-identical results, but its scratch (expert
+ * activations and router logits) lives in a fixed 4 MiB device array per GPU
+ * that the library holds until the process ends, and it calls no allocator.
+ * Shapes needing more than 4 MiB (B*k*I*2 rounded up to 256 plus B*E*4 bytes)
+ * are rejected with NEON_EINVAL.  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams or threads) race.  No
+ * counterpart in the reference, which has no model code; it exists for
+ * callers that cannot allocate. */
+neon_status neon_moe_layer_noalloc(const uint16_t* x, const uint16_t* router_w,
+                                   const uint16_t* router_b, const uint8_t* gu_codes,
+                                   const uint8_t* gu_scales, const uint16_t* gu_bias,
+                                   const uint8_t* dn_codes, const uint8_t* dn_scales,
+                                   const uint16_t* dn_bias, const uint16_t* residual,
+                                   uint16_t* out, int32_t* idx, float* score, int B,
+                                   int E, int H, int I, int k, float alpha,
+                                   float limit, void* stream);
+
 /* Grouped expert FFN alone (HF GptOssExperts): for each row b and slot s,
  * expert e = idx[b][s]: gate_up GEMV -> SwiGLU-clamp -> down GEMV, weighted
  * by score[b][s] and summed over the k slots; out as in neon_moe_layer.

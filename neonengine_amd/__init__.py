@@ -33,7 +33,7 @@ EXPORTS = (
     "neon_rope_yarn", "neon_router_topk", "neon_moe_layer", "neon_moe_experts",
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
     "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
-    "neon_gemv_bf16_mfma", "neon_device_check",
+    "neon_gemv_bf16_mfma", "neon_device_check", "neon_moe_layer_noalloc",
 )
 
 
@@ -110,6 +110,7 @@ def lib():
             "neon_set_decode_mode": [_P, _I],
             "neon_gemv_bf16_mfma": [_P, _P, _P, _P, _I, _I, _I, _P],
             "neon_device_check": [_P],
+            "neon_moe_layer_noalloc": [_P] * 13 + [_I] * 5 + [_F, _F, _P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -208,6 +209,17 @@ def moe_layer(x, router_w, router_b, gu_codes, gu_scales, gu_bias, dn_codes, dn_
               dn_bias, residual, out, idx, score, B, E, H, I, k, alpha=1.702, limit=7.0,
               stream=None):
     _check(lib().neon_moe_layer(
+        _ptr(x), _ptr(router_w), _ptr(router_b), _ptr(gu_codes), _ptr(gu_scales),
+        _ptr(gu_bias), _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(residual),
+        _ptr(out), _ptr(idx), _ptr(score), B, E, H, I, k, alpha, limit, _stream(stream)))
+
+
+def moe_layer_noalloc(x, router_w, router_b, gu_codes, gu_scales, gu_bias, dn_codes,
+                      dn_scales, dn_bias, residual, out, idx, score, B, E, H, I, k,
+                      alpha=1.702, limit=7.0, stream=None):
+    """neon_moe_layer with its scratch in the library's fixed per-GPU array
+    (no allocation; overlapping calls on one GPU race)."""
+    _check(lib().neon_moe_layer_noalloc(
         _ptr(x), _ptr(router_w), _ptr(router_b), _ptr(gu_codes), _ptr(gu_scales),
         _ptr(gu_bias), _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(residual),
         _ptr(out), _ptr(idx), _ptr(score), B, E, H, I, k, alpha, limit, _stream(stream)))

@@ -1375,6 +1375,77 @@ extern "C" neon_status neon_moe_layer(
   return NEON_OK;
 }
 
+// ---- neon_moe_layer without allocation -----------------------------------
+// Scratch of neon_moe_layer_noalloc: a file-scope device array, one copy per
+// GPU, held until the process ends.  Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in symbol): it resolves the
+// device address once per device with hipGetSymbolAddress and uses that.
+constexpr size_t kNoAllocScratchBytes = (size_t)4 << 20;  // 4 MiB
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static char* g_scratch_ptr[256];
+
+// Device address of `scratch` on the current device (resolved on the first
+// call per device, with that device current).
+static neon_status scratch_address(char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256)
+    KFAIL(NEON_EHIP, "neon_moe_layer_noalloc: no current HIP device");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      KFAIL(NEON_EHIP, "neon_moe_layer_noalloc: hipGetSymbolAddress failed: %s",
+            hipGetErrorString(e));
+    g_scratch_ptr[dev] = (char*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_moe_layer_noalloc(
+    const uint16_t* x, const uint16_t* router_w, const uint16_t* router_b,
+    const uint8_t* gu_codes, const uint8_t* gu_scales, const uint16_t* gu_bias,
+    const uint8_t* dn_codes, const uint8_t* dn_scales, const uint16_t* dn_bias,
+    const uint16_t* residual, uint16_t* out, int32_t* idx, float* score, int B,
+    int E, int H, int I, int k, float alpha, float limit, void* stream) {
+  if (!x || !router_w || !router_b || !gu_codes || !gu_scales || !gu_bias ||
+      !dn_codes || !dn_scales || !dn_bias || !out)
+    KFAIL(NEON_EINVAL, "neon_moe_layer_noalloc: null pointer");
+  if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E ||
+      H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
+    KFAIL(NEON_EINVAL, "neon_moe_layer_noalloc: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H,
+          I, k);
+  // the same scratch as neon_moe_layer: act [B][k][I] bf16, then the router
+  // logits [B][E] fp32 (both written in full before they are read)
+  const size_t act_b = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
+  const size_t need = act_b + (size_t)B * E * 4;
+  if (need > kNoAllocScratchBytes)
+    KFAIL(NEON_EINVAL, "neon_moe_layer_noalloc: B=%d k=%d I=%d E=%d needs %zu scratch bytes, "
+          "above the fixed %zu (use neon_moe_layer)", B, k, I, E, need, kNoAllocScratchBytes);
+  char* base = nullptr;
+  const neon_status s = scratch_address(&base);
+  if (s != NEON_OK) return s;
+  hipStream_t st = S(stream);
+  uint16_t* act = (uint16_t*)base;
+  float* lg = (float*)(base + act_b);
+  RouterArgs r;
+  r.x = x; r.W = router_w; r.bias = router_b; r.lg_out = lg;
+  r.B = B; r.E = E; r.H = H; r.k = k;
+  launch_router(r, st);
+  MoeArgs m;
+  m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
+  m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
+  m.router_lg = lg; m.idx = nullptr; m.score = nullptr; m.idx_out = idx;
+  m.score_out = score; m.E = E; m.xn = x; m.act = act; m.residual = residual;
+  m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
+  m.err = nullptr;  // the ids come from the in-kernel top-k: always in [0, E)
+  launch_moe(m, st);
+  KLAUNCHED();
+}
+
 extern "C" neon_status neon_moe_experts(
     const uint16_t* x, const int32_t* idx, const float* score,
     const uint8_t* gu_codes, const uint8_t* gu_scales, const uint16_t* gu_bias,

@@ -105,6 +105,14 @@ def test_kernel_entry_points_validate_on_host():
                               None) == ne.NEON_EINVAL                              # I % 32
     assert L.neon_attn_prefill(p, p, p, p, p, 16, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
     assert L.neon_attn_prefill(p, p, p, p, p, 65, 64, 8, 64, 64, 0, None) == ne.NEON_EINVAL   # T_max < M
+    # the allocation-free MoE layer: same shape checks, plus its fixed 4 MiB
+    # scratch (B = 200 rows of 4 x 2880 activations need 4.6 MB); rejected on
+    # the host before any device call
+    assert L.neon_moe_layer_noalloc(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 0,
+                                    1.702, 7.0, None) == ne.NEON_EINVAL
+    assert L.neon_moe_layer_noalloc(*([p] * 9), None, p, None, None, 200, 32, 2880, 2880, 4,
+                                    1.702, 7.0, None) == ne.NEON_EINVAL
+    assert b"scratch" in L.neon_last_error(None)
     assert L.neon_set_prefill_mode(None, 0) == ne.NEON_EINVAL
     assert L.neon_mxfp4_dequant(None, p, 1, p, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_dequant(p, p, 0, p, None) == ne.NEON_OK  # empty is a no-op
