@@ -12,9 +12,12 @@ Weights, KV cache and token ids stay in HBM throughout.
 Printed: one JSON line with tokens/s (`value`), the whole-step fraction of
 the HBM roofline, and a `roofline` object for the MoE expert FFN (the MXFP4
 gate_up+SwiGLU and down+combine kernels), timed live with HIP events over
-launches that rotate through all 24 layers' expert weights (1.27 GB, beyond
-the 256 MB last-level cache).  `cpu_baseline` times the CPU oracle
-(oracle/, test infrastructure) on a bounded sample of the same workload.
+graph replays of the 24 layers' launch pairs with the experts their routers
+pick (1.27 GB of distinct weights, beyond the 256 MB last-level cache), next
+to a device-copy figure for the achievable HBM rate.  `cpu_baseline` times
+the CPU oracle (oracle/, test infrastructure) on a bounded sample of the same
+workload at the same KV length.  `--sweep gemv` / `--sweep attn` measure
+BASELINE configs 1 and 2 instead.
 """
 from __future__ import annotations
 
@@ -65,67 +68,233 @@ def moe_bytes(cfg) -> int:
 
 def time_moe(ne, torch, eng, cfg, reps: int):
     """Average duration of one expert-FFN launch pair (gate_up+SwiGLU, down+
-    combine) measured with HIP events on the launch stream."""
+    combine), batch 1, over all layers' experts (1.27 GB of distinct weights
+    per rotation, beyond the 256 MB last-level cache).  Each layer's experts
+    are the ones its own router picks for an N(0, 1) activation row
+    (neon_rmsnorm + neon_router_topk), and the 24 launch pairs are captured in
+    one graph, so consecutive kernels meet the same launch boundaries as in the
+    decode graph; the replays are timed with HIP events on the replay stream."""
     H, I, k, E, L = cfg.hidden, cfg.intermediate, cfg.top_k, cfg.n_experts, cfg.n_layers
     dev = "cuda"
     g = torch.Generator(device="cpu").manual_seed(0)
-    x = (torch.randn(H, generator=g) ).to(torch.bfloat16).to(dev)
+    x = torch.randn(H, generator=g).to(torch.bfloat16).view(torch.int16).to(dev)
     act = torch.empty(k * I, dtype=torch.int16, device=dev)
     out = torch.empty(H, dtype=torch.int16, device=dev)
-    score = torch.full((k,), 1.0 / k, dtype=torch.float32, device=dev)
-    idx = [torch.tensor([(l * 7 + s * (E // k)) % E for s in range(k)], dtype=torch.int32,
-                        device=dev) for l in range(L)]
-    ptrs = []
+    ptrs, xn, idx, score = [], [], [], []
     for l in range(L):
-        p = "model.layers.%d.mlp.experts." % l
-        ptrs.append([eng.tensor_ptr(p + n)[0] for n in (
+        p = "model.layers.%d." % l
+        w = {n: eng.tensor_ptr(p + n)[0] for n in (
+            "post_attention_layernorm.weight", "mlp.router.weight", "mlp.router.bias",
+            "mlp.experts.gate_up_proj_blocks", "mlp.experts.gate_up_proj_scales",
+            "mlp.experts.gate_up_proj_bias", "mlp.experts.down_proj_blocks",
+            "mlp.experts.down_proj_scales", "mlp.experts.down_proj_bias")}
+        xn.append(torch.empty(H, dtype=torch.int16, device=dev))
+        idx.append(torch.empty(k, dtype=torch.int32, device=dev))
+        score.append(torch.empty(k, dtype=torch.float32, device=dev))
+        ne.rmsnorm(x, w["post_attention_layernorm.weight"], xn[l], 1, H, cfg.rms_eps)
+        ne.router_topk(xn[l], w["mlp.router.weight"], w["mlp.router.bias"], idx[l], score[l],
+                       None, 1, E, H, k)
+        ptrs.append([w["mlp.experts." + n] for n in (
             "gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
             "down_proj_blocks", "down_proj_scales", "down_proj_bias")])
+    ne.device_check()  # also sets up the status word before the capture
+
+    def launch_all():
+        for l in range(L):
+            gc, gs, gb, dc, ds, db = ptrs[l]
+            ne.moe_experts(xn[l], idx[l], score[l], gc, gs, gb, dc, ds, db, None, out, act,
+                           1, E, H, I, k, cfg.swiglu_alpha, cfg.swiglu_limit)
+
+    launch_all()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_all()
     stream = torch.cuda.current_stream()
-
-    def launch(l):
-        gc, gs, gb, dc, ds, db = ptrs[l]
-        ne.moe_experts(x, idx[l], score, gc, gs, gb, dc, ds, db, None, out, act,
-                       1, E, H, I, k, cfg.swiglu_alpha, cfg.swiglu_limit, stream)
-
-    for l in range(L):
-        launch(l)
+    for _ in range(2):
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(reps):
-        for l in range(L):
-            launch(l)
+        graph.replay()
     e1.record(stream)
     e1.synchronize()
     return e0.elapsed_time(e1) / (reps * L) * 1e-3  # seconds per launch pair
 
 
-def cpu_baseline(seed: int, prompt_len: int, steps: int):
-    """Build's CPU oracle (scalar C + OpenMP) on a bounded sample: a short
-    prompt then `steps` greedy decode steps of the same 20b-shaped model."""
+def cpu_info():
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return dict(cpu_model=model, nproc=os.cpu_count(), usable_cpus=usable)
+
+
+def cpu_baseline(seed: int, kv_len: int, steps: int):
+    """The build's CPU oracle (C, OpenMP over the rows of each GEMV) decoding
+    the same 20b-shaped model at the GPU line's KV length: a synthetic
+    N(0, 1) KV history of kv_len positions in every layer, then `steps`
+    greedy decode steps (one warm-up step untimed)."""
     import numpy as np
     from oracle import oracle as orc
     if not os.path.exists(orc._LIB_PATH):
         orc.build()
-    cfg = orc.make_config(max_seq=prompt_len + steps + 1)
+    cfg = orc.make_config(max_seq=kv_len + steps + 2)
     t0 = time.perf_counter()
     m = orc.Model(cfg, seed=seed, batch=1)
+    m.fill_kv(kv_len)
     gen_s = time.perf_counter() - t0
-    ids = np.array([101], np.int32)
-    for t in range(prompt_len):
-        ids, _ = m.step(np.array([(7919 * t + 101) % cfg.vocab], np.int32), want_logits=False)
+    ids, _ = m.step(np.array([101], np.int32), want_logits=False)
     t0 = time.perf_counter()
     for _ in range(steps):
         ids, _ = m.step(ids, want_logits=False)
     dt = time.perf_counter() - t0
     m.close()
+    info = cpu_info()
     return dict(value=round(steps / dt, 4), unit="tokens/s", cores=orc.num_threads(),
                 kind="port",
-                sample=f"build's CPU oracle, gpt-oss-20b shape, {steps} greedy decode steps "
-                       f"after a {prompt_len}-token prompt (KV length <= {prompt_len + steps}; "
-                       f"weight generation {gen_s:.1f}s untimed); label: build's CPU oracle, "
-                       f"not the reference")
+                sample=f"build's CPU oracle, gpt-oss-20b shape, {steps} greedy decode steps at "
+                       f"KV length {kv_len + 1}..{kv_len + steps} (synthetic KV history; weight "
+                       f"generation {gen_s:.1f}s untimed); label: build's CPU oracle, not the "
+                       f"reference", **info)
+
+
+def hbm_copy_peak(torch, nbytes=1 << 30, reps=5):
+    """Achievable HBM bandwidth: a plain device copy of nbytes (read + write)."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    del src, dst
+    return round(2 * nbytes / t / 1e9, 1)
+
+
+def graph_time(torch, calls, reps):
+    """Seconds per call: the calls captured once into a graph (so host launch
+    overhead does not gap the kernels), replayed `reps` times between HIP
+    events on the replay stream."""
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (reps * len(calls))
+
+
+def eager_time(torch, calls, reps):
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for c in calls:
+            c()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (reps * len(calls))
+
+
+def rotation(nbytes_one, want=1 << 30, cap=4 << 30):
+    """Copies of a working set so that one rotation reads >= `want` distinct
+    bytes (past the 256 MB last-level cache), at most `cap` bytes in all."""
+    n = max(1, -(-want // nbytes_one))
+    return max(1, min(n, cap // nbytes_one))
+
+
+def sweep_gemv(ne, torch, reps=20):
+    """MXFP4 GEMV [N x 2880] (codes uniform, E8M0 exponent
+    uniform in [-8, -3]) times a bf16 batch, N in {2880, 5760, 4096}, batch
+    in {1, 4, 16, 64}, rotating >= 1 GB of distinct weight copies."""
+    K, out = 2880, []
+    for N in (2880, 5760, 4096):
+        mb = N * K * 17 // 32
+        n = rotation(mb)
+        codes = torch.randint(0, 256, (n, N * K // 2), dtype=torch.uint8, device="cuda")
+        scales = torch.randint(119, 125, (n, N * K // 32), dtype=torch.uint8, device="cuda")
+        for B in (1, 4, 16, 64):
+            x = torch.randn(B, K, device="cuda").to(torch.bfloat16).view(torch.int16)
+            y = torch.empty(B, N, dtype=torch.int16, device="cuda")
+
+            calls = [lambda i=i: ne.mxfp4_gemv(codes[i], scales[i], None, x, y, N, K, B)
+                     for i in range(n)]
+            t = graph_time(torch, calls, reps)
+            byt = mb + 2 * B * (K + N)
+            out.append(dict(N=N, K=K, B=B, us=round(t * 1e6, 3), bytes=byt,
+                            gbs=round(byt / t / 1e9, 1), frac=round(byt / t / 1e9 / HBM_PEAK_GBS, 4),
+                            tflops=round(2 * N * K * B / t / 1e12, 3), copies=n))
+            log(f"[bench] gemv N={N} B={B}: {t * 1e6:.2f} us, {byt / t / 1e9:.0f} GB/s "
+                f"({n} weight copies)")
+        del codes, scales
+    return out
+
+
+def sweep_attn(ne, torch, reps=10):
+    """sink attention decode, 64 q / 8 kv heads, d = 64,
+    bf16 q / k / v / sinks ~ N(0, 1), KV length T in {1024, 8192, 32768},
+    batch in {1, 8, 32}, sliding-128 and full layers; >= 1 GB of distinct
+    caches per rotation where it fits in 4 GB (sliding windows move with the
+    position, so consecutive launches read different keys)."""
+    Hq, Hkv, D, out = 64, 8, 64, []
+    for T in (1024, 8192, 32768):
+        for B in (1, 8, 32):
+            cache = B * Hkv * T * D * 2  # one of K / V
+            n = rotation(2 * cache)
+            kc = torch.randn(n, B * Hkv * T * D, device="cuda").to(torch.bfloat16).view(torch.int16)
+            vc = torch.randn(n, B * Hkv * T * D, device="cuda").to(torch.bfloat16).view(torch.int16)
+            q = torch.randn(B, Hq * D, device="cuda").to(torch.bfloat16).view(torch.int16)
+            sinks = torch.randn(Hq, device="cuda").to(torch.bfloat16).view(torch.int16)
+            o = torch.empty(B, Hq * D, dtype=torch.int16, device="cuda")
+            for window in (128, 0):
+                npos = 16 if window else 1
+                pos = [torch.full((B,), T - 1 - 129 * j if window else T - 1, dtype=torch.int32,
+                                  device="cuda") for j in range(npos)]
+
+                calls = [lambda c=c: ne.attn_decode(q, kc[c % n], vc[c % n], sinks, pos[c % npos],
+                                                    o, B, Hq, Hkv, D, T, window)
+                         for c in range(max(n, npos))]
+                try:
+                    t, how = graph_time(torch, calls, reps), "graph"
+                except Exception as exc:  # capture refused: time eager launches
+                    log(f"[bench] graph capture of attn_decode failed ({exc}); eager timing")
+                    t, how = eager_time(torch, calls, reps), "eager"
+                t_eff = min(T, window) if window else T
+                byt = B * t_eff * 2048 + 2 * B * Hq * D * 2
+                out.append(dict(T=T, B=B, window=window, us=round(t * 1e6, 3), bytes=byt,
+                                gbs=round(byt / t / 1e9, 1),
+                                frac=round(byt / t / 1e9 / HBM_PEAK_GBS, 4), copies=n,
+                                timing=how))
+                log(f"[bench] attn T={T} B={B} window={window}: {t * 1e6:.2f} us, "
+                    f"{byt / t / 1e9:.0f} GB/s ({n} cache copies)")
+            del kc, vc
+    return out
 
 
 COPY_BYTES = 256 << 20
@@ -195,7 +364,10 @@ def main():
     ap.add_argument("--matrix", action="store_true",
                     help="run steps of 2+ sequences on the matrix cores (NEON_DECODE_MATRIX)")
     ap.add_argument("--moe-reps", type=int, default=20)
-    ap.add_argument("--cpu-steps", type=int, default=48)
+    ap.add_argument("--cpu-steps", type=int, default=12)
+    ap.add_argument("--sweep", choices=["gemv", "attn"],
+                    help="BASELINE config 1 (MXFP4 GEMV) or config 2 (sink attention) sweep "
+                         "instead of the decode benchmark; prints one JSON line")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prompt-only", type=int, default=0, metavar="N",
                     help="profiling aid: run the matrix-core prompt pass N times and exit")
@@ -221,6 +393,11 @@ def main():
     torch.cuda.set_device(0)
     if args.moe_only:
         moe_only(ne, torch, args)
+        return
+    if args.sweep:
+        pts = sweep_gemv(ne, torch) if args.sweep == "gemv" else sweep_attn(ne, torch)
+        print(json.dumps({"sweep": args.sweep, "config": 1 if args.sweep == "gemv" else 2,
+                          "peak_gbs": HBM_PEAK_GBS, "points": pts}), flush=True)
         return
     if args.prompt_only:
         cfg = ne.config_preset(args.model, max_seq=args.prompt + 8, max_batch=1)
@@ -319,11 +496,15 @@ def main():
         log(f"[bench] MoE expert FFN: {moe_s * 1e6:.2f} us per launch pair, {moe_gbs:.0f} GB/s")
     eng.close()
 
+    copy_gbs = hbm_copy_peak(torch) if headline else None
+    if copy_gbs:
+        log(f"[bench] device copy (1 GiB read + 1 GiB write): {copy_gbs:.0f} GB/s")
     cpu = None
     if not args.no_cpu_baseline and headline:
         log("[bench] CPU baseline (build's oracle) ...")
-        cpu = cpu_baseline(args.seed, 4, args.cpu_steps)
-        log(f"[bench] CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads")
+        cpu = cpu_baseline(args.seed, kv_mid, args.cpu_steps)
+        log(f"[bench] CPU baseline {cpu['value']} tok/s on {cpu['cores']} threads "
+            f"({cpu['cpu_model']}, {cpu['usable_cpus']} usable of {cpu['nproc']})")
 
     line = {
         "metric": METRIC,
@@ -353,7 +534,9 @@ def main():
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": moe_gbs and round(moe_gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic() if moe_gbs else None, "bytes_per_launch": mb,
-                     "us_per_launch": moe_s and round(moe_s * 1e6, 3)},
+                     "us_per_launch": moe_s and round(moe_s * 1e6, 3),
+                     "achievable_copy_gbs": copy_gbs,
+                     "frac_of_copy": moe_gbs and copy_gbs and round(moe_gbs / copy_gbs, 4)},
         "cpu_baseline": cpu,
         "prefill": prefill,
     }

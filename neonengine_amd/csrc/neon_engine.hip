@@ -84,6 +84,7 @@ struct neon_ctx {
   int32_t *tokens = nullptr, *pos = nullptr, *prompt_len = nullptr,
           *last_ids = nullptr;
   int32_t* dev_err = nullptr;  // status word the step's kernels set (kDevErr* bits)
+  int32_t* moe_sync = nullptr;  // [L][kMoeSyncInts] counters of the one-launch experts
   int tok_stride = 0;
   int lm_nblk = 0;
   int s_full = 1, s_slide = 1;
@@ -106,6 +107,11 @@ struct neon_ctx {
   float* sample_scratch = nullptr;  // [max_batch][vocab] exp values
   // batched steps on the matrix cores (max_batch >= 2)
   int decode_mode = NEON_DECODE_EXACT;
+  // batch-1 experts as one launch with a grid-wide wait (k_moe_fused) when
+  // NEON_MOE_FUSED=1; the default is the gate_up / down kernel pair, which
+  // measured faster on MI355X (the in-kernel wait plus every block fetching
+  // act past its L2 cost more than the kernel boundary they replace)
+  bool fused_moe = getenv("NEON_MOE_FUSED") && getenv("NEON_MOE_FUSED")[0] == '1';
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -397,6 +403,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
                o_pl = take(Bm * 4), o_last = take(Bm * 4), o_err = take(4),
+               o_msync = take(L * kMoeSyncInts * 4),
                o_cos = take((size_t)c.max_seq * half * 4),
                o_sin = take((size_t)c.max_seq * half * 4);
   if (hipMalloc(&ctx->work, off) != hipSuccess) {
@@ -417,6 +424,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
   ctx->last_ids = (int32_t*)(W + o_last); ctx->cos_t = (float*)(W + o_cos);
   ctx->dev_err = (int32_t*)(W + o_err);
+  ctx->moe_sync = (int32_t*)(W + o_msync);
   ctx->sin_t = (float*)(W + o_sin);
   ctx->row_pos = (int32_t*)(W + o_rpos); ctx->row_seq = (int32_t*)(W + o_rseq);
   ctx->sample_scratch = (float*)(W + o_samp);
@@ -663,6 +671,10 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
     r.idx = grouped ? ctx->moe_idx : nullptr; r.score = grouped ? ctx->moe_score : nullptr;
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
+    // batch 1: the experts run as one launch whose arrival counters the
+    // router zeroes first
+    int32_t* sync = B == 1 && ctx->fused_moe ? ctx->moe_sync + (size_t)l * kMoeSyncInts : nullptr;
+    r.zero = sync; r.zero_n = sync ? kMoeSyncZero : 0;
     launch_router(r, st);
     MoeArgs m;
     m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
@@ -673,6 +685,7 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     m.E = c.n_experts; m.xn = ctx->xn; m.act = ctx->act;
     m.residual = ctx->h; m.out = ctx->h; m.B = B; m.H = H; m.I = c.intermediate;
     m.k = c.top_k; m.alpha = c.swiglu_alpha; m.limit = c.swiglu_limit; m.err = ctx->dev_err;
+    m.sync = sync;
     if (grouped && moe_batched_supported(m)) launch_moe_batched(m, st);
     else launch_moe(m, st);
   }
@@ -1119,6 +1132,9 @@ static neon_status check_dev_err(neon_ctx* ctx) {
   HIPCHK(ctx, hipMemcpy(&bits, ctx->dev_err, 4, hipMemcpyDeviceToHost));
   if (bits == 0) return NEON_OK;
   HIPCHK(ctx, hipMemset(ctx->dev_err, 0, 4));
+  if (bits & kDevErrSyncTimeout)
+    FAIL(ctx, NEON_EHIP, "a grid-wide wait inside a kernel timed out (status bits 0x%x); "
+         "the step's results are invalid", bits);
   FAIL(ctx, NEON_EINVAL, "a kernel of this context saw an expert id outside [0, %d) "
        "(status bits 0x%x); that slot was dropped", ctx->cfg.n_experts, bits);
 }
@@ -1226,6 +1242,9 @@ extern "C" neon_status neon_device_check(void* stream) {
     KFAIL(NEON_EHIP, "neon_device_check: status read failed");
   if (bits == 0) return NEON_OK;
   if (hipMemset(w, 0, 4) != hipSuccess) KFAIL(NEON_EHIP, "neon_device_check: status clear failed");
+  if (bits & kDevErrSyncTimeout)
+    KFAIL(NEON_EHIP, "a grid-wide wait inside a kernel-level call timed out (status bits 0x%x); "
+          "its results are invalid", bits);
   KFAIL(NEON_EINVAL, "a kernel-level call saw an expert id outside [0, E) (status bits 0x%x); "
         "that slot was dropped", bits);
 }
@@ -1350,16 +1369,20 @@ extern "C" neon_status neon_moe_layer(
       H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
     KFAIL(NEON_EINVAL, "neon_moe_layer: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
   hipStream_t st = S(stream);
-  // scratch: act [B][k][I] bf16, then the router logits [B][E]
+  // scratch: act [B][k][I] bf16, the router logits [B][E], and the arrival
+  // counters of the one-launch experts (batch 1)
   const size_t act_b = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
+  const size_t lg_b = ((size_t)B * E * 4 + 255) & ~(size_t)255;
   char* scratch = nullptr;
-  if (hipMallocAsync((void**)&scratch, act_b + (size_t)B * E * 4, st) != hipSuccess)
+  if (hipMallocAsync((void**)&scratch, act_b + lg_b + kMoeSyncInts * 4, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_moe_layer: scratch allocation failed");
   uint16_t* act = (uint16_t*)scratch;
   float* lg = (float*)(scratch + act_b);
+  int32_t* sync = (int32_t*)(scratch + act_b + lg_b);
   RouterArgs r;
   r.x = x; r.W = router_w; r.bias = router_b; r.lg_out = lg;
   r.B = B; r.E = E; r.H = H; r.k = k;
+  r.zero = sync; r.zero_n = kMoeSyncZero;
   launch_router(r, st);
   MoeArgs m;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
@@ -1368,6 +1391,7 @@ extern "C" neon_status neon_moe_layer(
   m.score_out = score; m.E = E; m.xn = x; m.act = act; m.residual = residual;
   m.out = out; m.B = B; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
   m.err = device_status_word();
+  m.sync = getenv("NEON_MOE_FUSED") && getenv("NEON_MOE_FUSED")[0] == '1' ? sync : nullptr;
   launch_moe(m, st);
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);

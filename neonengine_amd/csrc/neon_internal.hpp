@@ -106,13 +106,20 @@ struct RouterArgs {
   int32_t* idx = nullptr;            // top-k outputs (NULL: logits only)
   float* score = nullptr;
   int B = 1, E = 0, H = 0, k = 0;
+  // zeroed by block (0, 0) before anything else (the counters of the
+  // one-launch expert kernel that follows), may be NULL
+  int32_t* zero = nullptr;
+  int zero_n = 0;
 };
 // router logits, then (when a.idx) the top-k / softmax
 void launch_router(const RouterArgs& a, hipStream_t st);
 
 // Status bits a kernel sets (vector atomicOr) in the caller's status word
 // when its input breaks a precondition it can only see on the device.
-constexpr int32_t kDevErrExpertId = 1;  // an expert id outside [0, E)
+constexpr int32_t kDevErrExpertId = 1;      // an expert id outside [0, E)
+constexpr int32_t kDevErrSyncTimeout = 2;   // a grid-wide wait gave up (results invalid)
+// polls a grid-wide wait makes before it gives up (~1 s)
+constexpr int kMoeSpinLimit = 1 << 20;
 
 struct MoeArgs {
   int32_t* err = nullptr;    // status word (kDevErr* bits), may be NULL
@@ -130,8 +137,21 @@ struct MoeArgs {
   uint16_t* out;             // [B][H]
   int B, H, I, k;
   float alpha, limit;
+  // batch 1: kMoeSyncShards zeroed int32 counters enable the one-launch
+  // expert kernel (k_moe_fused); NULL keeps the two-kernel form
+  int32_t* sync = nullptr;
 };
 void launch_moe(const MoeArgs& a, hipStream_t st);
+// the one-launch form (batch 1, k <= 4, I % 4 == 0, sync given); returns
+// false when it does not apply (nothing launched)
+bool moe_fused_supported(const MoeArgs& a);
+bool launch_moe_fused(const MoeArgs& a, hipStream_t st);
+constexpr int kMoeSyncWords = 32;    // arrival counter shards per fused launch,
+constexpr int kMoeGoCopies = 8;      // then the copies of its go flag,
+constexpr int kMoeSyncStride = 64;   // each on its own 256-byte line (in int32)
+constexpr int kMoeSyncInts = (kMoeSyncWords + kMoeGoCopies) * kMoeSyncStride;
+constexpr int kMoeSyncZero = kMoeSyncWords + kMoeGoCopies;  // words to zero
+constexpr int kMoeFusedMaxUnits = 96;  // H / 32 of the one-launch experts (H <= 3072)
 
 // ---- batched decode on the matrix cores (neon_mx.hip) ----------------------
 constexpr int kMxMaxRows = 64;   // rows per step

@@ -1465,8 +1465,9 @@ __global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
     const uint16_t* __restrict__ bias, float* __restrict__ lg_out, int E,
-    int H) {
+    int H, int32_t* __restrict__ zero, int zero_n) {
   const int e = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  if (e == 0 && b == 0 && lane < zero_n) zero[(size_t)lane * kMoeSyncStride] = 0;
   const int U = H / 8;
   const uint16_t bias_e = bias[e];  // bias, x and norm loads first, then the row
   XBf16Raw<P> xraw;
@@ -1537,11 +1538,11 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
     if (a.norm_w != nullptr)                                                     \
       hipLaunchKernelGGL((k_router_logits<PP, true>), grid, dim3(64), 0, st, a.x, \
                          a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E,  \
-                         a.H);                                                   \
+                         a.H, a.zero, a.zero_n);                                 \
     else                                                                         \
       hipLaunchKernelGGL((k_router_logits<PP, false>), grid, dim3(64), 0, st,    \
                          a.x, a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out,  \
-                         a.E, a.H);                                              \
+                         a.E, a.H, a.zero, a.zero_n);                            \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)
@@ -2024,6 +2025,416 @@ __global__ __launch_bounds__(256) void k_moe_down_bt(
   }
 }
 
+// ===========================================================================
+// The expert FFN of one row in ONE launch (batch 1): the work of k_moe_gate_up
+// and k_moe_down with a grid-wide wait between them instead of a kernel
+// boundary, so down's weight rows are already on their way while the last
+// gate_up columns finish.  Every dot product is the batch-1 kernels' (same
+// lane units and butterflies), so the output bits are the same.
+//
+//   1. each block routes (wave 0) and loads x once;
+//   2. gate_up: wave task t = (slot, 4 intermediate columns), tasks dealt
+//      round-robin over the grid's waves; the 4 act values of a task are
+//      published with one 8-byte agent-scope store (it completes at the
+//      device's coherence point, past this XCD's L2);
+//   3. each wave waits for its stores (vmcnt 0), the block arrives on one of
+//      kMoeSyncWords counters (agent-scope atomic add);
+//   4. down: block task d = 4 output rows, wave = slot; the task's weight rows
+//      are requested, then wave 0 polls the counters until all gridDim.x
+//      blocks have arrived (a bounded spin: on time-out it flags
+//      kDevErrSyncTimeout and goes on, so every wave exits), then act is read
+//      with agent-scope loads and the slots are combined as in k_moe_down.
+// The grid must be co-resident (the host caps it at the occupancy limit), so
+// every block that others wait for is running.  The counters must be 0 at
+// launch (the router kernel before it zeroes them).
+// ===========================================================================
+// 16 bytes written by other blocks of this launch: two 8-byte agent-scope
+// loads, served at the coherence point rather than from this XCD's L2.
+__device__ __forceinline__ uint4 load_agent16(const uint16_t* p) {
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+
+// How the down phase reads act after the grid-wide wait: false = agent-scope
+// loads (each block fetches its own copy past the L2; measured 3.2 us after
+// the wait at the 20b shape); true = one agent-scope acquire (L1/L2
+// invalidate) per block, then plain loads that the XCD's L2 serves to all its
+// blocks (measured 5.6 us: the invalidations cost more than they share).
+#ifndef NEON_ACT_ACQUIRE
+#define NEON_ACT_ACQUIRE 0
+#endif
+constexpr bool kActAcquire = NEON_ACT_ACQUIRE != 0;
+
+// x_fp4_issue / x_fp4_issue_pair over agent-scope loads
+template <int P, bool PAIR>
+__device__ __forceinline__ void x_fp4_issue_agent(uint4 (&raw)[P][4],
+                                                  const uint16_t* __restrict__ x, int U,
+                                                  int lane) {
+  const int r = U - 64 * (P - 1);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    int u;
+    if (PAIR) u = p < P - 1 ? lane + 64 * p : 64 * (P - 1) + min(lane >= r ? lane - r : lane, r - 1);
+    else u = min(lane + 64 * p, U - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      raw[p][q] = kActAcquire ? reinterpret_cast<const uint4*>(x)[u * 4 + q]
+                              : load_agent16(x + (size_t)(u * 4 + q) * 8);
+  }
+}
+
+__device__ __forceinline__ int wave_isum(int v) {
+  v += xor_lane_i<32>(v);
+  v += xor_lane_i<16>(v);
+  v += xor_lane_i<8>(v);
+  v += xor_lane_i<4>(v);
+  v += xor_lane_i<2>(v);
+  v += xor_lane_i<1>(v);
+  return v;
+}
+
+// Grid-wide wait of the one-launch kernels.  Layout of the sync words (all
+// zero at launch): arrival shard s at ctr[s * kMoeSyncStride], s <
+// kMoeSyncWords, then go flag copy c at ctr[(kMoeSyncWords + c) *
+// kMoeSyncStride], c < kMoeGoCopies, each word on its own 256-byte line, so
+// the arrivals and the polls do not queue on one line.
+//
+// Block 0's wave 0 is the aggregator: it polls the shards until they add up
+// to `target` and then sets every go copy; every other block's wave 0 polls
+// one go copy, with a back-off (its polls compete with the weight streams).
+// Both loops are bounded (spin_limit polls); false on time-out.
+__device__ __forceinline__ bool wave_wait_grid(int32_t* ctr, int target, int spin_limit,
+                                               int lane) {
+  if (blockIdx.x == 0) {
+    const int32_t* mine = ctr + (size_t)min(lane, kMoeSyncWords - 1) * kMoeSyncStride;
+    for (int it = 0; it < spin_limit; ++it) {
+      const int v = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (wave_isum(lane < kMoeSyncWords ? v : 0) >= target) {  // uniform
+        if (lane < kMoeGoCopies)
+          __hip_atomic_store(ctr + (size_t)(kMoeSyncWords + lane) * kMoeSyncStride, 1,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+  }
+  const int32_t* go = ctr + (size_t)(kMoeSyncWords + blockIdx.x % kMoeGoCopies) * kMoeSyncStride;
+  for (int it = 0; it < spin_limit; ++it) {
+    if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return true;
+    __builtin_amdgcn_s_sleep(8);
+  }
+  return false;
+}
+
+template <int P, bool PAIR>
+__global__ __launch_bounds__(256) void k_moe_fused(
+    const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,
+    const uint16_t* __restrict__ gu_bias, const uint8_t* __restrict__ dn_codes,
+    const uint8_t* __restrict__ dn_scales, const uint16_t* __restrict__ dn_bias,
+    const float* __restrict__ router_lg, const int32_t* __restrict__ idx,
+    const float* __restrict__ score, int32_t* __restrict__ idx_out,
+    float* __restrict__ score_out, int E, const uint16_t* __restrict__ xn, uint16_t* act,
+    const uint16_t* residual, uint16_t* out, int H, int I, int k, float alpha, float limit,
+    int32_t* __restrict__ err, int32_t* sync, int spin_limit) {
+  __shared__ TopK tk;
+  __shared__ float red[kMaxTopK][kMoeRpw];
+  // x in fp32, unit u's 32 elements at xs[u * 33 ..]: the lanes of a wave read
+  // 64 different units at one element, 33 floats apart (all 64 banks)
+  __shared__ float xs[kMoeFusedMaxUnits * 33];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int Ug = H / 32, Ud = I / 32;
+  // ---- routing (wave 0, with weights) and x, loaded once ----
+  RouteRaw rr;
+  if (wave == 0) moe_route_issue<true>(router_lg, idx, score, 0, E, k, lane, rr);
+  for (int i = threadIdx.x; i < H / 8; i += 256) {  // 8 elements per thread and step
+    const uint4 v = reinterpret_cast<const uint4*>(xn)[i];
+    float f[8];
+    unpack8(v, f);
+    const int u = i >> 2, e0 = (i & 3) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[u * 33 + e0 + j] = f[j];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) {
+    (void)moe_route_finish<true>(router_lg, E, k, 0, lane, rr, tk);
+    if (blockIdx.x == 0 && idx_out != nullptr && lane < k) {
+      idx_out[lane] = tk.id[lane];
+      score_out[lane] = tk.sc[lane];
+    }
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    bool bad = false;
+    for (int s = 0; s < k; ++s) bad |= (unsigned)tk.id[s] >= (unsigned)E;
+    if (bad) flag_dev_err(err, kDevErrExpertId);
+  }
+  // ---- gate_up + SwiGLU, 4 columns per wave task ----
+  const int tiles = I / kMoeJpw;  // I % 4 == 0 (host-checked)
+  const size_t rows = (size_t)2 * I;
+  for (int t = blockIdx.x * 4 + wave; t < k * tiles; t += gridDim.x * 4) {
+    const int slot = t / tiles, j0 = (t % tiles) * kMoeJpw;
+    const int e = tk.id[slot];
+    if ((unsigned)e >= (unsigned)E) continue;  // dropped slot (uniform)
+    const uint8_t* codes = gu_codes + (size_t)e * rows * (H / 2);
+    const uint8_t* scales = gu_scales + (size_t)e * rows * Ug;
+    const uint16_t* bias = gu_bias + (size_t)e * rows;
+    const uint32_t bgu =
+        load_pinned_u32(reinterpret_cast<const uint32_t*>(bias + 2 * (j0 + (lane >> 4))));
+    float a[2 * kMoeJpw];
+    if constexpr (PAIR) {
+      Fp4RowPair<P> rp[kMoeJpw];
+#pragma unroll
+      for (int c = 0; c < kMoeJpw; ++c) {
+        const int row = 2 * (j0 + c);
+        fp4_load_pair<P>(rp[c], codes + (size_t)row * (H / 2), scales + (size_t)row * Ug,
+                         codes + (size_t)(row + 1) * (H / 2), scales + (size_t)(row + 1) * Ug,
+                         Ug, lane);
+      }
+      // every row load issued before any use (else the scheduler waits for
+      // the first pass's loads before it issues the rest: one memory round
+      // trip per pass)
+      __builtin_amdgcn_sched_barrier(0);
+      // the rows' lane partials pass by pass (the same per-row order as
+      // fp4_pair_partials), x of each pass read from LDS when it is needed
+      const int r_tail = Ug - 64 * (P - 1);
+#pragma unroll
+      for (int c = 0; c < kMoeJpw; ++c) { a[2 * c] = 0.0f; a[2 * c + 1] = 0.0f; }
+#pragma unroll
+      for (int p = 0; p < P - 1; ++p) {
+        float xp[32];
+        const float* src = xs + (lane + 64 * p) * 33;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) xp[j] = src[j];
+#pragma unroll
+        for (int c = 0; c < kMoeJpw; ++c) {
+          a[2 * c] = __fadd_rn(a[2 * c], e8m0_scale(fp4_unit_dot(rp[c].c[0][p], xp), rp[c].s[0][p]));
+          a[2 * c + 1] =
+              __fadd_rn(a[2 * c + 1], e8m0_scale(fp4_unit_dot(rp[c].c[1][p], xp), rp[c].s[1][p]));
+        }
+      }
+      {
+        float xp[32];
+        const int ut = 64 * (P - 1) + min(lane >= r_tail ? lane - r_tail : lane, r_tail - 1);
+        const float* src = xs + ut * 33;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) xp[j] = src[j];
+#pragma unroll
+        for (int c = 0; c < kMoeJpw; ++c) {
+          const float tt = e8m0_scale(fp4_unit_dot(rp[c].tc, xp), rp[c].ts);
+          const float tb = __shfl(tt, min(lane + r_tail, 63), 64);  // row B's tail
+          const float a2 = __fadd_rn(a[2 * c], tt), b2 = __fadd_rn(a[2 * c + 1], tb);
+          a[2 * c] = lane < r_tail ? a2 : a[2 * c];
+          a[2 * c + 1] = lane < r_tail ? b2 : a[2 * c + 1];
+        }
+      }
+    } else {
+      Fp4Row<P> rw[2 * kMoeJpw];
+#pragma unroll
+      for (int r = 0; r < 2 * kMoeJpw; ++r) {
+        const int row = 2 * (j0 + r / 2) + (r & 1);
+        fp4_load_row<P>(rw[r], codes + (size_t)row * (H / 2), scales + (size_t)row * Ug, Ug, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every row load issued before any use
+#pragma unroll
+      for (int r = 0; r < 2 * kMoeJpw; ++r) a[r] = 0.0f;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float xp[32];
+        const bool on = lane + 64 * p < Ug;
+        const float* src = xs + min(lane + 64 * p, Ug - 1) * 33;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) xp[j] = src[j];
+#pragma unroll
+        for (int r = 0; r < 2 * kMoeJpw; ++r) {
+          const float t2 = __fadd_rn(a[r], e8m0_scale(fp4_unit_dot(rw[r].c[p], xp), rw[r].s[p]));
+          a[r] = on ? t2 : a[r];  // padded units leave the partial untouched
+        }
+      }
+    }
+    const float tg = wave_sum_8rows(a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], lane);
+    const float tu = xor_lane<8>(tg);  // lane 16 c: column j0 + c's (gate, up) totals
+    const float gb = __fadd_rn(tg, bf_lo(bgu));
+    const float ub = __fadd_rn(tu, bf_hi(bgu));
+    const uint32_t v = f2bf(swiglu_clamp(gb, ub, alpha, limit));
+    const uint64_t packed = (uint64_t)__builtin_amdgcn_readlane(v, 0) |
+                            ((uint64_t)__builtin_amdgcn_readlane(v, 16) << 16) |
+                            ((uint64_t)__builtin_amdgcn_readlane(v, 32) << 32) |
+                            ((uint64_t)__builtin_amdgcn_readlane(v, 48) << 48);
+    if (lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(act + (size_t)slot * I + j0), packed,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // ---- arrive: this block's act stores have completed ----
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(sync + (size_t)(blockIdx.x % kMoeSyncWords) * kMoeSyncStride, 1,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ---- down + weighted sum (+ residual), 4 output rows per block task ----
+  const int slot = wave;
+  const int slot_c = min(slot, k - 1);
+  int e = tk.id[slot_c];
+  const bool e_ok = slot < k && (unsigned)e < (unsigned)E;
+  if (!e_ok) e = 0;  // expert 0's rows are read (in bounds) and dropped
+  const uint8_t* dcodes = dn_codes + (size_t)e * H * (I / 2);
+  const uint8_t* dscales = dn_scales + (size_t)e * H * Ud;
+  const uint16_t* dbias = dn_bias + (size_t)e * H;
+  // act of this wave's slot, kept as bf16 and unpacked one pass at a time
+  uint4 araw[P][4];
+  bool waited = false;
+  for (int d = blockIdx.x; d * kMoeRpw < H; d += gridDim.x) {
+    const int n0 = d * kMoeRpw;
+    const uint16_t res = load_pinned_u16((residual != nullptr ? residual : out) +
+                                         min(n0 + (lane & 3), H - 1));
+    const uint16_t bl = load_pinned_u16(dbias + min(n0 + (lane >> 4), H - 1));
+    float a[kMoeRpw];
+    if constexpr (PAIR) {
+      Fp4RowPair<P> rp[kMoeRpw / 2];
+#pragma unroll
+      for (int c = 0; c < kMoeRpw / 2; ++c) {
+        const int na = min(n0 + 2 * c, H - 1), nb = min(n0 + 2 * c + 1, H - 1);
+        fp4_load_pair<P>(rp[c], dcodes + (size_t)na * (I / 2), dscales + (size_t)na * Ud,
+                         dcodes + (size_t)nb * (I / 2), dscales + (size_t)nb * Ud, Ud, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every row load issued before the wait or any use
+      if (!waited) {  // the first task's rows are in flight during the wait
+        bool ok = true;
+        if (wave == 0) ok = wave_wait_grid(sync, gridDim.x, spin_limit, lane);
+        if (!ok && lane == 0) flag_dev_err(err, kDevErrSyncTimeout);
+        // acquire: act lines cached in this CU's L1 or XCD's L2 are dropped
+        if (kActAcquire && wave == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __syncthreads();
+        x_fp4_issue_agent<P, true>(araw, act + (size_t)slot_c * I, Ud, lane);
+        waited = true;
+      }
+      // fp4_pair_partials, pass by pass (same per-row order)
+      const int r_tail = Ud - 64 * (P - 1);
+#pragma unroll
+      for (int c = 0; c < kMoeRpw / 2; ++c) { a[2 * c] = 0.0f; a[2 * c + 1] = 0.0f; }
+#pragma unroll
+      for (int p = 0; p < P - 1; ++p) {
+        float xp[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(araw[p][q], &xp[8 * q]);
+#pragma unroll
+        for (int c = 0; c < kMoeRpw / 2; ++c) {
+          a[2 * c] = __fadd_rn(a[2 * c], e8m0_scale(fp4_unit_dot(rp[c].c[0][p], xp), rp[c].s[0][p]));
+          a[2 * c + 1] =
+              __fadd_rn(a[2 * c + 1], e8m0_scale(fp4_unit_dot(rp[c].c[1][p], xp), rp[c].s[1][p]));
+        }
+      }
+      {
+        float xp[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(araw[P - 1][q], &xp[8 * q]);
+#pragma unroll
+        for (int c = 0; c < kMoeRpw / 2; ++c) {
+          const float tt = e8m0_scale(fp4_unit_dot(rp[c].tc, xp), rp[c].ts);
+          const float tb = __shfl(tt, min(lane + r_tail, 63), 64);  // row B's tail
+          const float a2 = __fadd_rn(a[2 * c], tt), b2 = __fadd_rn(a[2 * c + 1], tb);
+          a[2 * c] = lane < r_tail ? a2 : a[2 * c];
+          a[2 * c + 1] = lane < r_tail ? b2 : a[2 * c + 1];
+        }
+      }
+    } else {
+      Fp4Row<P> rw[kMoeRpw];
+#pragma unroll
+      for (int r = 0; r < kMoeRpw; ++r) {
+        const int n = min(n0 + r, H - 1);
+        fp4_load_row<P>(rw[r], dcodes + (size_t)n * (I / 2), dscales + (size_t)n * Ud, Ud, lane);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (!waited) {
+        bool ok = true;
+        if (wave == 0) ok = wave_wait_grid(sync, gridDim.x, spin_limit, lane);
+        if (!ok && lane == 0) flag_dev_err(err, kDevErrSyncTimeout);
+        // acquire: act lines cached in this CU's L1 or XCD's L2 are dropped
+        if (kActAcquire && wave == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __syncthreads();
+        x_fp4_issue_agent<P, false>(araw, act + (size_t)slot_c * I, Ud, lane);
+        waited = true;
+      }
+#pragma unroll
+      for (int r = 0; r < kMoeRpw; ++r) a[r] = 0.0f;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float xp[32];
+        const bool on = lane + 64 * p < Ud;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(araw[p][q], &xp[8 * q]);
+#pragma unroll
+        for (int r = 0; r < kMoeRpw; ++r) {
+          const float t2 = __fadd_rn(a[r], e8m0_scale(fp4_unit_dot(rw[r].c[p], xp), rw[r].s[p]));
+          a[r] = on ? t2 : a[r];  // padded units leave the partial untouched
+        }
+      }
+    }
+    const float t = wave_sum_4rows(a[0], a[1], a[2], a[3], lane);
+    if ((lane & 15) == 0) red[slot][lane >> 4] = e_ok ? __fadd_rn(t, bf2f(bl)) : 0.0f;
+    __syncthreads();
+    if (threadIdx.x < min(kMoeRpw, H - n0)) {
+      const int r = threadIdx.x, n = n0 + r;
+      float y = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kMaxTopK; ++s)
+        if (s < k) y = __builtin_fmaf(tk.sc[s], red[s][r], y);
+      const uint16_t m = f2bf(y);
+      out[n] = residual ? f2bf(__fadd_rn(bf2f(res), bf2f(m))) : m;
+    }
+    __syncthreads();  // red is reused by the next task
+  }
+}
+
+bool moe_fused_supported(const MoeArgs& a) {
+  return a.sync != nullptr && a.B == 1 && a.k >= 1 && a.k <= 4 && a.I % kMoeJpw == 0 &&
+         a.H / 32 <= kMoeFusedMaxUnits &&
+         (a.router_lg != nullptr || (a.idx != nullptr && a.score != nullptr));
+}
+
+template <int P, bool PR>
+static int moe_fused_capacity() {
+  static int cap = -1;
+  if (cap < 0) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_fused<P, PR>, 256, 0) !=
+            hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      per_cu = cus = 0;
+    cap = per_cu * cus;
+  }
+  return cap;
+}
+
+// Returns false (nothing launched) when the grid could not be co-resident.
+template <int P, bool PR>
+static bool launch_moe_fused_p(const MoeArgs& a, hipStream_t st) {
+  const int n_dn = (a.H + kMoeRpw - 1) / kMoeRpw;
+  const int cap = moe_fused_capacity<P, PR>();
+  const int grid = min(n_dn, cap);
+  if (grid < 1) return false;
+  hipLaunchKernelGGL((k_moe_fused<P, PR>), dim3(grid), dim3(256), 0, st, a.gu_codes,
+                     a.gu_scales, a.gu_bias, a.dn_codes, a.dn_scales, a.dn_bias, a.router_lg,
+                     a.idx, a.score, a.idx_out, a.score_out, a.E, a.xn, a.act, a.residual, a.out,
+                     a.H, a.I, a.k, a.alpha, a.limit, a.err, a.sync, kMoeSpinLimit);
+  return true;
+}
+
+bool launch_moe_fused(const MoeArgs& a, hipStream_t st) {
+  const int Pg = (a.H / 32 + 63) / 64, Pd = (a.I / 32 + 63) / 64;
+  if (Pg != Pd) return false;  // one P for both halves
+  const bool pr = fp4_pair_ok(a.H / 32, Pg) && fp4_pair_ok(a.I / 32, Pd);
+  switch (Pg) {
+    case 1: return launch_moe_fused_p<1, false>(a, st);
+    case 2: return pr ? launch_moe_fused_p<2, true>(a, st) : launch_moe_fused_p<2, false>(a, st);
+    case 3: return pr ? launch_moe_fused_p<3, true>(a, st) : launch_moe_fused_p<3, false>(a, st);
+    default: return false;
+  }
+}
+
 bool moe_batched_supported(const MoeArgs& a) {
   return a.B >= 2 && a.B * a.k <= 64 && a.idx != nullptr && a.score != nullptr &&
          a.router_lg == nullptr && a.k <= kMaxTopK;
@@ -2060,6 +2471,7 @@ void launch_moe_batched(const MoeArgs& a, hipStream_t st) {
 }
 
 void launch_moe(const MoeArgs& a, hipStream_t st) {
+  if (moe_fused_supported(a) && launch_moe_fused(a, st)) return;
   const int Pg = (a.H / 32 + 63) / 64;  // gate_up reduces over H
   const int Pd = (a.I / 32 + 63) / 64;  // down reduces over I
   const int gblk = (a.I + 4 * kMoeJpw - 1) / (4 * kMoeJpw);

@@ -228,6 +228,31 @@ def test_moe_layer_config0(orc, B):
     assert np.array_equal(got, ref)
 
 
+def test_moe_layer_one_launch(orc, monkeypatch):
+    """neon_moe_layer at batch 1 with the opt-in one-launch expert kernel
+    (NEON_MOE_FUSED=1): ids, weights and outputs bit-identical to the oracle,
+    with and without the residual."""
+    monkeypatch.setenv("NEON_MOE_FUSED", "1")
+    E, H, I, k, B = 32, 2880, 2880, 4, 1
+    d = moe_inputs(orc, E, H, I, B, seed=8)
+    res = orc.fill_bf16(8, 60, B * H, 0.0, 10.0)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    ref, ridx, rsc = orc.moe_layer(d["x"], d["rw"], d["rb"], d["guc"], d["gus"], d["gub"],
+                                   d["dnc"], d["dns"], d["dnb"], E, H, I, k)
+    for residual in (None, res):
+        out = empty_dev((B, H), np.uint16)
+        idx, sc = empty_dev((B, k), np.int32), empty_dev((B, k), np.float32)
+        ne.moe_layer(dv["x"], dv["rw"], dv["rb"], dv["guc"], dv["gus"], dv["gub"], dv["dnc"],
+                     dv["dns"], dv["dnb"], None if residual is None else to_dev(residual), out,
+                     idx, sc, B, E, H, I, k)
+        ne.device_check()
+        assert np.array_equal(to_host(idx), ridx)
+        assert np.array_equal(to_host(sc).view(np.uint32), rsc.view(np.uint32))
+        want = ref if residual is None else orc.f32_to_bf16(
+            orc.bf16_to_f32(residual) + orc.bf16_to_f32(ref).reshape(-1)).reshape(B, H)
+        assert np.array_equal(to_host(out), want)
+
+
 def test_moe_layer_residual(orc):
     E, H, I, k, B = 8, 256, 512, 2, 2
     d = moe_inputs(orc, E, H, I, B, seed=3)

@@ -222,6 +222,15 @@ def test_gpt_oss_20b_greedy_64(orc):
     assert e1 < 2e-2 and e2 < 2e-2
 
 
+def test_gpt_oss_20b_greedy_one_launch_experts(orc, monkeypatch):
+    """The opt-in one-launch expert kernel (NEON_MOE_FUSED=1: gate_up and down
+    with a grid-wide wait between them) gives the same bits as the oracle."""
+    monkeypatch.setenv("NEON_MOE_FUSED", "1")
+    cfg, ocfg = pair(orc, max_seq=64)
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 4, [[7, 2002, 30003, 200001]], 24)
+    assert same.all()
+
+
 def test_engine_errors_on_gpu(orc):
     torch_cuda()
     cfg, _ = pair(orc, **dict(SMALL, max_seq=16))
