@@ -176,6 +176,13 @@ struct MxArgs {
   float alpha, limit;
 };
 bool mx_shape_ok(int N, int K, int B);
+// standalone MXFP4 GEMV on the matrix cores (checkpoint layout, K % 32 == 0,
+// K <= 8192, any N and B): equal to the canonical GEMV up to the order of the
+// fp32 additions
+void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const uint16_t* bias,
+                            const uint16_t* x, uint16_t* y, int N, int K, int B,
+                            hipStream_t st);
+constexpr int kMxfp4GemvMfmaMinB = 16;  // batch rows from which neon_mxfp4_gemv uses it
 bool mx_moe_shape_ok(int H, int I, int E, int k, int B);
 // MFMA lane-order copies (each load instruction of the matrix-core kernels
 // then reads 1 KB contiguous): sizes in bytes, and the packing launches.

@@ -413,102 +413,6 @@ __device__ __forceinline__ float bf16_row_partial(const uint4 (&w)[P],
 }
 
 
-// ===========================================================================
-// Standalone MXFP4 GEMV: y[b][n] = bf16(dot(W[n], x[b]) + bias[n]).
-// grid (ceil(N / (4 rpw)), 1, B), block 256; wave w of block i owns rows
-// [(4i + w) rpw, +rpw).  The next row's codes load while the current row is
-// reduced.
-// ===========================================================================
-template <int P>
-__global__ __launch_bounds__(256) void k_mxfp4_gemv(
-    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
-    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
-    uint16_t* __restrict__ y, int N, int K, int rpw) {
-  const int U = K / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int b = blockIdx.z;
-  const int r0 = (blockIdx.x * 4 + wave) * rpw;
-  const int r1 = min(r0 + rpw, N);
-  if (r0 >= r1) return;
-  Fp4Row<P> cur;
-  fp4_load_row<P>(cur, codes + (size_t)r0 * (K / 2), scales + (size_t)r0 * U, U, lane);
-  float xr[P][32];
-  wave_load_x_fp4<P>(xr, x + (size_t)b * K, U, lane);
-  for (int r = r0; r < r1; ++r) {
-    Fp4Row<P> nxt;
-    if (r + 1 < r1)
-      fp4_load_row<P>(nxt, codes + (size_t)(r + 1) * (K / 2),
-                      scales + (size_t)(r + 1) * U, U, lane);
-    float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
-    if (lane == 0) {
-      if (bias) acc = __fadd_rn(acc, bf2f(bias[r]));
-      y[(size_t)b * N + r] = f2bf(acc);
-    }
-    cur = nxt;
-  }
-}
-
-template <int P>
-static void launch_mxfp4_gemv_p(const uint8_t* codes, const uint8_t* scales,
-                                const uint16_t* bias, const uint16_t* x,
-                                uint16_t* y, int N, int K, int B,
-                                hipStream_t st) {
-  int rpw = 1;
-  while (rpw < 8 && (N + 4 * rpw * 2 - 1) / (4 * rpw * 2) >= 512) rpw *= 2;
-  const int nblk = (N + 4 * rpw - 1) / (4 * rpw);
-  hipLaunchKernelGGL(k_mxfp4_gemv<P>, dim3(nblk, 1, B), dim3(256), 0, st,
-                     codes, scales, bias, x, y, N, K, rpw);
-}
-
-void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
-                       const uint16_t* bias, const uint16_t* x, uint16_t* y,
-                       int N, int K, int B, hipStream_t st) {
-  const int P = (K / 32 + 63) / 64;
-  switch (P) {
-    case 1: launch_mxfp4_gemv_p<1>(codes, scales, bias, x, y, N, K, B, st); break;
-    case 2: launch_mxfp4_gemv_p<2>(codes, scales, bias, x, y, N, K, B, st); break;
-    case 3: launch_mxfp4_gemv_p<3>(codes, scales, bias, x, y, N, K, B, st); break;
-    default: launch_mxfp4_gemv_p<4>(codes, scales, bias, x, y, N, K, B, st); break;
-  }
-}
-
-// ===========================================================================
-// bf16 GEMV with fused prologue (optional RMSNorm of x) and epilogue:
-//   MODE_STORE : y[b][n] = bf16(dot + bias[n])
-//   MODE_RESID : y[b][n] = bf16(y[b][n] + bf16(dot + bias[n]))  (residual add,
-//                HFM:365,375)
-//   MODE_LOGITS: logits[b][n] = dot (fp32), plus the block's (max, lowest
-//                argmax) written to part_val/part_idx [B][gridDim.x]
-// grid (nblk, 1, B), block 256; a wave takes groups of R consecutive rows
-// (grid-strided, so huge N such as lm_head runs on a bounded grid), loads
-// all R rows before any arithmetic and reduces them together with the
-// R-row xor butterfly (bit-identical to R separate butterflies); lane
-// (64 / R) r then holds row r, so the R epilogues run in parallel lanes.
-// R = 2 for the projections (more waves in flight), 4 for lm_head.
-// ===========================================================================
-// (value, index) candidates of lanes l ^ OFF for OFF = LO, 2 LO, .. HI: keep
-// the larger value, the lower index on ties (an order-free reduction)
-template <int LO, int HI>
-__device__ __forceinline__ void argmax_steps(float& v, int32_t& i) {
-  if constexpr (LO <= HI) {
-    const float ov = xor_lane<LO>(v);
-    const int32_t oi = xor_lane_i<LO>(i);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-    argmax_steps<2 * LO, HI>(v, i);
-  }
-}
-
-enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2, MODE_QKV = 3 };
-
-
-// Row r of wave group g.  MODE_QKV pairs dims d and d + 32 of one 64-dim
-// head (group g: head g / 32, d = g % 32) so that the RoPE pair of a q or k
-// head finishes in one wave; the other modes take R consecutive rows.
-template <int MODE, int R>
-__device__ __forceinline__ int group_row(int g, int r) {
-  if constexpr (MODE == MODE_QKV) return ((g >> 5) << 6) + (g & 31) + 32 * r;
-  else return g * R + r;
-}
-
 // xor butterfly (off = 32 .. 1) of 8 rows at once, on named scalars.  Both
 // lanes of an xor pair hold the same sum after every step (fp32 addition
 // commutes), so at step `off` a lane keeps half of its rows and sends the
@@ -565,6 +469,252 @@ __device__ __forceinline__ float wave_sum_2rows(float a0, float a1, int lane) {
   t = __fadd_rn(t, xor_lane<1>(t));
   return t;
 }
+
+// ===========================================================================
+// Standalone MXFP4 GEMV: y[b][n] = bf16(dot(W[n], x[b]) + bias[n]).
+// grid (ceil(N / (4 rpw)), 1, B), block 256; wave w of block i owns rows
+// [(4i + w) rpw, +rpw).  The next row's codes load while the current row is
+// reduced.
+// ===========================================================================
+template <int P>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ y, int N, int K, int rpw) {
+  const int U = K / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.z;
+  const int r0 = (blockIdx.x * 4 + wave) * rpw;
+  const int r1 = min(r0 + rpw, N);
+  if (r0 >= r1) return;
+  Fp4Row<P> cur;
+  fp4_load_row<P>(cur, codes + (size_t)r0 * (K / 2), scales + (size_t)r0 * U, U, lane);
+  float xr[P][32];
+  wave_load_x_fp4<P>(xr, x + (size_t)b * K, U, lane);
+  for (int r = r0; r < r1; ++r) {
+    Fp4Row<P> nxt;
+    if (r + 1 < r1)
+      fp4_load_row<P>(nxt, codes + (size_t)(r + 1) * (K / 2),
+                      scales + (size_t)(r + 1) * U, U, lane);
+    float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
+    if (lane == 0) {
+      if (bias) acc = __fadd_rn(acc, bf2f(bias[r]));
+      y[(size_t)b * N + r] = f2bf(acc);
+    }
+    cur = nxt;
+  }
+}
+
+template <int P>
+static void launch_mxfp4_gemv_p(const uint8_t* codes, const uint8_t* scales,
+                                const uint16_t* bias, const uint16_t* x,
+                                uint16_t* y, int N, int K, int B,
+                                hipStream_t st) {
+  int rpw = 1;
+  while (rpw < 8 && (N + 4 * rpw * 2 - 1) / (4 * rpw * 2) >= 512) rpw *= 2;
+  const int nblk = (N + 4 * rpw - 1) / (4 * rpw);
+  hipLaunchKernelGGL(k_mxfp4_gemv<P>, dim3(nblk, 1, B), dim3(256), 0, st,
+                     codes, scales, bias, x, y, N, K, rpw);
+}
+
+// Register "copies" the compiler cannot see through: inside the per-pair
+// loops the weight words are laundered once per iteration, so the E2M1
+// conversions are not hoisted out of the loop (which keeps every converted
+// value live and drops the kernel to one wave per SIMD).  No code is emitted.
+__device__ __forceinline__ void launder(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+__device__ __forceinline__ void launder(uint32_t& v) { asm volatile("" : "+v"(v)); }
+template <int P>
+__device__ __forceinline__ void launder(Fp4RowPair<P>& q) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int p = 0; p < P - 1; ++p) { launder(q.c[i][p]); launder(q.s[i][p]); }
+  launder(q.tc);
+  launder(q.ts);
+}
+template <int P>
+__device__ __forceinline__ void launder(Fp4Row<P>& r) {
+#pragma unroll
+  for (int p = 0; p < P; ++p) { launder(r.c[p]); launder(r.s[p]); }
+}
+
+// Batched form (B >= 2): every weight row is read once for all B input rows.
+// Wave w of block i owns rows 4 (4 i + w) .. +3, held in registers; it walks
+// the batch rows, the next row's x loading while the current one is reduced.
+// Each (row, batch row) dot is the canonical one above (x of a pass unpacked
+// when it is used), so y is bit-identical to B separate batch-1 launches.
+template <int P, bool PAIR>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv_bt(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ y, int N, int K, int B) {
+  const int U = K / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * 4 + wave) * 4;
+  if (n0 >= N) return;
+  const uint16_t bl =
+      bias != nullptr ? load_pinned_u16(bias + min(n0 + (lane >> 4), N - 1)) : (uint16_t)0;
+  Fp4RowPair<P> rp[2];
+  Fp4Row<P> rw[PAIR ? 1 : 4];
+  if constexpr (PAIR) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int na = min(n0 + 2 * c, N - 1), nb = min(n0 + 2 * c + 1, N - 1);
+      fp4_load_pair<P>(rp[c], codes + (size_t)na * (K / 2), scales + (size_t)na * U,
+                       codes + (size_t)nb * (K / 2), scales + (size_t)nb * U, U, lane);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = min(n0 + r, N - 1);
+      fp4_load_row<P>(rw[r], codes + (size_t)n * (K / 2), scales + (size_t)n * U, U, lane);
+    }
+  }
+  uint4 xraw[P][4];
+  if (PAIR) x_fp4_issue_pair<P>(xraw, x, U, lane);
+  else x_fp4_issue<P>(xraw, x, U, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int r_tail = U - 64 * (P - 1);
+  for (int b = 0; b < B; ++b) {
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) launder(rp[c]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) { launder(rw[r].c[p]); launder(rw[r].s[p]); }
+      }
+    }
+    uint4 cur[P][4];
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cur[p][q] = xraw[p][q];
+    if (b + 1 < B) {
+      if (PAIR) x_fp4_issue_pair<P>(xraw, x + (size_t)(b + 1) * K, U, lane);
+      else x_fp4_issue<P>(xraw, x + (size_t)(b + 1) * K, U, lane);
+    }
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int p = 0; p < P - 1; ++p) {
+        float xp[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(cur[p][q], &xp[8 * q]);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          a[2 * c] = __fadd_rn(a[2 * c], e8m0_scale(fp4_unit_dot(rp[c].c[0][p], xp), rp[c].s[0][p]));
+          a[2 * c + 1] =
+              __fadd_rn(a[2 * c + 1], e8m0_scale(fp4_unit_dot(rp[c].c[1][p], xp), rp[c].s[1][p]));
+        }
+      }
+      float xp[32];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) unpack8(cur[P - 1][q], &xp[8 * q]);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float tt = e8m0_scale(fp4_unit_dot(rp[c].tc, xp), rp[c].ts);
+        const float tb = __shfl(tt, min(lane + r_tail, 63), 64);  // row B's tail
+        const float a2 = __fadd_rn(a[2 * c], tt), b2 = __fadd_rn(a[2 * c + 1], tb);
+        a[2 * c] = lane < r_tail ? a2 : a[2 * c];
+        a[2 * c + 1] = lane < r_tail ? b2 : a[2 * c + 1];
+      }
+    } else {
+      const uint4 zero = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const bool on = lane + 64 * p < U;
+        float xp[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) unpack8(on ? cur[p][q] : zero, &xp[8 * q]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float t2 = __fadd_rn(a[r], e8m0_scale(fp4_unit_dot(rw[r].c[p], xp), rw[r].s[p]));
+          a[r] = on ? t2 : a[r];  // padded units leave the partial untouched
+        }
+      }
+    }
+    const float t = wave_sum_4rows(a[0], a[1], a[2], a[3], lane);
+    const int n = n0 + (lane >> 4);
+    if ((lane & 15) == 0 && n < N) {
+      float v = t;
+      if (bias != nullptr) v = __fadd_rn(v, bf2f(bl));
+      y[(size_t)b * N + n] = f2bf(v);
+    }
+  }
+}
+
+void launch_mxfp4_gemv(const uint8_t* codes, const uint8_t* scales,
+                       const uint16_t* bias, const uint16_t* x, uint16_t* y,
+                       int N, int K, int B, hipStream_t st) {
+  const int P = (K / 32 + 63) / 64;
+  if (B >= kMxfp4GemvMfmaMinB) {  // a dense contraction: the matrix cores
+    launch_mxfp4_gemv_mfma(codes, scales, bias, x, y, N, K, B, st);
+    return;
+  }
+  if (B >= 2) {
+    const int nblk = (N + 15) / 16;
+    const bool pr = fp4_pair_ok(K / 32, P);
+#define BT_CASE(PP)                                                                          \
+  case PP:                                                                                   \
+    if (pr) hipLaunchKernelGGL((k_mxfp4_gemv_bt<PP, true>), dim3(nblk), dim3(256), 0, st,   \
+                               codes, scales, bias, x, y, N, K, B);                         \
+    else hipLaunchKernelGGL((k_mxfp4_gemv_bt<PP, false>), dim3(nblk), dim3(256), 0, st,     \
+                            codes, scales, bias, x, y, N, K, B);                            \
+    return;
+    switch (P) {
+      BT_CASE(1) BT_CASE(2) BT_CASE(3)
+      default: BT_CASE(4)
+    }
+#undef BT_CASE
+  }
+  switch (P) {
+    case 1: launch_mxfp4_gemv_p<1>(codes, scales, bias, x, y, N, K, B, st); break;
+    case 2: launch_mxfp4_gemv_p<2>(codes, scales, bias, x, y, N, K, B, st); break;
+    case 3: launch_mxfp4_gemv_p<3>(codes, scales, bias, x, y, N, K, B, st); break;
+    default: launch_mxfp4_gemv_p<4>(codes, scales, bias, x, y, N, K, B, st); break;
+  }
+}
+
+// ===========================================================================
+// bf16 GEMV with fused prologue (optional RMSNorm of x) and epilogue:
+//   MODE_STORE : y[b][n] = bf16(dot + bias[n])
+//   MODE_RESID : y[b][n] = bf16(y[b][n] + bf16(dot + bias[n]))  (residual add,
+//                HFM:365,375)
+//   MODE_LOGITS: logits[b][n] = dot (fp32), plus the block's (max, lowest
+//                argmax) written to part_val/part_idx [B][gridDim.x]
+// grid (nblk, 1, B), block 256; a wave takes groups of R consecutive rows
+// (grid-strided, so huge N such as lm_head runs on a bounded grid), loads
+// all R rows before any arithmetic and reduces them together with the
+// R-row xor butterfly (bit-identical to R separate butterflies); lane
+// (64 / R) r then holds row r, so the R epilogues run in parallel lanes.
+// R = 2 for the projections (more waves in flight), 4 for lm_head.
+// ===========================================================================
+// (value, index) candidates of lanes l ^ OFF for OFF = LO, 2 LO, .. HI: keep
+// the larger value, the lower index on ties (an order-free reduction)
+template <int LO, int HI>
+__device__ __forceinline__ void argmax_steps(float& v, int32_t& i) {
+  if constexpr (LO <= HI) {
+    const float ov = xor_lane<LO>(v);
+    const int32_t oi = xor_lane_i<LO>(i);
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    argmax_steps<2 * LO, HI>(v, i);
+  }
+}
+
+enum { MODE_STORE = 0, MODE_RESID = 1, MODE_LOGITS = 2, MODE_QKV = 3 };
+
+
+// Row r of wave group g.  MODE_QKV pairs dims d and d + 32 of one 64-dim
+// head (group g: head g / 32, d = g % 32) so that the RoPE pair of a q or k
+// head finishes in one wave; the other modes take R consecutive rows.
+template <int MODE, int R>
+__device__ __forceinline__ int group_row(int g, int r) {
+  if constexpr (MODE == MODE_QKV) return ((g >> 5) << 6) + (g & 31) + 32 * r;
+  else return g * R + r;
+}
+
 
 template <int R>
 constexpr int log2_rows() { return R == 4 ? 2 : (R == 2 ? 1 : 0); }
@@ -1822,29 +1972,6 @@ __global__ __launch_bounds__(1024) void k_moe_down(
 // dot is the canonical one of the batch-1 kernels, so the outputs are
 // bit-identical to a batch-1 step.
 // ===========================================================================
-// Register "copies" the compiler cannot see through: inside the per-pair
-// loops the weight words are laundered once per iteration, so the E2M1
-// conversions are not hoisted out of the loop (which keeps every converted
-// value live and drops the kernel to one wave per SIMD).  No code is emitted.
-__device__ __forceinline__ void launder(uint4& v) {
-  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
-}
-__device__ __forceinline__ void launder(uint32_t& v) { asm volatile("" : "+v"(v)); }
-template <int P>
-__device__ __forceinline__ void launder(Fp4RowPair<P>& q) {
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int p = 0; p < P - 1; ++p) { launder(q.c[i][p]); launder(q.s[i][p]); }
-  launder(q.tc);
-  launder(q.ts);
-}
-template <int P>
-__device__ __forceinline__ void launder(Fp4Row<P>& r) {
-#pragma unroll
-  for (int p = 0; p < P; ++p) { launder(r.c[p]); launder(r.s[p]); }
-}
-
 template <int P, bool PAIR>
 __global__ __launch_bounds__(256) void k_moe_gate_up_bt(
     const uint8_t* __restrict__ gu_codes, const uint8_t* __restrict__ gu_scales,

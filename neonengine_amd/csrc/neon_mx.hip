@@ -176,6 +176,134 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
   }
 }
 
+// Standalone MXFP4 GEMV on the matrix cores (neon_mxfp4_gemv at B >= 16):
+// y[b][n] = bf16(sum_k x[b][k] dq(W[n][k]) + bias[n]) with the weights in the
+// checkpoint layout (codes [N][K/2], scales [N][K/32]).  A block owns rows
+// n0 .. n0 + 15 and up to 64 batch rows (BT tiles of 16); its 4 waves split
+// K.  In K step q (128 elements = 4 MXFP4 units) lane (j, g) loads all of
+// unit 4 q + g of row n0 + j (16 code bytes and its scale) and feeds it to
+// 4 MFMAs, 8 elements each; the x operand is loaded with the same lane-to-
+// unit map, so every k is summed exactly once (in another order than the
+// checkpoint's).  E2M1 x 2^(s - 127) converts exactly to bf16 (scale byte
+// 0xFF gives NaN), products of two bf16 values are exact in fp32, and the
+// 4 waves' partial tiles are added in wave order; only the order of the fp32
+// additions differs from the canonical GEMV.
+template <int BT, int IT>
+__global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ y, int N, int K, int B) {
+  __shared__ mx_f32x4 red[3][BT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int U = K / 32;
+  const int n0 = blockIdx.x * 16;
+  const int nr = min(n0 + j, N - 1);  // rows past N re-read row N - 1 (not stored)
+  const int b0 = blockIdx.y * 64;
+  // this wave's units: 4 (w + 4 i) + g for i < IT (clamped; zero A past U)
+  uint4 wc[IT];
+  uint32_t ws[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int u = min(4 * (w + 4 * i) + g, U - 1);
+    wc[i] = mx_load_nt(codes + (size_t)nr * (K / 2) + (size_t)u * 16);
+    ws[i] = __builtin_nontemporal_load(scales + (size_t)nr * U + u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t* xrow[BT];
+  bool rv[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    const int r = b0 + 16 * bt + j;
+    rv[bt] = r < B;
+    xrow[bt] = x + (size_t)(rv[bt] ? r : B - 1) * K;
+  }
+  mx_f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int u_raw = 4 * (w + 4 * i) + g;
+    const bool uok = u_raw < U;
+    const int u = min(u_raw, U - 1);
+    uint4 xq[BT][4];
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint4 v = reinterpret_cast<const uint4*>(xrow[bt] + (size_t)u * 32)[t];
+        xq[bt][t] = (uok && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);  // zero A drops it
+      }
+    const float sc = ws[i] == 0xFFu ? __builtin_nanf("")
+                                    : __builtin_amdgcn_ldexpf(1.0f, (int)ws[i] - 127);
+    const uint32_t cw[4] = {wc[i].x, wc[i].y, wc[i].z, wc[i].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const mx_bf16x8 bw = mx_fp4x8(cw[t], sc);
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt)
+        acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw, acc[bt],
+                                                          0, 0, 0);
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+  const int n = n0 + j;
+  const float bv = (bias != nullptr && n < N) ? bf2f(bias[n]) : 0.0f;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    mx_f32x4 tot = acc[bt];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const mx_f32x4 p = red[v][bt][lane];
+      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
+      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = b0 + 16 * bt + 4 * g + r;
+      if (ri < B && n < N) {
+        const float v = bias != nullptr ? __fadd_rn(tot[r], bv) : tot[r];
+        y[(size_t)ri * N + n] = f2bf(v);
+      }
+    }
+  }
+}
+
+template <int BT>
+static void launch_mxfp4_gemv_mfma_bt(const uint8_t* codes, const uint8_t* scales,
+                                      const uint16_t* bias, const uint16_t* x, uint16_t* y,
+                                      int N, int K, int B, hipStream_t st) {
+  const int steps = (K / 32 + 3) / 4;        // K steps of 4 units
+  const int it = (steps + 3) / 4;            // per wave
+  const dim3 grid((N + 15) / 16, (B + 63) / 64);
+#define MF_CASE(ITV)                                                                     \
+  if (it <= ITV) {                                                                       \
+    hipLaunchKernelGGL((k_mxfp4_gemv_mfma<BT, ITV>), grid, dim3(256), 0, st, codes,     \
+                       scales, bias, x, y, N, K, B);                                     \
+    return;                                                                              \
+  }
+  MF_CASE(2) MF_CASE(4) MF_CASE(6) MF_CASE(8) MF_CASE(12) MF_CASE(16)
+#undef MF_CASE
+}
+
+void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const uint16_t* bias,
+                            const uint16_t* x, uint16_t* y, int N, int K, int B,
+                            hipStream_t st) {
+  // batch tiles of the widest block (B > 64 runs several blocks in y)
+  const int bt = B >= 64 ? 4 : (B + 15) / 16;
+  switch (bt) {
+    case 1: launch_mxfp4_gemv_mfma_bt<1>(codes, scales, bias, x, y, N, K, B, st); break;
+    case 2: launch_mxfp4_gemv_mfma_bt<2>(codes, scales, bias, x, y, N, K, B, st); break;
+    case 3: launch_mxfp4_gemv_mfma_bt<3>(codes, scales, bias, x, y, N, K, B, st); break;
+    default: launch_mxfp4_gemv_mfma_bt<4>(codes, scales, bias, x, y, N, K, B, st); break;
+  }
+}
+
 // weight tiles of 16 rows per wave and rows per block.  Measured at the 20b
 // shape (tok/s at B = 16 / 64): 4 tiles (228 VGPRs, 2 waves per SIMD)
 // 3754 / 7924, 2 tiles (146 VGPRs) 4141 / 9400, 1 tile 4206 / 9499 -- more

@@ -22,6 +22,16 @@ from tests.gpu_util import torch_cuda
 pytestmark = pytest.mark.gpu
 
 FIX = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "model_fixtures.npz")
+COND = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "conditioning.npz")
+
+
+def conditioning(key):
+    """Per-(step, row) relative max logit error between the oracle's canonical
+    fp32 order and its fp64-accumulation order on the same inputs (written by
+    tests/golden/make_conditioning.py): what a change of summation order alone
+    does to this random-init model at that depth."""
+    with np.load(COND, allow_pickle=False) as z:
+        return z[key]
 
 
 def say(*a):
@@ -151,10 +161,44 @@ def matrix_vs_oracle(orc, seed, fixed_routing, steps=2, B=16):
     return np.stack(rels)
 
 
+def check_against_conditioning(rels, key, per_step=True):
+    """The matrix-core steps may differ from the canonical oracle by no more
+    than twice what the oracle's own fp64-accumulation order differs from it
+    on the same inputs (median and worst row).  Two independent roundings of
+    the same sums differ by about sqrt(2) of one, so 2x holds for any order of
+    fp32 additions and fails for an actual arithmetic error.  per_step=False
+    compares all (step, row) samples at once: with free routing the errors
+    come from expert flips and are too heavy-tailed for a 16-row median."""
+    ref = conditioning(key)
+    assert rels.shape == ref.shape
+    for s in range(len(rels)):
+        say(f"  step {s}: median {np.median(rels[s]):.3e} (reorder {np.median(ref[s]):.3e}), "
+            f"max {rels[s].max():.3e} (reorder {ref[s].max():.3e})")
+        if per_step:
+            assert np.median(rels[s]) <= 2 * np.median(ref[s])
+            assert rels[s].max() <= 2 * ref[s].max()
+    say(f"  all steps: median {np.median(rels):.3e} (reorder {np.median(ref):.3e}), "
+        f"max {rels.max():.3e} (reorder {ref.max():.3e})")
+    assert np.median(rels) <= 2 * np.median(ref)
+    assert rels.max() <= 2 * ref.max()
+
+
 def test_config3_batch16_matrix_vs_oracle_fixed_routing(orc):
     """NEON_DECODE_MATRIX at the full 24-layer 20b shape, batch 16, against the
     live oracle fed the same tokens, with routing fixed in both (so only the
-    kernels' summation order differs): relative max logit error <= 2e-2 at
-    every step (north_star's bar), flips only within twice that error."""
+    kernels' summation order differs).  north_star's 2e-2 bar holds up to a
+    few layers (tests/test_gpu_mx.py); at 24 layers even the oracle in another
+    summation order differs from itself by 6.6e-2 (max) / 3.9e-2 (median), so
+    the bar is twice that measured reorder error (tests/golden/
+    conditioning.npz), and flips only within twice the row's error."""
     rels = matrix_vs_oracle(orc, 7, fixed_routing=True)
-    assert rels.max() <= 2e-2
+    check_against_conditioning(rels, "fixed_24")
+
+
+def test_config3_batch16_matrix_vs_oracle_free_routing(orc):
+    """The same with the routers as initialised: a change of summation order
+    alone flips near-tied expert choices (the oracle against itself: half the
+    greedy ids of this run differ), so the bar is again twice the oracle's own
+    reorder error on these inputs."""
+    rels = matrix_vs_oracle(orc, 7, fixed_routing=False)
+    check_against_conditioning(rels, "free_24", per_step=False)

@@ -233,12 +233,19 @@ def test_gpt_oss_20b_batched_prefill_full_depth():
     2.5e-2 and 6.7e-2 (relative) at 2, 6, 12 and 24 layers.  With free routing
     some rows' 4th and 5th router logits also lie within rounding of each
     other, so the modes pick different experts (0.52 at 12 layers).  The bar
-    here is 0.1 with the routing fixed; the exact prompt modes stay the
-    default."""
+    is twice what a change of summation order alone does to this model at 24
+    layers with the routing fixed: the CPU oracle in its fp64-accumulation
+    order differs from its canonical fp32 order by up to 6.6e-2
+    (tests/golden/conditioning.npz), so 0.13; the exact prompt modes stay
+    the default."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "conditioning.npz")
+    with np.load(path, allow_pickle=False) as z:
+        bar = 2 * float(z["fixed_24"].max())
     cfg = ne.config_preset("gpt-oss-20b", max_seq=512)
     prompt = [[(1009 * i + 17) % 201088 for i in range(300)]]
-    rel, _ = compare_modes(cfg, 0, prompt, 16, fixed_routing=True, bar=0.1)
-    assert rel < 0.1
+    rel, _ = compare_modes(cfg, 0, prompt, 16, fixed_routing=True, bar=bar)
+    assert rel < bar
 
 
 def test_prefill_mode_validation():
