@@ -6,7 +6,8 @@
 // :131; failures propagate to main, NeonEngine/src/main.cpp:21-26).
 // neon::Engine keeps that shape for the gpt-oss token loop: construct, load
 // weights (checkpoint tensors or deterministic random init), prefill, decode.
-// Everything goes through the C-ABI, so this header needs no HIP includes.
+// Everything goes through the C-ABI, so this header needs no HIP includes;
+// tests/cpp/engine_greedy.cpp is a host program built on it.
 #pragma once
 
 #include <cstdint>
@@ -51,7 +52,7 @@ class Config {
 
 class Engine {
  public:
-  Engine(const Config& cfg, int device = 0) {
+  Engine(const Config& cfg, int device = 0) : vocab_(cfg.raw().vocab) {
     check(neon_ctx_create(&cfg.raw(), device, &ctx_), nullptr);
   }
   ~Engine() { neon_ctx_destroy(ctx_); }
@@ -67,15 +68,24 @@ class Engine {
   }
 
   // Prompt mode: NEON_PREFILL_CHUNKED (16 prompt rows per pass, default),
-  // NEON_PREFILL_STEPWISE (every prompt token as a decode step) or
-  // NEON_PREFILL_BATCHED (matrix cores; switched off).
+  // NEON_PREFILL_STEPWISE (every prompt token as a decode step), both
+  // bit-identical; or NEON_PREFILL_BATCHED (all prompt rows at once on the
+  // matrix cores, equal to the others up to bf16 rounding).
   void set_prefill_mode(int mode) { check(neon_set_prefill_mode(ctx_, mode), ctx_); }
+  // Steps of two or more sequences: NEON_DECODE_EXACT (default) or
+  // NEON_DECODE_MATRIX (matrix cores).
+  void set_decode_mode(int mode) { check(neon_set_decode_mode(ctx_, mode), ctx_); }
+  // Next-token choice: temperature 0 (default) is greedy argmax; otherwise
+  // nucleus sampling (top_p in (0, 1]) reproducible for a seed.
+  void set_sampling(float temperature, float top_p = 1.0f, uint64_t seed = 0) {
+    check(neon_set_sampling(ctx_, temperature, top_p, seed), ctx_);
+  }
 
   // Forward: prefill `batch` prompts of equal length (row-major ids), then
-  // greedy decode steps; tokens() returns prompt + generated ids per row.
+  // decode steps; tokens() returns prompt + generated ids per row.
   void prefill(const std::vector<int32_t>& ids, int batch, void* stream = nullptr) {
-    if (batch < 1 || ids.size() % (size_t)batch)
-      throw Error(NEON_EINVAL, "prefill: ids.size() must be a multiple of batch");
+    if (batch < 1 || ids.empty() || ids.size() % (size_t)batch)
+      throw Error(NEON_EINVAL, "prefill: ids.size() must be a positive multiple of batch");
     check(neon_prefill(ctx_, ids.data(), batch, (int)(ids.size() / batch), stream), ctx_);
     batch_ = batch;
   }
@@ -89,16 +99,21 @@ class Engine {
     check(neon_read_tokens(ctx_, 0, n, out.data(), stream), ctx_);
     return out;
   }
-  std::vector<float> logits(int vocab, void* stream = nullptr) {
-    std::vector<float> out((size_t)batch_ * vocab);
+  // fp32 logits of the last step, [batch][vocab] (vocab from the config the
+  // engine was built with)
+  std::vector<float> logits(void* stream = nullptr) {
+    std::vector<float> out((size_t)batch_ * vocab_);
     check(neon_read_logits(ctx_, out.data(), stream), ctx_);
     return out;
   }
+  int batch() const { return batch_; }
+  int vocab() const { return vocab_; }
   neon_ctx* handle() { return ctx_; }
 
  private:
   neon_ctx* ctx_ = nullptr;
   int batch_ = 0;
+  int vocab_ = 0;
 };
 
 }  // namespace neon

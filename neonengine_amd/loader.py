@@ -42,18 +42,39 @@ def checkpoint_files(path: str) -> list[str]:
     return files
 
 
+def check_tensor(name: str, t, expected) -> None:
+    """Raises ValueError when a checkpoint tensor's shape or element type is
+    not the one the engine's config gives for that name (a transposed q_proj
+    or o_proj, or experts stored in another order, has the right byte count
+    but the wrong shape)."""
+    import torch
+    shape, kind = expected
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, the model expects {tuple(shape)}")
+    if kind == "u8" and t.dtype != torch.uint8:
+        raise ValueError(f"{name}: MXFP4 tensor must be uint8, got {t.dtype}")
+    if kind == "bf16" and not t.is_floating_point():
+        raise ValueError(f"{name}: expected a floating-point tensor, got {t.dtype}")
+
+
 def load_checkpoint(engine, path: str, strict: bool = True) -> int:
     """Loads every tensor of the checkpoint at `path` into `engine` and returns
-    how many it loaded.  A name the model does not have, or a size that does
-    not match the engine's shape, raises NeonError (from neon_load_tensor);
-    with `strict`, a checkpoint that lacks one of the model's tensors raises
-    KeyError after the others were loaded."""
+    how many it loaded.  A known tensor whose shape or element type differs
+    from the engine's config raises ValueError before anything of it is
+    copied; a name the model does not have, or a size that does not match,
+    raises NeonError (from neon_load_tensor); with `strict`, a checkpoint that
+    lacks one of the model's tensors raises KeyError after the others were
+    loaded."""
     from safetensors import safe_open
+    shapes = checkpoint_shapes(engine.cfg)
     seen = set()
     for f in checkpoint_files(path):
         with safe_open(f, framework="pt") as sf:
             for name in sf.keys():
-                engine.load_tensor(name, tensor_data(name, sf.get_tensor(name)))
+                t = sf.get_tensor(name)
+                if name in shapes:
+                    check_tensor(name, t, shapes[name])
+                engine.load_tensor(name, tensor_data(name, t))
                 seen.add(name)
     if strict:
         missing = [n for n in checkpoint_names(engine.cfg) if n not in seen]

@@ -129,6 +129,20 @@ def test_no_device_reports_ehip():
     assert b"device" in ne.lib().neon_last_error(None)
 
 
+def test_cpp_host_program_reports_no_device():
+    """tests/cpp/engine_greedy (neon::Engine over the C-ABI) builds with g++
+    and, without a GPU, fails at construction with neon::Error(NEON_EHIP)."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present (tests/test_gpu_cpp_host.py runs it)")
+    import subprocess
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
+    r = subprocess.run([os.path.join(ROOT, "tests", "cpp", "engine_greedy"), "small", "2", "1"],
+                       capture_output=True, text=True, timeout=60)
+    assert r.returncode == 3, (r.stdout, r.stderr)
+    assert "neon::Error 3" in r.stderr and "device" in r.stderr
+
+
 def test_engine_header_is_self_contained_cpp(tmp_path):
     """include/neon_engine.hpp compiles standalone against the C header."""
     import shutil

@@ -97,3 +97,33 @@ def test_strict_reports_missing_tensors(tmp_path):
     for n, a in eng.got.items():  # every tensor arrived whole
         s, dt = shapes[n]
         assert a.size == int(np.prod(s)) and a.dtype == (np.uint8 if dt == "u8" else np.uint16)
+
+
+@pytest.mark.parametrize("name,bad", [
+    ("model.layers.0.self_attn.q_proj.weight", lambda s: (s[1], s[0])),   # transposed
+    ("model.layers.1.self_attn.o_proj.weight", lambda s: (s[1], s[0])),   # transposed
+    ("model.layers.0.mlp.experts.gate_up_proj_blocks", lambda s: (s[1], s[0], s[2], s[3])),
+    ("model.layers.1.mlp.experts.down_proj_scales", lambda s: (s[0] * s[1] * s[2],)),
+])
+def test_shape_mismatch_of_equal_size_is_rejected(tmp_path, name, bad):
+    """A tensor with the right number of elements in the wrong layout (HF's
+    q_proj stored transposed, experts in another order, a flattened scale
+    tensor) is refused before anything of it reaches the engine."""
+    cfg = ne.config_preset("gpt-oss-20b", **dict(TINY, head_dim=32))  # q / o not square
+    shape, dt = loader.checkpoint_shapes(cfg)[name]
+    assert bad(shape) != shape
+    t = torch.zeros(bad(shape), dtype=torch.uint8 if dt == "u8" else torch.bfloat16)
+    st.save_file({name: t}, str(tmp_path / "m.safetensors"))
+    eng = Recorder(cfg)
+    with pytest.raises(ValueError, match="shape"):
+        loader.load_checkpoint(eng, str(tmp_path), strict=False)
+    assert name not in eng.got
+
+
+def test_expert_tensor_dtype_is_checked(tmp_path):
+    cfg = ne.config_preset("gpt-oss-20b", **TINY)
+    name = "model.layers.0.mlp.experts.down_proj_blocks"
+    shape, _ = loader.checkpoint_shapes(cfg)[name]
+    st.save_file({name: torch.zeros(shape, dtype=torch.float16)}, str(tmp_path / "m.safetensors"))
+    with pytest.raises(ValueError, match="uint8"):
+        loader.load_checkpoint(Recorder(cfg), str(tmp_path), strict=False)
