@@ -154,6 +154,11 @@ neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
  *   "moe_in"    last layer's normalised MoE input, bf16 [batch][hidden]
  *   "moe_idx"   last layer's expert ids, int32 [batch][top_k]
  *   "moe_score" last layer's routing weights, fp32 [batch][top_k]
+ *   "mx_route"  after a NEON_DECODE_MATRIX step of two or more sequences: the
+ *               last layer's route table, int32 [2 S + 64 S] with S =
+ *               min(n_experts, batch top_k): used expert of slot y (ascending,
+ *               -1 past the used ones), its pair count, then its pairs
+ *               q = b top_k + s in ascending order (64 entries per slot)
  * `bytes` must equal the buffer's size. */
 neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
                                  size_t bytes, void* stream);

@@ -15,7 +15,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libneon_gptoss.so")
+# NEON_GPTOSS_LIB selects another build of the library (e.g. the host-
+# sanitizer build neonengine_amd/_asan/libneon_gptoss.so)
+LIB_PATH = os.environ.get("NEON_GPTOSS_LIB") or os.path.join(HERE, "libneon_gptoss.so")
 
 NEON_OK, NEON_EINVAL, NEON_ENOMEM, NEON_EHIP = 0, 1, 2, 3
 NEON_ENAN_SCALE, NEON_EKV_FULL, NEON_ERANGE_TOKEN, NEON_ESTATE = 4, 5, 6, 7
@@ -371,6 +373,13 @@ class Engine:
         """One activation buffer of the last step (see neon_read_activation)."""
         import numpy as np
         c = self.cfg
+        if name == "mx_route":
+            S = min(c.n_experts, self.batch * c.top_k)
+            out = np.empty(66 * S, np.int32)
+            self._chk(lib().neon_read_activation(self._ctx, name.encode(),
+                                                 out.ctypes.data_as(C.c_void_p), out.nbytes,
+                                                 _stream(stream)))
+            return out
         width = {"hidden": c.hidden, "moe_in": c.hidden, "moe_idx": c.top_k,
                  "moe_score": c.top_k, "qkv": (c.n_heads + 2 * c.n_kv_heads) * c.head_dim,
                  "attn_out": c.n_heads * c.head_dim}[name]

@@ -71,5 +71,40 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+# Host sanitizers for the library's host code (argument validation, config
+# checks, context set-up: all in neon_engine.hip); the device code is
+# unchanged.  Each -fsanitize= is a host-only flag.
+SANITIZE_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                 "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-g",
+                 "-Xarch_host", "-fno-omit-frame-pointer"]
+ASAN_DIR = os.path.join(HERE, "_asan")
+ASAN_LIB = os.path.join(ASAN_DIR, "libneon_gptoss.so")
+
+
+def build_sanitized(verbose: bool = False) -> str:
+    """neonengine_amd/_asan/libneon_gptoss.so: neon_engine.hip recompiled with
+    the host sanitizers, linked with the regular objects of build()."""
+    os.makedirs(ASAN_DIR, exist_ok=True)
+    obj = os.path.join(ASAN_DIR, "neon_engine.o")
+    cmd = [hipcc()] + [f for f in HIPCC_FLAGS if f != "-shared"] + SANITIZE_HOST + [
+        "-I", os.path.join(ROOT, "include"), "-c", os.path.join(CSRC, "neon_engine.hip"), "-o", obj]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed: {' '.join(cmd)}\n{r.stdout.decode(errors='replace')}")
+    others = [os.path.join(HERE, "_build", s.replace(".hip", ".o")) for s in SOURCES
+              if s != "neon_engine.hip"]
+    tmp = ASAN_LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
+           "-Xarch_host", "-fsanitize=undefined", "-Xarch_host", "-shared-libasan", "-o", tmp,
+           obj] + others
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout.decode(errors='replace')}")
+    os.replace(tmp, ASAN_LIB)
+    return ASAN_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))

@@ -1181,6 +1181,13 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
   else if (nm == "moe_in") { src = ctx->xn; n = B * c.hidden * 2; }
   else if (nm == "moe_idx") { src = ctx->moe_idx; n = B * c.top_k * 4; }
   else if (nm == "moe_score") { src = ctx->moe_score; n = B * c.top_k * 4; }
+  else if (nm == "mx_route") {
+    if (ctx->mx_route == nullptr || ctx->decode_mode != NEON_DECODE_MATRIX || B < 2)
+      FAIL(ctx, NEON_EINVAL, "neon_read_activation: 'mx_route' exists after matrix-core steps "
+           "of two or more sequences");
+    const size_t S = std::min<size_t>(c.n_experts, B * c.top_k);
+    src = ctx->mx_route; n = (2 * S + 64 * S) * 4;
+  }
   else FAIL(ctx, NEON_EINVAL, "neon_read_activation: unknown buffer '%s'", name);
   if (bytes != n)
     FAIL(ctx, NEON_EINVAL, "neon_read_activation: '%s' holds %zu bytes, %zu requested", name, n, bytes);

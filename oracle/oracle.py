@@ -15,7 +15,8 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libneon_oracle.so")
+# NEON_ORACLE_LIB selects another build (the host-sanitizer build in _asan/)
+_LIB_PATH = os.environ.get("NEON_ORACLE_LIB") or os.path.join(_HERE, "libneon_oracle.so")
 
 
 def build() -> None:

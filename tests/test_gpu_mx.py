@@ -234,3 +234,32 @@ def test_matrix_mode_sampling_reproducible():
     say(f"matrix-mode sampling: {runs[0][0, 6:].tolist()}")
     assert np.array_equal(runs[0], runs[1])
     assert (runs[0] >= 0).all() and (runs[0] < cfg.vocab).all()
+
+
+@pytest.mark.parametrize("E,B", [(32, 16), (128, 16), (8, 5)])
+def test_route_lists_match_host(E, B):
+    """The route table k_topk_route writes for the matrix-core experts (used
+    experts in ascending order, their pair counts and ascending pair lists)
+    equals one built on the host from the same step's expert ids."""
+    torch_cuda()
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_experts=E, max_batch=B, max_seq=32))
+    eng = ne.Engine(cfg)
+    eng.init_random(3)
+    eng.set_decode_mode(ne.DECODE_MATRIX)
+    eng.prefill([[(37 * b + 11 * t + 1) % cfg.vocab for t in range(3)] for b in range(B)])
+    eng.decode(2)
+    idx = eng.read_activation("moe_idx").reshape(-1)
+    route = eng.read_activation("mx_route")
+    eng.close()
+    k = cfg.top_k
+    S = min(E, B * k)
+    used = sorted(set(int(e) for e in idx))
+    say(f"route lists E={E} B={B}: {len(used)} used experts of {S} slots")
+    for y in range(S):
+        if y < len(used):
+            e = used[y]
+            pairs = [q for q in range(B * k) if idx[q] == e]
+            assert route[y] == e and route[S + y] == len(pairs), y
+            assert list(route[2 * S + 64 * y: 2 * S + 64 * y + len(pairs)]) == pairs, y
+        else:
+            assert route[y] == -1 and route[S + y] == 0, y
