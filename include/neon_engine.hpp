@@ -82,12 +82,29 @@ class Engine {
   }
 
   // Forward: prefill `batch` prompts of equal length (row-major ids), then
-  // decode steps; tokens() returns prompt + generated ids per row.
+  // decode steps; tokens() returns prompt + generated ids per row (0 past a
+  // shorter sequence's length).
   void prefill(const std::vector<int32_t>& ids, int batch, void* stream = nullptr) {
     if (batch < 1 || ids.empty() || ids.size() % (size_t)batch)
       throw Error(NEON_EINVAL, "prefill: ids.size() must be a positive multiple of batch");
     check(neon_prefill(ctx_, ids.data(), batch, (int)(ids.size() / batch), stream), ctx_);
     batch_ = batch;
+  }
+  // Prompts of different lengths (each sequence keeps its own position).
+  void prefill(const std::vector<std::vector<int32_t>>& prompts, void* stream = nullptr) {
+    std::vector<int32_t> flat, lens;
+    for (const auto& p : prompts) {
+      flat.insert(flat.end(), p.begin(), p.end());
+      lens.push_back((int32_t)p.size());
+    }
+    check(neon_prefill_ragged(ctx_, flat.data(), lens.data(), (int)prompts.size(), stream), ctx_);
+    batch_ = (int)prompts.size();
+  }
+  // Tokens held by each sequence (prompt + generated).
+  std::vector<int32_t> seq_lens() const {
+    std::vector<int32_t> out((size_t)batch_);
+    check(neon_seq_lens(ctx_, out.data()), ctx_);
+    return out;
   }
   void decode(int n_steps, void* stream = nullptr) {
     check(neon_decode(ctx_, n_steps, stream), ctx_);

@@ -105,6 +105,20 @@ neon_status neon_load_tensor(neon_ctx* ctx, const char* name,
 neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
                          int n_tokens, void* stream);
 
+/* neon_prefill for prompts of different lengths: sequence b's prompt is
+ * lens[b] >= 1 ids, the prompts stored one after another in `ids` (sum of
+ * lens[] entries).  Every sequence keeps its own position: afterwards
+ * sequence b holds lens[b] + 1 tokens (neon_seq_lens), its KV cache rows
+ * 0 .. lens[b]-1, and each decode step adds one token to every sequence.
+ * NEON_PREFILL_CHUNKED packs the prompt rows of all sequences into its
+ * 16-row passes (a sequence's rows in position order), STEPWISE runs them
+ * one row at a time and BATCHED one matrix-core pass per sequence; in the
+ * exact modes each sequence's logits are bit-identical to prefilling it
+ * alone.  neon_read_tokens gives 0 past a sequence's length.  max_seq bounds
+ * the longest sequence.  (No counterpart in the reference.) */
+neon_status neon_prefill_ragged(neon_ctx* ctx, const int32_t* ids,
+                                const int32_t* lens, int batch, void* stream);
+
 enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1, NEON_PREFILL_CHUNKED = 2 };
 /* Selects how neon_prefill runs the prompt (default NEON_PREFILL_CHUNKED). */
 neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
@@ -163,8 +177,13 @@ neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
 neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
                                  size_t bytes, void* stream);
 
-/* Number of tokens held by each sequence (prompt + generated). */
+/* Number of tokens held by the longest sequence (prompt + generated); with
+ * equal prompt lengths every sequence holds this many. */
 neon_status neon_seq_len(const neon_ctx* ctx, int* out);
+
+/* Number of tokens held by each sequence (prompt + generated), out[batch];
+ * NEON_ESTATE before the first prefill. */
+neon_status neon_seq_lens(const neon_ctx* ctx, int32_t* out);
 
 /* Device pointer of a weight tensor (same names as neon_load_tensor), for
  * tests and tools; *bytes receives its size.  Read it freely; bytes written

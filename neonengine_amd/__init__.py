@@ -36,6 +36,7 @@ EXPORTS = (
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
     "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
     "neon_gemv_bf16_mfma", "neon_device_check", "neon_moe_layer_noalloc",
+    "neon_prefill_ragged", "neon_seq_lens",
 )
 
 
@@ -88,11 +89,13 @@ def lib():
             "neon_init_random": [_P, _U64, _P],
             "neon_load_tensor": [_P, C.c_char_p, _P, _SZ],
             "neon_prefill": [_P, _P, _I, _I, _P],
+            "neon_prefill_ragged": [_P, _P, _P, _I, _P],
             "neon_decode": [_P, _I, _P],
             "neon_read_tokens": [_P, _I, _I, _P, _P],
             "neon_read_logits": [_P, _P, _P],
             "neon_read_activation": [_P, C.c_char_p, _P, _SZ, _P],
             "neon_seq_len": [_P, _P],
+            "neon_seq_lens": [_P, _P],
             "neon_tensor_ptr": [_P, C.c_char_p, _P, _P],
             "neon_mxfp4_dequant": [_P, _P, _I64, _P, _P],
             "neon_mxfp4_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
@@ -343,14 +346,36 @@ class Engine:
         self._chk(lib().neon_set_sampling(self._ctx, temperature, top_p, seed))
 
     def prefill(self, ids, stream=None):
-        """ids: nested list / array [batch][n_tokens] of int."""
+        """ids: nested list / array [batch][n_tokens] of int, or a list of
+        prompts of different lengths (neon_prefill_ragged)."""
         import numpy as np
+        if isinstance(ids, (list, tuple)) and ids and not np.isscalar(ids[0]) and \
+                len({len(p) for p in ids}) > 1:
+            return self.prefill_ragged(ids, stream)
         a = np.ascontiguousarray(ids, dtype=np.int32)
         if a.ndim == 1:
             a = a[None, :]
         self._chk(lib().neon_prefill(self._ctx, a.ctypes.data_as(C.c_void_p), a.shape[0],
                                      a.shape[1], _stream(stream)))
         self.batch = a.shape[0]
+
+    def prefill_ragged(self, prompts, stream=None):
+        """prompts: one sequence of int ids per sequence, lengths free."""
+        import numpy as np
+        lens = np.ascontiguousarray([len(p) for p in prompts], dtype=np.int32)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int64) for p in prompts])
+                                    if len(prompts) else np.zeros(0), dtype=np.int32)
+        self._chk(lib().neon_prefill_ragged(self._ctx, flat.ctypes.data_as(C.c_void_p),
+                                            lens.ctypes.data_as(C.c_void_p), len(prompts),
+                                            _stream(stream)))
+        self.batch = len(prompts)
+
+    def seq_lens(self):
+        """Tokens held by each sequence (prompt + generated), int32 [batch]."""
+        import numpy as np
+        out = np.empty(max(self.batch, 1), np.int32)
+        self._chk(lib().neon_seq_lens(self._ctx, out.ctypes.data_as(C.c_void_p)))
+        return out[:self.batch]
 
     def decode(self, n_steps: int, stream=None):
         self._chk(lib().neon_decode(self._ctx, n_steps, _stream(stream)))

@@ -90,7 +90,8 @@ struct neon_ctx {
   int s_full = 1, s_slide = 1;
   // sequence state (host mirror)
   int batch = 0;
-  int host_pos = 0;
+  int host_pos = 0;                // the longest sequence's position
+  std::vector<int> host_plen;      // prompt length of each sequence
   bool weights_ready = false;
   // batched prefill (M prompt rows per pass): scratch grown on demand
   int prefill_mode = NEON_PREFILL_CHUNKED;
@@ -957,80 +958,105 @@ extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
   return NEON_OK;
 }
 
-extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
-                                    int n_tokens, void* stream) {
-  if (!ctx) return NEON_EINVAL;
+// The prompt pass shared by neon_prefill and neon_prefill_ragged: sequence
+// b's prompt is ids[start[b] .. start[b] + lens[b]).  Each sequence keeps its
+// own position: rows 0 .. lens[b]-2 fill its KV cache, then one decode step
+// at position lens[b]-1 (every sequence at its own) gives each its first
+// generated token.
+static neon_status prefill_seqs(neon_ctx* ctx, const int32_t* ids, const int32_t* lens,
+                                int batch, hipStream_t st, const char* fn) {
   const neon_config& c = ctx->cfg;
-  if (!ids) FAIL(ctx, NEON_EINVAL, "neon_prefill: null ids");
+  if (!ids || !lens) FAIL(ctx, NEON_EINVAL, "%s: null ids or lengths", fn);
   if (batch < 1 || batch > c.max_batch)
-    FAIL(ctx, NEON_EINVAL, "neon_prefill: batch %d outside [1, %d]", batch, c.max_batch);
-  if (n_tokens < 1) FAIL(ctx, NEON_EINVAL, "neon_prefill: n_tokens must be >= 1");
-  if (n_tokens > c.max_seq)
-    FAIL(ctx, NEON_EKV_FULL, "neon_prefill: %d tokens exceed max_seq %d", n_tokens, c.max_seq);
-  for (int64_t i = 0; i < (int64_t)batch * n_tokens; ++i)
+    FAIL(ctx, NEON_EINVAL, "%s: batch %d outside [1, %d]", fn, batch, c.max_batch);
+  std::vector<int64_t> start(batch + 1, 0);
+  int max_len = 0;
+  bool equal = true;
+  for (int b = 0; b < batch; ++b) {
+    if (lens[b] < 1) FAIL(ctx, NEON_EINVAL, "%s: sequence %d has %d tokens; need >= 1", fn, b, lens[b]);
+    if (lens[b] > c.max_seq)
+      FAIL(ctx, NEON_EKV_FULL, "%s: %d tokens of sequence %d exceed max_seq %d", fn, lens[b], b,
+           c.max_seq);
+    start[b + 1] = start[b] + lens[b];
+    max_len = std::max(max_len, lens[b]);
+    equal = equal && lens[b] == lens[0];
+  }
+  for (int64_t i = 0; i < start[batch]; ++i)
     if (ids[i] < 0 || ids[i] >= c.vocab)
-      FAIL(ctx, NEON_ERANGE_TOKEN, "neon_prefill: token id %d at %lld outside [0, %d)",
-           ids[i], (long long)i, c.vocab);
-  if (!ctx->weights_ready) FAIL(ctx, NEON_ESTATE, "neon_prefill: no weights loaded");
+      FAIL(ctx, NEON_ERANGE_TOKEN, "%s: token id %d at %lld outside [0, %d)", fn, ids[i],
+           (long long)i, c.vocab);
+  if (!ctx->weights_ready) FAIL(ctx, NEON_ESTATE, "%s: no weights loaded", fn);
   HIPCHK(ctx, hipSetDevice(ctx->device));
-  hipStream_t st = S(stream);
   std::vector<int32_t> tok((size_t)batch * ctx->tok_stride, 0);
   for (int b = 0; b < batch; ++b)
-    memcpy(&tok[(size_t)b * ctx->tok_stride], ids + (size_t)b * n_tokens, n_tokens * 4);
-  std::vector<int32_t> zeros(batch, 0), plen(batch, n_tokens);
+    memcpy(&tok[(size_t)b * ctx->tok_stride], ids + start[b], (size_t)lens[b] * 4);
+  std::vector<int32_t> zeros(batch, 0), plen(lens, lens + batch);
   HIPCHK(ctx, hipMemcpyAsync(ctx->tokens, tok.data(), tok.size() * 4, hipMemcpyHostToDevice, st));
   HIPCHK(ctx, hipMemcpyAsync(ctx->pos, zeros.data(), batch * 4, hipMemcpyHostToDevice, st));
   HIPCHK(ctx, hipMemcpyAsync(ctx->prompt_len, plen.data(), batch * 4, hipMemcpyHostToDevice, st));
   HIPCHK(ctx, hipStreamSynchronize(st));  // host staging buffers die here
   ctx->batch = batch;
   ctx->host_pos = 0;
-  if (ctx->prefill_mode == NEON_PREFILL_CHUNKED && n_tokens > 1) {
-    // prompt rows 0 .. n-2 of each sequence, kPromptRows at a time through the
-    // layers (their k / v fill the cache; row p attends to keys <= p), then
-    // the last prompt token as an ordinary decode step (logits, first token).
-    // The passes' (position, sequence) rows are staged up front and stay
-    // alive until the stream is synchronised below.
-    const int M = n_tokens - 1;
-    const int per_seq = (M + kPromptRows - 1) / kPromptRows;
-    std::vector<int32_t> rows((size_t)batch * per_seq * 2 * kPromptRows, 0);
+  ctx->host_plen.assign(lens, lens + batch);
+  if (max_len == 1 || (ctx->prefill_mode == NEON_PREFILL_STEPWISE && equal)) {
+    // every prompt token as a decode step of all sequences together
+    neon_status s = run_steps(ctx, max_len, st);
+    if (s != NEON_OK) return s;
+    ctx->host_pos = max_len;
+    return NEON_OK;
+  }
+  if (ctx->prefill_mode == NEON_PREFILL_BATCHED) {
+    // each sequence's rows 0 .. n-2 in one matrix-core pass
+    neon_status s = ensure_prefill_scratch(ctx, max_len - 1, st);
+    if (s != NEON_OK) return s;
     for (int b = 0; b < batch; ++b)
-      for (int i = 0; i < per_seq; ++i) {
-        const int p0 = i * kPromptRows, R = std::min(kPromptRows, M - p0);
-        int32_t* r = &rows[((size_t)b * per_seq + i) * 2 * kPromptRows];
-        for (int j = 0; j < R; ++j) { r[j] = p0 + j; r[kPromptRows + j] = b; }
-        HIPCHK(ctx, hipMemcpyAsync(ctx->row_pos, r, R * 4, hipMemcpyHostToDevice, st));
-        HIPCHK(ctx, hipMemcpyAsync(ctx->row_seq, r + kPromptRows, R * 4, hipMemcpyHostToDevice, st));
-        enqueue_rows(ctx, R, ctx->row_pos, ctx->row_seq, st);
-      }
-    HIPCHK(ctx, hipGetLastError());
-    std::vector<int32_t> pm(batch, M);
-    HIPCHK(ctx, hipMemcpyAsync(ctx->pos, pm.data(), batch * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipStreamSynchronize(st));  // rows and pm die here
-    neon_status s = run_steps(ctx, 1, st);
-    if (s != NEON_OK) return s;
-    ctx->host_pos = n_tokens;
-    return NEON_OK;
+      if (lens[b] > 1) enqueue_prefill_rows(ctx, b, lens[b] - 1, st);
+  } else {
+    // NEON_PREFILL_CHUNKED: the (position, sequence) rows of all sequences,
+    // each sequence's in position order, kPromptRows at a time through the
+    // batched decode kernels (their k / v fill the cache before the pass's
+    // attention, so row p attends to its sequence's keys <= p).
+    // NEON_PREFILL_STEPWISE with different lengths: the same rows one at a
+    // time.  The rows are staged up front and stay alive until the stream is
+    // synchronised below.
+    const int per = ctx->prefill_mode == NEON_PREFILL_STEPWISE ? 1 : kPromptRows;
+    std::vector<int32_t> rp, rs;
+    for (int b = 0; b < batch; ++b)
+      for (int p = 0; p + 1 < lens[b]; ++p) { rp.push_back(p); rs.push_back(b); }
+    const size_t n_rows = rp.size();
+    for (size_t r0 = 0; r0 < n_rows; r0 += per) {
+      const int R = (int)std::min<size_t>(per, n_rows - r0);
+      HIPCHK(ctx, hipMemcpyAsync(ctx->row_pos, &rp[r0], R * 4, hipMemcpyHostToDevice, st));
+      HIPCHK(ctx, hipMemcpyAsync(ctx->row_seq, &rs[r0], R * 4, hipMemcpyHostToDevice, st));
+      enqueue_rows(ctx, R, ctx->row_pos, ctx->row_seq, st);
+    }
+    HIPCHK(ctx, hipStreamSynchronize(st));  // rp and rs die here
   }
-  if (ctx->prefill_mode == NEON_PREFILL_BATCHED && n_tokens > 1) {
-    // prompt rows 0 .. n-2 in one pass per sequence, then the last prompt
-    // token as an ordinary decode step (logits, first generated token)
-    const int M = n_tokens - 1;
-    neon_status s = ensure_prefill_scratch(ctx, M, st);
-    if (s != NEON_OK) return s;
-    for (int b = 0; b < batch; ++b) enqueue_prefill_rows(ctx, b, M, st);
-    HIPCHK(ctx, hipGetLastError());
-    std::vector<int32_t> pm(batch, M);
-    HIPCHK(ctx, hipMemcpyAsync(ctx->pos, pm.data(), batch * 4, hipMemcpyHostToDevice, st));
-    HIPCHK(ctx, hipStreamSynchronize(st));  // pm dies here
-    s = run_steps(ctx, 1, st);
-    if (s != NEON_OK) return s;
-    ctx->host_pos = n_tokens;
-    return NEON_OK;
-  }
-  neon_status s = run_steps(ctx, n_tokens, st);
+  HIPCHK(ctx, hipGetLastError());
+  std::vector<int32_t> pm(batch);
+  for (int b = 0; b < batch; ++b) pm[b] = lens[b] - 1;
+  HIPCHK(ctx, hipMemcpyAsync(ctx->pos, pm.data(), batch * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipStreamSynchronize(st));  // pm dies here
+  neon_status s = run_steps(ctx, 1, st);
   if (s != NEON_OK) return s;
-  ctx->host_pos = n_tokens;
+  ctx->host_pos = max_len;
   return NEON_OK;
+}
+
+extern "C" neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
+                                    int n_tokens, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (n_tokens < 1) FAIL(ctx, NEON_EINVAL, "neon_prefill: n_tokens must be >= 1");
+  if (batch < 1 || batch > ctx->cfg.max_batch)
+    FAIL(ctx, NEON_EINVAL, "neon_prefill: batch %d outside [1, %d]", batch, ctx->cfg.max_batch);
+  const std::vector<int32_t> lens(batch, n_tokens);
+  return prefill_seqs(ctx, ids, lens.data(), batch, S(stream), "neon_prefill");
+}
+
+extern "C" neon_status neon_prefill_ragged(neon_ctx* ctx, const int32_t* ids,
+                                           const int32_t* lens, int batch, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  return prefill_seqs(ctx, ids, lens, batch, S(stream), "neon_prefill_ragged");
 }
 
 extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
@@ -1200,6 +1226,15 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
 extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
   if (!ctx || !out) return NEON_EINVAL;
   *out = ctx->host_pos + (ctx->batch ? 1 : 0);
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_seq_lens(const neon_ctx* ctx, int32_t* out) {
+  if (!ctx || !out) return NEON_EINVAL;
+  if (ctx->batch == 0) return NEON_ESTATE;
+  const int max_plen = *std::max_element(ctx->host_plen.begin(), ctx->host_plen.end());
+  for (int b = 0; b < ctx->batch; ++b)
+    out[b] = ctx->host_plen[b] + 1 + (ctx->host_pos - max_plen);
   return NEON_OK;
 }
 

@@ -1266,6 +1266,11 @@ void or_model_step(or_model* m, const int32_t* ids, float* logits,
     }
     for (size_t i = 0; i < (size_t)B * H; ++i) m->h[i] = TOBF(BF(m->h[i]) + BF(tmp[i]));
   }
+  if (!logits && !out_ids) {  /* a teacher-forced prompt row: no lm_head */
+    for (int b = 0; b < B; ++b) m->pos[b] = m->pos[b] + 1;
+    free(xn); free(qkv); free(qr); free(ao); free(tmp); free(lg); free(idx); free(sc);
+    return;
+  }
   m_rmsnorm(m->h, m->final_norm, B, H, c->rms_eps, xn);
   m_gemv_bf16(m->lm_head, NULL, xn, B, (int)V, H, NULL, lg);
   for (int b = 0; b < B; ++b) {

@@ -155,7 +155,9 @@ int or_model_set_tensor(or_model* m, int layer, int kind, const void* data, size
 void or_set_accumulation(int mode);
 void or_model_free(or_model* m);
 /* One decode step for every sequence: consumes ids[b] at position pos[b],
- * writes logits (fp32 [B][V], may be NULL) and greedy ids. */
+ * writes logits (fp32 [B][V], may be NULL) and greedy ids (may be NULL).
+ * With both NULL the step is a teacher-forced prompt row: the KV cache and
+ * positions advance and lm_head is skipped. */
 void or_model_step(or_model* m, const int32_t* ids, float* logits,
                    int32_t* out_ids);
 /* hidden state (bf16 [B][H]) after the last completed step, before the final

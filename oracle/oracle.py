@@ -427,6 +427,12 @@ class Model:
         lib().or_model_step(self._h, _p(ids), _p(lg), _p(out))
         return out, lg
 
+    def prompt_step(self, ids):
+        """A teacher-forced prompt row for every sequence: fills the KV cache
+        at each sequence's position and advances it, without lm_head."""
+        ids = _c(ids, np.int32).reshape(self.batch)
+        lib().or_model_step(self._h, _p(ids), None, None)
+
     def set_tensor(self, layer, kind, data):
         a = np.ascontiguousarray(data)
         if lib().or_model_set_tensor(self._h, layer, kind, _p(a), a.nbytes) != 0:

@@ -14,6 +14,9 @@ Cases:
             regenerates each chosen expert from the counter RNG, so the
             65 GB of experts never sit in host memory), 4 prompt tokens, then
             24 greedy steps.
+  ragged20b gpt-oss-20b shape, four sequences with prompts of 5, 77, 300
+            and 1000 tokens decoding together (neon_prefill_ragged), then 16
+            greedy steps; the oracle runs each sequence alone at batch 1.
 
 Run: python tests/golden/make_model_fixtures.py [case ...]   (CPU only; the
 20b prompt case takes about 40 minutes on 8 cores).  Test infrastructure: it
@@ -39,6 +42,8 @@ CASES = {
                     prompt_seed=16),
     "l120b": dict(shape="120b", seed=2, batch=1, prompt_len=4, steps=24, max_seq=64,
                   prompt_seed=120),
+    "ragged20b": dict(shape="20b", seed=4, lens=(5, 77, 300, 1000), steps=16, max_seq=1040,
+                      prompt_seed=1382),
 }
 
 
@@ -53,7 +58,51 @@ def digest(row):
                          np.uint8)
 
 
+def run_ragged_case(name):
+    """Each sequence alone through a batch-1 oracle: teacher-forced prompt rows
+    (no lm_head), then the last prompt token and `steps` greedy steps."""
+    case = CASES[name]
+    lens = case["lens"]
+    B, n = len(lens), case["steps"] + 1
+    rng = np.random.default_rng(case["prompt_seed"])
+    flat = rng.integers(0, orc.GPT_OSS_20B["vocab"], sum(lens), dtype=np.int32)
+    cfg = orc.make_config(**dict(orc.GPT_OSS_20B, max_seq=case["max_seq"], max_batch=1))
+    out_ids = np.zeros((B, n), np.int32)
+    sha = np.zeros((B, n, 32), np.uint8)
+    margin = np.zeros((B, n), np.float32)
+    top_id = np.zeros((B, n, 8), np.int32)
+    top_val = np.zeros((B, n, 8), np.float32)
+    t0 = time.time()
+    start = 0
+    for b, L in enumerate(lens):
+        prompt = flat[start:start + L]
+        start += L
+        m = orc.Model(cfg, seed=case["seed"], batch=1)
+        for t in range(L - 1):
+            m.prompt_step(prompt[t:t + 1])
+            if t % 128 == 0:
+                print(f"[{name}] sequence {b} prompt {t}/{L} {time.time() - t0:.0f}s", flush=True)
+        ids = prompt[-1:]
+        for s in range(n):
+            ids, lg = m.step(ids)
+            order = np.argsort(-lg[0], kind="stable")[:8]
+            top_id[b, s] = order
+            top_val[b, s] = lg[0, order]
+            margin[b, s] = lg[0, order[0]] - lg[0, order[1]]
+            sha[b, s] = digest(lg[0])
+            out_ids[b, s] = ids[0]
+        print(f"[{name}] sequence {b} ids {out_ids[b, :6]} {time.time() - t0:.0f}s", flush=True)
+        m.close()
+    return {f"{name}__{k}": v for k, v in dict(
+        prompt=flat, lens=np.array(lens, np.int32), ids=out_ids, sha=sha, margin=margin,
+        top_id=top_id, top_val=top_val,
+        meta=np.array([case["seed"], B, 0, case["steps"], case["max_seq"], 24],
+                      np.int64)).items()}
+
+
 def run_case(name):
+    if "lens" in CASES[name]:
+        return run_ragged_case(name)
     case = CASES[name]
     shape = orc.GPT_OSS_20B if case["shape"] == "20b" else orc.GPT_OSS_120B
     B = case["batch"]

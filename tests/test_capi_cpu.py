@@ -68,6 +68,8 @@ def test_context_calls_reject_null_context():
     assert L.neon_read_logits(None, None, None) == ne.NEON_EINVAL
     assert L.neon_read_activation(None, b"hidden", None, 0, None) == ne.NEON_EINVAL
     assert L.neon_seq_len(None, None) == ne.NEON_EINVAL
+    assert L.neon_prefill_ragged(None, None, None, 1, None) == ne.NEON_EINVAL
+    assert L.neon_seq_lens(None, None) == ne.NEON_EINVAL
     assert L.neon_set_sampling(None, 1.0, 0.9, 0) == ne.NEON_EINVAL
     L.neon_ctx_destroy(None)  # no-op
 

@@ -579,3 +579,21 @@ def test_c_attn_split_count_only_reorders(orc):
     assert orc.attn_splits(4096, 128) == 1 and orc.attn_splits(4096, 0) == 32
     assert orc.attn_splits(100, 0) == 1 and orc.attn_splits(1, 0) == 1
     assert orc.attn_splits(256, 0) == 1 and orc.attn_splits(257, 0) == 5
+
+
+def test_prompt_step_equals_full_step(orc):
+    """A teacher-forced prompt row without lm_head leaves the model in the
+    same state as a full step: the next step's logits are identical."""
+    cfg = orc.make_config(n_layers=2, hidden=128, n_heads=8, n_kv_heads=2, n_experts=4, top_k=2,
+                          intermediate=128, vocab=512, sliding_window=4, max_seq=16, max_batch=2)
+    prompt = np.array([[3, 9, 27, 81, 5, 7], [1, 2, 3, 4, 5, 6]], np.int32)
+    a = orc.Model(cfg, seed=4, batch=2)
+    b = orc.Model(cfg, seed=4, batch=2)
+    for t in range(prompt.shape[1] - 1):
+        a.step(prompt[:, t])
+        b.prompt_step(prompt[:, t])
+    ia, la = a.step(prompt[:, -1])
+    ib, lb = b.step(prompt[:, -1])
+    a.close()
+    b.close()
+    assert np.array_equal(la, lb) and np.array_equal(ia, ib)
