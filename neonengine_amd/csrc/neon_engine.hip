@@ -1555,8 +1555,10 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   hipStream_t st = S(stream);
   const int nsplit = attn_splits(T_max, window);
   const size_t np = (size_t)B * Hq * nsplit;
-  float* scratch = nullptr;  // split partials: o [np][D], then (m, l) [np][2]
-  if (hipMallocAsync((void**)&scratch, np * (D + 2) * 4, st) != hipSuccess)
+  // split partials: o [np][D], then (m, l) [np][2]; one split finishes in
+  // the split kernel and needs none
+  float* scratch = nullptr;
+  if (nsplit > 1 && hipMallocAsync((void**)&scratch, np * (D + 2) * 4, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
   AttnArgs a;
   a.q = q; a.kc = k_cache; a.vc = v_cache;
@@ -1566,7 +1568,7 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   a.S = nsplit; a.q_stride = Hq * D;
   launch_attn(a, st);
   hipError_t e = hipGetLastError();
-  (void)hipFreeAsync(scratch, st);
+  if (scratch) (void)hipFreeAsync(scratch, st);
   if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
   return NEON_OK;
 }

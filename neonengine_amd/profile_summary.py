@@ -3,10 +3,14 @@
     python -m neonengine_amd.profile_summary <run_kernel_trace.csv> \
         --last-steps K --kernels-per-step N [--bytes name=BYTES ...]
     python -m neonengine_amd.profile_summary --pmc <run_counter_collection.csv>
+    python -m neonengine_amd.profile_summary --segments <run_kernel_trace.csv>
 
 The first form reads a kernel trace; the second averages each counter per
 dispatch and kernel name (rocprofv3 --pmc output, e.g. FETCH_SIZE and
-WRITE_SIZE in KiB per dispatch).
+WRITE_SIZE in KiB per dispatch); the third splits a trace into segments of
+consecutive dispatches of one kernel with one grid, or of two kernels in
+turn (a sweep point's timed launches), and prints each segment's count and
+average duration in order.
 
 Keeps the last K decode steps (K * N dispatches; the gpt-oss step has
 N = 1 + 6 n_layers + (one attention merge per layer with several key splits)
@@ -46,10 +50,50 @@ def pmc_summary(path: str):
         print(f"| {key[0]} | {key[1]} | {n} | {vals[key] / n:.1f} |")
 
 
+def segments(path: str, min_count: int):
+    """Runs of consecutive dispatches that repeat one kernel (one grid), or a
+    pair of kernels in turn (a split kernel and its merge): one row per run,
+    with the average duration of one repetition (the pair's sum)."""
+    rows = []
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            grid = tuple(r.get(f"Grid_Size_{d}", "") for d in "XYZ")
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                         (short(r["Kernel_Name"]), "x".join(grid))))
+    rows.sort()
+    rows = [r for r in rows if not r[2][0].startswith("__amd")]
+    segs, i = [], 0
+    while i < len(rows):
+        key = rows[i][2]
+        period = 1
+        if (i + 2 < len(rows) and rows[i + 1][2] != key and rows[i + 2][2] == key
+                and (i + 3 >= len(rows) or rows[i + 3][2] == rows[i + 1][2])):
+            period = 2
+        unit = [rows[i + j][2] for j in range(period)]
+        reps = []
+        while i + period <= len(rows) and [rows[i + j][2] for j in range(period)] == unit:
+            reps.append(sum(rows[i + j][1] - rows[i + j][0] for j in range(period)))
+            i += period
+        segs.append((unit, reps))
+    print("| segment | kernel(s) | grid(s) | repetitions | avg us | min us |")
+    print("|---|---|---|---|---|---|")
+    n = 0
+    for unit, d in segs:
+        if len(d) < min_count:
+            continue
+        print(f"| {n} | {' + '.join(k for k, _ in unit)} | {' + '.join(g for _, g in unit)} | "
+              f"{len(d)} | {sum(d) / len(d) / 1e3:.2f} | {min(d) / 1e3:.2f} |")
+        n += 1
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
     ap.add_argument("--pmc", action="store_true", help="the file is counter_collection.csv")
+    ap.add_argument("--segments", action="store_true",
+                    help="per-segment table of consecutive same-kernel, same-grid dispatches")
+    ap.add_argument("--min-count", type=int, default=8,
+                    help="--segments: skip segments with fewer dispatches")
     ap.add_argument("--last-steps", type=int)
     ap.add_argument("--kernels-per-step", type=int)
     ap.add_argument("--bytes", action="append", default=[],
@@ -60,6 +104,9 @@ def main(argv=None):
     a = ap.parse_args(argv)
     if a.pmc:
         pmc_summary(a.trace)
+        return
+    if a.segments:
+        segments(a.trace, a.min_count)
         return
     if not a.last_steps or not a.kernels_per_step:
         sys.exit("--last-steps and --kernels-per-step are required for a kernel trace")
