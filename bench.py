@@ -371,6 +371,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prompt-only", type=int, default=0, metavar="N",
                     help="profiling aid: run the matrix-core prompt pass N times and exit")
+    ap.add_argument("--mx8", action="store_true",
+                    help="with --prompt-only: the MXFP8 x MXFP4 expert GEMMs (NEON_PREFILL_MX8)")
     ap.add_argument("--moe-only", action="store_true",
                     help="only the MoE launch-pair timing plus a plain 256 MiB device copy "
                          "(the reference kernel for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -403,7 +405,7 @@ def main():
         cfg = ne.config_preset(args.model, max_seq=args.prompt + 8, max_batch=1)
         eng = ne.Engine(cfg, device=0)
         eng.init_random(args.seed)
-        eng.set_prefill_mode(ne.PREFILL_BATCHED)
+        eng.set_prefill_mode(ne.PREFILL_MX8 if args.mx8 else ne.PREFILL_BATCHED)
         prompt = np.random.default_rng(args.seed).integers(0, cfg.vocab, size=(1, args.prompt))
         for i in range(args.prompt_only):
             eng.prefill(prompt)
@@ -447,6 +449,12 @@ def main():
         mfma_s = timed_prefill()
         log(f"[bench] matrix-core prompt pass: {mfma_s * 1e3:.1f} ms = "
             f"{args.prompt / mfma_s:.0f} tok/s")
+        # the same with the expert GEMMs on the scaled fp8 x fp4 instruction
+        eng.set_prefill_mode(ne.PREFILL_MX8)
+        eng.prefill(prompt, stream)
+        mx8_s = timed_prefill()
+        log(f"[bench] matrix-core prompt pass, MXFP8 x MXFP4 experts: {mx8_s * 1e3:.1f} ms = "
+            f"{args.prompt / mx8_s:.0f} tok/s")
         # then the library's default mode, whose cache the decode steps use:
         # prompt rows 16 at a time through the batched decode kernels
         # (bit-identical to running every prompt token as a decode step)
@@ -462,6 +470,10 @@ def main():
                        "tflop_per_s": round(flops / mfma_s / 1e12, 1),
                        "frac_of_bf16_mfma_peak": round(flops / mfma_s / 1e12
                                                        / MFMA_BF16_PEAK_TFLOPS, 4)},
+                   "matrix_core_pass_mx8_experts": {
+                       "ms": round(mx8_s * 1e3, 3),
+                       "tokens_per_s": round(args.prompt / mx8_s, 1),
+                       "tflop_per_s": round(flops / mx8_s / 1e12, 1)},
                    "flop_batched_form": flops}
         log(f"[bench] prompt pass: {pre_s * 1e3:.1f} ms = {args.prompt / pre_s:.0f} tok/s")
     eng.decode(args.warmup, stream)

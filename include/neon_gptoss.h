@@ -119,7 +119,16 @@ neon_status neon_prefill(neon_ctx* ctx, const int32_t* ids, int batch,
 neon_status neon_prefill_ragged(neon_ctx* ctx, const int32_t* ids,
                                 const int32_t* lens, int batch, void* stream);
 
-enum { NEON_PREFILL_BATCHED = 0, NEON_PREFILL_STEPWISE = 1, NEON_PREFILL_CHUNKED = 2 };
+enum {
+  NEON_PREFILL_BATCHED = 0,
+  NEON_PREFILL_STEPWISE = 1,
+  NEON_PREFILL_CHUNKED = 2,
+  /* NEON_PREFILL_BATCHED with the expert GEMMs on the scaled fp8 x fp4
+   * matrix instruction: each bf16 input block of 32 carried as two MXFP8
+   * (E4M3) terms, the MXFP4 expert rows read as stored (hidden and
+   * intermediate are multiples of 64 in every context). */
+  NEON_PREFILL_MX8 = 3
+};
 /* Selects how neon_prefill runs the prompt (default NEON_PREFILL_CHUNKED). */
 neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
 
@@ -329,6 +338,32 @@ neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
                              const uint16_t* dn_bias, uint16_t* h, int M, int E,
                              int H, int I, int k, float alpha, float limit,
                              void* stream);
+
+/* neon_moe_prefill with both expert GEMMs on the scaled fp8 x fp4 matrix
+ * instruction (v_mfma_scale_f32_32x32x64_f8f6f4): the GEMM inputs (x, then
+ * the SwiGLU output) become two MXFP8 terms per 32-element block
+ * (neon_mx8_quant), the MXFP4 expert rows are read as stored.  H and I
+ * multiples of 64.  Used by NEON_PREFILL_MX8.  (No counterpart in the
+ * reference.) */
+neon_status neon_moe_prefill_mx8(const uint16_t* x, const int32_t* idx,
+                                 const float* score, const uint8_t* gu_codes,
+                                 const uint8_t* gu_scales, const uint16_t* gu_bias,
+                                 const uint8_t* dn_codes, const uint8_t* dn_scales,
+                                 const uint16_t* dn_bias, uint16_t* h, int M, int E,
+                                 int H, int I, int k, float alpha, float limit,
+                                 void* stream);
+
+/* The two-term MXFP8 image of bf16 rows x [rows][K] (K % 32 == 0): for each
+ * 32-element block, hi = E4M3(x / 2^e1) rounded to nearest even, with
+ * e1 = floor(log2 amax) - 8, plus one when amax's significand exceeds 1.75
+ * (so no element passes 448), and scale byte s_hi = e1 + 127; lo = the same
+ * rule on the exact residual x - hi 2^e1.  hi + lo is within
+ * 2^(floor(log2 amax) - 8) of every finite element.
+ * hi, lo [rows][K]; s_hi, s_lo [rows][K/32].  A zero block gets scale 127
+ * and zero codes; a non-finite element gets the NaN code 0x7F in hi and 0
+ * in lo.  (OCP MX v1.0; no counterpart in the reference.) */
+neon_status neon_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi,
+                           uint8_t* lo, uint8_t* s_hi, uint8_t* s_lo, void* stream);
 
 /* Causal sink attention over a prompt: q [M][Hq][D] (rotated) at positions
  * 0 .. M-1, caches [Hkv][T_max][D] holding keys/values 0 .. M-1; row t sees

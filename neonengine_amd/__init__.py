@@ -36,7 +36,7 @@ EXPORTS = (
     "neon_attn_decode", "neon_set_prefill_mode", "neon_gemm_bf16", "neon_moe_prefill",
     "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
     "neon_gemv_bf16_mfma", "neon_device_check", "neon_moe_layer_noalloc",
-    "neon_prefill_ragged", "neon_seq_lens",
+    "neon_prefill_ragged", "neon_seq_lens", "neon_moe_prefill_mx8", "neon_mx8_quant",
 )
 
 
@@ -109,6 +109,8 @@ def lib():
             "neon_set_prefill_mode": [_P, _I],
             "neon_gemm_bf16": [_P] * 4 + [_I] * 4 + [_P],
             "neon_moe_prefill": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
+            "neon_moe_prefill_mx8": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
+            "neon_mx8_quant": [_P, _I64, _I, _P, _P, _P, _P, _P],
             "neon_attn_prefill": [_P] * 5 + [_I] * 6 + [_P],
             "neon_set_sampling": [_P, _F, _F, _U64],
             "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P],
@@ -258,6 +260,19 @@ def moe_prefill(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales
         _stream(stream)))
 
 
+def moe_prefill_mx8(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
+                    h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None):
+    _check(lib().neon_moe_prefill_mx8(
+        _ptr(x), _ptr(idx), _ptr(score), _ptr(gu_codes), _ptr(gu_scales), _ptr(gu_bias),
+        _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(h), M, E, H, I, k, alpha, limit,
+        _stream(stream)))
+
+
+def mx8_quant(x, rows, K, hi, lo, s_hi, s_lo, stream=None):
+    _check(lib().neon_mx8_quant(_ptr(x), rows, K, _ptr(hi), _ptr(lo), _ptr(s_hi), _ptr(s_lo),
+                                _stream(stream)))
+
+
 def attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, D, T_max, window, stream=None):
     _check(lib().neon_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(sinks),
                                    _ptr(out), M, Hq, Hkv, D, T_max, window, _stream(stream)))
@@ -268,7 +283,7 @@ def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=N
                              _ptr(out_ids), _stream(stream)))
 
 
-PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED = 0, 1, 2
+PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED, PREFILL_MX8 = 0, 1, 2, 3
 DECODE_EXACT, DECODE_MATRIX = 0, 1
 
 

@@ -99,6 +99,7 @@ struct neon_ctx {
   int pf_rows = 0;
   uint16_t *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
            *pf_ao = nullptr, *pf_act = nullptr, *pf_ks = nullptr, *pf_vs = nullptr;
+  uint8_t *pf_qh = nullptr, *pf_ql = nullptr, *pf_qsh = nullptr, *pf_qsl = nullptr;
   float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
   int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
           *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
@@ -871,6 +872,10 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
                o_eo = take((E + 1) * 4), o_te = take(tiles * 4), o_tr = take(tiles * 4),
                o_nt = take(4), o_ks = take(M * c.n_kv_heads * c.head_dim * 2),
                o_vs = take(M * c.n_kv_heads * c.head_dim * 2);
+  // MXFP8 images of the expert GEMM inputs (NEON_PREFILL_MX8): xn rows, then
+  // the act rows, in the same buffers
+  const size_t qn = std::max(M * H, M * k * I);
+  const size_t o_qh = take(qn), o_ql = take(qn), o_qsh = take(qn / 32), o_qsl = take(qn / 32);
   if (ctx->pf) {
     HIPCHK(ctx, hipStreamSynchronize(st));  // earlier prefill work may still read it
     (void)hipFree(ctx->pf);
@@ -891,6 +896,8 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
   ctx->pf_eoff = (int32_t*)(P + o_eo); ctx->pf_tile_e = (int32_t*)(P + o_te);
   ctx->pf_tile_r0 = (int32_t*)(P + o_tr); ctx->pf_ntiles = (int32_t*)(P + o_nt);
   ctx->pf_ks = (uint16_t*)(P + o_ks); ctx->pf_vs = (uint16_t*)(P + o_vs);
+  ctx->pf_qh = (uint8_t*)(P + o_qh); ctx->pf_ql = (uint8_t*)(P + o_ql);
+  ctx->pf_qsh = (uint8_t*)(P + o_qsh); ctx->pf_qsl = (uint8_t*)(P + o_qsl);
   ctx->pf_rows = (int)M;
   return NEON_OK;
 }
@@ -939,6 +946,9 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
     m.list_tok = ctx->pf_ltok; m.list_slot = ctx->pf_lslot; m.e_off = ctx->pf_eoff;
     m.tile_e = ctx->pf_tile_e; m.tile_r0 = ctx->pf_tile_r0; m.n_tiles = ctx->pf_ntiles;
     m.act = ctx->pf_act; m.ybuf = ctx->pf_ybuf; m.err = ctx->dev_err;
+    if (ctx->prefill_mode == NEON_PREFILL_MX8) {
+      m.q_hi = ctx->pf_qh; m.q_lo = ctx->pf_ql; m.qs_hi = ctx->pf_qsh; m.qs_lo = ctx->pf_qsl;
+    }
     launch_moe_prefill(m, st);
   }
 }
@@ -950,9 +960,9 @@ static const bool kBatchedPrefillEnabled = true;
 extern "C" neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode) {
   if (!ctx) return NEON_EINVAL;
   if (mode != NEON_PREFILL_BATCHED && mode != NEON_PREFILL_STEPWISE &&
-      mode != NEON_PREFILL_CHUNKED)
+      mode != NEON_PREFILL_CHUNKED && mode != NEON_PREFILL_MX8)
     FAIL(ctx, NEON_EINVAL, "neon_set_prefill_mode: unknown mode %d", mode);
-  if (mode == NEON_PREFILL_BATCHED && !kBatchedPrefillEnabled)
+  if ((mode == NEON_PREFILL_BATCHED || mode == NEON_PREFILL_MX8) && !kBatchedPrefillEnabled)
     FAIL(ctx, NEON_ESTATE, "neon_set_prefill_mode: the batched prompt pass is switched off");
   ctx->prefill_mode = mode;
   return NEON_OK;
@@ -1005,7 +1015,7 @@ static neon_status prefill_seqs(neon_ctx* ctx, const int32_t* ids, const int32_t
     ctx->host_pos = max_len;
     return NEON_OK;
   }
-  if (ctx->prefill_mode == NEON_PREFILL_BATCHED) {
+  if (ctx->prefill_mode == NEON_PREFILL_BATCHED || ctx->prefill_mode == NEON_PREFILL_MX8) {
     // each sequence's rows 0 .. n-2 in one matrix-core pass
     neon_status s = ensure_prefill_scratch(ctx, max_len - 1, st);
     if (s != NEON_OK) return s;
@@ -1604,33 +1614,37 @@ extern "C" neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
   KLAUNCHED();
 }
 
-extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
-                                        const float* score, const uint8_t* gu_codes,
-                                        const uint8_t* gu_scales, const uint16_t* gu_bias,
-                                        const uint8_t* dn_codes, const uint8_t* dn_scales,
-                                        const uint16_t* dn_bias, uint16_t* h, int M, int E,
-                                        int H, int I, int k, float alpha, float limit,
-                                        void* stream) {
+// The kernel-level expert FFN over prompt rows, with the bf16-dequantising
+// GEMMs or (mx8) the scaled MXFP8 x MXFP4 ones.
+static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const float* score,
+                                    const uint8_t* gu_codes, const uint8_t* gu_scales,
+                                    const uint16_t* gu_bias, const uint8_t* dn_codes,
+                                    const uint8_t* dn_scales, const uint16_t* dn_bias,
+                                    uint16_t* h, int M, int E, int H, int I, int k, float alpha,
+                                    float limit, void* stream, bool mx8, const char* fn) {
   if (!x || !idx || !score || !gu_codes || !gu_scales || !gu_bias || !dn_codes ||
       !dn_scales || !dn_bias || !h)
-    KFAIL(NEON_EINVAL, "neon_moe_prefill: null pointer");
-  if (M < 1 || M > (1 << 20) || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < 32 ||
-      H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
-    KFAIL(NEON_EINVAL, "neon_moe_prefill: bad shape M=%d E=%d H=%d I=%d k=%d", M, E, H, I, k);
+    KFAIL(NEON_EINVAL, "%s: null pointer", fn);
+  const int kq = mx8 ? 64 : 32;
+  if (M < 1 || M > (1 << 20) || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < kq ||
+      H % kq || H > 8192 || I < kq || I % kq || I > 8192)
+    KFAIL(NEON_EINVAL, "%s: bad shape M=%d E=%d H=%d I=%d k=%d", fn, M, E, H, I, k);
   if (!kBatchedPrefillEnabled)
-    KFAIL(NEON_ESTATE, "neon_moe_prefill: the batched prompt pass is switched off");
+    KFAIL(NEON_ESTATE, "%s: the batched prompt pass is switched off", fn);
   // idx is device data: an entry outside [0, E) drops its slot and sets the
   // device status word (neon_device_check reports it).
   hipStream_t st = S(stream);
   const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
+  const size_t qn = mx8 ? std::max((size_t)M * H, pairs * I) : 0;
   size_t off = 0;
   auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
   const size_t o_yb = take(pairs * H * 4), o_act = take(pairs * I * 2), o_lt = take(pairs * 4),
                o_ls = take(pairs * 4), o_eo = take((E + 1) * 4), o_te = take(tiles * 4),
-               o_tr = take(tiles * 4), o_nt = take(16);
+               o_tr = take(tiles * 4), o_nt = take(16), o_qh = take(qn), o_ql = take(qn),
+               o_qsh = take(qn / 32), o_qsl = take(qn / 32);
   char* scratch = nullptr;
   if (hipMallocAsync((void**)&scratch, off, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_moe_prefill: scratch allocation failed");
+    KFAIL(NEON_ENOMEM, "%s: scratch allocation failed", fn);
   MoePrefillArgs m;
   m.idx = idx; m.score = score; m.xn = x; m.h = h;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
@@ -1640,12 +1654,50 @@ extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
   m.list_tok = (int32_t*)(scratch + o_lt); m.list_slot = (int32_t*)(scratch + o_ls);
   m.e_off = (int32_t*)(scratch + o_eo); m.tile_e = (int32_t*)(scratch + o_te);
   m.tile_r0 = (int32_t*)(scratch + o_tr); m.n_tiles = (int32_t*)(scratch + o_nt);
+  if (mx8) {
+    m.q_hi = (uint8_t*)(scratch + o_qh); m.q_lo = (uint8_t*)(scratch + o_ql);
+    m.qs_hi = (uint8_t*)(scratch + o_qsh); m.qs_lo = (uint8_t*)(scratch + o_qsl);
+  }
   m.err = device_status_word();
   launch_moe_prefill(m, st);
   hipError_t e = hipGetLastError();
   (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_moe_prefill: launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) KFAIL(NEON_EHIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
   return NEON_OK;
+}
+
+extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
+                                        const float* score, const uint8_t* gu_codes,
+                                        const uint8_t* gu_scales, const uint16_t* gu_bias,
+                                        const uint8_t* dn_codes, const uint8_t* dn_scales,
+                                        const uint16_t* dn_bias, uint16_t* h, int M, int E,
+                                        int H, int I, int k, float alpha, float limit,
+                                        void* stream) {
+  return moe_prefill_impl(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
+                          dn_bias, h, M, E, H, I, k, alpha, limit, stream, false,
+                          "neon_moe_prefill");
+}
+
+extern "C" neon_status neon_moe_prefill_mx8(const uint16_t* x, const int32_t* idx,
+                                            const float* score, const uint8_t* gu_codes,
+                                            const uint8_t* gu_scales, const uint16_t* gu_bias,
+                                            const uint8_t* dn_codes, const uint8_t* dn_scales,
+                                            const uint16_t* dn_bias, uint16_t* h, int M, int E,
+                                            int H, int I, int k, float alpha, float limit,
+                                            void* stream) {
+  return moe_prefill_impl(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
+                          dn_bias, h, M, E, H, I, k, alpha, limit, stream, true,
+                          "neon_moe_prefill_mx8");
+}
+
+extern "C" neon_status neon_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi,
+                                      uint8_t* lo, uint8_t* s_hi, uint8_t* s_lo,
+                                      void* stream) {
+  if (!x || !hi || !lo || !s_hi || !s_lo) KFAIL(NEON_EINVAL, "neon_mx8_quant: null pointer");
+  if (rows < 1 || K < 32 || K % 32 || rows > ((int64_t)1 << 40) / K)
+    KFAIL(NEON_EINVAL, "neon_mx8_quant: bad shape rows=%lld K=%d", (long long)rows, K);
+  launch_mx8_quant(x, rows, K, hi, lo, s_hi, s_lo, S(stream));
+  KLAUNCHED();
 }
 
 extern "C" neon_status neon_attn_prefill(const uint16_t* q, const uint16_t* k_cache,

@@ -271,8 +271,14 @@ struct MoePrefillArgs {
   int32_t* n_tiles;               // [1]
   uint16_t* act;                  // [M k][I]
   float* ybuf;                    // [M][k][H]
+  // MXFP8 expert GEMMs (scaled matrix instruction) when q_hi is given:
+  // two E4M3 terms of the GEMM input, [max(M H, M k I)] bytes each, and their
+  // scales [max(M H, M k I) / 32]; H and I multiples of 64
+  uint8_t *q_hi = nullptr, *q_lo = nullptr, *qs_hi = nullptr, *qs_lo = nullptr;
 };
 int moe_prefill_max_tiles(int M, int k, int E);
+void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
+                      uint8_t* s_hi, uint8_t* s_lo, hipStream_t st);
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st);
 
 }  // namespace neon

@@ -22,6 +22,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // staging (no struct copies)
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ void unpack8(const uint4& v, float* o) {
   o[0] = bf_lo(v.x); o[1] = bf_hi(v.x); o[2] = bf_lo(v.y); o[3] = bf_hi(v.y);
@@ -91,6 +92,9 @@ struct GemmParams {
   const int32_t* a_rows;               // token of each list row (gate_up), or NULL
   float* ybuf; int topk;
   float alpha, limit;
+  // MXFP8 A operand (k_gemm_mx8): two E4M3 terms [rows][K] and their E8M0
+  // scales [rows][K/32]
+  const uint8_t *qa_hi, *qa_lo, *qs_hi, *qs_lo;
 };
 
 __device__ __forceinline__ float swiglu_clamp_p(float g, float u, float alpha, float limit) {
@@ -126,6 +130,48 @@ __device__ __forceinline__ void fp4x16_to_bf16(u32x2_t c, uint32_t s, u32x4_t& l
   }
   lo = u32x4_t{o[0], o[1], o[2], o[3]};
   hi = u32x4_t{o[4], o[5], o[6], o[7]};
+}
+
+// Epilogue of the 128 x 128 GEMM tiles (both operand kinds): acc[im][in][i]
+// is row 8 (i/4) + 4 (lane/32) + i%4, column lane%32 of the wave's 32 x 32
+// block (im, in) -- the D layout of the 32 x 32 MFMA shapes.
+template <int MODE, bool GROUPED>
+__device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[2][2], const GemmParams& p,
+                                              int lane, int wm, int wn, int n0, int r0,
+                                              int rows, int e) {
+  const uint16_t* bias = p.bias ? p.bias + (GROUPED ? (size_t)e * p.N : 0) : nullptr;
+#pragma unroll
+  for (int im = 0; im < 2; ++im)
+#pragma unroll
+    for (int in = 0; in < 2; ++in) {
+      const int col = n0 + wn * 64 + in * 32 + (lane & 31);
+      const float bcol = (bias && col < p.N) ? bf2f(bias[col]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = wm * 64 + im * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        const float v = bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
+        if (MODE == GEMM_SWIGLU) {
+          // gate (even column) and up (odd column) sit in adjacent lanes
+          const float u = __shfl_xor(v, 1, 64);
+          if ((lane & 1) == 0 && r < rows && col + 1 < p.N)
+            p.C[(size_t)(r0 + r) * p.ldc + col / 2] = f2bf(swiglu_clamp_p(v, u, p.alpha, p.limit));
+          continue;
+        }
+        if (r >= rows || col >= p.N) continue;
+        const size_t gr = (size_t)(r0 + r);
+        if (MODE == GEMM_STORE) {
+          p.C[gr * p.ldc + col] = f2bf(v);
+        } else if (MODE == GEMM_RESID) {
+          uint16_t* c = p.C + gr * p.ldc + col;
+          *c = f2bf(__fadd_rn(bf2f(*c), bf2f(f2bf(v))));
+        } else if (MODE == GEMM_F32) {
+          p.Cf[gr * p.ldc + col] = v;
+        } else {  // GEMM_SCATTER
+          const int t = p.list_tok[gr], s = p.list_slot[gr];
+          p.ybuf[((size_t)t * p.topk + s) * p.N + col] = v;
+        }
+      }
+    }
 }
 
 template <int MODE, bool FP4, bool GROUPED>
@@ -252,40 +298,254 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   }
 #undef GEMM_STAGE
 
-  // ---- epilogue: acc[im][in][i] is row 8 (i/4) + 4 (lane/32) + i%4, col lane%32
-  const uint16_t* bias = p.bias ? p.bias + (GROUPED ? (size_t)e * p.N : 0) : nullptr;
+  gemm_epilogue<MODE, GROUPED>(acc, p, lane, wm, wn, n0, r0, rows, e);
+}
+
+// ===========================================================================
+// MXFP8 activations x MXFP4 experts on the scaled matrix instruction
+// (v_mfma_scale_f32_32x32x64_f8f6f4: A E4M3, B E2M1, one E8M0 scale per
+// 32-element block of each operand, fp32 accumulate).
+//
+// Activation quantisation (k_mx8_quant): each 32-element block of a bf16
+// row becomes two MXFP8 terms, hi = the OCP MX rule (shared exponent
+// floor(log2 amax) - 8, one more when amax's significand exceeds 1.75 so
+// nothing saturates; round to nearest even) and lo = the same rule on the
+// exact fp32 residual x - hi.  Together they carry the bf16 value to within
+// 2^(floor(log2 amax) - 8), half a bf16 unit of the block maximum, so the
+// expert GEMM runs two instructions per 64-deep step (A_hi B, A_lo B) into
+// one accumulator.  The CPU oracle's or_mx8_quant states the same rule and
+// this kernel matches it bit for bit.
+//
+// Operand lanes of the 32x32x64 shape, measured on gfx950 with an in-bounds
+// probe (random E4M3 / E2M1 data and scales, exact fp32 match):
+//   - B (E2M1, 16 bytes in the first 4 VGPRs): lane n + 32 h holds column n,
+//     k 32 h .. 32 h + 31, low nibble first -- exactly one stored MXFP4 block
+//     of a weight row, so the expert rows are read straight from memory;
+//   - A (E4M3, 32 bytes): lane i + 32 h holds row i, bytes 0-15 = k 16 h ..
+//     16 h + 15 and bytes 16-31 = k 32 + 16 h .. 32 + 16 h + 15;
+//   - scales: the scale of (row / column i, k block b) is byte 0 of lane
+//     i + 32 b's scale operand;
+//   - D: as the other 32x32 shapes (row 8 (r/4) + 4 (lane/32) + r%4,
+//     column lane%32).
+// ===========================================================================
+__device__ __forceinline__ int ilog2f_dev(float a) {
+  const uint32_t b = __float_as_uint(a);
+  const int ef = (b >> 23) & 255;
+  if (ef) return ef - 127;
+  return (31 - __builtin_clz(b & 0x7FFFFFu)) - 149;
+}
+
+__device__ __forceinline__ uint32_t e4m3_encode_dev(float v) {
+  const uint32_t b = __float_as_uint(v);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7Fu;  // NaN
+  const uint32_t sgn = (b >> 24) & 0x80u;
+  const float a = __uint_as_float(b & 0x7FFFFFFFu);
+  if (a >= 448.0f) return sgn | 0x7Eu;
+  if (a < 0.015625f) return sgn | (uint32_t)(int)__builtin_rintf(__fmul_rn(a, 512.0f));
+  int e = ilog2f_dev(a);
+  int q = (int)__builtin_rintf(__fmul_rn(__fsub_rn(__builtin_amdgcn_ldexpf(a, -e), 1.0f), 8.0f));
+  if (q == 8) { e += 1; q = 0; }
+  return sgn | (uint32_t)(((e + 7) << 3) | q);
+}
+
+// finite codes only (the quantiser never decodes the NaN code)
+__device__ __forceinline__ float e4m3_decode_dev(uint32_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  const float v = e == 0 ? __builtin_amdgcn_ldexpf((float)m, -9)
+                         : __builtin_amdgcn_ldexpf((float)(8 + m), e - 10);
+  return (c & 0x80u) ? -v : v;
+}
+
+// smallest shared exponent with amax / 2^e <= 448: floor(log2 amax) - 8, one
+// more when amax's significand exceeds 1.75
+__device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
+  if (!(amax > 0.0f)) return 127u;
+  int e = ilog2f_dev(amax);
+  if (__builtin_amdgcn_ldexpf(amax, -e) > 1.75f) e += 1;
+  e = e - 8 + 127;
+  return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+}
+
+// one thread per 32-element block: rows x K/32 threads
+__global__ __launch_bounds__(256) void k_mx8_quant(const uint16_t* __restrict__ x, int64_t n_blocks,
+                                                   int K, uint8_t* __restrict__ hi,
+                                                   uint8_t* __restrict__ lo,
+                                                   uint8_t* __restrict__ s_hi,
+                                                   uint8_t* __restrict__ s_lo) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n_blocks) return;
+  const int nb = K / 32;
+  const int64_t r = t / nb, blk = t - r * nb;
+  const int64_t o = r * K + blk * 32;
+  float v[32];
 #pragma unroll
-  for (int im = 0; im < 2; ++im)
+  for (int c = 0; c < 4; ++c) {
+    const uint4 w = *reinterpret_cast<const uint4*>(x + o + 8 * c);
+    unpack8(w, v + 8 * c);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float a = fabsf(v[j]);
+    if (a < INFINITY && a > amax) amax = a;  // NaN compares false
+  }
+  const uint32_t b1 = mx8_scale_byte(amax);
+  uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float res[32], rmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const bool fin = fabsf(v[j]) < INFINITY;
+    const uint32_t c = fin ? e4m3_encode_dev(__builtin_amdgcn_ldexpf(v[j], 127 - (int)b1)) : 0x7Fu;
+    res[j] = fin ? __fsub_rn(v[j], __builtin_amdgcn_ldexpf(e4m3_decode_dev(c), (int)b1 - 127))
+                 : 0.0f;
+    rmax = fmaxf(rmax, fabsf(res[j]));
+    qh[j >> 2] |= c << (8 * (j & 3));
+  }
+  const uint32_t b2 = mx8_scale_byte(rmax);
+  uint32_t ql[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < 32; ++j)
+    ql[j >> 2] |= e4m3_encode_dev(__builtin_amdgcn_ldexpf(res[j], 127 - (int)b2)) << (8 * (j & 3));
+  uint4* dh = reinterpret_cast<uint4*>(hi + o);
+  uint4* dl = reinterpret_cast<uint4*>(lo + o);
+  dh[0] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+  dh[1] = make_uint4(qh[4], qh[5], qh[6], qh[7]);
+  dl[0] = make_uint4(ql[0], ql[1], ql[2], ql[3]);
+  dl[1] = make_uint4(ql[4], ql[5], ql[6], ql[7]);
+  s_hi[t] = (uint8_t)b1;
+  s_lo[t] = (uint8_t)b2;
+}
+
+void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
+                      uint8_t* s_hi, uint8_t* s_lo, hipStream_t st) {
+  const int64_t n = rows * (K / 32);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_mx8_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, K,
+                     hi, lo, s_hi, s_lo);
+}
+
+// Grouped expert GEMM, A in two MXFP8 terms (staged through LDS 64 k at a
+// time: row stride kQS bytes = 64 hi + 64 lo + 16 padding), B the expert's
+// MXFP4 rows read from memory into registers one step ahead.  Same tiles,
+// grouping and epilogues as k_gemm<MODE, true, true>.  K % 64 == 0.
+constexpr int kQS = 144;
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_gemm_mx8(GemmParams p) {
+  __shared__ __align__(16) uint8_t Aq[2][kGM * kQS];
+  __shared__ uint32_t Asc[2][kGM];  // per row: bytes s_hi b0, s_hi b1, s_lo b0, s_lo b1
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * kGN;
+  if ((int)blockIdx.y >= *p.n_tiles) return;  // uniform for the block
+  const int e = p.tile_e[blockIdx.y];
+  const int r0 = p.e_off[e] + p.tile_r0[blockIdx.y];
+  const int rows = min(kGM, p.e_off[e + 1] - r0);
+  const int K = p.K, KB = K / 32;
+  // A staging: chunk c = tid + 256 i of the tile's 128 rows x 8 pieces of 16
+  // bytes (pieces 0-3 hi, 4-7 lo)
+  const int pc = tid & 7;
+  const uint8_t* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (tid + 256 * i) >> 3;
+    const int lr = r0 + min(r, rows - 1);
+    const int ar = p.a_rows ? p.a_rows[lr] : lr;
+    asrc[i] = (pc < 4 ? p.qa_hi : p.qa_lo) + (size_t)ar * K + 16 * (pc & 3);
+  }
+  const uint16_t* ssh = nullptr;  // 2 scale bytes per step (threads 0..127: row tid)
+  const uint16_t* ssl = nullptr;
+  if (tid < kGM) {
+    const int lr = r0 + min(tid, rows - 1);
+    const int ar = p.a_rows ? p.a_rows[lr] : lr;
+    ssh = reinterpret_cast<const uint16_t*>(p.qs_hi + (size_t)ar * KB);
+    ssl = reinterpret_cast<const uint16_t*>(p.qs_lo + (size_t)ar * KB);
+  }
+  // B: this lane's column of each 32-column block `in`, k block half h
+  const int h = lane >> 5;
+  const uint8_t* bc[2];
+  const uint8_t* bs[2];
+#pragma unroll
+  for (int in = 0; in < 2; ++in) {
+    const int n = min(n0 + wn * 64 + in * 32 + (lane & 31), p.N - 1);
+    const size_t row = (size_t)e * p.N + n;
+    bc[in] = p.codes + row * (K / 2) + 16 * h;
+    bs[in] = p.scales + row * KB + h;
+  }
+  u32x4_t ra[4];
+  uint32_t rsh = 0, rsl = 0;
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4_t*>(asrc[i] + kt * 64);
+    if (tid < kGM) { rsh = ssh[kt]; rsl = ssl[kt]; }
+  };
+  u32x4_t rb[2], rbn[2];
+  uint32_t sb[2], sbn[2];
+  auto load_b = [&](int kt, u32x4_t* c, uint32_t* sc) {
 #pragma unroll
     for (int in = 0; in < 2; ++in) {
-      const int col = n0 + wn * 64 + in * 32 + (lane & 31);
-      const float bcol = (bias && col < p.N) ? bf2f(bias[col]) : 0.0f;
+      c[in] = *reinterpret_cast<const u32x4_t*>(bc[in] + kt * 32);
+      sc[in] = bs[in][2 * kt];
+    }
+  };
+  auto stage_a = [&](int buf) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = wm * 64 + im * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        const float v = bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
-        if (MODE == GEMM_SWIGLU) {
-          // gate (even column) and up (odd column) sit in adjacent lanes
-          const float u = __shfl_xor(v, 1, 64);
-          if ((lane & 1) == 0 && r < rows && col + 1 < p.N)
-            p.C[(size_t)(r0 + r) * p.ldc + col / 2] = f2bf(swiglu_clamp_p(v, u, p.alpha, p.limit));
-          continue;
-        }
-        if (r >= rows || col >= p.N) continue;
-        const size_t gr = (size_t)(r0 + r);
-        if (MODE == GEMM_STORE) {
-          p.C[gr * p.ldc + col] = f2bf(v);
-        } else if (MODE == GEMM_RESID) {
-          uint16_t* c = p.C + gr * p.ldc + col;
-          *c = f2bf(__fadd_rn(bf2f(*c), bf2f(f2bf(v))));
-        } else if (MODE == GEMM_F32) {
-          p.Cf[gr * p.ldc + col] = v;
-        } else {  // GEMM_SCATTER
-          const int t = p.list_tok[gr], s = p.list_slot[gr];
-          p.ybuf[((size_t)t * p.topk + s) * p.N + col] = v;
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int r = (tid + 256 * i) >> 3;
+      *reinterpret_cast<u32x4_t*>(&Aq[buf][r * kQS + 16 * pc]) = ra[i];
+    }
+    if (tid < kGM) Asc[buf][tid] = rsh | (rsl << 16);
+  };
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+  const int nk = K / 64;
+  load_a(0);
+  load_b(0, rbn, sbn);
+  stage_a(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+#pragma unroll
+    for (int in = 0; in < 2; ++in) { rb[in] = rbn[in]; sb[in] = sbn[in]; }
+    if (kt + 1 < nk) {  // next step's loads before this step's math
+      load_a(kt + 1);
+      load_b(kt + 1, rbn, sbn);
+    }
+#pragma unroll
+    for (int im = 0; im < 2; ++im) {
+      const int rr = wm * 64 + im * 32 + (lane & 31);
+      const uint8_t* base = &Aq[cur][rr * kQS + 16 * h];
+      const u32x4_t h0 = *reinterpret_cast<const u32x4_t*>(base);
+      const u32x4_t h1 = *reinterpret_cast<const u32x4_t*>(base + 32);
+      const u32x4_t l0 = *reinterpret_cast<const u32x4_t*>(base + 64);
+      const u32x4_t l1 = *reinterpret_cast<const u32x4_t*>(base + 96);
+      const uint32_t sc = Asc[cur][rr];
+      const int sa_hi = (int)((sc >> (8 * h)) & 0xFFu);
+      const int sa_lo = (int)((sc >> (16 + 8 * h)) & 0xFFu);
+      const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
+                           (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
+                           (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+      for (int in = 0; in < 2; ++in) {
+        const i32x8_t bq = {(int)rb[in].x, (int)rb[in].y, (int)rb[in].z, (int)rb[in].w,
+                            0, 0, 0, 0};
+        const int s_b = (int)sb[in];
+        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            ahi, bq, acc[im][in], 0, 4, 0, sa_hi, 0, s_b);
+        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            alo, bq, acc[im][in], 0, 4, 0, sa_lo, 0, s_b);
       }
     }
+    if (kt + 1 < nk) stage_a(cur ^ 1);
+    __syncthreads();
+  }
+  gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, e);
 }
 
 void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
@@ -414,18 +674,24 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   p.tile_e = a.tile_e; p.tile_r0 = a.tile_r0; p.n_tiles = a.n_tiles; p.e_off = a.e_off;
   p.list_tok = a.list_tok; p.list_slot = a.list_slot; p.topk = a.k;
   p.alpha = a.alpha; p.limit = a.limit;
+  p.qa_hi = a.q_hi; p.qa_lo = a.q_lo; p.qs_hi = a.qs_hi; p.qs_lo = a.qs_lo;
+  const bool mx8 = a.q_hi != nullptr;
   // gate_up + SwiGLU: A = xn rows of the listed tokens, N = 2 I, out act [list][I]
+  if (mx8) launch_mx8_quant(a.xn, a.M, a.H, a.q_hi, a.q_lo, a.qs_hi, a.qs_lo, st);
   p.A = a.xn; p.lda = a.H; p.a_rows = a.list_tok;
   p.codes = a.gu_codes; p.scales = a.gu_scales; p.bias = a.gu_bias;
   p.C = a.act; p.ldc = a.I; p.N = 2 * a.I; p.K = a.H;
-  hipLaunchKernelGGL((k_gemm<GEMM_SWIGLU, true, true>), dim3((2 * a.I + kGN - 1) / kGN, max_tiles),
-                     dim3(256), 0, st, p);
+  const dim3 g_gu((2 * a.I + kGN - 1) / kGN, max_tiles);
+  if (mx8) hipLaunchKernelGGL((k_gemm_mx8<GEMM_SWIGLU>), g_gu, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((k_gemm<GEMM_SWIGLU, true, true>), g_gu, dim3(256), 0, st, p);
   // down: A = act rows in list order, N = H, out ybuf[token][slot]
+  if (mx8) launch_mx8_quant(a.act, (int64_t)a.M * a.k, a.I, a.q_hi, a.q_lo, a.qs_hi, a.qs_lo, st);
   p.A = a.act; p.lda = a.I; p.a_rows = nullptr;
   p.codes = a.dn_codes; p.scales = a.dn_scales; p.bias = a.dn_bias;
   p.ybuf = a.ybuf; p.N = a.H; p.K = a.I; p.C = nullptr;
-  hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), dim3((a.H + kGN - 1) / kGN, max_tiles),
-                     dim3(256), 0, st, p);
+  const dim3 g_dn((a.H + kGN - 1) / kGN, max_tiles);
+  if (mx8) hipLaunchKernelGGL((k_gemm_mx8<GEMM_SCATTER>), g_dn, dim3(256), 0, st, p);
+  else hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), g_dn, dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.idx, a.E,
                      a.k, a.H, a.h);
 }

@@ -157,6 +157,79 @@ static inline float e8m0_exp2(uint8_t s, float v) {
   return ldexpf(v, (int)s - 127);
 }
 
+/* ---- MXFP8 (E4M3) activations: OCP MX v1.0 sec. 5.3 (E4M3: bias 7, no
+ * infinities, S.1111.111 = NaN, max normal 448) and sec. 6.3 (shared
+ * exponent from floor(log2(amax)) - emax_elem, emax_elem = 8 for E4M3; the
+ * clamp of out-of-range magnitudes to the largest normal, here only a guard
+ * since the exponent is chosen so that no finite element exceeds 448). ---- */
+float or_e4m3_decode(uint8_t code) {
+  const int e = (code >> 3) & 15, m = code & 7;
+  const float sgn = (code & 0x80) ? -1.0f : 1.0f;
+  if (e == 15 && m == 7) return NAN;
+  if (e == 0) return sgn * ldexpf((float)m, -9);
+  return sgn * ldexpf((float)(8 + m), e - 10);
+}
+
+int or_ilog2f(float a) {
+  uint32_t b;
+  memcpy(&b, &a, 4);
+  const int ef = (b >> 23) & 255;
+  if (ef) return ef - 127;
+  const uint32_t m = b & 0x7FFFFFu;
+  return (31 - __builtin_clz(m)) - 149;
+}
+
+uint8_t or_e4m3_encode(float v) {
+  if (isnan(v)) return 0x7F;
+  const uint8_t sgn = signbit(v) ? 0x80 : 0;
+  const float a = fabsf(v);
+  if (a >= 448.0f) return sgn | 0x7E;
+  if (a < 0.015625f) return sgn | (uint8_t)(int)rintf(a * 512.0f); /* step 2^-9; 8 = 2^-6 */
+  int e = or_ilog2f(a);
+  int q = (int)rintf((ldexpf(a, -e) - 1.0f) * 8.0f);
+  if (q == 8) { e += 1; q = 0; }
+  return sgn | (uint8_t)(((e + 7) << 3) | q);
+}
+
+/* The smallest shared exponent at which the block maximum is representable:
+ * floor(log2 amax) - 8 (OCP's rule, E4M3 emax 8), one more when amax's
+ * significand exceeds 1.75 (amax / 2^(floor - 8) would pass 448, the largest
+ * E4M3 normal, and OCP's rule would clamp it). */
+static uint8_t mx8_scale_byte(float amax) {
+  if (!(amax > 0.0f)) return 127;
+  int e = or_ilog2f(amax);
+  if (ldexpf(amax, -e) > 1.75f) e += 1;
+  e = e - 8 + 127;
+  return (uint8_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+}
+
+void or_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi,
+                  uint8_t* lo, uint8_t* s_hi, uint8_t* s_lo) {
+  const int nb = K / 32;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int blk = 0; blk < nb; ++blk) {
+      const int64_t o = r * K + (int64_t)blk * 32;
+      float v[32], res[32], amax = 0.0f, rmax = 0.0f;
+      for (int j = 0; j < 32; ++j) {
+        v[j] = or_bf16_to_f32(x[o + j]);
+        if (isfinite(v[j]) && fabsf(v[j]) > amax) amax = fabsf(v[j]);
+      }
+      const uint8_t b1 = mx8_scale_byte(amax);
+      for (int j = 0; j < 32; ++j) {
+        if (!isfinite(v[j])) { hi[o + j] = 0x7F; res[j] = 0.0f; continue; }
+        hi[o + j] = or_e4m3_encode(ldexpf(v[j], 127 - (int)b1));
+        res[j] = v[j] - ldexpf(or_e4m3_decode(hi[o + j]), (int)b1 - 127);
+        if (fabsf(res[j]) > rmax) rmax = fabsf(res[j]);
+      }
+      const uint8_t b2 = mx8_scale_byte(rmax);
+      for (int j = 0; j < 32; ++j) lo[o + j] = or_e4m3_encode(ldexpf(res[j], 127 - (int)b2));
+      s_hi[r * nb + blk] = b1;
+      s_lo[r * nb + blk] = b2;
+    }
+  }
+}
+
 void or_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,
                       int64_t n_blocks, float* out) {
 #pragma omp parallel for schedule(static)

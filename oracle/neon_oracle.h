@@ -19,6 +19,11 @@
  * Pinning (what checks each function, besides the GPU):
  *   or_mxfp4_dequant  exhaustive 16 x 256 (code, scale) table vs the closed
  *                     form; torch.float8_e8m0fnu scale decode.
+ *   or_e4m3_*         all 256 codes vs torch.float8_e4m3fn decode; encode of
+ *                     every bf16 value of magnitude <= 448 vs torch's
+ *                     round-to-nearest-even cast; clamp above 448.
+ *   or_mx8_quant      scale rule vs the OCP closed form; reconstruction
+ *                     error bound (<= one bf16 unit of the block maximum).
  *   or_gemv_*         fp64 brute force within the fp32 accumulation bound.
  *   or_rmsnorm        constant-vector closed form; HF GptOssRMSNorm fixtures.
  *   or_yarn_*         HF _compute_yarn_parameters fixtures; position-0 and
@@ -71,6 +76,23 @@ void or_fill_scales_at(uint64_t seed, uint64_t stream, int64_t start, int64_t n,
 /* ---- numeric helpers ------------------------------------------------------ */
 float or_bf16_to_f32(uint16_t b);
 uint16_t or_f32_to_bf16(float f);
+
+/* ---- MXFP8 activations (E4M3 elements, E8M0 scales; OCP MX v1.0 sec. 5-6) --
+ * For the opt-in matrix-core prompt mode whose expert GEMMs use the scaled
+ * fp8 x fp4 matrix instruction.  A bf16 activation block of 32 is carried as
+ * two MXFP8 terms, x ~= dec(hi) 2^(s_hi-127) + dec(lo) 2^(s_lo-127): hi is
+ * the block quantised with the MX rule (shared exponent floor(log2 amax)
+ * minus E4M3's emax 8, plus one when amax's significand exceeds 1.75 so that
+ * no element passes 448; elements rounded to nearest even), lo is the same
+ * rule applied to the exact residual x - hi.  Every finite element comes
+ * back to within 2^(floor(log2 amax) - 8).  Blocks of zeros get scale byte
+ * 127 and zero codes; a non-finite element becomes the E4M3 NaN code 0x7F in
+ * hi and 0 in lo and is left out of the block maxima. */
+float or_e4m3_decode(uint8_t code);
+uint8_t or_e4m3_encode(float v);
+int or_ilog2f(float a); /* floor(log2 a) for finite a > 0, subnormals included */
+void or_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi,
+                  uint8_t* lo, uint8_t* s_hi, uint8_t* s_lo);
 
 /* ---- MXFP4 --------------------------------------------------------------- */
 void or_mxfp4_dequant(const uint8_t* codes, const uint8_t* scales,

@@ -92,6 +92,10 @@ def _declare(L):
         "or_bf16_to_f32": (_F, [C.c_uint16]),
         "or_f32_to_bf16": (C.c_uint16, [_F]),
         "or_mxfp4_dequant": (None, [_P, _P, _I64, _P]),
+        "or_e4m3_decode": (_F, [C.c_uint8]),
+        "or_e4m3_encode": (C.c_uint8, [_F]),
+        "or_ilog2f": (_I, [_F]),
+        "or_mx8_quant": (None, [_P, _I64, _I, _P, _P, _P, _P]),
         "or_mxfp4_gemv": (None, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
         "or_gemv_bf16": (None, [_P, _P, _P, _I, _I, _I, _P, _P]),
         "or_rmsnorm": (None, [_P, _P, _I, _I, _F, _P]),
@@ -213,6 +217,33 @@ def mxfp4_dequant(codes, scales) -> np.ndarray:
     out = np.empty(nb * 32, np.float32)
     lib().or_mxfp4_dequant(_p(codes), _p(scales), nb, _p(out))
     return out
+
+
+def e4m3_decode(code) -> float:
+    return lib().or_e4m3_decode(int(code))
+
+
+def e4m3_encode(v) -> int:
+    return int(lib().or_e4m3_encode(float(v)))
+
+
+def mx8_quant(x):
+    """bf16 bits [rows][K] -> (hi, lo uint8 [rows][K], s_hi, s_lo uint8
+    [rows][K/32]): the two-term MXFP8 image of the rows."""
+    x = _c(x, np.uint16)
+    rows, K = x.shape
+    hi, lo = np.empty((rows, K), np.uint8), np.empty((rows, K), np.uint8)
+    sh, sl = np.empty((rows, K // 32), np.uint8), np.empty((rows, K // 32), np.uint8)
+    lib().or_mx8_quant(_p(x), rows, K, _p(hi), _p(lo), _p(sh), _p(sl))
+    return hi, lo, sh, sl
+
+
+def mx8_dequant(hi, lo, s_hi, s_lo) -> np.ndarray:
+    """float64 [rows][K] = dec(hi) 2^(s_hi-127) + dec(lo) 2^(s_lo-127)."""
+    table = np.array([lib().or_e4m3_decode(c) for c in range(256)], np.float64)
+    sh = np.repeat(np.asarray(s_hi, np.int64), 32, axis=1) - 127
+    sl = np.repeat(np.asarray(s_lo, np.int64), 32, axis=1) - 127
+    return table[hi] * np.exp2(sh) + table[lo] * np.exp2(sl)
 
 
 def mxfp4_gemv(codes, scales, bias, x, N, K):

@@ -179,14 +179,15 @@ def prompt_pass(cfg, seed, prompt, n_steps, mode, fixed_routing=False):
     return first, toks
 
 
-def compare_modes(cfg, seed, prompt, n_steps, fixed_routing=False, bar=2e-2):
-    """Batched prompt pass vs the stepwise one (decode kernels, bit-identical
-    to the oracle)."""
+def compare_modes(cfg, seed, prompt, n_steps, fixed_routing=False, bar=2e-2,
+                  mode=ne.PREFILL_BATCHED):
+    """A matrix-core prompt pass (`mode`) vs the stepwise one (decode
+    kernels, bit-identical to the oracle)."""
     torch_cuda()
     say(f"prefill modes layers={cfg.n_layers} hidden={cfg.hidden} batch={len(prompt)} "
-        f"prompt={len(prompt[0])} fixed_routing={fixed_routing}")
+        f"prompt={len(prompt[0])} fixed_routing={fixed_routing} mode={mode}")
     lg_s, tok_s = prompt_pass(cfg, seed, prompt, n_steps, ne.PREFILL_STEPWISE, fixed_routing)
-    lg_b, tok_b = prompt_pass(cfg, seed, prompt, n_steps, ne.PREFILL_BATCHED, fixed_routing)
+    lg_b, tok_b = prompt_pass(cfg, seed, prompt, n_steps, mode, fixed_routing)
     rel = np.abs(lg_b - lg_s).max() / np.abs(lg_s).max()
     top2 = np.sort(lg_s, axis=1)[:, -2:]
     margin = (top2[:, 1] - top2[:, 0]) / np.abs(lg_s).max(axis=1)
@@ -258,4 +259,113 @@ def test_prefill_mode_validation():
     eng.set_prefill_mode(ne.PREFILL_BATCHED)
     eng.set_prefill_mode(ne.PREFILL_STEPWISE)
     eng.set_prefill_mode(ne.PREFILL_CHUNKED)
+    eng.close()
+
+
+# ---------------------------------------------------------------------------
+# MXFP8 x MXFP4 expert GEMMs (NEON_PREFILL_MX8, v_mfma_scale_f32_32x32x64_f8f6f4)
+# ---------------------------------------------------------------------------
+def test_mx8_quant_bitexact(orc):
+    """The device quantiser gives the oracle's bytes: both E4M3 terms and both
+    scale bytes of every block, over rows spanning 2^-130 .. 2^120 with zero
+    blocks, NaN and infinite elements, and blocks whose maximum's
+    significand is above and below 1.75."""
+    torch_cuda()
+    rng = np.random.default_rng(11)
+    rows, K = 257, 2880
+    x = (rng.standard_normal((rows, K)) *
+         np.exp2(rng.integers(-60, 60, (rows, 1)))).astype(np.float32)
+    x[1, :64] = 0.0
+    x[2, 5], x[2, 40], x[2, 77] = np.nan, np.inf, -np.inf
+    x[3, :] *= np.float32(2.0 ** -70)
+    x[4, :32] = np.float32(2.0 ** -130)       # bf16 subnormals
+    x[5, :] = np.float32(2.0 ** 100) * rng.standard_normal(K).astype(np.float32)
+    xb = orc.f32_to_bf16(x.ravel()).reshape(rows, K)
+    want = orc.mx8_quant(xb)
+    hi, lo = empty_dev((rows, K), np.uint8), empty_dev((rows, K), np.uint8)
+    sh, sl = empty_dev((rows, K // 32), np.uint8), empty_dev((rows, K // 32), np.uint8)
+    say(f"mx8_quant rows={rows} K={K}")
+    ne.mx8_quant(to_dev(xb), rows, K, hi, lo, sh, sl)
+    for name, g, w in zip(("hi", "lo", "s_hi", "s_lo"), (hi, lo, sh, sl), want):
+        got = to_host(g)
+        bad = np.argwhere(got != w)
+        if len(bad):
+            r, c = bad[0]
+            say(f"  {name} differs at {r},{c}: gpu {got[r, c]:#x} oracle {w[r, c]:#x}")
+        assert not len(bad), name
+
+
+@pytest.mark.parametrize("M,E,H,I,k", [(300, 32, 2880, 2880, 4), (37, 8, 256, 512, 2)])
+def test_moe_prefill_mx8_vs_oracle(orc, M, E, H, I, k):
+    """neon_moe_prefill_mx8 against the canonical per-row MoE at the bars of
+    the bf16 grouped form (2e-2 relative max, median within 2^-8 of the rms):
+    the two-term MXFP8 inputs carry each bf16 block to within half a bf16
+    unit of its maximum, so the errors stay of the bf16 form's size, which
+    the test prints beside them."""
+    d = moe_weights(orc, E, H, I, seed=2)
+    x = orc.fill_bf16(2, 51, M * H, 0.0, 1.0)
+    ref, ridx, rsc = orc.moe_layer(x, d["rw"], d["rb"], d["guc"], d["gus"], d["gub"], d["dnc"],
+                                   d["dns"], d["dnb"], E, H, I, k)
+    say(f"moe_prefill_mx8 M={M} E={E} H={H} I={I} k={k}")
+    dv = {n: to_dev(v) for n, v in d.items()}
+    r = orc.bf16_to_f32(ref).astype(np.float64)
+    rms = np.sqrt((r ** 2).mean())
+    out = {}
+    for name, fn in (("bf16", ne.moe_prefill), ("mx8", ne.moe_prefill_mx8)):
+        h = to_dev(np.zeros((M, H), np.uint16))
+        fn(to_dev(x), to_dev(ridx), to_dev(rsc), dv["guc"], dv["gus"], dv["gub"],
+           dv["dnc"], dv["dns"], dv["dnb"], h, M, E, H, I, k)
+        err = np.abs(orc.bf16_to_f32(to_host(h)).astype(np.float64) - r)
+        out[name] = (err.max() / np.abs(r).max(), np.median(err) / rms)
+        say(f"  {name}: max error / max|ref| = {out[name][0]:.3e}, "
+            f"median |err| / rms = {out[name][1]:.3e}")
+    assert out["mx8"][0] < 2e-2
+    assert out["mx8"][1] <= 2.0 ** -8
+
+
+def test_small_model_mx8_prefill():
+    cfg = ne.config_preset("gpt-oss-20b", **SMALL)
+    prompt = [[(7 * i + 3) % 4096 for i in range(150)], [(11 * i + 5) % 4096 for i in range(150)]]
+    compare_modes(cfg, 9, prompt, 16, mode=ne.PREFILL_MX8)
+
+
+def test_gpt_oss_20b_mx8_prefill():
+    """Full 20b width, four layers, 300-token prompt: the 2e-2 bar."""
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=512, n_layers=4)
+    prompt = [[(1009 * i + 17) % 201088 for i in range(300)]]
+    compare_modes(cfg, 0, prompt, 16, mode=ne.PREFILL_MX8)
+
+
+def test_gpt_oss_20b_mx8_prefill_full_depth():
+    """All 24 layers with the routing fixed: the conditioning bar of the
+    batched pass (twice the oracle's own reorder error at 24 layers)."""
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "conditioning.npz")
+    with np.load(path, allow_pickle=False) as z:
+        bar = 2 * float(z["fixed_24"].max())
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=512)
+    prompt = [[(1009 * i + 17) % 201088 for i in range(300)]]
+    rel, _ = compare_modes(cfg, 0, prompt, 16, fixed_routing=True, bar=bar, mode=ne.PREFILL_MX8)
+    assert rel < bar
+
+
+def test_mx8_validation(orc):
+    """The kernel-level MXFP8 expert FFN needs H and I multiples of 64 (the
+    64-deep steps of the scaled instruction); the mode itself is accepted by
+    every context (whose widths are multiples of 64)."""
+    torch_cuda()
+    M, E, H, I, k = 5, 4, 288, 352, 2
+    d = moe_weights(orc, E, H, I, seed=3)
+    dv = {n: to_dev(v) for n, v in d.items()}
+    x = to_dev(orc.fill_bf16(3, 51, M * H, 0.0, 1.0))
+    idx = to_dev(np.zeros((M, k), np.int32))
+    sc = to_dev(np.full((M, k), 0.5, np.float32))
+    h = to_dev(np.zeros((M, H), np.uint16))
+    with pytest.raises(ne.NeonError) as e:
+        ne.moe_prefill_mx8(x, idx, sc, dv["guc"], dv["gus"], dv["gub"], dv["dnc"], dv["dns"],
+                           dv["dnb"], h, M, E, H, I, k)
+    assert e.value.status == ne.NEON_EINVAL
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_seq=16))
+    eng = ne.Engine(cfg)
+    eng.set_prefill_mode(ne.PREFILL_MX8)
     eng.close()

@@ -597,3 +597,72 @@ def test_prompt_step_equals_full_step(orc):
     a.close()
     b.close()
     assert np.array_equal(la, lb) and np.array_equal(ia, ib)
+
+
+def test_e4m3_decode_all_codes_vs_torch(orc):
+    """All 256 E4M3 codes against torch.float8_e4m3fn (OCP E4M3: bias 7, no
+    infinities, S.1111.111 = NaN, max normal 448)."""
+    torch = pytest.importorskip("torch")
+    codes = np.arange(256, dtype=np.uint8)
+    mine = np.array([orc.e4m3_decode(c) for c in codes], np.float32)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(mine), np.isnan(ref))
+    assert np.array_equal(mine[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert orc.e4m3_decode(0x7E) == 448.0 and orc.e4m3_decode(0x01) == 2.0 ** -9
+
+
+def test_e4m3_encode_vs_torch_rne(orc):
+    """Every bf16 value of magnitude <= 448 (subnormals, ties, both signs)
+    encodes as torch's round-to-nearest-even cast; above 448 the MX rule
+    clamps to the largest normal (torch would give NaN); NaN stays NaN."""
+    torch = pytest.importorskip("torch")
+    b = np.arange(65536, dtype=np.uint16)
+    v = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).float().numpy()
+    ok = np.isfinite(v) & (np.abs(v) <= 448)
+    vv = v[ok]
+    enc = np.array([orc.e4m3_encode(x) for x in vv], np.uint8)
+    ref = torch.from_numpy(vv).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(enc, ref)
+    for big in (448.5, 464.0, 500.0, 1e6, float("inf")):
+        assert orc.e4m3_encode(big) == 0x7E and orc.e4m3_encode(-big) == 0xFE
+    assert orc.e4m3_encode(float("nan")) == 0x7F
+
+
+def test_mx8_quant_scale_rule_and_reconstruction(orc):
+    """The shared exponent is floor(log2 amax) - 8 (OCP MX, E4M3 emax 8), one
+    more when amax's significand exceeds 1.75 (so nothing saturates at 448),
+    hi is the block over 2^e1 rounded to E4M3, and hi + lo reconstruct every
+    finite element to within 2^(floor(log2 amax) - 8) -- half a bf16 unit of
+    the block maximum.  Zero blocks get scale 127; a NaN element gets the
+    NaN code in hi, 0 in lo, and stays out of the block maximum."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    rows, K = 64, 256
+    x = (rng.standard_normal((rows, K)) * np.exp2(rng.integers(-20, 20, (rows, 1)))).astype(np.float32)
+    x[3, 32:64] = 0.0                      # a zero block
+    x[5, 70] = np.nan                      # a NaN element
+    x[7, 0:32] *= np.exp2(-110)            # tiny values (bf16 subnormal range)
+    x[9, 96:128] = rng.standard_normal(32).astype(np.float32) * 2.0 ** 100
+    xb = orc.f32_to_bf16(x.ravel()).reshape(rows, K)
+    xf = orc.bf16_to_f32(xb.ravel()).reshape(rows, K).astype(np.float64)
+    hi, lo, sh, sl = orc.mx8_quant(xb)
+    blocks = xf.reshape(rows, K // 32, 32)
+    fin = np.where(np.isfinite(blocks), np.abs(blocks), 0.0)
+    amax = fin.max(axis=2)
+    fl = np.floor(np.log2(np.where(amax > 0, amax, 1.0)))
+    bump = (np.where(amax > 0, amax, 1.0) / np.exp2(fl) > 1.75).astype(np.float64)
+    want_sh = np.where(amax > 0, np.clip(fl + bump - 8 + 127, 0, 254), 127).astype(np.uint8)
+    assert bump.any() and not bump.all()  # both branches of the rule occur
+    assert np.array_equal(sh, want_sh)
+    e1 = np.repeat(sh.astype(np.int64) - 127, 32, axis=1).reshape(rows, K)
+    scaled = xf / np.exp2(e1)
+    assert np.nanmax(np.abs(scaled)) <= 448
+    fin_el = np.isfinite(xf)
+    want_hi = torch.from_numpy(scaled[fin_el].astype(np.float32)).to(torch.float8_e4m3fn)
+    assert np.array_equal(hi[fin_el], want_hi.view(torch.uint8).numpy())
+    assert hi[5, 70] == 0x7F and lo[5, 70] == 0
+    deq = orc.mx8_dequant(hi, lo, sh, sl)
+    bound = np.repeat(np.exp2(fl - 8), 32, axis=1).reshape(rows, K)
+    err = np.abs(deq - xf)
+    assert (err[fin_el] <= bound[fin_el]).all()
+    assert np.array_equal(hi[3, 32:64], np.zeros(32, np.uint8)) and sh[3, 1] == 127
