@@ -99,7 +99,8 @@ struct neon_ctx {
   int pf_rows = 0;
   uint16_t *pf_h = nullptr, *pf_xn = nullptr, *pf_qkv = nullptr, *pf_q = nullptr,
            *pf_ao = nullptr, *pf_act = nullptr, *pf_ks = nullptr, *pf_vs = nullptr;
-  uint8_t *pf_qh = nullptr, *pf_ql = nullptr, *pf_qsh = nullptr, *pf_qsl = nullptr;
+  uint8_t* pf_mxq = nullptr;   // MXFP8 step lines of the expert GEMM inputs
+  uint32_t* pf_mxqs = nullptr;
   float *pf_lg = nullptr, *pf_score = nullptr, *pf_ybuf = nullptr;
   int32_t *pf_idx = nullptr, *pf_ltok = nullptr, *pf_lslot = nullptr, *pf_eoff = nullptr,
           *pf_tile_e = nullptr, *pf_tile_r0 = nullptr, *pf_ntiles = nullptr;
@@ -875,7 +876,7 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
   // MXFP8 images of the expert GEMM inputs (NEON_PREFILL_MX8): xn rows, then
   // the act rows, in the same buffers
   const size_t qn = std::max(M * H, M * k * I);
-  const size_t o_qh = take(qn), o_ql = take(qn), o_qsh = take(qn / 32), o_qsl = take(qn / 32);
+  const size_t o_mxq = take(2 * qn), o_mxqs = take(qn / 16);
   if (ctx->pf) {
     HIPCHK(ctx, hipStreamSynchronize(st));  // earlier prefill work may still read it
     (void)hipFree(ctx->pf);
@@ -896,8 +897,7 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
   ctx->pf_eoff = (int32_t*)(P + o_eo); ctx->pf_tile_e = (int32_t*)(P + o_te);
   ctx->pf_tile_r0 = (int32_t*)(P + o_tr); ctx->pf_ntiles = (int32_t*)(P + o_nt);
   ctx->pf_ks = (uint16_t*)(P + o_ks); ctx->pf_vs = (uint16_t*)(P + o_vs);
-  ctx->pf_qh = (uint8_t*)(P + o_qh); ctx->pf_ql = (uint8_t*)(P + o_ql);
-  ctx->pf_qsh = (uint8_t*)(P + o_qsh); ctx->pf_qsl = (uint8_t*)(P + o_qsl);
+  ctx->pf_mxq = (uint8_t*)(P + o_mxq); ctx->pf_mxqs = (uint32_t*)(P + o_mxqs);
   ctx->pf_rows = (int)M;
   return NEON_OK;
 }
@@ -947,7 +947,7 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
     m.tile_e = ctx->pf_tile_e; m.tile_r0 = ctx->pf_tile_r0; m.n_tiles = ctx->pf_ntiles;
     m.act = ctx->pf_act; m.ybuf = ctx->pf_ybuf; m.err = ctx->dev_err;
     if (ctx->prefill_mode == NEON_PREFILL_MX8) {
-      m.q_hi = ctx->pf_qh; m.q_lo = ctx->pf_ql; m.qs_hi = ctx->pf_qsh; m.qs_lo = ctx->pf_qsl;
+      m.q = ctx->pf_mxq; m.qs = ctx->pf_mxqs;
     }
     launch_moe_prefill(m, st);
   }
@@ -1640,8 +1640,7 @@ static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const
   auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
   const size_t o_yb = take(pairs * H * 4), o_act = take(pairs * I * 2), o_lt = take(pairs * 4),
                o_ls = take(pairs * 4), o_eo = take((E + 1) * 4), o_te = take(tiles * 4),
-               o_tr = take(tiles * 4), o_nt = take(16), o_qh = take(qn), o_ql = take(qn),
-               o_qsh = take(qn / 32), o_qsl = take(qn / 32);
+               o_tr = take(tiles * 4), o_nt = take(16), o_q = take(2 * qn), o_qs = take(qn / 16);
   char* scratch = nullptr;
   if (hipMallocAsync((void**)&scratch, off, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "%s: scratch allocation failed", fn);
@@ -1655,8 +1654,7 @@ static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const
   m.e_off = (int32_t*)(scratch + o_eo); m.tile_e = (int32_t*)(scratch + o_te);
   m.tile_r0 = (int32_t*)(scratch + o_tr); m.n_tiles = (int32_t*)(scratch + o_nt);
   if (mx8) {
-    m.q_hi = (uint8_t*)(scratch + o_qh); m.q_lo = (uint8_t*)(scratch + o_ql);
-    m.qs_hi = (uint8_t*)(scratch + o_qsh); m.qs_lo = (uint8_t*)(scratch + o_qsl);
+    m.q = (uint8_t*)(scratch + o_q); m.qs = (uint32_t*)(scratch + o_qs);
   }
   m.err = device_status_word();
   launch_moe_prefill(m, st);

@@ -271,14 +271,21 @@ struct MoePrefillArgs {
   int32_t* n_tiles;               // [1]
   uint16_t* act;                  // [M k][I]
   float* ybuf;                    // [M][k][H]
-  // MXFP8 expert GEMMs (scaled matrix instruction) when q_hi is given:
-  // two E4M3 terms of the GEMM input, [max(M H, M k I)] bytes each, and their
-  // scales [max(M H, M k I) / 32]; H and I multiples of 64
-  uint8_t *q_hi = nullptr, *q_lo = nullptr, *qs_hi = nullptr, *qs_lo = nullptr;
+  // MXFP8 expert GEMMs (scaled matrix instruction) when q is given: the GEMM
+  // input's two E4M3 terms in step lines (per row and 64-element step, 64
+  // hi bytes then 64 lo bytes), 2 max(M H, M k I) bytes, and their scales
+  // (one dword per row and step: s_hi of both 32-blocks, then s_lo),
+  // max(M H, M k I) / 16 bytes; H and I multiples of 64
+  uint8_t* q = nullptr;
+  uint32_t* qs = nullptr;
 };
 int moe_prefill_max_tiles(int M, int k, int E);
+// the two-term MXFP8 image of bf16 rows: separate hi / lo / s_hi / s_lo
+// arrays (the kernel-level layout), or (q, qs) step lines for the GEMMs
 void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
                       uint8_t* s_hi, uint8_t* s_lo, hipStream_t st);
+void launch_mx8_quant_lines(const uint16_t* x, int64_t rows, int K, uint8_t* q, uint32_t* qs,
+                            hipStream_t st);
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st);
 
 }  // namespace neon

@@ -92,9 +92,10 @@ struct GemmParams {
   const int32_t* a_rows;               // token of each list row (gate_up), or NULL
   float* ybuf; int topk;
   float alpha, limit;
-  // MXFP8 A operand (k_gemm_mx8): two E4M3 terms [rows][K] and their E8M0
-  // scales [rows][K/32]
-  const uint8_t *qa_hi, *qa_lo, *qs_hi, *qs_lo;
+  // MXFP8 A operand (k_gemm_mx8), in step lines: per row and 64-element
+  // step 128 bytes (64 E4M3 hi, 64 lo) and one scale dword (s_hi of the two
+  // 32-blocks, then s_lo)
+  const uint8_t* qa; const uint32_t* qsc;
 };
 
 __device__ __forceinline__ float swiglu_clamp_p(float g, float u, float alpha, float limit) {
@@ -366,7 +367,12 @@ __device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
   return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
 }
 
-// one thread per 32-element block: rows x K/32 threads
+// one thread per 32-element block: rows x K/32 threads.  LINES: hi / lo
+// into step lines (hi = the lines, K % 64 == 0; block b of a row goes to
+// line b / 2 at bytes 32 (b % 2) (hi) and 64 + 32 (b % 2) (lo), its scale
+// bytes to bytes b % 2 and 2 + b % 2 of the step's dword in s_hi); else the
+// four arrays of the kernel-level layout.
+template <bool LINES>
 __global__ __launch_bounds__(256) void k_mx8_quant(const uint16_t* __restrict__ x, int64_t n_blocks,
                                                    int K, uint8_t* __restrict__ hi,
                                                    uint8_t* __restrict__ lo,
@@ -406,34 +412,65 @@ __global__ __launch_bounds__(256) void k_mx8_quant(const uint16_t* __restrict__ 
 #pragma unroll
   for (int j = 0; j < 32; ++j)
     ql[j >> 2] |= e4m3_encode_dev(__builtin_amdgcn_ldexpf(res[j], 127 - (int)b2)) << (8 * (j & 3));
-  uint4* dh = reinterpret_cast<uint4*>(hi + o);
-  uint4* dl = reinterpret_cast<uint4*>(lo + o);
+  uint4 *dh, *dl;
+  if (LINES) {
+    const int64_t line = r * (K / 64) + (blk >> 1);
+    const int half = (int)(blk & 1);
+    dh = reinterpret_cast<uint4*>(hi + line * 128 + 32 * half);
+    dl = reinterpret_cast<uint4*>(hi + line * 128 + 64 + 32 * half);
+    s_hi[line * 4 + half] = (uint8_t)b1;
+    s_hi[line * 4 + 2 + half] = (uint8_t)b2;
+  } else {
+    dh = reinterpret_cast<uint4*>(hi + o);
+    dl = reinterpret_cast<uint4*>(lo + o);
+    s_hi[t] = (uint8_t)b1;
+    s_lo[t] = (uint8_t)b2;
+  }
   dh[0] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
   dh[1] = make_uint4(qh[4], qh[5], qh[6], qh[7]);
   dl[0] = make_uint4(ql[0], ql[1], ql[2], ql[3]);
   dl[1] = make_uint4(ql[4], ql[5], ql[6], ql[7]);
-  s_hi[t] = (uint8_t)b1;
-  s_lo[t] = (uint8_t)b2;
 }
 
 void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
                       uint8_t* s_hi, uint8_t* s_lo, hipStream_t st) {
   const int64_t n = rows * (K / 32);
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_mx8_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, K,
-                     hi, lo, s_hi, s_lo);
+  hipLaunchKernelGGL(k_mx8_quant<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
+                     n, K, hi, lo, s_hi, s_lo);
 }
 
-// Grouped expert GEMM, A in two MXFP8 terms (staged through LDS 64 k at a
-// time: row stride kQS bytes = 64 hi + 64 lo + 16 padding), B the expert's
-// MXFP4 rows read from memory into registers one step ahead.  Same tiles,
-// grouping and epilogues as k_gemm<MODE, true, true>.  K % 64 == 0.
+void launch_mx8_quant_lines(const uint16_t* x, int64_t rows, int K, uint8_t* q, uint32_t* qs,
+                            hipStream_t st) {
+  const int64_t n = rows * (K / 32);
+  if (n <= 0) return;
+  hipLaunchKernelGGL(k_mx8_quant<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
+                     n, K, q, nullptr, reinterpret_cast<uint8_t*>(qs), nullptr);
+}
+
+// Grouped expert GEMM on the scaled matrix instruction.  What bounds this
+// shape is operand fetch (the matrix units idle most of the time
+// otherwise), so every global fetch uses whole 128-byte lines:
+//   - A (the two MXFP8 terms of the input rows, step-line layout: one line
+//     per row and 64-deep step) is staged through LDS a step at a time
+//     (row stride kQS = 64 hi + 64 lo + 16 padding, two buffers), fetched
+//     kRingA - 1 steps ahead through a register ring;
+//   - B (the expert's MXFP4 rows as stored) is staged through LDS a group
+//     of kPipe steps (128 bytes of each row) at a time, fetched a group
+//     ahead (two buffers, column stride kQS), with its scale bytes.
+// Same tiles, grouping and epilogues as k_gemm<MODE, true, true>.
+// K % 64 == 0.
+__device__ __forceinline__ int h_of(int lane) { return lane >> 5; }
 constexpr int kQS = 144;
+constexpr int kPipe = 4;   // B steps per group
+constexpr int kRingA = 4;  // A register sets (A runs kRingA - 1 steps ahead)
 
 template <int MODE>
-__global__ __launch_bounds__(256) void k_gemm_mx8(GemmParams p) {
+__global__ __launch_bounds__(256, 2) void k_gemm_mx8(GemmParams p) {
   __shared__ __align__(16) uint8_t Aq[2][kGM * kQS];
-  __shared__ uint32_t Asc[2][kGM];  // per row: bytes s_hi b0, s_hi b1, s_lo b0, s_lo b1
+  __shared__ uint32_t Asc[2][kGM];              // per row: s_hi b0, s_hi b1, s_lo b0, s_lo b1
+  __shared__ __align__(16) uint8_t Bq[2][kGN * kQS];   // per column: kPipe steps x 32 B
+  __shared__ uint16_t Bsc[2][kGN * kPipe];       // per column and step: the 2 blocks' scales
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int n0 = blockIdx.x * kGN;
@@ -441,61 +478,37 @@ __global__ __launch_bounds__(256) void k_gemm_mx8(GemmParams p) {
   const int e = p.tile_e[blockIdx.y];
   const int r0 = p.e_off[e] + p.tile_r0[blockIdx.y];
   const int rows = min(kGM, p.e_off[e + 1] - r0);
-  const int K = p.K, KB = K / 32;
-  // A staging: chunk c = tid + 256 i of the tile's 128 rows x 8 pieces of 16
-  // bytes (pieces 0-3 hi, 4-7 lo)
+  const int K = p.K, KB = K / 32, KS = K / 64;
+  const int nk = KS;
+  // staging map shared by A and B: piece c = tid + 256 i (i = 0..3) is row /
+  // column c >> 3, 16-byte piece c & 7 of its 128 bytes
   const int pc = tid & 7;
   const uint8_t* asrc[4];
+  const uint8_t* bsrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = (tid + 256 * i) >> 3;
     const int lr = r0 + min(r, rows - 1);
     const int ar = p.a_rows ? p.a_rows[lr] : lr;
-    asrc[i] = (pc < 4 ? p.qa_hi : p.qa_lo) + (size_t)ar * K + 16 * (pc & 3);
+    asrc[i] = p.qa + (size_t)ar * KS * 128 + 16 * pc;
+    bsrc[i] = p.codes + ((size_t)e * p.N + min(n0 + r, p.N - 1)) * (K / 2) + 16 * (pc & 1);
   }
-  const uint16_t* ssh = nullptr;  // 2 scale bytes per step (threads 0..127: row tid)
-  const uint16_t* ssl = nullptr;
-  if (tid < kGM) {
-    const int lr = r0 + min(tid, rows - 1);
+  // A scales: every thread fetches row (tid & 127)'s dword, threads < 128
+  // stage it (one load per thread keeps every wave's load count equal)
+  const uint32_t* ssrc;
+  {
+    const int lr = r0 + min(tid & 127, rows - 1);
     const int ar = p.a_rows ? p.a_rows[lr] : lr;
-    ssh = reinterpret_cast<const uint16_t*>(p.qs_hi + (size_t)ar * KB);
-    ssl = reinterpret_cast<const uint16_t*>(p.qs_lo + (size_t)ar * KB);
+    ssrc = p.qsc + (size_t)ar * KS;
   }
-  // B: this lane's column of each 32-column block `in`, k block half h
-  const int h = lane >> 5;
-  const uint8_t* bc[2];
-  const uint8_t* bs[2];
-#pragma unroll
-  for (int in = 0; in < 2; ++in) {
-    const int n = min(n0 + wn * 64 + in * 32 + (lane & 31), p.N - 1);
-    const size_t row = (size_t)e * p.N + n;
-    bc[in] = p.codes + row * (K / 2) + 16 * h;
-    bs[in] = p.scales + row * KB + h;
-  }
-  u32x4_t ra[4];
-  uint32_t rsh = 0, rsl = 0;
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ra[i] = *reinterpret_cast<const u32x4_t*>(asrc[i] + kt * 64);
-    if (tid < kGM) { rsh = ssh[kt]; rsl = ssl[kt]; }
-  };
-  u32x4_t rb[2], rbn[2];
-  uint32_t sb[2], sbn[2];
-  auto load_b = [&](int kt, u32x4_t* c, uint32_t* sc) {
-#pragma unroll
-    for (int in = 0; in < 2; ++in) {
-      c[in] = *reinterpret_cast<const u32x4_t*>(bc[in] + kt * 32);
-      sc[in] = bs[in][2 * kt];
-    }
-  };
-  auto stage_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (tid + 256 * i) >> 3;
-      *reinterpret_cast<u32x4_t*>(&Aq[buf][r * kQS + 16 * pc]) = ra[i];
-    }
-    if (tid < kGM) Asc[buf][tid] = rsh | (rsl << 16);
-  };
+  // B scales: thread tid fetches column (tid & 127)'s two blocks of steps
+  // 2 (tid >> 7) and 2 (tid >> 7) + 1 of a group
+  const uint8_t* bssrc = p.scales + ((size_t)e * p.N + min(n0 + (tid & 127), p.N - 1)) * KB;
+  const int bsj = 2 * (tid >> 7);
+  u32x4_t ra[kRingA][4];
+  uint32_t rsc[kRingA];
+  u32x4_t rbq[4];
+  uint32_t rbs[2];
   f32x16_t acc[2][2];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
@@ -503,48 +516,115 @@ __global__ __launch_bounds__(256) void k_gemm_mx8(GemmParams p) {
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
-  const int nk = K / 64;
-  load_a(0);
-  load_b(0, rbn, sbn);
-  stage_a(0);
+  // Every load is unconditional (steps past the end re-read the last one and
+  // are never used), so each iteration issues the same loads and the wait
+  // before a step's first use counts only the loads issued after it.
+#define MX8_LOAD_A(u, kt)                                                            \
+  do {                                                                               \
+    for (int i = 0; i < 4; ++i)                                                      \
+      ra[u][i] = *reinterpret_cast<const u32x4_t*>(asrc[i] + (size_t)(kt) * 128);    \
+    rsc[u] = ssrc[kt];                                                               \
+  } while (0)
+  // group g of B: piece pc of each column is step g kPipe + pc / 2, half pc % 2
+#define MX8_LOAD_B(g)                                                                \
+  do {                                                                               \
+    const int st = min((g) * kPipe + (pc >> 1), nk - 1);                             \
+    for (int i = 0; i < 4; ++i)                                                      \
+      rbq[i] = *reinterpret_cast<const u32x4_t*>(bsrc[i] + (size_t)st * 32);         \
+    for (int j = 0; j < 2; ++j) {                                                    \
+      const int sj = min((g) * kPipe + bsj + j, nk - 1);                             \
+      rbs[j] = *reinterpret_cast<const uint16_t*>(bssrc + 2 * sj);                   \
+    }                                                                                \
+  } while (0)
+#define MX8_STAGE_A(u, buf)                                                          \
+  do {                                                                               \
+    for (int i = 0; i < 4; ++i) {                                                    \
+      const int r = (tid + 256 * i) >> 3;                                            \
+      *reinterpret_cast<u32x4_t*>(&Aq[buf][r * kQS + 16 * pc]) = ra[u][i];           \
+    }                                                                                \
+    if (tid < kGM) Asc[buf][tid] = rsc[u];                                           \
+  } while (0)
+#define MX8_STAGE_B(buf)                                                             \
+  do {                                                                               \
+    for (int i = 0; i < 4; ++i) {                                                    \
+      const int c = (tid + 256 * i) >> 3;                                            \
+      *reinterpret_cast<u32x4_t*>(&Bq[buf][c * kQS + 16 * pc]) = rbq[i];             \
+    }                                                                                \
+    for (int j = 0; j < 2; ++j) Bsc[buf][(tid & 127) * kPipe + bsj + j] = (uint16_t)rbs[j]; \
+  } while (0)
+#pragma unroll
+  for (int u = 0; u < kRingA; ++u) MX8_LOAD_A(u, min(u, nk - 1));
+  MX8_LOAD_B(0);
+  MX8_STAGE_A(0, 0);
+  MX8_STAGE_B(0);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
+  static_assert(kPipe % kRingA == 0 || kRingA % kPipe == 0, "ring and group must nest");
+  for (int kt0 = 0; kt0 < nk; kt0 += kPipe) {
+    const int gb = (kt0 / kPipe) & 1;
+    MX8_LOAD_B(kt0 / kPipe + 1);  // the next group, staged at this group's end
 #pragma unroll
-    for (int in = 0; in < 2; ++in) { rb[in] = rbn[in]; sb[in] = sbn[in]; }
-    if (kt + 1 < nk) {  // next step's loads before this step's math
-      load_a(kt + 1);
-      load_b(kt + 1, rbn, sbn);
-    }
+    for (int u = 0; u < kPipe; ++u) {
+      const int kt = kt0 + u;
+      const int cur = kt & 1;
+      const int ua = u % kRingA;
+      // A of step kt + kRingA into the set staged at the end of the last step
+      MX8_LOAD_A(ua, min(kt + kRingA, nk - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt < nk) {  // uniform for the block
+        // all operands first, then the four independent hi products, then
+        // the lo ones (each lo MFMA is four instructions behind the hi one
+        // that wrote its accumulator)
+        i32x8_t ahi[2], alo[2], bq[2];
+        int sa_hi[2], sa_lo[2], s_b[2];
 #pragma unroll
-    for (int im = 0; im < 2; ++im) {
-      const int rr = wm * 64 + im * 32 + (lane & 31);
-      const uint8_t* base = &Aq[cur][rr * kQS + 16 * h];
-      const u32x4_t h0 = *reinterpret_cast<const u32x4_t*>(base);
-      const u32x4_t h1 = *reinterpret_cast<const u32x4_t*>(base + 32);
-      const u32x4_t l0 = *reinterpret_cast<const u32x4_t*>(base + 64);
-      const u32x4_t l1 = *reinterpret_cast<const u32x4_t*>(base + 96);
-      const uint32_t sc = Asc[cur][rr];
-      const int sa_hi = (int)((sc >> (8 * h)) & 0xFFu);
-      const int sa_lo = (int)((sc >> (16 + 8 * h)) & 0xFFu);
-      const i32x8_t ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
-                           (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-      const i32x8_t alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
-                           (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+        for (int im = 0; im < 2; ++im) {
+          const int rr = wm * 64 + im * 32 + (lane & 31);
+          const uint8_t* base = &Aq[cur][rr * kQS + 16 * h_of(lane)];
+          const u32x4_t h0 = *reinterpret_cast<const u32x4_t*>(base);
+          const u32x4_t h1 = *reinterpret_cast<const u32x4_t*>(base + 32);
+          const u32x4_t l0 = *reinterpret_cast<const u32x4_t*>(base + 64);
+          const u32x4_t l1 = *reinterpret_cast<const u32x4_t*>(base + 96);
+          const uint32_t sc = Asc[cur][rr];
+          sa_hi[im] = (int)((sc >> (8 * h_of(lane))) & 0xFFu);
+          sa_lo[im] = (int)((sc >> (16 + 8 * h_of(lane))) & 0xFFu);
+          ahi[im] = i32x8_t{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
+                            (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+          alo[im] = i32x8_t{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
+                            (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+        }
 #pragma unroll
-      for (int in = 0; in < 2; ++in) {
-        const i32x8_t bq = {(int)rb[in].x, (int)rb[in].y, (int)rb[in].z, (int)rb[in].w,
-                            0, 0, 0, 0};
-        const int s_b = (int)sb[in];
-        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            ahi, bq, acc[im][in], 0, 4, 0, sa_hi, 0, s_b);
-        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-            alo, bq, acc[im][in], 0, 4, 0, sa_lo, 0, s_b);
+        for (int in = 0; in < 2; ++in) {
+          const int cn = wn * 64 + in * 32 + (lane & 31);
+          const u32x4_t b4 =
+              *reinterpret_cast<const u32x4_t*>(&Bq[gb][cn * kQS + u * 32 + 16 * h_of(lane)]);
+          bq[in] = i32x8_t{(int)b4.x, (int)b4.y, (int)b4.z, (int)b4.w, 0, 0, 0, 0};
+          s_b[in] = (int)((Bsc[gb][cn * kPipe + u] >> (8 * h_of(lane))) & 0xFFu);
+        }
+#pragma unroll
+        for (int im = 0; im < 2; ++im)
+#pragma unroll
+          for (int in = 0; in < 2; ++in)
+            acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                ahi[im], bq[in], acc[im][in], 0, 4, 0, sa_hi[im], 0, s_b[in]);
+#pragma unroll
+        for (int im = 0; im < 2; ++im)
+#pragma unroll
+          for (int in = 0; in < 2; ++in)
+            acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                alo[im], bq[in], acc[im][in], 0, 4, 0, sa_lo[im], 0, s_b[in]);
       }
+      // A of step kt + 1 (fetched kRingA - 1 steps ago) into the other buffer
+      // (past the last step it is never read); at the group's last step, the
+      // next group of B (fetched at the group's start)
+      MX8_STAGE_A((ua + 1) % kRingA, cur ^ 1);
+      if (u == kPipe - 1) MX8_STAGE_B(gb ^ 1);
+      __syncthreads();
     }
-    if (kt + 1 < nk) stage_a(cur ^ 1);
-    __syncthreads();
   }
+#undef MX8_LOAD_A
+#undef MX8_LOAD_B
+#undef MX8_STAGE_A
+#undef MX8_STAGE_B
   gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, e);
 }
 
@@ -674,24 +754,30 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   p.tile_e = a.tile_e; p.tile_r0 = a.tile_r0; p.n_tiles = a.n_tiles; p.e_off = a.e_off;
   p.list_tok = a.list_tok; p.list_slot = a.list_slot; p.topk = a.k;
   p.alpha = a.alpha; p.limit = a.limit;
-  p.qa_hi = a.q_hi; p.qa_lo = a.q_lo; p.qs_hi = a.qs_hi; p.qs_lo = a.qs_lo;
-  const bool mx8 = a.q_hi != nullptr;
+  p.qa = a.q; p.qsc = a.qs;
+  const bool mx8 = a.q != nullptr;
   // gate_up + SwiGLU: A = xn rows of the listed tokens, N = 2 I, out act [list][I]
-  if (mx8) launch_mx8_quant(a.xn, a.M, a.H, a.q_hi, a.q_lo, a.qs_hi, a.qs_lo, st);
+  if (mx8) launch_mx8_quant_lines(a.xn, a.M, a.H, a.q, a.qs, st);
   p.A = a.xn; p.lda = a.H; p.a_rows = a.list_tok;
   p.codes = a.gu_codes; p.scales = a.gu_scales; p.bias = a.gu_bias;
   p.C = a.act; p.ldc = a.I; p.N = 2 * a.I; p.K = a.H;
-  const dim3 g_gu((2 * a.I + kGN - 1) / kGN, max_tiles);
-  if (mx8) hipLaunchKernelGGL((k_gemm_mx8<GEMM_SWIGLU>), g_gu, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((k_gemm<GEMM_SWIGLU, true, true>), g_gu, dim3(256), 0, st, p);
+  if (mx8)
+    hipLaunchKernelGGL((k_gemm_mx8<GEMM_SWIGLU>), dim3((2 * a.I + kGN - 1) / kGN, max_tiles),
+                       dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_gemm<GEMM_SWIGLU, true, true>),
+                       dim3((2 * a.I + kGN - 1) / kGN, max_tiles), dim3(256), 0, st, p);
   // down: A = act rows in list order, N = H, out ybuf[token][slot]
-  if (mx8) launch_mx8_quant(a.act, (int64_t)a.M * a.k, a.I, a.q_hi, a.q_lo, a.qs_hi, a.qs_lo, st);
+  if (mx8) launch_mx8_quant_lines(a.act, (int64_t)a.M * a.k, a.I, a.q, a.qs, st);
   p.A = a.act; p.lda = a.I; p.a_rows = nullptr;
   p.codes = a.dn_codes; p.scales = a.dn_scales; p.bias = a.dn_bias;
   p.ybuf = a.ybuf; p.N = a.H; p.K = a.I; p.C = nullptr;
-  const dim3 g_dn((a.H + kGN - 1) / kGN, max_tiles);
-  if (mx8) hipLaunchKernelGGL((k_gemm_mx8<GEMM_SCATTER>), g_dn, dim3(256), 0, st, p);
-  else hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), g_dn, dim3(256), 0, st, p);
+  if (mx8)
+    hipLaunchKernelGGL((k_gemm_mx8<GEMM_SCATTER>), dim3((a.H + kGN - 1) / kGN, max_tiles),
+                       dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), dim3((a.H + kGN - 1) / kGN, max_tiles),
+                       dim3(256), 0, st, p);
   hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.idx, a.E,
                      a.k, a.H, a.h);
 }
