@@ -363,6 +363,9 @@ def main():
                          "larger batches are reported as a separate line)")
     ap.add_argument("--matrix", action="store_true",
                     help="run steps of 2+ sequences on the matrix cores (NEON_DECODE_MATRIX)")
+    ap.add_argument("--matrix-mx8", action="store_true",
+                    help="as --matrix, with the expert GEMMs on the scaled fp8 x fp4 "
+                         "instruction (NEON_DECODE_MATRIX_MX8)")
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--cpu-steps", type=int, default=12)
     ap.add_argument("--sweep", choices=["gemv", "attn"],
@@ -420,7 +423,9 @@ def main():
     eng = ne.Engine(cfg, device=0)
     stream = torch.cuda.current_stream()
     eng.init_random(args.seed, stream)
-    if args.matrix:
+    if args.matrix_mx8:
+        eng.set_decode_mode(ne.DECODE_MATRIX_MX8)
+    elif args.matrix:
         eng.set_decode_mode(ne.DECODE_MATRIX)
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, cfg.vocab, size=(B, args.prompt), dtype=np.int64)
@@ -535,7 +540,8 @@ def main():
                                f"{args.prompt}-token prompt (BASELINE config "
                                f"{3 if args.model == 'gpt-oss-20b' else 4})",
                    "batch": B, "prompt": args.prompt,
-                   "decode_mode": "matrix" if args.matrix and B > 1 else "exact",
+                   "decode_mode": ("matrix-mx8" if args.matrix_mx8 and B > 1 else
+                                   "matrix" if args.matrix and B > 1 else "exact"),
                    "kv_len": [kv0, kv0 + args.steps], "parallelism": "none (1 GPU)"},
         # bytes per token of a batch-1 step (at batch > 1 weights are shared)
         "step_bytes_per_token": bpt if B == 1 else None,

@@ -132,7 +132,7 @@ enum {
 /* Selects how neon_prefill runs the prompt (default NEON_PREFILL_CHUNKED). */
 neon_status neon_set_prefill_mode(neon_ctx* ctx, int mode);
 
-enum { NEON_DECODE_EXACT = 0, NEON_DECODE_MATRIX = 1 };
+enum { NEON_DECODE_EXACT = 0, NEON_DECODE_MATRIX = 1, NEON_DECODE_MATRIX_MX8 = 2 };
 /* Selects how decode steps of two or more sequences run (a step of one
  * sequence always runs the exact kernels):
  *  - NEON_DECODE_EXACT (default): every dot product in the canonical fp32
@@ -142,7 +142,11 @@ enum { NEON_DECODE_EXACT = 0, NEON_DECODE_MATRIX = 1 };
  *    rows dequantised exactly to bf16); the same rounding points, with fp32
  *    additions in another order.  Needs max_batch <= 64, output widths that
  *    are multiples of 16 and reductions that are multiples of 32 up to 4096
- *    (NEON_EINVAL otherwise).
+ *    (NEON_EINVAL otherwise);
+ *  - NEON_DECODE_MATRIX_MX8: NEON_DECODE_MATRIX with the expert GEMMs on
+ *    v_mfma_scale_f32_16x16x128_f8f6f4 (the MXFP4 expert rows as the scaled
+ *    B operand, each expert input as two MXFP8 terms per 32-element block,
+ *    within 2^(floor(log2 amax) - 8) of the bf16 values).
  * No counterpart in the reference, which has no model code. */
 neon_status neon_set_decode_mode(neon_ctx* ctx, int mode);
 

@@ -284,7 +284,7 @@ def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=N
 
 
 PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED, PREFILL_MX8 = 0, 1, 2, 3
-DECODE_EXACT, DECODE_MATRIX = 0, 1
+DECODE_EXACT, DECODE_MATRIX, DECODE_MATRIX_MX8 = 0, 1, 2
 
 
 # ---------------------------------------------------------------------------

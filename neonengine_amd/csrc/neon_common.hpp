@@ -304,4 +304,86 @@ __host__ __device__ __forceinline__ uint64_t stream_id(int layer, int kind) {
   return ((uint64_t)(layer + 1) << 16) | (uint64_t)kind;
 }
 
+// ---- MXFP8 (E4M3) activations: the two-term image of a bf16 32-block ----
+// (OCP MX v1.0 E4M3 and shared-exponent rule, without saturation; the CPU
+// oracle's or_mx8_quant states the same arithmetic, bit for bit.)
+__device__ __forceinline__ int ilog2f_dev(float a) {
+  const uint32_t b = __float_as_uint(a);
+  const int ef = (b >> 23) & 255;
+  if (ef) return ef - 127;
+  return (31 - __builtin_clz(b & 0x7FFFFFu)) - 149;
+}
+
+// smallest shared exponent with amax / 2^e <= 448: floor(log2 amax) - 8, one
+// more when amax's significand exceeds 1.75
+__device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
+  if (!(amax > 0.0f)) return 127u;
+  int e = ilog2f_dev(amax);
+  if (__builtin_amdgcn_ldexpf(amax, -e) > 1.75f) e += 1;
+  e = e - 8 + 127;
+  return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
+}
+
+// Four E4M3 codes (one dword, element j in byte j) of f[0..3], each of
+// magnitude <= 448, by the hardware conversion (round to nearest even; it
+// gives the CPU oracle's or_e4m3_encode bytes for every bf16 value of
+// magnitude <= 448, every midpoint between E4M3 neighbours and the fp32
+// values one unit either side, and 1M random fp32 values, all checked on
+// gfx950)
+__device__ __forceinline__ uint32_t e4m3x4(float f0, float f1, float f2, float f3) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(f0, f1, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(f2, f3, w, true);
+  return (uint32_t)w;
+}
+
+// The 8 elements v of this lane, one quarter (q = lane & 3 of four adjacent
+// lanes) of a 32-element block: its hi and lo E4M3 codes (4 per dword) and
+// the block's two scale bytes.  Every lane of the quad must take part.
+__device__ __forceinline__ void mx8_quant8(const float (&v)[8], uint32_t (&qh)[2],
+                                           uint32_t (&ql)[2], uint32_t& b1, uint32_t& b2) {
+  float amax = 0.0f;
+  uint32_t nonfin = 0;  // bit j: element j is NaN or infinite
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float a = fabsf(v[j]);
+    if (a < INFINITY) amax = fmaxf(amax, a);
+    else nonfin |= 1u << j;
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  b1 = mx8_scale_byte(amax);
+  float t[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    t[j] = (nonfin >> j) & 1 ? 0.0f : __builtin_amdgcn_ldexpf(v[j], 127 - (int)b1);
+  qh[0] = e4m3x4(t[0], t[1], t[2], t[3]);
+  qh[1] = e4m3x4(t[4], t[5], t[6], t[7]);
+  const float hv[8] = {__builtin_amdgcn_cvt_f32_fp8((int)qh[0], 0),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[0], 1),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[0], 2),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[0], 3),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[1], 0),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[1], 1),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[1], 2),
+                       __builtin_amdgcn_cvt_f32_fp8((int)qh[1], 3)};
+  float res[8], rmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    res[j] = (nonfin >> j) & 1 ? 0.0f
+                               : __fsub_rn(v[j], __builtin_amdgcn_ldexpf(hv[j], (int)b1 - 127));
+    rmax = fmaxf(rmax, fabsf(res[j]));
+  }
+  // a non-finite element: the NaN code in hi, 0 in lo
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    if ((nonfin >> j) & 1) qh[j >> 2] = (qh[j >> 2] & ~(0xFFu << (8 * (j & 3)))) | (0x7Fu << (8 * (j & 3)));
+  rmax = fmaxf(rmax, __shfl_xor(rmax, 1, 64));
+  rmax = fmaxf(rmax, __shfl_xor(rmax, 2, 64));
+  b2 = mx8_scale_byte(rmax);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t[j] = __builtin_amdgcn_ldexpf(res[j], 127 - (int)b2);
+  ql[0] = e4m3x4(t[0], t[1], t[2], t[3]);
+  ql[1] = e4m3x4(t[4], t[5], t[6], t[7]);
+}
+
 }  // namespace neon

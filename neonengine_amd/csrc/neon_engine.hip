@@ -123,6 +123,7 @@ struct neon_ctx {
   // that mode is first selected; refreshed before a step after any change)
   struct MxLayer { uint16_t *wqkv, *wo; uint8_t *gu_c, *gu_s, *dn_c, *dn_s; };
   char* mx_w = nullptr;
+  uint8_t* mx8_q = nullptr;  // NEON_DECODE_MATRIX_MX8: MXFP8 images of the expert inputs
   std::vector<MxLayer> mxp;
   uint16_t* mx_lm = nullptr;
   bool mx_dirty = true;
@@ -289,6 +290,7 @@ extern "C" void neon_ctx_destroy(neon_ctx* ctx) {
   if (ctx->work) (void)hipFree(ctx->work);
   if (ctx->pf) (void)hipFree(ctx->pf);
   if (ctx->mx_w) (void)hipFree(ctx->mx_w);
+  if (ctx->mx8_q) (void)hipFree(ctx->mx8_q);
   delete ctx;
 }
 
@@ -736,6 +738,16 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
     r.idx = nullptr; r.score = nullptr;  // the top-k runs with the route lists
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
+    const bool mx8 = ctx->decode_mode == NEON_DECODE_MATRIX_MX8;
+    // the MXFP8 images: xn [B][H] then the SwiGLU output [B k][I], each hi,
+    // lo, then the two scale arrays
+    uint8_t* q8 = ctx->mx8_q;
+    const size_t nx = (size_t)c.max_batch * H, ny = (size_t)c.max_batch * c.top_k * I;
+    size_t off = 0;  // every piece 256-byte aligned (16-byte loads and stores)
+    auto take = [&](size_t bytes) { uint8_t* p = q8 + off; off = align_up(off + bytes); return p; };
+    uint8_t *xh = take(nx), *xl = take(nx), *xsh = take(nx / 32), *xsl = take(nx / 32);
+    uint8_t *yh = take(ny), *yl = take(ny), *ysh = take(ny / 32), *ysl = take(ny / 32);
+    if (mx8) { r.xq_hi = xh; r.xq_lo = xl; r.xs_hi = xsh; r.xs_lo = xsl; }
     launch_router(r, st);
     launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
                       ctx->mx_route, st);
@@ -752,7 +764,13 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k; dn.err = ctx->dev_err;
-    launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
+    if (mx8) {
+      gu.xq_hi = xh; gu.xq_lo = xl; gu.xs_hi = xsh; gu.xs_lo = xsl;
+      gu.yq_hi = yh; gu.yq_lo = yl; gu.ys_hi = ysh; gu.ys_lo = ysl;
+      launch_mx_moe8(gu, dn, ctx->moe_score, ctx->h, st);
+    } else {
+      launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
+    }
   }
   launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
   MxArgs lm{};
@@ -763,7 +781,8 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
 }
 
 static void enqueue_step(neon_ctx* ctx, int B, hipStream_t st) {
-  if (ctx->decode_mode == NEON_DECODE_MATRIX && B >= 2) {
+  if ((ctx->decode_mode == NEON_DECODE_MATRIX || ctx->decode_mode == NEON_DECODE_MATRIX_MX8) &&
+      B >= 2) {
     const neon_config& c = ctx->cfg;
     enqueue_rows_mx(ctx, B, st);
     if (ctx->temperature > 0.0f)
@@ -832,7 +851,8 @@ static void mx_repack(neon_ctx* ctx, hipStream_t st) {
 }
 
 static neon_status run_steps(neon_ctx* ctx, int n, hipStream_t st) {
-  if (ctx->decode_mode == NEON_DECODE_MATRIX && ctx->batch >= 2 && ctx->mx_dirty) {
+  if ((ctx->decode_mode == NEON_DECODE_MATRIX || ctx->decode_mode == NEON_DECODE_MATRIX_MX8) &&
+      ctx->batch >= 2 && ctx->mx_dirty) {
     mx_repack(ctx, st);
     HIPCHK(ctx, hipGetLastError());
     ctx->mx_dirty = false;
@@ -1071,9 +1091,10 @@ extern "C" neon_status neon_prefill_ragged(neon_ctx* ctx, const int32_t* ids,
 
 extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
   if (!ctx) return NEON_EINVAL;
-  if (mode != NEON_DECODE_EXACT && mode != NEON_DECODE_MATRIX)
+  if (mode != NEON_DECODE_EXACT && mode != NEON_DECODE_MATRIX && mode != NEON_DECODE_MATRIX_MX8)
     FAIL(ctx, NEON_EINVAL, "neon_set_decode_mode: unknown mode %d", mode);
-  if (mode == NEON_DECODE_MATRIX) {
+  const bool matrix = mode == NEON_DECODE_MATRIX || mode == NEON_DECODE_MATRIX_MX8;
+  if (matrix) {
     const neon_config& c = ctx->cfg;
     const int H = c.hidden, qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
     if (c.max_batch < 2 || c.max_batch > kMxMaxRows)
@@ -1086,7 +1107,19 @@ extern "C" neon_status neon_set_decode_mode(neon_ctx* ctx, int mode) {
                              "width a multiple of 16 (expert widths of 64), every reduction "
                              "a multiple of 32 up to %d and max_batch * top_k <= 256", kMxMaxK);
   }
-  if (mode == NEON_DECODE_MATRIX && !ctx->mx_w) {
+  if (mode == NEON_DECODE_MATRIX_MX8 && !ctx->mx8_q) {
+    const neon_config& c = ctx->cfg;
+    const size_t Bm = c.max_batch;
+    const size_t nx = Bm * c.hidden, ny = Bm * c.top_k * c.intermediate;
+    HIPCHK(ctx, hipSetDevice(ctx->device));
+    const size_t bytes = align_up(nx) * 2 + align_up(nx / 32) * 2 + align_up(ny) * 2 +
+                         align_up(ny / 32) * 2;
+    if (hipMalloc(&ctx->mx8_q, bytes) != hipSuccess) {
+      ctx->mx8_q = nullptr;
+      FAIL(ctx, NEON_ENOMEM, "neon_set_decode_mode: hipMalloc of the MXFP8 buffers failed");
+    }
+  }
+  if (matrix && !ctx->mx_w) {
     const neon_config& c = ctx->cfg;
     const int H = c.hidden, I = c.intermediate, E = c.n_experts;
     const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim;
@@ -1218,7 +1251,8 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
   else if (nm == "moe_idx") { src = ctx->moe_idx; n = B * c.top_k * 4; }
   else if (nm == "moe_score") { src = ctx->moe_score; n = B * c.top_k * 4; }
   else if (nm == "mx_route") {
-    if (ctx->mx_route == nullptr || ctx->decode_mode != NEON_DECODE_MATRIX || B < 2)
+    if (ctx->mx_route == nullptr || B < 2 ||
+        (ctx->decode_mode != NEON_DECODE_MATRIX && ctx->decode_mode != NEON_DECODE_MATRIX_MX8))
       FAIL(ctx, NEON_EINVAL, "neon_read_activation: 'mx_route' exists after matrix-core steps "
            "of two or more sequences");
     const size_t S = std::min<size_t>(c.n_experts, B * c.top_k);

@@ -110,6 +110,9 @@ struct RouterArgs {
   // one-launch expert kernel that follows), may be NULL
   int32_t* zero = nullptr;
   int zero_n = 0;
+  // with xn_out: its two-term MXFP8 image (hi, lo [B][H], scales [B][H/32]),
+  // written by the same wave (NULL: none)
+  uint8_t *xq_hi = nullptr, *xq_lo = nullptr, *xs_hi = nullptr, *xs_lo = nullptr;
 };
 // router logits, then (when a.idx) the top-k / softmax
 void launch_router(const RouterArgs& a, hipStream_t st);
@@ -174,6 +177,11 @@ struct MxArgs {
                              // launch_mx_moe before the expert kernels
   int B, N, K, E, k;
   float alpha, limit;
+  // expert modes on the scaled fp8 x fp4 instruction (launch_mx_moe8): the
+  // input rows' two-term MXFP8 image, hi / lo [rows][K], scales [rows][K/32];
+  // gate_up also writes its SwiGLU output's image into yq_* ([B k][N / 2])
+  const uint8_t *xq_hi = nullptr, *xq_lo = nullptr, *xs_hi = nullptr, *xs_lo = nullptr;
+  uint8_t *yq_hi = nullptr, *yq_lo = nullptr, *ys_hi = nullptr, *ys_lo = nullptr;
 };
 bool mx_shape_ok(int N, int K, int B);
 // standalone MXFP4 GEMV on the matrix cores (checkpoint layout, K % 32 == 0,
@@ -200,6 +208,12 @@ void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);
 // copies in Wp / sp)
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
                    hipStream_t st);
+// launch_mx_moe with the expert GEMMs on v_mfma_scale_f32_16x16x128_f8f6f4:
+// gate_up.xq_* hold the MXFP8 image of gate_up.x (the router writes it),
+// gate_up.yq_* receive the image of the SwiGLU output that down reads; the
+// packed MXFP4 pieces feed the B operand as they are
+void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
+                    hipStream_t st);
 // top-k of B rows of router logits and the route lists of their pairs
 // (B k <= 256, E <= 256) in one launch
 void launch_topk_route(const float* lg, int32_t* idx, float* score, int B, int E, int k,

@@ -1615,7 +1615,8 @@ __global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
     const uint16_t* __restrict__ bias, float* __restrict__ lg_out, int E,
-    int H, int32_t* __restrict__ zero, int zero_n) {
+    int H, int32_t* __restrict__ zero, int zero_n, uint8_t* __restrict__ xq_hi,
+    uint8_t* __restrict__ xq_lo, uint8_t* __restrict__ xs_hi, uint8_t* __restrict__ xs_lo) {
   const int e = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   if (e == 0 && b == 0 && lane < zero_n) zero[(size_t)lane * kMoeSyncStride] = 0;
   const int U = H / 8;
@@ -1630,6 +1631,28 @@ __global__ __launch_bounds__(64) void k_router_logits(
   wave_x_bf16_finish<P, NORM>(xr, xraw, eps, H, lane,
                               (xn_out != nullptr && e == 0) ? xn_out + (size_t)b * H
                                                             : nullptr);
+  if (xq_hi != nullptr) {  // uniform: the MXFP8 image of the bf16 row
+    // unit u = lane + 64 p holds elements 8 u .. 8 u + 7; four adjacent lanes
+    // make one 32-block (U % 4 == 0, so a quad is valid or padding as a
+    // whole); every wave holds the whole row, and wave e takes the passes
+    // p = e (mod E)
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      if (p % E != e) continue;  // uniform
+      const int u = lane + 64 * p;
+      uint32_t qh[2], ql[2], b1, b2;
+      mx8_quant8(xr[p], qh, ql, b1, b2);
+      if (u < U) {
+        const size_t o = (size_t)b * H + 8 * (size_t)u;
+        *reinterpret_cast<uint2*>(xq_hi + o) = make_uint2(qh[0], qh[1]);
+        *reinterpret_cast<uint2*>(xq_lo + o) = make_uint2(ql[0], ql[1]);
+        if ((u & 3) == 0) {
+          xs_hi[(size_t)b * (H / 32) + u / 4] = (uint8_t)b1;
+          xs_lo[(size_t)b * (H / 32) + u / 4] = (uint8_t)b2;
+        }
+      }
+    }
+  }
   const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
   if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias_e));
 }
@@ -1688,11 +1711,13 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
     if (a.norm_w != nullptr)                                                     \
       hipLaunchKernelGGL((k_router_logits<PP, true>), grid, dim3(64), 0, st, a.x, \
                          a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E,  \
-                         a.H, a.zero, a.zero_n);                                 \
+                         a.H, a.zero, a.zero_n, a.xq_hi, a.xq_lo, a.xs_hi,       \
+                         a.xs_lo);                                               \
     else                                                                         \
       hipLaunchKernelGGL((k_router_logits<PP, false>), grid, dim3(64), 0, st,    \
                          a.x, a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out,  \
-                         a.E, a.H, a.zero, a.zero_n);                            \
+                         a.E, a.H, a.zero, a.zero_n, a.xq_hi, a.xq_lo, a.xs_hi,  \
+                         a.xs_lo);                                               \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)

@@ -684,6 +684,208 @@ void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st) {
   else mx_launch<MX_LOGITS>(a, grid, st);
 }
 
+// ---- experts on the scaled fp8 x fp4 instruction ---------------------------
+// k_mx_moe16 with v_mfma_scale_f32_16x16x128_f8f6f4 (A = the pairs' input
+// rows as two MXFP8 terms, B = the packed MXFP4 pieces as they are, each with
+// its E8M0 scale).  Operand lanes of this shape, measured on gfx950 with an
+// in-bounds probe (exact fp32 match on random codes and scales): a B lane
+// j + 16 g holds column j, k 32 g .. 32 g + 31 (one MX block); an A lane
+// holds row j, k 16 g .. 16 g + 15 in bytes 0-15 and k 64 + 16 g .. in bytes
+// 16-31; the scale of (row or column j, k block b) is byte 0 of lane
+// j + 16 b's scale operand.  One instruction covers the four units
+// 4 b + su (b = 0..3) of a chunk -- the pieces lane j + 16 g already holds
+// for slot su -- so A takes the same units from LDS.  Two instructions (hi,
+// lo) replace k_mx_moe16's four bf16 ones and its E2M1 conversions.
+typedef int mx_i32x8 __attribute__((ext_vector_type(8)));
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
+  constexpr int CKU = 16, CK = 32 * CKU, XQ = 2 * CK + 16;
+  constexpr int TT = kMxMoeTiles;
+  __shared__ __align__(16) uint8_t xq[2][16][XQ];      // per row: CK hi bytes, CK lo bytes
+  __shared__ uint8_t xsc[2][16][2 * CKU];              // per row: CKU hi scales, CKU lo
+  // gate_up: the block's 64 weight rows are 32 SwiGLU columns of its 16
+  // pairs, exactly one 32-block of the down input, quantised here
+  __shared__ float ytile[16][32];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, U = K / 32;
+  const int G = (a.B + 15) / 16;
+  const int slot = blockIdx.y / G, grp = blockIdx.y % G;
+  const int S = gridDim.y / G;
+  const int e = a.route[slot];
+  if (e < 0) return;  // fewer used experts than slots (uniform)
+  if (e >= a.E) {     // a corrupt route table: never read past the experts
+    if (tid == 0) flag_dev_err(a.err, kDevErrExpertId);
+    return;
+  }
+  const int Rall = min(a.route[S + slot], 64);
+  if (16 * grp >= Rall) return;  // (uniform)
+  const int R = min(16, Rall - 16 * grp);
+  const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
+  const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;
+  const bool wave_on = nw0 < N;
+  const int nch = (U + CKU - 1) / CKU;
+  // staging: thread tid copies 16-byte pieces sp and sp + 16 of row sr's
+  // chunk, hi and lo, and unit sp's two scale bytes
+  const int sr = tid >> 4, sp = tid & 15;
+  const bool s_ok = sr < R;
+  int xr = 0;
+  if (s_ok) {
+    const unsigned q = min((unsigned)rows[sr], (unsigned)(a.B * a.k - 1));
+    xr = MODE == MX_GATE_UP ? (int)q / a.k : (int)q;
+  }
+  const uint8_t* qh = a.xq_hi + (size_t)xr * K;
+  const uint8_t* ql = a.xq_lo + (size_t)xr * K;
+  const uint8_t* qsh = a.xs_hi + (size_t)xr * U;
+  const uint8_t* qsl = a.xs_lo + (size_t)xr * U;
+  auto x_load = [&](int c, uint4 (&xv)[4], uint32_t (&sv)[2]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int el = c * CK + 16 * (sp + 16 * (q & 1));
+      const uint8_t* src = (q < 2 ? qh : ql) + el;
+      xv[q] = (s_ok && el < K) ? *reinterpret_cast<const uint4*>(src)
+                               : make_uint4(0u, 0u, 0u, 0u);
+    }
+    const int u = c * CKU + sp;
+    sv[0] = (s_ok && u < U) ? qsh[u] : 127u;
+    sv[1] = (s_ok && u < U) ? qsl[u] : 127u;
+  };
+  auto x_store = [&](int buf, const uint4 (&xv)[4], const uint32_t (&sv)[2]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<uint4*>(&xq[buf][sr][(q < 2 ? 0 : CK) + 16 * (sp + 16 * (q & 1))]) = xv[q];
+    xsc[buf][sr][sp] = (uint8_t)sv[0];
+    xsc[buf][sr][CKU + sp] = (uint8_t)sv[1];
+  };
+  const uint8_t* Pc = static_cast<const uint8_t*>(a.Wp);
+  auto w_load = [&](int c, uint4 (&wv)[TT][4], uint32_t (&sb)[TT][4]) {
+    if (!wave_on) return;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const size_t et = (size_t)e * (N / 16) + nw0 / 16 + tt;
+#pragma unroll
+      for (int su = 0; su < 4; ++su) {
+        const size_t piece = ((et * nch + c) * 4 + su) * 64 + lane;
+        wv[tt][su] = mx_load_nt(Pc + piece * 16);
+        sb[tt][su] = a.sp[piece];
+      }
+    }
+  };
+  mx_f32x4 acc[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) acc[tt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int buf, const uint4 (&wv)[TT][4], const uint32_t (&sb)[TT][4]) {
+    const uint8_t* rowp = &xq[buf][j][16 * (g & 1)];
+#pragma unroll
+    for (int su = 0; su < 4; ++su) {
+      const int u0 = 4 * (g >> 1) + su, u1 = 4 * (2 + (g >> 1)) + su;
+      const uint4 h0 = *reinterpret_cast<const uint4*>(rowp + 32 * u0);
+      const uint4 h1 = *reinterpret_cast<const uint4*>(rowp + 32 * u1);
+      const uint4 l0 = *reinterpret_cast<const uint4*>(rowp + CK + 32 * u0);
+      const uint4 l1 = *reinterpret_cast<const uint4*>(rowp + CK + 32 * u1);
+      const int sa_hi = xsc[buf][j][4 * g + su];
+      const int sa_lo = xsc[buf][j][CKU + 4 * g + su];
+      const mx_i32x8 ahi = {(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
+                            (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      const mx_i32x8 alo = {(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
+                            (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const mx_i32x8 bq = {(int)wv[tt][su].x, (int)wv[tt][su].y, (int)wv[tt][su].z,
+                             (int)wv[tt][su].w, 0, 0, 0, 0};
+        const int s_b = (int)sb[tt][su];
+        acc[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ahi, bq, acc[tt], 0, 4, 0,
+                                                                  sa_hi, 0, s_b);
+        acc[tt] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(alo, bq, acc[tt], 0, 4, 0,
+                                                                  sa_lo, 0, s_b);
+      }
+    }
+  };
+  uint4 wA[TT][4], wB[TT][4];
+  uint32_t sA[TT][4], sB[TT][4];
+  uint4 xv[4];
+  uint32_t xs_v[2];
+  x_load(0, xv, xs_v);
+  w_load(0, wA, sA);
+  x_store(0, xv, xs_v);
+  for (int c = 0; c < nch; c += 2) {
+    const bool has1 = c + 1 < nch, has2 = c + 2 < nch;
+    if (has1) x_load(c + 1, xv, xs_v);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has1) w_load(c + 1, wB, sB);
+    __syncthreads();  // chunk c staged; chunk c - 1's buffer is free
+    if (wave_on) compute(0, wA, sA);
+    if (has1) x_store(1, xv, xs_v);
+    if (!has1) break;
+    if (has2) x_load(c + 2, xv, xs_v);
+    __builtin_amdgcn_sched_barrier(0);
+    if (has2) w_load(c + 2, wA, sA);
+    __syncthreads();  // chunk c + 1 staged; chunk c's buffer is free
+    if (wave_on) compute(1, wB, sB);
+    if (has2) x_store(0, xv, xs_v);
+  }
+  static_assert(TT == 1, "the gate_up epilogue assumes one 16-row tile per wave");
+  if (wave_on) {
+    const int n = nw0 + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 4 * g + r;
+      const bool ok = ri < R && (unsigned)rows[min(ri, R - 1)] < (unsigned)(a.B * a.k);
+      const float d = acc[0][r];
+      if constexpr (MODE == MX_GATE_UP) {
+        const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        const float other = __shfl_xor(v, 1);
+        const uint16_t y = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
+        if ((j & 1) == 0) ytile[ri][8 * w + j / 2] = bf2f(y);
+        if (ok && (j & 1) == 0) a.y[(size_t)rows[ri] * (N / 2) + n / 2] = y;
+      } else {
+        if (ok) a.out_f[(size_t)rows[ri] * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+      }
+    }
+  }
+  if constexpr (MODE == MX_GATE_UP) {
+    // wave 0: row tid / 4's 32 SwiGLU values, a quarter per lane -> the
+    // block of the down input's MXFP8 image (blockIdx.x = its 32-block
+    // index; N / 2 % 32 == 0 and 64-row blocks keep it aligned)
+    __syncthreads();
+    if (w == 0) {
+      const int ri = lane >> 2, q = lane & 3;
+      float v[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) v[t] = ytile[ri][8 * q + t];
+      uint32_t qh[2], ql[2], b1, b2;
+      mx8_quant8(v, qh, ql, b1, b2);
+      const bool ok = ri < R && (unsigned)rows[min(ri, R - 1)] < (unsigned)(a.B * a.k);
+      if (ok) {
+        const int I = N / 2;
+        const size_t o = (size_t)rows[ri] * I + 32 * blockIdx.x + 8 * q;
+        *reinterpret_cast<uint2*>(a.yq_hi + o) = make_uint2(qh[0], qh[1]);
+        *reinterpret_cast<uint2*>(a.yq_lo + o) = make_uint2(ql[0], ql[1]);
+        if (q == 0) {
+          a.ys_hi[(size_t)rows[ri] * (I / 32) + blockIdx.x] = (uint8_t)b1;
+          a.ys_lo[(size_t)rows[ri] * (I / 32) + blockIdx.x] = (uint8_t)b2;
+        }
+      }
+    }
+  }
+}
+
+void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
+                    hipStream_t st) {
+  const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
+  const int G = (gate_up.B + 15) / 16;
+  down.xq_hi = gate_up.yq_hi; down.xq_lo = gate_up.yq_lo;
+  down.xs_hi = gate_up.ys_hi; down.xs_lo = gate_up.ys_lo;
+  hipLaunchKernelGGL(k_mx8_moe16<MX_GATE_UP>,
+                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G), dim3(256), 0, st,
+                     gate_up);
+  hipLaunchKernelGGL(k_mx8_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
+                     dim3(256), 0, st, down);
+  hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
+                     down.out_f, score, h, down.N, down.k);
+}
+
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
                    hipStream_t st) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);

@@ -329,123 +329,66 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 //   - D: as the other 32x32 shapes (row 8 (r/4) + 4 (lane/32) + r%4,
 //     column lane%32).
 // ===========================================================================
-__device__ __forceinline__ int ilog2f_dev(float a) {
-  const uint32_t b = __float_as_uint(a);
-  const int ef = (b >> 23) & 255;
-  if (ef) return ef - 127;
-  return (31 - __builtin_clz(b & 0x7FFFFFu)) - 149;
-}
-
-__device__ __forceinline__ uint32_t e4m3_encode_dev(float v) {
-  const uint32_t b = __float_as_uint(v);
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7Fu;  // NaN
-  const uint32_t sgn = (b >> 24) & 0x80u;
-  const float a = __uint_as_float(b & 0x7FFFFFFFu);
-  if (a >= 448.0f) return sgn | 0x7Eu;
-  if (a < 0.015625f) return sgn | (uint32_t)(int)__builtin_rintf(__fmul_rn(a, 512.0f));
-  int e = ilog2f_dev(a);
-  int q = (int)__builtin_rintf(__fmul_rn(__fsub_rn(__builtin_amdgcn_ldexpf(a, -e), 1.0f), 8.0f));
-  if (q == 8) { e += 1; q = 0; }
-  return sgn | (uint32_t)(((e + 7) << 3) | q);
-}
-
-// finite codes only (the quantiser never decodes the NaN code)
-__device__ __forceinline__ float e4m3_decode_dev(uint32_t c) {
-  const int e = (c >> 3) & 15, m = c & 7;
-  const float v = e == 0 ? __builtin_amdgcn_ldexpf((float)m, -9)
-                         : __builtin_amdgcn_ldexpf((float)(8 + m), e - 10);
-  return (c & 0x80u) ? -v : v;
-}
-
-// smallest shared exponent with amax / 2^e <= 448: floor(log2 amax) - 8, one
-// more when amax's significand exceeds 1.75
-__device__ __forceinline__ uint32_t mx8_scale_byte(float amax) {
-  if (!(amax > 0.0f)) return 127u;
-  int e = ilog2f_dev(amax);
-  if (__builtin_amdgcn_ldexpf(amax, -e) > 1.75f) e += 1;
-  e = e - 8 + 127;
-  return (uint32_t)(e < 0 ? 0 : (e > 254 ? 254 : e));
-}
-
-// one thread per 32-element block: rows x K/32 threads.  LINES: hi / lo
-// into step lines (hi = the lines, K % 64 == 0; block b of a row goes to
-// line b / 2 at bytes 32 (b % 2) (hi) and 64 + 32 (b % 2) (lo), its scale
-// bytes to bytes b % 2 and 2 + b % 2 of the step's dword in s_hi); else the
-// four arrays of the kernel-level layout.
+// Four lanes per 32-element block (8 elements each; the block maxima by a
+// quad exchange): rows x K/32 x 4 threads.  LINES: hi / lo into step lines
+// (hi = the lines, K % 64 == 0; block b of a row goes to line b / 2 at bytes
+// 32 (b % 2) (hi) and 64 + 32 (b % 2) (lo), its scale bytes to bytes b % 2
+// and 2 + b % 2 of the step's dword in s_hi); else the four arrays of the
+// kernel-level layout.
 template <bool LINES>
 __global__ __launch_bounds__(256) void k_mx8_quant(const uint16_t* __restrict__ x, int64_t n_blocks,
                                                    int K, uint8_t* __restrict__ hi,
                                                    uint8_t* __restrict__ lo,
                                                    uint8_t* __restrict__ s_hi,
                                                    uint8_t* __restrict__ s_lo) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_blocks) return;
+  const int64_t tq = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = (int)(tq & 3);
+  const bool on = (tq >> 2) < n_blocks;  // the same for the 4 lanes of a block
+  const int64_t t = on ? (tq >> 2) : n_blocks - 1;  // past the end: lanes stay for the exchange
   const int nb = K / 32;
   const int64_t r = t / nb, blk = t - r * nb;
-  const int64_t o = r * K + blk * 32;
-  float v[32];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint4 w = *reinterpret_cast<const uint4*>(x + o + 8 * c);
-    unpack8(w, v + 8 * c);
-  }
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const float a = fabsf(v[j]);
-    if (a < INFINITY && a > amax) amax = a;  // NaN compares false
-  }
-  const uint32_t b1 = mx8_scale_byte(amax);
-  uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  float res[32], rmax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const bool fin = fabsf(v[j]) < INFINITY;
-    const uint32_t c = fin ? e4m3_encode_dev(__builtin_amdgcn_ldexpf(v[j], 127 - (int)b1)) : 0x7Fu;
-    res[j] = fin ? __fsub_rn(v[j], __builtin_amdgcn_ldexpf(e4m3_decode_dev(c), (int)b1 - 127))
-                 : 0.0f;
-    rmax = fmaxf(rmax, fabsf(res[j]));
-    qh[j >> 2] |= c << (8 * (j & 3));
-  }
-  const uint32_t b2 = mx8_scale_byte(rmax);
-  uint32_t ql[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-  for (int j = 0; j < 32; ++j)
-    ql[j >> 2] |= e4m3_encode_dev(__builtin_amdgcn_ldexpf(res[j], 127 - (int)b2)) << (8 * (j & 3));
-  uint4 *dh, *dl;
+  const int64_t o = r * K + blk * 32 + 8 * q;
+  float v[8];
+  unpack8(*reinterpret_cast<const uint4*>(x + o), v);
+  uint32_t qh[2], ql[2], b1, b2;
+  mx8_quant8(v, qh, ql, b1, b2);
+  if (!on) return;
+  uint2 *dh, *dl;
   if (LINES) {
     const int64_t line = r * (K / 64) + (blk >> 1);
     const int half = (int)(blk & 1);
-    dh = reinterpret_cast<uint4*>(hi + line * 128 + 32 * half);
-    dl = reinterpret_cast<uint4*>(hi + line * 128 + 64 + 32 * half);
-    s_hi[line * 4 + half] = (uint8_t)b1;
-    s_hi[line * 4 + 2 + half] = (uint8_t)b2;
+    dh = reinterpret_cast<uint2*>(hi + line * 128 + 32 * half + 8 * q);
+    dl = reinterpret_cast<uint2*>(hi + line * 128 + 64 + 32 * half + 8 * q);
+    if (q == 0) {
+      s_hi[line * 4 + half] = (uint8_t)b1;
+      s_hi[line * 4 + 2 + half] = (uint8_t)b2;
+    }
   } else {
-    dh = reinterpret_cast<uint4*>(hi + o);
-    dl = reinterpret_cast<uint4*>(lo + o);
-    s_hi[t] = (uint8_t)b1;
-    s_lo[t] = (uint8_t)b2;
+    dh = reinterpret_cast<uint2*>(hi + o);
+    dl = reinterpret_cast<uint2*>(lo + o);
+    if (q == 0) {
+      s_hi[t] = (uint8_t)b1;
+      s_lo[t] = (uint8_t)b2;
+    }
   }
-  dh[0] = make_uint4(qh[0], qh[1], qh[2], qh[3]);
-  dh[1] = make_uint4(qh[4], qh[5], qh[6], qh[7]);
-  dl[0] = make_uint4(ql[0], ql[1], ql[2], ql[3]);
-  dl[1] = make_uint4(ql[4], ql[5], ql[6], ql[7]);
+  *dh = make_uint2(qh[0], qh[1]);
+  *dl = make_uint2(ql[0], ql[1]);
 }
 
 void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
                       uint8_t* s_hi, uint8_t* s_lo, hipStream_t st) {
   const int64_t n = rows * (K / 32);
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_mx8_quant<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
-                     n, K, hi, lo, s_hi, s_lo);
+  hipLaunchKernelGGL(k_mx8_quant<false>, dim3((unsigned)((4 * n + 255) / 256)), dim3(256), 0, st,
+                     x, n, K, hi, lo, s_hi, s_lo);
 }
 
 void launch_mx8_quant_lines(const uint16_t* x, int64_t rows, int K, uint8_t* q, uint32_t* qs,
                             hipStream_t st) {
   const int64_t n = rows * (K / 32);
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_mx8_quant<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
-                     n, K, q, nullptr, reinterpret_cast<uint8_t*>(qs), nullptr);
+  hipLaunchKernelGGL(k_mx8_quant<true>, dim3((unsigned)((4 * n + 255) / 256)), dim3(256), 0, st,
+                     x, n, K, q, nullptr, reinterpret_cast<uint8_t*>(qs), nullptr);
 }
 
 // Grouped expert GEMM on the scaled matrix instruction.  What bounds this

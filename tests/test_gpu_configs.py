@@ -155,7 +155,7 @@ def fixed_routing_bias(E, layer):
     return (b.view(np.uint32) >> 16).astype(np.uint16)
 
 
-def matrix_vs_oracle(orc, seed, fixed_routing, steps=2, B=16):
+def matrix_vs_oracle(orc, seed, fixed_routing, steps=2, B=16, mode=ne.DECODE_MATRIX):
     torch_cuda()
     cfg = ne.config_preset("gpt-oss-20b", max_seq=32, max_batch=B)
     rng = np.random.default_rng(seed)
@@ -172,7 +172,7 @@ def matrix_vs_oracle(orc, seed, fixed_routing, steps=2, B=16):
             eng.load_tensor(p + "bias", bias)
             m.set_tensor(layer, orc.T_ROUTER_W, zeros)
             m.set_tensor(layer, orc.T_ROUTER_B, bias)
-    eng.set_decode_mode(ne.DECODE_MATRIX)
+    eng.set_decode_mode(mode)
     eng.prefill(prompt)
     m.step(prompt[:, 0], want_logits=False)
     ids = prompt[:, 1]
@@ -244,3 +244,13 @@ def test_config3_batch16_matrix_vs_oracle_free_routing(orc):
     reorder error on these inputs."""
     rels = matrix_vs_oracle(orc, 7, fixed_routing=False)
     check_against_conditioning(rels, "free_24", per_step=False)
+
+
+def test_config3_batch16_matrix_mx8_vs_oracle_fixed_routing(orc):
+    """NEON_DECODE_MATRIX_MX8 (expert GEMMs on the scaled fp8 x fp4
+    instruction) at the full 24-layer 20b shape, batch 16, routing fixed:
+    the same bar as the bf16 matrix steps, twice the oracle's own reorder
+    error (the two-term MXFP8 inputs stay within half a bf16 unit of each
+    block's maximum, an error of the size of one more bf16 rounding)."""
+    rels = matrix_vs_oracle(orc, 7, fixed_routing=True, mode=ne.DECODE_MATRIX_MX8)
+    check_against_conditioning(rels, "fixed_24")

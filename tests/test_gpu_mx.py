@@ -68,14 +68,14 @@ def run(cfg, seed, prompt, n_steps, mode, fixed_routing=False):
     return first, toks
 
 
-def compare(cfg, seed, B, plen, n_steps, fixed_routing=False):
+def compare(cfg, seed, B, plen, n_steps, fixed_routing=False, mode=ne.DECODE_MATRIX):
     torch_cuda()
     say(f"decode modes layers={cfg.n_layers} hidden={cfg.hidden} E={cfg.n_experts} B={B} "
-        f"prompt={plen} fixed_routing={fixed_routing}")
+        f"prompt={plen} fixed_routing={fixed_routing} mode={mode}")
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, cfg.vocab, size=(B, plen)).tolist()
     lg_e, tok_e = run(cfg, seed, prompt, n_steps, ne.DECODE_EXACT, fixed_routing)
-    lg_m, tok_m = run(cfg, seed, prompt, n_steps, ne.DECODE_MATRIX, fixed_routing)
+    lg_m, tok_m = run(cfg, seed, prompt, n_steps, mode, fixed_routing)
     rel = np.abs(lg_m - lg_e).max() / np.abs(lg_e).max()
     top2 = np.sort(lg_e, axis=1)[:, -2:]
     margin = (top2[:, 1] - top2[:, 0]) / np.abs(lg_e).max(axis=1)
@@ -118,20 +118,20 @@ def test_small_model_128_experts_matrix():
     routed_alike_compare(cfg, 5, 16, 12, 12)
 
 
-def routed_alike_compare(cfg, seed, B, plen, min_same):
+def routed_alike_compare(cfg, seed, B, plen, min_same, mode=ne.DECODE_MATRIX):
     """First-step logits of both modes for rows whose experts agree (the
     step's moe_idx is read back); returns (rows alike, worst rel error)."""
     torch_cuda()
     prompt = np.random.default_rng(seed).integers(0, cfg.vocab, size=(B, plen)).tolist()
     got = {}
-    for mode in (ne.DECODE_EXACT, ne.DECODE_MATRIX):
+    for m in (ne.DECODE_EXACT, mode):
         eng = ne.Engine(cfg)
         eng.init_random(seed)
-        eng.set_decode_mode(mode)
+        eng.set_decode_mode(m)
         eng.prefill(prompt)
-        got[mode] = (eng.read_logits(), eng.read_activation("moe_idx"))
+        got[m] = (eng.read_logits(), eng.read_activation("moe_idx"))
         eng.close()
-    (lg_e, id_e), (lg_m, id_m) = got[ne.DECODE_EXACT], got[ne.DECODE_MATRIX]
+    (lg_e, id_e), (lg_m, id_m) = got[ne.DECODE_EXACT], got[mode]
     same = (np.sort(id_e, axis=1) == np.sort(id_m, axis=1)).all(axis=1)
     rel = np.abs(lg_m - lg_e).max(axis=1) / np.abs(lg_e).max(axis=1)
     say(f"  rows routed alike {same.sum()}/{B}; worst rel error among them {rel[same].max():.3e}")
@@ -161,6 +161,35 @@ def test_gpt_oss_20b_width_matrix_steps():
     compare(cfg, 1, 16, 24, 16)
     cfg = ne.config_preset("gpt-oss-20b", n_layers=4, max_seq=64, max_batch=16)
     compare(cfg, 1, 16, 24, 16, fixed_routing=True)
+
+
+# ---- the expert GEMMs on the scaled fp8 x fp4 instruction (DECODE_MATRIX_MX8)
+@pytest.mark.parametrize("B", [2, 16, 33, 64])
+def test_small_model_matrix_mx8_steps(B):
+    """Each expert input carried as two MXFP8 terms (within half a bf16 unit
+    of each 32-block's maximum): the same 2e-2 bar against the exact steps."""
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=B))
+    compare(cfg, 3, B, 20, 24, mode=ne.DECODE_MATRIX_MX8)
+
+
+def test_small_model_matrix_mx8_long_context():
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_seq=1024, max_batch=4))
+    compare(cfg, 6, 4, 600, 8, mode=ne.DECODE_MATRIX_MX8)
+
+
+def test_gpt_oss_20b_width_matrix_mx8_steps():
+    """Full 20b width, 16 sequences: one layer with free routing, four with the
+    routing fixed (the reasons of test_gpt_oss_20b_width_matrix_steps)."""
+    cfg = ne.config_preset("gpt-oss-20b", n_layers=1, max_seq=64, max_batch=16)
+    compare(cfg, 1, 16, 24, 16, mode=ne.DECODE_MATRIX_MX8)
+    cfg = ne.config_preset("gpt-oss-20b", n_layers=4, max_seq=64, max_batch=16)
+    compare(cfg, 1, 16, 24, 16, fixed_routing=True, mode=ne.DECODE_MATRIX_MX8)
+
+
+def test_gpt_oss_120b_width_matrix_mx8_one_layer():
+    cfg = ne.config_preset("gpt-oss-120b", n_layers=1, max_seq=64, max_batch=16)
+    say("matrix mode with MXFP8 experts, 120b width, one layer, 16 rows")
+    routed_alike_compare(cfg, 8, 16, 10, 12, mode=ne.DECODE_MATRIX_MX8)
 
 
 def test_decode_mode_validation():
