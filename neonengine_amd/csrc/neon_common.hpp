@@ -107,6 +107,16 @@ __device__ __forceinline__ float e8m0_scale(float v, uint32_t s) {
   return s == 0xFFu ? __builtin_nanf("") : r;
 }
 
+// 16 bytes written by other blocks of the same launch: two 8-byte agent-scope
+// loads, served at the device's coherence point rather than from this XCD's
+// L2 (which may hold an older copy or none).
+__device__ __forceinline__ uint4 load_agent16(const uint16_t* p) {
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
+
 // Sets status bits in the caller's status word (a vector-memory atomic).
 __device__ __forceinline__ void flag_dev_err(int32_t* err, int32_t bits) {
   if (err != nullptr) atomicOr(err, bits);

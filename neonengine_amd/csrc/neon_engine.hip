@@ -78,6 +78,7 @@ struct neon_ctx {
   float* moe_score = nullptr;
   float* router_lg = nullptr;
   float *attn_po = nullptr, *attn_pml = nullptr;  // split partials
+  int32_t* attn_arrive = nullptr;  // [Br][Hkv] arrival counters of the split kernel
   float* logits = nullptr;
   float* lm_part_val = nullptr;
   int32_t* lm_part_idx = nullptr;
@@ -115,6 +116,17 @@ struct neon_ctx {
   // measured faster on MI355X (the in-kernel wait plus every block fetching
   // act past its L2 cost more than the kernel boundary they replace)
   bool fused_moe = getenv("NEON_MOE_FUSED") && getenv("NEON_MOE_FUSED")[0] == '1';
+  // follow-up work run by the producing launch (same bits, one launch fewer):
+  // the attention merge by the last split block of each kv head (fuse_merge,
+  // on by default: 1.2197 against 1.2248 ms per 20b step), and at batch 1 the
+  // router logits by tail blocks of the O projection (fuse_router, off by
+  // default: 1.2595 ms, its arrival round trip and agent-scope reads cost
+  // more than the launch they save).  NEON_FUSE_TAILS: unset or "a" the
+  // merge only, "1" both, "r" the router only, "0" neither
+  const char* fuse_env = getenv("NEON_FUSE_TAILS");
+  bool fuse_merge = !fuse_env || fuse_env[0] == '1' || fuse_env[0] == 'a';
+  bool fuse_router = fuse_env && (fuse_env[0] == '1' || fuse_env[0] == 'r');
+  int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -398,6 +410,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_rlg = take(Br * c.n_experts * 4),
                o_apo = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * c.head_dim * 4),
                o_apml = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
+               o_aarr = take(Br * (size_t)c.n_kv_heads * kAttnArriveStride * 4),
+               o_orarr = take((kMoeSyncWords + 1) * kMoeSyncStride * 4),
                o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
                o_samp = take(Bm * (size_t)c.vocab * 4),
                o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
@@ -424,6 +438,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->moe_score = (float*)(W + o_sc);
   ctx->router_lg = (float*)(W + o_rlg);
   ctx->attn_po = (float*)(W + o_apo); ctx->attn_pml = (float*)(W + o_apml);
+  ctx->attn_arrive = (int32_t*)(W + o_aarr);  // zeroed above; every launch leaves it at 0
+  ctx->or_arrive = (int32_t*)(W + o_orarr);    // likewise
   ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
@@ -657,6 +673,7 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     AttnArgs a;
     a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = pos;
     a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml; a.seq = seq;
+    a.arrive = ctx->fuse_merge ? ctx->attn_arrive : nullptr;  // the last split block merges
     a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
     a.window = sliding ? c.sliding_window : 0;
@@ -666,7 +683,6 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     o.mode = 1; o.W = w.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
     o.N = H; o.K = c.n_heads * D; o.B = B;
     o.nblk = gemv_default_grid(o.N, o.mode);
-    launch_gemv_step(o, B, st);
     // batch >= 2: the top-k runs once per row before the experts, which then
     // group the rows by expert (each used expert's weights read once);
     // batch 1: the expert kernels choose from the logits themselves
@@ -680,7 +696,13 @@ static void enqueue_rows(neon_ctx* ctx, int B, const int32_t* pos, const int32_t
     // router zeroes first
     int32_t* sync = B == 1 && ctx->fused_moe ? ctx->moe_sync + (size_t)l * kMoeSyncInts : nullptr;
     r.zero = sync; r.zero_n = sync ? kMoeSyncZero : 0;
-    launch_router(r, st);
+    r.arrive = ctx->or_arrive; r.err = ctx->dev_err;
+    if (ctx->fuse_router && o_router_supported(o, r)) {
+      launch_gemv_o_router(o, r, st);  // batch 1: O, then the router in the same launch
+    } else {
+      launch_gemv_step(o, B, st);
+      launch_router(r, st);
+    }
     MoeArgs m;
     m.gu_codes = w.gu_codes; m.gu_scales = w.gu_scales; m.gu_bias = w.gu_bias;
     m.dn_codes = w.dn_codes; m.dn_scales = w.dn_scales; m.dn_bias = w.dn_bias;
@@ -1599,15 +1621,22 @@ extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cac
   hipStream_t st = S(stream);
   const int nsplit = attn_splits(T_max, window);
   const size_t np = (size_t)B * Hq * nsplit;
-  // split partials: o [np][D], then (m, l) [np][2]; one split finishes in
-  // the split kernel and needs none
+  // split partials: o [np][D], then (m, l) [np][2], then the arrival
+  // counters [B][Hkv] (zeroed here; the last split block of each kv head
+  // merges); one split finishes in the split kernel and needs none
+  const size_t n_arr = (size_t)B * Hkv * kAttnArriveStride;
   float* scratch = nullptr;
-  if (nsplit > 1 && hipMallocAsync((void**)&scratch, np * (D + 2) * 4, st) != hipSuccess)
+  if (nsplit > 1 && hipMallocAsync((void**)&scratch, (np * (D + 2) + n_arr) * 4, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
+  int32_t* arrive = nsplit > 1 ? reinterpret_cast<int32_t*>(scratch + np * (D + 2)) : nullptr;
+  if (arrive != nullptr && hipMemsetAsync(arrive, 0, n_arr * 4, st) != hipSuccess) {
+    (void)hipFreeAsync(scratch, st);
+    KFAIL(NEON_EHIP, "neon_attn_decode: clearing the arrival counters failed");
+  }
   AttnArgs a;
   a.q = q; a.kc = k_cache; a.vc = v_cache;
   a.sinks = sinks; a.pos = pos; a.out = out;
-  a.part_o = scratch; a.part_ml = scratch + np * D; a.seq = nullptr;
+  a.part_o = scratch; a.part_ml = scratch + np * D; a.seq = nullptr; a.arrive = arrive;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.key_mask = -1; a.window = window;
   a.S = nsplit; a.q_stride = Hq * D;
   launch_attn(a, st);

@@ -113,9 +113,18 @@ struct RouterArgs {
   // with xn_out: its two-term MXFP8 image (hi, lo [B][H], scales [B][H/32]),
   // written by the same wave (NULL: none)
   uint8_t *xq_hi = nullptr, *xq_lo = nullptr, *xs_hi = nullptr, *xs_lo = nullptr;
+  // launch_gemv_o_router only: kMoeSyncWords + 1 words kMoeSyncStride ints
+  // apart (0 at launch, left at 0) and the device status word
+  int32_t* arrive = nullptr;
+  int32_t* err = nullptr;
 };
 // router logits, then (when a.idx) the top-k / softmax
 void launch_router(const RouterArgs& a, hipStream_t st);
+// O projection + residual (o, mode 1) and the router logits of its output (r)
+// in one launch, batch 1; bit-identical to launch_gemv_bf16(o) then
+// launch_router(r)
+bool o_router_supported(const GemvArgs& o, const RouterArgs& r);
+void launch_gemv_o_router(const GemvArgs& o, const RouterArgs& r, hipStream_t st);
 
 // Status bits a kernel sets (vector atomicOr) in the caller's status word
 // when its input breaks a precondition it can only see on the device.
@@ -241,7 +250,13 @@ struct AttnArgs {
   // key j sits in cache row j & key_mask: -1 for a cache of every position,
   // rows - 1 for a power-of-two ring that holds the last `rows` positions
   int key_mask;
+  // arrival counters [B][Hkv] (stride kAttnArriveStride ints, 0 at launch and
+  // left at 0): with S > 1 the split kernel's last block per (row, kv head)
+  // merges; NULL: a separate merge kernel (launch_attn only)
+  int32_t* arrive = nullptr;
 };
+// ints between consecutive arrival counters (one 256-byte line each)
+constexpr int kAttnArriveStride = 64;
 // decode attention of the matrix-core steps (same partials and merge as launch_attn)
 void launch_mx_attn(const AttnArgs& a, hipStream_t st);
 void launch_attn_merge(const AttnArgs& a, hipStream_t st);

@@ -722,7 +722,7 @@ constexpr int log2_rows() { return R == 4 ? 2 : (R == 2 ? 1 : 0); }
 // One group of R rows.  FIRST: the wave's first group, which also finishes
 // the input (and its RMSNorm) from the raw loads issued before the rows, so
 // that work overlaps the row loads; later groups reuse xr.
-template <int P, int MODE, bool NORM, bool FIRST, int R>
+template <int P, int MODE, bool NORM, bool FIRST, int R, bool AGENT_Y = false>
 __device__ __forceinline__ void gemv_bf16_group(
     int g, const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
     uint16_t bias_first, float (&xr)[P][8], const XBf16Raw<P>& xraw, float eps,
@@ -791,8 +791,15 @@ __device__ __forceinline__ void gemv_bf16_group(
     } else if ((lane & kLead) == 0) {
       const float v = bias ? __fadd_rn(tot, bf2f(bias_b)) : tot;
       const size_t o = (size_t)b * N + r;
-      if (MODE == MODE_STORE) y[o] = f2bf(v);
-      else y[o] = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
+      if (MODE == MODE_STORE) {
+        y[o] = f2bf(v);
+      } else {
+        const uint16_t yo = f2bf(__fadd_rn(bf2f(y[o]), bf2f(f2bf(v))));
+        if (AGENT_Y)  // read by other blocks of this launch
+          __hip_atomic_store(y + o, yo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          y[o] = yo;
+      }
     }
   }
 }
@@ -1729,6 +1736,160 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
                        a.score, a.E, a.k);
 }
 
+// ===========================================================================
+// O projection + residual, then the router logits, in one launch (batch 1).
+// Blocks 0 .. nblk - 1 are k_gemv_bf16<P, MODE_RESID, false, 1>'s blocks,
+// except that their residual stores are agent-scope (they complete at the
+// device's coherence point) and each block then arrives on arr[0].  The
+// ceil(E / 4) blocks after them are k_router_logits' waves, one expert each:
+// every input that does not depend on h (bias, norm weights, router row) is
+// loaded first, then wave 0 polls arr[0] until all nblk blocks have arrived,
+// then h is read at agent scope and the logit formed with exactly
+// k_router_logits' operations (same norm, same dot), so the bits match the
+// two-launch form.  The O blocks never wait and the whole grid is far below
+// the device's capacity, so the wait always ends; it is bounded anyway
+// (kDevErrSyncTimeout).  The O blocks arrive on kMoeSyncWords shards (block i
+// on shard i % kMoeSyncWords, each on its own 256-byte line: hundreds of
+// atomics on one address queue behind each other), which the polling wave
+// sums.  Each router block then counts itself on the word after the shards;
+// the last one sets every word back to 0, ready for the next launch (they
+// must be 0 at launch).
+// ===========================================================================
+__device__ __forceinline__ int wave_isum(int v) {
+  v += xor_lane_i<32>(v);
+  v += xor_lane_i<16>(v);
+  v += xor_lane_i<8>(v);
+  v += xor_lane_i<4>(v);
+  v += xor_lane_i<2>(v);
+  v += xor_lane_i<1>(v);
+  return v;
+}
+
+template <int P, int PR>
+__global__ __launch_bounds__(256) void k_gemv_o_router(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ bias,
+    const uint16_t* __restrict__ x, uint16_t* y, int N, int K, int nblk,
+    const uint16_t* __restrict__ nw, float eps, uint16_t* __restrict__ xn_out,
+    const uint16_t* __restrict__ Wr, const uint16_t* __restrict__ br, float* __restrict__ lg_out,
+    int E, int32_t* __restrict__ zero, int zero_n, int32_t* arr, int32_t* __restrict__ err,
+    int spin_limit) {
+  __shared__ int32_t wait_ok;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if ((int)blockIdx.x < nblk) {
+    // ---- O + residual (k_gemv_bf16's block body, batch row 0) ----
+    const int ngroups = N;  // one row per wave group
+    const int gstride = nblk * 4;
+    const int g0 = blockIdx.x * 4 + wave;
+    const uint16_t bias_first = (bias != nullptr ? bias : W)[min(g0, N - 1)];
+    float xr[P][8];
+    XBf16Raw<P> xraw;
+    wave_x_bf16_issue<P, false>(xraw, x, nullptr, K, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    float best_v = -INFINITY;
+    int32_t best_i = 0;
+    RopeArgs rp{};
+    if (g0 < ngroups) {
+      gemv_bf16_group<P, MODE_RESID, false, true, 1, true>(g0, W, bias, bias_first, xr, xraw,
+                                                           0.0f, y, nullptr, 0, N, K, lane,
+                                                           best_v, best_i, rp, 0, 0);
+      for (int g = g0 + gstride; g < ngroups; g += gstride)
+        gemv_bf16_group<P, MODE_RESID, false, false, 1, true>(g, W, bias, 0, xr, xraw, 0.0f, y,
+                                                              nullptr, 0, N, K, lane, best_v,
+                                                              best_i, rp, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's h stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(arr + (size_t)(blockIdx.x % kMoeSyncWords) * kMoeSyncStride, 1,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  // ---- router logits: expert e per wave ----
+  const int e = ((int)blockIdx.x - nblk) * 4 + wave;
+  const int ec = min(e, E - 1);
+  if (e == 0 && lane < zero_n) zero[(size_t)lane * kMoeSyncStride] = 0;
+  const int H = N, U = H / 8;
+  const uint16_t bias_e = br[ec];
+  XBf16Raw<PR> xraw;
+  {
+    const uint4* wv = reinterpret_cast<const uint4*>(nw);
+#pragma unroll
+    for (int p = 0; p < PR; ++p) xraw.w[p] = wv[min(lane + 64 * p, U - 1)];
+  }
+  uint4 w[PR];
+  bf16_load_row<PR>(w, Wr + (size_t)ec * H, U, lane);
+  int32_t* done_w = arr + (size_t)kMoeSyncWords * kMoeSyncStride;
+  if (wave == 0) {
+    const int32_t* mine = arr + (size_t)min(lane, kMoeSyncWords - 1) * kMoeSyncStride;
+    bool ok = false;
+    for (int it = 0; it < spin_limit; ++it) {
+      const int v = __hip_atomic_load(mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (wave_isum(lane < kMoeSyncWords ? v : 0) >= nblk) {  // uniform
+        ok = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) wait_ok = ok;
+  }
+  __syncthreads();
+  int32_t done = 0;
+  if (threadIdx.x == 0) {
+    if (!wait_ok) flag_dev_err(err, kDevErrSyncTimeout);
+    done = __hip_atomic_fetch_add(done_w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int p = 0; p < PR; ++p) xraw.x[p] = load_agent16(y + 8 * (size_t)min(lane + 64 * p, U - 1));
+  float xr[PR][8];
+  wave_x_bf16_finish<PR, true>(xr, xraw, eps, H, lane, e == 0 ? xn_out : nullptr);
+  const float acc = wave_sum(bf16_row_partial<PR>(w, xr, U, lane));
+  if (e < E && lane == 0) lg_out[e] = __fadd_rn(acc, bf2f(bias_e));
+  // every router block has seen all arrivals: ready for the next launch
+  if (wave == 0 && __builtin_amdgcn_readfirstlane(done) == (int32_t)gridDim.x - nblk - 1 &&
+      lane <= kMoeSyncWords)
+    __hip_atomic_store(arr + (size_t)lane * kMoeSyncStride, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+bool o_router_supported(const GemvArgs& o, const RouterArgs& r) {
+  return o.B == 1 && r.B == 1 && o.mode == MODE_RESID && o.norm_w == nullptr &&
+         r.norm_w != nullptr && r.idx == nullptr && r.xq_hi == nullptr && r.x == o.y &&
+         r.H == o.N && o.N % 8 == 0 && o.K % 8 == 0 && r.E >= 1 && r.arrive != nullptr &&
+         (o.K / 8 + 63) / 64 <= 8 && (r.H / 8 + 63) / 64 <= 8;
+}
+
+void launch_gemv_o_router(const GemvArgs& o, const RouterArgs& r, hipStream_t st) {
+  const int P = (o.K / 8 + 63) / 64, PR = (r.H / 8 + 63) / 64;
+  const int grid = o.nblk + (r.E + 3) / 4;
+#define OR_LAUNCH(PP, QQ)                                                                 \
+  hipLaunchKernelGGL((k_gemv_o_router<PP, QQ>), dim3(grid), dim3(256), 0, st, o.W, o.bias, \
+                     o.x, o.y, o.N, o.K, o.nblk, r.norm_w, r.eps, r.xn_out, r.W, r.bias,  \
+                     r.lg_out, r.E, r.zero, r.zero_n, r.arrive, r.err, kMoeSpinLimit)
+#define OR_P(PP)                                       \
+  switch (PR) {                                        \
+    case 1: OR_LAUNCH(PP, 1); break;                   \
+    case 2: OR_LAUNCH(PP, 2); break;                   \
+    case 3: OR_LAUNCH(PP, 3); break;                   \
+    case 4: OR_LAUNCH(PP, 4); break;                   \
+    case 5: OR_LAUNCH(PP, 5); break;                   \
+    case 6: OR_LAUNCH(PP, 6); break;                   \
+    case 7: OR_LAUNCH(PP, 7); break;                   \
+    default: OR_LAUNCH(PP, 8); break;                  \
+  }
+  switch (P) {
+    case 1: OR_P(1); break;
+    case 2: OR_P(2); break;
+    case 3: OR_P(3); break;
+    case 4: OR_P(4); break;
+    case 5: OR_P(5); break;
+    case 6: OR_P(6); break;
+    case 7: OR_P(7); break;
+    default: OR_P(8); break;
+  }
+#undef OR_P
+#undef OR_LAUNCH
+}
+
 // Row b's experts into the wave's LDS slice t: chosen from the router logits
 // when lg is given, else copied from idx (and score, when WEIGHTS).  The
 // loads (moe_route_issue) are separate from the choice (moe_route_finish) so
@@ -2200,15 +2361,6 @@ __global__ __launch_bounds__(256) void k_moe_down_bt(
 // every block that others wait for is running.  The counters must be 0 at
 // launch (the router kernel before it zeroes them).
 // ===========================================================================
-// 16 bytes written by other blocks of this launch: two 8-byte agent-scope
-// loads, served at the coherence point rather than from this XCD's L2.
-__device__ __forceinline__ uint4 load_agent16(const uint16_t* p) {
-  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
-}
-
 // How the down phase reads act after the grid-wide wait: false = agent-scope
 // loads (each block fetches its own copy past the L2; measured 3.2 us after
 // the wait at the 20b shape); true = one agent-scope acquire (L1/L2
@@ -2235,16 +2387,6 @@ __device__ __forceinline__ void x_fp4_issue_agent(uint4 (&raw)[P][4],
       raw[p][q] = kActAcquire ? reinterpret_cast<const uint4*>(x)[u * 4 + q]
                               : load_agent16(x + (size_t)(u * 4 + q) * 8);
   }
-}
-
-__device__ __forceinline__ int wave_isum(int v) {
-  v += xor_lane_i<32>(v);
-  v += xor_lane_i<16>(v);
-  v += xor_lane_i<8>(v);
-  v += xor_lane_i<4>(v);
-  v += xor_lane_i<2>(v);
-  v += xor_lane_i<1>(v);
-  return v;
 }
 
 // Grid-wide wait of the one-launch kernels.  Layout of the sync words (all
@@ -2722,10 +2864,22 @@ constexpr int kMaxSplits = 32;
     }                                                                           \
   } while (0)
 
+// Splits' partials written by other blocks of the same launch (AGENT):
+// agent-scope loads, served at the device's coherence point rather than from
+// this XCD's L2, which may hold none of them.
+template <bool AGENT>
+__device__ __forceinline__ float attn_part_load(const float* p) {
+  if (AGENT)
+    return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p),
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  return *p;
+}
+
 // One wave merges the S partials of head h (rows pi0 .. pi0 + S - 1 of
 // part_o / part_ml) with the sink, lane = output dim.  Every load goes out
 // first; each lane t < S computes its split's factor f_t = exp(m_t - M) (0 for
 // an empty split), then den and acc take the splits in order with fmaf.
+template <bool AGENT>
 __device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o,
                                                 const float* __restrict__ part_ml,
                                                 size_t pi0, int S, float sk, int lane,
@@ -2733,9 +2887,9 @@ __device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o
   float ov[kMaxSplits];
 #pragma unroll
   for (int t = 0; t < kMaxSplits; ++t)
-    ov[t] = t < S ? part_o[(pi0 + t) * kD + lane] : 0.0f;
-  const float mt_l = lane < S ? part_ml[(pi0 + lane) * 2] : -INFINITY;
-  const float lt_l = lane < S ? part_ml[(pi0 + lane) * 2 + 1] : 0.0f;
+    ov[t] = t < S ? attn_part_load<AGENT>(part_o + (pi0 + t) * kD + lane) : 0.0f;
+  const float mt_l = lane < S ? attn_part_load<AGENT>(part_ml + (pi0 + lane) * 2) : -INFINITY;
+  const float lt_l = lane < S ? attn_part_load<AGENT>(part_ml + (pi0 + lane) * 2 + 1) : 0.0f;
   const float M = fmaxf(sk, wave_max(mt_l));
   const float f_l = (mt_l == -INFINITY) ? 0.0f : neon_expf(__fsub_rn(mt_l, M));
   float den = neon_expf(__fsub_rn(sk, M));
@@ -2757,11 +2911,12 @@ __global__ __launch_bounds__(512) void k_attn_split(
     float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out,
     const int32_t* __restrict__ seq, int Hq, int Hkv, int G, int HB, int T_max, int key_mask,
-    int window, int S, int q_stride) {
+    int window, int S, int q_stride, int32_t* __restrict__ arrive) {
   __shared__ __align__(16) uint4 kt[2][64 * 8];  // [key][word], words rotated by key
   __shared__ __align__(16) uint4 vt[2][64 * 8];  // [key][word]
   __shared__ __align__(16) float qs[8][kD];
   __shared__ float ps[8][64];
+  __shared__ int merge_here;
   // blockDim = 64 max(HB, 4): waves w >= HB only help stage the tiles
   const int nt = blockDim.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -2876,7 +3031,9 @@ __global__ __launch_bounds__(512) void k_attn_split(
       ATTN_STORE_WORD(nk1, nv1, tid + nt, buf);
     }
   }
-  if (!active) return;
+  // with `arrive` every wave of the block reaches the arrival barrier below,
+  // so the helper waves stay until then
+  if (!active && (S == 1 || arrive == nullptr)) return;
   // reduce o over the 8 key groups (lane bits 3..5)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -2907,12 +3064,48 @@ __global__ __launch_bounds__(512) void k_attn_split(
     return;
   }
   const size_t pi = ((size_t)b * Hq + h) * S + s;
-  if (kg == 0) {
-    float4* po = reinterpret_cast<float4*>(part_o + pi * kD + dq * 8);
-    po[0] = make_float4(o[0], o[1], o[2], o[3]);
-    po[1] = make_float4(o[4], o[5], o[6], o[7]);
+  if (arrive == nullptr) {  // the partials go to k_attn_merge
+    if (kg == 0) {
+      float4* po = reinterpret_cast<float4*>(part_o + pi * kD + dq * 8);
+      po[0] = make_float4(o[0], o[1], o[2], o[3]);
+      po[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (lane == 0) { part_ml[pi * 2] = m; part_ml[pi * 2 + 1] = l; }
+    return;
   }
-  if (lane == 0) { part_ml[pi * 2] = m; part_ml[pi * 2 + 1] = l; }
+  // Merge in this launch: the partials are stored at agent scope (they
+  // complete at the device's coherence point, past this XCD's L2), each
+  // block arrives on its (row, kv head) counter once its stores are done,
+  // and the block that arrives last merges the G heads of that kv head
+  // (attn_merge_head, reading the partials at agent scope) and sets the
+  // counter back to 0 for the next launch.  No block waits for another.
+  if (active) {
+    auto pack = [](float a, float c) {
+      return (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(c) << 32);
+    };
+    if (kg == 0) {
+      uint64_t* po = reinterpret_cast<uint64_t*>(part_o + pi * kD + dq * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        __hip_atomic_store(po + e, pack(o[2 * e], o[2 * e + 1]), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (lane == 0)
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(part_ml + pi * 2), pack(m, l),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores have completed
+  __syncthreads();
+  int32_t* ctr = arrive + ((size_t)b * Hkv + g) * kAttnArriveStride;
+  if (tid == 0)
+    merge_here = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 S - 1;
+  __syncthreads();
+  if (!merge_here) return;
+  if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (active)
+    attn_merge_head<true>(part_o, part_ml, ((size_t)b * Hq + h) * S, S, bf2f(sink_raw), lane,
+                          out + ((size_t)b * Hq + h) * kD);
 }
 
 __global__ __launch_bounds__(64) void k_attn_merge(
@@ -2920,8 +3113,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq,
     int S) {
   const int h = blockIdx.x, b = blockIdx.y;
-  attn_merge_head(part_o, part_ml, ((size_t)b * Hq + h) * S, S, bf2f(sinks[h]), threadIdx.x,
-                  out + ((size_t)b * Hq + h) * kD);
+  attn_merge_head<false>(part_o, part_ml, ((size_t)b * Hq + h) * S, S, bf2f(sinks[h]),
+                         threadIdx.x, out + ((size_t)b * Hq + h) * kD);
 }
 
 #undef ATTN_LOAD_WORD
@@ -2940,8 +3133,11 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(k_attn_split, dim3(a.Hkv * (G / HB) * a.S, a.B),
                      dim3(64 * (HB < 4 ? 4 : HB)), 0, st, a.q, a.kc, a.vc, a.pos,
                      a.part_o, a.part_ml, a.sinks, a.out, a.seq, a.Hq, a.Hkv, G, HB,
-                     a.T_max, a.key_mask, a.window, a.S, a.q_stride);
-  if (a.S > 1)  // one split finishes in the split kernel
+                     a.T_max, a.key_mask, a.window, a.S, a.q_stride,
+                     a.S > 1 ? a.arrive : nullptr);
+  // one split finishes in the split kernel; several merge there too when the
+  // arrival counters are given, else in k_attn_merge
+  if (a.S > 1 && a.arrive == nullptr)
     hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
                        a.part_ml, a.sinks, a.out, a.Hq, a.S);
 }

@@ -231,6 +231,19 @@ def test_gpt_oss_20b_greedy_one_launch_experts(orc, monkeypatch):
     assert same.all()
 
 
+@pytest.mark.parametrize("fuse", ["1", "0"])
+def test_gpt_oss_20b_greedy_tail_fusions(orc, monkeypatch, fuse):
+    """The launch forms of the step's follow-up work give the oracle's bits:
+    NEON_FUSE_TAILS=1 runs the router logits in tail blocks of the O
+    projection (opt-in) as well as the attention merge in the split kernel
+    (the default); 0 runs both as separate launches.  max_seq 320 gives the
+    full layers 5 key splits, so the merge runs."""
+    monkeypatch.setenv("NEON_FUSE_TAILS", fuse)
+    cfg, ocfg = pair(orc, max_seq=320)
+    same, e1, e2 = run_parity(orc, cfg, ocfg, 6, [[5, 2002, 30003, 200002]], 40)
+    assert same.all()
+
+
 def test_engine_errors_on_gpu(orc):
     torch_cuda()
     cfg, _ = pair(orc, **dict(SMALL, max_seq=16))
