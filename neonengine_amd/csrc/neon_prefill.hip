@@ -814,6 +814,73 @@ __device__ __forceinline__ pf_bf16x8 pf_as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(pf_bf16x8, v);
 }
 
+// Scores of one tile for the 16 query columns (qt, j) of this lane: the
+// softmax state m (log2 domain), l, o, and the P^T fragments (hi, lo) for
+// V^T P^T.  s2 = (q.k) * log2(e) / 8 in one rounding; p = 2^(s2 - m).
+// MASK: the tile crosses the causal diagonal or the window's lower edge, so
+// each key is checked; other tiles are valid for every query of the block.
+template <bool MASK>
+__device__ __forceinline__ void attn_prefill_softmax(
+    const pf_f32x4 (&sacc)[4][4], int qt, int t0, int j0, int j, int g, int window,
+    float& m, float& l, pf_f32x4 (&o)[4], uint4 (&phi)[2], uint4 (&plo)[2]) {
+  constexpr float kScale = 0.125f * 1.44269504088896340736f;  // 1/sqrt(64) * log2(e)
+  const int t = t0 + 16 * qt + j;
+  const int lo_t = window > 0 ? max(0, t - window + 1) : 0;
+  float sv[4][4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = __fmul_rn(sacc[kt][qt][r], kScale);
+      if (MASK) {
+        const int key = j0 + 16 * kt + 4 * g + r;
+        v = (key >= lo_t && key <= t) ? v : -INFINITY;
+      }
+      sv[kt][r] = v;
+      mx = fmaxf(mx, v);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float mt = fmaxf(m, mx);
+  // no valid key yet (a window's first tile): every p and the rescale are 0
+  const float mb = mt == -INFINITY ? 0.0f : mt;
+  const float sc = __builtin_amdgcn_exp2f(m - mb);  // 2^(-inf) = 0
+  l *= sc;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    o[dt][0] *= sc; o[dt][1] *= sc; o[dt][2] *= sc; o[dt][3] *= sc;
+  }
+  m = mt;
+  float pv[4][4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pv[kt][r] = __builtin_amdgcn_exp2f(sv[kt][r] - mb);  // masked: 2^(-inf) = 0
+      l += pv[kt][r];
+    }
+  // P^T as bf16 hi + lo, two values per conversion
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const float a0 = pv[2 * pp + half][2 * r2], a1 = pv[2 * pp + half][2 * r2 + 1];
+        const uint32_t hv = pack_bf2(a0, a1);
+        const float h0 = __uint_as_float(hv << 16), h1 = __uint_as_float(hv & 0xFFFF0000u);
+        hw[2 * half + r2] = hv;
+        lw[2 * half + r2] = pack_bf2(a0 - h0, a1 - h1);
+      }
+    phi[pp] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    plo[pp] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+}
+
+// NWD = 512 / blockDim: the 16-byte words of a K (and a V) tile per thread.
+template <int NWD>
 __global__ __launch_bounds__(512) void k_attn_prefill(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const uint16_t* __restrict__ sinks,
@@ -840,28 +907,44 @@ __global__ __launch_bounds__(512) void k_attn_prefill(
   for (int qt = 0; qt < 4; ++qt)
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[qt][dt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  float m[4], l[4];  // per query column (qt, j); l is this lane's partial sum
+  float m[4], l[4];  // per query column (qt, j), log2 domain; l is this lane's partial sum
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) { m[qt] = -INFINITY; l[qt] = 0.0f; }
   const int hi_blk = min(M - 1, t0 + 63);
   const int lo_blk = window > 0 ? max(0, t0 - window + 1) : 0;
   const uint16_t* kg = kc + (size_t)gkv * T_max * 64;
   const uint16_t* vg = vc + (size_t)gkv * T_max * 64;
-  for (int j0 = (lo_blk / 64) * 64; j0 <= hi_blk; j0 += 64) {
+  // a tile is 64 keys x 8 words of 16 bytes for K and for V; thread tid owns
+  // words tid + i 512 / NWD (i < NWD), and the next tile's words are loaded
+  // while the current one is computed
+  constexpr int nthr = 512 / NWD;
+  uint4 kn[NWD], vn[NWD];
+  auto load_tile = [&](int jb) {
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) {
+      const int c = tid + i * nthr;
+      const int key = min(jb + (c >> 3), T_max - 1);
+      kn[i] = *reinterpret_cast<const uint4*>(kg + (size_t)key * 64 + (c & 7) * 8);
+      vn[i] = *reinterpret_cast<const uint4*>(vg + (size_t)key * 64 + (c & 7) * 8);
+    }
+  };
+  const int jstart = (lo_blk / 64) * 64;
+  load_tile(jstart);
+  for (int j0 = jstart; j0 <= hi_blk; j0 += 64) {
     __syncthreads();  // the previous tile is consumed
-    for (int c = tid; c < 64 * 8; c += blockDim.x) {
+#pragma unroll
+    for (int i = 0; i < NWD; ++i) {
+      const int c = tid + i * nthr;
       const int kl = c >> 3, dq = (c & 7) * 8;
-      const int key = min(j0 + kl, T_max - 1);
-      const uint4 kv = *reinterpret_cast<const uint4*>(kg + (size_t)key * 64 + dq);
-      const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * 64 + dq);
-      *reinterpret_cast<uint4*>(&ks[kl * 64 + dq]) = kv;
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      *reinterpret_cast<uint4*>(&ks[kl * 64 + dq]) = kn[i];
+      const uint32_t vw[4] = {vn[i].x, vn[i].y, vn[i].z, vn[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vt[(dq + 2 * e) * VT + kl] = (uint16_t)(vw[e] & 0xFFFFu);
         vt[(dq + 2 * e + 1) * VT + kl] = (uint16_t)(vw[e] >> 16);
       }
     }
+    if (j0 + 64 <= hi_blk) load_tile(j0 + 64);  // in flight during this tile
     __syncthreads();
     // S^T tiles
     pf_f32x4 sacc[4][4];  // [kt][qt]
@@ -879,57 +962,18 @@ __global__ __launch_bounds__(512) void k_attn_prefill(
         sacc[kt][qt] = acc;
       }
     }
-    // scale, mask, online softmax; P^T (hi, lo) packed per key pair p
+    // scale, mask (tiles that cross the diagonal or the window edge only),
+    // online softmax; P^T (hi, lo) packed per key pair p
+    const bool full = j0 + 63 <= t0 && (window <= 0 || j0 >= t0 + 64 - window);
     uint4 phi[4][2], plo[4][2];  // [qt][p]
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
-      const int t = t0 + 16 * qt + j;
-      const int lo_t = window > 0 ? max(0, t - window + 1) : 0;
-      float sv[4][4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = j0 + 16 * kt + 4 * g + r;
-          const bool valid = key >= lo_t && key <= t;
-          sv[kt][r] = valid ? __fmul_rn(sacc[kt][qt][r], 0.125f) : -INFINITY;
-          mx = fmaxf(mx, sv[kt][r]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mt = fmaxf(m[qt], mx);
-      const float sc = mt == -INFINITY ? 1.0f : __expf(m[qt] - mt);  // m = -inf -> 0
-      l[qt] *= sc;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        o[qt][dt][0] *= sc; o[qt][dt][1] *= sc; o[qt][dt][2] *= sc; o[qt][dt][3] *= sc;
-      }
-      m[qt] = mt;
-      float pv[4][4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pv[kt][r] = sv[kt][r] == -INFINITY ? 0.0f : __expf(sv[kt][r] - mt);
-          l[qt] += pv[kt][r];
-        }
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
-            const float a0 = pv[2 * pp + half][2 * r2], a1 = pv[2 * pp + half][2 * r2 + 1];
-            const uint16_t h0 = f2bf(a0), h1 = f2bf(a1);
-            const uint16_t l0 = f2bf(a0 - bf2f(h0)), l1 = f2bf(a1 - bf2f(h1));
-            hw[2 * half + r2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-            lw[2 * half + r2] = (uint32_t)l0 | ((uint32_t)l1 << 16);
-          }
-        phi[qt][pp] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        plo[qt][pp] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-      }
+      if (full)  // uniform
+        attn_prefill_softmax<false>(sacc, qt, t0, j0, j, g, window, m[qt], l[qt], o[qt],
+                                    phi[qt], plo[qt]);
+      else
+        attn_prefill_softmax<true>(sacc, qt, t0, j0, j, g, window, m[qt], l[qt], o[qt],
+                                   phi[qt], plo[qt]);
     }
     // O^T += V^T P^T
 #pragma unroll
@@ -950,15 +994,15 @@ __global__ __launch_bounds__(512) void k_attn_prefill(
       }
     }
   }
-  const float sk = bf2f(sinks[h]);
+  const float sk = __fmul_rn(bf2f(sinks[h]), 1.44269504088896340736f);  // log2 domain
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
     float lt = l[qt];
     lt += __shfl_xor(lt, 16);
     lt += __shfl_xor(lt, 32);
     const float mt = fmaxf(m[qt], sk);
-    const float sc = __expf(m[qt] - mt);
-    const float inv = 1.0f / (lt * sc + __expf(sk - mt));
+    const float sc = __builtin_amdgcn_exp2f(m[qt] - mt);
+    const float inv = 1.0f / (lt * sc + __builtin_amdgcn_exp2f(sk - mt));
     const int t = t0 + 16 * qt + j;
     if (t < M) {
       uint16_t* dst = out + (size_t)t * Hq * 64 + (size_t)h * 64;
@@ -976,8 +1020,15 @@ void launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* 
                          const uint16_t* sinks, uint16_t* out, int M, int Hq, int Hkv,
                          int T_max, int window, hipStream_t st) {
   dim3 grid(Hkv, (M + 63) / 64);
-  hipLaunchKernelGGL(k_attn_prefill, grid, dim3(64 * (Hq / Hkv)), 0, st, q, kc, vc, sinks,
-                     out, M, Hq, Hkv, T_max, window);
+  const int G = Hq / Hkv;  // 1, 2, 4 or 8 (checked by the callers)
+#define AP_LAUNCH(NWD)                                                                  \
+  hipLaunchKernelGGL(k_attn_prefill<NWD>, grid, dim3(64 * G), 0, st, q, kc, vc, sinks, out, \
+                     M, Hq, Hkv, T_max, window)
+  if (G == 8) AP_LAUNCH(1);
+  else if (G == 4) AP_LAUNCH(2);
+  else if (G == 2) AP_LAUNCH(4);
+  else AP_LAUNCH(8);
+#undef AP_LAUNCH
 }
 
 }  // namespace neon
