@@ -69,6 +69,8 @@ void launch_embed_rows(const int32_t* ids, int M, const uint16_t* embed,
 // ===========================================================================
 constexpr int kGM = 128, kGN = 128, kGK = 64, kGS = 72;  // tile, LDS row stride
 
+constexpr int kNarrowMaxN = 64;   // k_gemm_narrow_f32: columns per launch (4 tiles)
+constexpr int kNarrowBatch = 6;   // its K chunks per wave loaded before their MFMAs
 enum {
   GEMM_STORE = 0,    // C = bf16(acc + bias)
   GEMM_RESID = 1,    // C = bf16(C + bf16(acc + bias))  (C holds the residual)
@@ -571,9 +573,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mx8(GemmParams p) {
   gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, e);
 }
 
+static void launch_gemm_narrow_f32(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
+                                   float* C, int M, int N, int K, hipStream_t st);
+
 void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
                       const uint16_t* bias, uint16_t* C, float* Cf, int ldc, int M,
                       int N, int K, int mode, hipStream_t st) {
+  if (mode == GEMM_F32 && N <= kNarrowMaxN && K % 32 == 0 && lda == K && ldw == K && ldc == N) {
+    // a narrow fp32 product (the prompt router logits, N = E): 128-wide
+    // column tiles would leave most of the device idle
+    launch_gemm_narrow_f32(A, W, bias, Cf, M, N, K, st);
+    return;
+  }
   GemmParams p{};
   p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.bias = bias; p.C = C; p.Cf = Cf;
   p.ldc = ldc; p.M = M; p.N = N; p.K = K;
@@ -1016,6 +1027,86 @@ __global__ __launch_bounds__(512) void k_attn_prefill(
         *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * g) = make_uint2(w0, w1);
       }
     }
+  }
+}
+
+// fp32 C[M][N] = A[M][K] W[N][K]^T + bias[N] for N <= kNarrowMaxN (the router
+// logits of the prompt pass, N = E): a block owns 16 rows of A and all N
+// columns (NT tiles of 16) on v_mfma_f32_16x16x32_bf16; its 4 waves take
+// the 32-element K chunks c = w, w + 4, ..., loading kNarrowBatch chunks at
+// a time before their MFMAs, then wave 0 adds the 4 partial tiles in wave
+// order and the bias.
+template <int NT>
+__global__ __launch_bounds__(256) void k_gemm_narrow_f32(const uint16_t* __restrict__ A,
+                                                         const uint16_t* __restrict__ W,
+                                                         const uint16_t* __restrict__ bias,
+                                                         float* __restrict__ C, int M, int N,
+                                                         int K) {
+  __shared__ pf_f32x4 red[3][NT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int r0 = blockIdx.x * 16;
+  const uint16_t* arow = A + (size_t)min(r0 + j, M - 1) * K + 8 * g;
+  const uint16_t* wrow[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) wrow[nt] = W + (size_t)min(16 * nt + j, N - 1) * K + 8 * g;
+  pf_f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int nch = K / 32;
+  for (int c0 = w; c0 < nch; c0 += 4 * kNarrowBatch) {
+    uint4 av[kNarrowBatch], wv[kNarrowBatch][NT];
+#pragma unroll
+    for (int i = 0; i < kNarrowBatch; ++i) {
+      const int c = min(c0 + 4 * i, nch - 1);  // past the end: re-read, then dropped
+      av[i] = *reinterpret_cast<const uint4*>(arow + 32 * (size_t)c);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        wv[i][nt] = *reinterpret_cast<const uint4*>(wrow[nt] + 32 * (size_t)c);
+    }
+#pragma unroll
+    for (int i = 0; i < kNarrowBatch; ++i) {
+      if (c0 + 4 * i >= nch) break;  // uniform
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(av[i]),
+                                                          pf_as_bf16x8(wv[i][nt]), acc[nt], 0,
+                                                          0, 0);
+    }
+  }
+  if (w > 0) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) red[w - 1][nt][lane] = acc[nt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    pf_f32x4 tot = acc[nt];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const pf_f32x4 p = red[v][nt][lane];
+      tot[0] += p[0]; tot[1] += p[1]; tot[2] += p[2]; tot[3] += p[3];
+    }
+    const int col = 16 * nt + j;
+    if (col >= N) continue;
+    const float b = bias != nullptr ? bf2f(bias[col]) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = r0 + 4 * g + r;  // D row of lane (j, g), register r
+      if (row < M) C[(size_t)row * N + col] = tot[r] + b;
+    }
+  }
+}
+
+static void launch_gemm_narrow_f32(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
+                                   float* C, int M, int N, int K, hipStream_t st) {
+  const dim3 grid((M + 15) / 16);
+  switch ((N + 15) / 16) {
+    case 1: hipLaunchKernelGGL(k_gemm_narrow_f32<1>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
+    case 2: hipLaunchKernelGGL(k_gemm_narrow_f32<2>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
+    case 3: hipLaunchKernelGGL(k_gemm_narrow_f32<3>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
+    default: hipLaunchKernelGGL(k_gemm_narrow_f32<4>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
   }
 }
 
