@@ -35,6 +35,10 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
 ]
 
+# hipBLASLt (the prompt pass's plain projection GEMMs), found at run time in
+# the ROCm tree the library was built against
+LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+
 
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -63,7 +67,7 @@ def build(verbose: bool = False) -> str:
         if p.returncode != 0:
             raise RuntimeError(f"hipcc failed ({p.returncode}): {' '.join(cmd)}\n{text}")
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + LINK_LIBS
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout.decode(errors='replace')}")
@@ -96,7 +100,7 @@ def build_sanitized(verbose: bool = False) -> str:
     tmp = ASAN_LIB + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-Xarch_host", "-fsanitize=address",
            "-Xarch_host", "-fsanitize=undefined", "-Xarch_host", "-shared-libasan", "-o", tmp,
-           obj] + others
+           obj] + others + LINK_LIBS
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout.decode(errors='replace')}")

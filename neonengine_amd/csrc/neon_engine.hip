@@ -964,8 +964,7 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
     uint16_t* vd = ring ? ctx->pf_vs : ctx->vc + kvo;
     const int Td = ring ? ctx->pf_rows : ctx->kv_rows[l];
     launch_rmsnorm(ctx->pf_h, w.attn_norm, ctx->pf_xn, M, H, c.rms_eps, st);
-    launch_gemm_bf16(ctx->pf_xn, H, w.wqkv, H, w.bqkv, ctx->pf_qkv, nullptr, qkv_rows, M,
-                     qkv_rows, H, 0, st);
+    launch_prompt_proj(ctx->pf_xn, w.wqkv, w.bqkv, ctx->pf_qkv, M, qkv_rows, H, 0, st);
     launch_rope_kv_rows(ctx->pf_qkv, qkv_rows, ctx->cos_t, ctx->sin_t, M, Hq, Hkv, Td,
                         ctx->pf_q, kd, vd, st);
     launch_attn_prefill(ctx->pf_q, kd, vd, w.sinks, ctx->pf_ao, M, Hq, Hkv, Td,
@@ -973,8 +972,7 @@ static void enqueue_prefill_rows(neon_ctx* ctx, int b, int M, hipStream_t st) {
     if (ring)
       launch_kv_ring_store(ctx->pf_ks, ctx->pf_vs, Td, std::max(0, M - ctx->kv_rows[l]), M,
                            Hkv, ctx->kv_rows[l], ctx->kc + kvo, ctx->vc + kvo, st);
-    launch_gemm_bf16(ctx->pf_ao, Hq * D, w.wo, Hq * D, w.bo, ctx->pf_h, nullptr, H, M, H,
-                     Hq * D, 1, st);
+    launch_prompt_proj(ctx->pf_ao, w.wo, w.bo, ctx->pf_h, M, H, Hq * D, 1, st);
     launch_rmsnorm(ctx->pf_h, w.mlp_norm, ctx->pf_xn, M, H, c.rms_eps, st);
     launch_gemm_bf16(ctx->pf_xn, H, w.router_w, H, w.router_b, nullptr, ctx->pf_lg,
                      c.n_experts, M, c.n_experts, H, 2, st);

@@ -16,6 +16,12 @@
 #include "neon_common.hpp"
 #include "neon_internal.hpp"
 
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <mutex>
+#include <vector>
+
 namespace neon {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -575,6 +581,91 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mx8(GemmParams p) {
 
 static void launch_gemm_narrow_f32(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
                                    float* C, int M, int N, int K, hipStream_t st);
+
+// ---- the prompt projections on hipBLASLt -----------------------------------
+// hipBLASLt is column-major: W [N][K] row-major is a K x N matrix (op T), x
+// [M][K] a K x M matrix (op N), and C [M][N] row-major the N x M result, so
+// D = op(W) x + bias (broadcast along D's rows = C's columns) (+ beta C).
+// A plan (descriptors and the heuristic's first workspace-free algorithm)
+// is built once per (device, M, N, K, residual); the bias pointer is set
+// on the shared descriptor just before each call, under the lock.
+namespace {
+struct BlasPlan {
+  int dev, M, N, K;
+  bool resid;
+  hipblasLtMatmulDesc_t desc;
+  hipblasLtMatrixLayout_t lw, lx, lc;
+  hipblasLtMatmulAlgo_t algo;
+};
+std::mutex g_blas_mu;
+std::vector<BlasPlan> g_blas_plans;
+std::vector<hipblasLtHandle_t> g_blas_handle;  // per device (created on first use)
+
+bool blas_plan(int dev, int M, int N, int K, bool resid, BlasPlan*& out) {
+  for (BlasPlan& p : g_blas_plans)
+    if (p.dev == dev && p.M == M && p.N == N && p.K == K && p.resid == resid) {
+      out = &p;
+      return true;
+    }
+  if ((int)g_blas_handle.size() <= dev) g_blas_handle.resize(dev + 1, nullptr);
+  if (g_blas_handle[dev] == nullptr && hipblasLtCreate(&g_blas_handle[dev]) != HIPBLAS_STATUS_SUCCESS) {
+    g_blas_handle[dev] = nullptr;
+    return false;
+  }
+  BlasPlan p{};
+  p.dev = dev; p.M = M; p.N = N; p.K = K; p.resid = resid;
+  bool ok = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
+  const int32_t opT = HIPBLAS_OP_T, opN = HIPBLAS_OP_N, bias_t = HIP_R_16BF;
+  const hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opT, sizeof(opT)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opN, sizeof(opN)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bias_t, sizeof(bias_t)) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_16BF, K, N, K) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.lx, HIP_R_16BF, K, M, K) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, N) == HIPBLAS_STATUS_SUCCESS;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
+  const uint64_t no_ws = 0;  // only algorithms that need no workspace
+  ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws, sizeof(no_ws)) == HIPBLAS_STATUS_SUCCESS;
+  hipblasLtMatmulHeuristicResult_t res[4];
+  int n = 0;
+  ok = ok && hipblasLtMatmulAlgoGetHeuristic(g_blas_handle[dev], p.desc, p.lw, p.lx, p.lc, p.lc, pref, 4, res, &n) == HIPBLAS_STATUS_SUCCESS;
+  if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+  int pick = -1;
+  for (int i = 0; ok && i < n && pick < 0; ++i)
+    if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize == 0) pick = i;
+  if (!ok || pick < 0) return false;  // (descriptors of a failed plan are kept: rare, small)
+  p.algo = res[pick].algo;
+  g_blas_plans.push_back(p);
+  out = &g_blas_plans.back();
+  return true;
+}
+
+bool prompt_blas_enabled() {
+  static const bool on = !(getenv("NEON_PROMPT_BLAS") && getenv("NEON_PROMPT_BLAS")[0] == '0');
+  return on;
+}
+}  // namespace
+
+void launch_prompt_proj(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
+                        uint16_t* C, int M, int N, int K, int mode, hipStream_t st) {
+  if (prompt_blas_enabled() && bias != nullptr && (mode == GEMM_STORE || mode == GEMM_RESID)) {
+    std::lock_guard<std::mutex> lk(g_blas_mu);
+    int dev = 0;
+    BlasPlan* p = nullptr;
+    if (hipGetDevice(&dev) == hipSuccess && blas_plan(dev, M, N, K, mode == GEMM_RESID, p)) {
+      const void* bp = bias;
+      const float alpha = 1.0f, beta = mode == GEMM_RESID ? 1.0f : 0.0f;
+      if (hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bp,
+                                          sizeof(bp)) == HIPBLAS_STATUS_SUCCESS &&
+          hipblasLtMatmul(g_blas_handle[dev], p->desc, &alpha, W, p->lw, A, p->lx, &beta, C,
+                          p->lc, C, p->lc, &p->algo, nullptr, 0, st) == HIPBLAS_STATUS_SUCCESS)
+        return;
+    }
+  }
+  launch_gemm_bf16(A, K, W, K, bias, C, nullptr, N, M, N, K, mode, st);
+}
 
 void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
                       const uint16_t* bias, uint16_t* C, float* Cf, int ldc, int M,
