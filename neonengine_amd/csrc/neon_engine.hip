@@ -131,6 +131,7 @@ struct neon_ctx {
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
   int32_t* mx_route = nullptr;       // used experts and their pair lists
+  uint16_t* mx_xp = nullptr;         // normalised rows in the packed activation layout
   // the weights in MFMA lane order for the matrix-core steps (allocated when
   // that mode is first selected; refreshed before a step after any change)
   struct MxLayer { uint16_t *wqkv, *wo; uint8_t *gu_c, *gu_s, *dn_c, *dn_s; };
@@ -418,6 +419,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_mxv = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_mxi = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_mxr = take(Bm > 1 ? (size_t)66 * 256 * 4 : 0),
+               o_mxp = take(Bm > 1 ? (size_t)((Bm + 15) / 16) * ((H + 127) / 128) * 2048 * 2 : 0),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -454,6 +456,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
     ctx->mx_part_val = (float*)(W + o_mxv);
     ctx->mx_part_idx = (int32_t*)(W + o_mxi);
     ctx->mx_route = (int32_t*)(W + o_mxr);
+    ctx->mx_xp = (uint16_t*)(W + o_mxp);
   }
   // ---- RoPE table ----
   std::vector<float> ct, st;
@@ -734,10 +737,15 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
     uint16_t* kc_l = ctx->kc + ctx->kv_off[l];
     uint16_t* vc_l = ctx->vc + ctx->kv_off[l];
-    launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
-    MxArgs q{};
+    // the normalised rows straight into the packed activation layout the
+    // QKV kernel reads (1 KB contiguous per operand)
     const neon_ctx::MxLayer& mp = ctx->mxp[l];
-    q.W = w.wqkv; q.Wp = mp.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.y = ctx->qkv;
+    const bool xp = mp.wqkv != nullptr;
+    if (xp) launch_rmsnorm_packed(ctx->h, w.attn_norm, ctx->mx_xp, B, H, c.rms_eps, st);
+    else launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
+    MxArgs q{};
+    q.W = w.wqkv; q.Wp = mp.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.xp = xp ? ctx->mx_xp : nullptr;
+    q.y = ctx->qkv;
     q.B = B; q.N = qkv_rows; q.K = H;
     launch_mx_gemv(q, 0, st);
     launch_mx_rope_append(ctx->qkv, ctx->pos, nullptr, ctx->cos_t, ctx->sin_t, ctx->q_rot, kc_l,
@@ -794,9 +802,12 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
       launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
     }
   }
-  launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
+  const bool lxp = ctx->mx_lm != nullptr;
+  if (lxp) launch_rmsnorm_packed(ctx->h, ctx->final_norm, ctx->mx_xp, B, H, c.rms_eps, st);
+  else launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
   MxArgs lm{};
-  lm.W = ctx->lm_head; lm.Wp = ctx->mx_lm; lm.x = ctx->xn; lm.out_f = ctx->logits;
+  lm.W = ctx->lm_head; lm.Wp = ctx->mx_lm; lm.x = ctx->xn; lm.xp = lxp ? ctx->mx_xp : nullptr;
+  lm.out_f = ctx->logits;
   lm.part_val = ctx->mx_part_val; lm.part_idx = ctx->mx_part_idx;
   lm.B = B; lm.N = c.vocab; lm.K = H;
   launch_mx_gemv(lm, 2, st);

@@ -87,6 +87,10 @@ void launch_embed(const int32_t* tokens, int tok_stride, const int32_t* pos,
                   const int32_t* seq,
                   const uint16_t* embed, uint16_t* h, int H, int B,
                   hipStream_t st);
+// the normalised rows in the matrix-core activation layout (k_rmsnorm_packed:
+// [ceil(B/16)][ceil(H/128)][4][64][8] bf16, zero past B and H)
+void launch_rmsnorm_packed(const uint16_t* x, const uint16_t* w, uint16_t* out, int B, int H,
+                           float eps, hipStream_t st);
 void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
                     int H, float eps, hipStream_t st);
 
@@ -174,6 +178,9 @@ struct MxArgs {
   const uint8_t* scales;     // MXFP4 scales [E][N][K/32] (expert modes)
   const uint16_t* bias;      // [N], [E][N] (expert modes) or NULL (dense modes)
   const uint16_t* x;         // input rows of K bf16: [B][K]; gate_up [B][K]; down [B k][K]
+  // dense modes with Wp: the input rows in the activation layout of
+  // launch_rmsnorm_packed instead of x (1 KB contiguous per MFMA operand), or NULL
+  const uint16_t* xp = nullptr;
   uint16_t* y;               // store / residual [B][N]; gate_up: act [B k][N / 2]
   float* out_f;              // logits [B][N]; down: per-pair dot + bias [B k][N]
   float* part_val;           // logits: per-block (max, lowest index) [B][N / 16]

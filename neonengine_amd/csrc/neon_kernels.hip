@@ -1456,6 +1456,61 @@ void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
   }
 }
 
+// The same normalised rows written in the matrix-core activation layout
+// [ceil(B/16)][NCH][4][64][8] (NCH = ceil(H / 128)): the 8 elements 8 u ..
+// 8 u + 7 of row r go to piece ((r / 16 * NCH + u / 16) * 4 + u % 16 / 4) * 64
+// + r % 16 + 16 (u % 4), so that one 16 x 16 x 32 MFMA operand (16 rows x 32
+// elements) is 1 KB contiguous.  Rows B .. 16 ceil(B/16) - 1 and units
+// H / 8 .. 16 NCH - 1 are written as zeros (one wave per row of the padded
+// tile).  Same arithmetic as k_rmsnorm.
+template <int P>
+__global__ __launch_bounds__(64) void k_rmsnorm_packed(const uint16_t* __restrict__ x,
+                                                       const uint16_t* __restrict__ w,
+                                                       uint16_t* __restrict__ out, int B, int H,
+                                                       float eps) {
+  const int r = blockIdx.x, lane = threadIdx.x;
+  const int U = H / 8, NCH = (H + 127) / 128;
+  uint4* o = reinterpret_cast<uint4*>(out);
+  const size_t tile = (size_t)(r / 16) * NCH * 4 * 64;
+  auto piece = [&](int u) { return tile + ((size_t)(u / 16) * 4 + (u % 16) / 4) * 64 + r % 16 + 16 * (u % 4); };
+  if (r >= B) {  // padding row (uniform)
+    for (int u = lane; u < 16 * NCH; u += 64) o[piece(u)] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  XBf16Raw<P> raw;
+  wave_x_bf16_issue<P, true>(raw, x + (size_t)r * H, w, H, lane);
+  float xr[P][8];
+  wave_x_bf16_finish<P, true>(xr, raw, eps, H, lane, nullptr);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = lane + 64 * p;
+    if (u < U) {
+      uint32_t q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[j] = pack_bf2(xr[p][2 * j], xr[p][2 * j + 1]);
+      o[piece(u)] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
+  for (int u = U + lane; u < 16 * NCH; u += 64) o[piece(u)] = make_uint4(0, 0, 0, 0);
+}
+
+void launch_rmsnorm_packed(const uint16_t* x, const uint16_t* w, uint16_t* out, int B, int H,
+                           float eps, hipStream_t st) {
+  const int P = (H / 8 + 63) / 64;
+  const int rows = 16 * ((B + 15) / 16);
+  switch (P) {
+#define NP_CASE(PP)                                                                      \
+  case PP:                                                                               \
+    hipLaunchKernelGGL(k_rmsnorm_packed<PP>, dim3(rows), dim3(64), 0, st, x, w, out, B, \
+                       H, eps);                                                          \
+    break;
+    NP_CASE(1) NP_CASE(2) NP_CASE(3) NP_CASE(4) NP_CASE(5) NP_CASE(6) NP_CASE(7)
+    NP_CASE(8)
+    default: NP_CASE(16)
+#undef NP_CASE
+  }
+}
+
 // ===========================================================================
 // RoPE (HFM:215-222): half-split rotation with the host-built YaRN table
 // (cos/sin [n_pos][D/2] fp32, HF modeling_rope_utils.py:429-483):

@@ -60,6 +60,58 @@ __device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
 
+// Epilogue of the dense matrix-core GEMVs: waves 1..3 hand their partial
+// tiles to wave 0, which adds them in wave order, then applies the mode's
+// bias / residual / bf16 rounding (or fp32 logits and the per-block
+// (max, lowest index) partials).
+template <int BT, int MODE>
+__device__ __forceinline__ void mx_gemv_epilogue(const MxArgs& a, const mx_f32x4 (&acc)[BT],
+                                                 mx_f32x4 (&red)[3][BT][64], int lane, int w,
+                                                 int n0, int j, int g, int N, int R) {
+  if (w > 0) {
+#pragma unroll
+    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
+  }
+  __syncthreads();
+  if (w != 0) return;
+  const int n = n0 + j;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+    if (16 * bt >= R) break;
+    mx_f32x4 tot = acc[bt];
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+      const mx_f32x4 p = red[v][bt][lane];
+      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
+      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 16 * bt + 4 * g + r;  // row of A / output row
+      const bool ok = ri < R;
+      const float d = tot[r];
+      if constexpr (MODE == MX_LOGITS) {
+        if (ok) a.out_f[(size_t)ri * N + n] = d;
+        float bv = ok ? d : -INFINITY;
+        int bi = n;
+        mx_argmax_step(bv, bi, 1);
+        mx_argmax_step(bv, bi, 2);
+        mx_argmax_step(bv, bi, 4);
+        mx_argmax_step(bv, bi, 8);
+        if (ok && j == 0) {
+          a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
+          a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
+        }
+      } else if (ok) {
+        const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
+        const size_t o = (size_t)ri * N + n;
+        if (MODE == MX_STORE) a.y[o] = f2bf(v);
+        else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
+      }
+    }
+  }
+}
+
 // Projections and lm_head: a block owns weight rows n0 .. n0 + 15 for all B
 // rows, and its 4 waves split K.  BT = row tiles of 16 (B <= 16 BT); IT = K
 // iterations per wave (K <= 512 IT).  Lane (j, g) reads elements
@@ -131,49 +183,143 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
                                                             0, 0, 0);
     }
   }
-  // waves 1..3 hand their partial sums to wave 0, which adds them in order
-  if (w > 0) {
-#pragma unroll
-    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
-  }
-  __syncthreads();
-  if (w != 0) return;
-  const int n = n0 + j;
+  mx_gemv_epilogue<BT, MODE>(a, acc, red, lane, w, n0, j, g, N, R);
+}
+
+// k_mx_gemv over the packed copy with the weights and activation rows of
+// each K iteration loaded one iteration ahead (two register sets), instead
+// of all of the wave's weight loads up front: more waves per SIMD and the
+// next iteration's loads in flight during this one's MFMAs.  Same lane map,
+// same order of every fp32 addition, so the same bits as k_mx_gemv.
+// Measured faster for one row tile (B <= 16: QKV 13.0 -> 11.5 us, O
+// 11.0 -> 9.7 us at the 20b shape, B = 16) and slower from BT = 2 on (two
+// sets of BT activation tiles), where k_mx_gemv stays.
+template <int BT, int IT, int MODE>
+__global__ __launch_bounds__(256) void k_mx_gemv_db(MxArgs a) {
+  __shared__ mx_f32x4 red[3][BT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, R = a.B;
+  const int n0 = blockIdx.x * 16;
+  const int NCH = (K + 127) / 128;
+  const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
+  const uint16_t* xrow[BT];
+  bool rv[BT];
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) {
-    if (16 * bt >= R) break;
-    mx_f32x4 tot = acc[bt];
+    const int r = 16 * bt + j;
+    rv[bt] = r < R;
+    xrow[bt] = a.x + (size_t)(rv[bt] ? r : R - 1) * K;
+  }
+  auto load_w = [&](int it, uint4 (&wq)[4]) {
+    const int ch = min(4 * it + w, NCH - 1);
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
-      const mx_f32x4 p = red[v][bt][lane];
-      tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
-      tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
+    for (int t = 0; t < 4; ++t)
+      wq[t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
+  };
+  auto load_x = [&](int it, uint4 (&xq)[BT][4]) {
+    const int base = 128 * (4 * it + w);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool ok = base + 32 * t < K;
+      const int el = ok ? base + 32 * t + 8 * g : 8 * g;
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow[bt] + el);
+        xq[bt][t] = (ok && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
+  };
+  mx_f32x4 acc[BT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ri = 16 * bt + 4 * g + r;  // row of A / output row
-      const bool ok = ri < R;
-      const float d = tot[r];
-      if constexpr (MODE == MX_LOGITS) {
-        if (ok) a.out_f[(size_t)ri * N + n] = d;
-        float bv = ok ? d : -INFINITY;
-        int bi = n;
-        mx_argmax_step(bv, bi, 1);
-        mx_argmax_step(bv, bi, 2);
-        mx_argmax_step(bv, bi, 4);
-        mx_argmax_step(bv, bi, 8);
-        if (ok && j == 0) {
-          a.part_val[(size_t)ri * gridDim.x + blockIdx.x] = bv;
-          a.part_idx[(size_t)ri * gridDim.x + blockIdx.x] = bi;
-        }
-      } else if (ok) {
-        const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
-        const size_t o = (size_t)ri * N + n;
-        if (MODE == MX_STORE) a.y[o] = f2bf(v);
-        else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint4 wc[4], wn[4], xc[BT][4], xn[BT][4];
+  load_w(0, wc);
+  load_x(0, xc);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (it + 1 < IT) { load_w(it + 1, wn); load_x(it + 1, xn); }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const mx_bf16x8 bw = mx_as_bf16x8(wc[t]);
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt)
+        if (16 * bt < R)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xc[bt][t]), bw, acc[bt],
+                                                            0, 0, 0);
+    }
+    if (it + 1 < IT) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        wc[t] = wn[t];
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt) xc[bt][t] = xn[bt][t];
       }
     }
   }
+  mx_gemv_epilogue<BT, MODE>(a, acc, red, lane, w, n0, j, g, N, R);
+}
+
+// k_mx_gemv over the packed weights with the activation rows in the packed
+// activation layout (MxArgs::xp, written by launch_rmsnorm_packed): every
+// operand load is 1 KB contiguous, the weights stream one K iteration ahead
+// (two register sets) and each iteration's activation tiles are loaded as it
+// starts.  Same lane map and the same order of every fp32 addition as
+// k_mx_gemv, so the same bits.  Measured at the 20b shape, B = 16 / 32 / 64:
+// QKV 11.6 / 19.4 / 38.2 -> 9.8 / 13.9 / 23.3 us, lm_head 276 / 405 / 753 ->
+// 245 / 293 / 582 us.
+template <int BT, int IT, int MODE>
+__global__ __launch_bounds__(256) void k_mx_gemv_px(MxArgs a) {
+  __shared__ mx_f32x4 red[3][BT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, R = a.B;
+  const int n0 = blockIdx.x * 16;
+  const int NCH = (K + 127) / 128;
+  const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
+  const uint16_t* X = a.xp;
+  auto load_w = [&](int it, uint4 (&wq)[4]) {
+    const int ch = min(4 * it + w, NCH - 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      wq[t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
+  };
+  mx_f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint4 wc[4], wn[4];
+  load_w(0, wc);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (it + 1 < IT) load_w(it + 1, wn);
+    // chunks past K: a zero A operand (the packed rows are zero past K only
+    // up to the last chunk)
+    const bool okc = 4 * it + w < NCH;
+    const int ch = min(4 * it + w, NCH - 1);
+    uint4 xq[BT][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) {
+        const uint4 v = *reinterpret_cast<const uint4*>(
+            X + ((((size_t)bt * NCH + ch) * 4 + t) * 64 + lane) * 8);
+        xq[bt][t] = okc ? v : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const mx_bf16x8 bw = mx_as_bf16x8(wc[t]);
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt)
+        if (16 * bt < R)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw, acc[bt],
+                                                            0, 0, 0);
+    }
+    if (it + 1 < IT) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) wc[t] = wn[t];
+    }
+  }
+  mx_gemv_epilogue<BT, MODE>(a, acc, red, lane, w, n0, j, g, N, R);
 }
 
 // Standalone MXFP4 GEMV on the matrix cores (neon_mxfp4_gemv at B >= 16):
@@ -644,6 +790,20 @@ __global__ __launch_bounds__(256) void k_mx_rope_append(
 template <int MODE, int BT, bool PK>
 static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
   const int it = (a.K / 32 + 15) / 16;
+  if (PK && a.xp != nullptr) {
+    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_px<BT, 2, MODE>), grid, dim3(256), 0, st, a);
+    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_px<BT, 4, MODE>), grid, dim3(256), 0, st, a);
+    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_px<BT, 6, MODE>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_px<BT, 8, MODE>), grid, dim3(256), 0, st, a);
+    return;
+  }
+  if (BT == 1 && PK) {
+    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_db<1, 2, MODE>), grid, dim3(256), 0, st, a);
+    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_db<1, 4, MODE>), grid, dim3(256), 0, st, a);
+    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_db<1, 6, MODE>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_db<1, 8, MODE>), grid, dim3(256), 0, st, a);
+    return;
+  }
   if (it <= 2) hipLaunchKernelGGL((k_mx_gemv<BT, 2, MODE, PK>), grid, dim3(256), 0, st, a);
   else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv<BT, 4, MODE, PK>), grid, dim3(256), 0, st, a);
   else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv<BT, 6, MODE, PK>), grid, dim3(256), 0, st, a);
