@@ -117,6 +117,16 @@ __device__ __forceinline__ uint4 load_agent16(const uint16_t* p) {
   return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
 }
 
+// Element offset of (row r, column k) in the packed activation layout of the
+// matrix-core GEMVs, [ceil(R/16)][NCH][4][64][8] bf16 with NCH = ceil(K/128):
+// one 16 x 32 MFMA operand (16 rows, 32 columns) is 1 KB contiguous, lane
+// r % 16 + 16 (u % 4) holding the 8 elements of unit u = k / 8.
+__device__ __forceinline__ size_t mx_packed_at(int r, int k, int NCH) {
+  const int u = k >> 3;
+  return ((((size_t)(r >> 4) * NCH + (u >> 4)) * 4 + ((u & 15) >> 2)) * 64 + (r & 15) +
+          16 * (u & 3)) * 8 + (k & 7);
+}
+
 // Sets status bits in the caller's status word (a vector-memory atomic).
 __device__ __forceinline__ void flag_dev_err(int32_t* err, int32_t bits) {
   if (err != nullptr) atomicOr(err, bits);

@@ -132,6 +132,7 @@ struct neon_ctx {
   int32_t* mx_part_idx = nullptr;
   int32_t* mx_route = nullptr;       // used experts and their pair lists
   uint16_t* mx_xp = nullptr;         // normalised rows in the packed activation layout
+  uint16_t* mx_ap = nullptr;         // attention output in the packed activation layout
   // the weights in MFMA lane order for the matrix-core steps (allocated when
   // that mode is first selected; refreshed before a step after any change)
   struct MxLayer { uint16_t *wqkv, *wo; uint8_t *gu_c, *gu_s, *dn_c, *dn_s; };
@@ -420,6 +421,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_mxi = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_mxr = take(Bm > 1 ? (size_t)66 * 256 * 4 : 0),
                o_mxp = take(Bm > 1 ? (size_t)((Bm + 15) / 16) * ((H + 127) / 128) * 2048 * 2 : 0),
+               o_mxa = take(Bm > 1 ? (size_t)((Bm + 15) / 16) * ((c.n_heads * c.head_dim + 127) / 128) * 2048 * 2 : 0),
                o_lg = take(Bm * (size_t)c.vocab * 4),
                o_pv = take(Bm * ctx->lm_nblk * 4), o_pi = take(Bm * ctx->lm_nblk * 4),
                o_tok = take(Bm * ctx->tok_stride * 4), o_pos = take(Bm * 4),
@@ -457,6 +459,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
     ctx->mx_part_idx = (int32_t*)(W + o_mxi);
     ctx->mx_route = (int32_t*)(W + o_mxr);
     ctx->mx_xp = (uint16_t*)(W + o_mxp);
+    ctx->mx_ap = (uint16_t*)(W + o_mxa);
   }
   // ---- RoPE table ----
   std::vector<float> ct, st;
@@ -758,9 +761,14 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
     a.window = sliding ? c.sliding_window : 0;
     a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
+    // the O projection reads a packed copy of the attention output (rows of
+    // Hq D = a multiple of 128 columns, so no column padding)
+    const bool ap = mp.wo != nullptr && (c.n_heads * D) % 128 == 0;
+    a.out_packed = ap ? ctx->mx_ap : nullptr;
     launch_mx_attn(a, st);
     MxArgs o{};
-    o.W = w.wo; o.Wp = mp.wo; o.bias = w.bo; o.x = ctx->attn_out; o.y = ctx->h;
+    o.W = w.wo; o.Wp = mp.wo; o.bias = w.bo; o.x = ctx->attn_out; o.xp = a.out_packed;
+    o.y = ctx->h;
     o.B = B; o.N = H; o.K = c.n_heads * D;
     launch_mx_gemv(o, 1, st);
     RouterArgs r;

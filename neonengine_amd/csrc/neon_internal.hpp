@@ -261,6 +261,9 @@ struct AttnArgs {
   // left at 0): with S > 1 the split kernel's last block per (row, kv head)
   // merges; NULL: a separate merge kernel (launch_attn only)
   int32_t* arrive = nullptr;
+  // matrix-core steps (launch_mx_attn): the output also in the packed
+  // activation layout (K = Hq D, a multiple of 128) for the O projection, or NULL
+  uint16_t* out_packed = nullptr;
 };
 // ints between consecutive arrival counters (one 256-byte line each)
 constexpr int kAttnArriveStride = 64;

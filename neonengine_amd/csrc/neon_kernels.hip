@@ -2938,7 +2938,9 @@ template <bool AGENT>
 __device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o,
                                                 const float* __restrict__ part_ml,
                                                 size_t pi0, int S, float sk, int lane,
-                                                uint16_t* __restrict__ out_row) {
+                                                uint16_t* __restrict__ out_row,
+                                                uint16_t* __restrict__ outp = nullptr,
+                                                size_t outp_at = 0) {
   float ov[kMaxSplits];
 #pragma unroll
   for (int t = 0; t < kMaxSplits; ++t)
@@ -2957,7 +2959,11 @@ __device__ __forceinline__ void attn_merge_head(const float* __restrict__ part_o
       acc = __builtin_fmaf(f, ov[t], acc);
     }
   }
-  out_row[lane] = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+  const uint16_t o = f2bf(__fmul_rn(acc, __fdiv_rn(1.0f, den)));
+  out_row[lane] = o;
+  // the packed copy: lane's column k0 + lane sits at outp_at + the offset of
+  // lane (units of 8 are contiguous, 16 B apart per 16-row lane group)
+  if (outp != nullptr) outp[outp_at + (size_t)(lane >> 5) * 512 + ((lane & 31) >> 3) * 128 + (lane & 7)] = o;
 }
 
 __global__ __launch_bounds__(512) void k_attn_split(
@@ -3166,10 +3172,13 @@ __global__ __launch_bounds__(512) void k_attn_split(
 __global__ __launch_bounds__(64) void k_attn_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq,
-    int S) {
+    int S, uint16_t* __restrict__ outp) {
   const int h = blockIdx.x, b = blockIdx.y;
+  // head h's 64 columns start at k0 = 64 h: unit 8 h (a multiple of 8), so
+  // they fill lanes b % 16 + 16 q (q = 0..3) of steps 2 (h % 2), +1 of chunk h / 2
+  const size_t at = outp != nullptr ? mx_packed_at(b, kD * h, Hq * kD / 128) : 0;
   attn_merge_head<false>(part_o, part_ml, ((size_t)b * Hq + h) * S, S, bf2f(sinks[h]),
-                         threadIdx.x, out + ((size_t)b * Hq + h) * kD);
+                         threadIdx.x, out + ((size_t)b * Hq + h) * kD, outp, at);
 }
 
 #undef ATTN_LOAD_WORD
@@ -3177,7 +3186,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(
 
 void launch_attn_merge(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o, a.part_ml,
-                     a.sinks, a.out, a.Hq, a.S);
+                     a.sinks, a.out, a.Hq, a.S, a.out_packed);
 }
 
 void launch_attn(const AttnArgs& a, hipStream_t st) {
@@ -3194,7 +3203,7 @@ void launch_attn(const AttnArgs& a, hipStream_t st) {
   // arrival counters are given, else in k_attn_merge
   if (a.S > 1 && a.arrive == nullptr)
     hipLaunchKernelGGL(k_attn_merge, dim3(a.Hq, a.B), dim3(64), 0, st, a.part_o,
-                       a.part_ml, a.sinks, a.out, a.Hq, a.S);
+                       a.part_ml, a.sinks, a.out, a.Hq, a.S, nullptr);
 }
 
 // Key splits for a cache of T_max rows: spans of at most 4 chunks (256 keys,

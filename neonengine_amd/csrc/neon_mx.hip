@@ -60,14 +60,14 @@ __device__ __forceinline__ void mx_argmax_step(float& v, int& i, int off) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
 
-// Epilogue of the dense matrix-core GEMVs: waves 1..3 hand their partial
-// tiles to wave 0, which adds them in wave order, then applies the mode's
+// Epilogue of the dense matrix-core GEMVs: waves 1 .. WAVES - 1 hand their
+// partial tiles to wave 0, which adds them in wave order, then applies the mode's
 // bias / residual / bf16 rounding (or fp32 logits and the per-block
 // (max, lowest index) partials).
-template <int BT, int MODE>
+template <int BT, int MODE, int WAVES = 4>
 __device__ __forceinline__ void mx_gemv_epilogue(const MxArgs& a, const mx_f32x4 (&acc)[BT],
-                                                 mx_f32x4 (&red)[3][BT][64], int lane, int w,
-                                                 int n0, int j, int g, int N, int R) {
+                                                 mx_f32x4 (&red)[WAVES - 1][BT][64], int lane,
+                                                 int w, int n0, int j, int g, int N, int R) {
   if (w > 0) {
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
@@ -80,7 +80,7 @@ __device__ __forceinline__ void mx_gemv_epilogue(const MxArgs& a, const mx_f32x4
     if (16 * bt >= R) break;
     mx_f32x4 tot = acc[bt];
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
+    for (int v = 0; v < WAVES - 1; ++v) {
       const mx_f32x4 p = red[v][bt][lane];
       tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
       tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
@@ -194,9 +194,9 @@ __global__ __launch_bounds__(256) void k_mx_gemv(MxArgs a) {
 // Measured faster for one row tile (B <= 16: QKV 13.0 -> 11.5 us, O
 // 11.0 -> 9.7 us at the 20b shape, B = 16) and slower from BT = 2 on (two
 // sets of BT activation tiles), where k_mx_gemv stays.
-template <int BT, int IT, int MODE>
-__global__ __launch_bounds__(256) void k_mx_gemv_db(MxArgs a) {
-  __shared__ mx_f32x4 red[3][BT][64];
+template <int BT, int IT, int MODE, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_db(MxArgs a) {
+  __shared__ mx_f32x4 red[WAVES - 1][BT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, R = a.B;
@@ -212,13 +212,13 @@ __global__ __launch_bounds__(256) void k_mx_gemv_db(MxArgs a) {
     xrow[bt] = a.x + (size_t)(rv[bt] ? r : R - 1) * K;
   }
   auto load_w = [&](int it, uint4 (&wq)[4]) {
-    const int ch = min(4 * it + w, NCH - 1);
+    const int ch = min(WAVES * it + w, NCH - 1);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       wq[t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
   };
   auto load_x = [&](int it, uint4 (&xq)[BT][4]) {
-    const int base = 128 * (4 * it + w);
+    const int base = 128 * (WAVES * it + w);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const bool ok = base + 32 * t < K;
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(256) void k_mx_gemv_db(MxArgs a) {
       }
     }
   }
-  mx_gemv_epilogue<BT, MODE>(a, acc, red, lane, w, n0, j, g, N, R);
+  mx_gemv_epilogue<BT, MODE, WAVES>(a, acc, red, lane, w, n0, j, g, N, R);
 }
 
 // k_mx_gemv over the packed weights with the activation rows in the packed
@@ -267,10 +267,13 @@ __global__ __launch_bounds__(256) void k_mx_gemv_db(MxArgs a) {
 // starts.  Same lane map and the same order of every fp32 addition as
 // k_mx_gemv, so the same bits.  Measured at the 20b shape, B = 16 / 32 / 64:
 // QKV 11.6 / 19.4 / 38.2 -> 9.8 / 13.9 / 23.3 us, lm_head 276 / 405 / 753 ->
-// 245 / 293 / 582 us.
-template <int BT, int IT, int MODE>
-__global__ __launch_bounds__(256) void k_mx_gemv_px(MxArgs a) {
-  __shared__ mx_f32x4 red[3][BT][64];
+// 245 / 293 / 582 us (377 us at B = 64 with 8 waves).  The O projection
+// (K = 4096, 8 iterations) runs faster with all of its weights requested at
+// the start (DEEP): 10.4 / 16.0 / 28.3 -> 9.5 / 12.9 / 19.9 us; QKV does not
+// (34.0 us at B = 64).
+template <int BT, int IT, int MODE, int WAVES, bool DEEP = false>
+__global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_px(MxArgs a) {
+  __shared__ mx_f32x4 red[WAVES - 1][BT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, R = a.B;
@@ -278,24 +281,28 @@ __global__ __launch_bounds__(256) void k_mx_gemv_px(MxArgs a) {
   const int NCH = (K + 127) / 128;
   const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
   const uint16_t* X = a.xp;
-  auto load_w = [&](int it, uint4 (&wq)[4]) {
-    const int ch = min(4 * it + w, NCH - 1);
+  // weights DEPTH iterations ahead: one (two register sets), or all of the
+  // wave's at the start (DEEP)
+  constexpr int DEPTH = DEEP ? IT : 1;
+  uint4 wq[DEPTH + 1][4];
+  auto load_w = [&](int it, uint4 (&dst)[4]) {
+    const int ch = min(WAVES * it + w, NCH - 1);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
-      wq[t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
+      dst[t] = mx_load_nt(P + ((((size_t)blockIdx.x * NCH + ch) * 4 + t) * 64 + lane) * 8);
   };
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) load_w(d, wq[d]);
   mx_f32x4 acc[BT];
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  uint4 wc[4], wn[4];
-  load_w(0, wc);
 #pragma unroll
   for (int it = 0; it < IT; ++it) {
-    if (it + 1 < IT) load_w(it + 1, wn);
+    if (it + DEPTH < IT) load_w(it + DEPTH, wq[(it + DEPTH) % (DEPTH + 1)]);
     // chunks past K: a zero A operand (the packed rows are zero past K only
     // up to the last chunk)
-    const bool okc = 4 * it + w < NCH;
-    const int ch = min(4 * it + w, NCH - 1);
+    const bool okc = WAVES * it + w < NCH;
+    const int ch = min(WAVES * it + w, NCH - 1);
     uint4 xq[BT][4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -307,19 +314,15 @@ __global__ __launch_bounds__(256) void k_mx_gemv_px(MxArgs a) {
       }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const mx_bf16x8 bw = mx_as_bf16x8(wc[t]);
+      const mx_bf16x8 bw = mx_as_bf16x8(wq[it % (DEPTH + 1)][t]);
 #pragma unroll
       for (int bt = 0; bt < BT; ++bt)
         if (16 * bt < R)
           acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(xq[bt][t]), bw, acc[bt],
                                                             0, 0, 0);
     }
-    if (it + 1 < IT) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) wc[t] = wn[t];
-    }
   }
-  mx_gemv_epilogue<BT, MODE>(a, acc, red, lane, w, n0, j, g, N, R);
+  mx_gemv_epilogue<BT, MODE, WAVES>(a, acc, red, lane, w, n0, j, g, N, R);
 }
 
 // Standalone MXFP4 GEMV on the matrix cores (neon_mxfp4_gemv at B >= 16):
@@ -604,7 +607,7 @@ __global__ __launch_bounds__(64) void k_mx_attn(
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     const int32_t* __restrict__ seq, float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv, int G,
-    int T_max, int key_mask, int window, int S, int q_stride) {
+    int T_max, int key_mask, int window, int S, int q_stride, uint16_t* __restrict__ outp) {
   constexpr int VT = 64 + 8;
   __shared__ __align__(16) uint16_t ks[64 * 64];
   __shared__ __align__(16) uint16_t vt[64 * VT];
@@ -725,6 +728,9 @@ __global__ __launch_bounds__(64) void k_mx_attn(
       const uint32_t w0 = pack_bf2(o[dt][0] * f * inv, o[dt][1] * f * inv);
       const uint32_t w1 = pack_bf2(o[dt][2] * f * inv, o[dt][3] * f * inv);
       *reinterpret_cast<uint2*>(dst + 16 * dt + 4 * gq) = make_uint2(w0, w1);
+      if (outp != nullptr)  // 4 columns of one unit: contiguous in the packed layout
+        *reinterpret_cast<uint2*>(outp + mx_packed_at(b, 64 * h + 16 * dt + 4 * gq, Hq / 2)) =
+            make_uint2(w0, w1);
     }
   } else {
     const size_t pi = ((size_t)b * Hq + h) * S + sp;
@@ -740,7 +746,7 @@ void launch_mx_attn(const AttnArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;
   hipLaunchKernelGGL(k_mx_attn, dim3(a.Hkv * a.S, a.B), dim3(64), 0, st, a.q, a.kc, a.vc,
                      a.pos, a.seq, a.part_o, a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G,
-                     a.T_max, a.key_mask, a.window, a.S, a.q_stride);
+                     a.T_max, a.key_mask, a.window, a.S, a.q_stride, a.out_packed);
   if (a.S > 1) launch_attn_merge(a, st);
 }
 
@@ -790,18 +796,34 @@ __global__ __launch_bounds__(256) void k_mx_rope_append(
 template <int MODE, int BT, bool PK>
 static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
   const int it = (a.K / 32 + 15) / 16;
+  if (PK && a.xp != nullptr && MODE == MX_LOGITS && BT >= 3) {
+    // lm_head from 33 rows on: 8 waves split K (4 iterations each at K <= 4096);
+    // 582 -> 377 us at the 20b shape, B = 64 (equal at B = 32)
+    const int it8 = ((a.K + 127) / 128 + 7) / 8;
+    if (it8 <= 2) hipLaunchKernelGGL((k_mx_gemv_px<BT, 2, MODE, 8>), grid, dim3(512), 0, st, a);
+    else if (it8 <= 4) hipLaunchKernelGGL((k_mx_gemv_px<BT, 4, MODE, 8>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_px<BT, 8, MODE, 8>), grid, dim3(512), 0, st, a);
+    return;
+  }
+  if (PK && a.xp != nullptr && MODE == MX_RESID) {
+    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_px<BT, 2, MODE, 4, true>), grid, dim3(256), 0, st, a);
+    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_px<BT, 4, MODE, 4, true>), grid, dim3(256), 0, st, a);
+    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_px<BT, 6, MODE, 4, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_px<BT, 8, MODE, 4, true>), grid, dim3(256), 0, st, a);
+    return;
+  }
   if (PK && a.xp != nullptr) {
-    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_px<BT, 2, MODE>), grid, dim3(256), 0, st, a);
-    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_px<BT, 4, MODE>), grid, dim3(256), 0, st, a);
-    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_px<BT, 6, MODE>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_mx_gemv_px<BT, 8, MODE>), grid, dim3(256), 0, st, a);
+    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_px<BT, 2, MODE, 4>), grid, dim3(256), 0, st, a);
+    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_px<BT, 4, MODE, 4>), grid, dim3(256), 0, st, a);
+    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_px<BT, 6, MODE, 4>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_px<BT, 8, MODE, 4>), grid, dim3(256), 0, st, a);
     return;
   }
   if (BT == 1 && PK) {
-    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_db<1, 2, MODE>), grid, dim3(256), 0, st, a);
-    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_db<1, 4, MODE>), grid, dim3(256), 0, st, a);
-    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_db<1, 6, MODE>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_mx_gemv_db<1, 8, MODE>), grid, dim3(256), 0, st, a);
+    if (it <= 2) hipLaunchKernelGGL((k_mx_gemv_db<1, 2, MODE, 4>), grid, dim3(256), 0, st, a);
+    else if (it <= 4) hipLaunchKernelGGL((k_mx_gemv_db<1, 4, MODE, 4>), grid, dim3(256), 0, st, a);
+    else if (it <= 6) hipLaunchKernelGGL((k_mx_gemv_db<1, 6, MODE, 4>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_mx_gemv_db<1, 8, MODE, 4>), grid, dim3(256), 0, st, a);
     return;
   }
   if (it <= 2) hipLaunchKernelGGL((k_mx_gemv<BT, 2, MODE, PK>), grid, dim3(256), 0, st, a);
