@@ -141,31 +141,87 @@ __device__ __forceinline__ void fp4x16_to_bf16(u32x2_t c, uint32_t s, u32x4_t& l
   hi = u32x4_t{o[4], o[5], o[6], o[7]};
 }
 
+// What the epilogue of a 128 x 128 tile reads besides the accumulators,
+// fetched when the block starts (gemm_epi_issue) so that the epilogue does
+// not wait on dependent loads one 32 x 32 block at a time (measured: 15 of
+// the 61 us a gate_up block of the MXFP8 expert GEMM lived): the lane's two
+// column biases, and for the scatter epilogue the (token, slot) of every row
+// of the tile (thread t < kGM holds row t's; gemm_epi_stage puts them in LDS
+// after the K loop).
+struct GemmEpi {
+  float bcol[2];
+  uint32_t tok, slot;  // scatter: row threadIdx.x's (token, slot), threads < kGM
+};
+struct GemmEpiLds {
+  int32_t tok[kGM], slot[kGM];
+};
+
+template <int MODE, bool GROUPED>
+__device__ __forceinline__ void gemm_epi_issue(const GemmParams& p, int lane, int wn, int n0,
+                                               int r0, int rows, int e, GemmEpi& ep,
+                                               GemmEpiLds& el) {
+  const uint16_t* bias = p.bias ? p.bias + (GROUPED ? (size_t)e * p.N : 0) : nullptr;
+#pragma unroll
+  for (int in = 0; in < 2; ++in) {
+    const int col = n0 + wn * 64 + in * 32 + (lane & 31);
+    ep.bcol[in] = (bias && col < p.N) ? bf2f(load_pinned_u16(bias + col)) : 0.0f;
+  }
+  if (MODE == GEMM_SCATTER) {  // every thread loads (threads >= kGM repeat row kGM - 1)
+    const size_t gr = (size_t)r0 + min(min((int)threadIdx.x, kGM - 1), rows - 1);
+    ep.tok = load_pinned_u32(reinterpret_cast<const uint32_t*>(p.list_tok + gr));
+    ep.slot = load_pinned_u32(reinterpret_cast<const uint32_t*>(p.list_slot + gr));
+  }
+}
+
+// After the K loop: the scatter rows' (token, slot) into LDS for the epilogue.
+template <int MODE>
+__device__ __forceinline__ void gemm_epi_stage(const GemmEpi& ep, GemmEpiLds& el) {
+  if (MODE != GEMM_SCATTER) return;
+  if (threadIdx.x < kGM) {
+    el.tok[threadIdx.x] = (int32_t)ep.tok;
+    el.slot[threadIdx.x] = (int32_t)ep.slot;
+  }
+  __syncthreads();
+}
+
 // Epilogue of the 128 x 128 GEMM tiles (both operand kinds): acc[im][in][i]
 // is row 8 (i/4) + 4 (lane/32) + i%4, column lane%32 of the wave's 32 x 32
-// block (im, in) -- the D layout of the 32 x 32 MFMA shapes.
+// block (im, in) -- the D layout of the 32 x 32 MFMA shapes.  el was written
+// by gemm_epi_stage.
 template <int MODE, bool GROUPED>
 __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[2][2], const GemmParams& p,
                                               int lane, int wm, int wn, int n0, int r0,
-                                              int rows, int e) {
-  const uint16_t* bias = p.bias ? p.bias + (GROUPED ? (size_t)e * p.N : 0) : nullptr;
+                                              int rows, const GemmEpi& ep,
+                                              const GemmEpiLds& el) {
+  const bool has_bias = p.bias != nullptr;
 #pragma unroll
   for (int im = 0; im < 2; ++im)
 #pragma unroll
     for (int in = 0; in < 2; ++in) {
       const int col = n0 + wn * 64 + in * 32 + (lane & 31);
-      const float bcol = (bias && col < p.N) ? bf2f(bias[col]) : 0.0f;
+      const float bcol = ep.bcol[in];
+      if constexpr (MODE == GEMM_SWIGLU) {
+        // gate (even column) and up (odd column) sit in adjacent lanes, and
+        // values i, i + 1 are rows r, r + 1: the even lane keeps row r's
+        // gate and receives its up, the odd lane keeps row r + 1's up and
+        // receives its gate, so every lane forms one SwiGLU per two values
+        const bool odd = (lane & 1) != 0;
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const int r = wm * 64 + im * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + (odd ? 1 : 0);
+          const float v0 = has_bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
+          const float v1 = has_bias ? __fadd_rn(acc[im][in][i + 1], bcol) : acc[im][in][i + 1];
+          const float got = __shfl_xor(odd ? v0 : v1, 1, 64);
+          const float gate = odd ? got : v0, up = odd ? v1 : got;
+          if (r < rows && (col | 1) < p.N)
+            p.C[(size_t)(r0 + r) * p.ldc + col / 2] = f2bf(swiglu_clamp_p(gate, up, p.alpha, p.limit));
+        }
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = wm * 64 + im * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-        const float v = bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
-        if (MODE == GEMM_SWIGLU) {
-          // gate (even column) and up (odd column) sit in adjacent lanes
-          const float u = __shfl_xor(v, 1, 64);
-          if ((lane & 1) == 0 && r < rows && col + 1 < p.N)
-            p.C[(size_t)(r0 + r) * p.ldc + col / 2] = f2bf(swiglu_clamp_p(v, u, p.alpha, p.limit));
-          continue;
-        }
+        const float v = has_bias ? __fadd_rn(acc[im][in][i], bcol) : acc[im][in][i];
         if (r >= rows || col >= p.N) continue;
         const size_t gr = (size_t)(r0 + r);
         if (MODE == GEMM_STORE) {
@@ -176,8 +232,8 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[2][2], const
         } else if (MODE == GEMM_F32) {
           p.Cf[gr * p.ldc + col] = v;
         } else {  // GEMM_SCATTER
-          const int t = p.list_tok[gr], s = p.list_slot[gr];
-          p.ybuf[((size_t)t * p.topk + s) * p.N + col] = v;
+          const int t = el.tok[r], sl = el.slot[r];
+          p.ybuf[((size_t)t * p.topk + sl) * p.N + col] = v;
         }
       }
     }
@@ -202,6 +258,9 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
     rows = min(kGM, p.M - r0);
   }
   const int K = p.K;
+  __shared__ GemmEpiLds epl;
+  GemmEpi ep;
+  gemm_epi_issue<MODE, GROUPED>(p, lane, wn, n0, r0, rows, e, ep, epl);
   // this thread's staging rows: A/W chunk c = tid + 256 i (i = 0, 1):
   // row c >> 2, k (c & 3) * 8; FP4 W: row tid >> 1, k half (tid & 1) * 16
   // staging: thread tid copies the 8-element piece (tid & 7) of rows
@@ -307,7 +366,8 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
   }
 #undef GEMM_STAGE
 
-  gemm_epilogue<MODE, GROUPED>(acc, p, lane, wm, wn, n0, r0, rows, e);
+  gemm_epi_stage<MODE>(ep, epl);
+  gemm_epilogue<MODE, GROUPED>(acc, p, lane, wm, wn, n0, r0, rows, ep, epl);
 }
 
 // ===========================================================================
@@ -429,6 +489,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mx8(GemmParams p) {
   const int e = p.tile_e[blockIdx.y];
   const int r0 = p.e_off[e] + p.tile_r0[blockIdx.y];
   const int rows = min(kGM, p.e_off[e + 1] - r0);
+  __shared__ GemmEpiLds epl;
+  GemmEpi ep;
+  gemm_epi_issue<MODE, true>(p, lane, wn, n0, r0, rows, e, ep, epl);
   const int K = p.K, KB = K / 32, KS = K / 64;
   const int nk = KS;
   // staging map shared by A and B: piece c = tid + 256 i (i = 0..3) is row /
@@ -576,7 +639,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_mx8(GemmParams p) {
 #undef MX8_LOAD_B
 #undef MX8_STAGE_A
 #undef MX8_STAGE_B
-  gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, e);
+  gemm_epi_stage<MODE>(ep, epl);
+  gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, ep, epl);
 }
 
 static void launch_gemm_narrow_f32(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
