@@ -937,7 +937,8 @@ static neon_status ensure_prefill_scratch(neon_ctx* ctx, int rows, hipStream_t s
   // MXFP8 images of the expert GEMM inputs (NEON_PREFILL_MX8): xn rows, then
   // the act rows, in the same buffers
   const size_t qn = std::max(M * H, M * k * I);
-  const size_t o_mxq = take(2 * qn), o_mxqs = take(qn / 16);
+  const size_t o_mxq = take(2 * qn),
+               o_mxqs = take(std::max(mx8_scale_bytes(M, H), mx8_scale_bytes(M * k, I)));
   if (ctx->pf) {
     HIPCHK(ctx, hipStreamSynchronize(st));  // earlier prefill work may still read it
     (void)hipFree(ctx->pf);
@@ -1720,7 +1721,8 @@ static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const
   auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
   const size_t o_yb = take(pairs * H * 4), o_act = take(pairs * I * 2), o_lt = take(pairs * 4),
                o_ls = take(pairs * 4), o_eo = take((E + 1) * 4), o_te = take(tiles * 4),
-               o_tr = take(tiles * 4), o_nt = take(16), o_q = take(2 * qn), o_qs = take(qn / 16);
+               o_tr = take(tiles * 4), o_nt = take(16), o_q = take(2 * qn),
+               o_qs = take(mx8 ? std::max(mx8_scale_bytes(M, H), mx8_scale_bytes(pairs, I)) : 0);
   char* scratch = nullptr;
   if (hipMallocAsync((void**)&scratch, off, st) != hipSuccess)
     KFAIL(NEON_ENOMEM, "%s: scratch allocation failed", fn);

@@ -329,6 +329,10 @@ int moe_prefill_max_tiles(int M, int k, int E);
 // arrays (the kernel-level layout), or (q, qs) step lines for the GEMMs
 void launch_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi, uint8_t* lo,
                       uint8_t* s_hi, uint8_t* s_lo, hipStream_t st);
+// scale dwords per row of the step-line layout (K / 64 steps, rounded up to
+// a multiple of 4) and the bytes of rows such rows
+__host__ __device__ inline int mx8_scale_stride(int K) { return ((K / 64) + 3) & ~3; }
+inline size_t mx8_scale_bytes(size_t rows, int K) { return rows * (size_t)mx8_scale_stride(K) * 4; }
 void launch_mx8_quant_lines(const uint16_t* x, int64_t rows, int K, uint8_t* q, uint32_t* qs,
                             hipStream_t st);
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st);
