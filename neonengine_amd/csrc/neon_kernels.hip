@@ -1731,6 +1731,9 @@ __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
 
 // Top-k of every row (k_topk's ranking) and the matrix-core experts' route
 // lists (mx_route_lists) in one launch: wave w of 16 ranks rows w, w + 16, ...
+// Each pass requests the logits of the wave's next 4 rows together and then
+// ranks them, so a batch of 64 waits for one load round trip instead of 4
+// (13.4 us per launch at batch 64 before).
 __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ lg, int B, int E,
                                                      int k, int32_t* __restrict__ idx,
                                                      float* __restrict__ score, int S,
@@ -1739,13 +1742,23 @@ __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ l
   __shared__ int32_t pair_e[256];
   __shared__ int cnt_e[256], slot_of[256], wave_used[4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int b = w; b < B; b += 16) {
-    wave_topk<true>(lg + (size_t)b * E, E, k, lane, t[w]);
-    if (lane < k) {
-      const int32_t id = t[w].id[lane];
-      idx[b * k + lane] = id;
-      score[b * k + lane] = t[w].sc[lane];
-      pair_e[b * k + lane] = id;
+  for (int b0 = w; b0 < B; b0 += 64) {
+    float v[4][kRouteQ];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)  // rows past B re-read row B - 1 (never ranked)
+      wave_topk_issue(lg + (size_t)min(b0 + 16 * i, B - 1) * E, E, lane, v[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = b0 + 16 * i;
+      if (b >= B) break;  // uniform for the wave
+      wave_topk_rank<true>(v[i], E, k, lane, t[w]);
+      if (lane < k) {
+        const int32_t id = t[w].id[lane];
+        idx[b * k + lane] = id;
+        score[b * k + lane] = t[w].sc[lane];
+        pair_e[b * k + lane] = id;
+      }
+      wave_lds_sync();  // every lane has read t[w] before the next row's ranking writes it
     }
   }
   __syncthreads();
