@@ -186,6 +186,11 @@ neon_status neon_set_sampling(neon_ctx* ctx, float temperature, float top_p,
  *               min(n_experts, batch top_k): used expert of slot y (ascending,
  *               -1 past the used ones), its pair count, then its pairs
  *               q = b top_k + s in ascending order (64 entries per slot)
+ *   "mx_items"  after the same steps: the expert kernels' work items, int32
+ *               [257]: the count n, then n items (slot | group << 8 |
+ *               expert << 10 | min(pair count, 64) << 19), group 0 of every
+ *               used slot first, then group 1 (pairs 16 .. 31) of the slots
+ *               with more than 16 pairs, and so on
  * `bytes` must equal the buffer's size. */
 neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
                                  size_t bytes, void* stream);

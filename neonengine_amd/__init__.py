@@ -420,6 +420,12 @@ class Engine:
                                                  out.ctypes.data_as(C.c_void_p), out.nbytes,
                                                  _stream(stream)))
             return out
+        if name == "mx_items":  # count, then up to 256 packed work items
+            out = np.empty(257, np.int32)
+            self._chk(lib().neon_read_activation(self._ctx, name.encode(),
+                                                 out.ctypes.data_as(C.c_void_p), out.nbytes,
+                                                 _stream(stream)))
+            return out
         width = {"hidden": c.hidden, "moe_in": c.hidden, "moe_idx": c.top_k,
                  "moe_score": c.top_k, "qkv": (c.n_heads + 2 * c.n_kv_heads) * c.head_dim,
                  "attn_out": c.n_heads * c.head_dim}[name]

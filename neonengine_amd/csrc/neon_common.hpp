@@ -201,6 +201,25 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
 // ascending q.  Every thread of the block calls it (threads 0 .. 255 work);
 // cnt_e / slot_of hold 256 ints, wave_used 4, all in LDS.  Slots come from a
 // lane-parallel ballot prefix over the 256 expert flags.
+// It also lists the expert kernels' work items, one per (slot, group of 16
+// pairs): route[kMxItemOff] = the item count n, route[kMxItemOff + 1 + y]
+// (y < n) = item y packed by mx_item_pack.  Group 0 of every used slot comes
+// first (item y = slot y), then group 1 of the slots with more than 16 pairs,
+// and so on, so a launch has one block row per item instead of one per
+// (slot, possible group).  n <= (nk + 15 S) / 16 <= 256.
+constexpr int kMxItemOff = 66 * 256;
+constexpr int kMxRouteWords = kMxItemOff + 1 + 256;
+__host__ __device__ __forceinline__ int32_t mx_item_pack(int slot, int grp, int e, int cnt) {
+  return slot | (grp << 8) | (e << 10) | (cnt << 19);  // 8 + 2 + 9 + 7 bits
+}
+__host__ __device__ __forceinline__ void mx_item_unpack(int32_t v, int& slot, int& grp, int& e,
+                                                        int& cnt) {
+  slot = v & 255; grp = (v >> 8) & 3; e = (v >> 10) & 511; cnt = (v >> 19) & 127;
+}
+// Block rows a launch needs to cover every item (the bound above).
+__host__ __device__ __forceinline__ int mx_item_rows(int nk, int S) {
+  return (nk + 15 * S) / 16 < 256 ? (nk + 15 * S) / 16 : 256;
+}
 __device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E, int S,
                                                int32_t* __restrict__ route, int* cnt_e,
                                                int* slot_of, int* wave_used) {
@@ -235,6 +254,23 @@ __device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E
     for (int q = 0; q < t; ++q) r += ids[q] == e;
     route[2 * S + 64 * slot_of[e] + r] = t;
   }
+  // work items, group by group (every thread reaches each barrier)
+  int base = 0;
+  for (int q = 0; q < 4; ++q) {
+    const bool has = t < 256 && c > 16 * q;
+    const unsigned long long bq = __ballot(has);
+    __syncthreads();  // the previous reads of wave_used are done
+    if (t < 256 && lane == 0) wave_used[w] = __popcll(bq);
+    __syncthreads();
+    if (has) {
+      const int before = (w > 0 ? wave_used[0] : 0) + (w > 1 ? wave_used[1] : 0) +
+                         (w > 2 ? wave_used[2] : 0);
+      const int y = base + before + __popcll(bq & ((1ull << lane) - 1ull));
+      route[kMxItemOff + 1 + y] = mx_item_pack(slot_of[t], q, t, c < 64 ? c : 64);
+    }
+    base += wave_used[0] + wave_used[1] + wave_used[2] + wave_used[3];
+  }
+  if (t == 0) route[kMxItemOff] = base;
 }
 
 // A load that stays where it is written.  The compiler sinks a plain load

@@ -419,7 +419,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
                o_mxv = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
                o_mxi = take(Bm > 1 ? Bm * (size_t)(c.vocab / 16) * 4 : 0),
-               o_mxr = take(Bm > 1 ? (size_t)66 * 256 * 4 : 0),
+               o_mxr = take(Bm > 1 ? (size_t)kMxRouteWords * 4 : 0),
                o_mxp = take(Bm > 1 ? (size_t)((Bm + 15) / 16) * ((H + 127) / 128) * 2048 * 2 : 0),
                o_mxa = take(Bm > 1 ? (size_t)((Bm + 15) / 16) * ((c.n_heads * c.head_dim + 127) / 128) * 2048 * 2 : 0),
                o_lg = take(Bm * (size_t)c.vocab * 4),
@@ -1297,6 +1297,13 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
            "of two or more sequences");
     const size_t S = std::min<size_t>(c.n_experts, B * c.top_k);
     src = ctx->mx_route; n = (2 * S + 64 * S) * 4;
+  }
+  else if (nm == "mx_items") {
+    if (ctx->mx_route == nullptr || B < 2 ||
+        (ctx->decode_mode != NEON_DECODE_MATRIX && ctx->decode_mode != NEON_DECODE_MATRIX_MX8))
+      FAIL(ctx, NEON_EINVAL, "neon_read_activation: 'mx_items' exists after matrix-core steps "
+           "of two or more sequences");
+    src = ctx->mx_route + kMxItemOff; n = (kMxRouteWords - kMxItemOff) * 4;
   }
   else FAIL(ctx, NEON_EINVAL, "neon_read_activation: unknown buffer '%s'", name);
   if (bytes != n)

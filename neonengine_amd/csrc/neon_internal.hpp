@@ -189,8 +189,10 @@ struct MxArgs {
   const void* Wp;            // the same weights in MFMA lane order (mx_pack_*), or NULL
   const uint8_t* sp;         // packed MXFP4 scales (with Wp, expert modes)
   const int32_t* route;      // expert modes: used experts, counts, pair lists
-                             // [2 S + 64 S] ints, S = min(E, B k), written by
-                             // launch_mx_moe before the expert kernels
+                             // [2 S + 64 S] ints, S = min(E, B k), and the work
+                             // items at kMxItemOff (kMxRouteWords ints in all),
+                             // written by launch_topk_route before the expert
+                             // kernels
   int B, N, K, E, k;
   float alpha, limit;
   // expert modes on the scaled fp8 x fp4 instruction (launch_mx_moe8): the

@@ -459,6 +459,24 @@ void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const u
 // waves in flight beat the activation reuse of wider waves.
 constexpr int kMxMoeTiles = 1, kMxMoeRows = 64 * kMxMoeTiles;
 
+// The work item of block row blockIdx.y (one load: the item count and the
+// packed item are read together, the item slot in bounds for any y < 256).
+// False for rows past the item count and for items whose expert is out of
+// range (a corrupt table: flagged, never read past the experts) or whose
+// group lies past the expert's pairs.
+__device__ __forceinline__ bool mx_block_item(const MxArgs& a, int tid, int& slot, int& grp,
+                                              int& e, int& cnt) {
+  const int n = a.route[kMxItemOff];
+  const int32_t v = a.route[kMxItemOff + 1 + blockIdx.y];
+  if ((int)blockIdx.y >= n) return false;
+  mx_item_unpack(v, slot, grp, e, cnt);
+  if (e >= a.E || slot >= min(a.E, a.B * a.k)) {
+    if (tid == 0) flag_dev_err(a.err, kDevErrExpertId);
+    return false;
+  }
+  return 16 * grp < cnt;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   constexpr int CKU = 16, CK = 32 * CKU, XS = CK + 8;
@@ -467,19 +485,11 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
-  // block row y = slot G + group: rows 16 group .. 16 group + 15 of the
-  // slot's pair list (G = ceil(B / 16) groups per used-expert slot)
-  const int G = (a.B + 15) / 16;
-  const int slot = blockIdx.y / G, grp = blockIdx.y % G;
-  const int S = gridDim.y / G;
-  const int e = a.route[slot];
-  if (e < 0) return;  // fewer used experts than slots (uniform)
-  if (e >= a.E) {     // a corrupt route table: never read past the experts
-    if (tid == 0) flag_dev_err(a.err, kDevErrExpertId);
-    return;
-  }
-  const int Rall = min(a.route[S + slot], 64);
-  if (16 * grp >= Rall) return;  // (uniform)
+  // block row y = work item y of the route table: rows 16 group .. 16 group
+  // + 15 of the slot's pair list
+  int slot, grp, e, Rall;
+  if (!mx_block_item(a, tid, slot, grp, e, Rall)) return;  // (uniform)
+  const int S = min(a.E, a.B * a.k);
   const int R = min(16, Rall - 16 * grp);
   const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
   const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;  // the wave's first row
@@ -892,17 +902,9 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
-  const int G = (a.B + 15) / 16;
-  const int slot = blockIdx.y / G, grp = blockIdx.y % G;
-  const int S = gridDim.y / G;
-  const int e = a.route[slot];
-  if (e < 0) return;  // fewer used experts than slots (uniform)
-  if (e >= a.E) {     // a corrupt route table: never read past the experts
-    if (tid == 0) flag_dev_err(a.err, kDevErrExpertId);
-    return;
-  }
-  const int Rall = min(a.route[S + slot], 64);
-  if (16 * grp >= Rall) return;  // (uniform)
+  int slot, grp, e, Rall;
+  if (!mx_block_item(a, tid, slot, grp, e, Rall)) return;  // (uniform)
+  const int S = min(a.E, a.B * a.k);
   const int R = min(16, Rall - 16 * grp);
   const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
   const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;
@@ -1056,13 +1058,13 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
 void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
                     hipStream_t st) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
-  const int G = (gate_up.B + 15) / 16;
+  const int Y = mx_item_rows(gate_up.B * gate_up.k, S);
   down.xq_hi = gate_up.yq_hi; down.xq_lo = gate_up.yq_lo;
   down.xs_hi = gate_up.ys_hi; down.xs_lo = gate_up.ys_lo;
   hipLaunchKernelGGL(k_mx8_moe16<MX_GATE_UP>,
-                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G), dim3(256), 0, st,
+                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, Y), dim3(256), 0, st,
                      gate_up);
-  hipLaunchKernelGGL(k_mx8_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
+  hipLaunchKernelGGL(k_mx8_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, Y),
                      dim3(256), 0, st, down);
   hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
                      down.out_f, score, h, down.N, down.k);
@@ -1071,11 +1073,11 @@ void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h
 void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
                    hipStream_t st) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
-  const int G = (gate_up.B + 15) / 16;
+  const int Y = mx_item_rows(gate_up.B * gate_up.k, S);
   hipLaunchKernelGGL(k_mx_moe16<MX_GATE_UP>,
-                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, S * G), dim3(256), 0, st,
+                     dim3((gate_up.N + kMxMoeRows - 1) / kMxMoeRows, Y), dim3(256), 0, st,
                      gate_up);
-  hipLaunchKernelGGL(k_mx_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, S * G),
+  hipLaunchKernelGGL(k_mx_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, Y),
                      dim3(256), 0, st, down);
   hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
                      down.out_f, score, h, down.N, down.k);

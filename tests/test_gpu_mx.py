@@ -265,7 +265,7 @@ def test_matrix_mode_sampling_reproducible():
     assert (runs[0] >= 0).all() and (runs[0] < cfg.vocab).all()
 
 
-@pytest.mark.parametrize("E,B", [(32, 16), (128, 16), (8, 5)])
+@pytest.mark.parametrize("E,B", [(32, 16), (128, 16), (8, 5), (8, 64), (32, 64)])
 def test_route_lists_match_host(E, B):
     """The route table k_topk_route writes for the matrix-core experts (used
     experts in ascending order, their pair counts and ascending pair lists)
@@ -279,6 +279,7 @@ def test_route_lists_match_host(E, B):
     eng.decode(2)
     idx = eng.read_activation("moe_idx").reshape(-1)
     route = eng.read_activation("mx_route")
+    items = eng.read_activation("mx_items")
     eng.close()
     k = cfg.top_k
     S = min(E, B * k)
@@ -292,3 +293,14 @@ def test_route_lists_match_host(E, B):
             assert list(route[2 * S + 64 * y: 2 * S + 64 * y + len(pairs)]) == pairs, y
         else:
             assert route[y] == -1 and route[S + y] == 0, y
+    # work items: (slot, group of 16 pairs), group 0 of every used slot, then
+    # group 1 of the slots with more than 16 pairs, ...
+    want = []
+    for q in range(4):
+        for y, e in enumerate(used):
+            n = int((idx == e).sum())
+            if n > 16 * q:
+                want.append(y | (q << 8) | (e << 10) | (min(n, 64) << 19))
+    assert items[0] == len(want)
+    assert list(items[1:1 + len(want)]) == want
+    assert len(want) <= (B * k + 15 * S) // 16  # the launch's block rows
