@@ -195,7 +195,8 @@ __device__ __forceinline__ float swiglu_clamp(float g, float u, float alpha,
 }
 
 // Pairs of every used expert for the matrix-core expert kernels, from the
-// experts ids[0 .. nk) of the pairs q = b k + s (nk <= 256, E <= 256):
+// experts ids[0 .. nk) of the pairs q = b k + s (nk <= 256, E <= 256; ids in
+// LDS, 16-byte aligned):
 // route[y] = the y-th used expert (ascending id; -1 past the last),
 // route[S + y] = its pair count, route[2 S + 64 y + r] = its r-th pair in
 // ascending q.  Every thread of the block calls it (threads 0 .. 255 work);
@@ -250,8 +251,18 @@ __device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E
   }
   __syncthreads();
   if (e >= 0) {
+    // rank of pair t among its expert's pairs: the ids before it, read 4 at a
+    // time (ids is 16-byte aligned LDS; every lane reads the same words, a
+    // broadcast), several reads in flight per iteration
+    const int4* iv = reinterpret_cast<const int4*>(ids);
     int r = 0;
-    for (int q = 0; q < t; ++q) r += ids[q] == e;
+    const int t4 = t >> 2;
+#pragma unroll 4
+    for (int q4 = 0; q4 < t4; ++q4) {
+      const int4 v = iv[q4];
+      r += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+    }
+    for (int q = 4 * t4; q < t; ++q) r += ids[q] == e;
     route[2 * S + 64 * slot_of[e] + r] = t;
   }
   // work items, group by group (every thread reaches each barrier)

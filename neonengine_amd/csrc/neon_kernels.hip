@@ -1739,7 +1739,7 @@ __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ l
                                                      float* __restrict__ score, int S,
                                                      int32_t* __restrict__ route) {
   __shared__ TopK t[16];
-  __shared__ int32_t pair_e[256];
+  __shared__ __align__(16) int32_t pair_e[256];
   __shared__ int cnt_e[256], slot_of[256], wave_used[4];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int b0 = w; b0 < B; b0 += 64) {
