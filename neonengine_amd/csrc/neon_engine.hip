@@ -133,6 +133,7 @@ struct neon_ctx {
   int32_t* mx_route = nullptr;       // used experts and their pair lists
   uint16_t* mx_xp = nullptr;         // normalised rows in the packed activation layout
   uint16_t* mx_ap = nullptr;         // attention output in the packed activation layout
+  bool mx_fuse_rope = true;          // RoPE + KV append inside the attention launch
   // the weights in MFMA lane order for the matrix-core steps (allocated when
   // that mode is first selected; refreshed before a step after any change)
   struct MxLayer { uint16_t *wqkv, *wo; uint8_t *gu_c, *gu_s, *dn_c, *dn_s; };
@@ -461,6 +462,8 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
     ctx->mx_xp = (uint16_t*)(W + o_mxp);
     ctx->mx_ap = (uint16_t*)(W + o_mxa);
   }
+  const char* fr_env = getenv("NEON_MX_FUSE_ROPE");
+  ctx->mx_fuse_rope = !(fr_env && fr_env[0] == '0');
   // ---- RoPE table ----
   std::vector<float> ct, st;
   rope_table_host(&c, c.max_seq, ct, st);
@@ -751,16 +754,22 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     q.y = ctx->qkv;
     q.B = B; q.N = qkv_rows; q.K = H;
     launch_mx_gemv(q, 0, st);
-    launch_mx_rope_append(ctx->qkv, ctx->pos, nullptr, ctx->cos_t, ctx->sin_t, ctx->q_rot, kc_l,
-                          vc_l, B, c.n_heads, c.n_kv_heads, ctx->kv_rows[l], ctx->kv_mask[l],
-                          st);
+    // RoPE and the KV append inside the attention launch (NEON_MX_FUSE_ROPE=0:
+    // a launch of their own before it; the same bits either way)
+    if (!ctx->mx_fuse_rope)
+      launch_mx_rope_append(ctx->qkv, ctx->pos, nullptr, ctx->cos_t, ctx->sin_t, ctx->q_rot, kc_l,
+                            vc_l, B, c.n_heads, c.n_kv_heads, ctx->kv_rows[l], ctx->kv_mask[l],
+                            st);
     AttnArgs a;
-    a.q = ctx->q_rot; a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
+    a.q = ctx->mx_fuse_rope ? ctx->qkv : ctx->q_rot;
+    a.kc = kc_l; a.vc = vc_l; a.sinks = w.sinks; a.pos = ctx->pos;
     a.out = ctx->attn_out; a.part_o = ctx->attn_po; a.part_ml = ctx->attn_pml; a.seq = nullptr;
     a.B = B; a.Hq = c.n_heads; a.Hkv = c.n_kv_heads;
     a.T_max = ctx->kv_rows[l]; a.key_mask = ctx->kv_mask[l];
     a.window = sliding ? c.sliding_window : 0;
-    a.S = sliding ? ctx->s_slide : ctx->s_full; a.q_stride = c.n_heads * D;
+    a.S = sliding ? ctx->s_slide : ctx->s_full;
+    a.q_stride = ctx->mx_fuse_rope ? qkv_rows : c.n_heads * D;
+    if (ctx->mx_fuse_rope) { a.rope_cos = ctx->cos_t; a.rope_sin = ctx->sin_t; }
     // the O projection reads a packed copy of the attention output (rows of
     // Hq D = a multiple of 128 columns, so no column padding)
     const bool ap = mp.wo != nullptr && (c.n_heads * D) % 128 == 0;

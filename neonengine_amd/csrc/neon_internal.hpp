@@ -266,6 +266,14 @@ struct AttnArgs {
   // matrix-core steps (launch_mx_attn): the output also in the packed
   // activation layout (K = Hq D, a multiple of 128) for the O projection, or NULL
   uint16_t* out_packed = nullptr;
+  // matrix-core steps: q is the projection's raw output row ([B][q_stride],
+  // q_stride = (Hq + 2 Hkv) D, q heads then k then v) and the attention
+  // kernel rotates q itself and, in the block that holds position pos[b],
+  // rotates k and appends k and v to the caches (launch_mx_rope_append's
+  // arithmetic); cos / sin are the RoPE tables [max_seq][D / 2].  NULL: q is
+  // already rotated and the new key already appended.
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
 };
 // ints between consecutive arrival counters (one 256-byte line each)
 constexpr int kAttnArriveStride = 64;

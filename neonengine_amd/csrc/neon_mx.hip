@@ -612,12 +612,33 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
 // masked, online softmax per head, O^T += V^T P^T with P in bf16 hi + lo.
 // One split finishes with the sink here; several leave (o, m, l) partials in
 // the exact kernels' layout for k_attn_merge.
+// RoPE of dims f, f + 1 (a, packed bf16) with their partners f + 32, f + 33
+// (c): rope_pair at the position whose table rows cp / sp are given.
+__device__ __forceinline__ void mx_rope2(uint32_t& a, uint32_t& c, const float* cp,
+                                         const float* sp, int f) {
+  float o1a, o2a, o1b, o2b;
+  rope_pair(bf_lo(a), bf_lo(c), cp[f], sp[f], o1a, o2a);
+  rope_pair(bf_hi(a), bf_hi(c), cp[f + 1], sp[f + 1], o1b, o2b);
+  a = (uint32_t)f2bf(o1a) | ((uint32_t)f2bf(o1b) << 16);
+  c = (uint32_t)f2bf(o2a) | ((uint32_t)f2bf(o2b) << 16);
+}
+// dims f0 .. f0 + 7 (x1) and their partners f0 + 32 .. f0 + 39 (x2)
+__device__ __forceinline__ void mx_rope8(uint4& x1, uint4& x2, const float* cp, const float* sp,
+                                         int f0) {
+  mx_rope2(x1.x, x2.x, cp, sp, f0);
+  mx_rope2(x1.y, x2.y, cp, sp, f0 + 2);
+  mx_rope2(x1.z, x2.z, cp, sp, f0 + 4);
+  mx_rope2(x1.w, x2.w, cp, sp, f0 + 6);
+}
+
 __global__ __launch_bounds__(64) void k_mx_attn(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
     const int32_t* __restrict__ seq, float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv, int G,
-    int T_max, int key_mask, int window, int S, int q_stride, uint16_t* __restrict__ outp) {
+    int T_max, int key_mask, int window, int S, int q_stride, uint16_t* __restrict__ outp,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    uint16_t* __restrict__ kc_w, uint16_t* __restrict__ vc_w) {
   constexpr int VT = 64 + 8;
   __shared__ __align__(16) uint16_t ks[64 * 64];
   __shared__ __align__(16) uint16_t vt[64 * VT];
@@ -637,6 +658,45 @@ __global__ __launch_bounds__(64) void k_mx_attn(
     qf[h2] = hv ? *reinterpret_cast<const uint4*>(q + (size_t)b * q_stride + (size_t)h * 64 +
                                                   32 * h2 + 8 * gq)
                 : make_uint4(0u, 0u, 0u, 0u);
+  // Raw projection output (cos_t given): the lane's q dims 8 gq + e and
+  // 32 + 8 gq + e are RoPE partners, rotated here.  The block whose split
+  // holds position p (the last: its last chunk ends at p) also rotates the
+  // kv head's new key, appends key and value to the caches, and stages them
+  // for every key index >= p (keys past p are masked) instead of reading
+  // them back.  Each rotation is rope_pair at position p, as in
+  // k_mx_rope_append, so the bits are those of the separate launch.
+  const bool fused = cos_t != nullptr;
+  const bool owner = fused && sp == S - 1;
+  uint4 knew = make_uint4(0u, 0u, 0u, 0u), vnew = knew;
+  const int dql = (lane & 7) * 8;  // the 8 dims this lane stages for every key
+  if (fused) {
+    const float* cp = cos_t + (size_t)p * 32;
+    const float* spn = sin_t + (size_t)p * 32;
+    if (hv) {
+      uint4 q0 = qf[0], q1 = qf[1];
+      mx_rope8(q0, q1, cp, spn, 8 * gq);
+      qf[0] = q0;
+      qf[1] = q1;
+    }
+    if (owner) {
+      // lane stages dims dql .. dql + 7: its partner dims are dql ^ 32
+      const uint16_t* kr = q + (size_t)b * q_stride + (size_t)(Hq + g) * 64;
+      const uint16_t* vr = q + (size_t)b * q_stride + (size_t)(Hq + Hkv + g) * 64;
+      const int f0 = dql & 31;
+      uint4 k1 = *reinterpret_cast<const uint4*>(kr + f0);
+      uint4 k2 = *reinterpret_cast<const uint4*>(kr + f0 + 32);
+      vnew = *reinterpret_cast<const uint4*>(vr + dql);
+      mx_rope8(k1, k2, cp, spn, f0);
+      const bool lo_half = dql < 32;  // the lane's dims are k1's, else k2's
+      knew = make_uint4(lo_half ? k1.x : k2.x, lo_half ? k1.y : k2.y, lo_half ? k1.z : k2.z,
+                        lo_half ? k1.w : k2.w);
+      if (lane < 8) {  // one lane per 8 dims writes the cache row
+        const size_t crow = kv_base + (size_t)(p & key_mask);
+        *reinterpret_cast<uint4*>(kc_w + crow * 64 + dql) = knew;
+        *reinterpret_cast<uint4*>(vc_w + crow * 64 + dql) = vnew;
+      }
+    }
+  }
   mx_f32x4 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -649,8 +709,15 @@ __global__ __launch_bounds__(64) void k_mx_attn(
       const int kl = 8 * i + (lane >> 3), dq = (lane & 7) * 8;
       const int key = min(kb + kl, p);  // keys past p are masked below
       const size_t row = kv_base + (size_t)(key & key_mask);
-      const uint4 kv = *reinterpret_cast<const uint4*>(kc + row * 64 + dq);
-      const uint4 vv = *reinterpret_cast<const uint4*>(vc + row * 64 + dq);
+      const bool fresh = owner && key == p;  // (dq == dql)
+      // both rows loaded, then selected word by word (a select between a
+      // load and a register value would put the value in private memory)
+      const uint4 kg = *reinterpret_cast<const uint4*>(kc + row * 64 + dq);
+      const uint4 vg = *reinterpret_cast<const uint4*>(vc + row * 64 + dq);
+      const uint4 kv = make_uint4(fresh ? knew.x : kg.x, fresh ? knew.y : kg.y,
+                                  fresh ? knew.z : kg.z, fresh ? knew.w : kg.w);
+      const uint4 vv = make_uint4(fresh ? vnew.x : vg.x, fresh ? vnew.y : vg.y,
+                                  fresh ? vnew.z : vg.z, fresh ? vnew.w : vg.w);
       *reinterpret_cast<uint4*>(&ks[kl * 64 + dq]) = kv;
       const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
@@ -756,7 +823,8 @@ void launch_mx_attn(const AttnArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;
   hipLaunchKernelGGL(k_mx_attn, dim3(a.Hkv * a.S, a.B), dim3(64), 0, st, a.q, a.kc, a.vc,
                      a.pos, a.seq, a.part_o, a.part_ml, a.sinks, a.out, a.Hq, a.Hkv, G,
-                     a.T_max, a.key_mask, a.window, a.S, a.q_stride, a.out_packed);
+                     a.T_max, a.key_mask, a.window, a.S, a.q_stride, a.out_packed, a.rope_cos,
+                     a.rope_sin, const_cast<uint16_t*>(a.kc), const_cast<uint16_t*>(a.vc));
   if (a.S > 1) launch_attn_merge(a, st);
 }
 

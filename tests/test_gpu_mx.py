@@ -163,6 +163,35 @@ def test_gpt_oss_20b_width_matrix_steps():
     compare(cfg, 1, 16, 24, 16, fixed_routing=True)
 
 
+@pytest.mark.parametrize("B,plen", [(5, 250), (16, 20)])
+def test_matrix_attention_rope_append_fused_bit_identical(monkeypatch, B, plen):
+    """The matrix-core attention rotates q, and in the block that holds the
+    new position rotates k and appends k and v, instead of a separate
+    launch before it: the logits and ids of every step equal the separate
+    launch's bit for bit (B = 5 crosses the 256-row ring of the sliding
+    layers)."""
+    torch_cuda()
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=B, max_seq=512))
+    rng = np.random.default_rng(11)
+    prompt = rng.integers(0, cfg.vocab, size=(B, plen)).tolist()
+    out = []
+    for fuse in ("0", "1"):
+        monkeypatch.setenv("NEON_MX_FUSE_ROPE", fuse)
+        eng = ne.Engine(cfg)
+        eng.init_random(4)
+        eng.set_decode_mode(ne.DECODE_MATRIX)
+        eng.prefill(prompt)
+        lg = []
+        for _ in range(12):
+            eng.decode(1)
+            lg.append(eng.read_logits())
+        out.append((np.stack(lg), eng.read_tokens()))
+        eng.close()
+    say(f"fused rope/append B={B} prompt={plen}: ids {out[1][1][0, plen:plen + 6].tolist()}")
+    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert np.array_equal(out[0][1], out[1][1])
+
+
 # ---- the expert GEMMs on the scaled fp8 x fp4 instruction (DECODE_MATRIX_MX8)
 @pytest.mark.parametrize("B", [2, 16, 33, 64])
 def test_small_model_matrix_mx8_steps(B):
