@@ -265,21 +265,27 @@ __device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E
     for (int q = 4 * t4; q < t; ++q) r += ids[q] == e;
     route[2 * S + 64 * slot_of[e] + r] = t;
   }
-  // work items, group by group (every thread reaches each barrier)
+  // work items: the four groups' ballots at once; each wave's counts go to
+  // cnt_e[4 q + w] (every thread read its count long before; one barrier)
+  unsigned long long bq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) bq[q] = __ballot(t < 256 && c > 16 * q);
+  __syncthreads();
+  if (t < 256 && lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cnt_e[4 * q + w] = __popcll(bq[q]);
+  }
+  __syncthreads();
   int base = 0;
+#pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const bool has = t < 256 && c > 16 * q;
-    const unsigned long long bq = __ballot(has);
-    __syncthreads();  // the previous reads of wave_used are done
-    if (t < 256 && lane == 0) wave_used[w] = __popcll(bq);
-    __syncthreads();
-    if (has) {
-      const int before = (w > 0 ? wave_used[0] : 0) + (w > 1 ? wave_used[1] : 0) +
-                         (w > 2 ? wave_used[2] : 0);
-      const int y = base + before + __popcll(bq & ((1ull << lane) - 1ull));
+    if (t < 256 && c > 16 * q) {
+      const int before = (w > 0 ? cnt_e[4 * q] : 0) + (w > 1 ? cnt_e[4 * q + 1] : 0) +
+                         (w > 2 ? cnt_e[4 * q + 2] : 0);
+      const int y = base + before + __popcll(bq[q] & ((1ull << lane) - 1ull));
       route[kMxItemOff + 1 + y] = mx_item_pack(slot_of[t], q, t, c < 64 ? c : 64);
     }
-    base += wave_used[0] + wave_used[1] + wave_used[2] + wave_used[3];
+    base += cnt_e[4 * q] + cnt_e[4 * q + 1] + cnt_e[4 * q + 2] + cnt_e[4 * q + 3];
   }
   if (t == 0) route[kMxItemOff] = base;
 }
