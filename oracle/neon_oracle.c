@@ -1044,6 +1044,7 @@ struct or_model {
   int lazy;
   uint64_t seed;
   uint8_t *lz_guc, *lz_gus, *lz_dnc, *lz_dns;
+  int64_t lz_key[64]; /* (layer, expert) held by each slot buffer, -1 none */
   /* last step, batch row 0, last layer: buffers named like the device's */
   uint16_t *t_qkv, *t_attn, *t_moe_in;
   int32_t t_idx[64];
@@ -1117,6 +1118,7 @@ or_model* or_model_create_ex(const or_config* cfg, uint64_t seed, int batch, int
     m->lz_gus = (uint8_t*)xmalloc(k * 2 * I * (H / 32));
     m->lz_dnc = (uint8_t*)xmalloc(k * H * (I / 2));
     m->lz_dns = (uint8_t*)xmalloc(k * H * (I / 32));
+    for (int t = 0; t < 64; ++t) m->lz_key[t] = -1;
   }
   m->cos_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
   m->sin_t = (float*)xmalloc(sizeof(float) * (size_t)cfg->max_seq * (D / 2));
@@ -1259,14 +1261,19 @@ static void model_moe(or_model* m, int l, const uint16_t* xn, int B, uint16_t* o
       const size_t e = (size_t)idx[r * K + t];
       uint8_t* a = m->lz_guc + t * gcs; uint8_t* b2 = m->lz_gus + t * gss;
       uint8_t* d = m->lz_dnc + t * dcs; uint8_t* f = m->lz_dns + t * dss;
-      or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_GU_CODES), (int64_t)(e * gcs),
-                       (int64_t)gcs, a);
-      or_fill_scales_at(m->seed, or_stream_id(l, OR_T_GU_SCALES), (int64_t)(e * gss),
-                        (int64_t)gss, 119, 6, b2);
-      or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_DN_CODES), (int64_t)(e * dcs),
-                       (int64_t)dcs, d);
-      or_fill_scales_at(m->seed, or_stream_id(l, OR_T_DN_SCALES), (int64_t)(e * dss),
-                        (int64_t)dss, 119, 6, f);
+      /* the slot buffer already holds this (layer, expert): same bytes */
+      const int64_t key = (int64_t)l * E + (int64_t)e;
+      if (m->lz_key[t] != key) {
+        m->lz_key[t] = key;
+        or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_GU_CODES), (int64_t)(e * gcs),
+                         (int64_t)gcs, a);
+        or_fill_scales_at(m->seed, or_stream_id(l, OR_T_GU_SCALES), (int64_t)(e * gss),
+                          (int64_t)gss, 119, 6, b2);
+        or_fill_bytes_at(m->seed, or_stream_id(l, OR_T_DN_CODES), (int64_t)(e * dcs),
+                         (int64_t)dcs, d);
+        or_fill_scales_at(m->seed, or_stream_id(l, OR_T_DN_SCALES), (int64_t)(e * dss),
+                          (int64_t)dss, 119, 6, f);
+      }
       guc[t] = a; gus[t] = b2; dnc[t] = d; dns[t] = f;
       gub[t] = L->gu_bias + e * 2 * I; dnb[t] = L->dn_bias + e * H;
     }
@@ -1356,6 +1363,203 @@ void or_model_step(or_model* m, const int32_t* ids, float* logits,
     m->pos[b] = m->pos[b] + 1;
   }
   free(xn); free(qkv); free(qr); free(ao); free(tmp); free(lg); free(idx); free(sc);
+}
+
+/* Teacher-forced prompt rows in layer-major order: sequence b consumes
+ * ids[b][0 .. n-1] at positions pos[b] .. pos[b] + n - 1 (no lm_head), as
+ * n calls of or_model_step with NULL outputs would.  A row's layer-l input
+ * depends only on its own layer-(l-1) output and on the layer-l keys and
+ * values of positions <= its own, so all B n rows can go through layer l
+ * before any enters layer l + 1, in position order within the layer's
+ * attention; every row sees the same operands in the same order, so the
+ * KV cache, positions and hidden state come out bit-identical.  The dense
+ * projections and the experts then read each weight row once for all rows,
+ * and a lazy model generates each layer's experts once (E experts' codes and
+ * scales of one layer in memory at a time) instead of per row. */
+void or_model_prompt(or_model* m, const int32_t* ids, int n) {
+  const or_config* c = &m->cfg;
+  const int H = c->hidden, D = c->head_dim, Hq = c->n_heads, Hkv = c->n_kv_heads;
+  const int K = c->top_k, B = m->batch, E = c->n_experts, I = c->intermediate;
+  const int QKV = (Hq + 2 * Hkv) * D, half = D / 2;
+  const size_t T = (size_t)c->max_seq, R = (size_t)B * n;
+  if (n <= 0) return;
+  uint16_t* hs = (uint16_t*)xmalloc(sizeof(uint16_t) * R * H);
+  uint16_t* xn = (uint16_t*)xmalloc(sizeof(uint16_t) * R * H);
+  uint16_t* qkv = (uint16_t*)xmalloc(sizeof(uint16_t) * R * QKV);
+  uint16_t* qr = (uint16_t*)xmalloc(sizeof(uint16_t) * R * Hq * D);
+  uint16_t* ao = (uint16_t*)xmalloc(sizeof(uint16_t) * R * Hq * D);
+  uint16_t* tmp = (uint16_t*)xmalloc(sizeof(uint16_t) * R * H);
+  int32_t* idx = (int32_t*)xmalloc(sizeof(int32_t) * R * K);
+  float* sc = (float*)xmalloc(sizeof(float) * R * K);
+  const size_t gu_c = (size_t)E * 2 * I * (H / 2), gu_s = (size_t)E * 2 * I * (H / 32);
+  const size_t dn_c = (size_t)E * H * (I / 2), dn_s = (size_t)E * H * (I / 32);
+  uint8_t *lguc = NULL, *lgus = NULL, *ldnc = NULL, *ldns = NULL;
+  if (m->lazy) {
+    lguc = (uint8_t*)xmalloc(gu_c); lgus = (uint8_t*)xmalloc(gu_s);
+    ldnc = (uint8_t*)xmalloc(dn_c); ldns = (uint8_t*)xmalloc(dn_s);
+  }
+  for (size_t r = 0; r < R; ++r)
+    memcpy(hs + r * H, m->embed + (size_t)ids[r] * H, sizeof(uint16_t) * H);
+  for (int l = 0; l < c->n_layers; ++l) {
+    const or_layer* L = &m->layers[l];
+    const int window = (l % 2 == 0) ? c->sliding_window : 0;
+    uint16_t* kc_l = m->kc + (size_t)l * B * Hkv * T * D;
+    uint16_t* vc_l = m->vc + (size_t)l * B * Hkv * T * D;
+    m_rmsnorm(hs, L->attn_norm, (int)R, H, c->rms_eps, xn);
+    m_gemv_bf16(L->wqkv, L->bqkv, xn, (int)R, QKV, H, qkv, NULL);
+    for (size_t r = 0; r < R; ++r) {
+      const int b = (int)(r / n), p = m->pos[b] + (int)(r % n);
+      const float* cr = m->cos_t + (size_t)p * half;
+      const float* sr = m->sin_t + (size_t)p * half;
+      const uint16_t* qb = qkv + r * QKV;
+      or_rope_apply(qb, Hq, D, cr, sr, qr + r * Hq * D);
+      uint16_t kr[4096];
+      or_rope_apply(qb + Hq * D, Hkv, D, cr, sr, kr);
+      for (int g = 0; g < Hkv; ++g) {
+        const size_t row = (((size_t)b * Hkv + g) * T + p) * D;
+        memcpy(kc_l + row, kr + g * D, sizeof(uint16_t) * D);
+        memcpy(vc_l + row, qb + (Hq + Hkv + g) * D, sizeof(uint16_t) * D);
+      }
+    }
+    /* row (b, t) attends to sequence b's keys at positions <= pos[b] + t */
+    for (size_t r = 0; r < R; ++r) {
+      const int b = (int)(r / n);
+      const int32_t p = m->pos[b] + (int)(r % n);
+      const size_t kvb = (size_t)b * Hkv * T * D;
+      if (g_acc_mode)
+        or_attn_decode(qr + r * Hq * D, kc_l + kvb, vc_l + kvb, L->sinks, 1, Hq, Hkv, D,
+                       (int)T, &p, window, ao + r * Hq * D, NULL);
+      else
+        or_c_attn_decode(qr + r * Hq * D, kc_l + kvb, vc_l + kvb, L->sinks, 1, Hq, Hkv, D,
+                         (int)T, &p, window, or_attn_splits((int)T, window),
+                         ao + r * Hq * D, NULL);
+    }
+    m_gemv_bf16(L->wo, L->bo, ao, (int)R, H, Hq * D, tmp, NULL);
+    for (size_t i = 0; i < R * H; ++i) hs[i] = TOBF(BF(hs[i]) + BF(tmp[i]));
+    m_rmsnorm(hs, L->mlp_norm, (int)R, H, c->rms_eps, xn);
+    const uint8_t *guc = L->gu_codes, *gus = L->gu_scales, *dnc = L->dn_codes,
+                  *dns = L->dn_scales;
+    if (m->lazy) {
+      or_fill_bytes(m->seed, or_stream_id(l, OR_T_GU_CODES), (int64_t)gu_c, lguc);
+      or_fill_scales(m->seed, or_stream_id(l, OR_T_GU_SCALES), (int64_t)gu_s, 119, 6, lgus);
+      or_fill_bytes(m->seed, or_stream_id(l, OR_T_DN_CODES), (int64_t)dn_c, ldnc);
+      or_fill_scales(m->seed, or_stream_id(l, OR_T_DN_SCALES), (int64_t)dn_s, 119, 6, ldns);
+      guc = lguc; gus = lgus; dnc = ldnc; dns = ldns;
+    }
+    or_moe_layer(xn, L->router_w, L->router_b, guc, gus, L->gu_bias, dnc, dns, L->dn_bias,
+                 (int)R, E, H, I, K, c->swiglu_alpha, c->swiglu_limit, tmp, idx, sc);
+    for (size_t i = 0; i < R * H; ++i) hs[i] = TOBF(BF(hs[i]) + BF(tmp[i]));
+  }
+  /* the hidden state of each sequence's last prompt row, as after a step */
+  for (int b = 0; b < B; ++b) {
+    memcpy(m->h + (size_t)b * H, hs + ((size_t)b * n + n - 1) * H, sizeof(uint16_t) * H);
+    m->pos[b] += n;
+  }
+  free(hs); free(xn); free(qkv); free(qr); free(ao); free(tmp); free(idx); free(sc);
+  free(lguc); free(lgus); free(ldnc); free(ldns);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Temperature + nucleus (top-p) sampling, the device's exact operation      */
+/* order (neon_sample / the context's sampled steps).  Row b's 1024 "threads"*/
+/* t = 64 w + l each own the indices t, t + 1024, ... for the max, the       */
+/* exponentials and the threshold sums; a block sum is the 64-lane xor       */
+/* butterfly of each wave, then the 16 wave totals added in order from 0.    */
+/*   m = max_i l_i;  e_i = exp((l_i - m) * (1 / T));  z = sum e_i            */
+/*   threshold t: the largest float (bisected bit 30 .. 0 of its bits) with  */
+/*     sum_{e_i >= t} e_i >= top_p * z  (t = 0 keeps all when top_p >= 1)   */
+/*   u = (splitmix64(seed ^ splitmix64(b << 32 | pos_b)) >> 40) * 2^-24      */
+/*   the pick: the first kept index whose running sum in vocabulary order    */
+/*   exceeds u * kept, with the running sum formed per contiguous slice of   */
+/*   ceil(V / 1024) indices (thread t owns slice t) after an exclusive       */
+/*   prefix of the slice totals in slice order.                              */
+/* ------------------------------------------------------------------------ */
+static uint64_t splitmix64_step(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+static float block_sum_1024_c(const float* part) {
+  float tot = 0.0f;
+  for (int w = 0; w < 16; ++w) {
+    float v[64];
+    memcpy(v, part + 64 * w, sizeof(v));
+    tot = tot + c_butterfly64(v);
+  }
+  return tot;
+}
+
+void or_sample(const float* logits, int B, int V, float temperature, float top_p,
+               uint64_t seed, const int32_t* pos, int32_t* out_ids) {
+  const float inv_temp = 1.0f / temperature;
+  float* e = (float*)xmalloc(sizeof(float) * (size_t)V);
+  float part[1024];
+  for (int b = 0; b < B; ++b) {
+    const float* l = logits + (size_t)b * V;
+    float m = -INFINITY;
+    for (int i = 0; i < V; ++i) m = fmaxf(m, l[i]);
+    for (int t = 0; t < 1024; ++t) {
+      float z = 0.0f;
+      for (int i = t; i < V; i += 1024) {
+        e[i] = or_expf((l[i] - m) * inv_temp);
+        z = z + e[i];
+      }
+      part[t] = z;
+    }
+    const float z = block_sum_1024_c(part);
+    uint32_t t_bits = 0;
+    float kept = z;
+    if (top_p < 1.0f) {
+      const float goal = top_p * z;
+      for (int bit = 30; bit >= 0; --bit) {
+        const uint32_t cand = t_bits | (1u << bit);
+        float th;
+        memcpy(&th, &cand, 4);
+        for (int t = 0; t < 1024; ++t) {
+          float sp = 0.0f;
+          for (int i = t; i < V; i += 1024) sp = sp + (e[i] >= th ? e[i] : 0.0f);
+          part[t] = sp;
+        }
+        const float sm = block_sum_1024_c(part);
+        if (sm >= goal) { t_bits = cand; kept = sm; }
+      }
+    }
+    float th;
+    memcpy(&th, &t_bits, 4);
+    const uint64_t r = splitmix64_step(
+        seed ^ splitmix64_step(((uint64_t)(uint32_t)b << 32) | (uint32_t)pos[b]));
+    const float u = (float)(r >> 40) * 0x1.0p-24f;
+    const float target = u * kept;
+    const int Cs = (V + 1023) / 1024;
+    float acc = 0.0f;
+    int32_t pick = -1;
+    for (int t = 0; t < 1024 && pick < 0; ++t) {
+      const int i0 = t * Cs < V ? t * Cs : V, i1 = i0 + Cs < V ? i0 + Cs : V;
+      float local = 0.0f;
+      for (int i = i0; i < i1; ++i) local = local + (e[i] >= th ? e[i] : 0.0f);
+      float run = acc;  /* exclusive prefix of the slice totals */
+      if (run <= target && local > 0.0f && run + local > target) {
+        int last = -1, found = -1;
+        for (int i = i0; i < i1; ++i)
+          if (e[i] >= th) {
+            last = i;
+            run = run + e[i];
+            if (run > target) { found = i; break; }
+          }
+        pick = found >= 0 ? found : last;
+      }
+      acc = acc + local;
+    }
+    if (pick < 0) {
+      for (int i = V - 1; i >= 0; --i)
+        if (e[i] >= th) { pick = i; break; }
+      if (pick < 0) pick = 0;
+    }
+    out_ids[b] = pick;
+  }
+  free(e);
 }
 
 #ifdef _OPENMP

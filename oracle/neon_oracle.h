@@ -156,6 +156,11 @@ void or_c_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                       int Hq, int Hkv, int D, int T_max, const int32_t* pos,
                       int window, int S, uint16_t* out, float* out_f32);
 
+/* Temperature + nucleus sampling in the device's exact operation order
+ * (neon_sample): ids [B] from logits [B][V] at positions pos [B]. */
+void or_sample(const float* logits, int B, int V, float temperature, float top_p,
+               uint64_t seed, const int32_t* pos, int32_t* out_ids);
+
 /* ---- full model (random init, identical to neon_init_random) -------------- */
 typedef struct or_model or_model;
 or_model* or_model_create(const or_config* cfg, uint64_t seed, int batch);
@@ -182,6 +187,12 @@ void or_model_free(or_model* m);
  * positions advance and lm_head is skipped. */
 void or_model_step(or_model* m, const int32_t* ids, float* logits,
                    int32_t* out_ids);
+/* Teacher-forced prompt rows, layer-major: sequence b consumes ids[b][0..n-1]
+ * (ids [B][n]) at positions pos[b] .. pos[b] + n - 1.  Bit-identical to n
+ * or_model_step calls with NULL outputs; each weight row is read once per
+ * layer for all B n rows, and a lazy model generates each layer's experts
+ * once. */
+void or_model_prompt(or_model* m, const int32_t* ids, int n);
 /* hidden state (bf16 [B][H]) after the last completed step, before the final
  * norm; for tests. */
 const uint16_t* or_model_hidden(const or_model* m);

@@ -116,6 +116,8 @@ def _declare(L):
         "or_fill_scales_at": (None, [_U64, _U64, _I64, _I64, _I, _I, _P]),
         "or_model_free": (None, [_P]),
         "or_model_step": (None, [_P, _P, _P, _P]),
+        "or_model_prompt": (None, [_P, _P, C.c_int]),
+        "or_sample": (None, [_P, _I, _I, _F, _F, _U64, _P, _P]),
         "or_model_hidden": (_P, [_P]),
         "or_model_pos": (C.c_int32, [_P, _I]),
         "or_model_tensor": (_P, [_P, _I, _I]),
@@ -427,6 +429,16 @@ def c_attn_decode(q, kc, vc, sinks, B, Hq, Hkv, D, T_max, pos, window, S=None):
     return out, outf
 
 
+def sample(logits, temperature, top_p, seed, pos):
+    """Ids [B] drawn from logits [B][V] in the device's exact order."""
+    lg = _c(logits, np.float32)
+    B, V = lg.shape
+    pos = _c(pos, np.int32).reshape(B)
+    out = np.empty(B, np.int32)
+    lib().or_sample(_p(lg), B, V, temperature, top_p, seed, _p(pos), _p(out))
+    return out
+
+
 class Model:
     """Random-init gpt-oss model (bit-identical weights to neon_init_random)."""
 
@@ -463,6 +475,13 @@ class Model:
         at each sequence's position and advances it, without lm_head."""
         ids = _c(ids, np.int32).reshape(self.batch)
         lib().or_model_step(self._h, _p(ids), None, None)
+
+    def prompt(self, ids):
+        """Teacher-forced prompt rows ids [B][n] in layer-major order
+        (or_model_prompt): the same KV cache, positions and hidden state as
+        n prompt_step calls, with each weight row read once per layer."""
+        ids = _c(ids, np.int32).reshape(self.batch, -1)
+        lib().or_model_prompt(self._h, _p(ids), ids.shape[1])
 
     def set_tensor(self, layer, kind, data):
         a = np.ascontiguousarray(data)

@@ -17,9 +17,16 @@ Cases:
   ragged20b gpt-oss-20b shape, four sequences with prompts of 5, 77, 300
             and 1000 tokens decoding together (neon_prefill_ragged), then 16
             greedy steps; the oracle runs each sequence alone at batch 1.
+  long120b  config 4: gpt-oss-120b shape, a 2048-token prompt uniform over
+            the vocab, then 64 greedy steps (batch 1, lazy experts).
 
-Run: python tests/golden/make_model_fixtures.py [case ...]   (CPU only; the
-20b prompt case takes about 40 minutes on 8 cores).  Test infrastructure: it
+Prompt rows go through the oracle's layer-major or_model_prompt (bit-identical
+to one teacher-forced step per row, tests/test_oracle.py; the long20b digests
+written row by row are reproduced by it), which generates a lazy model's
+experts once per layer instead of once per row.
+
+Run: python tests/golden/make_model_fixtures.py [case ...]   (CPU only).
+`--check case` recomputes a stored case and compares it with the file.  Test infrastructure: it
 runs the oracle, never the product.
 """
 import hashlib
@@ -44,6 +51,8 @@ CASES = {
                   prompt_seed=120),
     "ragged20b": dict(shape="20b", seed=4, lens=(5, 77, 300, 1000), steps=16, max_seq=1040,
                       prompt_seed=1382),
+    "long120b": dict(shape="120b", seed=3, batch=1, prompt_len=2048, steps=64, max_seq=2176,
+                     prompt_seed=4096),
 }
 
 
@@ -111,10 +120,8 @@ def run_case(name):
     t0 = time.time()
     m = orc.Model(cfg, seed=case["seed"], batch=B, lazy_experts=case["shape"] == "120b")
     print(f"[{name}] model ready in {time.time() - t0:.0f}s", flush=True)
-    for t in range(case["prompt_len"] - 1):
-        m.step(prompt[:, t], want_logits=False)
-        if t % 128 == 0:
-            print(f"[{name}] prompt {t}/{case['prompt_len']} {time.time() - t0:.0f}s", flush=True)
+    m.prompt(prompt[:, :-1])
+    print(f"[{name}] prompt of {case['prompt_len'] - 1} rows {time.time() - t0:.0f}s", flush=True)
     ids = prompt[:, -1]
     n = case["steps"] + 1
     out_ids = np.zeros((B, n), np.int32)
@@ -139,6 +146,16 @@ def run_case(name):
                        36 if case["shape"] == "120b" else 24], np.int64)).items()}
 
 
+def check(name):
+    """Recompute a stored case and compare every array with the file."""
+    with np.load(OUT, allow_pickle=False) as z:
+        want = {k: z[k] for k in z.files if k.startswith(name + "__")}
+    got = run_case(name)
+    bad = [k for k in want if not np.array_equal(want[k], got[k])]
+    print(f"[{name}] {'identical' if not bad else 'DIFFERS in ' + ', '.join(bad)}", flush=True)
+    return not bad
+
+
 def main(names):
     data = {}
     if os.path.exists(OUT):
@@ -152,4 +169,6 @@ def main(names):
 
 
 if __name__ == "__main__":
+    if sys.argv[1:2] == ["--check"]:
+        sys.exit(0 if all(check(n) for n in sys.argv[2:]) else 1)
     main(sys.argv[1:] or list(CASES))

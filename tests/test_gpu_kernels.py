@@ -386,7 +386,9 @@ def test_moe_layer_config4(orc, B):
     (300, 3, 0, 300), (1, 2, 128, 256), (3, 1, 0, 2048), (200, 2, 128, 4096),
     # config 2 at batch 32
     (1024, 32, 0, 1024), (1024, 32, 128, 1024), (8192, 32, 0, 8192), (8192, 32, 128, 8192),
-    (32768, 32, 0, 32768), (32768, 32, 128, 32768)])
+    (32768, 32, 0, 32768), (32768, 32, 128, 32768),
+    # config 2 at batch 8: T = 32768 both windows, T = 1024 full
+    (32768, 8, 0, 32768), (32768, 8, 128, 32768), (1024, 8, 0, 1024)])
 def test_attn_decode_config2(orc, T, B, window, Tm):
     """64 q / 8 kv heads, d=64, Q/K/V and sinks ~N(0,1) bf16 (T keys live in a
     cache of Tm rows; small T in a large cache leaves empty splits)."""

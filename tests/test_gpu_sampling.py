@@ -1,8 +1,13 @@
-"""GPU checks of temperature / nucleus sampling.  Sampling has no bit-level
-oracle; what the mathematics fixes is checked instead: the draw frequencies
-against softmax(logits / T) (chi-square over thousands of rows, each row its
-own RNG stream), the nucleus (only the top-p set ever appears, in the ratio
-of its probabilities), the limits (T -> 0 and top_p -> 0 give the argmax),
+"""GPU checks of temperature / nucleus sampling.  The draw is bit-exact
+against the oracle's or_sample, which restates the kernel's operation order
+(itself pinned on the CPU against an fp64 inverse-CDF restatement,
+tests/test_oracle.py): every id over a grid of temperatures, top_p, seeds and
+positions, rows with ties, and a 201088-entry row; and the context's sampled
+steps against the oracle's logits fed through or_sample.  What the
+mathematics fixes is checked as well: the draw frequencies against
+softmax(logits / T) (chi-square over thousands of rows, each row its own RNG
+stream), the nucleus (only the top-p set ever appears, in the ratio of its
+probabilities), the limits (T -> 0 and top_p -> 0 give the argmax),
 reproducibility for a seed, and that temperature 0 keeps the exact greedy
 path."""
 import sys
@@ -28,6 +33,67 @@ def draws(logits_row, n, temperature, top_p, seed, pos0=0):
     out = empty_dev((n,), np.int32)
     ne.sample_logits(to_dev(lg), n, V, temperature, top_p, seed, to_dev(pos), out)
     return to_host(out).astype(np.int64)
+
+
+def test_sample_bit_exact_vs_oracle(orc):
+    """neon_sample against or_sample: identical ids over temperature x top_p x
+    seed x position, on rows with a block of tied values, flat rows, rows with
+    -inf entries, and the 201088-entry vocabulary."""
+    torch_cuda()
+    rng = np.random.default_rng(17)
+    cases = [(1000, 48), (4099, 24), (201088, 4)]
+    total = 0
+    for V, B in cases:
+        lg = (rng.normal(size=(B, V)) * rng.uniform(0.5, 4.0, (B, 1))).astype(np.float32)
+        lg[1, rng.integers(0, V, V // 3)] = lg[1, 0]  # ties
+        lg[2] = 0.0                                   # flat
+        lg[3, : V // 2] = -np.inf                     # masked half
+        dl = to_dev(lg)
+        for temperature in (0.3, 1.0, 2.0):
+            for top_p in (0.1, 0.5, 0.95, 1.0):
+                for seed in (0, 99, 2 ** 50 + 1):
+                    pos = rng.integers(0, 30000, B).astype(np.int32)
+                    out = empty_dev((B,), np.int32)
+                    ne.sample_logits(dl, B, V, temperature, top_p, seed, to_dev(pos), out)
+                    got = to_host(out)
+                    want = orc.sample(lg, temperature, top_p, seed, pos)
+                    assert np.array_equal(got, want), (V, temperature, top_p, seed, got, want)
+                    total += B
+    say(f"{total} draws identical to the oracle")
+
+
+def test_engine_sampled_steps_match_oracle(orc):
+    """The context's sampled steps (neon_set_sampling): each step's fp32
+    logits are the exact path's, and the id drawn from them at the row's
+    position equals or_sample's on the oracle's logits."""
+    torch_cuda()
+    cfg = ne.config_preset("gpt-oss-20b", **SMALL)
+    T, top_p, seed = 0.9, 0.8, 31
+    prompt = np.array([[5, 6, 7, 8], [9, 10, 11, 12]], np.int32)
+    eng = ne.Engine(cfg)
+    eng.init_random(4)
+    eng.set_sampling(T, top_p, seed)
+    eng.prefill(prompt)
+    m = orc.Model(orc.make_config(**cfg.as_dict()), seed=4, batch=2)
+    for t in range(prompt.shape[1] - 1):
+        m.prompt_step(prompt[:, t])
+    ids = prompt[:, -1]
+    n = 20
+    for s in range(n):
+        if s:
+            eng.decode(1)
+        pos = np.array([m_pos(m, b) for b in range(2)], np.int32)
+        _, lg = m.step(ids)
+        ids = orc.sample(lg, T, top_p, seed, pos)
+        got = eng.read_tokens(start=4 + s, count=1)[:, 0]
+        assert np.array_equal(got, ids), (s, got, ids)
+    m.close()
+    eng.close()
+
+
+def m_pos(m, b):
+    from oracle import oracle as orc_mod
+    return orc_mod.lib().or_model_pos(m._h, b)
 
 
 def chi2(counts, probs):

@@ -599,6 +599,46 @@ def test_prompt_step_equals_full_step(orc):
     assert np.array_equal(la, lb) and np.array_equal(ia, ib)
 
 
+@pytest.mark.parametrize("batch,lazy", [(1, False), (3, False), (1, True), (2, True)])
+def test_layer_major_prompt_equals_row_by_row(orc, batch, lazy):
+    """or_model_prompt (every prompt row through layer l before layer l + 1,
+    weights read once per layer, a lazy model's experts generated once per
+    layer) leaves the KV cache, positions and hidden state exactly as one
+    teacher-forced step per row does: the following greedy steps give the
+    same logits bit for bit.  The prompt crosses the sliding window (4) and
+    the lazy slot cache serves repeated experts."""
+    cfg = orc.make_config(n_layers=3, hidden=128, n_heads=8, n_kv_heads=2, n_experts=6, top_k=2,
+                          intermediate=64, vocab=512, sliding_window=4, max_seq=24,
+                          max_batch=batch)
+    rng = np.random.default_rng(11 + batch)
+    prompt = rng.integers(0, cfg.vocab, (batch, 13), dtype=np.int32)
+    a = orc.Model(cfg, seed=5, batch=batch, lazy_experts=lazy)
+    b = orc.Model(cfg, seed=5, batch=batch, lazy_experts=lazy)
+    for t in range(prompt.shape[1] - 1):
+        a.prompt_step(prompt[:, t])
+    b.prompt(prompt[:, :-1])
+    assert np.array_equal(a.hidden(), b.hidden())
+    ids = prompt[:, -1]
+    for _ in range(4):
+        ia, la = a.step(ids)
+        ib, lb = b.step(ids)
+        assert np.array_equal(la, lb) and np.array_equal(ia, ib)
+        ids = ia
+    a.close()
+    b.close()
+    # and a lazy model's layer-major prompt equals the eager model's
+    if lazy:
+        c = orc.Model(cfg, seed=5, batch=batch)
+        d = orc.Model(cfg, seed=5, batch=batch, lazy_experts=True)
+        c.prompt(prompt[:, :-1])
+        d.prompt(prompt[:, :-1])
+        _, lc = c.step(prompt[:, -1])
+        _, ld = d.step(prompt[:, -1])
+        c.close()
+        d.close()
+        assert np.array_equal(lc, ld)
+
+
 def test_e4m3_decode_all_codes_vs_torch(orc):
     """All 256 E4M3 codes against torch.float8_e4m3fn (OCP E4M3: bias 7, no
     infinities, S.1111.111 = NaN, max normal 448)."""
@@ -666,3 +706,90 @@ def test_mx8_quant_scale_rule_and_reconstruction(orc):
     err = np.abs(deq - xf)
     assert (err[fin_el] <= bound[fin_el]).all()
     assert np.array_equal(hi[3, 32:64], np.zeros(32, np.uint8)) and sh[3, 1] == 127
+
+
+def _splitmix64(x):
+    m = (1 << 64) - 1
+    x = (x + 0x9E3779B97F4A7C15) & m
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & m
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & m
+    return x ^ (x >> 31)
+
+
+def _sample_fp64(row, temperature, top_p, seed, b, pos):
+    """Independent restatement in fp64 (numpy sort and cumulative sums, no
+    shared code with or_sample): the nucleus is the smallest set of largest
+    probabilities whose mass reaches top_p (ties at its edge kept), and the
+    draw is the inverse CDF of the kept mass in vocabulary order at
+    u = (splitmix64(seed ^ splitmix64(b << 32 | pos)) >> 40) 2^-24.  Returns
+    the id and the distance of the draw from the nearest decision boundary
+    (relative to the kept mass), so that rounding ties can be excused."""
+    x = row.astype(np.float64)
+    e = np.exp((x - x.max()) / temperature)
+    z = e.sum()
+    if top_p < 1.0:
+        srt = np.sort(e)[::-1]
+        cum = np.cumsum(srt)
+        k = int(np.searchsorted(cum, top_p * z))  # first prefix with mass >= goal
+        k = min(k, len(srt) - 1)
+        th = srt[k]
+        edge = abs(cum[k] - top_p * z) / z
+        if k > 0:
+            edge = min(edge, abs(cum[k - 1] - top_p * z) / z)
+    else:
+        th, edge = 0.0, 1.0
+    kept = np.where(e >= th, e, 0.0)
+    r = _splitmix64(seed ^ _splitmix64(((b & 0xFFFFFFFF) << 32) | (pos & 0xFFFFFFFF)))
+    u = (r >> 40) * 2.0 ** -24
+    run = np.cumsum(kept)
+    target = u * run[-1]
+    i = int(np.searchsorted(run, target, side="right"))
+    i = min(i, len(row) - 1)
+    gap = np.abs(run - target).min() / run[-1]
+    return i, min(edge, gap)
+
+
+@pytest.mark.parametrize("V", [8, 1000, 4099])
+def test_sample_is_inverse_cdf_of_nucleus(orc, V):
+    """or_sample against the fp64 inverse-CDF restatement over a grid of
+    temperatures, top_p, seeds and positions, logits with repeated values
+    (ties) included: the same id wherever the draw is not within 1e-5 of a
+    decision boundary (fp32 running sums against fp64)."""
+    rng = np.random.default_rng(V)
+    rows, params = [], []
+    for temperature in (0.25, 0.8, 1.0, 2.5):
+        for top_p in (0.05, 0.5, 0.9, 1.0):
+            for seed in (0, 7, 2 ** 40 + 3):
+                lg = rng.normal(size=V).astype(np.float32) * rng.uniform(0.5, 4.0)
+                lg[rng.integers(0, V, V // 4)] = lg[0]  # a block of ties
+                rows.append(lg)
+                params.append((temperature, top_p, seed))
+    checked = excused = 0
+    for j, (lg, (temperature, top_p, seed)) in enumerate(zip(rows, params)):
+        pos = np.array([j * 37 % 5000, j], np.int32)
+        got = orc.sample(np.stack([lg, lg[::-1].copy()]), temperature, top_p, seed, pos)
+        for b, row in enumerate((lg, lg[::-1])):
+            want, margin = _sample_fp64(row, temperature, top_p, seed, b, int(pos[b]))
+            if margin < 1e-5:
+                excused += 1
+                continue
+            checked += 1
+            assert got[b] == want, (V, temperature, top_p, seed, b, got[b], want)
+    assert checked >= 0.9 * (checked + excused)
+
+
+def test_sample_limits(orc):
+    """T -> 0 and top_p -> 0 give the argmax; a one-hot row always gives its
+    hot index; positions and seeds change the draw (different streams)."""
+    rng = np.random.default_rng(3)
+    lg = rng.normal(size=(16, 513)).astype(np.float32)
+    pos = np.arange(16, dtype=np.int32)
+    assert np.array_equal(orc.sample(lg, 1e-6, 1.0, 1, pos), lg.argmax(1))
+    assert np.array_equal(orc.sample(lg, 1.0, 1e-7, 1, pos), lg.argmax(1))
+    hot = np.full((4, 300), -np.inf, np.float32)
+    hot[np.arange(4), [0, 17, 299, 150]] = 0.0
+    assert orc.sample(hot, 1.0, 1.0, 9, np.arange(4, dtype=np.int32)).tolist() == [0, 17, 299, 150]
+    flat = np.zeros((64, 1000), np.float32)
+    a = orc.sample(flat, 1.0, 1.0, 1, np.arange(64, dtype=np.int32))
+    b = orc.sample(flat, 1.0, 1.0, 2, np.arange(64, dtype=np.int32))
+    assert len(set(a.tolist())) > 40 and (a != b).sum() > 40
