@@ -80,6 +80,7 @@ def time_moe(ne, torch, eng, cfg, reps: int):
     x = torch.randn(H, generator=g).to(torch.bfloat16).view(torch.int16).to(dev)
     act = torch.empty(k * I, dtype=torch.int16, device=dev)
     out = torch.empty(H, dtype=torch.int16, device=dev)
+    lg = torch.empty(E, dtype=torch.float32, device=dev)
     ptrs, xn, idx, score = [], [], [], []
     for l in range(L):
         p = "model.layers.%d." % l
@@ -93,7 +94,7 @@ def time_moe(ne, torch, eng, cfg, reps: int):
         score.append(torch.empty(k, dtype=torch.float32, device=dev))
         ne.rmsnorm(x, w["post_attention_layernorm.weight"], xn[l], 1, H, cfg.rms_eps)
         ne.router_topk(xn[l], w["mlp.router.weight"], w["mlp.router.bias"], idx[l], score[l],
-                       None, 1, E, H, k)
+                       lg, 1, E, H, k)
         ptrs.append([w["mlp.experts." + n] for n in (
             "gate_up_proj_blocks", "gate_up_proj_scales", "gate_up_proj_bias",
             "down_proj_blocks", "down_proj_scales", "down_proj_bias")])
@@ -277,8 +278,14 @@ def sweep_attn(ne, torch, reps=10):
                 pos = [torch.full((B,), T - 1 - 129 * j if window else T - 1, dtype=torch.int32,
                                   device="cuda") for j in range(npos)]
 
+                # one caller workspace and one zeroed counter array for every
+                # call (the library allocates nothing per call)
+                wb, cb = ne.attn_decode_workspace(B, Hq, Hkv, D, T, window)
+                ws = torch.empty(max(wb, 4), dtype=torch.uint8, device="cuda")
+                cnt = torch.zeros(max(cb, 4), dtype=torch.uint8, device="cuda")
                 calls = [lambda c=c: ne.attn_decode(q, kc[c % n], vc[c % n], sinks, pos[c % npos],
-                                                    o, B, Hq, Hkv, D, T, window)
+                                                    o, B, Hq, Hkv, D, T, window, workspace=ws,
+                                                    counters=cnt)
                          for c in range(max(n, npos))]
                 try:
                     t, how = graph_time(torch, calls, reps), "graph"

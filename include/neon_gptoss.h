@@ -212,6 +212,12 @@ neon_status neon_tensor_ptr(neon_ctx* ctx, const char* name, void** ptr,
                             size_t* bytes);
 
 /* ---- kernel-level API (device pointers; stream-ordered) ------------------ */
+/* No kernel-level call allocates device memory: scratch space is a caller-
+ * owned workspace whose size the matching *_workspace query returns (the
+ * reference's idiom: buffers created once with the System, dispatches
+ * recorded per frame without allocation, water_physics.cpp:103,449 and
+ * :165-436).  A workspace may be reused by later calls; calls that overlap
+ * on one device must not share one. */
 
 /* Synchronises `stream`, then reports (and clears) the status bits that the
  * kernel-level calls on the current device have set since the last check:
@@ -250,14 +256,22 @@ neon_status neon_gemv_bf16(const uint16_t* W, const uint16_t* bias,
 neon_status neon_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out,
                          int B, int H, float eps, void* stream);
 
+/* YaRN RoPE table for positions 0 .. n_pos-1 from cfg's rope fields (HFR
+ * yarn inv_freq, cos/sin times the attention factor), written to the device
+ * array table [2][n_pos][head_dim/2] fp32 (cos, then sin).  A set-up call:
+ * it returns after the copy has completed. */
+neon_status neon_rope_table(const neon_config* cfg, int n_pos, float* table, void* stream);
+
 /* In-place YaRN RoPE (half-split rotation) on x [n_tok][n_heads][head_dim]
- * at positions pos[n_tok] (device int32), using cfg's rope fields. */
-neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok,
-                           int n_heads, const neon_config* cfg, void* stream);
+ * at positions pos[n_tok] (device int32, each in [0, n_pos)), with a table
+ * from neon_rope_table. */
+neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok, int n_heads,
+                           int head_dim, const float* table, int n_pos, void* stream);
 
 /* Router: logits = x W^T + b (fp32, one canonical reduction order), top-k
  * over the logits (ties -> lower index), softmax over the k values.
- * idx [B][k] int32, score [B][k] fp32, logits [B][E] fp32 (may be NULL). */
+ * idx [B][k] int32, score [B][k] fp32, logits [B][E] fp32 (required: the
+ * top-k reads it back). */
 neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
                              const uint16_t* b, int32_t* idx, float* score,
                              float* logits, int B, int E, int H, int k,
@@ -266,7 +280,10 @@ neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
 /* MoE block on normalised x [B][H]: router + top-k experts, each
  * gate_up (MXFP4 [E][2I][H], bias [E][2I]) -> SwiGLU-clamp -> down (MXFP4
  * [E][H][I], bias [E][H]), weighted sum.  out [B][H] bf16; if residual is
- * not NULL, out = bf16(residual + bf16(moe)).  idx/score may be NULL. */
+ * not NULL, out = bf16(residual + bf16(moe)).  idx/score may be NULL.
+ * workspace: at least neon_moe_layer_workspace(B, E, I, k) bytes (expert
+ * activations, router logits, arrival counters), any contents. */
+size_t neon_moe_layer_workspace(int B, int E, int I, int k);
 neon_status neon_moe_layer(const uint16_t* x, const uint16_t* router_w,
                            const uint16_t* router_b, const uint8_t* gu_codes,
                            const uint8_t* gu_scales, const uint16_t* gu_bias,
@@ -274,12 +291,14 @@ neon_status neon_moe_layer(const uint16_t* x, const uint16_t* router_w,
                            const uint16_t* dn_bias, const uint16_t* residual,
                            uint16_t* out, int32_t* idx, float* score, int B,
                            int E, int H, int I, int k, float alpha,
-                           float limit, void* stream);
+                           float limit, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /* neon_moe_layer for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
- * same arguments and bit-identical results, but its scratch (expert
- * activations and router logits) lives in a fixed 4 MiB device array per GPU
+ * the same arguments without the workspace, bit-identical results; its
+ * scratch (expert activations and router logits) lives in a fixed 4 MiB
+ * device array per GPU
  * that the library holds until the process ends, and it calls no allocator.
  * Shapes needing more than 4 MiB (B*k*I*2 rounded up to 256 plus B*E*4 bytes)
  * are rejected with NEON_EINVAL.  Every call on a GPU shares that GPU's array:
@@ -312,18 +331,32 @@ neon_status neon_moe_experts(const uint16_t* x, const int32_t* idx,
 /* GQA decode attention with per-head sinks.  q [B][Hq][D] (already rotated),
  * caches [B][Hkv][T_max][D], sinks [Hq] bf16, pos [B] device int32 (the
  * current token's position: keys 0..pos, or the last `window` of them when
- * window > 0).  out [B][Hq*D] bf16.  D == 64. */
+ * window > 0).  out [B][Hq*D] bf16.  D == 64.
+ * Spans of more than 256 keys are split (one split per 64-key chunk, at
+ * most 32) and the splits are merged inside the launch:
+ *   workspace  the split partials, neon_attn_decode_workspace(...) bytes
+ *              (0, and workspace may be NULL, with one split), any contents;
+ *   counters   the arrival counters, neon_attn_decode_counters(B, Hkv)
+ *              bytes, zero-filled by the caller before their first use;
+ *              every call leaves them zero, so one array serves every later
+ *              call whose (B, Hkv) fits. */
+size_t neon_attn_decode_workspace(int B, int Hq, int Hkv, int D, int T_max, int window);
+size_t neon_attn_decode_counters(int B, int Hkv);
 neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                              const uint16_t* v_cache, const uint16_t* sinks,
                              const int32_t* pos, uint16_t* out, int B, int Hq,
-                             int Hkv, int D, int T_max, int window,
-                             void* stream);
+                             int Hkv, int D, int T_max, int window, float* workspace,
+                             size_t workspace_bytes, int32_t* counters,
+                             size_t counter_bytes, void* stream);
 
 /* One draw per row from logits [B][V] (device fp32), as neon_set_sampling
  * describes; pos [B] (device int32) keys the RNG; out_ids [B] device int32.
- * temperature > 0, top_p in (0, 1]. */
+ * temperature > 0, top_p in (0, 1].  workspace: neon_sample_workspace(B, V)
+ * bytes (the exponentials), any contents. */
+size_t neon_sample_workspace(int B, int V);
 neon_status neon_sample(const float* logits, int B, int V, float temperature, float top_p,
-                        uint64_t seed, const int32_t* pos, int32_t* out_ids, void* stream);
+                        uint64_t seed, const int32_t* pos, int32_t* out_ids, float* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* ---- prefill kernels (matrix cores; fp32 accumulate in the MFMA order) --- */
 
@@ -339,14 +372,17 @@ neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
  * to x[t] (normalised, bf16 [M][H]); h[t] = bf16(h[t] + bf16(sum_s
  * score[t][s] y_ts)) in place.  Rows are grouped by expert into MXFP4
  * matrix-core GEMMs (weights dequantised exactly to bf16).  An id outside
- * [0, E) drops its slot; neon_device_check then returns NEON_EINVAL. */
+ * [0, E) drops its slot; neon_device_check then returns NEON_EINVAL.
+ * workspace: neon_moe_prefill_workspace(M, E, H, I, k, 0) bytes (mx8 = 1 for
+ * neon_moe_prefill_mx8), any contents. */
+size_t neon_moe_prefill_workspace(int M, int E, int H, int I, int k, int mx8);
 neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
                              const float* score, const uint8_t* gu_codes,
                              const uint8_t* gu_scales, const uint16_t* gu_bias,
                              const uint8_t* dn_codes, const uint8_t* dn_scales,
                              const uint16_t* dn_bias, uint16_t* h, int M, int E,
                              int H, int I, int k, float alpha, float limit,
-                             void* stream);
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* neon_moe_prefill with both expert GEMMs on the scaled fp8 x fp4 matrix
  * instruction (v_mfma_scale_f32_32x32x64_f8f6f4): the GEMM inputs (x, then
@@ -360,7 +396,7 @@ neon_status neon_moe_prefill_mx8(const uint16_t* x, const int32_t* idx,
                                  const uint8_t* dn_codes, const uint8_t* dn_scales,
                                  const uint16_t* dn_bias, uint16_t* h, int M, int E,
                                  int H, int I, int k, float alpha, float limit,
-                                 void* stream);
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* The two-term MXFP8 image of bf16 rows x [rows][K] (K % 32 == 0): for each
  * 32-element block, hi = E4M3(x / 2^e1) rounded to nearest even, with

@@ -37,6 +37,8 @@ EXPORTS = (
     "neon_attn_prefill", "neon_set_sampling", "neon_sample", "neon_set_decode_mode",
     "neon_gemv_bf16_mfma", "neon_device_check", "neon_moe_layer_noalloc",
     "neon_prefill_ragged", "neon_seq_lens", "neon_moe_prefill_mx8", "neon_mx8_quant",
+    "neon_rope_table", "neon_moe_layer_workspace", "neon_attn_decode_workspace",
+    "neon_attn_decode_counters", "neon_sample_workspace", "neon_moe_prefill_workspace",
 )
 
 
@@ -101,19 +103,20 @@ def lib():
             "neon_mxfp4_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
             "neon_gemv_bf16": [_P, _P, _P, _P, _I, _I, _I, _P],
             "neon_rmsnorm": [_P, _P, _P, _I, _I, _F, _P],
-            "neon_rope_yarn": [_P, _P, _I, _I, _P, _P],
+            "neon_rope_table": [_P, _I, _P, _P],
+            "neon_rope_yarn": [_P, _P, _I, _I, _I, _P, _I, _P],
             "neon_router_topk": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
-            "neon_moe_layer": [_P] * 13 + [_I] * 5 + [_F, _F, _P],
+            "neon_moe_layer": [_P] * 13 + [_I] * 5 + [_F, _F, _P, _SZ, _P],
             "neon_moe_experts": [_P] * 12 + [_I] * 5 + [_F, _F, _P],
-            "neon_attn_decode": [_P] * 6 + [_I] * 6 + [_P],
+            "neon_attn_decode": [_P] * 6 + [_I] * 6 + [_P, _SZ, _P, _SZ, _P],
             "neon_set_prefill_mode": [_P, _I],
             "neon_gemm_bf16": [_P] * 4 + [_I] * 4 + [_P],
-            "neon_moe_prefill": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
-            "neon_moe_prefill_mx8": [_P] * 10 + [_I] * 5 + [_F, _F, _P],
+            "neon_moe_prefill": [_P] * 10 + [_I] * 5 + [_F, _F, _P, _SZ, _P],
+            "neon_moe_prefill_mx8": [_P] * 10 + [_I] * 5 + [_F, _F, _P, _SZ, _P],
             "neon_mx8_quant": [_P, _I64, _I, _P, _P, _P, _P, _P],
             "neon_attn_prefill": [_P] * 5 + [_I] * 6 + [_P],
             "neon_set_sampling": [_P, _F, _F, _U64],
-            "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P],
+            "neon_sample": [_P, _I, _I, _F, _F, _U64, _P, _P, _P, _SZ, _P],
             "neon_set_decode_mode": [_P, _I],
             "neon_gemv_bf16_mfma": [_P, _P, _P, _P, _I, _I, _I, _P],
             "neon_device_check": [_P],
@@ -123,6 +126,15 @@ def lib():
             f = getattr(L, name)
             f.argtypes = args
             f.restype = C.c_int
+        # workspace-size queries (size_t results)
+        for name, args in {"neon_moe_layer_workspace": [_I] * 4,
+                           "neon_attn_decode_workspace": [_I] * 6,
+                           "neon_attn_decode_counters": [_I] * 2,
+                           "neon_sample_workspace": [_I] * 2,
+                           "neon_moe_prefill_workspace": [_I] * 6}.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = _SZ
         L.neon_ctx_destroy.restype = None
         L.neon_last_error.restype = C.c_char_p
         _lib = L
@@ -158,6 +170,13 @@ def _ptr(t):
             raise ValueError("tensor must be contiguous")
         return C.c_void_p(t.data_ptr())
     return C.c_void_p(int(t))
+
+
+def _nbytes(t):
+    """Size in bytes of a torch tensor (None -> 0)."""
+    if t is None:
+        return 0
+    return t.numel() * t.element_size()
 
 
 def _stream(stream):
@@ -202,23 +221,46 @@ def rmsnorm(x, w, out, B, H, eps=1e-5, stream=None):
     _check(lib().neon_rmsnorm(_ptr(x), _ptr(w), _ptr(out), B, H, eps, _stream(stream)))
 
 
-def rope_yarn(x, pos, n_tok, n_heads, cfg: Config, stream=None):
-    _check(lib().neon_rope_yarn(_ptr(x), _ptr(pos), n_tok, n_heads, C.byref(cfg),
-                                _stream(stream)))
+def rope_table(cfg: Config, n_pos, table, stream=None):
+    """table: device fp32 [2][n_pos][head_dim / 2] (cos, then sin)."""
+    _check(lib().neon_rope_table(C.byref(cfg), n_pos, _ptr(table), _stream(stream)))
+
+
+def rope_yarn(x, pos, n_tok, n_heads, head_dim, table, n_pos, stream=None):
+    _check(lib().neon_rope_yarn(_ptr(x), _ptr(pos), n_tok, n_heads, head_dim, _ptr(table),
+                                n_pos, _stream(stream)))
+
+
+def _workspace(nbytes, zero=False):
+    """A caller-side device buffer of nbytes (torch), for callers that do not
+    keep their own workspace; the library itself allocates nothing."""
+    import torch
+    n = max(int(nbytes), 1)
+    return torch.zeros(n, dtype=torch.uint8, device="cuda") if zero else \
+        torch.empty(n, dtype=torch.uint8, device="cuda")
 
 
 def router_topk(x, W, b, idx, score, logits, B, E, H, k, stream=None):
+    if logits is None:  # the C-ABI takes the logits buffer from the caller
+        logits = _workspace(B * E * 4)
     _check(lib().neon_router_topk(_ptr(x), _ptr(W), _ptr(b), _ptr(idx), _ptr(score),
                                   _ptr(logits), B, E, H, k, _stream(stream)))
 
 
+def moe_layer_workspace(B, E, I, k):
+    return lib().neon_moe_layer_workspace(B, E, I, k)
+
+
 def moe_layer(x, router_w, router_b, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
               dn_bias, residual, out, idx, score, B, E, H, I, k, alpha=1.702, limit=7.0,
-              stream=None):
+              stream=None, workspace=None):
+    if workspace is None:
+        workspace = _workspace(moe_layer_workspace(B, E, I, k))
     _check(lib().neon_moe_layer(
         _ptr(x), _ptr(router_w), _ptr(router_b), _ptr(gu_codes), _ptr(gu_scales),
         _ptr(gu_bias), _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(residual),
-        _ptr(out), _ptr(idx), _ptr(score), B, E, H, I, k, alpha, limit, _stream(stream)))
+        _ptr(out), _ptr(idx), _ptr(score), B, E, H, I, k, alpha, limit, _ptr(workspace),
+        _nbytes(workspace), _stream(stream)))
 
 
 def moe_layer_noalloc(x, router_w, router_b, gu_codes, gu_scales, gu_bias, dn_codes,
@@ -240,11 +282,25 @@ def moe_experts(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales
         B, E, H, I, k, alpha, limit, _stream(stream)))
 
 
+def attn_decode_workspace(B, Hq, Hkv, D, T_max, window):
+    """(workspace bytes, counter bytes) of neon_attn_decode."""
+    L = lib()
+    return (L.neon_attn_decode_workspace(B, Hq, Hkv, D, T_max, window),
+            L.neon_attn_decode_counters(B, Hkv))
+
+
 def attn_decode(q, k_cache, v_cache, sinks, pos, out, B, Hq, Hkv, D, T_max, window,
-                stream=None):
+                stream=None, workspace=None, counters=None):
+    """counters: zero-filled once by the caller (each call leaves it zero)."""
+    wb, cb = attn_decode_workspace(B, Hq, Hkv, D, T_max, window)
+    if workspace is None and wb:
+        workspace = _workspace(wb)
+    if counters is None:
+        counters = _workspace(cb, zero=True)
     _check(lib().neon_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(sinks),
                                   _ptr(pos), _ptr(out), B, Hq, Hkv, D, T_max, window,
-                                  _stream(stream)))
+                                  _ptr(workspace), _nbytes(workspace), _ptr(counters),
+                                  _nbytes(counters), _stream(stream)))
 
 
 def gemm_bf16(A, W, bias, C_, M, N, K, accumulate=False, stream=None):
@@ -252,20 +308,28 @@ def gemm_bf16(A, W, bias, C_, M, N, K, accumulate=False, stream=None):
                                 1 if accumulate else 0, _stream(stream)))
 
 
+def moe_prefill_workspace(M, E, H, I, k, mx8=False):
+    return lib().neon_moe_prefill_workspace(M, E, H, I, k, 1 if mx8 else 0)
+
+
 def moe_prefill(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
-                h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None):
+                h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None, workspace=None):
+    if workspace is None:
+        workspace = _workspace(moe_prefill_workspace(M, E, H, I, k))
     _check(lib().neon_moe_prefill(
         _ptr(x), _ptr(idx), _ptr(score), _ptr(gu_codes), _ptr(gu_scales), _ptr(gu_bias),
         _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(h), M, E, H, I, k, alpha, limit,
-        _stream(stream)))
+        _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def moe_prefill_mx8(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales, dn_bias,
-                    h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None):
+                    h, M, E, H, I, k, alpha=1.702, limit=7.0, stream=None, workspace=None):
+    if workspace is None:
+        workspace = _workspace(moe_prefill_workspace(M, E, H, I, k, mx8=True))
     _check(lib().neon_moe_prefill_mx8(
         _ptr(x), _ptr(idx), _ptr(score), _ptr(gu_codes), _ptr(gu_scales), _ptr(gu_bias),
         _ptr(dn_codes), _ptr(dn_scales), _ptr(dn_bias), _ptr(h), M, E, H, I, k, alpha, limit,
-        _stream(stream)))
+        _ptr(workspace), _nbytes(workspace), _stream(stream)))
 
 
 def mx8_quant(x, rows, K, hi, lo, s_hi, s_lo, stream=None):
@@ -278,9 +342,17 @@ def attn_prefill(q, k_cache, v_cache, sinks, out, M, Hq, Hkv, D, T_max, window, 
                                    _ptr(out), M, Hq, Hkv, D, T_max, window, _stream(stream)))
 
 
-def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=None):
+def sample_workspace(B, V):
+    return lib().neon_sample_workspace(B, V)
+
+
+def sample_logits(logits, B, V, temperature, top_p, seed, pos, out_ids, stream=None,
+                  workspace=None):
+    if workspace is None:
+        workspace = _workspace(sample_workspace(B, V))
     _check(lib().neon_sample(_ptr(logits), B, V, temperature, top_p, seed, _ptr(pos),
-                             _ptr(out_ids), _stream(stream)))
+                             _ptr(out_ids), _ptr(workspace), _nbytes(workspace),
+                             _stream(stream)))
 
 
 PREFILL_BATCHED, PREFILL_STEPWISE, PREFILL_CHUNKED, PREFILL_MX8 = 0, 1, 2, 3

@@ -1356,8 +1356,11 @@ extern "C" neon_status neon_seq_lens(const neon_ctx* ctx, int32_t* out) {
     return NEON_OK;                                                         \
   } while (0)
 
-// One status word per device for the kernel-level calls (allocated on a
-// device's first such call, held until the process ends).
+// One status word per device for the kernel-level calls: a file-scope device
+// array (zero when the code object loads, one copy per GPU), so no kernel-
+// level call allocates.  Host code never passes the array's name to a kernel:
+// it resolves the device address once per device with hipGetSymbolAddress.
+static __device__ __align__(256) int32_t g_kernel_status[64];
 static std::mutex g_status_mu;
 static int32_t* g_status_word[256];
 
@@ -1366,10 +1369,9 @@ static int32_t* device_status_word() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 256) return nullptr;
   std::lock_guard<std::mutex> lk(g_status_mu);
   if (g_status_word[dev] == nullptr) {
-    int32_t* p = nullptr;
-    if (hipMalloc((void**)&p, 256) != hipSuccess) return nullptr;
-    if (hipMemset(p, 0, 256) != hipSuccess) { (void)hipFree(p); return nullptr; }
-    g_status_word[dev] = p;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_kernel_status)) != hipSuccess) return nullptr;
+    g_status_word[dev] = (int32_t*)p;
   }
   return g_status_word[dev];
 }
@@ -1448,54 +1450,74 @@ extern "C" neon_status neon_rmsnorm(const uint16_t* x, const uint16_t* w,
   KLAUNCHED();
 }
 
-extern "C" neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok,
-                                      int n_heads, const neon_config* cfg,
-                                      void* stream) {
-  if (!x || !pos || !cfg) KFAIL(NEON_EINVAL, "neon_rope_yarn: null pointer");
-  if (n_tok < 1 || n_heads < 1 || cfg->head_dim < 2 || cfg->head_dim % 2 ||
-      cfg->head_dim > 512 || cfg->max_seq < 1 || !(cfg->rope_theta > 1.0f) ||
-      !(cfg->rope_factor >= 1.0f) || cfg->rope_orig_max_pos < 1)
-    KFAIL(NEON_EINVAL, "neon_rope_yarn: bad shape or rope parameters");
-  // Positions must lie in [0, cfg->max_seq); the table is built for that range.
+static bool rope_cfg_ok(const neon_config* cfg) {
+  return cfg->head_dim >= 2 && cfg->head_dim % 2 == 0 && cfg->head_dim <= 512 &&
+         cfg->rope_theta > 1.0f && cfg->rope_factor >= 1.0f && cfg->rope_orig_max_pos >= 1;
+}
+
+extern "C" neon_status neon_rope_table(const neon_config* cfg, int n_pos, float* table,
+                                       void* stream) {
+  if (!cfg || !table) KFAIL(NEON_EINVAL, "neon_rope_table: null pointer");
+  if (n_pos < 1 || !rope_cfg_ok(cfg)) KFAIL(NEON_EINVAL, "neon_rope_table: bad n_pos or rope parameters");
   std::vector<float> ct, stb;
-  rope_table_host(cfg, cfg->max_seq, ct, stb);
-  const int half = cfg->head_dim / 2;
-  float* tab = nullptr;
-  const size_t tn = (size_t)cfg->max_seq * half;
-  if (hipMallocAsync((void**)&tab, tn * 2 * 4, S(stream)) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_rope_yarn: table allocation failed");
-  if (hipMemcpyAsync(tab, ct.data(), tn * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess ||
-      hipMemcpyAsync(tab + tn, stb.data(), tn * 4, hipMemcpyHostToDevice, S(stream)) != hipSuccess)
-    KFAIL(NEON_EHIP, "neon_rope_yarn: copy failed");
-  launch_rope_apply(x, pos, tab, tab + tn, n_tok, n_heads, cfg->head_dim, S(stream));
-  hipError_t e = hipGetLastError();
-  if (hipStreamSynchronize(S(stream)) != hipSuccess)  // host tables die here
-    KFAIL(NEON_EHIP, "neon_rope_yarn: synchronize failed");
-  (void)hipFreeAsync(tab, S(stream));
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_rope_yarn: launch failed: %s", hipGetErrorString(e));
+  rope_table_host(cfg, n_pos, ct, stb);
+  const size_t tn = (size_t)n_pos * (cfg->head_dim / 2);
+  // a set-up call (the reference's constructor-time uploads): the host
+  // tables are copied before it returns
+  hipStream_t st = S(stream);
+  if (hipMemcpyAsync(table, ct.data(), tn * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+      hipMemcpyAsync(table + tn, stb.data(), tn * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    KFAIL(NEON_EHIP, "neon_rope_table: copy failed");
   return NEON_OK;
+}
+
+extern "C" neon_status neon_rope_yarn(uint16_t* x, const int32_t* pos, int n_tok,
+                                      int n_heads, int head_dim, const float* table,
+                                      int n_pos, void* stream) {
+  if (!x || !pos || !table) KFAIL(NEON_EINVAL, "neon_rope_yarn: null pointer");
+  if (n_tok < 1 || n_heads < 1 || head_dim < 2 || head_dim % 2 || head_dim > 512 || n_pos < 1)
+    KFAIL(NEON_EINVAL, "neon_rope_yarn: bad shape n_tok=%d n_heads=%d head_dim=%d n_pos=%d",
+          n_tok, n_heads, head_dim, n_pos);
+  // pos[t] must lie in [0, n_pos): device data, trusted by the kernel
+  const size_t tn = (size_t)n_pos * (head_dim / 2);
+  launch_rope_apply(x, pos, table, table + tn, n_tok, n_heads, head_dim, S(stream));
+  KLAUNCHED();
 }
 
 extern "C" neon_status neon_router_topk(const uint16_t* x, const uint16_t* W,
                                         const uint16_t* b, int32_t* idx,
                                         float* score, float* logits, int B, int E,
                                         int H, int k, void* stream) {
-  if (!x || !W || !b || !idx || !score) KFAIL(NEON_EINVAL, "neon_router_topk: null pointer");
+  if (!x || !W || !b || !idx || !score || !logits)
+    KFAIL(NEON_EINVAL, "neon_router_topk: null pointer");
   if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < 8 ||
       H % 8 || H > 8192)
     KFAIL(NEON_EINVAL, "neon_router_topk: bad shape B=%d E=%d H=%d k=%d", B, E, H, k);
-  hipStream_t st = S(stream);
-  float* scratch = nullptr;
-  if (!logits && hipMallocAsync((void**)&scratch, (size_t)B * E * 4, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_router_topk: scratch allocation failed");
   RouterArgs r;
-  r.x = x; r.W = W; r.bias = b; r.lg_out = logits ? logits : scratch; r.idx = idx;
+  r.x = x; r.W = W; r.bias = b; r.lg_out = logits; r.idx = idx;
   r.score = score; r.B = B; r.E = E; r.H = H; r.k = k;
-  launch_router(r, st);
-  hipError_t e = hipGetLastError();
-  if (scratch) (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_router_topk: launch failed: %s", hipGetErrorString(e));
-  return NEON_OK;
+  launch_router(r, S(stream));
+  KLAUNCHED();
+}
+
+// Workspace of neon_moe_layer: act [B][k][I] bf16, the router logits [B][E]
+// fp32, and the arrival counters of the one-launch experts (NEON_MOE_FUSED;
+// the router launch clears them), each 256-byte aligned.
+struct MoeLayerWs {
+  size_t act, lg, total;
+};
+static MoeLayerWs moe_layer_ws(int B, int E, int I, int k) {
+  MoeLayerWs w;
+  w.act = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
+  w.lg = ((size_t)B * E * 4 + 255) & ~(size_t)255;
+  w.total = w.act + w.lg + (size_t)kMoeSyncInts * 4;
+  return w;
+}
+
+extern "C" size_t neon_moe_layer_workspace(int B, int E, int I, int k) {
+  if (B < 1 || E < 1 || I < 1 || k < 1) return 0;
+  return moe_layer_ws(B, E, I, k).total;
 }
 
 extern "C" neon_status neon_moe_layer(
@@ -1503,24 +1525,23 @@ extern "C" neon_status neon_moe_layer(
     const uint8_t* gu_codes, const uint8_t* gu_scales, const uint16_t* gu_bias,
     const uint8_t* dn_codes, const uint8_t* dn_scales, const uint16_t* dn_bias,
     const uint16_t* residual, uint16_t* out, int32_t* idx, float* score, int B,
-    int E, int H, int I, int k, float alpha, float limit, void* stream) {
+    int E, int H, int I, int k, float alpha, float limit, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (!x || !router_w || !router_b || !gu_codes || !gu_scales || !gu_bias ||
-      !dn_codes || !dn_scales || !dn_bias || !out)
+      !dn_codes || !dn_scales || !dn_bias || !out || !workspace)
     KFAIL(NEON_EINVAL, "neon_moe_layer: null pointer");
   if (B < 1 || B > 65535 || E < 1 || E > 256 || k < 1 || k > 16 || k > E ||
       H < 32 || H % 32 || H > 8192 || I < 32 || I % 32 || I > 8192)
     KFAIL(NEON_EINVAL, "neon_moe_layer: bad shape B=%d E=%d H=%d I=%d k=%d", B, E, H, I, k);
+  const MoeLayerWs w = moe_layer_ws(B, E, I, k);
+  if (workspace_bytes < w.total)
+    KFAIL(NEON_EINVAL, "neon_moe_layer: workspace of %zu bytes, %zu needed "
+          "(neon_moe_layer_workspace)", workspace_bytes, w.total);
   hipStream_t st = S(stream);
-  // scratch: act [B][k][I] bf16, the router logits [B][E], and the arrival
-  // counters of the one-launch experts (batch 1)
-  const size_t act_b = ((size_t)B * k * I * 2 + 255) & ~(size_t)255;
-  const size_t lg_b = ((size_t)B * E * 4 + 255) & ~(size_t)255;
-  char* scratch = nullptr;
-  if (hipMallocAsync((void**)&scratch, act_b + lg_b + kMoeSyncInts * 4, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_moe_layer: scratch allocation failed");
-  uint16_t* act = (uint16_t*)scratch;
-  float* lg = (float*)(scratch + act_b);
-  int32_t* sync = (int32_t*)(scratch + act_b + lg_b);
+  char* base = (char*)workspace;
+  uint16_t* act = (uint16_t*)base;
+  float* lg = (float*)(base + w.act);
+  int32_t* sync = (int32_t*)(base + w.act + w.lg);
   RouterArgs r;
   r.x = x; r.W = router_w; r.bias = router_b; r.lg_out = lg;
   r.B = B; r.E = E; r.H = H; r.k = k;
@@ -1535,10 +1556,7 @@ extern "C" neon_status neon_moe_layer(
   m.err = device_status_word();
   m.sync = getenv("NEON_MOE_FUSED") && getenv("NEON_MOE_FUSED")[0] == '1' ? sync : nullptr;
   launch_moe(m, st);
-  hipError_t e = hipGetLastError();
-  (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_moe_layer: launch failed: %s", hipGetErrorString(e));
-  return NEON_OK;
+  KLAUNCHED();
 }
 
 // ---- neon_moe_layer without allocation -----------------------------------
@@ -1638,66 +1656,87 @@ extern "C" neon_status neon_moe_experts(
   KLAUNCHED();
 }
 
+static bool attn_shape_ok(int B, int Hq, int Hkv, int D, int T_max, int window) {
+  if (D != 64 || B < 1 || B > 65535 || Hkv < 1 || Hq < Hkv || Hq % Hkv || T_max < 1 ||
+      window < 0)
+    return false;
+  const int G = Hq / Hkv;
+  return G == 1 || G == 2 || G == 4 || G == 8;
+}
+
+// Split partials of neon_attn_decode: o [B][Hq][S][D], then (m, l)
+// [B][Hq][S][2], fp32; none with one split.
+extern "C" size_t neon_attn_decode_workspace(int B, int Hq, int Hkv, int D, int T_max,
+                                             int window) {
+  if (!attn_shape_ok(B, Hq, Hkv, D, T_max, window)) return 0;
+  const int nsplit = attn_splits(T_max, window);
+  if (nsplit == 1) return 0;
+  return (size_t)B * Hq * nsplit * (D + 2) * 4;
+}
+
+// Arrival counters: one 256-byte line per (row, kv head).
+extern "C" size_t neon_attn_decode_counters(int B, int Hkv) {
+  if (B < 1 || Hkv < 1) return 0;
+  return (size_t)B * Hkv * kAttnArriveStride * 4;
+}
+
 extern "C" neon_status neon_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                                         const uint16_t* v_cache,
                                         const uint16_t* sinks, const int32_t* pos,
                                         uint16_t* out, int B, int Hq, int Hkv, int D,
-                                        int T_max, int window, void* stream) {
+                                        int T_max, int window, float* workspace,
+                                        size_t workspace_bytes, int32_t* counters,
+                                        size_t counter_bytes, void* stream) {
   if (!q || !k_cache || !v_cache || !sinks || !pos || !out)
     KFAIL(NEON_EINVAL, "neon_attn_decode: null pointer");
-  if (D != 64 || B < 1 || B > 65535 || Hkv < 1 || Hq < Hkv || Hq % Hkv || T_max < 1 ||
-      window < 0)
-    KFAIL(NEON_EINVAL, "neon_attn_decode: bad shape");
-  const int G = Hq / Hkv;
-  if (G != 1 && G != 2 && G != 4 && G != 8)
-    KFAIL(NEON_EINVAL, "neon_attn_decode: Hq/Hkv must be 1, 2, 4 or 8");
+  if (!attn_shape_ok(B, Hq, Hkv, D, T_max, window))
+    KFAIL(NEON_EINVAL, "neon_attn_decode: bad shape (D must be 64, Hq/Hkv 1, 2, 4 or 8)");
   // pos[b] must lie in [0, T_max); it is device data, so the kernel trusts it.
-  hipStream_t st = S(stream);
   const int nsplit = attn_splits(T_max, window);
+  const size_t need = neon_attn_decode_workspace(B, Hq, Hkv, D, T_max, window);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+    KFAIL(NEON_EINVAL, "neon_attn_decode: %d key splits need a workspace of %zu bytes "
+          "(given %zu)", nsplit, need, workspace_bytes);
+  if (nsplit > 1 && (counters == nullptr || counter_bytes < neon_attn_decode_counters(B, Hkv)))
+    KFAIL(NEON_EINVAL, "neon_attn_decode: %d key splits need %zu bytes of arrival counters "
+          "(given %zu)", nsplit, neon_attn_decode_counters(B, Hkv), counter_bytes);
+  // the last split block of each (row, kv head) to arrive on its counter
+  // merges and sets the counter back to 0: the caller zeroes the counters
+  // once, every call leaves them zero
   const size_t np = (size_t)B * Hq * nsplit;
-  // split partials: o [np][D], then (m, l) [np][2], then the arrival
-  // counters [B][Hkv] (zeroed here; the last split block of each kv head
-  // merges); one split finishes in the split kernel and needs none
-  const size_t n_arr = (size_t)B * Hkv * kAttnArriveStride;
-  float* scratch = nullptr;
-  if (nsplit > 1 && hipMallocAsync((void**)&scratch, (np * (D + 2) + n_arr) * 4, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_attn_decode: scratch allocation failed");
-  int32_t* arrive = nsplit > 1 ? reinterpret_cast<int32_t*>(scratch + np * (D + 2)) : nullptr;
-  if (arrive != nullptr && hipMemsetAsync(arrive, 0, n_arr * 4, st) != hipSuccess) {
-    (void)hipFreeAsync(scratch, st);
-    KFAIL(NEON_EHIP, "neon_attn_decode: clearing the arrival counters failed");
-  }
   AttnArgs a;
   a.q = q; a.kc = k_cache; a.vc = v_cache;
   a.sinks = sinks; a.pos = pos; a.out = out;
-  a.part_o = scratch; a.part_ml = scratch + np * D; a.seq = nullptr; a.arrive = arrive;
+  a.part_o = nsplit > 1 ? workspace : nullptr;
+  a.part_ml = nsplit > 1 ? workspace + np * D : nullptr;
+  a.seq = nullptr; a.arrive = nsplit > 1 ? counters : nullptr;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.T_max = T_max; a.key_mask = -1; a.window = window;
   a.S = nsplit; a.q_stride = Hq * D;
-  launch_attn(a, st);
-  hipError_t e = hipGetLastError();
-  if (scratch) (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_attn_decode: launch failed: %s", hipGetErrorString(e));
-  return NEON_OK;
+  launch_attn(a, S(stream));
+  KLAUNCHED();
+}
+
+extern "C" size_t neon_sample_workspace(int B, int V) {
+  if (B < 1 || V < 1) return 0;
+  return (size_t)B * V * 4;
 }
 
 extern "C" neon_status neon_sample(const float* logits, int B, int V, float temperature,
                                    float top_p, uint64_t seed, const int32_t* pos,
-                                   int32_t* out_ids, void* stream) {
-  if (!logits || !pos || !out_ids) KFAIL(NEON_EINVAL, "neon_sample: null pointer");
+                                   int32_t* out_ids, float* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  if (!logits || !pos || !out_ids || !workspace) KFAIL(NEON_EINVAL, "neon_sample: null pointer");
   if (B < 1 || B > 65535 || V < 1 || !(temperature > 0.0f) || !(temperature < 3.0e38f) ||
       !(top_p > 0.0f && top_p <= 1.0f))
     KFAIL(NEON_EINVAL, "neon_sample: bad shape or sampling parameters");
-  hipStream_t st = S(stream);
-  float* scratch = nullptr;  // the exp values [B][V]
-  if (hipMallocAsync((void**)&scratch, (size_t)B * V * 4, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "neon_sample: scratch allocation failed");
-  // pos is read only (advance = false): cast for the shared kernel signature
-  launch_sample(logits, B, V, temperature, top_p, seed, const_cast<int32_t*>(pos), scratch,
-                out_ids, nullptr, 0, nullptr, false, st);
-  hipError_t e = hipGetLastError();
-  (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "neon_sample: launch failed: %s", hipGetErrorString(e));
-  return NEON_OK;
+  if (workspace_bytes < neon_sample_workspace(B, V))
+    KFAIL(NEON_EINVAL, "neon_sample: workspace of %zu bytes, %zu needed", workspace_bytes,
+          neon_sample_workspace(B, V));
+  // the exp values [B][V] go to the workspace; pos is read only (advance =
+  // false): cast for the shared kernel signature
+  launch_sample(logits, B, V, temperature, top_p, seed, const_cast<int32_t*>(pos), workspace,
+                out_ids, nullptr, 0, nullptr, false, S(stream));
+  KLAUNCHED();
 }
 
 extern "C" neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
@@ -1711,6 +1750,38 @@ extern "C" neon_status neon_gemm_bf16(const uint16_t* A, const uint16_t* W,
   KLAUNCHED();
 }
 
+// Workspace layout of the kernel-level expert FFN over prompt rows: fp32
+// slot outputs, the SwiGLU output, the expert grouping (per-pair token and
+// slot lists, expert offsets, tile lists) and, for the MXFP8 form, the
+// two-term quantised GEMM inputs and their scales; each 256-byte aligned.
+struct MoePrefillWs {
+  size_t yb, act, lt, ls, eo, te, tr, nt, q, qs, total;
+};
+static MoePrefillWs moe_prefill_ws(int M, int E, int H, int I, int k, bool mx8) {
+  const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
+  const size_t qn = mx8 ? std::max((size_t)M * H, pairs * I) : 0;
+  MoePrefillWs w;
+  size_t off = 0;
+  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
+  w.yb = take(pairs * H * 4); w.act = take(pairs * I * 2); w.lt = take(pairs * 4);
+  w.ls = take(pairs * 4); w.eo = take((E + 1) * 4); w.te = take(tiles * 4);
+  w.tr = take(tiles * 4); w.nt = take(16); w.q = take(2 * qn);
+  w.qs = take(mx8 ? std::max(mx8_scale_bytes(M, H), mx8_scale_bytes(pairs, I)) : 0);
+  w.total = off;
+  return w;
+}
+
+static bool moe_prefill_shape_ok(int M, int E, int H, int I, int k, bool mx8) {
+  const int kq = mx8 ? 64 : 32;
+  return M >= 1 && M <= (1 << 20) && E >= 1 && E <= 256 && k >= 1 && k <= 16 && k <= E &&
+         H >= kq && H % kq == 0 && H <= 8192 && I >= kq && I % kq == 0 && I <= 8192;
+}
+
+extern "C" size_t neon_moe_prefill_workspace(int M, int E, int H, int I, int k, int mx8) {
+  if (!moe_prefill_shape_ok(M, E, H, I, k, mx8 != 0)) return 0;
+  return moe_prefill_ws(M, E, H, I, k, mx8 != 0).total;
+}
+
 // The kernel-level expert FFN over prompt rows, with the bf16-dequantising
 // GEMMs or (mx8) the scaled MXFP8 x MXFP4 ones.
 static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const float* score,
@@ -1718,48 +1789,37 @@ static neon_status moe_prefill_impl(const uint16_t* x, const int32_t* idx, const
                                     const uint16_t* gu_bias, const uint8_t* dn_codes,
                                     const uint8_t* dn_scales, const uint16_t* dn_bias,
                                     uint16_t* h, int M, int E, int H, int I, int k, float alpha,
-                                    float limit, void* stream, bool mx8, const char* fn) {
+                                    float limit, void* workspace, size_t workspace_bytes,
+                                    void* stream, bool mx8, const char* fn) {
   if (!x || !idx || !score || !gu_codes || !gu_scales || !gu_bias || !dn_codes ||
-      !dn_scales || !dn_bias || !h)
+      !dn_scales || !dn_bias || !h || !workspace)
     KFAIL(NEON_EINVAL, "%s: null pointer", fn);
-  const int kq = mx8 ? 64 : 32;
-  if (M < 1 || M > (1 << 20) || E < 1 || E > 256 || k < 1 || k > 16 || k > E || H < kq ||
-      H % kq || H > 8192 || I < kq || I % kq || I > 8192)
+  if (!moe_prefill_shape_ok(M, E, H, I, k, mx8))
     KFAIL(NEON_EINVAL, "%s: bad shape M=%d E=%d H=%d I=%d k=%d", fn, M, E, H, I, k);
   if (!kBatchedPrefillEnabled)
     KFAIL(NEON_ESTATE, "%s: the batched prompt pass is switched off", fn);
+  const MoePrefillWs w = moe_prefill_ws(M, E, H, I, k, mx8);
+  if (workspace_bytes < w.total)
+    KFAIL(NEON_EINVAL, "%s: workspace of %zu bytes, %zu needed (neon_moe_prefill_workspace)",
+          fn, workspace_bytes, w.total);
   // idx is device data: an entry outside [0, E) drops its slot and sets the
   // device status word (neon_device_check reports it).
-  hipStream_t st = S(stream);
-  const size_t pairs = (size_t)M * k, tiles = (size_t)moe_prefill_max_tiles(M, k, E);
-  const size_t qn = mx8 ? std::max((size_t)M * H, pairs * I) : 0;
-  size_t off = 0;
-  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b); return o; };
-  const size_t o_yb = take(pairs * H * 4), o_act = take(pairs * I * 2), o_lt = take(pairs * 4),
-               o_ls = take(pairs * 4), o_eo = take((E + 1) * 4), o_te = take(tiles * 4),
-               o_tr = take(tiles * 4), o_nt = take(16), o_q = take(2 * qn),
-               o_qs = take(mx8 ? std::max(mx8_scale_bytes(M, H), mx8_scale_bytes(pairs, I)) : 0);
-  char* scratch = nullptr;
-  if (hipMallocAsync((void**)&scratch, off, st) != hipSuccess)
-    KFAIL(NEON_ENOMEM, "%s: scratch allocation failed", fn);
+  char* base = (char*)workspace;
   MoePrefillArgs m;
   m.idx = idx; m.score = score; m.xn = x; m.h = h;
   m.gu_codes = gu_codes; m.gu_scales = gu_scales; m.gu_bias = gu_bias;
   m.dn_codes = dn_codes; m.dn_scales = dn_scales; m.dn_bias = dn_bias;
   m.M = M; m.E = E; m.H = H; m.I = I; m.k = k; m.alpha = alpha; m.limit = limit;
-  m.ybuf = (float*)(scratch + o_yb); m.act = (uint16_t*)(scratch + o_act);
-  m.list_tok = (int32_t*)(scratch + o_lt); m.list_slot = (int32_t*)(scratch + o_ls);
-  m.e_off = (int32_t*)(scratch + o_eo); m.tile_e = (int32_t*)(scratch + o_te);
-  m.tile_r0 = (int32_t*)(scratch + o_tr); m.n_tiles = (int32_t*)(scratch + o_nt);
+  m.ybuf = (float*)(base + w.yb); m.act = (uint16_t*)(base + w.act);
+  m.list_tok = (int32_t*)(base + w.lt); m.list_slot = (int32_t*)(base + w.ls);
+  m.e_off = (int32_t*)(base + w.eo); m.tile_e = (int32_t*)(base + w.te);
+  m.tile_r0 = (int32_t*)(base + w.tr); m.n_tiles = (int32_t*)(base + w.nt);
   if (mx8) {
-    m.q = (uint8_t*)(scratch + o_q); m.qs = (uint32_t*)(scratch + o_qs);
+    m.q = (uint8_t*)(base + w.q); m.qs = (uint32_t*)(base + w.qs);
   }
   m.err = device_status_word();
-  launch_moe_prefill(m, st);
-  hipError_t e = hipGetLastError();
-  (void)hipFreeAsync(scratch, st);
-  if (e != hipSuccess) KFAIL(NEON_EHIP, "%s: launch failed: %s", fn, hipGetErrorString(e));
-  return NEON_OK;
+  launch_moe_prefill(m, S(stream));
+  KLAUNCHED();
 }
 
 extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
@@ -1768,10 +1828,11 @@ extern "C" neon_status neon_moe_prefill(const uint16_t* x, const int32_t* idx,
                                         const uint8_t* dn_codes, const uint8_t* dn_scales,
                                         const uint16_t* dn_bias, uint16_t* h, int M, int E,
                                         int H, int I, int k, float alpha, float limit,
+                                        void* workspace, size_t workspace_bytes,
                                         void* stream) {
   return moe_prefill_impl(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
-                          dn_bias, h, M, E, H, I, k, alpha, limit, stream, false,
-                          "neon_moe_prefill");
+                          dn_bias, h, M, E, H, I, k, alpha, limit, workspace, workspace_bytes,
+                          stream, false, "neon_moe_prefill");
 }
 
 extern "C" neon_status neon_moe_prefill_mx8(const uint16_t* x, const int32_t* idx,
@@ -1780,10 +1841,11 @@ extern "C" neon_status neon_moe_prefill_mx8(const uint16_t* x, const int32_t* id
                                             const uint8_t* dn_codes, const uint8_t* dn_scales,
                                             const uint16_t* dn_bias, uint16_t* h, int M, int E,
                                             int H, int I, int k, float alpha, float limit,
+                                            void* workspace, size_t workspace_bytes,
                                             void* stream) {
   return moe_prefill_impl(x, idx, score, gu_codes, gu_scales, gu_bias, dn_codes, dn_scales,
-                          dn_bias, h, M, E, H, I, k, alpha, limit, stream, true,
-                          "neon_moe_prefill_mx8");
+                          dn_bias, h, M, E, H, I, k, alpha, limit, workspace, workspace_bytes,
+                          stream, true, "neon_moe_prefill_mx8");
 }
 
 extern "C" neon_status neon_mx8_quant(const uint16_t* x, int64_t rows, int K, uint8_t* hi,

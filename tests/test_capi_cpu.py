@@ -77,11 +77,11 @@ def test_context_calls_reject_null_context():
 def test_kernel_entry_points_validate_on_host():
     L = ne.lib()
     p = C.c_void_p(16)  # never dereferenced: validation fails first
-    assert L.neon_sample(None, 1, 8, 1.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL
-    assert L.neon_sample(p, 1, 8, 0.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL   # temperature
-    assert L.neon_sample(p, 1, 8, 1.0, 0.0, 0, p, p, None) == ne.NEON_EINVAL   # top_p
-    assert L.neon_sample(p, 1, 8, 1.0, 1.5, 0, p, p, None) == ne.NEON_EINVAL
-    assert L.neon_sample(p, 0, 8, 1.0, 1.0, 0, p, p, None) == ne.NEON_EINVAL
+    assert L.neon_sample(None, 1, 8, 1.0, 1.0, 0, p, p, p, 1 << 20, None) == ne.NEON_EINVAL
+    assert L.neon_sample(p, 1, 8, 0.0, 1.0, 0, p, p, p, 1 << 20, None) == ne.NEON_EINVAL   # temperature
+    assert L.neon_sample(p, 1, 8, 1.0, 0.0, 0, p, p, p, 1 << 20, None) == ne.NEON_EINVAL   # top_p
+    assert L.neon_sample(p, 1, 8, 1.0, 1.5, 0, p, p, p, 1 << 20, None) == ne.NEON_EINVAL
+    assert L.neon_sample(p, 0, 8, 1.0, 1.0, 0, p, p, p, 1 << 20, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_gemv(None, p, None, p, p, 8, 64, 1, None) == ne.NEON_EINVAL
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 8, 48, 1, None) == ne.NEON_EINVAL   # K % 32
     assert L.neon_mxfp4_gemv(p, p, None, p, p, 0, 64, 1, None) == ne.NEON_EINVAL
@@ -95,16 +95,48 @@ def test_kernel_entry_points_validate_on_host():
     assert L.neon_rmsnorm(p, p, p, 1, 2880, 0.0, None) == ne.NEON_EINVAL
     assert L.neon_router_topk(p, p, p, p, p, None, 1, 32, 2880, 40, None) == ne.NEON_EINVAL
     assert L.neon_moe_layer(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 0, 1.702, 7.0,
-                            None) == ne.NEON_EINVAL
-    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
-    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 5, 64, 64, 0, None) == ne.NEON_EINVAL   # Hq % Hkv
+                            p, 1 << 30, None) == ne.NEON_EINVAL
+    # a workspace smaller than neon_moe_layer_workspace's figure
+    need = L.neon_moe_layer_workspace(1, 32, 2880, 4)
+    assert need >= 4 * 2880 * 2 + 32 * 4
+    assert L.neon_moe_layer(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 4, 1.702, 7.0,
+                            p, need - 1, None) == ne.NEON_EINVAL
+    assert L.neon_moe_layer(*([p] * 9), None, p, None, None, 1, 32, 2880, 2880, 4, 1.702, 7.0,
+                            None, need, None) == ne.NEON_EINVAL
+    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 8, 128, 64, 0, p, 1 << 30, p, 1 << 30,
+                              None) == ne.NEON_EINVAL  # D
+    assert L.neon_attn_decode(p, p, p, p, p, p, 1, 64, 5, 64, 64, 0, p, 1 << 30, p, 1 << 30,
+                              None) == ne.NEON_EINVAL  # Hq % Hkv
+    # split partials and arrival counters sized by the queries: one split
+    # (the 128-key window) needs neither, 32 splits need both
+    assert L.neon_attn_decode_workspace(4, 64, 8, 64, 32768, 128) == 0
+    ws = L.neon_attn_decode_workspace(4, 64, 8, 64, 32768, 0)
+    assert ws == 4 * 64 * 32 * 66 * 4
+    cn = L.neon_attn_decode_counters(4, 8)
+    assert cn >= 4 * 8 * 4
+    assert L.neon_attn_decode(p, p, p, p, p, p, 4, 64, 8, 64, 32768, 0, p, ws - 4, p, cn,
+                              None) == ne.NEON_EINVAL
+    assert L.neon_attn_decode(p, p, p, p, p, p, 4, 64, 8, 64, 32768, 0, p, ws, p, cn - 4,
+                              None) == ne.NEON_EINVAL
+    assert L.neon_attn_decode(p, p, p, p, p, p, 4, 64, 8, 64, 32768, 0, None, ws, p, cn,
+                              None) == ne.NEON_EINVAL
+    assert L.neon_sample_workspace(3, 1000) == 3 * 1000 * 4
+    assert L.neon_sample(p, 3, 1000, 1.0, 0.9, 0, p, p, p, 3 * 1000 * 4 - 4,
+                         None) == ne.NEON_EINVAL
+    assert L.neon_router_topk(p, p, p, p, p, None, 1, 32, 2880, 4, None) == ne.NEON_EINVAL
     assert L.neon_gemm_bf16(None, p, None, p, 8, 8, 64, 0, None) == ne.NEON_EINVAL
     assert L.neon_gemm_bf16(p, p, None, p, 8, 8, 48, 0, None) == ne.NEON_EINVAL     # K % 32
     assert L.neon_gemm_bf16(p, p, None, p, 0, 8, 64, 0, None) == ne.NEON_EINVAL
-    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2880, 0, 1.702, 7.0,
+    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2880, 0, 1.702, 7.0, p, 1 << 30,
                               None) == ne.NEON_EINVAL                              # k = 0
-    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2872, 4, 1.702, 7.0,
+    assert L.neon_moe_prefill(*([p] * 10), 4, 32, 2880, 2872, 4, 1.702, 7.0, p, 1 << 30,
                               None) == ne.NEON_EINVAL                              # I % 32
+    need = L.neon_moe_prefill_workspace(64, 32, 2880, 2880, 4, 0)
+    need8 = L.neon_moe_prefill_workspace(64, 32, 2880, 2880, 4, 1)
+    assert need >= 64 * 4 * 2880 * 4 and need8 > need
+    assert L.neon_moe_prefill_workspace(64, 32, 2880, 2880, 4, 1) == need8
+    assert L.neon_moe_prefill(*([p] * 10), 64, 32, 2880, 2880, 4, 1.702, 7.0, p, need - 1,
+                              None) == ne.NEON_EINVAL
     assert L.neon_attn_prefill(p, p, p, p, p, 16, 64, 8, 128, 64, 0, None) == ne.NEON_EINVAL  # D
     assert L.neon_attn_prefill(p, p, p, p, p, 65, 64, 8, 64, 64, 0, None) == ne.NEON_EINVAL   # T_max < M
     # the allocation-free MoE layer: same shape checks, plus its fixed 4 MiB
@@ -176,3 +208,19 @@ def test_one_hip_runtime_per_process():
     maps = ast.literal_eval(out.strip().splitlines()[-1])
     assert sum("libamdhip64" in m for m in maps) == 1, maps
     assert sum("libhsa-runtime64" in m for m in maps) == 1, maps
+
+
+def test_kernel_tier_allocates_nothing():
+    """No kernel-level entry point allocates device memory: the library's
+    sources hold no stream-ordered allocation at all, and every hipMalloc
+    fills a member of the context (weights, KV cache, work and prompt
+    buffers, the matrix-core copies), allocated at set-up like the
+    reference's System buffers.  The kernel tier's scratch is caller-owned
+    (the *_workspace queries) and its status word a file-scope device array."""
+    import re
+    src = os.path.join(ROOT, "neonengine_amd", "csrc")
+    for name in os.listdir(src):
+        text = open(os.path.join(src, name)).read()
+        assert "hipMallocAsync" not in text and "hipFreeAsync" not in text, name
+        for m in re.finditer(r"hipMalloc\(([^,]*),", text):
+            assert m.group(1).strip().startswith("&ctx->"), (name, m.group(0))

@@ -177,7 +177,10 @@ def test_rope_yarn(orc):
     nh = 9
     x = orc.fill_bf16(0, 31, len(pos) * nh * 64, 0.0, 1.0)
     xd = to_dev(x)
-    ne.rope_yarn(xd, to_dev(pos), len(pos), nh, cfg)
+    torch = torch_cuda()
+    table = torch.empty(2 * 40000 * 32, dtype=torch.float32, device="cuda")
+    ne.rope_table(cfg, 40000, table)
+    ne.rope_yarn(xd, to_dev(pos), len(pos), nh, 64, table, 40000)
     got = to_host(xd).reshape(len(pos), nh * 64).astype(np.int32)
     c, s = orc.rope_table(ocfg, 40000)
     for t, p in enumerate(pos):
