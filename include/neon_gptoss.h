@@ -199,9 +199,24 @@ neon_status neon_read_activation(neon_ctx* ctx, const char* name, void* out,
  * equal prompt lengths every sequence holds this many. */
 neon_status neon_seq_len(const neon_ctx* ctx, int* out);
 
-/* Number of tokens held by each sequence (prompt + generated), out[batch];
- * NEON_ESTATE before the first prefill. */
+/* Number of tokens held by each sequence (prompt + generated), out[batch]
+ * (0 for a free row); NEON_ESTATE before the first prefill. */
 neon_status neon_seq_lens(const neon_ctx* ctx, int32_t* out);
+
+/* Continuous batching: a sequence joins a running context.  Its prompt
+ * ids[0 .. n-1] takes the lowest free batch row (one never used, or freed by
+ * neon_seq_remove) with that row's KV block, goes through the context's
+ * prompt mode, and its first generated token is chosen (written at
+ * position n of the row); no other sequence advances.  *slot receives the
+ * row.  Later neon_decode steps advance every held row.  NEON_EKV_FULL when
+ * every row of max_batch holds a sequence or n > max_seq.  (The reference
+ * has no counterpart: it renders one fixed scene per frame.) */
+neon_status neon_seq_add(neon_ctx* ctx, const int32_t* ids, int n, int* slot, void* stream);
+
+/* A sequence leaves: its batch row and KV block become free for the next
+ * neon_seq_add.  Steps leave a free row untouched (no token, no advance);
+ * free rows at the end of the batch leave the step altogether. */
+neon_status neon_seq_remove(neon_ctx* ctx, int slot, void* stream);
 
 /* Device pointer of a weight tensor (same names as neon_load_tensor), for
  * tests and tools; *bytes receives its size.  Read it freely; bytes written

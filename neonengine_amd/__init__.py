@@ -39,6 +39,7 @@ EXPORTS = (
     "neon_prefill_ragged", "neon_seq_lens", "neon_moe_prefill_mx8", "neon_mx8_quant",
     "neon_rope_table", "neon_moe_layer_workspace", "neon_attn_decode_workspace",
     "neon_attn_decode_counters", "neon_sample_workspace", "neon_moe_prefill_workspace",
+    "neon_seq_add", "neon_seq_remove",
 )
 
 
@@ -98,6 +99,8 @@ def lib():
             "neon_read_activation": [_P, C.c_char_p, _P, _SZ, _P],
             "neon_seq_len": [_P, _P],
             "neon_seq_lens": [_P, _P],
+            "neon_seq_add": [_P, _P, _I, _P, _P],
+            "neon_seq_remove": [_P, _I, _P],
             "neon_tensor_ptr": [_P, C.c_char_p, _P, _P],
             "neon_mxfp4_dequant": [_P, _P, _I64, _P, _P],
             "neon_mxfp4_gemv": [_P, _P, _P, _P, _P, _I, _I, _I, _P],
@@ -456,6 +459,26 @@ class Engine:
                                             lens.ctypes.data_as(C.c_void_p), len(prompts),
                                             _stream(stream)))
         self.batch = len(prompts)
+
+    def seq_add(self, prompt, stream=None) -> int:
+        """A sequence joins the running batch (neon_seq_add): returns its row."""
+        import numpy as np
+        ids = np.ascontiguousarray(prompt, dtype=np.int32)
+        slot = C.c_int(-1)
+        self._chk(lib().neon_seq_add(self._ctx, ids.ctypes.data_as(C.c_void_p), len(ids),
+                                     C.byref(slot), _stream(stream)))
+        self.batch = max(self.batch, slot.value + 1)
+        return slot.value
+
+    def seq_remove(self, slot: int, stream=None):
+        """A sequence leaves (neon_seq_remove): its row and KV block are free;
+        free rows at the end of the batch leave it."""
+        import numpy as np
+        held = self.seq_lens() if self.batch else np.zeros(0, np.int32)
+        self._chk(lib().neon_seq_remove(self._ctx, slot, _stream(stream)))
+        held[slot] = 0
+        nz = np.nonzero(held)[0]
+        self.batch = int(nz[-1]) + 1 if len(nz) else 0
 
     def seq_lens(self):
         """Tokens held by each sequence (prompt + generated), int32 [batch]."""

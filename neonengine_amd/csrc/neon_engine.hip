@@ -93,6 +93,11 @@ struct neon_ctx {
   int batch = 0;
   int host_pos = 0;                // the longest sequence's position
   std::vector<int> host_plen;      // prompt length of each sequence
+  // per batch row: the position of its next input token (the tokens it
+  // holds - 1) and whether a sequence holds it (neon_seq_add /
+  // neon_seq_remove); rows past `batch` are free
+  std::vector<int> host_seq_pos;
+  std::vector<char> host_active;
   bool weights_ready = false;
   // batched prefill (M prompt rows per pass): scratch grown on demand
   int prefill_mode = NEON_PREFILL_CHUNKED;
@@ -1076,7 +1081,11 @@ static neon_status prefill_seqs(neon_ctx* ctx, const int32_t* ids, const int32_t
   HIPCHK(ctx, hipStreamSynchronize(st));  // host staging buffers die here
   ctx->batch = batch;
   ctx->host_pos = 0;
-  ctx->host_plen.assign(lens, lens + batch);
+  ctx->host_plen.assign(c.max_batch, 0);
+  std::copy(lens, lens + batch, ctx->host_plen.begin());
+  ctx->host_seq_pos.assign(c.max_batch, 0);
+  ctx->host_active.assign(c.max_batch, 0);
+  for (int b = 0; b < batch; ++b) { ctx->host_seq_pos[b] = lens[b]; ctx->host_active[b] = 1; }
   if (max_len == 1 || (ctx->prefill_mode == NEON_PREFILL_STEPWISE && equal)) {
     // every prompt token as a decode step of all sequences together
     neon_status s = run_steps(ctx, max_len, st);
@@ -1233,13 +1242,18 @@ extern "C" neon_status neon_decode(neon_ctx* ctx, int n_steps, void* stream) {
   if (!ctx) return NEON_EINVAL;
   if (n_steps < 0) FAIL(ctx, NEON_EINVAL, "neon_decode: n_steps must be >= 0");
   if (ctx->batch == 0) FAIL(ctx, NEON_ESTATE, "neon_decode: call neon_prefill first");
-  if ((int64_t)ctx->host_pos + n_steps > ctx->cfg.max_seq)
+  int longest = 0;  // the longest sequence held (free rows do not advance)
+  for (int b = 0; b < ctx->batch; ++b)
+    if (ctx->host_active[b]) longest = std::max(longest, ctx->host_seq_pos[b]);
+  if ((int64_t)longest + n_steps > ctx->cfg.max_seq)
     FAIL(ctx, NEON_EKV_FULL, "neon_decode: %d steps from position %d exceed max_seq %d",
-         n_steps, ctx->host_pos, ctx->cfg.max_seq);
+         n_steps, longest, ctx->cfg.max_seq);
   HIPCHK(ctx, hipSetDevice(ctx->device));
   neon_status s = run_steps(ctx, n_steps, S(stream));
   if (s != NEON_OK) return s;
-  ctx->host_pos += n_steps;
+  for (int b = 0; b < ctx->batch; ++b)
+    if (ctx->host_active[b]) ctx->host_seq_pos[b] += n_steps;
+  ctx->host_pos = std::max(ctx->host_pos, longest + n_steps);
   return NEON_OK;
 }
 
@@ -1332,9 +1346,127 @@ extern "C" neon_status neon_seq_len(const neon_ctx* ctx, int* out) {
 extern "C" neon_status neon_seq_lens(const neon_ctx* ctx, int32_t* out) {
   if (!ctx || !out) return NEON_EINVAL;
   if (ctx->batch == 0) return NEON_ESTATE;
-  const int max_plen = *std::max_element(ctx->host_plen.begin(), ctx->host_plen.end());
   for (int b = 0; b < ctx->batch; ++b)
-    out[b] = ctx->host_plen[b] + 1 + (ctx->host_pos - max_plen);
+    out[b] = ctx->host_active[b] ? ctx->host_seq_pos[b] + 1 : 0;
+  return NEON_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Sequences joining and leaving a running batch.  Each batch row owns one KV
+// block (max_seq positions of every layer, a 256-row ring on sliding layers)
+// for as long as a sequence holds it; a removed sequence's row and block go
+// back to the pool and the next neon_seq_add takes the lowest free row.  The
+// steps run rows 0 .. batch-1; a free row keeps position 0, writes no token
+// and advances nothing (prompt_len < 0 on the device).
+// ---------------------------------------------------------------------------
+extern "C" neon_status neon_seq_add(neon_ctx* ctx, const int32_t* ids, int n, int* slot_out,
+                                    void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  const neon_config& c = ctx->cfg;
+  if (!ids || !slot_out) FAIL(ctx, NEON_EINVAL, "neon_seq_add: null ids or slot");
+  if (n < 1) FAIL(ctx, NEON_EINVAL, "neon_seq_add: the prompt needs >= 1 token");
+  if (n > c.max_seq)
+    FAIL(ctx, NEON_EKV_FULL, "neon_seq_add: %d prompt tokens exceed max_seq %d", n, c.max_seq);
+  for (int i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= c.vocab)
+      FAIL(ctx, NEON_ERANGE_TOKEN, "neon_seq_add: token id %d at %d outside [0, %d)", ids[i], i,
+           c.vocab);
+  if (!ctx->weights_ready) FAIL(ctx, NEON_ESTATE, "neon_seq_add: no weights loaded");
+  if ((int)ctx->host_active.size() != c.max_batch) {
+    ctx->host_active.assign(c.max_batch, 0);
+    ctx->host_seq_pos.assign(c.max_batch, 0);
+    ctx->host_plen.assign(c.max_batch, 0);
+  }
+  int slot = -1;
+  for (int b = 0; b < c.max_batch && slot < 0; ++b)
+    if (!ctx->host_active[b]) slot = b;
+  if (slot < 0)
+    FAIL(ctx, NEON_EKV_FULL, "neon_seq_add: all %d batch rows hold a sequence", c.max_batch);
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  hipStream_t st = S(stream);
+  // the row's tokens, its prompt length and the position of the last prompt
+  // token (the row's final prompt step below consumes it)
+  std::vector<int32_t> tok(ctx->tok_stride, 0);
+  memcpy(tok.data(), ids, (size_t)n * 4);
+  const int32_t meta[2] = {n - 1, n};
+  HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + (size_t)slot * ctx->tok_stride, tok.data(),
+                             tok.size() * 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->pos + slot, &meta[0], 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->prompt_len + slot, &meta[1], 4, hipMemcpyHostToDevice, st));
+  // rows 0 .. n-2 with the context's prompt mode (every row bit-identical to
+  // the same row of neon_prefill)
+  if (n > 1 && (ctx->prefill_mode == NEON_PREFILL_BATCHED ||
+                ctx->prefill_mode == NEON_PREFILL_MX8)) {
+    neon_status s = ensure_prefill_scratch(ctx, n - 1, st);
+    if (s != NEON_OK) return s;
+    enqueue_prefill_rows(ctx, slot, n - 1, st);
+  } else {
+    const int per = ctx->prefill_mode == NEON_PREFILL_STEPWISE ? 1 : kPromptRows;
+    std::vector<int32_t> rp, rs;
+    for (int p = 0; p < n; ++p) { rp.push_back(p); rs.push_back(slot); }
+    for (int r0 = 0; r0 + 1 < n; r0 += per) {
+      const int R = std::min(per, n - 1 - r0);
+      HIPCHK(ctx, hipMemcpyAsync(ctx->row_pos, &rp[r0], R * 4, hipMemcpyHostToDevice, st));
+      HIPCHK(ctx, hipMemcpyAsync(ctx->row_seq, &rs[r0], R * 4, hipMemcpyHostToDevice, st));
+      enqueue_rows(ctx, R, ctx->row_pos, ctx->row_seq, st);
+    }
+    HIPCHK(ctx, hipStreamSynchronize(st));  // rp and rs die here
+  }
+  // the last prompt token as a one-row step of this sequence alone: its
+  // logits land in the row's logits row, and the argmax (or the sampler,
+  // keyed by the row like a batch step) writes tokens[slot][n] and
+  // advances pos[slot] to n
+  const int32_t last[2] = {n - 1, slot};
+  HIPCHK(ctx, hipMemcpyAsync(ctx->row_pos, &last[0], 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->row_seq, &last[1], 4, hipMemcpyHostToDevice, st));
+  enqueue_rows(ctx, 1, ctx->row_pos, ctx->row_seq, st);
+  GemvArgs lm;
+  lm.mode = 2; lm.W = ctx->lm_head; lm.x = ctx->h; lm.norm_w = ctx->final_norm;
+  lm.eps = c.rms_eps; lm.logits = ctx->logits + (size_t)slot * c.vocab;
+  lm.part_val = ctx->lm_part_val; lm.part_idx = ctx->lm_part_idx; lm.N = c.vocab;
+  lm.K = c.hidden; lm.B = 1; lm.nblk = ctx->lm_nblk;
+  const int parts = launch_gemv_step(lm, 1, st);
+  int32_t* trow = ctx->tokens + (size_t)slot * ctx->tok_stride;
+  if (ctx->temperature > 0.0f)
+    launch_sample(ctx->logits + (size_t)slot * c.vocab, 1, c.vocab, ctx->temperature,
+                  ctx->top_p, ctx->sample_seed, ctx->pos + slot, ctx->sample_scratch,
+                  ctx->last_ids + slot, trow, ctx->tok_stride, ctx->prompt_len + slot, true, st,
+                  slot);
+  else
+    launch_argmax_advance(ctx->lm_part_val, ctx->lm_part_idx, parts, trow, ctx->tok_stride,
+                          ctx->pos + slot, ctx->prompt_len + slot, ctx->last_ids + slot, 1, st);
+  HIPCHK(ctx, hipGetLastError());
+  HIPCHK(ctx, hipStreamSynchronize(st));  // tok, meta and last die here
+  ctx->host_active[slot] = 1;
+  ctx->host_seq_pos[slot] = n;
+  ctx->host_plen[slot] = n;
+  ctx->batch = std::max(ctx->batch, slot + 1);
+  ctx->host_pos = std::max(ctx->host_pos, n);
+  *slot_out = slot;
+  return NEON_OK;
+}
+
+extern "C" neon_status neon_seq_remove(neon_ctx* ctx, int slot, void* stream) {
+  if (!ctx) return NEON_EINVAL;
+  if (slot < 0 || slot >= ctx->batch || (int)ctx->host_active.size() <= slot ||
+      !ctx->host_active[slot])
+    FAIL(ctx, NEON_EINVAL, "neon_seq_remove: batch row %d holds no sequence", slot);
+  HIPCHK(ctx, hipSetDevice(ctx->device));
+  hipStream_t st = S(stream);
+  // free row: position 0 (every later step writes its k / v at row 0 of its
+  // own block and reads a valid token id), prompt length -1 (no token
+  // written, nothing advanced)
+  const int32_t zero = 0, freed = -1;
+  HIPCHK(ctx, hipMemcpyAsync(ctx->pos + slot, &zero, 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->prompt_len + slot, &freed, 4, hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipMemcpyAsync(ctx->tokens + (size_t)slot * ctx->tok_stride, &zero, 4,
+                             hipMemcpyHostToDevice, st));
+  HIPCHK(ctx, hipStreamSynchronize(st));  // zero and freed die here
+  ctx->host_active[slot] = 0;
+  ctx->host_seq_pos[slot] = 0;
+  ctx->host_plen[slot] = 0;
+  // trailing free rows leave the step
+  while (ctx->batch > 0 && !ctx->host_active[ctx->batch - 1]) --ctx->batch;
   return NEON_OK;
 }
 

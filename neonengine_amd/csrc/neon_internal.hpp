@@ -78,7 +78,7 @@ int gemv_bt_grid(int N, int mode);
 void launch_sample(const float* logits, int B, int V, float temperature, float top_p,
                    uint64_t seed, int32_t* pos, float* scratch, int32_t* out_ids,
                    int32_t* tokens, int tok_stride, const int32_t* prompt_len, bool advance,
-                   hipStream_t st);
+                   hipStream_t st, int row0 = 0);
 void launch_argmax_advance(const float* part_val, const int32_t* part_idx,
                            int nparts, int32_t* tokens, int tok_stride,
                            int32_t* pos, const int32_t* prompt_len,

@@ -1218,7 +1218,8 @@ hipError_t launch_gemv_bf16_batched(const GemvArgs& a, hipStream_t st) {
 // Final argmax over the lm_head partials; advances the sequence.
 // grid B, block 256.  Greedy id = largest logit, ties to the lowest index.
 // tokens[b][pos+1] receives it unless that slot still belongs to the prompt
-// (teacher forcing); pos[b] += 1.
+// (teacher forcing); pos[b] += 1.  A free batch row (prompt_len < 0: a slot
+// no sequence holds) is left as it is.
 // ===========================================================================
 __global__ __launch_bounds__(256) void k_argmax_advance(
     const float* __restrict__ part_val, const int32_t* __restrict__ part_idx,
@@ -1245,10 +1246,12 @@ __global__ __launch_bounds__(256) void k_argmax_advance(
     for (int w = 1; w < (int)(blockDim.x >> 6); ++w)
       if (sv[w] > v || (sv[w] == v && si[w] < i)) { v = sv[w]; i = si[w]; }
     if (i == 0x7fffffff) i = 0;
-    const int p = pos[b];
-    if (p + 1 >= prompt_len[b]) tokens[(size_t)b * tok_stride + p + 1] = i;
-    last_ids[b] = i;
-    pos[b] = p + 1;
+    const int p = pos[b], pl = prompt_len[b];
+    if (pl >= 0) {
+      if (p + 1 >= pl) tokens[(size_t)b * tok_stride + p + 1] = i;
+      last_ids[b] = i;
+      pos[b] = p + 1;
+    }
   }
 }
 
@@ -1310,7 +1313,7 @@ __global__ __launch_bounds__(1024) void k_sample(
     const float* __restrict__ logits, int V, float inv_temp, float top_p, uint64_t seed,
     int32_t* __restrict__ pos, float* __restrict__ scratch, int32_t* __restrict__ out_ids,
     int32_t* __restrict__ tokens, int tok_stride, const int32_t* __restrict__ prompt_len,
-    int advance) {
+    int advance, int row0) {
   __shared__ float red[16];
   __shared__ float scan[1024];
   __shared__ int32_t pick;
@@ -1345,7 +1348,10 @@ __global__ __launch_bounds__(1024) void k_sample(
     }
   }
   const float t = __builtin_bit_cast(float, t_bits);
-  const uint64_t r = splitmix64(seed ^ splitmix64(((uint64_t)(uint32_t)b << 32) | (uint32_t)p));
+  // the RNG key is the batch row (row0 + b: a launch for one row of a batch
+  // keys it like the batch step) and the position
+  const uint64_t r = splitmix64(seed ^ splitmix64(((uint64_t)(uint32_t)(row0 + b) << 32) |
+                                                  (uint32_t)p));
   const float u = (float)(r >> 40) * 0x1.0p-24f;
   const float target = __fmul_rn(u, kept);
   // running sums in vocab order: thread tid owns the contiguous slice
@@ -1387,8 +1393,10 @@ __global__ __launch_bounds__(1024) void k_sample(
       for (int i = V - 1; i >= 0; --i) if (e[i] >= t) { id = i; break; }
       if (id < 0) id = 0;
     }
-    out_ids[b] = id;
-    if (advance) {
+    if (!advance) {
+      out_ids[b] = id;
+    } else if (prompt_len[b] >= 0) {  // a free batch row is left as it is
+      out_ids[b] = id;
       if (p + 1 >= prompt_len[b]) tokens[(size_t)b * tok_stride + p + 1] = id;
       pos[b] = p + 1;
     }
@@ -1398,10 +1406,10 @@ __global__ __launch_bounds__(1024) void k_sample(
 void launch_sample(const float* logits, int B, int V, float temperature, float top_p,
                    uint64_t seed, int32_t* pos, float* scratch, int32_t* out_ids,
                    int32_t* tokens, int tok_stride, const int32_t* prompt_len, bool advance,
-                   hipStream_t st) {
+                   hipStream_t st, int row0) {
   hipLaunchKernelGGL(k_sample, dim3(B), dim3(1024), 0, st, logits, V, 1.0f / temperature,
                      top_p, seed, pos, scratch, out_ids, tokens, tok_stride, prompt_len,
-                     advance ? 1 : 0);
+                     advance ? 1 : 0, row0);
 }
 
 // ===========================================================================

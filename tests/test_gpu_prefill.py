@@ -180,13 +180,13 @@ def prompt_pass(cfg, seed, prompt, n_steps, mode, fixed_routing=False):
 
 
 def compare_modes(cfg, seed, prompt, n_steps, fixed_routing=False, bar=2e-2,
-                  mode=ne.PREFILL_BATCHED):
-    """A matrix-core prompt pass (`mode`) vs the stepwise one (decode
-    kernels, bit-identical to the oracle)."""
+                  mode=ne.PREFILL_BATCHED, ref_mode=ne.PREFILL_STEPWISE):
+    """A matrix-core prompt pass (`mode`) vs an exact one (`ref_mode`:
+    stepwise or chunked, both bit-identical to the oracle)."""
     torch_cuda()
     say(f"prefill modes layers={cfg.n_layers} hidden={cfg.hidden} batch={len(prompt)} "
-        f"prompt={len(prompt[0])} fixed_routing={fixed_routing} mode={mode}")
-    lg_s, tok_s = prompt_pass(cfg, seed, prompt, n_steps, ne.PREFILL_STEPWISE, fixed_routing)
+        f"prompt={len(prompt[0])} fixed_routing={fixed_routing} mode={mode} ref={ref_mode}")
+    lg_s, tok_s = prompt_pass(cfg, seed, prompt, n_steps, ref_mode, fixed_routing)
     lg_b, tok_b = prompt_pass(cfg, seed, prompt, n_steps, mode, fixed_routing)
     rel = np.abs(lg_b - lg_s).max() / np.abs(lg_s).max()
     top2 = np.sort(lg_s, axis=1)[:, -2:]
@@ -246,6 +246,46 @@ def test_gpt_oss_20b_batched_prefill_full_depth():
     cfg = ne.config_preset("gpt-oss-20b", max_seq=512)
     prompt = [[(1009 * i + 17) % 201088 for i in range(300)]]
     rel, _ = compare_modes(cfg, 0, prompt, 16, fixed_routing=True, bar=bar)
+    assert rel < bar
+
+
+def conditioning_bar(key):
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "conditioning.npz")
+    with np.load(path, allow_pickle=False) as z:
+        return 2 * float(z[key].max())
+
+
+@pytest.mark.parametrize("mode", [ne.PREFILL_BATCHED, ne.PREFILL_MX8])
+def test_gpt_oss_20b_matrix_prefill_2048(mode):
+    """The matrix-core prompt passes at the length the bench quotes them: the
+    24-layer 20b model, a 2048-token prompt (32 key tiles per query tile in
+    the prompt attention, ~8k (row, slot) pairs in the expert grouping, the
+    XCD block order over many row tiles per expert), routing fixed, against
+    the exact chunked pass: the first token's logits within twice the
+    oracle's own reorder error at 24 layers."""
+    bar = conditioning_bar("fixed_24")
+    cfg = ne.config_preset("gpt-oss-20b", max_seq=2048 + 32)
+    rng = np.random.default_rng(2048)
+    prompt = [rng.integers(0, cfg.vocab, 2048).tolist()]
+    rel, _ = compare_modes(cfg, 0, prompt, 8, fixed_routing=True, bar=bar, mode=mode,
+                           ref_mode=ne.PREFILL_CHUNKED)
+    assert rel < bar
+
+
+@pytest.mark.parametrize("plen", [2048, 16384])
+def test_gpt_oss_120b_mx8_prefill(plen):
+    """Config 4: the gpt-oss-120b shape (36 layers, 128 experts), a 2048- and
+    a 16384-token prompt in the MXFP8 matrix-core pass against the exact
+    chunked pass, routing fixed: the first token's logits within twice the
+    oracle's own reorder error at 36 layers; then 8 greedy steps decode on
+    top of each."""
+    bar = conditioning_bar("fixed_36")
+    cfg = ne.config_preset("gpt-oss-120b", max_seq=plen + 16)
+    rng = np.random.default_rng(plen)
+    prompt = [rng.integers(0, cfg.vocab, plen).tolist()]
+    rel, _ = compare_modes(cfg, 1, prompt, 8, fixed_routing=True, bar=bar, mode=ne.PREFILL_MX8,
+                           ref_mode=ne.PREFILL_CHUNKED)
     assert rel < bar
 
 
