@@ -508,7 +508,7 @@ def main():
     bpt = step_bytes(cfg, kv_mid)
     log(f"[bench] {args.steps} steps x batch {B} in {elapsed * 1e3:.1f} ms -> {tok_s:.1f} tok/s"
         + (f" ({bpt * tok_s / 1e9:.0f} GB/s algorithmic)" if B == 1 else ""))
-    toks = eng.read_tokens(args.prompt, 8)
+    toks = eng.read_tokens(args.prompt, min(8, args.warmup + args.steps + 1))
     log(f"[bench] first generated ids {toks[0].tolist()}")
 
     mb = moe_bytes(cfg)

@@ -107,6 +107,102 @@ def test_config4_120b_greedy():
     run_fixture("l120b", "gpt-oss-120b")
 
 
+def test_config4_120b_2048_prompt_then_64_greedy():
+    """Config 4: gpt-oss-120b shape (36 layers, 128 experts), a 2048-token
+    prompt (default chunked pass), then 64 greedy steps: every logits row
+    bit-identical to the oracle (long120b fixture, lazy experts)."""
+    run_fixture("long120b", "gpt-oss-120b")
+
+
+def ragged_after_fixture(f, B, vocab, seed):
+    """Row 0: the fixture's prompt; rows 1 .. B-1: other prompts of 40 to
+    300 tokens (mixed lengths, several across the 256-row sliding ring)."""
+    rng = np.random.default_rng(seed)
+    rows = [f["prompt"][0].tolist()]
+    rows += [rng.integers(0, vocab, int(n)).tolist() for n in rng.integers(40, 300, B - 1)]
+    return rows
+
+
+@pytest.mark.parametrize("B", [16, 64])
+def test_config4_120b_batch_exact_row0_is_the_fixture(B):
+    """Config 4 at batch 16 and 64 (exact mode): row 0 holds the long120b
+    prompt, the other rows other prompts; exact batch rows are computed as at
+    batch 1, so row 0's 65 logits rows equal the batch-1 oracle's (SHA-256)."""
+    torch_cuda()
+    f = fixture("long120b")
+    seed, _, plen, steps, max_seq, layers = (int(v) for v in f["meta"])
+    cfg = ne.config_preset("gpt-oss-120b", max_seq=max_seq, max_batch=B)
+    eng = ne.Engine(cfg)
+    eng.init_random(seed)
+    eng.prefill_ragged(ragged_after_fixture(f, B, cfg.vocab, 100 + B))
+    bad = []
+    for s in range(steps + 1):
+        if s:
+            eng.decode(1)
+        lg = eng.read_logits()
+        if not np.array_equal(digest(lg[0]), f["sha"][0, s]):
+            bad.append(s)
+            break
+    toks = eng.read_tokens(start=plen, count=steps + 1)[0]
+    eng.close()
+    say(f"120b batch {B}: row 0 {'bit-identical' if not bad else 'DIFFERS at step %d' % bad[0]}")
+    assert not bad
+    assert np.array_equal(toks, f["ids"][0])
+
+
+def run_steps_120b(B, mode, prompts, n_steps, seed=3):
+    cfg = ne.config_preset("gpt-oss-120b", max_seq=2048 + 32, max_batch=B)
+    eng = ne.Engine(cfg)
+    eng.init_random(seed)
+    E, H = cfg.n_experts, cfg.hidden
+    for layer in range(cfg.n_layers):
+        p = f"model.layers.{layer}.mlp.router."
+        eng.load_tensor(p + "weight", np.zeros(E * H, np.uint16))
+        eng.load_tensor(p + "bias", fixed_routing_bias(E, layer))
+    eng.set_decode_mode(mode)
+    eng.prefill_ragged(prompts)  # the exact chunked prompt pass in both runs
+    lgs = []
+    for s in range(n_steps + 1):
+        if s:
+            eng.decode(1)
+        lgs.append(eng.read_logits())
+    toks = eng.read_tokens(start=0, count=max(len(p) for p in prompts) + n_steps + 1)
+    eng.close()
+    gen = np.stack([toks[b, len(p):len(p) + n_steps + 1] for b, p in enumerate(prompts)])
+    return lgs, gen
+
+
+@pytest.mark.parametrize("B", [16, 64])
+def test_config4_120b_matrix_decode_vs_exact_fixed_routing(B):
+    """Config 4, NEON_DECODE_MATRIX at batch 16 and 64 on the 120b shape
+    after mixed prompts up to 2048 tokens (row 0 the long120b prompt), routing
+    fixed, against the exact steps on the same inputs (the exact path is the
+    oracle's bits, test above): every row of every step while the greedy ids
+    agree within twice the oracle's own reorder error at 36 layers (median
+    and maximum, tests/golden/conditioning.npz fixed_36)."""
+    torch_cuda()
+    f = fixture("long120b")
+    prompts = ragged_after_fixture(f, B, 201088, 200 + B)
+    n = 4
+    lg_x, gen_x = run_steps_120b(B, ne.DECODE_EXACT, prompts, n)
+    lg_m, gen_m = run_steps_120b(B, ne.DECODE_MATRIX, prompts, n)
+    ref = conditioning("fixed_36")
+    rels = []
+    for s in range(n + 1):
+        # step s consumed generated tokens 0 .. s-1: compare the rows whose
+        # tokens so far agree (a near-tied greedy choice may flip a row)
+        rows = np.array([np.array_equal(gen_m[b, :s], gen_x[b, :s]) for b in range(B)])
+        scale = np.abs(lg_x[s][rows]).max(axis=1)
+        rel = np.abs(lg_m[s][rows].astype(np.float64) - lg_x[s][rows]).max(axis=1) / scale
+        rels.append(rel)
+        say(f"  step {s}: {rows.sum()} rows, median {np.median(rel):.3e} max {rel.max():.3e} "
+            f"(reorder median {np.median(ref):.3e} max {ref.max():.3e})")
+    rels = np.concatenate(rels)
+    assert len(rels) >= B
+    assert np.median(rels) <= 2 * np.median(ref)
+    assert rels.max() <= 2 * ref.max()
+
+
 def test_config3_batch16_after_2048_prompt():
     """Config 3 at batch 16 after 2048-token prompts (exact mode): row 0
     holds the long20b fixture's prompt, rows 1-15 other 2048-token prompts.
