@@ -296,9 +296,8 @@ void launch_gemm_bf16(const uint16_t* A, int lda, const uint16_t* W, int ldw,
                       const uint16_t* bias, uint16_t* C, float* Cf, int ldc, int M,
                       int N, int K, int mode, hipStream_t st);
 // The prompt pass's projections (dense, lda = ldw = K, ldc = N; mode 0 or 1
-// as launch_gemm_bf16): hipBLASLt's bf16 GEMM with the bias epilogue (and
-// beta = 1 into C for the residual: one rounding of acc + bias + C), or
-// launch_gemm_bf16 when hipBLASLt offers no algorithm or NEON_PROMPT_BLAS=0.
+// as launch_gemm_bf16, whose direct-load kernel takes them; for the residual
+// C = bf16(C + bf16(acc + bias))).
 void launch_prompt_proj(const uint16_t* A, const uint16_t* W, const uint16_t* bias,
                         uint16_t* C, int M, int N, int K, int mode, hipStream_t st);
 void launch_rope_kv_rows(const uint16_t* qkv, int q_stride, const float* cos_t,

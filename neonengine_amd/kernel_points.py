@@ -2,13 +2,16 @@
 
     python3 -m neonengine_amd.kernel_points attn T B WINDOW [--reps R]
     python3 -m neonengine_amd.kernel_points gemv N B [--reps R]
+    python3 -m neonengine_amd.kernel_points gemm M N K RESID [--reps R]
 
 `attn` runs neon_attn_decode (64 q / 8 kv heads, d = 64, N(0, 1) bf16 q, K,
 V and sinks; every row at position T - 1; full layer when WINDOW is 0) and
 `gemv` runs neon_mxfp4_gemv on an [N x 2880] MXFP4 matrix (codes uniform,
 E8M0 exponents in [-8, -3]) with a batch of B bf16 rows.  Inputs rotate over
 copies holding >= 1 GB of distinct weights or caches (at most 4 GB), so the
-256 MB last-level cache cannot serve them, as in bench.py's sweeps; the
+256 MB last-level cache cannot serve them, as in bench.py's sweeps (`gemm`,
+the prompt pass's projection, runs neon_gemm_bf16 on one N(0, 1) bf16 A and
+one W; RESID 1 adds into C as the O projection does); the
 workspace and the zeroed arrival counters are allocated once.  Each launch's
 duration and counters come from rocprofv3 around this program; it prints the
 configuration and the number of launches.
@@ -56,9 +59,20 @@ def run_gemv(ne, torch, N, B, reps):
     return f"gemv N={N} K={K} B={B}: {reps} launches over {n} weight copies"
 
 
+def run_gemm(ne, torch, M, N, K, resid, reps):
+    A = torch.randn(M, K, device="cuda").to(torch.bfloat16).view(torch.int16)
+    W = (0.02 * torch.randn(N, K, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    b = (0.02 * torch.randn(N, device="cuda")).to(torch.bfloat16).view(torch.int16)
+    C = torch.zeros(M, N, dtype=torch.int16, device="cuda")
+    for _ in range(reps):
+        ne.gemm_bf16(A, W, b, C, M, N, K, accumulate=bool(resid))
+    torch.cuda.synchronize()
+    return f"gemm M={M} N={N} K={K} resid={resid}: {reps} launches"
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("kind", choices=["attn", "gemv"])
+    ap.add_argument("kind", choices=["attn", "gemv", "gemm"])
     ap.add_argument("args", nargs="+", type=int)
     ap.add_argument("--reps", type=int, default=16)
     a = ap.parse_args(argv)
@@ -68,9 +82,12 @@ def main(argv=None):
     if a.kind == "attn":
         T, B, window = a.args
         msg = run_attn(ne, torch, T, B, window, a.reps)
-    else:
+    elif a.kind == "gemv":
         N, B = a.args
         msg = run_gemv(ne, torch, N, B, a.reps)
+    else:
+        M, N, K, resid = a.args
+        msg = run_gemm(ne, torch, M, N, K, resid, a.reps)
     print(msg, flush=True)
 
 
