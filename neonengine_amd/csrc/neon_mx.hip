@@ -632,13 +632,15 @@ __device__ __forceinline__ void mx_rope8(uint4& x1, uint4& x2, const float* cp, 
 }
 
 __global__ __launch_bounds__(64) void k_mx_attn(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos_arr,
+    const uint16_t* __restrict__ q, const uint16_t* kc,
+    const uint16_t* vc, const int32_t* __restrict__ pos_arr,
     const int32_t* __restrict__ seq, float* __restrict__ part_o, float* __restrict__ part_ml,
     const uint16_t* __restrict__ sinks, uint16_t* __restrict__ out, int Hq, int Hkv, int G,
     int T_max, int key_mask, int window, int S, int q_stride, uint16_t* __restrict__ outp,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-    uint16_t* __restrict__ kc_w, uint16_t* __restrict__ vc_w) {
+    uint16_t* kc_w, uint16_t* vc_w) {
+  // kc / vc and kc_w / vc_w are the same caches (read by every block, the
+  // new row written by the block of the last split): no __restrict__ on them
   constexpr int VT = 64 + 8;
   __shared__ __align__(16) uint16_t ks[64 * 64];
   __shared__ __align__(16) uint16_t vt[64 * VT];
