@@ -325,6 +325,171 @@ __global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_px(MxArgs a) {
   mx_gemv_epilogue<BT, MODE, WAVES>(a, acc, red, lane, w, n0, j, g, N, R);
 }
 
+// k_mx_gemv over the packed weights and packed activations with the
+// activations shared through LDS: wave w of block i owns weight tile
+// WAVES i + w (16 rows) over the whole K, and the block's waves read every
+// 128-element K chunk of the BT activation tiles from one LDS copy instead
+// of each fetching it from L2.  Every operand piece (1 KB: the activation
+// tiles of a chunk, each wave's weight tile of a chunk) is copied into LDS
+// by global_load_lds_dwordx4 (lane l writes bytes 16 l .. 16 l + 15 of the
+// piece), NS - 1 chunks ahead in a ring of NS stages, so no register holds
+// an operand in flight.  A wave issues the same number of pieces for every
+// chunk (past the last chunk it re-reads the last one into a stage that is
+// never consumed), so "chunk c has landed" is one fixed vmcnt.  Per tile the
+// fp32 sums run over k in chunk order with each chunk's 4 MFMAs in order;
+// only the order of fp32 additions differs from k_mx_gemv.  Measured at the
+// 20b shape, B = 64, weights cold (one launch in isolation): lm_head (8
+// waves, 3 stages) 380 -> 251 us, QKV (2 waves, 4 stages) 15.6 -> 12.0 us;
+// the O projection stays on k_mx_gemv_px (11.8 against 14.2 us).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define MX_LDS_LOAD(g, l) __builtin_amdgcn_global_load_lds((g), (l), 16, 0, 0)
+#else
+#define MX_LDS_LOAD(g, l) ((void)(g), (void)(l))
+#endif
+template <int N>
+__device__ __forceinline__ void mx_wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int BT, int MODE, int WAVES, int NS>
+__global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_lx(MxArgs a) {
+  extern __shared__ uint4 mx_lds[];
+  constexpr int PX = 4 * BT;                 // activation pieces per chunk (shared)
+  constexpr int STAGE = PX + 4 * WAVES;      // + 4 weight pieces per wave
+  constexpr int LX = (PX + WAVES - 1) / WAVES;
+  constexpr int LT = LX + 4;                 // pieces one wave issues per chunk
+  static_assert(NS >= 2 && (NS - 2) * LT <= 63, "chunk arrival must fit one vmcnt");
+  // the launcher picks BT = ceil(B / 16), so every row tile holds rows
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int N = a.N, K = a.K, R = a.B;
+  const int NCH = (K + 127) / 128, NT = N / 16;
+  const int tile = blockIdx.x * WAVES + w;
+  const int tl = min(tile, NT - 1);          // waves past N load a real tile, store nothing
+  const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
+  const uint16_t* X = a.xp;
+  auto issue = [&](int c, int stage) {
+    const int ch = min(c, NCH - 1);
+    uint4* base = mx_lds + stage * STAGE * 64;
+#pragma unroll
+    for (int i = 0; i < LX; ++i) {
+      const int q = min(w + WAVES * i, PX - 1);  // a duplicate writes the same bytes
+      MX_LDS_LOAD(X + ((((size_t)(q >> 2) * NCH + ch) * 4 + (q & 3)) * 64 + lane) * 8,
+                  base + q * 64);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      MX_LDS_LOAD(P + ((((size_t)tl * NCH + ch) * 4 + t) * 64 + lane) * 8,
+                  base + (PX + 4 * w + t) * 64);
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  mx_f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < NCH; c0 += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int c = c0 + s;
+      if (c >= NCH) break;  // uniform
+      mx_wait_vmcnt<(NS - 2) * LT>();  // this wave's pieces of chunk c have landed
+      // every wave's have, and every wave's reads of stage (c - 1) % NS are
+      // complete (lgkmcnt 0), so the copies issued next may overwrite it.  No
+      // fence: the waits on the copies are the vmcnt above
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(c + NS - 1, (s + NS - 1) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint4* st = mx_lds + s * STAGE * 64;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const mx_bf16x8 bw = mx_as_bf16x8(st[(PX + 4 * w + t) * 64 + lane]);
+#pragma unroll
+        for (int bt = 0; bt < BT; ++bt)  // BT = ceil(R / 16): every tile has rows
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              mx_as_bf16x8(st[(4 * bt + t) * 64 + lane]), bw, acc[bt], 0, 0, 0);
+      }
+    }
+  }
+  mx_wait_vmcnt<0>();  // the ring's last (unused) copies have landed before exit
+  if (tile >= NT) return;
+  const int n = 16 * tile + j;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = 16 * bt + 4 * g + r;
+      const bool ok = ri < R;
+      const float d = acc[bt][r];
+      if constexpr (MODE == MX_LOGITS) {
+        if (ok) a.out_f[(size_t)ri * N + n] = d;
+        float bv = ok ? d : -INFINITY;
+        int bi = n;
+        mx_argmax_step(bv, bi, 1);
+        mx_argmax_step(bv, bi, 2);
+        mx_argmax_step(bv, bi, 4);
+        mx_argmax_step(bv, bi, 8);
+        if (ok && j == 0) {  // partials per 16-column tile, as k_mx_gemv's per block
+          a.part_val[(size_t)ri * NT + tile] = bv;
+          a.part_idx[(size_t)ri * NT + tile] = bi;
+        }
+      } else if (ok) {
+        const float v = a.bias ? __fadd_rn(d, bf2f(a.bias[n])) : d;
+        const size_t o = (size_t)ri * N + n;
+        if (MODE == MX_STORE) a.y[o] = f2bf(v);
+        else a.y[o] = f2bf(__fadd_rn(bf2f(a.y[o]), bf2f(f2bf(v))));
+      }
+    }
+  }
+}
+#undef MX_LDS_LOAD
+
+template <int BT, int MODE, int WAVES, int NS>
+static void launch_mx_gemv_lx(const MxArgs& a, hipStream_t st) {
+  constexpr int bytes = NS * (4 * BT + 4 * WAVES) * 1024;
+  static const hipError_t optin =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_mx_gemv_lx<BT, MODE, WAVES, NS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  (void)optin;  // a refused opt-in surfaces as the launch's error
+  const int nt = a.N / 16;
+  hipLaunchKernelGGL((k_mx_gemv_lx<BT, MODE, WAVES, NS>), dim3((nt + WAVES - 1) / WAVES),
+                     dim3(64 * WAVES), bytes, st, a);
+}
+
+// Block shape of k_mx_gemv_lx per mode from 49 rows on: waves (weight tiles
+// per block) and ring stages; waves 0 = k_mx_gemv_px instead.  Defaults from
+// the measurements above; NEON_MX_LX_STORE / _RESID / _LOGITS = "W,NS"
+// override them (W in {0, 1, 2, 4, 8}, NS in {3, 4}) for comparisons.
+struct MxLxShape { int waves, ns; };
+static MxLxShape mx_lx_shape(int mode) {
+  static const MxLxShape dflt[3] = {{2, 4}, {0, 0}, {8, 3}};
+  static MxLxShape sel[3] = {{-1, 0}, {-1, 0}, {-1, 0}};
+  if (mode < 0 || mode > 2) return {0, 0};
+  if (sel[mode].waves < 0) {
+    static const char* names[3] = {"NEON_MX_LX_STORE", "NEON_MX_LX_RESID", "NEON_MX_LX_LOGITS"};
+    MxLxShape v = dflt[mode];
+    if (const char* e = getenv(names[mode])) {
+      int w = -1, ns = -1;
+      if (sscanf(e, "%d,%d", &w, &ns) >= 1) {
+        v.waves = w;
+        v.ns = ns > 0 ? ns : 3;
+      }
+    }
+    sel[mode] = v;
+  }
+  return sel[mode];
+}
+
+template <int MODE>
+static bool launch_mx_gemv_lx_sel(const MxArgs& a, hipStream_t st) {
+  const MxLxShape v = mx_lx_shape(MODE);
+#define LX_SEL(W, NS) \
+  if (v.waves == W && v.ns == NS) { launch_mx_gemv_lx<4, MODE, W, NS>(a, st); return true; }
+  LX_SEL(1, 3) LX_SEL(1, 4) LX_SEL(2, 3) LX_SEL(2, 4) LX_SEL(4, 3) LX_SEL(4, 4) LX_SEL(8, 3)
+#undef LX_SEL
+  return false;  // 0 (or an unsupported shape): k_mx_gemv_px
+}
+
 // Standalone MXFP4 GEMV on the matrix cores (neon_mxfp4_gemv at B >= 16):
 // y[b][n] = bf16(sum_k x[b][k] dq(W[n][k]) + bias[n]) with the weights in the
 // checkpoint layout (codes [N][K/2], scales [N][K/32]).  A block owns rows
@@ -876,6 +1041,7 @@ __global__ __launch_bounds__(256) void k_mx_rope_append(
 template <int MODE, int BT, bool PK>
 static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
   const int it = (a.K / 32 + 15) / 16;
+  if (PK && a.xp != nullptr && BT == 4 && launch_mx_gemv_lx_sel<MODE>(a, st)) return;
   if (PK && a.xp != nullptr && MODE == MX_LOGITS && BT >= 3) {
     // lm_head from 33 rows on: 8 waves split K (4 iterations each at K <= 4096);
     // 582 -> 377 us at the 20b shape, B = 64 (equal at B = 32)
