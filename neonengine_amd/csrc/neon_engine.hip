@@ -132,6 +132,10 @@ struct neon_ctx {
   bool fuse_merge = !fuse_env || fuse_env[0] == '1' || fuse_env[0] == 'a';
   bool fuse_router = fuse_env && (fuse_env[0] == '1' || fuse_env[0] == 'r');
   int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
+  int32_t* rr_arrive = nullptr;  // one word (router + route lists, matrix-core steps)
+  // the router, top-k and route lists of the matrix-core steps in one launch
+  // (NEON_ROUTER_ROUTE=0: the two launches, for comparisons)
+  bool fuse_route = !(getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '0');
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -420,6 +424,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_apml = take(Br * c.n_heads * (size_t)std::max(ctx->s_full, ctx->s_slide) * 2 * 4),
                o_aarr = take(Br * (size_t)c.n_kv_heads * kAttnArriveStride * 4),
                o_orarr = take((kMoeSyncWords + 1) * kMoeSyncStride * 4),
+               o_rrarr = take(kMoeSyncStride * 4),
                o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
                o_samp = take(Bm * (size_t)c.vocab * 4),
                o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
@@ -450,6 +455,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->attn_po = (float*)(W + o_apo); ctx->attn_pml = (float*)(W + o_apml);
   ctx->attn_arrive = (int32_t*)(W + o_aarr);  // zeroed above; every launch leaves it at 0
   ctx->or_arrive = (int32_t*)(W + o_orarr);    // likewise
+  ctx->rr_arrive = (int32_t*)(W + o_rrarr);    // likewise
   ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
@@ -800,9 +806,14 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     uint8_t *xh = take(nx), *xl = take(nx), *xsh = take(nx / 32), *xsl = take(nx / 32);
     uint8_t *yh = take(ny), *yl = take(ny), *ysh = take(ny / 32), *ysl = take(ny / 32);
     if (mx8) { r.xq_hi = xh; r.xq_lo = xl; r.xs_hi = xsh; r.xs_lo = xsl; }
-    launch_router(r, st);
-    launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
-                      ctx->mx_route, st);
+    r.arrive = ctx->rr_arrive;
+    if (ctx->fuse_route && router_route_supported(r)) {
+      launch_router_route(r, ctx->moe_idx, ctx->moe_score, ctx->mx_route, st);
+    } else {
+      launch_router(r, st);
+      launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
+                        ctx->mx_route, st);
+    }
     MxArgs gu{};
     gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.Wp = mp.gu_c; gu.sp = mp.gu_s;
     gu.bias = w.gu_bias; gu.x = ctx->xn;

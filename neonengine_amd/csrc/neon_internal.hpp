@@ -234,6 +234,11 @@ void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h
                     hipStream_t st);
 // top-k of B rows of router logits and the route lists of their pairs
 // (B k <= 256, E <= 256) in one launch
+// launch_router (norm fused, no MXFP8 image) + launch_topk_route in one
+// launch for B >= 2: a.arrive = one int, 0 at launch and left at 0
+bool router_route_supported(const RouterArgs& a);
+void launch_router_route(const RouterArgs& a, int32_t* idx, float* score, int32_t* route,
+                         hipStream_t st);
 void launch_topk_route(const float* lg, int32_t* idx, float* score, int B, int E, int k,
                        int32_t* route, hipStream_t st);
 void launch_mx_rope_append(const uint16_t* qkv, const int32_t* pos, const int32_t* seq,

@@ -485,7 +485,7 @@ static bool launch_mx_gemv_lx_sel(const MxArgs& a, hipStream_t st) {
   const MxLxShape v = mx_lx_shape(MODE);
 #define LX_SEL(W, NS) \
   if (v.waves == W && v.ns == NS) { launch_mx_gemv_lx<4, MODE, W, NS>(a, st); return true; }
-  LX_SEL(1, 3) LX_SEL(1, 4) LX_SEL(2, 3) LX_SEL(2, 4) LX_SEL(4, 3) LX_SEL(4, 4) LX_SEL(8, 3)
+  LX_SEL(1, 4) LX_SEL(2, 3) LX_SEL(2, 4) LX_SEL(2, 6) LX_SEL(4, 3) LX_SEL(4, 5) LX_SEL(8, 3)
 #undef LX_SEL
   return false;  // 0 (or an unsupported shape): k_mx_gemv_px
 }
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
   const int U = K / 32;
   const int n0 = blockIdx.x * 16;
   const int nr = min(n0 + j, N - 1);  // rows past N re-read row N - 1 (not stored)
-  const int b0 = blockIdx.y * 64;
+  const int b0 = blockIdx.y * 16 * BT;
   // this wave's units: 4 (w + 4 i) + g for i < IT (clamped; zero A past U)
   uint4 wc[IT];
   uint32_t ws[IT];
@@ -594,7 +594,7 @@ static void launch_mxfp4_gemv_mfma_bt(const uint8_t* codes, const uint8_t* scale
                                       int N, int K, int B, hipStream_t st) {
   const int steps = (K / 32 + 3) / 4;        // K steps of 4 units
   const int it = (steps + 3) / 4;            // per wave
-  const dim3 grid((N + 15) / 16, (B + 63) / 64);
+  const dim3 grid((N + 15) / 16, (B + 16 * BT - 1) / (16 * BT));
 #define MF_CASE(ITV)                                                                     \
   if (it <= ITV) {                                                                       \
     hipLaunchKernelGGL((k_mxfp4_gemv_mfma<BT, ITV>), grid, dim3(256), 0, st, codes,     \
@@ -608,7 +608,10 @@ static void launch_mxfp4_gemv_mfma_bt(const uint8_t* codes, const uint8_t* scale
 void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const uint16_t* bias,
                             const uint16_t* x, uint16_t* y, int N, int K, int B,
                             hipStream_t st) {
-  // batch tiles of the widest block (B > 64 runs several blocks in y)
+  // batch tiles per block (B past 64 rows runs several blocks in y).  One
+  // or two tiles per block with more blocks in y measured slower at B = 64
+  // (16.5 / 16.8 against 15.6 us at N = 2880, 20.8 / 16.8 against 15.8 at
+  // N = 4096); only N = 5760 gained with two (24.1 against 28.0 us)
   const int bt = B >= 64 ? 4 : (B + 15) / 16;
   switch (bt) {
     case 1: launch_mxfp4_gemv_mfma_bt<1>(codes, scales, bias, x, y, N, K, B, st); break;

@@ -70,11 +70,14 @@ def test_mxfp4_gemv_config1(orc, N, B):
     assert ok.all()
 
 
-@pytest.mark.parametrize("N,K,B", [(37, 2880, 17), (130, 4096, 65), (5, 8192, 20), (16, 32, 16)])
+@pytest.mark.parametrize("N,K,B", [(37, 2880, 17), (130, 4096, 65), (5, 8192, 20), (16, 32, 16),
+                                   (21, 5760, 40), (2880, 2880, 64), (40, 2880, 130)])
 def test_mxfp4_gemv_matrix_cores_ragged(orc, N, K, B):
     """B >= 16 runs on the matrix cores: ragged N, B past one 64-row block,
-    K = 8192, and the smallest K; each output within one bf16 rounding plus
-    the fp32-accumulation slack of the fp64 result."""
+    K = 8192, and the smallest K (the register-fed kernel), and K = 2880 /
+    4096 / 5760 (the kernel that shares the input rows through LDS: ragged N
+    and B, a partial last K chunk, three 64-row blocks); each output within
+    one bf16 rounding plus the fp32-accumulation slack of the fp64 result."""
     codes, scales = mx_weights(orc, N, K, 79)
     x = orc.fill_bf16(0, 80, B * K, 0.0, 1.0)
     bias = orc.fill_bf16(0, 81, N, 0.0, 0.02)
@@ -90,8 +93,9 @@ def test_mxfp4_gemv_matrix_cores_ragged(orc, N, K, B):
     assert ok.all()
 
 
-def test_mxfp4_gemv_matrix_cores_nan_scale(orc):
-    N, K, B = 20, 64, 16
+@pytest.mark.parametrize("K", [64, 2880])
+def test_mxfp4_gemv_matrix_cores_nan_scale(orc, K):
+    N, B = 20, 16
     codes, scales = mx_weights(orc, N, K, 82)
     scales = scales.copy()
     scales[3 * (K // 32) + 1] = 0xFF  # row 3, second block

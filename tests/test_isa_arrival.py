@@ -1,5 +1,6 @@
-"""CPU check of the in-launch merge protocol of the split attention kernel
-(k_attn_split in neon_kernels.hip), in its compiled gfx950 assembly.
+"""CPU check of the in-launch arrival protocols of the split attention kernel
+(k_attn_split) and the batched router kernel (k_router_route) in
+neon_kernels.hip, in their compiled gfx950 assembly.
 
 With several key splits, each block stores its partial softmax state with
 relaxed agent-scope stores, waits for them (s_waitcnt vmcnt(0)), meets its
@@ -85,16 +86,30 @@ def test_detector_catches_misorderings():
         assert arrival_problems(bad), bad
 
 
-def test_attention_merge_arrival_order(tmp_path):
+@pytest.fixture(scope="module")
+def kernels_asm(tmp_path_factory):
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(hipcc):
         pytest.skip("hipcc not available")
     from neonengine_amd import _build
     flags = [f for f in _build.HIPCC_FLAGS if f != "-shared"]
     src = os.path.join(ROOT, "neonengine_amd", "csrc", "neon_kernels.hip")
-    out = tmp_path / "neon_kernels.s"
+    out = tmp_path_factory.mktemp("isa") / "neon_kernels.s"
     subprocess.run([hipcc] + flags + ["-I", os.path.join(ROOT, "include"), "--cuda-device-only",
                                       "-S", src, "-o", str(out)],
                    check=True, capture_output=True, timeout=900)
-    problems = arrival_problems(kernel_asm(out.read_text(), "k_attn_split"))
+    return out.read_text()
+
+
+def test_attention_merge_arrival_order(kernels_asm):
+    problems = arrival_problems(kernel_asm(kernels_asm, "k_attn_split"))
+    assert problems == [], problems[:4]
+
+
+def test_router_route_arrival_order(kernels_asm):
+    """k_router_route (router logits + top-k + route lists, one block per
+    row): each row's expert ids are stored at agent scope, waited for and
+    met at a barrier before the row's arrival; the last block reads every
+    row's ids with agent-scope loads."""
+    problems = arrival_problems(kernel_asm(kernels_asm, "k_router_route"))
     assert problems == [], problems[:4]
