@@ -491,13 +491,16 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv(
   float xr[P][32];
   wave_load_x_fp4<P>(xr, x + (size_t)b * K, U, lane);
   for (int r = r0; r < r1; ++r) {
+    // the row's bias is requested before its dot product (a load issued
+    // after the butterfly would be one more round trip per row)
+    const uint16_t br = bias != nullptr ? load_pinned_u16(bias + r) : (uint16_t)0;
     Fp4Row<P> nxt;
     if (r + 1 < r1)
       fp4_load_row<P>(nxt, codes + (size_t)(r + 1) * (K / 2),
                       scales + (size_t)(r + 1) * U, U, lane);
     float acc = wave_sum(fp4_row_partial<P>(cur, xr, U, lane));
     if (lane == 0) {
-      if (bias) acc = __fadd_rn(acc, bf2f(bias[r]));
+      if (bias) acc = __fadd_rn(acc, bf2f(br));
       y[(size_t)b * N + r] = f2bf(acc);
     }
     cur = nxt;

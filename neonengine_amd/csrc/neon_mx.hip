@@ -548,24 +548,26 @@ static bool launch_mx_gemv_lx_sel(const MxArgs& a, hipStream_t st) {
 // 0xFF gives NaN), products of two bf16 values are exact in fp32, and the
 // 4 waves' partial tiles are added in wave order; only the order of the fp32
 // additions differs from the canonical GEMV.
-template <int BT, int IT>
-__global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
+template <int BT, int IT, int WV>
+__global__ __launch_bounds__(64 * WV) void k_mxfp4_gemv_mfma(
     const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
     const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
     uint16_t* __restrict__ y, int N, int K, int B) {
-  __shared__ mx_f32x4 red[3][BT][64];
+  __shared__ mx_f32x4 red[WV][BT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int U = K / 32;
   const int n0 = blockIdx.x * 16;
   const int nr = min(n0 + j, N - 1);  // rows past N re-read row N - 1 (not stored)
+  // the bias of column n0 + j, requested now (the epilogue then waits for no load)
+  const float bv = (bias != nullptr && n0 + j < N) ? bf2f(load_pinned_u16(bias + n0 + j)) : 0.0f;
   const int b0 = blockIdx.y * 16 * BT;
-  // this wave's units: 4 (w + 4 i) + g for i < IT (clamped; zero A past U)
+  // this wave's units: 4 (w + WV i) + g for i < IT (clamped; zero A past U)
   uint4 wc[IT];
   uint32_t ws[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
-    const int u = min(4 * (w + 4 * i) + g, U - 1);
+    const int u = min(4 * (w + WV * i) + g, U - 1);
     wc[i] = mx_load_nt(codes + (size_t)nr * (K / 2) + (size_t)u * 16);
     ws[i] = __builtin_nontemporal_load(scales + (size_t)nr * U + u);
   }
@@ -581,12 +583,12 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
   mx_f32x4 acc[BT];
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-  for (int i = 0; i < IT; ++i) {
-    const int u_raw = 4 * (w + 4 * i) + g;
+  // each iteration's input rows load as it starts (loading the next
+  // iteration's during this one's MFMAs measured no faster)
+  auto x_load = [&](int i, uint4 (&xq)[BT][4]) {
+    const int u_raw = 4 * (w + WV * i) + g;
     const bool uok = u_raw < U;
     const int u = min(u_raw, U - 1);
-    uint4 xq[BT][4];
 #pragma unroll
     for (int bt = 0; bt < BT; ++bt)
 #pragma unroll
@@ -594,6 +596,11 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
         const uint4 v = reinterpret_cast<const uint4*>(xrow[bt] + (size_t)u * 32)[t];
         xq[bt][t] = (uok && rv[bt]) ? v : make_uint4(0u, 0u, 0u, 0u);  // zero A drops it
       }
+  };
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    uint4 xq[BT][4];
+    x_load(i, xq);
     const float sc = ws[i] == 0xFFu ? __builtin_nanf("")
                                     : __builtin_amdgcn_ldexpf(1.0f, (int)ws[i] - 127);
     const uint32_t cw[4] = {wc[i].x, wc[i].y, wc[i].z, wc[i].w};
@@ -606,19 +613,18 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
                                                           0, 0, 0);
     }
   }
-  if (w > 0) {
+  // every wave hands its partial tiles to LDS; tile bt is finished by wave
+  // bt % WV, adding the WV partials in wave order
 #pragma unroll
-    for (int bt = 0; bt < BT; ++bt) red[w - 1][bt][lane] = acc[bt];
-  }
+  for (int bt = 0; bt < BT; ++bt) red[w][bt][lane] = acc[bt];
   __syncthreads();
-  if (w != 0) return;
   const int n = n0 + j;
-  const float bv = (bias != nullptr && n < N) ? bf2f(bias[n]) : 0.0f;
+  if (n >= N) return;
 #pragma unroll
-  for (int bt = 0; bt < BT; ++bt) {
-    mx_f32x4 tot = acc[bt];
+  for (int bt = w; bt < BT; bt += WV) {
+    mx_f32x4 tot = red[0][bt][lane];
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
+    for (int v = 1; v < WV; ++v) {
       const mx_f32x4 p = red[v][bt][lane];
       tot[0] = __fadd_rn(tot[0], p[0]); tot[1] = __fadd_rn(tot[1], p[1]);
       tot[2] = __fadd_rn(tot[2], p[2]); tot[3] = __fadd_rn(tot[3], p[3]);
@@ -626,7 +632,7 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_mfma(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int ri = b0 + 16 * bt + 4 * g + r;
-      if (ri < B && n < N) {
+      if (ri < B) {
         const float v = bias != nullptr ? __fadd_rn(tot[r], bv) : tot[r];
         y[(size_t)ri * N + n] = f2bf(v);
       }
@@ -639,11 +645,11 @@ static void launch_mxfp4_gemv_mfma_bt(const uint8_t* codes, const uint8_t* scale
                                       const uint16_t* bias, const uint16_t* x, uint16_t* y,
                                       int N, int K, int B, hipStream_t st) {
   const int steps = (K / 32 + 3) / 4;        // K steps of 4 units
-  const int it = (steps + 3) / 4;            // per wave
+  const int it = (steps + 3) / 4;            // per wave (8 waves of half the K measured slower)
   const dim3 grid((N + 15) / 16, (B + 16 * BT - 1) / (16 * BT));
 #define MF_CASE(ITV)                                                                     \
   if (it <= ITV) {                                                                       \
-    hipLaunchKernelGGL((k_mxfp4_gemv_mfma<BT, ITV>), grid, dim3(256), 0, st, codes,     \
+    hipLaunchKernelGGL((k_mxfp4_gemv_mfma<BT, ITV, 4>), grid, dim3(256), 0, st, codes,  \
                        scales, bias, x, y, N, K, B);                                     \
     return;                                                                              \
   }
@@ -1208,6 +1214,14 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
   const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;
   const bool wave_on = nw0 < N;
   const int nch = (U + CKU - 1) / CKU;
+  // the epilogue's bias and output rows, requested now (as in k_mx_moe16)
+  const float bias_pre =
+      wave_on ? bf2f(load_pinned_u16(a.bias + (size_t)e * N + nw0 + j)) : 0.0f;
+  int32_t row_pre[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    row_pre[r] = (int32_t)load_pinned_u32(reinterpret_cast<const uint32_t*>(rows) +
+                                          min(4 * g + r, R - 1));
   // staging: thread tid copies 16-byte pieces sp and sp + 16 of row sr's
   // chunk, hi and lo, and unit sp's two scale bytes
   const int sr = tid >> 4, sp = tid & 15;
@@ -1313,16 +1327,16 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int ri = 4 * g + r;
-      const bool ok = ri < R && (unsigned)rows[min(ri, R - 1)] < (unsigned)(a.B * a.k);
+      const bool ok = ri < R && (unsigned)row_pre[r] < (unsigned)(a.B * a.k);
       const float d = acc[0][r];
       if constexpr (MODE == MX_GATE_UP) {
-        const float v = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        const float v = __fadd_rn(d, bias_pre);
         const float other = __shfl_xor(v, 1);
         const uint16_t y = f2bf(swiglu_clamp(v, other, a.alpha, a.limit));
         if ((j & 1) == 0) ytile[ri][8 * w + j / 2] = bf2f(y);
-        if (ok && (j & 1) == 0) a.y[(size_t)rows[ri] * (N / 2) + n / 2] = y;
+        if (ok && (j & 1) == 0) a.y[(size_t)row_pre[r] * (N / 2) + n / 2] = y;
       } else {
-        if (ok) a.out_f[(size_t)rows[ri] * N + n] = __fadd_rn(d, bf2f(a.bias[(size_t)e * N + n]));
+        if (ok) a.out_f[(size_t)row_pre[r] * N + n] = __fadd_rn(d, bias_pre);
       }
     }
   }
