@@ -502,10 +502,12 @@ static void launch_mx_gemv_lx(const MxArgs& a, hipStream_t st) {
                      dim3(64 * WAVES), bytes, st, a);
 }
 
-// Block shape of k_mx_gemv_lx per mode from 49 rows on: waves (weight tiles
-// per block) and ring stages; waves 0 = k_mx_gemv_px instead.  Defaults from
-// the measurements above; NEON_MX_LX_STORE / _RESID / _LOGITS = "W,NS"
-// override them (W in {0, 1, 2, 4, 8}, NS in {3, 4}) for comparisons.
+// Block shape of k_mx_gemv_lx per mode: waves (weight tiles per block) and
+// ring stages; waves 0 = k_mx_gemv_px instead.  Defaults from the
+// measurements above (the same shapes were best at 16, 32 and 48 rows too:
+// 4837 -> 4909, 8606 -> 8863, 11,741 -> 12,574 tok/s for the 20b step);
+// NEON_MX_LX_STORE / _RESID / _LOGITS = "W,NS" override them (W in
+// {0, 1, 2, 4, 8}, NS in {3, 4, 5}) for comparisons.
 struct MxLxShape { int waves, ns; };
 static MxLxShape mx_lx_shape(int mode) {
   static const MxLxShape dflt[3] = {{2, 4}, {0, 0}, {8, 3}};
@@ -528,10 +530,20 @@ static MxLxShape mx_lx_shape(int mode) {
 
 template <int MODE>
 static bool launch_mx_gemv_lx_sel(const MxArgs& a, hipStream_t st) {
+  const int bt = (a.B + 15) / 16;
+  if (bt > 4) return false;
   const MxLxShape v = mx_lx_shape(MODE);
-#define LX_SEL(W, NS) \
-  if (v.waves == W && v.ns == NS) { launch_mx_gemv_lx<4, MODE, W, NS>(a, st); return true; }
-  LX_SEL(1, 4) LX_SEL(2, 3) LX_SEL(2, 4) LX_SEL(2, 6) LX_SEL(4, 3) LX_SEL(4, 5) LX_SEL(8, 3)
+#define LX_SEL(W, NS)                                                  \
+  if (v.waves == W && v.ns == NS) {                                    \
+    switch (bt) {                                                      \
+      case 1: launch_mx_gemv_lx<1, MODE, W, NS>(a, st); break;         \
+      case 2: launch_mx_gemv_lx<2, MODE, W, NS>(a, st); break;         \
+      case 3: launch_mx_gemv_lx<3, MODE, W, NS>(a, st); break;         \
+      default: launch_mx_gemv_lx<4, MODE, W, NS>(a, st); break;        \
+    }                                                                  \
+    return true;                                                       \
+  }
+  LX_SEL(1, 4) LX_SEL(2, 4) LX_SEL(4, 3) LX_SEL(4, 5) LX_SEL(8, 3)
 #undef LX_SEL
   return false;  // 0 (or an unsupported shape): k_mx_gemv_px
 }
@@ -1109,7 +1121,7 @@ __global__ __launch_bounds__(256) void k_mx_rope_append(
 template <int MODE, int BT, bool PK>
 static void mx_launch_it(const MxArgs& a, dim3 grid, hipStream_t st) {
   const int it = (a.K / 32 + 15) / 16;
-  if (PK && a.xp != nullptr && BT == 4 && launch_mx_gemv_lx_sel<MODE>(a, st)) return;
+  if (PK && a.xp != nullptr && launch_mx_gemv_lx_sel<MODE>(a, st)) return;
   if (PK && a.xp != nullptr && MODE == MX_LOGITS && BT >= 3) {
     // lm_head from 33 rows on: 8 waves split K (4 iterations each at K <= 4096);
     // 582 -> 377 us at the 20b shape, B = 64 (equal at B = 32)
