@@ -134,7 +134,7 @@ struct neon_ctx {
   int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
   int32_t* rr_arrive = nullptr;  // one word (router + route lists, matrix-core steps)
   // the router, top-k and route lists of the matrix-core steps in one launch
-  // (NEON_ROUTER_ROUTE=0: the two launches, for comparisons)
+  // from 49 rows (NEON_ROUTER_ROUTE=0: always the two launches, for comparisons)
   bool fuse_route = !(getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '0');
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
@@ -807,7 +807,10 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     uint8_t *yh = take(ny), *yl = take(ny), *ysh = take(ny / 32), *ysl = take(ny / 32);
     if (mx8) { r.xq_hi = xh; r.xq_lo = xl; r.xs_hi = xsh; r.xs_lo = xsl; }
     r.arrive = ctx->rr_arrive;
-    if (ctx->fuse_route && router_route_supported(r)) {
+    // one launch from 49 rows (20b step, tok/s fused / two launches: B = 64
+    // 15,896 / 15,706, 48 12,585 / 12,584, 32 8884 / 8994, 16 4909 / 5056:
+    // below that the arrival round trip costs more than the launch it saves)
+    if (ctx->fuse_route && B > 48 && router_route_supported(r)) {
       launch_router_route(r, ctx->moe_idx, ctx->moe_score, ctx->mx_route, st);
     } else {
       launch_router(r, st);
