@@ -359,21 +359,24 @@ __global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_px(MxArgs a) {
 }
 
 // k_mx_gemv over the packed weights and packed activations with the
-// activations shared through LDS: wave w of block i owns weight tile
-// WAVES i + w (16 rows) over the whole K, and the block's waves read every
-// 128-element K chunk of the BT activation tiles from one LDS copy instead
-// of each fetching it from L2.  Every operand piece (1 KB: the activation
-// tiles of a chunk, each wave's weight tile of a chunk) is copied into LDS
-// by global_load_lds_dwordx4 (lane l writes bytes 16 l .. 16 l + 15 of the
+// activations shared through LDS.  A block holds WT weight tiles (16 rows
+// each) and splits K into KS parts: wave w owns tile w % WT over the 128-
+// element K chunks of part w / WT, and the WT waves of a part read each
+// chunk of the BT activation tiles from one LDS copy instead of each
+// fetching it from L2.  Every operand piece (1 KB: the activation tiles of a
+// chunk, each wave's weight tile of a chunk) is copied into LDS by
+// global_load_lds_dwordx4 (lane l writes bytes 16 l .. 16 l + 15 of the
 // piece), NS - 1 chunks ahead in a ring of NS stages, so no register holds
 // an operand in flight.  A wave issues the same number of pieces for every
-// chunk (past the last chunk it re-reads the last one into a stage that is
-// never consumed), so "chunk c has landed" is one fixed vmcnt.  Per tile the
-// fp32 sums run over k in chunk order with each chunk's 4 MFMAs in order;
-// only the order of fp32 additions differs from k_mx_gemv.  Measured at the
-// 20b shape, B = 64, weights cold (one launch in isolation): lm_head (8
-// waves, 3 stages) 380 -> 251 us, QKV (2 waves, 4 stages) 15.6 -> 12.0 us;
-// the O projection stays on k_mx_gemv_px (11.8 against 14.2 us).
+// step (past its part's end it re-reads the last chunk into a stage that is
+// never consumed), so "the step's pieces have landed" is one fixed vmcnt.
+// Per tile the fp32 sums run over each part's chunks in order, with each
+// chunk's 4 MFMAs in order, and the parts are added in part order; only the
+// order of fp32 additions differs from k_mx_gemv.  Measured at the 20b
+// shape, B = 64, weights cold (one launch in isolation, one part): lm_head
+// (8 tiles, 3 stages) 380 -> 251 us, QKV (2 tiles, 4 stages) 15.6 -> 12.0
+// us; in the step, QKV and O gain from shorter chains (K in 2 or 4 parts,
+// mx_lx_shape).
 #if defined(__HIP_DEVICE_COMPILE__)
 #define MX_LDS_LOAD(g, l) __builtin_amdgcn_global_load_lds((g), (l), 16, 0, 0)
 #else
@@ -385,20 +388,28 @@ __device__ __forceinline__ void mx_wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int BT, int MODE, int WAVES, int NS>
-__global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_lx(MxArgs a) {
+template <int BT, int MODE, int WT, int KS, int NS>
+__global__ __launch_bounds__(64 * WT * KS) void k_mx_gemv_lx(MxArgs a) {
+  // WT weight tiles per block, K split KS ways: wave w owns tile w % WT for
+  // the K chunks of part kh = w / WT; the parts' partial tiles are added in
+  // part order at the end.  Every stage holds, per part, the chunk's PX
+  // activation pieces and the WT tiles' 4 weight pieces each.
   extern __shared__ uint4 mx_lds[];
   constexpr int PX = 4 * BT;                 // activation pieces per chunk (shared)
-  constexpr int STAGE = PX + 4 * WAVES;      // + 4 weight pieces per wave
-  constexpr int LX = (PX + WAVES - 1) / WAVES;
+  constexpr int PART = PX + 4 * WT;          // pieces per part and stage
+  constexpr int STAGE = KS * PART;
+  constexpr int LX = (PX + WT - 1) / WT;
   constexpr int LT = LX + 4;                 // pieces one wave issues per chunk
   static_assert(NS >= 2 && (NS - 2) * LT <= 63, "chunk arrival must fit one vmcnt");
   // the launcher picks BT = ceil(B / 16), so every row tile holds rows
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wt = w % WT, kh = w / WT;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, R = a.B;
   const int NCH = (K + 127) / 128, NT = N / 16;
-  const int tile = blockIdx.x * WAVES + w;
+  const int CPK = (NCH + KS - 1) / KS;       // chunks per part
+  const int cb = kh * CPK;                   // this wave's first chunk
+  const int tile = blockIdx.x * WT + wt;
   const int tl = min(tile, NT - 1);          // waves past N load a real tile, store nothing
   const uint16_t* P = static_cast<const uint16_t*>(a.Wp);
   const uint16_t* X = a.xp;
@@ -415,49 +426,70 @@ __global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_lx(MxArgs a) {
       for (int r = 0; r < 4; ++r)
         res[bt][r] = load_pinned_u16(a.y + (size_t)min(16 * bt + 4 * g + r, R - 1) * N + nl);
   }
-  auto issue = [&](int c, int stage) {
-    const int ch = min(c, NCH - 1);
-    uint4* base = mx_lds + stage * STAGE * 64;
+  auto issue = [&](int i, int stage) {
+    const int ch = min(cb + i, NCH - 1);  // past the part's end: a copy never consumed
+    uint4* base = mx_lds + (stage * STAGE + kh * PART) * 64;
 #pragma unroll
-    for (int i = 0; i < LX; ++i) {
-      const int q = min(w + WAVES * i, PX - 1);  // a duplicate writes the same bytes
+    for (int ii = 0; ii < LX; ++ii) {
+      const int q = min(wt + WT * ii, PX - 1);  // a duplicate writes the same bytes
       MX_LDS_LOAD(X + ((((size_t)(q >> 2) * NCH + ch) * 4 + (q & 3)) * 64 + lane) * 8,
                   base + q * 64);
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t)
       MX_LDS_LOAD(P + ((((size_t)tl * NCH + ch) * 4 + t) * 64 + lane) * 8,
-                  base + (PX + 4 * w + t) * 64);
+                  base + (PX + 4 * wt + t) * 64);
   };
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue(s, s);
   mx_f32x4 acc[BT];
 #pragma unroll
   for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = 0; c0 < NCH; c0 += NS) {
+  for (int i0 = 0; i0 < CPK; i0 += NS) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int c = c0 + s;
-      if (c >= NCH) break;  // uniform
-      mx_wait_vmcnt<(NS - 2) * LT>();  // this wave's pieces of chunk c have landed
-      // every wave's have, and every wave's reads of stage (c - 1) % NS are
+      const int i = i0 + s;
+      if (i >= CPK) break;  // uniform
+      mx_wait_vmcnt<(NS - 2) * LT>();  // this wave's pieces of step i have landed
+      // every wave's have, and every wave's reads of stage (i - 1) % NS are
       // complete (lgkmcnt 0), so the copies issued next may overwrite it.  No
       // fence: the waits on the copies are the vmcnt above
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      issue(c + NS - 1, (s + NS - 1) % NS);
+      issue(i + NS - 1, (s + NS - 1) % NS);
       __builtin_amdgcn_sched_barrier(0);
-      const uint4* st = mx_lds + s * STAGE * 64;
+      if (cb + i < NCH) {  // uniform per wave (the last part may be shorter)
+        const uint4* st = mx_lds + (s * STAGE + kh * PART) * 64;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const mx_bf16x8 bw = mx_as_bf16x8(st[(PX + 4 * w + t) * 64 + lane]);
+        for (int t = 0; t < 4; ++t) {
+          const mx_bf16x8 bw = mx_as_bf16x8(st[(PX + 4 * wt + t) * 64 + lane]);
 #pragma unroll
-        for (int bt = 0; bt < BT; ++bt)  // BT = ceil(R / 16): every tile has rows
-          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              mx_as_bf16x8(st[(4 * bt + t) * 64 + lane]), bw, acc[bt], 0, 0, 0);
+          for (int bt = 0; bt < BT; ++bt)  // BT = ceil(R / 16): every tile has rows
+            acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                mx_as_bf16x8(st[(4 * bt + t) * 64 + lane]), bw, acc[bt], 0, 0, 0);
+        }
       }
     }
   }
-  mx_wait_vmcnt<0>();  // the ring's last (unused) copies have landed before exit
+  mx_wait_vmcnt<0>();  // the ring's last (unused) copies have landed
+  if constexpr (KS > 1) {
+    // parts 1 .. KS - 1 hand their tiles over through the (now idle) ring
+    mx_f32x4* red = reinterpret_cast<mx_f32x4*>(mx_lds);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kh > 0) {
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) red[(((kh - 1) * WT + wt) * BT + bt) * 64 + lane] = acc[bt];
+    }
+    __syncthreads();
+    if (kh > 0) return;
+#pragma unroll
+    for (int v = 1; v < KS; ++v)
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) {
+        const mx_f32x4 p = red[(((v - 1) * WT + wt) * BT + bt) * 64 + lane];
+        acc[bt][0] = __fadd_rn(acc[bt][0], p[0]); acc[bt][1] = __fadd_rn(acc[bt][1], p[1]);
+        acc[bt][2] = __fadd_rn(acc[bt][2], p[2]); acc[bt][3] = __fadd_rn(acc[bt][3], p[3]);
+      }
+  }
   if (tile >= NT) return;
   const int n = 16 * tile + j;
 #pragma unroll
@@ -490,60 +522,68 @@ __global__ __launch_bounds__(64 * WAVES) void k_mx_gemv_lx(MxArgs a) {
 }
 #undef MX_LDS_LOAD
 
-template <int BT, int MODE, int WAVES, int NS>
+template <int BT, int MODE, int WT, int KS, int NS>
 static void launch_mx_gemv_lx(const MxArgs& a, hipStream_t st) {
-  constexpr int bytes = NS * (4 * BT + 4 * WAVES) * 1024;
+  constexpr int bytes = NS * KS * (4 * BT + 4 * WT) * 1024;
+  static_assert(bytes <= 160 * 1024, "LDS");
   static const hipError_t optin =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(k_mx_gemv_lx<BT, MODE, WAVES, NS>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_mx_gemv_lx<BT, MODE, WT, KS, NS>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   (void)optin;  // a refused opt-in surfaces as the launch's error
   const int nt = a.N / 16;
-  hipLaunchKernelGGL((k_mx_gemv_lx<BT, MODE, WAVES, NS>), dim3((nt + WAVES - 1) / WAVES),
-                     dim3(64 * WAVES), bytes, st, a);
+  hipLaunchKernelGGL((k_mx_gemv_lx<BT, MODE, WT, KS, NS>), dim3((nt + WT - 1) / WT),
+                     dim3(64 * WT * KS), bytes, st, a);
 }
 
-// Block shape of k_mx_gemv_lx per mode: waves (weight tiles per block) and
-// ring stages; waves 0 = k_mx_gemv_px instead.  Defaults from the
-// measurements above (the same shapes were best at 16, 32 and 48 rows too:
-// 4837 -> 4909, 8606 -> 8863, 11,741 -> 12,574 tok/s for the 20b step);
-// NEON_MX_LX_STORE / _RESID / _LOGITS = "W,NS" override them (W in
-// {0, 1, 2, 4, 8}, NS in {3, 4, 5}) for comparisons.
-struct MxLxShape { int waves, ns; };
-static MxLxShape mx_lx_shape(int mode) {
-  static const MxLxShape dflt[3] = {{2, 4}, {0, 0}, {8, 3}};
-  static MxLxShape sel[3] = {{-1, 0}, {-1, 0}, {-1, 0}};
-  if (mode < 0 || mode > 2) return {0, 0};
-  if (sel[mode].waves < 0) {
+// Block shape of k_mx_gemv_lx per mode: weight tiles per block, ring stages
+// and K parts; tiles 0 = k_mx_gemv_px instead.  Defaults measured on the 20b
+// step (tok/s at B = 64 / 32 / 16 after 16-token prompts): one K part for
+// every mode, QKV 2 tiles x 4 stages and lm_head 8 x 3, O on k_mx_gemv_px:
+// 15,832 / 8977 / 5078; QKV with its K in two parts (2 tiles, 3 stages) and
+// O on 1 tile with 2 parts (4 stages): 16,240 / 9118 / 5121; O with 4 parts
+// (2 stages): 16,353 / 9081 / 5062.  NEON_MX_LX_STORE / _RESID / _LOGITS =
+// "W,NS[,KS]" override them for comparisons (the shapes listed in
+// launch_mx_gemv_lx_sel).
+struct MxLxShape { int waves, ns, ks; };
+static MxLxShape mx_lx_shape(int mode, int bt) {
+  static MxLxShape env[3] = {{-2, 0, 1}, {-2, 0, 1}, {-2, 0, 1}};
+  if (mode < 0 || mode > 2) return {0, 0, 1};
+  if (env[mode].waves == -2) {
     static const char* names[3] = {"NEON_MX_LX_STORE", "NEON_MX_LX_RESID", "NEON_MX_LX_LOGITS"};
-    MxLxShape v = dflt[mode];
+    MxLxShape v = {-1, 0, 1};  // -1: the default below
     if (const char* e = getenv(names[mode])) {
-      int w = -1, ns = -1;
-      if (sscanf(e, "%d,%d", &w, &ns) >= 1) {
+      int w = -1, ns = -1, ks = 1;
+      if (sscanf(e, "%d,%d,%d", &w, &ns, &ks) >= 1) {
         v.waves = w;
         v.ns = ns > 0 ? ns : 3;
+        v.ks = ks > 0 ? ks : 1;
       }
     }
-    sel[mode] = v;
+    env[mode] = v;
   }
-  return sel[mode];
+  if (env[mode].waves >= 0) return env[mode];
+  if (mode == MX_STORE) return {2, 3, 2};
+  if (mode == MX_RESID) return bt >= 4 ? MxLxShape{1, 2, 4} : MxLxShape{1, 4, 2};
+  return {8, 3, 1};
 }
 
 template <int MODE>
 static bool launch_mx_gemv_lx_sel(const MxArgs& a, hipStream_t st) {
   const int bt = (a.B + 15) / 16;
   if (bt > 4) return false;
-  const MxLxShape v = mx_lx_shape(MODE);
-#define LX_SEL(W, NS)                                                  \
-  if (v.waves == W && v.ns == NS) {                                    \
-    switch (bt) {                                                      \
-      case 1: launch_mx_gemv_lx<1, MODE, W, NS>(a, st); break;         \
-      case 2: launch_mx_gemv_lx<2, MODE, W, NS>(a, st); break;         \
-      case 3: launch_mx_gemv_lx<3, MODE, W, NS>(a, st); break;         \
-      default: launch_mx_gemv_lx<4, MODE, W, NS>(a, st); break;        \
-    }                                                                  \
-    return true;                                                       \
+  const MxLxShape v = mx_lx_shape(MODE, bt);
+#define LX_SEL(W, NS, KS)                                                   \
+  if (v.waves == W && v.ns == NS && v.ks == KS) {                           \
+    switch (bt) {                                                           \
+      case 1: launch_mx_gemv_lx<1, MODE, W, KS, NS>(a, st); break;          \
+      case 2: launch_mx_gemv_lx<2, MODE, W, KS, NS>(a, st); break;          \
+      case 3: launch_mx_gemv_lx<3, MODE, W, KS, NS>(a, st); break;          \
+      default: launch_mx_gemv_lx<4, MODE, W, KS, NS>(a, st); break;         \
+    }                                                                       \
+    return true;                                                            \
   }
-  LX_SEL(1, 4) LX_SEL(2, 4) LX_SEL(4, 3) LX_SEL(4, 5) LX_SEL(8, 3)
+  LX_SEL(1, 4, 1) LX_SEL(2, 4, 1) LX_SEL(4, 3, 1) LX_SEL(8, 3, 1)
+  LX_SEL(1, 4, 2) LX_SEL(2, 3, 2) LX_SEL(1, 2, 4) LX_SEL(4, 2, 2)
 #undef LX_SEL
   return false;  // 0 (or an unsupported shape): k_mx_gemv_px
 }
