@@ -541,7 +541,10 @@ static void launch_mx_gemv_lx(const MxArgs& a, hipStream_t st) {
 // every mode, QKV 2 tiles x 4 stages and lm_head 8 x 3, O on k_mx_gemv_px:
 // 15,832 / 8977 / 5078; QKV with its K in two parts (2 tiles, 3 stages) and
 // O on 1 tile with 2 parts (4 stages): 16,240 / 9118 / 5121; O with 4 parts
-// (2 stages): 16,353 / 9081 / 5062.  NEON_MX_LX_STORE / _RESID / _LOGITS =
+// (2 stages): 16,353 / 9081 / 5062.  The K parts are used from 49 rows: below
+// that they gained under 2%, and at B = 16 their summation order flipped
+// more routing near-ties in the free-routing check against the oracle
+// (median row error 0.446 against its 0.433 bar).  NEON_MX_LX_STORE / _RESID / _LOGITS =
 // "W,NS[,KS]" override them for comparisons (the shapes listed in
 // launch_mx_gemv_lx_sel).
 struct MxLxShape { int waves, ns, ks; };
@@ -562,8 +565,8 @@ static MxLxShape mx_lx_shape(int mode, int bt) {
     env[mode] = v;
   }
   if (env[mode].waves >= 0) return env[mode];
-  if (mode == MX_STORE) return {2, 3, 2};
-  if (mode == MX_RESID) return bt >= 4 ? MxLxShape{1, 2, 4} : MxLxShape{1, 4, 2};
+  if (mode == MX_STORE) return bt >= 4 ? MxLxShape{2, 3, 2} : MxLxShape{2, 4, 1};
+  if (mode == MX_RESID) return bt >= 4 ? MxLxShape{1, 2, 4} : MxLxShape{0, 0, 1};
   return {8, 3, 1};
 }
 
