@@ -303,6 +303,17 @@ __device__ __forceinline__ uint16_t load_pinned_u16(const uint16_t* p) {
 __device__ __forceinline__ float load_pinned_f32(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
+// Two ways an early load still gets waited for at once, and their remedies:
+//   - a load under a condition (`p ? load(p) : 0`) is waited for where the
+//     branches join: load from an address that is always valid instead and
+//     select the value afterwards;
+//   - a value the compiler proves uniform across the wave (a load from a
+//     block-uniform address) is copied to a scalar register right after the
+//     load, so it is waited for there: add lane_zero(n) to its index, which
+//     is 0 at run time for n >= 0 but depends on the lane as far as the
+//     compiler can tell, so the value stays in vector registers and is
+//     waited for at its first use.
+__device__ __forceinline__ int lane_zero(int n) { return (int)threadIdx.x & (n >> 31); }
 
 // ---- lane exchange: lane l receives lane (l ^ OFF)'s value ----------------
 // The values __shfl_xor(v, OFF, 64) gives, without the LDS permute unit (a

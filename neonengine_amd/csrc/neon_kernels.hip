@@ -555,8 +555,9 @@ __global__ __launch_bounds__(256) void k_mxfp4_gemv_bt(
   const int U = K / 32, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n0 = (blockIdx.x * 4 + wave) * 4;
   if (n0 >= N) return;
-  const uint16_t bl =
-      bias != nullptr ? load_pinned_u16(bias + min(n0 + (lane >> 4), N - 1)) : (uint16_t)0;
+  const uint16_t bq =  // unconditional (the input when there is no bias): no branch to join
+      load_pinned_u16(bias != nullptr ? bias + min(n0 + (lane >> 4), N - 1) : x);
+  const uint16_t bl = bias != nullptr ? bq : (uint16_t)0;
   Fp4RowPair<P> rp[2];
   Fp4Row<P> rw[PAIR ? 1 : 4];
   if constexpr (PAIR) {
@@ -827,6 +828,10 @@ __global__ __launch_bounds__(256) void k_gemv_bf16(
   // waiting for them then does not wait for the rows (the vector-memory
   // counter drains in issue order).  Both loads are unconditional (clamped
   // addresses) so that no branch makes the compiler wait for everything.
+  // (The position and sequence below are block-uniform, so the compiler
+  // reads them into scalar registers and waits for them first; keeping them
+  // in vector registers (lane_zero) so that the rows go out before that wait
+  // measured 0.3% slower over the 20b step: 1.2271 against 1.2230 ms.)
   const int p = MODE == MODE_QKV ? (int)load_pinned_u32(
                                         reinterpret_cast<const uint32_t*>(rp.pos) + b)
                                   : 0;
@@ -1007,13 +1012,17 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_bt(
   // the value this lane holds after the butterfly: (row r, batch row bb)
   const int v_l = lane >> LS, r_l = v_l / BT, bb_l = v_l % BT, b_l = b0 + bb_l;
   const bool lead = (lane & ((1 << LS) - 1)) == 0 && b_l < B;
-  const int p_l = MODE == MODE_QKV ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.pos) +
-                                                          min(b_l, B - 1))
-                                   : 0;
-  const int s_l = (MODE == MODE_QKV && rp.seq != nullptr)
-                      ? (int)load_pinned_u32(reinterpret_cast<const uint32_t*>(rp.seq) +
-                                             min(b_l, B - 1))
-                      : b_l;
+  // position and sequence of the lane's row: vector registers, no branch
+  // (lane_zero), so the rows' loads below are not held up by them
+  int p_l = 0, s_l = b_l;
+  if constexpr (MODE == MODE_QKV) {
+    const int bi = min(b_l, B - 1) + lane_zero(B);
+    const uint32_t* pp = reinterpret_cast<const uint32_t*>(rp.pos) + bi;
+    const uint32_t* sp = rp.seq != nullptr ? reinterpret_cast<const uint32_t*>(rp.seq) + bi : pp;
+    p_l = (int)load_pinned_u32(pp);
+    const int sv = (int)load_pinned_u32(sp);
+    s_l = rp.seq != nullptr ? sv : b_l;
+  }
   float best_v = -INFINITY;
   int32_t best_i = 0x7fffffff;
   const int ngroups = (N + R - 1) / R;
@@ -1023,8 +1032,9 @@ __global__ __launch_bounds__(512) void k_gemv_bf16_bt(
     for (int r = 0; r < R; ++r)
       bf16_load_row<P>(w[r], W + (size_t)min(group_row<MODE, R>(g, r), N - 1) * K, U, lane);
     const int row_l = group_row<MODE, R>(g, r_l);
-    uint16_t bias_l = 0;
-    if (MODE != MODE_LOGITS && bias != nullptr) bias_l = load_pinned_u16(bias + min(row_l, N - 1));
+    // unconditional (the weights when there is no bias): no branch to join
+    const uint16_t bias_l =
+        MODE != MODE_LOGITS ? load_pinned_u16((bias != nullptr ? bias : W) + min(row_l, N - 1)) : 0;
     float rc = 0.0f, rs = 0.0f;
     if (MODE == MODE_QKV) {
       rc = load_pinned_f32(rp.cos_t + (size_t)p_l * 32 + (g & 31));

@@ -80,7 +80,13 @@ template <int BT, int MODE, int WAVES>
 __device__ __forceinline__ void mx_epi_prefetch(const MxArgs& a, MxEpiPre<BT, WAVES>& p, int w,
                                                 int n0, int j, int g, int N, int R) {
   const int n = n0 + j;
-  p.bias = (MODE != MX_LOGITS && a.bias != nullptr) ? bf2f(load_pinned_u16(a.bias + n)) : 0.0f;
+  // unconditional (a valid address when there is no bias): a load under a
+  // branch would be waited for where the branches join
+  p.bias = 0.0f;
+  if constexpr (MODE != MX_LOGITS) {
+    const uint16_t bq = load_pinned_u16(a.bias != nullptr ? a.bias + min(n, N - 1) : a.y);
+    p.bias = a.bias != nullptr ? bf2f(bq) : 0.0f;
+  }
   if constexpr (MODE == MX_RESID) {
 #pragma unroll
     for (int i = 0; i < MxEpiPre<BT, WAVES>::TPW; ++i)
@@ -416,8 +422,11 @@ __global__ __launch_bounds__(64 * WT * KS) void k_mx_gemv_lx(MxArgs a) {
   // the epilogue's bias and residual values, requested now (see
   // mx_gemv_epilogue)
   const int nl = 16 * tl + j;
-  const float bias_n =
-      (MODE != MX_LOGITS && a.bias != nullptr) ? bf2f(load_pinned_u16(a.bias + nl)) : 0.0f;
+  float bias_n = 0.0f;
+  if constexpr (MODE != MX_LOGITS) {  // unconditional: see mx_epi_prefetch
+    const uint16_t bq = load_pinned_u16(a.bias != nullptr ? a.bias + nl : a.y);
+    bias_n = a.bias != nullptr ? bf2f(bq) : 0.0f;
+  }
   uint16_t res[BT][4];
   if constexpr (MODE == MX_RESID) {
 #pragma unroll
@@ -615,7 +624,8 @@ __global__ __launch_bounds__(64 * WV) void k_mxfp4_gemv_mfma(
   const int n0 = blockIdx.x * 16;
   const int nr = min(n0 + j, N - 1);  // rows past N re-read row N - 1 (not stored)
   // the bias of column n0 + j, requested now (the epilogue then waits for no load)
-  const float bv = (bias != nullptr && n0 + j < N) ? bf2f(load_pinned_u16(bias + n0 + j)) : 0.0f;
+  const uint16_t bq = load_pinned_u16(bias != nullptr ? bias + nr : x);  // unconditional
+  const float bv = (bias != nullptr && n0 + j < N) ? bf2f(bq) : 0.0f;
   const int b0 = blockIdx.y * 16 * BT;
   // this wave's units: 4 (w + WV i) + g for i < IT (clamped; zero A past U)
   uint4 wc[IT];
@@ -712,6 +722,233 @@ static void launch_mxfp4_gemv_mfma_bt(const uint8_t* codes, const uint8_t* scale
 #undef MF_CASE
 }
 
+// k_mxfp4_gemv_mfma with its operands copied into LDS by global_load_lds
+// through a ring of NS stages (no register staging).  A block owns WT
+// 16-row weight tiles and BT 16-row batch tiles; its K chunks (128
+// elements, 4 MXFP4 units) are split into KS contiguous parts, wave
+// w = kh WT + wt taking tile wt over part kh, and the parts' partial tiles
+// are added in part order at the end.  Per part a stage holds:
+//   - the chunk of the block's input rows, 256 bytes a row, copied a whole
+//     row segment at a time (4 rows per 1 KB copy, each row's 256 bytes one
+//     contiguous read) with 16-byte slot s of row r at physical slot
+//     s ^ (r % 16), so that the MFMA operand reads of 16 rows (one slot
+//     each) fall on 16 different bank groups;
+//   - per weight tile the 16 code bytes of unit 4 q + g of row 16 tl + j
+//     for lane (j, g) -- the operand order itself, one 1 KB copy -- and that
+//     unit's scale byte inside the aligned dword that holds it (a dword
+//     copy; an aligned dword never crosses a page).
+// Every wave issues the same number of copies a chunk (duplicates where the
+// input pieces do not divide evenly), so one vmcnt covers a chunk.  Units
+// past K read the last unit and their input operand is zeroed; rows past N
+// or B read the last row and are not stored.  Lane (j, g) multiplies the
+// same k values as in k_mxfp4_gemv_mfma; only the order of the fp32
+// additions differs (the chunks of a part in order, then the parts).
+constexpr int kMxgX = 64;   // uint4 per input piece (4 rows x 256 B)
+constexpr int kMxgW = 80;   // uint4 per weight tile: 64 code + 16 scale (256 B)
+template <int BT, int WT, int KS, int NS>
+struct MxgCfg {
+  static constexpr int PX = 4 * BT;                   // input pieces per chunk
+  static constexpr int PART = PX * kMxgX + WT * kMxgW;  // uint4 per part and stage
+  static constexpr int STAGE = KS * PART;
+  static constexpr int LX = (PX + WT - 1) / WT;       // input copies per wave
+  static constexpr int LT = LX + 2;                   // copies per wave and chunk
+  static constexpr size_t BYTES = (size_t)NS * STAGE * 16;
+};
+template <int BT, int WT, int KS, int NS>
+__global__ __launch_bounds__(64 * WT * KS) void k_mxfp4_gemv_lx(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+    const uint16_t* __restrict__ bias, const uint16_t* __restrict__ x,
+    uint16_t* __restrict__ y, int N, int K, int B) {
+  using C = MxgCfg<BT, WT, KS, NS>;
+  constexpr int PX = C::PX, PART = C::PART, STAGE = C::STAGE, LX = C::LX, LT = C::LT;
+  static_assert(NS >= 2 && (NS - 2) * LT <= 63, "chunk arrival must fit one vmcnt");
+  extern __shared__ uint4 mxg_lds[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wt = w % WT, kh = w / WT;
+  const int j = lane & 15, g = lane >> 4;
+  const int U = K / 32, NCH = (K + 127) / 128, NT = (N + 15) / 16;
+  const int CPK = (NCH + KS - 1) / KS;  // chunks per part
+  const int cb = kh * CPK;              // this wave's first chunk
+  const int tile = blockIdx.x * WT + wt;
+  const int tl = min(tile, NT - 1);     // waves past N load a real tile, store nothing
+  const int b0 = blockIdx.y * 16 * BT;
+  const int nr = min(16 * tl + j, N - 1);
+  const int n = 16 * tile + j;
+  // the epilogue's bias, requested now from an address that is always valid
+  // (a conditional load would be waited for where the branches join)
+  const uint16_t bq = load_pinned_u16(bias != nullptr ? bias + min(n, N - 1) : x);
+  const float bv = (bias != nullptr && n < N) ? bf2f(bq) : 0.0f;
+  const uint8_t* crow = codes + (size_t)nr * (K / 2);
+  const uint8_t* srow = scales + (size_t)nr * U;
+  const int spar = (int)(reinterpret_cast<uintptr_t>(srow) & 3);
+#if defined(__HIP_DEVICE_COMPILE__)
+#define MXG_LOAD(gp, lp, sz) __builtin_amdgcn_global_load_lds((gp), (lp), (sz), 0, 0)
+#else
+#define MXG_LOAD(gp, lp, sz) ((void)(gp), (void)(lp))
+#endif
+  auto issue = [&](int i, int stage) {
+    const int ch = min(cb + i, NCH - 1);  // past the part's end: a copy never consumed
+    uint4* base = mxg_lds + stage * STAGE + kh * PART;
+#pragma unroll
+    for (int ii = 0; ii < LX; ++ii) {
+      const int q = min(wt + WT * ii, PX - 1);  // a duplicate writes the same bytes
+      const int rr = 4 * q + (lane >> 4);       // the block's row
+      const int ls = (lane & 15) ^ (rr & 15);   // logical 16-byte slot of the row's chunk
+      const int u = min(4 * ch + (ls >> 2), U - 1);
+      const int gr = min(b0 + rr, B - 1);
+      MXG_LOAD(x + (size_t)gr * K + u * 32 + 8 * (ls & 3), base + q * kMxgX, 16);
+    }
+    const int u = min(4 * ch + g, U - 1);
+    uint4* wb = base + PX * kMxgX + wt * kMxgW;
+    MXG_LOAD(crow + (size_t)u * 16, wb, 16);
+    const uintptr_t sa = reinterpret_cast<uintptr_t>(srow + u) & ~(uintptr_t)3;
+    MXG_LOAD(reinterpret_cast<const void*>(sa), reinterpret_cast<uint32_t*>(wb + 64), 4);
+  };
+#undef MXG_LOAD
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  mx_f32x4 acc[BT];
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt) acc[bt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i0 = 0; i0 < CPK; i0 += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int i = i0 + s;
+      if (i >= CPK) break;  // uniform
+      mx_wait_vmcnt<(NS - 2) * LT>();  // this wave's copies of chunk i have landed
+      // every wave's have, and every wave's reads of stage (i - 1) % NS are
+      // complete (lgkmcnt 0), so the copies issued next may overwrite it.  No
+      // fence: the waits on the copies are the vmcnt above
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(i + NS - 1, (s + NS - 1) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+      const int ch = cb + i;
+      if (ch < NCH) {  // uniform per wave (the last part may be shorter)
+        const uint4* st = mxg_lds + s * STAGE + kh * PART;
+        const uint4* wb = st + PX * kMxgX + wt * kMxgW;
+        const bool uok = 4 * ch + g < U;
+        const int u = min(4 * ch + g, U - 1);
+        const uint32_t sd = reinterpret_cast<const uint32_t*>(wb + 64)[lane];
+        const uint32_t sb = (sd >> (8 * ((spar + u) & 3))) & 0xFFu;
+        const float sc = sb == 0xFFu ? __builtin_nanf("") : __builtin_amdgcn_ldexpf(1.0f, (int)sb - 127);
+        const mx_u32x4 cw = *reinterpret_cast<const mx_u32x4*>(wb + lane);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const mx_bf16x8 bw = mx_fp4x8(cw[t], sc);
+#pragma unroll
+          for (int bt = 0; bt < BT; ++bt) {
+            // row 16 bt + j, logical slot 4 g + t
+            const mx_u32x4 xv = *reinterpret_cast<const mx_u32x4*>(
+                st + (4 * bt + (j >> 2)) * kMxgX + ((j & 3) << 4) + ((4 * g + t) ^ j));
+            const mx_u32x4 xa = uok ? xv : mx_u32x4{0u, 0u, 0u, 0u};  // zero A drops the unit
+            acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(mx_bf16x8, xa), bw, acc[bt], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+  mx_wait_vmcnt<0>();  // the ring's last (unused) copies have landed
+  if constexpr (KS > 1) {
+    // parts 1 .. KS - 1 hand their tiles over through the (now idle) ring
+    mx_f32x4* red = reinterpret_cast<mx_f32x4*>(mxg_lds);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kh > 0) {
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) red[(((kh - 1) * WT + wt) * BT + bt) * 64 + lane] = acc[bt];
+    }
+    __syncthreads();
+    if (kh > 0) return;
+#pragma unroll
+    for (int v = 1; v < KS; ++v)
+#pragma unroll
+      for (int bt = 0; bt < BT; ++bt) {
+        const mx_f32x4 p = red[(((v - 1) * WT + wt) * BT + bt) * 64 + lane];
+        acc[bt][0] = __fadd_rn(acc[bt][0], p[0]); acc[bt][1] = __fadd_rn(acc[bt][1], p[1]);
+        acc[bt][2] = __fadd_rn(acc[bt][2], p[2]); acc[bt][3] = __fadd_rn(acc[bt][3], p[3]);
+      }
+  }
+  if (n >= N || tile >= NT) return;
+#pragma unroll
+  for (int bt = 0; bt < BT; ++bt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ri = b0 + 16 * bt + 4 * g + r;
+      if (ri < B) {
+        const float v = bias != nullptr ? __fadd_rn(acc[bt][r], bv) : acc[bt][r];
+        y[(size_t)ri * N + n] = f2bf(v);
+      }
+    }
+}
+
+template <int BT, int WT, int KS, int NS>
+static void launch_mxfp4_gemv_lx(const uint8_t* codes, const uint8_t* scales,
+                                 const uint16_t* bias, const uint16_t* x, uint16_t* y, int N,
+                                 int K, int B, hipStream_t st) {
+  constexpr size_t bytes = MxgCfg<BT, WT, KS, NS>::BYTES;
+  static_assert(bytes <= 160 * 1024 && bytes >= (size_t)(KS - 1) * WT * BT * 1024,
+                "LDS (ring, and the part hand-over)");
+  static const hipError_t optin =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(k_mxfp4_gemv_lx<BT, WT, KS, NS>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  (void)optin;  // a refused opt-in surfaces as the launch's error
+  const int nt = (N + 15) / 16;
+  hipLaunchKernelGGL((k_mxfp4_gemv_lx<BT, WT, KS, NS>),
+                     dim3((nt + WT - 1) / WT, (B + 16 * BT - 1) / (16 * BT)),
+                     dim3(64 * WT * KS), bytes, st, codes, scales, bias, x, y, N, K, B);
+}
+
+// Block shape of k_mxfp4_gemv_lx: batch tiles, weight tiles, K parts,
+// stages.  Measured over BASELINE config 1 (K = 2880, N = 2880 / 5760 /
+// 4096, us; the register-fed k_mxfp4_gemv_mfma in brackets):
+//   B = 16: (1,1,8,3) 5.81 / 10.06 / 5.98, (1,2,4,3) 6.65 / 6.95 / 6.74
+//           [6.45 / 10.61 / 6.61];
+//   B = 64: (2,2,4,3) 8.78 / 14.87 / 8.81, (2,4,2,3) 10.88 / 11.37 / 11.02,
+//           (1,2,2,4) 9.66 / 14.44 / 10.85, (1,4,2,4) 9.49 / 14.65 / 9.41
+//           [14.99 / 26.51 / 15.23].
+// The 8-wave shapes hold 126 KB of LDS (one block per CU): up to 256 blocks
+// they all start at once, beyond that the shapes with more weight tiles per
+// block keep the grid within one round.  NEON_MXFP4_LX = "BT,WT,KS,NS" picks
+// one of the shapes listed in launch_mxfp4_gemv_lx_sel for comparisons, "0"
+// the register-fed kernel.
+struct MxgShape { int bt, wt, ks, ns; };
+static MxgShape mxg_shape(int B, int N) {
+  static MxgShape env = {-2, 0, 0, 0};
+  if (env.bt == -2) {
+    MxgShape v = {-1, 0, 0, 0};
+    if (const char* e = getenv("NEON_MXFP4_LX")) {
+      int a = -1, b = 0, c = 0, d = 0;
+      if (sscanf(e, "%d,%d,%d,%d", &a, &b, &c, &d) >= 1) v = {a, b, c, d};
+    }
+    env = v;
+  }
+  if (env.bt >= 0) return env;
+  const bool one_round = (N + 15) / 16 <= 256;
+  if (B <= 16) return one_round ? MxgShape{1, 1, 8, 3} : MxgShape{1, 2, 4, 3};
+  return one_round ? MxgShape{2, 2, 4, 3} : MxgShape{2, 4, 2, 3};
+}
+
+static bool launch_mxfp4_gemv_lx_sel(const uint8_t* codes, const uint8_t* scales,
+                                     const uint16_t* bias, const uint16_t* x, uint16_t* y,
+                                     int N, int K, int B, hipStream_t st) {
+  // its 16-byte copies read whole 16-byte pieces of x and of the code rows
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes)) & 15) != 0)
+    return false;
+  const MxgShape v = mxg_shape(B, N);
+#define MXG_SEL(BT, WT, KS, NS)                                                     \
+  if (v.bt == BT && v.wt == WT && v.ks == KS && v.ns == NS) {                       \
+    launch_mxfp4_gemv_lx<BT, WT, KS, NS>(codes, scales, bias, x, y, N, K, B, st);   \
+    return true;                                                                    \
+  }
+  MXG_SEL(1, 2, 2, 4) MXG_SEL(1, 4, 1, 4) MXG_SEL(1, 1, 4, 4) MXG_SEL(1, 2, 4, 3)
+  MXG_SEL(1, 1, 2, 4) MXG_SEL(1, 2, 1, 4) MXG_SEL(2, 2, 2, 4) MXG_SEL(2, 4, 2, 3)
+  MXG_SEL(4, 2, 2, 3) MXG_SEL(4, 4, 1, 4) MXG_SEL(1, 1, 8, 3) MXG_SEL(2, 1, 4, 3)
+  MXG_SEL(1, 2, 2, 6) MXG_SEL(1, 4, 2, 4) MXG_SEL(1, 4, 4, 3) MXG_SEL(1, 2, 4, 4)
+  MXG_SEL(1, 2, 8, 3) MXG_SEL(2, 4, 4, 2) MXG_SEL(2, 2, 4, 3)
+#undef MXG_SEL
+  return false;
+}
+
 void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const uint16_t* bias,
                             const uint16_t* x, uint16_t* y, int N, int K, int B,
                             hipStream_t st) {
@@ -719,6 +956,7 @@ void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const u
   // or two tiles per block with more blocks in y measured slower at B = 64
   // (16.5 / 16.8 against 15.6 us at N = 2880, 20.8 / 16.8 against 15.8 at
   // N = 4096); only N = 5760 gained with two (24.1 against 28.0 us)
+  if (launch_mxfp4_gemv_lx_sel(codes, scales, bias, x, y, N, K, B, st)) return;
   const int bt = B >= 64 ? 4 : (B + 15) / 16;
   switch (bt) {
     case 1: launch_mxfp4_gemv_mfma_bt<1>(codes, scales, bias, x, y, N, K, B, st); break;
@@ -777,8 +1015,8 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   int32_t row_pre[4];
 #pragma unroll
   for (int tt = 0; tt < TT; ++tt)
-    bias_pre[tt] = wave_on ? bf2f(load_pinned_u16(a.bias + (size_t)e * N + nw0 + 16 * tt + j))
-                           : 0.0f;
+    bias_pre[tt] = bf2f(load_pinned_u16(  // unconditional (clamped): no branch to join
+        a.bias + (size_t)e * N + min(nw0 + 16 * tt + j, N - 1)));
 #pragma unroll
   for (int r = 0; r < 4; ++r)
     row_pre[r] = (int32_t)load_pinned_u32(reinterpret_cast<const uint32_t*>(rows) +
@@ -1270,8 +1508,8 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
   const bool wave_on = nw0 < N;
   const int nch = (U + CKU - 1) / CKU;
   // the epilogue's bias and output rows, requested now (as in k_mx_moe16)
-  const float bias_pre =
-      wave_on ? bf2f(load_pinned_u16(a.bias + (size_t)e * N + nw0 + j)) : 0.0f;
+  const float bias_pre =  // unconditional (clamped): no branch to join
+      bf2f(load_pinned_u16(a.bias + (size_t)e * N + min(nw0 + j, N - 1)));
   int32_t row_pre[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
