@@ -161,7 +161,12 @@ __device__ __forceinline__ void gemm_epi_issue(const GemmParams& p, int lane, in
 #pragma unroll
   for (int in = 0; in < 2; ++in) {
     const int col = n0 + wn * 64 + in * 32 + (lane & 31);
-    ep.bcol[in] = (bias && col < p.N) ? bf2f(load_pinned_u16(bias + col)) : 0.0f;
+    // unconditional (clamped; the weights when there is no bias): a load under
+    // a branch is waited for where the branches join, before the operands
+    const uint16_t bq = load_pinned_u16(
+        bias ? bias + min(col, p.N - 1)
+             : (GROUPED ? reinterpret_cast<const uint16_t*>(p.codes) : p.W));
+    ep.bcol[in] = (bias && col < p.N) ? bf2f(bq) : 0.0f;
   }
   if (MODE == GEMM_SCATTER) {  // every thread loads (threads >= kGM repeat row kGM - 1)
     const size_t gr = (size_t)r0 + min(min((int)threadIdx.x, kGM - 1), rows - 1);
@@ -739,18 +744,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-// Wait until at most `pending` stages of L loads each are outstanding.
-template <int L, int NS>
-__device__ __forceinline__ void wait_stages(int pending) {
-  switch (pending) {
-    case 0: wait_vmcnt<0>(); break;
-    case 1: if constexpr (NS > 2) { wait_vmcnt<L>(); break; } [[fallthrough]];
-    case 2: if constexpr (NS > 3) { wait_vmcnt<2 * L>(); break; } [[fallthrough]];
-    case 3: if constexpr (NS > 4) { wait_vmcnt<3 * L>(); break; } [[fallthrough]];
-    case 4: if constexpr (NS > 5) { wait_vmcnt<4 * L>(); break; } [[fallthrough]];
-    default: if constexpr (NS > 6) { wait_vmcnt<5 * L>(); break; } else { wait_vmcnt<0>(); }
-  }
-}
 
 template <int MODE, int BM, int NB, int BK, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_lds(GemmParams p) {
@@ -775,7 +768,9 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_lds(GemmParams p) {
 #pragma unroll
   for (int in = 0; in < JN; ++in) {
     const int col = n0 + 32 * (JN * wn + in) + (lane & 31);
-    bcol[in] = (p.bias != nullptr && col < N) ? bf2f(load_pinned_u16(p.bias + col)) : 0.0f;
+    const uint16_t bq =  // unconditional: see gemm_epi_issue
+        load_pinned_u16(p.bias != nullptr ? p.bias + min(col, N - 1) : p.W);
+    bcol[in] = (p.bias != nullptr && col < N) ? bf2f(bq) : 0.0f;
   }
   // this lane's rows and chunk for the direct loads: instruction j covers
   // rows RPI j .. RPI j + RPI - 1; lane l fills row RPI j + l / CH, slot
@@ -811,25 +806,32 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_lds(GemmParams p) {
 #else
 #define GEMM_LDS_LOAD(g, l) ((void)(g), (void)(l))
 #endif
-#define GEMM_LDS_ISSUE(kt_)                                                                \
+  // every wave issues the same copies at every step (past the last step the
+  // last one again, into a stage that is not read any more), so one vmcnt
+  // value covers a step
+#define GEMM_LDS_ISSUE(kt_, slot_)                                                         \
   do {                                                                                     \
-    uint4* base_ = lds + ((kt_) % G::NS) * G::STAGE;                                       \
-    const int ko_ = (kt_) * G::BK;                                                         \
+    uint4* base_ = lds + (slot_) * G::STAGE;                                               \
+    const int ko_ = min((kt_), nk - 1) * G::BK;                                            \
     _Pragma("unroll") for (int i = 0; i < G::A_LOADS; ++i)                                 \
       GEMM_LDS_LOAD(ag[i] + ko_, base_ + (w + WAVES * i) * 64);                            \
     _Pragma("unroll") for (int i = 0; i < G::B_LOADS; ++i)                                 \
       GEMM_LDS_LOAD(bg[i] + ko_, base_ + G::A_UNITS + (w + WAVES * i) * 64);               \
   } while (0)
 #pragma unroll
-  for (int s = 0; s < G::NS - 1; ++s)
-    if (s < nk) GEMM_LDS_ISSUE(s);
+  for (int s = 0; s < G::NS - 1; ++s) GEMM_LDS_ISSUE(s, s);
   // fragment units: row r, 16-k step ks -> chunk 2 ks + lane / 32 at slot c ^ swz(r)
   const int fr = lane & 31, fh = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
     // stage kt complete (the stages after it that were issued may still load)
-    wait_stages<G::LOADS, G::NS>(min(G::NS - 2, nk - 1 - kt));
-    __syncthreads();  // every wave's loads landed; stage (kt - 1) % NS is free
-    if (kt + G::NS - 1 < nk) GEMM_LDS_ISSUE(kt + G::NS - 1);
+    wait_vmcnt<(G::NS - 2) * G::LOADS>();  // this wave's copies of step kt have landed
+    // every wave's have, and every wave's reads of stage (kt - 1) % NS are
+    // complete (lgkmcnt 0), so it may be refilled.  Not __syncthreads(): its
+    // fence waits for every outstanding copy (vmcnt 0), the later stages'
+    // too, which leaves the ring one stage deep
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    GEMM_LDS_ISSUE(kt + G::NS - 1, (kt + G::NS - 1) % G::NS);
+    __builtin_amdgcn_sched_barrier(0);  // the copies go out before this step's reads
     const uint4* st = lds + (kt % G::NS) * G::STAGE;
     // fragments of 16-k step ks into register set ks % 2; the next step's
     // reads are issued before this step's MFMAs, so LDS latency hides behind
@@ -862,6 +864,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_lds(GemmParams p) {
     }
 #undef GEMM_LDS_FRAGS
   }
+  wait_vmcnt<0>();  // the ring's last (unread) copies have landed before LDS is reused
 #undef GEMM_LDS_ISSUE
 #undef GEMM_LDS_LOAD
   // epilogue: acc[im][in][i] is row 32 IM wm + 32 im + 8 (i / 4) + 4 (lane / 32) + i % 4,
@@ -940,9 +943,12 @@ static void launch_gemm_lds_v(const GemmParams& p, hipStream_t st) {
 // the one with the fewest rounds of the device times per-block MFMA work
 // (BM x BN), ties to the larger tile (fewer operand re-reads).  Every tile
 // runs 8 waves, two per SIMD, with 64-deep K steps.  Measured at the
-// prompt pass's shapes (M = 2047): QKV (N 5120, K 2880, 256 x 192) 76 us,
-// O + residual (N 2880, K 4096, 128 x 192) 76 us; 4 waves per block, or
-// 32-deep steps with more stages in flight, were 3 to 25% slower.
+// prompt pass's shapes (M = 2047): QKV (N 5120, K 2880, 256 x 192, 2
+// stages) 69 us, O + residual (N 2880, K 4096, 128 x 192, 3 stages) 62 us
+// (71 us while the step barrier also waited for the later stages' copies);
+// QKV on 128 x 192 tiles 85 us; 32-deep steps with 5-9 stages in flight
+// (256 x 128 and 128 x 128) 108-117 us for QKV and 72-94 us for O; 4 waves
+// per block 3 to 25% slower.
 static void gemm_lds_tile(int M, int N, int& bm, int& nb) {
   long best = -1;
   for (int b : {256, 128})
@@ -953,10 +959,21 @@ static void gemm_lds_tile(int M, int N, int& bm, int& nb) {
     }
 }
 
+// NEON_GEMM_LDS = "BM,NB,64" forces one of the shapes below, for comparisons
 template <int MODE>
 static void launch_gemm_lds(const GemmParams& p, hipStream_t st) {
   int bm = 256, nb = 6;
   gemm_lds_tile(p.M, p.N, bm, nb);
+  static int force[3] = {-1, 0, 0};
+  if (force[0] == -1) {
+    force[0] = 0;
+    if (const char* e = getenv("NEON_GEMM_LDS")) sscanf(e, "%d,%d,%d", &force[0], &force[1], &force[2]);
+  }
+  if (force[0] > 0 && force[2] == 64 && (force[0] == 256 || force[0] == 128) &&
+      (force[1] == 6 || force[1] == 4)) {
+    bm = force[0];
+    nb = force[1];
+  }
   if (bm == 256) {
     if (nb == 6) launch_gemm_lds_v<MODE, 256, 6, 64, 8, 1>(p, st);
     else launch_gemm_lds_v<MODE, 256, 4, 64, 8, 1>(p, st);
