@@ -1454,17 +1454,19 @@ __global__ __launch_bounds__(512) void k_attn_prefill(
 
 // fp32 C[M][N] = A[M][K] W[N][K]^T + bias[N] for N <= kNarrowMaxN (the router
 // logits of the prompt pass, N = E): a block owns 16 rows of A and all N
-// columns (NT tiles of 16) on v_mfma_f32_16x16x32_bf16; its 4 waves take
-// the 32-element K chunks c = w, w + 4, ..., loading kNarrowBatch chunks at
-// a time before their MFMAs, then wave 0 adds the 4 partial tiles in wave
-// order and the bias.
+// columns (NT tiles of 16) on v_mfma_f32_16x16x32_bf16; its kNarrowWaves
+// waves take the 32-element K chunks c = w, w + kNarrowWaves, ..., loading
+// kNarrowBatch chunks at a time before their MFMAs (every load is used by
+// an MFMA, chunks past K with both operands zeroed: a load used only under
+// a branch is sunk into it by the compiler and waited for alone, which made
+// this kernel one memory round trip per chunk, 26 us per prompt layer), then
+// wave 0 adds the partial tiles in wave order and the bias.
+constexpr int kNarrowWaves = 8;
 template <int NT>
-__global__ __launch_bounds__(256) void k_gemm_narrow_f32(const uint16_t* __restrict__ A,
-                                                         const uint16_t* __restrict__ W,
-                                                         const uint16_t* __restrict__ bias,
-                                                         float* __restrict__ C, int M, int N,
-                                                         int K) {
-  __shared__ pf_f32x4 red[3][NT][64];
+__global__ __launch_bounds__(64 * kNarrowWaves) void k_gemm_narrow_f32(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ W,
+    const uint16_t* __restrict__ bias, float* __restrict__ C, int M, int N, int K) {
+  __shared__ pf_f32x4 red[kNarrowWaves - 1][NT][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * 16;
@@ -1476,25 +1478,31 @@ __global__ __launch_bounds__(256) void k_gemm_narrow_f32(const uint16_t* __restr
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = pf_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const int nch = K / 32;
-  for (int c0 = w; c0 < nch; c0 += 4 * kNarrowBatch) {
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  for (int c0 = w; c0 < nch; c0 += kNarrowWaves * kNarrowBatch) {
     uint4 av[kNarrowBatch], wv[kNarrowBatch][NT];
 #pragma unroll
     for (int i = 0; i < kNarrowBatch; ++i) {
-      const int c = min(c0 + 4 * i, nch - 1);  // past the end: re-read, then dropped
-      av[i] = *reinterpret_cast<const uint4*>(arow + 32 * (size_t)c);
+      const bool ok = c0 + kNarrowWaves * i < nch;
+      const int c = min(c0 + kNarrowWaves * i, nch - 1);  // past the end: re-read, zeroed
+      const uint4 a = *reinterpret_cast<const uint4*>(arow + 32 * (size_t)c);
+      av[i] = ok ? a : z;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-        wv[i][nt] = *reinterpret_cast<const uint4*>(wrow[nt] + 32 * (size_t)c);
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint4 b = *reinterpret_cast<const uint4*>(wrow[nt] + 32 * (size_t)c);
+        wv[i][nt] = ok ? b : z;
+      }
     }
+    // keep the scheduler from placing the selects (which wait for their
+    // loads) between the loads
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < kNarrowBatch; ++i) {
-      if (c0 + 4 * i >= nch) break;  // uniform
+    for (int i = 0; i < kNarrowBatch; ++i)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
         acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf_as_bf16x8(av[i]),
                                                           pf_as_bf16x8(wv[i][nt]), acc[nt], 0,
                                                           0, 0);
-    }
   }
   if (w > 0) {
 #pragma unroll
@@ -1506,7 +1514,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow_f32(const uint16_t* __restr
   for (int nt = 0; nt < NT; ++nt) {
     pf_f32x4 tot = acc[nt];
 #pragma unroll
-    for (int v = 0; v < 3; ++v) {
+    for (int v = 0; v < kNarrowWaves - 1; ++v) {
       const pf_f32x4 p = red[v][nt][lane];
       tot[0] += p[0]; tot[1] += p[1]; tot[2] += p[2]; tot[3] += p[3];
     }
@@ -1525,10 +1533,10 @@ static void launch_gemm_narrow_f32(const uint16_t* A, const uint16_t* W, const u
                                    float* C, int M, int N, int K, hipStream_t st) {
   const dim3 grid((M + 15) / 16);
   switch ((N + 15) / 16) {
-    case 1: hipLaunchKernelGGL(k_gemm_narrow_f32<1>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
-    case 2: hipLaunchKernelGGL(k_gemm_narrow_f32<2>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
-    case 3: hipLaunchKernelGGL(k_gemm_narrow_f32<3>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
-    default: hipLaunchKernelGGL(k_gemm_narrow_f32<4>, grid, dim3(256), 0, st, A, W, bias, C, M, N, K); break;
+    case 1: hipLaunchKernelGGL(k_gemm_narrow_f32<1>, grid, dim3(64 * kNarrowWaves), 0, st, A, W, bias, C, M, N, K); break;
+    case 2: hipLaunchKernelGGL(k_gemm_narrow_f32<2>, grid, dim3(64 * kNarrowWaves), 0, st, A, W, bias, C, M, N, K); break;
+    case 3: hipLaunchKernelGGL(k_gemm_narrow_f32<3>, grid, dim3(64 * kNarrowWaves), 0, st, A, W, bias, C, M, N, K); break;
+    default: hipLaunchKernelGGL(k_gemm_narrow_f32<4>, grid, dim3(64 * kNarrowWaves), 0, st, A, W, bias, C, M, N, K); break;
   }
 }
 
