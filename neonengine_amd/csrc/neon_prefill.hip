@@ -1115,6 +1115,54 @@ __global__ void k_moe_combine(const float* __restrict__ ybuf,
   }
 }
 
+// k_moe_combine with 8 consecutive columns per thread (32-byte loads of each
+// slot's fp32 row, 16-byte load and store of the residual): the same
+// operations per element in the same order, for KSL slots (the model's
+// top-k).  The slots' ids and scores are read once per block.  H % 8 == 0.
+template <int KSL>
+__global__ __launch_bounds__(384) void k_moe_combine8(const float* __restrict__ ybuf,
+                                                      const float* __restrict__ score,
+                                                      const int32_t* __restrict__ idx, int E,
+                                                      int H, uint16_t* __restrict__ h) {
+  const int t = blockIdx.x;
+  float sc[KSL];
+  bool ok[KSL];
+#pragma unroll
+  for (int s = 0; s < KSL; ++s) {
+    sc[s] = score[t * KSL + s];
+    // pairs with an id outside [0, E) were never computed: they add 0
+    ok[s] = (unsigned)idx[t * KSL + s] < (unsigned)E;
+  }
+  for (int n = 8 * threadIdx.x; n < H; n += 8 * blockDim.x) {
+    float4 v[KSL][2];
+#pragma unroll
+    for (int s = 0; s < KSL; ++s) {
+      const float4* src = reinterpret_cast<const float4*>(ybuf + ((size_t)t * KSL + s) * H + n);
+      v[s][0] = src[0];
+      v[s][1] = src[1];
+    }
+    uint4* cp = reinterpret_cast<uint4*>(h + (size_t)t * H + n);
+    const uint4 c = *cp;
+    float y[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KSL; ++s) {
+      const float e[8] = {v[s][0].x, v[s][0].y, v[s][0].z, v[s][0].w,
+                          v[s][1].x, v[s][1].y, v[s][1].z, v[s][1].w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) y[q] = __builtin_fmaf(sc[s], ok[s] ? e[q] : 0.0f, y[q]);
+    }
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = __fadd_rn(bf2f((uint16_t)(cw[q] & 0xFFFFu)), bf2f(f2bf(y[2 * q])));
+      const float hi = __fadd_rn(bf2f((uint16_t)(cw[q] >> 16)), bf2f(f2bf(y[2 * q + 1])));
+      o[q] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    }
+    *cp = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // MoE layer over M tokens: experts from idx/score [M][k], input xn [M][H],
 // residual stream h [M][H] updated in place.  Scratch: list_tok/list_slot
 // [M k], e_off [E+1], tile_e/tile_r0 [max_tiles], n_tiles [1], act [M k][I]
@@ -1154,8 +1202,12 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   else
     hipLaunchKernelGGL((k_gemm<GEMM_SCATTER, true, true>), dim3((a.H + kGN - 1) / kGN, max_tiles),
                        dim3(256), 0, st, p);
-  hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.idx, a.E,
-                     a.k, a.H, a.h);
+  if (a.H % 8 == 0 && a.k == 4)  // the gpt-oss top-4
+    hipLaunchKernelGGL(k_moe_combine8<4>, dim3(a.M), dim3(min(384, (a.H / 8 + 63) / 64 * 64)),
+                       0, st, a.ybuf, a.score, a.idx, a.E, a.H, a.h);
+  else
+    hipLaunchKernelGGL(k_moe_combine, dim3(a.M), dim3(256), 0, st, a.ybuf, a.score, a.idx, a.E,
+                       a.k, a.H, a.h);
 }
 
 int moe_prefill_max_tiles(int M, int k, int E) {
