@@ -969,7 +969,9 @@ void launch_mxfp4_gemv_mfma(const uint8_t* codes, const uint8_t* scales, const u
 // weight tiles of 16 rows per wave and rows per block.  Measured at the 20b
 // shape (tok/s at B = 16 / 64): 4 tiles (228 VGPRs, 2 waves per SIMD)
 // 3754 / 7924, 2 tiles (146 VGPRs) 4141 / 9400, 1 tile 4206 / 9499 -- more
-// waves in flight beat the activation reuse of wider waves.
+// waves in flight beat the activation reuse of wider waves.  Likewise 8
+// waves of one tile per block (128 rows sharing each staged input chunk,
+// half the blocks): 4711 / 15,454 against 4943 / 15,836 with 4.
 constexpr int kMxMoeTiles = 1, kMxMoeRows = 64 * kMxMoeTiles;
 
 // The work item of block row blockIdx.y (one load: the item count and the
