@@ -745,6 +745,210 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// k_gemm_mx8 with the A operand (the input rows' MXFP8 step lines) copied
+// into LDS by global_load_lds instead of through a register ring, and the
+// next step's fragments read from LDS while this step's MFMAs run (two
+// register sets).  A goes through two stages: step k + 2 is copied while
+// step k multiplies, into the stage whose fragments (step k) were read
+// during step k - 1; lane l of a copy writes the 16 bytes at base + 16 l and
+// fetches 16-byte slot (l % 8) ^ swa(row) of its row's line, so the reads of
+// 8 or 16 consecutive rows hit different banks.  B (the expert's MXFP4
+// rows, a group of kPipe steps = one 128-byte line per column) and the
+// scales keep k_gemm_mx8's register staging; a group's B is staged two
+// steps after its loads go out, a step's A scale dword two steps ahead.
+// One barrier per step.  Same MFMA sequence and operands as k_gemm_mx8, so
+// the outputs are bit-identical to it.
+__device__ __forceinline__ int mx8b_swa(int r) { return (r ^ (r >> 3)) & 7; }
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void k_gemm_mx8b(GemmParams p) {
+  // A step lines of the two stages, slot s of row r at s ^ swa(r) (two
+  // arrays: the compiler then sees that a copy into one stage does not touch
+  // the other, and does not wait for it before reading the other)
+  __shared__ __align__(16) uint4 Ar0[kGM * 8], Ar1[kGM * 8];
+  __shared__ uint32_t Asc[2][kGM];                // per row: s_hi b0, s_hi b1, s_lo b0, s_lo b1
+  __shared__ __align__(16) uint8_t Bq[2][kGN * kQS];   // per column: kPipe steps x 32 B
+  __shared__ uint16_t Bsc[2][kGN * kPipe];       // per column and step: the 2 blocks' scales
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int n0, e, r0, rows;
+  if (!mx8_block_map(p, n0, e, r0, rows)) return;  // uniform for the block
+  __shared__ GemmEpiLds epl;
+  GemmEpi ep;
+  gemm_epi_issue<MODE, true>(p, lane, wn, n0, r0, rows, e, ep, epl);
+  const int K = p.K, KB = K / 32, nk = K / 64;
+  // A copies: wave w copies pieces w + 4 i (rows 8 p .. 8 p + 7 of the tile)
+  const uint8_t* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (wave + 4 * i) + (lane >> 3);
+    const int lr = r0 + min(r, rows - 1);
+    const int ar = p.a_rows ? p.a_rows[lr] : lr;
+    asrc[i] = p.qa + (size_t)ar * nk * 128 + 16 * ((lane & 7) ^ mx8b_swa(r));
+  }
+  // B staging map (k_gemm_mx8's): piece c = tid + 256 i is column c >> 3,
+  // 16-byte piece c & 7 of its group line
+  const int pc = tid & 7;
+  const uint8_t* bsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = (tid + 256 * i) >> 3;
+    bsrc[i] = p.codes + ((size_t)e * p.N + min(n0 + c, p.N - 1)) * (K / 2) + 16 * (pc & 1);
+  }
+  const uint32_t* ssrc;
+  {
+    const int lr = r0 + min(tid & 127, rows - 1);
+    const int ar = p.a_rows ? p.a_rows[lr] : lr;
+    ssrc = p.qsc + (size_t)ar * mx8_scale_stride(K);
+  }
+  const int ng = (nk + kPipe - 1) / kPipe;
+  const uint8_t* bssrc = p.scales + ((size_t)e * p.N + min(n0 + (tid & 127), p.N - 1)) * KB;
+  const int bsj = 2 * (tid >> 7);
+  u32x4_t rsg_cur, rsg_next;  // A scales of this group and the next
+  u32x4_t rbq[4];
+  uint32_t rbs[2];
+#if defined(__HIP_DEVICE_COMPILE__)
+#define MX8B_COPY(g, l) __builtin_amdgcn_global_load_lds((g), (l), 16, 0, 0)
+#else
+#define MX8B_COPY(g, l) ((void)(g), (void)(l))
+#endif
+  auto issue_a = [&](int kt, int slot) {
+    const int st = min(kt, nk - 1);  // past the last step: a copy never read
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      MX8B_COPY(asrc[i] + (size_t)st * 128, (slot ? Ar1 : Ar0) + (wave + 4 * i) * 64);
+  };
+#undef MX8B_COPY
+  auto load_b = [&](int g) {
+    const int st = min(g * kPipe + (pc >> 1), nk - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      rbq[i] = *reinterpret_cast<const u32x4_t*>(bsrc[i] + (size_t)st * 32);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int sj = min(g * kPipe + bsj + j, nk - 1);
+      rbs[j] = *reinterpret_cast<const uint16_t*>(bssrc + 2 * sj);
+    }
+  };
+  auto stage_b = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = (tid + 256 * i) >> 3;
+      *reinterpret_cast<u32x4_t*>(&Bq[buf][c * kQS + 16 * pc]) = rbq[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) Bsc[buf][(tid & 127) * kPipe + bsj + j] = (uint16_t)rbs[j];
+  };
+  struct Frag {
+    i32x8_t ahi[2], alo[2], bq[2];
+    int sa_hi[2], sa_lo[2], s_b[2];
+  };
+  const int h = h_of(lane);
+  // the fragments of step kt (A stage kt % 2, B group buffer gb, step u of it)
+  auto read_frag = [&](int slot, int gb, int u, Frag& f) {
+#pragma unroll
+    for (int im = 0; im < 2; ++im) {
+      const int rr = wm * 64 + im * 32 + (lane & 31);
+      const uint4* row = (slot ? Ar1 : Ar0) + rr * 8;
+      const int sw = mx8b_swa(rr);
+      const u32x4_t h0 = *reinterpret_cast<const u32x4_t*>(row + ((h + 0) ^ sw));
+      const u32x4_t h1 = *reinterpret_cast<const u32x4_t*>(row + ((h + 2) ^ sw));
+      const u32x4_t l0 = *reinterpret_cast<const u32x4_t*>(row + ((h + 4) ^ sw));
+      const u32x4_t l1 = *reinterpret_cast<const u32x4_t*>(row + ((h + 6) ^ sw));
+      const uint32_t sc = Asc[slot][rr];
+      f.sa_hi[im] = (int)((sc >> (8 * h)) & 0xFFu);
+      f.sa_lo[im] = (int)((sc >> (16 + 8 * h)) & 0xFFu);
+      f.ahi[im] = i32x8_t{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w,
+                          (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+      f.alo[im] = i32x8_t{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w,
+                          (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+    }
+#pragma unroll
+    for (int in = 0; in < 2; ++in) {
+      const int cn = wn * 64 + in * 32 + (lane & 31);
+      const u32x4_t b4 = *reinterpret_cast<const u32x4_t*>(&Bq[gb][cn * kQS + u * 32 + 16 * h]);
+      f.bq[in] = i32x8_t{(int)b4.x, (int)b4.y, (int)b4.z, (int)b4.w, 0, 0, 0, 0};
+      f.s_b[in] = (int)((Bsc[gb][cn * kPipe + u] >> (8 * h)) & 0xFFu);
+    }
+  };
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+  auto mfma = [&](const Frag& f) {
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+      for (int in = 0; in < 2; ++in)
+        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f.ahi[im], f.bq[in], acc[im][in], 0, 4, 0, f.sa_hi[im], 0, f.s_b[in]);
+#pragma unroll
+    for (int im = 0; im < 2; ++im)
+#pragma unroll
+      for (int in = 0; in < 2; ++in)
+        acc[im][in] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f.alo[im], f.bq[in], acc[im][in], 0, 4, 0, f.sa_lo[im], 0, f.s_b[in]);
+  };
+  // prologue: A of steps 0 and 1, B and scales of group 0, staged
+  issue_a(0, 0);
+  issue_a(1, 1);
+  load_b(0);
+  rsg_cur = *reinterpret_cast<const u32x4_t*>(ssrc);
+  rsg_next = *reinterpret_cast<const u32x4_t*>(ssrc + 4 * min(1, ng - 1));
+  stage_b(0);
+  if (tid < kGM) {
+    Asc[0][tid] = rsg_cur.x;
+    Asc[1][tid] = rsg_cur.y;
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  Frag fr[2];
+  read_frag(0, 0, 0, fr[0]);
+  for (int kt0 = 0; kt0 < nk; kt0 += kPipe) {
+    const int g = kt0 / kPipe, gb = g & 1;
+#pragma unroll
+    for (int u = 0; u < kPipe; ++u) {
+      const int kt = kt0 + u;
+      if (kt >= nk) break;  // uniform for the block
+      // A of step kt + 1 (copied during step kt - 1; then group g's B loads
+      // went out after it at u = 1) has landed for this wave; the barrier:
+      // for every wave, and every wave's reads of step kt's stage and of the
+      // scale dwords staged two steps back are done
+      if (u == 1) wait_vmcnt<7>();
+      else wait_vmcnt<0>();
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue_a(kt + 2, u & 1);  // into the stage of step kt, read during step kt - 1
+      if (u == 0) {
+        load_b(g + 1);  // group g + 1's B, staged at u = 2
+        if (g > 0) rsg_cur = rsg_next;
+        rsg_next = *reinterpret_cast<const u32x4_t*>(ssrc + 4 * min(g + 1, ng - 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < nk)  // uniform
+        read_frag((u + 1) & 1, u == kPipe - 1 ? gb ^ 1 : gb, (u + 1) % kPipe, fr[(u + 1) & 1]);
+      mfma(fr[u & 1]);
+      // the scale dword of step kt + 2 into its stage (that of step kt)
+      if (tid < kGM)
+        Asc[u & 1][tid] = u == 0 ? rsg_cur.z : u == 1 ? rsg_cur.w : u == 2 ? rsg_next.x : rsg_next.y;
+      if (u == 2) stage_b(gb ^ 1);  // group g + 1 (its buffer's last reads were in step 4 g - 2)
+    }
+  }
+  wait_vmcnt<0>();  // the last (unread) copies have landed before LDS is reused
+  gemm_epi_stage<MODE>(ep, epl);
+  gemm_epilogue<MODE, true>(acc, p, lane, wm, wn, n0, r0, rows, ep, epl);
+}
+
+// The MXFP8 expert GEMMs run k_gemm_mx8b: at the 2048-token 20b shape 367 /
+// 201 us per layer (gate_up / down) against 388 / 215 us for k_gemm_mx8 in
+// the same run, the same bits.  NEON_MX8_GEMM = "a" selects k_gemm_mx8, for
+// comparisons.
+static bool mx8_gemm_b() {
+  static const bool v = !(getenv("NEON_MX8_GEMM") && getenv("NEON_MX8_GEMM")[0] == 'a');
+  return v;
+}
+
 template <int MODE, int BM, int NB, int BK, int WM, int WN>
 __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_lds(GemmParams p) {
   using G = GemmLdsCfg<BM, NB, BK, WM, WN>;
@@ -1185,7 +1389,10 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   p.A = a.xn; p.lda = a.H; p.a_rows = a.list_tok;
   p.codes = a.gu_codes; p.scales = a.gu_scales; p.bias = a.gu_bias;
   p.C = a.act; p.ldc = a.I; p.N = 2 * a.I; p.K = a.H;
-  if (mx8)
+  if (mx8 && mx8_gemm_b())
+    hipLaunchKernelGGL((k_gemm_mx8b<GEMM_SWIGLU>), mx8_grid(2 * a.I, max_tiles),
+                       dim3(256), 0, st, p);
+  else if (mx8)
     hipLaunchKernelGGL((k_gemm_mx8<GEMM_SWIGLU>), mx8_grid(2 * a.I, max_tiles),
                        dim3(256), 0, st, p);
   else
@@ -1196,7 +1403,10 @@ void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   p.A = a.act; p.lda = a.I; p.a_rows = nullptr;
   p.codes = a.dn_codes; p.scales = a.dn_scales; p.bias = a.dn_bias;
   p.ybuf = a.ybuf; p.N = a.H; p.K = a.I; p.C = nullptr;
-  if (mx8)
+  if (mx8 && mx8_gemm_b())
+    hipLaunchKernelGGL((k_gemm_mx8b<GEMM_SCATTER>), mx8_grid(a.H, max_tiles),
+                       dim3(256), 0, st, p);
+  else if (mx8)
     hipLaunchKernelGGL((k_gemm_mx8<GEMM_SCATTER>), mx8_grid(a.H, max_tiles),
                        dim3(256), 0, st, p);
   else
