@@ -1068,14 +1068,13 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   auto compute = [&](int c, int buf, const uint4 (&wv)[TT][4], const float (&sv)[TT][4]) {
 #pragma unroll
     for (int su = 0; su < 4; ++su) {
-      const int ur = CKU * c + 4 * g + su;
-      const bool uv = ur < U;  // a zero A value drops a padded unit
+      // units past K (the last chunk's padding) hold zero codes at scale
+      // 2^0 in the packed copy and zero inputs in xs (x_load), so their
+      // products are +0 like those of any zero input: no mask is needed
       uint4 af[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint4 v = *reinterpret_cast<const uint4*>(&xs[buf][j][32 * (4 * g + su) + 8 * t]);
-        af[t] = uv ? v : make_uint4(0u, 0u, 0u, 0u);
-      }
+      for (int t = 0; t < 4; ++t)
+        af[t] = *reinterpret_cast<const uint4*>(&xs[buf][j][32 * (4 * g + su) + 8 * t]);
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         const uint4 cw = wv[tt][su];
