@@ -134,8 +134,10 @@ struct neon_ctx {
   int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
   int32_t* rr_arrive = nullptr;  // one word (router + route lists, matrix-core steps)
   // the router, top-k and route lists of the matrix-core steps in one launch
-  // from 49 rows (NEON_ROUTER_ROUTE=0: always the two launches, for comparisons)
+  // from 49 rows (NEON_ROUTER_ROUTE=0: always the two launches, =2: the one
+  // launch from 2 rows, for comparisons)
   bool fuse_route = !(getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '0');
+  int fuse_route_min = getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '2' ? 2 : 49;
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -809,8 +811,9 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     r.arrive = ctx->rr_arrive;
     // one launch from 49 rows (20b step, tok/s fused / two launches: B = 64
     // 15,896 / 15,706, 48 12,585 / 12,584, 32 8884 / 8994, 16 4909 / 5056:
-    // below that the arrival round trip costs more than the launch it saves)
-    if (ctx->fuse_route && B > 48 && router_route_supported(r)) {
+    // below that the arrival round trip costs more than the launch it saves;
+    // with the 8-wave router kernel, B = 32 8899 / 9017, 16 4945 / 5091)
+    if (ctx->fuse_route && B >= ctx->fuse_route_min && router_route_supported(r)) {
       launch_router_route(r, ctx->moe_idx, ctx->moe_score, ctx->mx_route, st);
     } else {
       launch_router(r, st);

@@ -1789,10 +1789,13 @@ __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ l
 }
 
 // Router logits, top-k and the matrix-core route lists in one launch (B >= 2,
-// no MXFP8 image): block b owns row b.  Its 16 waves each normalise the row
-// (k_router_logits' wave_x_bf16 operations, wave 0 writing xn) and form the
-// logits of experts w, w + 16, ... with k_router_logits' dot and bias add, so
-// every logit has its bits; wave 0 then ranks the row (k_topk's ranking) from
+// no MXFP8 image): block b owns row b.  Its 8 waves each request their
+// router rows (experts w, w + 8, w + 16, w + 24 of each 32) together with the
+// input row, normalise the row (k_router_logits' wave_x_bf16 operations,
+// wave 0 writing xn) and form the logits with k_router_logits' dot and bias
+// add, so every logit has its bits (16 waves of two rows each, which waited
+// for the normalised row before requesting their rows, ran B = 64 at 16,133
+// against 16,200 tok/s); wave 0 then ranks the row (k_topk's ranking) from
 // LDS.  The row's expert ids are stored at agent scope (written through to
 // the device's coherence point), every wave waits for its stores (vmcnt 0),
 // the block meets at a barrier, and one thread arrives on arrive[0] with an
@@ -1801,8 +1804,9 @@ __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ l
 // arrive[0] back to 0 (it must be 0 at launch).  At the 20b shape, B = 64:
 // 15.3 us per layer against 5.1 + 12.0 us for k_router_logits + k_topk_route
 // (14,764 against 14,615 tok/s).
+constexpr int kRRWaves = 8;  // k_router_route: waves per block
 template <int P>
-__global__ __launch_bounds__(1024) void k_router_route(
+__global__ __launch_bounds__(64 * kRRWaves) void k_router_route(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
     const uint16_t* __restrict__ bias, float* __restrict__ lg_out, int32_t* idx,
@@ -1818,27 +1822,37 @@ __global__ __launch_bounds__(1024) void k_router_route(
   const int U = H / 8;
   XBf16Raw<P> xraw;
   wave_x_bf16_issue<P, true>(xraw, x + (size_t)b * H, nw, H, lane);
+  // the wave's router rows (experts w + 8 q of each group of 32) go out
+  // before the input row is normalised: they do not depend on it
+  uint4 wr[4][P];
+  uint16_t bvv[4];
+  auto load_rows = [&](int e0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = min(e0 + kRRWaves * q, E - 1);
+      bvv[q] = bias[e];
+      bf16_load_row<P>(wr[q], W + (size_t)e * H, U, lane);
+    }
+  };
+  load_rows(w);
   __builtin_amdgcn_sched_barrier(0);
   float xr[P][8];
   wave_x_bf16_finish<P, true>(xr, xraw, eps, H, lane,
                               (xn_out != nullptr && w == 0) ? xn_out + (size_t)b * H : nullptr);
-  // experts w + 16 i, two at a time with both rows requested together
-  for (int e0 = w; e0 < E; e0 += 32) {  // uniform per wave
-    const int e1 = e0 + 16;
-    const uint16_t b0v = bias[e0], b1v = bias[min(e1, E - 1)];
-    uint4 wr0[P], wr1[P];
-    bf16_load_row<P>(wr0, W + (size_t)e0 * H, U, lane);
-    bf16_load_row<P>(wr1, W + (size_t)min(e1, E - 1) * H, U, lane);
-    const float acc0 = wave_sum(bf16_row_partial<P>(wr0, xr, U, lane));
-    const float acc1 = wave_sum(bf16_row_partial<P>(wr1, xr, U, lane));
+  for (int e0 = w; e0 < E; e0 += 4 * kRRWaves) {  // uniform per wave
+    if (e0 != w) load_rows(e0);
+    float acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = wave_sum(bf16_row_partial<P>(wr[q], xr, U, lane));
     if (lane == 0) {
-      const float v0 = __fadd_rn(acc0, bf2f(b0v));
-      lg_s[e0] = v0;
-      lg_out[(size_t)b * E + e0] = v0;
-      if (e1 < E) {
-        const float v1 = __fadd_rn(acc1, bf2f(b1v));
-        lg_s[e1] = v1;
-        lg_out[(size_t)b * E + e1] = v1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = e0 + kRRWaves * q;
+        if (e < E) {
+          const float v = __fadd_rn(acc[q], bf2f(bvv[q]));
+          lg_s[e] = v;
+          lg_out[(size_t)b * E + e] = v;
+        }
       }
     }
   }
@@ -1865,7 +1879,7 @@ __global__ __launch_bounds__(1024) void k_router_route(
   __syncthreads();
   if (!is_last) return;  // uniform
   const int nk = B * k;
-  for (int q = tid; q < nk; q += 1024)
+  for (int q = tid; q < nk; q += 64 * kRRWaves)
     pair_e[q] = __hip_atomic_load(idx + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   mx_route_lists(pair_e, nk, E, S, route, cnt_e, slot_of, wave_used);
@@ -1884,9 +1898,9 @@ void launch_router_route(const RouterArgs& a, int32_t* idx, float* score, int32_
   const int P = (a.H / 8 + 63) / 64;
 #define RR_CASE(PP)                                                                       \
   case PP:                                                                                \
-    hipLaunchKernelGGL((k_router_route<PP>), dim3(a.B), dim3(1024), 0, st, a.x, a.norm_w,  \
-                       a.eps, a.xn_out, a.W, a.bias, a.lg_out, idx, score, a.B, a.E, a.H, \
-                       a.k, S, route, a.arrive, a.zero, a.zero_n);                       \
+    hipLaunchKernelGGL((k_router_route<PP>), dim3(a.B), dim3(64 * kRRWaves), 0, st, a.x,    \
+                       a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, idx, score, a.B, \
+                       a.E, a.H, a.k, S, route, a.arrive, a.zero, a.zero_n);             \
     break;
   switch (P) {
     RR_CASE(1) RR_CASE(2) RR_CASE(3) RR_CASE(4) RR_CASE(5)
