@@ -1230,19 +1230,35 @@ __global__ __launch_bounds__(64) void k_mx_attn(
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = mx_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   float m = -INFINITY, l = 0.0f;
-  for (int c = c0; c < c1; ++c) {
+  // a chunk's K and V pieces (lane: keys 8 i + lane / 8, dims 8 (lane % 8)
+  // .. + 7); the next chunk's are requested before this one is staged and
+  // multiplied, so a split of several chunks pays one memory round trip
+  // instead of one per chunk
+  uint4 kq[8], vq[8];
+  auto load_chunk = [&](int c, uint4 (&kd)[8], uint4 (&vd)[8]) {
+    const int kb = lo + 64 * c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kl = 8 * i + (lane >> 3), dq = (lane & 7) * 8;
+      const int key = min(kb + kl, p);  // keys past p are masked below
+      const size_t row = kv_base + (size_t)(key & key_mask);
+      kd[i] = *reinterpret_cast<const uint4*>(kc + row * 64 + dq);
+      vd[i] = *reinterpret_cast<const uint4*>(vc + row * 64 + dq);
+    }
+  };
+  // chunk c (its pieces in kd / vd) into LDS, then into the running state
+  auto process = [&](int c, const uint4 (&kd)[8], const uint4 (&vd)[8]) {
     const int kb = lo + 64 * c;
     __syncthreads();  // the previous chunk is consumed
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int kl = 8 * i + (lane >> 3), dq = (lane & 7) * 8;
       const int key = min(kb + kl, p);  // keys past p are masked below
-      const size_t row = kv_base + (size_t)(key & key_mask);
       const bool fresh = owner && key == p;  // (dq == dql)
       // both rows loaded, then selected word by word (a select between a
       // load and a register value would put the value in private memory)
-      const uint4 kg = *reinterpret_cast<const uint4*>(kc + row * 64 + dq);
-      const uint4 vg = *reinterpret_cast<const uint4*>(vc + row * 64 + dq);
+      const uint4 kg = kd[i];
+      const uint4 vg = vd[i];
       const uint4 kv = make_uint4(fresh ? knew.x : kg.x, fresh ? knew.y : kg.y,
                                   fresh ? knew.z : kg.z, fresh ? knew.w : kg.w);
       const uint4 vv = make_uint4(fresh ? vnew.x : vg.x, fresh ? vnew.y : vg.y,
@@ -1318,6 +1334,26 @@ __global__ __launch_bounds__(64) void k_mx_attn(
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mx_as_bf16x8(vfrag), mx_as_bf16x8(plo),
                                                         o[dt], 0, 0, 0);
       }
+    }
+  };
+  if (c1 - c0 <= 1) {  // uniform: one chunk (or none) in this split
+    if (c0 < c1) {
+      load_chunk(c0, kq, vq);
+      process(c0, kq, vq);
+    }
+  } else {
+    // two register sets in turn (a copy from one to the other would be
+    // scheduled inside the chunk's work and wait for the loads there); the
+    // loads are unconditional (past the last chunk the last one again): a
+    // conditional load is waited for where the two paths join
+    uint4 kn[8], vn[8];
+    load_chunk(c0, kq, vq);
+    for (int c = c0; c < c1; c += 2) {
+      load_chunk(min(c + 1, c1 - 1), kn, vn);
+      process(c, kq, vq);
+      if (c + 1 >= c1) break;  // uniform
+      load_chunk(min(c + 2, c1 - 1), kq, vq);
+      process(c + 1, kn, vn);
     }
   }
   l += __shfl_xor(l, 16);
