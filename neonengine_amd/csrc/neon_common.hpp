@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "neon_internal.hpp"  // the device status bits (kDevErr*)
+
 namespace neon {
 
 constexpr int kWave = 64;
@@ -288,6 +290,78 @@ __device__ __forceinline__ void mx_route_lists(const int32_t* ids, int nk, int E
     base += cnt_e[4 * q] + cnt_e[4 * q + 1] + cnt_e[4 * q + 2] + cnt_e[4 * q + 3];
   }
   if (t == 0) route[kMxItemOff] = base;
+}
+
+// One expert block's share of mx_route_lists, built from the pair ids by the
+// block itself (blockDim 256, nk <= 256, E <= 256): work item y's (slot,
+// group, expert, min(count, 64)) and the pair indices 16 group .. 16 group +
+// 15 of that expert, in ascending pair index, in rows[].  It is the same item
+// and the same pairs as the route table's item y (the same per-expert counts
+// and the same ballot ranks), so a launch that reads the ids directly needs
+// no table, and the launch before it no step that waits for all its rows.
+// Pair ids outside [0, E) join no expert (flagged by block (0, 0)).  False
+// when y is past the last item (uniform for the block).
+struct MxRouteLds {
+  int cnt[256];     // pairs per expert
+  int wq[4][4];     // [group q][wave]: experts with more than 16 q pairs
+  int we[4];        // [wave]: pairs of the block's expert
+  int item[4];      // slot, group, expert, count; expert -1 for no item
+  int32_t rows[16];
+};
+__device__ __forceinline__ bool mx_route_item(const int32_t* __restrict__ ids, int nk, int E,
+                                              int y, int32_t* err, MxRouteLds& s, int& slot,
+                                              int& grp, int& e, int& cnt) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int id = t < nk ? ids[t] : -1;
+  if (t < nk && (unsigned)id >= (unsigned)E) {
+    if (blockIdx.x == 0 && blockIdx.y == 0) flag_dev_err(err, kDevErrExpertId);
+    id = -1;
+  }
+  s.cnt[t] = 0;
+  if (t == 0) s.item[2] = -1;
+  __syncthreads();
+  if (id >= 0) atomicAdd(&s.cnt[id], 1);
+  __syncthreads();
+  const int c = t < E ? s.cnt[t] : 0;
+  unsigned long long bq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) bq[q] = __ballot(c > 16 * q);
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s.wq[q][w] = __popcll(bq[q]);
+  }
+  __syncthreads();
+  // items: group 0 of every used expert in ascending id (item = slot), then
+  // group 1 of the experts with more than 16 pairs, ...
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  const int slot_t = (w > 0 ? s.wq[0][0] : 0) + (w > 1 ? s.wq[0][1] : 0) +
+                     (w > 2 ? s.wq[0][2] : 0) + __popcll(bq[0] & lt);
+  int base = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (c > 16 * q) {
+      const int before = (w > 0 ? s.wq[q][0] : 0) + (w > 1 ? s.wq[q][1] : 0) +
+                         (w > 2 ? s.wq[q][2] : 0);
+      if (base + before + __popcll(bq[q] & lt) == y) {
+        s.item[0] = slot_t; s.item[1] = q; s.item[2] = t; s.item[3] = c < 64 ? c : 64;
+      }
+    }
+    base += s.wq[q][0] + s.wq[q][1] + s.wq[q][2] + s.wq[q][3];
+  }
+  __syncthreads();
+  slot = s.item[0]; grp = s.item[1]; e = s.item[2]; cnt = s.item[3];
+  if (e < 0) return false;
+  // the expert's pairs ranked 16 grp .. 16 grp + 15
+  const unsigned long long be = __ballot(id == e);
+  if (lane == 0) s.we[w] = __popcll(be);
+  __syncthreads();
+  if (id == e) {
+    const int r = (w > 0 ? s.we[0] : 0) + (w > 1 ? s.we[1] : 0) + (w > 2 ? s.we[2] : 0) +
+                  __popcll(be & lt) - 16 * grp;
+    if (r >= 0 && r < 16) s.rows[r] = t;
+  }
+  __syncthreads();
+  return true;
 }
 
 // A load that stays where it is written.  The compiler sinks a plain load

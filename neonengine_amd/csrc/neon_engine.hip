@@ -133,11 +133,17 @@ struct neon_ctx {
   bool fuse_router = fuse_env && (fuse_env[0] == '1' || fuse_env[0] == 'r');
   int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
   int32_t* rr_arrive = nullptr;  // one word (router + route lists, matrix-core steps)
-  // the router, top-k and route lists of the matrix-core steps in one launch
-  // from 49 rows (NEON_ROUTER_ROUTE=0: always the two launches, =2: the one
-  // launch from 2 rows, for comparisons)
-  bool fuse_route = !(getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '0');
-  int fuse_route_min = getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '2' ? 2 : 49;
+  // How the matrix-core steps route (NEON_ROUTER_ROUTE): by default the
+  // router logits launch, then a top-k launch that stores each row's expert
+  // ids, and every expert block builds its own work item from the ids
+  // (mx_route_item), so no launch waits for all rows ("2": logits and top-k
+  // in one launch, a block per row, for comparisons).  "0" builds the route
+  // table in the top-k launch, "1" inside a one-launch router (its last
+  // block), and the expert kernels then read the table (the same items).
+  int route_table = getenv("NEON_ROUTER_ROUTE") && (getenv("NEON_ROUTER_ROUTE")[0] == '0' ||
+                                                    getenv("NEON_ROUTER_ROUTE")[0] == '1')
+                        ? getenv("NEON_ROUTER_ROUTE")[0] - '0' : -1;
+  bool route_one = getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '2';
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -809,28 +815,38 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     uint8_t *yh = take(ny), *yl = take(ny), *ysh = take(ny / 32), *ysl = take(ny / 32);
     if (mx8) { r.xq_hi = xh; r.xq_lo = xl; r.xs_hi = xsh; r.xs_lo = xsl; }
     r.arrive = ctx->rr_arrive;
-    // one launch from 49 rows (20b step, tok/s fused / two launches: B = 64
-    // 15,896 / 15,706, 48 12,585 / 12,584, 32 8884 / 8994, 16 4909 / 5056:
-    // below that the arrival round trip costs more than the launch it saves;
-    // with the 8-wave router kernel, B = 32 8899 / 9017, 16 4945 / 5091)
-    if (ctx->fuse_route && B >= ctx->fuse_route_min && router_route_supported(r)) {
-      launch_router_route(r, ctx->moe_idx, ctx->moe_score, ctx->mx_route, st);
+    // Measured at the 20b step after 16-token prompts (tok/s).  The table
+    // built by the last block of a one-launch router against two launches:
+    // B = 64 15,896 / 15,706, 48 12,585 / 12,584, 32 8899 / 9017, 16 4945 /
+    // 5091 (the wait for the last row costs about the launch it saves).
+    // Without a table, two launches / one launch / the earlier default (one
+    // launch with the table from 49 rows, else two with it): B = 64 17,642 /
+    // 17,331 / 17,067, 56 15,576 / 15,289, 48 13,464 / 13,199 / 13,049, 32
+    // 9577 / 9388 / 9441, 16 5370 / 5206 / 5352 -- one block per row reads
+    // every router row, so the one-launch router loses even without its wait.
+    int32_t* table = ctx->route_table >= 0 ? ctx->mx_route : nullptr;
+    const bool one = ctx->route_table == 1 || (ctx->route_table < 0 && ctx->route_one);
+    if (one && router_route_supported(r)) {
+      launch_router_route(r, ctx->moe_idx, ctx->moe_score, table, st);
     } else {
       launch_router(r, st);
-      launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
-                        ctx->mx_route, st);
+      if (table != nullptr)
+        launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts,
+                          c.top_k, table, st);
+      else
+        launch_topk(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k, st);
     }
     MxArgs gu{};
     gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.Wp = mp.gu_c; gu.sp = mp.gu_s;
     gu.bias = w.gu_bias; gu.x = ctx->xn;
-    gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.route = ctx->mx_route; gu.B = B; gu.N = 2 * I;
+    gu.y = ctx->act; gu.idx = ctx->moe_idx; gu.route = table; gu.B = B; gu.N = 2 * I;
     gu.K = H;
     gu.E = c.n_experts; gu.k = c.top_k; gu.alpha = c.swiglu_alpha; gu.limit = c.swiglu_limit;
     gu.err = ctx->dev_err;
     MxArgs dn{};
     dn.W = w.dn_codes; dn.scales = w.dn_scales; dn.Wp = mp.dn_c; dn.sp = mp.dn_s;
     dn.bias = w.dn_bias; dn.x = ctx->act;
-    dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = ctx->mx_route; dn.B = B;
+    dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = table; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k; dn.err = ctx->dev_err;
     if (mx8) {
@@ -1331,18 +1347,18 @@ extern "C" neon_status neon_read_activation(neon_ctx* ctx, const char* name,
   else if (nm == "moe_idx") { src = ctx->moe_idx; n = B * c.top_k * 4; }
   else if (nm == "moe_score") { src = ctx->moe_score; n = B * c.top_k * 4; }
   else if (nm == "mx_route") {
-    if (ctx->mx_route == nullptr || B < 2 ||
+    if (ctx->mx_route == nullptr || B < 2 || ctx->route_table < 0 ||
         (ctx->decode_mode != NEON_DECODE_MATRIX && ctx->decode_mode != NEON_DECODE_MATRIX_MX8))
       FAIL(ctx, NEON_EINVAL, "neon_read_activation: 'mx_route' exists after matrix-core steps "
-           "of two or more sequences");
+           "of two or more sequences with a route table (NEON_ROUTER_ROUTE=0 or 1)");
     const size_t S = std::min<size_t>(c.n_experts, B * c.top_k);
     src = ctx->mx_route; n = (2 * S + 64 * S) * 4;
   }
   else if (nm == "mx_items") {
-    if (ctx->mx_route == nullptr || B < 2 ||
+    if (ctx->mx_route == nullptr || B < 2 || ctx->route_table < 0 ||
         (ctx->decode_mode != NEON_DECODE_MATRIX && ctx->decode_mode != NEON_DECODE_MATRIX_MX8))
       FAIL(ctx, NEON_EINVAL, "neon_read_activation: 'mx_items' exists after matrix-core steps "
-           "of two or more sequences");
+           "of two or more sequences with a route table (NEON_ROUTER_ROUTE=0 or 1)");
     src = ctx->mx_route + kMxItemOff; n = (kMxRouteWords - kMxItemOff) * 4;
   }
   else FAIL(ctx, NEON_EINVAL, "neon_read_activation: unknown buffer '%s'", name);

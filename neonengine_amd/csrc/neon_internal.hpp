@@ -191,8 +191,9 @@ struct MxArgs {
   const int32_t* route;      // expert modes: used experts, counts, pair lists
                              // [2 S + 64 S] ints, S = min(E, B k), and the work
                              // items at kMxItemOff (kMxRouteWords ints in all),
-                             // written by launch_topk_route before the expert
-                             // kernels
+                             // written by launch_topk_route / launch_router_route
+                             // before the expert kernels; or NULL: each expert
+                             // block builds its item from idx (mx_route_item)
   int B, N, K, E, k;
   float alpha, limit;
   // expert modes on the scaled fp8 x fp4 instruction (launch_mx_moe8): the

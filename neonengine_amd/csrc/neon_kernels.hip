@@ -1796,14 +1796,16 @@ __global__ __launch_bounds__(1024) void k_topk_route(const float* __restrict__ l
 // add, so every logit has its bits (16 waves of two rows each, which waited
 // for the normalised row before requesting their rows, ran B = 64 at 16,133
 // against 16,200 tok/s); wave 0 then ranks the row (k_topk's ranking) from
-// LDS.  The row's expert ids are stored at agent scope (written through to
-// the device's coherence point), every wave waits for its stores (vmcnt 0),
-// the block meets at a barrier, and one thread arrives on arrive[0] with an
+// LDS.  With route NULL the block ends there: the expert kernels build
+// their work items from the ids (mx_route_item).  Given a route table, the
+// row's expert ids are stored at agent scope (written through to the
+// device's coherence point), every wave waits for its stores (vmcnt 0), the
+// block meets at a barrier, and one thread arrives on arrive[0] with an
 // agent-scope fetch_add.  The block that arrives last reads every row's ids
 // with agent-scope loads, builds the route lists (mx_route_lists) and sets
 // arrive[0] back to 0 (it must be 0 at launch).  At the 20b shape, B = 64:
-// 15.3 us per layer against 5.1 + 12.0 us for k_router_logits + k_topk_route
-// (14,764 against 14,615 tok/s).
+// 15.3 us per layer with the table against 5.1 + 12.0 us for
+// k_router_logits + k_topk_route (14,764 against 14,615 tok/s).
 constexpr int kRRWaves = 8;  // k_router_route: waves per block
 template <int P>
 __global__ __launch_bounds__(64 * kRRWaves) void k_router_route(
@@ -1870,8 +1872,10 @@ __global__ __launch_bounds__(64 * kRRWaves) void k_router_route(
       __hip_atomic_store(score + (size_t)b * k + lane, t.sc[lane], __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ids have reached the coherence point
+    if (route != nullptr)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ids have reached the coherence point
   }
+  if (route == nullptr) return;  // (uniform) no table: the expert blocks read the ids
   __syncthreads();
   if (tid == 0)
     is_last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==

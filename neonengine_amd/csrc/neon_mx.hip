@@ -992,6 +992,21 @@ __device__ __forceinline__ bool mx_block_item(const MxArgs& a, int tid, int& slo
   return 16 * grp < cnt;
 }
 
+// The block's work item and its 16 pair rows in s.rows (entries from the
+// item's pair count R = min(16, cnt - 16 grp) on are not read): from the
+// route table when the router step wrote one (a.route), else built by the
+// block from the pair ids (mx_route_item: the same item, the same pairs).
+__device__ __forceinline__ bool mx_block_work(const MxArgs& a, int tid, MxRouteLds& s,
+                                              int& slot, int& grp, int& e, int& cnt) {
+  if (a.route == nullptr)
+    return mx_route_item(a.idx, a.B * a.k, a.E, blockIdx.y, a.err, s, slot, grp, e, cnt);
+  if (!mx_block_item(a, tid, slot, grp, e, cnt)) return false;  // (uniform)
+  const int S = min(a.E, a.B * a.k);
+  if (tid < 16) s.rows[tid] = a.route[2 * S + 64 * slot + 16 * grp + tid];  // within the 64-entry list
+  __syncthreads();
+  return true;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   constexpr int CKU = 16, CK = 32 * CKU, XS = CK + 8;
@@ -1000,13 +1015,13 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
-  // block row y = work item y of the route table: rows 16 group .. 16 group
-  // + 15 of the slot's pair list
+  // block row y = work item y (the route table's order): rows 16 group ..
+  // 16 group + 15 of the slot's pair list
+  __shared__ MxRouteLds rl;
   int slot, grp, e, Rall;
-  if (!mx_block_item(a, tid, slot, grp, e, Rall)) return;  // (uniform)
-  const int S = min(a.E, a.B * a.k);
+  if (!mx_block_work(a, tid, rl, slot, grp, e, Rall)) return;  // (uniform)
   const int R = min(16, Rall - 16 * grp);
-  const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
+  const int32_t* rows = rl.rows;
   const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;  // the wave's first row
   const bool wave_on = nw0 < N;               // uniform per wave
   const int nch = (U + CKU - 1) / CKU;
@@ -1020,9 +1035,7 @@ __global__ __launch_bounds__(256) void k_mx_moe16(MxArgs a) {
     bias_pre[tt] = bf2f(load_pinned_u16(  // unconditional (clamped): no branch to join
         a.bias + (size_t)e * N + min(nw0 + 16 * tt + j, N - 1)));
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    row_pre[r] = (int32_t)load_pinned_u32(reinterpret_cast<const uint32_t*>(rows) +
-                                          min(4 * g + r, R - 1));
+  for (int r = 0; r < 4; ++r) row_pre[r] = rows[min(4 * g + r, R - 1)];
   // staging: thread tid copies 8-element pieces (tid & 15) + 16 q of row tid >> 4
   const int sr = tid >> 4, sp = tid & 15;
   const bool s_ok = sr < R;
@@ -1536,11 +1549,11 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int N = a.N, K = a.K, U = K / 32;
+  __shared__ MxRouteLds rl;
   int slot, grp, e, Rall;
-  if (!mx_block_item(a, tid, slot, grp, e, Rall)) return;  // (uniform)
-  const int S = min(a.E, a.B * a.k);
+  if (!mx_block_work(a, tid, rl, slot, grp, e, Rall)) return;  // (uniform)
   const int R = min(16, Rall - 16 * grp);
-  const int32_t* rows = a.route + 2 * S + 64 * slot + 16 * grp;
+  const int32_t* rows = rl.rows;
   const int nw0 = blockIdx.x * 64 * TT + 16 * TT * w;
   const bool wave_on = nw0 < N;
   const int nch = (U + CKU - 1) / CKU;
@@ -1549,9 +1562,7 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
       bf2f(load_pinned_u16(a.bias + (size_t)e * N + min(nw0 + j, N - 1)));
   int32_t row_pre[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    row_pre[r] = (int32_t)load_pinned_u32(reinterpret_cast<const uint32_t*>(rows) +
-                                          min(4 * g + r, R - 1));
+  for (int r = 0; r < 4; ++r) row_pre[r] = rows[min(4 * g + r, R - 1)];
   // staging: thread tid copies 16-byte pieces sp and sp + 16 of row sr's
   // chunk, hi and lo, and unit sp's two scale bytes
   const int sr = tid >> 4, sp = tid & 15;

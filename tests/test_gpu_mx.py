@@ -294,12 +294,16 @@ def test_matrix_mode_sampling_reproducible():
     assert (runs[0] >= 0).all() and (runs[0] < cfg.vocab).all()
 
 
+@pytest.mark.parametrize("table", ["0", "1"])
 @pytest.mark.parametrize("E,B", [(32, 16), (128, 16), (8, 5), (8, 64), (32, 64)])
-def test_route_lists_match_host(E, B):
-    """The route table k_topk_route writes for the matrix-core experts (used
-    experts in ascending order, their pair counts and ascending pair lists)
-    equals one built on the host from the same step's expert ids."""
+def test_route_lists_match_host(monkeypatch, E, B, table):
+    """The route table the matrix-core steps write when one is asked for
+    (NEON_ROUTER_ROUTE=0: k_topk_route after the router logits, =1: the last
+    block of the router launch) -- used experts in ascending order, their pair
+    counts and ascending pair lists, and the work items -- equals one built
+    on the host from the same step's expert ids."""
     torch_cuda()
+    monkeypatch.setenv("NEON_ROUTER_ROUTE", table)
     cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_experts=E, max_batch=B, max_seq=32))
     eng = ne.Engine(cfg)
     eng.init_random(3)
@@ -333,3 +337,41 @@ def test_route_lists_match_host(E, B):
     assert items[0] == len(want)
     assert list(items[1:1 + len(want)]) == want
     assert len(want) <= (B * k + 15 * S) // 16  # the launch's block rows
+
+
+@pytest.mark.parametrize("mode", ["matrix", "mx8"])
+@pytest.mark.parametrize("E,B", [(32, 16), (128, 16), (8, 5), (8, 64), (32, 64), (128, 64)])
+def test_route_from_ids_bit_identical(monkeypatch, E, B, mode):
+    """By default every expert block of a matrix-core step builds its work
+    item and pair rows from the step's expert ids (mx_route_item) instead of
+    reading a route table: the logits and ids of every step equal those of
+    the table path (test_route_lists_match_host pins the table to the host)
+    bit for bit, with the table built in either launch form, and so do those
+    of the one-launch router without a table (NEON_ROUTER_ROUTE=2)."""
+    torch_cuda()
+    cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_experts=E, max_batch=B, max_seq=64))
+    rng = np.random.default_rng(E + B)
+    prompt = rng.integers(0, cfg.vocab, size=(B, 5)).tolist()
+    out = {}
+    for table in (None, "0", "1", "2"):
+        if table is None:
+            monkeypatch.delenv("NEON_ROUTER_ROUTE", raising=False)
+        else:
+            monkeypatch.setenv("NEON_ROUTER_ROUTE", table)
+        eng = ne.Engine(cfg)
+        eng.init_random(6)
+        eng.set_decode_mode(ne.DECODE_MATRIX if mode == "matrix" else ne.DECODE_MATRIX_MX8)
+        eng.prefill(prompt)
+        lg = []
+        for _ in range(4):
+            eng.decode(1)
+            lg.append(eng.read_logits())
+        ids = eng.read_activation("moe_idx").reshape(-1)
+        out[table] = (np.stack(lg), eng.read_tokens(), ids)
+        eng.close()
+    used = len(set(int(e) for e in out[None][2]))
+    say(f"route from ids E={E} B={B} {mode}: {used} used experts in the last step")
+    for table in ("0", "1", "2"):
+        assert np.array_equal(out[None][0].view(np.uint32), out[table][0].view(np.uint32)), table
+        assert np.array_equal(out[None][1], out[table][1]), table
+        assert np.array_equal(out[None][2], out[table][2]), table
