@@ -144,6 +144,10 @@ struct neon_ctx {
                                                     getenv("NEON_ROUTER_ROUTE")[0] == '1')
                         ? getenv("NEON_ROUTER_ROUTE")[0] - '0' : -1;
   bool route_one = getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '2';
+  // the matrix-core steps' expert combine also writes the next RMSNorm (the
+  // next layer's, or the final one) into the packed layout, one launch fewer
+  // per layer (NEON_MX_COMBINE_NORM=0: separate launches; the same bits)
+  bool mx_combine_norm = !(getenv("NEON_MX_COMBINE_NORM") && getenv("NEON_MX_COMBINE_NORM")[0] == '0');
   float* mx_ybuf = nullptr;          // [max_batch][top_k][hidden] expert dot + bias
   float* mx_part_val = nullptr;      // [max_batch][vocab / 16] lm_head partial argmax
   int32_t* mx_part_idx = nullptr;
@@ -757,6 +761,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
   const int H = c.hidden, D = c.head_dim, I = c.intermediate;
   const int qkv_rows = (c.n_heads + 2 * c.n_kv_heads) * D;
   launch_embed(ctx->tokens, ctx->tok_stride, ctx->pos, nullptr, ctx->embed, ctx->h, H, B, st);
+  bool normed = false;  // the previous layer's combine wrote this layer's packed norm
   for (int l = 0; l < c.n_layers; ++l) {
     const LayerW& w = ctx->layers[l];
     const bool sliding = (l % 2 == 0) && c.sliding_window > 0;  // HFC:75-78
@@ -766,8 +771,11 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     // QKV kernel reads (1 KB contiguous per operand)
     const neon_ctx::MxLayer& mp = ctx->mxp[l];
     const bool xp = mp.wqkv != nullptr;
-    if (xp) launch_rmsnorm_packed(ctx->h, w.attn_norm, ctx->mx_xp, B, H, c.rms_eps, st);
-    else launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
+    if (xp) {
+      if (!normed) launch_rmsnorm_packed(ctx->h, w.attn_norm, ctx->mx_xp, B, H, c.rms_eps, st);
+    } else {
+      launch_rmsnorm(ctx->h, w.attn_norm, ctx->xn, B, H, c.rms_eps, st);
+    }
     MxArgs q{};
     q.W = w.wqkv; q.Wp = mp.wqkv; q.bias = w.bqkv; q.x = ctx->xn; q.xp = xp ? ctx->mx_xp : nullptr;
     q.y = ctx->qkv;
@@ -849,17 +857,26 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     dn.out_f = ctx->mx_ybuf; dn.idx = ctx->moe_idx; dn.route = table; dn.B = B;
     dn.N = H; dn.K = I;
     dn.E = c.n_experts; dn.k = c.top_k; dn.err = ctx->dev_err;
+    // the norm that reads this layer's output, when it goes to the packed layout
+    const uint16_t* next_norm = nullptr;
+    if (ctx->mx_combine_norm) {
+      if (l + 1 < c.n_layers) next_norm = ctx->mxp[l + 1].wqkv ? ctx->layers[l + 1].attn_norm : nullptr;
+      else next_norm = ctx->mx_lm ? ctx->final_norm : nullptr;
+    }
     if (mx8) {
       gu.xq_hi = xh; gu.xq_lo = xl; gu.xs_hi = xsh; gu.xs_lo = xsl;
       gu.yq_hi = yh; gu.yq_lo = yl; gu.ys_hi = ysh; gu.ys_lo = ysl;
-      launch_mx_moe8(gu, dn, ctx->moe_score, ctx->h, st);
+      normed = launch_mx_moe8(gu, dn, ctx->moe_score, ctx->h, st, next_norm, c.rms_eps, ctx->mx_xp);
     } else {
-      launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st);
+      normed = launch_mx_moe(gu, dn, ctx->moe_score, ctx->h, st, next_norm, c.rms_eps, ctx->mx_xp);
     }
   }
   const bool lxp = ctx->mx_lm != nullptr;
-  if (lxp) launch_rmsnorm_packed(ctx->h, ctx->final_norm, ctx->mx_xp, B, H, c.rms_eps, st);
-  else launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
+  if (lxp) {
+    if (!normed) launch_rmsnorm_packed(ctx->h, ctx->final_norm, ctx->mx_xp, B, H, c.rms_eps, st);
+  } else {
+    launch_rmsnorm(ctx->h, ctx->final_norm, ctx->xn, B, H, c.rms_eps, st);
+  }
   MxArgs lm{};
   lm.W = ctx->lm_head; lm.Wp = ctx->mx_lm; lm.x = ctx->xn; lm.xp = lxp ? ctx->mx_xp : nullptr;
   lm.out_f = ctx->logits;

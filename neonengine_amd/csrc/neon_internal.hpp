@@ -93,6 +93,12 @@ void launch_rmsnorm_packed(const uint16_t* x, const uint16_t* w, uint16_t* out, 
                            float eps, hipStream_t st);
 void launch_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* out, int B,
                     int H, float eps, hipStream_t st);
+// the matrix-core experts' combine (ybuf [B][k][H] fp32, slots in order) into
+// h and the following launch_rmsnorm_packed(h, nw, out) in one launch; false
+// (nothing launched) when the shape is not covered (k != 4, H % 8, H > 4096)
+bool launch_mx_combine_norm(const float* ybuf, const float* score, uint16_t* h,
+                            const uint16_t* nw, uint16_t* out, int B, int H, int k, float eps,
+                            hipStream_t st);
 
 // ---- RoPE ---------------------------------------------------------------------
 void launch_rope_apply(uint16_t* x, const int32_t* pos, const float* cos_t,
@@ -223,16 +229,20 @@ void launch_mx_pack_fp4(const uint8_t* codes, const uint8_t* scales, int E, int 
 void launch_mx_gemv(const MxArgs& a, int mode, hipStream_t st);
 // experts of B rows: gate_up + SwiGLU into act, down + bias per pair, then the
 // slot-ordered combine h = bf16(h + bf16(sum_s score_s (dot_s + bias_s)))
-// (the route lists come from launch_topk_route; the weights from the packed
-// copies in Wp / sp)
-void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
-                   hipStream_t st);
+// (the work items from the route table or the expert ids; the weights from
+// the packed copies in Wp / sp).  With next_norm given, the combine also
+// writes launch_rmsnorm_packed(h, next_norm, next_xp) when it can (the
+// return value says whether it did).
+bool launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
+                   hipStream_t st, const uint16_t* next_norm = nullptr, float eps = 0.0f,
+                   uint16_t* next_xp = nullptr);
 // launch_mx_moe with the expert GEMMs on v_mfma_scale_f32_16x16x128_f8f6f4:
 // gate_up.xq_* hold the MXFP8 image of gate_up.x (the router writes it),
 // gate_up.yq_* receive the image of the SwiGLU output that down reads; the
 // packed MXFP4 pieces feed the B operand as they are
-void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
-                    hipStream_t st);
+bool launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
+                    hipStream_t st, const uint16_t* next_norm = nullptr, float eps = 0.0f,
+                    uint16_t* next_xp = nullptr);
 // top-k of B rows of router logits and the route lists of their pairs
 // (B k <= 256, E <= 256) in one launch
 // launch_router (norm fused, no MXFP8 image) + launch_topk_route in one

@@ -1534,6 +1534,117 @@ void launch_rmsnorm_packed(const uint16_t* x, const uint16_t* w, uint16_t* out, 
   }
 }
 
+// The matrix-core steps' expert combine and the next RMSNorm in one launch:
+// block r (256 threads) owns row r of the padded tile.  Wave w combines the
+// row's units u = lane + 64 p for the passes p = w, w + 4, ... with
+// k_mx_combine's arithmetic (y = fmaf chain over the KSL slots in order from
+// 0, then h = bf16(h + bf16(y))), stores them to h and to LDS, and after the
+// barrier wave 0 normalises the row from LDS with k_rmsnorm_packed's
+// arithmetic (wave_x_bf16_finish) and writes its packed pieces.  Rows past B
+// write the zero pieces only.  Every load is issued before any is used
+// (units past the row re-read its last unit and are not stored).
+template <int P, int KSL>
+__global__ __launch_bounds__(256) void k_mx_combine_norm(const float* __restrict__ ybuf,
+                                                         const float* __restrict__ score,
+                                                         uint16_t* __restrict__ h,
+                                                         const uint16_t* __restrict__ nw,
+                                                         uint16_t* __restrict__ out, int B,
+                                                         int H, float eps) {
+  constexpr int PW = (P + 3) / 4;  // passes per wave
+  __shared__ uint4 hs[64 * P];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int U = H / 8, NCH = (H + 127) / 128;
+  uint4* o = reinterpret_cast<uint4*>(out);
+  const size_t tile = (size_t)(r / 16) * NCH * 4 * 64;
+  auto piece = [&](int u) { return tile + ((size_t)(u / 16) * 4 + (u % 16) / 4) * 64 + r % 16 + 16 * (u % 4); };
+  if (r >= B) {  // padding row (uniform)
+    for (int u = tid; u < 16 * NCH; u += 256) o[piece(u)] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  XBf16Raw<P> raw;
+  const uint4* wv = reinterpret_cast<const uint4*>(nw);
+#pragma unroll
+  for (int p = 0; p < P; ++p) raw.w[p] = wv[min(lane + 64 * p, U - 1)];  // used by wave 0
+  float sc[KSL];
+#pragma unroll
+  for (int s = 0; s < KSL; ++s) sc[s] = score[r * KSL + s];
+  uint4* hrow = reinterpret_cast<uint4*>(h + (size_t)r * H);
+  float4 yv[PW][KSL][2];
+  uint4 hv[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int u = min(lane + 64 * min(w + 4 * i, P - 1), U - 1);
+#pragma unroll
+    for (int s = 0; s < KSL; ++s) {
+      const float4* src = reinterpret_cast<const float4*>(ybuf + ((size_t)r * KSL + s) * H + 8 * u);
+      yv[i][s][0] = src[0];
+      yv[i][s][1] = src[1];
+    }
+    hv[i] = hrow[u];
+  }
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int p = w + 4 * i, u = lane + 64 * p;
+    float y[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KSL; ++s) {
+      const float e[8] = {yv[i][s][0].x, yv[i][s][0].y, yv[i][s][0].z, yv[i][s][0].w,
+                          yv[i][s][1].x, yv[i][s][1].y, yv[i][s][1].z, yv[i][s][1].w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) y[q] = __builtin_fmaf(sc[s], e[q], y[q]);
+    }
+    const uint32_t cw[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float lo = __fadd_rn(bf2f((uint16_t)(cw[q] & 0xFFFFu)), bf2f(f2bf(y[2 * q])));
+      const float hi = __fadd_rn(bf2f((uint16_t)(cw[q] >> 16)), bf2f(f2bf(y[2 * q + 1])));
+      ow[q] = (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    }
+    if (p < P && u < U) {
+      const uint4 nv = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      hrow[u] = nv;
+      hs[u] = nv;
+    }
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int p = 0; p < P; ++p) raw.x[p] = hs[min(lane + 64 * p, U - 1)];
+  float xr[P][8];
+  wave_x_bf16_finish<P, true>(xr, raw, eps, H, lane, nullptr);
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = lane + 64 * p;
+    if (u < U) {
+      uint32_t q[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[j] = pack_bf2(xr[p][2 * j], xr[p][2 * j + 1]);
+      o[piece(u)] = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
+  for (int u = U + lane; u < 16 * NCH; u += 64) o[piece(u)] = make_uint4(0, 0, 0, 0);
+}
+
+bool launch_mx_combine_norm(const float* ybuf, const float* score, uint16_t* h,
+                            const uint16_t* nw, uint16_t* out, int B, int H, int k, float eps,
+                            hipStream_t st) {
+  const int P = (H / 8 + 63) / 64;
+  if (k != 4 || H % 8 != 0 || P > 8) return false;
+  const dim3 grid(16 * ((B + 15) / 16));
+  switch (P) {
+#define CN_CASE(PP)                                                                          \
+  case PP:                                                                                   \
+    hipLaunchKernelGGL((k_mx_combine_norm<PP, 4>), grid, dim3(256), 0, st, ybuf, score, h, \
+                       nw, out, B, H, eps);                                                  \
+    break;
+    CN_CASE(1) CN_CASE(2) CN_CASE(3) CN_CASE(4) CN_CASE(5) CN_CASE(6) CN_CASE(7)
+    default: CN_CASE(8)
+#undef CN_CASE
+  }
+  return true;
+}
+
 // ===========================================================================
 // RoPE (HFM:215-222): half-split rotation with the host-built YaRN table
 // (cos/sin [n_pos][D/2] fp32, HF modeling_rope_utils.py:429-483):

@@ -1708,8 +1708,21 @@ __global__ __launch_bounds__(256) void k_mx8_moe16(MxArgs a) {
   }
 }
 
-void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
-                    hipStream_t st) {
+// The combine after the down GEMM, with the next RMSNorm when asked and
+// covered (launch_mx_combine_norm); true when the norm was written.
+static bool mx_combine(const MxArgs& down, const float* score, uint16_t* h, hipStream_t st,
+                       const uint16_t* next_norm, float eps, uint16_t* next_xp) {
+  if (next_norm != nullptr && next_xp != nullptr &&
+      launch_mx_combine_norm(down.out_f, score, h, next_norm, next_xp, down.B, down.N, down.k,
+                             eps, st))
+    return true;
+  hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
+                     down.out_f, score, h, down.N, down.k);
+  return false;
+}
+
+bool launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h,
+                    hipStream_t st, const uint16_t* next_norm, float eps, uint16_t* next_xp) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
   const int Y = mx_item_rows(gate_up.B * gate_up.k, S);
   down.xq_hi = gate_up.yq_hi; down.xq_lo = gate_up.yq_lo;
@@ -1719,12 +1732,11 @@ void launch_mx_moe8(MxArgs gate_up, MxArgs down, const float* score, uint16_t* h
                      gate_up);
   hipLaunchKernelGGL(k_mx8_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, Y),
                      dim3(256), 0, st, down);
-  hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
-                     down.out_f, score, h, down.N, down.k);
+  return mx_combine(down, score, h, st, next_norm, eps, next_xp);
 }
 
-void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
-                   hipStream_t st) {
+bool launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score, uint16_t* h,
+                   hipStream_t st, const uint16_t* next_norm, float eps, uint16_t* next_xp) {
   const int S = std::min(gate_up.E, gate_up.B * gate_up.k);
   const int Y = mx_item_rows(gate_up.B * gate_up.k, S);
   hipLaunchKernelGGL(k_mx_moe16<MX_GATE_UP>,
@@ -1732,8 +1744,7 @@ void launch_mx_moe(const MxArgs& gate_up, const MxArgs& down, const float* score
                      gate_up);
   hipLaunchKernelGGL(k_mx_moe16<MX_DOWN>, dim3((down.N + kMxMoeRows - 1) / kMxMoeRows, Y),
                      dim3(256), 0, st, down);
-  hipLaunchKernelGGL(k_mx_combine, dim3((down.N + 255) / 256, down.B), dim3(256), 0, st,
-                     down.out_f, score, h, down.N, down.k);
+  return mx_combine(down, score, h, st, next_norm, eps, next_xp);
 }
 
 void launch_mx_rope_append(const uint16_t* qkv, const int32_t* pos, const int32_t* seq,

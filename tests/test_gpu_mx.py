@@ -192,6 +192,41 @@ def test_matrix_attention_rope_append_fused_bit_identical(monkeypatch, B, plen):
     assert np.array_equal(out[0][1], out[1][1])
 
 
+@pytest.mark.parametrize("mode", ["matrix", "mx8"])
+@pytest.mark.parametrize("shape,B", [("small", 5), ("small", 33), ("20b", 16), ("20b", 7),
+                                     ("20b", 64)])
+def test_combine_norm_fused_bit_identical(monkeypatch, shape, B, mode):
+    """The expert combine writes the next layer's (and after the last layer
+    the final) RMSNorm into the packed layout in the same launch: the logits
+    and ids of every step equal those of the separate combine and norm
+    launches (NEON_MX_COMBINE_NORM=0) bit for bit, at hidden 512 (one pass
+    per lane) and at the 20b width (six), with padding rows in the tile."""
+    torch_cuda()
+    if shape == "small":
+        cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, max_batch=B, max_seq=64))
+    else:
+        cfg = ne.config_preset("gpt-oss-20b", n_layers=2, max_batch=B, max_seq=64)
+    rng = np.random.default_rng(B)
+    prompt = rng.integers(0, cfg.vocab, size=(B, 4)).tolist()
+    out = []
+    for fused in ("1", "0"):
+        monkeypatch.setenv("NEON_MX_COMBINE_NORM", fused)
+        eng = ne.Engine(cfg)
+        eng.init_random(8)
+        eng.set_decode_mode(ne.DECODE_MATRIX if mode == "matrix" else ne.DECODE_MATRIX_MX8)
+        eng.prefill(prompt)
+        lg = []
+        for _ in range(3):
+            eng.decode(1)
+            lg.append(eng.read_logits())
+        out.append((np.stack(lg), eng.read_tokens(), eng.read_activation("hidden")))
+        eng.close()
+    say(f"combine + norm {shape} B={B} {mode}: ids {out[0][1][0, 4:].tolist()}")
+    assert np.array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+    assert np.array_equal(out[0][1], out[1][1])
+    assert np.array_equal(out[0][2], out[1][2])
+
+
 # ---- the expert GEMMs on the scaled fp8 x fp4 instruction (DECODE_MATRIX_MX8)
 @pytest.mark.parametrize("B", [2, 16, 33, 64])
 def test_small_model_matrix_mx8_steps(B):
