@@ -133,6 +133,7 @@ struct neon_ctx {
   bool fuse_router = fuse_env && (fuse_env[0] == '1' || fuse_env[0] == 'r');
   int32_t* or_arrive = nullptr;  // kMoeSyncWords + 1 words (O -> router)
   int32_t* rr_arrive = nullptr;  // one word (router + route lists, matrix-core steps)
+  int32_t* rl_arrive = nullptr;  // [max_batch] row counters (top-k in the logits launch)
   // How the matrix-core steps route (NEON_ROUTER_ROUTE): by default the
   // router logits launch, then a top-k launch that stores each row's expert
   // ids, and every expert block builds its own work item from the ids
@@ -144,6 +145,9 @@ struct neon_ctx {
                                                     getenv("NEON_ROUTER_ROUTE")[0] == '1')
                         ? getenv("NEON_ROUTER_ROUTE")[0] - '0' : -1;
   bool route_one = getenv("NEON_ROUTER_ROUTE") && getenv("NEON_ROUTER_ROUTE")[0] == '2';
+  // without a table, the top-k finishes in the router logits launch (the
+  // last wave of each row ranks it; NEON_ROUTER_RANK=0: a top-k launch)
+  bool route_rank = !(getenv("NEON_ROUTER_RANK") && getenv("NEON_ROUTER_RANK")[0] == '0');
   // the matrix-core steps' expert combine also writes the next RMSNorm (the
   // next layer's, or the final one) into the packed layout, one launch fewer
   // per layer (NEON_MX_COMBINE_NORM=0: separate launches; the same bits)
@@ -437,6 +441,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
                o_aarr = take(Br * (size_t)c.n_kv_heads * kAttnArriveStride * 4),
                o_orarr = take((kMoeSyncWords + 1) * kMoeSyncStride * 4),
                o_rrarr = take(kMoeSyncStride * 4),
+               o_rlarr = take(Bm * kMoeSyncStride * 4),
                o_rpos = take(kPromptRows * 4), o_rseq = take(kPromptRows * 4),
                o_samp = take(Bm * (size_t)c.vocab * 4),
                o_mxy = take(Bm > 1 ? Bm * (size_t)c.top_k * H * 4 : 0),
@@ -468,6 +473,7 @@ static neon_status ctx_alloc(neon_ctx* ctx) {
   ctx->attn_arrive = (int32_t*)(W + o_aarr);  // zeroed above; every launch leaves it at 0
   ctx->or_arrive = (int32_t*)(W + o_orarr);    // likewise
   ctx->rr_arrive = (int32_t*)(W + o_rrarr);    // likewise
+  ctx->rl_arrive = (int32_t*)(W + o_rlarr);    // likewise
   ctx->logits = (float*)(W + o_lg); ctx->lm_part_val = (float*)(W + o_pv);
   ctx->lm_part_idx = (int32_t*)(W + o_pi); ctx->tokens = (int32_t*)(W + o_tok);
   ctx->pos = (int32_t*)(W + o_pos); ctx->prompt_len = (int32_t*)(W + o_pl);
@@ -810,7 +816,7 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     RouterArgs r;
     r.x = ctx->h; r.norm_w = w.mlp_norm; r.eps = c.rms_eps; r.xn_out = ctx->xn;
     r.W = w.router_w; r.bias = w.router_b; r.lg_out = ctx->router_lg;
-    r.idx = nullptr; r.score = nullptr;  // the top-k runs with the route lists
+    r.idx = nullptr; r.score = nullptr;  // per launch form, below
     r.B = B; r.E = c.n_experts; r.H = H; r.k = c.top_k;
     const bool mx8 = ctx->decode_mode == NEON_DECODE_MATRIX_MX8;
     // the MXFP8 images: xn [B][H] then the SwiGLU output [B k][I], each hi,
@@ -836,13 +842,14 @@ static void enqueue_rows_mx(neon_ctx* ctx, int B, hipStream_t st) {
     const bool one = ctx->route_table == 1 || (ctx->route_table < 0 && ctx->route_one);
     if (one && router_route_supported(r)) {
       launch_router_route(r, ctx->moe_idx, ctx->moe_score, table, st);
-    } else {
+    } else if (table != nullptr) {
       launch_router(r, st);
-      if (table != nullptr)
-        launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts,
-                          c.top_k, table, st);
-      else
-        launch_topk(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k, st);
+      launch_topk_route(ctx->router_lg, ctx->moe_idx, ctx->moe_score, B, c.n_experts, c.top_k,
+                        table, st);
+    } else {
+      r.idx = ctx->moe_idx; r.score = ctx->moe_score;
+      r.row_arrive = ctx->route_rank ? ctx->rl_arrive : nullptr;  // else a k_topk launch
+      launch_router(r, st);
     }
     MxArgs gu{};
     gu.W = w.gu_codes; gu.scales = w.gu_scales; gu.Wp = mp.gu_c; gu.sp = mp.gu_s;

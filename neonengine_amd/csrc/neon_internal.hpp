@@ -127,6 +127,10 @@ struct RouterArgs {
   // apart (0 at launch, left at 0) and the device status word
   int32_t* arrive = nullptr;
   int32_t* err = nullptr;
+  // launch_router with idx: B counters kMoeSyncStride ints apart (0 at
+  // launch, left at 0); the top-k then finishes in the logits launch (the
+  // last wave of each row ranks it) instead of a launch of its own
+  int32_t* row_arrive = nullptr;
 };
 // router logits, then (when a.idx) the top-k / softmax
 void launch_router(const RouterArgs& a, hipStream_t st);

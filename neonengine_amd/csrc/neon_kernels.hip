@@ -1806,13 +1806,22 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int E,
   wave_topk_rank<WEIGHTS>(v, E, k, lane, t);
 }
 
+// Router logits, a wave per (expert e, row b).  With row_arrive given, the
+// row's top-k finishes in the same launch (k_topk's ranking and weights): the
+// wave stores its logit at agent scope (written through to the device's
+// coherence point), waits for the store (vmcnt 0) and arrives on its row's
+// counter (row_arrive[b kMoeSyncStride], its own 256-byte line) with an
+// agent-scope fetch_add; the row's last wave reads the E logits with
+// agent-scope loads, ranks them into idx / score and sets the counter back
+// to 0 (0 at launch).
 template <int P, bool NORM>
 __global__ __launch_bounds__(64) void k_router_logits(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
     uint16_t* __restrict__ xn_out, const uint16_t* __restrict__ W,
     const uint16_t* __restrict__ bias, float* __restrict__ lg_out, int E,
     int H, int32_t* __restrict__ zero, int zero_n, uint8_t* __restrict__ xq_hi,
-    uint8_t* __restrict__ xq_lo, uint8_t* __restrict__ xs_hi, uint8_t* __restrict__ xs_lo) {
+    uint8_t* __restrict__ xq_lo, uint8_t* __restrict__ xs_hi, uint8_t* __restrict__ xs_lo,
+    int32_t* __restrict__ idx, float* __restrict__ score, int k, int32_t* row_arrive) {
   const int e = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
   if (e == 0 && b == 0 && lane < zero_n) zero[(size_t)lane * kMoeSyncStride] = 0;
   const int U = H / 8;
@@ -1850,7 +1859,31 @@ __global__ __launch_bounds__(64) void k_router_logits(
     }
   }
   const float acc = wave_sum(bf16_row_partial<P>(w, xr, U, lane));
-  if (lane == 0) lg_out[(size_t)b * E + e] = __fadd_rn(acc, bf2f(bias_e));
+  const float lv = __fadd_rn(acc, bf2f(bias_e));
+  if (row_arrive == nullptr) {  // uniform
+    if (lane == 0) lg_out[(size_t)b * E + e] = lv;
+    return;
+  }
+  __shared__ TopK t;
+  __shared__ int is_last;
+  if (lane == 0) {
+    __hip_atomic_store(lg_out + (size_t)b * E + e, lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the logit has reached the coherence point
+    is_last = __hip_atomic_fetch_add(row_arrive + (size_t)b * kMoeSyncStride, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == E - 1;
+  }
+  wave_lds_sync();
+  if (!is_last) return;  // uniform
+  float v[kRouteQ];
+#pragma unroll
+  for (int q = 0; q < kRouteQ; ++q)
+    v[q] = __hip_atomic_load(lg_out + (size_t)b * E + min(lane + 64 * q, E - 1), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  wave_topk_rank<true>(v, E, k, lane, t);
+  if (lane < k) { idx[b * k + lane] = t.id[lane]; score[b * k + lane] = t.sc[lane]; }
+  if (lane == 0)
+    __hip_atomic_store(row_arrive + (size_t)b * kMoeSyncStride, 0, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ __launch_bounds__(64) void k_topk(const float* __restrict__ lg,
@@ -2039,6 +2072,8 @@ void launch_topk(const float* lg, int32_t* idx, float* score, int B, int E, int 
 void launch_router(const RouterArgs& a, hipStream_t st) {
   const int P = (a.H / 8 + 63) / 64;
   dim3 grid(a.E, a.B);
+  // the top-k in the logits launch (row arrival) when counters are given
+  int32_t* ra = (a.idx != nullptr && a.row_arrive != nullptr) ? a.row_arrive : nullptr;
   switch (P) {
 #define R_CASE(PP)                                                               \
   case PP:                                                                       \
@@ -2046,19 +2081,19 @@ void launch_router(const RouterArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((k_router_logits<PP, true>), grid, dim3(64), 0, st, a.x, \
                          a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out, a.E,  \
                          a.H, a.zero, a.zero_n, a.xq_hi, a.xq_lo, a.xs_hi,       \
-                         a.xs_lo);                                               \
+                         a.xs_lo, a.idx, a.score, a.k, ra);                      \
     else                                                                         \
       hipLaunchKernelGGL((k_router_logits<PP, false>), grid, dim3(64), 0, st,    \
                          a.x, a.norm_w, a.eps, a.xn_out, a.W, a.bias, a.lg_out,  \
                          a.E, a.H, a.zero, a.zero_n, a.xq_hi, a.xq_lo, a.xs_hi,  \
-                         a.xs_lo);                                               \
+                         a.xs_lo, a.idx, a.score, a.k, ra);                      \
     break;
     R_CASE(1) R_CASE(2) R_CASE(3) R_CASE(4) R_CASE(5) R_CASE(6) R_CASE(7)
     R_CASE(8)
     default: R_CASE(16)
 #undef R_CASE
   }
-  if (a.idx != nullptr)
+  if (a.idx != nullptr && ra == nullptr)
     hipLaunchKernelGGL(k_topk, dim3(a.B), dim3(64), 0, st, a.lg_out, a.idx,
                        a.score, a.E, a.k);
 }

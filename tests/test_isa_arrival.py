@@ -1,6 +1,6 @@
 """CPU check of the in-launch arrival protocols of the split attention kernel
-(k_attn_split) and the batched router kernel (k_router_route) in
-neon_kernels.hip, in their compiled gfx950 assembly.
+(k_attn_split) and the batched router kernels (k_router_route,
+k_router_logits) in neon_kernels.hip, in their compiled gfx950 assembly.
 
 With several key splits, each block stores its partial softmax state with
 relaxed agent-scope stores, waits for them (s_waitcnt vmcnt(0)), meets its
@@ -32,8 +32,10 @@ BARRIER = re.compile(r"^\s*s_barrier\b")
 LOAD = re.compile(r"^\s*global_load_dword\w*\b")
 
 
-def arrival_problems(asm: str):
-    """Ordering faults of the arrival protocol in one kernel's assembly."""
+def arrival_problems(asm: str, barrier: bool = True):
+    """Ordering faults of the arrival protocol in one kernel's assembly
+    (barrier False: one-wave blocks, whose arrival needs only the wave's own
+    stores completed)."""
     lines = [l for l in asm.split("\n") if l.strip() and not l.strip().startswith(";")]
     out = []
     arrivals = [i for i, l in enumerate(lines) if ARRIVE.match(l)]
@@ -51,7 +53,7 @@ def arrival_problems(asm: str):
         b = next((k for k, l in enumerate(between) if BARRIER.match(l)), None)
         if w is None:
             out.append(f"arrival at {a}: no s_waitcnt vmcnt(0) after the last store")
-        elif b is None or b < w:
+        elif barrier and (b is None or b < w):
             out.append(f"arrival at {a}: no s_barrier after the wait")
         # the stores of the partials just before: agent scope (sc1)
         k = s
@@ -84,6 +86,10 @@ def test_detector_catches_misorderings():
     assert arrival_problems(good) == []
     for bad in (no_wait, wait_after_barrier, plain_store, cached_load):
         assert arrival_problems(bad), bad
+    # one-wave form: the barrier is not required, the wait and scopes are
+    assert arrival_problems(good.replace("\ts_barrier\n", ""), barrier=False) == []
+    for bad in (no_wait, plain_store, cached_load):
+        assert arrival_problems(bad.replace("\ts_barrier\n", ""), barrier=False), bad
 
 
 @pytest.fixture(scope="module")
@@ -112,4 +118,13 @@ def test_router_route_arrival_order(kernels_asm):
     met at a barrier before the row's arrival; the last block reads every
     row's ids with agent-scope loads."""
     problems = arrival_problems(kernel_asm(kernels_asm, "k_router_route"))
+    assert problems == [], problems[:4]
+
+
+def test_router_logits_row_arrival_order(kernels_asm):
+    """k_router_logits with row counters (the top-k in the logits launch):
+    each one-wave block stores its logit at agent scope and waits for it
+    before its row's arrival; the row's last block reads the row's logits
+    with agent-scope loads."""
+    problems = arrival_problems(kernel_asm(kernels_asm, "k_router_logits"), barrier=False)
     assert problems == [], problems[:4]
