@@ -553,7 +553,12 @@ static void launch_mx_gemv_lx(const MxArgs& a, hipStream_t st) {
 // (2 stages): 16,353 / 9081 / 5062.  The K parts are used from 49 rows: below
 // that they gained under 2%, and at B = 16 their summation order flipped
 // more routing near-ties in the free-routing check against the oracle
-// (median row error 0.446 against its 0.433 bar).  NEON_MX_LX_STORE / _RESID / _LOGITS =
+// (median row error 0.446 against its 0.433 bar).  At B = 64 one block of
+// these shapes fills a CU's LDS, so QKV runs 160 blocks and O 180 on the 256
+// CUs; shapes with half the LDS or less (two or more blocks per CU: QKV
+// 1,2,2 / 2,2,2 / 1,2,1 / 2,2,1, O 1,2,2 / 2,2,2 / 1,2,1) were all slower
+// (17,479 / 17,808 / 17,042 / 17,230 and 17,591 / 17,494 / 16,415 tok/s
+// against 17,982).  NEON_MX_LX_STORE / _RESID / _LOGITS =
 // "W,NS[,KS]" override them for comparisons (the shapes listed in
 // launch_mx_gemv_lx_sel).
 struct MxLxShape { int waves, ns, ks; };
