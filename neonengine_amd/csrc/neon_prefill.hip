@@ -1300,6 +1300,55 @@ __global__ __launch_bounds__(1024) void k_moe_group(
     if (idx[q] == e) { list_tok[o] = q / k; list_slot[o] = q % k; ++o; }
 }
 
+// Expert grouping in one launch (block e of E): every block counts the pairs
+// of every expert (LDS atomics, k_moe_count's counts), two block scans over
+// the experts give the offsets and the first tile of each, then block e
+// writes e_off[e] and its expert's tiles (block 0 also e_off[E] and
+// n_tiles) and places the expert's pairs as k_moe_group does.  The same
+// lists and tiles as k_moe_count + k_moe_group, one launch and one
+// dependent round trip fewer.
+__global__ __launch_bounds__(1024) void k_moe_group1(
+    const int32_t* __restrict__ idx, int n_pairs, int k, int E, int32_t* __restrict__ e_off,
+    int32_t* __restrict__ tile_e, int32_t* __restrict__ tile_r0, int32_t* __restrict__ n_tiles,
+    int32_t* __restrict__ list_tok, int32_t* __restrict__ list_slot, int32_t* __restrict__ err) {
+  __shared__ int cnt[256];
+  __shared__ int scan_lds[17];
+  __shared__ int mine[2];
+  const int e = blockIdx.x, tid = threadIdx.x;
+  if (tid < 256) cnt[tid] = 0;
+  __syncthreads();
+  const int per = (n_pairs + 1023) / 1024;
+  const int p0 = tid * per, p1 = min(p0 + per, n_pairs);
+  int c = 0;
+  bool bad = false;
+  for (int q = p0; q < p1; ++q) {
+    const int id = idx[q];
+    // a pair whose id lies outside [0, E) joins no group; the combine drops it
+    if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[id], 1);
+    else bad = true;
+    c += id == e;
+  }
+  if (bad && e == 0) flag_dev_err(err, kDevErrExpertId);
+  __syncthreads();
+  const int ce = tid < E ? cnt[tid] : 0;
+  const int off = block_excl_scan_1024(ce, scan_lds);  // pairs of the experts before tid
+  const int total = scan_lds[16];
+  const int toff = block_excl_scan_1024((ce + kGM - 1) / kGM, scan_lds);  // their tiles
+  const int ttot = scan_lds[16];
+  if (tid == e) { mine[0] = off; mine[1] = toff; }
+  if (e == 0 && tid == 0) { e_off[E] = total; *n_tiles = ttot; }
+  __syncthreads();
+  const int base = mine[0], t0 = mine[1], ne = cnt[e];
+  if (tid == 0) e_off[e] = base;
+  for (int r = tid * kGM; r < ne; r += 1024 * kGM) {
+    tile_e[t0 + r / kGM] = e;
+    tile_r0[t0 + r / kGM] = r;
+  }
+  int o = base + block_excl_scan_1024(c, scan_lds);
+  for (int q = p0; q < p1; ++q)
+    if (idx[q] == e) { list_tok[o] = q / k; list_slot[o] = q % k; ++o; }
+}
+
 // out[t] = bf16(residual[t] + bf16(sum_s score[t][s] * y[t][s]))  in slot
 // order with fmaf, as the decode combine (HFM:111-112).
 __global__ void k_moe_combine(const float* __restrict__ ybuf,
@@ -1373,10 +1422,18 @@ __global__ __launch_bounds__(384) void k_moe_combine8(const float* __restrict__ 
 // bf16, ybuf [M][k][H] fp32.
 void launch_moe_prefill(const MoePrefillArgs& a, hipStream_t st) {
   const int n_pairs = a.M * a.k;
-  hipLaunchKernelGGL(k_moe_count, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.E, a.e_off,
-                     a.tile_e, a.tile_r0, a.n_tiles, a.err);
-  hipLaunchKernelGGL(k_moe_group, dim3(a.E), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.e_off,
-                     a.list_tok, a.list_slot);
+  // the grouping in one launch (NEON_PREFILL_GROUP=2: k_moe_count, then
+  // k_moe_group; the same lists)
+  static const bool two = getenv("NEON_PREFILL_GROUP") && getenv("NEON_PREFILL_GROUP")[0] == '2';
+  if (two) {
+    hipLaunchKernelGGL(k_moe_count, dim3(1), dim3(1024), 0, st, a.idx, n_pairs, a.E, a.e_off,
+                       a.tile_e, a.tile_r0, a.n_tiles, a.err);
+    hipLaunchKernelGGL(k_moe_group, dim3(a.E), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.e_off,
+                       a.list_tok, a.list_slot);
+  } else {
+    hipLaunchKernelGGL(k_moe_group1, dim3(a.E), dim3(1024), 0, st, a.idx, n_pairs, a.k, a.E,
+                       a.e_off, a.tile_e, a.tile_r0, a.n_tiles, a.list_tok, a.list_slot, a.err);
+  }
   const int max_tiles = moe_prefill_max_tiles(a.M, a.k, a.E);
   GemmParams p{};
   p.tile_e = a.tile_e; p.tile_r0 = a.tile_r0; p.n_tiles = a.n_tiles; p.e_off = a.e_off;
