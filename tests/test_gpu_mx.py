@@ -382,15 +382,21 @@ def test_route_from_ids_bit_identical(monkeypatch, E, B, mode):
     reading a route table: the logits and ids of every step equal those of
     the table path (test_route_lists_match_host pins the table to the host)
     bit for bit, with the table built in either launch form, and so do those
-    of the one-launch router without a table (NEON_ROUTER_ROUTE=2)."""
+    of the one-launch router without a table (NEON_ROUTER_ROUTE=2) and of a
+    top-k launch of its own instead of the router's last wave per row
+    (NEON_ROUTER_RANK=0)."""
     torch_cuda()
     cfg = ne.config_preset("gpt-oss-20b", **dict(SMALL, n_experts=E, max_batch=B, max_seq=64))
     rng = np.random.default_rng(E + B)
     prompt = rng.integers(0, cfg.vocab, size=(B, 5)).tolist()
     out = {}
-    for table in (None, "0", "1", "2"):
+    for table in (None, "0", "1", "2", "rank0"):
+        monkeypatch.delenv("NEON_ROUTER_RANK", raising=False)
         if table is None:
             monkeypatch.delenv("NEON_ROUTER_ROUTE", raising=False)
+        elif table == "rank0":
+            monkeypatch.delenv("NEON_ROUTER_ROUTE", raising=False)
+            monkeypatch.setenv("NEON_ROUTER_RANK", "0")
         else:
             monkeypatch.setenv("NEON_ROUTER_ROUTE", table)
         eng = ne.Engine(cfg)
@@ -406,7 +412,7 @@ def test_route_from_ids_bit_identical(monkeypatch, E, B, mode):
         eng.close()
     used = len(set(int(e) for e in out[None][2]))
     say(f"route from ids E={E} B={B} {mode}: {used} used experts in the last step")
-    for table in ("0", "1", "2"):
+    for table in ("0", "1", "2", "rank0"):
         assert np.array_equal(out[None][0].view(np.uint32), out[table][0].view(np.uint32)), table
         assert np.array_equal(out[None][1], out[table][1]), table
         assert np.array_equal(out[None][2], out[table][2]), table
